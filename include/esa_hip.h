@@ -1,0 +1,143 @@
+/*
+ * esa_hip.h — C ABI of the MI355X (gfx950) edge-set-attention hot path.
+ *
+ * Conventions shared by every entry point:
+ *   - Every pointer is a device pointer to a caller-allocated buffer.  The
+ *     library never allocates, frees or synchronises; scratch memory is passed
+ *     in as `workspace`, sized by the matching *_workspace_size() query.
+ *   - Work is enqueued on `stream` (a hipStream_t passed as void*).
+ *   - Return value: 0 on success, a negative ESA_ERR_* code for an argument
+ *     error (nothing is launched), or a positive hipError_t from the launch.
+ *   - Token tensors are packed: [total, heads, head_dim] contiguous, one
+ *     segment (graph) after another, with int32 cu_seqlens [batch + 1].
+ *   - Features are bf16 (ESA_BF16) or fp32 (ESA_F32) as each entry point says;
+ *     indices and offsets are int32.
+ */
+#ifndef ESA_HIP_H
+#define ESA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#if defined(__GNUC__) || defined(__clang__)
+#define ESA_API __attribute__((visibility("default")))
+#else
+#define ESA_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ESA_OK 0
+#define ESA_ERR_NULL (-1)       /* a required pointer is null */
+#define ESA_ERR_SHAPE (-2)      /* a size or count is out of range */
+#define ESA_ERR_HEAD_DIM (-3)   /* head_dim other than 16 */
+#define ESA_ERR_WORKSPACE (-4)  /* workspace smaller than the query says */
+#define ESA_ERR_DTYPE (-5)      /* unsupported dtype code */
+#define ESA_ERR_ALIGN (-6)      /* pointer not 16-byte aligned */
+#define ESA_ERR_MASK (-7)       /* edge mask needs total_q == total_k */
+
+#define ESA_F32 0
+#define ESA_BF16 1
+
+/* Library version and build target, e.g. "esa_hip 0.1 gfx950". */
+ESA_API const char* esa_version(void);
+
+/* ------------------------------------------------------------------------ */
+/* Varlen attention over packed segments (bf16 in/out, fp32 softmax).        */
+/*                                                                           */
+/* Replaces flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k,      */
+/* max_seqlen_q, max_seqlen_k, dropout_p=0, softmax_scale, causal=False)     */
+/* called at esa/mha_flash_varlen.py:177-184, and the per-graph attention of */
+/* memory_efficient_attention / SDPA at esa/mha.py:76 and :80-83.            */
+/*                                                                           */
+/* Edge-adjacency mask: when tok_src/tok_dst are non-null (self-attention,   */
+/* total_q == total_k, same cu_seqlens), query token i attends to key token  */
+/* j of the same segment iff i != j and {src_i, dst_i} and {src_j, dst_j}    */
+/* share a node — the predicate of create_edge_adjacency_mask               */
+/* (esa/masked_layers.py:121-142) that get_adj_mask_from_edge_index_edge      */
+/* (:217-268) turns into a 0 / -99999 bias.  It is evaluated on the fly; no  */
+/* mask is stored.  A query with no admissible key gets output 0 and        */
+/* lse = -inf.                                                              */
+/*                                                                           */
+/* softmax_lse is [heads, total_q] fp32 (natural log), as flash-attn's.      */
+/* ------------------------------------------------------------------------ */
+ESA_API int esa_varlen_attn_workspace_size(int total_q, int total_k, int heads,
+                                   int head_dim, int masked, int backward,
+                                   size_t* bytes);
+
+ESA_API int esa_varlen_attn_fwd(const void* q, const void* k, const void* v,
+                        const int* cu_seqlens_q, const int* cu_seqlens_k,
+                        int batch, int total_q, int total_k,
+                        int max_seqlen_q, int max_seqlen_k,
+                        int heads, int head_dim, float softmax_scale,
+                        const int* tok_src, const int* tok_dst,
+                        void* out, float* softmax_lse,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
+/* Gradients of esa_varlen_attn_fwd; replaces flash-attn's varlen backward. */
+ESA_API int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k,
+                        const void* v, const void* out,
+                        const float* softmax_lse,
+                        const int* cu_seqlens_q, const int* cu_seqlens_k,
+                        int batch, int total_q, int total_k,
+                        int max_seqlen_q, int max_seqlen_k,
+                        int heads, int head_dim, float softmax_scale,
+                        const int* tok_src, const int* tok_dst,
+                        void* dq, void* dk, void* dv,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
+/* Materialises the edge-adjacency mask of each segment as a padded
+ * [batch, max_items, max_items] uint8 array (1 = attend), the same entries
+ * get_adj_mask_from_edge_index_edge (esa/masked_layers.py:217-268) sets to 0
+ * in its bias.  For tests and debugging on small inputs only. */
+ESA_API int esa_edge_mask_dense(const int* tok_src, const int* tok_dst,
+                        const int* cu_seqlens, int batch, int total,
+                        int max_items, uint8_t* mask_out, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Edge-token gather: out[e] = [x[src[e]] || x[dst[e]]], out is [E, 2F].     */
+/* Replaces the gather + torch.cat at core/pretraining_model.py:153-155 and  */
+/* esa/models.py:307-309.  dtype is ESA_F32 or ESA_BF16; bit-exact copy.     */
+/* ------------------------------------------------------------------------ */
+ESA_API int esa_edge_gather(const void* x, const int* src, const int* dst,
+                    int64_t num_edges, int num_nodes, int features, int dtype,
+                    void* out, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* CSR construction by a key array (e.g. dst): indptr[N+1] and perm[E], perm */
+/* listing edge ids grouped by key in ascending edge order (a stable sort).  */
+/* The layout torch_scatter's segment_*_csr consumes                        */
+/* (GET/utils/sorted_segment_ops.py:17-41).                                  */
+/* ------------------------------------------------------------------------ */
+ESA_API int esa_csr_workspace_size(int64_t num_edges, int num_nodes, size_t* bytes);
+
+ESA_API int esa_csr_build(const int* keys, int64_t num_edges, int num_nodes,
+                  int* indptr, int* perm,
+                  void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Deterministic segmented sum: out[n] = sum_{i in [indptr[n], indptr[n+1])} */
+/* y[perm ? perm[i] : i], accumulated in fp32 in ascending i and rounded     */
+/* once.  y is [E, F], out is [N, F], both of `dtype`.  Replaces the atomic  */
+/* scatter_add edge->node reductions (core/molecular_encoder.py:241-242)     */
+/* with the CSR semantics of GET/utils/sorted_segment_ops.py:40-41.          */
+/* ------------------------------------------------------------------------ */
+ESA_API int esa_csr_segment_sum(const void* y, const int* perm, const int* indptr,
+                        int num_nodes, int features, int dtype, void* out,
+                        void* stream);
+
+/* Backward of esa_edge_gather: gx[n] = sum over edges with src == n of
+ * g[e, :F] + sum over edges with dst == n of g[e, F:], via two CSRs, each
+ * accumulated in fp32 in ascending edge order (deterministic). */
+ESA_API int esa_edge_gather_bwd(const void* g, const int* src_perm,
+                        const int* src_indptr, const int* dst_perm,
+                        const int* dst_indptr, int num_nodes, int features,
+                        int dtype, void* gx, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ESA_HIP_H */

@@ -1,0 +1,101 @@
+"""ctypes binding of ``libesa_hip.so`` (the C ABI in ``include/esa_hip.h``).
+
+The library is loaded after ``torch`` so that it binds to the HIP runtime
+torch already mapped (both carry the soname ``libamdhip64.so.7``): device
+pointers and streams from torch are then valid inside the library.  There is
+no fallback: if the library is missing or the process has no GPU, every entry
+point raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "lib" / "libesa_hip.so"
+
+ESA_F32 = 0
+ESA_BF16 = 1
+
+ERRORS = {
+    -1: "ESA_ERR_NULL (a required pointer is null)",
+    -2: "ESA_ERR_SHAPE (a size or count is out of range)",
+    -3: "ESA_ERR_HEAD_DIM (head_dim must be 16)",
+    -4: "ESA_ERR_WORKSPACE (workspace too small)",
+    -5: "ESA_ERR_DTYPE (unsupported dtype)",
+    -6: "ESA_ERR_ALIGN (pointer not 16-byte aligned)",
+    -7: "ESA_ERR_MASK (edge mask needs total_q == total_k)",
+}
+
+_c_int, _c_i64, _c_f, _c_sz, _vp = ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_size_t, ctypes.c_void_p
+
+_PROTOS = {
+    "esa_version": (ctypes.c_char_p, []),
+    "esa_varlen_attn_workspace_size": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int, ctypes.POINTER(_c_sz)]),
+    "esa_varlen_attn_fwd": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
+                                     _c_f, _vp, _vp, _vp, _vp, _vp, _c_sz, _vp]),
+    "esa_varlen_attn_bwd": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int,
+                                     _c_int, _c_int, _c_f, _vp, _vp, _vp, _vp, _vp, _vp, _c_sz, _vp]),
+    "esa_edge_mask_dense": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _vp]),
+    "esa_edge_gather": (_c_int, [_vp, _vp, _vp, _c_i64, _c_int, _c_int, _c_int, _vp, _vp]),
+    "esa_csr_workspace_size": (_c_int, [_c_i64, _c_int, ctypes.POINTER(_c_sz)]),
+    "esa_csr_build": (_c_int, [_vp, _c_i64, _c_int, _vp, _vp, _vp, _c_sz, _vp]),
+    "esa_csr_segment_sum": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _vp]),
+    "esa_edge_gather_bwd": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _vp]),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+class EsaError(RuntimeError):
+    """Nonzero status from a C-ABI entry point."""
+
+
+def load() -> ctypes.CDLL:
+    """Load (once) and return the library with argument types set."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise EsaError(f"{LIB_PATH} is not built; run `python -m mind_amd._build` (hipcc, gfx950)")
+            lib = ctypes.CDLL(str(LIB_PATH), mode=ctypes.RTLD_LOCAL)
+            for name, (res, args) in _PROTOS.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = lib
+    return _lib
+
+
+def exported_symbols() -> list[str]:
+    return list(_PROTOS)
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        if rc < 0:
+            raise EsaError(f"{what}: {ERRORS.get(rc, rc)}")
+        raise EsaError(f"{what}: HIP error {rc}")
+
+
+def require_gpu(*tensors: torch.Tensor) -> None:
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise EsaError("the MI355X kernels take device tensors; got a tensor on " + str(t.device))
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def version() -> str:
+    return load().esa_version().decode()

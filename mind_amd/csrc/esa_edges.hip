@@ -1,0 +1,440 @@
+// Edge-token gather, CSR construction and deterministic segmented sums on
+// gfx950.  All three are HBM-bound byte/integer work: 16-byte vector
+// accesses, one wave per output row (segment sums) or one lane per 16-byte
+// chunk (gather), nontemporal stores for the streamed gather output.
+//
+// Gather semantics: h_e = [x[src_e] || x[dst_e]] (core/pretraining_model.py:153-155,
+// esa/models.py:307-309).  Segment sum semantics: out_n = sum over the CSR
+// segment of n in ascending position (GET/utils/sorted_segment_ops.py:40-41),
+// fp32 accumulation, rounded once.
+#include "esa_common.h"
+#include "../../include/esa_hip.h"
+
+namespace {
+
+// ------------------------------------------------------------------ gather
+
+// One lane moves one 16-byte chunk; a block covers `epb` consecutive edges.
+// Rows whose node index is outside [0, num_nodes) are written as zeros.
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(256) void edge_gather_kernel(const u32x4* __restrict__ x,
+                                                          const int* __restrict__ src,
+                                                          const int* __restrict__ dst, long num_edges,
+                                                          int num_nodes, int chunks, int epb,
+                                                          u32x4* __restrict__ out) {
+  const long e0 = (long)blockIdx.x * epb;
+  const long rem = num_edges - e0;
+  const int ne = rem < epb ? (int)rem : epb;
+  const int per_edge = 2 * chunks;
+  const int items = ne * per_edge;
+#pragma unroll 4
+  for (int it = threadIdx.x; it < items; it += blockDim.x) {
+    const int el = it / per_edge;
+    const int c = it - el * per_edge;
+    const long e = e0 + el;
+    const bool first = c < chunks;
+    const int node = first ? src[e] : dst[e];
+    const int cc = first ? c : c - chunks;
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if ((unsigned)node < (unsigned)num_nodes) v = x[(size_t)node * chunks + cc];
+    __builtin_nontemporal_store(v, &out[(size_t)e * per_edge + c]);
+  }
+}
+
+// Element-wise fallback for rows that are not a multiple of 16 bytes.
+template <typename T>
+__global__ void edge_gather_scalar_kernel(const T* __restrict__ x, const int* __restrict__ src,
+                                          const int* __restrict__ dst, long num_edges, int num_nodes,
+                                          int features, T* __restrict__ out) {
+  const long n = num_edges * 2 * features;
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) {
+    const long e = i / (2 * features);
+    const int c = (int)(i - e * 2 * features);
+    const bool first = c < features;
+    const int node = first ? src[e] : dst[e];
+    const int f = first ? c : c - features;
+    out[i] = (unsigned)node < (unsigned)num_nodes ? x[(size_t)node * features + f] : (T)0.f;
+  }
+}
+
+// ------------------------------------------------------------------ CSR
+
+__global__ void zero_int_kernel(int* __restrict__ p, long n) {
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) p[i] = 0;
+}
+
+__global__ void count_keys_kernel(const int* __restrict__ keys, long num_edges, int num_nodes,
+                                  int* __restrict__ counts) {
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < num_edges; i += (long)gridDim.x * blockDim.x) {
+    const int k = keys[i];
+    if ((unsigned)k < (unsigned)num_nodes) atomicAdd(&counts[k], 1);
+  }
+}
+
+constexpr int kScanBlock = 1024;
+constexpr int kScanItems = 4;  // per thread
+constexpr int kScanTile = kScanBlock * kScanItems;
+
+// Block-wide exclusive scan of one value per thread (Hillis-Steele in LDS).
+DEVI int block_exclusive_scan(int v, int* sh, int& total) {
+  const int tid = threadIdx.x;
+  sh[tid] = v;
+  __syncthreads();
+  for (int off = 1; off < kScanBlock; off <<= 1) {
+    const int add = tid >= off ? sh[tid - off] : 0;
+    __syncthreads();
+    sh[tid] += add;
+    __syncthreads();
+  }
+  total = sh[kScanBlock - 1];
+  const int incl = sh[tid];
+  __syncthreads();
+  return incl - v;
+}
+
+// Pass 1: per-tile sums of counts[0..n).
+__global__ __launch_bounds__(kScanBlock) void scan_reduce_kernel(const int* __restrict__ in, int n,
+                                                                 int* __restrict__ tile_sums) {
+  __shared__ int sh[kScanBlock];
+  const int base = blockIdx.x * kScanTile + threadIdx.x * kScanItems;
+  int s = 0;
+#pragma unroll
+  for (int j = 0; j < kScanItems; ++j) s += base + j < n ? in[base + j] : 0;
+  int total;
+  block_exclusive_scan(s, sh, total);
+  if (threadIdx.x == 0) tile_sums[blockIdx.x] = total;
+}
+
+// Pass 2: exclusive scan of the tile sums in one block (loops over chunks).
+__global__ __launch_bounds__(kScanBlock) void scan_tiles_kernel(int* __restrict__ tile_sums, int ntiles) {
+  __shared__ int sh[kScanBlock];
+  int carry = 0;
+  for (int base = 0; base < ntiles; base += kScanBlock) {
+    const int i = base + threadIdx.x;
+    const int v = i < ntiles ? tile_sums[i] : 0;
+    int total;
+    const int ex = block_exclusive_scan(v, sh, total);
+    if (i < ntiles) tile_sums[i] = carry + ex;
+    carry += total;
+  }
+}
+
+// Pass 3: indptr[i] = exclusive prefix of counts, indptr[n] = total;
+// cursor[i] = indptr[i] (fill cursor).
+__global__ __launch_bounds__(kScanBlock) void scan_apply_kernel(const int* __restrict__ in, int n,
+                                                                const int* __restrict__ tile_offsets,
+                                                                int* __restrict__ indptr,
+                                                                int* __restrict__ cursor) {
+  __shared__ int sh[kScanBlock];
+  const int base = blockIdx.x * kScanTile + threadIdx.x * kScanItems;
+  int v[kScanItems];
+  int s = 0;
+#pragma unroll
+  for (int j = 0; j < kScanItems; ++j) { v[j] = base + j < n ? in[base + j] : 0; s += v[j]; }
+  int total;
+  int run = block_exclusive_scan(s, sh, total) + tile_offsets[blockIdx.x];
+#pragma unroll
+  for (int j = 0; j < kScanItems; ++j) {
+    if (base + j < n) { indptr[base + j] = run; cursor[base + j] = run; }
+    run += v[j];
+  }
+  if (blockIdx.x == gridDim.x - 1 && threadIdx.x == kScanBlock - 1) indptr[n] = run;
+}
+
+__global__ void fill_perm_kernel(const int* __restrict__ keys, long num_edges, int num_nodes,
+                                 int* __restrict__ cursor, int* __restrict__ perm) {
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < num_edges; i += (long)gridDim.x * blockDim.x) {
+    const int k = keys[i];
+    if ((unsigned)k < (unsigned)num_nodes) perm[atomicAdd(&cursor[k], 1)] = (int)i;
+  }
+}
+
+// The atomic fill leaves each segment in arbitrary order; sorting every
+// segment ascending makes perm the stable (ascending edge id) order, so the
+// result does not depend on atomic timing.  Insertion sort, one thread per
+// node: O(degree^2) per node.
+__global__ void sort_segments_kernel(const int* __restrict__ indptr, int num_nodes, int* __restrict__ perm) {
+  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= num_nodes) return;
+  const int a = indptr[n], b = indptr[n + 1];
+  for (int i = a + 1; i < b; ++i) {
+    const int x = perm[i];
+    int j = i - 1;
+    while (j >= a && perm[j] > x) { perm[j + 1] = perm[j]; --j; }
+    perm[j + 1] = x;
+  }
+}
+
+// ------------------------------------------------------------------ segment sums
+
+template <typename T> struct Vec16;
+template <> struct Vec16<float> { static constexpr int N = 4; };
+template <> struct Vec16<bf16> { static constexpr int N = 8; };
+
+template <typename T>
+DEVI void load16(const T* p, float* v);
+template <>
+DEVI void load16<float>(const float* p, float* v) {
+  const f32x4 x = *reinterpret_cast<const f32x4*>(p);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = x[i];
+}
+template <>
+DEVI void load16<bf16>(const bf16* p, float* v) {
+  const bf16x8 x = *reinterpret_cast<const bf16x8*>(p);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = (float)x[i];
+}
+template <typename T>
+DEVI void store16(T* p, const float* v);
+template <>
+DEVI void store16<float>(float* p, const float* v) {
+  f32x4 x;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) x[i] = v[i];
+  *reinterpret_cast<f32x4*>(p) = x;
+}
+template <>
+DEVI void store16<bf16>(bf16* p, const float* v) {
+  bf16x8 x;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) x[i] = (bf16)v[i];
+  *reinterpret_cast<bf16x8*>(p) = x;
+}
+
+// Adds segment [a, b) of rows y[perm[i]*ld + off ...] into acc, ascending i.
+// Loads are issued four rows ahead; the additions stay in ascending order.
+template <typename T>
+DEVI void accumulate_segment(const T* __restrict__ y, const int* __restrict__ perm, int a, int b, long ld,
+                             int off, float* acc) {
+  constexpr int V = Vec16<T>::N;
+  int i = a;
+  for (; i + 4 <= b; i += 4) {
+    float r[4][V];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const long e = perm ? perm[i + u] : i + u;
+      load16<T>(y + e * ld + off, r[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int k = 0; k < V; ++k) acc[k] += r[u][k];
+  }
+  for (; i < b; ++i) {
+    const long e = perm ? perm[i] : i;
+    float r[V];
+    load16<T>(y + e * ld + off, r);
+#pragma unroll
+    for (int k = 0; k < V; ++k) acc[k] += r[k];
+  }
+}
+
+// One wave per node (grid-stride); each lane owns 16-byte column chunks.
+// out[n] = seg(y, csr1, off1) (+ seg(y, csr2, off2) when indptr2 != null).
+template <typename T>
+__global__ __launch_bounds__(256) void segment_sum_kernel(const T* __restrict__ y, long ld,
+                                                          const int* __restrict__ perm1,
+                                                          const int* __restrict__ indptr1, int off1,
+                                                          const int* __restrict__ perm2,
+                                                          const int* __restrict__ indptr2, int off2,
+                                                          int num_nodes, int features, T* __restrict__ out) {
+  constexpr int V = Vec16<T>::N;
+  const int lane = threadIdx.x & 63;
+  const int chunks = features / V;
+  const int waves = gridDim.x * (blockDim.x >> 6);
+  for (int n = __builtin_amdgcn_readfirstlane(blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)); n < num_nodes;
+       n += waves) {
+    const int a1 = indptr1[n], b1 = indptr1[n + 1];
+    int a2 = 0, b2 = 0;
+    if (indptr2) { a2 = indptr2[n]; b2 = indptr2[n + 1]; }
+    for (int c = lane; c < chunks; c += 64) {
+      float acc[V];
+#pragma unroll
+      for (int k = 0; k < V; ++k) acc[k] = 0.f;
+      accumulate_segment<T>(y, perm1, a1, b1, ld, off1 + c * V, acc);
+      if (indptr2) accumulate_segment<T>(y, perm2, a2, b2, ld, off2 + c * V, acc);
+      store16<T>(out + (size_t)n * features + c * V, acc);
+    }
+  }
+}
+
+// Element-wise fallback for feature counts that are not a multiple of 16 bytes.
+template <typename T>
+__global__ void segment_sum_scalar_kernel(const T* __restrict__ y, long ld, const int* __restrict__ perm1,
+                                          const int* __restrict__ indptr1, int off1,
+                                          const int* __restrict__ perm2, const int* __restrict__ indptr2,
+                                          int off2, int num_nodes, int features, T* __restrict__ out) {
+  const long total = (long)num_nodes * features;
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (long)gridDim.x * blockDim.x) {
+    const int n = (int)(i / features), f = (int)(i - (long)n * features);
+    float acc = 0.f;
+    for (int j = indptr1[n]; j < indptr1[n + 1]; ++j) {
+      const long e = perm1 ? perm1[j] : j;
+      acc += (float)y[e * ld + off1 + f];
+    }
+    if (indptr2)
+      for (int j = indptr2[n]; j < indptr2[n + 1]; ++j) {
+        const long e = perm2 ? perm2[j] : j;
+        acc += (float)y[e * ld + off2 + f];
+      }
+    out[i] = (T)acc;
+  }
+}
+
+unsigned grid_for(long n, int block, long cap = 1L << 20) {
+  long g = (n + block - 1) / block;
+  if (g < 1) g = 1;
+  if (g > cap) g = cap;
+  return (unsigned)g;
+}
+
+bool misaligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) != 0; }
+
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+struct CsrWs { size_t counts, cursor, tiles, total; };
+CsrWs csr_ws(int num_nodes) {
+  CsrWs w;
+  const int ntiles = (num_nodes + kScanTile - 1) / kScanTile;
+  size_t off = 0;
+  w.counts = off; off += align256((size_t)num_nodes * 4);
+  w.cursor = off; off += align256((size_t)num_nodes * 4);
+  w.tiles = off; off += align256((size_t)(ntiles > 0 ? ntiles : 1) * 4);
+  w.total = off;
+  return w;
+}
+
+template <typename T>
+int launch_segsum(const T* y, long ld, const int* perm1, const int* indptr1, int off1, const int* perm2,
+                  const int* indptr2, int off2, int num_nodes, int features, T* out, hipStream_t st) {
+  constexpr int V = Vec16<T>::N;
+  const bool vec = features % V == 0 && ld % V == 0 && off1 % V == 0 && off2 % V == 0 && !misaligned16(y) &&
+                   !misaligned16(out);
+  if (vec) {
+    const unsigned blocks = grid_for((long)num_nodes, 4, 1L << 18);
+    hipLaunchKernelGGL(segment_sum_kernel<T>, dim3(blocks), dim3(256), 0, st, y, ld, perm1, indptr1, off1, perm2,
+                       indptr2, off2, num_nodes, features, out);
+  } else {
+    hipLaunchKernelGGL(segment_sum_scalar_kernel<T>, dim3(grid_for((long)num_nodes * features, 256)), dim3(256), 0,
+                       st, y, ld, perm1, indptr1, off1, perm2, indptr2, off2, num_nodes, features, out);
+  }
+  ESA_LAUNCH_CHECK();
+  return ESA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int esa_edge_gather(const void* x, const int* src, const int* dst, int64_t num_edges, int num_nodes,
+                    int features, int dtype, void* out, void* stream) {
+  if (num_edges < 0 || num_nodes < 0 || features < 1) return ESA_ERR_SHAPE;
+  if (dtype != ESA_F32 && dtype != ESA_BF16) return ESA_ERR_DTYPE;
+  if (num_edges == 0) return ESA_OK;
+  if (!x || !src || !dst || !out) return ESA_ERR_NULL;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int es = dtype == ESA_F32 ? 4 : 2;
+  const long row_bytes = (long)features * es;
+  if (row_bytes % 16 == 0 && !misaligned16(x) && !misaligned16(out)) {
+    const int chunks = (int)(row_bytes / 16);
+    // About 4096 chunk moves per block.
+    int epb = (int)(4096 / (2 * chunks));
+    if (epb < 1) epb = 1;
+    const long blocks = (num_edges + epb - 1) / epb;
+    hipLaunchKernelGGL(edge_gather_kernel, dim3((unsigned)blocks), dim3(256), 0, st,
+                       static_cast<const u32x4*>(x), src, dst, (long)num_edges, num_nodes, chunks, epb,
+                       static_cast<u32x4*>(out));
+  } else if (dtype == ESA_F32) {
+    hipLaunchKernelGGL(edge_gather_scalar_kernel<float>, dim3(grid_for(num_edges * 2 * features, 256)), dim3(256), 0,
+                       st, static_cast<const float*>(x), src, dst, (long)num_edges, num_nodes, features,
+                       static_cast<float*>(out));
+  } else {
+    hipLaunchKernelGGL(edge_gather_scalar_kernel<bf16>, dim3(grid_for(num_edges * 2 * features, 256)), dim3(256), 0,
+                       st, static_cast<const bf16*>(x), src, dst, (long)num_edges, num_nodes, features,
+                       static_cast<bf16*>(out));
+  }
+  ESA_LAUNCH_CHECK();
+  return ESA_OK;
+}
+
+int esa_csr_workspace_size(int64_t num_edges, int num_nodes, size_t* bytes) {
+  if (!bytes) return ESA_ERR_NULL;
+  if (num_edges < 0 || num_nodes < 0 || num_edges >= (1LL << 31)) return ESA_ERR_SHAPE;
+  *bytes = csr_ws(num_nodes).total;
+  return ESA_OK;
+}
+
+int esa_csr_build(const int* keys, int64_t num_edges, int num_nodes, int* indptr, int* perm, void* workspace,
+                  size_t workspace_bytes, void* stream) {
+  if (!indptr || !workspace || (num_edges > 0 && (!keys || !perm))) return ESA_ERR_NULL;
+  if (num_edges < 0 || num_nodes < 0 || num_edges >= (1LL << 31)) return ESA_ERR_SHAPE;
+  const CsrWs w = csr_ws(num_nodes);
+  if (workspace_bytes < w.total) return ESA_ERR_WORKSPACE;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  int* counts = reinterpret_cast<int*>(ws + w.counts);
+  int* cursor = reinterpret_cast<int*>(ws + w.cursor);
+  int* tiles = reinterpret_cast<int*>(ws + w.tiles);
+  const int ntiles = (num_nodes + kScanTile - 1) / kScanTile;
+  if (num_nodes == 0) {
+    hipLaunchKernelGGL(zero_int_kernel, dim3(1), dim3(64), 0, st, indptr, 1L);
+    ESA_LAUNCH_CHECK();
+    return ESA_OK;
+  }
+  hipLaunchKernelGGL(zero_int_kernel, dim3(grid_for(num_nodes, 256, 4096)), dim3(256), 0, st, counts, (long)num_nodes);
+  ESA_LAUNCH_CHECK();
+  if (num_edges > 0) {
+    hipLaunchKernelGGL(count_keys_kernel, dim3(grid_for(num_edges, 256, 8192)), dim3(256), 0, st, keys,
+                       (long)num_edges, num_nodes, counts);
+    ESA_LAUNCH_CHECK();
+  }
+  hipLaunchKernelGGL(scan_reduce_kernel, dim3(ntiles), dim3(kScanBlock), 0, st, counts, num_nodes, tiles);
+  ESA_LAUNCH_CHECK();
+  hipLaunchKernelGGL(scan_tiles_kernel, dim3(1), dim3(kScanBlock), 0, st, tiles, ntiles);
+  ESA_LAUNCH_CHECK();
+  hipLaunchKernelGGL(scan_apply_kernel, dim3(ntiles), dim3(kScanBlock), 0, st, counts, num_nodes, tiles, indptr,
+                     cursor);
+  ESA_LAUNCH_CHECK();
+  if (num_edges > 0) {
+    hipLaunchKernelGGL(fill_perm_kernel, dim3(grid_for(num_edges, 256, 8192)), dim3(256), 0, st, keys,
+                       (long)num_edges, num_nodes, cursor, perm);
+    ESA_LAUNCH_CHECK();
+    hipLaunchKernelGGL(sort_segments_kernel, dim3(grid_for(num_nodes, 256)), dim3(256), 0, st, indptr, num_nodes,
+                       perm);
+    ESA_LAUNCH_CHECK();
+  }
+  return ESA_OK;
+}
+
+int esa_csr_segment_sum(const void* y, const int* perm, const int* indptr, int num_nodes, int features, int dtype,
+                        void* out, void* stream) {
+  if (!indptr || !out || (!y && num_nodes > 0)) return ESA_ERR_NULL;
+  if (num_nodes < 0 || features < 1) return ESA_ERR_SHAPE;
+  if (dtype != ESA_F32 && dtype != ESA_BF16) return ESA_ERR_DTYPE;
+  if (num_nodes == 0) return ESA_OK;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (dtype == ESA_F32)
+    return launch_segsum<float>(static_cast<const float*>(y), features, perm, indptr, 0, nullptr, nullptr, 0,
+                                num_nodes, features, static_cast<float*>(out), st);
+  return launch_segsum<bf16>(static_cast<const bf16*>(y), features, perm, indptr, 0, nullptr, nullptr, 0, num_nodes,
+                             features, static_cast<bf16*>(out), st);
+}
+
+int esa_edge_gather_bwd(const void* g, const int* src_perm, const int* src_indptr, const int* dst_perm,
+                        const int* dst_indptr, int num_nodes, int features, int dtype, void* gx, void* stream) {
+  if (!g || !src_indptr || !dst_indptr || !gx) return ESA_ERR_NULL;
+  if (num_nodes < 0 || features < 1) return ESA_ERR_SHAPE;
+  if (dtype != ESA_F32 && dtype != ESA_BF16) return ESA_ERR_DTYPE;
+  if (num_nodes == 0) return ESA_OK;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const long ld = 2L * features;
+  if (dtype == ESA_F32)
+    return launch_segsum<float>(static_cast<const float*>(g), ld, src_perm, src_indptr, 0, dst_perm, dst_indptr,
+                                features, num_nodes, features, static_cast<float*>(gx), st);
+  return launch_segsum<bf16>(static_cast<const bf16*>(g), ld, src_perm, src_indptr, 0, dst_perm, dst_indptr, features,
+                             num_nodes, features, static_cast<bf16*>(gx), st);
+}
+
+}  // extern "C"

@@ -1,0 +1,133 @@
+"""Edge-token gather and deterministic CSR segmented sums on the gfx950 kernels.
+
+``edge_gather(x, src, dst)`` builds the edge tokens ``[x[src] || x[dst]]`` of
+core/pretraining_model.py:153-155 and esa/models.py:307-309 in one pass (no
+intermediate ``x[src]`` / ``x[dst]`` tensors); its backward is two CSR
+segmented sums (by src and by dst), accumulated in a fixed order, so the
+gradient is bitwise reproducible — unlike the atomic scatter_add of the
+reference's edge->node reductions (core/molecular_encoder.py:241-242).
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+_DTYPES = {torch.float32: _lib.ESA_F32, torch.bfloat16: _lib.ESA_BF16}
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    try:
+        return _DTYPES[t.dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {t.dtype}; use float32 or bfloat16") from None
+
+
+def _as_index(t: torch.Tensor, name: str) -> torch.Tensor:
+    if t.dtype not in (torch.int32, torch.int64):
+        raise TypeError(f"{name} must be an integer tensor")
+    return t.to(torch.int32).contiguous()
+
+
+class CSR:
+    """CSR grouping of ``num_edges`` items by an int key in [0, num_nodes).
+
+    ``indptr`` [N+1] int32 and ``perm`` [E] int32: the edge ids of key n are
+    ``perm[indptr[n]:indptr[n+1]]`` in ascending order (a stable sort).
+    """
+
+    def __init__(self, indptr: torch.Tensor, perm: torch.Tensor, num_nodes: int):
+        self.indptr, self.perm, self.num_nodes = indptr, perm, num_nodes
+
+    @classmethod
+    def build(cls, keys: torch.Tensor, num_nodes: int) -> "CSR":
+        keys = _as_index(keys, "keys")
+        _lib.require_gpu(keys)
+        lib = _lib.load()
+        e = keys.numel()
+        nbytes = ctypes.c_size_t(0)
+        _lib.check(lib.esa_csr_workspace_size(e, num_nodes, ctypes.byref(nbytes)), "esa_csr_workspace_size")
+        ws = torch.empty(max(int(nbytes.value), 256), dtype=torch.uint8, device=keys.device)
+        indptr = torch.empty(num_nodes + 1, dtype=torch.int32, device=keys.device)
+        perm = torch.empty(e, dtype=torch.int32, device=keys.device)
+        _lib.check(lib.esa_csr_build(keys.data_ptr(), e, num_nodes, indptr.data_ptr(), perm.data_ptr(),
+                                     ws.data_ptr(), ws.numel(), _lib.stream_of(keys)), "esa_csr_build")
+        return cls(indptr, perm, num_nodes)
+
+
+def segment_sum_csr(y: torch.Tensor, indptr: torch.Tensor, perm: torch.Tensor | None = None) -> torch.Tensor:
+    """out[n] = sum of rows y[perm[i]] (or y[i]) for i in [indptr[n], indptr[n+1]).
+
+    fp32 accumulation in ascending i, one rounding at the end: deterministic.
+    """
+    _lib.require_gpu(y, indptr, perm)
+    if y.dim() != 2:
+        raise ValueError("y must be [E, F]")
+    y = y.contiguous()
+    indptr = _as_index(indptr, "indptr")
+    perm = None if perm is None else _as_index(perm, "perm")
+    n = indptr.numel() - 1
+    out = torch.empty((n, y.shape[1]), dtype=y.dtype, device=y.device)
+    rc = _lib.load().esa_csr_segment_sum(y.data_ptr(), _lib.ptr(perm), indptr.data_ptr(), n, y.shape[1],
+                                         _dtype_code(y), out.data_ptr(), _lib.stream_of(y))
+    _lib.check(rc, "esa_csr_segment_sum")
+    return out
+
+
+def _gather_raw(x: torch.Tensor, src: torch.Tensor, dst: torch.Tensor) -> torch.Tensor:
+    _lib.require_gpu(x, src, dst)
+    x = x.contiguous()
+    e = src.numel()
+    out = torch.empty((e, 2 * x.shape[1]), dtype=x.dtype, device=x.device)
+    rc = _lib.load().esa_edge_gather(x.data_ptr(), src.data_ptr(), dst.data_ptr(), e, x.shape[0], x.shape[1],
+                                     _dtype_code(x), out.data_ptr(), _lib.stream_of(x))
+    _lib.check(rc, "esa_edge_gather")
+    return out
+
+
+def _gather_bwd_raw(g: torch.Tensor, src_csr: CSR, dst_csr: CSR, num_nodes: int, features: int) -> torch.Tensor:
+    g = g.contiguous()
+    gx = torch.empty((num_nodes, features), dtype=g.dtype, device=g.device)
+    rc = _lib.load().esa_edge_gather_bwd(g.data_ptr(), src_csr.perm.data_ptr(), src_csr.indptr.data_ptr(),
+                                         dst_csr.perm.data_ptr(), dst_csr.indptr.data_ptr(), num_nodes, features,
+                                         _dtype_code(g), gx.data_ptr(), _lib.stream_of(g))
+    _lib.check(rc, "esa_edge_gather_bwd")
+    return gx
+
+
+class _EdgeGather(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, src, dst, src_csr, dst_csr):
+        ctx.save_for_backward(src, dst)
+        ctx.csrs = (src_csr, dst_csr)
+        ctx.shape = x.shape
+        return _gather_raw(x, src, dst)
+
+    @staticmethod
+    def backward(ctx, g):
+        src, dst = ctx.saved_tensors
+        src_csr, dst_csr = ctx.csrs
+        n, f = ctx.shape
+        if src_csr is None:
+            src_csr = CSR.build(src, n)
+        if dst_csr is None:
+            dst_csr = CSR.build(dst, n)
+        return _gather_bwd_raw(g, src_csr, dst_csr, n, f), None, None, None, None
+
+
+def edge_gather(x: torch.Tensor, src: torch.Tensor, dst: torch.Tensor, src_csr: CSR | None = None,
+                dst_csr: CSR | None = None) -> torch.Tensor:
+    """Edge tokens ``[x[src] || x[dst]]`` ([E, 2F], dtype of x: float32 or bfloat16).
+
+    Indices outside [0, N) produce zero rows.  The CSRs used by the backward
+    are built on demand unless given (reuse them across layers of one batch).
+    """
+    if x.dim() != 2:
+        raise ValueError("x must be [N, F]")
+    src = _as_index(src, "src")
+    dst = _as_index(dst, "dst")
+    if src.shape != dst.shape or src.dim() != 1:
+        raise ValueError("src and dst must be 1-D and of equal length")
+    return _EdgeGather.apply(x, src, dst, src_csr, dst_csr)

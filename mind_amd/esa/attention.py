@@ -1,0 +1,152 @@
+"""Varlen attention over packed edge-token segments, on the gfx950 kernels.
+
+``varlen_attention`` is the drop-in for ``flash_attn_varlen_func`` as the
+reference calls it (esa/mha_flash_varlen.py:177-184: causal=False, dropout 0,
+``softmax_scale=None`` meaning 1/sqrt(head_dim)), extended with the
+edge-adjacency mask of esa/masked_layers.py:121-142 evaluated on the fly from
+per-token ``(src, dst)`` node ids.  Tensors are packed ``[total, heads, 16]``
+bf16 with int32 ``cu_seqlens``.  Backward is deterministic.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from .. import _lib
+
+HEAD_DIM = 16
+
+
+def _workspace(device: torch.device, total_q: int, total_k: int, heads: int, masked: bool, backward: bool):
+    lib = _lib.load()
+    n = _lib.ctypes.c_size_t(0)
+    _lib.check(lib.esa_varlen_attn_workspace_size(total_q, total_k, heads, HEAD_DIM, int(masked), int(backward),
+                                                  _lib.ctypes.byref(n)), "esa_varlen_attn_workspace_size")
+    return torch.empty(max(int(n.value), 256), dtype=torch.uint8, device=device)
+
+
+def _check_tokens(name: str, t: torch.Tensor, heads: int | None = None) -> None:
+    if t.dtype != torch.bfloat16:
+        raise TypeError(f"{name} must be bfloat16 (got {t.dtype})")
+    if t.dim() != 3 or t.shape[2] != HEAD_DIM:
+        raise ValueError(f"{name} must be [total, heads, {HEAD_DIM}] (got {tuple(t.shape)})")
+    if heads is not None and t.shape[1] != heads:
+        raise ValueError(f"{name} has {t.shape[1]} heads, expected {heads}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def _check_index(name: str, t: torch.Tensor | None, n: int | None = None) -> None:
+    if t is None:
+        return
+    if t.dtype != torch.int32 or t.dim() != 1 or not t.is_contiguous():
+        raise TypeError(f"{name} must be a contiguous 1-D int32 tensor (got {t.dtype}, {tuple(t.shape)})")
+    if n is not None and t.numel() != n:
+        raise ValueError(f"{name} has {t.numel()} entries, expected {n}")
+
+
+def attn_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale,
+             edge_src=None, edge_dst=None):
+    """Raw forward: returns ``(out [Tq,H,16] bf16, softmax_lse [H,Tq] fp32)``."""
+    _lib.require_gpu(q, k, v, cu_seqlens_q, cu_seqlens_k, edge_src, edge_dst)
+    heads = q.shape[1]
+    _check_tokens("q", q)
+    _check_tokens("k", k, heads)
+    _check_tokens("v", v, heads)
+    if k.shape[0] != v.shape[0]:
+        raise ValueError("k and v must have the same number of tokens")
+    batch = cu_seqlens_q.numel() - 1
+    _check_index("cu_seqlens_q", cu_seqlens_q)
+    _check_index("cu_seqlens_k", cu_seqlens_k, batch + 1)
+    masked = edge_src is not None
+    if masked:
+        _check_index("edge_src", edge_src, q.shape[0])
+        _check_index("edge_dst", edge_dst, q.shape[0])
+    tq, tk = q.shape[0], k.shape[0]
+    out = torch.empty_like(q)
+    lse = torch.empty((heads, tq), dtype=torch.float32, device=q.device)
+    ws = _workspace(q.device, tq, tk, heads, masked, False)
+    lib = _lib.load()
+    rc = lib.esa_varlen_attn_fwd(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(), batch, tq, tk,
+        int(max_seqlen_q), int(max_seqlen_k), heads, HEAD_DIM, float(softmax_scale),
+        _lib.ptr(edge_src), _lib.ptr(edge_dst), out.data_ptr(), lse.data_ptr(), ws.data_ptr(), ws.numel(),
+        _lib.stream_of(q))
+    _lib.check(rc, "esa_varlen_attn_fwd")
+    return out, lse
+
+
+def attn_bwd(dout, q, k, v, out, lse, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale,
+             edge_src=None, edge_dst=None):
+    """Raw backward: returns ``(dq, dk, dv)`` (bf16, shapes of q, k, v)."""
+    _lib.require_gpu(dout, q, k, v, out, lse)
+    heads = q.shape[1]
+    _check_tokens("dout", dout, heads)
+    if dout.shape != q.shape:
+        raise ValueError("dout must have the shape of q")
+    batch = cu_seqlens_q.numel() - 1
+    tq, tk = q.shape[0], k.shape[0]
+    masked = edge_src is not None
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    ws = _workspace(q.device, tq, tk, heads, masked, True)
+    lib = _lib.load()
+    rc = lib.esa_varlen_attn_bwd(
+        dout.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr(),
+        cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(), batch, tq, tk, int(max_seqlen_q), int(max_seqlen_k),
+        heads, HEAD_DIM, float(softmax_scale), _lib.ptr(edge_src), _lib.ptr(edge_dst),
+        dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_of(q))
+    _lib.check(rc, "esa_varlen_attn_bwd")
+    return dq, dk, dv
+
+
+class _VarlenAttention(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, cu_q, cu_k, max_q, max_k, scale, edge_src, edge_dst):
+        out, lse = attn_fwd(q, k, v, cu_q, cu_k, max_q, max_k, scale, edge_src, edge_dst)
+        ctx.save_for_backward(q, k, v, out, lse, cu_q, cu_k, edge_src, edge_dst)
+        ctx.meta = (max_q, max_k, scale)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        q, k, v, out, lse, cu_q, cu_k, edge_src, edge_dst = ctx.saved_tensors
+        max_q, max_k, scale = ctx.meta
+        dq, dk, dv = attn_bwd(dout.contiguous(), q, k, v, out, lse, cu_q, cu_k, max_q, max_k, scale,
+                              edge_src, edge_dst)
+        return dq, dk, dv, None, None, None, None, None, None, None
+
+
+def varlen_attention(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, dropout_p=0.0,
+                     softmax_scale=None, causal=False, edge_src=None, edge_dst=None):
+    """``flash_attn_varlen_func``-compatible entry (plus the edge mask).
+
+    q: [Tq, H, 16] bf16; k, v: [Tk, H, 16] bf16; cu_seqlens_*: int32 [B+1].
+    edge_src / edge_dst: optional int32 [Tq] node ids per token (self-attention
+    only); token i then attends to token j of its segment iff i != j and the
+    two edges share an endpoint.
+    """
+    if causal:
+        raise NotImplementedError("causal attention is not on the ESA path (the reference uses causal=False)")
+    if dropout_p:
+        raise NotImplementedError("attention dropout is not supported (dropout is 0 in every reference config)")
+    if softmax_scale is None:
+        softmax_scale = 1.0 / math.sqrt(q.shape[-1])
+    if (edge_src is None) != (edge_dst is None):
+        raise ValueError("edge_src and edge_dst must be given together")
+    return _VarlenAttention.apply(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
+                                  float(softmax_scale), edge_src, edge_dst)
+
+
+def edge_mask_dense(edge_src, edge_dst, cu_seqlens, max_items):
+    """Debug materialisation of the edge mask: uint8 [B, max_items, max_items]."""
+    _lib.require_gpu(edge_src, edge_dst, cu_seqlens)
+    _check_index("edge_src", edge_src)
+    _check_index("edge_dst", edge_dst, edge_src.numel())
+    _check_index("cu_seqlens", cu_seqlens)
+    batch = cu_seqlens.numel() - 1
+    out = torch.empty((batch, max_items, max_items), dtype=torch.uint8, device=edge_src.device)
+    rc = _lib.load().esa_edge_mask_dense(edge_src.data_ptr(), edge_dst.data_ptr(), cu_seqlens.data_ptr(), batch,
+                                         edge_src.numel(), int(max_items), out.data_ptr(), _lib.stream_of(edge_src))
+    _lib.check(rc, "esa_edge_mask_dense")
+    return out

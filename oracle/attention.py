@@ -1,0 +1,104 @@
+"""Textbook per-segment softmax attention (test infrastructure; see oracle/__init__.py).
+
+Restates what the reference's attention calls compute on each graph:
+flash_attn_varlen_func over cu_seqlens (esa/mha_flash_varlen.py:177-184),
+memory_efficient_attention / SDPA with the additive edge bias (esa/mha.py:76,
+:80-83), with softmax_scale = 1/sqrt(head_dim) by default.  A masked entry
+is -inf here; the reference's -99999 bias gives the same probabilities
+whenever a row has an admissible key (exp(-99999 + s - max) underflows to 0).
+A row with no admissible key returns 0 and lse = -inf.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from .mask import edge_adjacency_segment
+
+
+def _segment_mask(edge_src, edge_dst, qs, qe, ks, ke):
+    if edge_src is None:
+        return None
+    assert (qs, qe) == (ks, ke), "the edge mask is self-attention only"
+    m = edge_adjacency_segment(np.asarray(edge_src), np.asarray(edge_dst), qs, qe)
+    return torch.as_tensor(m)
+
+
+def varlen_attention(q, k, v, cu_q, cu_k, scale, edge_src=None, edge_dst=None, dtype=torch.float64):
+    """q [Tq,H,D], k/v [Tk,H,D] -> (out [Tq,H,D], lse [H,Tq]) in ``dtype``."""
+    q, k, v = (t.detach().cpu().to(dtype) for t in (q, k, v))
+    cu_q = np.asarray(cu_q, dtype=np.int64)
+    cu_k = np.asarray(cu_k, dtype=np.int64)
+    tq, h, d = q.shape
+    out = torch.zeros(tq, h, d, dtype=dtype)
+    lse = torch.full((h, tq), float("-inf"), dtype=dtype)
+    for b in range(len(cu_q) - 1):
+        qs, qe, ks, ke = int(cu_q[b]), int(cu_q[b + 1]), int(cu_k[b]), int(cu_k[b + 1])
+        if qe == qs or ke == ks:
+            continue
+        qb = q[qs:qe].permute(1, 0, 2).contiguous()     # [H, Lq, D]
+        kb = k[ks:ke].permute(1, 2, 0).contiguous()     # [H, D, Lk]
+        vb = v[ks:ke].permute(1, 0, 2).contiguous()     # [H, Lk, D]
+        s = torch.matmul(qb, kb) * scale                # [H, Lq, Lk]
+        m = _segment_mask(edge_src, edge_dst, qs, qe, ks, ke)
+        if m is not None:
+            s = s.masked_fill(~m, float("-inf"))
+        l = torch.logsumexp(s, dim=-1)                  # [H, Lq]
+        p = torch.exp(s - l[..., None])
+        p = torch.nan_to_num(p, nan=0.0)                # rows with no admissible key
+        out[qs:qe] = torch.matmul(p, vb).permute(1, 0, 2)
+        lse[:, qs:qe] = l
+    return out, lse
+
+
+def varlen_attention_bwd(dout, q, k, v, cu_q, cu_k, scale, edge_src=None, edge_dst=None, dtype=torch.float64):
+    """Analytic gradients of ``varlen_attention``: (dq, dk, dv).
+
+    With P = softmax(scale Q K^T + mask), O = P V, D = rowsum(dO * O):
+    dV = P^T dO, dP = dO V^T, dS = P * (dP - D), dQ = scale dS K,
+    dK = scale dS^T Q.
+    """
+    dout, q, k, v = (t.detach().cpu().to(dtype) for t in (dout, q, k, v))
+    cu_q = np.asarray(cu_q, dtype=np.int64)
+    cu_k = np.asarray(cu_k, dtype=np.int64)
+    dq, dk, dv = torch.zeros_like(q), torch.zeros_like(k), torch.zeros_like(v)
+    for b in range(len(cu_q) - 1):
+        qs, qe, ks, ke = int(cu_q[b]), int(cu_q[b + 1]), int(cu_k[b]), int(cu_k[b + 1])
+        if qe == qs or ke == ks:
+            continue
+        qb = q[qs:qe].permute(1, 0, 2).contiguous()
+        kb = k[ks:ke].permute(1, 0, 2).contiguous()
+        vb = v[ks:ke].permute(1, 0, 2).contiguous()
+        gb = dout[qs:qe].permute(1, 0, 2).contiguous()
+        s = torch.matmul(qb, kb.transpose(1, 2).contiguous()) * scale
+        m = _segment_mask(edge_src, edge_dst, qs, qe, ks, ke)
+        if m is not None:
+            s = s.masked_fill(~m, float("-inf"))
+        l = torch.logsumexp(s, dim=-1)
+        p = torch.nan_to_num(torch.exp(s - l[..., None]), nan=0.0)
+        o = torch.matmul(p, vb)
+        dvb = torch.matmul(p.transpose(1, 2).contiguous(), gb)
+        dp = torch.matmul(gb, vb.transpose(1, 2).contiguous())
+        drow = (gb * o).sum(-1, keepdim=True)
+        ds = p * (dp - drow)
+        dq[qs:qe] = (torch.matmul(ds, kb) * scale).permute(1, 0, 2)
+        dk[ks:ke] = (torch.matmul(ds.transpose(1, 2).contiguous(), qb) * scale).permute(1, 0, 2)
+        dv[ks:ke] = dvb.permute(1, 0, 2)
+    return dq, dk, dv
+
+
+def padded_attention(q, k, v, scale, bias=None, dtype=torch.float64):
+    """Dense [B, N, H, D] attention with an optional additive bias [B, 1|H, Nq, Nk].
+
+    Restates memory_efficient_attention(Q, K, V, attn_bias) at esa/mha.py:76
+    (BMHK layout), which attends to every position including padding.
+    """
+    q, k, v = (t.detach().cpu().to(dtype) for t in (q, k, v))
+    qb = q.permute(0, 2, 1, 3).contiguous()
+    kb = k.permute(0, 2, 3, 1).contiguous()
+    vb = v.permute(0, 2, 1, 3).contiguous()
+    s = torch.matmul(qb, kb) * scale
+    if bias is not None:
+        s = s + bias.detach().cpu().to(dtype)
+    p = torch.softmax(s, dim=-1)
+    return torch.matmul(p, vb).permute(0, 2, 1, 3)

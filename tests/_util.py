@@ -1,0 +1,36 @@
+"""Shared test helpers: seeded inputs and error metrics."""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+# Tolerances of the north-star parity bar for bf16 attention outputs.
+BF16_MAX_ABS = 2e-2
+BF16_MEAN_ABS = 2e-3
+
+
+def seeded_normal(shape, seed, dtype=torch.bfloat16):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(*shape, generator=g, dtype=torch.float32).to(dtype)
+
+
+def err(a: torch.Tensor, b: torch.Tensor) -> tuple[float, float]:
+    d = (a.detach().double().cpu() - b.detach().double().cpu()).abs()
+    return float(d.max()) if d.numel() else 0.0, float(d.mean()) if d.numel() else 0.0
+
+
+def assert_bf16_close(got, ref, scale: float = 1.0, what: str = ""):
+    """max-abs <= 2e-2 * scale and mean-abs <= 2e-3 * scale."""
+    mx, mn = err(got, ref)
+    assert mx <= BF16_MAX_ABS * scale and mn <= BF16_MEAN_ABS * scale, (
+        f"{what}: max-abs {mx:.3e} (bar {BF16_MAX_ABS * scale:.3e}), mean-abs {mn:.3e} "
+        f"(bar {BF16_MEAN_ABS * scale:.3e})")
+
+
+def grad_scale(ref: torch.Tensor) -> float:
+    """Gradients are checked relative to their own magnitude (at least 1)."""
+    return max(1.0, float(ref.abs().max()))
+
+
+def cu_from_lengths(lengths) -> np.ndarray:
+    return np.concatenate([[0], np.cumsum(np.asarray(lengths, dtype=np.int64))]).astype(np.int32)
