@@ -136,6 +136,19 @@ ESA_API int esa_edge_gather_bwd(const void* g, const int* src_perm,
                         const int* dst_indptr, int num_nodes, int features,
                         int dtype, void* gx, void* stream);
 
+/* ------------------------------------------------------------------------ */
+/* Profiling hook (no counterpart in the reference; used by the benchmark).  */
+/* While enabled, every kernel launch of the entry points above is           */
+/* bracketed by hipEvents on its stream.  esa_profile_collect waits for the  */
+/* recorded events (it synchronises), returns the summed milliseconds and    */
+/* launch count per kernel id (capacity >= ESA_PROFILE_KERNELS) and clears   */
+/* the record.  Not for concurrent use from several threads.                 */
+/* ------------------------------------------------------------------------ */
+#define ESA_PROFILE_KERNELS 10
+ESA_API int esa_profile_enable(int on);
+ESA_API int esa_profile_collect(float* total_ms, int* launches, int capacity);
+ESA_API const char* esa_profile_kernel_name(int kernel);
+
 #ifdef __cplusplus
 }
 #endif

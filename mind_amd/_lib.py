@@ -44,7 +44,12 @@ _PROTOS = {
     "esa_csr_build": (_c_int, [_vp, _c_i64, _c_int, _vp, _vp, _vp, _c_sz, _vp]),
     "esa_csr_segment_sum": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _vp]),
     "esa_edge_gather_bwd": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _vp]),
+    "esa_profile_enable": (_c_int, [_c_int]),
+    "esa_profile_collect": (_c_int, [ctypes.POINTER(_c_f), ctypes.POINTER(_c_int), _c_int]),
+    "esa_profile_kernel_name": (ctypes.c_char_p, [_c_int]),
 }
+
+PROFILE_KERNELS = 10
 
 _lock = threading.Lock()
 _lib = None
@@ -99,3 +104,16 @@ def stream_of(t: torch.Tensor) -> int:
 
 def version() -> str:
     return load().esa_version().decode()
+
+
+def profile_enable(on: bool) -> None:
+    check(load().esa_profile_enable(int(on)), "esa_profile_enable")
+
+
+def profile_collect() -> dict[str, tuple[float, int]]:
+    """Per-kernel (total ms, launches) recorded since the last collect (synchronises)."""
+    lib = load()
+    ms = (_c_f * PROFILE_KERNELS)()
+    n = (_c_int * PROFILE_KERNELS)()
+    check(lib.esa_profile_collect(ms, n, PROFILE_KERNELS), "esa_profile_collect")
+    return {lib.esa_profile_kernel_name(i).decode(): (float(ms[i]), int(n[i])) for i in range(PROFILE_KERNELS)}

@@ -31,6 +31,7 @@
 //   tile-transposed layout [T/8][H][16][8] so each lane's A operand is one
 //   aligned 16-byte load.
 #include "esa_common.h"
+#include "esa_profile.h"
 #include "../../include/esa_hip.h"
 
 namespace {
@@ -511,24 +512,32 @@ int launch_tt(const bf16* x, int total, int heads, bf16* xt, hipStream_t st) {
   const int tp = round32(total);
   const long n = (long)(tp / 8) * heads * kHd;
   if (n == 0) return ESA_OK;
-  hipLaunchKernelGGL(tt_transpose_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x, total, heads, tp, xt);
+  ESA_TIMED(esa_profile::kAttnPrep, st,
+            hipLaunchKernelGGL(tt_transpose_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x, total,
+                               heads, tp, xt));
   ESA_LAUNCH_CHECK();
   return ESA_OK;
 }
 
 int launch_mask_meta(const int* src, const int* dst, int total, int2* nodes, int4* meta, hipStream_t st) {
   const int tp = round32(total);
-  hipLaunchKernelGGL(nodes_pack_kernel, dim3((unsigned)((tp + 255) / 256)), dim3(256), 0, st, src, dst, total, tp, nodes);
+  ESA_TIMED(esa_profile::kAttnPrep, st,
+            hipLaunchKernelGGL(nodes_pack_kernel, dim3((unsigned)((tp + 255) / 256)), dim3(256), 0, st, src, dst,
+                               total, tp, nodes));
   ESA_LAUNCH_CHECK();
   const int nt = tp / kTile;
-  hipLaunchKernelGGL(tile_meta_kernel, dim3((unsigned)((nt + 255) / 256)), dim3(256), 0, st, nodes, total, nt, meta);
+  ESA_TIMED(esa_profile::kAttnPrep, st,
+            hipLaunchKernelGGL(tile_meta_kernel, dim3((unsigned)((nt + 255) / 256)), dim3(256), 0, st, nodes, total,
+                               nt, meta));
   ESA_LAUNCH_CHECK();
   return ESA_OK;
 }
 
 int launch_plan(const int* cu_outer, const int* cu_inner, int nseg, int total_outer, int* plan, hipStream_t st) {
   const int nt = round32(total_outer) / kTile;
-  hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(1024), 0, st, cu_outer, cu_inner, nseg, total_outer, nt, plan);
+  ESA_TIMED(esa_profile::kAttnPrep, st,
+            hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(1024), 0, st, cu_outer, cu_inner, nseg, total_outer, nt,
+                               plan));
   ESA_LAUNCH_CHECK();
   return ESA_OK;
 }
@@ -587,9 +596,11 @@ int esa_varlen_attn_fwd(const void* q, const void* k, const void* v, const int* 
   if ((rc = launch_plan(cu_seqlens_q, cu_seqlens_k, batch, total_q, reinterpret_cast<int*>(ws + L.plan_q), st))) return rc;
   const unsigned grid = (unsigned)a.n_tiles * (unsigned)((heads + 3) / 4);
   if (masked)
-    hipLaunchKernelGGL((attn_qouter_kernel<true, false>), dim3(grid), dim3(256), 0, st, a);
+    ESA_TIMED(esa_profile::kAttnFwdMasked, st,
+              hipLaunchKernelGGL((attn_qouter_kernel<true, false>), dim3(grid), dim3(256), 0, st, a));
   else
-    hipLaunchKernelGGL((attn_qouter_kernel<false, false>), dim3(grid), dim3(256), 0, st, a);
+    ESA_TIMED(esa_profile::kAttnFwd, st,
+              hipLaunchKernelGGL((attn_qouter_kernel<false, false>), dim3(grid), dim3(256), 0, st, a));
   ESA_LAUNCH_CHECK();
   return ESA_OK;
 }
@@ -636,9 +647,10 @@ int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k, const vo
   if ((rc = launch_tt(static_cast<const bf16*>(dout), total_q, heads, dot, st))) return rc;
   {
     const long n = (long)heads * tqp;
-    hipLaunchKernelGGL(bwd_prep_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
-                       static_cast<const bf16*>(dout), static_cast<const bf16*>(out), softmax_lse, total_q,
-                       heads, tqp, lse2, dvec);
+    ESA_TIMED(esa_profile::kAttnPrep, st,
+              hipLaunchKernelGGL(bwd_prep_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                                 static_cast<const bf16*>(dout), static_cast<const bf16*>(out), softmax_lse,
+                                 total_q, heads, tqp, lse2, dvec));
     ESA_LAUNCH_CHECK();
   }
   const int2* nodes = nullptr;
@@ -664,9 +676,11 @@ int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k, const vo
   ka.dk = static_cast<bf16*>(dk); ka.dv = static_cast<bf16*>(dv);
   const unsigned kgrid = (unsigned)ka.n_tiles * groups;
   if (masked)
-    hipLaunchKernelGGL((attn_kouter_kernel<true>), dim3(kgrid), dim3(256), 0, st, ka);
+    ESA_TIMED(esa_profile::kAttnBwdDkdvMasked, st,
+              hipLaunchKernelGGL((attn_kouter_kernel<true>), dim3(kgrid), dim3(256), 0, st, ka));
   else
-    hipLaunchKernelGGL((attn_kouter_kernel<false>), dim3(kgrid), dim3(256), 0, st, ka);
+    ESA_TIMED(esa_profile::kAttnBwdDkdv, st,
+              hipLaunchKernelGGL((attn_kouter_kernel<false>), dim3(kgrid), dim3(256), 0, st, ka));
   ESA_LAUNCH_CHECK();
 
   QOuterArgs qa{};
@@ -677,9 +691,11 @@ int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k, const vo
   qa.plan = plan_q; qa.n_tiles = tqp / kTile; qa.dq = static_cast<bf16*>(dq);
   const unsigned qgrid = (unsigned)qa.n_tiles * groups;
   if (masked)
-    hipLaunchKernelGGL((attn_qouter_kernel<true, true>), dim3(qgrid), dim3(256), 0, st, qa);
+    ESA_TIMED(esa_profile::kAttnBwdDqMasked, st,
+              hipLaunchKernelGGL((attn_qouter_kernel<true, true>), dim3(qgrid), dim3(256), 0, st, qa));
   else
-    hipLaunchKernelGGL((attn_qouter_kernel<false, true>), dim3(qgrid), dim3(256), 0, st, qa);
+    ESA_TIMED(esa_profile::kAttnBwdDq, st,
+              hipLaunchKernelGGL((attn_qouter_kernel<false, true>), dim3(qgrid), dim3(256), 0, st, qa));
   ESA_LAUNCH_CHECK();
   return ESA_OK;
 }

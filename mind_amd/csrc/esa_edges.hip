@@ -8,6 +8,7 @@
 // segment of n in ascending position (GET/utils/sorted_segment_ops.py:40-41),
 // fp32 accumulation, rounded once.
 #include "esa_common.h"
+#include "esa_profile.h"
 #include "../../include/esa_hip.h"
 
 namespace {
@@ -314,8 +315,9 @@ int launch_segsum(const T* y, long ld, const int* perm1, const int* indptr1, int
                    !misaligned16(out);
   if (vec) {
     const unsigned blocks = grid_for((long)num_nodes, 4, 1L << 18);
-    hipLaunchKernelGGL(segment_sum_kernel<T>, dim3(blocks), dim3(256), 0, st, y, ld, perm1, indptr1, off1, perm2,
-                       indptr2, off2, num_nodes, features, out);
+    ESA_TIMED(esa_profile::kSegmentSum, st,
+              hipLaunchKernelGGL(segment_sum_kernel<T>, dim3(blocks), dim3(256), 0, st, y, ld, perm1, indptr1, off1,
+                                 perm2, indptr2, off2, num_nodes, features, out));
   } else {
     hipLaunchKernelGGL(segment_sum_scalar_kernel<T>, dim3(grid_for((long)num_nodes * features, 256)), dim3(256), 0,
                        st, y, ld, perm1, indptr1, off1, perm2, indptr2, off2, num_nodes, features, out);
@@ -343,9 +345,10 @@ int esa_edge_gather(const void* x, const int* src, const int* dst, int64_t num_e
     int epb = (int)(4096 / (2 * chunks));
     if (epb < 1) epb = 1;
     const long blocks = (num_edges + epb - 1) / epb;
-    hipLaunchKernelGGL(edge_gather_kernel, dim3((unsigned)blocks), dim3(256), 0, st,
-                       static_cast<const u32x4*>(x), src, dst, (long)num_edges, num_nodes, chunks, epb,
-                       static_cast<u32x4*>(out));
+    ESA_TIMED(esa_profile::kEdgeGather, st,
+              hipLaunchKernelGGL(edge_gather_kernel, dim3((unsigned)blocks), dim3(256), 0, st,
+                                 static_cast<const u32x4*>(x), src, dst, (long)num_edges, num_nodes, chunks, epb,
+                                 static_cast<u32x4*>(out)));
   } else if (dtype == ESA_F32) {
     hipLaunchKernelGGL(edge_gather_scalar_kernel<float>, dim3(grid_for(num_edges * 2 * features, 256)), dim3(256), 0,
                        st, static_cast<const float*>(x), src, dst, (long)num_edges, num_nodes, features,
