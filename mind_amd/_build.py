@@ -24,14 +24,17 @@ LIB = LIBDIR / "libesa_hip.so"
 INCLUDE = PKG.parent / "include"
 
 ARCH = "gfx950"
-# Packed fp32 VALU ops are disabled for all device code (see DESIGN.md,
-# "toolchain"); the host pass warns that it does not know the feature.
+# Packed fp32 VALU ops (v_pk_*_f32) are disabled for all device code: some of
+# their forms have given wrong results on the target machines.  The host pass
+# warns that it does not know the feature; that is harmless.
 HIPFLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
     "-std=c++17",
     "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in ordinary VGPRs (no AGPR copies around the softmax).
+    "-mllvm", "-amdgpu-mfma-vgpr-form=true",
     "-fvisibility=hidden",
     f"-I{INCLUDE}",
 ]

@@ -26,10 +26,21 @@
 //   the B operand of the P V product, with no data movement.
 //   O^T = [V^T ; 1] * P^T : rows 0..15 are the output dims, rows 16..31 are
 //   ones, so the MFMA also produces the softmax row sum.  Softmax statistics
-//   stay per lane (one query per lane; the two half-waves exchange one max).
+//   stay per lane (one query per lane).
 //   V^T (and K^T, Q^T, dO^T in backward) is pre-transposed into a
-//   tile-transposed layout [T/8][H][16][8] so each lane's A operand is one
-//   aligned 16-byte load.
+//   tile-transposed layout [T/8][H][rows][8] so each lane's A operand is one
+//   aligned 16-byte load; the forward's V^T carries the ones as rows 16..31.
+//
+// Softmax reference point.  By Cauchy-Schwarz every score of query i obeys
+// c*|S_ij| <= c*|q_i|*max_j|k_j| =: b_i (c = scale*log2 e).  When b_i <= 60 for
+// every query of a wave, exp2(c*S_ij - b_i) lies in [2^-120, 1]: no overflow,
+// no underflow, so softmax(S) = p / sum(p) with the fixed reference b_i is
+// exact up to rounding and needs no running max and no rescaling.  Waves with
+// a larger bound take the online (running-max) path.
+//
+// Loads go through buffer resources with the tensor's byte size as range:
+// the hardware returns 0 for any part of a load past the end, so tiles that
+// run past the last token need no index clamping.
 #include "esa_common.h"
 #include "esa_profile.h"
 #include "../../include/esa_hip.h"
@@ -38,6 +49,16 @@ namespace {
 
 constexpr int kTile = 32;
 constexpr int kHd = 16;
+constexpr float kStaticBound = 60.f;
+
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+DEVI rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+DEVI bf16x8 bload16(rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
 
 DEVI int kperm(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
 
@@ -69,23 +90,10 @@ DEVI void load_nodes16(const int2* __restrict__ nodes, int base, int half, int2 
 
 DEVI int row_token(int base, int r, int half) { return base + 16 * (r >> 3) + 8 * half + (r & 7); }
 
-DEVI bf16x8 splat8(float x) {
-  bf16x8 r;
+DEVI float wave_max(float x) {
 #pragma unroll
-  for (int e = 0; e < 8; ++e) r[e] = (bf16)x;
-  return r;
-}
-
-// A-operand fragment from a tile-transposed [T/8][H][16][8] array: rows are
-// the 16 feature dims (lanes with l%32 >= 16 get `fill`), slots are the 8
-// tokens starting at chunk `chunk`.
-DEVI bf16x8 tt_frag(const bf16* __restrict__ tt, int chunk, int heads, int head, int col, bf16x8 fill) {
-  const bf16x8 v = *reinterpret_cast<const bf16x8*>(tt + ((size_t)(chunk * heads + head) * kHd + (col & 15)) * 8);
-  return col < 16 ? v : fill;
-}
-
-DEVI bf16x8 row_frag(const bf16* __restrict__ x, int token, int heads, int head, int half) {
-  return *reinterpret_cast<const bf16x8*>(x + ((size_t)token * heads + head) * kHd + 8 * half);
+  for (int o = 32; o >= 1; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+  return x;
 }
 
 DEVI void store_rows8(bf16* __restrict__ dst, const f32x16& acc, float mul, int half) {
@@ -99,14 +107,23 @@ DEVI void store_rows8(bf16* __restrict__ dst, const f32x16& acc, float mul, int 
   *reinterpret_cast<bf16x4*>(dst + 8 + 4 * half) = o1;
 }
 
+DEVI bf16x8 cvt8(const float* p) {
+  bf16x8 r;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) r[e] = (bf16)p[e];
+  return r;
+}
+
 struct QOuterArgs {
   const bf16* q; const bf16* k; const bf16* v;
-  const bf16* at;          // forward: V^T (tile-transposed); dQ pass: K^T
+  const bf16* at;          // forward: V^T with ones rows [Tk/8][H][32][8]; dQ pass: K^T [Tk/8][H][16][8]
+  uint32_t at_bytes;
   const bf16* dout;        // dQ pass
-  const float* lse2;       // dQ pass: log2-domain LSE [H][tq_pad], +inf = dead row
+  const float* lse2;       // dQ pass: log2-domain LSE [H][tq_pad], +inf = row without keys
   const float* dvec;       // dQ pass: rowsum(dO * O) [H][tq_pad]
+  const float* knorm;      // forward: max |k| per (head, key tile) [H][tk_tiles]
   const int* cu_q; const int* cu_k; int nseg;
-  int total_q, total_k, heads, tq_pad;
+  int total_q, total_k, heads, tq_pad, tk_tiles;
   float c;                 // softmax_scale * log2(e)
   float scale;
   const int2* nodes; const int4* meta;
@@ -114,6 +131,36 @@ struct QOuterArgs {
   bf16* out; float* lse;   // forward outputs
   bf16* dq;                // dQ pass output
 };
+
+// Per-wave state of a Q-outer pass.
+struct QWave {
+  int col, half, qi, klo, khi, klo_max, khi_min, kt_beg, kt_end;
+  bf16x8 qf;
+  int2 qn;
+  int4 qmeta;
+};
+
+// Score tile S^T for key tile kt (K fragment kf) with out-of-segment /
+// masked entries at -inf.
+template <bool MASKED>
+DEVI f32x16 score_tile(const QOuterArgs& a, const QWave& w, const bf16x8& kf, int kt) {
+  const f32x16 zero = {};
+  f32x16 s = mfma32(kf, w.qf, zero);
+  const int k0 = kt * kTile;
+  const bool full = !MASKED && k0 >= w.klo_max && k0 + kTile <= w.khi_min;
+  if (!full) {
+    int2 kn[16];
+    if (MASKED) load_nodes16(a.nodes, k0, w.half, kn);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int key = row_token(k0, r, w.half);
+      bool ok = key >= w.klo && key < w.khi;
+      if (MASKED) ok = ok && key != w.qi && node_adjacent(kn[r], w.qn);
+      s[r] = ok ? s[r] : -INFINITY;
+    }
+  }
+  return s;
+}
 
 // One wave = one (query tile, head).  DQ=false: forward.  DQ=true: dQ pass.
 template <bool MASKED, bool DQ>
@@ -126,110 +173,135 @@ __global__ __launch_bounds__(256) void attn_qouter_kernel(const QOuterArgs a) {
   const int H = a.heads;
   const int qt = a.plan[item];
   const int q0 = qt * kTile;
-  const int col = lane & 31, half = lane >> 5;
-  const int qi = q0 + col;
-  const bool qvalid = qi < a.total_q;
-  const int qc = qvalid ? qi : a.total_q - 1;
+  QWave w;
+  w.col = lane & 31;
+  w.half = lane >> 5;
+  const int col = w.col, half = w.half;
+  w.qi = q0 + col;
+  const bool qvalid = w.qi < a.total_q;
+  const int qc = qvalid ? w.qi : a.total_q - 1;
   const int q_last = min(q0 + kTile - 1, a.total_q - 1);
   const int seg_first = seg_of(a.cu_q, a.nseg, q0);
   const int seg_last = seg_of(a.cu_q, a.nseg, q_last);
   const int seg = seg_of(a.cu_q, a.nseg, qc);
-  int klo = a.cu_k[seg], khi = a.cu_k[seg + 1];
-  if (!qvalid) { klo = 0; khi = 0; }
+  w.klo = qvalid ? a.cu_k[seg] : 0;
+  w.khi = qvalid ? a.cu_k[seg + 1] : 0;
   const int kbeg = a.cu_k[seg_first], kend = a.cu_k[seg_last + 1];
-  const int klo_max = a.cu_k[seg_last], khi_min = a.cu_k[seg_first + 1];
+  w.klo_max = a.cu_k[seg_last];
+  w.khi_min = a.cu_k[seg_first + 1];
+  w.kt_beg = kbeg >> 5;
+  w.kt_end = (kend + kTile - 1) >> 5;
+  w.qf = *reinterpret_cast<const bf16x8*>(a.q + ((size_t)qc * H + head) * kHd + 8 * half);
+  w.qn = make_int2(0, 0);
+  w.qmeta = make_int4(0, 0, 0, 0);
+  if (MASKED) { w.qn = a.nodes[qc]; w.qmeta = a.meta[qt]; }
 
-  const bf16x8 qf = row_frag(a.q, qc, H, head, half);
-  int2 qn = make_int2(0, 0);
-  int4 qmeta = make_int4(0, 0, 0, 0);
-  if (MASKED) { qn = a.nodes[qc]; qmeta = a.meta[qt]; }
-  bf16x8 dof = splat8(0.f);
-  float lse2q = 0.f, dq_d = 0.f;
-  if (DQ) {
-    dof = row_frag(a.dout, qc, H, head, half);
-    lse2q = a.lse2[(size_t)head * a.tq_pad + qc];
-    dq_d = a.dvec[(size_t)head * a.tq_pad + qc];
-  }
-  const bf16x8 fill = splat8(DQ ? 0.f : 1.f);
-  const f32x16 zero = {};
+  const rsrc_t rk = make_rsrc(a.k, (uint32_t)a.total_k * H * kHd * 2);
+  const rsrc_t ra = make_rsrc(a.at, a.at_bytes);
+  constexpr int ROWS = DQ ? 16 : 32;
+  const uint32_t k_step = (uint32_t)kTile * H * kHd * 2;
+  const uint32_t chunk_bytes = (uint32_t)H * ROWS * 16;
+  uint32_t koff = ((uint32_t)(w.kt_beg * kTile + kperm(col)) * H + head) * (kHd * 2) + 16u * half;
+  uint32_t aoff = ((uint32_t)(w.kt_beg * 4 + half) * H * ROWS + head * ROWS + (DQ ? (col & 15) : col)) * 16u;
+  const uint32_t a_step = 4u * chunk_bytes;
+
   f32x16 acc = {};
-  float m_run = -INFINITY;
-
-  const int kt_beg = kbeg >> 5, kt_end = (kend + kTile - 1) >> 5;
-  for (int kt = kt_beg; kt < kt_end; ++kt) {
-    const int k0 = kt * kTile;
-    if (MASKED) {
-      if (!tiles_may_touch(qmeta, a.meta[kt])) continue;
-    }
-    const int kr = min(k0 + kperm(col), a.total_k - 1);
-    const bf16x8 kf = row_frag(a.k, kr, H, head, half);
-    f32x16 s = mfma32(kf, qf, zero);
-    const bool full = !MASKED && k0 >= klo_max && k0 + kTile <= khi_min;
-    if (!full) {
-      int2 kn[16];
-      if (MASKED) load_nodes16(a.nodes, k0, half, kn);
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = row_token(k0, r, half);
-        bool ok = key >= klo && key < khi;
-        if (MASKED) ok = ok && key != qi && node_adjacent(kn[r], qn);
-        s[r] = ok ? s[r] : -INFINITY;
-      }
-    }
-    if (!DQ) {
-      float mt = s[0];
-#pragma unroll
-      for (int r = 1; r < 16; ++r) mt = fmaxf(mt, s[r]);
-      mt = fmaxf(mt, __shfl_xor(mt, 32));
-      const float m_new = fmaxf(m_run, mt * a.c);
-      const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = fast_exp2(m_run - m_use);
-      m_run = m_new;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[r] *= alpha;
-      bf16x8 p0, p1;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        p0[e] = (bf16)fast_exp2(fmaf(s[e], a.c, -m_use));
-        p1[e] = (bf16)fast_exp2(fmaf(s[8 + e], a.c, -m_use));
-      }
-      const bf16x8 v0 = tt_frag(a.at, (k0 >> 3) + half, H, head, col, fill);
-      const bf16x8 v1 = tt_frag(a.at, (k0 >> 3) + 2 + half, H, head, col, fill);
-      acc = mfma32(v0, p0, acc);
-      acc = mfma32(v1, p1, acc);
-    } else {
-      const bf16x8 vf = row_frag(a.v, kr, H, head, half);
-      const f32x16 dp = mfma32(vf, dof, zero);
-      bf16x8 d0, d1;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float p0 = fast_exp2(fmaf(s[e], a.c, -lse2q));
-        const float p1 = fast_exp2(fmaf(s[8 + e], a.c, -lse2q));
-        d0[e] = (bf16)(p0 * (dp[e] - dq_d));
-        d1[e] = (bf16)(p1 * (dp[8 + e] - dq_d));
-      }
-      const bf16x8 k0f = tt_frag(a.at, (k0 >> 3) + half, H, head, col, fill);
-      const bf16x8 k1f = tt_frag(a.at, (k0 >> 3) + 2 + half, H, head, col, fill);
-      acc = mfma32(k0f, d0, acc);
-      acc = mfma32(k1f, d1, acc);
-    }
-  }
-
-  if (!qvalid) return;
   if (!DQ) {
+    // Reference point b = c |q| max|k| (see the file comment).
+    float qq = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qq = fmaf((float)w.qf[e], (float)w.qf[e], qq);
+    qq += __shfl_xor(qq, 32);
+    float km = 0.f;
+    for (int t = w.kt_beg + lane; t < w.kt_end; t += 64) km = fmaxf(km, a.knorm[(size_t)head * a.tk_tiles + t]);
+    km = wave_max(km);
+    const float b = a.c * sqrtf(qq) * km;
+    const bool fixed_ref = wave_max(qvalid ? b : 0.f) <= kStaticBound;
+    float m_run;
+    if (fixed_ref) {
+      m_run = b;
+      // Loads run one tile ahead (past the end they read zeros, unused).
+      bf16x8 kf = bload16(rk, koff);
+      for (int kt = w.kt_beg; kt < w.kt_end; ++kt) {
+        if (MASKED && !tiles_may_touch(w.qmeta, a.meta[kt])) {
+          koff += k_step; aoff += a_step;
+          kf = bload16(rk, koff);
+          continue;
+        }
+        const bf16x8 v0 = bload16(ra, aoff), v1 = bload16(ra, aoff + 2 * chunk_bytes);
+        const f32x16 s = score_tile<MASKED>(a, w, kf, kt);
+        koff += k_step; aoff += a_step;
+        kf = bload16(rk, koff);
+        float p[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) p[r] = fast_exp2(fmaf(s[r], a.c, -b));
+        acc = mfma32(v0, cvt8(p), acc);
+        acc = mfma32(v1, cvt8(p + 8), acc);
+      }
+    } else {
+      m_run = -INFINITY;
+      for (int kt = w.kt_beg; kt < w.kt_end; ++kt, koff += k_step, aoff += a_step) {
+        if (MASKED && !tiles_may_touch(w.qmeta, a.meta[kt])) continue;
+        const f32x16 s = score_tile<MASKED>(a, w, bload16(rk, koff), kt);
+        float mt = s[0];
+#pragma unroll
+        for (int r = 1; r < 16; ++r) mt = fmaxf(mt, s[r]);
+        mt = fmaxf(mt, __shfl_xor(mt, 32));
+        const float m_new = fmaxf(m_run, mt * a.c);
+        if (__ballot(m_new > m_run)) {
+          const float alpha = fast_exp2(m_run - (m_new == -INFINITY ? 0.f : m_new));
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[r] *= alpha;
+          m_run = m_new;
+        }
+        const float m_use = m_run == -INFINITY ? 0.f : m_run;
+        float p[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) p[r] = fast_exp2(fmaf(s[r], a.c, -m_use));
+        acc = mfma32(bload16(ra, aoff), cvt8(p), acc);
+        acc = mfma32(bload16(ra, aoff + 2 * chunk_bytes), cvt8(p + 8), acc);
+      }
+    }
+    if (!qvalid) return;
     const float l = acc[8];  // a ones row of [V^T; 1] P^T: the softmax row sum
     const float inv = l > 0.f ? 1.f / l : 0.f;
-    store_rows8(a.out + ((size_t)qi * H + head) * kHd, acc, inv, half);
+    store_rows8(a.out + ((size_t)w.qi * H + head) * kHd, acc, inv, half);
     if (half == 0)
-      a.lse[(size_t)head * a.total_q + qi] = l > 0.f ? (m_run + fast_log2(l)) * kLn2 : -INFINITY;
+      a.lse[(size_t)head * a.total_q + w.qi] = l > 0.f ? (m_run + fast_log2(l)) * kLn2 : -INFINITY;
   } else {
-    store_rows8(a.dq + ((size_t)qi * H + head) * kHd, acc, a.scale, half);
+    const bf16x8 dof = *reinterpret_cast<const bf16x8*>(a.dout + ((size_t)qc * H + head) * kHd + 8 * half);
+    const float lse2q = a.lse2[(size_t)head * a.tq_pad + qc];
+    const float dq_d = a.dvec[(size_t)head * a.tq_pad + qc];
+    const rsrc_t rv = make_rsrc(a.v, (uint32_t)a.total_k * H * kHd * 2);
+    const f32x16 zero = {};
+    // Loads run one tile ahead (past the end they read zeros, unused).
+    bf16x8 kf = bload16(rk, koff), vf = bload16(rv, koff);
+    for (int kt = w.kt_beg; kt < w.kt_end; ++kt) {
+      if (MASKED && !tiles_may_touch(w.qmeta, a.meta[kt])) {
+        koff += k_step; aoff += a_step;
+        kf = bload16(rk, koff); vf = bload16(rv, koff);
+        continue;
+      }
+      const bf16x8 t0 = bload16(ra, aoff), t1 = bload16(ra, aoff + 2 * chunk_bytes);
+      const f32x16 s = score_tile<MASKED>(a, w, kf, kt);
+      const f32x16 dp = mfma32(vf, dof, zero);   // dP^T = V dO^T (V rows in K's order)
+      koff += k_step; aoff += a_step;
+      kf = bload16(rk, koff); vf = bload16(rv, koff);
+      float ds[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) ds[r] = fast_exp2(fmaf(s[r], a.c, -lse2q)) * (dp[r] - dq_d);
+      acc = mfma32(t0, cvt8(ds), acc);
+      acc = mfma32(t1, cvt8(ds + 8), acc);
+    }
+    if (!qvalid) return;
+    store_rows8(a.dq + ((size_t)w.qi * H + head) * kHd, acc, a.scale, half);
   }
 }
 
 struct KOuterArgs {
   const bf16* q; const bf16* k; const bf16* v; const bf16* dout;
-  const bf16* qt; const bf16* dot;   // tile-transposed Q and dO
+  const bf16* qt; const bf16* dot;   // tile-transposed Q and dO [Tq/8][H][16][8]
+  uint32_t tt_bytes;
   const float* lse2; const float* dvec;
   const int* cu_q; const int* cu_k; int nseg;
   int total_q, total_k, heads, tq_pad;
@@ -259,40 +331,50 @@ __global__ __launch_bounds__(256) void attn_kouter_kernel(const KOuterArgs a) {
   const int seg_first = seg_of(a.cu_k, a.nseg, k0);
   const int seg_last = seg_of(a.cu_k, a.nseg, k_last);
   const int seg = seg_of(a.cu_k, a.nseg, kc);
-  int qlo = a.cu_q[seg], qhi = a.cu_q[seg + 1];
-  if (!kvalid) { qlo = 0; qhi = 0; }
+  const int qlo = kvalid ? a.cu_q[seg] : 0, qhi = kvalid ? a.cu_q[seg + 1] : 0;
   const int qbeg = a.cu_q[seg_first], qend = a.cu_q[seg_last + 1];
   const int qlo_max = a.cu_q[seg_last], qhi_min = a.cu_q[seg_first + 1];
 
-  const bf16x8 kf = row_frag(a.k, kc, H, head, half);
-  const bf16x8 vf = row_frag(a.v, kc, H, head, half);
+  const bf16x8 kf = *reinterpret_cast<const bf16x8*>(a.k + ((size_t)kc * H + head) * kHd + 8 * half);
+  const bf16x8 vf = *reinterpret_cast<const bf16x8*>(a.v + ((size_t)kc * H + head) * kHd + 8 * half);
   int2 kn = make_int2(0, 0);
   int4 kmeta = make_int4(0, 0, 0, 0);
   if (MASKED) { kn = a.nodes[kc]; kmeta = a.meta[kt]; }
-  const bf16x8 zfill = splat8(0.f);
   const f32x16 zero = {};
   f32x16 dva = {}, dka = {};
-  const float* lse2h = a.lse2 + (size_t)head * a.tq_pad;
-  const float* dvech = a.dvec + (size_t)head * a.tq_pad;
+  const float* lse2h = a.lse2 + (size_t)head * a.tq_pad + 8 * half;
+  const float* dvech = a.dvec + (size_t)head * a.tq_pad + 8 * half;
 
+  const rsrc_t rq = make_rsrc(a.q, (uint32_t)a.total_q * H * kHd * 2);
+  const rsrc_t rdo = make_rsrc(a.dout, (uint32_t)a.total_q * H * kHd * 2);
+  const rsrc_t rqt = make_rsrc(a.qt, a.tt_bytes);
+  const rsrc_t rdot = make_rsrc(a.dot, a.tt_bytes);
   const int qt_beg = qbeg >> 5, qt_end = (qend + kTile - 1) >> 5;
+  const uint32_t q_step = (uint32_t)kTile * H * kHd * 2;
+  const uint32_t chunk_bytes = (uint32_t)H * 16 * 16;
+  uint32_t qoff = ((uint32_t)(qt_beg * kTile + kperm(col)) * H + head) * (kHd * 2) + 16u * half;
+  uint32_t toff = ((uint32_t)(qt_beg * 4 + half) * H * 16 + head * 16 + (col & 15)) * 16u;
+
+  // Row fragments run one tile ahead (past the end they read zeros, unused).
+  bf16x8 qa = bload16(rq, qoff), da = bload16(rdo, qoff);
   for (int qt = qt_beg; qt < qt_end; ++qt) {
     const int q0 = qt * kTile;
-    if (MASKED) {
-      if (!tiles_may_touch(a.meta[qt], kmeta)) continue;
+    if (MASKED && !tiles_may_touch(a.meta[qt], kmeta)) {
+      qoff += q_step; toff += 4 * chunk_bytes;
+      qa = bload16(rq, qoff); da = bload16(rdo, qoff);
+      continue;
     }
-    const int qr = min(q0 + kperm(col), a.total_q - 1);
-    const bf16x8 qfa = row_frag(a.q, qr, H, head, half);
-    const f32x16 s = mfma32(qfa, kf, zero);
-    const bf16x8 dofa = row_frag(a.dout, qr, H, head, half);
-    const f32x16 dp = mfma32(dofa, vf, zero);
+    const bf16x8 o0 = bload16(rdot, toff), o1 = bload16(rdot, toff + 2 * chunk_bytes);
+    const bf16x8 t0 = bload16(rqt, toff), t1 = bload16(rqt, toff + 2 * chunk_bytes);
+    const f32x16 s = mfma32(qa, kf, zero);     // S = Q K^T, lane = key
+    const f32x16 dp = mfma32(da, vf, zero);    // dP = dO V^T
+    qoff += q_step; toff += 4 * chunk_bytes;
+    qa = bload16(rq, qoff); da = bload16(rdo, qoff);
     // Per-row (query) statistics: rows r -> q0 + 16(r>>3) + 8h + (r&7).
-    const f32x4* l2p0 = reinterpret_cast<const f32x4*>(lse2h + q0 + 8 * half);
-    const f32x4* l2p1 = reinterpret_cast<const f32x4*>(lse2h + q0 + 16 + 8 * half);
-    const f32x4* dvp0 = reinterpret_cast<const f32x4*>(dvech + q0 + 8 * half);
-    const f32x4* dvp1 = reinterpret_cast<const f32x4*>(dvech + q0 + 16 + 8 * half);
-    const f32x4 la = l2p0[0], lb = l2p0[1], lc = l2p1[0], ld = l2p1[1];
-    const f32x4 da = dvp0[0], db = dvp0[1], dc = dvp1[0], dd = dvp1[1];
+    const f32x4* l2p = reinterpret_cast<const f32x4*>(lse2h + q0);
+    const f32x4* dvp = reinterpret_cast<const f32x4*>(dvech + q0);
+    const f32x4 la = l2p[0], lb = l2p[1], lc = l2p[4], ld = l2p[5];
+    const f32x4 da = dvp[0], db = dvp[1], dc = dvp[4], dd = dvp[5];
     float l2[16], dr[16];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -314,51 +396,77 @@ __global__ __launch_bounds__(256) void attn_kouter_kernel(const KOuterArgs a) {
         p[r] = ok ? p[r] : 0.f;
       }
     }
-    bf16x8 p0, p1, s0, s1;
+    float ds[16];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      p0[e] = (bf16)p[e];
-      p1[e] = (bf16)p[8 + e];
-      s0[e] = (bf16)(p[e] * (dp[e] - dr[e]));
-      s1[e] = (bf16)(p[8 + e] * (dp[8 + e] - dr[8 + e]));
-    }
-    const int ch = (q0 >> 3) + half;
-    dva = mfma32(tt_frag(a.dot, ch, H, head, col, zfill), p0, dva);
-    dva = mfma32(tt_frag(a.dot, ch + 2, H, head, col, zfill), p1, dva);
-    dka = mfma32(tt_frag(a.qt, ch, H, head, col, zfill), s0, dka);
-    dka = mfma32(tt_frag(a.qt, ch + 2, H, head, col, zfill), s1, dka);
+    for (int r = 0; r < 16; ++r) ds[r] = p[r] * (dp[r] - dr[r]);
+    dva = mfma32(o0, cvt8(p), dva);
+    dva = mfma32(o1, cvt8(p + 8), dva);
+    dka = mfma32(t0, cvt8(ds), dka);
+    dka = mfma32(t1, cvt8(ds + 8), dka);
   }
   if (!kvalid) return;
   store_rows8(a.dv + ((size_t)ki * H + head) * kHd, dva, 1.f, half);
   store_rows8(a.dk + ((size_t)ki * H + head) * kHd, dka, a.scale, half);
 }
 
-// x [total][H][16] -> xt [tpad/8][H][16][8], zero beyond `total`.
-__global__ void tt_transpose_kernel(const bf16* __restrict__ x, int total, int heads, int tpad,
-                                    bf16* __restrict__ xt) {
-  const long n = (long)(tpad / 8) * heads * kHd;
-  const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= n) return;
-  const int d = (int)(idx % kHd);
-  const int h = (int)((idx / kHd) % heads);
-  const int c = (int)(idx / ((long)kHd * heads));
-  bf16x8 r;
+// ------------------------------------------------------------------ prep kernels
+
+// One block per 32-token tile of x [total][H][16].
+//  - xt != null: writes the tile-transposed layout [T/8][H][rows][8] for the
+//    tile's four 8-token chunks: rows 0..15 are x's feature dims (zero past
+//    `total`); rows 16..31 (rows == 32) are ones.
+//  - knorm != null: writes max over the tile's tokens of |x_t| per head to
+//    knorm[h * n_tiles + tile].
+__global__ __launch_bounds__(256) void tile_transpose_kernel(const bf16* __restrict__ x, int total, int heads,
+                                                             int rows, bf16* __restrict__ xt,
+                                                             float* __restrict__ knorm, int n_tiles) {
+  const int tile = blockIdx.x;
+  const int t0 = tile * kTile;
+  if (xt) {
+    const int items = 4 * heads * rows;
+    for (int it = threadIdx.x; it < items; it += blockDim.x) {
+      const int r = it % rows;
+      const int h = (it / rows) % heads;
+      const int c = it / (rows * heads);
+      bf16x8 o;
+      if (r < kHd) {
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int t = c * 8 + i;
-    r[i] = t < total ? x[((size_t)t * heads + h) * kHd + d] : (bf16)0.f;
+        for (int i = 0; i < 8; ++i) {
+          const int t = t0 + c * 8 + i;
+          o[i] = t < total ? x[((size_t)t * heads + h) * kHd + r] : (bf16)0.f;
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[i] = (bf16)1.f;
+      }
+      *reinterpret_cast<bf16x8*>(xt + (((size_t)(tile * 4 + c) * heads + h) * rows + r) * 8) = o;
+    }
   }
-  *reinterpret_cast<bf16x8*>(xt + idx * 8) = r;
+  if (knorm) {
+    // one thread per head: max over the tile's tokens of the squared norm
+    for (int h = threadIdx.x; h < heads; h += blockDim.x) {
+      float m = 0.f;
+      for (int i = 0; i < kTile && t0 + i < total; ++i) {
+        const bf16x8* p = reinterpret_cast<const bf16x8*>(x + ((size_t)(t0 + i) * heads + h) * kHd);
+        const bf16x8 u = p[0], v = p[1];
+        float s = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s = fmaf((float)u[e], (float)u[e], fmaf((float)v[e], (float)v[e], s));
+        m = fmaxf(m, s);
+      }
+      knorm[(size_t)h * n_tiles + tile] = sqrtf(m);
+    }
+  }
 }
 
 // lse2 = lse * log2(e) (+inf for rows with no admissible key, and padding),
-// dvec = rowsum(dO * O) in fp32.
-__global__ void bwd_prep_kernel(const bf16* __restrict__ dout, const bf16* __restrict__ out,
-                                const float* __restrict__ lse, int total_q, int heads, int tq_pad,
-                                float* __restrict__ lse2, float* __restrict__ dvec) {
+// dvec = rowsum(dO * O) in fp32.  Thread per (token, head), head fastest.
+__global__ void bwd_rowstats_kernel(const bf16* __restrict__ dout, const bf16* __restrict__ out,
+                                    const float* __restrict__ lse, int total_q, int heads, int tq_pad,
+                                    float* __restrict__ lse2, float* __restrict__ dvec) {
   const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= (long)heads * tq_pad) return;
-  const int h = (int)(idx / tq_pad), t = (int)(idx % tq_pad);
+  const int h = (int)(idx % heads), t = (int)(idx / heads);
   float l2 = INFINITY, dsum = 0.f;
   if (t < total_q) {
     const float l = lse[(size_t)h * total_q + t];
@@ -372,8 +480,8 @@ __global__ void bwd_prep_kernel(const bf16* __restrict__ dout, const bf16* __res
       for (int e = 0; e < 8; ++e) dsum = fmaf((float)o[e], (float)g[e], dsum);
     }
   }
-  lse2[idx] = l2;
-  dvec[idx] = dsum;
+  lse2[(size_t)h * tq_pad + t] = l2;
+  dvec[(size_t)h * tq_pad + t] = dsum;
 }
 
 __global__ void nodes_pack_kernel(const int* __restrict__ src, const int* __restrict__ dst, int total,
@@ -403,14 +511,14 @@ __global__ void tile_meta_kernel(const int2* __restrict__ nodes, int total, int 
 }
 
 // Longest-first order of the outer tiles by the number of inner tiles they
-// visit (counting sort, one block).
+// visit (counting sort in one block; parallel scan of the bucket counts).
 __global__ __launch_bounds__(1024) void plan_kernel(const int* __restrict__ cu_outer,
                                                     const int* __restrict__ cu_inner, int nseg,
                                                     int total_outer, int n_tiles, int* __restrict__ plan) {
   constexpr int NB = 1024;
   __shared__ int hist[NB];
   const int tid = threadIdx.x;
-  for (int i = tid; i < NB; i += blockDim.x) hist[i] = 0;
+  hist[tid] = 0;
   __syncthreads();
   auto bucket = [&](int t) {
     const int o0 = t * kTile, o1 = min(o0 + kTile - 1, total_outer - 1);
@@ -419,14 +527,19 @@ __global__ __launch_bounds__(1024) void plan_kernel(const int* __restrict__ cu_o
     const int cost = ie > ib ? ((ie + kTile - 1) >> 5) - (ib >> 5) : 0;
     return NB - 1 - min(cost, NB - 1);
   };
-  for (int t = tid; t < n_tiles; t += blockDim.x) atomicAdd(&hist[bucket(t)], 1);
+  for (int t = tid; t < n_tiles; t += NB) atomicAdd(&hist[bucket(t)], 1);
   __syncthreads();
-  if (tid == 0) {
-    int run = 0;
-    for (int i = 0; i < NB; ++i) { const int h = hist[i]; hist[i] = run; run += h; }
+  // inclusive Hillis-Steele scan over the buckets, then shift to exclusive
+  const int own = hist[tid];
+  for (int off = 1; off < NB; off <<= 1) {
+    const int add = tid >= off ? hist[tid - off] : 0;
+    __syncthreads();
+    hist[tid] += add;
+    __syncthreads();
   }
+  hist[tid] -= own;
   __syncthreads();
-  for (int t = tid; t < n_tiles; t += blockDim.x) plan[atomicAdd(&hist[bucket(t)], 1)] = t;
+  for (int t = tid; t < n_tiles; t += NB) plan[atomicAdd(&hist[bucket(t)], 1)] = t;
 }
 
 __global__ void edge_mask_dense_kernel(const int* __restrict__ src, const int* __restrict__ dst,
@@ -441,11 +554,16 @@ __global__ void edge_mask_dense_kernel(const int* __restrict__ src, const int* _
   const int start = cu[b], len = cu[b + 1] - start;
   uint8_t m = 0;
   if (i < len && j < len && i != j) {
-    const int2 a = make_int2(src[start + i], dst[start + i]);
-    const int2 c = make_int2(src[start + j], dst[start + j]);
-    m = node_adjacent(a, c) ? 1 : 0;
+    const int2 x = make_int2(src[start + i], dst[start + i]);
+    const int2 y = make_int2(src[start + j], dst[start + j]);
+    m = node_adjacent(x, y) ? 1 : 0;
   }
   mask[idx] = m;
+}
+
+__global__ void zero16_kernel(uint4* __restrict__ p, long n) {
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x)
+    p[i] = make_uint4(0u, 0u, 0u, 0u);
 }
 
 // ---------------------------------------------------------------- host side
@@ -454,21 +572,25 @@ size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 int round32(int x) { return (x + kTile - 1) / kTile * kTile; }
 
 struct WsLayout {
-  size_t vt = 0, qt = 0, kt = 0, dot = 0, lse2 = 0, dvec = 0, plan_q = 0, plan_k = 0,
+  size_t vt = 0, knorm = 0, qt = 0, kt = 0, dot = 0, lse2 = 0, dvec = 0, plan_q = 0, plan_k = 0,
          nodes = 0, meta = 0, total = 0;
+  size_t vt_bytes = 0, tt_q_bytes = 0, tt_k_bytes = 0;
 };
 
 WsLayout ws_layout(int total_q, int total_k, int heads, bool masked, bool backward) {
   WsLayout L;
   const int tqp = round32(total_q), tkp = round32(total_k);
-  const size_t ttq = (size_t)tqp * heads * kHd * 2, ttk = (size_t)tkp * heads * kHd * 2;
   size_t off = 0;
   if (!backward) {
-    L.vt = off; off += align256(ttk);
+    L.vt_bytes = (size_t)tkp * heads * 32 * 2;
+    L.vt = off; off += align256(L.vt_bytes);
+    L.knorm = off; off += align256((size_t)heads * (tkp / kTile) * 4);
   } else {
-    L.qt = off; off += align256(ttq);
-    L.kt = off; off += align256(ttk);
-    L.dot = off; off += align256(ttq);
+    L.tt_q_bytes = (size_t)tqp * heads * kHd * 2;
+    L.tt_k_bytes = (size_t)tkp * heads * kHd * 2;
+    L.qt = off; off += align256(L.tt_q_bytes);
+    L.kt = off; off += align256(L.tt_k_bytes);
+    L.dot = off; off += align256(L.tt_q_bytes);
     L.lse2 = off; off += align256((size_t)heads * tqp * 4);
     L.dvec = off; off += align256((size_t)heads * tqp * 4);
   }
@@ -487,14 +609,11 @@ bool misaligned(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) !
 int check_common(int batch, int total_q, int total_k, int heads, int head_dim, bool masked) {
   if (head_dim != kHd) return ESA_ERR_HEAD_DIM;
   if (batch < 1 || heads < 1 || total_q < 0 || total_k < 0) return ESA_ERR_SHAPE;
-  if ((long)total_q * heads * kHd >= (1L << 31) || (long)total_k * heads * kHd >= (1L << 31)) return ESA_ERR_SHAPE;
+  // Buffer-resource ranges are 32-bit byte counts; the forward's V^T has 32 rows per head.
+  const long lim = (1L << 31) - 1;
+  if ((long)round32(total_q) * heads * 64 > lim || (long)round32(total_k) * heads * 64 > lim) return ESA_ERR_SHAPE;
   if (masked && total_q != total_k) return ESA_ERR_MASK;
   return ESA_OK;
-}
-
-__global__ void zero16_kernel(uint4* __restrict__ p, long n) {
-  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x)
-    p[i] = make_uint4(0u, 0u, 0u, 0u);
 }
 
 // Zero `bytes` (a multiple of 16) at a 16-byte aligned pointer.
@@ -508,13 +627,12 @@ int launch_zero(void* p, size_t bytes, hipStream_t st) {
   return ESA_OK;
 }
 
-int launch_tt(const bf16* x, int total, int heads, bf16* xt, hipStream_t st) {
-  const int tp = round32(total);
-  const long n = (long)(tp / 8) * heads * kHd;
-  if (n == 0) return ESA_OK;
+int launch_tt(const bf16* x, int total, int heads, int rows, bf16* xt, float* knorm, hipStream_t st) {
+  const int nt = round32(total) / kTile;
+  if (nt == 0) return ESA_OK;
   ESA_TIMED(esa_profile::kAttnPrep, st,
-            hipLaunchKernelGGL(tt_transpose_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x, total,
-                               heads, tp, xt));
+            hipLaunchKernelGGL(tile_transpose_kernel, dim3((unsigned)nt), dim3(256), 0, st, x, total, heads, rows,
+                               xt, knorm, nt));
   ESA_LAUNCH_CHECK();
   return ESA_OK;
 }
@@ -546,7 +664,7 @@ int launch_plan(const int* cu_outer, const int* cu_inner, int nseg, int total_ou
 
 extern "C" {
 
-const char* esa_version(void) { return "esa_hip 0.1 gfx950"; }
+const char* esa_version(void) { return "esa_hip 0.2 gfx950"; }
 
 int esa_varlen_attn_workspace_size(int total_q, int total_k, int heads, int head_dim, int masked,
                                    int backward, size_t* bytes) {
@@ -570,6 +688,7 @@ int esa_varlen_attn_fwd(const void* q, const void* k, const void* v, const int* 
   if (total_q == 0) return ESA_OK;
   if (!q || !k || !v || !cu_seqlens_q || !cu_seqlens_k || !out || !softmax_lse || !workspace) return ESA_ERR_NULL;
   if (misaligned(q) || misaligned(k) || misaligned(v) || misaligned(out) || misaligned(workspace)) return ESA_ERR_ALIGN;
+  if (!(softmax_scale > 0.f)) return ESA_ERR_SHAPE;
   const WsLayout L = ws_layout(total_q, total_k, heads, masked, false);
   if (workspace_bytes < L.total) return ESA_ERR_WORKSPACE;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
@@ -578,14 +697,18 @@ int esa_varlen_attn_fwd(const void* q, const void* k, const void* v, const int* 
   QOuterArgs a{};
   a.q = static_cast<const bf16*>(q); a.k = static_cast<const bf16*>(k); a.v = static_cast<const bf16*>(v);
   a.at = reinterpret_cast<const bf16*>(ws + L.vt);
+  a.at_bytes = (uint32_t)L.vt_bytes;
+  a.knorm = reinterpret_cast<const float*>(ws + L.knorm);
   a.cu_q = cu_seqlens_q; a.cu_k = cu_seqlens_k; a.nseg = batch;
   a.total_q = total_q; a.total_k = total_k; a.heads = heads; a.tq_pad = round32(total_q);
+  a.tk_tiles = round32(total_k) / kTile;
   a.scale = softmax_scale; a.c = softmax_scale * kLog2e;
   a.plan = reinterpret_cast<const int*>(ws + L.plan_q);
   a.n_tiles = round32(total_q) / kTile;
   a.out = static_cast<bf16*>(out); a.lse = softmax_lse;
   if (total_k > 0) {
-    if ((rc = launch_tt(a.v, total_k, heads, reinterpret_cast<bf16*>(ws + L.vt), st))) return rc;
+    if ((rc = launch_tt(a.v, total_k, heads, 32, reinterpret_cast<bf16*>(ws + L.vt), nullptr, st))) return rc;
+    if ((rc = launch_tt(a.k, total_k, heads, 0, nullptr, reinterpret_cast<float*>(ws + L.knorm), st))) return rc;
   }
   if (masked) {
     a.nodes = reinterpret_cast<const int2*>(ws + L.nodes);
@@ -616,12 +739,14 @@ int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k, const vo
   if (masked && (!tok_src || !tok_dst)) return ESA_ERR_NULL;
   int rc = check_common(batch, total_q, total_k, heads, head_dim, masked);
   if (rc) return rc;
+  if (total_q == 0 && total_k == 0) return ESA_OK;
   if (!dout || !q || !k || !v || !out || !softmax_lse || !cu_seqlens_q || !cu_seqlens_k || !dq || !dk ||
       !dv || !workspace)
     return ESA_ERR_NULL;
   if (misaligned(dout) || misaligned(q) || misaligned(k) || misaligned(v) || misaligned(out) ||
       misaligned(dq) || misaligned(dk) || misaligned(dv) || misaligned(workspace))
     return ESA_ERR_ALIGN;
+  if (!(softmax_scale > 0.f)) return ESA_ERR_SHAPE;
   const WsLayout L = ws_layout(total_q, total_k, heads, masked, true);
   if (workspace_bytes < L.total) return ESA_ERR_WORKSPACE;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
@@ -642,13 +767,13 @@ int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k, const vo
   float* dvec = reinterpret_cast<float*>(ws + L.dvec);
   int* plan_q = reinterpret_cast<int*>(ws + L.plan_q);
   int* plan_k = reinterpret_cast<int*>(ws + L.plan_k);
-  if ((rc = launch_tt(static_cast<const bf16*>(q), total_q, heads, qt, st))) return rc;
-  if ((rc = launch_tt(static_cast<const bf16*>(k), total_k, heads, ktt, st))) return rc;
-  if ((rc = launch_tt(static_cast<const bf16*>(dout), total_q, heads, dot, st))) return rc;
+  if ((rc = launch_tt(static_cast<const bf16*>(q), total_q, heads, 16, qt, nullptr, st))) return rc;
+  if ((rc = launch_tt(static_cast<const bf16*>(k), total_k, heads, 16, ktt, nullptr, st))) return rc;
+  if ((rc = launch_tt(static_cast<const bf16*>(dout), total_q, heads, 16, dot, nullptr, st))) return rc;
   {
     const long n = (long)heads * tqp;
     ESA_TIMED(esa_profile::kAttnPrep, st,
-              hipLaunchKernelGGL(bwd_prep_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+              hipLaunchKernelGGL(bwd_rowstats_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
                                  static_cast<const bf16*>(dout), static_cast<const bf16*>(out), softmax_lse,
                                  total_q, heads, tqp, lse2, dvec));
     ESA_LAUNCH_CHECK();
@@ -668,7 +793,8 @@ int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k, const vo
 
   KOuterArgs ka{};
   ka.q = static_cast<const bf16*>(q); ka.k = static_cast<const bf16*>(k); ka.v = static_cast<const bf16*>(v);
-  ka.dout = static_cast<const bf16*>(dout); ka.qt = qt; ka.dot = dot; ka.lse2 = lse2; ka.dvec = dvec;
+  ka.dout = static_cast<const bf16*>(dout); ka.qt = qt; ka.dot = dot; ka.tt_bytes = (uint32_t)L.tt_q_bytes;
+  ka.lse2 = lse2; ka.dvec = dvec;
   ka.cu_q = cu_seqlens_q; ka.cu_k = cu_seqlens_k; ka.nseg = batch;
   ka.total_q = total_q; ka.total_k = total_k; ka.heads = heads; ka.tq_pad = tqp;
   ka.c = c; ka.scale = softmax_scale; ka.nodes = nodes; ka.meta = meta;
@@ -684,9 +810,11 @@ int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k, const vo
   ESA_LAUNCH_CHECK();
 
   QOuterArgs qa{};
-  qa.q = ka.q; qa.k = ka.k; qa.v = ka.v; qa.at = ktt; qa.dout = ka.dout; qa.lse2 = lse2; qa.dvec = dvec;
+  qa.q = ka.q; qa.k = ka.k; qa.v = ka.v; qa.at = ktt; qa.at_bytes = (uint32_t)L.tt_k_bytes;
+  qa.dout = ka.dout; qa.lse2 = lse2; qa.dvec = dvec;
   qa.cu_q = cu_seqlens_q; qa.cu_k = cu_seqlens_k; qa.nseg = batch;
   qa.total_q = total_q; qa.total_k = total_k; qa.heads = heads; qa.tq_pad = tqp;
+  qa.tk_tiles = round32(total_k) / kTile;
   qa.c = c; qa.scale = softmax_scale; qa.nodes = nodes; qa.meta = meta;
   qa.plan = plan_q; qa.n_tiles = tqp / kTile; qa.dq = static_cast<bf16*>(dq);
   const unsigned qgrid = (unsigned)qa.n_tiles * groups;

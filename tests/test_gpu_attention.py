@@ -59,8 +59,8 @@ def _check(device, lengths_q, lengths_k, seed, src=None, dst=None, heads=H, chec
         if fin.any():
             # The kernel's row sum is an MFMA over the bf16-rounded probabilities
             # (the same values that weight V), so the sum carries at most the
-            # bf16 rounding 2^-9 relative: |d lse| <= ln(1 + 2^-9) = 1.95e-3.
-            assert float((lse[fin] - lse_ref[fin]).abs().max()) < 2.0e-3
+            # bf16 unit roundoff 2^-8 relative: |d lse| <= ln(1 + 2^-8) = 3.9e-3.
+            assert float((lse[fin] - lse_ref[fin]).abs().max()) < 3.9e-3
     rdq, rdk, rdv = OA.varlen_attention_bwd(g, q, k, v, cu_q, cu_k, 0.25, src, dst)
     assert_bf16_close(dq, rdq, grad_scale(rdq), "dq")
     assert_bf16_close(dk, rdk, grad_scale(rdk), "dk")
