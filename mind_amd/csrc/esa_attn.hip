@@ -12,11 +12,15 @@
 // 217-268) and memory_efficient_attention applies (esa/mha.py:73-77).
 //
 // Tiling.  Tokens are cut into 32-token tiles aligned to the global token
-// index, so every vector load is aligned; a tile may straddle segments, which
-// the per-element validity test (key in the query's segment) resolves.  One
-// wave computes one (32-token tile, head) pair; a 256-thread block holds four
-// heads of the same tile.  Tiles are dispatched longest-first (a per-call
-// plan kernel sorts them by the number of partner tiles).
+// index; a tile may straddle segments, which the per-element validity test
+// (partner token in the lane's segment) resolves.  A 256-thread block is
+// four waves of ONE head working on four consecutive tiles (a 128-token
+// group); every partner tile the group needs is loaded from HBM/L2 once per
+// block into double-buffered LDS and read by all four waves, transposed on
+// the way in where an MFMA operand wants the token dimension contiguous.
+// Groups are dispatched longest-first (a per-call plan kernel sorts them by
+// the number of partner tiles); consecutive blocks are different heads, so
+// all blocks of a head land on the same XCD and share its L2.
 //
 // Register layout (head_dim = 16 = the MFMA K of 32x32x16):
 //   S^T = K_tile * Q_tile^T : lane l owns query column l%32; its 16 fp32
@@ -27,9 +31,10 @@
 //   O^T = [V^T ; 1] * P^T : rows 0..15 are the output dims, rows 16..31 are
 //   ones, so the MFMA also produces the softmax row sum.  Softmax statistics
 //   stay per lane (one query per lane).
-//   V^T (and K^T, Q^T, dO^T in backward) is pre-transposed into a
-//   tile-transposed layout [T/8][H][rows][8] so each lane's A operand is one
-//   aligned 16-byte load; the forward's V^T carries the ones as rows 16..31.
+//   The dK/dV pass keeps keys on lanes; per-query row statistics (LSE, D)
+//   enter through an extra MFMA whose A operand carries (hi, lo) bf16 halves
+//   of -LSE/c and -D per row and whose B operand is a column of ones: it
+//   broadcasts each row's value across the lanes in fp32 at no VALU cost.
 //
 // Softmax reference point.  By Cauchy-Schwarz every score of query i obeys
 // c*|S_ij| <= c*|q_i|*max_j|k_j| =: b_i (c = scale*log2 e).  When b_i <= 60 for
@@ -38,9 +43,11 @@
 // exact up to rounding and needs no running max and no rescaling.  Waves with
 // a larger bound take the online (running-max) path.
 //
-// Loads go through buffer resources with the tensor's byte size as range:
-// the hardware returns 0 for any part of a load past the end, so tiles that
-// run past the last token need no index clamping.
+// Global loads go through buffer resources with the tensor's byte size as
+// range: the hardware returns 0 for any part of a load past the end, so tiles
+// that run past the last token need no index clamping.
+#include <type_traits>
+
 #include "esa_common.h"
 #include "esa_profile.h"
 #include "../../include/esa_hip.h"
@@ -49,16 +56,21 @@ namespace {
 
 constexpr int kTile = 32;
 constexpr int kHd = 16;
+constexpr int kWaves = 4;
+constexpr int kGroupTok = kWaves * kTile;   // 128 tokens per block
+constexpr int kRowStride = 24;              // bf16 per row of a [32 tokens][16] LDS tile (48 B)
+constexpr int kTrStride = 40;               // bf16 per row of a [rows][32 tokens] LDS tile (80 B)
 constexpr float kStaticBound = 60.f;
+constexpr float kDeadRow = -1.0e30f;        // -LSE/c for rows without keys: every exp2 underflows to 0
 
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
+typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 DEVI rsrc_t make_rsrc(const void* p, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
 }
-DEVI bf16x8 bload16(rsrc_t r, uint32_t off) {
-  return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
-}
+DEVI i32x4 bload(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0); }
+DEVI bf16x8 as_bf16x8(i32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
 DEVI int kperm(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
 
@@ -72,23 +84,7 @@ DEVI bool tiles_may_touch(int4 a, int4 b) {
   if (a.y < b.x || b.y < a.x) return false;
   return ((a.z & b.z) | (a.w & b.w)) != 0;
 }
-
-// Node pairs of the 16 tokens a half-wave's accumulator rows refer to:
-// tokens base + 8h + 0..7 and base + 16 + 8h + 0..7.
-DEVI void load_nodes16(const int2* __restrict__ nodes, int base, int half, int2 out[16]) {
-  const int4* p0 = reinterpret_cast<const int4*>(nodes + base + 8 * half);
-  const int4* p1 = reinterpret_cast<const int4*>(nodes + base + 16 + 8 * half);
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    int4 a = p0[j], b = p1[j];
-    out[2 * j] = make_int2(a.x, a.y);
-    out[2 * j + 1] = make_int2(a.z, a.w);
-    out[8 + 2 * j] = make_int2(b.x, b.y);
-    out[8 + 2 * j + 1] = make_int2(b.z, b.w);
-  }
-}
-
-DEVI int row_token(int base, int r, int half) { return base + 16 * (r >> 3) + 8 * half + (r & 7); }
+DEVI int4 no_touch() { return make_int4(INT_MAX, INT_MIN, 0, 0); }
 
 DEVI float wave_max(float x) {
 #pragma unroll
@@ -114,363 +110,504 @@ DEVI bf16x8 cvt8(const float* p) {
   return r;
 }
 
-struct QOuterArgs {
-  const bf16* q; const bf16* k; const bf16* v;
-  const bf16* at;          // forward: V^T with ones rows [Tk/8][H][32][8]; dQ pass: K^T [Tk/8][H][16][8]
-  uint32_t at_bytes;
-  const bf16* dout;        // dQ pass
-  const float* lse2;       // dQ pass: log2-domain LSE [H][tq_pad], +inf = row without keys
-  const float* dvec;       // dQ pass: rowsum(dO * O) [H][tq_pad]
-  const float* knorm;      // forward: max |k| per (head, key tile) [H][tk_tiles]
-  const int* cu_q; const int* cu_k; int nseg;
-  int total_q, total_k, heads, tq_pad, tk_tiles;
-  float c;                 // softmax_scale * log2(e)
-  float scale;
-  const int2* nodes; const int4* meta;
-  const int* plan; int n_tiles;
-  bf16* out; float* lse;   // forward outputs
-  bf16* dq;                // dQ pass output
-};
+DEVI bf16x8 lds8(const bf16* p) { return *reinterpret_cast<const bf16x8*>(p); }
 
-// Per-wave state of a Q-outer pass.
-struct QWave {
-  int col, half, qi, klo, khi, klo_max, khi_min, kt_beg, kt_end;
-  bf16x8 qf;
-  int2 qn;
-  int4 qmeta;
-};
-
-// Score tile S^T for key tile kt (K fragment kf) with out-of-segment /
-// masked entries at -inf.
-template <bool MASKED>
-DEVI f32x16 score_tile(const QOuterArgs& a, const QWave& w, const bf16x8& kf, int kt) {
-  const f32x16 zero = {};
-  f32x16 s = mfma32(kf, w.qf, zero);
-  const int k0 = kt * kTile;
-  const bool full = !MASKED && k0 >= w.klo_max && k0 + kTile <= w.khi_min;
-  if (!full) {
-    int2 kn[16];
-    if (MASKED) load_nodes16(a.nodes, k0, w.half, kn);
+// Node pairs of the 16 partner tokens of a half-wave's accumulator rows
+// (tile-local 16(r>>3) + 8h + (r&7)), from an LDS tile of 32 node pairs.
+DEVI void lds_nodes16(const int2* sn, int half, int2 out[16]) {
+  const int4* p0 = reinterpret_cast<const int4*>(sn + 8 * half);
+  const int4* p1 = reinterpret_cast<const int4*>(sn + 16 + 8 * half);
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int key = row_token(k0, r, w.half);
-      bool ok = key >= w.klo && key < w.khi;
-      if (MASKED) ok = ok && key != w.qi && node_adjacent(kn[r], w.qn);
-      s[r] = ok ? s[r] : -INFINITY;
-    }
+  for (int j = 0; j < 4; ++j) {
+    const int4 a = p0[j], b = p1[j];
+    out[2 * j] = make_int2(a.x, a.y);
+    out[2 * j + 1] = make_int2(a.z, a.w);
+    out[8 + 2 * j] = make_int2(b.x, b.y);
+    out[8 + 2 * j + 1] = make_int2(b.z, b.w);
   }
-  return s;
 }
 
-// One wave = one (query tile, head).  DQ=false: forward.  DQ=true: dQ pass.
-template <bool MASKED, bool DQ>
-__global__ __launch_bounds__(256) void attn_qouter_kernel(const QOuterArgs a) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int groups = (a.heads + 3) >> 2;
-  const int item = blockIdx.x / groups;
-  const int head = (blockIdx.x - item * groups) * 4 + wave;
-  if (head >= a.heads) return;
+DEVI int row_local(int r, int half) { return 16 * (r >> 3) + 8 * half + (r & 7); }
+
+// Partner-tile range of a 128-token group: from the segment of its first
+// token to the segment of its last valid token.
+DEVI void group_range(const int* cu_outer, const int* cu_inner, int nseg, int total_outer, int t0, int& beg,
+                      int& end) {
+  const int last = min(t0 + kGroupTok - 1, total_outer - 1);
+  const int s0 = seg_of(cu_outer, nseg, t0), s1 = seg_of(cu_outer, nseg, last);
+  beg = __builtin_amdgcn_readfirstlane(cu_inner[s0] >> 5);
+  end = max(beg, __builtin_amdgcn_readfirstlane((cu_inner[s1 + 1] + kTile - 1) >> 5));
+}
+
+// The outer tile a wave owns: per-lane partner range and wave-level bounds.
+struct OuterTile {
+  bool active;         // tile starts before `total`
+  int oi;              // this lane's outer token
+  bool valid;          // oi < total
+  int oc;              // oi clamped into [0, total)
+  int plo, phi;        // partner range of the lane's segment (empty when !valid)
+  int plo_max, phi_min;
+  int pt_beg, pt_end;  // partner tiles this wave visits
+};
+
+DEVI OuterTile outer_tile(const int* cu_outer, const int* cu_inner, int nseg, int total, int o0, int col) {
+  OuterTile t;
+  t.oi = o0 + col;
+  t.active = o0 < total;
+  t.valid = t.oi < total;
+  t.oc = t.valid ? t.oi : total - 1;
+  if (!t.active) {
+    t.plo = t.phi = 0;
+    t.plo_max = INT_MAX;
+    t.phi_min = INT_MIN;
+    t.pt_beg = t.pt_end = 0;
+    return t;
+  }
+  const int last = min(o0 + kTile - 1, total - 1);
+  const int s0 = seg_of(cu_outer, nseg, o0), s1 = seg_of(cu_outer, nseg, last), s = seg_of(cu_outer, nseg, t.oc);
+  t.plo = t.valid ? cu_inner[s] : 0;
+  t.phi = t.valid ? cu_inner[s + 1] : 0;
+  // Wave-uniform values live in scalar registers (uniform branches).
+  t.plo_max = __builtin_amdgcn_readfirstlane(cu_inner[s1]);
+  t.phi_min = __builtin_amdgcn_readfirstlane(cu_inner[s0 + 1]);
+  t.pt_beg = __builtin_amdgcn_readfirstlane(cu_inner[s0] >> 5);
+  t.pt_end = max(t.pt_beg, __builtin_amdgcn_readfirstlane((cu_inner[s1 + 1] + kTile - 1) >> 5));
+  return t;
+}
+
+// First partner tile >= x that some wave of the block needs (masked mode
+// skips tiles whose node sets cannot meet any of the block's four tiles).
+template <bool MASKED>
+DEVI int next_needed(int x, int end, const int4* meta, const int4 gm[kWaves]) {
+  if (!MASKED) return x;
+  for (; x < end; ++x) {
+    const int4 m = meta[x];
+    if (tiles_may_touch(gm[0], m) | tiles_may_touch(gm[1], m) | tiles_may_touch(gm[2], m) |
+        tiles_may_touch(gm[3], m))
+      break;
+  }
+  return x;
+}
+
+struct AttnArgs {
+  const bf16* q; const bf16* k; const bf16* v; const bf16* out; const bf16* dout;
+  const float* lse;         // [H][total_q] natural log (forward output / backward input)
+  const uint2* aux;         // dK/dV pass: per (head, query) packed bf16 (hi, lo) of -LSE2/c and of -D
+  const float* knorm;       // forward: max |k| per (head, key tile) [H][tk_tiles]
+  const int* cu_q; const int* cu_k; int nseg;
+  int total_q, total_k, heads, tq_pad, tk_tiles;
+  float c;                  // softmax_scale * log2(e)
+  float scale;
+  const int2* nodes; const int4* meta;   // masked mode: per-token node pairs (padded), per-tile metadata
+  const int* plan;
+  bf16* o; float* lse_out;  // forward outputs
+  bf16* dq; bf16* dk; bf16* dv;
+};
+
+// ======================================================================== forward
+template <bool MASKED>
+__global__ __launch_bounds__(256) void attn_fwd_kernel(const AttnArgs a) {
+  __shared__ __align__(16) bf16 sK[2][kTile * kRowStride];   // K rows [key][16]
+  __shared__ __align__(16) bf16 sVT[2][32 * kTrStride];      // [V^T ; 1]: rows 0..15 dims, 16..31 ones
+  __shared__ __align__(16) int2 sN[2][kTile];
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 31, half = lane >> 5;
   const int H = a.heads;
-  const int qt = a.plan[item];
-  const int q0 = qt * kTile;
-  QWave w;
-  w.col = lane & 31;
-  w.half = lane >> 5;
-  const int col = w.col, half = w.half;
-  w.qi = q0 + col;
-  const bool qvalid = w.qi < a.total_q;
-  const int qc = qvalid ? w.qi : a.total_q - 1;
-  const int q_last = min(q0 + kTile - 1, a.total_q - 1);
-  const int seg_first = seg_of(a.cu_q, a.nseg, q0);
-  const int seg_last = seg_of(a.cu_q, a.nseg, q_last);
-  const int seg = seg_of(a.cu_q, a.nseg, qc);
-  w.klo = qvalid ? a.cu_k[seg] : 0;
-  w.khi = qvalid ? a.cu_k[seg + 1] : 0;
-  const int kbeg = a.cu_k[seg_first], kend = a.cu_k[seg_last + 1];
-  w.klo_max = a.cu_k[seg_last];
-  w.khi_min = a.cu_k[seg_first + 1];
-  w.kt_beg = kbeg >> 5;
-  w.kt_end = (kend + kTile - 1) >> 5;
-  w.qf = *reinterpret_cast<const bf16x8*>(a.q + ((size_t)qc * H + head) * kHd + 8 * half);
-  w.qn = make_int2(0, 0);
-  w.qmeta = make_int4(0, 0, 0, 0);
-  if (MASKED) { w.qn = a.nodes[qc]; w.qmeta = a.meta[qt]; }
+  const int item = blockIdx.x / H;
+  const int head = blockIdx.x - item * H;
+  const int t0 = a.plan[item] * kGroupTok;
 
-  const rsrc_t rk = make_rsrc(a.k, (uint32_t)a.total_k * H * kHd * 2);
-  const rsrc_t ra = make_rsrc(a.at, a.at_bytes);
-  constexpr int ROWS = DQ ? 16 : 32;
-  const uint32_t k_step = (uint32_t)kTile * H * kHd * 2;
-  const uint32_t chunk_bytes = (uint32_t)H * ROWS * 16;
-  uint32_t koff = ((uint32_t)(w.kt_beg * kTile + kperm(col)) * H + head) * (kHd * 2) + 16u * half;
-  uint32_t aoff = ((uint32_t)(w.kt_beg * 4 + half) * H * ROWS + head * ROWS + (DQ ? (col & 15) : col)) * 16u;
-  const uint32_t a_step = 4u * chunk_bytes;
+  for (int i = tid; i < 2 * 16 * kTrStride; i += 256) {
+    const int st = i / (16 * kTrStride);
+    sVT[st][16 * kTrStride + (i - st * 16 * kTrStride)] = (bf16)1.f;
+  }
+  int gbeg, gend;
+  group_range(a.cu_q, a.cu_k, a.nseg, a.total_q, t0, gbeg, gend);
+  const OuterTile ot = outer_tile(a.cu_q, a.cu_k, a.nseg, a.total_q, t0 + wave * kTile, col);
+  const bf16x8 qf = *reinterpret_cast<const bf16x8*>(a.q + ((size_t)ot.oc * H + head) * kHd + 8 * half);
+  int2 qn = make_int2(0, 0);
+  int4 gm[kWaves], own_meta = no_touch();
+  if (MASKED) {
+    qn = a.nodes[ot.oc];
+    const int tile0 = t0 / kTile;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) gm[w] = (t0 + w * kTile < a.total_q) ? a.meta[tile0 + w] : no_touch();
+    own_meta = (t0 + wave * kTile < a.total_q) ? a.meta[tile0 + wave] : no_touch();
+  }
 
-  f32x16 acc = {};
-  if (!DQ) {
-    // Reference point b = c |q| max|k| (see the file comment).
+  // Reference point b = c |q| max|k| over the keys this wave visits.
+  float b = 0.f;
+  bool fixed_ref = true;
+  if (ot.active) {
     float qq = 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) qq = fmaf((float)w.qf[e], (float)w.qf[e], qq);
+    for (int e = 0; e < 8; ++e) qq = fmaf((float)qf[e], (float)qf[e], qq);
     qq += __shfl_xor(qq, 32);
     float km = 0.f;
-    for (int t = w.kt_beg + lane; t < w.kt_end; t += 64) km = fmaxf(km, a.knorm[(size_t)head * a.tk_tiles + t]);
+    for (int t = ot.pt_beg + lane; t < ot.pt_end; t += 64) km = fmaxf(km, a.knorm[(size_t)head * a.tk_tiles + t]);
     km = wave_max(km);
-    const float b = a.c * sqrtf(qq) * km;
-    const bool fixed_ref = wave_max(qvalid ? b : 0.f) <= kStaticBound;
-    float m_run;
-    if (fixed_ref) {
-      m_run = b;
-      // Loads run one tile ahead (past the end they read zeros, unused).
-      bf16x8 kf = bload16(rk, koff);
-      for (int kt = w.kt_beg; kt < w.kt_end; ++kt) {
-        if (MASKED && !tiles_may_touch(w.qmeta, a.meta[kt])) {
-          koff += k_step; aoff += a_step;
-          kf = bload16(rk, koff);
-          continue;
+    b = a.c * sqrtf(qq) * km;
+    fixed_ref = __builtin_amdgcn_readfirstlane((int)(wave_max(ot.valid ? b : 0.f) <= kStaticBound)) != 0;
+  }
+  float m_run = fixed_ref ? b : -INFINITY;
+
+  // Staging roles: wave 0 copies K rows, wave 1 transposes V rows into
+  // V^T, wave 2 copies node pairs (masked mode).
+  const rsrc_t rsrc = make_rsrc(wave == 0 ? (const void*)a.k : (const void*)a.v, (uint32_t)a.total_k * H * kHd * 2);
+  const int skey = lane >> 1, sdh = lane & 1;
+  auto gload = [&](int pt) -> i32x4 {
+    if (wave < 2) return bload(rsrc, ((uint32_t)(pt * kTile + skey) * H + head) * (kHd * 2) + 16u * sdh);
+    if (MASKED && wave == 2 && lane < kTile) {
+      const int2 n = a.nodes[pt * kTile + lane];
+      return i32x4{n.x, n.y, 0, 0};
+    }
+    return i32x4{0, 0, 0, 0};
+  };
+  auto lstore = [&](int st, i32x4 v) {
+    if (wave == 0) {
+      *reinterpret_cast<i32x4*>(&sK[st][skey * kRowStride + 8 * sdh]) = v;
+    } else if (wave == 1) {
+      const bf16x8 x = as_bf16x8(v);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sVT[st][(8 * sdh + e) * kTrStride + skey] = x[e];
+    } else if (MASKED && wave == 2 && lane < kTile) {
+      sN[st][lane] = make_int2(v.x, v.y);
+    }
+  };
+
+  f32x16 acc = {};
+  // The fixed-reference and the online (running-max) loops are separate
+  // instantiations so the accumulator stays in place across iterations.
+  auto run = [&](auto online_tag) {
+    constexpr bool ONLINE = decltype(online_tag)::value;
+    const f32x16 zero = {};
+    int pt = next_needed<MASKED>(gbeg, gend, a.meta, gm);
+    i32x4 stg = {0, 0, 0, 0};
+    if (pt < gend) stg = gload(pt);
+    lstore(0, stg);
+    __syncthreads();
+    for (int cur = 0; pt < gend; cur ^= 1) {
+      const int nxt = next_needed<MASKED>(pt + 1, gend, a.meta, gm);
+      if (nxt < gend) stg = gload(nxt);
+      if (pt >= ot.pt_beg && pt < ot.pt_end && (!MASKED || tiles_may_touch(own_meta, a.meta[pt]))) {
+        const int k0 = pt * kTile;
+        f32x16 s = mfma32(lds8(&sK[cur][kperm(col) * kRowStride + 8 * half]), qf, zero);
+        const bool full = !MASKED && k0 >= ot.plo_max && k0 + kTile <= ot.phi_min;
+        if (!full) {
+          int2 kn[16];
+          if (MASKED) lds_nodes16(sN[cur], half, kn);
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int key = k0 + row_local(r, half);
+            bool ok = key >= ot.plo && key < ot.phi;
+            if (MASKED) ok = ok && key != ot.oi && node_adjacent(kn[r], qn);
+            s[r] = ok ? s[r] : -INFINITY;
+          }
         }
-        const bf16x8 v0 = bload16(ra, aoff), v1 = bload16(ra, aoff + 2 * chunk_bytes);
-        const f32x16 s = score_tile<MASKED>(a, w, kf, kt);
-        koff += k_step; aoff += a_step;
-        kf = bload16(rk, koff);
-        float p[16];
+        if (ONLINE) {
+          float mt = s[0];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) p[r] = fast_exp2(fmaf(s[r], a.c, -b));
-        acc = mfma32(v0, cvt8(p), acc);
-        acc = mfma32(v1, cvt8(p + 8), acc);
-      }
-    } else {
-      m_run = -INFINITY;
-      for (int kt = w.kt_beg; kt < w.kt_end; ++kt, koff += k_step, aoff += a_step) {
-        if (MASKED && !tiles_may_touch(w.qmeta, a.meta[kt])) continue;
-        const f32x16 s = score_tile<MASKED>(a, w, bload16(rk, koff), kt);
-        float mt = s[0];
+          for (int r = 1; r < 16; ++r) mt = fmaxf(mt, s[r]);
+          mt = fmaxf(mt, __shfl_xor(mt, 32));
+          const float m_new = fmaxf(m_run, mt * a.c);
+          if (__ballot(m_new > m_run)) {
+            const float alpha = fast_exp2(m_run - (m_new == -INFINITY ? 0.f : m_new));
 #pragma unroll
-        for (int r = 1; r < 16; ++r) mt = fmaxf(mt, s[r]);
-        mt = fmaxf(mt, __shfl_xor(mt, 32));
-        const float m_new = fmaxf(m_run, mt * a.c);
-        if (__ballot(m_new > m_run)) {
-          const float alpha = fast_exp2(m_run - (m_new == -INFINITY ? 0.f : m_new));
-#pragma unroll
-          for (int r = 0; r < 16; ++r) acc[r] *= alpha;
-          m_run = m_new;
+            for (int r = 0; r < 16; ++r) acc[r] *= alpha;
+            m_run = m_new;
+          }
         }
-        const float m_use = m_run == -INFINITY ? 0.f : m_run;
+        const float m_use = ONLINE ? (m_run == -INFINITY ? 0.f : m_run) : b;
         float p[16];
 #pragma unroll
         for (int r = 0; r < 16; ++r) p[r] = fast_exp2(fmaf(s[r], a.c, -m_use));
-        acc = mfma32(bload16(ra, aoff), cvt8(p), acc);
-        acc = mfma32(bload16(ra, aoff + 2 * chunk_bytes), cvt8(p + 8), acc);
+        acc = mfma32(lds8(&sVT[cur][col * kTrStride + 8 * half]), cvt8(p), acc);
+        acc = mfma32(lds8(&sVT[cur][col * kTrStride + 16 + 8 * half]), cvt8(p + 8), acc);
       }
+      if (nxt < gend) lstore(cur ^ 1, stg);
+      __syncthreads();
+      pt = nxt;
     }
-    if (!qvalid) return;
-    const float l = acc[8];  // a ones row of [V^T; 1] P^T: the softmax row sum
-    const float inv = l > 0.f ? 1.f / l : 0.f;
-    store_rows8(a.out + ((size_t)w.qi * H + head) * kHd, acc, inv, half);
-    if (half == 0)
-      a.lse[(size_t)head * a.total_q + w.qi] = l > 0.f ? (m_run + fast_log2(l)) * kLn2 : -INFINITY;
-  } else {
-    const bf16x8 dof = *reinterpret_cast<const bf16x8*>(a.dout + ((size_t)qc * H + head) * kHd + 8 * half);
-    const float lse2q = a.lse2[(size_t)head * a.tq_pad + qc];
-    const float dq_d = a.dvec[(size_t)head * a.tq_pad + qc];
-    const rsrc_t rv = make_rsrc(a.v, (uint32_t)a.total_k * H * kHd * 2);
-    const f32x16 zero = {};
-    // Loads run one tile ahead (past the end they read zeros, unused).
-    bf16x8 kf = bload16(rk, koff), vf = bload16(rv, koff);
-    for (int kt = w.kt_beg; kt < w.kt_end; ++kt) {
-      if (MASKED && !tiles_may_touch(w.qmeta, a.meta[kt])) {
-        koff += k_step; aoff += a_step;
-        kf = bload16(rk, koff); vf = bload16(rv, koff);
-        continue;
+  };
+  if (fixed_ref)
+    run(std::integral_constant<bool, false>{});
+  else
+    run(std::integral_constant<bool, true>{});
+  if (!ot.valid) return;
+  const float l = acc[8];  // a ones row of [V^T; 1] P^T: the softmax row sum
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  store_rows8(a.o + ((size_t)ot.oi * H + head) * kHd, acc, inv, half);
+  if (half == 0)
+    a.lse_out[(size_t)head * a.total_q + ot.oi] = l > 0.f ? (m_run + fast_log2(l)) * kLn2 : -INFINITY;
+}
+
+// ======================================================================== dQ pass
+// One wave = one query tile: dQ = scale * dS K with dS = P * (dP - D),
+// recomputing P from the saved LSE.  D = rowsum(dO * O) is computed per lane.
+template <bool MASKED>
+__global__ __launch_bounds__(256) void attn_dq_kernel(const AttnArgs a) {
+  __shared__ __align__(16) bf16 sK[2][kTile * kRowStride];    // K rows
+  __shared__ __align__(16) bf16 sV[2][kTile * kRowStride];    // V rows
+  __shared__ __align__(16) bf16 sKT[2][16 * kTrStride];       // K^T
+  __shared__ __align__(16) int2 sN[2][kTile];
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 31, half = lane >> 5;
+  const int H = a.heads;
+  const int item = blockIdx.x / H;
+  const int head = blockIdx.x - item * H;
+  const int t0 = a.plan[item] * kGroupTok;
+
+  int gbeg, gend;
+  group_range(a.cu_q, a.cu_k, a.nseg, a.total_q, t0, gbeg, gend);
+  const OuterTile ot = outer_tile(a.cu_q, a.cu_k, a.nseg, a.total_q, t0 + wave * kTile, col);
+  const size_t row = ((size_t)ot.oc * H + head) * kHd + 8 * half;
+  const bf16x8 qf = *reinterpret_cast<const bf16x8*>(a.q + row);
+  const bf16x8 dof = *reinterpret_cast<const bf16x8*>(a.dout + row);
+  const bf16x8 of = *reinterpret_cast<const bf16x8*>(a.out + row);
+  float dsum = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) dsum = fmaf((float)dof[e], (float)of[e], dsum);
+  dsum += __shfl_xor(dsum, 32);
+  const float lq = a.lse[(size_t)head * a.total_q + ot.oc];
+  const float lse2q = lq == -INFINITY ? INFINITY : lq * kLog2e;
+  f32x16 cd;  // accumulator seed of dP^T: -D in every row of this lane's column
+#pragma unroll
+  for (int r = 0; r < 16; ++r) cd[r] = -dsum;
+  int2 qn = make_int2(0, 0);
+  int4 gm[kWaves], own_meta = no_touch();
+  if (MASKED) {
+    qn = a.nodes[ot.oc];
+    const int tile0 = t0 / kTile;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) gm[w] = (t0 + w * kTile < a.total_q) ? a.meta[tile0 + w] : no_touch();
+    own_meta = (t0 + wave * kTile < a.total_q) ? a.meta[tile0 + wave] : no_touch();
+  }
+
+  const rsrc_t rsrc = make_rsrc(wave == 0 ? (const void*)a.k : (const void*)a.v, (uint32_t)a.total_k * H * kHd * 2);
+  const int skey = lane >> 1, sdh = lane & 1;
+  auto gload = [&](int pt) -> i32x4 {
+    if (wave < 2) return bload(rsrc, ((uint32_t)(pt * kTile + skey) * H + head) * (kHd * 2) + 16u * sdh);
+    if (MASKED && wave == 2 && lane < kTile) {
+      const int2 n = a.nodes[pt * kTile + lane];
+      return i32x4{n.x, n.y, 0, 0};
+    }
+    return i32x4{0, 0, 0, 0};
+  };
+  auto lstore = [&](int st, i32x4 v) {
+    if (wave == 0) {
+      *reinterpret_cast<i32x4*>(&sK[st][skey * kRowStride + 8 * sdh]) = v;
+      const bf16x8 x = as_bf16x8(v);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sKT[st][(8 * sdh + e) * kTrStride + skey] = x[e];
+    } else if (wave == 1) {
+      *reinterpret_cast<i32x4*>(&sV[st][skey * kRowStride + 8 * sdh]) = v;
+    } else if (MASKED && wave == 2 && lane < kTile) {
+      sN[st][lane] = make_int2(v.x, v.y);
+    }
+  };
+
+  f32x16 acc = {};
+  const f32x16 zero = {};
+  int pt = next_needed<MASKED>(gbeg, gend, a.meta, gm);
+  i32x4 stg = {0, 0, 0, 0};
+  if (pt < gend) stg = gload(pt);
+  lstore(0, stg);
+  __syncthreads();
+  for (int cur = 0; pt < gend; cur ^= 1) {
+    const int nxt = next_needed<MASKED>(pt + 1, gend, a.meta, gm);
+    if (nxt < gend) stg = gload(nxt);
+    if (pt >= ot.pt_beg && pt < ot.pt_end && (!MASKED || tiles_may_touch(own_meta, a.meta[pt]))) {
+      const int k0 = pt * kTile;
+      f32x16 s = mfma32(lds8(&sK[cur][kperm(col) * kRowStride + 8 * half]), qf, zero);
+      const f32x16 dp = mfma32(lds8(&sV[cur][kperm(col) * kRowStride + 8 * half]), dof, cd);  // dP^T - D
+      const bool full = !MASKED && k0 >= ot.plo_max && k0 + kTile <= ot.phi_min;
+      if (!full) {
+        int2 kn[16];
+        if (MASKED) lds_nodes16(sN[cur], half, kn);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = k0 + row_local(r, half);
+          bool ok = key >= ot.plo && key < ot.phi;
+          if (MASKED) ok = ok && key != ot.oi && node_adjacent(kn[r], qn);
+          s[r] = ok ? s[r] : -INFINITY;
+        }
       }
-      const bf16x8 t0 = bload16(ra, aoff), t1 = bload16(ra, aoff + 2 * chunk_bytes);
-      const f32x16 s = score_tile<MASKED>(a, w, kf, kt);
-      const f32x16 dp = mfma32(vf, dof, zero);   // dP^T = V dO^T (V rows in K's order)
-      koff += k_step; aoff += a_step;
-      kf = bload16(rk, koff); vf = bload16(rv, koff);
       float ds[16];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) ds[r] = fast_exp2(fmaf(s[r], a.c, -lse2q)) * (dp[r] - dq_d);
-      acc = mfma32(t0, cvt8(ds), acc);
-      acc = mfma32(t1, cvt8(ds + 8), acc);
+      for (int r = 0; r < 16; ++r) ds[r] = fast_exp2(fmaf(s[r], a.c, -lse2q)) * dp[r];
+      const int trow = (col & 15) * kTrStride + 8 * half;
+      acc = mfma32(lds8(&sKT[cur][trow]), cvt8(ds), acc);
+      acc = mfma32(lds8(&sKT[cur][trow + 16]), cvt8(ds + 8), acc);
     }
-    if (!qvalid) return;
-    store_rows8(a.dq + ((size_t)w.qi * H + head) * kHd, acc, a.scale, half);
+    if (nxt < gend) lstore(cur ^ 1, stg);
+    __syncthreads();
+    pt = nxt;
   }
+  if (!ot.valid) return;
+  store_rows8(a.dq + ((size_t)ot.oi * H + head) * kHd, acc, a.scale, half);
 }
 
-struct KOuterArgs {
-  const bf16* q; const bf16* k; const bf16* v; const bf16* dout;
-  const bf16* qt; const bf16* dot;   // tile-transposed Q and dO [Tq/8][H][16][8]
-  uint32_t tt_bytes;
-  const float* lse2; const float* dvec;
-  const int* cu_q; const int* cu_k; int nseg;
-  int total_q, total_k, heads, tq_pad;
-  float c, scale;
-  const int2* nodes; const int4* meta;
-  const int* plan; int n_tiles;
-  bf16* dk; bf16* dv;
-};
-
-// One wave = one (key tile, head): dV = P^T dO and dK = scale * dS^T Q,
-// accumulated over every query tile of the key tile's segments.
+// ======================================================================== dK/dV pass
+// One wave = one key tile (keys on lanes): dV = P^T dO, dK = scale * dS^T Q.
 template <bool MASKED>
-__global__ __launch_bounds__(256) void attn_kouter_kernel(const KOuterArgs a) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int groups = (a.heads + 3) >> 2;
-  const int item = blockIdx.x / groups;
-  const int head = (blockIdx.x - item * groups) * 4 + wave;
-  if (head >= a.heads) return;
-  const int H = a.heads;
-  const int kt = a.plan[item];
-  const int k0 = kt * kTile;
+__global__ __launch_bounds__(256) void attn_dkdv_kernel(const AttnArgs a) {
+  __shared__ __align__(16) bf16 sQ[2][kTile * kRowStride];    // Q rows
+  __shared__ __align__(16) bf16 sDO[2][kTile * kRowStride];   // dO rows
+  __shared__ __align__(16) bf16 sQT[2][16 * kTrStride];       // Q^T
+  __shared__ __align__(16) bf16 sDOT[2][16 * kTrStride];      // dO^T
+  __shared__ __align__(16) uint2 sAux[2][kTile];              // row-statistic MFMA operands
+  __shared__ __align__(16) int2 sN[2][kTile];
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 31, half = lane >> 5;
-  const int ki = k0 + col;
-  const bool kvalid = ki < a.total_k;
-  const int kc = kvalid ? ki : a.total_k - 1;
-  const int k_last = min(k0 + kTile - 1, a.total_k - 1);
-  const int seg_first = seg_of(a.cu_k, a.nseg, k0);
-  const int seg_last = seg_of(a.cu_k, a.nseg, k_last);
-  const int seg = seg_of(a.cu_k, a.nseg, kc);
-  const int qlo = kvalid ? a.cu_q[seg] : 0, qhi = kvalid ? a.cu_q[seg + 1] : 0;
-  const int qbeg = a.cu_q[seg_first], qend = a.cu_q[seg_last + 1];
-  const int qlo_max = a.cu_q[seg_last], qhi_min = a.cu_q[seg_first + 1];
+  const int H = a.heads;
+  const int item = blockIdx.x / H;
+  const int head = blockIdx.x - item * H;
+  const int t0 = a.plan[item] * kGroupTok;
 
-  const bf16x8 kf = *reinterpret_cast<const bf16x8*>(a.k + ((size_t)kc * H + head) * kHd + 8 * half);
-  const bf16x8 vf = *reinterpret_cast<const bf16x8*>(a.v + ((size_t)kc * H + head) * kHd + 8 * half);
+  int gbeg, gend;
+  group_range(a.cu_k, a.cu_q, a.nseg, a.total_k, t0, gbeg, gend);
+  const OuterTile ot = outer_tile(a.cu_k, a.cu_q, a.nseg, a.total_k, t0 + wave * kTile, col);
+  const size_t row = ((size_t)ot.oc * H + head) * kHd + 8 * half;
+  const bf16x8 kf = *reinterpret_cast<const bf16x8*>(a.k + row);
+  const bf16x8 vf = *reinterpret_cast<const bf16x8*>(a.v + row);
+  // B operand of the row-statistic MFMA: ones in slots 0 and 1 (half 0).
+  bf16x8 ones2 = {};
+  if (half == 0) { ones2[0] = (bf16)1.f; ones2[1] = (bf16)1.f; }
   int2 kn = make_int2(0, 0);
-  int4 kmeta = make_int4(0, 0, 0, 0);
-  if (MASKED) { kn = a.nodes[kc]; kmeta = a.meta[kt]; }
-  const f32x16 zero = {};
+  int4 gm[kWaves], own_meta = no_touch();
+  if (MASKED) {
+    kn = a.nodes[ot.oc];
+    const int tile0 = t0 / kTile;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) gm[w] = (t0 + w * kTile < a.total_k) ? a.meta[tile0 + w] : no_touch();
+    own_meta = (t0 + wave * kTile < a.total_k) ? a.meta[tile0 + wave] : no_touch();
+  }
+
+  // Staging roles: wave 0 Q rows (+ Q^T), wave 1 dO rows (+ dO^T),
+  // wave 2 row statistics, wave 3 node pairs (masked mode).
+  const rsrc_t rsrc = make_rsrc(wave == 0 ? (const void*)a.q : (const void*)a.dout, (uint32_t)a.total_q * H * kHd * 2);
+  const int sq = lane >> 1, sdh = lane & 1;
+  auto gload = [&](int pt) -> i32x4 {
+    if (wave < 2) return bload(rsrc, ((uint32_t)(pt * kTile + sq) * H + head) * (kHd * 2) + 16u * sdh);
+    if (wave == 2 && lane < kTile) {
+      const uint2 x = a.aux[(size_t)head * a.tq_pad + pt * kTile + lane];
+      return i32x4{(int)x.x, (int)x.y, 0, 0};
+    }
+    if (MASKED && wave == 3 && lane < kTile) {
+      const int2 n = a.nodes[pt * kTile + lane];
+      return i32x4{n.x, n.y, 0, 0};
+    }
+    return i32x4{0, 0, 0, 0};
+  };
+  auto lstore = [&](int st, i32x4 v) {
+    if (wave < 2) {
+      bf16* rows = wave == 0 ? sQ[st] : sDO[st];
+      bf16* tr = wave == 0 ? sQT[st] : sDOT[st];
+      *reinterpret_cast<i32x4*>(&rows[sq * kRowStride + 8 * sdh]) = v;
+      const bf16x8 x = as_bf16x8(v);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) tr[(8 * sdh + e) * kTrStride + sq] = x[e];
+    } else if (wave == 2 && lane < kTile) {
+      sAux[st][lane] = make_uint2((uint32_t)v.x, (uint32_t)v.y);
+    } else if (MASKED && wave == 3 && lane < kTile) {
+      sN[st][lane] = make_int2(v.x, v.y);
+    }
+  };
+
   f32x16 dva = {}, dka = {};
-  const float* lse2h = a.lse2 + (size_t)head * a.tq_pad + 8 * half;
-  const float* dvech = a.dvec + (size_t)head * a.tq_pad + 8 * half;
-
-  const rsrc_t rq = make_rsrc(a.q, (uint32_t)a.total_q * H * kHd * 2);
-  const rsrc_t rdo = make_rsrc(a.dout, (uint32_t)a.total_q * H * kHd * 2);
-  const rsrc_t rqt = make_rsrc(a.qt, a.tt_bytes);
-  const rsrc_t rdot = make_rsrc(a.dot, a.tt_bytes);
-  const int qt_beg = qbeg >> 5, qt_end = (qend + kTile - 1) >> 5;
-  const uint32_t q_step = (uint32_t)kTile * H * kHd * 2;
-  const uint32_t chunk_bytes = (uint32_t)H * 16 * 16;
-  uint32_t qoff = ((uint32_t)(qt_beg * kTile + kperm(col)) * H + head) * (kHd * 2) + 16u * half;
-  uint32_t toff = ((uint32_t)(qt_beg * 4 + half) * H * 16 + head * 16 + (col & 15)) * 16u;
-
-  // Row fragments run one tile ahead (past the end they read zeros, unused).
-  bf16x8 qa = bload16(rq, qoff), da = bload16(rdo, qoff);
-  for (int qt = qt_beg; qt < qt_end; ++qt) {
-    const int q0 = qt * kTile;
-    if (MASKED && !tiles_may_touch(a.meta[qt], kmeta)) {
-      qoff += q_step; toff += 4 * chunk_bytes;
-      qa = bload16(rq, qoff); da = bload16(rdo, qoff);
-      continue;
-    }
-    const bf16x8 o0 = bload16(rdot, toff), o1 = bload16(rdot, toff + 2 * chunk_bytes);
-    const bf16x8 t0 = bload16(rqt, toff), t1 = bload16(rqt, toff + 2 * chunk_bytes);
-    const f32x16 s = mfma32(qa, kf, zero);     // S = Q K^T, lane = key
-    const f32x16 dp = mfma32(da, vf, zero);    // dP = dO V^T
-    qoff += q_step; toff += 4 * chunk_bytes;
-    qa = bload16(rq, qoff); da = bload16(rdo, qoff);
-    // Per-row (query) statistics: rows r -> q0 + 16(r>>3) + 8h + (r&7).
-    const f32x4* l2p = reinterpret_cast<const f32x4*>(lse2h + q0);
-    const f32x4* dvp = reinterpret_cast<const f32x4*>(dvech + q0);
-    const f32x4 la = l2p[0], lb = l2p[1], lc = l2p[4], ld = l2p[5];
-    const f32x4 da = dvp[0], db = dvp[1], dc = dvp[4], dd = dvp[5];
-    float l2[16], dr[16];
+  const f32x16 zero = {};
+  int pt = next_needed<MASKED>(gbeg, gend, a.meta, gm);
+  i32x4 stg = {0, 0, 0, 0};
+  if (pt < gend) stg = gload(pt);
+  lstore(0, stg);
+  __syncthreads();
+  for (int cur = 0; pt < gend; cur ^= 1) {
+    const int nxt = next_needed<MASKED>(pt + 1, gend, a.meta, gm);
+    if (nxt < gend) stg = gload(nxt);
+    if (pt >= ot.pt_beg && pt < ot.pt_end && (!MASKED || tiles_may_touch(own_meta, a.meta[pt]))) {
+      const int q0 = pt * kTile;
+      const int rrow = kperm(col) * kRowStride + 8 * half;
+      const uint2 ax = sAux[cur][kperm(col)];
+      const bf16x8 aux_s = as_bf16x8(i32x4{(int)ax.x, 0, 0, 0});
+      const bf16x8 aux_d = as_bf16x8(i32x4{(int)ax.y, 0, 0, 0});
+      // S' = Q K^T - LSE2/c and dP' = dO V^T - D, rows = queries, lanes = keys.
+      const f32x16 s = mfma32(lds8(&sQ[cur][rrow]), kf, mfma32(aux_s, ones2, zero));
+      const f32x16 dp = mfma32(lds8(&sDO[cur][rrow]), vf, mfma32(aux_d, ones2, zero));
+      float p[16];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      l2[i] = la[i]; l2[4 + i] = lb[i]; l2[8 + i] = lc[i]; l2[12 + i] = ld[i];
-      dr[i] = da[i]; dr[4 + i] = db[i]; dr[8 + i] = dc[i]; dr[12 + i] = dd[i];
-    }
-    float p[16];
+      for (int r = 0; r < 16; ++r) p[r] = fast_exp2(s[r] * a.c);
+      const bool full = !MASKED && q0 >= ot.plo_max && q0 + kTile <= ot.phi_min;
+      if (!full) {
+        int2 qn[16];
+        if (MASKED) lds_nodes16(sN[cur], half, qn);
 #pragma unroll
-    for (int r = 0; r < 16; ++r) p[r] = fast_exp2(fmaf(s[r], a.c, -l2[r]));
-    const bool full = !MASKED && q0 >= qlo_max && q0 + kTile <= qhi_min;
-    if (!full) {
-      int2 qn[16];
-      if (MASKED) load_nodes16(a.nodes, q0, half, qn);
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int qq = row_token(q0, r, half);
-        bool ok = qq >= qlo && qq < qhi;
-        if (MASKED) ok = ok && qq != ki && node_adjacent(qn[r], kn);
-        p[r] = ok ? p[r] : 0.f;
-      }
-    }
-    float ds[16];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) ds[r] = p[r] * (dp[r] - dr[r]);
-    dva = mfma32(o0, cvt8(p), dva);
-    dva = mfma32(o1, cvt8(p + 8), dva);
-    dka = mfma32(t0, cvt8(ds), dka);
-    dka = mfma32(t1, cvt8(ds + 8), dka);
-  }
-  if (!kvalid) return;
-  store_rows8(a.dv + ((size_t)ki * H + head) * kHd, dva, 1.f, half);
-  store_rows8(a.dk + ((size_t)ki * H + head) * kHd, dka, a.scale, half);
-}
-
-// ------------------------------------------------------------------ prep kernels
-
-// One block per 32-token tile of x [total][H][16].
-//  - xt != null: writes the tile-transposed layout [T/8][H][rows][8] for the
-//    tile's four 8-token chunks: rows 0..15 are x's feature dims (zero past
-//    `total`); rows 16..31 (rows == 32) are ones.
-//  - knorm != null: writes max over the tile's tokens of |x_t| per head to
-//    knorm[h * n_tiles + tile].
-__global__ __launch_bounds__(256) void tile_transpose_kernel(const bf16* __restrict__ x, int total, int heads,
-                                                             int rows, bf16* __restrict__ xt,
-                                                             float* __restrict__ knorm, int n_tiles) {
-  const int tile = blockIdx.x;
-  const int t0 = tile * kTile;
-  if (xt) {
-    const int items = 4 * heads * rows;
-    for (int it = threadIdx.x; it < items; it += blockDim.x) {
-      const int r = it % rows;
-      const int h = (it / rows) % heads;
-      const int c = it / (rows * heads);
-      bf16x8 o;
-      if (r < kHd) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const int t = t0 + c * 8 + i;
-          o[i] = t < total ? x[((size_t)t * heads + h) * kHd + r] : (bf16)0.f;
+        for (int r = 0; r < 16; ++r) {
+          const int qq = q0 + row_local(r, half);
+          bool ok = qq >= ot.plo && qq < ot.phi;
+          if (MASKED) ok = ok && qq != ot.oi && node_adjacent(qn[r], kn);
+          p[r] = ok ? p[r] : 0.f;
         }
-      } else {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) o[i] = (bf16)1.f;
       }
-      *reinterpret_cast<bf16x8*>(xt + (((size_t)(tile * 4 + c) * heads + h) * rows + r) * 8) = o;
-    }
-  }
-  if (knorm) {
-    // one thread per head: max over the tile's tokens of the squared norm
-    for (int h = threadIdx.x; h < heads; h += blockDim.x) {
-      float m = 0.f;
-      for (int i = 0; i < kTile && t0 + i < total; ++i) {
-        const bf16x8* p = reinterpret_cast<const bf16x8*>(x + ((size_t)(t0 + i) * heads + h) * kHd);
-        const bf16x8 u = p[0], v = p[1];
-        float s = 0.f;
+      float ds[16];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) s = fmaf((float)u[e], (float)u[e], fmaf((float)v[e], (float)v[e], s));
-        m = fmaxf(m, s);
-      }
-      knorm[(size_t)h * n_tiles + tile] = sqrtf(m);
+      for (int r = 0; r < 16; ++r) ds[r] = p[r] * dp[r];
+      const int trow = (col & 15) * kTrStride + 8 * half;
+      dva = mfma32(lds8(&sDOT[cur][trow]), cvt8(p), dva);
+      dva = mfma32(lds8(&sDOT[cur][trow + 16]), cvt8(p + 8), dva);
+      dka = mfma32(lds8(&sQT[cur][trow]), cvt8(ds), dka);
+      dka = mfma32(lds8(&sQT[cur][trow + 16]), cvt8(ds + 8), dka);
     }
+    if (nxt < gend) lstore(cur ^ 1, stg);
+    __syncthreads();
+    pt = nxt;
   }
+  if (!ot.valid) return;
+  store_rows8(a.dv + ((size_t)ot.oi * H + head) * kHd, dva, 1.f, half);
+  store_rows8(a.dk + ((size_t)ot.oi * H + head) * kHd, dka, a.scale, half);
 }
 
-// lse2 = lse * log2(e) (+inf for rows with no admissible key, and padding),
-// dvec = rowsum(dO * O) in fp32.  Thread per (token, head), head fastest.
+// ======================================================================== prep kernels
+
+// max over each 32-token tile of |k_t| per head: knorm[h * n_tiles + tile].
+__global__ __launch_bounds__(256) void key_norm_kernel(const bf16* __restrict__ k, int total, int heads,
+                                                       int n_tiles, float* __restrict__ knorm) {
+  // thread -> (tile, head), head fastest: a wave reads contiguous rows.
+  const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (long)n_tiles * heads) return;
+  const int h = (int)(idx % heads), tile = (int)(idx / heads);
+  float m = 0.f;
+  for (int i = 0; i < kTile; ++i) {
+    const int t = tile * kTile + i;
+    if (t >= total) break;
+    const bf16x8* p = reinterpret_cast<const bf16x8*>(k + ((size_t)t * heads + h) * kHd);
+    const bf16x8 u = p[0], v = p[1];
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s = fmaf((float)u[e], (float)u[e], fmaf((float)v[e], (float)v[e], s));
+    m = fmaxf(m, s);
+  }
+  knorm[(size_t)h * n_tiles + tile] = sqrtf(m);
+}
+
+DEVI uint32_t split_bf16_pair(float x) {
+  const bf16 hi = (bf16)x;
+  const bf16 lo = (bf16)(x - (float)hi);
+  return (uint32_t)__builtin_bit_cast(uint16_t, hi) | ((uint32_t)__builtin_bit_cast(uint16_t, lo) << 16);
+}
+
+// Row statistics of the dK/dV pass, as bf16 (hi, lo) pairs (x = hi + lo to
+// ~2^-16 relative): aux.x for -LSE2/c, aux.y for -D = -rowsum(dO * O).
+// Rows without keys and padding get -LSE2/c = -1e30 (their P is 0).
 __global__ void bwd_rowstats_kernel(const bf16* __restrict__ dout, const bf16* __restrict__ out,
-                                    const float* __restrict__ lse, int total_q, int heads, int tq_pad,
-                                    float* __restrict__ lse2, float* __restrict__ dvec) {
+                                    const float* __restrict__ lse, int total_q, int heads, int tq_pad, float c,
+                                    uint2* __restrict__ aux) {
   const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= (long)heads * tq_pad) return;
   const int h = (int)(idx % heads), t = (int)(idx / heads);
-  float l2 = INFINITY, dsum = 0.f;
+  float xs = kDeadRow, dsum = 0.f;
   if (t < total_q) {
     const float l = lse[(size_t)h * total_q + t];
-    l2 = l == -INFINITY ? INFINITY : l * kLog2e;
+    if (l != -INFINITY) xs = -(l * kLog2e) / c;
     const bf16x8* po = reinterpret_cast<const bf16x8*>(out + ((size_t)t * heads + h) * kHd);
     const bf16x8* pd = reinterpret_cast<const bf16x8*>(dout + ((size_t)t * heads + h) * kHd);
 #pragma unroll
@@ -480,8 +617,7 @@ __global__ void bwd_rowstats_kernel(const bf16* __restrict__ dout, const bf16* _
       for (int e = 0; e < 8; ++e) dsum = fmaf((float)o[e], (float)g[e], dsum);
     }
   }
-  lse2[(size_t)h * tq_pad + t] = l2;
-  dvec[(size_t)h * tq_pad + t] = dsum;
+  aux[(size_t)h * tq_pad + t] = make_uint2(split_bf16_pair(xs), split_bf16_pair(-dsum));
 }
 
 __global__ void nodes_pack_kernel(const int* __restrict__ src, const int* __restrict__ dst, int total,
@@ -510,26 +646,23 @@ __global__ void tile_meta_kernel(const int2* __restrict__ nodes, int total, int 
   meta[t] = make_int4(lo, hi, (int)(sig & 0xffffffffull), (int)(sig >> 32));
 }
 
-// Longest-first order of the outer tiles by the number of inner tiles they
-// visit (counting sort in one block; parallel scan of the bucket counts).
+// Longest-first order of the 128-token outer groups by the number of partner
+// tiles they visit (counting sort in one block; parallel bucket scan).
 __global__ __launch_bounds__(1024) void plan_kernel(const int* __restrict__ cu_outer,
                                                     const int* __restrict__ cu_inner, int nseg,
-                                                    int total_outer, int n_tiles, int* __restrict__ plan) {
+                                                    int total_outer, int n_groups, int* __restrict__ plan) {
   constexpr int NB = 1024;
   __shared__ int hist[NB];
   const int tid = threadIdx.x;
   hist[tid] = 0;
   __syncthreads();
-  auto bucket = [&](int t) {
-    const int o0 = t * kTile, o1 = min(o0 + kTile - 1, total_outer - 1);
-    const int s0 = seg_of(cu_outer, nseg, o0), s1 = seg_of(cu_outer, nseg, o1);
-    const int ib = cu_inner[s0], ie = cu_inner[s1 + 1];
-    const int cost = ie > ib ? ((ie + kTile - 1) >> 5) - (ib >> 5) : 0;
-    return NB - 1 - min(cost, NB - 1);
+  auto bucket = [&](int g) {
+    int beg, end;
+    group_range(cu_outer, cu_inner, nseg, total_outer, g * kGroupTok, beg, end);
+    return NB - 1 - min(end - beg, NB - 1);
   };
-  for (int t = tid; t < n_tiles; t += NB) atomicAdd(&hist[bucket(t)], 1);
+  for (int g = tid; g < n_groups; g += NB) atomicAdd(&hist[bucket(g)], 1);
   __syncthreads();
-  // inclusive Hillis-Steele scan over the buckets, then shift to exclusive
   const int own = hist[tid];
   for (int off = 1; off < NB; off <<= 1) {
     const int add = tid >= off ? hist[tid - off] : 0;
@@ -539,7 +672,7 @@ __global__ __launch_bounds__(1024) void plan_kernel(const int* __restrict__ cu_o
   }
   hist[tid] -= own;
   __syncthreads();
-  for (int t = tid; t < n_tiles; t += NB) plan[atomicAdd(&hist[bucket(t)], 1)] = t;
+  for (int g = tid; g < n_groups; g += NB) plan[atomicAdd(&hist[bucket(g)], 1)] = g;
 }
 
 __global__ void edge_mask_dense_kernel(const int* __restrict__ src, const int* __restrict__ dst,
@@ -566,15 +699,14 @@ __global__ void zero16_kernel(uint4* __restrict__ p, long n) {
     p[i] = make_uint4(0u, 0u, 0u, 0u);
 }
 
-// ---------------------------------------------------------------- host side
+// ======================================================================== host side
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 int round32(int x) { return (x + kTile - 1) / kTile * kTile; }
+int groups_of(int total) { return (total + kGroupTok - 1) / kGroupTok; }
 
 struct WsLayout {
-  size_t vt = 0, knorm = 0, qt = 0, kt = 0, dot = 0, lse2 = 0, dvec = 0, plan_q = 0, plan_k = 0,
-         nodes = 0, meta = 0, total = 0;
-  size_t vt_bytes = 0, tt_q_bytes = 0, tt_k_bytes = 0;
+  size_t knorm = 0, aux = 0, plan_q = 0, plan_k = 0, nodes = 0, meta = 0, total = 0;
 };
 
 WsLayout ws_layout(int total_q, int total_k, int heads, bool masked, bool backward) {
@@ -582,20 +714,12 @@ WsLayout ws_layout(int total_q, int total_k, int heads, bool masked, bool backwa
   const int tqp = round32(total_q), tkp = round32(total_k);
   size_t off = 0;
   if (!backward) {
-    L.vt_bytes = (size_t)tkp * heads * 32 * 2;
-    L.vt = off; off += align256(L.vt_bytes);
     L.knorm = off; off += align256((size_t)heads * (tkp / kTile) * 4);
   } else {
-    L.tt_q_bytes = (size_t)tqp * heads * kHd * 2;
-    L.tt_k_bytes = (size_t)tkp * heads * kHd * 2;
-    L.qt = off; off += align256(L.tt_q_bytes);
-    L.kt = off; off += align256(L.tt_k_bytes);
-    L.dot = off; off += align256(L.tt_q_bytes);
-    L.lse2 = off; off += align256((size_t)heads * tqp * 4);
-    L.dvec = off; off += align256((size_t)heads * tqp * 4);
+    L.aux = off; off += align256((size_t)heads * tqp * 8);
   }
-  L.plan_q = off; off += align256((size_t)(tqp / kTile) * 4);
-  if (backward) { L.plan_k = off; off += align256((size_t)(tkp / kTile) * 4); }
+  L.plan_q = off; off += align256((size_t)groups_of(total_q) * 4 + 4);
+  if (backward) { L.plan_k = off; off += align256((size_t)groups_of(total_k) * 4 + 4); }
   if (masked) {
     L.nodes = off; off += align256((size_t)tqp * 8);
     L.meta = off; off += align256((size_t)(tqp / kTile) * 16);
@@ -609,9 +733,9 @@ bool misaligned(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) !
 int check_common(int batch, int total_q, int total_k, int heads, int head_dim, bool masked) {
   if (head_dim != kHd) return ESA_ERR_HEAD_DIM;
   if (batch < 1 || heads < 1 || total_q < 0 || total_k < 0) return ESA_ERR_SHAPE;
-  // Buffer-resource ranges are 32-bit byte counts; the forward's V^T has 32 rows per head.
+  // Buffer-resource ranges are 32-bit byte counts.
   const long lim = (1L << 31) - 1;
-  if ((long)round32(total_q) * heads * 64 > lim || (long)round32(total_k) * heads * 64 > lim) return ESA_ERR_SHAPE;
+  if ((long)round32(total_q) * heads * 32 > lim || (long)round32(total_k) * heads * 32 > lim) return ESA_ERR_SHAPE;
   if (masked && total_q != total_k) return ESA_ERR_MASK;
   return ESA_OK;
 }
@@ -623,16 +747,6 @@ int launch_zero(void* p, size_t bytes, hipStream_t st) {
   long g = (n + 255) / 256;
   if (g > 65536) g = 65536;
   hipLaunchKernelGGL(zero16_kernel, dim3((unsigned)g), dim3(256), 0, st, static_cast<uint4*>(p), n);
-  ESA_LAUNCH_CHECK();
-  return ESA_OK;
-}
-
-int launch_tt(const bf16* x, int total, int heads, int rows, bf16* xt, float* knorm, hipStream_t st) {
-  const int nt = round32(total) / kTile;
-  if (nt == 0) return ESA_OK;
-  ESA_TIMED(esa_profile::kAttnPrep, st,
-            hipLaunchKernelGGL(tile_transpose_kernel, dim3((unsigned)nt), dim3(256), 0, st, x, total, heads, rows,
-                               xt, knorm, nt));
   ESA_LAUNCH_CHECK();
   return ESA_OK;
 }
@@ -652,9 +766,9 @@ int launch_mask_meta(const int* src, const int* dst, int total, int2* nodes, int
 }
 
 int launch_plan(const int* cu_outer, const int* cu_inner, int nseg, int total_outer, int* plan, hipStream_t st) {
-  const int nt = round32(total_outer) / kTile;
+  const int ng = groups_of(total_outer);
   ESA_TIMED(esa_profile::kAttnPrep, st,
-            hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(1024), 0, st, cu_outer, cu_inner, nseg, total_outer, nt,
+            hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(1024), 0, st, cu_outer, cu_inner, nseg, total_outer, ng,
                                plan));
   ESA_LAUNCH_CHECK();
   return ESA_OK;
@@ -664,7 +778,7 @@ int launch_plan(const int* cu_outer, const int* cu_inner, int nseg, int total_ou
 
 extern "C" {
 
-const char* esa_version(void) { return "esa_hip 0.2 gfx950"; }
+const char* esa_version(void) { return "esa_hip 0.3 gfx950"; }
 
 int esa_varlen_attn_workspace_size(int total_q, int total_k, int heads, int head_dim, int masked,
                                    int backward, size_t* bytes) {
@@ -694,21 +808,21 @@ int esa_varlen_attn_fwd(const void* q, const void* k, const void* v, const int* 
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
 
-  QOuterArgs a{};
+  AttnArgs a{};
   a.q = static_cast<const bf16*>(q); a.k = static_cast<const bf16*>(k); a.v = static_cast<const bf16*>(v);
-  a.at = reinterpret_cast<const bf16*>(ws + L.vt);
-  a.at_bytes = (uint32_t)L.vt_bytes;
   a.knorm = reinterpret_cast<const float*>(ws + L.knorm);
   a.cu_q = cu_seqlens_q; a.cu_k = cu_seqlens_k; a.nseg = batch;
   a.total_q = total_q; a.total_k = total_k; a.heads = heads; a.tq_pad = round32(total_q);
   a.tk_tiles = round32(total_k) / kTile;
   a.scale = softmax_scale; a.c = softmax_scale * kLog2e;
   a.plan = reinterpret_cast<const int*>(ws + L.plan_q);
-  a.n_tiles = round32(total_q) / kTile;
-  a.out = static_cast<bf16*>(out); a.lse = softmax_lse;
+  a.o = static_cast<bf16*>(out); a.lse_out = softmax_lse;
   if (total_k > 0) {
-    if ((rc = launch_tt(a.v, total_k, heads, 32, reinterpret_cast<bf16*>(ws + L.vt), nullptr, st))) return rc;
-    if ((rc = launch_tt(a.k, total_k, heads, 0, nullptr, reinterpret_cast<float*>(ws + L.knorm), st))) return rc;
+    const long n = (long)a.tk_tiles * heads;
+    ESA_TIMED(esa_profile::kAttnPrep, st,
+              hipLaunchKernelGGL(key_norm_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a.k, total_k,
+                                 heads, a.tk_tiles, reinterpret_cast<float*>(ws + L.knorm)));
+    ESA_LAUNCH_CHECK();
   }
   if (masked) {
     a.nodes = reinterpret_cast<const int2*>(ws + L.nodes);
@@ -717,13 +831,12 @@ int esa_varlen_attn_fwd(const void* q, const void* k, const void* v, const int* 
                                reinterpret_cast<int4*>(ws + L.meta), st))) return rc;
   }
   if ((rc = launch_plan(cu_seqlens_q, cu_seqlens_k, batch, total_q, reinterpret_cast<int*>(ws + L.plan_q), st))) return rc;
-  const unsigned grid = (unsigned)a.n_tiles * (unsigned)((heads + 3) / 4);
+  const unsigned grid = (unsigned)groups_of(total_q) * (unsigned)heads;
   if (masked)
     ESA_TIMED(esa_profile::kAttnFwdMasked, st,
-              hipLaunchKernelGGL((attn_qouter_kernel<true, false>), dim3(grid), dim3(256), 0, st, a));
+              hipLaunchKernelGGL((attn_fwd_kernel<true>), dim3(grid), dim3(256), 0, st, a));
   else
-    ESA_TIMED(esa_profile::kAttnFwd, st,
-              hipLaunchKernelGGL((attn_qouter_kernel<false, false>), dim3(grid), dim3(256), 0, st, a));
+    ESA_TIMED(esa_profile::kAttnFwd, st, hipLaunchKernelGGL((attn_fwd_kernel<false>), dim3(grid), dim3(256), 0, st, a));
   ESA_LAUNCH_CHECK();
   return ESA_OK;
 }
@@ -759,71 +872,51 @@ int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k, const vo
     if ((rc = launch_zero(dv, (size_t)total_k * heads * kHd * 2, st))) return rc;
     return ESA_OK;
   }
-  const int tqp = round32(total_q);
-  bf16* qt = reinterpret_cast<bf16*>(ws + L.qt);
-  bf16* ktt = reinterpret_cast<bf16*>(ws + L.kt);
-  bf16* dot = reinterpret_cast<bf16*>(ws + L.dot);
-  float* lse2 = reinterpret_cast<float*>(ws + L.lse2);
-  float* dvec = reinterpret_cast<float*>(ws + L.dvec);
-  int* plan_q = reinterpret_cast<int*>(ws + L.plan_q);
-  int* plan_k = reinterpret_cast<int*>(ws + L.plan_k);
-  if ((rc = launch_tt(static_cast<const bf16*>(q), total_q, heads, 16, qt, nullptr, st))) return rc;
-  if ((rc = launch_tt(static_cast<const bf16*>(k), total_k, heads, 16, ktt, nullptr, st))) return rc;
-  if ((rc = launch_tt(static_cast<const bf16*>(dout), total_q, heads, 16, dot, nullptr, st))) return rc;
+  AttnArgs a{};
+  a.q = static_cast<const bf16*>(q); a.k = static_cast<const bf16*>(k); a.v = static_cast<const bf16*>(v);
+  a.out = static_cast<const bf16*>(out); a.dout = static_cast<const bf16*>(dout); a.lse = softmax_lse;
+  a.aux = reinterpret_cast<const uint2*>(ws + L.aux);
+  a.cu_q = cu_seqlens_q; a.cu_k = cu_seqlens_k; a.nseg = batch;
+  a.total_q = total_q; a.total_k = total_k; a.heads = heads; a.tq_pad = round32(total_q);
+  a.tk_tiles = round32(total_k) / kTile;
+  a.scale = softmax_scale; a.c = softmax_scale * kLog2e;
+  a.dq = static_cast<bf16*>(dq); a.dk = static_cast<bf16*>(dk); a.dv = static_cast<bf16*>(dv);
   {
-    const long n = (long)heads * tqp;
+    const long n = (long)heads * a.tq_pad;
     ESA_TIMED(esa_profile::kAttnPrep, st,
-              hipLaunchKernelGGL(bwd_rowstats_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
-                                 static_cast<const bf16*>(dout), static_cast<const bf16*>(out), softmax_lse,
-                                 total_q, heads, tqp, lse2, dvec));
+              hipLaunchKernelGGL(bwd_rowstats_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a.dout,
+                                 a.out, softmax_lse, total_q, heads, a.tq_pad, a.c,
+                                 reinterpret_cast<uint2*>(ws + L.aux)));
     ESA_LAUNCH_CHECK();
   }
-  const int2* nodes = nullptr;
-  const int4* meta = nullptr;
   if (masked) {
-    nodes = reinterpret_cast<const int2*>(ws + L.nodes);
-    meta = reinterpret_cast<const int4*>(ws + L.meta);
+    a.nodes = reinterpret_cast<const int2*>(ws + L.nodes);
+    a.meta = reinterpret_cast<const int4*>(ws + L.meta);
     if ((rc = launch_mask_meta(tok_src, tok_dst, total_q, reinterpret_cast<int2*>(ws + L.nodes),
                                reinterpret_cast<int4*>(ws + L.meta), st))) return rc;
   }
+  int* plan_q = reinterpret_cast<int*>(ws + L.plan_q);
+  int* plan_k = reinterpret_cast<int*>(ws + L.plan_k);
   if ((rc = launch_plan(cu_seqlens_q, cu_seqlens_k, batch, total_q, plan_q, st))) return rc;
   if ((rc = launch_plan(cu_seqlens_k, cu_seqlens_q, batch, total_k, plan_k, st))) return rc;
-  const float c = softmax_scale * kLog2e;
-  const unsigned groups = (unsigned)((heads + 3) / 4);
 
-  KOuterArgs ka{};
-  ka.q = static_cast<const bf16*>(q); ka.k = static_cast<const bf16*>(k); ka.v = static_cast<const bf16*>(v);
-  ka.dout = static_cast<const bf16*>(dout); ka.qt = qt; ka.dot = dot; ka.tt_bytes = (uint32_t)L.tt_q_bytes;
-  ka.lse2 = lse2; ka.dvec = dvec;
-  ka.cu_q = cu_seqlens_q; ka.cu_k = cu_seqlens_k; ka.nseg = batch;
-  ka.total_q = total_q; ka.total_k = total_k; ka.heads = heads; ka.tq_pad = tqp;
-  ka.c = c; ka.scale = softmax_scale; ka.nodes = nodes; ka.meta = meta;
-  ka.plan = plan_k; ka.n_tiles = round32(total_k) / kTile;
-  ka.dk = static_cast<bf16*>(dk); ka.dv = static_cast<bf16*>(dv);
-  const unsigned kgrid = (unsigned)ka.n_tiles * groups;
+  a.plan = plan_k;
+  const unsigned kgrid = (unsigned)groups_of(total_k) * (unsigned)heads;
   if (masked)
     ESA_TIMED(esa_profile::kAttnBwdDkdvMasked, st,
-              hipLaunchKernelGGL((attn_kouter_kernel<true>), dim3(kgrid), dim3(256), 0, st, ka));
+              hipLaunchKernelGGL((attn_dkdv_kernel<true>), dim3(kgrid), dim3(256), 0, st, a));
   else
     ESA_TIMED(esa_profile::kAttnBwdDkdv, st,
-              hipLaunchKernelGGL((attn_kouter_kernel<false>), dim3(kgrid), dim3(256), 0, st, ka));
+              hipLaunchKernelGGL((attn_dkdv_kernel<false>), dim3(kgrid), dim3(256), 0, st, a));
   ESA_LAUNCH_CHECK();
 
-  QOuterArgs qa{};
-  qa.q = ka.q; qa.k = ka.k; qa.v = ka.v; qa.at = ktt; qa.at_bytes = (uint32_t)L.tt_k_bytes;
-  qa.dout = ka.dout; qa.lse2 = lse2; qa.dvec = dvec;
-  qa.cu_q = cu_seqlens_q; qa.cu_k = cu_seqlens_k; qa.nseg = batch;
-  qa.total_q = total_q; qa.total_k = total_k; qa.heads = heads; qa.tq_pad = tqp;
-  qa.tk_tiles = round32(total_k) / kTile;
-  qa.c = c; qa.scale = softmax_scale; qa.nodes = nodes; qa.meta = meta;
-  qa.plan = plan_q; qa.n_tiles = tqp / kTile; qa.dq = static_cast<bf16*>(dq);
-  const unsigned qgrid = (unsigned)qa.n_tiles * groups;
+  a.plan = plan_q;
+  const unsigned qgrid = (unsigned)groups_of(total_q) * (unsigned)heads;
   if (masked)
     ESA_TIMED(esa_profile::kAttnBwdDqMasked, st,
-              hipLaunchKernelGGL((attn_qouter_kernel<true, true>), dim3(qgrid), dim3(256), 0, st, qa));
+              hipLaunchKernelGGL((attn_dq_kernel<true>), dim3(qgrid), dim3(256), 0, st, a));
   else
-    ESA_TIMED(esa_profile::kAttnBwdDq, st,
-              hipLaunchKernelGGL((attn_qouter_kernel<false, true>), dim3(qgrid), dim3(256), 0, st, qa));
+    ESA_TIMED(esa_profile::kAttnBwdDq, st, hipLaunchKernelGGL((attn_dq_kernel<false>), dim3(qgrid), dim3(256), 0, st, a));
   ESA_LAUNCH_CHECK();
   return ESA_OK;
 }
