@@ -106,10 +106,11 @@ class _VarlenAttention(torch.autograd.Function):
         out, lse = attn_fwd(q, k, v, cu_q, cu_k, max_q, max_k, scale, edge_src, edge_dst)
         ctx.save_for_backward(q, k, v, out, lse, cu_q, cu_k, edge_src, edge_dst)
         ctx.meta = (max_q, max_k, scale)
-        return out
+        ctx.mark_non_differentiable(lse)
+        return out, lse
 
     @staticmethod
-    def backward(ctx, dout):
+    def backward(ctx, dout, _dlse):
         q, k, v, out, lse, cu_q, cu_k, edge_src, edge_dst = ctx.saved_tensors
         max_q, max_k, scale = ctx.meta
         dq, dk, dv = attn_bwd(dout.contiguous(), q, k, v, out, lse, cu_q, cu_k, max_q, max_k, scale,
@@ -118,13 +119,15 @@ class _VarlenAttention(torch.autograd.Function):
 
 
 def varlen_attention(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, dropout_p=0.0,
-                     softmax_scale=None, causal=False, edge_src=None, edge_dst=None):
+                     softmax_scale=None, causal=False, edge_src=None, edge_dst=None, return_lse=False):
     """``flash_attn_varlen_func``-compatible entry (plus the edge mask).
 
     q: [Tq, H, 16] bf16; k, v: [Tk, H, 16] bf16; cu_seqlens_*: int32 [B+1].
     edge_src / edge_dst: optional int32 [Tq] node ids per token (self-attention
     only); token i then attends to token j of its segment iff i != j and the
-    two edges share an endpoint.
+    two edges share an endpoint.  With return_lse, also returns the
+    (non-differentiable) softmax log-sum-exp [H, Tq]; -inf marks a query with
+    no admissible key (its output is 0).
     """
     if causal:
         raise NotImplementedError("causal attention is not on the ESA path (the reference uses causal=False)")
@@ -134,8 +137,9 @@ def varlen_attention(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seql
         softmax_scale = 1.0 / math.sqrt(q.shape[-1])
     if (edge_src is None) != (edge_dst is None):
         raise ValueError("edge_src and edge_dst must be given together")
-    return _VarlenAttention.apply(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
-                                  float(softmax_scale), edge_src, edge_dst)
+    out, lse = _VarlenAttention.apply(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
+                                      float(softmax_scale), edge_src, edge_dst)
+    return (out, lse) if return_lse else out
 
 
 def edge_mask_dense(edge_src, edge_dst, cu_seqlens, max_items):

@@ -1,0 +1,262 @@
+"""ESA backbone blocks with the interfaces of esa/masked_layers.py.
+
+``SABComplete``, ``PMAComplete`` and ``ESA`` keep the constructor arguments,
+submodule names and the tuple-in / tuple-out forwards of
+esa/masked_layers.py:271-936, so a PretrainingESAModel or Estimator can hold
+them unchanged and existing state_dicts load.  The difference is the mask:
+``get_adj_mask_from_edge_index_edge`` returns an ``EdgeAdjacency`` descriptor
+(O(E) device memory) instead of the [B, 1, N, N] bias built from a global
+E x E comparison (esa/masked_layers.py:121-142, 217-268); the attention
+kernels evaluate the share-an-endpoint predicate from it on the fly.
+
+Backend ``xformers_or_torch_attn``:
+  "xformers" / "torch"  the reference's padded semantics (see mha.py);
+  "flash_varlen"        the reference's MABFlashVarlen path, quirks included
+                        (seq_lens = node counts per graph, mask dropped,
+                        V = fc_v(fc_k(K)), esa/masked_layers.py:422-438);
+  "hip"                 native packed path: every attention layer works on the
+                        valid tokens only (edge counts per graph), the masked
+                        layers apply the edge mask, PMA pools over valid tokens.
+"""
+from __future__ import annotations
+
+import torch
+from torch import nn
+from torch.nn import functional as F
+
+from .attention import varlen_attention
+from .mha import PMA, SAB, _heads, pooled_attention
+from .mha_flash_varlen import PMAFlashVarlen, SABFlashVarlen
+from .mlp_utils import GatedMLPMulti, SmallMLP
+from .norm_layers import LN
+from .packing import EdgeAdjacency
+
+
+def get_adj_mask_from_edge_index_edge(edge_index, batch_size, max_items, batch_mapping, xformers_or_torch_attn=None,
+                                      use_bfloat16=True, device=None):
+    """Edge-adjacency mask descriptor for the edge tokens of a batch.
+
+    Replaces esa/masked_layers.py:217-268 (same arguments).  Token e is edge
+    e of ``edge_index``; tokens e, f of one graph attend iff e != f and the
+    edges share an endpoint.
+    """
+    return EdgeAdjacency.from_edge_index(edge_index, batch_mapping, batch_size, max_items)
+
+
+def get_adj_mask_from_edge_index_node(*args, **kwargs):
+    """Node-mode adjacency (esa/masked_layers.py:79-118) is not on the HIP path yet."""
+    raise NotImplementedError("node-mode masked attention (apply_attention_on='node') is not implemented on the "
+                              "HIP kernels; use edge mode")
+
+
+def _backend_check(name: str) -> None:
+    if name not in ("xformers", "torch", "flash_varlen", "hip"):
+        raise ValueError(f"unknown attention backend {name!r}")
+
+
+class SABComplete(nn.Module):
+    """Pre/post-norm SAB / MAB block (esa/masked_layers.py:271-494)."""
+
+    def __init__(self, dim_in, dim_out, num_heads, dropout, idx, norm_type, use_mlp=False, mlp_hidden_size=64,
+                 mlp_type="standard", node_or_edge="edge", xformers_or_torch_attn="xformers", residual_dropout=0,
+                 set_max_items=0, use_bfloat16=True, num_mlp_layers=3, pre_or_post="pre",
+                 num_layers_for_residual=0, use_mlp_ln=False, mlp_dropout=0, use_equivariant=False,
+                 equivariant_lmax=2, equivariant_num_features=16, equivariant_fusion_method="add",
+                 equivariant_cross_connection=True):
+        super().__init__()
+        _backend_check(xformers_or_torch_attn)
+        if use_equivariant:
+            raise NotImplementedError("EquivariantSAB (esa/equivariant_sab.py) is outside the ESA attention path")
+        if pre_or_post != "pre":
+            raise NotImplementedError("post-norm blocks are not on the benchmarked path (every config is pre-norm)")
+        if norm_type != "LN":
+            raise NotImplementedError("BatchRenorm blocks are not on the HIP path; use norm_type='LN'")
+        self.dim_in, self.dim_out, self.num_heads = dim_in, dim_out, num_heads
+        self.use_mlp, self.idx, self.mlp_hidden_size = use_mlp, idx, mlp_hidden_size
+        self.node_or_edge = node_or_edge
+        self.xformers_or_torch_attn = xformers_or_torch_attn
+        self.residual_dropout = residual_dropout
+        self.set_max_items = set_max_items
+        self.use_bfloat16 = use_bfloat16
+        self.num_mlp_layers = num_mlp_layers
+        self.pre_or_post = pre_or_post
+        self.use_equivariant = False
+        if dim_in != dim_out:
+            self.proj_1 = nn.Linear(dim_in, dim_out)
+        if xformers_or_torch_attn == "flash_varlen":
+            self.sab = SABFlashVarlen(dim_in, dim_out, num_heads, dropout)
+        else:
+            self.sab = SAB(dim_in, dim_out, num_heads, dropout, xformers_or_torch_attn)
+        self.norm = LN(dim_in, num_elements=set_max_items if idx != 2 else None)
+        self.mlp_type = mlp_type
+        if use_mlp:
+            cls = SmallMLP if mlp_type == "standard" else GatedMLPMulti
+            self.mlp = cls(in_dim=dim_out, out_dim=dim_out, inter_dim=mlp_hidden_size, dropout_p=mlp_dropout,
+                           num_layers=num_mlp_layers, use_ln=use_mlp_ln)
+        self.norm_mlp = LN(dim_out, num_elements=set_max_items if idx != 2 else None)
+
+    def forward(self, inp):
+        X, edge_index, batch_mapping, max_items, adj_mask = inp[:5]
+        X = self.norm(X)
+        if isinstance(self.sab, SABFlashVarlen):
+            # the reference's seq_lens: node counts per graph, mask dropped (esa/masked_layers.py:422-438)
+            seq_lens = torch.bincount(batch_mapping, minlength=X.size(0)).to(torch.int32)
+            out_attn = self.sab(X, seq_lens=seq_lens, adj_mask=None)
+        elif self.idx == 1:
+            out_attn = self.sab(X, adj_mask)
+        elif self.idx == 0 and self.xformers_or_torch_attn == "hip" and isinstance(adj_mask, EdgeAdjacency):
+            out_attn = _sab_valid_only(self.sab, X, adj_mask)
+        else:
+            out_attn = self.sab(X, None)
+        if out_attn.shape[-1] != X.shape[-1]:
+            X = self.proj_1(X)
+        out = X + out_attn
+        if self.use_mlp:
+            out_mlp = self.mlp(self.norm_mlp(out))
+            if out.shape[-1] == out_mlp.shape[-1]:
+                out = out_mlp + out
+        if self.residual_dropout > 0:
+            out = F.dropout(out, p=self.residual_dropout)
+        return out, edge_index, batch_mapping, max_items, adj_mask
+
+
+def _sab_valid_only(sab: SAB, X: torch.Tensor, tokens: EdgeAdjacency) -> torch.Tensor:
+    """Unmasked self-attention over each graph's valid tokens (the "hip" backend's S layers)."""
+    mab = sab.mab
+    q = mab.fc_q(X)
+    v = mab.fc_v(X)
+    k = mab.fc_k(X)
+    h, d, n = mab.num_heads, q.shape[-1], X.shape[1]
+    cu = tokens.cu_seqlens
+    out = varlen_attention(_heads(tokens.unpad(q), h), _heads(tokens.unpad(k), h), _heads(tokens.unpad(v), h),
+                           cu, cu, n, n)
+    out = tokens.pad(out.reshape(-1, d)).to(q.dtype)
+    return out + F.mish(mab.fc_o(out))
+
+
+class PMAComplete(nn.Module):
+    """Pre-norm PMA block (esa/masked_layers.py:497-621)."""
+
+    def __init__(self, dim_hidden, num_heads, num_outputs, norm_type, dropout=0, use_mlp=False,
+                 mlp_hidden_size=64, mlp_type="standard", xformers_or_torch_attn="xformers", set_max_items=0,
+                 use_bfloat16=True, num_mlp_layers=3, pre_or_post="pre", num_layers_for_residual=0,
+                 residual_dropout=0, use_mlp_ln=False, mlp_dropout=0):
+        super().__init__()
+        _backend_check(xformers_or_torch_attn)
+        if pre_or_post != "pre":
+            raise NotImplementedError("post-norm blocks are not on the benchmarked path (every config is pre-norm)")
+        if norm_type != "LN":
+            raise NotImplementedError("BatchRenorm blocks are not on the HIP path; use norm_type='LN'")
+        self.use_mlp, self.mlp_hidden_size, self.num_heads = use_mlp, mlp_hidden_size, num_heads
+        self.xformers_or_torch_attn = xformers_or_torch_attn
+        self.set_max_items, self.use_bfloat16 = set_max_items, use_bfloat16
+        self.residual_dropout, self.num_mlp_layers, self.pre_or_post = residual_dropout, num_mlp_layers, pre_or_post
+        if xformers_or_torch_attn == "flash_varlen":
+            self.pma = PMAFlashVarlen(dim_hidden, num_heads, num_outputs, dropout)
+        else:
+            self.pma = PMA(dim_hidden, num_heads, num_outputs, dropout, xformers_or_torch_attn)
+        self.norm = LN(dim_hidden)
+        self.mlp_type = mlp_type
+        if use_mlp:
+            cls = SmallMLP if mlp_type == "standard" else GatedMLPMulti
+            self.mlp = cls(in_dim=dim_hidden, out_dim=dim_hidden, inter_dim=mlp_hidden_size, dropout_p=mlp_dropout,
+                           num_layers=num_mlp_layers, use_ln=use_mlp_ln)
+        self.norm_mlp = LN(dim_hidden)
+
+    def forward(self, inp):
+        X, edge_index, batch_mapping, max_items, adj_mask = inp[:5]
+        X = self.norm(X)
+        if isinstance(self.pma, PMAFlashVarlen):
+            seq_lens = torch.bincount(batch_mapping, minlength=X.size(0)).to(torch.int32)
+            out_attn = self.pma(X, seq_lens=seq_lens)
+        elif self.xformers_or_torch_attn == "hip" and isinstance(adj_mask, EdgeAdjacency):
+            out_attn = pooled_attention(self.pma.mab, self.pma.S.repeat(X.size(0), 1, 1), X, adj_mask)
+        else:
+            out_attn = self.pma(X)
+        if out_attn.shape[-2] == X.shape[-2]:
+            out = X + out_attn
+        else:
+            out = out_attn
+        if self.use_mlp:
+            out_mlp = self.mlp(self.norm_mlp(out))
+            if out.shape[-2] == out_mlp.shape[-2]:
+                out = out_mlp + out
+        if self.residual_dropout > 0:
+            out = F.dropout(out, p=self.residual_dropout)
+        return out, edge_index, batch_mapping, max_items, adj_mask
+
+
+class ESA(nn.Module):
+    """Edge-set attention encoder + PMA decoder (esa/masked_layers.py:624-936)."""
+
+    def __init__(self, num_outputs, dim_output, dim_hidden, num_heads, layer_types, node_or_edge="edge",
+                 xformers_or_torch_attn="xformers", pre_or_post="pre", norm_type="LN", sab_dropout=0.0,
+                 mab_dropout=0.0, pma_dropout=0.0, residual_dropout=0.0, pma_residual_dropout=0.0, use_mlps=False,
+                 mlp_hidden_size=64, num_mlp_layers=2, mlp_type="gated_mlp", mlp_dropout=0.0, use_mlp_ln=False,
+                 set_max_items=0, use_bfloat16=True, use_equivariant=False, equivariant_lmax=2,
+                 equivariant_num_features=16, equivariant_fusion_method="add", equivariant_cross_connection=True):
+        super().__init__()
+        assert len(layer_types) == len(dim_hidden) and len(layer_types) == len(num_heads)
+        _backend_check(xformers_or_torch_attn)
+        if node_or_edge != "edge":
+            raise NotImplementedError("node-mode ESA is not on the HIP path yet; use node_or_edge='edge'")
+        self.dim_hidden, self.num_heads, self.layer_types = dim_hidden, num_heads, layer_types
+        self.node_or_edge = node_or_edge
+        self.xformers_or_torch_attn = xformers_or_torch_attn
+        self.pre_or_post, self.norm_type = pre_or_post, norm_type
+        self.use_bfloat16 = use_bfloat16
+        self.use_distance_bias = False
+        common = dict(pre_or_post=pre_or_post, use_mlp=use_mlps, mlp_hidden_size=mlp_hidden_size,
+                      mlp_dropout=mlp_dropout, num_mlp_layers=num_mlp_layers, use_mlp_ln=use_mlp_ln,
+                      norm_type=norm_type, mlp_type=mlp_type, set_max_items=set_max_items,
+                      use_bfloat16=use_bfloat16, num_layers_for_residual=len(dim_hidden) * 2)
+        has_pma = "P" in layer_types
+        encoder, decoder = [], None
+        pma_encountered, dim_pma, tracker = False, -1, 0
+        for lt in layer_types:
+            d_in, heads = dim_hidden[tracker], num_heads[tracker]
+            d_out = (dim_hidden[tracker + 1] if has_pma else dim_hidden[tracker]) if lt != "P" else -1
+            if lt == "S" and not pma_encountered:
+                encoder.append(SABComplete(d_in, d_out, heads, idx=0, dropout=sab_dropout, node_or_edge=node_or_edge,
+                                           xformers_or_torch_attn=xformers_or_torch_attn,
+                                           residual_dropout=residual_dropout, **common))
+            if lt == "M" and not pma_encountered:
+                encoder.append(SABComplete(d_in, d_out, heads, idx=1, dropout=mab_dropout, node_or_edge=node_or_edge,
+                                           xformers_or_torch_attn=xformers_or_torch_attn,
+                                           residual_dropout=residual_dropout, **common))
+            if lt == "P":
+                pma_encountered = True
+                dim_pma = d_in
+                pcommon = {k: v for k, v in common.items() if k not in ("num_layers_for_residual",)}
+                # a later "P" replaces the decoder (esa/masked_layers.py:778)
+                decoder = [PMAComplete(d_in, heads, num_outputs, dropout=pma_dropout,
+                                       residual_dropout=pma_residual_dropout,
+                                       xformers_or_torch_attn=xformers_or_torch_attn,
+                                       num_layers_for_residual=len(dim_hidden) * 2, **pcommon)]
+            if lt == "S" and pma_encountered:
+                decoder.append(SABComplete(d_in, d_out, heads, idx=2, dropout=sab_dropout, node_or_edge=node_or_edge,
+                                           xformers_or_torch_attn=xformers_or_torch_attn,
+                                           residual_dropout=residual_dropout, **common))
+            if lt != "P":
+                tracker += 1
+        self.encoder = nn.Sequential(*encoder)
+        if pma_encountered:
+            self.decoder = nn.Sequential(*decoder)
+        self.decoder_linear = nn.Linear(dim_hidden[-1], dim_output, bias=True)
+        if has_pma and dim_hidden[0] != dim_pma:
+            self.out_proj = nn.Linear(dim_hidden[0], dim_pma)
+            self.dim_pma = dim_pma
+
+    def forward(self, X, edge_index, batch_mapping, num_max_items, pos=None):
+        adj_mask = get_adj_mask_from_edge_index_edge(edge_index=edge_index, batch_mapping=batch_mapping,
+                                                     batch_size=X.shape[0], max_items=num_max_items)
+        enc, _, _, _, _ = self.encoder((X, edge_index, batch_mapping, num_max_items, adj_mask))
+        if hasattr(self, "dim_pma") and self.dim_hidden[0] != self.dim_pma:
+            X = self.out_proj(X)
+        enc = enc + X
+        node_embeddings_before_pma = enc
+        if hasattr(self, "decoder"):
+            out, _, _, _, _ = self.decoder((enc, edge_index, batch_mapping, num_max_items, adj_mask))
+            out = out.mean(dim=1)
+            return F.mish(self.decoder_linear(out)), node_embeddings_before_pma
+        return F.mish(self.decoder_linear(enc)), enc

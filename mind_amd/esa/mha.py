@@ -1,0 +1,174 @@
+"""MAB / SAB / PMA with the signatures of esa/mha.py, on the gfx950 kernels.
+
+Constructors, parameter names (``fc_q``, ``fc_k``, ``fc_v``, ``fc_o``, ``S``,
+``mab``) and the forward signatures match esa/mha.py:9-109, so existing
+state_dicts load.  Attention semantics by ``adj_mask``:
+
+  None            every query attends to every one of the N positions of its
+                  batch element, padding included — what memory_efficient_attention
+                  and SDPA compute at esa/mha.py:76 and :80-83 without a bias.
+  EdgeAdjacency   the edge-adjacency mask of esa/masked_layers.py:121-142,
+                  evaluated on the fly in the kernel (no [B, 1, N, N] bias).
+                  ``xformers_or_torch_attn`` picks the semantics:
+                    "hip"                 packed valid tokens only; a query with
+                                          no admissible key gets 0;
+                    "xformers" / "torch"  the reference's padded semantics
+                                          exactly: a row whose bias is -99999
+                                          everywhere (padding, or an edge sharing
+                                          no node) softmaxes over all N keys, as
+                                          a constant bias shift leaves softmax
+                                          unchanged.  (The "torch" backend's
+                                          inverted bool mask, esa/masked_layers.py:
+                                          264-265, is a reference defect and is
+                                          not reproduced.)
+
+Attention is computed in bf16 with fp32 softmax statistics, as the reference's
+bf16-mixed training does; outputs return in the input's dtype.
+"""
+from __future__ import annotations
+
+import torch
+from torch import nn
+from torch.nn import functional as F
+from torch.nn.init import xavier_normal_
+
+from .attention import HEAD_DIM, varlen_attention
+from .packing import EdgeAdjacency
+
+BACKENDS = ("xformers", "torch", "flash_varlen", "hip")
+
+
+def _uniform_cu(batch: int, n: int, device) -> torch.Tensor:
+    return torch.arange(batch + 1, device=device, dtype=torch.int32) * n
+
+
+def _heads(x: torch.Tensor, heads: int) -> torch.Tensor:
+    """[..., H * 16] -> contiguous bf16 [tokens, H, 16]."""
+    return x.reshape(-1, heads, x.shape[-1] // heads).to(torch.bfloat16).contiguous()
+
+
+def dense_attention(q, k, v, heads):
+    """Per-batch-element attention over all positions: q [B, Nq, D], k/v [B, Nk, D] -> [B, Nq, D]."""
+    b, nq, d = q.shape
+    nk = k.shape[1]
+    if d // heads != HEAD_DIM:
+        raise ValueError(f"head_dim {d // heads} is not supported by the kernels (16)")
+    out = varlen_attention(_heads(q, heads), _heads(k, heads), _heads(v, heads), _uniform_cu(b, nq, q.device),
+                           _uniform_cu(b, nk, q.device), nq, nk)
+    return out.reshape(b, nq, d)
+
+
+def masked_attention(q, k, v, heads, mask: EdgeAdjacency, packed: bool):
+    """Edge-masked self-attention over [B, N, D] inputs laid out as ``mask`` says."""
+    b, n, d = q.shape
+    if k.shape[1] != n or n != mask.max_items or b != mask.batch_size:
+        raise ValueError("the edge mask needs queries and keys in the descriptor's [B, N] layout")
+    if packed:
+        cu = mask.cu_seqlens
+        out = varlen_attention(_heads(mask.unpad(q), heads), _heads(mask.unpad(k), heads),
+                               _heads(mask.unpad(v), heads), cu, cu, n, n, edge_src=mask.edge_src,
+                               edge_dst=mask.edge_dst)
+        return mask.pad(out.reshape(-1, d))
+    src, dst = mask.padded_nodes()
+    cu = _uniform_cu(b, n, q.device)
+    qh, kh, vh = _heads(q, heads), _heads(k, heads), _heads(v, heads)
+    out_m, lse = varlen_attention(qh, kh, vh, cu, cu, n, n, edge_src=src, edge_dst=dst, return_lse=True)
+    out_d = varlen_attention(qh, kh, vh, cu, cu, n, n)
+    dead = torch.isneginf(lse[0]).view(-1, 1, 1)   # the mask is the same for every head
+    return torch.where(dead, out_d, out_m).reshape(b, n, d)
+
+
+class MAB(nn.Module):
+    """Multihead attention block (esa/mha.py:9-89): out = O + mish(fc_o(O)), V = fc_v(K)."""
+
+    def __init__(self, dim_Q, dim_K, dim_V, num_heads, dropout_p=0.0, xformers_or_torch_attn="xformers"):
+        super().__init__()
+        if xformers_or_torch_attn not in BACKENDS:
+            raise ValueError(f"unknown attention backend {xformers_or_torch_attn!r}; one of {BACKENDS}")
+        self.xformers_or_torch_attn = xformers_or_torch_attn
+        self.dim_Q, self.dim_K, self.dim_V = dim_Q, dim_K, dim_V
+        self.num_heads = num_heads
+        self.dropout_p = dropout_p
+        self.fc_q = nn.Linear(dim_Q, dim_V, bias=True)
+        self.fc_k = nn.Linear(dim_K, dim_V, bias=True)
+        self.fc_v = nn.Linear(dim_K, dim_V, bias=True)
+        self.fc_o = nn.Linear(dim_V, dim_V, bias=True)
+        xavier_normal_(self.fc_q.weight)
+        xavier_normal_(self.fc_k.weight)
+        xavier_normal_(self.fc_v.weight)
+        xavier_normal_(self.fc_o.weight)
+
+    def forward(self, Q, K, adj_mask=None):
+        if self.dim_V % self.num_heads:
+            raise ValueError("Embedding dim is not divisible by nheads")
+        if self.training and self.dropout_p > 0:
+            raise NotImplementedError("attention dropout is not supported on the HIP path")
+        q = self.fc_q(Q)
+        v = self.fc_v(K)
+        k = self.fc_k(K)
+        if adj_mask is None:
+            out = dense_attention(q, k, v, self.num_heads)
+        elif isinstance(adj_mask, EdgeAdjacency):
+            out = masked_attention(q, k, v, self.num_heads, adj_mask, packed=self.xformers_or_torch_attn == "hip")
+        else:
+            raise TypeError("adj_mask must be None or an EdgeAdjacency (build it with "
+                            "get_adj_mask_from_edge_index_edge); dense bias tensors are not materialised")
+        out = out.to(q.dtype)
+        return out + F.mish(self.fc_o(out))
+
+
+class SAB(nn.Module):
+    """Self-attention block (esa/mha.py:92-98)."""
+
+    def __init__(self, dim_in, dim_out, num_heads, dropout, xformers_or_torch_attn):
+        super().__init__()
+        self.mab = MAB(dim_in, dim_in, dim_out, num_heads, dropout, xformers_or_torch_attn)
+
+    def forward(self, X, adj_mask=None):
+        return self.mab(X, X, adj_mask=adj_mask)
+
+
+class PMA(nn.Module):
+    """Pooling by multihead attention with learned seeds S [1, k, dim] (esa/mha.py:101-109).
+
+    Without ``seq_lens`` the seeds attend over all N positions (the reference,
+    which passes no mask at its call site, esa/masked_layers.py:593).  With
+    ``seq_lens`` (an int tensor [B] or an EdgeAdjacency) they attend over each
+    set's valid tokens only.
+    """
+
+    def __init__(self, dim, num_heads, num_seeds, dropout, xformers_or_torch_attn):
+        super().__init__()
+        self.S = nn.Parameter(torch.Tensor(1, num_seeds, dim))
+        nn.init.xavier_normal_(self.S)
+        self.mab = MAB(dim, dim, dim, num_heads, dropout_p=dropout, xformers_or_torch_attn=xformers_or_torch_attn)
+
+    def forward(self, X, adj_mask=None, seq_lens=None):
+        S = self.S.repeat(X.size(0), 1, 1)
+        if seq_lens is None:
+            return self.mab(S, X, adj_mask=adj_mask)
+        return pooled_attention(self.mab, S, X, seq_lens)
+
+
+def pooled_attention(mab: MAB, S: torch.Tensor, X: torch.Tensor, seq_lens) -> torch.Tensor:
+    """MAB(S, X) with each batch element's keys restricted to its first seq_lens[b] tokens."""
+    b, n, d = X.shape
+    k_seeds = S.shape[1]
+    if isinstance(seq_lens, EdgeAdjacency):
+        xk = seq_lens.unpad(X)
+        cu_k = seq_lens.cu_seqlens
+    else:
+        lens = seq_lens.to(device=X.device, dtype=torch.int64)
+        valid = torch.arange(n, device=X.device)[None, :] < lens[:, None]
+        xk = X.reshape(b * n, d)[valid.reshape(-1)]
+        cu_k = torch.zeros(b + 1, dtype=torch.int32, device=X.device)
+        cu_k[1:] = torch.cumsum(lens, 0).to(torch.int32)
+    q = mab.fc_q(S)
+    v = mab.fc_v(xk)
+    k = mab.fc_k(xk)
+    h = mab.num_heads
+    out = varlen_attention(_heads(q, h), _heads(k, h), _heads(v, h), _uniform_cu(b, k_seeds, X.device), cu_k,
+                           k_seeds, n)
+    out = out.reshape(b, k_seeds, d).to(q.dtype)
+    return out + F.mish(mab.fc_o(out))
+

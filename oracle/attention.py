@@ -26,28 +26,33 @@ def _segment_mask(edge_src, edge_dst, qs, qe, ks, ke):
 
 def varlen_attention(q, k, v, cu_q, cu_k, scale, edge_src=None, edge_dst=None, dtype=torch.float64):
     """q [Tq,H,D], k/v [Tk,H,D] -> (out [Tq,H,D], lse [H,Tq]) in ``dtype``."""
-    q, k, v = (t.detach().cpu().to(dtype) for t in (q, k, v))
+    q, k, v = (torch.as_tensor(t).cpu().to(dtype) for t in (q, k, v))
     cu_q = np.asarray(cu_q, dtype=np.int64)
     cu_k = np.asarray(cu_k, dtype=np.int64)
     tq, h, d = q.shape
-    out = torch.zeros(tq, h, d, dtype=dtype)
-    lse = torch.full((h, tq), float("-inf"), dtype=dtype)
+    outs, lses = [], []
     for b in range(len(cu_q) - 1):
         qs, qe, ks, ke = int(cu_q[b]), int(cu_q[b + 1]), int(cu_k[b]), int(cu_k[b + 1])
-        if qe == qs or ke == ks:
+        if qe == qs:
             continue
-        qb = q[qs:qe].permute(1, 0, 2).contiguous()     # [H, Lq, D]
-        kb = k[ks:ke].permute(1, 2, 0).contiguous()     # [H, D, Lk]
-        vb = v[ks:ke].permute(1, 0, 2).contiguous()     # [H, Lk, D]
+        if ke == ks:
+            outs.append(torch.zeros(qe - qs, h, d, dtype=dtype))
+            lses.append(torch.full((h, qe - qs), float("-inf"), dtype=dtype))
+            continue
+        qb = q[qs:qe].permute(1, 0, 2)                  # [H, Lq, D]
+        kb = k[ks:ke].permute(1, 2, 0)                  # [H, D, Lk]
+        vb = v[ks:ke].permute(1, 0, 2)                  # [H, Lk, D]
         s = torch.matmul(qb, kb) * scale                # [H, Lq, Lk]
         m = _segment_mask(edge_src, edge_dst, qs, qe, ks, ke)
         if m is not None:
             s = s.masked_fill(~m, float("-inf"))
         l = torch.logsumexp(s, dim=-1)                  # [H, Lq]
-        p = torch.exp(s - l[..., None])
-        p = torch.nan_to_num(p, nan=0.0)                # rows with no admissible key
-        out[qs:qe] = torch.matmul(p, vb).permute(1, 0, 2)
-        lse[:, qs:qe] = l
+        # rows with no admissible key: every s is -inf; keep p = 0 without NaN
+        p = torch.exp(s - torch.where(torch.isfinite(l), l, torch.zeros_like(l))[..., None])
+        outs.append(torch.matmul(p, vb).permute(1, 0, 2))
+        lses.append(l)
+    out = torch.cat(outs, 0) if outs else torch.zeros(0, h, d, dtype=dtype)
+    lse = torch.cat(lses, 1) if lses else torch.zeros(h, 0, dtype=dtype)
     return out, lse
 
 
@@ -58,7 +63,7 @@ def varlen_attention_bwd(dout, q, k, v, cu_q, cu_k, scale, edge_src=None, edge_d
     dV = P^T dO, dP = dO V^T, dS = P * (dP - D), dQ = scale dS K,
     dK = scale dS^T Q.
     """
-    dout, q, k, v = (t.detach().cpu().to(dtype) for t in (dout, q, k, v))
+    dout, q, k, v = (torch.as_tensor(t).detach().cpu().to(dtype) for t in (dout, q, k, v))
     cu_q = np.asarray(cu_q, dtype=np.int64)
     cu_k = np.asarray(cu_k, dtype=np.int64)
     dq, dk, dv = torch.zeros_like(q), torch.zeros_like(k), torch.zeros_like(v)
@@ -75,7 +80,7 @@ def varlen_attention_bwd(dout, q, k, v, cu_q, cu_k, scale, edge_src=None, edge_d
         if m is not None:
             s = s.masked_fill(~m, float("-inf"))
         l = torch.logsumexp(s, dim=-1)
-        p = torch.nan_to_num(torch.exp(s - l[..., None]), nan=0.0)
+        p = torch.exp(s - torch.where(torch.isfinite(l), l, torch.zeros_like(l))[..., None])
         o = torch.matmul(p, vb)
         dvb = torch.matmul(p.transpose(1, 2).contiguous(), gb)
         dp = torch.matmul(gb, vb.transpose(1, 2).contiguous())
@@ -93,12 +98,12 @@ def padded_attention(q, k, v, scale, bias=None, dtype=torch.float64):
     Restates memory_efficient_attention(Q, K, V, attn_bias) at esa/mha.py:76
     (BMHK layout), which attends to every position including padding.
     """
-    q, k, v = (t.detach().cpu().to(dtype) for t in (q, k, v))
+    q, k, v = (torch.as_tensor(t).cpu().to(dtype) for t in (q, k, v))
     qb = q.permute(0, 2, 1, 3).contiguous()
     kb = k.permute(0, 2, 3, 1).contiguous()
     vb = v.permute(0, 2, 1, 3).contiguous()
     s = torch.matmul(qb, kb) * scale
     if bias is not None:
-        s = s + bias.detach().cpu().to(dtype)
+        s = s + torch.as_tensor(bias).cpu().to(dtype)
     p = torch.softmax(s, dim=-1)
     return torch.matmul(p, vb).permute(0, 2, 1, 3)

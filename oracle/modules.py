@@ -1,0 +1,113 @@
+"""Reference block arithmetic on CPU (test infrastructure; see oracle/__init__.py).
+
+Functions take a module's state_dict (``prefix`` selects the submodule) and
+restate the forward of the reference block in float64:
+  mab_padded      esa/mha.py:48-89 with an optional additive [B, 1, N, N] bias
+  mab_varlen      esa/mha_flash_varlen.py:129-201 (V = fc_v(fc_k(K)), valid tokens)
+  mab_packed      the same block over packed valid tokens with an optional
+                  boolean per-graph mask (the native "hip" path's arithmetic)
+  sab_complete    esa/masked_layers.py:408-494 (pre-norm branch)
+  pma_complete    esa/masked_layers.py:574-621 (pre-norm branch)
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+from .attention import padded_attention, varlen_attention
+
+DT = torch.float64
+
+
+def _p(sd, prefix, name):
+    return sd[prefix + name].cpu().to(DT)
+
+
+def linear(sd, prefix, x):
+    return x @ _p(sd, prefix, "weight").T + _p(sd, prefix, "bias")
+
+
+def layer_norm(sd, prefix, x, eps=1e-8):
+    """nn.LayerNorm(eps=1e-8) (esa/utils/norm_layers.py:36)."""
+    mu = x.mean(-1, keepdim=True)
+    var = ((x - mu) ** 2).mean(-1, keepdim=True)
+    return (x - mu) / torch.sqrt(var + eps) * _p(sd, prefix, "weight") + _p(sd, prefix, "bias")
+
+
+def mish(x):
+    return x * torch.tanh(F.softplus(x))
+
+
+def _heads(x, h):
+    return x.reshape(*x.shape[:-1], h, x.shape[-1] // h)
+
+
+def mab_padded(sd, prefix, Q, K, heads, bias=None):
+    """MAB over padded [B, N, D]: V = fc_v(K); softmax(QK^T/sqrt(hd) + bias) V; out + mish(fc_o(out))."""
+    Q, K = Q.cpu().to(DT), K.cpu().to(DT)
+    q = linear(sd, prefix + "fc_q.", Q)
+    v = linear(sd, prefix + "fc_v.", K)
+    k = linear(sd, prefix + "fc_k.", K)
+    hd = q.shape[-1] // heads
+    o = padded_attention(_heads(q, heads), _heads(k, heads), _heads(v, heads), 1.0 / np.sqrt(hd), bias)
+    o = o.reshape(Q.shape[0], Q.shape[1], -1)
+    return o + mish(linear(sd, prefix + "fc_o.", o))
+
+
+def mab_packed(sd, prefix, Qp, Kp, cu_q, cu_k, heads, edge_src=None, edge_dst=None, v_from_k=False):
+    """MAB over packed tokens [T, D] per segment; optional edge mask; V = fc_v(K) or fc_v(fc_k(K))."""
+    Qp, Kp = torch.as_tensor(Qp).cpu().to(DT), torch.as_tensor(Kp).cpu().to(DT)
+    q = linear(sd, prefix + "fc_q.", Qp)
+    k = linear(sd, prefix + "fc_k.", Kp)
+    v = linear(sd, prefix + "fc_v.", k if v_from_k else Kp)
+    hd = q.shape[-1] // heads
+    o, _ = varlen_attention(_heads(q, heads), _heads(k, heads), _heads(v, heads), cu_q, cu_k, 1.0 / np.sqrt(hd),
+                            edge_src, edge_dst)
+    o = o.reshape(Qp.shape[0], -1)
+    return o + mish(linear(sd, prefix + "fc_o.", o))
+
+
+def mab_varlen(sd, prefix, Q, K, seq_lens, heads):
+    """MABFlashVarlen._forward_varlen on padded [B, N, D] with seq_lens: valid tokens, zeros at padding."""
+    Q, K = Q.cpu().to(DT), K.cpu().to(DT)
+    b, n, d = Q.shape
+    lens = np.asarray(seq_lens, dtype=np.int64)
+    valid = np.arange(n)[None, :] < lens[:, None]
+    idx = torch.as_tensor(np.nonzero(valid.reshape(-1))[0])
+    cu = np.concatenate([[0], np.cumsum(valid.sum(1))])
+    q = linear(sd, prefix + "fc_q.", Q).reshape(b * n, d)[idx]
+    k = linear(sd, prefix + "fc_k.", K).reshape(b * n, d)[idx]
+    v = linear(sd, prefix + "fc_v.", k)
+    o, _ = varlen_attention(_heads(q, heads), _heads(k, heads), _heads(v, heads), cu, cu, 1.0 / np.sqrt(d // heads))
+    out = torch.zeros(b * n, d, dtype=DT)
+    out[idx] = o.reshape(-1, d)
+    out = out.reshape(b, n, d)
+    return out + mish(linear(sd, prefix + "fc_o.", out))
+
+
+def mlp_standard(sd, prefix, x, num_layers):
+    """SmallMLP without LayerNorm/dropout (esa/mlp_utils.py:6-48): Linear+Mish ... Linear."""
+    if num_layers == 1:
+        return mish(linear(sd, prefix + "mlp.0.", x))
+    i = 0
+    for layer in range(num_layers):
+        x = linear(sd, prefix + f"mlp.{i}.", x)
+        i += 1
+        if layer != num_layers - 1:
+            x = mish(x)
+            i += 1
+    return x
+
+
+def sab_complete(sd, prefix, X, heads, attn, num_mlp_layers=None):
+    """Pre-norm block: X' = LN(X); out = X' + attn(X'); out += MLP(LN2(out)) (esa/masked_layers.py:418-483).
+
+    ``attn(sd, prefix_of_mab, X')`` computes the attention sub-block.
+    """
+    X = X.cpu().to(DT)
+    xn = layer_norm(sd, prefix + "norm.ln.", X)
+    out = xn + attn(sd, prefix + "sab.mab.", xn)
+    if num_mlp_layers:
+        out = out + mlp_standard(sd, prefix + "mlp.", layer_norm(sd, prefix + "norm_mlp.ln.", out), num_mlp_layers)
+    return out

@@ -1,0 +1,208 @@
+"""GPU parity of the reference-signature modules (MAB/SAB/PMA, MABFlashVarlen, blocks, ESA) against the oracle.
+
+Weights are the modules' own random initialisation; the oracle reads the same
+state_dict and restates the reference block in float64 on the CPU.  Attention
+runs in bf16 on the GPU, so the bar is the bf16 one (max-abs 2e-2, mean-abs
+2e-3) scaled by max(1, max |reference|).
+"""
+import numpy as np
+import pytest
+import torch
+
+from mind_amd import generators
+from mind_amd.esa import masked_layers as ML
+from mind_amd.esa.mha import MAB, PMA, SAB
+from mind_amd.esa.mha_flash_varlen import MABFlashVarlen, PMAFlashVarlen
+from mind_amd.esa.packing import EdgeAdjacency, nearest_multiple_of_8
+from oracle import mask as OM
+from oracle import modules as OMod
+from tests._util import assert_bf16_close
+
+pytestmark = pytest.mark.gpu
+
+D, H = 128, 8
+
+
+def _scale(ref):
+    return max(1.0, float(ref.abs().max()))
+
+
+def _batch(seed=0, num_graphs=5):
+    gb, _ = generators.small_molecules(seed=seed, num_graphs=num_graphs)
+    n = nearest_multiple_of_8(int(gb.edge_counts.max()) + 1)
+    return gb, n
+
+
+def _padded_tokens(gb, n, seed):
+    x = torch.randn(gb.num_graphs, n, D, generator=torch.Generator().manual_seed(seed))
+    valid = torch.zeros(gb.num_graphs, n, dtype=torch.bool)
+    for b, L in enumerate(gb.edge_counts):
+        valid[b, :L] = True
+    return x, valid
+
+
+def _sd(m):
+    return {k: v.detach().cpu() for k, v in m.state_dict().items()}
+
+
+def test_mab_dense_all_positions(device):
+    torch.manual_seed(0)
+    m = MAB(D, D, D, H).to(device)
+    Q = torch.randn(3, 40, D, generator=torch.Generator().manual_seed(1))
+    K = torch.randn(3, 56, D, generator=torch.Generator().manual_seed(2))
+    got = m(Q.to(device), K.to(device)).cpu()
+    ref = OMod.mab_padded(_sd(m), "", Q, K, H)
+    assert_bf16_close(got, ref, _scale(ref), "MAB dense")
+
+
+@pytest.mark.parametrize("backend", ["xformers", "torch"])
+def test_sab_edge_mask_reference_semantics(device, backend):
+    """Padded layout with the -99999 edge bias, every row including padding (esa/mha.py:73-77)."""
+    gb, n = _batch(1)
+    torch.manual_seed(1)
+    m = SAB(D, D, H, 0.0, backend).to(device)
+    X, _ = _padded_tokens(gb, n, 3)
+    ei = torch.as_tensor(gb.edge_index)
+    gid = np.repeat(np.arange(gb.num_graphs), gb.edge_counts)
+    mask = EdgeAdjacency.from_edge_index(ei.to(device), torch.as_tensor(gb.batch).to(device), gb.num_graphs, n)
+    got = m(X.to(device), adj_mask=mask).cpu()
+    bias = OM.edge_bias_padded(gb.edge_index, gid, gb.num_graphs, n, dtype=torch.float64)
+    ref = OMod.mab_padded(_sd(m), "mab.", X, X, H, bias)
+    assert_bf16_close(got, ref, _scale(ref), f"SAB {backend} edge mask")
+
+
+def test_sab_edge_mask_packed_hip(device):
+    gb, n = _batch(2)
+    torch.manual_seed(2)
+    m = SAB(D, D, H, 0.0, "hip").to(device)
+    X, valid = _padded_tokens(gb, n, 4)
+    mask = EdgeAdjacency.from_edge_index(torch.as_tensor(gb.edge_index).to(device),
+                                         torch.as_tensor(gb.batch).to(device), gb.num_graphs, n)
+    got = m(X.to(device), adj_mask=mask).cpu()
+    cu = gb.cu_seqlens
+    Xp = X[valid]
+    src, dst = gb.edge_index[0], gb.edge_index[1]
+    ref_p = OMod.mab_packed(_sd(m), "mab.", Xp, Xp, cu, cu, H, src, dst)
+    assert_bf16_close(got[valid], ref_p, _scale(ref_p), "SAB hip valid rows")
+    # padding rows: attention output 0, then 0 + mish(fc_o(0))
+    pad_ref = OMod.mish(OMod._p(_sd(m), "mab.", "fc_o.bias"))
+    assert_bf16_close(got[~valid], pad_ref.expand(int((~valid).sum()), D), 1.0, "SAB hip padding rows")
+
+
+def test_sab_hip_backward(device):
+    gb, n = _batch(3, num_graphs=3)
+    torch.manual_seed(3)
+    m = SAB(D, D, H, 0.0, "hip").to(device)
+    X, valid = _padded_tokens(gb, n, 5)
+    mask = EdgeAdjacency.from_edge_index(torch.as_tensor(gb.edge_index).to(device),
+                                         torch.as_tensor(gb.batch).to(device), gb.num_graphs, n)
+    xd = X.to(device).requires_grad_(True)
+    g = torch.randn(gb.num_graphs, n, D, generator=torch.Generator().manual_seed(6))
+    m(xd, adj_mask=mask).backward(g.to(device))
+    sd = {k: v.detach().cpu().double().requires_grad_(True) for k, v in m.state_dict().items()}
+    xr = X.double()[valid].clone().requires_grad_(True)
+    cu = gb.cu_seqlens
+    ref = OMod.mab_packed(sd, "mab.", xr, xr, cu, cu, H, gb.edge_index[0], gb.edge_index[1])
+    ref.backward(g.double()[valid])
+    assert_bf16_close(xd.grad.cpu()[valid], xr.grad, _scale(xr.grad), "dX")
+    for name, p in m.named_parameters():
+        assert_bf16_close(p.grad.cpu(), sd[name].grad, _scale(sd[name].grad), f"d{name}")
+
+
+def test_mab_flash_varlen_path(device):
+    gb, n = _batch(4)
+    torch.manual_seed(4)
+    m = MABFlashVarlen(D, D, D, H).to(device)
+    X, _ = _padded_tokens(gb, n, 7)
+    Xb = X.to(torch.bfloat16)
+    lens = torch.as_tensor(gb.edge_counts, dtype=torch.int32)
+    got = m(Xb.to(device), Xb.to(device), seq_lens=lens.to(device)).float().cpu()
+    ref = OMod.mab_varlen(_sd(m), "", Xb, Xb, gb.edge_counts, H)
+    assert_bf16_close(got, ref, _scale(ref), "MABFlashVarlen varlen")
+
+
+def test_pma_dense_and_pooled(device):
+    gb, n = _batch(5)
+    torch.manual_seed(5)
+    m = PMA(D, H, 4, 0.0, "hip").to(device)
+    X, valid = _padded_tokens(gb, n, 8)
+    S = m.S.detach().cpu().repeat(gb.num_graphs, 1, 1)
+    got = m(X.to(device)).cpu()                        # reference semantics: all N positions
+    ref = OMod.mab_padded(_sd(m), "mab.", S, X, H)
+    assert_bf16_close(got, ref, _scale(ref), "PMA over all positions")
+    lens = torch.as_tensor(gb.edge_counts)
+    got_v = m(X.to(device), seq_lens=lens.to(device)).cpu()
+    cu_q = np.arange(gb.num_graphs + 1) * 4
+    ref_v = OMod.mab_packed(_sd(m), "mab.", S.reshape(-1, D), X[valid], cu_q, gb.cu_seqlens, H)
+    assert_bf16_close(got_v.reshape(-1, D), ref_v, _scale(ref_v), "PMA over valid tokens")
+    pf = PMAFlashVarlen(D, H, 4, 0.0).to(device)
+    pf.load_state_dict(m.state_dict())
+    got_f = pf(X.to(device), seq_lens=lens.to(device)).cpu()   # reference: padded fallback
+    assert_bf16_close(got_f, ref, _scale(ref), "PMAFlashVarlen padded fallback")
+
+
+@pytest.mark.parametrize("backend", ["hip", "xformers"])
+def test_esa_block_config0_shape(device, backend):
+    """M (masked), S, P(1 seed) with pre-norm and standard MLPs on a small-molecule batch."""
+    gb, n = _batch(6, num_graphs=8)
+    torch.manual_seed(6)
+    model = ML.ESA(num_outputs=1, dim_output=D, dim_hidden=[D, D, D], num_heads=[H, H, H], layer_types="MSP",
+                   xformers_or_torch_attn=backend, use_mlps=True, mlp_hidden_size=2 * D, num_mlp_layers=2,
+                   mlp_type="standard").to(device)
+    X, valid = _padded_tokens(gb, n, 9)
+    ei = torch.as_tensor(gb.edge_index).to(device)
+    bm = torch.as_tensor(gb.batch).to(device)
+    g_emb, enc = model(X.to(device), ei, bm, n)
+    g_emb, enc = g_emb.cpu(), enc.cpu()
+    sd = _sd(model)
+    cu = gb.cu_seqlens
+    src, dst = gb.edge_index[0], gb.edge_index[1]
+    gid = np.repeat(np.arange(gb.num_graphs), gb.edge_counts)
+    if backend == "hip":
+        def m_attn(sd_, pre, x):
+            return OMod.mab_packed(sd_, pre, x, x, cu, cu, H, src, dst)
+
+        def s_attn(sd_, pre, x):
+            return OMod.mab_packed(sd_, pre, x, x, cu, cu, H)
+
+        xp = X.double()[valid]
+        h = OMod.sab_complete(sd, "encoder.0.", xp, H, m_attn, 2)
+        h = OMod.sab_complete(sd, "encoder.1.", h, H, s_attn, 2)
+        enc_ref = h + xp
+        hn = OMod.layer_norm(sd, "decoder.0.norm.ln.", enc_ref)
+        S = OMod._p(sd, "decoder.0.pma.", "S").reshape(1, D).repeat(gb.num_graphs, 1)
+        pooled = OMod.mab_packed(sd, "decoder.0.pma.mab.", S, hn, np.arange(gb.num_graphs + 1), cu, H)
+        pooled = pooled + OMod.mlp_standard(sd, "decoder.0.mlp.",
+                                            OMod.layer_norm(sd, "decoder.0.norm_mlp.ln.", pooled), 2)
+        g_ref = OMod.mish(OMod.linear(sd, "decoder_linear.", pooled))
+        assert_bf16_close(enc[valid], enc_ref, _scale(enc_ref), "ESA enc (valid rows)")
+    else:
+        bias = OM.edge_bias_padded(gb.edge_index, gid, gb.num_graphs, n, dtype=torch.float64)
+
+        def m_attn(sd_, pre, x):
+            return OMod.mab_padded(sd_, pre, x, x, H, bias)
+
+        def s_attn(sd_, pre, x):
+            return OMod.mab_padded(sd_, pre, x, x, H)
+
+        xd = X.double()
+        h = OMod.sab_complete(sd, "encoder.0.", xd, H, m_attn, 2)
+        h = OMod.sab_complete(sd, "encoder.1.", h, H, s_attn, 2)
+        enc_ref = h + xd
+        hn = OMod.layer_norm(sd, "decoder.0.norm.ln.", enc_ref)
+        S = OMod._p(sd, "decoder.0.pma.", "S").repeat(gb.num_graphs, 1, 1)
+        pooled = OMod.mab_padded(sd, "decoder.0.pma.mab.", S, hn, H)
+        pooled = pooled + OMod.mlp_standard(sd, "decoder.0.mlp.",
+                                            OMod.layer_norm(sd, "decoder.0.norm_mlp.ln.", pooled), 2)
+        g_ref = OMod.mish(OMod.linear(sd, "decoder_linear.", pooled.mean(1)))
+        assert_bf16_close(enc, enc_ref, _scale(enc_ref), "ESA enc (all rows)")
+    assert_bf16_close(g_emb.reshape(g_ref.shape), g_ref, _scale(g_ref), "ESA graph embedding")
+
+
+def test_state_dict_names_match_reference_layout():
+    m = ML.ESA(num_outputs=4, dim_output=32, dim_hidden=[32, 32, 32], num_heads=[2, 2, 2], layer_types="MSP",
+               xformers_or_torch_attn="hip", use_mlps=True, mlp_hidden_size=64, mlp_type="gated_mlp")
+    names = set(m.state_dict())
+    for key in ("encoder.0.sab.mab.fc_q.weight", "encoder.0.norm.ln.weight", "encoder.1.mlp.mlp.0.fc1.weight",
+                "decoder.0.pma.S", "decoder.0.pma.mab.fc_o.bias", "decoder_linear.weight"):
+        assert key in names, key

@@ -1,0 +1,67 @@
+"""Host-side logic that needs no GPU: generators and the EdgeAdjacency descriptor."""
+import numpy as np
+import torch
+
+from mind_amd import generators
+from mind_amd.esa.packing import EdgeAdjacency, cu_seqlens_from_counts, nearest_multiple_of_8
+from oracle import packing as OP
+
+
+def test_radius_edges_definition():
+    rng = np.random.default_rng(0)
+    pos = rng.normal(scale=2.0, size=(40, 3))
+    e = generators.radius_edges(pos, 3.0)
+    d = np.linalg.norm(pos[:, None] - pos[None], axis=-1)
+    want = {(j, i) for i in range(40) for j in range(40) if i != j and d[j, i] <= 3.0}
+    assert set(map(tuple, e.T.tolist())) == want
+    # ordered by target then source
+    keys = e[1] * 1000 + e[0]
+    assert np.all(np.diff(keys) > 0)
+
+
+def test_radius_edges_cap_keeps_nearest():
+    rng = np.random.default_rng(1)
+    pos = rng.normal(scale=1.0, size=(60, 3))
+    e = generators.radius_edges(pos, 10.0, cap=5)
+    counts = np.bincount(e[1], minlength=60)
+    assert np.all(counts == 5)
+    d = np.linalg.norm(pos[:, None] - pos[None], axis=-1)
+    for i in range(60):
+        kept = e[0][e[1] == i]
+        order = np.lexsort((np.arange(60), d[i]))
+        order = order[order != i][:5]
+        assert set(kept) == set(order)
+
+
+def test_generators_are_deterministic_and_consistent():
+    a = generators.protein_like(seed=3, num_graphs=4)
+    b = generators.protein_like(seed=3, num_graphs=4)
+    assert np.array_equal(a.edge_index, b.edge_index)
+    assert a.num_tokens == int(a.edge_counts.sum()) == a.cu_seqlens[-1]
+    gid_of_edge = a.batch[a.edge_index[0]]
+    assert np.array_equal(gid_of_edge, np.repeat(np.arange(4), a.edge_counts))
+    assert np.all(a.batch[a.edge_index[0]] == a.batch[a.edge_index[1]])
+    assert not np.any(a.edge_index[0] == a.edge_index[1])
+    c = generators.protein_budget(seed=1, token_budget=20000)
+    assert c.num_tokens <= 20000
+    src, dst = generators.block_local_edges(0, num_nodes=4096, num_edges=10000)
+    assert np.all(src // 512 == dst // 512) and src.max() < 4096
+
+
+def test_edge_adjacency_descriptor_cpu():
+    gb, _ = generators.small_molecules(seed=2, num_graphs=5)
+    n = nearest_multiple_of_8(int(gb.edge_counts.max()) + 1)
+    ei = torch.as_tensor(gb.edge_index)
+    m = EdgeAdjacency.from_edge_index(ei, torch.as_tensor(gb.batch), gb.num_graphs, n)
+    assert np.array_equal(m.cu_seqlens.numpy(), gb.cu_seqlens)
+    gid = np.repeat(np.arange(gb.num_graphs), gb.edge_counts)
+    assert np.array_equal(m.position.numpy(), OP.positions(gid))
+    x = torch.randn(gb.num_graphs, n, 7)
+    packed = m.unpad(x)
+    dense, valid = OP.to_dense_batch(packed, gid, gb.num_graphs, n)
+    assert torch.equal(dense[valid], packed)
+    assert torch.equal(m.pad(packed)[valid], packed) and torch.all(m.pad(packed)[~valid] == 0)
+    src, dst = m.padded_nodes()
+    pad_ids = torch.cat([src[(~valid).reshape(-1)], dst[(~valid).reshape(-1)]])
+    assert torch.all(pad_ids < 0) and pad_ids.unique().numel() == pad_ids.numel()
+    assert torch.equal(cu_seqlens_from_counts(torch.tensor([2, 0, 3])), torch.tensor([0, 2, 2, 5], dtype=torch.int32))
