@@ -9,12 +9,14 @@ point raises.
 from __future__ import annotations
 
 import ctypes
+import os
 import threading
 from pathlib import Path
 
 import torch
 
-LIB_PATH = Path(__file__).resolve().parent / "lib" / "libesa_hip.so"
+# MIND_AMD_LIB selects another build of the library (same C ABI).
+LIB_PATH = Path(os.environ.get("MIND_AMD_LIB") or Path(__file__).resolve().parent / "lib" / "libesa_hip.so")
 
 ESA_F32 = 0
 ESA_BF16 = 1

@@ -135,8 +135,8 @@ DEVI void group_range(const int* cu_outer, const int* cu_inner, int nseg, int to
                       int& end) {
   const int last = min(t0 + kGroupTok - 1, total_outer - 1);
   const int s0 = seg_of(cu_outer, nseg, t0), s1 = seg_of(cu_outer, nseg, last);
-  beg = __builtin_amdgcn_readfirstlane(cu_inner[s0] >> 5);
-  end = max(beg, __builtin_amdgcn_readfirstlane((cu_inner[s1 + 1] + kTile - 1) >> 5));
+  beg = (cu_inner[s0] >> 5);
+  end = max(beg, ((cu_inner[s1 + 1] + kTile - 1) >> 5));
 }
 
 // The outer tile a wave owns: per-lane partner range and wave-level bounds.
@@ -167,11 +167,10 @@ DEVI OuterTile outer_tile(const int* cu_outer, const int* cu_inner, int nseg, in
   const int s0 = seg_of(cu_outer, nseg, o0), s1 = seg_of(cu_outer, nseg, last), s = seg_of(cu_outer, nseg, t.oc);
   t.plo = t.valid ? cu_inner[s] : 0;
   t.phi = t.valid ? cu_inner[s + 1] : 0;
-  // Wave-uniform values live in scalar registers (uniform branches).
-  t.plo_max = __builtin_amdgcn_readfirstlane(cu_inner[s1]);
-  t.phi_min = __builtin_amdgcn_readfirstlane(cu_inner[s0 + 1]);
-  t.pt_beg = __builtin_amdgcn_readfirstlane(cu_inner[s0] >> 5);
-  t.pt_end = max(t.pt_beg, __builtin_amdgcn_readfirstlane((cu_inner[s1 + 1] + kTile - 1) >> 5));
+  t.plo_max = cu_inner[s1];
+  t.phi_min = cu_inner[s0 + 1];
+  t.pt_beg = (cu_inner[s0] >> 5);
+  t.pt_end = max(t.pt_beg, ((cu_inner[s1 + 1] + kTile - 1) >> 5));
   return t;
 }
 
