@@ -46,7 +46,22 @@ def parse():
     ap.add_argument("--cpu-sample-graphs", type=int, default=3,
                     help="graphs of the batch timed on the CPU for the baseline")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain 1 GiB device-to-device copy three times (HBM counter calibration)")
     return ap.parse_args()
+
+
+def copy_calibration():
+    """A copy of known size: 1 GiB read + 1 GiB written per launch, for scaling FETCH_SIZE / WRITE_SIZE."""
+    import torch
+
+    n = 1 << 28   # fp32 elements = 1 GiB
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_read": 4 * n, "copy_bytes_written": 4 * n, "launches": 3}), flush=True)
 
 
 def cpu_baseline(gb, seed: int, n_graphs: int) -> dict:
@@ -92,6 +107,10 @@ def main():
               "The ESA attention batch shards by whole graphs with no exchange; run one process per GPU.",
               file=sys.stderr)
         sys.exit(2)
+
+    if args.copy_calibration:
+        copy_calibration()
+        return
 
     import numpy as np
     import torch
