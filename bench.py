@@ -22,6 +22,8 @@ import sys
 import time
 from pathlib import Path
 
+import numpy as np
+
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
@@ -46,6 +48,10 @@ def parse():
     ap.add_argument("--cpu-sample-graphs", type=int, default=3,
                     help="graphs of the batch timed on the CPU for the baseline")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--config", choices=["varlen", "masked", "gather"], default="varlen",
+                    help="varlen: configuration 1 (default, the headline metric); masked: configuration 2 "
+                         "(edge-masked MAB attention fwd+bwd); gather: configuration 3 (edge gather + CSR "
+                         "segment sum, HBM-bound)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy three times (HBM counter calibration)")
     return ap.parse_args()
@@ -111,16 +117,44 @@ def main():
     if args.copy_calibration:
         copy_calibration()
         return
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    {"varlen": bench_varlen, "masked": bench_masked, "gather": bench_gather}[args.config](args)
 
+
+def timed(step, steps: int, warmup: int):
+    """Run warm-up steps, then time `steps` steps with HIP events and the per-kernel profiling hook."""
+    import torch
+
+    from mind_amd import _lib
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    _lib.profile_enable(True)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    ev0.record()
+    for _ in range(steps):
+        step()
+    ev1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    _lib.profile_enable(False)
+    kern = {name: {"avg_us": 1e3 * ms / n, "launches": n} for name, (ms, n) in _lib.profile_collect().items() if n}
+    return ev0.elapsed_time(ev1) / steps, 1e3 * wall / steps, kern
+
+
+def bench_varlen(args):
     import numpy as np
     import torch
 
     from mind_amd import _lib, generators
     from mind_amd.esa import attention
 
-    if not torch.cuda.is_available():
-        print("bench.py needs a GPU", file=sys.stderr)
-        sys.exit(1)
     dev = torch.device("cuda", 0)
     gb = generators.protein_like(seed=args.seed)
     cu_np = gb.cu_seqlens
@@ -136,31 +170,10 @@ def main():
         out, lse = attention.attn_fwd(q, k, v, cu, cu, maxlen, maxlen, scale)
         attention.attn_bwd(go, q, k, v, out, lse, cu, cu, maxlen, maxlen, scale)
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    _lib.profile_enable(True)
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    wall0 = time.perf_counter()
-    ev0.record()
-    for _ in range(args.steps):
-        step()
-    ev1.record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - wall0
-    _lib.profile_enable(False)
-    kern = _lib.profile_collect()
-    ms_per_step = ev0.elapsed_time(ev1) / args.steps
-
+    ms_per_step, wall_ms, per_kernel = timed(step, args.steps, args.warmup)
     tokens_per_s = t / (ms_per_step * 1e-3)
     total_flops = 14 * DIM * pairs
     tflops = total_flops / (ms_per_step * 1e-3) / 1e12
-
-    per_kernel = {}
-    for name, (ms, n) in kern.items():
-        if n:
-            per_kernel[name] = {"avg_us": 1e3 * ms / n, "launches": n}
     dom = max((n for n in FLOPS_PER_PAIR if n in per_kernel), key=lambda n: per_kernel[n]["avg_us"])
     dom_flops = FLOPS_PER_PAIR[dom] * pairs
     dom_avg_s = per_kernel[dom]["avg_us"] * 1e-6
@@ -195,13 +208,306 @@ def main():
         "mfma_util_pct": 100.0 * tflops / PEAK_BF16_TFLOPS,
         "achieved_tflops": tflops,
         "algorithmic_flops_per_step": total_flops,
-        "wall_ms_per_step": 1e3 * wall / args.steps,
+        "wall_ms_per_step": wall_ms,
         "kernels": per_kernel,
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": achieved, "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": achieved / PEAK_BF16_TFLOPS, "traffic": traffic},
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(gb, args.seed, args.cpu_sample_graphs)
+    print(json.dumps(result), flush=True)
+
+
+def edge_mask_stats(src: np.ndarray, dst: np.ndarray, cu: np.ndarray, tile: int = 32) -> dict:
+    """Exact pair count of the share-an-endpoint mask and its 32x32 tile occupancy, per graph.
+
+    nnz = #{(i, j): i != j, {s_i, d_i} and {s_j, d_j} intersect}; tiles count
+    the (query tile, key tile) blocks of each graph with at least one such pair.
+    """
+    nnz = tiles_any = tiles_all = 0
+    for b in range(len(cu) - 1):
+        s, e = int(cu[b]), int(cu[b + 1])
+        if e == s:
+            continue
+        a, c = src[s:e], dst[s:e]
+        m = ((a[:, None] == a[None, :]) | (c[:, None] == c[None, :]) |
+             (a[:, None] == c[None, :]) | (c[:, None] == a[None, :]))
+        np.fill_diagonal(m, False)
+        nnz += int(m.sum())
+        nt = -(-(e - s) // tile)
+        pad = np.zeros((nt * tile, nt * tile), dtype=bool)
+        pad[: e - s, : e - s] = m
+        tiles_any += int(pad.reshape(nt, tile, nt, tile).any(axis=(1, 3)).sum())
+        tiles_all += nt * nt
+    return {"nnz": nnz, "tiles_nonempty": tiles_any, "tiles_total": tiles_all}
+
+
+def cpu_baseline_masked(gb, seed: int, n_graphs: int) -> dict:
+    """Oracle per-graph edge-masked attention fwd+bwd in fp32 on the host cores, bounded sample."""
+    import torch
+
+    from oracle import attention as oracle_attention
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    order = np.argsort(gb.edge_counts)
+    pick = sorted(set(int(order[int(i)]) for i in np.linspace(0, len(order) - 1, n_graphs)))
+    cu_all = gb.cu_seqlens.astype(np.int64)
+    idx = np.concatenate([np.arange(cu_all[b], cu_all[b + 1]) for b in pick])
+    lens = gb.edge_counts[pick]
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    src, dst = gb.edge_index[0][idx], gb.edge_index[1][idx]
+    t = int(cu[-1])
+    g = torch.Generator().manual_seed(seed + 99)
+    q, k, v, go = (torch.randn(t, HEADS, HEAD_DIM, generator=g) for _ in range(4))
+
+    def step():
+        oracle_attention.varlen_attention(q, k, v, cu, cu, 0.25, src, dst, dtype=torch.float32)
+        oracle_attention.varlen_attention_bwd(go, q, k, v, cu, cu, 0.25, src, dst, dtype=torch.float32)
+
+    step()
+    times = []
+    budget = time.perf_counter() + 12.0
+    while len(times) < 3 or (time.perf_counter() < budget and len(times) < 20):
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    return {"value": t / med, "unit": "edge-tokens/s", "cores": cores, "kind": "port",
+            "sample": (f"oracle fp32 per-graph edge-masked attention fwd+bwd (torch CPU, {cores} threads; the mask "
+                       f"built per graph from src/dst) on {len(pick)} graphs of the batch ({t} tokens, lengths "
+                       f"{lens.tolist()}), median of {len(times)} runs")}
+
+
+def bench_masked(args):
+    """Configuration 2: edge-masked attention fwd+bwd on a 65,536-edge-token budget batch.
+
+    The timed step is the attention kernels with the on-the-fly edge mask; the
+    full SAB block (projections, attention, fc_o + mish) fwd+bwd on the same
+    batch is timed after it and reported beside.
+    """
+    import torch
+
+    from mind_amd import generators
+    from mind_amd.esa import attention
+    from mind_amd.esa.mha import SAB
+    from mind_amd.esa.packing import EdgeAdjacency, nearest_multiple_of_8
+
+    dev = torch.device("cuda", 0)
+    gb = generators.protein_budget(seed=args.seed, token_budget=65536)
+    cu_np = gb.cu_seqlens
+    t = int(cu_np[-1])
+    src_np, dst_np = gb.edge_index[0].astype(np.int32), gb.edge_index[1].astype(np.int32)
+    stats = edge_mask_stats(src_np, dst_np, cu_np)
+    g = torch.Generator().manual_seed(args.seed)
+    q, k, v, go = (torch.randn(t, HEADS, HEAD_DIM, generator=g).to(torch.bfloat16).to(dev) for _ in range(4))
+    cu = torch.as_tensor(cu_np).to(dev)
+    src, dst = torch.as_tensor(src_np).to(dev), torch.as_tensor(dst_np).to(dev)
+    maxlen = gb.max_seqlen
+    scale = 1.0 / HEAD_DIM ** 0.5
+
+    def step():
+        out, lse = attention.attn_fwd(q, k, v, cu, cu, maxlen, maxlen, scale, src, dst)
+        attention.attn_bwd(go, q, k, v, out, lse, cu, cu, maxlen, maxlen, scale, src, dst)
+
+    ms_per_step, wall_ms, per_kernel = timed(step, args.steps, args.warmup)
+    eff_flops = 14 * DIM * stats["nnz"]
+    exec_flops = 14 * DIM * stats["tiles_nonempty"] * 32 * 32
+    tflops = eff_flops / (ms_per_step * 1e-3) / 1e12
+    masked = {n + "_masked": f for n, f in FLOPS_PER_PAIR.items()}
+    dom = max((n for n in masked if n in per_kernel), key=lambda n: per_kernel[n]["avg_us"])
+    achieved = masked[dom] * stats["nnz"] / (per_kernel[dom]["avg_us"] * 1e-6) / 1e12
+
+    # the SAB block on the same batch: padded [B, N, 256] input, EdgeAdjacency mask
+    n_max = nearest_multiple_of_8(maxlen)
+    ei = torch.as_tensor(gb.edge_index).to(dev)
+    bm = torch.as_tensor(gb.batch).to(dev)
+    adj = EdgeAdjacency.from_edge_index(ei, bm, gb.num_graphs, n_max)
+    torch.manual_seed(args.seed)
+    sab = SAB(DIM, DIM, HEADS, 0.0, "hip").to(dev)
+    x = torch.zeros(gb.num_graphs * n_max, DIM, device=dev)
+    x[adj.padded_index] = torch.randn(t, DIM, device=dev)
+    x = x.view(gb.num_graphs, n_max, DIM).requires_grad_(True)
+    gy = torch.randn(gb.num_graphs, n_max, DIM, device=dev)
+
+    def block_step():
+        y = sab(x, adj)
+        y.backward(gy)
+
+    block_ms, _, _ = timed(block_step, max(5, args.steps // 5), max(2, args.warmup // 5))
+
+    result = {
+        "metric": "edge-tokens/sec through ESA attn fwd+bwd; MFMA util % of bf16 peak",
+        "value": t / (ms_per_step * 1e-3),
+        "unit": "edge-tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded lognormal protein-like graphs packed to a 65,536 edge-token budget; "
+                "q, k, v, dO ~ N(0,1))",
+        "config": {
+            "workload": "config2: edge-masked attention fwd+bwd (mask evaluated from src/dst in the tile loop)",
+            "graphs": gb.num_graphs, "edge_tokens": t, "max_seqlen": maxlen, "sum_L2": gb.sum_sq,
+            "mask_nnz": stats["nnz"], "mask_density": stats["nnz"] / gb.sum_sq,
+            "tiles_nonempty": stats["tiles_nonempty"], "tiles_total": stats["tiles_total"],
+            "heads": HEADS, "head_dim": HEAD_DIM, "dim": DIM, "seed": args.seed,
+        },
+        "mfma_util_pct": 100.0 * tflops / PEAK_BF16_TFLOPS,
+        "achieved_tflops_effective": tflops,
+        "achieved_tflops_executed_tiles": exec_flops / (ms_per_step * 1e-3) / 1e12,
+        "wall_ms_per_step": wall_ms,
+        "kernels": per_kernel,
+        "roofline": {"bound": "mfma", "kernel": dom, "achieved": achieved, "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": achieved / PEAK_BF16_TFLOPS, "traffic": None,
+                     "flops": "effective (nnz of the mask)"},
+        "sab_block": {"ms_per_step": block_ms, "edge_tokens_per_s": t / (block_ms * 1e-3),
+                      "what": "SAB(256, 256, 16 heads, 'hip') fwd+bwd incl. projections, fc_o + mish, padded "
+                              f"[{gb.num_graphs}, {n_max}, {DIM}] fp32 input"},
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline_masked(gb, args.seed, args.cpu_sample_graphs)
+    print(json.dumps(result), flush=True)
+
+
+GATHER_N, GATHER_E, GATHER_F, GATHER_BLOCK = 1 << 21, 1 << 25, 256, 512
+
+
+def gather_bytes(e: int, n: int, f: int, s: int) -> dict:
+    """Compulsory HBM bytes: gather writes E*2F, reads each node row once and both index arrays;
+    the segment sum reads E*F and indptr, writes N*F."""
+    return {"edge_gather": e * 2 * f * s + n * f * s + 8 * e,
+            "segment_sum": e * f * s + n * f * s + 4 * (n + 1)}
+
+
+def cpu_baseline_gather(src, dst, seed: int, slice_edges: int) -> dict:
+    """Oracle gather + fp32 sequential segment sum on a dst-sorted slice, scaled to GB/s of algorithmic bytes."""
+    from oracle import edges as oracle_edges
+
+    rng = np.random.default_rng(seed + 7)
+    lo = int(dst[0])
+    s, d = src[:slice_edges].astype(np.int64), dst[:slice_edges].astype(np.int64)
+    hi = int(d[-1]) + 1
+    nodes = hi - lo
+    x = rng.standard_normal((int(max(s.max(), d.max())) + 1, GATHER_F), dtype=np.float32)
+    y = rng.standard_normal((slice_edges, GATHER_F), dtype=np.float32)
+    indptr = np.concatenate([[0], np.cumsum(np.bincount(d - lo, minlength=nodes))])
+    bytes_ = gather_bytes(slice_edges, nodes, GATHER_F, 4)
+    total = bytes_["edge_gather"] + bytes_["segment_sum"]
+
+    def step():
+        oracle_edges.edge_gather(x, s, d)
+        oracle_edges.segment_sum_sequential(y, None, indptr)
+
+    step()
+    times = []
+    budget = time.perf_counter() + 12.0
+    while len(times) < 3 or (time.perf_counter() < budget and len(times) < 10):
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    return {"value": total / med / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": (f"oracle numpy gather [x[src] || x[dst]] + fp32 sequential CSR segment sum (single thread) on "
+                       f"the first {slice_edges} dst-sorted edges ({nodes} nodes), fp32, median of {len(times)} runs; "
+                       f"GB/s of the same algorithmic bytes, so the full-size time scales linearly")}
+
+
+def bench_gather(args):
+    """Configuration 3: edge-token gather and CSR segment sum at 2^21 nodes x 2^25 edges x 256 features."""
+    import torch
+
+    from mind_amd import generators
+    from mind_amd.edges import CSR, _gather_raw, segment_sum_csr
+
+    dev = torch.device("cuda", 0)
+    src_np, dst_np = generators.block_local_edges(seed=args.seed, num_nodes=GATHER_N, num_edges=GATHER_E,
+                                                  block=GATHER_BLOCK)
+    src_gen, dst_gen = torch.as_tensor(src_np).to(dev), torch.as_tensor(dst_np).to(dev)
+    del src_np, dst_np
+    # canonical order: edges sorted by dst (the CSR order); the sort itself is timed separately
+    csr = CSR.build(dst_gen, GATHER_N)
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(5):
+        CSR.build(dst_gen, GATHER_N)
+    ev1.record()
+    torch.cuda.synchronize()
+    csr_ms = ev0.elapsed_time(ev1) / 5
+    src = src_gen.index_select(0, csr.perm.long()).contiguous()
+    dst = dst_gen.index_select(0, csr.perm.long()).contiguous()
+    indptr = csr.indptr
+
+    results = {}
+    for dtype, name in ((torch.float32, "f32"), (torch.bfloat16, "bf16")):
+        s = torch.tensor([], dtype=dtype).element_size()
+        g = torch.Generator(device=dev).manual_seed(args.seed)
+        x = torch.randn(GATHER_N, GATHER_F, device=dev, generator=g).to(dtype)
+        y = torch.randn(GATHER_E, GATHER_F, device=dev, generator=g).to(dtype)
+        out = torch.empty(GATHER_E, 2 * GATHER_F, device=dev, dtype=dtype)
+        agg = torch.empty(GATHER_N, GATHER_F, device=dev, dtype=dtype)
+
+        def step():
+            _gather_raw(x, src, dst, out)
+            segment_sum_csr(y, indptr, out=agg)
+
+        ms, wall_ms, kern = timed(step, args.steps, args.warmup)
+        by = gather_bytes(GATHER_E, GATHER_N, GATHER_F, s)
+        for kname, b in by.items():
+            if kname in kern:
+                kern[kname]["algorithmic_bytes"] = b
+                kern[kname]["achieved_gbs"] = b / (kern[kname]["avg_us"] * 1e-6) / 1e9
+        # generation order: gather with the unsorted indices, segment sum through perm
+
+        def step_gen():
+            _gather_raw(x, src_gen, dst_gen, out)
+            segment_sum_csr(y, indptr, csr.perm, out=agg)
+
+        ms_gen, _, kern_gen = timed(step_gen, max(5, args.steps // 2), 2)
+        results[name] = {"ms_per_step": ms, "wall_ms_per_step": wall_ms, "kernels": kern,
+                         "gb_per_s": (by["edge_gather"] + by["segment_sum"]) / (ms * 1e-3) / 1e9,
+                         "generation_order": {"ms_per_step": ms_gen, "kernels": kern_gen}}
+        del x, y, out, agg
+        torch.cuda.empty_cache()
+
+    f32 = results["f32"]
+    dom = max(("edge_gather", "segment_sum"), key=lambda n: f32["kernels"][n]["avg_us"])
+    achieved = f32["kernels"][dom]["achieved_gbs"]
+    traffic = None
+    tfile = ROOT / "profiles" / f"{dom}_config3_traffic.json"
+    if tfile.exists():
+        traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
+    result = {
+        "metric": "GB/s of algorithmic HBM bytes through edge gather + CSR segment sum",
+        "value": f32["gb_per_s"],
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": f32["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded block-local edges; x, y ~ N(0,1))",
+        "config": {
+            "workload": "config3: edge gather [x[src] || x[dst]] + deterministic CSR segment sum to dst",
+            "nodes": GATHER_N, "edges": GATHER_E, "features": GATHER_F, "block": GATHER_BLOCK,
+            "order": "dst-sorted (CSR); generation order reported beside", "seed": args.seed,
+        },
+        "csr_build_ms": csr_ms,
+        "f32": f32,
+        "bf16": results["bf16"],
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": achieved / PEAK_HBM_GBS, "traffic": traffic},
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline_gather(src.cpu().numpy(), dst.cpu().numpy(), args.seed, 1 << 18)
     print(json.dumps(result), flush=True)
 
 

@@ -174,18 +174,83 @@ DEVI OuterTile outer_tile(const int* cu_outer, const int* cu_inner, int nseg, in
   return t;
 }
 
-// First partner tile >= x that some wave of the block needs (masked mode
-// skips tiles whose node sets cannot meet any of the block's four tiles).
-template <bool MASKED>
-DEVI int next_needed(int x, int end, const int4* meta, const int4 gm[kWaves]) {
-  if (!MASKED) return x;
-  for (; x < end; ++x) {
+// Masked mode visits only the partner tiles whose node sets may meet one of
+// the block's four outer tiles.  The block tests up to kListCap partner tiles
+// at once (one per thread) and compacts the survivors, in ascending order,
+// into an LDS list; an entry is the tile index plus, in bits 28..31, which
+// waves' outer tiles it may touch.  Tile indices are < 2^21 (check_common
+// bounds total * heads * 32 bytes by 2^31).
+constexpr int kListCap = 256;
+constexpr uint32_t kPtMask = (1u << 28) - 1;
+
+struct TileList {
+  uint32_t entry[kListCap];
+  int count[kWaves];
+};
+
+DEVI int build_list(TileList& tl, int base, int end, const int4* __restrict__ meta, const int4 gm[kWaves],
+                    int tid) {
+  const int x = base + tid;
+  uint32_t bits = 0;
+  if (x < end) {
     const int4 m = meta[x];
-    if (tiles_may_touch(gm[0], m) | tiles_may_touch(gm[1], m) | tiles_may_touch(gm[2], m) |
-        tiles_may_touch(gm[3], m))
-      break;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) bits |= (uint32_t)tiles_may_touch(gm[w], m) << w;
   }
-  return x;
+  const unsigned long long bal = __ballot(bits != 0);
+  const int lane = tid & 63, wave = tid >> 6;
+  const int before = __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+  if (lane == 0) tl.count[wave] = __popcll(bal);
+  __syncthreads();
+  int off = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) off += w < wave ? tl.count[w] : 0;
+  const int n = tl.count[0] + tl.count[1] + tl.count[2] + tl.count[3];
+  if (bits) tl.entry[off + before] = (uint32_t)x | (bits << 28);
+  __syncthreads();
+  return n;
+}
+
+// Double-buffered walk over the partner tiles [gbeg, gend) of a block:
+// gload(pt) fetches a tile's staging registers, lstore(buf, regs) writes them
+// to LDS buffer `buf`, body(pt, buf, waves) consumes a staged tile (`waves`
+// = the wave mask that may need it).  One barrier per tile.
+template <bool MASKED, class Load, class Store, class Body>
+DEVI void tile_loop(int gbeg, int gend, const int4* __restrict__ meta, const int4 gm[kWaves], TileList& tl,
+                    int tid, Load gload, Store lstore, Body body) {
+  if (!MASKED) {
+    int pt = gbeg;
+    i32x4 stg = {0, 0, 0, 0};
+    if (pt < gend) stg = gload(pt);
+    lstore(0, stg);
+    __syncthreads();
+    for (int cur = 0; pt < gend; cur ^= 1) {
+      const int nxt = pt + 1;
+      if (nxt < gend) stg = gload(nxt);
+      body(pt, cur, 0xfu);
+      if (nxt < gend) lstore(cur ^ 1, stg);
+      __syncthreads();
+      pt = nxt;
+    }
+    return;
+  }
+  for (int base = gbeg; base < gend; base += kListCap) {
+    const int n = build_list(tl, base, gend, meta, gm, tid);
+    if (n == 0) continue;
+    uint32_t e = tl.entry[0];
+    i32x4 stg = gload((int)(e & kPtMask));
+    lstore(0, stg);
+    __syncthreads();
+    for (int i = 0, cur = 0; i < n; ++i, cur ^= 1) {
+      const bool more = i + 1 < n;
+      const uint32_t en = more ? tl.entry[i + 1] : 0u;
+      if (more) stg = gload((int)(en & kPtMask));
+      body((int)(e & kPtMask), cur, e >> 28);
+      if (more) lstore(cur ^ 1, stg);
+      __syncthreads();
+      e = en;
+    }
+  }
 }
 
 struct AttnArgs {
@@ -209,6 +274,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const AttnArgs a) {
   __shared__ __align__(16) bf16 sK[2][kTile * kRowStride];   // K rows [key][16]
   __shared__ __align__(16) bf16 sVT[2][32 * kTrStride];      // [V^T ; 1]: rows 0..15 dims, 16..31 ones
   __shared__ __align__(16) int2 sN[2][kTile];
+  __shared__ TileList sL;
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 31, half = lane >> 5;
   const int H = a.heads;
@@ -225,13 +291,12 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const AttnArgs a) {
   const OuterTile ot = outer_tile(a.cu_q, a.cu_k, a.nseg, a.total_q, t0 + wave * kTile, col);
   const bf16x8 qf = *reinterpret_cast<const bf16x8*>(a.q + ((size_t)ot.oc * H + head) * kHd + 8 * half);
   int2 qn = make_int2(0, 0);
-  int4 gm[kWaves], own_meta = no_touch();
+  int4 gm[kWaves];
   if (MASKED) {
     qn = a.nodes[ot.oc];
     const int tile0 = t0 / kTile;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) gm[w] = (t0 + w * kTile < a.total_q) ? a.meta[tile0 + w] : no_touch();
-    own_meta = (t0 + wave * kTile < a.total_q) ? a.meta[tile0 + wave] : no_touch();
   }
 
   // Reference point b = c |q| max|k| over the keys this wave visits.
@@ -280,15 +345,8 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const AttnArgs a) {
   auto run = [&](auto online_tag) {
     constexpr bool ONLINE = decltype(online_tag)::value;
     const f32x16 zero = {};
-    int pt = next_needed<MASKED>(gbeg, gend, a.meta, gm);
-    i32x4 stg = {0, 0, 0, 0};
-    if (pt < gend) stg = gload(pt);
-    lstore(0, stg);
-    __syncthreads();
-    for (int cur = 0; pt < gend; cur ^= 1) {
-      const int nxt = next_needed<MASKED>(pt + 1, gend, a.meta, gm);
-      if (nxt < gend) stg = gload(nxt);
-      if (pt >= ot.pt_beg && pt < ot.pt_end && (!MASKED || tiles_may_touch(own_meta, a.meta[pt]))) {
+    tile_loop<MASKED>(gbeg, gend, a.meta, gm, sL, tid, gload, lstore, [&](int pt, int cur, uint32_t waves) {
+      if (((waves >> wave) & 1u) && pt >= ot.pt_beg && pt < ot.pt_end) {
         const int k0 = pt * kTile;
         f32x16 s = mfma32(lds8(&sK[cur][kperm(col) * kRowStride + 8 * half]), qf, zero);
         const bool full = !MASKED && k0 >= ot.plo_max && k0 + kTile <= ot.phi_min;
@@ -323,10 +381,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const AttnArgs a) {
         acc = mfma32(lds8(&sVT[cur][col * kTrStride + 8 * half]), cvt8(p), acc);
         acc = mfma32(lds8(&sVT[cur][col * kTrStride + 16 + 8 * half]), cvt8(p + 8), acc);
       }
-      if (nxt < gend) lstore(cur ^ 1, stg);
-      __syncthreads();
-      pt = nxt;
-    }
+    });
   };
   if (fixed_ref)
     run(std::integral_constant<bool, false>{});
@@ -349,6 +404,7 @@ __global__ __launch_bounds__(256) void attn_dq_kernel(const AttnArgs a) {
   __shared__ __align__(16) bf16 sV[2][kTile * kRowStride];    // V rows
   __shared__ __align__(16) bf16 sKT[2][16 * kTrStride];       // K^T
   __shared__ __align__(16) int2 sN[2][kTile];
+  __shared__ TileList sL;
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 31, half = lane >> 5;
   const int H = a.heads;
@@ -373,13 +429,12 @@ __global__ __launch_bounds__(256) void attn_dq_kernel(const AttnArgs a) {
 #pragma unroll
   for (int r = 0; r < 16; ++r) cd[r] = -dsum;
   int2 qn = make_int2(0, 0);
-  int4 gm[kWaves], own_meta = no_touch();
+  int4 gm[kWaves];
   if (MASKED) {
     qn = a.nodes[ot.oc];
     const int tile0 = t0 / kTile;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) gm[w] = (t0 + w * kTile < a.total_q) ? a.meta[tile0 + w] : no_touch();
-    own_meta = (t0 + wave * kTile < a.total_q) ? a.meta[tile0 + wave] : no_touch();
   }
 
   const rsrc_t rsrc = make_rsrc(wave == 0 ? (const void*)a.k : (const void*)a.v, (uint32_t)a.total_k * H * kHd * 2);
@@ -407,15 +462,8 @@ __global__ __launch_bounds__(256) void attn_dq_kernel(const AttnArgs a) {
 
   f32x16 acc = {};
   const f32x16 zero = {};
-  int pt = next_needed<MASKED>(gbeg, gend, a.meta, gm);
-  i32x4 stg = {0, 0, 0, 0};
-  if (pt < gend) stg = gload(pt);
-  lstore(0, stg);
-  __syncthreads();
-  for (int cur = 0; pt < gend; cur ^= 1) {
-    const int nxt = next_needed<MASKED>(pt + 1, gend, a.meta, gm);
-    if (nxt < gend) stg = gload(nxt);
-    if (pt >= ot.pt_beg && pt < ot.pt_end && (!MASKED || tiles_may_touch(own_meta, a.meta[pt]))) {
+  tile_loop<MASKED>(gbeg, gend, a.meta, gm, sL, tid, gload, lstore, [&](int pt, int cur, uint32_t waves) {
+    if (((waves >> wave) & 1u) && pt >= ot.pt_beg && pt < ot.pt_end) {
       const int k0 = pt * kTile;
       f32x16 s = mfma32(lds8(&sK[cur][kperm(col) * kRowStride + 8 * half]), qf, zero);
       const f32x16 dp = mfma32(lds8(&sV[cur][kperm(col) * kRowStride + 8 * half]), dof, cd);  // dP^T - D
@@ -438,10 +486,7 @@ __global__ __launch_bounds__(256) void attn_dq_kernel(const AttnArgs a) {
       acc = mfma32(lds8(&sKT[cur][trow]), cvt8(ds), acc);
       acc = mfma32(lds8(&sKT[cur][trow + 16]), cvt8(ds + 8), acc);
     }
-    if (nxt < gend) lstore(cur ^ 1, stg);
-    __syncthreads();
-    pt = nxt;
-  }
+  });
   if (!ot.valid) return;
   store_rows8(a.dq + ((size_t)ot.oi * H + head) * kHd, acc, a.scale, half);
 }
@@ -456,6 +501,7 @@ __global__ __launch_bounds__(256) void attn_dkdv_kernel(const AttnArgs a) {
   __shared__ __align__(16) bf16 sDOT[2][16 * kTrStride];      // dO^T
   __shared__ __align__(16) uint2 sAux[2][kTile];              // row-statistic MFMA operands
   __shared__ __align__(16) int2 sN[2][kTile];
+  __shared__ TileList sL;
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 31, half = lane >> 5;
   const int H = a.heads;
@@ -473,13 +519,12 @@ __global__ __launch_bounds__(256) void attn_dkdv_kernel(const AttnArgs a) {
   bf16x8 ones2 = {};
   if (half == 0) { ones2[0] = (bf16)1.f; ones2[1] = (bf16)1.f; }
   int2 kn = make_int2(0, 0);
-  int4 gm[kWaves], own_meta = no_touch();
+  int4 gm[kWaves];
   if (MASKED) {
     kn = a.nodes[ot.oc];
     const int tile0 = t0 / kTile;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) gm[w] = (t0 + w * kTile < a.total_k) ? a.meta[tile0 + w] : no_touch();
-    own_meta = (t0 + wave * kTile < a.total_k) ? a.meta[tile0 + wave] : no_touch();
   }
 
   // Staging roles: wave 0 Q rows (+ Q^T), wave 1 dO rows (+ dO^T),
@@ -515,15 +560,8 @@ __global__ __launch_bounds__(256) void attn_dkdv_kernel(const AttnArgs a) {
 
   f32x16 dva = {}, dka = {};
   const f32x16 zero = {};
-  int pt = next_needed<MASKED>(gbeg, gend, a.meta, gm);
-  i32x4 stg = {0, 0, 0, 0};
-  if (pt < gend) stg = gload(pt);
-  lstore(0, stg);
-  __syncthreads();
-  for (int cur = 0; pt < gend; cur ^= 1) {
-    const int nxt = next_needed<MASKED>(pt + 1, gend, a.meta, gm);
-    if (nxt < gend) stg = gload(nxt);
-    if (pt >= ot.pt_beg && pt < ot.pt_end && (!MASKED || tiles_may_touch(own_meta, a.meta[pt]))) {
+  tile_loop<MASKED>(gbeg, gend, a.meta, gm, sL, tid, gload, lstore, [&](int pt, int cur, uint32_t waves) {
+    if (((waves >> wave) & 1u) && pt >= ot.pt_beg && pt < ot.pt_end) {
       const int q0 = pt * kTile;
       const int rrow = kperm(col) * kRowStride + 8 * half;
       const uint2 ax = sAux[cur][kperm(col)];
@@ -556,10 +594,7 @@ __global__ __launch_bounds__(256) void attn_dkdv_kernel(const AttnArgs a) {
       dka = mfma32(lds8(&sQT[cur][trow]), cvt8(ds), dka);
       dka = mfma32(lds8(&sQT[cur][trow + 16]), cvt8(ds + 8), dka);
     }
-    if (nxt < gend) lstore(cur ^ 1, stg);
-    __syncthreads();
-    pt = nxt;
-  }
+  });
   if (!ot.valid) return;
   store_rows8(a.dv + ((size_t)ot.oi * H + head) * kHd, dva, 1.f, half);
   store_rows8(a.dk + ((size_t)ot.oi * H + head) * kHd, dka, a.scale, half);

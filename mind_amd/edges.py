@@ -57,10 +57,12 @@ class CSR:
         return cls(indptr, perm, num_nodes)
 
 
-def segment_sum_csr(y: torch.Tensor, indptr: torch.Tensor, perm: torch.Tensor | None = None) -> torch.Tensor:
+def segment_sum_csr(y: torch.Tensor, indptr: torch.Tensor, perm: torch.Tensor | None = None,
+                    out: torch.Tensor | None = None) -> torch.Tensor:
     """out[n] = sum of rows y[perm[i]] (or y[i]) for i in [indptr[n], indptr[n+1]).
 
     fp32 accumulation in ascending i, one rounding at the end: deterministic.
+    ``out`` ([N, F], dtype of y, contiguous) is written in place when given.
     """
     _lib.require_gpu(y, indptr, perm)
     if y.dim() != 2:
@@ -69,18 +71,27 @@ def segment_sum_csr(y: torch.Tensor, indptr: torch.Tensor, perm: torch.Tensor | 
     indptr = _as_index(indptr, "indptr")
     perm = None if perm is None else _as_index(perm, "perm")
     n = indptr.numel() - 1
-    out = torch.empty((n, y.shape[1]), dtype=y.dtype, device=y.device)
+    out = _output(out, (n, y.shape[1]), y)
     rc = _lib.load().esa_csr_segment_sum(y.data_ptr(), _lib.ptr(perm), indptr.data_ptr(), n, y.shape[1],
                                          _dtype_code(y), out.data_ptr(), _lib.stream_of(y))
     _lib.check(rc, "esa_csr_segment_sum")
     return out
 
 
-def _gather_raw(x: torch.Tensor, src: torch.Tensor, dst: torch.Tensor) -> torch.Tensor:
+def _output(out: torch.Tensor | None, shape: tuple, like: torch.Tensor) -> torch.Tensor:
+    if out is None:
+        return torch.empty(shape, dtype=like.dtype, device=like.device)
+    if tuple(out.shape) != tuple(shape) or out.dtype != like.dtype or out.device != like.device \
+            or not out.is_contiguous():
+        raise ValueError(f"out must be a contiguous {like.dtype} tensor of shape {tuple(shape)} on {like.device}")
+    return out
+
+
+def _gather_raw(x: torch.Tensor, src: torch.Tensor, dst: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     _lib.require_gpu(x, src, dst)
     x = x.contiguous()
     e = src.numel()
-    out = torch.empty((e, 2 * x.shape[1]), dtype=x.dtype, device=x.device)
+    out = _output(out, (e, 2 * x.shape[1]), x)
     rc = _lib.load().esa_edge_gather(x.data_ptr(), src.data_ptr(), dst.data_ptr(), e, x.shape[0], x.shape[1],
                                      _dtype_code(x), out.data_ptr(), _lib.stream_of(x))
     _lib.check(rc, "esa_edge_gather")
