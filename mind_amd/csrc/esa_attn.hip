@@ -61,7 +61,7 @@ constexpr int kGroupTok = kWaves * kTile;   // 128 tokens per block
 constexpr int kRowStride = 24;              // bf16 per row of a [32 tokens][16] LDS tile (48 B)
 constexpr int kTrStride = 40;               // bf16 per row of a [rows][32 tokens] LDS tile (80 B)
 constexpr float kStaticBound = 60.f;
-constexpr float kDeadRow = -1.0e30f;        // -LSE/c for rows without keys: every exp2 underflows to 0
+constexpr float kDeadRow = -1.0e30f;        // -LSE2/c for rows without keys: every exp2 underflows to 0
 
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 typedef int i32x4 __attribute__((ext_vector_type(4)));
@@ -112,6 +112,25 @@ DEVI bf16x8 cvt8(const float* p) {
 
 DEVI bf16x8 lds8(const bf16* p) { return *reinterpret_cast<const bf16x8*>(p); }
 
+// c * x as an unevaluated pair of bf16 vectors (hi + lo carries ~16
+// significant bits): two MFMAs with hi and lo give c * (a . x) in fp32
+// without a VALU multiply per score.
+DEVI void split_scaled(const bf16x8& x, float c, bf16x8& hi, bf16x8& lo) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float v = (float)x[e] * c;
+    hi[e] = (bf16)v;
+    lo[e] = (bf16)(v - (float)hi[e]);
+  }
+}
+
+DEVI f32x16 splat16(float x) {
+  f32x16 r;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) r[i] = x;
+  return r;
+}
+
 // Node pairs of the 16 partner tokens of a half-wave's accumulator rows
 // (tile-local 16(r>>3) + 8h + (r&7)), from an LDS tile of 32 node pairs.
 DEVI void lds_nodes16(const int2* sn, int half, int2 out[16]) {
@@ -150,106 +169,164 @@ struct OuterTile {
   int pt_beg, pt_end;  // partner tiles this wave visits
 };
 
-DEVI OuterTile outer_tile(const int* cu_outer, const int* cu_inner, int nseg, int total, int o0, int col) {
+DEVI int wave_reduce_max(int x) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) x = max(x, __shfl_xor(x, o));
+  return x;
+}
+DEVI int wave_reduce_min(int x) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) x = min(x, __shfl_xor(x, o));
+  return x;
+}
+
+// bounds[t] = partner range [cu_inner[s], cu_inner[s+1]) of token t's segment
+// s (precomputed once per call, so no kernel searches cu_seqlens).  Lanes
+// 32..63 mirror lanes 0..31.
+DEVI OuterTile outer_tile(const int2* __restrict__ bounds, int total, int o0, int col) {
   OuterTile t;
   t.oi = o0 + col;
   t.active = o0 < total;
   t.valid = t.oi < total;
-  t.oc = t.valid ? t.oi : total - 1;
-  if (!t.active) {
-    t.plo = t.phi = 0;
-    t.plo_max = INT_MAX;
-    t.phi_min = INT_MIN;
-    t.pt_beg = t.pt_end = 0;
-    return t;
-  }
-  const int last = min(o0 + kTile - 1, total - 1);
-  const int s0 = seg_of(cu_outer, nseg, o0), s1 = seg_of(cu_outer, nseg, last), s = seg_of(cu_outer, nseg, t.oc);
-  t.plo = t.valid ? cu_inner[s] : 0;
-  t.phi = t.valid ? cu_inner[s + 1] : 0;
-  t.plo_max = cu_inner[s1];
-  t.phi_min = cu_inner[s0 + 1];
-  t.pt_beg = (cu_inner[s0] >> 5);
-  t.pt_end = max(t.pt_beg, ((cu_inner[s1 + 1] + kTile - 1) >> 5));
+  t.oc = t.valid ? t.oi : max(total - 1, 0);
+  t.plo = t.phi = 0;
+  t.plo_max = INT_MAX;
+  t.phi_min = INT_MIN;
+  t.pt_beg = t.pt_end = 0;
+  if (!t.active) return t;
+  const int2 b = bounds[t.oc];
+  if (t.valid) { t.plo = b.x; t.phi = b.y; }
+  t.plo_max = wave_reduce_max(t.valid ? b.x : INT_MIN);
+  t.phi_min = wave_reduce_min(t.valid ? b.y : INT_MAX);
+  const int lo = wave_reduce_min(t.valid ? b.x : INT_MAX);
+  const int hi = wave_reduce_max(t.valid ? b.y : INT_MIN);
+  t.pt_beg = lo >> 5;
+  t.pt_end = max(t.pt_beg, (hi + kTile - 1) >> 5);
   return t;
 }
 
-// Masked mode visits only the partner tiles whose node sets may meet one of
-// the block's four outer tiles.  The block tests up to kListCap partner tiles
-// at once (one per thread) and compacts the survivors, in ascending order,
-// into an LDS list; an entry is the tile index plus, in bits 28..31, which
-// waves' outer tiles it may touch.  Tile indices are < 2^21 (check_common
-// bounds total * heads * 32 bytes by 2^31).
-constexpr int kListCap = 256;
-constexpr uint32_t kPtMask = (1u << 28) - 1;
-
-struct TileList {
-  uint32_t entry[kListCap];
-  int count[kWaves];
-};
-
-DEVI int build_list(TileList& tl, int base, int end, const int4* __restrict__ meta, const int4 gm[kWaves],
-                    int tid) {
-  const int x = base + tid;
-  uint32_t bits = 0;
-  if (x < end) {
-    const int4 m = meta[x];
+// Masked mode: keep accumulator row r of this lane (partner token
+// p0 + row_local(r, half)) only if the partner shares an endpoint with the
+// lane's own token, lies in the lane's segment and is not the token itself;
+// other rows become `off`.  Endpoint sharing is min over the four xors == 0
+// (plain VALU, no lane-mask juggling); segment bounds and the diagonal are
+// only tested on tiles that straddle a segment bound of the wave or hold the
+// wave's own tokens (o0 == p0), a wave-uniform branch.
+template <class Rows>
+DEVI void mask_rows(Rows& x, float off, const OuterTile& ot, int p0, int o0, int half, const int2* sn, int2 own) {
+  int2 pn[16];
+  lds_nodes16(sn, half, pn);
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) bits |= (uint32_t)tiles_may_touch(gm[w], m) << w;
+  for (int r = 0; r < 16; ++r) {
+    const uint32_t d = min(min((uint32_t)(pn[r].x ^ own.x), (uint32_t)(pn[r].x ^ own.y)),
+                           min((uint32_t)(pn[r].y ^ own.x), (uint32_t)(pn[r].y ^ own.y)));
+    x[r] = d == 0u ? x[r] : off;
   }
-  const unsigned long long bal = __ballot(bits != 0);
-  const int lane = tid & 63, wave = tid >> 6;
-  const int before = __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
-  if (lane == 0) tl.count[wave] = __popcll(bal);
-  __syncthreads();
-  int off = 0;
+  if (!(p0 >= ot.plo_max && p0 + kTile <= ot.phi_min) || p0 == o0) {
 #pragma unroll
-  for (int w = 0; w < kWaves; ++w) off += w < wave ? tl.count[w] : 0;
-  const int n = tl.count[0] + tl.count[1] + tl.count[2] + tl.count[3];
-  if (bits) tl.entry[off + before] = (uint32_t)x | (bits << 28);
-  __syncthreads();
-  return n;
+    for (int r = 0; r < 16; ++r) {
+      const int p = p0 + row_local(r, half);
+      x[r] = (p >= ot.plo && p < ot.phi && p != ot.oi) ? x[r] : off;
+    }
+  }
 }
 
-// Double-buffered walk over the partner tiles [gbeg, gend) of a block:
-// gload(pt) fetches a tile's staging registers, lstore(buf, regs) writes them
-// to LDS buffer `buf`, body(pt, buf, waves) consumes a staged tile (`waves`
-// = the wave mask that may need it).  One barrier per tile.
-template <bool MASKED, class Load, class Store, class Body>
-DEVI void tile_loop(int gbeg, int gend, const int4* __restrict__ meta, const int4 gm[kWaves], TileList& tl,
-                    int tid, Load gload, Store lstore, Body body) {
-  if (!MASKED) {
-    int pt = gbeg;
-    i32x4 stg = {0, 0, 0, 0};
-    if (pt < gend) stg = gload(pt);
-    lstore(0, stg);
-    __syncthreads();
-    for (int cur = 0; pt < gend; cur ^= 1) {
-      const int nxt = pt + 1;
-      if (nxt < gend) stg = gload(nxt);
-      body(pt, cur, 0xfu);
-      if (nxt < gend) lstore(cur ^ 1, stg);
-      __syncthreads();
-      pt = nxt;
-    }
-    return;
+// ---------------------------------------------------------------- tile walks
+//
+// Dense mode: the four waves of a block share every partner tile of their
+// 128-token group.  Each tile is loaded once per block, one staging role per
+// wave, into double-buffered LDS, with a block barrier per tile.
+//
+// Masked mode: each wave walks, on its own, only the partner tiles whose
+// node sets may meet its outer tile (node range and 64-bit signature test of
+// the per-tile metadata; 64 candidates per ballot), staging them into its own
+// double-buffered LDS region.  No block barrier: a wave never waits for
+// another wave's tiles.
+
+constexpr int kWaitVmem = 0x0F70;   // s_waitcnt vmcnt(0) expcnt(7) lgkmcnt(15) (gfx9 encoding)
+
+// LDS writes of one wave become visible to its other lanes in issue order;
+// the fences only keep the compiler from moving LDS accesses across.
+DEVI void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+DEVI void block_sync() { __syncthreads(); }
+
+// Walk over n partner tiles: next(waves) returns the next tile index (in
+// order; past the end it repeats the last one) and its wave mask,
+// gload(pt) fetches a tile's staging registers, lstore(buf, regs) writes
+// them to LDS buffer `buf`, body(pt, buf, waves) consumes a staged tile,
+// sync() orders LDS writes before reads.  Two LDS buffers and two tiles'
+// loads in flight: tile i+2 is requested before tile i is consumed and tile
+// i+1 is written to LDS after it.  Loads are issued unconditionally (past the
+// end they re-read the last tile and are not consumed) so each wait covers
+// exactly the older load; the loop is unrolled by two so the staging
+// registers never move (a register copy would wait for its load) and the
+// LDS buffer index is a constant in each half.
+template <class Next, class Load, class Store, class Sync, class Body>
+DEVI void tile_pipeline(int n, Next next, Load gload, Store lstore, Sync sync, Body body) {
+  if (n <= 0) return;
+  uint32_t w0 = 0, w1 = 0;
+  int p0 = next(w0);
+  const auto s0 = gload(p0);
+  int p1 = next(w1);
+  auto sb = gload(p1);
+  decltype(sb) sa;
+  lstore(0, s0);
+  sync();
+  for (int i = 0; i < n; i += 2) {
+    // buffer 0 holds tile i (p0, w0); sb is tile i+1 (p1, w1), in flight
+    uint32_t w2 = 0;
+    const int p2 = next(w2);
+    sa = gload(p2);
+    body(p0, 0, w0);
+    if (i + 1 < n) lstore(1, sb);
+    sync();
+    if (i + 1 >= n) break;
+    // buffer 1 holds tile i+1 (p1, w1); sa is tile i+2 (p2, w2), in flight
+    uint32_t w3 = 0;
+    const int p3 = next(w3);
+    sb = gload(p3);
+    body(p1, 1, w1);
+    if (i + 2 < n) lstore(0, sa);
+    sync();
+    p0 = p2; w0 = w2;
+    p1 = p3; w1 = w3;
   }
-  for (int base = gbeg; base < gend; base += kListCap) {
-    const int n = build_list(tl, base, gend, meta, gm, tid);
-    if (n == 0) continue;
-    uint32_t e = tl.entry[0];
-    i32x4 stg = gload((int)(e & kPtMask));
-    lstore(0, stg);
-    __syncthreads();
-    for (int i = 0, cur = 0; i < n; ++i, cur ^= 1) {
-      const bool more = i + 1 < n;
-      const uint32_t en = more ? tl.entry[i + 1] : 0u;
-      if (more) stg = gload((int)(en & kPtMask));
-      body((int)(e & kPtMask), cur, e >> 28);
-      if (more) lstore(cur ^ 1, stg);
-      __syncthreads();
-      e = en;
-    }
+}
+
+// Both walks start with every earlier vector-memory load complete: a
+// prologue load still pending inside the loop would be waited for with
+// vmcnt(0), which also waits for the prefetches in flight.
+template <class Load, class Store, class Body>
+DEVI void block_tile_walk(int gbeg, int gend, Load gload, Store lstore, Body body) {
+  __builtin_amdgcn_s_waitcnt(kWaitVmem);
+  const int n = gend - gbeg;
+  int i = 0;
+  tile_pipeline(n, [&](uint32_t& w) { w = 0xfu; const int p = gbeg + min(i, n - 1); ++i; return p; }, gload, lstore,
+                block_sync, body);
+}
+
+template <class Load, class Store, class Body>
+DEVI void wave_tile_walk(int pt_beg, int pt_end, int4 own, const int4* __restrict__ meta, int lane, Load gload,
+                         Store lstore, Body body) {
+  __builtin_amdgcn_s_waitcnt(kWaitVmem);
+  for (int base = pt_beg; base < pt_end; base += 64) {
+    const int x = base + lane;
+    bool need = false;
+    if (x < pt_end) need = tiles_may_touch(own, meta[x]);
+    unsigned long long bits = __ballot(need);
+    int last = base;
+    tile_pipeline(__popcll(bits), [&](uint32_t& w) {
+      w = 0xfu;
+      if (bits) {
+        last = base + __builtin_ctzll(bits);
+        bits &= bits - 1;
+      }
+      return last;
+    }, gload, lstore, wave_sync, body);
   }
 }
 
@@ -263,43 +340,85 @@ struct AttnArgs {
   float c;                  // softmax_scale * log2(e)
   float scale;
   const int2* nodes; const int4* meta;   // masked mode: per-token node pairs (padded), per-tile metadata
-  const int* plan;
+  const int4* plan;         // per block group: (group, first partner tile, end partner tile, -)
+  const int2* bounds;       // per outer token: partner range of its segment
   bf16* o; float* lse_out;  // forward outputs
   bf16* dq; bf16* dk; bf16* dv;
 };
 
+// Staging source of one lane: a buffer resource plus this lane's 16-byte
+// chunk of a tile.  Loads past the resource return zeros without touching
+// memory (also the empty resource of a wave without a role).
+struct StageSrc {
+  rsrc_t rsrc;
+  uint32_t base, step;   // byte offset of this lane's chunk in tile 0; bytes per tile
+  DEVI uint32_t offset(int pt) const { return base + (uint32_t)pt * step; }
+  DEVI i32x4 load(int pt) const { return bload(rsrc, offset(pt)); }
+};
+
+// Token rows [T][H][16] bf16: lane l reads half (l & 1) of token l >> 1.
+// Per-token 8-byte records [T]: lanes 0..15 read two records each; the other
+// lanes read beyond the resource (zeros).
+DEVI StageSrc rows_src(const void* p, int bytes, int H, int head, int lane) {
+  return StageSrc{make_rsrc(p, (uint32_t)bytes),
+                  ((uint32_t)(lane >> 1) * H + head) * (kHd * 2) + 16u * (lane & 1), (uint32_t)(kTile * H * kHd * 2)};
+}
+DEVI StageSrc records_src(const void* p, int n_records, int lane) {
+  return StageSrc{make_rsrc(p, (uint32_t)n_records * 8u), lane < 16 ? 16u * lane : 0x80000000u, (uint32_t)kTile * 8u};
+}
+DEVI StageSrc empty_src() { return StageSrc{make_rsrc(nullptr, 0u), 0u, 0u}; }
+
+// LDS writes of a staged 32-token tile: rows [token][16] (padded stride),
+// transposed [16 dims][token], and 8-byte records (lanes 0..15).
+DEVI void put_rows(bf16* rows, i32x4 v, int lane) {
+  *reinterpret_cast<i32x4*>(&rows[(lane >> 1) * kRowStride + 8 * (lane & 1)]) = v;
+}
+DEVI void put_rows_t(bf16* tr, i32x4 v, int lane) {
+  const bf16x8 x = as_bf16x8(v);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) tr[(8 * (lane & 1) + e) * kTrStride + (lane >> 1)] = x[e];
+}
+template <class R>
+DEVI void put_records(R* rec, i32x4 v, int lane) {
+  if (lane < 16) *reinterpret_cast<i32x4*>(&rec[2 * lane]) = v;
+}
+
+struct Stage3 { i32x4 a, b, c; };
+struct Stage4 { i32x4 a, b, c, d; };
+
 // ======================================================================== forward
+// Occupancy targets (waves per SIMD) keep the kernels inside the VGPR budget
+// that the compiler would otherwise overshoot by a few registers.
 template <bool MASKED>
-__global__ __launch_bounds__(256) void attn_fwd_kernel(const AttnArgs a) {
-  __shared__ __align__(16) bf16 sK[2][kTile * kRowStride];   // K rows [key][16]
-  __shared__ __align__(16) bf16 sVT[2][32 * kTrStride];      // [V^T ; 1]: rows 0..15 dims, 16..31 ones
-  __shared__ __align__(16) int2 sN[2][kTile];
-  __shared__ TileList sL;
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MASKED ? 3 : 6))) void attn_fwd_kernel(
+    const AttnArgs a) {
+  constexpr int W = MASKED ? kWaves : 1;   // LDS staging regions: per wave (masked) or per block
+  __shared__ __align__(16) bf16 sK[W][2][kTile * kRowStride];   // K rows [key][16]
+  __shared__ __align__(16) bf16 sVT[W][2][32 * kTrStride];      // [V^T ; 1]: rows 0..15 dims, 16..31 ones
+  __shared__ __align__(16) int2 sN[W][2][kTile];
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 31, half = lane >> 5;
+  const int sw = MASKED ? wave : 0;
   const int H = a.heads;
   const int item = blockIdx.x / H;
   const int head = blockIdx.x - item * H;
-  const int t0 = a.plan[item] * kGroupTok;
+  const int4 pl = a.plan[item];
+  const int t0 = pl.x * kGroupTok;
 
-  for (int i = tid; i < 2 * 16 * kTrStride; i += 256) {
+  for (int i = tid; i < W * 2 * 16 * kTrStride; i += 256) {
     const int st = i / (16 * kTrStride);
-    sVT[st][16 * kTrStride + (i - st * 16 * kTrStride)] = (bf16)1.f;
+    sVT[st >> 1][st & 1][16 * kTrStride + (i - st * 16 * kTrStride)] = (bf16)1.f;
   }
-  int gbeg, gend;
-  group_range(a.cu_q, a.cu_k, a.nseg, a.total_q, t0, gbeg, gend);
-  const OuterTile ot = outer_tile(a.cu_q, a.cu_k, a.nseg, a.total_q, t0 + wave * kTile, col);
+  const OuterTile ot = outer_tile(a.bounds, a.total_q, t0 + wave * kTile, col);
   const bf16x8 qf = *reinterpret_cast<const bf16x8*>(a.q + ((size_t)ot.oc * H + head) * kHd + 8 * half);
   int2 qn = make_int2(0, 0);
-  int4 gm[kWaves];
+  int4 own = no_touch();
   if (MASKED) {
     qn = a.nodes[ot.oc];
-    const int tile0 = t0 / kTile;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) gm[w] = (t0 + w * kTile < a.total_q) ? a.meta[tile0 + w] : no_touch();
+    if (ot.active) own = a.meta[(t0 + wave * kTile) / kTile];
   }
 
-  // Reference point b = c |q| max|k| over the keys this wave visits.
+  // Bound b = c |q| max|k| over the keys this wave visits.
   float b = 0.f;
   bool fixed_ref = true;
   if (ot.active) {
@@ -313,31 +432,14 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const AttnArgs a) {
     b = a.c * sqrtf(qq) * km;
     fixed_ref = __builtin_amdgcn_readfirstlane((int)(wave_max(ot.valid ? b : 0.f) <= kStaticBound)) != 0;
   }
-  float m_run = fixed_ref ? b : -INFINITY;
-
-  // Staging roles: wave 0 copies K rows, wave 1 transposes V rows into
-  // V^T, wave 2 copies node pairs (masked mode).
-  const rsrc_t rsrc = make_rsrc(wave == 0 ? (const void*)a.k : (const void*)a.v, (uint32_t)a.total_k * H * kHd * 2);
-  const int skey = lane >> 1, sdh = lane & 1;
-  auto gload = [&](int pt) -> i32x4 {
-    if (wave < 2) return bload(rsrc, ((uint32_t)(pt * kTile + skey) * H + head) * (kHd * 2) + 16u * sdh);
-    if (MASKED && wave == 2 && lane < kTile) {
-      const int2 n = a.nodes[pt * kTile + lane];
-      return i32x4{n.x, n.y, 0, 0};
-    }
-    return i32x4{0, 0, 0, 0};
-  };
-  auto lstore = [&](int st, i32x4 v) {
-    if (wave == 0) {
-      *reinterpret_cast<i32x4*>(&sK[st][skey * kRowStride + 8 * sdh]) = v;
-    } else if (wave == 1) {
-      const bf16x8 x = as_bf16x8(v);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) sVT[st][(8 * sdh + e) * kTrStride + skey] = x[e];
-    } else if (MASKED && wave == 2 && lane < kTile) {
-      sN[st][lane] = make_int2(v.x, v.y);
-    }
-  };
+  // With |S'| <= b <= kStaticBound every exp2(S') is a normal fp32 / bf16
+  // value and a row sum of up to 2^31 such terms cannot overflow, so the
+  // fixed path needs no reference point at all: P = exp2(S') with
+  // S' = K (c q)^T straight out of the MFMA.  Otherwise the running max is
+  // tracked (online softmax).
+  float m_run = fixed_ref ? 0.f : -INFINITY;
+  bf16x8 qh, ql;
+  split_scaled(qf, a.c, qh, ql);
 
   f32x16 acc = {};
   // The fixed-reference and the online (running-max) loops are separate
@@ -345,20 +447,18 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const AttnArgs a) {
   auto run = [&](auto online_tag) {
     constexpr bool ONLINE = decltype(online_tag)::value;
     const f32x16 zero = {};
-    tile_loop<MASKED>(gbeg, gend, a.meta, gm, sL, tid, gload, lstore, [&](int pt, int cur, uint32_t waves) {
+    auto body = [&](int pt, int cur, uint32_t waves) {
       if (((waves >> wave) & 1u) && pt >= ot.pt_beg && pt < ot.pt_end) {
         const int k0 = pt * kTile;
-        f32x16 s = mfma32(lds8(&sK[cur][kperm(col) * kRowStride + 8 * half]), qf, zero);
-        const bool full = !MASKED && k0 >= ot.plo_max && k0 + kTile <= ot.phi_min;
-        if (!full) {
-          int2 kn[16];
-          if (MASKED) lds_nodes16(sN[cur], half, kn);
+        const bf16x8 kr = lds8(&sK[sw][cur][kperm(col) * kRowStride + 8 * half]);
+        f32x16 s = mfma32(kr, ql, mfma32(kr, qh, zero));
+        if (MASKED) {
+          mask_rows(s, -INFINITY, ot, k0, t0 + wave * kTile, half, sN[sw][cur], qn);
+        } else if (!(k0 >= ot.plo_max && k0 + kTile <= ot.phi_min)) {
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const int key = k0 + row_local(r, half);
-            bool ok = key >= ot.plo && key < ot.phi;
-            if (MASKED) ok = ok && key != ot.oi && node_adjacent(kn[r], qn);
-            s[r] = ok ? s[r] : -INFINITY;
+            s[r] = (key >= ot.plo && key < ot.phi) ? s[r] : -INFINITY;
           }
         }
         if (ONLINE) {
@@ -366,7 +466,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const AttnArgs a) {
 #pragma unroll
           for (int r = 1; r < 16; ++r) mt = fmaxf(mt, s[r]);
           mt = fmaxf(mt, __shfl_xor(mt, 32));
-          const float m_new = fmaxf(m_run, mt * a.c);
+          const float m_new = fmaxf(m_run, mt);
           if (__ballot(m_new > m_run)) {
             const float alpha = fast_exp2(m_run - (m_new == -INFINITY ? 0.f : m_new));
 #pragma unroll
@@ -374,14 +474,43 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const AttnArgs a) {
             m_run = m_new;
           }
         }
-        const float m_use = ONLINE ? (m_run == -INFINITY ? 0.f : m_run) : b;
         float p[16];
+        if (ONLINE) {
+          const float m_use = m_run == -INFINITY ? 0.f : m_run;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) p[r] = fast_exp2(fmaf(s[r], a.c, -m_use));
-        acc = mfma32(lds8(&sVT[cur][col * kTrStride + 8 * half]), cvt8(p), acc);
-        acc = mfma32(lds8(&sVT[cur][col * kTrStride + 16 + 8 * half]), cvt8(p + 8), acc);
+          for (int r = 0; r < 16; ++r) p[r] = fast_exp2(s[r] - m_use);
+        } else {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) p[r] = fast_exp2(s[r]);
+        }
+        acc = mfma32(lds8(&sVT[sw][cur][col * kTrStride + 8 * half]), cvt8(p), acc);
+        acc = mfma32(lds8(&sVT[sw][cur][col * kTrStride + 16 + 8 * half]), cvt8(p + 8), acc);
       }
-    });
+    };
+    const int kv_bytes = a.total_k * H * kHd * 2;
+    if constexpr (MASKED) {
+      // Every wave stages K rows, V^T and node pairs of its own tiles.
+      const StageSrc sk = rows_src(a.k, kv_bytes, H, head, lane), sv = rows_src(a.v, kv_bytes, H, head, lane);
+      const StageSrc sn = records_src(a.nodes, a.tq_pad, lane);
+      wave_tile_walk(ot.pt_beg, ot.pt_end, own, a.meta, lane,
+                     [&](int pt) { return Stage3{sk.load(pt), sv.load(pt), sn.load(pt)}; },
+                     [&](int st, const Stage3& g) {
+                       put_rows(sK[sw][st], g.a, lane);
+                       put_rows_t(sVT[sw][st], g.b, lane);
+                       put_records(sN[sw][st], g.c, lane);
+                     },
+                     body);
+    } else {
+      // Staging roles: wave 0 copies K rows, wave 1 transposes V rows into V^T.
+      const StageSrc src = wave == 0 ? rows_src(a.k, kv_bytes, H, head, lane)
+                                     : wave == 1 ? rows_src(a.v, kv_bytes, H, head, lane) : empty_src();
+      block_tile_walk(pl.y, pl.z, [&](int pt) { return src.load(pt); },
+                      [&](int st, i32x4 v) {
+                        if (wave == 0) put_rows(sK[0][st], v, lane);
+                        else if (wave == 1) put_rows_t(sVT[0][st], v, lane);
+                      },
+                      body);
+    }
   };
   if (fixed_ref)
     run(std::integral_constant<bool, false>{});
@@ -399,22 +528,22 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const AttnArgs a) {
 // One wave = one query tile: dQ = scale * dS K with dS = P * (dP - D),
 // recomputing P from the saved LSE.  D = rowsum(dO * O) is computed per lane.
 template <bool MASKED>
-__global__ __launch_bounds__(256) void attn_dq_kernel(const AttnArgs a) {
-  __shared__ __align__(16) bf16 sK[2][kTile * kRowStride];    // K rows
-  __shared__ __align__(16) bf16 sV[2][kTile * kRowStride];    // V rows
-  __shared__ __align__(16) bf16 sKT[2][16 * kTrStride];       // K^T
-  __shared__ __align__(16) int2 sN[2][kTile];
-  __shared__ TileList sL;
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MASKED ? 3 : 4))) void attn_dq_kernel(const AttnArgs a) {
+  constexpr int W = MASKED ? kWaves : 1;
+  __shared__ __align__(16) bf16 sK[W][2][kTile * kRowStride];    // K rows
+  __shared__ __align__(16) bf16 sV[W][2][kTile * kRowStride];    // V rows
+  __shared__ __align__(16) bf16 sKT[W][2][16 * kTrStride];       // K^T
+  __shared__ __align__(16) int2 sN[W][2][kTile];
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 31, half = lane >> 5;
+  const int sw = MASKED ? wave : 0;
   const int H = a.heads;
   const int item = blockIdx.x / H;
   const int head = blockIdx.x - item * H;
-  const int t0 = a.plan[item] * kGroupTok;
+  const int4 pl = a.plan[item];
+  const int t0 = pl.x * kGroupTok;
 
-  int gbeg, gend;
-  group_range(a.cu_q, a.cu_k, a.nseg, a.total_q, t0, gbeg, gend);
-  const OuterTile ot = outer_tile(a.cu_q, a.cu_k, a.nseg, a.total_q, t0 + wave * kTile, col);
+  const OuterTile ot = outer_tile(a.bounds, a.total_q, t0 + wave * kTile, col);
   const size_t row = ((size_t)ot.oc * H + head) * kHd + 8 * half;
   const bf16x8 qf = *reinterpret_cast<const bf16x8*>(a.q + row);
   const bf16x8 dof = *reinterpret_cast<const bf16x8*>(a.dout + row);
@@ -425,68 +554,66 @@ __global__ __launch_bounds__(256) void attn_dq_kernel(const AttnArgs a) {
   dsum += __shfl_xor(dsum, 32);
   const float lq = a.lse[(size_t)head * a.total_q + ot.oc];
   const float lse2q = lq == -INFINITY ? INFINITY : lq * kLog2e;
-  f32x16 cd;  // accumulator seed of dP^T: -D in every row of this lane's column
-#pragma unroll
-  for (int r = 0; r < 16; ++r) cd[r] = -dsum;
+  const f32x16 cd = splat16(-dsum);  // accumulator seed of dP^T: -D in every row of this lane's column
   int2 qn = make_int2(0, 0);
-  int4 gm[kWaves];
+  int4 own = no_touch();
   if (MASKED) {
     qn = a.nodes[ot.oc];
-    const int tile0 = t0 / kTile;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) gm[w] = (t0 + w * kTile < a.total_q) ? a.meta[tile0 + w] : no_touch();
+    if (ot.active) own = a.meta[(t0 + wave * kTile) / kTile];
   }
-
-  const rsrc_t rsrc = make_rsrc(wave == 0 ? (const void*)a.k : (const void*)a.v, (uint32_t)a.total_k * H * kHd * 2);
-  const int skey = lane >> 1, sdh = lane & 1;
-  auto gload = [&](int pt) -> i32x4 {
-    if (wave < 2) return bload(rsrc, ((uint32_t)(pt * kTile + skey) * H + head) * (kHd * 2) + 16u * sdh);
-    if (MASKED && wave == 2 && lane < kTile) {
-      const int2 n = a.nodes[pt * kTile + lane];
-      return i32x4{n.x, n.y, 0, 0};
-    }
-    return i32x4{0, 0, 0, 0};
-  };
-  auto lstore = [&](int st, i32x4 v) {
-    if (wave == 0) {
-      *reinterpret_cast<i32x4*>(&sK[st][skey * kRowStride + 8 * sdh]) = v;
-      const bf16x8 x = as_bf16x8(v);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) sKT[st][(8 * sdh + e) * kTrStride + skey] = x[e];
-    } else if (wave == 1) {
-      *reinterpret_cast<i32x4*>(&sV[st][skey * kRowStride + 8 * sdh]) = v;
-    } else if (MASKED && wave == 2 && lane < kTile) {
-      sN[st][lane] = make_int2(v.x, v.y);
-    }
-  };
 
   f32x16 acc = {};
   const f32x16 zero = {};
-  tile_loop<MASKED>(gbeg, gend, a.meta, gm, sL, tid, gload, lstore, [&](int pt, int cur, uint32_t waves) {
+  auto body = [&](int pt, int cur, uint32_t waves) {
     if (((waves >> wave) & 1u) && pt >= ot.pt_beg && pt < ot.pt_end) {
       const int k0 = pt * kTile;
-      f32x16 s = mfma32(lds8(&sK[cur][kperm(col) * kRowStride + 8 * half]), qf, zero);
-      const f32x16 dp = mfma32(lds8(&sV[cur][kperm(col) * kRowStride + 8 * half]), dof, cd);  // dP^T - D
-      const bool full = !MASKED && k0 >= ot.plo_max && k0 + kTile <= ot.phi_min;
-      if (!full) {
-        int2 kn[16];
-        if (MASKED) lds_nodes16(sN[cur], half, kn);
+      f32x16 s = mfma32(lds8(&sK[sw][cur][kperm(col) * kRowStride + 8 * half]), qf, zero);
+      const f32x16 dp = mfma32(lds8(&sV[sw][cur][kperm(col) * kRowStride + 8 * half]), dof, cd);  // dP^T - D
+      if (MASKED) {
+        mask_rows(s, -INFINITY, ot, k0, t0 + wave * kTile, half, sN[sw][cur], qn);
+      } else if (!(k0 >= ot.plo_max && k0 + kTile <= ot.phi_min)) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int key = k0 + row_local(r, half);
-          bool ok = key >= ot.plo && key < ot.phi;
-          if (MASKED) ok = ok && key != ot.oi && node_adjacent(kn[r], qn);
-          s[r] = ok ? s[r] : -INFINITY;
+          s[r] = (key >= ot.plo && key < ot.phi) ? s[r] : -INFINITY;
         }
       }
       float ds[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) ds[r] = fast_exp2(fmaf(s[r], a.c, -lse2q)) * dp[r];
       const int trow = (col & 15) * kTrStride + 8 * half;
-      acc = mfma32(lds8(&sKT[cur][trow]), cvt8(ds), acc);
-      acc = mfma32(lds8(&sKT[cur][trow + 16]), cvt8(ds + 8), acc);
+      acc = mfma32(lds8(&sKT[sw][cur][trow]), cvt8(ds), acc);
+      acc = mfma32(lds8(&sKT[sw][cur][trow + 16]), cvt8(ds + 8), acc);
     }
-  });
+  };
+  const int kv_bytes = a.total_k * H * kHd * 2;
+  if constexpr (MASKED) {
+    const StageSrc sk = rows_src(a.k, kv_bytes, H, head, lane), sv = rows_src(a.v, kv_bytes, H, head, lane);
+    const StageSrc sn = records_src(a.nodes, a.tq_pad, lane);
+    wave_tile_walk(ot.pt_beg, ot.pt_end, own, a.meta, lane,
+                   [&](int pt) { return Stage3{sk.load(pt), sv.load(pt), sn.load(pt)}; },
+                   [&](int st, const Stage3& g) {
+                     put_rows(sK[sw][st], g.a, lane);
+                     put_rows_t(sKT[sw][st], g.a, lane);
+                     put_rows(sV[sw][st], g.b, lane);
+                     put_records(sN[sw][st], g.c, lane);
+                   },
+                   body);
+  } else {
+    // Staging roles: wave 0 K rows and K^T, wave 1 V rows.
+    const StageSrc src = wave == 0 ? rows_src(a.k, kv_bytes, H, head, lane)
+                                   : wave == 1 ? rows_src(a.v, kv_bytes, H, head, lane) : empty_src();
+    block_tile_walk(pl.y, pl.z, [&](int pt) { return src.load(pt); },
+                    [&](int st, i32x4 v) {
+                      if (wave == 0) {
+                        put_rows(sK[0][st], v, lane);
+                        put_rows_t(sKT[0][st], v, lane);
+                      } else if (wave == 1) {
+                        put_rows(sV[0][st], v, lane);
+                      }
+                    },
+                    body);
+  }
   if (!ot.valid) return;
   store_rows8(a.dq + ((size_t)ot.oi * H + head) * kHd, acc, a.scale, half);
 }
@@ -494,24 +621,25 @@ __global__ __launch_bounds__(256) void attn_dq_kernel(const AttnArgs a) {
 // ======================================================================== dK/dV pass
 // One wave = one key tile (keys on lanes): dV = P^T dO, dK = scale * dS^T Q.
 template <bool MASKED>
-__global__ __launch_bounds__(256) void attn_dkdv_kernel(const AttnArgs a) {
-  __shared__ __align__(16) bf16 sQ[2][kTile * kRowStride];    // Q rows
-  __shared__ __align__(16) bf16 sDO[2][kTile * kRowStride];   // dO rows
-  __shared__ __align__(16) bf16 sQT[2][16 * kTrStride];       // Q^T
-  __shared__ __align__(16) bf16 sDOT[2][16 * kTrStride];      // dO^T
-  __shared__ __align__(16) uint2 sAux[2][kTile];              // row-statistic MFMA operands
-  __shared__ __align__(16) int2 sN[2][kTile];
-  __shared__ TileList sL;
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MASKED ? 2 : 4))) void attn_dkdv_kernel(
+    const AttnArgs a) {
+  constexpr int W = MASKED ? kWaves : 1;
+  __shared__ __align__(16) bf16 sQ[W][2][kTile * kRowStride];    // Q rows
+  __shared__ __align__(16) bf16 sDO[W][2][kTile * kRowStride];   // dO rows
+  __shared__ __align__(16) bf16 sQT[W][2][16 * kTrStride];       // Q^T
+  __shared__ __align__(16) bf16 sDOT[W][2][16 * kTrStride];      // dO^T
+  __shared__ __align__(16) uint2 sAux[W][2][kTile];              // row-statistic MFMA operands
+  __shared__ __align__(16) int2 sN[W][2][kTile];
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 31, half = lane >> 5;
+  const int sw = MASKED ? wave : 0;
   const int H = a.heads;
   const int item = blockIdx.x / H;
   const int head = blockIdx.x - item * H;
-  const int t0 = a.plan[item] * kGroupTok;
+  const int4 pl = a.plan[item];
+  const int t0 = pl.x * kGroupTok;
 
-  int gbeg, gend;
-  group_range(a.cu_k, a.cu_q, a.nseg, a.total_k, t0, gbeg, gend);
-  const OuterTile ot = outer_tile(a.cu_k, a.cu_q, a.nseg, a.total_k, t0 + wave * kTile, col);
+  const OuterTile ot = outer_tile(a.bounds, a.total_k, t0 + wave * kTile, col);
   const size_t row = ((size_t)ot.oc * H + head) * kHd + 8 * half;
   const bf16x8 kf = *reinterpret_cast<const bf16x8*>(a.k + row);
   const bf16x8 vf = *reinterpret_cast<const bf16x8*>(a.v + row);
@@ -519,108 +647,190 @@ __global__ __launch_bounds__(256) void attn_dkdv_kernel(const AttnArgs a) {
   bf16x8 ones2 = {};
   if (half == 0) { ones2[0] = (bf16)1.f; ones2[1] = (bf16)1.f; }
   int2 kn = make_int2(0, 0);
-  int4 gm[kWaves];
+  int4 own = no_touch();
   if (MASKED) {
     kn = a.nodes[ot.oc];
-    const int tile0 = t0 / kTile;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) gm[w] = (t0 + w * kTile < a.total_k) ? a.meta[tile0 + w] : no_touch();
+    if (ot.active) own = a.meta[(t0 + wave * kTile) / kTile];
   }
-
-  // Staging roles: wave 0 Q rows (+ Q^T), wave 1 dO rows (+ dO^T),
-  // wave 2 row statistics, wave 3 node pairs (masked mode).
-  const rsrc_t rsrc = make_rsrc(wave == 0 ? (const void*)a.q : (const void*)a.dout, (uint32_t)a.total_q * H * kHd * 2);
-  const int sq = lane >> 1, sdh = lane & 1;
-  auto gload = [&](int pt) -> i32x4 {
-    if (wave < 2) return bload(rsrc, ((uint32_t)(pt * kTile + sq) * H + head) * (kHd * 2) + 16u * sdh);
-    if (wave == 2 && lane < kTile) {
-      const uint2 x = a.aux[(size_t)head * a.tq_pad + pt * kTile + lane];
-      return i32x4{(int)x.x, (int)x.y, 0, 0};
-    }
-    if (MASKED && wave == 3 && lane < kTile) {
-      const int2 n = a.nodes[pt * kTile + lane];
-      return i32x4{n.x, n.y, 0, 0};
-    }
-    return i32x4{0, 0, 0, 0};
-  };
-  auto lstore = [&](int st, i32x4 v) {
-    if (wave < 2) {
-      bf16* rows = wave == 0 ? sQ[st] : sDO[st];
-      bf16* tr = wave == 0 ? sQT[st] : sDOT[st];
-      *reinterpret_cast<i32x4*>(&rows[sq * kRowStride + 8 * sdh]) = v;
-      const bf16x8 x = as_bf16x8(v);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) tr[(8 * sdh + e) * kTrStride + sq] = x[e];
-    } else if (wave == 2 && lane < kTile) {
-      sAux[st][lane] = make_uint2((uint32_t)v.x, (uint32_t)v.y);
-    } else if (MASKED && wave == 3 && lane < kTile) {
-      sN[st][lane] = make_int2(v.x, v.y);
-    }
-  };
 
   f32x16 dva = {}, dka = {};
   const f32x16 zero = {};
-  tile_loop<MASKED>(gbeg, gend, a.meta, gm, sL, tid, gload, lstore, [&](int pt, int cur, uint32_t waves) {
+  auto body = [&](int pt, int cur, uint32_t waves) {
     if (((waves >> wave) & 1u) && pt >= ot.pt_beg && pt < ot.pt_end) {
       const int q0 = pt * kTile;
       const int rrow = kperm(col) * kRowStride + 8 * half;
-      const uint2 ax = sAux[cur][kperm(col)];
+      const uint2 ax = sAux[sw][cur][kperm(col)];
       const bf16x8 aux_s = as_bf16x8(i32x4{(int)ax.x, 0, 0, 0});
       const bf16x8 aux_d = as_bf16x8(i32x4{(int)ax.y, 0, 0, 0});
       // S' = Q K^T - LSE2/c and dP' = dO V^T - D, rows = queries, lanes = keys.
-      const f32x16 s = mfma32(lds8(&sQ[cur][rrow]), kf, mfma32(aux_s, ones2, zero));
-      const f32x16 dp = mfma32(lds8(&sDO[cur][rrow]), vf, mfma32(aux_d, ones2, zero));
+      const f32x16 s = mfma32(lds8(&sQ[sw][cur][rrow]), kf, mfma32(aux_s, ones2, zero));
+      const f32x16 dp = mfma32(lds8(&sDO[sw][cur][rrow]), vf, mfma32(aux_d, ones2, zero));
       float p[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) p[r] = fast_exp2(s[r] * a.c);
-      const bool full = !MASKED && q0 >= ot.plo_max && q0 + kTile <= ot.phi_min;
-      if (!full) {
-        int2 qn[16];
-        if (MASKED) lds_nodes16(sN[cur], half, qn);
+      if (MASKED) {
+        mask_rows(p, 0.f, ot, q0, t0 + wave * kTile, half, sN[sw][cur], kn);
+      } else if (!(q0 >= ot.plo_max && q0 + kTile <= ot.phi_min)) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int qq = q0 + row_local(r, half);
-          bool ok = qq >= ot.plo && qq < ot.phi;
-          if (MASKED) ok = ok && qq != ot.oi && node_adjacent(qn[r], kn);
-          p[r] = ok ? p[r] : 0.f;
+          p[r] = (qq >= ot.plo && qq < ot.phi) ? p[r] : 0.f;
         }
       }
       float ds[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) ds[r] = p[r] * dp[r];
       const int trow = (col & 15) * kTrStride + 8 * half;
-      dva = mfma32(lds8(&sDOT[cur][trow]), cvt8(p), dva);
-      dva = mfma32(lds8(&sDOT[cur][trow + 16]), cvt8(p + 8), dva);
-      dka = mfma32(lds8(&sQT[cur][trow]), cvt8(ds), dka);
-      dka = mfma32(lds8(&sQT[cur][trow + 16]), cvt8(ds + 8), dka);
+      dva = mfma32(lds8(&sDOT[sw][cur][trow]), cvt8(p), dva);
+      dva = mfma32(lds8(&sDOT[sw][cur][trow + 16]), cvt8(p + 8), dva);
+      dka = mfma32(lds8(&sQT[sw][cur][trow]), cvt8(ds), dka);
+      dka = mfma32(lds8(&sQT[sw][cur][trow + 16]), cvt8(ds + 8), dka);
     }
-  });
+  };
+  const int q_bytes = a.total_q * H * kHd * 2;
+  const uint2* aux_head = a.aux + (size_t)head * a.tq_pad;
+  if constexpr (MASKED) {
+    const StageSrc sq = rows_src(a.q, q_bytes, H, head, lane), sd = rows_src(a.dout, q_bytes, H, head, lane);
+    const StageSrc sa = records_src(aux_head, a.tq_pad, lane), sn = records_src(a.nodes, a.tq_pad, lane);
+    wave_tile_walk(ot.pt_beg, ot.pt_end, own, a.meta, lane,
+                   [&](int pt) { return Stage4{sq.load(pt), sd.load(pt), sa.load(pt), sn.load(pt)}; },
+                   [&](int st, const Stage4& g) {
+                     put_rows(sQ[sw][st], g.a, lane);
+                     put_rows_t(sQT[sw][st], g.a, lane);
+                     put_rows(sDO[sw][st], g.b, lane);
+                     put_rows_t(sDOT[sw][st], g.b, lane);
+                     put_records(sAux[sw][st], g.c, lane);
+                     put_records(sN[sw][st], g.d, lane);
+                   },
+                   body);
+  } else {
+    // Staging roles: wave 0 Q rows (+ Q^T), wave 1 dO rows (+ dO^T), wave 2
+    // row statistics of this head.
+    const StageSrc src = wave == 0 ? rows_src(a.q, q_bytes, H, head, lane)
+                       : wave == 1 ? rows_src(a.dout, q_bytes, H, head, lane)
+                       : wave == 2 ? records_src(aux_head, a.tq_pad, lane) : empty_src();
+    block_tile_walk(pl.y, pl.z, [&](int pt) { return src.load(pt); },
+                    [&](int st, i32x4 v) {
+                      if (wave == 0) {
+                        put_rows(sQ[0][st], v, lane);
+                        put_rows_t(sQT[0][st], v, lane);
+                      } else if (wave == 1) {
+                        put_rows(sDO[0][st], v, lane);
+                        put_rows_t(sDOT[0][st], v, lane);
+                      } else if (wave == 2) {
+                        put_records(sAux[0][st], v, lane);
+                      }
+                    },
+                    body);
+  }
   if (!ot.valid) return;
   store_rows8(a.dv + ((size_t)ot.oi * H + head) * kHd, dva, 1.f, half);
   store_rows8(a.dk + ((size_t)ot.oi * H + head) * kHd, dka, a.scale, half);
 }
 
-// ======================================================================== prep kernels
+// ======================================================================== prep kernel
+// Everything the attention kernels need besides q, k, v (per-call metadata)
+// is built by one launch whose blocks split into independent tasks: a plan
+// per direction (one block each), per-tile key norms (forward), row
+// statistics (backward), per-token segment bounds and, in masked mode, the
+// packed node pairs and per-tile node metadata.
 
-// max over each 32-token tile of |k_t| per head: knorm[h * n_tiles + tile].
-__global__ __launch_bounds__(256) void key_norm_kernel(const bf16* __restrict__ k, int total, int heads,
-                                                       int n_tiles, float* __restrict__ knorm) {
-  // thread -> (tile, head), head fastest: a wave reads contiguous rows.
-  const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= (long)n_tiles * heads) return;
-  const int h = (int)(idx % heads), tile = (int)(idx / heads);
-  float m = 0.f;
-  for (int i = 0; i < kTile; ++i) {
-    const int t = tile * kTile + i;
-    if (t >= total) break;
-    const bf16x8* p = reinterpret_cast<const bf16x8*>(k + ((size_t)t * heads + h) * kHd);
-    const bf16x8 u = p[0], v = p[1];
-    float s = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) s = fmaf((float)u[e], (float)u[e], fmaf((float)v[e], (float)v[e], s));
-    m = fmaxf(m, s);
+enum PrepTask { kPlanQ, kPlanK, kKnorm, kRows, kBoundsQ, kBoundsK, kNodes, kMeta, kPrepTasks };
+
+struct PrepArgs {
+  const int* cu_q; const int* cu_k; int nseg;
+  int total_q, total_k, heads, tq_pad, tk_pad;
+  int4* plan_q; int4* plan_k;          // plan_k: backward only
+  int2* bounds_q; int2* bounds_k;      // bounds_k: backward only
+  const bf16* k; float* knorm;         // forward
+  const bf16* dout; const bf16* out; const float* lse; float c; uint2* aux;   // backward
+  const int* tok_src; const int* tok_dst; int2* nodes; int4* meta;          // masked
+  int nb[kPrepTasks];                  // blocks per task, in dispatch order
+};
+
+// Longest-first order of the 128-token outer groups by the number of partner
+// tiles they visit (capped at 1023): a counting sort in one block.
+// plan[i] = (group, first partner tile, end partner tile, 0).  Groups with
+// equal counts may come in any order: every group's outputs are computed by
+// one block, so the order changes no result, only the schedule.  The
+// cu_seqlens arrays are staged in LDS when they fit (kCuCap entries), so the
+// per-group segment searches do not wait on memory.
+constexpr int kCuCap = 2048;
+
+DEVI void plan_block(const int* __restrict__ cu_outer_g, const int* __restrict__ cu_inner_g, int nseg,
+                     int total_outer, int4* __restrict__ plan, int tid) {
+  constexpr int NB = 1024, PER = NB / 256;
+  __shared__ int hist[NB];
+  __shared__ int part[256];
+  __shared__ int scu[2][kCuCap];
+  const int n_groups = (total_outer + kGroupTok - 1) / kGroupTok;
+  const bool staged = nseg + 1 <= kCuCap;
+  if (staged) {
+    for (int i = tid; i <= nseg; i += 256) {
+      scu[0][i] = cu_outer_g[i];
+      scu[1][i] = cu_inner_g[i];
+    }
   }
-  knorm[(size_t)h * n_tiles + tile] = sqrtf(m);
+  for (int i = tid; i < NB; i += 256) hist[i] = 0;
+  __syncthreads();
+  const int* cu_outer = staged ? scu[0] : cu_outer_g;
+  const int* cu_inner = staged ? scu[1] : cu_inner_g;
+  auto bucket = [&](int beg, int end) { return NB - 1 - min(end - beg, NB - 1); };
+  for (int g = tid; g < n_groups; g += 256) {
+    int beg, end;
+    group_range(cu_outer, cu_inner, nseg, total_outer, g * kGroupTok, beg, end);
+    atomicAdd(&hist[bucket(beg, end)], 1);
+  }
+  __syncthreads();
+  int loc[PER], sum = 0;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    loc[i] = sum;
+    sum += hist[tid * PER + i];
+  }
+  part[tid] = sum;
+  __syncthreads();
+  for (int off = 1; off < 256; off <<= 1) {
+    const int add = tid >= off ? part[tid - off] : 0;
+    __syncthreads();
+    part[tid] += add;
+    __syncthreads();
+  }
+  const int base = part[tid] - sum;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) hist[tid * PER + i] = base + loc[i];
+  __syncthreads();
+  for (int g = tid; g < n_groups; g += 256) {
+    int beg, end;
+    group_range(cu_outer, cu_inner, nseg, total_outer, g * kGroupTok, beg, end);
+    plan[atomicAdd(&hist[bucket(beg, end)], 1)] = make_int4(g, beg, end, 0);
+  }
+}
+
+// max |k_t| over one 32-token key tile, per head: knorm[h * n_tiles + tile].
+// Consecutive threads read consecutive heads of a token (contiguous rows).
+DEVI void knorm_block(const bf16* __restrict__ k, int total, int heads, int n_tiles, float* __restrict__ knorm,
+                      int tile, int tid) {
+  __shared__ int smax[256];
+  for (int h0 = 0; h0 < heads; h0 += 256) {
+    const int hn = min(256, heads - h0);
+    if (tid < hn) smax[tid] = 0;
+    __syncthreads();
+    for (int i = tid; i < kTile * hn; i += 256) {
+      const int t = tile * kTile + i / hn, h = h0 + i % hn;
+      if (t < total) {
+        const bf16x8* p = reinterpret_cast<const bf16x8*>(k + ((size_t)t * heads + h) * kHd);
+        const bf16x8 u = p[0], v = p[1];
+        float x = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x = fmaf((float)u[e], (float)u[e], fmaf((float)v[e], (float)v[e], x));
+        atomicMax(&smax[h - h0], __float_as_int(x));   // x >= 0: int order is float order
+      }
+    }
+    __syncthreads();
+    if (tid < hn) knorm[(size_t)(h0 + tid) * n_tiles + tile] = sqrtf(__int_as_float(smax[tid]));
+    __syncthreads();
+  }
 }
 
 DEVI uint32_t split_bf16_pair(float x) {
@@ -630,20 +840,18 @@ DEVI uint32_t split_bf16_pair(float x) {
 }
 
 // Row statistics of the dK/dV pass, as bf16 (hi, lo) pairs (x = hi + lo to
-// ~2^-16 relative): aux.x for -LSE2/c, aux.y for -D = -rowsum(dO * O).
-// Rows without keys and padding get -LSE2/c = -1e30 (their P is 0).
-__global__ void bwd_rowstats_kernel(const bf16* __restrict__ dout, const bf16* __restrict__ out,
-                                    const float* __restrict__ lse, int total_q, int heads, int tq_pad, float c,
-                                    uint2* __restrict__ aux) {
-  const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= (long)heads * tq_pad) return;
-  const int h = (int)(idx % heads), t = (int)(idx / heads);
+// ~2^-16 relative): aux.x for -LSE2/c (LSE2 = log2(e) LSE), aux.y for
+// -D = -rowsum(dO * O).  Rows without keys and padding get -LSE2/c = -1e30
+// (their P is 0).  Thread per (query, head), head fastest.
+DEVI void rowstats_item(const PrepArgs& p, long idx) {
+  if (idx >= (long)p.heads * p.tq_pad) return;
+  const int h = (int)(idx % p.heads), t = (int)(idx / p.heads);
   float xs = kDeadRow, dsum = 0.f;
-  if (t < total_q) {
-    const float l = lse[(size_t)h * total_q + t];
-    if (l != -INFINITY) xs = -(l * kLog2e) / c;
-    const bf16x8* po = reinterpret_cast<const bf16x8*>(out + ((size_t)t * heads + h) * kHd);
-    const bf16x8* pd = reinterpret_cast<const bf16x8*>(dout + ((size_t)t * heads + h) * kHd);
+  if (t < p.total_q) {
+    const float l = p.lse[(size_t)h * p.total_q + t];
+    if (l != -INFINITY) xs = -(l * kLog2e) / p.c;
+    const bf16x8* po = reinterpret_cast<const bf16x8*>(p.out + ((size_t)t * p.heads + h) * kHd);
+    const bf16x8* pd = reinterpret_cast<const bf16x8*>(p.dout + ((size_t)t * p.heads + h) * kHd);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const bf16x8 o = po[j], g = pd[j];
@@ -651,62 +859,73 @@ __global__ void bwd_rowstats_kernel(const bf16* __restrict__ dout, const bf16* _
       for (int e = 0; e < 8; ++e) dsum = fmaf((float)o[e], (float)g[e], dsum);
     }
   }
-  aux[(size_t)h * tq_pad + t] = make_uint2(split_bf16_pair(xs), split_bf16_pair(-dsum));
+  p.aux[(size_t)h * p.tq_pad + t] = make_uint2(split_bf16_pair(xs), split_bf16_pair(-dsum));
 }
 
-__global__ void nodes_pack_kernel(const int* __restrict__ src, const int* __restrict__ dst, int total,
-                                  int tpad, int2* __restrict__ nodes) {
-  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+// Per outer token: the partner range of its segment; padding tokens get an
+// empty range.
+DEVI void bounds_item(const int* __restrict__ cu_outer, const int* __restrict__ cu_inner, int nseg, int total,
+                      int tpad, int2* __restrict__ bounds, int t) {
   if (t >= tpad) return;
-  nodes[t] = t < total ? make_int2(src[t], dst[t]) : make_int2(-1, -1);
+  int2 b = make_int2(0, 0);
+  if (t < total) {
+    const int sg = seg_of(cu_outer, nseg, t);
+    b = make_int2(cu_inner[sg], cu_inner[sg + 1]);
+  }
+  bounds[t] = b;
 }
 
 // Per 32-token tile: min / max node id over both endpoints and a 64-bit
 // signature of (node & 63).
-__global__ void tile_meta_kernel(const int2* __restrict__ nodes, int total, int n_tiles,
-                                 int4* __restrict__ meta) {
-  const int t = blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= n_tiles) return;
+DEVI void meta_item(const int* __restrict__ src, const int* __restrict__ dst, int total, int4* __restrict__ meta,
+                    int tile) {
+  // All 64 loads are independent and issued before the first use.
+  int a[kTile], b[kTile];
+  const int t0 = tile * kTile;
+#pragma unroll
+  for (int i = 0; i < kTile; ++i) {
+    const bool in = t0 + i < total;
+    a[i] = in ? src[t0 + i] : 0;
+    b[i] = in ? dst[t0 + i] : 0;
+  }
   int lo = INT_MAX, hi = INT_MIN;
   unsigned long long sig = 0ull;
+#pragma unroll
   for (int i = 0; i < kTile; ++i) {
-    const int tok = t * kTile + i;
-    if (tok >= total) break;
-    const int2 n = nodes[tok];
-    lo = min(lo, min(n.x, n.y));
-    hi = max(hi, max(n.x, n.y));
-    sig |= (1ull << (n.x & 63)) | (1ull << (n.y & 63));
+    if (t0 + i < total) {
+      lo = min(lo, min(a[i], b[i]));
+      hi = max(hi, max(a[i], b[i]));
+      sig |= (1ull << (a[i] & 63)) | (1ull << (b[i] & 63));
+    }
   }
-  meta[t] = make_int4(lo, hi, (int)(sig & 0xffffffffull), (int)(sig >> 32));
+  meta[tile] = make_int4(lo, hi, (int)(sig & 0xffffffffull), (int)(sig >> 32));
 }
 
-// Longest-first order of the 128-token outer groups by the number of partner
-// tiles they visit (counting sort in one block; parallel bucket scan).
-__global__ __launch_bounds__(1024) void plan_kernel(const int* __restrict__ cu_outer,
-                                                    const int* __restrict__ cu_inner, int nseg,
-                                                    int total_outer, int n_groups, int* __restrict__ plan) {
-  constexpr int NB = 1024;
-  __shared__ int hist[NB];
+__global__ __launch_bounds__(256) void prep_kernel(const PrepArgs p) {
   const int tid = threadIdx.x;
-  hist[tid] = 0;
-  __syncthreads();
-  auto bucket = [&](int g) {
-    int beg, end;
-    group_range(cu_outer, cu_inner, nseg, total_outer, g * kGroupTok, beg, end);
-    return NB - 1 - min(end - beg, NB - 1);
-  };
-  for (int g = tid; g < n_groups; g += NB) atomicAdd(&hist[bucket(g)], 1);
-  __syncthreads();
-  const int own = hist[tid];
-  for (int off = 1; off < NB; off <<= 1) {
-    const int add = tid >= off ? hist[tid - off] : 0;
-    __syncthreads();
-    hist[tid] += add;
-    __syncthreads();
+  int b = blockIdx.x;
+  if (b < p.nb[kPlanQ]) { plan_block(p.cu_q, p.cu_k, p.nseg, p.total_q, p.plan_q, tid); return; }
+  b -= p.nb[kPlanQ];
+  if (b < p.nb[kPlanK]) { plan_block(p.cu_k, p.cu_q, p.nseg, p.total_k, p.plan_k, tid); return; }
+  b -= p.nb[kPlanK];
+  if (b < p.nb[kKnorm]) { knorm_block(p.k, p.total_k, p.heads, p.tk_pad / kTile, p.knorm, b, tid); return; }
+  b -= p.nb[kKnorm];
+  if (b < p.nb[kRows]) { rowstats_item(p, (long)b * 256 + tid); return; }
+  b -= p.nb[kRows];
+  if (b < p.nb[kBoundsQ]) { bounds_item(p.cu_q, p.cu_k, p.nseg, p.total_q, p.tq_pad, p.bounds_q, b * 256 + tid); return; }
+  b -= p.nb[kBoundsQ];
+  if (b < p.nb[kBoundsK]) { bounds_item(p.cu_k, p.cu_q, p.nseg, p.total_k, p.tk_pad, p.bounds_k, b * 256 + tid); return; }
+  b -= p.nb[kBoundsK];
+  if (b < p.nb[kNodes]) {
+    const int t = b * 256 + tid;
+    if (t < p.tq_pad) p.nodes[t] = t < p.total_q ? make_int2(p.tok_src[t], p.tok_dst[t]) : make_int2(-1, -1);
+    return;
   }
-  hist[tid] -= own;
-  __syncthreads();
-  for (int g = tid; g < n_groups; g += NB) plan[atomicAdd(&hist[bucket(g)], 1)] = g;
+  b -= p.nb[kNodes];
+  if (b < p.nb[kMeta]) {
+    const int tile = b * 256 + tid;
+    if (tile < p.tq_pad / kTile) meta_item(p.tok_src, p.tok_dst, p.total_q, p.meta, tile);
+  }
 }
 
 __global__ void edge_mask_dense_kernel(const int* __restrict__ src, const int* __restrict__ dst,
@@ -740,7 +959,7 @@ int round32(int x) { return (x + kTile - 1) / kTile * kTile; }
 int groups_of(int total) { return (total + kGroupTok - 1) / kGroupTok; }
 
 struct WsLayout {
-  size_t knorm = 0, aux = 0, plan_q = 0, plan_k = 0, nodes = 0, meta = 0, total = 0;
+  size_t knorm = 0, aux = 0, plan_q = 0, plan_k = 0, bounds_q = 0, bounds_k = 0, nodes = 0, meta = 0, total = 0;
 };
 
 WsLayout ws_layout(int total_q, int total_k, int heads, bool masked, bool backward) {
@@ -752,8 +971,12 @@ WsLayout ws_layout(int total_q, int total_k, int heads, bool masked, bool backwa
   } else {
     L.aux = off; off += align256((size_t)heads * tqp * 8);
   }
-  L.plan_q = off; off += align256((size_t)groups_of(total_q) * 4 + 4);
-  if (backward) { L.plan_k = off; off += align256((size_t)groups_of(total_k) * 4 + 4); }
+  L.plan_q = off; off += align256((size_t)groups_of(total_q) * 16 + 16);
+  L.bounds_q = off; off += align256((size_t)tqp * 8);
+  if (backward) {
+    L.plan_k = off; off += align256((size_t)groups_of(total_k) * 16 + 16);
+    L.bounds_k = off; off += align256((size_t)tkp * 8);
+  }
   if (masked) {
     L.nodes = off; off += align256((size_t)tqp * 8);
     L.meta = off; off += align256((size_t)(tqp / kTile) * 16);
@@ -785,25 +1008,21 @@ int launch_zero(void* p, size_t bytes, hipStream_t st) {
   return ESA_OK;
 }
 
-int launch_mask_meta(const int* src, const int* dst, int total, int2* nodes, int4* meta, hipStream_t st) {
-  const int tp = round32(total);
-  ESA_TIMED(esa_profile::kAttnPrep, st,
-            hipLaunchKernelGGL(nodes_pack_kernel, dim3((unsigned)((tp + 255) / 256)), dim3(256), 0, st, src, dst,
-                               total, tp, nodes));
-  ESA_LAUNCH_CHECK();
-  const int nt = tp / kTile;
-  ESA_TIMED(esa_profile::kAttnPrep, st,
-            hipLaunchKernelGGL(tile_meta_kernel, dim3((unsigned)((nt + 255) / 256)), dim3(256), 0, st, nodes, total,
-                               nt, meta));
-  ESA_LAUNCH_CHECK();
-  return ESA_OK;
-}
+int blocks_for(long items) { return (int)((items + 255) / 256); }
 
-int launch_plan(const int* cu_outer, const int* cu_inner, int nseg, int total_outer, int* plan, hipStream_t st) {
-  const int ng = groups_of(total_outer);
+int launch_prep(PrepArgs& p, bool forward, bool masked, hipStream_t st) {
+  p.nb[kPlanQ] = 1;
+  p.nb[kPlanK] = forward ? 0 : 1;
+  p.nb[kKnorm] = forward ? p.tk_pad / kTile : 0;
+  p.nb[kRows] = forward ? 0 : blocks_for((long)p.heads * p.tq_pad);
+  p.nb[kBoundsQ] = blocks_for(p.tq_pad);
+  p.nb[kBoundsK] = forward ? 0 : blocks_for(p.tk_pad);
+  p.nb[kNodes] = masked ? blocks_for(p.tq_pad) : 0;
+  p.nb[kMeta] = masked ? blocks_for(p.tq_pad / kTile) : 0;
+  long grid = 0;
+  for (int i = 0; i < kPrepTasks; ++i) grid += p.nb[i];
   ESA_TIMED(esa_profile::kAttnPrep, st,
-            hipLaunchKernelGGL(plan_kernel, dim3(1), dim3(1024), 0, st, cu_outer, cu_inner, nseg, total_outer, ng,
-                               plan));
+            hipLaunchKernelGGL(prep_kernel, dim3((unsigned)grid), dim3(256), 0, st, p));
   ESA_LAUNCH_CHECK();
   return ESA_OK;
 }
@@ -849,22 +1068,24 @@ int esa_varlen_attn_fwd(const void* q, const void* k, const void* v, const int* 
   a.total_q = total_q; a.total_k = total_k; a.heads = heads; a.tq_pad = round32(total_q);
   a.tk_tiles = round32(total_k) / kTile;
   a.scale = softmax_scale; a.c = softmax_scale * kLog2e;
-  a.plan = reinterpret_cast<const int*>(ws + L.plan_q);
+  a.plan = reinterpret_cast<const int4*>(ws + L.plan_q);
+  a.bounds = reinterpret_cast<const int2*>(ws + L.bounds_q);
   a.o = static_cast<bf16*>(out); a.lse_out = softmax_lse;
-  if (total_k > 0) {
-    const long n = (long)a.tk_tiles * heads;
-    ESA_TIMED(esa_profile::kAttnPrep, st,
-              hipLaunchKernelGGL(key_norm_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a.k, total_k,
-                                 heads, a.tk_tiles, reinterpret_cast<float*>(ws + L.knorm)));
-    ESA_LAUNCH_CHECK();
-  }
+  PrepArgs pa{};
+  pa.cu_q = cu_seqlens_q; pa.cu_k = cu_seqlens_k; pa.nseg = batch;
+  pa.total_q = total_q; pa.total_k = total_k; pa.heads = heads;
+  pa.tq_pad = round32(total_q); pa.tk_pad = round32(total_k);
+  pa.plan_q = reinterpret_cast<int4*>(ws + L.plan_q);
+  pa.bounds_q = reinterpret_cast<int2*>(ws + L.bounds_q);
+  pa.k = a.k; pa.knorm = reinterpret_cast<float*>(ws + L.knorm);
   if (masked) {
-    a.nodes = reinterpret_cast<const int2*>(ws + L.nodes);
-    a.meta = reinterpret_cast<const int4*>(ws + L.meta);
-    if ((rc = launch_mask_meta(tok_src, tok_dst, total_q, reinterpret_cast<int2*>(ws + L.nodes),
-                               reinterpret_cast<int4*>(ws + L.meta), st))) return rc;
+    pa.tok_src = tok_src; pa.tok_dst = tok_dst;
+    pa.nodes = reinterpret_cast<int2*>(ws + L.nodes);
+    pa.meta = reinterpret_cast<int4*>(ws + L.meta);
+    a.nodes = pa.nodes;
+    a.meta = pa.meta;
   }
-  if ((rc = launch_plan(cu_seqlens_q, cu_seqlens_k, batch, total_q, reinterpret_cast<int*>(ws + L.plan_q), st))) return rc;
+  if ((rc = launch_prep(pa, true, masked, st))) return rc;
   const unsigned grid = (unsigned)groups_of(total_q) * (unsigned)heads;
   if (masked)
     ESA_TIMED(esa_profile::kAttnFwdMasked, st,
@@ -915,26 +1136,31 @@ int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k, const vo
   a.tk_tiles = round32(total_k) / kTile;
   a.scale = softmax_scale; a.c = softmax_scale * kLog2e;
   a.dq = static_cast<bf16*>(dq); a.dk = static_cast<bf16*>(dk); a.dv = static_cast<bf16*>(dv);
-  {
-    const long n = (long)heads * a.tq_pad;
-    ESA_TIMED(esa_profile::kAttnPrep, st,
-              hipLaunchKernelGGL(bwd_rowstats_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, a.dout,
-                                 a.out, softmax_lse, total_q, heads, a.tq_pad, a.c,
-                                 reinterpret_cast<uint2*>(ws + L.aux)));
-    ESA_LAUNCH_CHECK();
-  }
+  PrepArgs pa{};
+  pa.cu_q = cu_seqlens_q; pa.cu_k = cu_seqlens_k; pa.nseg = batch;
+  pa.total_q = total_q; pa.total_k = total_k; pa.heads = heads;
+  pa.tq_pad = round32(total_q); pa.tk_pad = round32(total_k);
+  pa.plan_q = reinterpret_cast<int4*>(ws + L.plan_q);
+  pa.plan_k = reinterpret_cast<int4*>(ws + L.plan_k);
+  pa.bounds_q = reinterpret_cast<int2*>(ws + L.bounds_q);
+  pa.bounds_k = reinterpret_cast<int2*>(ws + L.bounds_k);
+  pa.dout = a.dout; pa.out = a.out; pa.lse = softmax_lse; pa.c = a.c;
+  pa.aux = reinterpret_cast<uint2*>(ws + L.aux);
   if (masked) {
-    a.nodes = reinterpret_cast<const int2*>(ws + L.nodes);
-    a.meta = reinterpret_cast<const int4*>(ws + L.meta);
-    if ((rc = launch_mask_meta(tok_src, tok_dst, total_q, reinterpret_cast<int2*>(ws + L.nodes),
-                               reinterpret_cast<int4*>(ws + L.meta), st))) return rc;
+    pa.tok_src = tok_src; pa.tok_dst = tok_dst;
+    pa.nodes = reinterpret_cast<int2*>(ws + L.nodes);
+    pa.meta = reinterpret_cast<int4*>(ws + L.meta);
+    a.nodes = pa.nodes;
+    a.meta = pa.meta;
   }
-  int* plan_q = reinterpret_cast<int*>(ws + L.plan_q);
-  int* plan_k = reinterpret_cast<int*>(ws + L.plan_k);
-  if ((rc = launch_plan(cu_seqlens_q, cu_seqlens_k, batch, total_q, plan_q, st))) return rc;
-  if ((rc = launch_plan(cu_seqlens_k, cu_seqlens_q, batch, total_k, plan_k, st))) return rc;
+  if ((rc = launch_prep(pa, false, masked, st))) return rc;
+  const int4* plan_q = pa.plan_q;
+  const int4* plan_k = pa.plan_k;
+  const int2* bounds_q = pa.bounds_q;
+  const int2* bounds_k = pa.bounds_k;
 
   a.plan = plan_k;
+  a.bounds = bounds_k;
   const unsigned kgrid = (unsigned)groups_of(total_k) * (unsigned)heads;
   if (masked)
     ESA_TIMED(esa_profile::kAttnBwdDkdvMasked, st,
@@ -945,6 +1171,7 @@ int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k, const vo
   ESA_LAUNCH_CHECK();
 
   a.plan = plan_q;
+  a.bounds = bounds_q;
   const unsigned qgrid = (unsigned)groups_of(total_q) * (unsigned)heads;
   if (masked)
     ESA_TIMED(esa_profile::kAttnBwdDqMasked, st,
