@@ -41,38 +41,49 @@ extern "C" {
 #define ESA_F32 0
 #define ESA_BF16 1
 
+/* Attention mask kinds (see esa_varlen_attn_fwd). */
+#define ESA_MASK_NONE 0
+#define ESA_MASK_EDGE 1
+
 /* Library version and build target, e.g. "esa_hip 0.1 gfx950". */
 ESA_API const char* esa_version(void);
 
 /* ------------------------------------------------------------------------ */
-/* Varlen attention over packed segments (bf16 in/out, fp32 softmax).        */
+/* Varlen attention over packed segments.                                    */
 /*                                                                           */
 /* Replaces flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k,      */
 /* max_seqlen_q, max_seqlen_k, dropout_p=0, softmax_scale, causal=False)     */
 /* called at esa/mha_flash_varlen.py:177-184, and the per-graph attention of */
 /* memory_efficient_attention / SDPA at esa/mha.py:76 and :80-83.            */
 /*                                                                           */
-/* Edge-adjacency mask: when tok_src/tok_dst are non-null (self-attention,   */
-/* total_q == total_k, same cu_seqlens), query token i attends to key token  */
-/* j of the same segment iff i != j and {src_i, dst_i} and {src_j, dst_j}    */
-/* share a node — the predicate of create_edge_adjacency_mask               */
-/* (esa/masked_layers.py:121-142) that get_adj_mask_from_edge_index_edge      */
-/* (:217-268) turns into a 0 / -99999 bias.  It is evaluated on the fly; no  */
-/* mask is stored.  A query with no admissible key gets output 0 and        */
-/* lse = -inf.                                                              */
+/* q [total_q, heads, 16], k and v [total_k, heads, 16], out like q, all of  */
+/* `dtype`: ESA_BF16 (bf16 MFMA, fp32 softmax; the bf16-mixed training path) */
+/* or ESA_F32 (fp32 throughout; the reference's fp32 modules).               */
+/*                                                                           */
+/* mask_kind ESA_MASK_EDGE: mask_a / mask_b are the per-token endpoint node  */
+/* ids src / dst [total_q] (self-attention, total_q == total_k, same         */
+/* cu_seqlens); query token i attends to key token j of the same segment iff */
+/* i != j and {src_i, dst_i} and {src_j, dst_j} share a node — the predicate */
+/* of create_edge_adjacency_mask (esa/masked_layers.py:121-142) that          */
+/* get_adj_mask_from_edge_index_edge (:217-268) turns into a 0 / -99999      */
+/* bias.  It is evaluated on the fly; no mask is stored.  n_mask_edges is    */
+/* unused.  ESA_MASK_NONE: mask_a, mask_b unused.                            */
+/* A query with no admissible key gets output 0 and lse = -inf.              */
 /*                                                                           */
 /* softmax_lse is [heads, total_q] fp32 (natural log), as flash-attn's.      */
 /* ------------------------------------------------------------------------ */
 ESA_API int esa_varlen_attn_workspace_size(int total_q, int total_k, int heads,
-                                   int head_dim, int masked, int backward,
+                                   int head_dim, int dtype, int mask_kind,
+                                   int n_mask_edges, int backward,
                                    size_t* bytes);
 
 ESA_API int esa_varlen_attn_fwd(const void* q, const void* k, const void* v,
                         const int* cu_seqlens_q, const int* cu_seqlens_k,
                         int batch, int total_q, int total_k,
                         int max_seqlen_q, int max_seqlen_k,
-                        int heads, int head_dim, float softmax_scale,
-                        const int* tok_src, const int* tok_dst,
+                        int heads, int head_dim, int dtype, float softmax_scale,
+                        int mask_kind, const int* mask_a, const int* mask_b,
+                        int n_mask_edges,
                         void* out, float* softmax_lse,
                         void* workspace, size_t workspace_bytes, void* stream);
 
@@ -83,8 +94,9 @@ ESA_API int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k,
                         const int* cu_seqlens_q, const int* cu_seqlens_k,
                         int batch, int total_q, int total_k,
                         int max_seqlen_q, int max_seqlen_k,
-                        int heads, int head_dim, float softmax_scale,
-                        const int* tok_src, const int* tok_dst,
+                        int heads, int head_dim, int dtype, float softmax_scale,
+                        int mask_kind, const int* mask_a, const int* mask_b,
+                        int n_mask_edges,
                         void* dq, void* dk, void* dv,
                         void* workspace, size_t workspace_bytes, void* stream);
 

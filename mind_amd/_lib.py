@@ -20,6 +20,8 @@ LIB_PATH = Path(os.environ.get("MIND_AMD_LIB") or Path(__file__).resolve().paren
 
 ESA_F32 = 0
 ESA_BF16 = 1
+ESA_MASK_NONE = 0
+ESA_MASK_EDGE = 1
 
 ERRORS = {
     -1: "ESA_ERR_NULL (a required pointer is null)",
@@ -28,18 +30,22 @@ ERRORS = {
     -4: "ESA_ERR_WORKSPACE (workspace too small)",
     -5: "ESA_ERR_DTYPE (unsupported dtype)",
     -6: "ESA_ERR_ALIGN (pointer not 16-byte aligned)",
-    -7: "ESA_ERR_MASK (edge mask needs total_q == total_k)",
+    -7: "ESA_ERR_MASK (unknown mask kind, or the edge mask without total_q == total_k)",
 }
 
 _c_int, _c_i64, _c_f, _c_sz, _vp = ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_size_t, ctypes.c_void_p
 
 _PROTOS = {
     "esa_version": (ctypes.c_char_p, []),
-    "esa_varlen_attn_workspace_size": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int, ctypes.POINTER(_c_sz)]),
+    "esa_varlen_attn_workspace_size": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
+                                                ctypes.POINTER(_c_sz)]),
+    # q k v cu_q cu_k | batch tq tk maxq maxk heads hd dtype | scale | mask_kind a b n | out lse ws bytes stream
     "esa_varlen_attn_fwd": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
-                                     _c_f, _vp, _vp, _vp, _vp, _vp, _c_sz, _vp]),
+                                     _c_int, _c_f, _c_int, _vp, _vp, _c_int, _vp, _vp, _vp, _c_sz, _vp]),
+    # dout q k v out lse cu_q cu_k | batch tq tk maxq maxk heads hd dtype | scale | mask_kind a b n | dq dk dv ws ...
     "esa_varlen_attn_bwd": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int,
-                                     _c_int, _c_int, _c_f, _vp, _vp, _vp, _vp, _vp, _vp, _c_sz, _vp]),
+                                     _c_int, _c_int, _c_int, _c_f, _c_int, _vp, _vp, _c_int, _vp, _vp, _vp, _vp, _c_sz,
+                                     _vp]),
     "esa_edge_mask_dense": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _vp]),
     "esa_edge_gather": (_c_int, [_vp, _vp, _vp, _c_i64, _c_int, _c_int, _c_int, _vp, _vp]),
     "esa_csr_workspace_size": (_c_int, [_c_i64, _c_int, ctypes.POINTER(_c_sz)]),

@@ -728,6 +728,218 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MASKED ? 2 
   store_rows8(a.dk + ((size_t)ot.oi * H + head) * kHd, dka, a.scale, half);
 }
 
+// ======================================================================== fp32 path
+// fp32 q, k, v, outputs and softmax (the reference's fp32 modules, compared
+// at 1e-5 relative).  One thread per (outer token, head) of a 128-token group
+// (the same plan and segment bounds as the bf16 kernels), partner tiles of 32
+// tokens staged in LDS and read by broadcast.  Scores, softmax and both
+// products are fp32 FMA chains in a fixed order; exp2f / log2f are the
+// device library's correctly rounded-to-1-ulp versions.
+
+struct AttnF32Args {
+  const float* q; const float* k; const float* v; const float* out; const float* dout;
+  const float2* rows;       // backward: per (head, query) (LSE2 or +inf for rows without keys, D) [H][tq_pad]
+  int total_q, total_k, heads, tq_pad;
+  float c, scale;           // c = softmax_scale * log2(e)
+  const int2* nodes;        // edge mask: per-token node pairs (padded)
+  const int4* plan;
+  const int2* bounds;
+  float* o; float* lse_out; float* dq; float* dk; float* dv;
+};
+
+constexpr int kF32Threads = kGroupTok;
+
+DEVI void load16(const float* p, float x[16]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float4 v = reinterpret_cast<const float4*>(p)[i];
+    x[4 * i] = v.x; x[4 * i + 1] = v.y; x[4 * i + 2] = v.z; x[4 * i + 3] = v.w;
+  }
+}
+DEVI void store16(float* p, const float x[16], float mul) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    reinterpret_cast<float4*>(p)[i] = make_float4(x[4 * i] * mul, x[4 * i + 1] * mul, x[4 * i + 2] * mul,
+                                                  x[4 * i + 3] * mul);
+}
+DEVI float dot16(const float x[16], const float4* y) {
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float4 v = y[i];
+    s = fmaf(x[4 * i], v.x, s); s = fmaf(x[4 * i + 1], v.y, s);
+    s = fmaf(x[4 * i + 2], v.z, s); s = fmaf(x[4 * i + 3], v.w, s);
+  }
+  return s;
+}
+DEVI void axpy16(float a, const float4* y, float x[16]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float4 v = y[i];
+    x[4 * i] = fmaf(a, v.x, x[4 * i]); x[4 * i + 1] = fmaf(a, v.y, x[4 * i + 1]);
+    x[4 * i + 2] = fmaf(a, v.z, x[4 * i + 2]); x[4 * i + 3] = fmaf(a, v.w, x[4 * i + 3]);
+  }
+}
+
+// Stage one 32-token tile of a [T][H][16] fp32 tensor into LDS [32][4] float4
+// (128 threads, one float4 each); tokens past `total` read as zeros.
+DEVI void stage_rows_f32(float4 (*dst)[4], const float* src, int total, int H, int head, int pt, int tid) {
+  const int t = pt * kTile + (tid >> 2), part = tid & 3;
+  dst[tid >> 2][part] = t < total ? reinterpret_cast<const float4*>(src + ((size_t)t * H + head) * kHd)[part]
+                                  : make_float4(0.f, 0.f, 0.f, 0.f);
+}
+
+// Admissible partner j of outer token oi (segment partner range [plo, phi)).
+template <bool MASKED>
+DEVI bool admissible_f32(int p, int plo, int phi, int oi, int2 pn, int2 own) {
+  bool ok = p >= plo && p < phi;
+  if (MASKED) ok = ok && p != oi && node_adjacent(pn, own);
+  return ok;
+}
+
+template <bool MASKED>
+__global__ __launch_bounds__(kF32Threads) void attn_fwd_f32_kernel(const AttnF32Args a) {
+  __shared__ float4 sK[kTile][4], sV[kTile][4];
+  __shared__ int2 sN[kTile];
+  const int tid = threadIdx.x, H = a.heads;
+  const int item = blockIdx.x / H, head = blockIdx.x - item * H;
+  const int4 pl = a.plan[item];
+  const int oi = pl.x * kGroupTok + tid;
+  const bool valid = oi < a.total_q;
+  const int oc = valid ? oi : a.total_q - 1;
+  const int2 bd = a.bounds[oc];
+  const int plo = valid ? bd.x : 0, phi = valid ? bd.y : 0;
+  float q[16], acc[16];
+  load16(a.q + ((size_t)oc * H + head) * kHd, q);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+  const int2 own = MASKED ? a.nodes[oc] : make_int2(0, 0);
+  float m = -INFINITY, l = 0.f;
+  for (int pt = pl.y; pt < pl.z; ++pt) {
+    __syncthreads();
+    stage_rows_f32(sK, a.k, a.total_k, H, head, pt, tid);
+    stage_rows_f32(sV, a.v, a.total_k, H, head, pt, tid);
+    if (MASKED && tid < kTile) sN[tid] = a.nodes[pt * kTile + tid];
+    __syncthreads();
+    const int k0 = pt * kTile;
+    if (max(plo, k0) >= min(phi, k0 + kTile)) continue;
+    float s[kTile];
+    float mt = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < kTile; ++j) {
+      const int2 pn = MASKED ? sN[j] : make_int2(0, 0);
+      s[j] = admissible_f32<MASKED>(k0 + j, plo, phi, oi, pn, own) ? a.c * dot16(q, sK[j]) : -INFINITY;
+      mt = fmaxf(mt, s[j]);
+    }
+    if (mt == -INFINITY) continue;
+    if (mt > m) {
+      const float alpha = exp2f(m - mt);   // 0 while m = -inf
+      l *= alpha;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[i] *= alpha;
+      m = mt;
+    }
+#pragma unroll
+    for (int j = 0; j < kTile; ++j) {
+      const float p = exp2f(s[j] - m);
+      l += p;
+      axpy16(p, sV[j], acc);
+    }
+  }
+  if (!valid) return;
+  store16(a.o + ((size_t)oi * H + head) * kHd, acc, l > 0.f ? 1.f / l : 0.f);
+  a.lse_out[(size_t)head * a.total_q + oi] = l > 0.f ? (m + log2f(l)) * kLn2 : -INFINITY;
+}
+
+// dQ = scale * sum_j P_ij (dP_ij - D_i) k_j, P recomputed from the saved LSE.
+template <bool MASKED>
+__global__ __launch_bounds__(kF32Threads) void attn_dq_f32_kernel(const AttnF32Args a) {
+  __shared__ float4 sK[kTile][4], sV[kTile][4];
+  __shared__ int2 sN[kTile];
+  const int tid = threadIdx.x, H = a.heads;
+  const int item = blockIdx.x / H, head = blockIdx.x - item * H;
+  const int4 pl = a.plan[item];
+  const int oi = pl.x * kGroupTok + tid;
+  const bool valid = oi < a.total_q;
+  const int oc = valid ? oi : a.total_q - 1;
+  const int2 bd = a.bounds[oc];
+  const int plo = valid ? bd.x : 0, phi = valid ? bd.y : 0;
+  float q[16], g[16], acc[16];
+  load16(a.q + ((size_t)oc * H + head) * kHd, q);
+  load16(a.dout + ((size_t)oc * H + head) * kHd, g);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+  const float2 rs = a.rows[(size_t)head * a.tq_pad + oc];   // (LSE2, D)
+  const int2 own = MASKED ? a.nodes[oc] : make_int2(0, 0);
+  for (int pt = pl.y; pt < pl.z; ++pt) {
+    __syncthreads();
+    stage_rows_f32(sK, a.k, a.total_k, H, head, pt, tid);
+    stage_rows_f32(sV, a.v, a.total_k, H, head, pt, tid);
+    if (MASKED && tid < kTile) sN[tid] = a.nodes[pt * kTile + tid];
+    __syncthreads();
+    const int k0 = pt * kTile;
+    if (max(plo, k0) >= min(phi, k0 + kTile)) continue;
+#pragma unroll
+    for (int j = 0; j < kTile; ++j) {
+      const int2 pn = MASKED ? sN[j] : make_int2(0, 0);
+      if (!admissible_f32<MASKED>(k0 + j, plo, phi, oi, pn, own)) continue;
+      const float p = exp2f(a.c * dot16(q, sK[j]) - rs.x);
+      const float ds = p * (dot16(g, sV[j]) - rs.y);
+      axpy16(ds, sK[j], acc);
+    }
+  }
+  if (!valid) return;
+  store16(a.dq + ((size_t)oi * H + head) * kHd, acc, a.scale);
+}
+
+// dV = sum_i P_ij dO_i, dK = scale * sum_i P_ij (dP_ij - D_i) q_i, one thread
+// per key; the partner tiles are query tiles with their (LSE2, D).
+template <bool MASKED>
+__global__ __launch_bounds__(kF32Threads) void attn_dkdv_f32_kernel(const AttnF32Args a) {
+  __shared__ float4 sQ[kTile][4], sG[kTile][4];
+  __shared__ float2 sR[kTile];
+  __shared__ int2 sN[kTile];
+  const int tid = threadIdx.x, H = a.heads;
+  const int item = blockIdx.x / H, head = blockIdx.x - item * H;
+  const int4 pl = a.plan[item];
+  const int oi = pl.x * kGroupTok + tid;
+  const bool valid = oi < a.total_k;
+  const int oc = valid ? oi : a.total_k - 1;
+  const int2 bd = a.bounds[oc];
+  const int plo = valid ? bd.x : 0, phi = valid ? bd.y : 0;
+  float kx[16], vx[16], dk[16], dv[16];
+  load16(a.k + ((size_t)oc * H + head) * kHd, kx);
+  load16(a.v + ((size_t)oc * H + head) * kHd, vx);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) dk[i] = dv[i] = 0.f;
+  const int2 own = MASKED ? a.nodes[oc] : make_int2(0, 0);
+  for (int pt = pl.y; pt < pl.z; ++pt) {
+    __syncthreads();
+    stage_rows_f32(sQ, a.q, a.total_q, H, head, pt, tid);
+    stage_rows_f32(sG, a.dout, a.total_q, H, head, pt, tid);
+    if (tid < kTile) {
+      sR[tid] = a.rows[(size_t)head * a.tq_pad + pt * kTile + tid];
+      if (MASKED) sN[tid] = a.nodes[pt * kTile + tid];
+    }
+    __syncthreads();
+    const int q0 = pt * kTile;
+    if (max(plo, q0) >= min(phi, q0 + kTile)) continue;
+#pragma unroll
+    for (int i = 0; i < kTile; ++i) {
+      const int2 pn = MASKED ? sN[i] : make_int2(0, 0);
+      if (!admissible_f32<MASKED>(q0 + i, plo, phi, oi, pn, own)) continue;
+      const float2 rs = sR[i];
+      const float p = exp2f(a.c * dot16(kx, sQ[i]) - rs.x);
+      axpy16(p, sG[i], dv);
+      const float ds = p * (dot16(vx, sG[i]) - rs.y);
+      axpy16(ds, sQ[i], dk);
+    }
+  }
+  if (!valid) return;
+  store16(a.dv + ((size_t)oi * H + head) * kHd, dv, 1.f);
+  store16(a.dk + ((size_t)oi * H + head) * kHd, dk, a.scale);
+}
+
 // ======================================================================== prep kernel
 // Everything the attention kernels need besides q, k, v (per-call metadata)
 // is built by one launch whose blocks split into independent tasks: a plan
@@ -743,7 +955,8 @@ struct PrepArgs {
   int4* plan_q; int4* plan_k;          // plan_k: backward only
   int2* bounds_q; int2* bounds_k;      // bounds_k: backward only
   const bf16* k; float* knorm;         // forward
-  const bf16* dout; const bf16* out; const float* lse; float c; uint2* aux;   // backward
+  const bf16* dout; const bf16* out; const float* lse; float c; uint2* aux;   // backward (bf16)
+  const float* dout_f; const float* out_f; float2* rows_f;                  // backward (fp32)
   const int* tok_src; const int* tok_dst; int2* nodes; int4* meta;          // masked
   int nb[kPrepTasks];                  // blocks per task, in dispatch order
 };
@@ -846,6 +1059,21 @@ DEVI uint32_t split_bf16_pair(float x) {
 DEVI void rowstats_item(const PrepArgs& p, long idx) {
   if (idx >= (long)p.heads * p.tq_pad) return;
   const int h = (int)(idx % p.heads), t = (int)(idx / p.heads);
+  if (p.rows_f) {
+    // fp32 path: (LSE2 = log2(e) LSE, or +inf for rows without keys, D).
+    float l2 = INFINITY, d = 0.f;
+    if (t < p.total_q) {
+      const float l = p.lse[(size_t)h * p.total_q + t];
+      if (l != -INFINITY) l2 = l * kLog2e;
+      float o[16], g[16];
+      load16(p.out_f + ((size_t)t * p.heads + h) * kHd, o);
+      load16(p.dout_f + ((size_t)t * p.heads + h) * kHd, g);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) d = fmaf(g[e], o[e], d);
+    }
+    p.rows_f[(size_t)h * p.tq_pad + t] = make_float2(l2, d);
+    return;
+  }
   float xs = kDeadRow, dsum = 0.f;
   if (t < p.total_q) {
     const float l = p.lse[(size_t)h * p.total_q + t];
@@ -962,14 +1190,14 @@ struct WsLayout {
   size_t knorm = 0, aux = 0, plan_q = 0, plan_k = 0, bounds_q = 0, bounds_k = 0, nodes = 0, meta = 0, total = 0;
 };
 
-WsLayout ws_layout(int total_q, int total_k, int heads, bool masked, bool backward) {
+WsLayout ws_layout(int total_q, int total_k, int heads, int dtype, bool masked, bool backward) {
   WsLayout L;
   const int tqp = round32(total_q), tkp = round32(total_k);
   size_t off = 0;
   if (!backward) {
-    L.knorm = off; off += align256((size_t)heads * (tkp / kTile) * 4);
+    if (dtype == ESA_BF16) { L.knorm = off; off += align256((size_t)heads * (tkp / kTile) * 4); }
   } else {
-    L.aux = off; off += align256((size_t)heads * tqp * 8);
+    L.aux = off; off += align256((size_t)heads * tqp * 8);   // bf16: uint2 (hi, lo) pairs; fp32: float2 rows
   }
   L.plan_q = off; off += align256((size_t)groups_of(total_q) * 16 + 16);
   L.bounds_q = off; off += align256((size_t)tqp * 8);
@@ -987,13 +1215,15 @@ WsLayout ws_layout(int total_q, int total_k, int heads, bool masked, bool backwa
 
 bool misaligned(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) != 0; }
 
-int check_common(int batch, int total_q, int total_k, int heads, int head_dim, bool masked) {
+int check_common(int batch, int total_q, int total_k, int heads, int head_dim, int dtype, int mask_kind) {
   if (head_dim != kHd) return ESA_ERR_HEAD_DIM;
+  if (dtype != ESA_BF16 && dtype != ESA_F32) return ESA_ERR_DTYPE;
   if (batch < 1 || heads < 1 || total_q < 0 || total_k < 0) return ESA_ERR_SHAPE;
   // Buffer-resource ranges are 32-bit byte counts.
   const long lim = (1L << 31) - 1;
   if ((long)round32(total_q) * heads * 32 > lim || (long)round32(total_k) * heads * 32 > lim) return ESA_ERR_SHAPE;
-  if (masked && total_q != total_k) return ESA_ERR_MASK;
+  if (mask_kind != ESA_MASK_NONE && mask_kind != ESA_MASK_EDGE) return ESA_ERR_MASK;
+  if (mask_kind == ESA_MASK_EDGE && total_q != total_k) return ESA_ERR_MASK;
   return ESA_OK;
 }
 
@@ -1013,7 +1243,7 @@ int blocks_for(long items) { return (int)((items + 255) / 256); }
 int launch_prep(PrepArgs& p, bool forward, bool masked, hipStream_t st) {
   p.nb[kPlanQ] = 1;
   p.nb[kPlanK] = forward ? 0 : 1;
-  p.nb[kKnorm] = forward ? p.tk_pad / kTile : 0;
+  p.nb[kKnorm] = forward && p.knorm ? p.tk_pad / kTile : 0;
   p.nb[kRows] = forward ? 0 : blocks_for((long)p.heads * p.tq_pad);
   p.nb[kBoundsQ] = blocks_for(p.tq_pad);
   p.nb[kBoundsK] = forward ? 0 : blocks_for(p.tk_pad);
@@ -1033,60 +1263,77 @@ extern "C" {
 
 const char* esa_version(void) { return "esa_hip 0.3 gfx950"; }
 
-int esa_varlen_attn_workspace_size(int total_q, int total_k, int heads, int head_dim, int masked,
-                                   int backward, size_t* bytes) {
+int esa_varlen_attn_workspace_size(int total_q, int total_k, int heads, int head_dim, int dtype, int mask_kind,
+                                   int n_mask_edges, int backward, size_t* bytes) {
+  (void)n_mask_edges;
   if (!bytes) return ESA_ERR_NULL;
-  const int rc = check_common(1, total_q, total_k, heads, head_dim, masked != 0);
+  const int rc = check_common(1, total_q, total_k, heads, head_dim, dtype, mask_kind);
   if (rc) return rc;
-  *bytes = ws_layout(total_q, total_k, heads, masked != 0, backward != 0).total;
+  *bytes = ws_layout(total_q, total_k, heads, dtype, mask_kind == ESA_MASK_EDGE, backward != 0).total;
   return ESA_OK;
 }
 
 int esa_varlen_attn_fwd(const void* q, const void* k, const void* v, const int* cu_seqlens_q,
                         const int* cu_seqlens_k, int batch, int total_q, int total_k,
-                        int max_seqlen_q, int max_seqlen_k, int heads, int head_dim,
-                        float softmax_scale, const int* tok_src, const int* tok_dst, void* out,
-                        float* softmax_lse, void* workspace, size_t workspace_bytes, void* stream) {
-  (void)max_seqlen_q; (void)max_seqlen_k;
-  const bool masked = tok_src != nullptr || tok_dst != nullptr;
-  if (masked && (!tok_src || !tok_dst)) return ESA_ERR_NULL;
-  int rc = check_common(batch, total_q, total_k, heads, head_dim, masked);
+                        int max_seqlen_q, int max_seqlen_k, int heads, int head_dim, int dtype,
+                        float softmax_scale, int mask_kind, const int* mask_a, const int* mask_b,
+                        int n_mask_edges, void* out, float* softmax_lse, void* workspace,
+                        size_t workspace_bytes, void* stream) {
+  (void)max_seqlen_q; (void)max_seqlen_k; (void)n_mask_edges;
+  int rc = check_common(batch, total_q, total_k, heads, head_dim, dtype, mask_kind);
   if (rc) return rc;
+  const bool masked = mask_kind == ESA_MASK_EDGE;
+  if (masked && (!mask_a || !mask_b)) return ESA_ERR_NULL;
   if (total_q == 0) return ESA_OK;
   if (!q || !k || !v || !cu_seqlens_q || !cu_seqlens_k || !out || !softmax_lse || !workspace) return ESA_ERR_NULL;
   if (misaligned(q) || misaligned(k) || misaligned(v) || misaligned(out) || misaligned(workspace)) return ESA_ERR_ALIGN;
   if (!(softmax_scale > 0.f)) return ESA_ERR_SHAPE;
-  const WsLayout L = ws_layout(total_q, total_k, heads, masked, false);
+  const WsLayout L = ws_layout(total_q, total_k, heads, dtype, masked, false);
   if (workspace_bytes < L.total) return ESA_ERR_WORKSPACE;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
+  const bool f32 = dtype == ESA_F32;
 
-  AttnArgs a{};
-  a.q = static_cast<const bf16*>(q); a.k = static_cast<const bf16*>(k); a.v = static_cast<const bf16*>(v);
-  a.knorm = reinterpret_cast<const float*>(ws + L.knorm);
-  a.cu_q = cu_seqlens_q; a.cu_k = cu_seqlens_k; a.nseg = batch;
-  a.total_q = total_q; a.total_k = total_k; a.heads = heads; a.tq_pad = round32(total_q);
-  a.tk_tiles = round32(total_k) / kTile;
-  a.scale = softmax_scale; a.c = softmax_scale * kLog2e;
-  a.plan = reinterpret_cast<const int4*>(ws + L.plan_q);
-  a.bounds = reinterpret_cast<const int2*>(ws + L.bounds_q);
-  a.o = static_cast<bf16*>(out); a.lse_out = softmax_lse;
   PrepArgs pa{};
   pa.cu_q = cu_seqlens_q; pa.cu_k = cu_seqlens_k; pa.nseg = batch;
   pa.total_q = total_q; pa.total_k = total_k; pa.heads = heads;
   pa.tq_pad = round32(total_q); pa.tk_pad = round32(total_k);
   pa.plan_q = reinterpret_cast<int4*>(ws + L.plan_q);
   pa.bounds_q = reinterpret_cast<int2*>(ws + L.bounds_q);
-  pa.k = a.k; pa.knorm = reinterpret_cast<float*>(ws + L.knorm);
+  if (!f32) { pa.k = static_cast<const bf16*>(k); pa.knorm = reinterpret_cast<float*>(ws + L.knorm); }
   if (masked) {
-    pa.tok_src = tok_src; pa.tok_dst = tok_dst;
+    pa.tok_src = mask_a; pa.tok_dst = mask_b;
     pa.nodes = reinterpret_cast<int2*>(ws + L.nodes);
     pa.meta = reinterpret_cast<int4*>(ws + L.meta);
-    a.nodes = pa.nodes;
-    a.meta = pa.meta;
   }
   if ((rc = launch_prep(pa, true, masked, st))) return rc;
   const unsigned grid = (unsigned)groups_of(total_q) * (unsigned)heads;
+
+  if (f32) {
+    AttnF32Args a{};
+    a.q = static_cast<const float*>(q); a.k = static_cast<const float*>(k); a.v = static_cast<const float*>(v);
+    a.total_q = total_q; a.total_k = total_k; a.heads = heads; a.tq_pad = pa.tq_pad;
+    a.c = softmax_scale * kLog2e; a.scale = softmax_scale;
+    a.nodes = pa.nodes; a.plan = pa.plan_q; a.bounds = pa.bounds_q;
+    a.o = static_cast<float*>(out); a.lse_out = softmax_lse;
+    if (masked)
+      hipLaunchKernelGGL((attn_fwd_f32_kernel<true>), dim3(grid), dim3(kF32Threads), 0, st, a);
+    else
+      hipLaunchKernelGGL((attn_fwd_f32_kernel<false>), dim3(grid), dim3(kF32Threads), 0, st, a);
+    ESA_LAUNCH_CHECK();
+    return ESA_OK;
+  }
+
+  AttnArgs a{};
+  a.q = static_cast<const bf16*>(q); a.k = static_cast<const bf16*>(k); a.v = static_cast<const bf16*>(v);
+  a.knorm = pa.knorm;
+  a.cu_q = cu_seqlens_q; a.cu_k = cu_seqlens_k; a.nseg = batch;
+  a.total_q = total_q; a.total_k = total_k; a.heads = heads; a.tq_pad = pa.tq_pad;
+  a.tk_tiles = pa.tk_pad / kTile;
+  a.scale = softmax_scale; a.c = softmax_scale * kLog2e;
+  a.plan = pa.plan_q; a.bounds = pa.bounds_q;
+  a.nodes = pa.nodes; a.meta = pa.meta;
+  a.o = static_cast<bf16*>(out); a.lse_out = softmax_lse;
   if (masked)
     ESA_TIMED(esa_profile::kAttnFwdMasked, st,
               hipLaunchKernelGGL((attn_fwd_kernel<true>), dim3(grid), dim3(256), 0, st, a));
@@ -1099,14 +1346,14 @@ int esa_varlen_attn_fwd(const void* q, const void* k, const void* v, const int* 
 int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k, const void* v, const void* out,
                         const float* softmax_lse, const int* cu_seqlens_q, const int* cu_seqlens_k,
                         int batch, int total_q, int total_k, int max_seqlen_q, int max_seqlen_k,
-                        int heads, int head_dim, float softmax_scale, const int* tok_src,
-                        const int* tok_dst, void* dq, void* dk, void* dv, void* workspace,
-                        size_t workspace_bytes, void* stream) {
-  (void)max_seqlen_q; (void)max_seqlen_k;
-  const bool masked = tok_src != nullptr || tok_dst != nullptr;
-  if (masked && (!tok_src || !tok_dst)) return ESA_ERR_NULL;
-  int rc = check_common(batch, total_q, total_k, heads, head_dim, masked);
+                        int heads, int head_dim, int dtype, float softmax_scale, int mask_kind,
+                        const int* mask_a, const int* mask_b, int n_mask_edges, void* dq, void* dk,
+                        void* dv, void* workspace, size_t workspace_bytes, void* stream) {
+  (void)max_seqlen_q; (void)max_seqlen_k; (void)n_mask_edges;
+  int rc = check_common(batch, total_q, total_k, heads, head_dim, dtype, mask_kind);
   if (rc) return rc;
+  const bool masked = mask_kind == ESA_MASK_EDGE;
+  if (masked && (!mask_a || !mask_b)) return ESA_ERR_NULL;
   if (total_q == 0 && total_k == 0) return ESA_OK;
   if (!dout || !q || !k || !v || !out || !softmax_lse || !cu_seqlens_q || !cu_seqlens_k || !dq || !dk ||
       !dv || !workspace)
@@ -1115,27 +1362,20 @@ int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k, const vo
       misaligned(dq) || misaligned(dk) || misaligned(dv) || misaligned(workspace))
     return ESA_ERR_ALIGN;
   if (!(softmax_scale > 0.f)) return ESA_ERR_SHAPE;
-  const WsLayout L = ws_layout(total_q, total_k, heads, masked, true);
+  const WsLayout L = ws_layout(total_q, total_k, heads, dtype, masked, true);
   if (workspace_bytes < L.total) return ESA_ERR_WORKSPACE;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
+  const bool f32 = dtype == ESA_F32;
+  const size_t esz = f32 ? 4 : 2;
   if (total_q == 0 || total_k == 0) {
     // No query/key pairs: every gradient is zero (a fill kernel, so the call
     // stays capturable in a HIP graph).
-    if ((rc = launch_zero(dq, (size_t)total_q * heads * kHd * 2, st))) return rc;
-    if ((rc = launch_zero(dk, (size_t)total_k * heads * kHd * 2, st))) return rc;
-    if ((rc = launch_zero(dv, (size_t)total_k * heads * kHd * 2, st))) return rc;
+    if ((rc = launch_zero(dq, (size_t)total_q * heads * kHd * esz, st))) return rc;
+    if ((rc = launch_zero(dk, (size_t)total_k * heads * kHd * esz, st))) return rc;
+    if ((rc = launch_zero(dv, (size_t)total_k * heads * kHd * esz, st))) return rc;
     return ESA_OK;
   }
-  AttnArgs a{};
-  a.q = static_cast<const bf16*>(q); a.k = static_cast<const bf16*>(k); a.v = static_cast<const bf16*>(v);
-  a.out = static_cast<const bf16*>(out); a.dout = static_cast<const bf16*>(dout); a.lse = softmax_lse;
-  a.aux = reinterpret_cast<const uint2*>(ws + L.aux);
-  a.cu_q = cu_seqlens_q; a.cu_k = cu_seqlens_k; a.nseg = batch;
-  a.total_q = total_q; a.total_k = total_k; a.heads = heads; a.tq_pad = round32(total_q);
-  a.tk_tiles = round32(total_k) / kTile;
-  a.scale = softmax_scale; a.c = softmax_scale * kLog2e;
-  a.dq = static_cast<bf16*>(dq); a.dk = static_cast<bf16*>(dk); a.dv = static_cast<bf16*>(dv);
   PrepArgs pa{};
   pa.cu_q = cu_seqlens_q; pa.cu_k = cu_seqlens_k; pa.nseg = batch;
   pa.total_q = total_q; pa.total_k = total_k; pa.heads = heads;
@@ -1144,24 +1384,60 @@ int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k, const vo
   pa.plan_k = reinterpret_cast<int4*>(ws + L.plan_k);
   pa.bounds_q = reinterpret_cast<int2*>(ws + L.bounds_q);
   pa.bounds_k = reinterpret_cast<int2*>(ws + L.bounds_k);
-  pa.dout = a.dout; pa.out = a.out; pa.lse = softmax_lse; pa.c = a.c;
-  pa.aux = reinterpret_cast<uint2*>(ws + L.aux);
+  pa.lse = softmax_lse; pa.c = softmax_scale * kLog2e;
+  if (f32) {
+    pa.dout_f = static_cast<const float*>(dout); pa.out_f = static_cast<const float*>(out);
+    pa.rows_f = reinterpret_cast<float2*>(ws + L.aux);
+  } else {
+    pa.dout = static_cast<const bf16*>(dout); pa.out = static_cast<const bf16*>(out);
+    pa.aux = reinterpret_cast<uint2*>(ws + L.aux);
+  }
   if (masked) {
-    pa.tok_src = tok_src; pa.tok_dst = tok_dst;
+    pa.tok_src = mask_a; pa.tok_dst = mask_b;
     pa.nodes = reinterpret_cast<int2*>(ws + L.nodes);
     pa.meta = reinterpret_cast<int4*>(ws + L.meta);
-    a.nodes = pa.nodes;
-    a.meta = pa.meta;
   }
   if ((rc = launch_prep(pa, false, masked, st))) return rc;
-  const int4* plan_q = pa.plan_q;
-  const int4* plan_k = pa.plan_k;
-  const int2* bounds_q = pa.bounds_q;
-  const int2* bounds_k = pa.bounds_k;
-
-  a.plan = plan_k;
-  a.bounds = bounds_k;
   const unsigned kgrid = (unsigned)groups_of(total_k) * (unsigned)heads;
+  const unsigned qgrid = (unsigned)groups_of(total_q) * (unsigned)heads;
+
+  if (f32) {
+    AttnF32Args a{};
+    a.q = static_cast<const float*>(q); a.k = static_cast<const float*>(k); a.v = static_cast<const float*>(v);
+    a.out = static_cast<const float*>(out); a.dout = static_cast<const float*>(dout);
+    a.rows = pa.rows_f;
+    a.total_q = total_q; a.total_k = total_k; a.heads = heads; a.tq_pad = pa.tq_pad;
+    a.c = softmax_scale * kLog2e; a.scale = softmax_scale;
+    a.nodes = pa.nodes;
+    a.dq = static_cast<float*>(dq); a.dk = static_cast<float*>(dk); a.dv = static_cast<float*>(dv);
+    a.plan = pa.plan_k; a.bounds = pa.bounds_k;
+    if (masked)
+      hipLaunchKernelGGL((attn_dkdv_f32_kernel<true>), dim3(kgrid), dim3(kF32Threads), 0, st, a);
+    else
+      hipLaunchKernelGGL((attn_dkdv_f32_kernel<false>), dim3(kgrid), dim3(kF32Threads), 0, st, a);
+    ESA_LAUNCH_CHECK();
+    a.plan = pa.plan_q; a.bounds = pa.bounds_q;
+    if (masked)
+      hipLaunchKernelGGL((attn_dq_f32_kernel<true>), dim3(qgrid), dim3(kF32Threads), 0, st, a);
+    else
+      hipLaunchKernelGGL((attn_dq_f32_kernel<false>), dim3(qgrid), dim3(kF32Threads), 0, st, a);
+    ESA_LAUNCH_CHECK();
+    return ESA_OK;
+  }
+
+  AttnArgs a{};
+  a.q = static_cast<const bf16*>(q); a.k = static_cast<const bf16*>(k); a.v = static_cast<const bf16*>(v);
+  a.out = static_cast<const bf16*>(out); a.dout = static_cast<const bf16*>(dout); a.lse = softmax_lse;
+  a.aux = pa.aux;
+  a.cu_q = cu_seqlens_q; a.cu_k = cu_seqlens_k; a.nseg = batch;
+  a.total_q = total_q; a.total_k = total_k; a.heads = heads; a.tq_pad = pa.tq_pad;
+  a.tk_tiles = pa.tk_pad / kTile;
+  a.scale = softmax_scale; a.c = softmax_scale * kLog2e;
+  a.nodes = pa.nodes; a.meta = pa.meta;
+  a.dq = static_cast<bf16*>(dq); a.dk = static_cast<bf16*>(dk); a.dv = static_cast<bf16*>(dv);
+
+  a.plan = pa.plan_k;
+  a.bounds = pa.bounds_k;
   if (masked)
     ESA_TIMED(esa_profile::kAttnBwdDkdvMasked, st,
               hipLaunchKernelGGL((attn_dkdv_kernel<true>), dim3(kgrid), dim3(256), 0, st, a));
@@ -1170,9 +1446,8 @@ int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k, const vo
               hipLaunchKernelGGL((attn_dkdv_kernel<false>), dim3(kgrid), dim3(256), 0, st, a));
   ESA_LAUNCH_CHECK();
 
-  a.plan = plan_q;
-  a.bounds = bounds_q;
-  const unsigned qgrid = (unsigned)groups_of(total_q) * (unsigned)heads;
+  a.plan = pa.plan_q;
+  a.bounds = pa.bounds_q;
   if (masked)
     ESA_TIMED(esa_profile::kAttnBwdDqMasked, st,
               hipLaunchKernelGGL((attn_dq_kernel<true>), dim3(qgrid), dim3(256), 0, st, a));

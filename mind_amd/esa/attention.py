@@ -5,7 +5,8 @@ reference calls it (esa/mha_flash_varlen.py:177-184: causal=False, dropout 0,
 ``softmax_scale=None`` meaning 1/sqrt(head_dim)), extended with the
 edge-adjacency mask of esa/masked_layers.py:121-142 evaluated on the fly from
 per-token ``(src, dst)`` node ids.  Tensors are packed ``[total, heads, 16]``
-bf16 with int32 ``cu_seqlens``.  Backward is deterministic.
+bf16 (MFMA kernels, fp32 softmax) or float32 (fp32 throughout) with int32
+``cu_seqlens``.  Backward is deterministic.
 """
 from __future__ import annotations
 
@@ -18,17 +19,30 @@ from .. import _lib
 HEAD_DIM = 16
 
 
-def _workspace(device: torch.device, total_q: int, total_k: int, heads: int, masked: bool, backward: bool):
+_DTYPES = {torch.bfloat16: _lib.ESA_BF16, torch.float32: _lib.ESA_F32}
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    try:
+        return _DTYPES[t.dtype]
+    except KeyError:
+        raise TypeError(f"attention tensors must be bfloat16 or float32 (got {t.dtype})") from None
+
+
+def _workspace(device: torch.device, total_q: int, total_k: int, heads: int, dtype: int, mask_kind: int,
+               backward: bool):
     lib = _lib.load()
     n = _lib.ctypes.c_size_t(0)
-    _lib.check(lib.esa_varlen_attn_workspace_size(total_q, total_k, heads, HEAD_DIM, int(masked), int(backward),
-                                                  _lib.ctypes.byref(n)), "esa_varlen_attn_workspace_size")
+    _lib.check(lib.esa_varlen_attn_workspace_size(total_q, total_k, heads, HEAD_DIM, dtype, mask_kind, 0,
+                                                  int(backward), _lib.ctypes.byref(n)),
+               "esa_varlen_attn_workspace_size")
     return torch.empty(max(int(n.value), 256), dtype=torch.uint8, device=device)
 
 
-def _check_tokens(name: str, t: torch.Tensor, heads: int | None = None) -> None:
-    if t.dtype != torch.bfloat16:
-        raise TypeError(f"{name} must be bfloat16 (got {t.dtype})")
+def _check_tokens(name: str, t: torch.Tensor, heads: int | None = None, dtype: torch.dtype | None = None) -> None:
+    _dtype_code(t)
+    if dtype is not None and t.dtype != dtype:
+        raise TypeError(f"{name} is {t.dtype}; all attention tensors must share one dtype ({dtype})")
     if t.dim() != 3 or t.shape[2] != HEAD_DIM:
         raise ValueError(f"{name} must be [total, heads, {HEAD_DIM}] (got {tuple(t.shape)})")
     if heads is not None and t.shape[1] != heads:
@@ -48,53 +62,57 @@ def _check_index(name: str, t: torch.Tensor | None, n: int | None = None) -> Non
 
 def attn_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale,
              edge_src=None, edge_dst=None):
-    """Raw forward: returns ``(out [Tq,H,16] bf16, softmax_lse [H,Tq] fp32)``."""
+    """Raw forward: returns ``(out [Tq,H,16] (dtype of q), softmax_lse [H,Tq] fp32)``."""
     _lib.require_gpu(q, k, v, cu_seqlens_q, cu_seqlens_k, edge_src, edge_dst)
     heads = q.shape[1]
     _check_tokens("q", q)
-    _check_tokens("k", k, heads)
-    _check_tokens("v", v, heads)
+    _check_tokens("k", k, heads, q.dtype)
+    _check_tokens("v", v, heads, q.dtype)
     if k.shape[0] != v.shape[0]:
         raise ValueError("k and v must have the same number of tokens")
     batch = cu_seqlens_q.numel() - 1
     _check_index("cu_seqlens_q", cu_seqlens_q)
     _check_index("cu_seqlens_k", cu_seqlens_k, batch + 1)
-    masked = edge_src is not None
-    if masked:
+    mask_kind = _lib.ESA_MASK_EDGE if edge_src is not None else _lib.ESA_MASK_NONE
+    if edge_src is not None:
         _check_index("edge_src", edge_src, q.shape[0])
         _check_index("edge_dst", edge_dst, q.shape[0])
     tq, tk = q.shape[0], k.shape[0]
+    dt = _dtype_code(q)
     out = torch.empty_like(q)
     lse = torch.empty((heads, tq), dtype=torch.float32, device=q.device)
-    ws = _workspace(q.device, tq, tk, heads, masked, False)
+    ws = _workspace(q.device, tq, tk, heads, dt, mask_kind, False)
     lib = _lib.load()
     rc = lib.esa_varlen_attn_fwd(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(), batch, tq, tk,
-        int(max_seqlen_q), int(max_seqlen_k), heads, HEAD_DIM, float(softmax_scale),
-        _lib.ptr(edge_src), _lib.ptr(edge_dst), out.data_ptr(), lse.data_ptr(), ws.data_ptr(), ws.numel(),
-        _lib.stream_of(q))
+        int(max_seqlen_q), int(max_seqlen_k), heads, HEAD_DIM, dt, float(softmax_scale),
+        mask_kind, _lib.ptr(edge_src), _lib.ptr(edge_dst), 0, out.data_ptr(), lse.data_ptr(), ws.data_ptr(),
+        ws.numel(), _lib.stream_of(q))
     _lib.check(rc, "esa_varlen_attn_fwd")
     return out, lse
 
 
 def attn_bwd(dout, q, k, v, out, lse, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale,
              edge_src=None, edge_dst=None):
-    """Raw backward: returns ``(dq, dk, dv)`` (bf16, shapes of q, k, v)."""
+    """Raw backward: returns ``(dq, dk, dv)`` (dtype and shapes of q, k, v)."""
     _lib.require_gpu(dout, q, k, v, out, lse)
     heads = q.shape[1]
-    _check_tokens("dout", dout, heads)
-    if dout.shape != q.shape:
-        raise ValueError("dout must have the shape of q")
+    _check_tokens("q", q)
+    for name, t in (("dout", dout), ("k", k), ("v", v), ("out", out)):
+        _check_tokens(name, t, heads, q.dtype)
+    if dout.shape != q.shape or out.shape != q.shape:
+        raise ValueError("dout and out must have the shape of q")
     batch = cu_seqlens_q.numel() - 1
     tq, tk = q.shape[0], k.shape[0]
-    masked = edge_src is not None
+    mask_kind = _lib.ESA_MASK_EDGE if edge_src is not None else _lib.ESA_MASK_NONE
+    dt = _dtype_code(q)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
-    ws = _workspace(q.device, tq, tk, heads, masked, True)
+    ws = _workspace(q.device, tq, tk, heads, dt, mask_kind, True)
     lib = _lib.load()
     rc = lib.esa_varlen_attn_bwd(
         dout.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr(),
         cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(), batch, tq, tk, int(max_seqlen_q), int(max_seqlen_k),
-        heads, HEAD_DIM, float(softmax_scale), _lib.ptr(edge_src), _lib.ptr(edge_dst),
+        heads, HEAD_DIM, dt, float(softmax_scale), mask_kind, _lib.ptr(edge_src), _lib.ptr(edge_dst), 0,
         dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_of(q))
     _lib.check(rc, "esa_varlen_attn_bwd")
     return dq, dk, dv
@@ -122,7 +140,8 @@ def varlen_attention(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seql
                      softmax_scale=None, causal=False, edge_src=None, edge_dst=None, return_lse=False):
     """``flash_attn_varlen_func``-compatible entry (plus the edge mask).
 
-    q: [Tq, H, 16] bf16; k, v: [Tk, H, 16] bf16; cu_seqlens_*: int32 [B+1].
+    q: [Tq, H, 16]; k, v: [Tk, H, 16], all bfloat16 or all float32;
+    cu_seqlens_*: int32 [B+1].
     edge_src / edge_dst: optional int32 [Tq] node ids per token (self-attention
     only); token i then attends to token j of its segment iff i != j and the
     two edges share an endpoint.  With return_lse, also returns the

@@ -43,8 +43,10 @@ def _uniform_cu(batch: int, n: int, device) -> torch.Tensor:
 
 
 def _heads(x: torch.Tensor, heads: int) -> torch.Tensor:
-    """[..., H * 16] -> contiguous bf16 [tokens, H, 16]."""
-    return x.reshape(-1, heads, x.shape[-1] // heads).to(torch.bfloat16).contiguous()
+    """[..., H * 16] -> contiguous [tokens, H, 16]: float32 stays float32 (the fp32 kernels), any other
+    dtype runs on the bf16 kernels."""
+    dt = torch.float32 if x.dtype == torch.float32 else torch.bfloat16
+    return x.reshape(-1, heads, x.shape[-1] // heads).to(dt).contiguous()
 
 
 def dense_attention(q, k, v, heads):

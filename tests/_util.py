@@ -27,6 +27,16 @@ def assert_bf16_close(got, ref, scale: float = 1.0, what: str = ""):
         f"(bar {BF16_MEAN_ABS * scale:.3e})")
 
 
+F32_REL = 1e-5
+
+
+def assert_f32_close(got, ref, what: str = ""):
+    """fp32 bar: max-abs <= 1e-5 * max(1, max |ref|) (relative, norm-wise)."""
+    mx, _ = err(got, ref)
+    bar = F32_REL * max(1.0, float(ref.abs().max()) if ref.numel() else 0.0)
+    assert mx <= bar, f"{what}: max-abs {mx:.3e} > {bar:.3e} (fp32 bar)"
+
+
 def grad_scale(ref: torch.Tensor) -> float:
     """Gradients are checked relative to their own magnitude (at least 1)."""
     return max(1.0, float(ref.abs().max()))

@@ -60,12 +60,17 @@ def test_argument_errors_need_no_gpu():
         pytest.skip("library not built")
     lib = _lib.load()
     n = ctypes.c_size_t(0)
-    assert lib.esa_varlen_attn_workspace_size(100, 100, 16, 32, 0, 0, ctypes.byref(n)) == -3
-    assert lib.esa_varlen_attn_workspace_size(100, 90, 16, 16, 1, 0, ctypes.byref(n)) == -7
-    assert lib.esa_varlen_attn_workspace_size(100, 100, 16, 16, 0, 1, ctypes.byref(n)) == 0 and n.value > 0
+    bf16, f32, none, edge = _lib.ESA_BF16, _lib.ESA_F32, _lib.ESA_MASK_NONE, _lib.ESA_MASK_EDGE
+    assert lib.esa_varlen_attn_workspace_size(100, 100, 16, 32, bf16, none, 0, 0, ctypes.byref(n)) == -3
+    assert lib.esa_varlen_attn_workspace_size(100, 90, 16, 16, bf16, edge, 0, 0, ctypes.byref(n)) == -7
+    assert lib.esa_varlen_attn_workspace_size(100, 100, 16, 16, 7, none, 0, 0, ctypes.byref(n)) == -5
+    assert lib.esa_varlen_attn_workspace_size(100, 100, 16, 16, bf16, 9, 0, 0, ctypes.byref(n)) == -7
+    for dt in (bf16, f32):
+        assert lib.esa_varlen_attn_workspace_size(100, 100, 16, 16, dt, none, 0, 1, ctypes.byref(n)) == 0
+        assert n.value > 0
     # fwd with a too-small workspace is rejected before anything is launched
-    rc = lib.esa_varlen_attn_fwd(16, 16, 16, 16, 16, 1, 100, 100, 100, 100, 16, 16, 0.25, None, None, 16, 16,
-                                 256, 10, None)
+    rc = lib.esa_varlen_attn_fwd(16, 16, 16, 16, 16, 1, 100, 100, 100, 100, 16, 16, bf16, 0.25, none, None, None, 0,
+                                 16, 16, 256, 10, None)
     assert rc == -4
     assert lib.esa_edge_gather(16, 16, 16, 10, 10, 8, 7, 16, None) == -5
     assert lib.esa_csr_workspace_size(-1, 10, ctypes.byref(n)) == -2
