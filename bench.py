@@ -475,6 +475,15 @@ def bench_gather(args):
         del x, y, out, agg
         torch.cuda.empty_cache()
 
+    # in-process reference: a plain device-to-device copy (torch) of the fp32 edge-output size, the practical
+    # streaming rate of this allocation on this box
+    a = torch.empty(GATHER_E, GATHER_F, device=dev)
+    b = torch.empty_like(a)
+    copy_ms, _, _ = timed(lambda: b.copy_(a), 5, 2)
+    copy_gbs = 2 * a.numel() * 4 / (copy_ms * 1e-3) / 1e9
+    del a, b
+    torch.cuda.empty_cache()
+
     f32 = results["f32"]
     dom = max(("edge_gather", "segment_sum"), key=lambda n: f32["kernels"][n]["avg_us"])
     achieved = f32["kernels"][dom]["achieved_gbs"]
@@ -501,6 +510,7 @@ def bench_gather(args):
             "order": "dst-sorted (CSR); generation order reported beside", "seed": args.seed,
         },
         "csr_build_ms": csr_ms,
+        "reference_copy_gbs": copy_gbs,
         "f32": f32,
         "bf16": results["bf16"],
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",

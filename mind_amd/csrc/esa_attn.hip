@@ -66,9 +66,6 @@ constexpr float kDeadRow = -1.0e30f;        // -LSE2/c for rows without keys: ev
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
-DEVI rsrc_t make_rsrc(const void* p, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
-}
 DEVI i32x4 bload(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0); }
 DEVI bf16x8 as_bf16x8(i32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 

@@ -43,3 +43,9 @@ DEVI int seg_of(const int* __restrict__ cu, int nseg, int t) {
 }
 
 DEVI int ceil_div(int a, int b) { return (a + b - 1) / b; }
+
+// Raw buffer resource over `bytes` bytes at p: a load whose byte range lies
+// past the end returns zeros without touching memory.
+DEVI __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}

@@ -43,6 +43,64 @@ __global__ __launch_bounds__(256) void edge_gather_kernel(const u32x4* __restric
   }
 }
 
+// Row mode (rows of 2 * chunks 16-byte pieces, chunks a multiple of 32): a
+// wave writes whole output rows, P pieces per lane per row, U = 16 / P edges
+// per step.  The step's src / dst ids arrive with one vector load (lanes
+// 0..U-1 and 32..32+U-1) and are broadcast with readlane, so all U * P gather
+// loads are in flight before the first store.  Loads go through a buffer
+// resource over x: a node id outside [0, num_nodes) reads zeros.  Each XCD
+// (hardware block b runs on XCD b % 8) walks one contiguous range of edges,
+// so the node rows an edge range touches stay in that XCD's L2.
+#ifndef ESA_GATHER_LOADS
+#define ESA_GATHER_LOADS 16   // 16-byte loads in flight per lane per step
+#endif
+#ifndef ESA_GATHER_EPW
+#define ESA_GATHER_EPW 32     // edges per wave
+#endif
+
+template <int P>
+__global__ __launch_bounds__(256) void edge_gather_rows_kernel(const void* x, uint32_t x_bytes,
+                                                               const int* __restrict__ src,
+                                                               const int* __restrict__ dst, long num_edges,
+                                                               int num_nodes, int chunks, int edges_per_wave,
+                                                               int blocks_per_xcd, u32x4* __restrict__ out) {
+  constexpr int U = ESA_GATHER_LOADS / P;
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(x, x_bytes);
+  const int lane = threadIdx.x & 63;
+  const int lb = (int)(blockIdx.x & 7) * blocks_per_xcd + (int)(blockIdx.x >> 3);
+  const long wave = (long)lb * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const long e_beg = wave * edges_per_wave;
+  const long e_end = min(e_beg + (long)edges_per_wave, num_edges);
+  const uint32_t row_bytes = (uint32_t)chunks * 16u;
+  const int per_row = 2 * chunks;
+  for (long e0 = e_beg; e0 < e_end; e0 += U) {
+    const long ei = min(e0 + (lane & 31), num_edges - 1);
+    const int idx = lane < 32 ? src[ei] : dst[ei];
+    u32x4 v[U][P];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int s = __builtin_amdgcn_readlane(idx, u), d = __builtin_amdgcn_readlane(idx, 32 + u);
+#pragma unroll
+      for (int j = 0; j < P; ++j) {
+        const int p = lane + 64 * j;
+        const bool first = p < chunks;
+        const int node = first ? s : d;
+        const uint32_t c = (uint32_t)(first ? p : p - chunks);
+        const uint32_t off = (unsigned)node < (unsigned)num_nodes ? (uint32_t)node * row_bytes + 16u * c : 0xFFFFFFF0u;
+        v[u][j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0));
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (e0 + u < e_end) {
+#pragma unroll
+        for (int j = 0; j < P; ++j)
+          __builtin_nontemporal_store(v[u][j], &out[(size_t)(e0 + u) * per_row + lane + 64 * j]);
+      }
+    }
+  }
+}
+
 // Element-wise fallback for rows that are not a multiple of 16 bytes.
 template <typename T>
 __global__ void edge_gather_scalar_kernel(const T* __restrict__ x, const int* __restrict__ src,
@@ -261,6 +319,159 @@ __global__ __launch_bounds__(256) void segment_sum_kernel(const T* __restrict__ 
   }
 }
 
+// Row mode: one wave per node and the whole row across the wave (VB bytes of
+// each row per lane, rows of 64 * VB bytes).  The CSR bounds and perm entries
+// are wave-uniform (scalar loads); U rows are in flight per step and are
+// added in ascending position, so the sum is the same fp32 left-to-right sum
+// as the one-lane-per-chunk kernel.
+constexpr int kSegU = 8;
+
+template <typename T, int VB> struct RowVec;
+template <> struct RowVec<float, 16> { typedef f32x4 type; static constexpr int N = 4; };
+template <> struct RowVec<bf16, 16> { typedef bf16x8 type; static constexpr int N = 8; };
+template <> struct RowVec<bf16, 8> { typedef bf16x4 type; static constexpr int N = 4; };
+template <> struct RowVec<float, 8> { typedef float __attribute__((ext_vector_type(2))) type; static constexpr int N = 2; };
+
+template <typename T, int VB>
+DEVI void segment_rows(const T* __restrict__ y, const int* __restrict__ perm, int a, int b, long ld, int col,
+                       float* acc) {
+  typedef typename RowVec<T, VB>::type V;
+  constexpr int N = RowVec<T, VB>::N;
+  const int lane = threadIdx.x & 63;
+  for (int i = a; i < b; i += kSegU) {
+    // perm entries of this step: one vector load, broadcast with readlane
+    const int pe = perm ? perm[min(i + (lane & (kSegU - 1)), b - 1)] : 0;
+    V r[kSegU];
+#pragma unroll
+    for (int u = 0; u < kSegU; ++u) {
+      const long e = perm ? __builtin_amdgcn_readlane(pe, u) : min(i + u, b - 1);
+      r[u] = *reinterpret_cast<const V*>(y + e * ld + col);
+    }
+#pragma unroll
+    for (int u = 0; u < kSegU; ++u) {
+      if (i + u < b) {
+#pragma unroll
+        for (int k = 0; k < N; ++k) acc[k] += (float)r[u][k];
+      }
+    }
+  }
+}
+
+template <typename T, int VB>
+__global__ __launch_bounds__(256) void segment_sum_rows_kernel(const T* __restrict__ y, long ld,
+                                                               const int* __restrict__ perm1,
+                                                               const int* __restrict__ indptr1, int off1,
+                                                               const int* __restrict__ perm2,
+                                                               const int* __restrict__ indptr2, int off2,
+                                                               int num_nodes, int features, T* __restrict__ out) {
+  typedef typename RowVec<T, VB>::type V;
+  constexpr int N = RowVec<T, VB>::N;
+  const int lane = threadIdx.x & 63;
+  const int waves = gridDim.x * 4;
+  for (int n = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); n < num_nodes; n += waves) {
+    const int a1 = indptr1[n], b1 = indptr1[n + 1];
+    for (int col = lane * N; col < features; col += 64 * N) {
+      float acc[N];
+#pragma unroll
+      for (int k = 0; k < N; ++k) acc[k] = 0.f;
+      segment_rows<T, VB>(y, perm1, a1, b1, ld, off1 + col, acc);
+      if (indptr2) segment_rows<T, VB>(y, perm2, indptr2[n], indptr2[n + 1], ld, off2 + col, acc);
+      V o;
+#pragma unroll
+      for (int k = 0; k < N; ++k) o[k] = (T)acc[k];
+      *reinterpret_cast<V*>(out + (size_t)n * features + col) = o;
+    }
+  }
+}
+
+// Stream mode for one CSR whose rows are exactly one wave-load wide
+// (features * sizeof(T) == 64 * VB): a wave owns `npw` consecutive nodes and
+// walks their positions indptr[n0] .. indptr[n0 + npw] as one stream, U rows
+// per step with the next step's loads in flight while the current step is
+// added (two register buffers, so no load is waited for early).  A node's
+// sum is stored when the stream crosses its end; every node still gets the
+// fp32 left-to-right sum of its own rows, starting from 0.  The wave's
+// indptr entries are held one per lane and read with readlane.
+#ifndef ESA_STREAM_BYTES
+#define ESA_STREAM_BYTES 128  // bytes in flight per lane per step
+#endif
+#ifndef ESA_STREAM_NODES
+#define ESA_STREAM_NODES 32   // nodes per wave (at most 63)
+#endif
+constexpr int kStreamNodes = ESA_STREAM_NODES;
+
+template <int VB> struct StreamU { static constexpr int value = ESA_STREAM_BYTES / VB; };
+
+template <typename T, int VB>
+DEVI void stream_load(const T* __restrict__ y, const int* __restrict__ perm, int i, int iend, int col,
+                      typename RowVec<T, VB>::type* r) {
+  typedef typename RowVec<T, VB>::type V;
+  constexpr int kStreamU = StreamU<VB>::value;
+  const int lane = threadIdx.x & 63;
+  const int pe = perm ? perm[min(i + (lane & (kStreamU - 1)), iend - 1)] : 0;
+#pragma unroll
+  for (int u = 0; u < kStreamU; ++u) {
+    const long e = perm ? __builtin_amdgcn_readlane(pe, u) : min(i + u, iend - 1);
+    // read once: nontemporal, so the stream does not evict reused lines from L2
+    r[u] = __builtin_nontemporal_load(reinterpret_cast<const V*>(y + e * (long)(64 * RowVec<T, VB>::N) + col));
+  }
+}
+
+template <typename T, int VB>
+__global__ __launch_bounds__(256) void segment_sum_stream_kernel(const T* __restrict__ y,
+                                                                 const int* __restrict__ perm,
+                                                                 const int* __restrict__ indptr, int num_nodes,
+                                                                 T* __restrict__ out) {
+  typedef typename RowVec<T, VB>::type V;
+  constexpr int N = RowVec<T, VB>::N;
+  constexpr int F = 64 * N;
+  constexpr int kStreamU = StreamU<VB>::value;
+  const int lane = threadIdx.x & 63;
+  const int wave = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int n0 = wave * kStreamNodes;
+  if (n0 >= num_nodes) return;
+  const int nn = min(kStreamNodes, num_nodes - n0);
+  const int ip = indptr[n0 + min(lane, nn)];   // lanes 0..nn: indptr[n0 .. n0 + nn]
+  const int col = lane * N;
+  int k = 0;                                    // current node n0 + k
+  int b = __builtin_amdgcn_readlane(ip, 1);     // its end
+  const int iend = __builtin_amdgcn_readlane(ip, nn);
+  float acc[N];
+#pragma unroll
+  for (int c = 0; c < N; ++c) acc[c] = 0.f;
+  auto flush = [&]() {
+    V o;
+#pragma unroll
+    for (int c = 0; c < N; ++c) { o[c] = (T)acc[c]; acc[c] = 0.f; }
+    *reinterpret_cast<V*>(out + (size_t)(n0 + k) * F + col) = o;
+    ++k;
+    b = __builtin_amdgcn_readlane(ip, min(k + 1, nn));
+  };
+  auto consume = [&](int i, const V* r) {
+#pragma unroll
+    for (int u = 0; u < kStreamU; ++u) {
+      const int row = i + u;
+      if (row >= iend) break;
+      while (row >= b) flush();
+#pragma unroll
+      for (int c = 0; c < N; ++c) acc[c] += (float)r[u][c];
+    }
+  };
+  int i = __builtin_amdgcn_readlane(ip, 0);
+  V ra[kStreamU], rb[kStreamU];
+  if (i < iend) stream_load<T, VB>(y, perm, i, iend, col, ra);
+  while (i < iend) {
+    if (i + kStreamU < iend) stream_load<T, VB>(y, perm, i + kStreamU, iend, col, rb);
+    consume(i, ra);
+    i += kStreamU;
+    if (i >= iend) break;
+    if (i + kStreamU < iend) stream_load<T, VB>(y, perm, i + kStreamU, iend, col, ra);
+    consume(i, rb);
+    i += kStreamU;
+  }
+  while (k < nn) flush();
+}
+
 // Element-wise fallback for feature counts that are not a multiple of 16 bytes.
 template <typename T>
 __global__ void segment_sum_scalar_kernel(const T* __restrict__ y, long ld, const int* __restrict__ perm1,
@@ -313,7 +524,31 @@ int launch_segsum(const T* y, long ld, const int* perm1, const int* indptr1, int
   constexpr int V = Vec16<T>::N;
   const bool vec = features % V == 0 && ld % V == 0 && off1 % V == 0 && off2 % V == 0 && !misaligned16(y) &&
                    !misaligned16(out);
-  if (vec) {
+  const long row_bytes = (long)features * (long)sizeof(T);
+  const bool rows_ok = !misaligned16(y) && !misaligned16(out) && (ld * (long)sizeof(T)) % 16 == 0 &&
+                       (off1 * (long)sizeof(T)) % 16 == 0 && (off2 * (long)sizeof(T)) % 16 == 0;
+  if (rows_ok && !perm2 && !indptr2 && off1 == 0 && ld == features && (row_bytes == 64 * 16 || row_bytes == 64 * 8)) {
+    const long waves = ((long)num_nodes + kStreamNodes - 1) / kStreamNodes;
+    const unsigned blocks = (unsigned)((waves + 3) / 4);
+    if (row_bytes == 64 * 16)
+      ESA_TIMED(esa_profile::kSegmentSum, st,
+                hipLaunchKernelGGL((segment_sum_stream_kernel<T, 16>), dim3(blocks), dim3(256), 0, st, y, perm1,
+                                   indptr1, num_nodes, out));
+    else
+      ESA_TIMED(esa_profile::kSegmentSum, st,
+                hipLaunchKernelGGL((segment_sum_stream_kernel<T, 8>), dim3(blocks), dim3(256), 0, st, y, perm1,
+                                   indptr1, num_nodes, out));
+  } else if (rows_ok && row_bytes % (64 * 16) == 0) {
+    const unsigned blocks = grid_for((long)num_nodes, 4, 1L << 18);
+    ESA_TIMED(esa_profile::kSegmentSum, st,
+              hipLaunchKernelGGL((segment_sum_rows_kernel<T, 16>), dim3(blocks), dim3(256), 0, st, y, ld, perm1,
+                                 indptr1, off1, perm2, indptr2, off2, num_nodes, features, out));
+  } else if (rows_ok && row_bytes % (64 * 8) == 0) {
+    const unsigned blocks = grid_for((long)num_nodes, 4, 1L << 18);
+    ESA_TIMED(esa_profile::kSegmentSum, st,
+              hipLaunchKernelGGL((segment_sum_rows_kernel<T, 8>), dim3(blocks), dim3(256), 0, st, y, ld, perm1,
+                                 indptr1, off1, perm2, indptr2, off2, num_nodes, features, out));
+  } else if (vec) {
     const unsigned blocks = grid_for((long)num_nodes, 4, 1L << 18);
     ESA_TIMED(esa_profile::kSegmentSum, st,
               hipLaunchKernelGGL(segment_sum_kernel<T>, dim3(blocks), dim3(256), 0, st, y, ld, perm1, indptr1, off1,
@@ -339,7 +574,25 @@ int esa_edge_gather(const void* x, const int* src, const int* dst, int64_t num_e
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int es = dtype == ESA_F32 ? 4 : 2;
   const long row_bytes = (long)features * es;
-  if (row_bytes % 16 == 0 && !misaligned16(x) && !misaligned16(out)) {
+  const long x_bytes = (long)num_nodes * row_bytes;
+  const int row_chunks = (int)(row_bytes / 16);
+  const int pieces = row_bytes % 16 == 0 ? 2 * row_chunks / 64 : 0;
+  if (row_bytes % 512 == 0 && !misaligned16(x) && !misaligned16(out) && x_bytes <= (1L << 31) &&
+      (pieces == 1 || pieces == 2 || pieces == 4)) {
+    // Row mode: 32 edges per wave, a multiple of 8 blocks (one share per XCD).
+    const int epw = ESA_GATHER_EPW;
+    const long waves = (num_edges + epw - 1) / epw;
+    const long blocks8 = ((waves + 3) / 4 + 7) / 8 * 8;
+    const int per_xcd = (int)(blocks8 / 8);
+    auto go = [&](auto kern) {
+      ESA_TIMED(esa_profile::kEdgeGather, st,
+                hipLaunchKernelGGL(kern, dim3((unsigned)blocks8), dim3(256), 0, st, x, (uint32_t)x_bytes, src, dst,
+                                   (long)num_edges, num_nodes, row_chunks, epw, per_xcd, static_cast<u32x4*>(out)));
+    };
+    if (pieces == 1) go(edge_gather_rows_kernel<1>);
+    else if (pieces == 2) go(edge_gather_rows_kernel<2>);
+    else go(edge_gather_rows_kernel<4>);
+  } else if (row_bytes % 16 == 0 && !misaligned16(x) && !misaligned16(out)) {
     const int chunks = (int)(row_bytes / 16);
     // About 4096 chunk moves per block.
     int epb = (int)(4096 / (2 * chunks));

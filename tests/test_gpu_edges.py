@@ -58,6 +58,32 @@ def test_segment_sum_bit_exact_fp32_order(device, dtype):
     assert np.allclose(out.float().numpy(), f64, rtol=1e-5 if dtype == torch.float32 else 1e-2, atol=1e-4 if dtype == torch.float32 else 5e-2)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("features", [128, 256, 512])
+@pytest.mark.parametrize("with_perm", [True, False])
+def test_segment_sum_row_kernels_bit_exact(device, dtype, features, with_perm):
+    """Rows of 512 / 1024 / 2048 bytes take the one-wave-per-row kernels: same fp32 left-to-right sums.
+
+    Node count 1037 (not a multiple of the per-wave node range), skewed degrees
+    (a hub of degree 300, many empty nodes), canonical (sorted) and permuted order.
+    """
+    rng = np.random.default_rng(features + with_perm)
+    n = 1037
+    keys = np.concatenate([rng.integers(0, n // 3, size=9000), np.full(300, 17)]).astype(np.int32)
+    rng.shuffle(keys)
+    e = keys.size
+    y = torch.randn(e, features, generator=torch.Generator().manual_seed(features)).to(dtype)
+    indptr, perm = OE.csr_build(keys, n)
+    if with_perm:
+        out = edges.segment_sum_csr(y.to(device), torch.as_tensor(indptr).to(device), torch.as_tensor(perm).to(device))
+        ref = OE.segment_sum_sequential(y.float().numpy(), perm, indptr, np.float32)
+    else:
+        ys = y[torch.as_tensor(perm).long()].contiguous()
+        out = edges.segment_sum_csr(ys.to(device), torch.as_tensor(indptr).to(device))
+        ref = OE.segment_sum_sequential(ys.float().numpy(), None, indptr, np.float32)
+    assert torch.equal(out.cpu(), torch.as_tensor(ref).to(dtype))
+
+
 def test_segment_sum_constant_rows_exact(device):
     n, e = 500, 9000
     keys = np.random.default_rng(0).integers(0, n, size=e).astype(np.int32)
@@ -83,23 +109,25 @@ def _csr(keys, n):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_gather_backward(device, dtype):
+@pytest.mark.parametrize("features", [32, 256])
+def test_gather_backward(device, dtype, features):
+    f = features
     src, dst = _graph(5, 800, 6000)
-    x = torch.randn(800, 32, generator=torch.Generator().manual_seed(5)).to(dtype)
+    x = torch.randn(800, f, generator=torch.Generator().manual_seed(5)).to(dtype)
     xd = x.to(device).requires_grad_(True)
     out = edges.edge_gather(xd, torch.as_tensor(src).to(device), torch.as_tensor(dst).to(device))
-    gy = torch.randn(6000, 64, generator=torch.Generator().manual_seed(6)).to(dtype)
+    gy = torch.randn(6000, 2 * f, generator=torch.Generator().manual_seed(6)).to(dtype)
     out.backward(gy.to(device))
     got = xd.grad.cpu()
     isrc, psrc = OE.csr_build(src, 800)
     idst, pdst = OE.csr_build(dst, 800)
     g = gy.float().numpy()
     # fp32 accumulation: the src segment (first half of g) then the dst segment (second half), one rounding
-    acc = OE.segment_sum_sequential(g[:, :32], psrc, isrc, np.float32)
+    acc = OE.segment_sum_sequential(g[:, :f], psrc, isrc, np.float32)
     deg = np.diff(idst)
     for j in range(int(deg.max())):
         rows = np.nonzero(deg > j)[0]
-        acc[rows] += g[pdst[idst[rows] + j], 32:]
+        acc[rows] += g[pdst[idst[rows] + j], f:]
     assert torch.equal(got, torch.as_tensor(acc).to(dtype))
 
 
