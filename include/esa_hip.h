@@ -36,7 +36,7 @@ extern "C" {
 #define ESA_ERR_WORKSPACE (-4)  /* workspace smaller than the query says */
 #define ESA_ERR_DTYPE (-5)      /* unsupported dtype code */
 #define ESA_ERR_ALIGN (-6)      /* pointer not 16-byte aligned */
-#define ESA_ERR_MASK (-7)       /* edge mask needs total_q == total_k */
+#define ESA_ERR_MASK (-7)       /* unknown mask kind, or the edge mask without total_q == total_k */
 
 #define ESA_F32 0
 #define ESA_BF16 1
@@ -44,6 +44,7 @@ extern "C" {
 /* Attention mask kinds (see esa_varlen_attn_fwd). */
 #define ESA_MASK_NONE 0
 #define ESA_MASK_EDGE 1
+#define ESA_MASK_NODE 2
 
 /* Library version and build target, e.g. "esa_hip 0.1 gfx950". */
 ESA_API const char* esa_version(void);
@@ -68,6 +69,16 @@ ESA_API const char* esa_version(void);
 /* get_adj_mask_from_edge_index_edge (:217-268) turns into a 0 / -99999      */
 /* bias.  It is evaluated on the fly; no mask is stored.  n_mask_edges is    */
 /* unused.  ESA_MASK_NONE: mask_a, mask_b unused.                            */
+/*                                                                           */
+/* mask_kind ESA_MASK_NODE: a CSR adjacency by query, mask_a = indptr        */
+/* [total_q + 1], mask_b = indices [n_mask_edges] (key token ids); query i   */
+/* attends to keys mask_b[mask_a[i] .. mask_a[i+1]) — the mask               */
+/* get_adj_mask_from_edge_index_node (esa/masked_layers.py:79-118) encodes   */
+/* as bias[b, src, dst] = 0 per edge src -> dst (query = src).  Each row     */
+/* lists its keys in ascending order; an entry equal to its predecessor      */
+/* counts once (a repeated edge); entries outside the query's segment are    */
+/* ignored.  Work is O(n_mask_edges * heads * 16).                           */
+/*                                                                           */
 /* A query with no admissible key gets output 0 and lse = -inf.              */
 /*                                                                           */
 /* softmax_lse is [heads, total_q] fp32 (natural log), as flash-attn's.      */
@@ -156,7 +167,7 @@ ESA_API int esa_edge_gather_bwd(const void* g, const int* src_perm,
 /* launch count per kernel id (capacity >= ESA_PROFILE_KERNELS) and clears   */
 /* the record.  Not for concurrent use from several threads.                 */
 /* ------------------------------------------------------------------------ */
-#define ESA_PROFILE_KERNELS 10
+#define ESA_PROFILE_KERNELS 13
 ESA_API int esa_profile_enable(int on);
 ESA_API int esa_profile_collect(float* total_ms, int* launches, int capacity);
 ESA_API const char* esa_profile_kernel_name(int kernel);

@@ -22,6 +22,7 @@ ESA_F32 = 0
 ESA_BF16 = 1
 ESA_MASK_NONE = 0
 ESA_MASK_EDGE = 1
+ESA_MASK_NODE = 2
 
 ERRORS = {
     -1: "ESA_ERR_NULL (a required pointer is null)",
@@ -57,7 +58,7 @@ _PROTOS = {
     "esa_profile_kernel_name": (ctypes.c_char_p, [_c_int]),
 }
 
-PROFILE_KERNELS = 10
+PROFILE_KERNELS = 13
 
 _lock = threading.Lock()
 _lib = None

@@ -49,6 +49,7 @@
 #include <type_traits>
 
 #include "esa_common.h"
+#include "esa_graph_attn.h"
 #include "esa_profile.h"
 #include "../../include/esa_hip.h"
 
@@ -1219,7 +1220,7 @@ int check_common(int batch, int total_q, int total_k, int heads, int head_dim, i
   // Buffer-resource ranges are 32-bit byte counts.
   const long lim = (1L << 31) - 1;
   if ((long)round32(total_q) * heads * 32 > lim || (long)round32(total_k) * heads * 32 > lim) return ESA_ERR_SHAPE;
-  if (mask_kind != ESA_MASK_NONE && mask_kind != ESA_MASK_EDGE) return ESA_ERR_MASK;
+  if (mask_kind != ESA_MASK_NONE && mask_kind != ESA_MASK_EDGE && mask_kind != ESA_MASK_NODE) return ESA_ERR_MASK;
   if (mask_kind == ESA_MASK_EDGE && total_q != total_k) return ESA_ERR_MASK;
   return ESA_OK;
 }
@@ -1262,10 +1263,13 @@ const char* esa_version(void) { return "esa_hip 0.3 gfx950"; }
 
 int esa_varlen_attn_workspace_size(int total_q, int total_k, int heads, int head_dim, int dtype, int mask_kind,
                                    int n_mask_edges, int backward, size_t* bytes) {
-  (void)n_mask_edges;
   if (!bytes) return ESA_ERR_NULL;
   const int rc = check_common(1, total_q, total_k, heads, head_dim, dtype, mask_kind);
   if (rc) return rc;
+  if (mask_kind == ESA_MASK_NODE) {
+    if (n_mask_edges < 0) return ESA_ERR_SHAPE;
+    return graph_attn_workspace_size(total_q, total_k, heads, n_mask_edges, backward != 0, bytes);
+  }
   *bytes = ws_layout(total_q, total_k, heads, dtype, mask_kind == ESA_MASK_EDGE, backward != 0).total;
   return ESA_OK;
 }
@@ -1276,9 +1280,25 @@ int esa_varlen_attn_fwd(const void* q, const void* k, const void* v, const int* 
                         float softmax_scale, int mask_kind, const int* mask_a, const int* mask_b,
                         int n_mask_edges, void* out, float* softmax_lse, void* workspace,
                         size_t workspace_bytes, void* stream) {
-  (void)max_seqlen_q; (void)max_seqlen_k; (void)n_mask_edges;
+  (void)max_seqlen_q; (void)max_seqlen_k;
   int rc = check_common(batch, total_q, total_k, heads, head_dim, dtype, mask_kind);
   if (rc) return rc;
+  if (mask_kind == ESA_MASK_NODE) {
+    if (n_mask_edges < 0) return ESA_ERR_SHAPE;
+    if (!mask_a || (n_mask_edges > 0 && !mask_b)) return ESA_ERR_NULL;
+    if (total_q == 0) return ESA_OK;
+    if (!q || !k || !v || !cu_seqlens_q || !cu_seqlens_k || !out || !softmax_lse) return ESA_ERR_NULL;
+    if (misaligned(q) || misaligned(k) || misaligned(v) || misaligned(out)) return ESA_ERR_ALIGN;
+    if (!(softmax_scale > 0.f)) return ESA_ERR_SHAPE;
+    GraphAttnArgs g{};
+    g.q = q; g.k = k; g.v = v; g.cu_q = cu_seqlens_q; g.cu_k = cu_seqlens_k; g.nseg = batch;
+    g.total_q = total_q; g.total_k = total_k; g.heads = heads;
+    g.indptr = mask_a; g.indices = mask_b; g.nnz = n_mask_edges;
+    g.c = softmax_scale * kLog2e; g.scale = softmax_scale;
+    g.out = out; g.lse = softmax_lse;
+    (void)workspace; (void)workspace_bytes;
+    return graph_attn_fwd(g, dtype, reinterpret_cast<hipStream_t>(stream));
+  }
   const bool masked = mask_kind == ESA_MASK_EDGE;
   if (masked && (!mask_a || !mask_b)) return ESA_ERR_NULL;
   if (total_q == 0) return ESA_OK;
@@ -1346,9 +1366,29 @@ int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k, const vo
                         int heads, int head_dim, int dtype, float softmax_scale, int mask_kind,
                         const int* mask_a, const int* mask_b, int n_mask_edges, void* dq, void* dk,
                         void* dv, void* workspace, size_t workspace_bytes, void* stream) {
-  (void)max_seqlen_q; (void)max_seqlen_k; (void)n_mask_edges;
+  (void)max_seqlen_q; (void)max_seqlen_k;
   int rc = check_common(batch, total_q, total_k, heads, head_dim, dtype, mask_kind);
   if (rc) return rc;
+  if (mask_kind == ESA_MASK_NODE) {
+    if (n_mask_edges < 0) return ESA_ERR_SHAPE;
+    if (!mask_a || (n_mask_edges > 0 && !mask_b)) return ESA_ERR_NULL;
+    if (total_q == 0 && total_k == 0) return ESA_OK;
+    if (!dout || !q || !k || !v || !out || !softmax_lse || !cu_seqlens_q || !cu_seqlens_k || !dq || !dk || !dv ||
+        !workspace)
+      return ESA_ERR_NULL;
+    if (misaligned(dout) || misaligned(q) || misaligned(k) || misaligned(v) || misaligned(out) || misaligned(dq) ||
+        misaligned(dk) || misaligned(dv) || misaligned(workspace))
+      return ESA_ERR_ALIGN;
+    if (!(softmax_scale > 0.f)) return ESA_ERR_SHAPE;
+    GraphAttnArgs g{};
+    g.q = q; g.k = k; g.v = v; g.cu_q = cu_seqlens_q; g.cu_k = cu_seqlens_k; g.nseg = batch;
+    g.total_q = total_q; g.total_k = total_k; g.heads = heads;
+    g.indptr = mask_a; g.indices = mask_b; g.nnz = n_mask_edges;
+    g.c = softmax_scale * kLog2e; g.scale = softmax_scale;
+    g.out_in = out; g.dout = dout; g.lse_in = softmax_lse;
+    g.dq = dq; g.dk = dk; g.dv = dv;
+    return graph_attn_bwd(g, dtype, workspace, workspace_bytes, reinterpret_cast<hipStream_t>(stream));
+  }
   const bool masked = mask_kind == ESA_MASK_EDGE;
   if (masked && (!mask_a || !mask_b)) return ESA_ERR_NULL;
   if (total_q == 0 && total_k == 0) return ESA_OK;

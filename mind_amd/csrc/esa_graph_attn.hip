@@ -1,0 +1,353 @@
+// Node-mode (graph-adjacency) masked attention on gfx950.
+//
+// Query token i attends to the key tokens listed in row i of a CSR
+// (indptr [total_q + 1], indices [nnz]): the mask that
+// get_adj_mask_from_edge_index_node (esa/masked_layers.py:79-118) builds as a
+// padded [B, 1, N, N] bias, 0 at (graph, src_local, dst_local) of every edge
+// and -99999 elsewhere, applied by memory_efficient_attention (esa/mha.py:76).
+// Rows must list their keys in ascending order; an entry equal to its
+// predecessor is a repeated edge and counts once, as repeated writes of 0 into
+// the reference's bias do.  Entries outside the query's segment are ignored.
+//
+// The work is O(nnz * heads * 16) — a few neighbours per node — so it is
+// gathered per token instead of tiled for MFMA: one wave per token, four lanes
+// per head with four dims each (a wave covers 16 heads per pass), fp32 scores,
+// softmax and accumulation.  The forward and dQ gather over the token's CSR
+// row; dK / dV gather over the transposed CSR (entries grouped by key, in
+// ascending position), built per call by the library's stable counting sort.
+// Every sum runs in a fixed order: the backward is deterministic.
+#include "esa_common.h"
+#include "esa_graph_attn.h"
+#include "esa_profile.h"
+#include "../../include/esa_hip.h"
+
+namespace {
+
+constexpr int kGU = 4;   // CSR entries per step: their K / V (or Q / dO) rows are loaded together
+
+template <typename T> struct Row4;
+template <> struct Row4<float> { typedef f32x4 type; };
+template <> struct Row4<bf16> { typedef bf16x4 type; };
+
+// Four consecutive values of a [T][H][16] row: this lane's dims of one head.
+template <typename T>
+DEVI void load4(const T* __restrict__ p, float v[4]) {
+  const typename Row4<T>::type x = *reinterpret_cast<const typename Row4<T>::type*>(p);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) v[i] = (float)x[i];
+}
+template <typename T>
+DEVI void store4(T* __restrict__ p, const float v[4], float mul) {
+  typename Row4<T>::type x;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) x[i] = (T)(v[i] * mul);
+  *reinterpret_cast<typename Row4<T>::type*>(p) = x;
+}
+
+// Sum over the four lanes of a head (quad DPP butterfly).  Addition is
+// commutative, so all four lanes hold the identical result.
+DEVI float quad_sum(float x) {
+  x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0xB1, 0xF, 0xF, true));
+  x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x4E, 0xF, 0xF, true));
+  return x;
+}
+DEVI float dot4(const float a[4], const float b[4]) {
+  return fmaf(a[3], b[3], fmaf(a[2], b[2], fmaf(a[1], b[1], a[0] * b[0])));
+}
+
+// fp32 path: the device library's exp2f / log2f; bf16 path: the hardware
+// approximations (as in the tiled kernels).
+template <typename T> DEVI float ex2(float x) { return fast_exp2(x); }
+template <> DEVI float ex2<float>(float x) { return exp2f(x); }
+template <typename T> DEVI float lg2(float x) { return fast_log2(x); }
+template <> DEVI float lg2<float>(float x) { return log2f(x); }
+
+// This wave's token (one wave per token, four waves per block).
+DEVI int wave_token() { return blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
+// Row [pa, pb) of a CSR clamped into [0, nnz).
+DEVI void csr_row(const int* __restrict__ indptr, int t, int nnz, int& pa, int& pb) {
+  pa = min(max(indptr[t], 0), nnz);
+  pb = min(max(indptr[t + 1], pa), nnz);
+}
+
+// kGU entries of a CSR row starting at position p: partner token, and whether
+// it counts (inside the row, inside [lo, hi), not a repeat of the previous
+// entry).  `prev` carries the last partner across steps.
+DEVI void next_entries(const int* __restrict__ list, const int* __restrict__ map, int p, int pb, int lo, int hi,
+                       int& prev, int j[kGU], bool ok[kGU]) {
+#pragma unroll
+  for (int u = 0; u < kGU; ++u) {
+    const int pp = min(p + u, pb - 1);
+    const int e = list[pp];
+    const int x = map ? map[e] : e;
+    ok[u] = p + u < pb && x >= lo && x < hi && x != prev;
+    if (p + u < pb) prev = x;
+    j[u] = ok[u] ? x : lo;
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void graph_attn_fwd_kernel(const GraphAttnArgs a) {
+  const T* __restrict__ q = static_cast<const T*>(a.q);
+  const T* __restrict__ k = static_cast<const T*>(a.k);
+  const T* __restrict__ v = static_cast<const T*>(a.v);
+  const int t = wave_token();
+  if (t >= a.total_q) return;
+  const int lane = threadIdx.x & 63, H = a.heads, d0 = 4 * (lane & 3);
+  const int sg = seg_of(a.cu_q, a.nseg, t);
+  const int lo = max(a.cu_k[sg], 0), hi = min(a.cu_k[sg + 1], a.total_k);
+  int pa, pb;
+  csr_row(a.indptr, t, a.nnz, pa, pb);
+  if (hi <= lo) pb = pa;
+  for (int h0 = 0; h0 < H; h0 += 16) {
+    const int h = h0 + (lane >> 2);
+    const int hc = min(h, H - 1);
+    float qv[4], acc[4] = {0.f, 0.f, 0.f, 0.f};
+    load4<T>(q + ((size_t)t * H + hc) * kHd16 + d0, qv);
+    float m = -INFINITY, l = 0.f;
+    int prev = INT_MIN;
+    for (int p = pa; p < pb; p += kGU) {
+      int j[kGU];
+      bool ok[kGU];
+      next_entries(a.indices, nullptr, p, pb, lo, hi, prev, j, ok);
+      float kr[kGU][4], vr[kGU][4];
+#pragma unroll
+      for (int u = 0; u < kGU; ++u) {
+        load4<T>(k + ((size_t)j[u] * H + hc) * kHd16 + d0, kr[u]);
+        load4<T>(v + ((size_t)j[u] * H + hc) * kHd16 + d0, vr[u]);
+      }
+      float s[kGU];
+      float mt = m;
+#pragma unroll
+      for (int u = 0; u < kGU; ++u) {
+        s[u] = ok[u] ? quad_sum(dot4(qv, kr[u])) * a.c : -INFINITY;
+        mt = fmaxf(mt, s[u]);
+      }
+      if (mt == -INFINITY) continue;   // nothing admissible yet (uniform per head)
+      const float alpha = ex2<T>(m - mt);   // 0 while m = -inf
+      l *= alpha;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i] *= alpha;
+#pragma unroll
+      for (int u = 0; u < kGU; ++u) {
+        const float pu = ex2<T>(s[u] - mt);
+        l += pu;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] = fmaf(pu, vr[u][i], acc[i]);
+      }
+      m = mt;
+    }
+    if (h < H) {
+      store4<T>(static_cast<T*>(a.out) + ((size_t)t * H + h) * kHd16 + d0, acc, l > 0.f ? 1.f / l : 0.f);
+      if ((lane & 3) == 0) a.lse[(size_t)h * a.total_q + t] = l > 0.f ? (m + lg2<T>(l)) * kLn2 : -INFINITY;
+    }
+  }
+}
+
+// dQ_i = scale * sum_j P_ij (dP_ij - D_i) k_j over row i; also writes
+// D_i = rowsum(dO_i * O_i) per head for the dK / dV pass.
+template <typename T>
+__global__ __launch_bounds__(256) void graph_attn_dq_kernel(const GraphAttnArgs a) {
+  const T* __restrict__ q = static_cast<const T*>(a.q);
+  const T* __restrict__ k = static_cast<const T*>(a.k);
+  const T* __restrict__ v = static_cast<const T*>(a.v);
+  const T* __restrict__ o = static_cast<const T*>(a.out_in);
+  const T* __restrict__ g = static_cast<const T*>(a.dout);
+  const int t = wave_token();
+  if (t >= a.total_q) return;
+  const int lane = threadIdx.x & 63, H = a.heads, d0 = 4 * (lane & 3);
+  const int sg = seg_of(a.cu_q, a.nseg, t);
+  const int lo = max(a.cu_k[sg], 0), hi = min(a.cu_k[sg + 1], a.total_k);
+  int pa, pb;
+  csr_row(a.indptr, t, a.nnz, pa, pb);
+  if (hi <= lo) pb = pa;
+  for (int h0 = 0; h0 < H; h0 += 16) {
+    const int h = h0 + (lane >> 2);
+    const int hc = min(h, H - 1);
+    const size_t row = ((size_t)t * H + hc) * kHd16 + d0;
+    float qv[4], gv[4], ov[4], acc[4] = {0.f, 0.f, 0.f, 0.f};
+    load4<T>(q + row, qv);
+    load4<T>(g + row, gv);
+    load4<T>(o + row, ov);
+    const float dsum = quad_sum(dot4(gv, ov));
+    const float l = a.lse_in[(size_t)hc * a.total_q + t];
+    const float l2 = l == -INFINITY ? INFINITY : l * kLog2e;
+    if (h < H && (lane & 3) == 0) a.dsum[(size_t)h * a.total_q + t] = dsum;
+    int prev = INT_MIN;
+    for (int p = pa; p < pb; p += kGU) {
+      int j[kGU];
+      bool ok[kGU];
+      next_entries(a.indices, nullptr, p, pb, lo, hi, prev, j, ok);
+      float kr[kGU][4], vr[kGU][4];
+#pragma unroll
+      for (int u = 0; u < kGU; ++u) {
+        load4<T>(k + ((size_t)j[u] * H + hc) * kHd16 + d0, kr[u]);
+        load4<T>(v + ((size_t)j[u] * H + hc) * kHd16 + d0, vr[u]);
+      }
+#pragma unroll
+      for (int u = 0; u < kGU; ++u) {
+        const float pu = ok[u] ? ex2<T>(fmaf(quad_sum(dot4(qv, kr[u])), a.c, -l2)) : 0.f;
+        const float ds = pu * (quad_sum(dot4(gv, vr[u])) - dsum);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] = fmaf(ds, kr[u][i], acc[i]);
+      }
+    }
+    if (h < H) store4<T>(static_cast<T*>(a.dq) + ((size_t)t * H + h) * kHd16 + d0, acc, a.scale);
+  }
+}
+
+// dV_j = sum_i P_ij dO_i, dK_j = scale * sum_i P_ij (dP_ij - D_i) q_i over the
+// queries i whose rows list key j (the transposed CSR, ascending position).
+template <typename T>
+__global__ __launch_bounds__(256) void graph_attn_dkdv_kernel(const GraphAttnArgs a) {
+  const T* __restrict__ q = static_cast<const T*>(a.q);
+  const T* __restrict__ k = static_cast<const T*>(a.k);
+  const T* __restrict__ v = static_cast<const T*>(a.v);
+  const T* __restrict__ g = static_cast<const T*>(a.dout);
+  const int t = wave_token();
+  if (t >= a.total_k) return;
+  const int lane = threadIdx.x & 63, H = a.heads, d0 = 4 * (lane & 3);
+  const int sg = seg_of(a.cu_k, a.nseg, t);
+  const int lo = max(a.cu_q[sg], 0), hi = min(a.cu_q[sg + 1], a.total_q);
+  const int pa = a.t_indptr[t], pb = hi > lo ? a.t_indptr[t + 1] : pa;
+  for (int h0 = 0; h0 < H; h0 += 16) {
+    const int h = h0 + (lane >> 2);
+    const int hc = min(h, H - 1);
+    const size_t row = ((size_t)t * H + hc) * kHd16 + d0;
+    float kv[4], vv[4], dk[4] = {0.f, 0.f, 0.f, 0.f}, dv[4] = {0.f, 0.f, 0.f, 0.f};
+    load4<T>(k + row, kv);
+    load4<T>(v + row, vv);
+    int prev = INT_MIN;
+    for (int p = pa; p < pb; p += kGU) {
+      int i[kGU];
+      bool ok[kGU];
+      next_entries(a.t_perm, a.row_of, p, pb, lo, hi, prev, i, ok);
+      float qr[kGU][4], gr[kGU][4], l2[kGU], ds_[kGU];
+#pragma unroll
+      for (int u = 0; u < kGU; ++u) {
+        const size_t r = ((size_t)i[u] * H + hc) * kHd16 + d0;
+        load4<T>(q + r, qr[u]);
+        load4<T>(g + r, gr[u]);
+        l2[u] = a.lse_in[(size_t)hc * a.total_q + i[u]] * kLog2e;
+        ds_[u] = a.dsum[(size_t)hc * a.total_q + i[u]];
+      }
+#pragma unroll
+      for (int u = 0; u < kGU; ++u) {
+        const float pu = ok[u] ? ex2<T>(fmaf(quad_sum(dot4(qr[u], kv)), a.c, -l2[u])) : 0.f;
+        const float ds = pu * (quad_sum(dot4(gr[u], vv)) - ds_[u]);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          dv[c] = fmaf(pu, gr[u][c], dv[c]);
+          dk[c] = fmaf(ds, qr[u][c], dk[c]);
+        }
+      }
+    }
+    if (h < H) {
+      store4<T>(static_cast<T*>(a.dk) + ((size_t)t * H + h) * kHd16 + d0, dk, a.scale);
+      store4<T>(static_cast<T*>(a.dv) + ((size_t)t * H + h) * kHd16 + d0, dv, 1.f);
+    }
+  }
+}
+
+// row_of[e] = the CSR row holding entry e (-1 for an entry no row covers).
+__global__ void fill_minus_one_kernel(int* __restrict__ p, long n) {
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) p[i] = -1;
+}
+__global__ void row_of_kernel(const int* __restrict__ indptr, int rows, int nnz, int* __restrict__ row_of) {
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= rows) return;
+  int pa, pb;
+  csr_row(indptr, t, nnz, pa, pb);
+  for (int p = pa; p < pb; ++p) row_of[p] = t;
+}
+
+size_t al256(size_t x) { return (x + 255) & ~size_t(255); }
+
+struct GraphWs { size_t dsum, row_of, t_indptr, t_perm, csr, total; };
+
+int graph_ws(int total_q, int total_k, int heads, int nnz, bool backward, GraphWs& w) {
+  w = GraphWs{};
+  if (!backward) { w.total = 0; return ESA_OK; }
+  size_t csr_bytes = 0;
+  const int rc = esa_csr_workspace_size(nnz, total_k, &csr_bytes);
+  if (rc) return rc;
+  size_t off = 0;
+  w.dsum = off; off += al256((size_t)heads * total_q * 4);
+  w.row_of = off; off += al256((size_t)nnz * 4 + 4);
+  w.t_indptr = off; off += al256(((size_t)total_k + 1) * 4);
+  w.t_perm = off; off += al256((size_t)nnz * 4 + 4);
+  w.csr = off; off += al256(csr_bytes);
+  w.total = off;
+  return ESA_OK;
+}
+
+unsigned token_blocks(int tokens) { return (unsigned)((tokens + 3) / 4); }
+
+}  // namespace
+
+int graph_attn_workspace_size(int total_q, int total_k, int heads, int nnz, bool backward, size_t* bytes) {
+  GraphWs w;
+  const int rc = graph_ws(total_q, total_k, heads, nnz, backward, w);
+  if (rc) return rc;
+  *bytes = w.total;
+  return ESA_OK;
+}
+
+int graph_attn_fwd(GraphAttnArgs a, int dtype, hipStream_t st) {
+  if (a.total_q == 0) return ESA_OK;
+  const dim3 grid(token_blocks(a.total_q)), block(256);
+  if (dtype == ESA_F32)
+    ESA_TIMED(esa_profile::kGraphFwd, st, hipLaunchKernelGGL(graph_attn_fwd_kernel<float>, grid, block, 0, st, a));
+  else
+    ESA_TIMED(esa_profile::kGraphFwd, st, hipLaunchKernelGGL(graph_attn_fwd_kernel<bf16>, grid, block, 0, st, a));
+  ESA_LAUNCH_CHECK();
+  return ESA_OK;
+}
+
+int graph_attn_bwd(GraphAttnArgs a, int dtype, void* workspace, size_t workspace_bytes, hipStream_t st) {
+  GraphWs w;
+  int rc = graph_ws(a.total_q, a.total_k, a.heads, a.nnz, true, w);
+  if (rc) return rc;
+  if (workspace_bytes < w.total) return ESA_ERR_WORKSPACE;
+  char* ws = static_cast<char*>(workspace);
+  a.dsum = reinterpret_cast<float*>(ws + w.dsum);
+  a.row_of = reinterpret_cast<int*>(ws + w.row_of);
+  a.t_indptr = reinterpret_cast<int*>(ws + w.t_indptr);
+  a.t_perm = reinterpret_cast<int*>(ws + w.t_perm);
+  // transposed CSR: entries grouped by key, ascending position inside a key
+  if (a.nnz > 0) {
+    const long nb = ((long)a.nnz + 255) / 256;
+    hipLaunchKernelGGL(fill_minus_one_kernel, dim3((unsigned)(nb < 4096 ? nb : 4096)), dim3(256), 0, st, a.row_of,
+                       (long)a.nnz);
+    ESA_LAUNCH_CHECK();
+    if (a.total_q > 0) {
+      hipLaunchKernelGGL(row_of_kernel, dim3((unsigned)((a.total_q + 255) / 256)), dim3(256), 0, st, a.indptr,
+                         a.total_q, a.nnz, a.row_of);
+      ESA_LAUNCH_CHECK();
+    }
+  }
+  size_t csr_bytes = 0;
+  if ((rc = esa_csr_workspace_size(a.nnz, a.total_k, &csr_bytes))) return rc;
+  if ((rc = esa_csr_build(a.indices, a.nnz, a.total_k, a.t_indptr, a.t_perm, ws + w.csr, csr_bytes, st))) return rc;
+  const dim3 block(256);
+  if (a.total_q > 0) {
+    if (dtype == ESA_F32)
+      ESA_TIMED(esa_profile::kGraphDq, st,
+                hipLaunchKernelGGL(graph_attn_dq_kernel<float>, dim3(token_blocks(a.total_q)), block, 0, st, a));
+    else
+      ESA_TIMED(esa_profile::kGraphDq, st,
+                hipLaunchKernelGGL(graph_attn_dq_kernel<bf16>, dim3(token_blocks(a.total_q)), block, 0, st, a));
+    ESA_LAUNCH_CHECK();
+  }
+  if (a.total_k > 0) {
+    if (dtype == ESA_F32)
+      ESA_TIMED(esa_profile::kGraphDkdv, st,
+                hipLaunchKernelGGL(graph_attn_dkdv_kernel<float>, dim3(token_blocks(a.total_k)), block, 0, st, a));
+    else
+      ESA_TIMED(esa_profile::kGraphDkdv, st,
+                hipLaunchKernelGGL(graph_attn_dkdv_kernel<bf16>, dim3(token_blocks(a.total_k)), block, 0, st, a));
+    ESA_LAUNCH_CHECK();
+  }
+  return ESA_OK;
+}

@@ -17,6 +17,9 @@ enum Kernel : int {
   kEdgeGather,
   kSegmentSum,
   kCsrBuild,
+  kGraphFwd,        // node-mode (CSR adjacency) attention
+  kGraphDq,
+  kGraphDkdv,
   kNumKernels
 };
 

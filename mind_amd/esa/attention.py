@@ -30,10 +30,10 @@ def _dtype_code(t: torch.Tensor) -> int:
 
 
 def _workspace(device: torch.device, total_q: int, total_k: int, heads: int, dtype: int, mask_kind: int,
-               backward: bool):
+               nnz: int, backward: bool):
     lib = _lib.load()
     n = _lib.ctypes.c_size_t(0)
-    _lib.check(lib.esa_varlen_attn_workspace_size(total_q, total_k, heads, HEAD_DIM, dtype, mask_kind, 0,
+    _lib.check(lib.esa_varlen_attn_workspace_size(total_q, total_k, heads, HEAD_DIM, dtype, mask_kind, nnz,
                                                   int(backward), _lib.ctypes.byref(n)),
                "esa_varlen_attn_workspace_size")
     return torch.empty(max(int(n.value), 256), dtype=torch.uint8, device=device)
@@ -60,10 +60,25 @@ def _check_index(name: str, t: torch.Tensor | None, n: int | None = None) -> Non
         raise ValueError(f"{name} has {t.numel()} entries, expected {n}")
 
 
+def _mask_args(tq: int, edge_src, edge_dst, adj_indptr, adj_indices):
+    """(mask_kind, mask_a, mask_b, n_mask_edges) of the C ABI for the given mask tensors."""
+    if edge_src is not None and adj_indptr is not None:
+        raise ValueError("give either the edge mask (edge_src / edge_dst) or the node adjacency, not both")
+    if edge_src is not None:
+        _check_index("edge_src", edge_src, tq)
+        _check_index("edge_dst", edge_dst, tq)
+        return _lib.ESA_MASK_EDGE, edge_src, edge_dst, 0
+    if adj_indptr is not None:
+        _check_index("adj_indptr", adj_indptr, tq + 1)
+        _check_index("adj_indices", adj_indices)
+        return _lib.ESA_MASK_NODE, adj_indptr, adj_indices, adj_indices.numel()
+    return _lib.ESA_MASK_NONE, None, None, 0
+
+
 def attn_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale,
-             edge_src=None, edge_dst=None):
+             edge_src=None, edge_dst=None, adj_indptr=None, adj_indices=None):
     """Raw forward: returns ``(out [Tq,H,16] (dtype of q), softmax_lse [H,Tq] fp32)``."""
-    _lib.require_gpu(q, k, v, cu_seqlens_q, cu_seqlens_k, edge_src, edge_dst)
+    _lib.require_gpu(q, k, v, cu_seqlens_q, cu_seqlens_k, edge_src, edge_dst, adj_indptr, adj_indices)
     heads = q.shape[1]
     _check_tokens("q", q)
     _check_tokens("k", k, heads, q.dtype)
@@ -73,27 +88,24 @@ def attn_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, so
     batch = cu_seqlens_q.numel() - 1
     _check_index("cu_seqlens_q", cu_seqlens_q)
     _check_index("cu_seqlens_k", cu_seqlens_k, batch + 1)
-    mask_kind = _lib.ESA_MASK_EDGE if edge_src is not None else _lib.ESA_MASK_NONE
-    if edge_src is not None:
-        _check_index("edge_src", edge_src, q.shape[0])
-        _check_index("edge_dst", edge_dst, q.shape[0])
     tq, tk = q.shape[0], k.shape[0]
+    mask_kind, mask_a, mask_b, nnz = _mask_args(tq, edge_src, edge_dst, adj_indptr, adj_indices)
     dt = _dtype_code(q)
     out = torch.empty_like(q)
     lse = torch.empty((heads, tq), dtype=torch.float32, device=q.device)
-    ws = _workspace(q.device, tq, tk, heads, dt, mask_kind, False)
+    ws = _workspace(q.device, tq, tk, heads, dt, mask_kind, nnz, False)
     lib = _lib.load()
     rc = lib.esa_varlen_attn_fwd(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(), batch, tq, tk,
         int(max_seqlen_q), int(max_seqlen_k), heads, HEAD_DIM, dt, float(softmax_scale),
-        mask_kind, _lib.ptr(edge_src), _lib.ptr(edge_dst), 0, out.data_ptr(), lse.data_ptr(), ws.data_ptr(),
+        mask_kind, _lib.ptr(mask_a), _lib.ptr(mask_b), nnz, out.data_ptr(), lse.data_ptr(), ws.data_ptr(),
         ws.numel(), _lib.stream_of(q))
     _lib.check(rc, "esa_varlen_attn_fwd")
     return out, lse
 
 
 def attn_bwd(dout, q, k, v, out, lse, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale,
-             edge_src=None, edge_dst=None):
+             edge_src=None, edge_dst=None, adj_indptr=None, adj_indices=None):
     """Raw backward: returns ``(dq, dk, dv)`` (dtype and shapes of q, k, v)."""
     _lib.require_gpu(dout, q, k, v, out, lse)
     heads = q.shape[1]
@@ -104,15 +116,15 @@ def attn_bwd(dout, q, k, v, out, lse, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, 
         raise ValueError("dout and out must have the shape of q")
     batch = cu_seqlens_q.numel() - 1
     tq, tk = q.shape[0], k.shape[0]
-    mask_kind = _lib.ESA_MASK_EDGE if edge_src is not None else _lib.ESA_MASK_NONE
+    mask_kind, mask_a, mask_b, nnz = _mask_args(tq, edge_src, edge_dst, adj_indptr, adj_indices)
     dt = _dtype_code(q)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
-    ws = _workspace(q.device, tq, tk, heads, dt, mask_kind, True)
+    ws = _workspace(q.device, tq, tk, heads, dt, mask_kind, nnz, True)
     lib = _lib.load()
     rc = lib.esa_varlen_attn_bwd(
         dout.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr(),
         cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(), batch, tq, tk, int(max_seqlen_q), int(max_seqlen_k),
-        heads, HEAD_DIM, dt, float(softmax_scale), mask_kind, _lib.ptr(edge_src), _lib.ptr(edge_dst), 0,
+        heads, HEAD_DIM, dt, float(softmax_scale), mask_kind, _lib.ptr(mask_a), _lib.ptr(mask_b), nnz,
         dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_of(q))
     _lib.check(rc, "esa_varlen_attn_bwd")
     return dq, dk, dv
@@ -120,31 +132,35 @@ def attn_bwd(dout, q, k, v, out, lse, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, 
 
 class _VarlenAttention(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, q, k, v, cu_q, cu_k, max_q, max_k, scale, edge_src, edge_dst):
-        out, lse = attn_fwd(q, k, v, cu_q, cu_k, max_q, max_k, scale, edge_src, edge_dst)
-        ctx.save_for_backward(q, k, v, out, lse, cu_q, cu_k, edge_src, edge_dst)
+    def forward(ctx, q, k, v, cu_q, cu_k, max_q, max_k, scale, edge_src, edge_dst, adj_indptr, adj_indices):
+        out, lse = attn_fwd(q, k, v, cu_q, cu_k, max_q, max_k, scale, edge_src, edge_dst, adj_indptr, adj_indices)
+        ctx.save_for_backward(q, k, v, out, lse, cu_q, cu_k, edge_src, edge_dst, adj_indptr, adj_indices)
         ctx.meta = (max_q, max_k, scale)
         ctx.mark_non_differentiable(lse)
         return out, lse
 
     @staticmethod
     def backward(ctx, dout, _dlse):
-        q, k, v, out, lse, cu_q, cu_k, edge_src, edge_dst = ctx.saved_tensors
+        q, k, v, out, lse, cu_q, cu_k, edge_src, edge_dst, adj_indptr, adj_indices = ctx.saved_tensors
         max_q, max_k, scale = ctx.meta
         dq, dk, dv = attn_bwd(dout.contiguous(), q, k, v, out, lse, cu_q, cu_k, max_q, max_k, scale,
-                              edge_src, edge_dst)
-        return dq, dk, dv, None, None, None, None, None, None, None
+                              edge_src, edge_dst, adj_indptr, adj_indices)
+        return dq, dk, dv, None, None, None, None, None, None, None, None, None
 
 
 def varlen_attention(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, dropout_p=0.0,
-                     softmax_scale=None, causal=False, edge_src=None, edge_dst=None, return_lse=False):
-    """``flash_attn_varlen_func``-compatible entry (plus the edge mask).
+                     softmax_scale=None, causal=False, edge_src=None, edge_dst=None, return_lse=False,
+                     adj_indptr=None, adj_indices=None):
+    """``flash_attn_varlen_func``-compatible entry (plus the ESA masks).
 
     q: [Tq, H, 16]; k, v: [Tk, H, 16], all bfloat16 or all float32;
     cu_seqlens_*: int32 [B+1].
     edge_src / edge_dst: optional int32 [Tq] node ids per token (self-attention
     only); token i then attends to token j of its segment iff i != j and the
-    two edges share an endpoint.  With return_lse, also returns the
+    two edges share an endpoint (edge mode).
+    adj_indptr [Tq+1] / adj_indices [nnz]: optional int32 CSR adjacency (node
+    mode): token i attends to the keys listed in its row, ascending, a
+    repeated entry counting once.  With return_lse, also returns the
     (non-differentiable) softmax log-sum-exp [H, Tq]; -inf marks a query with
     no admissible key (its output is 0).
     """
@@ -156,8 +172,10 @@ def varlen_attention(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seql
         softmax_scale = 1.0 / math.sqrt(q.shape[-1])
     if (edge_src is None) != (edge_dst is None):
         raise ValueError("edge_src and edge_dst must be given together")
+    if (adj_indptr is None) != (adj_indices is None):
+        raise ValueError("adj_indptr and adj_indices must be given together")
     out, lse = _VarlenAttention.apply(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
-                                      float(softmax_scale), edge_src, edge_dst)
+                                      float(softmax_scale), edge_src, edge_dst, adj_indptr, adj_indices)
     return (out, lse) if return_lse else out
 
 

@@ -8,6 +8,8 @@ them unchanged and existing state_dicts load.  The difference is the mask:
 (O(E) device memory) instead of the [B, 1, N, N] bias built from a global
 E x E comparison (esa/masked_layers.py:121-142, 217-268); the attention
 kernels evaluate the share-an-endpoint predicate from it on the fly.
+``get_adj_mask_from_edge_index_node`` returns a ``NodeAdjacency`` (a CSR of
+the edges) instead of the node-mode bias (esa/masked_layers.py:79-118).
 
 Backend ``xformers_or_torch_attn``:
   "xformers" / "torch"  the reference's padded semantics (see mha.py);
@@ -29,7 +31,7 @@ from .mha import PMA, SAB, _heads, pooled_attention
 from .mha_flash_varlen import PMAFlashVarlen, SABFlashVarlen
 from .mlp_utils import GatedMLPMulti, SmallMLP
 from .norm_layers import LN
-from .packing import EdgeAdjacency
+from .packing import EdgeAdjacency, NodeAdjacency, PackedSets
 
 
 def get_adj_mask_from_edge_index_edge(edge_index, batch_size, max_items, batch_mapping, xformers_or_torch_attn=None,
@@ -43,10 +45,16 @@ def get_adj_mask_from_edge_index_edge(edge_index, batch_size, max_items, batch_m
     return EdgeAdjacency.from_edge_index(edge_index, batch_mapping, batch_size, max_items)
 
 
-def get_adj_mask_from_edge_index_node(*args, **kwargs):
-    """Node-mode adjacency (esa/masked_layers.py:79-118) is not on the HIP path yet."""
-    raise NotImplementedError("node-mode masked attention (apply_attention_on='node') is not implemented on the "
-                              "HIP kernels; use edge mode")
+def get_adj_mask_from_edge_index_node(edge_index, batch_size, max_items, batch_mapping, xformers_or_torch_attn=None,
+                                      use_bfloat16=True, device=None):
+    """Node-mode mask descriptor for the node tokens of a batch.
+
+    Replaces esa/masked_layers.py:79-118 (same arguments): instead of the
+    [B, 1, N, N] bias with 0 at (graph, local src, local dst) of every edge,
+    a CSR adjacency by query node (``NodeAdjacency``); query node src attends
+    to key node dst for every edge src -> dst.
+    """
+    return NodeAdjacency.from_edge_index(edge_index, batch_mapping, batch_size, max_items)
 
 
 def _backend_check(name: str) -> None:
@@ -104,7 +112,7 @@ class SABComplete(nn.Module):
             out_attn = self.sab(X, seq_lens=seq_lens, adj_mask=None)
         elif self.idx == 1:
             out_attn = self.sab(X, adj_mask)
-        elif self.idx == 0 and self.xformers_or_torch_attn == "hip" and isinstance(adj_mask, EdgeAdjacency):
+        elif self.idx == 0 and self.xformers_or_torch_attn == "hip" and isinstance(adj_mask, PackedSets):
             out_attn = _sab_valid_only(self.sab, X, adj_mask)
         else:
             out_attn = self.sab(X, None)
@@ -120,7 +128,7 @@ class SABComplete(nn.Module):
         return out, edge_index, batch_mapping, max_items, adj_mask
 
 
-def _sab_valid_only(sab: SAB, X: torch.Tensor, tokens: EdgeAdjacency) -> torch.Tensor:
+def _sab_valid_only(sab: SAB, X: torch.Tensor, tokens: PackedSets) -> torch.Tensor:
     """Unmasked self-attention over each graph's valid tokens (the "hip" backend's S layers)."""
     mab = sab.mab
     q = mab.fc_q(X)
@@ -169,7 +177,7 @@ class PMAComplete(nn.Module):
         if isinstance(self.pma, PMAFlashVarlen):
             seq_lens = torch.bincount(batch_mapping, minlength=X.size(0)).to(torch.int32)
             out_attn = self.pma(X, seq_lens=seq_lens)
-        elif self.xformers_or_torch_attn == "hip" and isinstance(adj_mask, EdgeAdjacency):
+        elif self.xformers_or_torch_attn == "hip" and isinstance(adj_mask, PackedSets):
             out_attn = pooled_attention(self.pma.mab, self.pma.S.repeat(X.size(0), 1, 1), X, adj_mask)
         else:
             out_attn = self.pma(X)
@@ -198,8 +206,8 @@ class ESA(nn.Module):
         super().__init__()
         assert len(layer_types) == len(dim_hidden) and len(layer_types) == len(num_heads)
         _backend_check(xformers_or_torch_attn)
-        if node_or_edge != "edge":
-            raise NotImplementedError("node-mode ESA is not on the HIP path yet; use node_or_edge='edge'")
+        if node_or_edge not in ("node", "edge"):
+            raise ValueError(f"node_or_edge must be 'node' or 'edge' (got {node_or_edge!r})")
         self.dim_hidden, self.num_heads, self.layer_types = dim_hidden, num_heads, layer_types
         self.node_or_edge = node_or_edge
         self.xformers_or_torch_attn = xformers_or_torch_attn
@@ -248,8 +256,9 @@ class ESA(nn.Module):
             self.dim_pma = dim_pma
 
     def forward(self, X, edge_index, batch_mapping, num_max_items, pos=None):
-        adj_mask = get_adj_mask_from_edge_index_edge(edge_index=edge_index, batch_mapping=batch_mapping,
-                                                     batch_size=X.shape[0], max_items=num_max_items)
+        build = get_adj_mask_from_edge_index_node if self.node_or_edge == "node" else get_adj_mask_from_edge_index_edge
+        adj_mask = build(edge_index=edge_index, batch_mapping=batch_mapping, batch_size=X.shape[0],
+                         max_items=num_max_items)
         enc, _, _, _, _ = self.encoder((X, edge_index, batch_mapping, num_max_items, adj_mask))
         if hasattr(self, "dim_pma") and self.dim_hidden[0] != self.dim_pma:
             X = self.out_proj(X)

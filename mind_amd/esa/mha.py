@@ -9,13 +9,16 @@ state_dicts load.  Attention semantics by ``adj_mask``:
                   and SDPA compute at esa/mha.py:76 and :80-83 without a bias.
   EdgeAdjacency   the edge-adjacency mask of esa/masked_layers.py:121-142,
                   evaluated on the fly in the kernel (no [B, 1, N, N] bias).
-                  ``xformers_or_torch_attn`` picks the semantics:
+  NodeAdjacency   the node-mode mask of esa/masked_layers.py:79-118 (query
+                  src attends to key dst per edge) as a CSR adjacency.
+                  For either mask ``xformers_or_torch_attn`` picks the semantics:
                     "hip"                 packed valid tokens only; a query with
                                           no admissible key gets 0;
                     "xformers" / "torch"  the reference's padded semantics
                                           exactly: a row whose bias is -99999
-                                          everywhere (padding, or an edge sharing
-                                          no node) softmaxes over all N keys, as
+                                          everywhere (padding, an edge sharing no
+                                          node, a node without out-edges) softmaxes
+                                          over all N keys, as
                                           a constant bias shift leaves softmax
                                           unchanged.  (The "torch" backend's
                                           inverted bool mask, esa/masked_layers.py:
@@ -33,7 +36,7 @@ from torch.nn import functional as F
 from torch.nn.init import xavier_normal_
 
 from .attention import HEAD_DIM, varlen_attention
-from .packing import EdgeAdjacency
+from .packing import PackedSets
 
 BACKENDS = ("xformers", "torch", "flash_varlen", "hip")
 
@@ -60,21 +63,19 @@ def dense_attention(q, k, v, heads):
     return out.reshape(b, nq, d)
 
 
-def masked_attention(q, k, v, heads, mask: EdgeAdjacency, packed: bool):
-    """Edge-masked self-attention over [B, N, D] inputs laid out as ``mask`` says."""
+def masked_attention(q, k, v, heads, mask: PackedSets, packed: bool):
+    """Masked self-attention (edge or node mode) over [B, N, D] inputs laid out as ``mask`` says."""
     b, n, d = q.shape
     if k.shape[1] != n or n != mask.max_items or b != mask.batch_size:
-        raise ValueError("the edge mask needs queries and keys in the descriptor's [B, N] layout")
+        raise ValueError("the mask needs queries and keys in the descriptor's [B, N] layout")
     if packed:
         cu = mask.cu_seqlens
         out = varlen_attention(_heads(mask.unpad(q), heads), _heads(mask.unpad(k), heads),
-                               _heads(mask.unpad(v), heads), cu, cu, n, n, edge_src=mask.edge_src,
-                               edge_dst=mask.edge_dst)
+                               _heads(mask.unpad(v), heads), cu, cu, n, n, **mask.kernel_mask(padded=False))
         return mask.pad(out.reshape(-1, d))
-    src, dst = mask.padded_nodes()
     cu = _uniform_cu(b, n, q.device)
     qh, kh, vh = _heads(q, heads), _heads(k, heads), _heads(v, heads)
-    out_m, lse = varlen_attention(qh, kh, vh, cu, cu, n, n, edge_src=src, edge_dst=dst, return_lse=True)
+    out_m, lse = varlen_attention(qh, kh, vh, cu, cu, n, n, return_lse=True, **mask.kernel_mask(padded=True))
     out_d = varlen_attention(qh, kh, vh, cu, cu, n, n)
     dead = torch.isneginf(lse[0]).view(-1, 1, 1)   # the mask is the same for every head
     return torch.where(dead, out_d, out_m).reshape(b, n, d)
@@ -110,11 +111,11 @@ class MAB(nn.Module):
         k = self.fc_k(K)
         if adj_mask is None:
             out = dense_attention(q, k, v, self.num_heads)
-        elif isinstance(adj_mask, EdgeAdjacency):
+        elif isinstance(adj_mask, PackedSets):
             out = masked_attention(q, k, v, self.num_heads, adj_mask, packed=self.xformers_or_torch_attn == "hip")
         else:
-            raise TypeError("adj_mask must be None or an EdgeAdjacency (build it with "
-                            "get_adj_mask_from_edge_index_edge); dense bias tensors are not materialised")
+            raise TypeError("adj_mask must be None or an EdgeAdjacency / NodeAdjacency (build it with "
+                            "get_adj_mask_from_edge_index_edge / _node); dense bias tensors are not materialised")
         out = out.to(q.dtype)
         return out + F.mish(self.fc_o(out))
 
@@ -135,7 +136,7 @@ class PMA(nn.Module):
 
     Without ``seq_lens`` the seeds attend over all N positions (the reference,
     which passes no mask at its call site, esa/masked_layers.py:593).  With
-    ``seq_lens`` (an int tensor [B] or an EdgeAdjacency) they attend over each
+    ``seq_lens`` (an int tensor [B] or a packed-set descriptor) they attend over each
     set's valid tokens only.
     """
 
@@ -156,7 +157,7 @@ def pooled_attention(mab: MAB, S: torch.Tensor, X: torch.Tensor, seq_lens) -> to
     """MAB(S, X) with each batch element's keys restricted to its first seq_lens[b] tokens."""
     b, n, d = X.shape
     k_seeds = S.shape[1]
-    if isinstance(seq_lens, EdgeAdjacency):
+    if isinstance(seq_lens, PackedSets):
         xk = seq_lens.unpad(X)
         cu_k = seq_lens.cu_seqlens
     else:

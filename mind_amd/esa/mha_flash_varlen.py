@@ -19,7 +19,7 @@ from torch.nn.init import xavier_normal_
 
 from .attention import varlen_attention
 from .mha import _heads, dense_attention, masked_attention
-from .packing import EdgeAdjacency
+from .packing import PackedSets
 
 
 def _linear(layer: nn.Linear, x: torch.Tensor) -> torch.Tensor:
@@ -64,10 +64,10 @@ class MABFlashVarlen(nn.Module):
         k = self.fc_k(K)
         if adj_mask is None:
             out = dense_attention(q, k, v, self.num_heads)
-        elif isinstance(adj_mask, EdgeAdjacency):
+        elif isinstance(adj_mask, PackedSets):
             out = masked_attention(q, k, v, self.num_heads, adj_mask, packed=False)
         else:
-            raise TypeError("adj_mask must be None or an EdgeAdjacency")
+            raise TypeError("adj_mask must be None or an EdgeAdjacency / NodeAdjacency")
         out = out.to(q.dtype)
         out = out + F.mish(self.fc_o(out))
         return out.to(input_dtype) if out.dtype != input_dtype else out

@@ -1,12 +1,14 @@
-"""Packed edge-token bookkeeping on the device (no host synchronisation).
+"""Packed token bookkeeping on the device.
 
 The reference pads every graph's edge tokens to ``num_max_items`` with
 ``to_dense_batch`` (core/pretraining_model.py:211, esa/models.py:317) and
-builds a dense [B, 1, N, N] edge-adjacency bias over the whole batch
-(esa/masked_layers.py:217-268).  Here a batch is described once by an
-``EdgeAdjacency``: per-token endpoint ids, int32 ``cu_seqlens`` and each
-token's slot in the padded [B, N] layout.  It is passed where the reference
-passes ``adj_mask``; the attention kernels evaluate the mask from it on the fly.
+builds a dense [B, 1, N, N] adjacency bias over the whole batch
+(esa/masked_layers.py:79-118 node mode, :217-268 edge mode).  Here a batch is
+described once by a ``PackedSets`` descriptor: int32 ``cu_seqlens``, each
+token's slot in the padded [B, N] layout and the mask in O(tokens + edges)
+memory — per-token endpoint ids (``EdgeAdjacency``: the kernels evaluate the
+share-an-endpoint predicate on the fly) or a CSR adjacency (``NodeAdjacency``).
+It is passed where the reference passes ``adj_mask``.
 """
 from __future__ import annotations
 
@@ -28,19 +30,15 @@ def cu_seqlens_from_counts(counts: torch.Tensor) -> torch.Tensor:
 
 
 @dataclass
-class EdgeAdjacency:
-    """Edge tokens of a batch and their share-an-endpoint mask, unmaterialised.
+class PackedSets:
+    """Tokens of a batch packed graph after graph, and their slots in the padded [B, N] layout.
 
-    edge_src, edge_dst : int32 [T] endpoint node ids of each token (global ids:
-                          different graphs never share a node)
     graph              : int64 [T] graph of each token
     position           : int64 [T] slot of the token inside its graph
     cu_seqlens         : int32 [B+1] token offsets per graph
     batch_size, max_items : the padded layout [B, N] the reference uses
     """
 
-    edge_src: torch.Tensor
-    edge_dst: torch.Tensor
     graph: torch.Tensor
     position: torch.Tensor
     cu_seqlens: torch.Tensor
@@ -49,29 +47,12 @@ class EdgeAdjacency:
 
     @property
     def num_tokens(self) -> int:
-        return int(self.edge_src.numel())
+        return int(self.graph.numel())
 
     @property
     def padded_index(self) -> torch.Tensor:
         """Flat index of each token in the padded [B * N] layout."""
         return self.graph * self.max_items + self.position
-
-    @classmethod
-    def from_edge_index(cls, edge_index: torch.Tensor, batch_mapping: torch.Tensor, batch_size: int,
-                        max_items: int) -> "EdgeAdjacency":
-        """Tokens = edges in edge_index order, grouped by graph (a PyG batch).
-
-        The graph of an edge is the graph of its source node
-        (core/pretraining_model.py:202, esa/models.py:316); its slot is its
-        rank among the graph's edges, as in to_dense_batch.
-        """
-        src, dst = edge_index[0], edge_index[1]
-        graph = batch_mapping.index_select(0, src).to(torch.int64)
-        counts = torch.bincount(graph, minlength=batch_size)
-        cu = cu_seqlens_from_counts(counts)
-        position = torch.arange(graph.numel(), device=graph.device, dtype=torch.int64) - cu[:-1].to(torch.int64)[graph]
-        return cls(src.to(torch.int32).contiguous(), dst.to(torch.int32).contiguous(), graph, position, cu,
-                   int(batch_size), int(max_items))
 
     def unpad(self, x: torch.Tensor) -> torch.Tensor:
         """[B, N, ...] -> [T, ...] (the valid tokens, in token order)."""
@@ -86,6 +67,46 @@ class EdgeAdjacency:
         out = out.index_copy(0, self.padded_index, y)
         return out.view(self.batch_size, self.max_items, *y.shape[1:])
 
+    def kernel_mask(self, padded: bool) -> dict:
+        """Keyword arguments of ``varlen_attention`` that apply this mask, for packed tokens or for the
+        padded [B * N] token layout."""
+        raise NotImplementedError
+
+
+def _positions(graph: torch.Tensor, batch_size: int) -> tuple[torch.Tensor, torch.Tensor]:
+    counts = torch.bincount(graph, minlength=batch_size)
+    cu = cu_seqlens_from_counts(counts)
+    position = torch.arange(graph.numel(), device=graph.device, dtype=torch.int64) - cu[:-1].to(torch.int64)[graph]
+    return cu, position
+
+
+@dataclass
+class EdgeAdjacency(PackedSets):
+    """Edge tokens of a batch and their share-an-endpoint mask, unmaterialised.
+
+    edge_src, edge_dst : int32 [T] endpoint node ids of each token (global ids:
+                          different graphs never share a node)
+    """
+
+    edge_src: torch.Tensor = None
+    edge_dst: torch.Tensor = None
+
+    @classmethod
+    def from_edge_index(cls, edge_index: torch.Tensor, batch_mapping: torch.Tensor, batch_size: int,
+                        max_items: int) -> "EdgeAdjacency":
+        """Tokens = edges in edge_index order, grouped by graph (a PyG batch).
+
+        The graph of an edge is the graph of its source node
+        (core/pretraining_model.py:202, esa/models.py:316); its slot is its
+        rank among the graph's edges, as in to_dense_batch.
+        """
+        src, dst = edge_index[0], edge_index[1]
+        graph = batch_mapping.index_select(0, src).to(torch.int64)
+        cu, position = _positions(graph, batch_size)
+        return cls(graph=graph, position=position, cu_seqlens=cu, batch_size=int(batch_size),
+                   max_items=int(max_items), edge_src=src.to(torch.int32).contiguous(),
+                   edge_dst=dst.to(torch.int32).contiguous())
+
     def padded_nodes(self) -> tuple[torch.Tensor, torch.Tensor]:
         """Endpoint ids in the padded layout; padding slots get ids that match nothing."""
         n = self.batch_size * self.max_items
@@ -95,3 +116,56 @@ class EdgeAdjacency:
         src = fill.clone().index_copy(0, self.padded_index, self.edge_src)
         dst = (fill - n).index_copy(0, self.padded_index, self.edge_dst)
         return src, dst
+
+    def kernel_mask(self, padded: bool) -> dict:
+        if padded:
+            src, dst = self.padded_nodes()
+            return {"edge_src": src, "edge_dst": dst}
+        return {"edge_src": self.edge_src, "edge_dst": self.edge_dst}
+
+
+@dataclass
+class NodeAdjacency(PackedSets):
+    """Node tokens of a batch and the node-mode mask (query src attends to key dst per edge).
+
+    The mask get_adj_mask_from_edge_index_node (esa/masked_layers.py:79-118)
+    writes into a [B, 1, N, N] bias, kept here as a CSR by query over packed
+    token ids: row t lists the dst nodes of t's out-edges in ascending order
+    (a repeated edge appears twice and counts once).
+
+    indptr  : int32 [T+1]
+    indices : int32 [nnz]
+    """
+
+    indptr: torch.Tensor = None
+    indices: torch.Tensor = None
+
+    @classmethod
+    def from_edge_index(cls, edge_index: torch.Tensor, batch_mapping: torch.Tensor, batch_size: int,
+                        max_items: int) -> "NodeAdjacency":
+        """Tokens = nodes in node order (a PyG batch: graphs contiguous and ascending), slot = node id
+        minus the graph's first node, as to_dense_batch and unbatch_edge_index number them."""
+        graph = batch_mapping.to(torch.int64)
+        cu, position = _positions(graph, batch_size)
+        nodes = graph.numel()
+        src, dst = edge_index[0].to(torch.int64), edge_index[1].to(torch.int64)
+        key = torch.sort(src * max(nodes, 1) + dst).values
+        s_sorted = torch.div(key, max(nodes, 1), rounding_mode="floor")
+        indptr = cu_seqlens_from_counts(torch.bincount(s_sorted, minlength=nodes)[:nodes])
+        indices = (key - s_sorted * max(nodes, 1)).to(torch.int32).contiguous()
+        return cls(graph=graph, position=position, cu_seqlens=cu, batch_size=int(batch_size),
+                   max_items=int(max_items), indptr=indptr, indices=indices)
+
+    def padded_csr(self) -> tuple[torch.Tensor, torch.Tensor]:
+        """The same CSR over the padded [B * N] token layout (padding rows are empty)."""
+        pidx = self.padded_index
+        deg = (self.indptr[1:] - self.indptr[:-1]).to(torch.int64)
+        counts = torch.zeros(self.batch_size * self.max_items, dtype=torch.int64, device=deg.device)
+        counts.index_copy_(0, pidx, deg)
+        return cu_seqlens_from_counts(counts), pidx.index_select(0, self.indices.to(torch.int64)).to(torch.int32)
+
+    def kernel_mask(self, padded: bool) -> dict:
+        if padded:
+            ip, ix = self.padded_csr()
+            return {"adj_indptr": ip, "adj_indices": ix}
+        return {"adj_indptr": self.indptr, "adj_indices": self.indices}

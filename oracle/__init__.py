@@ -16,6 +16,10 @@ torch_geometric and torch_scatter are absent):
       brute force vs an independent set-intersection loop on tiny graphs;
       invariants: symmetric, zero diagonal, (u->v) ~ (v->u), no cross-graph
       pairs; nnz closed form sum_v c_v(c_v-1) - sum_{u<v} m_uv(m_uv-1).
+  mask.node_adjacency_segment / node_bias_padded
+      node_bias_padded restates esa/masked_layers.py:79-118 from edge_index;
+      the CSR blocks equal its zero entries per graph, and both agree with a
+      plain loop over the edges (repeated edges and self-loops included).
   attention.varlen_attention (fwd, lse)
       torch.nn.functional.scaled_dot_product_attention (math backend, fp64)
       per segment; special cases L=1 (out = v), q = 0 (out = mean v), a

@@ -13,10 +13,12 @@ from __future__ import annotations
 import numpy as np
 import torch
 
-from .mask import edge_adjacency_segment
+from .mask import edge_adjacency_segment, node_adjacency_segment
 
 
-def _segment_mask(edge_src, edge_dst, qs, qe, ks, ke):
+def _segment_mask(edge_src, edge_dst, qs, qe, ks, ke, adj=None):
+    if adj is not None:
+        return torch.as_tensor(node_adjacency_segment(adj[0], adj[1], qs, qe, ks, ke))
     if edge_src is None:
         return None
     assert (qs, qe) == (ks, ke), "the edge mask is self-attention only"
@@ -24,8 +26,12 @@ def _segment_mask(edge_src, edge_dst, qs, qe, ks, ke):
     return torch.as_tensor(m)
 
 
-def varlen_attention(q, k, v, cu_q, cu_k, scale, edge_src=None, edge_dst=None, dtype=torch.float64):
-    """q [Tq,H,D], k/v [Tk,H,D] -> (out [Tq,H,D], lse [H,Tq]) in ``dtype``."""
+def varlen_attention(q, k, v, cu_q, cu_k, scale, edge_src=None, edge_dst=None, dtype=torch.float64, adj=None):
+    """q [Tq,H,D], k/v [Tk,H,D] -> (out [Tq,H,D], lse [H,Tq]) in ``dtype``.
+
+    ``edge_src`` / ``edge_dst``: edge-mode mask; ``adj`` = (indptr, indices):
+    node-mode CSR adjacency (query i attends to the keys of row i).
+    """
     q, k, v = (torch.as_tensor(t).cpu().to(dtype) for t in (q, k, v))
     cu_q = np.asarray(cu_q, dtype=np.int64)
     cu_k = np.asarray(cu_k, dtype=np.int64)
@@ -43,7 +49,7 @@ def varlen_attention(q, k, v, cu_q, cu_k, scale, edge_src=None, edge_dst=None, d
         kb = k[ks:ke].permute(1, 2, 0)                  # [H, D, Lk]
         vb = v[ks:ke].permute(1, 0, 2)                  # [H, Lk, D]
         s = torch.matmul(qb, kb) * scale                # [H, Lq, Lk]
-        m = _segment_mask(edge_src, edge_dst, qs, qe, ks, ke)
+        m = _segment_mask(edge_src, edge_dst, qs, qe, ks, ke, adj)
         if m is not None:
             s = s.masked_fill(~m, float("-inf"))
         l = torch.logsumexp(s, dim=-1)                  # [H, Lq]
@@ -56,7 +62,8 @@ def varlen_attention(q, k, v, cu_q, cu_k, scale, edge_src=None, edge_dst=None, d
     return out, lse
 
 
-def varlen_attention_bwd(dout, q, k, v, cu_q, cu_k, scale, edge_src=None, edge_dst=None, dtype=torch.float64):
+def varlen_attention_bwd(dout, q, k, v, cu_q, cu_k, scale, edge_src=None, edge_dst=None, dtype=torch.float64,
+                         adj=None):
     """Analytic gradients of ``varlen_attention``: (dq, dk, dv).
 
     With P = softmax(scale Q K^T + mask), O = P V, D = rowsum(dO * O):
@@ -76,7 +83,7 @@ def varlen_attention_bwd(dout, q, k, v, cu_q, cu_k, scale, edge_src=None, edge_d
         vb = v[ks:ke].permute(1, 0, 2).contiguous()
         gb = dout[qs:qe].permute(1, 0, 2).contiguous()
         s = torch.matmul(qb, kb.transpose(1, 2).contiguous()) * scale
-        m = _segment_mask(edge_src, edge_dst, qs, qe, ks, ke)
+        m = _segment_mask(edge_src, edge_dst, qs, qe, ks, ke, adj)
         if m is not None:
             s = s.masked_fill(~m, float("-inf"))
         l = torch.logsumexp(s, dim=-1)

@@ -65,6 +65,24 @@ def node_bias_padded(edge_index: np.ndarray, batch_mapping: np.ndarray, batch_si
     return bias.unsqueeze(1)
 
 
+def node_adjacency_segment(indptr: np.ndarray, indices: np.ndarray, qs: int, qe: int, ks: int,
+                           ke: int) -> np.ndarray:
+    """[Lq, Lk] bool block of a CSR adjacency: query i attends to key j iff j is listed in row i.
+
+    The per-graph block of get_adj_mask_from_edge_index_node
+    (esa/masked_layers.py:110-112): 0 (attend) at (src_local, dst_local) of
+    every edge; repeated edges set the same entry again.
+    """
+    indptr = np.asarray(indptr, dtype=np.int64)
+    indices = np.asarray(indices, dtype=np.int64)
+    m = np.zeros((qe - qs, ke - ks), dtype=bool)
+    for i in range(qs, qe):
+        js = indices[indptr[i]:indptr[i + 1]]
+        js = js[(js >= ks) & (js < ke)]
+        m[i - qs, js - ks] = True
+    return m
+
+
 def edge_mask_nnz(src: np.ndarray, dst: np.ndarray) -> int:
     """Closed-form count of true entries of edge_adjacency_global.
 

@@ -55,15 +55,16 @@ def mab_padded(sd, prefix, Q, K, heads, bias=None):
     return o + mish(linear(sd, prefix + "fc_o.", o))
 
 
-def mab_packed(sd, prefix, Qp, Kp, cu_q, cu_k, heads, edge_src=None, edge_dst=None, v_from_k=False):
-    """MAB over packed tokens [T, D] per segment; optional edge mask; V = fc_v(K) or fc_v(fc_k(K))."""
+def mab_packed(sd, prefix, Qp, Kp, cu_q, cu_k, heads, edge_src=None, edge_dst=None, v_from_k=False, adj=None):
+    """MAB over packed tokens [T, D] per segment; optional edge mask or node CSR ``adj``; V = fc_v(K) or
+    fc_v(fc_k(K))."""
     Qp, Kp = torch.as_tensor(Qp).cpu().to(DT), torch.as_tensor(Kp).cpu().to(DT)
     q = linear(sd, prefix + "fc_q.", Qp)
     k = linear(sd, prefix + "fc_k.", Kp)
     v = linear(sd, prefix + "fc_v.", k if v_from_k else Kp)
     hd = q.shape[-1] // heads
     o, _ = varlen_attention(_heads(q, heads), _heads(k, heads), _heads(v, heads), cu_q, cu_k, 1.0 / np.sqrt(hd),
-                            edge_src, edge_dst)
+                            edge_src, edge_dst, adj=adj)
     o = o.reshape(Qp.shape[0], -1)
     return o + mish(linear(sd, prefix + "fc_o.", o))
 

@@ -44,3 +44,23 @@ def grad_scale(ref: torch.Tensor) -> float:
 
 def cu_from_lengths(lengths) -> np.ndarray:
     return np.concatenate([[0], np.cumsum(np.asarray(lengths, dtype=np.int64))]).astype(np.int32)
+
+
+def node_graph(seed, sizes, extra_dup=True, self_loops=True):
+    """A PyG-style node batch (edge_index [2, E], batch [N]): random directed edges inside each graph, plus
+    repeated edges (the first five again) and, optionally, self-loops."""
+    rng = np.random.default_rng(seed)
+    bm = np.concatenate([np.full(n, b) for b, n in enumerate(sizes)]).astype(np.int64)
+    first = np.concatenate([[0], np.cumsum(sizes)[:-1]])
+    src, dst = [], []
+    for b, n in enumerate(sizes):
+        e = 3 * n
+        s = rng.integers(0, n, size=e) + first[b]
+        d = rng.integers(0, n, size=e) + first[b]
+        keep = s != d if not self_loops else np.ones(e, bool)
+        src.append(s[keep])
+        dst.append(d[keep])
+    src, dst = np.concatenate(src), np.concatenate(dst)
+    if extra_dup:
+        src, dst = np.concatenate([src, src[:5]]), np.concatenate([dst, dst[:5]])
+    return np.stack([src, dst]).astype(np.int64), bm

@@ -1,0 +1,184 @@
+"""GPU parity of node-mode (CSR adjacency) attention against the oracle.
+
+The mask is the one get_adj_mask_from_edge_index_node (esa/masked_layers.py:79-118)
+builds: query node src attends to key node dst for every edge src -> dst.
+Kernels are called through the C ABI (mind_amd.esa.attention, mask kind
+ESA_MASK_NODE).  Bars: bf16 max-abs 2e-2 / mean-abs 2e-3 (gradients scaled by
+max(1, max|ref|)); fp32 1e-5 relative.  Graphs include repeated edges,
+self-loops, nodes without out-edges, empty and one-node graphs.
+"""
+import numpy as np
+import pytest
+import torch
+
+from mind_amd import generators
+from mind_amd.esa import attention as A
+from mind_amd.esa import masked_layers as ML
+from mind_amd.esa.mha import SAB
+from mind_amd.esa.packing import NodeAdjacency, nearest_multiple_of_8
+from oracle import attention as OA
+from oracle import mask as OM
+from oracle import modules as OMod
+from tests._util import assert_bf16_close, assert_f32_close, grad_scale, node_graph, seeded_normal
+
+pytestmark = pytest.mark.gpu
+
+D = 16
+
+
+def _run(device, sizes, seed, heads, dtype, ei=None, bm=None):
+    if ei is None:
+        ei, bm = node_graph(seed, sizes)
+    na = NodeAdjacency.from_edge_index(torch.as_tensor(ei), torch.as_tensor(bm), len(sizes), max(sizes + [1]))
+    t = len(bm)
+    q, k, v, g = (seeded_normal((t, heads, D), seed + i, dtype) for i in range(4))
+    cu = na.cu_seqlens
+    qd, kd, vd = (x.to(device).requires_grad_(True) for x in (q, k, v))
+    ip, ix = na.indptr.to(device), na.indices.to(device)
+    out, lse = A.varlen_attention(qd, kd, vd, cu.to(device), cu.to(device), 0, 0, softmax_scale=0.25,
+                                  adj_indptr=ip, adj_indices=ix, return_lse=True)
+    out.backward(g.to(device))
+    torch.cuda.synchronize()
+    adj = (na.indptr.numpy(), na.indices.numpy())
+    ref, lse_ref = OA.varlen_attention(q, k, v, cu.numpy(), cu.numpy(), 0.25, adj=adj)
+    grads = OA.varlen_attention_bwd(g, q, k, v, cu.numpy(), cu.numpy(), 0.25, adj=adj)
+    got = (out.detach().cpu(), lse.cpu(), qd.grad.cpu(), kd.grad.cpu(), vd.grad.cpu())
+    return got, (ref, lse_ref) + tuple(grads), na
+
+
+def _check(got, ref, dtype):
+    out, lse, dq, dk, dv = got
+    rout, rlse, rdq, rdk, rdv = ref
+    fin = torch.isfinite(rlse)
+    assert torch.equal(torch.isfinite(lse), fin), "lse -inf pattern (nodes without out-edges)"
+    if dtype == torch.float32:
+        assert_f32_close(out, rout, "out")
+        assert float((lse.double()[fin] - rlse[fin]).abs().max()) <= 1e-5 * max(1.0, float(rlse[fin].abs().max()))
+        for name, a, b in (("dq", dq, rdq), ("dk", dk, rdk), ("dv", dv, rdv)):
+            assert_f32_close(a, b, name)
+    else:
+        assert_bf16_close(out, rout, what="out")
+        # fp32 softmax over bf16 inputs: the LSE carries only fp32 rounding of bf16-exact scores
+        assert float((lse.double()[fin] - rlse[fin]).abs().max()) < 1e-3
+        for name, a, b in (("dq", dq, rdq), ("dk", dk, rdk), ("dv", dv, rdv)):
+            assert_bf16_close(a, b, grad_scale(b), name)
+    # rows without an admissible key: output 0
+    dead = ~fin[0]
+    assert (out[dead] == 0).all()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("heads", [16, 32, 5])
+def test_node_mask_random_graphs(device, dtype, heads):
+    sizes = [9, 1, 30, 17, 2, 25]
+    got, ref, _ = _run(device, sizes, 11 + heads, heads, dtype)
+    _check(got, ref, dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_node_mask_isolated_nodes_and_empty_graph(device, dtype):
+    """Graph 1 has no nodes, graph 2 no edges; node 0 has no out-edges."""
+    sizes = [4, 0, 3, 5]
+    ei = np.array([[1, 1, 2, 2, 2, 7, 8, 11, 11], [0, 2, 1, 3, 3, 8, 7, 10, 11]], dtype=np.int64)
+    bm = np.concatenate([np.full(n, b) for b, n in enumerate(sizes)]).astype(np.int64)
+    got, ref, na = _run(device, sizes, 3, 16, dtype, ei, bm)
+    _check(got, ref, dtype)
+    lse = got[1]
+    for node in (0, 3, 4, 5, 6, 9, 10):      # no out-edges
+        assert torch.isneginf(lse[:, node]).all()
+
+
+def test_node_mask_protein_like_full_size(device):
+    """Config-1 protein graphs in node mode (radius edges, cap 16): every node attends to its neighbours."""
+    gb = generators.protein_like(seed=0)
+    sizes = [int(n) for n in gb.node_counts]
+    got, ref, _ = _run(device, sizes, 5, 16, torch.bfloat16, gb.edge_index, gb.batch)
+    _check(got, ref, torch.bfloat16)
+
+
+def test_node_mask_backward_deterministic(device):
+    sizes = [40, 33, 51]
+    ei, bm = node_graph(2, sizes)
+    na = NodeAdjacency.from_edge_index(torch.as_tensor(ei).to(device), torch.as_tensor(bm).to(device), 3, 51)
+    t = len(bm)
+    q, k, v, g = (seeded_normal((t, 16, D), 20 + i).to(device) for i in range(4))
+    cu = na.cu_seqlens
+    out, lse = A.attn_fwd(q, k, v, cu, cu, 0, 0, 0.25, adj_indptr=na.indptr, adj_indices=na.indices)
+    r1 = A.attn_bwd(g, q, k, v, out, lse, cu, cu, 0, 0, 0.25, adj_indptr=na.indptr, adj_indices=na.indices)
+    r2 = A.attn_bwd(g, q, k, v, out, lse, cu, cu, 0, 0, 0.25, adj_indptr=na.indptr, adj_indices=na.indices)
+    for a, b in zip(r1, r2):
+        assert torch.equal(a, b)
+
+
+def _padded_nodes(sizes, n, d, seed):
+    x = torch.randn(len(sizes), n, d, generator=torch.Generator().manual_seed(seed))
+    valid = torch.zeros(len(sizes), n, dtype=torch.bool)
+    for b, L in enumerate(sizes):
+        valid[b, :L] = True
+    return x, valid
+
+
+@pytest.mark.parametrize("backend", ["hip", "xformers"])
+def test_sab_node_mask(device, backend):
+    """SAB with the node-mode mask: "hip" over valid nodes; "xformers" the reference's padded -99999 bias,
+    rows without edges (and padding) softmaxing over all N positions."""
+    sizes = [7, 12, 3, 10]
+    dm, h = 64, 4
+    n = nearest_multiple_of_8(max(sizes) + 1)
+    ei, bm = node_graph(8, sizes)
+    torch.manual_seed(4)
+    m = SAB(dm, dm, h, 0.0, backend).to(device)
+    X, valid = _padded_nodes(sizes, n, dm, 9)
+    mask = ML.get_adj_mask_from_edge_index_node(torch.as_tensor(ei).to(device), len(sizes), n,
+                                                torch.as_tensor(bm).to(device))
+    got = m(X.to(device), adj_mask=mask).cpu()
+    sd = {kk: vv.detach().cpu() for kk, vv in m.state_dict().items()}
+    if backend == "hip":
+        cu = mask.cu_seqlens.cpu().numpy()
+        ref = OMod.mab_packed(sd, "mab.", X[valid], X[valid], cu, cu, h,
+                              adj=(mask.indptr.cpu().numpy(), mask.indices.cpu().numpy()))
+        assert_f32_close(got[valid], ref, "SAB hip node mask")
+    else:
+        bias = OM.node_bias_padded(ei, bm, len(sizes), n, dtype=torch.float64)
+        ref = OMod.mab_padded(sd, "mab.", X, X, h, bias)
+        assert_f32_close(got, ref, "SAB xformers node mask")
+
+
+def test_esa_node_mode(device):
+    """ESA in node mode (every MIND YAML's apply_attention_on: node): M, S, P over node tokens, "hip" backend."""
+    sizes = [11, 6, 14]
+    dm, h = 64, 4
+    n = nearest_multiple_of_8(max(sizes) + 1)
+    ei, bm = node_graph(12, sizes)
+    torch.manual_seed(7)
+    model = ML.ESA(num_outputs=1, dim_output=dm, dim_hidden=[dm, dm, dm], num_heads=[h, h, h], layer_types="MSP",
+                   node_or_edge="node", xformers_or_torch_attn="hip", use_mlps=True, mlp_hidden_size=2 * dm,
+                   num_mlp_layers=2, mlp_type="standard").to(device)
+    X, valid = _padded_nodes(sizes, n, dm, 13)
+    g_emb, enc = model(X.to(device), torch.as_tensor(ei).to(device), torch.as_tensor(bm).to(device), n)
+    sd = {kk: vv.detach().cpu() for kk, vv in model.state_dict().items()}
+    na = NodeAdjacency.from_edge_index(torch.as_tensor(ei), torch.as_tensor(bm), len(sizes), n)
+    cu = na.cu_seqlens.numpy()
+    adj = (na.indptr.numpy(), na.indices.numpy())
+    xp = X.double()[valid]
+    h1 = OMod.sab_complete(sd, "encoder.0.", xp, h, lambda s_, p_, x: OMod.mab_packed(s_, p_, x, x, cu, cu, h, adj=adj), 2)
+    h2 = OMod.sab_complete(sd, "encoder.1.", h1, h, lambda s_, p_, x: OMod.mab_packed(s_, p_, x, x, cu, cu, h), 2)
+    enc_ref = h2 + xp
+    assert_f32_close(enc.cpu()[valid], enc_ref, "ESA node-mode encoder (valid rows)")
+    hn = OMod.layer_norm(sd, "decoder.0.norm.ln.", enc_ref)
+    S = OMod._p(sd, "decoder.0.pma.", "S").reshape(1, dm).repeat(len(sizes), 1)
+    pooled = OMod.mab_packed(sd, "decoder.0.pma.mab.", S, hn, np.arange(len(sizes) + 1), cu, h)
+    pooled = pooled + OMod.mlp_standard(sd, "decoder.0.mlp.", OMod.layer_norm(sd, "decoder.0.norm_mlp.ln.", pooled), 2)
+    g_ref = OMod.mish(OMod.linear(sd, "decoder_linear.", pooled))
+    assert_f32_close(g_emb.cpu().reshape(g_ref.shape), g_ref, "ESA node-mode graph embedding")
+
+
+def test_node_mask_argument_errors(device):
+    q = torch.zeros(4, 16, 16, dtype=torch.bfloat16, device=device)
+    cu = torch.tensor([0, 4], dtype=torch.int32, device=device)
+    ip = torch.tensor([0, 1, 1, 2], dtype=torch.int32, device=device)   # 3 rows for 4 queries
+    ix = torch.tensor([1, 0], dtype=torch.int32, device=device)
+    with pytest.raises(ValueError):
+        A.attn_fwd(q, q, q, cu, cu, 4, 4, 0.25, adj_indptr=ip, adj_indices=ix)
+    with pytest.raises(ValueError):
+        A.attn_fwd(q, q, q, cu, cu, 4, 4, 0.25, edge_src=ix, edge_dst=ix, adj_indptr=ip, adj_indices=ix)

@@ -21,6 +21,7 @@ from oracle import edges as OE
 from oracle import mask as OM
 from oracle import modules as OMod
 from oracle import packing as OP
+from tests._util import node_graph
 
 
 # ---------------------------------------------------------------- mask
@@ -82,6 +83,59 @@ def test_node_bias_padded_local_ids():
     bias = OM.node_bias_padded(ei, bm, 2, 3)
     assert bias[0, 0, 0, 1] == 0 and bias[0, 0, 1, 0] == 0 and bias[1, 0, 0, 1] == 0 and bias[1, 0, 1, 0] == 0
     assert (bias == 0).sum() == 4
+
+
+def test_node_adjacency_csr_matches_reference_bias():
+    """The CSR blocks equal the zero entries of the restated node-mode bias, and a plain loop over the edges."""
+    from mind_amd.esa.packing import NodeAdjacency
+    sizes = [7, 1, 12, 5]
+    ei, bm = node_graph(3, sizes)
+    n = 16
+    na = NodeAdjacency.from_edge_index(torch.as_tensor(ei), torch.as_tensor(bm), len(sizes), n)
+    indptr, indices = na.indptr.numpy(), na.indices.numpy()
+    assert indptr[0] == 0 and indptr[-1] == indices.size == ei.shape[1]
+    for i in range(len(bm)):   # rows ascending (a repeated edge appears twice, adjacent)
+        row = indices[indptr[i]:indptr[i + 1]]
+        assert np.all(np.diff(row) >= 0)
+    bias = OM.node_bias_padded(ei, bm, len(sizes), n)
+    cu = na.cu_seqlens.numpy()
+    for b in range(len(sizes)):
+        s, e = int(cu[b]), int(cu[b + 1])
+        blk = OM.node_adjacency_segment(indptr, indices, s, e, s, e)
+        assert np.array_equal(blk, bias[b, 0, : e - s, : e - s].numpy() == 0)
+        loop = np.zeros((e - s, e - s), bool)
+        for a_, c_ in ei.T:
+            if s <= a_ < e:
+                loop[a_ - s, c_ - s] = True
+        assert np.array_equal(blk, loop)
+    # the padded CSR reproduces the same pattern over [B * N] slots
+    ip, ix = (t.numpy() for t in na.padded_csr())
+    full = OM.node_adjacency_segment(ip, ix, 0, len(sizes) * n, 0, len(sizes) * n)
+    for b in range(len(sizes)):
+        blk = full[b * n:(b + 1) * n, b * n:(b + 1) * n]
+        assert np.array_equal(blk, bias[b, 0].numpy() == 0)
+
+
+def test_node_mask_attention_matches_reference_bias():
+    """Oracle attention with the CSR mask equals the padded attention with the reference's -99999 node bias on
+    every row with at least one out-edge."""
+    from mind_amd.esa.packing import NodeAdjacency
+    sizes = [6, 9, 4]
+    ei, bm = node_graph(5, sizes)
+    n, h, d = 12, 2, 16
+    na = NodeAdjacency.from_edge_index(torch.as_tensor(ei), torch.as_tensor(bm), len(sizes), n)
+    t = len(bm)
+    g = torch.Generator().manual_seed(1)
+    q, k, v = (torch.randn(t, h, d, generator=g, dtype=torch.float64) for _ in range(3))
+    cu = na.cu_seqlens.numpy()
+    out, lse = OA.varlen_attention(q, k, v, cu, cu, 0.25, adj=(na.indptr.numpy(), na.indices.numpy()))
+    pad = lambda x: na.pad(x)   # [B, N, H, D]
+    ref = OA.padded_attention(pad(q), pad(k), pad(v), 0.25, OM.node_bias_padded(ei, bm, len(sizes), n,
+                                                                                 dtype=torch.float64))
+    ref = na.unpad(ref)
+    has = torch.as_tensor(np.diff(na.indptr.numpy()) > 0)
+    assert torch.allclose(out[has], ref[has], atol=1e-12)
+    assert torch.isneginf(lse[:, ~has]).all() and (out[~has] == 0).all()
 
 
 # ---------------------------------------------------------------- attention
