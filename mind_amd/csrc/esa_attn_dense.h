@@ -1,0 +1,20 @@
+// Internal interface of the segment-tiled dense (unmasked) bf16 attention
+// kernels; the C ABI entry points in esa_attn.hip dispatch here for
+// ESA_MASK_NONE with ESA_BF16.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+
+struct DenseAttnCall {
+  const void* q; const void* k; const void* v;
+  const int* cu_q; const int* cu_k; int nseg;
+  int total_q, total_k, heads;
+  float scale;
+  void* out; float* lse;                             // forward outputs
+  const void* out_in; const void* dout; const float* lse_in;   // backward inputs
+  void* dq; void* dk; void* dv;                      // backward outputs
+};
+
+size_t dense_attn_workspace_size(int total_q, int total_k, int heads, bool backward);
+int dense_attn_fwd(const DenseAttnCall& c, void* workspace, size_t workspace_bytes, hipStream_t st);
+int dense_attn_bwd(const DenseAttnCall& c, void* workspace, size_t workspace_bytes, hipStream_t st);

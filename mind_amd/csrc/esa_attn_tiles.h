@@ -1,0 +1,134 @@
+// Tile constants and device helpers shared by the bf16 attention kernels
+// (the masked walks in esa_attn.hip, the segment-tiled dense kernels in
+// esa_attn_dense.hip): MFMA operand layouts, LDS tile strides, bf16 splits.
+#pragma once
+#include <climits>
+
+#include "esa_common.h"
+
+namespace {
+
+constexpr int kTile = 32;
+constexpr int kHd = 16;
+constexpr int kWaves = 4;
+constexpr int kGroupTok = kWaves * kTile;   // 128 tokens per block
+constexpr int kRowStride = 24;              // bf16 per row of a [32 tokens][16] LDS tile (48 B)
+constexpr int kTrStride = 40;               // bf16 per row of a [rows][32 tokens] LDS tile (80 B)
+constexpr float kStaticBound = 60.f;
+constexpr float kDeadRow = -1.0e30f;        // -LSE2/c for rows without keys: every exp2 underflows to 0
+
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+DEVI i32x4 bload(rsrc_t r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0); }
+DEVI bf16x8 as_bf16x8(i32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+DEVI int kperm(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
+
+DEVI bool node_adjacent(int2 a, int2 b) {
+  return (a.x == b.x) | (a.x == b.y) | (a.y == b.x) | (a.y == b.y);
+}
+
+// Conservative tile-pair test for the edge mask: node-id ranges must overlap
+// and the 64-bit node signatures (bit n & 63) must intersect.
+DEVI bool tiles_may_touch(int4 a, int4 b) {
+  if (a.y < b.x || b.y < a.x) return false;
+  return ((a.z & b.z) | (a.w & b.w)) != 0;
+}
+DEVI int4 no_touch() { return make_int4(INT_MAX, INT_MIN, 0, 0); }
+
+DEVI float wave_max(float x) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+  return x;
+}
+
+DEVI void store_rows8(bf16* __restrict__ dst, const f32x16& acc, float mul, int half) {
+  bf16x4 o0, o1;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    o0[i] = (bf16)(acc[i] * mul);
+    o1[i] = (bf16)(acc[4 + i] * mul);
+  }
+  *reinterpret_cast<bf16x4*>(dst + 4 * half) = o0;
+  *reinterpret_cast<bf16x4*>(dst + 8 + 4 * half) = o1;
+}
+
+DEVI bf16x8 cvt8(const float* p) {
+  bf16x8 r;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) r[e] = (bf16)p[e];
+  return r;
+}
+
+DEVI bf16x8 lds8(const bf16* p) { return *reinterpret_cast<const bf16x8*>(p); }
+
+// c * x as an unevaluated pair of bf16 vectors (hi + lo carries ~16
+// significant bits): two MFMAs with hi and lo give c * (a . x) in fp32
+// without a VALU multiply per score.
+DEVI void split_scaled(const bf16x8& x, float c, bf16x8& hi, bf16x8& lo) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float v = (float)x[e] * c;
+    hi[e] = (bf16)v;
+    lo[e] = (bf16)(v - (float)hi[e]);
+  }
+}
+
+DEVI f32x16 splat16(float x) {
+  f32x16 r;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) r[i] = x;
+  return r;
+}
+
+// Node pairs of the 16 partner tokens of a half-wave's accumulator rows
+// (tile-local 16(r>>3) + 8h + (r&7)), from an LDS tile of 32 node pairs.
+DEVI void lds_nodes16(const int2* sn, int half, int2 out[16]) {
+  const int4* p0 = reinterpret_cast<const int4*>(sn + 8 * half);
+  const int4* p1 = reinterpret_cast<const int4*>(sn + 16 + 8 * half);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int4 a = p0[j], b = p1[j];
+    out[2 * j] = make_int2(a.x, a.y);
+    out[2 * j + 1] = make_int2(a.z, a.w);
+    out[8 + 2 * j] = make_int2(b.x, b.y);
+    out[8 + 2 * j + 1] = make_int2(b.z, b.w);
+  }
+}
+
+DEVI int row_local(int r, int half) { return 16 * (r >> 3) + 8 * half + (r & 7); }
+
+// max |k_t| over one 32-token key tile, per head: knorm[h * n_tiles + tile].
+// Consecutive threads read consecutive heads of a token (contiguous rows).
+DEVI void knorm_block(const bf16* __restrict__ k, int total, int heads, int n_tiles, float* __restrict__ knorm,
+                      int tile, int tid) {
+  __shared__ int smax[256];
+  for (int h0 = 0; h0 < heads; h0 += 256) {
+    const int hn = min(256, heads - h0);
+    if (tid < hn) smax[tid] = 0;
+    __syncthreads();
+    for (int i = tid; i < kTile * hn; i += 256) {
+      const int t = tile * kTile + i / hn, h = h0 + i % hn;
+      if (t < total) {
+        const bf16x8* p = reinterpret_cast<const bf16x8*>(k + ((size_t)t * heads + h) * kHd);
+        const bf16x8 u = p[0], v = p[1];
+        float x = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x = fmaf((float)u[e], (float)u[e], fmaf((float)v[e], (float)v[e], x));
+        atomicMax(&smax[h - h0], __float_as_int(x));   // x >= 0: int order is float order
+      }
+    }
+    __syncthreads();
+    if (tid < hn) knorm[(size_t)(h0 + tid) * n_tiles + tile] = sqrtf(__int_as_float(smax[tid]));
+    __syncthreads();
+  }
+}
+
+DEVI uint32_t split_bf16_pair(float x) {
+  const bf16 hi = (bf16)x;
+  const bf16 lo = (bf16)(x - (float)hi);
+  return (uint32_t)__builtin_bit_cast(uint16_t, hi) | ((uint32_t)__builtin_bit_cast(uint16_t, lo) << 16);
+}
+
+}  // namespace
