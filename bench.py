@@ -48,10 +48,11 @@ def parse():
     ap.add_argument("--cpu-sample-graphs", type=int, default=3,
                     help="graphs of the batch timed on the CPU for the baseline")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--config", choices=["varlen", "masked", "gather"], default="varlen",
+    ap.add_argument("--config", choices=["varlen", "masked", "gather", "block", "stack"], default="varlen",
                     help="varlen: configuration 1 (default, the headline metric); masked: configuration 2 "
                          "(edge-masked MAB attention fwd+bwd); gather: configuration 3 (edge gather + CSR "
-                         "segment sum, HBM-bound)")
+                         "segment sum, HBM-bound); block: configuration 0 (fp32 ESA block forward on small "
+                         "molecules); stack: configuration 4 (bf16 ESA encoder stack train step)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy three times (HBM counter calibration)")
     return ap.parse_args()
@@ -121,7 +122,8 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
-    {"varlen": bench_varlen, "masked": bench_masked, "gather": bench_gather}[args.config](args)
+    {"varlen": bench_varlen, "masked": bench_masked, "gather": bench_gather, "block": bench_block,
+     "stack": bench_stack}[args.config](args)
 
 
 def timed(step, steps: int, warmup: int):
@@ -518,6 +520,187 @@ def bench_gather(args):
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline_gather(src.cpu().numpy(), dst.cpu().numpy(), args.seed, 1 << 18)
+    print(json.dumps(result), flush=True)
+
+
+def _edge_tokens(gb, types, emb, proj, device):
+    """Config-0 edge tokens: one-hot atom types -> Linear(16, 128) -> [x_src || x_dst] -> Linear(256, 128), padded
+    to [B, N, 128] (core/pretraining_model.py:152-211, esa/models.py:306-317)."""
+    import torch
+
+    from mind_amd.edges import edge_gather
+    from mind_amd.esa.packing import EdgeAdjacency, nearest_multiple_of_8
+
+    onehot = torch.nn.functional.one_hot(torch.as_tensor(types).to(device), 16).float()
+    ei = torch.as_tensor(gb.edge_index).to(device)
+    bm = torch.as_tensor(gb.batch).to(device)
+    n = nearest_multiple_of_8(gb.max_seqlen + 1)
+    tok = proj(edge_gather(emb(onehot), ei[0].int(), ei[1].int()))
+    adj = EdgeAdjacency.from_edge_index(ei, bm, gb.num_graphs, n)
+    return adj.pad(tok), ei, bm, n
+
+
+def bench_block(args):
+    """Configuration 0: the ESA block forward in fp32 (edge tokens, masked MAB + SAB + PMA(1 seed), D=128, H=8)."""
+    import torch
+
+    from mind_amd import generators
+    from mind_amd.esa.masked_layers import ESA
+
+    dev = torch.device("cuda", 0)
+    gb, types = generators.small_molecules(seed=args.seed)
+    torch.manual_seed(args.seed)
+    d, h = 128, 8
+    emb, proj = torch.nn.Linear(16, d).to(dev), torch.nn.Linear(2 * d, d).to(dev)
+    model = ESA(num_outputs=1, dim_output=d, dim_hidden=[d, d, d], num_heads=[h, h, h], layer_types="MSP",
+                xformers_or_torch_attn="hip", use_mlps=True, mlp_hidden_size=2 * d, num_mlp_layers=2,
+                mlp_type="standard").to(dev).eval()
+    t = gb.num_tokens
+
+    def step():
+        with torch.no_grad():
+            x, ei, bm, n = _edge_tokens(gb, types, emb, proj, dev)
+            model(x, ei, bm, n)
+
+    ms, wall_ms, kern = timed(step, args.steps, args.warmup)
+    result = {
+        "metric": "edge-tokens/sec through the ESA block forward (fp32)",
+        "value": t / (ms * 1e-3), "unit": "edge-tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (seeded small molecules: 64 graphs, 9-29 atoms, radius 5 A; random-init weights)",
+        "config": {"workload": "config0: edge tokens (embed, gather, project) + ESA block M-S-P(1 seed) forward",
+                   "graphs": gb.num_graphs, "edge_tokens": t, "max_seqlen": gb.max_seqlen, "dim": d, "heads": h,
+                   "seed": args.seed},
+        "wall_ms_per_step": wall_ms, "kernels": kern,
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline_block(gb, types, emb, proj, model, h)
+    print(json.dumps(result), flush=True)
+
+
+def cpu_baseline_block(gb, types, emb, proj, model, heads) -> dict:
+    """The reference's padded path on the host cores in fp32: per-graph edge bias, M, S, PMA blocks.
+
+    The oracle's block restatement (oracle/modules.py) runs with the model's weights in fp32 on the same
+    inputs; the per-graph block-diagonal bias gives the global E x E mask's entries
+    (esa/masked_layers.py:217-268) without the E x E temporaries.
+    """
+    import torch
+
+    from mind_amd.esa.packing import nearest_multiple_of_8
+    from oracle import mask as OM
+    from oracle import modules as OMod
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    OMod.DT = torch.float32   # time the restatement in fp32, the reference modules' dtype
+    sd = {k: v.detach().cpu() for k, v in model.state_dict().items()}
+    with torch.no_grad():
+        e_sd = {"w": emb.weight.detach().cpu(), "b": emb.bias.detach().cpu()}
+        p_sd = {"w": proj.weight.detach().cpu(), "b": proj.bias.detach().cpu()}
+    n = nearest_multiple_of_8(gb.max_seqlen + 1)
+    cu = gb.cu_seqlens
+    gid = np.repeat(np.arange(gb.num_graphs), gb.edge_counts)
+
+    def step():
+        x = torch.nn.functional.one_hot(torch.as_tensor(types), 16).float() @ e_sd["w"].T + e_sd["b"]
+        src, dst = torch.as_tensor(gb.edge_index[0]), torch.as_tensor(gb.edge_index[1])
+        tok = torch.cat([x[src], x[dst]], 1) @ p_sd["w"].T + p_sd["b"]
+        X = torch.zeros(gb.num_graphs * n, tok.shape[1])
+        pos = torch.as_tensor(np.arange(gb.num_tokens) - np.repeat(cu[:-1], gb.edge_counts))
+        X[torch.as_tensor(gid) * n + pos] = tok
+        X = X.view(gb.num_graphs, n, -1)
+        bias = torch.full((gb.num_graphs, 1, n, n), OM.MASK_FILL)
+        for b in range(gb.num_graphs):
+            s, e = int(cu[b]), int(cu[b + 1])
+            blk = OM.edge_adjacency_segment(gb.edge_index[0], gb.edge_index[1], s, e)
+            bias[b, 0, : e - s, : e - s][torch.as_tensor(blk)] = 0.0
+        h = OMod.sab_complete(sd, "encoder.0.", X, heads, lambda s_, p_, x_: OMod.mab_padded(s_, p_, x_, x_, heads,
+                                                                                               bias), 2)
+        h = OMod.sab_complete(sd, "encoder.1.", h, heads, lambda s_, p_, x_: OMod.mab_padded(s_, p_, x_, x_, heads),
+                              2)
+        enc = h + X
+        hn = OMod.layer_norm(sd, "decoder.0.norm.ln.", enc)
+        S = OMod._p(sd, "decoder.0.pma.", "S").repeat(gb.num_graphs, 1, 1)
+        pooled = OMod.mab_padded(sd, "decoder.0.pma.mab.", S, hn, heads)
+        pooled = pooled + OMod.mlp_standard(sd, "decoder.0.mlp.", OMod.layer_norm(sd, "decoder.0.norm_mlp.ln.",
+                                                                                  pooled), 2)
+        OMod.mish(OMod.linear(sd, "decoder_linear.", pooled.mean(1)))
+
+    try:
+        step()
+        times = []
+        budget = time.perf_counter() + 15.0
+        while len(times) < 3 or (time.perf_counter() < budget and len(times) < 10):
+            t0 = time.perf_counter()
+            step()
+            times.append(time.perf_counter() - t0)
+    finally:
+        OMod.DT = torch.float64
+    med = float(np.median(times))
+    return {"value": gb.num_tokens / med, "unit": "edge-tokens/s", "cores": cores, "kind": "port",
+            "sample": (f"the whole config-0 batch ({gb.num_tokens} edge tokens, {gb.num_graphs} graphs) through the "
+                       f"oracle's fp32 restatement of the reference's padded path (torch CPU, {cores} threads: "
+                       f"embedding, gather, per-graph edge bias, M + S + PMA blocks), median of {len(times)} runs")}
+
+
+def bench_stack(args):
+    """Configuration 4: ESA encoder stack M-M-S-S-M-M-S-S-P(4 seeds), D=512, H=32, MLP 2048, bf16 train step.
+
+    bf16-mixed as the reference trains (core/train_pretrain.py:753): fp32 parameters under
+    torch.autocast(bfloat16), so projections and MLPs run bf16 GEMMs and attention the bf16 kernels; a step is
+    forward, backward and an AdamW update.
+    """
+    import torch
+
+    from mind_amd import generators
+    from mind_amd.esa.masked_layers import ESA
+    from mind_amd.esa.packing import EdgeAdjacency, nearest_multiple_of_8
+
+    dev = torch.device("cuda", 0)
+    gb = generators.protein_budget(seed=args.seed, token_budget=131072)
+    d, h, layers = 512, 32, "MMSSMMSSP"
+    torch.manual_seed(args.seed)
+    model = ESA(num_outputs=4, dim_output=d, dim_hidden=[d] * len(layers), num_heads=[h] * len(layers),
+                layer_types=layers, xformers_or_torch_attn="hip", use_mlps=True, mlp_hidden_size=2048,
+                num_mlp_layers=2, mlp_type="standard").to(dev)
+    with torch.no_grad():
+        for name, prm in model.named_parameters():
+            if name.endswith("weight") and prm.dim() >= 2 or name.endswith(".S"):
+                prm.normal_(0.0, 0.02)
+            elif name.endswith("bias"):
+                prm.zero_()
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-4)
+    n = nearest_multiple_of_8(gb.max_seqlen + 1)
+    ei = torch.as_tensor(gb.edge_index).to(dev)
+    bm = torch.as_tensor(gb.batch).to(dev)
+    adj = EdgeAdjacency.from_edge_index(ei, bm, gb.num_graphs, n)
+    t = gb.num_tokens
+    g = torch.Generator(device=dev).manual_seed(args.seed)
+    x = adj.pad(torch.randn(t, d, device=dev, generator=g))
+
+    def step():
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            emb, _ = model(x, ei, bm, n)
+        loss = emb.float().pow(2).mean()
+        loss.backward()
+        opt.step()
+        opt.zero_grad(set_to_none=True)
+
+    ms, wall_ms, kern = timed(step, args.steps, args.warmup)
+    attn_ms = sum(k["avg_us"] * k["launches"] for k in kern.values()) / 1e3 / args.steps
+    result = {
+        "metric": "edge-tokens/sec through the ESA encoder stack train step (fwd+bwd+AdamW, bf16-mixed)",
+        "value": t / (ms * 1e-3), "unit": "edge-tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded lognormal protein-like graphs packed to a 131,072 edge-token budget; x ~ N(0,1); "
+                "weights N(0, 0.02))",
+        "config": {"workload": "config4: ESA encoder stack M-M-S-S-M-M-S-S-P(4 seeds) train step",
+                   "graphs": gb.num_graphs, "edge_tokens": t, "max_seqlen": gb.max_seqlen, "padded_items": n,
+                   "dim": d, "heads": h, "mlp_hidden": 2048, "seed": args.seed},
+        "wall_ms_per_step": wall_ms, "kernels": kern,
+        "library_kernel_ms_per_step": attn_ms,
+    }
     print(json.dumps(result), flush=True)
 
 

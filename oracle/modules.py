@@ -17,7 +17,7 @@ import torch.nn.functional as F
 
 from .attention import padded_attention, varlen_attention
 
-DT = torch.float64
+DT = torch.float64   # the checker's precision (the CPU baseline of bench.py times it in float32)
 
 
 def _p(sd, prefix, name):
@@ -50,7 +50,7 @@ def mab_padded(sd, prefix, Q, K, heads, bias=None):
     v = linear(sd, prefix + "fc_v.", K)
     k = linear(sd, prefix + "fc_k.", K)
     hd = q.shape[-1] // heads
-    o = padded_attention(_heads(q, heads), _heads(k, heads), _heads(v, heads), 1.0 / np.sqrt(hd), bias)
+    o = padded_attention(_heads(q, heads), _heads(k, heads), _heads(v, heads), 1.0 / np.sqrt(hd), bias, dtype=DT)
     o = o.reshape(Q.shape[0], Q.shape[1], -1)
     return o + mish(linear(sd, prefix + "fc_o.", o))
 
@@ -64,7 +64,7 @@ def mab_packed(sd, prefix, Qp, Kp, cu_q, cu_k, heads, edge_src=None, edge_dst=No
     v = linear(sd, prefix + "fc_v.", k if v_from_k else Kp)
     hd = q.shape[-1] // heads
     o, _ = varlen_attention(_heads(q, heads), _heads(k, heads), _heads(v, heads), cu_q, cu_k, 1.0 / np.sqrt(hd),
-                            edge_src, edge_dst, adj=adj)
+                            edge_src, edge_dst, dtype=DT, adj=adj)
     o = o.reshape(Qp.shape[0], -1)
     return o + mish(linear(sd, prefix + "fc_o.", o))
 
@@ -80,7 +80,8 @@ def mab_varlen(sd, prefix, Q, K, seq_lens, heads):
     q = linear(sd, prefix + "fc_q.", Q).reshape(b * n, d)[idx]
     k = linear(sd, prefix + "fc_k.", K).reshape(b * n, d)[idx]
     v = linear(sd, prefix + "fc_v.", k)
-    o, _ = varlen_attention(_heads(q, heads), _heads(k, heads), _heads(v, heads), cu, cu, 1.0 / np.sqrt(d // heads))
+    o, _ = varlen_attention(_heads(q, heads), _heads(k, heads), _heads(v, heads), cu, cu, 1.0 / np.sqrt(d // heads),
+                            dtype=DT)
     out = torch.zeros(b * n, d, dtype=DT)
     out[idx] = o.reshape(-1, d)
     out = out.reshape(b, n, d)
