@@ -33,12 +33,8 @@ namespace {
 constexpr int kStageTok = 64;      // partner tokens per staging step (two tiles)
 constexpr int kPlanBuckets = 1024;
 
-// Build-time tuning: issue both tiles' score MFMAs of a stage before either
-// tile's exponentials (1), or finish one tile before starting the next (0);
-// minimum waves per SIMD each kernel is compiled for (0 = compiler's choice).
-#ifndef ESA_DENSE_PAIRED
-#define ESA_DENSE_PAIRED 0
-#endif
+// Build-time tuning: minimum waves per SIMD each kernel is compiled for
+// (0 = compiler's choice).
 #ifndef ESA_DENSE_WAVES_FWD
 #define ESA_DENSE_WAVES_FWD 0
 #endif
@@ -52,7 +48,7 @@ constexpr int kPlanBuckets = 1024;
 
 struct DenseArgs {
   const bf16* q; const bf16* k; const bf16* v; const bf16* out; const bf16* dout;
-  const uint2* aux;            // dK/dV: per (head, query) bf16 (hi, lo) pairs of -LSE2 and of -D, [H][tq_pad]
+  const float2* aux;           // dK/dV: per (head, query) {-LSE2, -D}, [H][tq_pad]
   const float* lse;            // dQ: [H][Tq] natural log
   const float* knorm;          // forward: max |k| per (head, global 32-token tile), [H][tk_tiles]
   int tk_tiles;
@@ -147,6 +143,39 @@ DEVI void stage_walk(int n_stages, Load gload, Store lstore, Compute compute) {
 }
 
 struct Stage2 { i32x4 a, b; };
+
+// ---- staging layouts of the 16x16 backward kernels (LDS bank-conflict free
+// for their reads and writes on gfx950).  Lane l of wave w stages dims
+// 8 h .. 8 h + 7, h = (l >> 4) & 1, of stage token 16 w + (l & 15), so 16
+// consecutive lanes write 256 contiguous bytes.
+DEVI int split_tok(int wave, int lane) { return 16 * wave + (lane & 15); }
+DEVI int split_half(int lane) { return (lane >> 4) & 1; }
+
+// Rows split by dims half, [2][kStageTok][8] bf16: an operand read of 16
+// consecutive tokens by a lane group covers 256 contiguous bytes.
+constexpr int kHalfRows = kStageTok * 8;   // bf16 per dims half
+DEVI void put_half(bf16* rows, int tok, int h, i32x4 v) {
+  *reinterpret_cast<i32x4*>(&rows[h * kHalfRows + tok * 8]) = v;
+}
+DEVI bf16x8 half_row8(const bf16* rows, int tok, int h) { return lds8(&rows[h * kHalfRows + tok * 8]); }
+DEVI bf16x4 half_row4(const bf16* rows, int tok, int q) {   // dims 4q .. 4q + 3
+  return lds4(&rows[(q >> 1) * kHalfRows + tok * 8 + 4 * (q & 1)]);
+}
+
+// Transposed tiles for the mfma16k32 A operand: per 32-token tile four slot
+// groups of [16 dims][8 slots] (256 B each).  Token t sits in slot
+// s = slot_col(t) of group s / 8, and dim d of group G is stored in row
+// d ^ G: the transposed writes of one dim by 16 tokens hit distinct banks,
+// and a lane group's read still covers its group's 256 bytes.
+constexpr int kTrTile = 4 * 16 * 8;   // bf16 per tile
+DEVI void put_tr(bf16* tr2, int tok, int h, i32x4 v) {
+  const bf16x8 x = as_bf16x8(v);
+  const int sl = slot_col(tok & 31), grp = sl >> 3;
+  bf16* t = tr2 + (tok >> 5) * kTrTile + grp * 128 + (sl & 7);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) t[((8 * h + e) ^ grp) * 8] = x[e];
+}
+DEVI bf16x8 tr_read(const bf16* tile, int c16, int grp) { return lds8(&tile[grp * 128 + (c16 ^ grp) * 8]); }
 
 // ------------------------------------------------------------------ forward
 // Each wave owns kFwdTiles consecutive 32-query tiles: every K row and V^T
@@ -287,199 +316,288 @@ __global__ __launch_bounds__(256) ESA_WAVES_ATTR(ESA_DENSE_WAVES_FWD) void dense
 }
 
 // ------------------------------------------------------------------ dQ pass
-// One wave = 32 queries (lanes); dQ = scale * sum_k P (dP - D) k with
-// S' = K (c q)^T - LSE2 from two MFMAs seeded with -LSE2, P = exp2(S').
+// One wave = kDqTiles tiles of 32 queries; dQ = scale * sum_k P (dP - D) k
+// in 16x16 blocks (esa_attn_tiles.h): S'^T = K (c q)^T - LSE2 by one
+// mfma16k32 per (key block, query block) with the hi / lo halves of c q in
+// its K slots and -LSE2 as the accumulator seed, dP^T - D by one mfma16k16
+// seeded with -D, P = exp2(S'), and dQ^T += K^T dS^T by one mfma16k32 per
+// query block over a key tile's 32 keys.  Every K, V and K^T operand read
+// from LDS feeds all of the wave's query blocks.
+
+#ifndef ESA_DQ_TILES
+#define ESA_DQ_TILES 1
+#endif
+constexpr int kDqTiles = ESA_DQ_TILES;
+constexpr int kDqGroup = kWaves * kTile * kDqTiles;   // queries per block
 
 __global__ __launch_bounds__(256) ESA_WAVES_ATTR(ESA_DENSE_WAVES_DQ) void dense_dq_kernel(const DenseArgs a) {
-  __shared__ __align__(16) bf16 sK[2][kStageTok * kRowStride];    // K rows
-  __shared__ __align__(16) bf16 sV[2][kStageTok * kRowStride];    // V rows
-  __shared__ __align__(16) bf16 sKT[2][2][16 * kTrStride];         // K^T per tile
+  constexpr int T = kDqTiles;
+  __shared__ __align__(16) bf16 sK[2][2 * kHalfRows];   // K rows split by dims half
+  __shared__ __align__(16) bf16 sV[2][2 * kHalfRows];   // V rows split by dims half
+  __shared__ __align__(16) bf16 sKT[2][2 * kTrTile];    // K^T per tile, slot groups
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int col = lane & 31, half = lane >> 5, hf = lane & 1;
+  const int c16 = lane & 15, grp = lane >> 4;
   const int H = a.heads;
   int item, head;
   block_item_head(H, item, head);
   if (item >= *a.count) return;
   const int4 g = a.groups[item];
 
-  const int o0 = g.x + wave * kTile;
-  const bool active = o0 < g.y;
-  const int t = o0 + col;
-  const bool valid = t < g.y;
-  const int tc = valid ? t : g.x;
-  const size_t row = ((size_t)tc * H + head) * kHd + 8 * half;
-  const bf16x8 qf = *reinterpret_cast<const bf16x8*>(a.q + row);
-  const bf16x8 dof = *reinterpret_cast<const bf16x8*>(a.dout + row);
-  const bf16x8 of = *reinterpret_cast<const bf16x8*>(a.out + row);
-  float dsum = 0.f;
+  const int o0 = g.x + wave * kTile * T;
+  bool active[T];
+  bf16x8 qs[T][2];     // B of the score MFMA: scaled hi / lo halves of q
+  bf16x4 ob[T][2];     // B of the dP MFMA: dO dims 4 grp..+3
+  f32x4 cl[T][2], cd[T][2];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) dsum = fmaf((float)dof[e], (float)of[e], dsum);
-  dsum += __shfl_xor(dsum, 32);
-  const float lq = a.lse[(size_t)head * a.total_q + tc];
-  const f32x16 cl = splat16(lq == -INFINITY ? -INFINITY : -lq * kLog2e);   // seed of S': -LSE2
-  const f32x16 cd = splat16(-dsum);                                        // seed of dP: -D
-  bf16x8 qh, ql;
-  split_scaled(qf, a.c, qh, ql);
+  for (int u = 0; u < T; ++u) {
+    active[u] = o0 + u * kTile < g.y;
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      const int t = o0 + u * kTile + 16 * qb + c16;
+      const int tc = t < g.y ? t : g.x;
+      const size_t row = ((size_t)tc * H + head) * kHd;
+      const bf16x8 d0 = *reinterpret_cast<const bf16x8*>(a.dout + row);
+      const bf16x8 d1 = *reinterpret_cast<const bf16x8*>(a.dout + row + 8);
+      const bf16x8 p0 = *reinterpret_cast<const bf16x8*>(a.out + row);
+      const bf16x8 p1 = *reinterpret_cast<const bf16x8*>(a.out + row + 8);
+      float dsum = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dsum = fmaf((float)d0[e], (float)p0[e], dsum);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dsum = fmaf((float)d1[e], (float)p1[e], dsum);
+      qs[u][qb] = scaled_half(*reinterpret_cast<const bf16x8*>(a.q + row + 8 * (grp & 1)), a.c, grp >= 2);
+      ob[u][qb] = *reinterpret_cast<const bf16x4*>(a.dout + row + 4 * grp);
+      const float lq = a.lse[(size_t)head * a.total_q + tc];
+      cl[u][qb] = splat4(lq == -INFINITY ? -INFINITY : -lq * kLog2e);   // seed of S': -LSE2
+      cd[u][qb] = splat4(-dsum);                                        // seed of dP: -D
+    }
+  }
 
   const int n_tiles = (g.w - g.z + kTile - 1) >> 5;
   const int n_stages = (n_tiles + 1) >> 1;
-  const int tok = stage_tok(wave, lane);
-  auto gload = [&](int st) { return stage_chunk(a.k, a.v, g.z + st * kStageTok + tok, a.total_k, H, head, hf, lane); };
+  const int tok = split_tok(wave, lane), hs = split_half(lane);
+  auto gload = [&](int st) { return stage_chunk(a.k, a.v, g.z + st * kStageTok + tok, a.total_k, H, head, hs, lane); };
   auto lstore = [&](int buf, i32x4 r) {
     if (lane < 32) {
-      put_row(sK[buf], tok, hf, r);
-      put_col<16>(&sKT[buf][0][0], tok, hf, r);
+      put_half(sK[buf], tok, hs, r);
+      put_tr(sKT[buf], tok, hs, r);
     } else {
-      put_row(sV[buf], tok, hf, r);
+      put_half(sV[buf], tok, hs, r);
     }
   };
 
-  f32x16 acc = {};
-  struct SP { f32x16 s, dp; };
-  auto scores = [&](int buf, int j) {
-    const int rrow = (32 * j + kperm(col)) * kRowStride + 8 * half;
-    const bf16x8 kr = lds8(&sK[buf][rrow]);
-    return SP{mfma32(kr, ql, mfma32(kr, qh, cl)), mfma32(lds8(&sV[buf][rrow]), dof, cd)};
-  };
-  auto tile = [&](int buf, int j, int k0, SP sp) {
-    f32x16& s = sp.s;
-    const f32x16& dp = sp.dp;
-    if (k0 + kTile > g.w) {
+  f32x4 acc[T][2];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) s[r] = k0 + row_local(r, half) < g.w ? s[r] : -INFINITY;
+  for (int u = 0; u < T; ++u) acc[u][0] = acc[u][1] = f32x4{};
+  // One key tile of the staged pair: every block's score and dP MFMAs
+  // first, then each query block's exponentials and dS K.
+  auto tile = [&](int buf, int j, int k0) {
+    bf16x8 ka[2];
+    bf16x4 va[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      ka[kb] = half_row8(sK[buf], 32 * j + 16 * kb + c16, grp & 1);
+      va[kb] = half_row4(sV[buf], 32 * j + 16 * kb + c16, grp);
     }
-    float ds[16];
+    f32x4 s[T][2][2], dp[T][2][2];   // [u][query block][key block]
 #pragma unroll
-    for (int r = 0; r < 16; ++r) ds[r] = fast_exp2(s[r]) * dp[r];
-    const int trow = (col & 15) * kTrStride + 8 * half;
-    acc = mfma32(lds8(&sKT[buf][j][trow]), cvt8(ds), acc);
-    acc = mfma32(lds8(&sKT[buf][j][trow + 16]), cvt8(ds + 8), acc);
+    for (int u = 0; u < T; ++u)
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+          s[u][qb][kb] = mfma16k32(ka[kb], qs[u][qb], cl[u][qb]);
+          dp[u][qb][kb] = mfma16k16(va[kb], ob[u][qb], cd[u][qb]);
+        }
+    const bf16x8 kt = tr_read(&sKT[buf][j * kTrTile], c16, grp);
+    if (k0 + kTile > g.w) {   // the segment's last, partial key tile
+#pragma unroll
+      for (int u = 0; u < T; ++u)
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              s[u][qb][kb][e] = k0 + 16 * kb + 4 * grp + e < g.w ? s[u][qb][kb][e] : -INFINITY;
+    }
+#pragma unroll
+    for (int u = 0; u < T; ++u) {
+      if (u > 0 && !active[u]) continue;   // wave-uniform
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        f32x4 ds[2];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) ds[kb][e] = fast_exp2(s[u][qb][kb][e]) * dp[u][qb][kb][e];
+        acc[u][qb] = mfma16k32(kt, cvt4x2(ds[0], ds[1]), acc[u][qb]);
+      }
+    }
   };
   stage_walk(n_stages, gload, lstore, [&](int buf, int st) {
-    if (!active) return;
+    if (!active[0]) return;
     const int k0 = g.z + st * kStageTok;
-    if (ESA_DENSE_PAIRED && 2 * st + 1 < n_tiles) {
-      const SP s0 = scores(buf, 0), s1 = scores(buf, 1);
-      tile(buf, 0, k0, s0);
-      tile(buf, 1, k0 + kTile, s1);
-    } else {
-      tile(buf, 0, k0, scores(buf, 0));
-      if (2 * st + 1 < n_tiles) tile(buf, 1, k0 + kTile, scores(buf, 1));
-    }
+    tile(buf, 0, k0);
+    if (2 * st + 1 < n_tiles) tile(buf, 1, k0 + kTile);
   });
-  if (!valid) return;
-  store_rows8(a.dq + ((size_t)t * H + head) * kHd, acc, a.scale, half);
+#pragma unroll
+  for (int u = 0; u < T; ++u)
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      const int t = o0 + u * kTile + 16 * qb + c16;
+      if (t < g.y) store_dims4(a.dq + ((size_t)t * H + head) * kHd, acc[u][qb], a.scale, grp);
+    }
 }
 
 // ------------------------------------------------------------------ dK/dV pass
-// One wave = 32 keys (lanes); rows are queries.  S' = Q (c k)^T - LSE2 with
-// -LSE2 broadcast per row by an MFMA of its bf16 (hi, lo) halves against a
-// ones column, likewise dP' = dO v^T - D; dV = P^T dO, dK = scale dS^T Q.
-// A query's statistics sit in one 16-byte LDS record {-LSE2 pair, -D pair,
-// 0, 0}: read once, it is the A operand of both statistic MFMAs, whose B
-// operands select the pair (ones in k slots 0, 1 or 2, 3).
+// One wave = kDkdvTiles tiles of 32 keys; rows are queries, in 16x16 blocks
+// (esa_attn_tiles.h): S' = Q (c k)^T - LSE2 by one mfma16k32 per (query
+// block, key block) with the hi / lo halves of c k in its K slots, dP - D by
+// one mfma16k16; the row statistics -LSE2 and -D are fp32 accumulator
+// seeds read from LDS (four consecutive queries per lane group).  dV^T +=
+// dO^T P^T and dK^T += Q^T dS^T by one mfma16k32 each per key block over a
+// query tile's 32 queries.  Every Q, dO, Q^T, dO^T and statistic read from
+// LDS feeds all of the wave's key blocks.
+
+#ifndef ESA_DKDV_TILES
+#define ESA_DKDV_TILES 1
+#endif
+constexpr int kDkdvTiles = ESA_DKDV_TILES;
+constexpr int kDkdvGroup = kWaves * kTile * kDkdvTiles;   // keys per block
 
 __global__ __launch_bounds__(256) ESA_WAVES_ATTR(ESA_DENSE_WAVES_DKDV) void dense_dkdv_kernel(const DenseArgs a) {
-  __shared__ __align__(16) bf16 sQ[2][kStageTok * kRowStride];
-  __shared__ __align__(16) bf16 sDO[2][kStageTok * kRowStride];
-  __shared__ __align__(16) bf16 sQT[2][2][16 * kTrStride];
-  __shared__ __align__(16) bf16 sDOT[2][2][16 * kTrStride];
-  __shared__ __align__(16) i32x4 sAux[2][kStageTok];   // per query {-LSE2 pair, -D pair, 0, 0}
+  constexpr int T = kDkdvTiles;
+  __shared__ __align__(16) bf16 sQ[2][2 * kHalfRows];     // rows split by dims half
+  __shared__ __align__(16) bf16 sDO[2][2 * kHalfRows];
+  __shared__ __align__(16) bf16 sQT[2][2 * kTrTile];      // transposed, slot groups
+  __shared__ __align__(16) bf16 sDOT[2][2 * kTrTile];
+  __shared__ __align__(16) float sLse[2][kStageTok];      // -LSE2 per query
+  __shared__ __align__(16) float sDel[2][kStageTok];      // -D per query
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int col = lane & 31, half = lane >> 5, hf = lane & 1;
+  const int c16 = lane & 15, grp = lane >> 4;
   const int H = a.heads;
   int item, head;
   block_item_head(H, item, head);
   if (item >= *a.count) return;
   const int4 g = a.groups[item];   // outer = keys, inner = queries
 
-  const int o0 = g.x + wave * kTile;
-  const bool active = o0 < g.y;
-  const int t = o0 + col;
-  const bool valid = t < g.y;
-  const int tc = valid ? t : g.x;
-  const size_t row = ((size_t)tc * H + head) * kHd + 8 * half;
-  const bf16x8 kf = *reinterpret_cast<const bf16x8*>(a.k + row);
-  const bf16x8 vf = *reinterpret_cast<const bf16x8*>(a.v + row);
-  bf16x8 kh, kl;
-  split_scaled(kf, a.c, kh, kl);
-  // B operands of the row-statistic MFMAs: ones in k slots 0, 1 (the -LSE2
-  // pair of the record) or 2, 3 (the -D pair); half-1 lanes carry k 8..15.
-  bf16x8 ones_s = {}, ones_d = {};
-  if (half == 0) {
-    ones_s[0] = ones_s[1] = (bf16)1.f;
-    ones_d[2] = ones_d[3] = (bf16)1.f;
+  const int o0 = g.x + wave * kTile * T;
+  bool active[T];
+  bf16x8 ks[T][2];     // B of the score MFMA: scaled hi / lo halves of k
+  bf16x4 vb[T][2];     // B of the dP MFMA: v dims 4 grp..+3
+#pragma unroll
+  for (int u = 0; u < T; ++u) {
+    active[u] = o0 + u * kTile < g.y;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      const int t = o0 + u * kTile + 16 * kb + c16;
+      const int tc = t < g.y ? t : g.x;
+      const size_t row = ((size_t)tc * H + head) * kHd;
+      ks[u][kb] = scaled_half(*reinterpret_cast<const bf16x8*>(a.k + row + 8 * (grp & 1)), a.c, grp >= 2);
+      vb[u][kb] = *reinterpret_cast<const bf16x4*>(a.v + row + 4 * grp);
+    }
   }
 
   const int n_tiles = (g.w - g.z + kTile - 1) >> 5;
   const int n_stages = (n_tiles + 1) >> 1;
   const rsrc_t rx = make_rsrc(a.aux + (size_t)head * a.tq_pad, (uint32_t)a.tq_pad * 8u);
-  const int tok = stage_tok(wave, lane);
+  const int tok = split_tok(wave, lane), hs = split_half(lane);
   // row statistics: lanes 0..7 of wave w fetch queries 16w .. 16w+15 (two 8-byte records per lane)
   const uint32_t aux0 = lane < 8 ? (uint32_t)(g.z + 16 * wave + 2 * lane) * 8u : kNoLoad;
   auto gload = [&](int st) {
     Stage2 r;
-    r.a = stage_chunk(a.q, a.dout, g.z + st * kStageTok + tok, a.total_q, H, head, hf, lane);
+    r.a = stage_chunk(a.q, a.dout, g.z + st * kStageTok + tok, a.total_q, H, head, hs, lane);
     r.b = bload(rx, lane < 8 ? aux0 + (uint32_t)st * (kStageTok * 8u) : aux0);
     return r;
   };
   auto lstore = [&](int buf, const Stage2& r) {
     if (lane < 32) {
-      put_row(sQ[buf], tok, hf, r.a);
-      put_col<16>(&sQT[buf][0][0], tok, hf, r.a);
+      put_half(sQ[buf], tok, hs, r.a);
+      put_tr(sQT[buf], tok, hs, r.a);
     } else {
-      put_row(sDO[buf], tok, hf, r.a);
-      put_col<16>(&sDOT[buf][0][0], tok, hf, r.a);
+      put_half(sDO[buf], tok, hs, r.a);
+      put_tr(sDOT[buf], tok, hs, r.a);
     }
     if (lane < 8) {
-      sAux[buf][16 * wave + 2 * lane] = i32x4{r.b.x, r.b.y, 0, 0};
-      sAux[buf][16 * wave + 2 * lane + 1] = i32x4{r.b.z, r.b.w, 0, 0};
+      const int q = 16 * wave + 2 * lane;
+      *reinterpret_cast<float2*>(&sLse[buf][q]) = make_float2(__int_as_float(r.b.x), __int_as_float(r.b.z));
+      *reinterpret_cast<float2*>(&sDel[buf][q]) = make_float2(__int_as_float(r.b.y), __int_as_float(r.b.w));
     }
   };
 
-  f32x16 dva = {}, dka = {};
-  const f32x16 zero = {};
-  struct SP { f32x16 s, dp; };
-  auto scores = [&](int buf, int j) {
-    const int rrow = (32 * j + kperm(col)) * kRowStride + 8 * half;
-    const bf16x8 ax = as_bf16x8(sAux[buf][32 * j + kperm(col)]);
-    const bf16x8 qr = lds8(&sQ[buf][rrow]);
-    return SP{mfma32(qr, kl, mfma32(qr, kh, mfma32(ax, ones_s, zero))),
-              mfma32(lds8(&sDO[buf][rrow]), vf, mfma32(ax, ones_d, zero))};
-  };
-  auto tile = [&](int buf, int j, int q0, const SP& sp) {
-    const f32x16& s = sp.s;
-    const f32x16& dp = sp.dp;
-    float p[16], ds[16];
+  f32x4 dva[T][2], dka[T][2];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) p[r] = fast_exp2(s[r]);
-    if (q0 + kTile > g.w) {
+  for (int u = 0; u < T; ++u) dva[u][0] = dva[u][1] = dka[u][0] = dka[u][1] = f32x4{};
+  // One query tile of the staged pair: every block's score and dP MFMAs,
+  // then each key block's exponentials, dV and dK.
+  auto tile = [&](int buf, int j, int q0) {
+    bf16x8 qa[2];
+    bf16x4 da[2];
+    f32x4 ls[2], dl[2];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) p[r] = q0 + row_local(r, half) < g.w ? p[r] : 0.f;
+    for (int qb = 0; qb < 2; ++qb) {
+      qa[qb] = half_row8(sQ[buf], 32 * j + 16 * qb + c16, grp & 1);
+      da[qb] = half_row4(sDO[buf], 32 * j + 16 * qb + c16, grp);
+      ls[qb] = ldsf4(&sLse[buf][32 * j + 16 * qb + 4 * grp]);
+      dl[qb] = ldsf4(&sDel[buf][32 * j + 16 * qb + 4 * grp]);
+    }
+    f32x4 s[T][2][2], dp[T][2][2];   // [u][key block][query block]
+#pragma unroll
+    for (int u = 0; u < T; ++u)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+          s[u][kb][qb] = mfma16k32(qa[qb], ks[u][kb], ls[qb]);
+          dp[u][kb][qb] = mfma16k16(da[qb], vb[u][kb], dl[qb]);
+        }
+    const bf16x8 dot = tr_read(&sDOT[buf][j * kTrTile], c16, grp);
+    const bf16x8 qt = tr_read(&sQT[buf][j * kTrTile], c16, grp);
+    if (q0 + kTile > g.w) {   // the segment's last, partial query tile
+#pragma unroll
+      for (int u = 0; u < T; ++u)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              s[u][kb][qb][e] = q0 + 16 * qb + 4 * grp + e < g.w ? s[u][kb][qb][e] : -INFINITY;
     }
 #pragma unroll
-    for (int r = 0; r < 16; ++r) ds[r] = p[r] * dp[r];
-    const int trow = (col & 15) * kTrStride + 8 * half;
-    dva = mfma32(lds8(&sDOT[buf][j][trow]), cvt8(p), dva);
-    dva = mfma32(lds8(&sDOT[buf][j][trow + 16]), cvt8(p + 8), dva);
-    dka = mfma32(lds8(&sQT[buf][j][trow]), cvt8(ds), dka);
-    dka = mfma32(lds8(&sQT[buf][j][trow + 16]), cvt8(ds + 8), dka);
+    for (int u = 0; u < T; ++u) {
+      if (u > 0 && !active[u]) continue;   // wave-uniform
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        f32x4 p[2], ds[2];
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            p[qb][e] = fast_exp2(s[u][kb][qb][e]);
+            ds[qb][e] = p[qb][e] * dp[u][kb][qb][e];
+          }
+        dva[u][kb] = mfma16k32(dot, cvt4x2(p[0], p[1]), dva[u][kb]);
+        dka[u][kb] = mfma16k32(qt, cvt4x2(ds[0], ds[1]), dka[u][kb]);
+      }
+    }
   };
   stage_walk(n_stages, gload, lstore, [&](int buf, int st) {
-    if (!active) return;
+    if (!active[0]) return;
     const int q0 = g.z + st * kStageTok;
-    if (ESA_DENSE_PAIRED && 2 * st + 1 < n_tiles) {
-      const SP s0 = scores(buf, 0), s1 = scores(buf, 1);
-      tile(buf, 0, q0, s0);
-      tile(buf, 1, q0 + kTile, s1);
-    } else {
-      tile(buf, 0, q0, scores(buf, 0));
-      if (2 * st + 1 < n_tiles) tile(buf, 1, q0 + kTile, scores(buf, 1));
-    }
+    tile(buf, 0, q0);
+    if (2 * st + 1 < n_tiles) tile(buf, 1, q0 + kTile);
   });
-  if (!valid) return;
-  store_rows8(a.dv + ((size_t)t * H + head) * kHd, dva, 1.f, half);
-  store_rows8(a.dk + ((size_t)t * H + head) * kHd, dka, a.scale, half);
+#pragma unroll
+  for (int u = 0; u < T; ++u)
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      const int t = o0 + u * kTile + 16 * kb + c16;
+      if (t >= g.y) continue;
+      store_dims4(a.dv + ((size_t)t * H + head) * kHd, dva[u][kb], 1.f, grp);
+      store_dims4(a.dk + ((size_t)t * H + head) * kHd, dka[u][kb], a.scale, grp);
+    }
 }
 
 // ------------------------------------------------------------------ prep
@@ -539,13 +657,13 @@ struct DensePrep {
   int4* plan_q; int* count_q; int4* plan_k; int* count_k;
   int gtok_q, gtok_k;                                 // tokens per group of each plan
   const bf16* k; float* knorm;                       // forward
-  const bf16* out; const bf16* dout; const float* lse; uint2* aux;   // backward
+  const bf16* out; const bf16* dout; const float* lse; float2* aux;   // backward
   int nb_plan_k, nb_knorm, nb_rows;
 };
 
-// Row statistics of the dK/dV pass as bf16 (hi, lo) pairs: aux.x = -LSE2
-// (LSE2 = log2(e) LSE; -1e30 for rows without keys and padding, so their P is
-// 0), aux.y = -D = -rowsum(dO * O).  Thread per (query, head), head fastest.
+// Row statistics of the dK/dV pass: aux.x = -LSE2 (LSE2 = log2(e) LSE;
+// -1e30 for rows without keys and padding, so their P is 0), aux.y = -D =
+// -rowsum(dO * O).  Thread per (query, head), head fastest.
 DEVI void dense_rows_item(const DensePrep& p, long idx) {
   if (idx >= (long)p.heads * p.tq_pad) return;
   const int h = (int)(idx % p.heads), t = (int)(idx / p.heads);
@@ -562,7 +680,7 @@ DEVI void dense_rows_item(const DensePrep& p, long idx) {
       for (int e = 0; e < 8; ++e) dsum = fmaf((float)o[e], (float)g[e], dsum);
     }
   }
-  p.aux[(size_t)h * p.tq_pad + t] = make_uint2(split_bf16_pair(xs), split_bf16_pair(-dsum));
+  p.aux[(size_t)h * p.tq_pad + t] = make_float2(xs, -dsum);
 }
 
 __global__ __launch_bounds__(256) void dense_prep_kernel(const DensePrep p) {
@@ -656,8 +774,8 @@ int dense_attn_bwd(const DenseAttnCall& c, void* workspace, size_t workspace_byt
   p.plan_q = reinterpret_cast<int4*>(ws + w.plan_q);
   p.plan_k = reinterpret_cast<int4*>(ws + w.plan_k);
   p.out = static_cast<const bf16*>(c.out_in); p.dout = static_cast<const bf16*>(c.dout); p.lse = c.lse_in;
-  p.aux = reinterpret_cast<uint2*>(ws + w.aux);
-  p.gtok_q = kGroupTok; p.gtok_k = kGroupTok;
+  p.aux = reinterpret_cast<float2*>(ws + w.aux);
+  p.gtok_q = kDqGroup; p.gtok_k = kDkdvGroup;
   p.nb_plan_k = 1; p.nb_knorm = 0; p.nb_rows = (int)(((long)c.heads * p.tq_pad + 255) / 256);
   ESA_TIMED(esa_profile::kAttnPrep, st,
             hipLaunchKernelGGL(dense_prep_kernel, dim3(2 + p.nb_rows), dim3(256), 0, st, p));
@@ -671,12 +789,12 @@ int dense_attn_bwd(const DenseAttnCall& c, void* workspace, size_t workspace_byt
   a.dq = static_cast<bf16*>(c.dq); a.dk = static_cast<bf16*>(c.dk); a.dv = static_cast<bf16*>(c.dv);
   a.groups = p.plan_k; a.count = p.count_k;
   ESA_TIMED(esa_profile::kAttnBwdDkdv, st,
-            hipLaunchKernelGGL(dense_dkdv_kernel, dim3(group_grid(c.total_k, c.nseg, c.heads, kGroupTok)), dim3(256),
+            hipLaunchKernelGGL(dense_dkdv_kernel, dim3(group_grid(c.total_k, c.nseg, c.heads, kDkdvGroup)), dim3(256),
                                0, st, a));
   ESA_LAUNCH_CHECK();
   a.groups = p.plan_q; a.count = p.count_q;
   ESA_TIMED(esa_profile::kAttnBwdDq, st,
-            hipLaunchKernelGGL(dense_dq_kernel, dim3(group_grid(c.total_q, c.nseg, c.heads, kGroupTok)), dim3(256), 0,
+            hipLaunchKernelGGL(dense_dq_kernel, dim3(group_grid(c.total_q, c.nseg, c.heads, kDqGroup)), dim3(256), 0,
                                st, a));
   ESA_LAUNCH_CHECK();
   return ESA_OK;

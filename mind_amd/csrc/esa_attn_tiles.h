@@ -75,6 +75,54 @@ DEVI void split_scaled(const bf16x8& x, float c, bf16x8& hi, bf16x8& lo) {
   }
 }
 
+// ---- 16x16 block layouts (dense backward kernels)
+// A 32x32 (partner x owned) tile is four 16x16 blocks.  The score MFMA
+// (mfma16k32) gives lane l partner rows 4G..4G+3 (G = l / 16) of a block
+// for owned token l % 16, so the tile's two partner blocks leave a lane 8
+// partner rows of one owned token, {4G..4G+3, 16+4G..16+4G+3}: exactly the
+// K slots 8G..8G+7 a lane supplies to the mfma16k32 that sums over the
+// tile's 32 partners.  Transposed LDS tiles store partner t at column
+// slot_col(t), so one 16-byte read at column 8G is the matching A operand.
+DEVI int slot_col(int t) { return 8 * ((t & 15) >> 2) + 4 * (t >> 4) + (t & 3); }
+
+// B operand of a scaled score mfma16k32: K slots 0..15 carry the bf16 hi
+// halves of c * x, slots 16..31 the lo halves (hi + lo carries ~16
+// significant bits), so one MFMA gives c * (a . x) in fp32.  Lane group G
+// supplies slots 8G..8G+7: x holds dims 8 (G & 1)..+7 and lo = (G >= 2).
+DEVI bf16x8 scaled_half(const bf16x8& x, float c, bool lo) {
+  bf16x8 r;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float v = (float)x[e] * c;
+    const bf16 hi = (bf16)v;
+    r[e] = lo ? (bf16)(v - (float)hi) : hi;
+  }
+  return r;
+}
+
+// B operand over a tile's 32 partners from the two partner blocks' results.
+DEVI bf16x8 cvt4x2(const f32x4& a, const f32x4& b) {
+  bf16x8 r;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    r[e] = (bf16)a[e];
+    r[4 + e] = (bf16)b[e];
+  }
+  return r;
+}
+
+DEVI f32x4 splat4(float x) { return f32x4{x, x, x, x}; }
+DEVI bf16x4 lds4(const bf16* p) { return *reinterpret_cast<const bf16x4*>(p); }
+DEVI f32x4 ldsf4(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
+
+// dims 4g..4g+3 of one token row: mul * acc (an mfma16k* result column).
+DEVI void store_dims4(bf16* __restrict__ row, const f32x4& acc, float mul, int g) {
+  bf16x4 o;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = (bf16)(acc[i] * mul);
+  *reinterpret_cast<bf16x4*>(row + 4 * g) = o;
+}
+
 DEVI f32x16 splat16(float x) {
   f32x16 r;
 #pragma unroll

@@ -31,6 +31,21 @@ DEVI f32x16 mfma32(const bf16x8& a, const bf16x8& b, const f32x16& c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
+// D(16x16, fp32) += A(16x32, bf16) * B(32x16, bf16).  Lane l supplies
+// A[l%16][8(l/16)..+7] and B[8(l/16)..+7][l%16]; it receives
+// D[4(l/16) + r][l%16] in accumulator register r.
+DEVI f32x4 mfma16k32(const bf16x8& a, const bf16x8& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// D(16x16, fp32) += A(16x16, bf16) * B(16x16, bf16).  Lane l supplies
+// A[l%16][4(l/16)..+3] and B[4(l/16)..+3][l%16]; result layout as mfma16k32.
+DEVI f32x4 mfma16k16(const bf16x4& a, const bf16x4& b, const f32x4& c) {
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a), __builtin_bit_cast(s16x4, b), c, 0,
+                                                   0, 0);
+}
+
 // Segment containing token t: the s in [0, nseg) with cu[s] <= t < cu[s+1]
 // (t < cu[nseg] required).  Empty segments are skipped naturally.
 DEVI int seg_of(const int* __restrict__ cu, int nseg, int t) {
