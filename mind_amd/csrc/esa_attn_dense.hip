@@ -36,10 +36,10 @@ constexpr int kPlanBuckets = 1024;
 // Build-time tuning: minimum waves per SIMD each kernel is compiled for
 // (0 = compiler's choice).
 #ifndef ESA_DENSE_WAVES_FWD
-#define ESA_DENSE_WAVES_FWD 0
+#define ESA_DENSE_WAVES_FWD 4
 #endif
 #ifndef ESA_DENSE_WAVES_DQ
-#define ESA_DENSE_WAVES_DQ 0
+#define ESA_DENSE_WAVES_DQ 5
 #endif
 #ifndef ESA_DENSE_WAVES_DKDV
 #define ESA_DENSE_WAVES_DKDV 0
@@ -89,9 +89,6 @@ unsigned group_blocks(int groups, int H) {
 
 // ------------------------------------------------------------------ staging
 
-// The stage token this lane stages (wave w: tokens 16w .. 16w+15) and its half.
-DEVI int stage_tok(int wave, int lane) { return 16 * wave + ((lane & 31) >> 1); }
-
 // This lane's 16-byte chunk of a stage: lanes 0..31 read tensor A, 32..63
 // tensor B, one global load with a per-lane address (a single instruction,
 // so a stage's load is waited for on its own and the next stage's load
@@ -105,40 +102,38 @@ DEVI i32x4 stage_chunk(const bf16* __restrict__ a, const bf16* __restrict__ b, i
 }
 constexpr uint32_t kNoLoad = 0xFFFFFFF0u;   // buffer offset past any range: the load returns zeros
 
-// LDS writes of one staged 16-byte chunk (8 dims of token `tok` of the stage).
-DEVI void put_row(bf16* rows, int tok, int hf, i32x4 v) {
-  *reinterpret_cast<i32x4*>(&rows[tok * kRowStride + 8 * hf]) = v;
-}
-template <int ROWS>   // tr2: two [ROWS][kTrStride] tiles (rows 0..15: the dims)
-DEVI void put_col(bf16* tr2, int tok, int hf, i32x4 v) {
-  const bf16x8 x = as_bf16x8(v);
-  bf16* t = tr2 + (tok >> 5) * (ROWS * kTrStride) + (tok & 31);
-#pragma unroll
-  for (int e = 0; e < 8; ++e) t[(8 * hf + e) * kTrStride] = x[e];
-}
-
-// Loads of stage `st` issued two stages ahead, two LDS buffers, one barrier
-// per stage.  gload(st) returns this lane's staging registers, lstore(buf, r)
+// Stage loads run kStageDepth stages ahead of the compute through a ring of
+// register sets, two LDS buffers, one barrier per stage: while stage s is
+// computed, stages s + 1 .. s + kStageDepth are in flight or held, so the
+// global latency of a stage is hidden behind kStageDepth - 1 stages of
+// compute.  gload(st) returns this lane's staging registers, lstore(buf, r)
 // writes them, compute(buf, st) consumes a staged stage.  Past the end the
 // loads re-read the last stage and are never stored; the loop is unrolled
-// by two so the staging registers never move.
+// by the depth so the ring's registers never move.
+#ifndef ESA_STAGE_DEPTH
+#define ESA_STAGE_DEPTH 2
+#endif
+constexpr int kStageDepth = ESA_STAGE_DEPTH;
+static_assert(kStageDepth >= 2 && kStageDepth % 2 == 0, "stage ring depth must be even");
+
 template <class Load, class Store, class Compute>
 DEVI void stage_walk(int n_stages, Load gload, Store lstore, Compute compute) {
   if (n_stages <= 0) return;
-  auto ra = gload(0);
-  auto rb = gload(min(1, n_stages - 1));
-  lstore(0, ra);
+  decltype(gload(0)) r[kStageDepth];
+#pragma unroll
+  for (int i = 0; i < kStageDepth; ++i) r[i] = gload(min(i, n_stages - 1));
+  lstore(0, r[0]);
   __syncthreads();
-  for (int st = 0; st < n_stages; st += 2) {
-    ra = gload(min(st + 2, n_stages - 1));
-    compute(0, st);
-    if (st + 1 < n_stages) lstore(1, rb);
-    __syncthreads();
-    if (st + 1 >= n_stages) break;
-    rb = gload(min(st + 3, n_stages - 1));
-    compute(1, st + 1);
-    if (st + 2 < n_stages) lstore(0, ra);
-    __syncthreads();
+  for (int st = 0; st < n_stages; st += kStageDepth) {
+#pragma unroll
+    for (int i = 0; i < kStageDepth; ++i) {
+      const int s = st + i;   // in LDS buffer i & 1; r[i] held it and is free
+      if (s >= n_stages) return;
+      r[i] = gload(min(s + kStageDepth, n_stages - 1));
+      compute(i & 1, s);
+      if (s + 1 < n_stages) lstore((i + 1) & 1, r[(i + 1) % kStageDepth]);
+      __syncthreads();
+    }
   }
 }
 
@@ -154,6 +149,7 @@ DEVI int split_half(int lane) { return (lane >> 4) & 1; }
 // Rows split by dims half, [2][kStageTok][8] bf16: an operand read of 16
 // consecutive tokens by a lane group covers 256 contiguous bytes.
 constexpr int kHalfRows = kStageTok * 8;   // bf16 per dims half
+constexpr int kSplitRows = 2 * kHalfRows;  // bf16 per staged stage
 DEVI void put_half(bf16* rows, int tok, int h, i32x4 v) {
   *reinterpret_cast<i32x4*>(&rows[h * kHalfRows + tok * 8]) = v;
 }
@@ -162,20 +158,32 @@ DEVI bf16x4 half_row4(const bf16* rows, int tok, int q) {   // dims 4q .. 4q + 3
   return lds4(&rows[(q >> 1) * kHalfRows + tok * 8 + 4 * (q & 1)]);
 }
 
-// Transposed tiles for the mfma16k32 A operand: per 32-token tile four slot
-// groups of [16 dims][8 slots] (256 B each).  Token t sits in slot
-// s = slot_col(t) of group s / 8, and dim d of group G is stored in row
-// d ^ G: the transposed writes of one dim by 16 tokens hit distinct banks,
-// and a lane group's read still covers its group's 256 bytes.
-constexpr int kTrTile = 4 * 16 * 8;   // bf16 per tile
-DEVI void put_tr(bf16* tr2, int tok, int h, i32x4 v) {
-  const bf16x8 x = as_bf16x8(v);
-  const int sl = slot_col(tok & 31), grp = sl >> 3;
-  bf16* t = tr2 + (tok >> 5) * kTrTile + grp * 128 + (sl & 7);
-#pragma unroll
-  for (int e = 0; e < 8; ++e) t[((8 * h + e) ^ grp) * 8] = x[e];
+// The mfma16k32 A operand over a tile's 32 partners (lane c16 + 16 grp:
+// dim c16 of the partners in K slots 8 grp .. 8 grp + 7, slot order of
+// slot_col) by two LDS transpose reads of the half-split rows.
+// ds_read_b64_tr_b16 gives lane i of a 16-lane group, as its element k,
+// element i % 4 of the 8-byte chunk addressed by lane 4k + i / 4 of the
+// group.  Lane j addresses token 4 grp + j / 4 (16 more for the second
+// read), dims 4 (j % 4) .. +3, so lane i receives dim i of four tokens.
+DEVI bf16x4 lds_tr4(const bf16* p) {
+  typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p);
 }
-DEVI bf16x8 tr_read(const bf16* tile, int c16, int grp) { return lds8(&tile[grp * 128 + (c16 ^ grp) * 8]); }
+DEVI bf16x8 tr_operand(const bf16* rows, int tile_tok, int c16, int grp) {
+  const int q = c16 & 3;
+  const bf16* p = rows + (q >> 1) * kHalfRows + (tile_tok + 4 * grp + (c16 >> 2)) * 8 + 4 * (q & 1);
+  const bf16x4 lo = lds_tr4(p), hi = lds_tr4(p + 16 * 8);
+  return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+// The two tiles of a staged stage, each reading its LDS operands right
+// before its compute (reading both tiles' operands first costs more in
+// registers and occupancy than the LDS latency it hides).
+template <class Ops, class Tile>
+DEVI void stage_tiles(int buf, int st, int n_tiles, Ops ops, Tile tile, int t0) {
+  tile(ops(buf, 0), t0);
+  if (2 * st + 1 < n_tiles) tile(ops(buf, 1), t0 + kTile);
+}
 
 // ------------------------------------------------------------------ forward
 // Each wave owns kFwdTiles consecutive 32-query tiles: every K row and V^T
@@ -190,20 +198,18 @@ constexpr int kFwdGroup = kWaves * kTile * kFwdTiles;   // queries per block
 
 __global__ __launch_bounds__(256) ESA_WAVES_ATTR(ESA_DENSE_WAVES_FWD) void dense_fwd_kernel(const DenseArgs a) {
   constexpr int T = kFwdTiles;
-  __shared__ __align__(16) bf16 sK[2][kStageTok * kRowStride];   // K rows [key][16]
-  __shared__ __align__(16) bf16 sVT[2][2][32 * kTrStride];        // per tile [V^T ; 1]: rows 0..15 dims, 16..31 ones
+  __shared__ __align__(16) bf16 sK[2][kSplitRows];   // K rows split by dims half
+  __shared__ __align__(16) bf16 sV[2][kSplitRows];   // V rows split by dims half
+  __shared__ __align__(16) bf16 sOnes[4];             // the ones rows of [V^T ; 1]
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int col = lane & 31, half = lane >> 5, hf = lane & 1;
+  const int col = lane & 31, half = lane >> 5, c16 = lane & 15, grp = lane >> 4;
   const int H = a.heads;
   int item, head;
   block_item_head(H, item, head);
   if (item >= *a.count) return;
   const int4 g = a.groups[item];
 
-  for (int i = tid; i < 2 * 2 * 16 * kTrStride; i += 256) {
-    const int tile = i / (16 * kTrStride);
-    sVT[tile >> 1][tile & 1][16 * kTrStride + (i - tile * 16 * kTrStride)] = (bf16)1.f;
-  }
+  if (tid < 4) sOnes[tid] = (bf16)1.f;   // visible after the walk's first barrier
   const int o0 = g.x + wave * kTile * T;
   int t[T];
   bool valid[T], active[T];
@@ -232,12 +238,16 @@ __global__ __launch_bounds__(256) ESA_WAVES_ATTR(ESA_DENSE_WAVES_FWD) void dense
 
   const int n_tiles = (g.w - g.z + kTile - 1) >> 5;
   const int n_stages = (n_tiles + 1) >> 1;
-  const int tok = stage_tok(wave, lane);
-  auto gload = [&](int st) { return stage_chunk(a.k, a.v, g.z + st * kStageTok + tok, a.total_k, H, head, hf, lane); };
-  auto lstore = [&](int buf, i32x4 r) {
-    if (lane < 32) put_row(sK[buf], tok, hf, r);
-    else put_col<32>(&sVT[buf][0][0], tok, hf, r);
-  };
+  const int tok = split_tok(wave, lane), hs = split_half(lane);
+  auto gload = [&](int st) { return stage_chunk(a.k, a.v, g.z + st * kStageTok + tok, a.total_k, H, head, hs, lane); };
+  auto lstore = [&](int buf, i32x4 r) { put_half(lane < 32 ? sK[buf] : sV[buf], tok, hs, r); };
+  // A operands [V^T ; 1] of the two P V MFMAs of key tile j (keys 0..15,
+  // 16..31 of the tile) by LDS transpose reads (as tr_operand): lane groups
+  // 0 and 2 (rows 0..15, K slots 0..7 and 8..15) read dims of 4 keys per
+  // read, groups 1 and 3 (the ones rows) all read sOnes.
+  const int q4 = c16 & 3;
+  const int vt_step = (grp & 1) ? 0 : 8;   // bf16 per key in the read address
+  const int vt_off = (grp & 1) ? 0 : (q4 >> 1) * kHalfRows + (8 * (grp >> 1) + (c16 >> 2)) * 8 + 4 * (q4 & 1);
 
   float m_run[T];
   f32x16 acc[T];
@@ -249,7 +259,7 @@ __global__ __launch_bounds__(256) ESA_WAVES_ATTR(ESA_DENSE_WAVES_FWD) void dense
   const f32x16 zero = {};
   auto run = [&](auto online_tag) {
     constexpr bool ONLINE = decltype(online_tag)::value;
-    auto k_rows = [&](int buf, int j) { return lds8(&sK[buf][(32 * j + kperm(col)) * kRowStride + 8 * half]); };
+    auto k_rows = [&](int buf, int j) { return half_row8(sK[buf], 32 * j + kperm(col), half); };
     auto scores = [&](const bf16x8& kr, int u) { return mfma32(kr, ql[u], mfma32(kr, qh[u], zero)); };
     // Softmax of query tile u's scores s against one key tile (keys k0..),
     // then P V into acc[u].
@@ -281,24 +291,31 @@ __global__ __launch_bounds__(256) ESA_WAVES_ATTR(ESA_DENSE_WAVES_FWD) void dense
       acc[u] = mfma32(vt0, cvt8(p), acc[u]);
       acc[u] = mfma32(vt1, cvt8(p + 8), acc[u]);
     };
-    // One key tile of the staged pair: the score MFMAs of all query tiles
-    // first, then each query tile's softmax and P V.
-    auto tile = [&](int buf, int j, int k0) {
-      const bf16x8 kr = k_rows(buf, j);
+    // LDS operands of key tile j: K rows and the two [V^T ; 1] operands.
+    struct Ops { bf16x8 kr, vt0, vt1; };
+    auto ops = [&](int buf, int j) {
+      Ops o;
+      o.kr = k_rows(buf, j);
+      const bf16* pv = (grp & 1) ? sOnes : sV[buf] + 32 * j * 8 + vt_off;
+      const bf16x4 v0 = lds_tr4(pv), v1 = lds_tr4(pv + 4 * vt_step);
+      const bf16x4 v2 = lds_tr4(pv + 16 * vt_step), v3 = lds_tr4(pv + 20 * vt_step);
+      o.vt0 = bf16x8{v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+      o.vt1 = bf16x8{v2[0], v2[1], v2[2], v2[3], v3[0], v3[1], v3[2], v3[3]};
+      return o;
+    };
+    // One key tile: the score MFMAs of all query tiles first, then each
+    // query tile's softmax and P V.
+    auto tile = [&](const Ops& o, int k0) {
       f32x16 s[T];
 #pragma unroll
-      for (int u = 0; u < T; ++u) s[u] = scores(kr, u);
-      const bf16x8 vt0 = lds8(&sVT[buf][j][col * kTrStride + 8 * half]);
-      const bf16x8 vt1 = lds8(&sVT[buf][j][col * kTrStride + 16 + 8 * half]);
+      for (int u = 0; u < T; ++u) s[u] = scores(o.kr, u);
 #pragma unroll
       for (int u = 0; u < T; ++u)
-        if (u == 0 || active[u]) softmax_pv(u, s[u], k0, vt0, vt1);   // active[u]: wave-uniform
+        if (u == 0 || active[u]) softmax_pv(u, s[u], k0, o.vt0, o.vt1);   // active[u]: wave-uniform
     };
     stage_walk(n_stages, gload, lstore, [&](int buf, int st) {
       if (!any_active) return;
-      const int k0 = g.z + st * kStageTok;
-      tile(buf, 0, k0);
-      if (2 * st + 1 < n_tiles) tile(buf, 1, k0 + kTile);
+      stage_tiles(buf, st, n_tiles, ops, tile, g.z + st * kStageTok);
     });
   };
   if (fixed_ref)
@@ -332,9 +349,8 @@ constexpr int kDqGroup = kWaves * kTile * kDqTiles;   // queries per block
 
 __global__ __launch_bounds__(256) ESA_WAVES_ATTR(ESA_DENSE_WAVES_DQ) void dense_dq_kernel(const DenseArgs a) {
   constexpr int T = kDqTiles;
-  __shared__ __align__(16) bf16 sK[2][2 * kHalfRows];   // K rows split by dims half
-  __shared__ __align__(16) bf16 sV[2][2 * kHalfRows];   // V rows split by dims half
-  __shared__ __align__(16) bf16 sKT[2][2 * kTrTile];    // K^T per tile, slot groups
+  __shared__ __align__(16) bf16 sK[2][kSplitRows];   // K rows split by dims half
+  __shared__ __align__(16) bf16 sV[2][kSplitRows];   // V rows split by dims half
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c16 = lane & 15, grp = lane >> 4;
   const int H = a.heads;
@@ -378,12 +394,7 @@ __global__ __launch_bounds__(256) ESA_WAVES_ATTR(ESA_DENSE_WAVES_DQ) void dense_
   const int tok = split_tok(wave, lane), hs = split_half(lane);
   auto gload = [&](int st) { return stage_chunk(a.k, a.v, g.z + st * kStageTok + tok, a.total_k, H, head, hs, lane); };
   auto lstore = [&](int buf, i32x4 r) {
-    if (lane < 32) {
-      put_half(sK[buf], tok, hs, r);
-      put_tr(sKT[buf], tok, hs, r);
-    } else {
-      put_half(sV[buf], tok, hs, r);
-    }
+    put_half(lane < 32 ? sK[buf] : sV[buf], tok, hs, r);
   };
 
   f32x4 acc[T][2];
@@ -391,14 +402,21 @@ __global__ __launch_bounds__(256) ESA_WAVES_ATTR(ESA_DENSE_WAVES_DQ) void dense_
   for (int u = 0; u < T; ++u) acc[u][0] = acc[u][1] = f32x4{};
   // One key tile of the staged pair: every block's score and dP MFMAs
   // first, then each query block's exponentials and dS K.
-  auto tile = [&](int buf, int j, int k0) {
-    bf16x8 ka[2];
-    bf16x4 va[2];
+  struct Ops { bf16x8 ka[2], kt; bf16x4 va[2]; };
+  auto ops = [&](int buf, int j) {
+    Ops o;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
-      ka[kb] = half_row8(sK[buf], 32 * j + 16 * kb + c16, grp & 1);
-      va[kb] = half_row4(sV[buf], 32 * j + 16 * kb + c16, grp);
+      o.ka[kb] = half_row8(sK[buf], 32 * j + 16 * kb + c16, grp & 1);
+      o.va[kb] = half_row4(sV[buf], 32 * j + 16 * kb + c16, grp);
     }
+    o.kt = tr_operand(sK[buf], 32 * j, c16, grp);
+    return o;
+  };
+  auto tile = [&](const Ops& o, int k0) {
+    const bf16x8* ka = o.ka;
+    const bf16x4* va = o.va;
+    const bf16x8& kt = o.kt;
     f32x4 s[T][2][2], dp[T][2][2];   // [u][query block][key block]
 #pragma unroll
     for (int u = 0; u < T; ++u)
@@ -409,7 +427,6 @@ __global__ __launch_bounds__(256) ESA_WAVES_ATTR(ESA_DENSE_WAVES_DQ) void dense_
           s[u][qb][kb] = mfma16k32(ka[kb], qs[u][qb], cl[u][qb]);
           dp[u][qb][kb] = mfma16k16(va[kb], ob[u][qb], cd[u][qb]);
         }
-    const bf16x8 kt = tr_read(&sKT[buf][j * kTrTile], c16, grp);
     if (k0 + kTile > g.w) {   // the segment's last, partial key tile
 #pragma unroll
       for (int u = 0; u < T; ++u)
@@ -437,9 +454,7 @@ __global__ __launch_bounds__(256) ESA_WAVES_ATTR(ESA_DENSE_WAVES_DQ) void dense_
   };
   stage_walk(n_stages, gload, lstore, [&](int buf, int st) {
     if (!active[0]) return;
-    const int k0 = g.z + st * kStageTok;
-    tile(buf, 0, k0);
-    if (2 * st + 1 < n_tiles) tile(buf, 1, k0 + kTile);
+    stage_tiles(buf, st, n_tiles, ops, tile, g.z + st * kStageTok);
   });
 #pragma unroll
   for (int u = 0; u < T; ++u)
@@ -468,10 +483,8 @@ constexpr int kDkdvGroup = kWaves * kTile * kDkdvTiles;   // keys per block
 
 __global__ __launch_bounds__(256) ESA_WAVES_ATTR(ESA_DENSE_WAVES_DKDV) void dense_dkdv_kernel(const DenseArgs a) {
   constexpr int T = kDkdvTiles;
-  __shared__ __align__(16) bf16 sQ[2][2 * kHalfRows];     // rows split by dims half
-  __shared__ __align__(16) bf16 sDO[2][2 * kHalfRows];
-  __shared__ __align__(16) bf16 sQT[2][2 * kTrTile];      // transposed, slot groups
-  __shared__ __align__(16) bf16 sDOT[2][2 * kTrTile];
+  __shared__ __align__(16) bf16 sQ[2][kSplitRows];     // rows split by dims half
+  __shared__ __align__(16) bf16 sDO[2][kSplitRows];
   __shared__ __align__(16) float sLse[2][kStageTok];      // -LSE2 per query
   __shared__ __align__(16) float sDel[2][kStageTok];      // -D per query
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -512,13 +525,7 @@ __global__ __launch_bounds__(256) ESA_WAVES_ATTR(ESA_DENSE_WAVES_DKDV) void dens
     return r;
   };
   auto lstore = [&](int buf, const Stage2& r) {
-    if (lane < 32) {
-      put_half(sQ[buf], tok, hs, r.a);
-      put_tr(sQT[buf], tok, hs, r.a);
-    } else {
-      put_half(sDO[buf], tok, hs, r.a);
-      put_tr(sDOT[buf], tok, hs, r.a);
-    }
+    put_half(lane < 32 ? sQ[buf] : sDO[buf], tok, hs, r.a);
     if (lane < 8) {
       const int q = 16 * wave + 2 * lane;
       *reinterpret_cast<float2*>(&sLse[buf][q]) = make_float2(__int_as_float(r.b.x), __int_as_float(r.b.z));
@@ -531,17 +538,27 @@ __global__ __launch_bounds__(256) ESA_WAVES_ATTR(ESA_DENSE_WAVES_DKDV) void dens
   for (int u = 0; u < T; ++u) dva[u][0] = dva[u][1] = dka[u][0] = dka[u][1] = f32x4{};
   // One query tile of the staged pair: every block's score and dP MFMAs,
   // then each key block's exponentials, dV and dK.
-  auto tile = [&](int buf, int j, int q0) {
-    bf16x8 qa[2];
-    bf16x4 da[2];
-    f32x4 ls[2], dl[2];
+  struct Ops { bf16x8 qa[2], dot, qt; bf16x4 da[2]; f32x4 ls[2], dl[2]; };
+  auto ops = [&](int buf, int j) {
+    Ops o;
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
-      qa[qb] = half_row8(sQ[buf], 32 * j + 16 * qb + c16, grp & 1);
-      da[qb] = half_row4(sDO[buf], 32 * j + 16 * qb + c16, grp);
-      ls[qb] = ldsf4(&sLse[buf][32 * j + 16 * qb + 4 * grp]);
-      dl[qb] = ldsf4(&sDel[buf][32 * j + 16 * qb + 4 * grp]);
+      o.qa[qb] = half_row8(sQ[buf], 32 * j + 16 * qb + c16, grp & 1);
+      o.da[qb] = half_row4(sDO[buf], 32 * j + 16 * qb + c16, grp);
+      o.ls[qb] = ldsf4(&sLse[buf][32 * j + 16 * qb + 4 * grp]);
+      o.dl[qb] = ldsf4(&sDel[buf][32 * j + 16 * qb + 4 * grp]);
     }
+    o.dot = tr_operand(sDO[buf], 32 * j, c16, grp);
+    o.qt = tr_operand(sQ[buf], 32 * j, c16, grp);
+    return o;
+  };
+  auto tile = [&](const Ops& o, int q0) {
+    const bf16x8* qa = o.qa;
+    const bf16x4* da = o.da;
+    const f32x4* ls = o.ls;
+    const f32x4* dl = o.dl;
+    const bf16x8& dot = o.dot;
+    const bf16x8& qt = o.qt;
     f32x4 s[T][2][2], dp[T][2][2];   // [u][key block][query block]
 #pragma unroll
     for (int u = 0; u < T; ++u)
@@ -552,8 +569,6 @@ __global__ __launch_bounds__(256) ESA_WAVES_ATTR(ESA_DENSE_WAVES_DKDV) void dens
           s[u][kb][qb] = mfma16k32(qa[qb], ks[u][kb], ls[qb]);
           dp[u][kb][qb] = mfma16k16(da[qb], vb[u][kb], dl[qb]);
         }
-    const bf16x8 dot = tr_read(&sDOT[buf][j * kTrTile], c16, grp);
-    const bf16x8 qt = tr_read(&sQT[buf][j * kTrTile], c16, grp);
     if (q0 + kTile > g.w) {   // the segment's last, partial query tile
 #pragma unroll
       for (int u = 0; u < T; ++u)
@@ -585,9 +600,7 @@ __global__ __launch_bounds__(256) ESA_WAVES_ATTR(ESA_DENSE_WAVES_DKDV) void dens
   };
   stage_walk(n_stages, gload, lstore, [&](int buf, int st) {
     if (!active[0]) return;
-    const int q0 = g.z + st * kStageTok;
-    tile(buf, 0, q0);
-    if (2 * st + 1 < n_tiles) tile(buf, 1, q0 + kTile);
+    stage_tiles(buf, st, n_tiles, ops, tile, g.z + st * kStageTok);
   });
 #pragma unroll
   for (int u = 0; u < T; ++u)
