@@ -434,6 +434,193 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MASKED ? 3 
     a.lse_out[(size_t)head * a.total_q + ot.oi] = l > 0.f ? (m_run + fast_log2(l)) * kLn2 : -INFINITY;
 }
 
+// ======================================================================== edge-mask forward, heads in pairs
+// One wave = one 32-query tile and kEdgeHeads heads of it (the four waves of
+// a block are four tiles of a 128-token group and walk on their own, as in
+// the masked walk above).  The mask of a candidate key tile is evaluated
+// once, into an additive bias of 0 or -inf per score, which is the
+// accumulator seed of every head's score MFMAs: masking is free per head,
+// and the wave's fixed costs (segment bounds, tile metadata, the candidate
+// ballot) are shared by its heads.  Each candidate tile stages K rows and V
+// rows (split by dims half; the [V^T ; 1] operands come from LDS transpose
+// reads) of all heads of the wave plus the 32 node pairs.
+
+#ifndef ESA_EDGE_V2
+#define ESA_EDGE_V2 1
+#endif
+#ifndef ESA_EDGE_HEADS
+#define ESA_EDGE_HEADS 2
+#endif
+constexpr int kEdgeHeads = ESA_EDGE_HEADS;
+constexpr int kTileHalf = kTile * 8;   // bf16 per dims half of a split-row tile
+
+// Bias (0 keep / -inf drop) of this lane's 16 accumulator rows (partner
+// token p0 + row_local(r, half)) against the lane's own token: keep if the
+// partner shares an endpoint with it, lies in its segment and is not the
+// token itself.  Segment bounds and the diagonal are only tested on tiles
+// that straddle a segment bound of the wave or hold its own tokens.
+DEVI f32x16 edge_bias(const OuterTile& ot, int p0, int o0, int half, const int2* sn, int2 own) {
+  int2 pn[16];
+  lds_nodes16(sn, half, pn);
+  f32x16 b;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const uint32_t d = min(min((uint32_t)(pn[r].x ^ own.x), (uint32_t)(pn[r].x ^ own.y)),
+                           min((uint32_t)(pn[r].y ^ own.x), (uint32_t)(pn[r].y ^ own.y)));
+    b[r] = d == 0u ? 0.f : -INFINITY;
+  }
+  if (!(p0 >= ot.plo_max && p0 + kTile <= ot.phi_min) || p0 == o0) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int p = p0 + row_local(r, half);
+      b[r] = (p >= ot.plo && p < ot.phi && p != ot.oi) ? b[r] : -INFINITY;
+    }
+  }
+  return b;
+}
+
+// Token rows [T][H][16] bf16 for split-row staging: lane l reads dims half
+// l >> 5 of token l & 31 (lanes 0..31 write 512 contiguous LDS bytes).
+DEVI StageSrc split_rows_src(const void* p, int bytes, int H, int head, int lane) {
+  return StageSrc{make_rsrc(p, (uint32_t)bytes),
+                  ((uint32_t)(lane & 31) * H + head) * (kHd * 2) + 16u * (lane >> 5), (uint32_t)(kTile * H * kHd * 2)};
+}
+
+template <int NH>
+struct StageEdge { i32x4 k[NH], v[NH], n; };
+
+#ifndef ESA_EDGE_WAVES
+#define ESA_EDGE_WAVES 3
+#endif
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ESA_EDGE_WAVES))) void edge_fwd_kernel(
+    const AttnArgs a) {
+  constexpr int NH = kEdgeHeads;
+  __shared__ __align__(16) bf16 sK[kWaves][2][NH][kTile * kRowStride];   // K rows [key][16]
+  __shared__ __align__(16) bf16 sV[kWaves][2][NH][2 * kTileHalf];        // V rows split by dims half
+  __shared__ __align__(16) int2 sN[kWaves][2][kTile];
+  __shared__ __align__(16) bf16 sOnes[4];                                 // the ones rows of [V^T ; 1]
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 31, half = lane >> 5, c16 = lane & 15, grp = lane >> 4;
+  const int H = a.heads, n_hg = (H + NH - 1) / NH;
+  const int item = blockIdx.x / n_hg, hg = blockIdx.x - item * n_hg;
+  const int h0 = hg * NH;
+  const int nh = min(NH, H - h0);   // heads of this wave
+  const int4 pl = a.plan[item];
+  const int t0 = pl.x * kGroupTok, o0 = t0 + wave * kTile;
+  if (tid < 4) sOnes[tid] = (bf16)1.f;
+  __syncthreads();
+
+  const OuterTile ot = outer_tile(a.bounds, a.total_q, o0, col);
+  const int2 qn = a.nodes[ot.oc];
+  const int4 own = ot.active ? a.meta[o0 / kTile] : no_touch();
+  bf16x8 qh[NH], ql[NH];
+  float bmax = 0.f;
+#pragma unroll
+  for (int u = 0; u < NH; ++u) {
+    const int hc = min(h0 + u, H - 1);
+    const bf16x8 qf = *reinterpret_cast<const bf16x8*>(a.q + ((size_t)ot.oc * H + hc) * kHd + 8 * half);
+    if (ot.active) {
+      // bound c |q| max|k| over the keys this wave visits
+      float qq = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qq = fmaf((float)qf[e], (float)qf[e], qq);
+      qq += __shfl_xor(qq, 32);
+      float km = 0.f;
+      for (int t = ot.pt_beg + lane; t < ot.pt_end; t += 64) km = fmaxf(km, a.knorm[(size_t)hc * a.tk_tiles + t]);
+      km = wave_max(km);
+      bmax = fmaxf(bmax, ot.valid ? a.c * sqrtf(qq) * km : 0.f);
+    }
+    split_scaled(qf, a.c, qh[u], ql[u]);
+  }
+  const bool fixed_ref = __builtin_amdgcn_readfirstlane((int)(wave_max(bmax) <= kStaticBound)) != 0;
+
+  float m_run[NH];
+  f32x16 acc[NH];
+#pragma unroll
+  for (int u = 0; u < NH; ++u) {
+    m_run[u] = fixed_ref ? 0.f : -INFINITY;
+    acc[u] = f32x16{};
+  }
+  const int kv_bytes = a.total_k * H * kHd * 2;
+  StageSrc sk[NH], sv[NH];
+#pragma unroll
+  for (int u = 0; u < NH; ++u) {
+    const int hc = min(h0 + u, H - 1);
+    sk[u] = rows_src(a.k, kv_bytes, H, hc, lane);
+    sv[u] = split_rows_src(a.v, kv_bytes, H, hc, lane);
+  }
+  const StageSrc sn = records_src(a.nodes, a.tq_pad, lane);
+  auto run = [&](auto online_tag) {
+    constexpr bool ONLINE = decltype(online_tag)::value;
+    auto body = [&](int pt, int cur, uint32_t) {
+      if (!(pt >= ot.pt_beg && pt < ot.pt_end)) return;
+      const int k0 = pt * kTile;
+      const f32x16 bias = edge_bias(ot, k0, o0, half, sN[wave][cur], qn);
+#pragma unroll
+      for (int u = 0; u < NH; ++u) {
+        if (u >= nh) break;   // wave-uniform
+        const bf16x8 kr = lds8(&sK[wave][cur][u][kperm(col) * kRowStride + 8 * half]);
+        f32x16 s = mfma32(kr, ql[u], mfma32(kr, qh[u], bias));
+        if (ONLINE) {
+          float mt = s[0];
+#pragma unroll
+          for (int r = 1; r < 16; ++r) mt = fmaxf(mt, s[r]);
+          mt = fmaxf(mt, __shfl_xor(mt, 32));
+          const float m_new = fmaxf(m_run[u], mt);
+          if (__ballot(m_new > m_run[u])) {
+            const float alpha = fast_exp2(m_run[u] - (m_new == -INFINITY ? 0.f : m_new));
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[u][r] *= alpha;
+            m_run[u] = m_new;
+          }
+        }
+        float p[16];
+        const float m_use = ONLINE ? (m_run[u] == -INFINITY ? 0.f : m_run[u]) : 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) p[r] = fast_exp2(ONLINE ? s[r] - m_use : s[r]);
+        bf16x8 vt0, vt1;
+        vt_ones<kTileHalf>(sV[wave][cur][u], 0, sOnes, c16, grp, vt0, vt1);
+        acc[u] = mfma32(vt0, cvt8(p), acc[u]);
+        acc[u] = mfma32(vt1, cvt8(p + 8), acc[u]);
+      }
+    };
+    wave_tile_walk(ot.pt_beg, ot.pt_end, own, a.meta, lane,
+                   [&](int pt) {
+                     StageEdge<NH> g;
+#pragma unroll
+                     for (int u = 0; u < NH; ++u) {
+                       g.k[u] = sk[u].load(pt);
+                       g.v[u] = sv[u].load(pt);
+                     }
+                     g.n = sn.load(pt);
+                     return g;
+                   },
+                   [&](int st, const StageEdge<NH>& g) {
+#pragma unroll
+                     for (int u = 0; u < NH; ++u) {
+                       put_rows(sK[wave][st][u], g.k[u], lane);
+                       put_half<kTileHalf>(sV[wave][st][u], lane & 31, lane >> 5, g.v[u]);
+                     }
+                     put_records(sN[wave][st], g.n, lane);
+                   },
+                   body);
+  };
+  if (fixed_ref)
+    run(std::integral_constant<bool, false>{});
+  else
+    run(std::integral_constant<bool, true>{});
+  if (!ot.valid) return;
+#pragma unroll
+  for (int u = 0; u < NH; ++u) {
+    if (u >= nh) break;
+    const int h = h0 + u;
+    const float l = acc[u][8];   // a ones row of [V^T; 1] P^T: the softmax row sum
+    store_rows8(a.o + ((size_t)ot.oi * H + h) * kHd, acc[u], l > 0.f ? 1.f / l : 0.f, half);
+    if (half == 0)
+      a.lse_out[(size_t)h * a.total_q + ot.oi] = l > 0.f ? (m_run[u] + fast_log2(l)) * kLn2 : -INFINITY;
+  }
+}
+
 // ======================================================================== dQ pass
 // One wave = one query tile: dQ = scale * dS K with dS = P * (dP - D),
 // recomputing P from the saved LSE.  D = rowsum(dO * O) is computed per lane.
@@ -1243,7 +1430,11 @@ int esa_varlen_attn_fwd(const void* q, const void* k, const void* v, const int* 
   a.plan = pa.plan_q; a.bounds = pa.bounds_q;
   a.nodes = pa.nodes; a.meta = pa.meta;
   a.o = static_cast<bf16*>(out); a.lse_out = softmax_lse;
-  if (masked)
+  if (masked && ESA_EDGE_V2)
+    ESA_TIMED(esa_profile::kAttnFwdMasked, st,
+              hipLaunchKernelGGL(edge_fwd_kernel, dim3((unsigned)groups_of(total_q) * (unsigned)((heads + kEdgeHeads - 1) / kEdgeHeads)),
+                                 dim3(256), 0, st, a));
+  else if (masked)
     ESA_TIMED(esa_profile::kAttnFwdMasked, st,
               hipLaunchKernelGGL((attn_fwd_kernel<true>), dim3(grid), dim3(256), 0, st, a));
   else

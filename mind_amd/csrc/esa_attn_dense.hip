@@ -146,35 +146,10 @@ struct Stage2 { i32x4 a, b; };
 DEVI int split_tok(int wave, int lane) { return 16 * wave + (lane & 15); }
 DEVI int split_half(int lane) { return (lane >> 4) & 1; }
 
-// Rows split by dims half, [2][kStageTok][8] bf16: an operand read of 16
-// consecutive tokens by a lane group covers 256 contiguous bytes.
+// Staged rows split by dims half (esa_attn_tiles.h), one stage of
+// kStageTok tokens per buffer.
 constexpr int kHalfRows = kStageTok * 8;   // bf16 per dims half
 constexpr int kSplitRows = 2 * kHalfRows;  // bf16 per staged stage
-DEVI void put_half(bf16* rows, int tok, int h, i32x4 v) {
-  *reinterpret_cast<i32x4*>(&rows[h * kHalfRows + tok * 8]) = v;
-}
-DEVI bf16x8 half_row8(const bf16* rows, int tok, int h) { return lds8(&rows[h * kHalfRows + tok * 8]); }
-DEVI bf16x4 half_row4(const bf16* rows, int tok, int q) {   // dims 4q .. 4q + 3
-  return lds4(&rows[(q >> 1) * kHalfRows + tok * 8 + 4 * (q & 1)]);
-}
-
-// The mfma16k32 A operand over a tile's 32 partners (lane c16 + 16 grp:
-// dim c16 of the partners in K slots 8 grp .. 8 grp + 7, slot order of
-// slot_col) by two LDS transpose reads of the half-split rows.
-// ds_read_b64_tr_b16 gives lane i of a 16-lane group, as its element k,
-// element i % 4 of the 8-byte chunk addressed by lane 4k + i / 4 of the
-// group.  Lane j addresses token 4 grp + j / 4 (16 more for the second
-// read), dims 4 (j % 4) .. +3, so lane i receives dim i of four tokens.
-DEVI bf16x4 lds_tr4(const bf16* p) {
-  typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
-  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p);
-}
-DEVI bf16x8 tr_operand(const bf16* rows, int tile_tok, int c16, int grp) {
-  const int q = c16 & 3;
-  const bf16* p = rows + (q >> 1) * kHalfRows + (tile_tok + 4 * grp + (c16 >> 2)) * 8 + 4 * (q & 1);
-  const bf16x4 lo = lds_tr4(p), hi = lds_tr4(p + 16 * 8);
-  return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-}
 
 // The two tiles of a staged stage, each reading its LDS operands right
 // before its compute (reading both tiles' operands first costs more in
@@ -240,14 +215,7 @@ __global__ __launch_bounds__(256) ESA_WAVES_ATTR(ESA_DENSE_WAVES_FWD) void dense
   const int n_stages = (n_tiles + 1) >> 1;
   const int tok = split_tok(wave, lane), hs = split_half(lane);
   auto gload = [&](int st) { return stage_chunk(a.k, a.v, g.z + st * kStageTok + tok, a.total_k, H, head, hs, lane); };
-  auto lstore = [&](int buf, i32x4 r) { put_half(lane < 32 ? sK[buf] : sV[buf], tok, hs, r); };
-  // A operands [V^T ; 1] of the two P V MFMAs of key tile j (keys 0..15,
-  // 16..31 of the tile) by LDS transpose reads (as tr_operand): lane groups
-  // 0 and 2 (rows 0..15, K slots 0..7 and 8..15) read dims of 4 keys per
-  // read, groups 1 and 3 (the ones rows) all read sOnes.
-  const int q4 = c16 & 3;
-  const int vt_step = (grp & 1) ? 0 : 8;   // bf16 per key in the read address
-  const int vt_off = (grp & 1) ? 0 : (q4 >> 1) * kHalfRows + (8 * (grp >> 1) + (c16 >> 2)) * 8 + 4 * (q4 & 1);
+  auto lstore = [&](int buf, i32x4 r) { put_half<kHalfRows>(lane < 32 ? sK[buf] : sV[buf], tok, hs, r); };
 
   float m_run[T];
   f32x16 acc[T];
@@ -259,7 +227,7 @@ __global__ __launch_bounds__(256) ESA_WAVES_ATTR(ESA_DENSE_WAVES_FWD) void dense
   const f32x16 zero = {};
   auto run = [&](auto online_tag) {
     constexpr bool ONLINE = decltype(online_tag)::value;
-    auto k_rows = [&](int buf, int j) { return half_row8(sK[buf], 32 * j + kperm(col), half); };
+    auto k_rows = [&](int buf, int j) { return half_row8<kHalfRows>(sK[buf], 32 * j + kperm(col), half); };
     auto scores = [&](const bf16x8& kr, int u) { return mfma32(kr, ql[u], mfma32(kr, qh[u], zero)); };
     // Softmax of query tile u's scores s against one key tile (keys k0..),
     // then P V into acc[u].
@@ -296,11 +264,7 @@ __global__ __launch_bounds__(256) ESA_WAVES_ATTR(ESA_DENSE_WAVES_FWD) void dense
     auto ops = [&](int buf, int j) {
       Ops o;
       o.kr = k_rows(buf, j);
-      const bf16* pv = (grp & 1) ? sOnes : sV[buf] + 32 * j * 8 + vt_off;
-      const bf16x4 v0 = lds_tr4(pv), v1 = lds_tr4(pv + 4 * vt_step);
-      const bf16x4 v2 = lds_tr4(pv + 16 * vt_step), v3 = lds_tr4(pv + 20 * vt_step);
-      o.vt0 = bf16x8{v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-      o.vt1 = bf16x8{v2[0], v2[1], v2[2], v2[3], v3[0], v3[1], v3[2], v3[3]};
+      vt_ones<kHalfRows>(sV[buf], 32 * j, sOnes, c16, grp, o.vt0, o.vt1);
       return o;
     };
     // One key tile: the score MFMAs of all query tiles first, then each
@@ -394,7 +358,7 @@ __global__ __launch_bounds__(256) ESA_WAVES_ATTR(ESA_DENSE_WAVES_DQ) void dense_
   const int tok = split_tok(wave, lane), hs = split_half(lane);
   auto gload = [&](int st) { return stage_chunk(a.k, a.v, g.z + st * kStageTok + tok, a.total_k, H, head, hs, lane); };
   auto lstore = [&](int buf, i32x4 r) {
-    put_half(lane < 32 ? sK[buf] : sV[buf], tok, hs, r);
+    put_half<kHalfRows>(lane < 32 ? sK[buf] : sV[buf], tok, hs, r);
   };
 
   f32x4 acc[T][2];
@@ -407,10 +371,10 @@ __global__ __launch_bounds__(256) ESA_WAVES_ATTR(ESA_DENSE_WAVES_DQ) void dense_
     Ops o;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
-      o.ka[kb] = half_row8(sK[buf], 32 * j + 16 * kb + c16, grp & 1);
-      o.va[kb] = half_row4(sV[buf], 32 * j + 16 * kb + c16, grp);
+      o.ka[kb] = half_row8<kHalfRows>(sK[buf], 32 * j + 16 * kb + c16, grp & 1);
+      o.va[kb] = half_row4<kHalfRows>(sV[buf], 32 * j + 16 * kb + c16, grp);
     }
-    o.kt = tr_operand(sK[buf], 32 * j, c16, grp);
+    o.kt = tr_operand<kHalfRows>(sK[buf], 32 * j, c16, grp);
     return o;
   };
   auto tile = [&](const Ops& o, int k0) {
@@ -525,7 +489,7 @@ __global__ __launch_bounds__(256) ESA_WAVES_ATTR(ESA_DENSE_WAVES_DKDV) void dens
     return r;
   };
   auto lstore = [&](int buf, const Stage2& r) {
-    put_half(lane < 32 ? sQ[buf] : sDO[buf], tok, hs, r.a);
+    put_half<kHalfRows>(lane < 32 ? sQ[buf] : sDO[buf], tok, hs, r.a);
     if (lane < 8) {
       const int q = 16 * wave + 2 * lane;
       *reinterpret_cast<float2*>(&sLse[buf][q]) = make_float2(__int_as_float(r.b.x), __int_as_float(r.b.z));
@@ -543,13 +507,13 @@ __global__ __launch_bounds__(256) ESA_WAVES_ATTR(ESA_DENSE_WAVES_DKDV) void dens
     Ops o;
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
-      o.qa[qb] = half_row8(sQ[buf], 32 * j + 16 * qb + c16, grp & 1);
-      o.da[qb] = half_row4(sDO[buf], 32 * j + 16 * qb + c16, grp);
+      o.qa[qb] = half_row8<kHalfRows>(sQ[buf], 32 * j + 16 * qb + c16, grp & 1);
+      o.da[qb] = half_row4<kHalfRows>(sDO[buf], 32 * j + 16 * qb + c16, grp);
       o.ls[qb] = ldsf4(&sLse[buf][32 * j + 16 * qb + 4 * grp]);
       o.dl[qb] = ldsf4(&sDel[buf][32 * j + 16 * qb + 4 * grp]);
     }
-    o.dot = tr_operand(sDO[buf], 32 * j, c16, grp);
-    o.qt = tr_operand(sQ[buf], 32 * j, c16, grp);
+    o.dot = tr_operand<kHalfRows>(sDO[buf], 32 * j, c16, grp);
+    o.qt = tr_operand<kHalfRows>(sQ[buf], 32 * j, c16, grp);
     return o;
   };
   auto tile = [&](const Ops& o, int q0) {

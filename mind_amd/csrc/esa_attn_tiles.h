@@ -81,8 +81,8 @@ DEVI void split_scaled(const bf16x8& x, float c, bf16x8& hi, bf16x8& lo) {
 // for owned token l % 16, so the tile's two partner blocks leave a lane 8
 // partner rows of one owned token, {4G..4G+3, 16+4G..16+4G+3}: exactly the
 // K slots 8G..8G+7 a lane supplies to the mfma16k32 that sums over the
-// tile's 32 partners.  Transposed LDS tiles store partner t at column
-// slot_col(t), so one 16-byte read at column 8G is the matching A operand.
+// tile's 32 partners.  slot_col(t) is the K slot of tile-local partner t
+// in that order; tr_operand (below) reads the matching A operand.
 DEVI int slot_col(int t) { return 8 * ((t & 15) >> 2) + 4 * (t >> 4) + (t & 3); }
 
 // B operand of a scaled score mfma16k32: K slots 0..15 carry the bf16 hi
@@ -121,6 +121,58 @@ DEVI void store_dims4(bf16* __restrict__ row, const f32x4& acc, float mul, int g
 #pragma unroll
   for (int i = 0; i < 4; ++i) o[i] = (bf16)(acc[i] * mul);
   *reinterpret_cast<bf16x4*>(row + 4 * g) = o;
+}
+
+// ---- staged rows split by dims half
+// An LDS tile of token rows as two [n][8] bf16 arrays (dims 0..7, 8..15),
+// HS bf16 apart: the 16 lanes of a lane group reading 16 consecutive
+// tokens' halves touch 256 contiguous bytes (no bank conflicts on gfx950).
+template <int HS>
+DEVI void put_half(bf16* rows, int tok, int h, i32x4 v) {
+  *reinterpret_cast<i32x4*>(&rows[h * HS + tok * 8]) = v;
+}
+template <int HS>
+DEVI bf16x8 half_row8(const bf16* rows, int tok, int h) { return lds8(&rows[h * HS + tok * 8]); }
+template <int HS>
+DEVI bf16x4 half_row4(const bf16* rows, int tok, int q) {   // dims 4q .. 4q + 3
+  return lds4(&rows[(q >> 1) * HS + tok * 8 + 4 * (q & 1)]);
+}
+
+// ds_read_b64_tr_b16 (gfx950): lane i of a 16-lane group receives, as its
+// element k, element i % 4 of the 8-byte chunk addressed by lane 4k + i / 4
+// of the group.
+DEVI bf16x4 lds_tr4(const bf16* p) {
+  typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p);
+}
+
+// The mfma16k32 A operand over the 32 tokens of a split-row tile starting at
+// token t0 (lane c16 + 16 grp: dim c16 of the tokens in K slots 8 grp ..
+// 8 grp + 7, slot order of slot_col) by two transpose reads: lane j of the
+// group addresses token 4 grp + j / 4 (16 more for the second read), dims
+// 4 (j % 4) .. +3, so lane i receives dim i of four tokens.
+template <int HS>
+DEVI bf16x8 tr_operand(const bf16* rows, int t0, int c16, int grp) {
+  const int q = c16 & 3;
+  const bf16* p = rows + (q >> 1) * HS + (t0 + 4 * grp + (c16 >> 2)) * 8 + 4 * (q & 1);
+  const bf16x4 lo = lds_tr4(p), hi = lds_tr4(p + 16 * 8);
+  return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+// A operands [V^T ; 1] of the two mfma32 P V products of the split-row tile
+// at token t0 (keys 0..15 and 16..31 of the tile), by transpose reads:
+// lane groups 0 and 2 (rows 0..15, K slots 0..7 and 8..15) read dims of four
+// keys per read, groups 1 and 3 (the ones rows) read the 4-element ones
+// array `ones`.
+template <int HS>
+DEVI void vt_ones(const bf16* rows, int t0, const bf16* ones, int c16, int grp, bf16x8& vt0, bf16x8& vt1) {
+  const int q = c16 & 3;
+  const int step = (grp & 1) ? 0 : 8;   // bf16 per key in the read address
+  const bf16* p = (grp & 1) ? ones : rows + (q >> 1) * HS + (t0 + 8 * (grp >> 1) + (c16 >> 2)) * 8 + 4 * (q & 1);
+  const bf16x4 v0 = lds_tr4(p), v1 = lds_tr4(p + 4 * step);
+  const bf16x4 v2 = lds_tr4(p + 16 * step), v3 = lds_tr4(p + 20 * step);
+  vt0 = bf16x8{v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+  vt1 = bf16x8{v2[0], v2[1], v2[2], v2[3], v3[0], v3[1], v3[2], v3[3]};
 }
 
 DEVI f32x16 splat16(float x) {

@@ -102,6 +102,22 @@ def test_masked_small_molecules(device):
     _check(device, gb.edge_counts, gb.edge_counts, seed=31, src=src, dst=dst)
 
 
+@pytest.mark.parametrize("heads", [1, 5])
+def test_masked_head_counts(device, heads):
+    # The edge-mask kernels take heads in groups; a last, partial group.
+    gb = generators.protein_like(seed=4, num_graphs=3, n_min=30, n_max=70)
+    src, dst = gb.edge_index[0].astype(np.int32), gb.edge_index[1].astype(np.int32)
+    _check(device, gb.edge_counts, gb.edge_counts, seed=41 + heads, src=src, dst=dst, heads=heads)
+
+
+def test_masked_segments_straddle_tiles(device):
+    # Short graphs packed back to back: most 32-token tiles hold tokens of
+    # several segments, and some graphs have a single edge.
+    gb, _ = generators.small_molecules(seed=9, num_graphs=24)
+    src, dst = gb.edge_index[0].astype(np.int32), gb.edge_index[1].astype(np.int32)
+    _check(device, gb.edge_counts, gb.edge_counts, seed=91, src=src, dst=dst)
+
+
 def test_masked_isolated_rows_give_zero(device):
     # Two disjoint edges in one segment: neither shares a node with the other.
     src = np.array([0, 2, 4], np.int32)
