@@ -1,4 +1,8 @@
-// Varlen (packed-segment) attention for edge-set attention on gfx950.
+// Varlen (packed-segment) attention for edge-set attention on gfx950: the
+// C ABI entry points, the edge-mask (share-an-endpoint) bf16 kernels, the
+// fp32 kernels (dense and edge mask) and the per-call prep.  Dense bf16
+// attention dispatches to esa_attn_dense.hip, the node-mode CSR mask to
+// esa_graph_attn.hip.
 //
 // Forward:  O = softmax(scale * Q K^T + mask) V per segment, fp32 softmax,
 //           bf16 MFMA (v_mfma_f32_32x32x16_bf16) for Q K^T and P V.
@@ -11,16 +15,17 @@
 // get_adj_mask_from_edge_index_edge builds (esa/masked_layers.py:121-142,
 // 217-268) and memory_efficient_attention applies (esa/mha.py:73-77).
 //
-// Tiling.  Tokens are cut into 32-token tiles aligned to the global token
-// index; a tile may straddle segments, which the per-element validity test
-// (partner token in the lane's segment) resolves.  A 256-thread block is
-// four waves of ONE head working on four consecutive tiles (a 128-token
-// group); every partner tile the group needs is loaded from HBM/L2 once per
-// block into double-buffered LDS and read by all four waves, transposed on
-// the way in where an MFMA operand wants the token dimension contiguous.
-// Groups are dispatched longest-first (a per-call plan kernel sorts them by
-// the number of partner tiles); consecutive blocks are different heads, so
-// all blocks of a head land on the same XCD and share its L2.
+// Edge-mask tiling.  Tokens are cut into 32-token tiles aligned to the
+// global token index; a tile may straddle segments, which the per-element
+// validity test (partner token in the lane's segment) resolves.  A wave owns
+// one outer tile and two heads; the four waves of a 256-thread block are the
+// four tiles of a 128-token group and walk on their own: each visits only
+// the partner tiles whose node sets may meet its tile (node-range and 64-bit
+// signature test of per-tile metadata), staging them into its own
+// double-buffered LDS region.  The mask of a visited tile is evaluated once
+// per wave into an additive bias (0 or -inf per score) that seeds the score
+// MFMA of each head.  Groups are dispatched longest-first (a per-call plan
+// kernel sorts them by the number of partner tiles).
 //
 // Register layout (head_dim = 16 = the MFMA K of 32x32x16):
 //   S^T = K_tile * Q_tile^T : lane l owns query column l%32; its 16 fp32
@@ -30,7 +35,9 @@
 //   the B operand of the P V product, with no data movement.
 //   O^T = [V^T ; 1] * P^T : rows 0..15 are the output dims, rows 16..31 are
 //   ones, so the MFMA also produces the softmax row sum.  Softmax statistics
-//   stay per lane (one query per lane).
+//   stay per lane (one query per lane).  Operands with the token dimension
+//   in the MFMA K slots (V^T, K^T, Q^T, dO^T) come from LDS transpose reads
+//   of rows staged split by dims half.
 //   The dK/dV pass keeps keys on lanes; per-query row statistics (LSE, D)
 //   enter through an extra MFMA whose A operand carries (hi, lo) bf16 halves
 //   of -LSE/c and -D per row and whose B operand is a column of ones: it
@@ -115,41 +122,11 @@ DEVI OuterTile outer_tile(const int2* __restrict__ bounds, int total, int o0, in
   return t;
 }
 
-// Masked mode: keep accumulator row r of this lane (partner token
-// p0 + row_local(r, half)) only if the partner shares an endpoint with the
-// lane's own token, lies in the lane's segment and is not the token itself;
-// other rows become `off`.  Endpoint sharing is min over the four xors == 0
-// (plain VALU, no lane-mask juggling); segment bounds and the diagonal are
-// only tested on tiles that straddle a segment bound of the wave or hold the
-// wave's own tokens (o0 == p0), a wave-uniform branch.
-template <class Rows>
-DEVI void mask_rows(Rows& x, float off, const OuterTile& ot, int p0, int o0, int half, const int2* sn, int2 own) {
-  int2 pn[16];
-  lds_nodes16(sn, half, pn);
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const uint32_t d = min(min((uint32_t)(pn[r].x ^ own.x), (uint32_t)(pn[r].x ^ own.y)),
-                           min((uint32_t)(pn[r].y ^ own.x), (uint32_t)(pn[r].y ^ own.y)));
-    x[r] = d == 0u ? x[r] : off;
-  }
-  if (!(p0 >= ot.plo_max && p0 + kTile <= ot.phi_min) || p0 == o0) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int p = p0 + row_local(r, half);
-      x[r] = (p >= ot.plo && p < ot.phi && p != ot.oi) ? x[r] : off;
-    }
-  }
-}
-
-// ---------------------------------------------------------------- tile walks
+// ---------------------------------------------------------------- tile walk
 //
-// Dense mode: the four waves of a block share every partner tile of their
-// 128-token group.  Each tile is loaded once per block, one staging role per
-// wave, into double-buffered LDS, with a block barrier per tile.
-//
-// Masked mode: each wave walks, on its own, only the partner tiles whose
-// node sets may meet its outer tile (node range and 64-bit signature test of
-// the per-tile metadata; 64 candidates per ballot), staging them into its own
+// Each wave walks, on its own, only the partner tiles whose node sets may
+// meet its outer tile (node range and 64-bit signature test of the per-tile
+// metadata; 64 candidates per ballot), staging them into its own
 // double-buffered LDS region.  No block barrier: a wave never waits for
 // another wave's tiles.
 
@@ -162,7 +139,6 @@ DEVI void wave_sync() {
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
-DEVI void block_sync() { __syncthreads(); }
 
 // Walk over n partner tiles: next(waves) returns the next tile index (in
 // order; past the end it repeats the last one) and its wave mask,
@@ -207,18 +183,9 @@ DEVI void tile_pipeline(int n, Next next, Load gload, Store lstore, Sync sync, B
   }
 }
 
-// Both walks start with every earlier vector-memory load complete: a
+// The walk starts with every earlier vector-memory load complete: a
 // prologue load still pending inside the loop would be waited for with
 // vmcnt(0), which also waits for the prefetches in flight.
-template <class Load, class Store, class Body>
-DEVI void block_tile_walk(int gbeg, int gend, Load gload, Store lstore, Body body) {
-  __builtin_amdgcn_s_waitcnt(kWaitVmem);
-  const int n = gend - gbeg;
-  int i = 0;
-  tile_pipeline(n, [&](uint32_t& w) { w = 0xfu; const int p = gbeg + min(i, n - 1); ++i; return p; }, gload, lstore,
-                block_sync, body);
-}
-
 template <class Load, class Store, class Body>
 DEVI void wave_tile_walk(int pt_beg, int pt_end, int4 own, const int4* __restrict__ meta, int lane, Load gload,
                          Store lstore, Body body) {
@@ -276,163 +243,17 @@ DEVI StageSrc rows_src(const void* p, int bytes, int H, int head, int lane) {
 DEVI StageSrc records_src(const void* p, int n_records, int lane) {
   return StageSrc{make_rsrc(p, (uint32_t)n_records * 8u), lane < 16 ? 16u * lane : 0x80000000u, (uint32_t)kTile * 8u};
 }
-DEVI StageSrc empty_src() { return StageSrc{make_rsrc(nullptr, 0u), 0u, 0u}; }
 
-// LDS writes of a staged 32-token tile: rows [token][16] (padded stride),
-// transposed [16 dims][token], and 8-byte records (lanes 0..15).
+// LDS writes of a staged 32-token tile: rows [token][16] (padded stride) and
+// 8-byte records (lanes 0..15).
 DEVI void put_rows(bf16* rows, i32x4 v, int lane) {
   *reinterpret_cast<i32x4*>(&rows[(lane >> 1) * kRowStride + 8 * (lane & 1)]) = v;
-}
-DEVI void put_rows_t(bf16* tr, i32x4 v, int lane) {
-  const bf16x8 x = as_bf16x8(v);
-#pragma unroll
-  for (int e = 0; e < 8; ++e) tr[(8 * (lane & 1) + e) * kTrStride + (lane >> 1)] = x[e];
 }
 template <class R>
 DEVI void put_records(R* rec, i32x4 v, int lane) {
   if (lane < 16) *reinterpret_cast<i32x4*>(&rec[2 * lane]) = v;
 }
 
-struct Stage3 { i32x4 a, b, c; };
-struct Stage4 { i32x4 a, b, c, d; };
-
-// ======================================================================== forward
-// Occupancy targets (waves per SIMD) keep the kernels inside the VGPR budget
-// that the compiler would otherwise overshoot by a few registers.
-template <bool MASKED>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MASKED ? 3 : 6))) void attn_fwd_kernel(
-    const AttnArgs a) {
-  constexpr int W = MASKED ? kWaves : 1;   // LDS staging regions: per wave (masked) or per block
-  __shared__ __align__(16) bf16 sK[W][2][kTile * kRowStride];   // K rows [key][16]
-  __shared__ __align__(16) bf16 sVT[W][2][32 * kTrStride];      // [V^T ; 1]: rows 0..15 dims, 16..31 ones
-  __shared__ __align__(16) int2 sN[W][2][kTile];
-  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int col = lane & 31, half = lane >> 5;
-  const int sw = MASKED ? wave : 0;
-  const int H = a.heads;
-  const int item = blockIdx.x / H;
-  const int head = blockIdx.x - item * H;
-  const int4 pl = a.plan[item];
-  const int t0 = pl.x * kGroupTok;
-
-  for (int i = tid; i < W * 2 * 16 * kTrStride; i += 256) {
-    const int st = i / (16 * kTrStride);
-    sVT[st >> 1][st & 1][16 * kTrStride + (i - st * 16 * kTrStride)] = (bf16)1.f;
-  }
-  const OuterTile ot = outer_tile(a.bounds, a.total_q, t0 + wave * kTile, col);
-  const bf16x8 qf = *reinterpret_cast<const bf16x8*>(a.q + ((size_t)ot.oc * H + head) * kHd + 8 * half);
-  int2 qn = make_int2(0, 0);
-  int4 own = no_touch();
-  if (MASKED) {
-    qn = a.nodes[ot.oc];
-    if (ot.active) own = a.meta[(t0 + wave * kTile) / kTile];
-  }
-
-  // Bound b = c |q| max|k| over the keys this wave visits.
-  float b = 0.f;
-  bool fixed_ref = true;
-  if (ot.active) {
-    float qq = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) qq = fmaf((float)qf[e], (float)qf[e], qq);
-    qq += __shfl_xor(qq, 32);
-    float km = 0.f;
-    for (int t = ot.pt_beg + lane; t < ot.pt_end; t += 64) km = fmaxf(km, a.knorm[(size_t)head * a.tk_tiles + t]);
-    km = wave_max(km);
-    b = a.c * sqrtf(qq) * km;
-    fixed_ref = __builtin_amdgcn_readfirstlane((int)(wave_max(ot.valid ? b : 0.f) <= kStaticBound)) != 0;
-  }
-  // With |S'| <= b <= kStaticBound every exp2(S') is a normal fp32 / bf16
-  // value and a row sum of up to 2^31 such terms cannot overflow, so the
-  // fixed path needs no reference point at all: P = exp2(S') with
-  // S' = K (c q)^T straight out of the MFMA.  Otherwise the running max is
-  // tracked (online softmax).
-  float m_run = fixed_ref ? 0.f : -INFINITY;
-  bf16x8 qh, ql;
-  split_scaled(qf, a.c, qh, ql);
-
-  f32x16 acc = {};
-  // The fixed-reference and the online (running-max) loops are separate
-  // instantiations so the accumulator stays in place across iterations.
-  auto run = [&](auto online_tag) {
-    constexpr bool ONLINE = decltype(online_tag)::value;
-    const f32x16 zero = {};
-    auto body = [&](int pt, int cur, uint32_t waves) {
-      if (((waves >> wave) & 1u) && pt >= ot.pt_beg && pt < ot.pt_end) {
-        const int k0 = pt * kTile;
-        const bf16x8 kr = lds8(&sK[sw][cur][kperm(col) * kRowStride + 8 * half]);
-        f32x16 s = mfma32(kr, ql, mfma32(kr, qh, zero));
-        if (MASKED) {
-          mask_rows(s, -INFINITY, ot, k0, t0 + wave * kTile, half, sN[sw][cur], qn);
-        } else if (!(k0 >= ot.plo_max && k0 + kTile <= ot.phi_min)) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int key = k0 + row_local(r, half);
-            s[r] = (key >= ot.plo && key < ot.phi) ? s[r] : -INFINITY;
-          }
-        }
-        if (ONLINE) {
-          float mt = s[0];
-#pragma unroll
-          for (int r = 1; r < 16; ++r) mt = fmaxf(mt, s[r]);
-          mt = fmaxf(mt, __shfl_xor(mt, 32));
-          const float m_new = fmaxf(m_run, mt);
-          if (__ballot(m_new > m_run)) {
-            const float alpha = fast_exp2(m_run - (m_new == -INFINITY ? 0.f : m_new));
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[r] *= alpha;
-            m_run = m_new;
-          }
-        }
-        float p[16];
-        if (ONLINE) {
-          const float m_use = m_run == -INFINITY ? 0.f : m_run;
-#pragma unroll
-          for (int r = 0; r < 16; ++r) p[r] = fast_exp2(s[r] - m_use);
-        } else {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) p[r] = fast_exp2(s[r]);
-        }
-        acc = mfma32(lds8(&sVT[sw][cur][col * kTrStride + 8 * half]), cvt8(p), acc);
-        acc = mfma32(lds8(&sVT[sw][cur][col * kTrStride + 16 + 8 * half]), cvt8(p + 8), acc);
-      }
-    };
-    const int kv_bytes = a.total_k * H * kHd * 2;
-    if constexpr (MASKED) {
-      // Every wave stages K rows, V^T and node pairs of its own tiles.
-      const StageSrc sk = rows_src(a.k, kv_bytes, H, head, lane), sv = rows_src(a.v, kv_bytes, H, head, lane);
-      const StageSrc sn = records_src(a.nodes, a.tq_pad, lane);
-      wave_tile_walk(ot.pt_beg, ot.pt_end, own, a.meta, lane,
-                     [&](int pt) { return Stage3{sk.load(pt), sv.load(pt), sn.load(pt)}; },
-                     [&](int st, const Stage3& g) {
-                       put_rows(sK[sw][st], g.a, lane);
-                       put_rows_t(sVT[sw][st], g.b, lane);
-                       put_records(sN[sw][st], g.c, lane);
-                     },
-                     body);
-    } else {
-      // Staging roles: wave 0 copies K rows, wave 1 transposes V rows into V^T.
-      const StageSrc src = wave == 0 ? rows_src(a.k, kv_bytes, H, head, lane)
-                                     : wave == 1 ? rows_src(a.v, kv_bytes, H, head, lane) : empty_src();
-      block_tile_walk(pl.y, pl.z, [&](int pt) { return src.load(pt); },
-                      [&](int st, i32x4 v) {
-                        if (wave == 0) put_rows(sK[0][st], v, lane);
-                        else if (wave == 1) put_rows_t(sVT[0][st], v, lane);
-                      },
-                      body);
-    }
-  };
-  if (fixed_ref)
-    run(std::integral_constant<bool, false>{});
-  else
-    run(std::integral_constant<bool, true>{});
-  if (!ot.valid) return;
-  const float l = acc[8];  // a ones row of [V^T; 1] P^T: the softmax row sum
-  const float inv = l > 0.f ? 1.f / l : 0.f;
-  store_rows8(a.o + ((size_t)ot.oi * H + head) * kHd, acc, inv, half);
-  if (half == 0)
-    a.lse_out[(size_t)head * a.total_q + ot.oi] = l > 0.f ? (m_run + fast_log2(l)) * kLn2 : -INFINITY;
-}
 
 // ======================================================================== edge-mask forward, heads in pairs
 // One wave = one 32-query tile and kEdgeHeads heads of it (the four waves of
@@ -445,9 +266,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MASKED ? 3 
 // rows (split by dims half; the [V^T ; 1] operands come from LDS transpose
 // reads) of all heads of the wave plus the 32 node pairs.
 
-#ifndef ESA_EDGE_V2
-#define ESA_EDGE_V2 1
-#endif
 #ifndef ESA_EDGE_HEADS
 #define ESA_EDGE_HEADS 2
 #endif
@@ -579,7 +397,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ESA_EDGE_WA
 #pragma unroll
         for (int r = 0; r < 16; ++r) p[r] = fast_exp2(ONLINE ? s[r] - m_use : s[r]);
         bf16x8 vt0, vt1;
-        vt_ones<kTileHalf>(sV[wave][cur][u], 0, sOnes, c16, grp, vt0, vt1);
+        tr_rows32<kTileHalf>(sV[wave][cur][u], 0, sOnes, c16, grp, vt0, vt1);
         acc[u] = mfma32(vt0, cvt8(p), acc[u]);
         acc[u] = mfma32(vt1, cvt8(p + 8), acc[u]);
       }
@@ -621,208 +439,233 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ESA_EDGE_WA
   }
 }
 
-// ======================================================================== dQ pass
-// One wave = one query tile: dQ = scale * dS K with dS = P * (dP - D),
-// recomputing P from the saved LSE.  D = rowsum(dO * O) is computed per lane.
-template <bool MASKED>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MASKED ? 3 : 4))) void attn_dq_kernel(const AttnArgs a) {
-  constexpr int W = MASKED ? kWaves : 1;
-  __shared__ __align__(16) bf16 sK[W][2][kTile * kRowStride];    // K rows
-  __shared__ __align__(16) bf16 sV[W][2][kTile * kRowStride];    // V rows
-  __shared__ __align__(16) bf16 sKT[W][2][16 * kTrStride];       // K^T
-  __shared__ __align__(16) int2 sN[W][2][kTile];
-  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int col = lane & 31, half = lane >> 5;
-  const int sw = MASKED ? wave : 0;
-  const int H = a.heads;
-  const int item = blockIdx.x / H;
-  const int head = blockIdx.x - item * H;
-  const int4 pl = a.plan[item];
-  const int t0 = pl.x * kGroupTok;
+// ======================================================================== edge-mask dQ pass
+// One wave = one 32-query tile and kEdgeHeads heads of it, as the forward:
+// dQ = scale * dS K with dS = P * (dP - D), P recomputed from the saved
+// LSE.  The mask bias of a candidate key tile is evaluated once and seeds
+// every head's score MFMA; K and V are staged as split rows, K^T comes from
+// LDS transpose reads.
 
-  const OuterTile ot = outer_tile(a.bounds, a.total_q, t0 + wave * kTile, col);
-  const size_t row = ((size_t)ot.oc * H + head) * kHd + 8 * half;
-  const bf16x8 qf = *reinterpret_cast<const bf16x8*>(a.q + row);
-  const bf16x8 dof = *reinterpret_cast<const bf16x8*>(a.dout + row);
-  const bf16x8 of = *reinterpret_cast<const bf16x8*>(a.out + row);
-  float dsum = 0.f;
+#ifndef ESA_EDGE_WAVES_DQ
+#define ESA_EDGE_WAVES_DQ 3
+#endif
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ESA_EDGE_WAVES_DQ))) void edge_dq_kernel(
+    const AttnArgs a) {
+  constexpr int NH = kEdgeHeads;
+  __shared__ __align__(16) bf16 sK[kWaves][2][NH][2 * kTileHalf];   // K rows split by dims half
+  __shared__ __align__(16) bf16 sV[kWaves][2][NH][2 * kTileHalf];   // V rows split by dims half
+  __shared__ __align__(16) int2 sN[kWaves][2][kTile];
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 31, half = lane >> 5, c16 = lane & 15, grp = lane >> 4;
+  const int H = a.heads, n_hg = (H + NH - 1) / NH;
+  const int item = blockIdx.x / n_hg, hg = blockIdx.x - item * n_hg;
+  const int h0 = hg * NH;
+  const int nh = min(NH, H - h0);   // heads of this wave
+  const int4 pl = a.plan[item];
+  const int o0 = pl.x * kGroupTok + wave * kTile;
+
+  const OuterTile ot = outer_tile(a.bounds, a.total_q, o0, col);
+  const int2 qn = a.nodes[ot.oc];
+  const int4 own = ot.active ? a.meta[o0 / kTile] : no_touch();
+  bf16x8 qf[NH], dof[NH];
+  float dsum[NH], lse2q[NH];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) dsum = fmaf((float)dof[e], (float)of[e], dsum);
-  dsum += __shfl_xor(dsum, 32);
-  const float lq = a.lse[(size_t)head * a.total_q + ot.oc];
-  const float lse2q = lq == -INFINITY ? INFINITY : lq * kLog2e;
-  const f32x16 cd = splat16(-dsum);  // accumulator seed of dP^T: -D in every row of this lane's column
-  int2 qn = make_int2(0, 0);
-  int4 own = no_touch();
-  if (MASKED) {
-    qn = a.nodes[ot.oc];
-    if (ot.active) own = a.meta[(t0 + wave * kTile) / kTile];
+  for (int u = 0; u < NH; ++u) {
+    const int hc = min(h0 + u, H - 1);
+    const size_t row = ((size_t)ot.oc * H + hc) * kHd + 8 * half;
+    qf[u] = *reinterpret_cast<const bf16x8*>(a.q + row);
+    dof[u] = *reinterpret_cast<const bf16x8*>(a.dout + row);
+    const bf16x8 of = *reinterpret_cast<const bf16x8*>(a.out + row);
+    float d = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) d = fmaf((float)dof[u][e], (float)of[e], d);
+    dsum[u] = d + __shfl_xor(d, 32);
+    const float lq = a.lse[(size_t)hc * a.total_q + ot.oc];
+    lse2q[u] = lq == -INFINITY ? INFINITY : lq * kLog2e;
   }
 
-  f32x16 acc = {};
-  const f32x16 zero = {};
-  auto body = [&](int pt, int cur, uint32_t waves) {
-    if (((waves >> wave) & 1u) && pt >= ot.pt_beg && pt < ot.pt_end) {
-      const int k0 = pt * kTile;
-      f32x16 s = mfma32(lds8(&sK[sw][cur][kperm(col) * kRowStride + 8 * half]), qf, zero);
-      const f32x16 dp = mfma32(lds8(&sV[sw][cur][kperm(col) * kRowStride + 8 * half]), dof, cd);  // dP^T - D
-      if (MASKED) {
-        mask_rows(s, -INFINITY, ot, k0, t0 + wave * kTile, half, sN[sw][cur], qn);
-      } else if (!(k0 >= ot.plo_max && k0 + kTile <= ot.phi_min)) {
+  f32x16 acc[NH];
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = k0 + row_local(r, half);
-          s[r] = (key >= ot.plo && key < ot.phi) ? s[r] : -INFINITY;
-        }
-      }
+  for (int u = 0; u < NH; ++u) acc[u] = f32x16{};
+  const f32x16 zero = {};
+  auto body = [&](int pt, int cur, uint32_t) {
+    if (!(pt >= ot.pt_beg && pt < ot.pt_end)) return;
+    const int k0 = pt * kTile;
+    const f32x16 bias = edge_bias(ot, k0, o0, half, sN[wave][cur], qn);
+#pragma unroll
+    for (int u = 0; u < NH; ++u) {
+      if (u >= nh) break;   // wave-uniform
+      const f32x16 s = mfma32(half_row8<kTileHalf>(sK[wave][cur][u], kperm(col), half), qf[u], bias);
+      const f32x16 dp = mfma32(half_row8<kTileHalf>(sV[wave][cur][u], kperm(col), half), dof[u], zero);
       float ds[16];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) ds[r] = fast_exp2(fmaf(s[r], a.c, -lse2q)) * dp[r];
-      const int trow = (col & 15) * kTrStride + 8 * half;
-      acc = mfma32(lds8(&sKT[sw][cur][trow]), cvt8(ds), acc);
-      acc = mfma32(lds8(&sKT[sw][cur][trow + 16]), cvt8(ds + 8), acc);
+      for (int r = 0; r < 16; ++r) ds[r] = fast_exp2(fmaf(s[r], a.c, -lse2q[u])) * (dp[r] - dsum[u]);
+      bf16x8 kt0, kt1;
+      tr_rows32<kTileHalf>(sK[wave][cur][u], 0, nullptr, c16, grp, kt0, kt1);
+      acc[u] = mfma32(kt0, cvt8(ds), acc[u]);
+      acc[u] = mfma32(kt1, cvt8(ds + 8), acc[u]);
     }
   };
   const int kv_bytes = a.total_k * H * kHd * 2;
-  if constexpr (MASKED) {
-    const StageSrc sk = rows_src(a.k, kv_bytes, H, head, lane), sv = rows_src(a.v, kv_bytes, H, head, lane);
-    const StageSrc sn = records_src(a.nodes, a.tq_pad, lane);
-    wave_tile_walk(ot.pt_beg, ot.pt_end, own, a.meta, lane,
-                   [&](int pt) { return Stage3{sk.load(pt), sv.load(pt), sn.load(pt)}; },
-                   [&](int st, const Stage3& g) {
-                     put_rows(sK[sw][st], g.a, lane);
-                     put_rows_t(sKT[sw][st], g.a, lane);
-                     put_rows(sV[sw][st], g.b, lane);
-                     put_records(sN[sw][st], g.c, lane);
-                   },
-                   body);
-  } else {
-    // Staging roles: wave 0 K rows and K^T, wave 1 V rows.
-    const StageSrc src = wave == 0 ? rows_src(a.k, kv_bytes, H, head, lane)
-                                   : wave == 1 ? rows_src(a.v, kv_bytes, H, head, lane) : empty_src();
-    block_tile_walk(pl.y, pl.z, [&](int pt) { return src.load(pt); },
-                    [&](int st, i32x4 v) {
-                      if (wave == 0) {
-                        put_rows(sK[0][st], v, lane);
-                        put_rows_t(sKT[0][st], v, lane);
-                      } else if (wave == 1) {
-                        put_rows(sV[0][st], v, lane);
-                      }
-                    },
-                    body);
+  StageSrc sk[NH], sv[NH];
+#pragma unroll
+  for (int u = 0; u < NH; ++u) {
+    const int hc = min(h0 + u, H - 1);
+    sk[u] = split_rows_src(a.k, kv_bytes, H, hc, lane);
+    sv[u] = split_rows_src(a.v, kv_bytes, H, hc, lane);
   }
+  const StageSrc sn = records_src(a.nodes, a.tq_pad, lane);
+  wave_tile_walk(ot.pt_beg, ot.pt_end, own, a.meta, lane,
+                 [&](int pt) {
+                   StageEdge<NH> g;
+#pragma unroll
+                   for (int u = 0; u < NH; ++u) {
+                     g.k[u] = sk[u].load(pt);
+                     g.v[u] = sv[u].load(pt);
+                   }
+                   g.n = sn.load(pt);
+                   return g;
+                 },
+                 [&](int st, const StageEdge<NH>& g) {
+#pragma unroll
+                   for (int u = 0; u < NH; ++u) {
+                     put_half<kTileHalf>(sK[wave][st][u], lane & 31, lane >> 5, g.k[u]);
+                     put_half<kTileHalf>(sV[wave][st][u], lane & 31, lane >> 5, g.v[u]);
+                   }
+                   put_records(sN[wave][st], g.n, lane);
+                 },
+                 body);
   if (!ot.valid) return;
-  store_rows8(a.dq + ((size_t)ot.oi * H + head) * kHd, acc, a.scale, half);
+#pragma unroll
+  for (int u = 0; u < NH; ++u) {
+    if (u >= nh) break;
+    store_rows8(a.dq + ((size_t)ot.oi * H + h0 + u) * kHd, acc[u], a.scale, half);
+  }
 }
 
-// ======================================================================== dK/dV pass
-// One wave = one key tile (keys on lanes): dV = P^T dO, dK = scale * dS^T Q.
-template <bool MASKED>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MASKED ? 2 : 4))) void attn_dkdv_kernel(
-    const AttnArgs a) {
-  constexpr int W = MASKED ? kWaves : 1;
-  __shared__ __align__(16) bf16 sQ[W][2][kTile * kRowStride];    // Q rows
-  __shared__ __align__(16) bf16 sDO[W][2][kTile * kRowStride];   // dO rows
-  __shared__ __align__(16) bf16 sQT[W][2][16 * kTrStride];       // Q^T
-  __shared__ __align__(16) bf16 sDOT[W][2][16 * kTrStride];      // dO^T
-  __shared__ __align__(16) uint2 sAux[W][2][kTile];              // row-statistic MFMA operands
-  __shared__ __align__(16) int2 sN[W][2][kTile];
-  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int col = lane & 31, half = lane >> 5;
-  const int sw = MASKED ? wave : 0;
-  const int H = a.heads;
-  const int item = blockIdx.x / H;
-  const int head = blockIdx.x - item * H;
-  const int4 pl = a.plan[item];
-  const int t0 = pl.x * kGroupTok;
+// ======================================================================== edge-mask dK/dV pass
+// One wave = one 32-key tile (keys on lanes, queries in rows) and
+// kEdgeHeadsKv heads of it: dV = P^T dO, dK = scale * dS^T Q.  Row
+// statistics (-LSE2/c, -D as bf16 hi/lo pairs) enter through MFMAs against a
+// ones column; the mask bias of a candidate query tile, evaluated once per
+// tile, seeds every head's -LSE2/c one.  Q and dO are staged as split rows,
+// Q^T and dO^T come from LDS transpose reads.
 
-  const OuterTile ot = outer_tile(a.bounds, a.total_k, t0 + wave * kTile, col);
-  const size_t row = ((size_t)ot.oc * H + head) * kHd + 8 * half;
-  const bf16x8 kf = *reinterpret_cast<const bf16x8*>(a.k + row);
-  const bf16x8 vf = *reinterpret_cast<const bf16x8*>(a.v + row);
-  // B operand of the row-statistic MFMA: ones in slots 0 and 1 (half 0).
+#ifndef ESA_EDGE_HEADS_KV
+#define ESA_EDGE_HEADS_KV 2
+#endif
+constexpr int kEdgeHeadsKv = ESA_EDGE_HEADS_KV;
+#ifndef ESA_EDGE_WAVES_DKDV
+#define ESA_EDGE_WAVES_DKDV 2
+#endif
+
+template <int NH>
+struct StageKv { i32x4 q[NH], d[NH], x[NH], n; };
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ESA_EDGE_WAVES_DKDV))) void edge_dkdv_kernel(
+    const AttnArgs a) {
+  constexpr int NH = kEdgeHeadsKv;
+  __shared__ __align__(16) bf16 sQ[kWaves][2][NH][2 * kTileHalf];    // Q rows split by dims half
+  __shared__ __align__(16) bf16 sDO[kWaves][2][NH][2 * kTileHalf];   // dO rows split by dims half
+  __shared__ __align__(16) uint2 sAux[kWaves][2][NH][kTile];         // row-statistic MFMA operands
+  __shared__ __align__(16) int2 sN[kWaves][2][kTile];
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 31, half = lane >> 5, c16 = lane & 15, grp = lane >> 4;
+  const int H = a.heads, n_hg = (H + NH - 1) / NH;
+  const int item = blockIdx.x / n_hg, hg = blockIdx.x - item * n_hg;
+  const int h0 = hg * NH;
+  const int nh = min(NH, H - h0);   // heads of this wave
+  const int4 pl = a.plan[item];
+  const int o0 = pl.x * kGroupTok + wave * kTile;
+
+  const OuterTile ot = outer_tile(a.bounds, a.total_k, o0, col);
+  bf16x8 kf[NH], vf[NH];
+#pragma unroll
+  for (int u = 0; u < NH; ++u) {
+    const size_t row = ((size_t)ot.oc * H + min(h0 + u, H - 1)) * kHd + 8 * half;
+    kf[u] = *reinterpret_cast<const bf16x8*>(a.k + row);
+    vf[u] = *reinterpret_cast<const bf16x8*>(a.v + row);
+  }
+  // B operand of the row-statistic MFMAs: ones in slots 0 and 1 (half 0).
   bf16x8 ones2 = {};
   if (half == 0) { ones2[0] = (bf16)1.f; ones2[1] = (bf16)1.f; }
-  int2 kn = make_int2(0, 0);
-  int4 own = no_touch();
-  if (MASKED) {
-    kn = a.nodes[ot.oc];
-    if (ot.active) own = a.meta[(t0 + wave * kTile) / kTile];
-  }
+  const int2 kn = a.nodes[ot.oc];
+  const int4 own = ot.active ? a.meta[o0 / kTile] : no_touch();
 
-  f32x16 dva = {}, dka = {};
+  f32x16 dva[NH], dka[NH];
+#pragma unroll
+  for (int u = 0; u < NH; ++u) dva[u] = dka[u] = f32x16{};
   const f32x16 zero = {};
-  auto body = [&](int pt, int cur, uint32_t waves) {
-    if (((waves >> wave) & 1u) && pt >= ot.pt_beg && pt < ot.pt_end) {
-      const int q0 = pt * kTile;
-      const int rrow = kperm(col) * kRowStride + 8 * half;
-      const uint2 ax = sAux[sw][cur][kperm(col)];
+  auto body = [&](int pt, int cur, uint32_t) {
+    if (!(pt >= ot.pt_beg && pt < ot.pt_end)) return;
+    const int q0 = pt * kTile;
+    const f32x16 bias = edge_bias(ot, q0, o0, half, sN[wave][cur], kn);
+#pragma unroll
+    for (int u = 0; u < NH; ++u) {
+      if (u >= nh) break;   // wave-uniform
+      const uint2 ax = sAux[wave][cur][u][kperm(col)];
       const bf16x8 aux_s = as_bf16x8(i32x4{(int)ax.x, 0, 0, 0});
       const bf16x8 aux_d = as_bf16x8(i32x4{(int)ax.y, 0, 0, 0});
-      // S' = Q K^T - LSE2/c and dP' = dO V^T - D, rows = queries, lanes = keys.
-      const f32x16 s = mfma32(lds8(&sQ[sw][cur][rrow]), kf, mfma32(aux_s, ones2, zero));
-      const f32x16 dp = mfma32(lds8(&sDO[sw][cur][rrow]), vf, mfma32(aux_d, ones2, zero));
-      float p[16];
+      // S' = Q K^T - LSE2/c + bias and dP' = dO V^T - D, rows = queries, lanes = keys.
+      const f32x16 s =
+          mfma32(half_row8<kTileHalf>(sQ[wave][cur][u], kperm(col), half), kf[u], mfma32(aux_s, ones2, bias));
+      const f32x16 dp =
+          mfma32(half_row8<kTileHalf>(sDO[wave][cur][u], kperm(col), half), vf[u], mfma32(aux_d, ones2, zero));
+      float p[16], ds[16];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) p[r] = fast_exp2(s[r] * a.c);
-      if (MASKED) {
-        mask_rows(p, 0.f, ot, q0, t0 + wave * kTile, half, sN[sw][cur], kn);
-      } else if (!(q0 >= ot.plo_max && q0 + kTile <= ot.phi_min)) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int qq = q0 + row_local(r, half);
-          p[r] = (qq >= ot.plo && qq < ot.phi) ? p[r] : 0.f;
-        }
+      for (int r = 0; r < 16; ++r) {
+        p[r] = fast_exp2(s[r] * a.c);
+        ds[r] = p[r] * dp[r];
       }
-      float ds[16];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) ds[r] = p[r] * dp[r];
-      const int trow = (col & 15) * kTrStride + 8 * half;
-      dva = mfma32(lds8(&sDOT[sw][cur][trow]), cvt8(p), dva);
-      dva = mfma32(lds8(&sDOT[sw][cur][trow + 16]), cvt8(p + 8), dva);
-      dka = mfma32(lds8(&sQT[sw][cur][trow]), cvt8(ds), dka);
-      dka = mfma32(lds8(&sQT[sw][cur][trow + 16]), cvt8(ds + 8), dka);
+      bf16x8 d0, d1, q0t, q1t;
+      tr_rows32<kTileHalf>(sDO[wave][cur][u], 0, nullptr, c16, grp, d0, d1);
+      tr_rows32<kTileHalf>(sQ[wave][cur][u], 0, nullptr, c16, grp, q0t, q1t);
+      dva[u] = mfma32(d0, cvt8(p), dva[u]);
+      dva[u] = mfma32(d1, cvt8(p + 8), dva[u]);
+      dka[u] = mfma32(q0t, cvt8(ds), dka[u]);
+      dka[u] = mfma32(q1t, cvt8(ds + 8), dka[u]);
     }
   };
   const int q_bytes = a.total_q * H * kHd * 2;
-  const uint2* aux_head = a.aux + (size_t)head * a.tq_pad;
-  if constexpr (MASKED) {
-    const StageSrc sq = rows_src(a.q, q_bytes, H, head, lane), sd = rows_src(a.dout, q_bytes, H, head, lane);
-    const StageSrc sa = records_src(aux_head, a.tq_pad, lane), sn = records_src(a.nodes, a.tq_pad, lane);
-    wave_tile_walk(ot.pt_beg, ot.pt_end, own, a.meta, lane,
-                   [&](int pt) { return Stage4{sq.load(pt), sd.load(pt), sa.load(pt), sn.load(pt)}; },
-                   [&](int st, const Stage4& g) {
-                     put_rows(sQ[sw][st], g.a, lane);
-                     put_rows_t(sQT[sw][st], g.a, lane);
-                     put_rows(sDO[sw][st], g.b, lane);
-                     put_rows_t(sDOT[sw][st], g.b, lane);
-                     put_records(sAux[sw][st], g.c, lane);
-                     put_records(sN[sw][st], g.d, lane);
-                   },
-                   body);
-  } else {
-    // Staging roles: wave 0 Q rows (+ Q^T), wave 1 dO rows (+ dO^T), wave 2
-    // row statistics of this head.
-    const StageSrc src = wave == 0 ? rows_src(a.q, q_bytes, H, head, lane)
-                       : wave == 1 ? rows_src(a.dout, q_bytes, H, head, lane)
-                       : wave == 2 ? records_src(aux_head, a.tq_pad, lane) : empty_src();
-    block_tile_walk(pl.y, pl.z, [&](int pt) { return src.load(pt); },
-                    [&](int st, i32x4 v) {
-                      if (wave == 0) {
-                        put_rows(sQ[0][st], v, lane);
-                        put_rows_t(sQT[0][st], v, lane);
-                      } else if (wave == 1) {
-                        put_rows(sDO[0][st], v, lane);
-                        put_rows_t(sDOT[0][st], v, lane);
-                      } else if (wave == 2) {
-                        put_records(sAux[0][st], v, lane);
-                      }
-                    },
-                    body);
+  StageSrc sq[NH], sd[NH], sa[NH];
+#pragma unroll
+  for (int u = 0; u < NH; ++u) {
+    const int hc = min(h0 + u, H - 1);
+    sq[u] = split_rows_src(a.q, q_bytes, H, hc, lane);
+    sd[u] = split_rows_src(a.dout, q_bytes, H, hc, lane);
+    sa[u] = records_src(a.aux + (size_t)hc * a.tq_pad, a.tq_pad, lane);
   }
+  const StageSrc sn = records_src(a.nodes, a.tq_pad, lane);
+  wave_tile_walk(ot.pt_beg, ot.pt_end, own, a.meta, lane,
+                 [&](int pt) {
+                   StageKv<NH> g;
+#pragma unroll
+                   for (int u = 0; u < NH; ++u) {
+                     g.q[u] = sq[u].load(pt);
+                     g.d[u] = sd[u].load(pt);
+                     g.x[u] = sa[u].load(pt);
+                   }
+                   g.n = sn.load(pt);
+                   return g;
+                 },
+                 [&](int st, const StageKv<NH>& g) {
+#pragma unroll
+                   for (int u = 0; u < NH; ++u) {
+                     put_half<kTileHalf>(sQ[wave][st][u], lane & 31, lane >> 5, g.q[u]);
+                     put_half<kTileHalf>(sDO[wave][st][u], lane & 31, lane >> 5, g.d[u]);
+                     put_records(sAux[wave][st][u], g.x[u], lane);
+                   }
+                   put_records(sN[wave][st], g.n, lane);
+                 },
+                 body);
   if (!ot.valid) return;
-  store_rows8(a.dv + ((size_t)ot.oi * H + head) * kHd, dva, 1.f, half);
-  store_rows8(a.dk + ((size_t)ot.oi * H + head) * kHd, dka, a.scale, half);
+#pragma unroll
+  for (int u = 0; u < NH; ++u) {
+    if (u >= nh) break;
+    const int h = h0 + u;
+    store_rows8(a.dv + ((size_t)ot.oi * H + h) * kHd, dva[u], 1.f, half);
+    store_rows8(a.dk + ((size_t)ot.oi * H + h) * kHd, dka[u], a.scale, half);
+  }
 }
 
 // ======================================================================== fp32 path
@@ -1430,15 +1273,8 @@ int esa_varlen_attn_fwd(const void* q, const void* k, const void* v, const int* 
   a.plan = pa.plan_q; a.bounds = pa.bounds_q;
   a.nodes = pa.nodes; a.meta = pa.meta;
   a.o = static_cast<bf16*>(out); a.lse_out = softmax_lse;
-  if (masked && ESA_EDGE_V2)
-    ESA_TIMED(esa_profile::kAttnFwdMasked, st,
-              hipLaunchKernelGGL(edge_fwd_kernel, dim3((unsigned)groups_of(total_q) * (unsigned)((heads + kEdgeHeads - 1) / kEdgeHeads)),
-                                 dim3(256), 0, st, a));
-  else if (masked)
-    ESA_TIMED(esa_profile::kAttnFwdMasked, st,
-              hipLaunchKernelGGL((attn_fwd_kernel<true>), dim3(grid), dim3(256), 0, st, a));
-  else
-    ESA_TIMED(esa_profile::kAttnFwd, st, hipLaunchKernelGGL((attn_fwd_kernel<false>), dim3(grid), dim3(256), 0, st, a));
+  const unsigned egrid = (unsigned)groups_of(total_q) * (unsigned)((heads + kEdgeHeads - 1) / kEdgeHeads);
+  ESA_TIMED(esa_profile::kAttnFwdMasked, st, hipLaunchKernelGGL(edge_fwd_kernel, dim3(egrid), dim3(256), 0, st, a));
   ESA_LAUNCH_CHECK();
   return ESA_OK;
 }
@@ -1565,21 +1401,15 @@ int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k, const vo
 
   a.plan = pa.plan_k;
   a.bounds = pa.bounds_k;
-  if (masked)
-    ESA_TIMED(esa_profile::kAttnBwdDkdvMasked, st,
-              hipLaunchKernelGGL((attn_dkdv_kernel<true>), dim3(kgrid), dim3(256), 0, st, a));
-  else
-    ESA_TIMED(esa_profile::kAttnBwdDkdv, st,
-              hipLaunchKernelGGL((attn_dkdv_kernel<false>), dim3(kgrid), dim3(256), 0, st, a));
+  const unsigned ekgrid = (unsigned)groups_of(total_k) * (unsigned)((heads + kEdgeHeadsKv - 1) / kEdgeHeadsKv);
+  ESA_TIMED(esa_profile::kAttnBwdDkdvMasked, st,
+            hipLaunchKernelGGL(edge_dkdv_kernel, dim3(ekgrid), dim3(256), 0, st, a));
   ESA_LAUNCH_CHECK();
 
   a.plan = pa.plan_q;
   a.bounds = pa.bounds_q;
-  if (masked)
-    ESA_TIMED(esa_profile::kAttnBwdDqMasked, st,
-              hipLaunchKernelGGL((attn_dq_kernel<true>), dim3(qgrid), dim3(256), 0, st, a));
-  else
-    ESA_TIMED(esa_profile::kAttnBwdDq, st, hipLaunchKernelGGL((attn_dq_kernel<false>), dim3(qgrid), dim3(256), 0, st, a));
+  const unsigned eqgrid = (unsigned)groups_of(total_q) * (unsigned)((heads + kEdgeHeads - 1) / kEdgeHeads);
+  ESA_TIMED(esa_profile::kAttnBwdDqMasked, st, hipLaunchKernelGGL(edge_dq_kernel, dim3(eqgrid), dim3(256), 0, st, a));
   ESA_LAUNCH_CHECK();
   return ESA_OK;
 }

@@ -264,7 +264,7 @@ __global__ __launch_bounds__(256) ESA_WAVES_ATTR(ESA_DENSE_WAVES_FWD) void dense
     auto ops = [&](int buf, int j) {
       Ops o;
       o.kr = k_rows(buf, j);
-      vt_ones<kHalfRows>(sV[buf], 32 * j, sOnes, c16, grp, o.vt0, o.vt1);
+      tr_rows32<kHalfRows>(sV[buf], 32 * j, sOnes, c16, grp, o.vt0, o.vt1);
       return o;
     };
     // One key tile: the score MFMAs of all query tiles first, then each

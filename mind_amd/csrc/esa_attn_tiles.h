@@ -1,6 +1,6 @@
 // Tile constants and device helpers shared by the bf16 attention kernels
-// (the masked walks in esa_attn.hip, the segment-tiled dense kernels in
-// esa_attn_dense.hip): MFMA operand layouts, LDS tile strides, bf16 splits.
+// (the edge-mask walks in esa_attn.hip, the segment-tiled dense kernels in
+// esa_attn_dense.hip): MFMA operand layouts, LDS layouts, bf16 splits.
 #pragma once
 #include <climits>
 
@@ -159,20 +159,23 @@ DEVI bf16x8 tr_operand(const bf16* rows, int t0, int c16, int grp) {
   return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
-// A operands [V^T ; 1] of the two mfma32 P V products of the split-row tile
-// at token t0 (keys 0..15 and 16..31 of the tile), by transpose reads:
-// lane groups 0 and 2 (rows 0..15, K slots 0..7 and 8..15) read dims of four
-// keys per read, groups 1 and 3 (the ones rows) read the 4-element ones
-// array `ones`.
+// A operands of the two mfma32 products that sum over the 32 tokens of a
+// split-row tile at token t0 (K slots = tokens 0..15, then 16..31; A rows =
+// the 16 dims), by transpose reads.  Lane groups 0 and 2 (rows 0..15, K
+// slots 0..7 and 8..15) read dims of four tokens per read.  Groups 1 and 3
+// (rows 16..31) read the 4-element array `ones` when it is given (the ones
+// rows of [V^T ; 1], whose product is the softmax row sum), else the same
+// dims again (rows 16..31 duplicate rows 0..15).
 template <int HS>
-DEVI void vt_ones(const bf16* rows, int t0, const bf16* ones, int c16, int grp, bf16x8& vt0, bf16x8& vt1) {
+DEVI void tr_rows32(const bf16* rows, int t0, const bf16* ones, int c16, int grp, bf16x8& op0, bf16x8& op1) {
   const int q = c16 & 3;
-  const int step = (grp & 1) ? 0 : 8;   // bf16 per key in the read address
-  const bf16* p = (grp & 1) ? ones : rows + (q >> 1) * HS + (t0 + 8 * (grp >> 1) + (c16 >> 2)) * 8 + 4 * (q & 1);
+  const bool one = ones && (grp & 1);
+  const int step = one ? 0 : 8;   // bf16 per token in the read address
+  const bf16* p = one ? ones : rows + (q >> 1) * HS + (t0 + 8 * (grp >> 1) + (c16 >> 2)) * 8 + 4 * (q & 1);
   const bf16x4 v0 = lds_tr4(p), v1 = lds_tr4(p + 4 * step);
   const bf16x4 v2 = lds_tr4(p + 16 * step), v3 = lds_tr4(p + 20 * step);
-  vt0 = bf16x8{v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-  vt1 = bf16x8{v2[0], v2[1], v2[2], v2[3], v3[0], v3[1], v3[2], v3[3]};
+  op0 = bf16x8{v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+  op1 = bf16x8{v2[0], v2[1], v2[2], v2[3], v3[0], v3[1], v3[2], v3[3]};
 }
 
 DEVI f32x16 splat16(float x) {
