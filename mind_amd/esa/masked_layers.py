@@ -19,6 +19,11 @@ Backend ``xformers_or_torch_attn``:
   "hip"                 native packed path: every attention layer works on the
                         valid tokens only (edge counts per graph), the masked
                         layers apply the edge mask, PMA pools over valid tokens.
+                        ESA runs its encoder and the PMA's keys on the packed
+                        [T, D] tokens end to end (layer norms, projections and
+                        MLPs included), so no work is spent on padding; only the
+                        returned token embeddings are padded again (zeros at
+                        padding slots).
 """
 from __future__ import annotations
 
@@ -27,7 +32,7 @@ from torch import nn
 from torch.nn import functional as F
 
 from .attention import varlen_attention
-from .mha import PMA, SAB, _heads, pooled_attention
+from .mha import PMA, SAB, _heads, _uniform_cu, pooled_attention
 from .mha_flash_varlen import PMAFlashVarlen, SABFlashVarlen
 from .mlp_utils import GatedMLPMulti, SmallMLP
 from .norm_layers import LN
@@ -140,6 +145,57 @@ def _sab_valid_only(sab: SAB, X: torch.Tensor, tokens: PackedSets) -> torch.Tens
                            cu, cu, n, n)
     out = tokens.pad(out.reshape(-1, d)).to(q.dtype)
     return out + F.mish(mab.fc_o(out))
+
+
+def _packed_mab(mab, xq: torch.Tensor, xk: torch.Tensor, cu_q: torch.Tensor, cu_k: torch.Tensor, max_q: int,
+                max_k: int, mask_kwargs: dict) -> torch.Tensor:
+    """MAB (esa/mha.py:48-89, V = fc_v(K)) on packed rows: queries xq [Tq, D] and keys xk [Tk, D] grouped by
+    cu_q / cu_k -> [Tq, D]."""
+    q = mab.fc_q(xq)
+    v = mab.fc_v(xk)
+    k = mab.fc_k(xk)
+    h, d = mab.num_heads, q.shape[-1]
+    out = varlen_attention(_heads(q, h), _heads(k, h), _heads(v, h), cu_q, cu_k, max_q, max_k, **mask_kwargs)
+    out = out.reshape(-1, d).to(q.dtype)
+    return out + F.mish(mab.fc_o(out))
+
+
+def _sab_forward_packed(blk: "SABComplete", X: torch.Tensor, tokens: PackedSets) -> torch.Tensor:
+    """SABComplete.forward (pre-norm, esa/masked_layers.py:418-483) on packed tokens X [T, D]: the masked
+    layers (idx 1) apply the descriptor's mask, the unmasked ones (idx 0) attend over each graph's tokens."""
+    X = blk.norm(X)
+    mask_kwargs = tokens.kernel_mask(padded=False) if blk.idx == 1 else {}
+    cu, n = tokens.cu_seqlens, tokens.max_items
+    out_attn = _packed_mab(blk.sab.mab, X, X, cu, cu, n, n, mask_kwargs)
+    if out_attn.shape[-1] != X.shape[-1]:
+        X = blk.proj_1(X)
+    out = X + out_attn
+    if blk.use_mlp:
+        out_mlp = blk.mlp(blk.norm_mlp(out))
+        if out.shape[-1] == out_mlp.shape[-1]:
+            out = out_mlp + out
+    if blk.residual_dropout > 0:
+        out = F.dropout(out, p=blk.residual_dropout)
+    return out
+
+
+def _pma_forward_packed(blk: "PMAComplete", X: torch.Tensor, tokens: PackedSets) -> torch.Tensor:
+    """PMAComplete.forward (esa/masked_layers.py:583-610) with packed keys X [T, D] -> [B, k, D]: the seeds
+    of each graph attend over its tokens."""
+    X = blk.norm(X)
+    b, (k_seeds, d) = tokens.batch_size, blk.pma.S.shape[1:]
+    seeds = blk.pma.S.reshape(k_seeds, d).repeat(b, 1)
+    out = _packed_mab(blk.pma.mab, seeds, X, _uniform_cu(b, k_seeds, X.device), tokens.cu_seqlens, k_seeds,
+                      tokens.max_items, {}).reshape(b, k_seeds, d)
+    if k_seeds == tokens.max_items:   # the reference's residual when the seed count equals N
+        out = tokens.pad(X) + out
+    if blk.use_mlp:
+        out_mlp = blk.mlp(blk.norm_mlp(out))
+        if out.shape[-2] == out_mlp.shape[-2]:
+            out = out_mlp + out
+    if blk.residual_dropout > 0:
+        out = F.dropout(out, p=blk.residual_dropout)
+    return out
 
 
 class PMAComplete(nn.Module):
@@ -259,6 +315,8 @@ class ESA(nn.Module):
         build = get_adj_mask_from_edge_index_node if self.node_or_edge == "node" else get_adj_mask_from_edge_index_edge
         adj_mask = build(edge_index=edge_index, batch_mapping=batch_mapping, batch_size=X.shape[0],
                          max_items=num_max_items)
+        if self.xformers_or_torch_attn == "hip" and isinstance(adj_mask, PackedSets):
+            return self._forward_packed(X, edge_index, batch_mapping, num_max_items, adj_mask)
         enc, _, _, _, _ = self.encoder((X, edge_index, batch_mapping, num_max_items, adj_mask))
         if hasattr(self, "dim_pma") and self.dim_hidden[0] != self.dim_pma:
             X = self.out_proj(X)
@@ -269,3 +327,22 @@ class ESA(nn.Module):
             out = out.mean(dim=1)
             return F.mish(self.decoder_linear(out)), node_embeddings_before_pma
         return F.mish(self.decoder_linear(enc)), enc
+
+    def _forward_packed(self, X, edge_index, batch_mapping, num_max_items, tokens: PackedSets):
+        """The "hip" forward: encoder and PMA keys on the packed tokens; the decoder's later layers act on
+        the [B, k, D] seeds as in the padded forward."""
+        xp = tokens.unpad(X)
+        h = xp
+        for blk in self.encoder:
+            h = _sab_forward_packed(blk, h, tokens)
+        if hasattr(self, "dim_pma") and self.dim_hidden[0] != self.dim_pma:
+            xp = self.out_proj(xp)
+        enc = h + xp
+        node_embeddings_before_pma = tokens.pad(enc)
+        if hasattr(self, "decoder"):
+            out = _pma_forward_packed(self.decoder[0], enc, tokens)
+            for blk in list(self.decoder)[1:]:
+                out, _, _, _, _ = blk((out, edge_index, batch_mapping, num_max_items, tokens))
+            out = out.mean(dim=1)
+            return F.mish(self.decoder_linear(out)), node_embeddings_before_pma
+        return F.mish(self.decoder_linear(node_embeddings_before_pma)), node_embeddings_before_pma

@@ -180,6 +180,49 @@ def test_pma_dense_and_pooled(device):
     assert_f32_close(got_f, ref, "PMAFlashVarlen padded fallback")
 
 
+def test_esa_hip_packed_backward(device):
+    """The "hip" ESA runs packed end to end: gradients of the input (valid rows) and of parameters of every
+    stage against autograd through the oracle; the returned embeddings are zero at padding slots."""
+    gb, n = _batch(7, num_graphs=6)
+    torch.manual_seed(7)
+    model = ML.ESA(num_outputs=2, dim_output=D, dim_hidden=[D, D, D], num_heads=[H, H, H], layer_types="MSP",
+                   xformers_or_torch_attn="hip", use_mlps=True, mlp_hidden_size=2 * D, num_mlp_layers=2,
+                   mlp_type="standard").to(device)
+    X, valid = _padded_tokens(gb, n, 17)
+    xd = X.to(device).requires_grad_(True)
+    ei = torch.as_tensor(gb.edge_index).to(device)
+    bm = torch.as_tensor(gb.batch).to(device)
+    g_emb, enc = model(xd, ei, bm, n)
+    gg = torch.randn(g_emb.shape, generator=torch.Generator().manual_seed(1))
+    ge = torch.randn(enc.shape, generator=torch.Generator().manual_seed(2)) * valid[..., None]
+    ((g_emb * gg.to(device)).sum() + (enc * ge.to(device)).sum()).backward()
+    assert float(enc.detach()[~valid.to(device)].abs().max()) == 0.0
+
+    sd = {k: v.detach().cpu().double().requires_grad_(True) for k, v in model.state_dict().items()}
+    cu = gb.cu_seqlens
+    src, dst = gb.edge_index[0], gb.edge_index[1]
+    xp = X.double()[valid].clone().requires_grad_(True)
+    h = OMod.sab_complete(sd, "encoder.0.", xp, H, lambda s, p, x: OMod.mab_packed(s, p, x, x, cu, cu, H, src, dst), 2)
+    h = OMod.sab_complete(sd, "encoder.1.", h, H, lambda s, p, x: OMod.mab_packed(s, p, x, x, cu, cu, H), 2)
+    enc_ref = h + xp
+    hn = OMod.layer_norm(sd, "decoder.0.norm.ln.", enc_ref)
+    S = OMod._p(sd, "decoder.0.pma.", "S").reshape(2, D).repeat(gb.num_graphs, 1)
+    pooled = OMod.mab_packed(sd, "decoder.0.pma.mab.", S, hn, np.arange(gb.num_graphs + 1) * 2, cu, H)
+    pooled = pooled + OMod.mlp_standard(sd, "decoder.0.mlp.", OMod.layer_norm(sd, "decoder.0.norm_mlp.ln.", pooled),
+                                        2)
+    pooled = pooled.reshape(gb.num_graphs, 2, D).mean(1)
+    g_ref = OMod.mish(OMod.linear(sd, "decoder_linear.", pooled))
+    ((g_ref * gg.double()).sum() + (enc_ref * ge.double()[valid]).sum()).backward()
+    assert_f32_close(g_emb.detach().cpu(), g_ref.detach(), "ESA graph embedding")
+    assert_f32_close(xd.grad.cpu()[valid], xp.grad, "dX (valid rows)")
+    params = dict(model.named_parameters())
+    for name in ("encoder.0.sab.mab.fc_q.weight", "encoder.1.mlp.mlp.0.weight", "decoder.0.pma.S",
+                 "decoder.0.pma.mab.fc_k.weight", "decoder_linear.weight"):
+        if name not in params:
+            continue
+        assert_f32_close(params[name].grad.cpu().reshape(sd[name].grad.shape), sd[name].grad, f"d {name}")
+
+
 @pytest.mark.parametrize("backend", ["hip", "xformers"])
 def test_esa_block_config0_shape(device, backend):
     """M (masked), S, P(1 seed) with pre-norm and standard MLPs on a small-molecule batch."""
