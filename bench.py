@@ -486,6 +486,9 @@ def bench_gather(args):
     del a, b
     torch.cuda.empty_cache()
 
+    fused = bench_fused_projection(x_dtype=torch.float32, src=src, dst=dst, steps=max(3, args.steps // 2),
+                                   warmup=2, seed=args.seed)
+
     f32 = results["f32"]
     dom = max(("edge_gather", "segment_sum"), key=lambda n: f32["kernels"][n]["avg_us"])
     achieved = f32["kernels"][dom]["achieved_gbs"]
@@ -513,6 +516,7 @@ def bench_gather(args):
         },
         "csr_build_ms": csr_ms,
         "reference_copy_gbs": copy_gbs,
+        "fused_projection": fused,
         "f32": f32,
         "bf16": results["bf16"],
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
@@ -521,6 +525,52 @@ def bench_gather(args):
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline_gather(src.cpu().numpy(), dst.cpu().numpy(), args.seed, 1 << 18)
     print(json.dumps(result), flush=True)
+
+
+def bench_fused_projection(x_dtype, src, dst, steps: int, warmup: int, seed: int) -> dict:
+    """The edge MLP's first Linear(2F -> F) over [x_src || x_dst] at configuration-3 sizes: the reference's form
+    (gather the [E, 2F] edge tokens, then one [E, 2F] x [2F, F] GEMM) against the fused form (one node-level
+    [N, F] x [F, 2F] GEMM, then the gather-add kernel writes out[e] = P[src e] + Q[dst e] + b)."""
+    import torch
+
+    from mind_amd.edges import _gather_raw, gather_add
+
+    dev = src.device
+    g = torch.Generator(device=dev).manual_seed(seed)
+    n, f, e = GATHER_N, GATHER_F, src.numel()
+    x = torch.randn(n, f, device=dev, generator=g).to(x_dtype)
+    w = (torch.randn(f, 2 * f, device=dev, generator=g) / (2 * f) ** 0.5).to(x_dtype)
+    b = torch.randn(f, device=dev, generator=g).to(x_dtype)
+    w2 = torch.cat((w[:, :f], w[:, f:]), 0)
+    out = torch.empty(e, f, device=dev, dtype=x_dtype)
+    pq = torch.empty(n, 2 * f, device=dev, dtype=x_dtype)
+
+    def fused():
+        torch.mm(x, w2.t(), out=pq)
+        gather_add(pq[:, :f], pq[:, f:], src, dst, b, out=out)
+
+    ms_f, _, kern_f = timed(fused, steps, warmup)
+    fused_out = out[:4096].clone()
+    del pq
+    h = torch.empty(e, 2 * f, device=dev, dtype=x_dtype)
+
+    def unfused():
+        _gather_raw(x, src, dst, h)
+        torch.addmm(b, h, w.t(), out=out)
+
+    ms_u, _, _ = timed(unfused, steps, warmup)
+    diff = float((out[:4096] - fused_out).abs().max() / out[:4096].abs().max())
+    del h, out, x
+    torch.cuda.empty_cache()
+    s = torch.tensor([], dtype=x_dtype).element_size()
+    ga = kern_f.get("edge_gather_add", {})
+    algo = e * f * s + 2 * n * f * s + 8 * e   # write out once, read each node row of P and Q once, indices
+    return {"dtype": str(x_dtype).replace("torch.", ""), "fused_ms": ms_f, "unfused_ms": ms_u,
+            "speedup": ms_u / ms_f, "gather_add_us": ga.get("avg_us"),
+            "gather_add_algorithmic_gbs": algo / (ga["avg_us"] * 1e-6) / 1e9 if ga else None,
+            "max_rel_diff_fused_vs_unfused": diff,
+            "what": "Linear(2F->F) over [x_src || x_dst], F=256: fused = node GEMM + gather-add; "
+                    "unfused = gather [E, 2F] + [E, 2F] x [2F, F] GEMM (the reference's form)"}
 
 
 def _edge_tokens(gb, types, emb, proj, device):

@@ -129,6 +129,21 @@ ESA_API int esa_edge_gather(const void* x, const int* src, const int* dst,
                     void* out, void* stream);
 
 /* ------------------------------------------------------------------------ */
+/* Fused edge-token projection: out[e] = a[src[e]] + b[dst[e]] + bias, out   */
+/* is [E, F] (contiguous), a and b are node rows lda / ldb elements apart,  */
+/* bias is [F] or NULL.  With a = x W_s^T and b = x W_d^T (node-level GEMMs  */
+/* of the two input halves of a Linear(2F', F) weight W = [W_s | W_d]) this  */
+/* is Linear(cat(x[src], x[dst])) (core/pretraining_model.py:153-198,        */
+/* esa/mlp_utils.py:28-32) without the [E, 2F'] intermediate.  Sums in fp32  */
+/* in the order (a + b) + bias, rounded once; dtype ESA_F32 or ESA_BF16;     */
+/* a node id outside [0, num_nodes) contributes zeros.                       */
+/* ------------------------------------------------------------------------ */
+ESA_API int esa_edge_gather_add(const void* a, int64_t lda, const void* b, int64_t ldb,
+                        const void* bias, const int* src, const int* dst,
+                        int64_t num_edges, int num_nodes, int features, int dtype,
+                        void* out, void* stream);
+
+/* ------------------------------------------------------------------------ */
 /* CSR construction by a key array (e.g. dst): indptr[N+1] and perm[E], perm */
 /* listing edge ids grouped by key in ascending edge order (a stable sort).  */
 /* The layout torch_scatter's segment_*_csr consumes                        */
@@ -167,7 +182,7 @@ ESA_API int esa_edge_gather_bwd(const void* g, const int* src_perm,
 /* launch count per kernel id (capacity >= ESA_PROFILE_KERNELS) and clears   */
 /* the record.  Not for concurrent use from several threads.                 */
 /* ------------------------------------------------------------------------ */
-#define ESA_PROFILE_KERNELS 13
+#define ESA_PROFILE_KERNELS 14
 ESA_API int esa_profile_enable(int on);
 ESA_API int esa_profile_collect(float* total_ms, int* launches, int capacity);
 ESA_API const char* esa_profile_kernel_name(int kernel);

@@ -117,6 +117,174 @@ __global__ void edge_gather_scalar_kernel(const T* __restrict__ x, const int* __
   }
 }
 
+// ------------------------------------------------------------------ gather-add
+// out_e = a[src_e] + b[dst_e] + bias: the edge-token Linear of
+// core/pretraining_model.py:153-198 (Linear over [x_src || x_dst],
+// esa/mlp_utils.py:28-32) with its weight split by input half, so a = x W_s^T
+// and b = x W_d^T are node-level GEMM outputs (rows lda / ldb elements apart)
+// and the 2F-wide token matrix is never formed.  Sums in fp32 in the order
+// (a + b) + bias, rounded once to the output type.  A node id outside
+// [0, num_nodes) contributes zeros.
+//
+// A lane owns one 16-byte column chunk (lanes per edge L = min(C, 64), C =
+// chunks per row; P = C / L chunks per lane), a wave step covers U * 64 / L
+// edges with all their loads in flight before the adds, and each wave walks
+// a contiguous edge range (XCD-contiguous, as the row gather).
+
+template <typename T>
+DEVI float4 chunk_f32(u32x4 v, int k);   // elements 4k..4k+3 of a 16-byte chunk as fp32
+template <>
+DEVI float4 chunk_f32<float>(u32x4 v, int k) {
+  (void)k;
+  return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+}
+template <>
+DEVI float4 chunk_f32<bf16>(u32x4 v, int k) {
+  const uint32_t lo = k == 0 ? v.x : v.z, hi = k == 0 ? v.y : v.w;
+  return make_float4(__uint_as_float(lo << 16), __uint_as_float(lo & 0xFFFF0000u), __uint_as_float(hi << 16),
+                     __uint_as_float(hi & 0xFFFF0000u));
+}
+
+template <typename T>
+DEVI u32x4 add3_chunk(u32x4 x, u32x4 y, u32x4 z) {
+  if constexpr (sizeof(T) == 4) {
+    return u32x4{__float_as_uint((__uint_as_float(x.x) + __uint_as_float(y.x)) + __uint_as_float(z.x)),
+                 __float_as_uint((__uint_as_float(x.y) + __uint_as_float(y.y)) + __uint_as_float(z.y)),
+                 __float_as_uint((__uint_as_float(x.z) + __uint_as_float(y.z)) + __uint_as_float(z.z)),
+                 __float_as_uint((__uint_as_float(x.w) + __uint_as_float(y.w)) + __uint_as_float(z.w))};
+  } else {
+    uint32_t w[4];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const float4 a = chunk_f32<bf16>(x, k), b = chunk_f32<bf16>(y, k), c = chunk_f32<bf16>(z, k);
+      const bf16 r0 = (bf16)((a.x + b.x) + c.x), r1 = (bf16)((a.y + b.y) + c.y);
+      const bf16 r2 = (bf16)((a.z + b.z) + c.z), r3 = (bf16)((a.w + b.w) + c.w);
+      w[2 * k] = (uint32_t)__builtin_bit_cast(uint16_t, r0) | ((uint32_t)__builtin_bit_cast(uint16_t, r1) << 16);
+      w[2 * k + 1] = (uint32_t)__builtin_bit_cast(uint16_t, r2) | ((uint32_t)__builtin_bit_cast(uint16_t, r3) << 16);
+    }
+    return u32x4{w[0], w[1], w[2], w[3]};
+  }
+}
+
+template <typename T, int P>
+__global__ __launch_bounds__(256) void edge_gather_add_kernel(const u32x4* __restrict__ a, long lda16,
+                                                              const u32x4* __restrict__ b, long ldb16,
+                                                              const u32x4* __restrict__ bias,
+                                                              const int* __restrict__ src,
+                                                              const int* __restrict__ dst, long num_edges,
+                                                              int num_nodes, int lanes_per_edge, long steps_per_wave,
+                                                              int blocks_per_xcd, u32x4* __restrict__ out) {
+  constexpr int U = 8 / P;   // edges per lane per step (8 chunk pairs in flight)
+  const int lane = threadIdx.x & 63;
+  const int lb = (int)(blockIdx.x & 7) * blocks_per_xcd + (int)(blockIdx.x >> 3);
+  const long wave = (long)lb * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int L = lanes_per_edge, R = 64 / L;        // edges per wave row
+  const int j = lane / L, c = lane - j * L;        // edge slot, chunk
+  const int C = L * P;                             // chunks per output row
+  u32x4 bz[P];
+#pragma unroll
+  for (int p = 0; p < P; ++p) bz[p] = bias ? bias[c + L * p] : u32x4{0u, 0u, 0u, 0u};
+  const long per_step = (long)U * R;
+  const long e_beg = wave * steps_per_wave * per_step;
+  const long e_end = min(e_beg + steps_per_wave * per_step, num_edges);
+  for (long e0 = e_beg; e0 < e_end; e0 += per_step) {
+    u32x4 va[U][P], vb[U][P];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const long e = e0 + (long)u * R + j;
+      const long ec = min(e, num_edges - 1);
+      const int s = src[ec], d = dst[ec];
+      const bool sok = (unsigned)s < (unsigned)num_nodes, dok = (unsigned)d < (unsigned)num_nodes;
+#pragma unroll
+      for (int p = 0; p < P; ++p) {
+        va[u][p] = sok ? a[(size_t)s * lda16 + c + L * p] : u32x4{0u, 0u, 0u, 0u};
+        vb[u][p] = dok ? b[(size_t)d * ldb16 + c + L * p] : u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const long e = e0 + (long)u * R + j;
+      if (e < e_end) {
+#pragma unroll
+        for (int p = 0; p < P; ++p)
+          __builtin_nontemporal_store(add3_chunk<T>(va[u][p], vb[u][p], bz[p]), &out[(size_t)e * C + c + L * p]);
+      }
+    }
+  }
+}
+
+// Whole-row variant for rows of a multiple of 64 chunks (one wave per output
+// row, P chunks per lane): a step's U = 16 / P edge ids arrive with one
+// vector load (lanes 0..U-1 src, 32..32+U-1 dst) and are broadcast with
+// readlane, so the row bases are wave-uniform and 16 chunk loads per lane
+// are in flight before the adds.
+#ifndef ESA_GADD_ROWS
+#define ESA_GADD_ROWS 1
+#endif
+template <typename T, int P>
+__global__ __launch_bounds__(256) void edge_gather_add_rows_kernel(const char* __restrict__ a, long lda_bytes,
+                                                                   const char* __restrict__ b, long ldb_bytes,
+                                                                   const u32x4* __restrict__ bias,
+                                                                   const int* __restrict__ src,
+                                                                   const int* __restrict__ dst, long num_edges,
+                                                                   int num_nodes, int edges_per_wave,
+                                                                   int blocks_per_xcd, u32x4* __restrict__ out) {
+  constexpr int U = 8 / P;
+  constexpr int C = 64 * P;
+  const int lane = threadIdx.x & 63;
+  const int lb = (int)(blockIdx.x & 7) * blocks_per_xcd + (int)(blockIdx.x >> 3);
+  const long wave = (long)lb * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const long e_beg = wave * edges_per_wave;
+  const long e_end = min(e_beg + (long)edges_per_wave, num_edges);
+  u32x4 bz[P];
+#pragma unroll
+  for (int p = 0; p < P; ++p) bz[p] = bias ? bias[lane + 64 * p] : u32x4{0u, 0u, 0u, 0u};
+  const u32x4 zero = {0u, 0u, 0u, 0u};
+  for (long e0 = e_beg; e0 < e_end; e0 += U) {
+    const long ei = min(e0 + (lane & 31), num_edges - 1);
+    const int idx = lane < 32 ? src[ei] : dst[ei];
+    u32x4 va[U][P], vb[U][P];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int s = __builtin_amdgcn_readlane(idx, u), d = __builtin_amdgcn_readlane(idx, 32 + u);
+      const u32x4* ra = reinterpret_cast<const u32x4*>(a + (size_t)(unsigned)s * lda_bytes);
+      const u32x4* rb = reinterpret_cast<const u32x4*>(b + (size_t)(unsigned)d * ldb_bytes);
+      const bool sok = (unsigned)s < (unsigned)num_nodes, dok = (unsigned)d < (unsigned)num_nodes;
+#pragma unroll
+      for (int p = 0; p < P; ++p) {
+        va[u][p] = sok ? ra[lane + 64 * p] : zero;
+        vb[u][p] = dok ? rb[lane + 64 * p] : zero;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (e0 + u < e_end) {
+#pragma unroll
+        for (int p = 0; p < P; ++p)
+          __builtin_nontemporal_store(add3_chunk<T>(va[u][p], vb[u][p], bz[p]), &out[(size_t)(e0 + u) * C + lane + 64 * p]);
+      }
+    }
+  }
+}
+
+// Element-wise fallback for rows or strides that are not 16-byte multiples.
+template <typename T>
+__global__ void edge_gather_add_scalar_kernel(const T* __restrict__ a, long lda, const T* __restrict__ b, long ldb,
+                                              const T* __restrict__ bias, const int* __restrict__ src,
+                                              const int* __restrict__ dst, long num_edges, int num_nodes,
+                                              int features, T* __restrict__ out) {
+  const long n = num_edges * features;
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) {
+    const long e = i / features;
+    const int f = (int)(i - e * features);
+    const int s = src[e], d = dst[e];
+    const float x = (unsigned)s < (unsigned)num_nodes ? (float)a[(size_t)s * lda + f] : 0.f;
+    const float y = (unsigned)d < (unsigned)num_nodes ? (float)b[(size_t)d * ldb + f] : 0.f;
+    const float z = bias ? (float)bias[f] : 0.f;
+    out[i] = (T)((x + y) + z);
+  }
+}
+
 // ------------------------------------------------------------------ CSR
 
 __global__ void zero_int_kernel(int* __restrict__ p, long n) {
@@ -609,6 +777,86 @@ int esa_edge_gather(const void* x, const int* src, const int* dst, int64_t num_e
   } else {
     hipLaunchKernelGGL(edge_gather_scalar_kernel<bf16>, dim3(grid_for(num_edges * 2 * features, 256)), dim3(256), 0,
                        st, static_cast<const bf16*>(x), src, dst, (long)num_edges, num_nodes, features,
+                       static_cast<bf16*>(out));
+  }
+  ESA_LAUNCH_CHECK();
+  return ESA_OK;
+}
+
+int esa_edge_gather_add(const void* a, int64_t lda, const void* b, int64_t ldb, const void* bias, const int* src,
+                        const int* dst, int64_t num_edges, int num_nodes, int features, int dtype, void* out,
+                        void* stream) {
+  if (num_edges < 0 || num_nodes < 0 || features < 1 || lda < features || ldb < features) return ESA_ERR_SHAPE;
+  if (dtype != ESA_F32 && dtype != ESA_BF16) return ESA_ERR_DTYPE;
+  if (num_edges == 0) return ESA_OK;
+  if (!a || !b || !src || !dst || !out) return ESA_ERR_NULL;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int es = dtype == ESA_F32 ? 4 : 2;
+  const long row_bytes = (long)features * es;
+  const int C = (int)(row_bytes / 16);
+  const bool vec_ok = row_bytes % 16 == 0 && (lda * es) % 16 == 0 && (ldb * es) % 16 == 0 && !misaligned16(a) &&
+                      !misaligned16(b) && !misaligned16(out) && (!bias || !misaligned16(bias));
+  const bool pow2 = C > 0 && (C & (C - 1)) == 0;
+  const int P = C > 64 ? C / 64 : 1;
+  if (ESA_GADD_ROWS && vec_ok && C % 64 == 0 && (P == 1 || P == 2 || P == 4 || P == 8)) {
+    const int epw = 32;
+    const long waves = (num_edges + epw - 1) / epw;
+    const long blocks8 = ((waves + 3) / 4 + 7) / 8 * 8;
+    const int per_xcd = (int)(blocks8 / 8);
+    auto go = [&](auto kern) {
+      ESA_TIMED(esa_profile::kEdgeGatherAdd, st,
+                hipLaunchKernelGGL(kern, dim3((unsigned)blocks8), dim3(256), 0, st, static_cast<const char*>(a),
+                                   (long)(lda * es), static_cast<const char*>(b), (long)(ldb * es),
+                                   static_cast<const u32x4*>(bias), src, dst, (long)num_edges, num_nodes, epw,
+                                   per_xcd, static_cast<u32x4*>(out)));
+    };
+    if (dtype == ESA_F32) {
+      if (P == 1) go(edge_gather_add_rows_kernel<float, 1>);
+      else if (P == 2) go(edge_gather_add_rows_kernel<float, 2>);
+      else if (P == 4) go(edge_gather_add_rows_kernel<float, 4>);
+      else go(edge_gather_add_rows_kernel<float, 8>);
+    } else {
+      if (P == 1) go(edge_gather_add_rows_kernel<bf16, 1>);
+      else if (P == 2) go(edge_gather_add_rows_kernel<bf16, 2>);
+      else if (P == 4) go(edge_gather_add_rows_kernel<bf16, 4>);
+      else go(edge_gather_add_rows_kernel<bf16, 8>);
+    }
+  } else if (vec_ok && ((C <= 64 && pow2) || (C % 64 == 0 && (P == 2 || P == 4 || P == 8)))) {
+    const int L = C < 64 ? C : 64;
+    const long per_step = (long)(8 / P) * (64 / L);
+    const long steps = (num_edges + per_step - 1) / per_step;
+    const long steps_per_wave = 4;
+    const long waves = (steps + steps_per_wave - 1) / steps_per_wave;
+    const long blocks8 = ((waves + 3) / 4 + 7) / 8 * 8;
+    const int per_xcd = (int)(blocks8 / 8);
+    const long lda16 = lda * es / 16, ldb16 = ldb * es / 16;
+    auto go = [&](auto kern) {
+      ESA_TIMED(esa_profile::kEdgeGatherAdd, st,
+                hipLaunchKernelGGL(kern, dim3((unsigned)blocks8), dim3(256), 0, st, static_cast<const u32x4*>(a),
+                                   lda16, static_cast<const u32x4*>(b), ldb16, static_cast<const u32x4*>(bias), src,
+                                   dst, (long)num_edges, num_nodes, L, steps_per_wave, per_xcd,
+                                   static_cast<u32x4*>(out)));
+    };
+    if (dtype == ESA_F32) {
+      if (P == 1) go(edge_gather_add_kernel<float, 1>);
+      else if (P == 2) go(edge_gather_add_kernel<float, 2>);
+      else if (P == 4) go(edge_gather_add_kernel<float, 4>);
+      else go(edge_gather_add_kernel<float, 8>);
+    } else {
+      if (P == 1) go(edge_gather_add_kernel<bf16, 1>);
+      else if (P == 2) go(edge_gather_add_kernel<bf16, 2>);
+      else if (P == 4) go(edge_gather_add_kernel<bf16, 4>);
+      else go(edge_gather_add_kernel<bf16, 8>);
+    }
+  } else if (dtype == ESA_F32) {
+    hipLaunchKernelGGL(edge_gather_add_scalar_kernel<float>, dim3(grid_for(num_edges * features, 256)), dim3(256), 0,
+                       st, static_cast<const float*>(a), (long)lda, static_cast<const float*>(b), (long)ldb,
+                       static_cast<const float*>(bias), src, dst, (long)num_edges, num_nodes, features,
+                       static_cast<float*>(out));
+  } else {
+    hipLaunchKernelGGL(edge_gather_add_scalar_kernel<bf16>, dim3(grid_for(num_edges * features, 256)), dim3(256), 0,
+                       st, static_cast<const bf16*>(a), (long)lda, static_cast<const bf16*>(b), (long)ldb,
+                       static_cast<const bf16*>(bias), src, dst, (long)num_edges, num_nodes, features,
                        static_cast<bf16*>(out));
   }
   ESA_LAUNCH_CHECK();

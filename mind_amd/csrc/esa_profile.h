@@ -20,6 +20,7 @@ enum Kernel : int {
   kGraphFwd,        // node-mode (CSR adjacency) attention
   kGraphDq,
   kGraphDkdv,
+  kEdgeGatherAdd,   // fused edge-token projection
   kNumKernels
 };
 

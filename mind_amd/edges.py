@@ -142,3 +142,112 @@ def edge_gather(x: torch.Tensor, src: torch.Tensor, dst: torch.Tensor, src_csr: 
     if src.shape != dst.shape or src.dim() != 1:
         raise ValueError("src and dst must be 1-D and of equal length")
     return _EdgeGather.apply(x, src, dst, src_csr, dst_csr)
+
+
+# ---------------------------------------------------------------- fused edge-token projection
+
+def gather_add(a: torch.Tensor, b: torch.Tensor, src: torch.Tensor, dst: torch.Tensor,
+               bias: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """out[e] = a[src[e]] + b[dst[e]] + bias ([E, F], dtype of a), fp32 sums in that order, rounded once.
+
+    a and b are [N, F] with unit column stride (row strides may differ, e.g. the two column halves of one
+    [N, 2F] GEMM output).  Node ids outside [0, N) contribute zeros.
+    """
+    _lib.require_gpu(a, b, src, dst, bias)
+    if a.dim() != 2 or b.shape != a.shape:
+        raise ValueError("a and b must be [N, F] of equal shape")
+    if a.dtype != b.dtype or (bias is not None and bias.dtype != a.dtype):
+        raise TypeError("a, b and bias must share one dtype")
+    for t, name in ((a, "a"), (b, "b")):
+        if t.stride(1) != 1:
+            raise ValueError(f"{name} needs unit column stride")
+    src = _as_index(src, "src")
+    dst = _as_index(dst, "dst")
+    if bias is not None:
+        bias = bias.contiguous()
+    n, f = a.shape
+    e = src.numel()
+    out = _output(out, (e, f), a)
+    rc = _lib.load().esa_edge_gather_add(a.data_ptr(), a.stride(0), b.data_ptr(), b.stride(0), _lib.ptr(bias),
+                                         src.data_ptr(), dst.data_ptr(), e, n, f, _dtype_code(a), out.data_ptr(),
+                                         _lib.stream_of(a))
+    _lib.check(rc, "esa_edge_gather_add")
+    return out
+
+
+class _EdgeTokenLinear(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, weight, bias, src, dst, src_csr, dst_csr):
+        n, f = x.shape
+        d = weight.shape[0]
+        w2 = torch.cat((weight[:, :f], weight[:, f:]), 0)   # [W_s ; W_d], [2D, F]
+        pq = x @ w2.t()                                       # node-level projections [N, 2D]
+        out = gather_add(pq[:, :d], pq[:, d:], src, dst, bias)
+        ctx.save_for_backward(x, w2, src, dst)
+        ctx.csrs = (src_csr, dst_csr)
+        ctx.has_bias = bias is not None
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        x, w2, src, dst = ctx.saved_tensors
+        src_csr, dst_csr = ctx.csrs
+        n, f = x.shape
+        d = w2.shape[0] // 2
+        g = g.contiguous()
+        if src_csr is None:
+            src_csr = CSR.build(src, n)
+        if dst_csr is None:
+            dst_csr = CSR.build(dst, n)
+        # d(a[src] + b[dst]) / d(a, b): per-node sums of the edge gradients, in ascending edge order
+        dpq = torch.cat((segment_sum_csr(g, src_csr.indptr, src_csr.perm),
+                         segment_sum_csr(g, dst_csr.indptr, dst_csr.perm)), 1)   # [N, 2D]
+        dx = dpq @ w2 if ctx.needs_input_grad[0] else None
+        dweight = None
+        if ctx.needs_input_grad[1]:
+            dw2 = dpq.t() @ x                                  # [2D, F]
+            dweight = torch.cat((dw2[:d], dw2[d:]), 1)         # [D, 2F]
+        dbias = g.sum(0) if ctx.has_bias and ctx.needs_input_grad[2] else None
+        return dx, dweight, dbias, None, None, None, None
+
+
+def edge_token_linear(x: torch.Tensor, src: torch.Tensor, dst: torch.Tensor, weight: torch.Tensor,
+                      bias: torch.Tensor | None = None, src_csr: CSR | None = None,
+                      dst_csr: CSR | None = None) -> torch.Tensor:
+    """``F.linear(torch.cat((x[src], x[dst]), 1), weight, bias)`` without the [E, 2F] edge tokens.
+
+    The Linear over concatenated endpoint features (core/pretraining_model.py:153-198, the first layer of
+    the edge MLP, esa/mlp_utils.py:28-32) splits by input half, W = [W_s | W_d]: one node-level GEMM
+    x [W_s ; W_d]^T gives both halves' projections, and the gather-add kernel writes
+    out[e] = (x W_s^T)[src e] + (x W_d^T)[dst e] + bias.  The backward sums the edge gradients per node
+    through two CSRs (deterministic) and finishes with GEMMs.  Computes in the dtype of x (float32 or
+    bfloat16); weight and bias must share it.  Mathematically equal to the reference; results differ
+    from it only by summation order.
+    """
+    if x.dim() != 2:
+        raise ValueError("x must be [N, F]")
+    if weight.dim() != 2 or weight.shape[1] != 2 * x.shape[1]:
+        raise ValueError("weight must be [D, 2F]")
+    if weight.dtype != x.dtype or (bias is not None and bias.dtype != x.dtype):
+        raise TypeError("x, weight and bias must share one dtype")
+    src = _as_index(src, "src")
+    dst = _as_index(dst, "dst")
+    if src.shape != dst.shape or src.dim() != 1:
+        raise ValueError("src and dst must be 1-D and of equal length")
+    return _EdgeTokenLinear.apply(x, weight, bias, src, dst, src_csr, dst_csr)
+
+
+class EdgeTokenLinear(torch.nn.Module):
+    """Drop-in for the ``nn.Linear(2F, D)`` applied to ``torch.cat((x[src], x[dst]), 1)``: same parameter
+    names and shapes (a reference state_dict loads), forward(x, src, dst) via ``edge_token_linear``."""
+
+    def __init__(self, in_features: int, out_features: int, bias: bool = True):
+        super().__init__()
+        lin = torch.nn.Linear(2 * in_features, out_features, bias=bias)
+        self.weight = lin.weight
+        self.bias = lin.bias
+        self.in_features, self.out_features = in_features, out_features
+
+    def forward(self, x: torch.Tensor, src: torch.Tensor, dst: torch.Tensor, src_csr: CSR | None = None,
+                dst_csr: CSR | None = None) -> torch.Tensor:
+        return edge_token_linear(x, src, dst, self.weight, self.bias, src_csr, dst_csr)

@@ -9,6 +9,14 @@ def edge_gather(x: np.ndarray, src: np.ndarray, dst: np.ndarray) -> np.ndarray:
     return np.concatenate([x[src], x[dst]], axis=1)
 
 
+def edge_token_linear(x: np.ndarray, src: np.ndarray, dst: np.ndarray, weight: np.ndarray,
+                      bias: np.ndarray | None = None) -> np.ndarray:
+    """Linear over the edge tokens: edge_gather(x, src, dst) @ weight^T + bias, in float64 —
+    core/pretraining_model.py:153-198 with the MLP's first Linear (esa/mlp_utils.py:28-32)."""
+    h = edge_gather(np.asarray(x, np.float64), src, dst) @ np.asarray(weight, np.float64).T
+    return h if bias is None else h + np.asarray(bias, np.float64)
+
+
 def csr_build(keys: np.ndarray, num_nodes: int) -> tuple[np.ndarray, np.ndarray]:
     """indptr [N+1] and perm [E] (edge ids grouped by key, ascending id within a key).
 

@@ -5,6 +5,7 @@ import torch
 
 from mind_amd import edges, generators
 from oracle import edges as OE
+from tests._util import assert_bf16_close, assert_f32_close, grad_scale
 
 pytestmark = pytest.mark.gpu
 
@@ -147,3 +148,89 @@ def test_config3_shape_properties(device):
     deg = torch.diff(csr.indptr).float()
     assert torch.equal(agg, xi * deg[:, None])
     assert torch.equal(h[:, :256], x[s.long()])
+
+
+# ---------------------------------------------------------------- fused edge-token projection
+
+def _bits(t):
+    return t.view(torch.int16 if t.dtype == torch.bfloat16 else torch.int32)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("features", [4, 8, 64, 128, 256, 512, 1024, 6])
+def test_gather_add_bit_exact(device, dtype, features):
+    # a and b are the two column halves of one [N, 2F] projection (row stride 2F); every vector layout
+    # (16, 32, 64 lanes per edge, 2/4/8 chunks per lane) and the element-wise fallback (F = 6)
+    n, e = 700, 3000
+    src, dst = _graph(2, n, e)
+    src, dst = src.copy(), dst.copy()
+    src[::97] = n + 5          # out-of-range ids contribute zeros
+    dst[::89] = -1
+    g = torch.Generator().manual_seed(features)
+    pq = torch.randn(n, 2 * features, generator=g).to(dtype)
+    bias = torch.randn(features, generator=g).to(dtype)
+    pqd = pq.to(device)
+    out = edges.gather_add(pqd[:, :features], pqd[:, features:], torch.as_tensor(src).to(device),
+                           torch.as_tensor(dst).to(device), bias.to(device)).cpu()
+    a, b = pq[:, :features].float(), pq[:, features:].float()
+    zero = torch.zeros(1, features)
+    sa = torch.as_tensor(src).long()
+    da = torch.as_tensor(dst).long()
+    ra = torch.where(((sa >= 0) & (sa < n))[:, None], a[sa.clamp(0, n - 1)], zero)
+    rb = torch.where(((da >= 0) & (da < n))[:, None], b[da.clamp(0, n - 1)], zero)
+    ref = ((ra + rb) + bias.float()).to(dtype)   # fp32, (a + b) + bias, one rounding
+    assert torch.equal(_bits(out), _bits(ref))
+
+
+def test_gather_add_without_bias_and_empty(device):
+    a = torch.randn(10, 16, device=device)
+    src = torch.tensor([3, 9, 0], dtype=torch.int32, device=device)
+    dst = torch.tensor([1, 1, 2], dtype=torch.int32, device=device)
+    out = edges.gather_add(a, a, src, dst)
+    assert torch.equal(out, a[src.long()] + a[dst.long()])
+    z = torch.zeros(0, dtype=torch.int32, device=device)
+    assert edges.gather_add(a, a, z, z).shape == (0, 16)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_edge_token_linear_fwd_bwd(device, dtype):
+    # Linear(cat(x[src], x[dst])) of the reference against the oracle (float64): forward, and the
+    # gradients of x, weight and bias through torch autograd of the oracle's expression
+    n, f, d, e = 300, 64, 96, 2500
+    src, dst = _graph(3, n, e)
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(n, f, generator=g)
+    lin = torch.nn.Linear(2 * f, d)
+    gy = torch.randn(e, d, generator=g)
+    xd = x.to(dtype).to(device).requires_grad_(True)
+    w = lin.weight.detach().to(dtype).to(device).requires_grad_(True)
+    bb = lin.bias.detach().to(dtype).to(device).requires_grad_(True)
+    out = edges.edge_token_linear(xd, torch.as_tensor(src).to(device), torch.as_tensor(dst).to(device), w, bb)
+    out.backward(gy.to(dtype).to(device))
+    xr = x.to(dtype).double().requires_grad_(True)
+    wr = lin.weight.detach().to(dtype).double().requires_grad_(True)
+    br = lin.bias.detach().to(dtype).double().requires_grad_(True)
+    ref = torch.nn.functional.linear(torch.cat((xr[torch.as_tensor(src).long()], xr[torch.as_tensor(dst).long()]), 1),
+                                     wr, br)
+    ref.backward(gy.to(dtype).double())
+    assert np.abs(OE.edge_token_linear(x.to(dtype).double().numpy(), src, dst, wr.detach().numpy(),
+                                       br.detach().numpy()) - ref.detach().numpy()).max() < 1e-10
+    check = assert_f32_close if dtype == torch.float32 else \
+        (lambda got, r, what: assert_bf16_close(got, r, grad_scale(r), what))
+    check(out.detach().cpu().double(), ref.detach(), "out")
+    check(xd.grad.cpu().double(), xr.grad, "dx")
+    check(w.grad.cpu().double(), wr.grad, "dweight")
+    check(bb.grad.cpu().double(), br.grad, "dbias")
+
+
+def test_edge_token_linear_module_loads_linear_state(device):
+    lin = torch.nn.Linear(2 * 32, 48)
+    m = edges.EdgeTokenLinear(32, 48)
+    m.load_state_dict(lin.state_dict())
+    m = m.to(device)
+    x = torch.randn(50, 32, device=device)
+    src = torch.randint(0, 50, (400,), device=device, dtype=torch.int32)
+    dst = torch.randint(0, 50, (400,), device=device, dtype=torch.int32)
+    ref = lin.to(device)(torch.cat((x[src.long()], x[dst.long()]), 1))
+    got = m(x, src, dst)
+    assert float((got - ref).abs().max()) <= 1e-5 * max(1.0, float(ref.abs().max()))

@@ -246,6 +246,22 @@ def test_gather_concatenates_src_then_dst():
     assert out.tolist() == [[10, 11, 2, 3], [0, 1, 2, 3], [4, 5, 8, 9]]
 
 
+def test_edge_token_linear_matches_reference_expression():
+    # the reference's own torch expression: Linear(torch.cat((x[src], x[dst]), 1))
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((9, 5))
+    src, dst = rng.integers(0, 9, 40), rng.integers(0, 9, 40)
+    lin = torch.nn.Linear(10, 7).double()
+    xt = torch.as_tensor(x)
+    ref = lin(torch.cat((xt[torch.as_tensor(src)], xt[torch.as_tensor(dst)]), 1)).detach().numpy()
+    got = OE.edge_token_linear(x, src, dst, lin.weight.detach().numpy(), lin.bias.detach().numpy())
+    assert np.abs(got - ref).max() < 1e-12
+    # and the split-weight identity the fused kernel relies on
+    w = lin.weight.detach().numpy()
+    split = x[src] @ w[:, :5].T + x[dst] @ w[:, 5:].T + lin.bias.detach().numpy()
+    assert np.abs(got - split).max() < 1e-12
+
+
 @given(st.lists(st.integers(0, 9), min_size=0, max_size=60))
 @settings(max_examples=60, deadline=None)
 def test_csr_build_loop(keys):
