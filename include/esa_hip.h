@@ -175,6 +175,22 @@ ESA_API int esa_edge_gather_bwd(const void* g, const int* src_perm,
                         int dtype, void* gx, void* stream);
 
 /* ------------------------------------------------------------------------ */
+/* Block epilogue: y = mish(z) (+ residual), elementwise over n values of    */
+/* `dtype` (ESA_F32 or ESA_BF16), evaluated in fp32 and rounded once.        */
+/* With residual = the MAB's attention output O and z = fc_o(O) this is      */
+/* `out + F.mish(fc_o(out))` (esa/mha.py:87, esa/mha_flash_varlen.py:195);  */
+/* with residual NULL it is the MLP activation nn.Mish                        */
+/* (esa/mlp_utils.py:24-37).  residual may be NULL; y may alias z or residual. */
+/* ------------------------------------------------------------------------ */
+ESA_API int esa_mish_fwd(const void* z, const void* residual, int64_t n, int dtype,
+                 void* y, void* stream);
+
+/* Backward of esa_mish_fwd: dz = grad * mish'(z) (the residual's gradient is */
+/* grad itself).  dz may alias z or grad.                                     */
+ESA_API int esa_mish_bwd(const void* z, const void* grad, int64_t n, int dtype,
+                 void* dz, void* stream);
+
+/* ------------------------------------------------------------------------ */
 /* Profiling hook (no counterpart in the reference; used by the benchmark).  */
 /* While enabled, every kernel launch of the entry points above is           */
 /* bracketed by hipEvents on its stream.  esa_profile_collect waits for the  */
@@ -182,7 +198,7 @@ ESA_API int esa_edge_gather_bwd(const void* g, const int* src_perm,
 /* launch count per kernel id (capacity >= ESA_PROFILE_KERNELS) and clears   */
 /* the record.  Not for concurrent use from several threads.                 */
 /* ------------------------------------------------------------------------ */
-#define ESA_PROFILE_KERNELS 14
+#define ESA_PROFILE_KERNELS 16
 ESA_API int esa_profile_enable(int on);
 ESA_API int esa_profile_collect(float* total_ms, int* launches, int capacity);
 ESA_API const char* esa_profile_kernel_name(int kernel);

@@ -55,12 +55,14 @@ _PROTOS = {
     "esa_edge_gather_bwd": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _vp]),
     "esa_edge_gather_add": (_c_int, [_vp, _c_i64, _vp, _c_i64, _vp, _vp, _vp, _c_i64, _c_int, _c_int, _c_int, _vp,
                                      _vp]),
+    "esa_mish_fwd": (_c_int, [_vp, _vp, _c_i64, _c_int, _vp, _vp]),
+    "esa_mish_bwd": (_c_int, [_vp, _vp, _c_i64, _c_int, _vp, _vp]),
     "esa_profile_enable": (_c_int, [_c_int]),
     "esa_profile_collect": (_c_int, [ctypes.POINTER(_c_f), ctypes.POINTER(_c_int), _c_int]),
     "esa_profile_kernel_name": (ctypes.c_char_p, [_c_int]),
 }
 
-PROFILE_KERNELS = 14
+PROFILE_KERNELS = 16
 
 _lock = threading.Lock()
 _lib = None

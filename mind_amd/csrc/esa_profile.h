@@ -21,6 +21,8 @@ enum Kernel : int {
   kGraphDq,
   kGraphDkdv,
   kEdgeGatherAdd,   // fused edge-token projection
+  kMishFwd,         // block epilogue: mish (+ residual)
+  kMishBwd,
   kNumKernels
 };
 

@@ -31,6 +31,7 @@ import torch
 from torch import nn
 from torch.nn import functional as F
 
+from .activations import mish
 from .attention import varlen_attention
 from .mha import PMA, SAB, _heads, _uniform_cu, pooled_attention
 from .mha_flash_varlen import PMAFlashVarlen, SABFlashVarlen
@@ -144,7 +145,7 @@ def _sab_valid_only(sab: SAB, X: torch.Tensor, tokens: PackedSets) -> torch.Tens
     out = varlen_attention(_heads(tokens.unpad(q), h), _heads(tokens.unpad(k), h), _heads(tokens.unpad(v), h),
                            cu, cu, n, n)
     out = tokens.pad(out.reshape(-1, d)).to(q.dtype)
-    return out + F.mish(mab.fc_o(out))
+    return mish(mab.fc_o(out), out)
 
 
 def _packed_mab(mab, xq: torch.Tensor, xk: torch.Tensor, cu_q: torch.Tensor, cu_k: torch.Tensor, max_q: int,
@@ -157,7 +158,7 @@ def _packed_mab(mab, xq: torch.Tensor, xk: torch.Tensor, cu_q: torch.Tensor, cu_
     h, d = mab.num_heads, q.shape[-1]
     out = varlen_attention(_heads(q, h), _heads(k, h), _heads(v, h), cu_q, cu_k, max_q, max_k, **mask_kwargs)
     out = out.reshape(-1, d).to(q.dtype)
-    return out + F.mish(mab.fc_o(out))
+    return mish(mab.fc_o(out), out)
 
 
 def _sab_forward_packed(blk: "SABComplete", X: torch.Tensor, tokens: PackedSets) -> torch.Tensor:
@@ -325,8 +326,8 @@ class ESA(nn.Module):
         if hasattr(self, "decoder"):
             out, _, _, _, _ = self.decoder((enc, edge_index, batch_mapping, num_max_items, adj_mask))
             out = out.mean(dim=1)
-            return F.mish(self.decoder_linear(out)), node_embeddings_before_pma
-        return F.mish(self.decoder_linear(enc)), enc
+            return mish(self.decoder_linear(out)), node_embeddings_before_pma
+        return mish(self.decoder_linear(enc)), enc
 
     def _forward_packed(self, X, edge_index, batch_mapping, num_max_items, tokens: PackedSets):
         """The "hip" forward: encoder and PMA keys on the packed tokens; the decoder's later layers act on
@@ -344,5 +345,5 @@ class ESA(nn.Module):
             for blk in list(self.decoder)[1:]:
                 out, _, _, _, _ = blk((out, edge_index, batch_mapping, num_max_items, tokens))
             out = out.mean(dim=1)
-            return F.mish(self.decoder_linear(out)), node_embeddings_before_pma
-        return F.mish(self.decoder_linear(node_embeddings_before_pma)), node_embeddings_before_pma
+            return mish(self.decoder_linear(out)), node_embeddings_before_pma
+        return mish(self.decoder_linear(node_embeddings_before_pma)), node_embeddings_before_pma

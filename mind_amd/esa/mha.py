@@ -32,9 +32,9 @@ from __future__ import annotations
 
 import torch
 from torch import nn
-from torch.nn import functional as F
 from torch.nn.init import xavier_normal_
 
+from .activations import mish
 from .attention import HEAD_DIM, varlen_attention
 from .packing import PackedSets
 
@@ -117,7 +117,7 @@ class MAB(nn.Module):
             raise TypeError("adj_mask must be None or an EdgeAdjacency / NodeAdjacency (build it with "
                             "get_adj_mask_from_edge_index_edge / _node); dense bias tensors are not materialised")
         out = out.to(q.dtype)
-        return out + F.mish(self.fc_o(out))
+        return mish(self.fc_o(out), out)
 
 
 class SAB(nn.Module):
@@ -173,5 +173,5 @@ def pooled_attention(mab: MAB, S: torch.Tensor, X: torch.Tensor, seq_lens) -> to
     out = varlen_attention(_heads(q, h), _heads(k, h), _heads(v, h), _uniform_cu(b, k_seeds, X.device), cu_k,
                            k_seeds, n)
     out = out.reshape(b, k_seeds, d).to(q.dtype)
-    return out + F.mish(mab.fc_o(out))
+    return mish(mab.fc_o(out), out)
 

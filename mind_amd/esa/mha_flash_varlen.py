@@ -17,6 +17,7 @@ from torch import nn
 from torch.nn import functional as F
 from torch.nn.init import xavier_normal_
 
+from .activations import mish
 from .attention import varlen_attention
 from .mha import _heads, dense_attention, masked_attention
 from .packing import PackedSets
@@ -69,7 +70,7 @@ class MABFlashVarlen(nn.Module):
         else:
             raise TypeError("adj_mask must be None or an EdgeAdjacency / NodeAdjacency")
         out = out.to(q.dtype)
-        out = out + F.mish(self.fc_o(out))
+        out = mish(self.fc_o(out), out)
         return out.to(input_dtype) if out.dtype != input_dtype else out
 
     def _forward_varlen(self, Q, K, seq_lens, adj_mask=None):
@@ -96,7 +97,7 @@ class MABFlashVarlen(nn.Module):
         vp = _heads(v.reshape(b * n, d).index_select(0, index), h)
         out_p = varlen_attention(qp, kp, vp, cu, cu, n, n).reshape(-1, d).to(q.dtype)
         out = q.new_zeros(b * n, d).index_copy(0, index, out_p).view(b, n, d)
-        out = out + F.mish(_linear(self.fc_o, out))
+        out = mish(_linear(self.fc_o, out), out)
         return out.to(input_dtype) if out.dtype != input_dtype else out
 
 

@@ -10,6 +10,8 @@ from __future__ import annotations
 from torch import nn
 from torch.nn import functional as F
 
+from .activations import Mish
+
 
 def swiglu(gate, y):
     return F.silu(gate) * y
@@ -24,7 +26,7 @@ class SmallMLP(nn.Module):
             self.mlp = nn.Sequential(
                 nn.Linear(in_dim, out_dim),
                 nn.Dropout(p=dropout_p) if dropout_p > 0 else nn.Identity(),
-                nn.Mish(),
+                Mish(),
             )
             return
         layers = []
@@ -35,7 +37,7 @@ class SmallMLP(nn.Module):
             if i != num_layers - 1:
                 if use_ln:
                     layers.append(nn.LayerNorm(inter_dim))
-                layers.append(nn.Mish())
+                layers.append(Mish())
             if dropout_p > 0:
                 layers.append(nn.Dropout(p=dropout_p))
         self.mlp = nn.Sequential(*layers)
@@ -72,7 +74,7 @@ class GatedMLPMulti(nn.Module):
             self.mlp = nn.Sequential(
                 GatedMLPSingle(in_dim, inter_dim, out_dim, dropout_p=dropout_p, use_ln=False),
                 nn.Dropout(p=dropout_p) if dropout_p > 0 else nn.Identity(),
-                nn.Mish(),
+                Mish(),
             )
             return
         layers = []
@@ -82,7 +84,7 @@ class GatedMLPMulti(nn.Module):
             layers.append(GatedMLPSingle(d_in, inter_dim, d_out, dropout_p=dropout_p, use_ln=use_ln))
             if dropout_p > 0:
                 layers.append(nn.Dropout(p=dropout_p))
-            layers.append(nn.Mish())
+            layers.append(Mish())
         self.mlp = nn.Sequential(*layers)
 
     def forward(self, x):

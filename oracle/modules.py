@@ -39,6 +39,13 @@ def mish(x):
     return x * torch.tanh(F.softplus(x))
 
 
+def mish_grad(x):
+    """d mish / dx = tanh(softplus x) + x sigmoid(x) (1 - tanh(softplus x)^2): the derivative of the F.mish /
+    nn.Mish of esa/mha.py:87 and esa/mlp_utils.py:24-37."""
+    t = torch.tanh(F.softplus(x))
+    return t + x * torch.sigmoid(x) * (1 - t * t)
+
+
 def _heads(x, h):
     return x.reshape(*x.shape[:-1], h, x.shape[-1] // h)
 

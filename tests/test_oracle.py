@@ -357,3 +357,18 @@ def test_layer_norm_matches_torch():
     ref = F.layer_norm(x, (d,), sd["ln.weight"], sd["ln.bias"], eps=1e-8)
     assert torch.allclose(OMod.layer_norm(sd, "ln.", x), ref, atol=1e-12)
     assert torch.allclose(OMod.mish(x), F.mish(x), atol=1e-12)
+
+
+def test_mish_grad_matches_autograd_and_closed_forms():
+    x = torch.linspace(-40, 40, 20001, dtype=torch.float64, requires_grad=True)
+    F.mish(x).sum().backward()
+    g = OMod.mish_grad(x.detach())
+    assert torch.allclose(g, x.grad, rtol=1e-12, atol=1e-15)
+    # mish'(0) = tanh(ln 2) = 3/5; mish' -> 1 for large x, -> 0 for very negative x
+    assert abs(float(OMod.mish_grad(torch.zeros(1, dtype=torch.float64))) - 0.6) < 1e-15
+    assert abs(float(OMod.mish_grad(torch.tensor([30.0], dtype=torch.float64))) - 1.0) < 1e-12
+    assert abs(float(OMod.mish_grad(torch.tensor([-60.0], dtype=torch.float64)))) < 1e-20
+    # the minimum of mish (x ~ -1.1924, mish ~ -0.30884): the derivative changes sign there
+    lo, hi = torch.tensor([-1.1925], dtype=torch.float64), torch.tensor([-1.1923], dtype=torch.float64)
+    assert float(OMod.mish_grad(lo)) < 0 < float(OMod.mish_grad(hi))
+    assert abs(float(OMod.mish(torch.tensor([-1.1924], dtype=torch.float64))) + 0.30884) < 1e-5
