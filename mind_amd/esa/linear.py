@@ -1,0 +1,90 @@
+"""nn.Linear for the packed ESA blocks, with a split-K weight gradient.
+
+On packed edge tokens a Linear's weight gradient dW = g^T x reduces over all
+T tokens of the batch (T = 131,072 in the encoder-stack benchmark) into a
+small [out, in] matrix: one GEMM with K = T has only a few dozen output tiles
+for 256 CUs.  ``linear`` computes it instead as S batched GEMMs over token
+chunks (``torch.bmm`` with fp32 outputs) and sums the S fp32 partials, so the
+reduction fills the chip and is rounded to the weight's dtype once, as the
+single GEMM's fp32 accumulator is.  Forward (F.linear) and dx = g W are
+unchanged; under autocast the inputs are cast as autocast casts F.linear's
+(x, weight and bias to the autocast dtype).
+
+Reference: the nn.Linear layers of the MAB (esa/mha.py:12-15) and of the MLPs
+(esa/mlp_utils.py:18-37).
+"""
+from __future__ import annotations
+
+import torch
+from torch import nn
+from torch.nn import functional as F
+
+_MIN_CHUNK = 4096               # tokens per chunk: below, a chunk's GEMM is too short to pay
+_MAX_PARTIAL = 16 * 1024 * 1024  # fp32 values of all partials (64 MiB)
+_MAX_SPLIT = 32
+
+
+def split_count(tokens: int, out_features: int, in_features: int) -> int:
+    """Chunks S of the split-K weight gradient (1 = a single GEMM): the largest power of two <= 32 with chunks
+    of >= 4096 tokens and S * out * in fp32 partials within 64 MiB."""
+    s = 1
+    while (2 * s <= _MAX_SPLIT and tokens // (2 * s) >= _MIN_CHUNK
+           and 2 * s * out_features * in_features <= _MAX_PARTIAL):
+        s *= 2
+    return s
+
+
+def weight_grad(g: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+    """g^T x for g [T, out], x [T, in] (same dtype) in fp32, by split_count(T, out, in) token chunks."""
+    t, o = g.shape
+    i = x.shape[1]
+    s = split_count(t, o, i)
+    if t < _MIN_CHUNK:
+        return g.t().float().mm(x.float())
+    c = t // s
+    t0 = s * c
+    kw = {} if g.dtype == torch.float32 else {"out_dtype": torch.float32}
+    parts = torch.bmm(g[:t0].view(s, c, o).transpose(1, 2), x[:t0].view(s, c, i), **kw)
+    dw = parts.sum(0)
+    if t0 < t:   # fewer than S leftover tokens
+        dw += g[t0:].t().float().mm(x[t0:].float())
+    return dw
+
+
+class _Linear(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, weight, bias):
+        ctx.save_for_backward(x, weight)
+        ctx.has_bias = bias is not None
+        return F.linear(x, weight, bias)
+
+    @staticmethod
+    def backward(ctx, g):
+        x, weight = ctx.saved_tensors
+        g = g.contiguous()
+        dx = g.mm(weight) if ctx.needs_input_grad[0] else None
+        dw = weight_grad(g, x).to(weight.dtype) if ctx.needs_input_grad[1] else None
+        db = g.sum(0) if ctx.has_bias and ctx.needs_input_grad[2] else None
+        return dx, dw, db
+
+
+def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None) -> torch.Tensor:
+    """F.linear(x, weight, bias) with the split-K weight gradient (device tensors; CPU tensors use F.linear)."""
+    if not x.is_cuda:
+        return F.linear(x, weight, bias)
+    if torch.is_autocast_enabled("cuda"):
+        dt = torch.get_autocast_dtype("cuda")
+        x, weight = x.to(dt), weight.to(dt)
+        bias = None if bias is None else bias.to(dt)
+    if x.dtype != weight.dtype or (bias is not None and bias.dtype != x.dtype):
+        return F.linear(x, weight, bias)   # mixed dtypes: torch's own type checks and errors
+    lead = x.shape[:-1]
+    y = _Linear.apply(x.reshape(-1, x.shape[-1]).contiguous(), weight, bias)
+    return y.view(*lead, weight.shape[0])
+
+
+def apply(layer: nn.Module, x: torch.Tensor) -> torch.Tensor:
+    """layer(x), with nn.Linear layers through ``linear``."""
+    if type(layer) is nn.Linear:
+        return linear(x, layer.weight, layer.bias)
+    return layer(x)

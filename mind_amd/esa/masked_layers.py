@@ -33,6 +33,7 @@ from torch.nn import functional as F
 
 from .activations import mish
 from .attention import varlen_attention
+from .linear import apply
 from .mha import PMA, SAB, _heads, _uniform_cu, pooled_attention
 from .mha_flash_varlen import PMAFlashVarlen, SABFlashVarlen
 from .mlp_utils import GatedMLPMulti, SmallMLP
@@ -137,28 +138,28 @@ class SABComplete(nn.Module):
 def _sab_valid_only(sab: SAB, X: torch.Tensor, tokens: PackedSets) -> torch.Tensor:
     """Unmasked self-attention over each graph's valid tokens (the "hip" backend's S layers)."""
     mab = sab.mab
-    q = mab.fc_q(X)
-    v = mab.fc_v(X)
-    k = mab.fc_k(X)
+    q = apply(mab.fc_q, X)
+    v = apply(mab.fc_v, X)
+    k = apply(mab.fc_k, X)
     h, d, n = mab.num_heads, q.shape[-1], X.shape[1]
     cu = tokens.cu_seqlens
     out = varlen_attention(_heads(tokens.unpad(q), h), _heads(tokens.unpad(k), h), _heads(tokens.unpad(v), h),
                            cu, cu, n, n)
     out = tokens.pad(out.reshape(-1, d)).to(q.dtype)
-    return mish(mab.fc_o(out), out)
+    return mish(apply(mab.fc_o, out), out)
 
 
 def _packed_mab(mab, xq: torch.Tensor, xk: torch.Tensor, cu_q: torch.Tensor, cu_k: torch.Tensor, max_q: int,
                 max_k: int, mask_kwargs: dict) -> torch.Tensor:
     """MAB (esa/mha.py:48-89, V = fc_v(K)) on packed rows: queries xq [Tq, D] and keys xk [Tk, D] grouped by
     cu_q / cu_k -> [Tq, D]."""
-    q = mab.fc_q(xq)
-    v = mab.fc_v(xk)
-    k = mab.fc_k(xk)
+    q = apply(mab.fc_q, xq)
+    v = apply(mab.fc_v, xk)
+    k = apply(mab.fc_k, xk)
     h, d = mab.num_heads, q.shape[-1]
     out = varlen_attention(_heads(q, h), _heads(k, h), _heads(v, h), cu_q, cu_k, max_q, max_k, **mask_kwargs)
     out = out.reshape(-1, d).to(q.dtype)
-    return mish(mab.fc_o(out), out)
+    return mish(apply(mab.fc_o, out), out)
 
 
 def _sab_forward_packed(blk: "SABComplete", X: torch.Tensor, tokens: PackedSets) -> torch.Tensor:

@@ -11,6 +11,7 @@ from torch import nn
 from torch.nn import functional as F
 
 from .activations import Mish
+from .linear import apply, linear
 
 
 def swiglu(gate, y):
@@ -43,7 +44,9 @@ class SmallMLP(nn.Module):
         self.mlp = nn.Sequential(*layers)
 
     def forward(self, x):
-        return self.mlp(x)
+        for layer in self.mlp:
+            x = apply(layer, x)
+        return x
 
 
 class GatedMLPSingle(nn.Module):
@@ -58,11 +61,11 @@ class GatedMLPSingle(nn.Module):
             self.ln = nn.LayerNorm(2 * inter_dim, eps=1e-8)
 
     def forward(self, x):
-        y = self.fc1(x)
+        y = linear(x, self.fc1.weight, self.fc1.bias)
         if self.use_ln:
             y = self.ln(y)
         y, gate = y.chunk(2, dim=-1)
-        return self.fc2(swiglu(gate, y))
+        return linear(swiglu(gate, y), self.fc2.weight, self.fc2.bias)
 
 
 class GatedMLPMulti(nn.Module):
@@ -88,4 +91,6 @@ class GatedMLPMulti(nn.Module):
         self.mlp = nn.Sequential(*layers)
 
     def forward(self, x):
-        return self.mlp(x)
+        for layer in self.mlp:
+            x = apply(layer, x)
+        return x

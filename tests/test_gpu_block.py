@@ -132,3 +132,57 @@ def test_mish_argument_errors(device):
     assert lib.esa_mish_bwd(None, None, 0, _lib.ESA_F32, None, None) == 0
     with pytest.raises(TypeError):
         mish(z.half())
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("tokens,out_f,in_f", [(100, 48, 40), (3 * 4096 + 7, 64, 96), (65536 + 3, 512, 512),
+                                               (40000, 2048, 512)])
+def test_split_k_linear(device, dtype, tokens, out_f, in_f):
+    """linear(x, W, b): forward and dx as F.linear's autograd; dW by token chunks against the fp64 oracle.
+
+    dW bar: fp32 1e-5 relative to max |dW| (plus the fp32 accumulation over T terms, T 2^-24 max|g x|); bf16
+    one rounding (2^-8 relative) plus the same accumulation term."""
+    from mind_amd.esa.linear import linear, split_count
+    gen = torch.Generator().manual_seed(tokens + out_f)
+    x = torch.randn(tokens, in_f, generator=gen).to(dtype)
+    w = (torch.randn(out_f, in_f, generator=gen) * 0.05).to(dtype)
+    b = torch.randn(out_f, generator=gen).to(dtype)
+    g = torch.randn(tokens, out_f, generator=gen).to(dtype)
+    xd, wd, bd = (t.to(device).requires_grad_(True) for t in (x, w, b))
+    y = linear(xd, wd, bd)
+    y.backward(g.to(device))
+    xr, wr, br = (t.to(device).requires_grad_(True) for t in (x, w, b))
+    yr = torch.nn.functional.linear(xr, wr, br)
+    yr.backward(g.to(device))
+    assert torch.equal(y, yr)
+    assert torch.equal(xd.grad, xr.grad)
+    assert torch.equal(bd.grad, br.grad)
+    ref = g.double().t() @ x.double()
+    acc = tokens * 2.0 ** -24 * float((g.double().abs().max() * x.double().abs().max()))
+    got = wd.grad.double().cpu()
+    if dtype == torch.float32:
+        assert float((got - ref).abs().max()) <= 1e-5 * float(ref.abs().max()) + acc
+    else:
+        assert bool(((got - ref).abs() <= 2.0 ** -8 * ref.abs() + acc).all())
+    if tokens >= 65536:
+        assert split_count(tokens, out_f, in_f) > 1
+
+
+@pytest.mark.gpu
+def test_split_k_linear_under_autocast(device):
+    """fp32 parameters under autocast(bf16): the output is bf16 and gradients reach the fp32 parameters."""
+    from mind_amd.esa.linear import linear
+    gen = torch.Generator().manual_seed(9)
+    lin = torch.nn.Linear(256, 128).to(device)
+    x = torch.randn(20000, 256, generator=gen).to(device)
+    g = torch.randn(20000, 128, generator=gen).to(device).to(torch.bfloat16)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        y = linear(x, lin.weight, lin.bias)
+        yr = lin(x)
+    assert y.dtype == torch.bfloat16 and torch.equal(y, yr)
+    y.backward(g)
+    assert lin.weight.grad.dtype == torch.float32
+    ref = g.double().t().cpu() @ x.to(torch.bfloat16).double().cpu()
+    assert_rel = (lin.weight.grad.double().cpu() - ref).abs() <= 2.0 ** -8 * ref.abs() + 20000 * 2.0 ** -24 * 40
+    assert bool(assert_rel.all())
+    assert torch.allclose(lin.bias.grad.double().cpu(), g.double().sum(0).cpu(), rtol=2.0 ** -7, atol=1e-2)
