@@ -191,6 +191,34 @@ ESA_API int esa_mish_bwd(const void* z, const void* grad, int64_t n, int dtype,
                  void* dz, void* stream);
 
 /* ------------------------------------------------------------------------ */
+/* Pre-norm LayerNorm over the last dimension of [rows, features] (features */
+/* a multiple of 4, at most 2048): nn.LayerNorm(features, eps) as the ESA    */
+/* blocks apply it (esa/utils/norm_layers.py:36; esa/masked_layers.py:418-  */
+/* 419, 478-483), fp32 statistics, y = (x - mean) rstd weight + bias with    */
+/* rstd = 1/sqrt(biased var + eps).  x is ESA_F32 or ESA_BF16; weight and    */
+/* bias are fp32 [features] or NULL (1 and 0).  Writes y (y_dtype) and/or    */
+/* its bf16 copy y_lp (either may be NULL, not both) and the per-row mean    */
+/* and rstd [rows] that the backward takes.  Pointers 16-byte aligned.       */
+/* ------------------------------------------------------------------------ */
+ESA_API int esa_layer_norm_fwd(const void* x, int x_dtype, const float* weight,
+                       const float* bias, int64_t rows, int features, float eps,
+                       void* y, int y_dtype, void* y_lp, float* mean, float* rstd,
+                       void* stream);
+
+ESA_API int esa_layer_norm_bwd_workspace_size(int64_t rows, int features, size_t* bytes);
+
+/* Backward: with g = dy + dy_lp (dy of dy_dtype and/or the bf16 gradient of */
+/* y_lp; NULL = zero, not both), dx (x_dtype) = rstd (g w - mean(g w) -      */
+/* xhat mean(g w xhat)) and, when dweight / dbias are given, the fp32 column */
+/* sums of g xhat / g, reduced in a fixed order (deterministic).  The        */
+/* workspace (size from the query) is needed only for dweight / dbias.       */
+ESA_API int esa_layer_norm_bwd(const void* x, int x_dtype, const float* weight,
+                       const float* mean, const float* rstd, const void* dy,
+                       int dy_dtype, const void* dy_lp, int64_t rows, int features,
+                       void* dx, float* dweight, float* dbias, void* workspace,
+                       size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------ */
 /* Profiling hook (no counterpart in the reference; used by the benchmark).  */
 /* While enabled, every kernel launch of the entry points above is           */
 /* bracketed by hipEvents on its stream.  esa_profile_collect waits for the  */
@@ -198,7 +226,7 @@ ESA_API int esa_mish_bwd(const void* z, const void* grad, int64_t n, int dtype,
 /* launch count per kernel id (capacity >= ESA_PROFILE_KERNELS) and clears   */
 /* the record.  Not for concurrent use from several threads.                 */
 /* ------------------------------------------------------------------------ */
-#define ESA_PROFILE_KERNELS 16
+#define ESA_PROFILE_KERNELS 18
 ESA_API int esa_profile_enable(int on);
 ESA_API int esa_profile_collect(float* total_ms, int* launches, int capacity);
 ESA_API const char* esa_profile_kernel_name(int kernel);

@@ -57,12 +57,18 @@ _PROTOS = {
                                      _vp]),
     "esa_mish_fwd": (_c_int, [_vp, _vp, _c_i64, _c_int, _vp, _vp]),
     "esa_mish_bwd": (_c_int, [_vp, _vp, _c_i64, _c_int, _vp, _vp]),
+    # x x_dtype w b rows features eps y y_dtype y_lp mean rstd stream
+    "esa_layer_norm_fwd": (_c_int, [_vp, _c_int, _vp, _vp, _c_i64, _c_int, _c_f, _vp, _c_int, _vp, _vp, _vp, _vp]),
+    "esa_layer_norm_bwd_workspace_size": (_c_int, [_c_i64, _c_int, ctypes.POINTER(_c_sz)]),
+    # x x_dtype w mean rstd dy dy_dtype dy_lp rows features dx dw db ws bytes stream
+    "esa_layer_norm_bwd": (_c_int, [_vp, _c_int, _vp, _vp, _vp, _vp, _c_int, _vp, _c_i64, _c_int, _vp, _vp, _vp, _vp,
+                                    _c_sz, _vp]),
     "esa_profile_enable": (_c_int, [_c_int]),
     "esa_profile_collect": (_c_int, [ctypes.POINTER(_c_f), ctypes.POINTER(_c_int), _c_int]),
     "esa_profile_kernel_name": (ctypes.c_char_p, [_c_int]),
 }
 
-PROFILE_KERNELS = 16
+PROFILE_KERNELS = 18
 
 _lock = threading.Lock()
 _lib = None

@@ -17,6 +17,14 @@
 // The ops are HBM-bound streams (one fp32 exp and one reciprocal per value):
 // each thread moves 16-byte chunks, kUnroll of them in flight, the chunks of
 // a block contiguous; misaligned pointers take an element-wise kernel.
+//
+// LayerNorm (the blocks' pre-norm, nn.LayerNorm(D, eps=1e-8) at
+// esa/utils/norm_layers.py:36, applied at esa/masked_layers.py:418-419 and
+// 478-483): fp32 row statistics (mean, biased variance), y = (x - mean) rstd
+// w + b with rstd = 1 / sqrt(var + eps).  The forward can write y in fp32 and
+// a bf16 copy in the same pass (under autocast the normed rows are both the
+// fp32 residual and the bf16 GEMM input); the backward takes the gradients of
+// both outputs and sums them, so no cast or add kernel runs beside it.
 #include "esa_common.h"
 #include "esa_profile.h"
 #include "../../include/esa_hip.h"
@@ -191,7 +199,322 @@ int mish_bwd_typed(const T* z, const T* g, T* dz, int64_t n, hipStream_t st) {
   return rc;
 }
 
+// ------------------------------------------------------------------ LayerNorm
+// One wave per row.  Lane l holds the row's 4-feature chunks l, l + 64, ...
+// (K chunks, D <= 256 K), so a chunk step of the wave reads one contiguous
+// run of the row; the statistics are wave sums (butterfly: every lane ends
+// with the same bits).
+constexpr int kLnMaxFeatures = 2048;
+constexpr int kLnMaxBlocks = 1024;   // backward: row-strided blocks (4 waves each)
+
+DEVI float wave_sum(float x) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) x += __shfl_xor(x, o);
+  return x;
+}
+
+DEVI f32x4 load4(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
+DEVI f32x4 load4(const bf16* p) {
+  const bf16x4 v = *reinterpret_cast<const bf16x4*>(p);
+  return f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
+}
+DEVI void store4(float* p, const f32x4& v) { *reinterpret_cast<f32x4*>(p) = v; }
+DEVI void store4(bf16* p, const f32x4& v) {
+  *reinterpret_cast<bf16x4*>(p) = bf16x4{(bf16)v[0], (bf16)v[1], (bf16)v[2], (bf16)v[3]};
+}
+
+template <typename TX, typename TY, int K>
+__global__ __launch_bounds__(256) void ln_fwd_kernel(const TX* __restrict__ x, const float* __restrict__ w,
+                                                     const float* __restrict__ b, int64_t rows, int D, float eps,
+                                                     TY* __restrict__ y, bf16* __restrict__ ylp,
+                                                     float* __restrict__ mean, float* __restrict__ rstd) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int64_t base = row * D;
+  f32x4 v[K];
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int f = 4 * (lane + 64 * k);
+    v[k] = f < D ? load4(x + base + f) : f32x4{0.f, 0.f, 0.f, 0.f};
+    s += (v[k][0] + v[k][1]) + (v[k][2] + v[k][3]);
+  }
+  const float mu = wave_sum(s) / (float)D;
+  float q = 0.f;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    if (4 * (lane + 64 * k) < D) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float d = v[k][e] - mu;
+        q = fmaf(d, d, q);
+      }
+    }
+  }
+  const float rs = rsqrtf(wave_sum(q) / (float)D + eps);
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int f = 4 * (lane + 64 * k);
+    if (f >= D) break;
+    const f32x4 wv = w ? load4(w + f) : f32x4{1.f, 1.f, 1.f, 1.f};
+    const f32x4 bv = b ? load4(b + f) : f32x4{0.f, 0.f, 0.f, 0.f};
+    f32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = fmaf((v[k][e] - mu) * rs, wv[e], bv[e]);
+    if (y) store4(y + base + f, o);
+    if (ylp) store4(ylp + base + f, o);
+  }
+  if (lane == 0) {
+    mean[row] = mu;
+    rstd[row] = rs;
+  }
+}
+
+// dx = rstd (g w - mean(g w) - xhat mean(g w xhat)), g = dy + dy_lp, per row;
+// dw = sum_rows g xhat, db = sum_rows g per column.  Wave w of block B takes
+// rows 4 B + w, then every 4 gridDim.x further (the next row's loads are in
+// flight while a row is computed); its column sums stay in registers, the
+// block adds its four waves in order into part[B] (two rows of D: dw, db).
+template <typename TX, typename TG, int K>
+__global__ __launch_bounds__(256) void ln_bwd_kernel(const TX* __restrict__ x, const float* __restrict__ w,
+                                                     const float* __restrict__ mean, const float* __restrict__ rstd,
+                                                     const TG* __restrict__ dy, const bf16* __restrict__ dylp,
+                                                     int64_t rows, int D, TX* __restrict__ dx,
+                                                     float* __restrict__ part) {
+  __shared__ float red[4][2][256 * K];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t stride = (int64_t)gridDim.x * 4;
+  f32x4 wv[K], aw[K], ab[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int f = 4 * (lane + 64 * k);
+    wv[k] = (w && f < D) ? load4(w + f) : f32x4{1.f, 1.f, 1.f, 1.f};
+    aw[k] = ab[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  auto load_row = [&](int64_t r, f32x4 (&xv)[K], f32x4 (&gv)[K]) {
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int f = 4 * (lane + 64 * k);
+      f32x4 g = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (f < D) {
+        xv[k] = load4(x + r * D + f);
+        if (dy) g = load4(dy + r * D + f);
+        if (dylp) {
+          const f32x4 h = load4(dylp + r * D + f);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) g[e] += h[e];
+        }
+      } else {
+        xv[k] = g;
+      }
+      gv[k] = g;
+    }
+  };
+  int64_t row = (int64_t)blockIdx.x * 4 + wave;
+  f32x4 xv[K], gv[K];
+  if (row < rows) load_row(row, xv, gv);
+  while (row < rows) {
+    const int64_t next = row + stride;
+    f32x4 xn[K], gn[K];
+    if (next < rows) load_row(next, xn, gn);
+    const float mu = mean[row], rs = rstd[row];
+    float c1 = 0.f, c2 = 0.f;
+    f32x4 xh[K], dh[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        xh[k][e] = (xv[k][e] - mu) * rs;
+        dh[k][e] = gv[k][e] * wv[k][e];
+        c1 = fmaf(dh[k][e], xh[k][e], c1);
+        c2 += dh[k][e];
+        aw[k][e] = fmaf(gv[k][e], xh[k][e], aw[k][e]);
+        ab[k][e] += gv[k][e];
+      }
+    }
+    c1 = wave_sum(c1) / (float)D;
+    c2 = wave_sum(c2) / (float)D;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int f = 4 * (lane + 64 * k);
+      if (f >= D) break;
+      f32x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = rs * (dh[k][e] - c2 - xh[k][e] * c1);
+      store4(dx + row * D + f, o);
+    }
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      xv[k] = xn[k];
+      gv[k] = gn[k];
+    }
+    row = next;
+  }
+  if (!part) return;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int f = 4 * (lane + 64 * k);
+    if (f < D) {
+      store4(&red[wave][0][f], aw[k]);
+      store4(&red[wave][1][f], ab[k]);
+    }
+  }
+  __syncthreads();
+  for (int c = threadIdx.x; c < D; c += 256) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      part[((size_t)blockIdx.x * 2 + j) * D + c] = ((red[0][j][c] + red[1][j][c]) + red[2][j][c]) + red[3][j][c];
+  }
+}
+
+// dw[c] / db[c] = sum over the backward's block partials in block order:
+// 64 columns per block, four thread groups take every fourth partial, then
+// the groups are added in order.
+__global__ __launch_bounds__(256) void ln_param_grad_kernel(const float* __restrict__ part, int nparts, int D,
+                                                            float* __restrict__ dw, float* __restrict__ db) {
+  __shared__ float s[2][4][64];
+  const int lane = threadIdx.x & 63, grp = threadIdx.x >> 6;
+  const int c = blockIdx.x * 64 + lane;
+  float a = 0.f, bb = 0.f;
+  if (c < D) {
+    for (int p = grp; p < nparts; p += 4) {
+      a += part[(size_t)(2 * p) * D + c];
+      bb += part[(size_t)(2 * p + 1) * D + c];
+    }
+  }
+  s[0][grp][lane] = a;
+  s[1][grp][lane] = bb;
+  __syncthreads();
+  if (grp == 0 && c < D) {
+    if (dw) dw[c] = ((s[0][0][lane] + s[0][1][lane]) + s[0][2][lane]) + s[0][3][lane];
+    if (db) db[c] = ((s[1][0][lane] + s[1][1][lane]) + s[1][2][lane]) + s[1][3][lane];
+  }
+}
+
+int ln_chunks(int D) {   // K of the kernels: 4-feature chunks per lane
+  const int k = (D + 255) / 256;
+  return k <= 1 ? 1 : k <= 2 ? 2 : k <= 4 ? 4 : 8;
+}
+
+int ln_bwd_blocks(int64_t rows) { return (int)std::min<int64_t>(kLnMaxBlocks, (rows + 3) / 4); }
+
+template <typename TX, typename TY>
+void ln_fwd_go(int K, dim3 grid, hipStream_t st, const TX* x, const float* w, const float* b, int64_t rows, int D,
+               float eps, TY* y, bf16* ylp, float* mean, float* rstd) {
+#define ESA_LN_FWD(KK) hipLaunchKernelGGL((ln_fwd_kernel<TX, TY, KK>), grid, dim3(256), 0, st, x, w, b, rows, D, eps, \
+                                          y, ylp, mean, rstd)
+  if (K == 1) ESA_LN_FWD(1);
+  else if (K == 2) ESA_LN_FWD(2);
+  else if (K == 4) ESA_LN_FWD(4);
+  else ESA_LN_FWD(8);
+#undef ESA_LN_FWD
+}
+
+template <typename TX, typename TG>
+void ln_bwd_go(int K, dim3 grid, hipStream_t st, const TX* x, const float* w, const float* mean, const float* rstd,
+               const TG* dy, const bf16* dylp, int64_t rows, int D, TX* dx, float* part) {
+#define ESA_LN_BWD(KK) hipLaunchKernelGGL((ln_bwd_kernel<TX, TG, KK>), grid, dim3(256), 0, st, x, w, mean, rstd, dy, \
+                                          dylp, rows, D, dx, part)
+  if (K == 1) ESA_LN_BWD(1);
+  else if (K == 2) ESA_LN_BWD(2);
+  else if (K == 4) ESA_LN_BWD(4);
+  else ESA_LN_BWD(8);
+#undef ESA_LN_BWD
+}
+
 }  // namespace
+
+extern "C" ESA_API int esa_layer_norm_fwd(const void* x, int x_dtype, const float* weight, const float* bias,
+                                          int64_t rows, int features, float eps, void* y, int y_dtype, void* y_lp,
+                                          float* mean, float* rstd, void* stream) {
+  if (rows < 0 || features < 4 || features > kLnMaxFeatures || features % 4) return ESA_ERR_SHAPE;
+  if ((x_dtype != ESA_F32 && x_dtype != ESA_BF16) || (y && y_dtype != ESA_F32 && y_dtype != ESA_BF16))
+    return ESA_ERR_DTYPE;
+  if (rows == 0) return ESA_OK;
+  if (!x || !mean || !rstd || (!y && !y_lp)) return ESA_ERR_NULL;
+  if (!aligned16(x) || !aligned16(weight) || !aligned16(bias) || !aligned16(y) || !aligned16(y_lp))
+    return ESA_ERR_ALIGN;
+  if ((rows + 3) / 4 > INT32_MAX) return ESA_ERR_SHAPE;
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid((unsigned)((rows + 3) / 4));
+  const int K = ln_chunks(features);
+  bf16* lp = (bf16*)y_lp;
+  ESA_TIMED(esa_profile::kLayerNormFwd, st, {
+    if (x_dtype == ESA_F32) {
+      if (!y || y_dtype == ESA_F32)
+        ln_fwd_go(K, grid, st, (const float*)x, weight, bias, rows, features, eps, (float*)y, lp, mean, rstd);
+      else
+        ln_fwd_go(K, grid, st, (const float*)x, weight, bias, rows, features, eps, (bf16*)y, lp, mean, rstd);
+    } else {
+      if (!y || y_dtype == ESA_F32)
+        ln_fwd_go(K, grid, st, (const bf16*)x, weight, bias, rows, features, eps, (float*)y, lp, mean, rstd);
+      else
+        ln_fwd_go(K, grid, st, (const bf16*)x, weight, bias, rows, features, eps, (bf16*)y, lp, mean, rstd);
+    }
+  });
+  ESA_LAUNCH_CHECK();
+  return ESA_OK;
+}
+
+extern "C" ESA_API int esa_layer_norm_bwd_workspace_size(int64_t rows, int features, size_t* bytes) {
+  if (!bytes) return ESA_ERR_NULL;
+  if (rows < 0 || features < 4 || features > kLnMaxFeatures || features % 4) return ESA_ERR_SHAPE;
+  *bytes = (size_t)ln_bwd_blocks(rows) * 2 * (size_t)features * sizeof(float);
+  return ESA_OK;
+}
+
+extern "C" ESA_API int esa_layer_norm_bwd(const void* x, int x_dtype, const float* weight, const float* mean,
+                                          const float* rstd, const void* dy, int dy_dtype, const void* dy_lp,
+                                          int64_t rows, int features, void* dx, float* dweight, float* dbias,
+                                          void* workspace, size_t workspace_bytes, void* stream) {
+  if (rows < 0 || features < 4 || features > kLnMaxFeatures || features % 4) return ESA_ERR_SHAPE;
+  if ((x_dtype != ESA_F32 && x_dtype != ESA_BF16) || (dy && dy_dtype != ESA_F32 && dy_dtype != ESA_BF16))
+    return ESA_ERR_DTYPE;
+  const bool params = dweight || dbias;
+  if (rows == 0) {   // empty input: zero parameter gradients (the reduction over no partials)
+    if (params) {
+      hipLaunchKernelGGL(ln_param_grad_kernel, dim3((unsigned)((features + 63) / 64)), dim3(256), 0,
+                         (hipStream_t)stream, nullptr, 0, features, dweight, dbias);
+      ESA_LAUNCH_CHECK();
+    }
+    return ESA_OK;
+  }
+  if (!x || !mean || !rstd || !dx || (!dy && !dy_lp)) return ESA_ERR_NULL;
+  if (!aligned16(x) || !aligned16(weight) || !aligned16(dy) || !aligned16(dy_lp) || !aligned16(dx) ||
+      !aligned16(workspace))
+    return ESA_ERR_ALIGN;
+  const int blocks = ln_bwd_blocks(rows);
+  const size_t need = (size_t)blocks * 2 * (size_t)features * sizeof(float);
+  if (params && (!workspace || workspace_bytes < need)) return ESA_ERR_WORKSPACE;
+  float* part = params ? (float*)workspace : nullptr;
+  hipStream_t st = (hipStream_t)stream;
+  const int K = ln_chunks(features);
+  const bf16* lp = (const bf16*)dy_lp;
+  ESA_TIMED(esa_profile::kLayerNormBwd, st, {
+    const dim3 grid((unsigned)blocks);
+    if (x_dtype == ESA_F32) {
+      if (!dy || dy_dtype == ESA_F32)
+        ln_bwd_go(K, grid, st, (const float*)x, weight, mean, rstd, (const float*)dy, lp, rows, features, (float*)dx,
+                  part);
+      else
+        ln_bwd_go(K, grid, st, (const float*)x, weight, mean, rstd, (const bf16*)dy, lp, rows, features, (float*)dx,
+                  part);
+    } else {
+      if (!dy || dy_dtype == ESA_F32)
+        ln_bwd_go(K, grid, st, (const bf16*)x, weight, mean, rstd, (const float*)dy, lp, rows, features, (bf16*)dx,
+                  part);
+      else
+        ln_bwd_go(K, grid, st, (const bf16*)x, weight, mean, rstd, (const bf16*)dy, lp, rows, features, (bf16*)dx,
+                  part);
+    }
+    if (params)
+      hipLaunchKernelGGL(ln_param_grad_kernel, dim3((unsigned)((features + 63) / 64)), dim3(256), 0, st, part, blocks,
+                         features, dweight, dbias);
+  });
+  ESA_LAUNCH_CHECK();
+  return ESA_OK;
+}
 
 extern "C" ESA_API int esa_mish_fwd(const void* z, const void* residual, int64_t n, int dtype, void* y,
                                     void* stream) {

@@ -23,6 +23,8 @@ enum Kernel : int {
   kEdgeGatherAdd,   // fused edge-token projection
   kMishFwd,         // block epilogue: mish (+ residual)
   kMishBwd,
+  kLayerNormFwd,    // block prologue: pre-norm
+  kLayerNormBwd,
   kNumKernels
 };
 

@@ -33,6 +33,7 @@ from torch.nn import functional as F
 
 from .activations import mish
 from .attention import varlen_attention
+from .layer_norm import layer_norm
 from .linear import apply
 from .mha import PMA, SAB, _heads, _uniform_cu, pooled_attention
 from .mha_flash_varlen import PMAFlashVarlen, SABFlashVarlen
@@ -162,18 +163,26 @@ def _packed_mab(mab, xq: torch.Tensor, xk: torch.Tensor, cu_q: torch.Tensor, cu_
     return mish(apply(mab.fc_o, out), out)
 
 
+def _gemm_input_norm(ln: nn.LayerNorm, x: torch.Tensor) -> torch.Tensor:
+    """ln(x) for a consumer that is a Linear: under autocast only the autocast-dtype rows are written (what
+    the Linear would cast ln's fp32 output to)."""
+    y, y_mm = layer_norm(x, ln, full=False, lowp=True)
+    return y if y_mm is None else y_mm
+
+
 def _sab_forward_packed(blk: "SABComplete", X: torch.Tensor, tokens: PackedSets) -> torch.Tensor:
     """SABComplete.forward (pre-norm, esa/masked_layers.py:418-483) on packed tokens X [T, D]: the masked
     layers (idx 1) apply the descriptor's mask, the unmasked ones (idx 0) attend over each graph's tokens."""
-    X = blk.norm(X)
+    X, x_mm = layer_norm(X, blk.norm.ln, full=True, lowp=True)
+    x_mm = X if x_mm is None else x_mm
     mask_kwargs = tokens.kernel_mask(padded=False) if blk.idx == 1 else {}
     cu, n = tokens.cu_seqlens, tokens.max_items
-    out_attn = _packed_mab(blk.sab.mab, X, X, cu, cu, n, n, mask_kwargs)
+    out_attn = _packed_mab(blk.sab.mab, x_mm, x_mm, cu, cu, n, n, mask_kwargs)
     if out_attn.shape[-1] != X.shape[-1]:
         X = blk.proj_1(X)
     out = X + out_attn
     if blk.use_mlp:
-        out_mlp = blk.mlp(blk.norm_mlp(out))
+        out_mlp = blk.mlp(_gemm_input_norm(blk.norm_mlp.ln, out))
         if out.shape[-1] == out_mlp.shape[-1]:
             out = out_mlp + out
     if blk.residual_dropout > 0:
@@ -184,15 +193,16 @@ def _sab_forward_packed(blk: "SABComplete", X: torch.Tensor, tokens: PackedSets)
 def _pma_forward_packed(blk: "PMAComplete", X: torch.Tensor, tokens: PackedSets) -> torch.Tensor:
     """PMAComplete.forward (esa/masked_layers.py:583-610) with packed keys X [T, D] -> [B, k, D]: the seeds
     of each graph attend over its tokens."""
-    X = blk.norm(X)
+    X, x_mm = layer_norm(X, blk.norm.ln, full=True, lowp=True)
+    x_mm = X if x_mm is None else x_mm
     b, (k_seeds, d) = tokens.batch_size, blk.pma.S.shape[1:]
     seeds = blk.pma.S.reshape(k_seeds, d).repeat(b, 1)
-    out = _packed_mab(blk.pma.mab, seeds, X, _uniform_cu(b, k_seeds, X.device), tokens.cu_seqlens, k_seeds,
+    out = _packed_mab(blk.pma.mab, seeds, x_mm, _uniform_cu(b, k_seeds, X.device), tokens.cu_seqlens, k_seeds,
                       tokens.max_items, {}).reshape(b, k_seeds, d)
     if k_seeds == tokens.max_items:   # the reference's residual when the seed count equals N
         out = tokens.pad(X) + out
     if blk.use_mlp:
-        out_mlp = blk.mlp(blk.norm_mlp(out))
+        out_mlp = blk.mlp(_gemm_input_norm(blk.norm_mlp.ln, out))
         if out.shape[-2] == out_mlp.shape[-2]:
             out = out_mlp + out
     if blk.residual_dropout > 0:

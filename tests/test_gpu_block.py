@@ -186,3 +186,106 @@ def test_split_k_linear_under_autocast(device):
     assert_rel = (lin.weight.grad.double().cpu() - ref).abs() <= 2.0 ** -8 * ref.abs() + 20000 * 2.0 ** -24 * 40
     assert bool(assert_rel.all())
     assert torch.allclose(lin.bias.grad.double().cpu(), g.double().sum(0).cpu(), rtol=2.0 ** -7, atol=1e-2)
+
+
+def _ln_oracle(x, w, b, g, eps=1e-8):
+    """fp64 LayerNorm (the oracle's restatement, pinned against F.layer_norm) and its autograd gradients."""
+    xd = x.double().requires_grad_(True)
+    wd = w.double().requires_grad_(True)
+    bd = b.double().requires_grad_(True)
+    sd = {"ln.weight": wd, "ln.bias": bd}
+    y = OMod.layer_norm(sd, "ln.", xd, eps=eps)
+    y.backward(g.double())
+    return y.detach(), xd.grad, wd.grad, bd.grad
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("rows,feat", [(1, 4), (5, 128), (1000, 512), (4099, 512), (300, 260), (64, 2048)])
+def test_layer_norm_fwd_bwd(device, dtype, rows, feat):
+    """y (x's dtype) plus its bf16 copy; backward with gradients on both outputs, against the fp64 oracle.
+
+    Bars: fp32 outputs 1e-5 * max(1, max|ref|) (the fp32 bar, norm-wise); bf16 outputs one rounding
+    (2^-8 relative) + 1e-5 * scale (the fp32 evaluation's error); dweight / dbias 1e-5 * max(1, max|ref|) plus
+    the fp32 accumulation over the rows (rows * 2^-24 * max|term|)."""
+    from mind_amd.esa.layer_norm import _LayerNorm
+    gen = torch.Generator().manual_seed(rows * 7 + feat)
+    x = (torch.randn(rows, feat, generator=gen) * 3 + 1.5).to(dtype)
+    w = torch.randn(feat, generator=gen)
+    b = torch.randn(feat, generator=gen)
+    gy = torch.randn(rows, feat, generator=gen).to(dtype)
+    gl = torch.randn(rows, feat, generator=gen).to(torch.bfloat16)
+    xd, wd, bd = x.to(device).requires_grad_(True), w.to(device).requires_grad_(True), b.to(device).requires_grad_(True)
+    y, ylp = _LayerNorm.apply(xd, wd, bd, 1e-8, dtype, True, True)
+    assert y.dtype == dtype and ylp.dtype == torch.bfloat16
+    assert torch.equal(ylp, y.to(torch.bfloat16))
+    torch.autograd.backward([y, ylp], [gy.to(device), gl.to(device)])
+    ref, rdx, rdw, rdb = _ln_oracle(x, w, b, gy.double() + gl.double())
+    if dtype == torch.float32:
+        assert_close = lambda got, r, what: _f32_norm_close(got, r, what)  # noqa: E731
+    else:
+        assert_close = lambda got, r, what: _check(got, r, torch.bfloat16, 10 * max(1.0, float(r.abs().max())),  # noqa: E731
+                                                   what)
+    assert_close(y.detach(), ref, "y")
+    _check(ylp.detach(), ref, torch.bfloat16, max(1.0, float(ref.abs().max())), "y_lp")
+    assert_close(xd.grad, rdx, "dx")
+    xhat = (x.double() - x.double().mean(1, keepdim=True)) / x.double().std(1, unbiased=False, keepdim=True)
+    gsum = (gy.double() + gl.double())
+    for got, r, term in ((wd.grad, rdw, gsum * xhat), (bd.grad, rdb, gsum)):
+        acc = rows * 2.0 ** -24 * float(term.abs().max())
+        assert float((got.double().cpu() - r).abs().max()) <= 1e-5 * max(1.0, float(r.abs().max())) + acc
+
+
+def _f32_norm_close(got, ref, what):
+    got = got.detach().double().cpu()
+    bar = 1e-5 * max(1.0, float(ref.abs().max()))
+    assert float((got - ref).abs().max()) <= bar, f"{what}: {float((got - ref).abs().max()):.3e} > {bar:.3e}"
+
+
+def test_layer_norm_module_under_autocast(device):
+    """layer_norm(x, ln) under autocast: y equals F.layer_norm's fp32 output to the fp32 bar, y_lp is y rounded
+    to bf16 bit for bit, gradients reach ln's fp32 parameters; the backward is deterministic."""
+    from mind_amd.esa.layer_norm import layer_norm
+    gen = torch.Generator().manual_seed(11)
+    ln = torch.nn.LayerNorm(512, eps=1e-8).to(device)
+    with torch.no_grad():
+        ln.weight.normal_(generator=None)
+        ln.bias.normal_()
+    x = (torch.randn(3000, 512, generator=gen) * 2).to(device)
+    g = torch.randn(3000, 512, generator=gen).to(device)
+    grads = []
+    for _ in range(2):
+        ln.zero_grad()
+        xd = x.clone().requires_grad_(True)
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            y, ylp = layer_norm(xd, ln, full=True, lowp=True)
+            only_lp = layer_norm(xd, ln, full=False, lowp=True)[1]
+        assert y.dtype == torch.float32 and ylp.dtype == torch.bfloat16
+        assert torch.equal(ylp, y.to(torch.bfloat16)) and torch.equal(only_lp, ylp)
+        ref = torch.nn.functional.layer_norm(x, (512,), ln.weight, ln.bias, 1e-8)
+        _f32_norm_close(y, ref.double().cpu(), "y vs F.layer_norm")
+        (y * g).sum().backward(retain_graph=True)
+        ylp.float().mul(g).sum().backward()
+        grads.append((xd.grad.clone(), ln.weight.grad.clone(), ln.bias.grad.clone()))
+    for a, b in zip(*grads):
+        assert torch.equal(a, b)
+
+
+def test_layer_norm_edge_cases(device):
+    """Constant rows (var = 0: y = bias), no rows (zero parameter gradients), unsupported widths via torch."""
+    from mind_amd.esa.layer_norm import _LayerNorm, layer_norm, supported
+    w = torch.randn(64, device=device, requires_grad=True)
+    b = torch.randn(64, device=device, requires_grad=True)
+    x = torch.full((3, 64), 2.5, device=device)
+    y = _LayerNorm.apply(x, w, b, 1e-8, torch.float32, True, False)
+    assert torch.allclose(y, b.detach().expand(3, 64), atol=1e-6)
+    e = torch.empty(0, 64, device=device, requires_grad=True)
+    ye = _LayerNorm.apply(e, w, b, 1e-8, torch.float32, True, False)
+    ye.sum().backward()
+    assert torch.equal(w.grad, torch.zeros_like(w)) and torch.equal(b.grad, torch.zeros_like(b))
+    ln = torch.nn.LayerNorm(6).to(device)
+    x6 = torch.randn(4, 6, device=device)
+    assert not supported(x6, ln)
+    assert torch.equal(layer_norm(x6, ln)[0], ln(x6))
+    lib = _lib.load()
+    assert lib.esa_layer_norm_fwd(x.data_ptr(), 0, None, None, 3, 6, 1e-8, x.data_ptr(), 0, None, x.data_ptr(),
+                                  x.data_ptr(), None) == -2
