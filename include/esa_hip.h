@@ -219,6 +219,17 @@ ESA_API int esa_layer_norm_bwd(const void* x, int x_dtype, const float* weight,
                        size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------ */
+/* Column sums out[c] = sum_r x[r][c] (fp32, [cols]) of x [rows, cols]      */
+/* (ESA_F32 or ESA_BF16; cols a multiple of 4): the bias gradient of the    */
+/* blocks' nn.Linear layers over packed tokens (their autograd in the       */
+/* reference, esa/mha.py:12-15, esa/mlp_utils.py:18-37).  Fixed summation   */
+/* order (deterministic); workspace size from the query.                    */
+/* ------------------------------------------------------------------------ */
+ESA_API int esa_column_sum_workspace_size(int64_t rows, int cols, size_t* bytes);
+ESA_API int esa_column_sum(const void* x, int dtype, int64_t rows, int cols, float* out,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------ */
 /* Profiling hook (no counterpart in the reference; used by the benchmark).  */
 /* While enabled, every kernel launch of the entry points above is           */
 /* bracketed by hipEvents on its stream.  esa_profile_collect waits for the  */
@@ -226,7 +237,7 @@ ESA_API int esa_layer_norm_bwd(const void* x, int x_dtype, const float* weight,
 /* launch count per kernel id (capacity >= ESA_PROFILE_KERNELS) and clears   */
 /* the record.  Not for concurrent use from several threads.                 */
 /* ------------------------------------------------------------------------ */
-#define ESA_PROFILE_KERNELS 18
+#define ESA_PROFILE_KERNELS 19
 ESA_API int esa_profile_enable(int on);
 ESA_API int esa_profile_collect(float* total_ms, int* launches, int capacity);
 ESA_API const char* esa_profile_kernel_name(int kernel);

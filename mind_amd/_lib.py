@@ -63,12 +63,14 @@ _PROTOS = {
     # x x_dtype w mean rstd dy dy_dtype dy_lp rows features dx dw db ws bytes stream
     "esa_layer_norm_bwd": (_c_int, [_vp, _c_int, _vp, _vp, _vp, _vp, _c_int, _vp, _c_i64, _c_int, _vp, _vp, _vp, _vp,
                                     _c_sz, _vp]),
+    "esa_column_sum_workspace_size": (_c_int, [_c_i64, _c_int, ctypes.POINTER(_c_sz)]),
+    "esa_column_sum": (_c_int, [_vp, _c_int, _c_i64, _c_int, _vp, _vp, _c_sz, _vp]),
     "esa_profile_enable": (_c_int, [_c_int]),
     "esa_profile_collect": (_c_int, [ctypes.POINTER(_c_f), ctypes.POINTER(_c_int), _c_int]),
     "esa_profile_kernel_name": (ctypes.c_char_p, [_c_int]),
 }
 
-PROFILE_KERNELS = 18
+PROFILE_KERNELS = 19
 
 _lock = threading.Lock()
 _lib = None

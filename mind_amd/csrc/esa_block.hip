@@ -368,28 +368,78 @@ __global__ __launch_bounds__(256) void ln_bwd_kernel(const TX* __restrict__ x, c
   }
 }
 
-// dw[c] / db[c] = sum over the backward's block partials in block order:
-// 64 columns per block, four thread groups take every fourth partial, then
-// the groups are added in order.
-__global__ __launch_bounds__(256) void ln_param_grad_kernel(const float* __restrict__ part, int nparts, int D,
-                                                            float* __restrict__ dw, float* __restrict__ db) {
-  __shared__ float s[2][4][64];
-  const int lane = threadIdx.x & 63, grp = threadIdx.x >> 6;
-  const int c = blockIdx.x * 64 + lane;
-  float a = 0.f, bb = 0.f;
-  if (c < D) {
-    for (int p = grp; p < nparts; p += 4) {
-      a += part[(size_t)(2 * p) * D + c];
-      bb += part[(size_t)(2 * p + 1) * D + c];
-    }
+// ---- deterministic column sums of a [nparts][width] fp32 partial matrix
+// Two passes, each a fixed order: slice s of the partial rows summed per
+// column into part2[s], then the slices in order; output columns below
+// `split` go to out0, the rest to out1 (either may be null).  nparts = 0
+// gives zeros.
+constexpr int kRedSlices = 16;
+
+__global__ __launch_bounds__(256) void col_reduce_slices_kernel(const float* __restrict__ part, int nparts, int width,
+                                                                int chunk, float* __restrict__ part2) {
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= width) return;
+  const int p0 = blockIdx.y * chunk, p1 = min(nparts, p0 + chunk);
+  float a = 0.f;
+#pragma unroll 8
+  for (int p = p0; p < p1; ++p) a += part[(size_t)p * width + c];
+  part2[(size_t)blockIdx.y * width + c] = a;
+}
+
+__global__ __launch_bounds__(256) void col_reduce_final_kernel(const float* __restrict__ part2, int slices, int width,
+                                                               int split, float* __restrict__ out0,
+                                                               float* __restrict__ out1) {
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= width) return;
+  float a = 0.f;
+  for (int s = 0; s < slices; ++s) a += part2[(size_t)s * width + c];
+  if (c < split) {
+    if (out0) out0[c] = a;
+  } else if (out1) {
+    out1[c - split] = a;
   }
-  s[0][grp][lane] = a;
-  s[1][grp][lane] = bb;
-  __syncthreads();
-  if (grp == 0 && c < D) {
-    if (dw) dw[c] = ((s[0][0][lane] + s[0][1][lane]) + s[0][2][lane]) + s[0][3][lane];
-    if (db) db[c] = ((s[1][0][lane] + s[1][1][lane]) + s[1][2][lane]) + s[1][3][lane];
+}
+
+size_t reduce_scratch_floats(int width) { return (size_t)kRedSlices * width; }
+
+void reduce_columns(const float* part, int nparts, int width, float* part2, int split, float* out0, float* out1,
+                    hipStream_t st) {
+  const int slices = std::max(1, std::min(kRedSlices, nparts));
+  const int chunk = (nparts + slices - 1) / slices;
+  const unsigned cb = (unsigned)((width + 255) / 256);
+  hipLaunchKernelGGL(col_reduce_slices_kernel, dim3(cb, (unsigned)slices), dim3(256), 0, st, part, nparts, width,
+                     chunk, part2);
+  hipLaunchKernelGGL(col_reduce_final_kernel, dim3(cb), dim3(256), 0, st, part2, slices, width, split, out0, out1);
+}
+
+// ------------------------------------------------------------------ column sums
+// out[c] = sum_r x[r][c] in fp32: the bias gradient of a Linear over packed
+// tokens (the autograd of the blocks' nn.Linear layers, esa/mha.py:12-15,
+// esa/mlp_utils.py:18-37).  Block (i, j) sums 4-column chunks of column tile
+// i over row range j, in row order, into part[j]; reduce_columns adds the
+// row ranges in order.
+constexpr int kColMaxRowBlocks = 1024;
+constexpr int kColMinRows = 32;   // rows per row range at least
+
+int colsum_row_blocks(int64_t rows) {
+  return (int)std::max<int64_t>(1, std::min<int64_t>(kColMaxRowBlocks, (rows + kColMinRows - 1) / kColMinRows));
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void col_sum_partial_kernel(const T* __restrict__ x, int64_t rows, int cols,
+                                                              int64_t rows_per_block, float* __restrict__ part) {
+  const int c = 4 * (blockIdx.x * blockDim.x + threadIdx.x);
+  if (c >= cols) return;
+  const int64_t r0 = (int64_t)blockIdx.y * rows_per_block;
+  const int64_t r1 = std::min<int64_t>(rows, r0 + rows_per_block);
+  f32x4 a = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
+  for (int64_t r = r0; r < r1; ++r) {
+    const f32x4 v = load4(x + r * cols + c);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) a[e] += v[e];
   }
+  store4(part + (size_t)blockIdx.y * cols + c, a);
 }
 
 int ln_chunks(int D) {   // K of the kernels: 4-feature chunks per lane
@@ -460,7 +510,7 @@ extern "C" ESA_API int esa_layer_norm_fwd(const void* x, int x_dtype, const floa
 extern "C" ESA_API int esa_layer_norm_bwd_workspace_size(int64_t rows, int features, size_t* bytes) {
   if (!bytes) return ESA_ERR_NULL;
   if (rows < 0 || features < 4 || features > kLnMaxFeatures || features % 4) return ESA_ERR_SHAPE;
-  *bytes = (size_t)ln_bwd_blocks(rows) * 2 * (size_t)features * sizeof(float);
+  *bytes = ((size_t)ln_bwd_blocks(rows) * 2 * features + reduce_scratch_floats(2 * features)) * sizeof(float);
   return ESA_OK;
 }
 
@@ -472,21 +522,22 @@ extern "C" ESA_API int esa_layer_norm_bwd(const void* x, int x_dtype, const floa
   if ((x_dtype != ESA_F32 && x_dtype != ESA_BF16) || (dy && dy_dtype != ESA_F32 && dy_dtype != ESA_BF16))
     return ESA_ERR_DTYPE;
   const bool params = dweight || dbias;
+  const size_t need = params ? ((size_t)ln_bwd_blocks(rows) * 2 * features + reduce_scratch_floats(2 * features)) *
+                                    sizeof(float)
+                              : 0;
+  if (params && (!workspace || workspace_bytes < need)) return ESA_ERR_WORKSPACE;
+  if (!aligned16(workspace)) return ESA_ERR_ALIGN;
   if (rows == 0) {   // empty input: zero parameter gradients (the reduction over no partials)
     if (params) {
-      hipLaunchKernelGGL(ln_param_grad_kernel, dim3((unsigned)((features + 63) / 64)), dim3(256), 0,
-                         (hipStream_t)stream, nullptr, 0, features, dweight, dbias);
+      reduce_columns(nullptr, 0, 2 * features, (float*)workspace, features, dweight, dbias, (hipStream_t)stream);
       ESA_LAUNCH_CHECK();
     }
     return ESA_OK;
   }
   if (!x || !mean || !rstd || !dx || (!dy && !dy_lp)) return ESA_ERR_NULL;
-  if (!aligned16(x) || !aligned16(weight) || !aligned16(dy) || !aligned16(dy_lp) || !aligned16(dx) ||
-      !aligned16(workspace))
+  if (!aligned16(x) || !aligned16(weight) || !aligned16(dy) || !aligned16(dy_lp) || !aligned16(dx))
     return ESA_ERR_ALIGN;
   const int blocks = ln_bwd_blocks(rows);
-  const size_t need = (size_t)blocks * 2 * (size_t)features * sizeof(float);
-  if (params && (!workspace || workspace_bytes < need)) return ESA_ERR_WORKSPACE;
   float* part = params ? (float*)workspace : nullptr;
   hipStream_t st = (hipStream_t)stream;
   const int K = ln_chunks(features);
@@ -509,8 +560,43 @@ extern "C" ESA_API int esa_layer_norm_bwd(const void* x, int x_dtype, const floa
                   part);
     }
     if (params)
-      hipLaunchKernelGGL(ln_param_grad_kernel, dim3((unsigned)((features + 63) / 64)), dim3(256), 0, st, part, blocks,
-                         features, dweight, dbias);
+      reduce_columns(part, blocks, 2 * features, part + (size_t)blocks * 2 * features, features, dweight, dbias, st);
+  });
+  ESA_LAUNCH_CHECK();
+  return ESA_OK;
+}
+
+extern "C" ESA_API int esa_column_sum_workspace_size(int64_t rows, int cols, size_t* bytes) {
+  if (!bytes) return ESA_ERR_NULL;
+  if (rows < 0 || cols < 4 || cols % 4) return ESA_ERR_SHAPE;
+  *bytes = ((size_t)colsum_row_blocks(rows) * cols + reduce_scratch_floats(cols)) * sizeof(float);
+  return ESA_OK;
+}
+
+extern "C" ESA_API int esa_column_sum(const void* x, int dtype, int64_t rows, int cols, float* out, void* workspace,
+                                      size_t workspace_bytes, void* stream) {
+  if (rows < 0 || cols < 4 || cols % 4) return ESA_ERR_SHAPE;
+  if (dtype != ESA_F32 && dtype != ESA_BF16) return ESA_ERR_DTYPE;
+  if (!out || !workspace || (rows > 0 && !x)) return ESA_ERR_NULL;
+  const int rb = colsum_row_blocks(rows);
+  if (workspace_bytes < ((size_t)rb * cols + reduce_scratch_floats(cols)) * sizeof(float)) return ESA_ERR_WORKSPACE;
+  if (!aligned16(x) || !aligned16(workspace)) return ESA_ERR_ALIGN;
+  hipStream_t st = (hipStream_t)stream;
+  float* part = (float*)workspace;
+  ESA_TIMED(esa_profile::kColumnSum, st, {
+    if (rows > 0) {
+      const int chunks = cols / 4;
+      const int tpb = std::min(256, (chunks + 63) / 64 * 64);
+      const dim3 grid((unsigned)((chunks + tpb - 1) / tpb), (unsigned)rb);
+      const int64_t rpb = (rows + rb - 1) / rb;
+      if (dtype == ESA_F32)
+        hipLaunchKernelGGL(col_sum_partial_kernel<float>, grid, dim3(tpb), 0, st, (const float*)x, rows, cols, rpb,
+                           part);
+      else
+        hipLaunchKernelGGL(col_sum_partial_kernel<bf16>, grid, dim3(tpb), 0, st, (const bf16*)x, rows, cols, rpb,
+                           part);
+    }
+    reduce_columns(part, rows > 0 ? rb : 0, cols, part + (size_t)rb * cols, cols, out, nullptr, st);
   });
   ESA_LAUNCH_CHECK();
   return ESA_OK;

@@ -25,6 +25,7 @@ enum Kernel : int {
   kMishBwd,
   kLayerNormFwd,    // block prologue: pre-norm
   kLayerNormBwd,
+  kColumnSum,       // Linear bias gradients
   kNumKernels
 };
 

@@ -7,17 +7,22 @@ for 256 CUs.  ``linear`` computes it instead as S batched GEMMs over token
 chunks (``torch.bmm`` with fp32 outputs) and sums the S fp32 partials, so the
 reduction fills the chip and is rounded to the weight's dtype once, as the
 single GEMM's fp32 accumulator is.  Forward (F.linear) and dx = g W are
-unchanged; under autocast the inputs are cast as autocast casts F.linear's
-(x, weight and bias to the autocast dtype).
+unchanged; the bias gradient is a deterministic column sum (esa_column_sum).
+Under autocast the inputs are cast as autocast casts F.linear's (x, weight
+and bias to the autocast dtype).
 
 Reference: the nn.Linear layers of the MAB (esa/mha.py:12-15) and of the MLPs
 (esa/mlp_utils.py:18-37).
 """
 from __future__ import annotations
 
+import ctypes
+
 import torch
 from torch import nn
 from torch.nn import functional as F
+
+from .. import _lib
 
 _MIN_CHUNK = 4096               # tokens per chunk: below, a chunk's GEMM is too short to pay
 _MAX_PARTIAL = 16 * 1024 * 1024  # fp32 values of all partials (64 MiB)
@@ -51,6 +56,26 @@ def weight_grad(g: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
     return dw
 
 
+_CODES = {torch.float32: _lib.ESA_F32, torch.bfloat16: _lib.ESA_BF16}
+
+
+def column_sum(g: torch.Tensor) -> torch.Tensor:
+    """g.sum(0) of a device [rows, cols] tensor in fp32 through esa_column_sum (fixed order); shapes the kernel
+    does not take (cols not a multiple of 4, other dtypes) use torch's sum."""
+    rows, cols = g.shape
+    if g.dtype not in _CODES or cols % 4 or cols < 4:
+        return g.float().sum(0)
+    g = g.contiguous()
+    lib = _lib.load()
+    n = ctypes.c_size_t(0)
+    _lib.check(lib.esa_column_sum_workspace_size(rows, cols, ctypes.byref(n)), "esa_column_sum_workspace_size")
+    ws = torch.empty(int(n.value), dtype=torch.uint8, device=g.device)
+    out = torch.empty(cols, dtype=torch.float32, device=g.device)
+    _lib.check(lib.esa_column_sum(g.data_ptr(), _CODES[g.dtype], rows, cols, out.data_ptr(), ws.data_ptr(),
+                                  ws.numel(), _lib.stream_of(g)), "esa_column_sum")
+    return out
+
+
 class _Linear(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, weight, bias):
@@ -64,7 +89,7 @@ class _Linear(torch.autograd.Function):
         g = g.contiguous()
         dx = g.mm(weight) if ctx.needs_input_grad[0] else None
         dw = weight_grad(g, x).to(weight.dtype) if ctx.needs_input_grad[1] else None
-        db = g.sum(0) if ctx.has_bias and ctx.needs_input_grad[2] else None
+        db = column_sum(g).to(g.dtype) if ctx.has_bias and ctx.needs_input_grad[2] else None
         return dx, dw, db
 
 
