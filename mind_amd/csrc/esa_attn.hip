@@ -670,9 +670,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ESA_EDGE_WA
 
 // ======================================================================== fp32 path
 // fp32 q, k, v, outputs and softmax (the reference's fp32 modules, compared
-// at 1e-5 relative).  One thread per (outer token, head) of a 128-token group
-// (the same plan and segment bounds as the bf16 kernels), partner tiles of 32
-// tokens staged in LDS and read by broadcast.  Scores, softmax and both
+// at 1e-5 relative).  One thread per (outer token, head) of a group of up to
+// 128 outer tokens of one segment (a per-segment plan, longest partner range
+// first: a block walks only its own segment's partners, so few-query
+// segments such as PMA seeds get one block per segment and head), partner
+// runs of 32 tokens staged in LDS and read by broadcast.  Scores, softmax and both
 // products are fp32 FMA chains in a fixed order; exp2f / log2f are the
 // device library's correctly rounded-to-1-ulp versions.
 
@@ -682,8 +684,8 @@ struct AttnF32Args {
   int total_q, total_k, heads, tq_pad;
   float c, scale;           // c = softmax_scale * log2(e)
   const int2* nodes;        // edge mask: per-token node pairs (padded)
-  const int4* plan;
-  const int2* bounds;
+  const int4* plan;         // (outer begin, outer segment end, partner begin, partner end) per group
+  const int* count;         // number of groups
   float* o; float* lse_out; float* dq; float* dk; float* dv;
 };
 
@@ -721,20 +723,33 @@ DEVI void axpy16(float a, const float4* y, float x[16]) {
   }
 }
 
-// Stage one 32-token tile of a [T][H][16] fp32 tensor into LDS [32][4] float4
-// (128 threads, one float4 each); tokens past `total` read as zeros.
-DEVI void stage_rows_f32(float4 (*dst)[4], const float* src, int total, int H, int head, int pt, int tid) {
-  const int t = pt * kTile + (tid >> 2), part = tid & 3;
-  dst[tid >> 2][part] = t < total ? reinterpret_cast<const float4*>(src + ((size_t)t * H + head) * kHd)[part]
-                                  : make_float4(0.f, 0.f, 0.f, 0.f);
+// Stage the 32 tokens from t0 of a [T][H][16] fp32 tensor into LDS [32][4]
+// float4 (128 threads, one float4 each); tokens at or past `end` read as zeros.
+DEVI void stage_rows_f32(float4 (*dst)[4], const float* src, int end, int H, int head, int t0, int tid) {
+  const int t = t0 + (tid >> 2), part = tid & 3;
+  dst[tid >> 2][part] = t < end ? reinterpret_cast<const float4*>(src + ((size_t)t * H + head) * kHd)[part]
+                                : make_float4(0.f, 0.f, 0.f, 0.f);
 }
 
-// Admissible partner j of outer token oi (segment partner range [plo, phi)).
+// Admissible partner p (below the segment's partner end phi) of outer token oi.
 template <bool MASKED>
-DEVI bool admissible_f32(int p, int plo, int phi, int oi, int2 pn, int2 own) {
-  bool ok = p >= plo && p < phi;
+DEVI bool admissible_f32(int p, int phi, int oi, int2 pn, int2 own) {
+  bool ok = p < phi;
   if (MASKED) ok = ok && p != oi && node_adjacent(pn, own);
   return ok;
+}
+
+// This thread's outer token of group g (clamped into the group when past its
+// segment's end).
+struct F32Outer { int oi, oc; bool valid; int plo, phi; };
+DEVI F32Outer f32_outer(const int4& g, int tid) {
+  F32Outer o;
+  o.oi = g.x + tid;
+  o.valid = o.oi < g.y;
+  o.oc = o.valid ? o.oi : g.x;
+  o.plo = g.z;
+  o.phi = g.w;
+  return o;
 }
 
 template <bool MASKED>
@@ -743,32 +758,29 @@ __global__ __launch_bounds__(kF32Threads) void attn_fwd_f32_kernel(const AttnF32
   __shared__ int2 sN[kTile];
   const int tid = threadIdx.x, H = a.heads;
   const int item = blockIdx.x / H, head = blockIdx.x - item * H;
-  const int4 pl = a.plan[item];
-  const int oi = pl.x * kGroupTok + tid;
-  const bool valid = oi < a.total_q;
-  const int oc = valid ? oi : a.total_q - 1;
-  const int2 bd = a.bounds[oc];
-  const int plo = valid ? bd.x : 0, phi = valid ? bd.y : 0;
+  if (item >= *a.count) return;
+  const F32Outer ot = f32_outer(a.plan[item], tid);
+  const int oi = ot.oi, oc = ot.oc, phi = ot.phi;
+  const bool valid = ot.valid;
   float q[16], acc[16];
   load16(a.q + ((size_t)oc * H + head) * kHd, q);
 #pragma unroll
   for (int i = 0; i < 16; ++i) acc[i] = 0.f;
   const int2 own = MASKED ? a.nodes[oc] : make_int2(0, 0);
   float m = -INFINITY, l = 0.f;
-  for (int pt = pl.y; pt < pl.z; ++pt) {
+  for (int k0 = ot.plo; k0 < phi; k0 += kTile) {
     __syncthreads();
-    stage_rows_f32(sK, a.k, a.total_k, H, head, pt, tid);
-    stage_rows_f32(sV, a.v, a.total_k, H, head, pt, tid);
-    if (MASKED && tid < kTile) sN[tid] = a.nodes[pt * kTile + tid];
+    stage_rows_f32(sK, a.k, phi, H, head, k0, tid);
+    stage_rows_f32(sV, a.v, phi, H, head, k0, tid);
+    if (MASKED && tid < kTile) sN[tid] = k0 + tid < phi ? a.nodes[k0 + tid] : make_int2(-1, -1);
     __syncthreads();
-    const int k0 = pt * kTile;
-    if (max(plo, k0) >= min(phi, k0 + kTile)) continue;
+    if (!valid) continue;
     float s[kTile];
     float mt = -INFINITY;
 #pragma unroll
     for (int j = 0; j < kTile; ++j) {
       const int2 pn = MASKED ? sN[j] : make_int2(0, 0);
-      s[j] = admissible_f32<MASKED>(k0 + j, plo, phi, oi, pn, own) ? a.c * dot16(q, sK[j]) : -INFINITY;
+      s[j] = admissible_f32<MASKED>(k0 + j, phi, oi, pn, own) ? a.c * dot16(q, sK[j]) : -INFINITY;
       mt = fmaxf(mt, s[j]);
     }
     if (mt == -INFINITY) continue;
@@ -798,12 +810,10 @@ __global__ __launch_bounds__(kF32Threads) void attn_dq_f32_kernel(const AttnF32A
   __shared__ int2 sN[kTile];
   const int tid = threadIdx.x, H = a.heads;
   const int item = blockIdx.x / H, head = blockIdx.x - item * H;
-  const int4 pl = a.plan[item];
-  const int oi = pl.x * kGroupTok + tid;
-  const bool valid = oi < a.total_q;
-  const int oc = valid ? oi : a.total_q - 1;
-  const int2 bd = a.bounds[oc];
-  const int plo = valid ? bd.x : 0, phi = valid ? bd.y : 0;
+  if (item >= *a.count) return;
+  const F32Outer ot = f32_outer(a.plan[item], tid);
+  const int oi = ot.oi, oc = ot.oc, phi = ot.phi;
+  const bool valid = ot.valid;
   float q[16], g[16], acc[16];
   load16(a.q + ((size_t)oc * H + head) * kHd, q);
   load16(a.dout + ((size_t)oc * H + head) * kHd, g);
@@ -811,18 +821,17 @@ __global__ __launch_bounds__(kF32Threads) void attn_dq_f32_kernel(const AttnF32A
   for (int i = 0; i < 16; ++i) acc[i] = 0.f;
   const float2 rs = a.rows[(size_t)head * a.tq_pad + oc];   // (LSE2, D)
   const int2 own = MASKED ? a.nodes[oc] : make_int2(0, 0);
-  for (int pt = pl.y; pt < pl.z; ++pt) {
+  for (int k0 = ot.plo; k0 < phi; k0 += kTile) {
     __syncthreads();
-    stage_rows_f32(sK, a.k, a.total_k, H, head, pt, tid);
-    stage_rows_f32(sV, a.v, a.total_k, H, head, pt, tid);
-    if (MASKED && tid < kTile) sN[tid] = a.nodes[pt * kTile + tid];
+    stage_rows_f32(sK, a.k, phi, H, head, k0, tid);
+    stage_rows_f32(sV, a.v, phi, H, head, k0, tid);
+    if (MASKED && tid < kTile) sN[tid] = k0 + tid < phi ? a.nodes[k0 + tid] : make_int2(-1, -1);
     __syncthreads();
-    const int k0 = pt * kTile;
-    if (max(plo, k0) >= min(phi, k0 + kTile)) continue;
+    if (!valid) continue;
 #pragma unroll
     for (int j = 0; j < kTile; ++j) {
       const int2 pn = MASKED ? sN[j] : make_int2(0, 0);
-      if (!admissible_f32<MASKED>(k0 + j, plo, phi, oi, pn, own)) continue;
+      if (!admissible_f32<MASKED>(k0 + j, phi, oi, pn, own)) continue;
       const float p = exp2f(a.c * dot16(q, sK[j]) - rs.x);
       const float ds = p * (dot16(g, sV[j]) - rs.y);
       axpy16(ds, sK[j], acc);
@@ -841,33 +850,31 @@ __global__ __launch_bounds__(kF32Threads) void attn_dkdv_f32_kernel(const AttnF3
   __shared__ int2 sN[kTile];
   const int tid = threadIdx.x, H = a.heads;
   const int item = blockIdx.x / H, head = blockIdx.x - item * H;
-  const int4 pl = a.plan[item];
-  const int oi = pl.x * kGroupTok + tid;
-  const bool valid = oi < a.total_k;
-  const int oc = valid ? oi : a.total_k - 1;
-  const int2 bd = a.bounds[oc];
-  const int plo = valid ? bd.x : 0, phi = valid ? bd.y : 0;
+  if (item >= *a.count) return;
+  const F32Outer ot = f32_outer(a.plan[item], tid);
+  const int oi = ot.oi, oc = ot.oc, phi = ot.phi;
+  const bool valid = ot.valid;
   float kx[16], vx[16], dk[16], dv[16];
   load16(a.k + ((size_t)oc * H + head) * kHd, kx);
   load16(a.v + ((size_t)oc * H + head) * kHd, vx);
 #pragma unroll
   for (int i = 0; i < 16; ++i) dk[i] = dv[i] = 0.f;
   const int2 own = MASKED ? a.nodes[oc] : make_int2(0, 0);
-  for (int pt = pl.y; pt < pl.z; ++pt) {
+  for (int q0 = ot.plo; q0 < phi; q0 += kTile) {
     __syncthreads();
-    stage_rows_f32(sQ, a.q, a.total_q, H, head, pt, tid);
-    stage_rows_f32(sG, a.dout, a.total_q, H, head, pt, tid);
+    stage_rows_f32(sQ, a.q, phi, H, head, q0, tid);
+    stage_rows_f32(sG, a.dout, phi, H, head, q0, tid);
     if (tid < kTile) {
-      sR[tid] = a.rows[(size_t)head * a.tq_pad + pt * kTile + tid];
-      if (MASKED) sN[tid] = a.nodes[pt * kTile + tid];
+      const bool in = q0 + tid < phi;
+      sR[tid] = in ? a.rows[(size_t)head * a.tq_pad + q0 + tid] : make_float2(INFINITY, 0.f);
+      if (MASKED) sN[tid] = in ? a.nodes[q0 + tid] : make_int2(-1, -1);
     }
     __syncthreads();
-    const int q0 = pt * kTile;
-    if (max(plo, q0) >= min(phi, q0 + kTile)) continue;
+    if (!valid) continue;
 #pragma unroll
     for (int i = 0; i < kTile; ++i) {
       const int2 pn = MASKED ? sN[i] : make_int2(0, 0);
-      if (!admissible_f32<MASKED>(q0 + i, plo, phi, oi, pn, own)) continue;
+      if (!admissible_f32<MASKED>(q0 + i, phi, oi, pn, own)) continue;
       const float2 rs = sR[i];
       const float p = exp2f(a.c * dot16(kx, sQ[i]) - rs.x);
       axpy16(p, sG[i], dv);
@@ -893,6 +900,7 @@ struct PrepArgs {
   const int* cu_q; const int* cu_k; int nseg;
   int total_q, total_k, heads, tq_pad, tk_pad;
   int4* plan_q; int4* plan_k;          // plan_k: backward only
+  int* count_q; int* count_k;          // fp32: per-segment plans (seg_plan_block) and their group counts
   int2* bounds_q; int2* bounds_k;      // bounds_k: backward only
   const bf16* k; float* knorm;         // forward
   const bf16* dout; const bf16* out; const float* lse; float c; uint2* aux;   // backward (bf16)
@@ -1041,9 +1049,17 @@ DEVI void meta_item(const int* __restrict__ src, const int* __restrict__ dst, in
 __global__ __launch_bounds__(256) void prep_kernel(const PrepArgs p) {
   const int tid = threadIdx.x;
   int b = blockIdx.x;
-  if (b < p.nb[kPlanQ]) { plan_block(p.cu_q, p.cu_k, p.nseg, p.total_q, p.plan_q, tid); return; }
+  if (b < p.nb[kPlanQ]) {
+    if (p.count_q) seg_plan_block(p.cu_q, p.cu_k, p.nseg, kGroupTok, p.plan_q, p.count_q, tid);
+    else plan_block(p.cu_q, p.cu_k, p.nseg, p.total_q, p.plan_q, tid);
+    return;
+  }
   b -= p.nb[kPlanQ];
-  if (b < p.nb[kPlanK]) { plan_block(p.cu_k, p.cu_q, p.nseg, p.total_k, p.plan_k, tid); return; }
+  if (b < p.nb[kPlanK]) {
+    if (p.count_k) seg_plan_block(p.cu_k, p.cu_q, p.nseg, kGroupTok, p.plan_k, p.count_k, tid);
+    else plan_block(p.cu_k, p.cu_q, p.nseg, p.total_k, p.plan_k, tid);
+    return;
+  }
   b -= p.nb[kPlanK];
   if (b < p.nb[kKnorm]) { knorm_block(p.k, p.total_k, p.heads, p.tk_pad / kTile, p.knorm, b, tid); return; }
   b -= p.nb[kKnorm];
@@ -1108,10 +1124,14 @@ WsLayout ws_layout(int total_q, int total_k, int heads, int dtype, bool masked, 
   } else {
     L.aux = off; off += align256((size_t)heads * tqp * 8);   // bf16: uint2 (hi, lo) pairs; fp32: float2 rows
   }
-  L.plan_q = off; off += align256((size_t)groups_of(total_q) * 16 + 16);
+  // fp32: a 16-byte group count, then per-segment groups (at most ceil(T / 128) + number of segments <= T).
+  auto plan_size = [&](int t) {
+    return align256(dtype == ESA_F32 ? 16 + ((size_t)groups_of(t) + t + 1) * 16 : (size_t)groups_of(t) * 16 + 16);
+  };
+  L.plan_q = off; off += plan_size(total_q);
   L.bounds_q = off; off += align256((size_t)tqp * 8);
   if (backward) {
-    L.plan_k = off; off += align256((size_t)groups_of(total_k) * 16 + 16);
+    L.plan_k = off; off += plan_size(total_k);
     L.bounds_k = off; off += align256((size_t)tkp * 8);
   }
   if (masked) {
@@ -1237,7 +1257,8 @@ int esa_varlen_attn_fwd(const void* q, const void* k, const void* v, const int* 
   pa.cu_q = cu_seqlens_q; pa.cu_k = cu_seqlens_k; pa.nseg = batch;
   pa.total_q = total_q; pa.total_k = total_k; pa.heads = heads;
   pa.tq_pad = round32(total_q); pa.tk_pad = round32(total_k);
-  pa.plan_q = reinterpret_cast<int4*>(ws + L.plan_q);
+  pa.plan_q = reinterpret_cast<int4*>(ws + L.plan_q + (f32 ? 16 : 0));
+  if (f32) pa.count_q = reinterpret_cast<int*>(ws + L.plan_q);
   pa.bounds_q = reinterpret_cast<int2*>(ws + L.bounds_q);
   if (!f32) { pa.k = static_cast<const bf16*>(k); pa.knorm = reinterpret_cast<float*>(ws + L.knorm); }
   if (masked) {
@@ -1253,12 +1274,13 @@ int esa_varlen_attn_fwd(const void* q, const void* k, const void* v, const int* 
     a.q = static_cast<const float*>(q); a.k = static_cast<const float*>(k); a.v = static_cast<const float*>(v);
     a.total_q = total_q; a.total_k = total_k; a.heads = heads; a.tq_pad = pa.tq_pad;
     a.c = softmax_scale * kLog2e; a.scale = softmax_scale;
-    a.nodes = pa.nodes; a.plan = pa.plan_q; a.bounds = pa.bounds_q;
+    a.nodes = pa.nodes; a.plan = pa.plan_q; a.count = pa.count_q;
     a.o = static_cast<float*>(out); a.lse_out = softmax_lse;
+    const dim3 fgrid((unsigned)(groups_of(total_q) + batch) * (unsigned)heads);
     if (masked)
-      hipLaunchKernelGGL((attn_fwd_f32_kernel<true>), dim3(grid), dim3(kF32Threads), 0, st, a);
+      hipLaunchKernelGGL((attn_fwd_f32_kernel<true>), fgrid, dim3(kF32Threads), 0, st, a);
     else
-      hipLaunchKernelGGL((attn_fwd_f32_kernel<false>), dim3(grid), dim3(kF32Threads), 0, st, a);
+      hipLaunchKernelGGL((attn_fwd_f32_kernel<false>), fgrid, dim3(kF32Threads), 0, st, a);
     ESA_LAUNCH_CHECK();
     return ESA_OK;
   }
@@ -1343,8 +1365,12 @@ int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k, const vo
   pa.cu_q = cu_seqlens_q; pa.cu_k = cu_seqlens_k; pa.nseg = batch;
   pa.total_q = total_q; pa.total_k = total_k; pa.heads = heads;
   pa.tq_pad = round32(total_q); pa.tk_pad = round32(total_k);
-  pa.plan_q = reinterpret_cast<int4*>(ws + L.plan_q);
-  pa.plan_k = reinterpret_cast<int4*>(ws + L.plan_k);
+  pa.plan_q = reinterpret_cast<int4*>(ws + L.plan_q + (f32 ? 16 : 0));
+  pa.plan_k = reinterpret_cast<int4*>(ws + L.plan_k + (f32 ? 16 : 0));
+  if (f32) {
+    pa.count_q = reinterpret_cast<int*>(ws + L.plan_q);
+    pa.count_k = reinterpret_cast<int*>(ws + L.plan_k);
+  }
   pa.bounds_q = reinterpret_cast<int2*>(ws + L.bounds_q);
   pa.bounds_k = reinterpret_cast<int2*>(ws + L.bounds_k);
   pa.lse = softmax_lse; pa.c = softmax_scale * kLog2e;
@@ -1373,17 +1399,19 @@ int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k, const vo
     a.c = softmax_scale * kLog2e; a.scale = softmax_scale;
     a.nodes = pa.nodes;
     a.dq = static_cast<float*>(dq); a.dk = static_cast<float*>(dk); a.dv = static_cast<float*>(dv);
-    a.plan = pa.plan_k; a.bounds = pa.bounds_k;
+    a.plan = pa.plan_k; a.count = pa.count_k;
+    const dim3 fkgrid((unsigned)(groups_of(total_k) + batch) * (unsigned)heads);
+    const dim3 fqgrid((unsigned)(groups_of(total_q) + batch) * (unsigned)heads);
     if (masked)
-      hipLaunchKernelGGL((attn_dkdv_f32_kernel<true>), dim3(kgrid), dim3(kF32Threads), 0, st, a);
+      hipLaunchKernelGGL((attn_dkdv_f32_kernel<true>), fkgrid, dim3(kF32Threads), 0, st, a);
     else
-      hipLaunchKernelGGL((attn_dkdv_f32_kernel<false>), dim3(kgrid), dim3(kF32Threads), 0, st, a);
+      hipLaunchKernelGGL((attn_dkdv_f32_kernel<false>), fkgrid, dim3(kF32Threads), 0, st, a);
     ESA_LAUNCH_CHECK();
-    a.plan = pa.plan_q; a.bounds = pa.bounds_q;
+    a.plan = pa.plan_q; a.count = pa.count_q;
     if (masked)
-      hipLaunchKernelGGL((attn_dq_f32_kernel<true>), dim3(qgrid), dim3(kF32Threads), 0, st, a);
+      hipLaunchKernelGGL((attn_dq_f32_kernel<true>), fqgrid, dim3(kF32Threads), 0, st, a);
     else
-      hipLaunchKernelGGL((attn_dq_f32_kernel<false>), dim3(qgrid), dim3(kF32Threads), 0, st, a);
+      hipLaunchKernelGGL((attn_dq_f32_kernel<false>), fqgrid, dim3(kF32Threads), 0, st, a);
     ESA_LAUNCH_CHECK();
     return ESA_OK;
   }

@@ -234,4 +234,56 @@ DEVI uint32_t split_bf16_pair(float x) {
   return (uint32_t)__builtin_bit_cast(uint16_t, hi) | ((uint32_t)__builtin_bit_cast(uint16_t, lo) << 16);
 }
 
+// ---- per-segment work plans (dense bf16 and fp32 attention kernels)
+// Groups of one direction: every segment's outer tokens cut into groups of
+// `gtok` tokens (one block each), segments ordered by partner tiles (longest first, counting sort in
+// one block; segments with equal counts in any order, which changes no
+// result).  groups[i] = (outer begin, outer segment end, inner begin, inner end).
+constexpr int kPlanBuckets = 1024;
+
+DEVI void seg_plan_block(const int* __restrict__ cu_outer, const int* __restrict__ cu_inner, int nseg, int gtok,
+                         int4* __restrict__ groups, int* __restrict__ count, int tid) {
+  constexpr int PER = kPlanBuckets / 256;
+  __shared__ int hist[kPlanBuckets];
+  __shared__ int part[256];
+  for (int i = tid; i < kPlanBuckets; i += 256) hist[i] = 0;
+  __syncthreads();
+  auto bucket = [&](int s) {
+    const int tiles = (cu_inner[s + 1] - cu_inner[s] + kTile - 1) / kTile;
+    return kPlanBuckets - 1 - min(max(tiles, 0), kPlanBuckets - 1);
+  };
+  for (int s = tid; s < nseg; s += 256) {
+    const int n = cu_outer[s + 1] - cu_outer[s];
+    if (n > 0) atomicAdd(&hist[bucket(s)], (n + gtok - 1) / gtok);
+  }
+  __syncthreads();
+  int loc[PER], sum = 0;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    loc[i] = sum;
+    sum += hist[tid * PER + i];
+  }
+  part[tid] = sum;
+  __syncthreads();
+  for (int off = 1; off < 256; off <<= 1) {
+    const int add = tid >= off ? part[tid - off] : 0;
+    __syncthreads();
+    part[tid] += add;
+    __syncthreads();
+  }
+  const int base = part[tid] - sum;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) hist[tid * PER + i] = base + loc[i];
+  if (tid == 255) *count = part[255];
+  __syncthreads();
+  for (int s = tid; s < nseg; s += 256) {
+    const int ob = cu_outer[s], oe = cu_outer[s + 1];
+    if (oe <= ob) continue;
+    const int ng = (oe - ob + gtok - 1) / gtok;
+    const int pos = atomicAdd(&hist[bucket(s)], ng);
+    const int ib = cu_inner[s], ie = cu_inner[s + 1];
+    for (int j = 0; j < ng; ++j) groups[pos + j] = make_int4(ob + j * gtok, oe, ib, max(ie, ib));
+  }
+}
+
 }  // namespace

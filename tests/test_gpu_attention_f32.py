@@ -64,9 +64,11 @@ def test_f32_dense_ragged(device, lengths):
 
 
 @pytest.mark.parametrize("seeds", [1, 4])
-def test_f32_cross_attention_pma_shape(device, seeds):
-    lk = [50, 1, 130, 77]
-    _check(device, [seeds] * len(lk), lk, seed=seeds + 1100)
+@pytest.mark.parametrize("lk", [[50, 1, 130, 77], [0, 9, 0, 260, 3], list(range(1, 41))])
+def test_f32_cross_attention_pma_shape(device, seeds, lk):
+    """PMA: k seeds per graph over the graph's tokens; graphs without tokens give zero rows; many short
+    segments (each segment's queries form their own group)."""
+    _check(device, [seeds] * len(lk), lk, seed=seeds + 1100 + len(lk))
 
 
 def test_f32_masked_small_molecules(device):
