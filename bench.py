@@ -720,7 +720,7 @@ def bench_stack(args):
                 prm.normal_(0.0, 0.02)
             elif name.endswith("bias"):
                 prm.zero_()
-    opt = torch.optim.AdamW(model.parameters(), lr=1e-4)
+    opt = torch.optim.AdamW(model.parameters(), lr=1e-4, fused=True)   # one fused update kernel per dtype group
     n = nearest_multiple_of_8(gb.max_seqlen + 1)
     ei = torch.as_tensor(gb.edge_index).to(dev)
     bm = torch.as_tensor(gb.batch).to(dev)
