@@ -191,6 +191,19 @@ ESA_API int esa_mish_bwd(const void* z, const void* grad, int64_t n, int dtype,
                  void* dz, void* stream);
 
 /* ------------------------------------------------------------------------ */
+/* The block residual over the MAB epilogue: y = x + r(o + mish(z)), x and y */
+/* fp32 [n] (the pre-norm block's residual stream, esa/masked_layers.py:    */
+/* 471-472), z = fc_o(o) and o of `dtype` (esa/mha.py:87), r() the rounding */
+/* to dtype that the MAB output gets.  Backward from g (fp32): g_o = r(g)   */
+/* (o's gradient through the residual) and dz = r(g_o * mish'(z)); x's      */
+/* gradient is g.                                                            */
+/* ------------------------------------------------------------------------ */
+ESA_API int esa_mab_residual_fwd(const void* z, const void* o, const float* x, int64_t n,
+                         int dtype, float* y, void* stream);
+ESA_API int esa_mab_residual_bwd(const void* z, const float* g, int64_t n, int dtype,
+                         void* dz, void* g_o, void* stream);
+
+/* ------------------------------------------------------------------------ */
 /* Pre-norm LayerNorm over the last dimension of [rows, features] (features */
 /* a multiple of 4, at most 2048): nn.LayerNorm(features, eps) as the ESA    */
 /* blocks apply it (esa/utils/norm_layers.py:36; esa/masked_layers.py:418-  */

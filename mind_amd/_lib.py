@@ -65,6 +65,8 @@ _PROTOS = {
                                     _c_sz, _vp]),
     "esa_column_sum_workspace_size": (_c_int, [_c_i64, _c_int, ctypes.POINTER(_c_sz)]),
     "esa_column_sum": (_c_int, [_vp, _c_int, _c_i64, _c_int, _vp, _vp, _c_sz, _vp]),
+    "esa_mab_residual_fwd": (_c_int, [_vp, _vp, _vp, _c_i64, _c_int, _vp, _vp]),
+    "esa_mab_residual_bwd": (_c_int, [_vp, _vp, _c_i64, _c_int, _vp, _vp, _vp]),
     "esa_profile_enable": (_c_int, [_c_int]),
     "esa_profile_collect": (_c_int, [ctypes.POINTER(_c_f), ctypes.POINTER(_c_int), _c_int]),
     "esa_profile_kernel_name": (ctypes.c_char_p, [_c_int]),

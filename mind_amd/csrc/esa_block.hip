@@ -473,6 +473,141 @@ void ln_bwd_go(int K, dim3 grid, hipStream_t st, const TX* x, const float* w, co
 #undef ESA_LN_BWD
 }
 
+// ------------------------------------------------------------------ MAB residual epilogue
+// The block residual on top of the MAB epilogue (esa/masked_layers.py:471-472
+// over esa/mha.py:87): y = x + r(o + mish(z)) with the residual stream x, y
+// in fp32, z = fc_o(o) and o of type T, and r() the rounding to T that the
+// MAB's own output gets.  Backward: g_o = r(g) (the gradient of o through the
+// residual, and what fc_o's input gradient adds to) and dz = r(g_o mish'(z));
+// x's gradient is g itself.  Four values per thread and step (16 bytes of
+// fp32), kUnroll steps in flight.
+DEVI float round_to(float v, float*) { return v; }
+DEVI float round_to(float v, bf16*) { return (float)(bf16)v; }
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void mab_residual_fwd_kernel(const T* __restrict__ z, const T* __restrict__ o,
+                                                                    const float* __restrict__ x,
+                                                                    float* __restrict__ y, int64_t quads) {
+  const int64_t c0 = (int64_t)blockIdx.x * (kUnroll * kThreads) + threadIdx.x;
+  f32x4 zv[kUnroll], ov[kUnroll], xv[kUnroll];
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int64_t c = c0 + u * kThreads;
+    if (c < quads) {
+      zv[u] = load4(z + 4 * c);
+      ov[u] = load4(o + 4 * c);
+      xv[u] = load4(x + 4 * c);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int64_t c = c0 + u * kThreads;
+    if (c >= quads) break;
+    f32x4 r;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) r[e] = xv[u][e] + round_to(ov[u][e] + mish_f(zv[u][e]), (T*)nullptr);
+    store4(y + 4 * c, r);
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void mab_residual_bwd_kernel(const T* __restrict__ z,
+                                                                    const float* __restrict__ g,
+                                                                    T* __restrict__ dz, T* __restrict__ g_o,
+                                                                    int64_t quads) {
+  const int64_t c0 = (int64_t)blockIdx.x * (kUnroll * kThreads) + threadIdx.x;
+  f32x4 zv[kUnroll], gv[kUnroll];
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int64_t c = c0 + u * kThreads;
+    if (c < quads) {
+      zv[u] = load4(z + 4 * c);
+      gv[u] = load4(g + 4 * c);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int64_t c = c0 + u * kThreads;
+    if (c >= quads) break;
+    f32x4 gl, d;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      gl[e] = round_to(gv[u][e], (T*)nullptr);
+      d[e] = gl[e] * mish_grad_f(zv[u][e]);
+    }
+    store4(g_o + 4 * c, gl);
+    store4(dz + 4 * c, d);
+  }
+}
+
+// Element-wise forms over [begin, end): the tail and misaligned pointers.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void mab_residual_fwd_elems_kernel(const T* z, const T* o, const float* x,
+                                                                          float* y, int64_t begin, int64_t end) {
+  for (int64_t i = begin + (int64_t)blockIdx.x * kThreads + threadIdx.x; i < end; i += (int64_t)gridDim.x * kThreads)
+    y[i] = x[i] + round_to(load_f(o, i) + mish_f(load_f(z, i)), (T*)nullptr);
+}
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void mab_residual_bwd_elems_kernel(const T* z, const float* g, T* dz, T* g_o,
+                                                                          int64_t begin, int64_t end) {
+  for (int64_t i = begin + (int64_t)blockIdx.x * kThreads + threadIdx.x; i < end;
+       i += (int64_t)gridDim.x * kThreads) {
+    const float gl = round_to(g[i], (T*)nullptr);
+    g_o[i] = (T)gl;
+    dz[i] = (T)(gl * mish_grad_f(load_f(z, i)));
+  }
+}
+
+// Quad-chunked launch over the aligned prefix plus an element-wise launch over the rest.
+template <class QuadGo, class ElemsGo>
+int launch_quads(int64_t n, bool vec_ok, QuadGo quad_go, ElemsGo elems_go) {
+  const int64_t quads = vec_ok ? n / 4 : 0;
+  if (quads > 0) {
+    const int64_t blocks = (quads + kUnroll * kThreads - 1) / (kUnroll * kThreads);
+    if (blocks > INT32_MAX) return ESA_ERR_SHAPE;
+    quad_go(dim3((unsigned)blocks), quads);
+  }
+  const int64_t begin = quads * 4;
+  if (begin < n) elems_go(dim3(elem_blocks(n - begin)), begin, n);
+  ESA_LAUNCH_CHECK();
+  return ESA_OK;
+}
+
+template <typename T>
+int mab_residual_fwd_typed(const T* z, const T* o, const float* x, float* y, int64_t n, hipStream_t st) {
+  const bool vec_ok = aligned16(z) && aligned16(o) && aligned16(x) && aligned16(y);
+  int rc = ESA_OK;
+  ESA_TIMED(esa_profile::kMishFwd, st,
+            rc = launch_quads(
+                n, vec_ok,
+                [&](dim3 grid, int64_t quads) {
+                  hipLaunchKernelGGL(mab_residual_fwd_kernel<T>, grid, dim3(kThreads), 0, st, z, o, x, y, quads);
+                },
+                [&](dim3 grid, int64_t b, int64_t e) {
+                  hipLaunchKernelGGL(mab_residual_fwd_elems_kernel<T>, grid, dim3(kThreads), 0, st, z, o, x, y, b,
+                                     e);
+                }));
+  return rc;
+}
+
+template <typename T>
+int mab_residual_bwd_typed(const T* z, const float* g, T* dz, T* g_o, int64_t n, hipStream_t st) {
+  const bool vec_ok = aligned16(z) && aligned16(g) && aligned16(dz) && aligned16(g_o);
+  int rc = ESA_OK;
+  ESA_TIMED(esa_profile::kMishBwd, st,
+            rc = launch_quads(
+                n, vec_ok,
+                [&](dim3 grid, int64_t quads) {
+                  hipLaunchKernelGGL(mab_residual_bwd_kernel<T>, grid, dim3(kThreads), 0, st, z, g, dz, g_o, quads);
+                },
+                [&](dim3 grid, int64_t b, int64_t e) {
+                  hipLaunchKernelGGL(mab_residual_bwd_elems_kernel<T>, grid, dim3(kThreads), 0, st, z, g, dz, g_o, b,
+                                     e);
+                }));
+  return rc;
+}
+
 }  // namespace
 
 extern "C" ESA_API int esa_layer_norm_fwd(const void* x, int x_dtype, const float* weight, const float* bias,
@@ -600,6 +735,28 @@ extern "C" ESA_API int esa_column_sum(const void* x, int dtype, int64_t rows, in
   });
   ESA_LAUNCH_CHECK();
   return ESA_OK;
+}
+
+extern "C" ESA_API int esa_mab_residual_fwd(const void* z, const void* o, const float* x, int64_t n, int dtype,
+                                            float* y, void* stream) {
+  if (n < 0) return ESA_ERR_SHAPE;
+  if (dtype != ESA_F32 && dtype != ESA_BF16) return ESA_ERR_DTYPE;
+  if (n == 0) return ESA_OK;
+  if (!z || !o || !x || !y) return ESA_ERR_NULL;
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == ESA_F32) return mab_residual_fwd_typed((const float*)z, (const float*)o, x, y, n, st);
+  return mab_residual_fwd_typed((const bf16*)z, (const bf16*)o, x, y, n, st);
+}
+
+extern "C" ESA_API int esa_mab_residual_bwd(const void* z, const float* g, int64_t n, int dtype, void* dz, void* g_o,
+                                            void* stream) {
+  if (n < 0) return ESA_ERR_SHAPE;
+  if (dtype != ESA_F32 && dtype != ESA_BF16) return ESA_ERR_DTYPE;
+  if (n == 0) return ESA_OK;
+  if (!z || !g || !dz || !g_o) return ESA_ERR_NULL;
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == ESA_F32) return mab_residual_bwd_typed((const float*)z, g, (float*)dz, (float*)g_o, n, st);
+  return mab_residual_bwd_typed((const bf16*)z, g, (bf16*)dz, (bf16*)g_o, n, st);
 }
 
 extern "C" ESA_API int esa_mish_fwd(const void* z, const void* residual, int64_t n, int dtype, void* y,

@@ -1,5 +1,10 @@
 """Mish and the MAB's ``out + mish(fc_o(out))`` epilogue on the gfx950 kernels.
 
+``mab_epilogue(o, fc_o, residual)`` fuses the whole epilogue of a MAB on
+packed rows: fc_o's GEMM, Mish and the residual(s) in one pass
+(``esa_mish_fwd``, or ``esa_mab_residual_fwd`` with the block's fp32
+residual stream), and a backward whose input gradient needs no add kernel.
+
 ``mish(z, residual)`` computes ``residual + mish(z)`` (``mish(z)`` without a
 residual) in one pass, evaluated in fp32 and rounded once, through
 ``esa_mish_fwd``; its backward is ``esa_mish_bwd``.  It serves the reference's
@@ -58,6 +63,65 @@ def mish(z: torch.Tensor, residual: torch.Tensor | None = None) -> torch.Tensor:
         # Mixed precision or broadcasting: torch's promotion rules for the add.
         return residual + _Mish.apply(z, None)
     return _Mish.apply(z, residual)
+
+
+class _MabEpilogue(torch.autograd.Function):
+    """y = o + mish(fc_o(o)) (x is None) or y = x + r(o + mish(fc_o(o))) (x the block's fp32 residual, r() the
+    rounding to o's dtype): fc_o's GEMM, then esa_mish_fwd / esa_mab_residual_fwd.  Backward: one kernel gives
+    dz (and o's residual gradient r(g) when x is given), and o's gradient is r(g) + dz W in one GEMM (addmm,
+    beta = 1)."""
+
+    @staticmethod
+    def forward(ctx, o, weight, bias, x):
+        z = F.linear(o, weight, bias)
+        lib, st, code = _lib.load(), _lib.stream_of(o), _DTYPES[o.dtype]
+        if x is None:
+            y = torch.empty_like(z)
+            _lib.check(lib.esa_mish_fwd(z.data_ptr(), o.data_ptr(), z.numel(), code, y.data_ptr(), st),
+                       "esa_mish_fwd")
+        else:
+            y = torch.empty(x.shape, dtype=torch.float32, device=x.device)
+            _lib.check(lib.esa_mab_residual_fwd(z.data_ptr(), o.data_ptr(), x.data_ptr(), z.numel(), code,
+                                                y.data_ptr(), st), "esa_mab_residual_fwd")
+        ctx.save_for_backward(o, weight, z)
+        ctx.has_x, ctx.has_bias = x is not None, bias is not None
+        return y
+
+    @staticmethod
+    def backward(ctx, g):
+        from .linear import column_sum, weight_grad   # deferred: linear.py is a sibling with its own imports
+        o, weight, z = ctx.saved_tensors
+        lib, st, code = _lib.load(), _lib.stream_of(z), _DTYPES[z.dtype]
+        dz = torch.empty_like(z)
+        if ctx.has_x:
+            g = g.float().contiguous()
+            g_o = torch.empty_like(z)
+            _lib.check(lib.esa_mab_residual_bwd(z.data_ptr(), g.data_ptr(), z.numel(), code, dz.data_ptr(),
+                                                g_o.data_ptr(), st), "esa_mab_residual_bwd")
+        else:
+            g_o = g.to(z.dtype).contiguous()
+            _lib.check(lib.esa_mish_bwd(z.data_ptr(), g_o.data_ptr(), z.numel(), code, dz.data_ptr(), st),
+                       "esa_mish_bwd")
+        do = torch.addmm(g_o, dz, weight) if ctx.needs_input_grad[0] else None
+        dw = weight_grad(dz, o).to(weight.dtype) if ctx.needs_input_grad[1] else None
+        db = column_sum(dz).to(dz.dtype) if ctx.has_bias and ctx.needs_input_grad[2] else None
+        return do, dw, db, (g if ctx.has_x and ctx.needs_input_grad[3] else None)
+
+
+def mab_epilogue(o: torch.Tensor, fc_o: nn.Linear, residual: torch.Tensor | None = None) -> torch.Tensor:
+    """``o + mish(fc_o(o))`` (esa/mha.py:87) on 2-D token rows, plus the block residual when given
+    (``residual + (o + mish(fc_o(o)))``, esa/masked_layers.py:471-472), fused on device tensors."""
+    if not o.is_cuda:
+        y = o + F.mish(fc_o(o))
+        return y if residual is None else residual + y
+    from .linear import autocast_params
+    o, w, b = autocast_params(o, fc_o.weight, fc_o.bias)
+    if o.dtype not in _DTYPES or w.dtype != o.dtype or (b is not None and b.dtype != o.dtype) or o.dim() != 2:
+        y = mish(F.linear(o, w, b), o)
+        return y if residual is None else residual + y
+    if residual is not None and (residual.dtype != torch.float32 or residual.shape != o.shape):
+        return residual + _MabEpilogue.apply(o.contiguous(), w, b, None)
+    return _MabEpilogue.apply(o.contiguous(), w, b, None if residual is None else residual.contiguous())
 
 
 class Mish(nn.Mish):

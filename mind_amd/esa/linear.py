@@ -97,15 +97,78 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = No
     """F.linear(x, weight, bias) with the split-K weight gradient (device tensors; CPU tensors use F.linear)."""
     if not x.is_cuda:
         return F.linear(x, weight, bias)
-    if torch.is_autocast_enabled("cuda"):
-        dt = torch.get_autocast_dtype("cuda")
-        x, weight = x.to(dt), weight.to(dt)
-        bias = None if bias is None else bias.to(dt)
+    x, weight, bias = autocast_params(x, weight, bias)
     if x.dtype != weight.dtype or (bias is not None and bias.dtype != x.dtype):
         return F.linear(x, weight, bias)   # mixed dtypes: torch's own type checks and errors
     lead = x.shape[:-1]
     y = _Linear.apply(x.reshape(-1, x.shape[-1]).contiguous(), weight, bias)
     return y.view(*lead, weight.shape[0])
+
+
+def autocast_params(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None):
+    """(x, weight, bias) cast as autocast casts F.linear's inputs (unchanged outside autocast)."""
+    if x.is_cuda and torch.is_autocast_enabled("cuda"):
+        dt = torch.get_autocast_dtype("cuda")
+        return x.to(dt), weight.to(dt), None if bias is None else bias.to(dt)
+    return x, weight, bias
+
+
+class _QKV(torch.autograd.Function):
+    """q = fc_q(xq), k = fc_k(xk), v = fc_v(xk) (the MAB's V = fc_v(K), esa/mha.py:54-56).  The backward
+    accumulates the input gradients of the projections that share an input in the GEMMs themselves
+    (addmm with beta = 1) instead of separate add kernels, so self-attention's dx = gq Wq + gk Wk + gv Wv is
+    three GEMMs and no add."""
+
+    @staticmethod
+    def forward(ctx, xq, xk, wq, bq, wk, bk, wv, bv):
+        same = xk is None
+        xk_ = xq if same else xk
+        q = F.linear(xq, wq, bq)
+        k = F.linear(xk_, wk, bk)
+        v = F.linear(xk_, wv, bv)
+        ctx.save_for_backward(xq, None if same else xk, wq, wk, wv)
+        ctx.same = same
+        ctx.biases = (bq is not None, bk is not None, bv is not None)
+        return q, k, v
+
+    @staticmethod
+    def backward(ctx, gq, gk, gv):
+        xq, xk, wq, wk, wv = ctx.saved_tensors
+        xk = xq if ctx.same else xk
+        gq, gk, gv = gq.contiguous(), gk.contiguous(), gv.contiguous()
+        dxq = dxk = None
+        if ctx.same:
+            if ctx.needs_input_grad[0]:
+                dxq = gq.mm(wq)
+                dxq.addmm_(gk, wk)
+                dxq.addmm_(gv, wv)
+        else:
+            if ctx.needs_input_grad[0]:
+                dxq = gq.mm(wq)
+            if ctx.needs_input_grad[1]:
+                dxk = gk.mm(wk)
+                dxk.addmm_(gv, wv)
+        grads = [dxq, dxk]
+        for i, (g, x, w) in enumerate(((gq, xq, wq), (gk, xk, wk), (gv, xk, wv))):
+            dw = weight_grad(g, x).to(w.dtype) if ctx.needs_input_grad[2 + 2 * i] else None
+            db = (column_sum(g).to(g.dtype) if ctx.biases[i] and ctx.needs_input_grad[3 + 2 * i] else None)
+            grads += [dw, db]
+        return tuple(grads)
+
+
+def qkv_projection(fc_q: nn.Linear, fc_k: nn.Linear, fc_v: nn.Linear, xq: torch.Tensor, xk: torch.Tensor):
+    """(fc_q(xq), fc_k(xk), fc_v(xk)) on 2-D token rows, with the fused-accumulation backward of _QKV on
+    device tensors (``xk is xq`` for self-attention)."""
+    if not xq.is_cuda:
+        return fc_q(xq), fc_k(xk), fc_v(xk)
+    same = xk is xq
+    xq, wq, bq = autocast_params(xq, fc_q.weight, fc_q.bias)
+    xk_, wk, bk = autocast_params(xk, fc_k.weight, fc_k.bias)
+    _, wv, bv = autocast_params(xk, fc_v.weight, fc_v.bias)
+    dts = {t.dtype for t in (xq, xk_, wq, wk, wv)}
+    if len(dts) != 1:
+        return F.linear(xq, wq, bq), F.linear(xk_, wk, bk), F.linear(xk_, wv, bv)
+    return _QKV.apply(xq.contiguous(), None if same else xk_.contiguous(), wq, bq, wk, bk, wv, bv)
 
 
 def apply(layer: nn.Module, x: torch.Tensor) -> torch.Tensor:

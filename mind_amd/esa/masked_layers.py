@@ -31,10 +31,10 @@ import torch
 from torch import nn
 from torch.nn import functional as F
 
-from .activations import mish
+from .activations import mab_epilogue, mish
 from .attention import varlen_attention
 from .layer_norm import layer_norm
-from .linear import apply
+from .linear import apply, qkv_projection
 from .mha import PMA, SAB, _heads, _uniform_cu, pooled_attention
 from .mha_flash_varlen import PMAFlashVarlen, SABFlashVarlen
 from .mlp_utils import GatedMLPMulti, SmallMLP
@@ -151,16 +151,14 @@ def _sab_valid_only(sab: SAB, X: torch.Tensor, tokens: PackedSets) -> torch.Tens
 
 
 def _packed_mab(mab, xq: torch.Tensor, xk: torch.Tensor, cu_q: torch.Tensor, cu_k: torch.Tensor, max_q: int,
-                max_k: int, mask_kwargs: dict) -> torch.Tensor:
+                max_k: int, mask_kwargs: dict, residual: torch.Tensor | None = None) -> torch.Tensor:
     """MAB (esa/mha.py:48-89, V = fc_v(K)) on packed rows: queries xq [Tq, D] and keys xk [Tk, D] grouped by
-    cu_q / cu_k -> [Tq, D]."""
-    q = apply(mab.fc_q, xq)
-    v = apply(mab.fc_v, xk)
-    k = apply(mab.fc_k, xk)
+    cu_q / cu_k -> [Tq, D] (``xk is xq`` for self-attention), plus the block residual when given.  The
+    projections and the fc_o + Mish epilogue run fused (qkv_projection, mab_epilogue)."""
+    q, k, v = qkv_projection(mab.fc_q, mab.fc_k, mab.fc_v, xq, xk)
     h, d = mab.num_heads, q.shape[-1]
     out = varlen_attention(_heads(q, h), _heads(k, h), _heads(v, h), cu_q, cu_k, max_q, max_k, **mask_kwargs)
-    out = out.reshape(-1, d).to(q.dtype)
-    return mish(apply(mab.fc_o, out), out)
+    return mab_epilogue(out.reshape(-1, d).to(q.dtype), mab.fc_o, residual)
 
 
 def _gemm_input_norm(ln: nn.LayerNorm, x: torch.Tensor) -> torch.Tensor:
@@ -177,10 +175,10 @@ def _sab_forward_packed(blk: "SABComplete", X: torch.Tensor, tokens: PackedSets)
     x_mm = X if x_mm is None else x_mm
     mask_kwargs = tokens.kernel_mask(padded=False) if blk.idx == 1 else {}
     cu, n = tokens.cu_seqlens, tokens.max_items
-    out_attn = _packed_mab(blk.sab.mab, x_mm, x_mm, cu, cu, n, n, mask_kwargs)
-    if out_attn.shape[-1] != X.shape[-1]:
-        X = blk.proj_1(X)
-    out = X + out_attn
+    if blk.sab.mab.dim_V == X.shape[-1]:   # the residual add fused into the epilogue
+        out = _packed_mab(blk.sab.mab, x_mm, x_mm, cu, cu, n, n, mask_kwargs, residual=X)
+    else:
+        out = blk.proj_1(X) + _packed_mab(blk.sab.mab, x_mm, x_mm, cu, cu, n, n, mask_kwargs)
     if blk.use_mlp:
         out_mlp = blk.mlp(_gemm_input_norm(blk.norm_mlp.ln, out))
         if out.shape[-1] == out_mlp.shape[-1]:

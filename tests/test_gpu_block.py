@@ -310,3 +310,77 @@ def test_column_sum(device, dtype, rows, cols):
     ref = x.double().sum(0)
     bar = 1e-5 * ref.abs() + rows * 2.0 ** -24 * (float(x.double().abs().max()) if rows else 0.0) + 1e-30
     assert bool(((a.double().cpu() - ref).abs() <= bar).all())
+
+
+def _bf16_bar(got, ref, what):
+    """The north-star bf16 bar, scaled by the reference's magnitude (at least 1)."""
+    from tests._util import assert_bf16_close, grad_scale
+    assert_bf16_close(got.detach().float().cpu(), ref, grad_scale(ref), what)
+
+
+@pytest.mark.parametrize("with_residual", [False, True])
+def test_mab_epilogue_fused(device, with_residual):
+    """mab_epilogue(o, fc_o, x) = x + (o + mish(fc_o(o))) under autocast(bf16) against the fp64 expression on the
+    same bf16-rounded operands; gradients of o, x, fc_o.weight and fc_o.bias by fp64 autograd."""
+    from mind_amd.esa.activations import mab_epilogue
+    gen = torch.Generator().manual_seed(21 + with_residual)
+    t, d = 3000, 256
+    fc = torch.nn.Linear(d, d).to(device)
+    o = torch.randn(t, d, generator=gen).to(torch.bfloat16)
+    x = torch.randn(t, d, generator=gen) if with_residual else None
+    up = torch.randn(t, d, generator=gen)
+    od = o.to(device).requires_grad_(True)
+    xd = x.to(device).requires_grad_(True) if with_residual else None
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        y = mab_epilogue(od, fc, xd)
+    assert y.dtype == (torch.float32 if with_residual else torch.bfloat16)
+    y.backward(up.to(device).to(y.dtype))
+    # fp64 reference on the operands autocast hands the GEMM (bf16 weight and bias)
+    w64 = fc.weight.detach().to(torch.bfloat16).double().cpu().requires_grad_(True)
+    b64 = fc.bias.detach().to(torch.bfloat16).double().cpu().requires_grad_(True)
+    o64 = o.double().requires_grad_(True)
+    ref = o64 + OMod.mish(o64 @ w64.t() + b64)
+    if with_residual:
+        x64 = x.double().requires_grad_(True)
+        ref = x64 + ref
+    g64 = up.to(y.dtype).double()
+    ref.backward(g64)
+    _bf16_bar(y, ref.detach(), "y")
+    _bf16_bar(od.grad, o64.grad, "d o")
+    _bf16_bar(fc.weight.grad, w64.grad, "d weight")
+    _bf16_bar(fc.bias.grad, b64.grad, "d bias")
+    if with_residual:
+        assert torch.equal(xd.grad.cpu(), up)
+
+
+@pytest.mark.parametrize("self_attn", [True, False])
+def test_qkv_projection(device, self_attn):
+    """qkv_projection: outputs are F.linear's (bit for bit); input and parameter gradients, with the shared
+    input's gradient accumulated inside the GEMMs, against fp64 autograd."""
+    from mind_amd.esa.linear import qkv_projection
+    gen = torch.Generator().manual_seed(31 + self_attn)
+    tq, tk, d = 2048 if self_attn else 64, 2048, 128
+    fcs = [torch.nn.Linear(d, d).to(device) for _ in range(3)]
+    xq = torch.randn(tq, d, generator=gen)
+    xk = xq if self_attn else torch.randn(tk, d, generator=gen)
+    gs = [torch.randn(tq, d, generator=gen), torch.randn(tk, d, generator=gen), torch.randn(tk, d, generator=gen)]
+    xqd = xq.to(device).requires_grad_(True)
+    xkd = xqd if self_attn else xk.to(device).requires_grad_(True)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        outs = qkv_projection(fcs[0], fcs[1], fcs[2], xqd, xkd)
+        refs = [fcs[0](xqd), fcs[1](xkd), fcs[2](xkd)]
+    for a, b in zip(outs, refs):
+        assert a.dtype == torch.bfloat16 and torch.equal(a, b)
+    torch.autograd.backward(list(outs), [g.to(device).to(torch.bfloat16) for g in gs])
+    ws = [f.weight.detach().to(torch.bfloat16).double().cpu().requires_grad_(True) for f in fcs]
+    bs = [f.bias.detach().to(torch.bfloat16).double().cpu().requires_grad_(True) for f in fcs]
+    xq64 = xq.to(torch.bfloat16).double().requires_grad_(True)
+    xk64 = xq64 if self_attn else xk.to(torch.bfloat16).double().requires_grad_(True)
+    r = [xq64 @ ws[0].t() + bs[0], xk64 @ ws[1].t() + bs[1], xk64 @ ws[2].t() + bs[2]]
+    torch.autograd.backward(r, [g.to(torch.bfloat16).double() for g in gs])
+    _bf16_bar(xqd.grad, xq64.grad, "d xq")
+    if not self_attn:
+        _bf16_bar(xkd.grad, xk64.grad, "d xk")
+    for f, w, b in zip(fcs, ws, bs):
+        _bf16_bar(f.weight.grad, w.grad, "d weight")
+        _bf16_bar(f.bias.grad, b.grad, "d bias")
