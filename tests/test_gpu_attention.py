@@ -155,6 +155,29 @@ def test_full_config1_size(device):
         assert_bf16_close(dv[s:e], rdv, grad_scale(rdv), f"dv segment {b}")
 
 
+def test_full_config2_size_masked(device):
+    """Configuration 2 (edge-masked MAB attention) at full size: the token-budgeted batch of up to 65,536
+    tokens; every output finite, and three segments (first, largest, last) checked against the oracle."""
+    gb = generators.protein_budget(seed=0, token_budget=65536)
+    cu = gb.cu_seqlens
+    t = int(cu[-1])
+    src, dst = gb.edge_index[0].astype(np.int32), gb.edge_index[1].astype(np.int32)
+    q, k, v, g = _inputs(t, t, 4321)
+    out, dq, dk, dv = _run(device, q, k, v, g, cu, cu, src, dst)
+    for x in (out, dq, dk, dv):
+        assert torch.isfinite(x.float()).all()
+    for b in (0, int(np.argmax(gb.edge_counts)), gb.num_graphs - 1):
+        s, e = int(cu[b]), int(cu[b + 1])
+        sub = np.array([0, e - s], np.int32)
+        ls, ld = src[s:e], dst[s:e]
+        ref, _ = OA.varlen_attention(q[s:e], k[s:e], v[s:e], sub, sub, 0.25, ls, ld)
+        assert_bf16_close(out[s:e], ref, what=f"segment {b}")
+        rdq, rdk, rdv = OA.varlen_attention_bwd(g[s:e], q[s:e], k[s:e], v[s:e], sub, sub, 0.25, ls, ld)
+        assert_bf16_close(dq[s:e], rdq, grad_scale(rdq), f"dq segment {b}")
+        assert_bf16_close(dk[s:e], rdk, grad_scale(rdk), f"dk segment {b}")
+        assert_bf16_close(dv[s:e], rdv, grad_scale(rdv), f"dv segment {b}")
+
+
 def test_edge_mask_dense_bits(device):
     """The on-device predicate materialised equals the oracle's global E x E mask, bit for bit."""
     from oracle import mask as OM

@@ -65,3 +65,38 @@ def test_edge_adjacency_descriptor_cpu():
     pad_ids = torch.cat([src[(~valid).reshape(-1)], dst[(~valid).reshape(-1)]])
     assert torch.all(pad_ids < 0) and pad_ids.unique().numel() == pad_ids.numel()
     assert torch.equal(cu_seqlens_from_counts(torch.tensor([2, 0, 3])), torch.tensor([0, 2, 2, 5], dtype=torch.int32))
+
+
+def test_split_count_rule():
+    """Split-K chunk count: largest power of two <= 32 with >= 4096-token chunks and <= 2^24 fp32 partials."""
+    from mind_amd.esa.linear import split_count
+    assert split_count(131072, 512, 512) == 32
+    assert split_count(131072, 2048, 512) == 16
+    assert split_count(131072, 1536, 512) == 16
+    assert split_count(8191, 512, 512) == 1
+    assert split_count(8192, 512, 512) == 2
+    assert split_count(10 ** 6, 4096, 4096) == 1
+    for t, o, i in ((131072, 512, 512), (50000, 256, 128), (4096, 64, 64)):
+        s = split_count(t, o, i)
+        assert s & (s - 1) == 0 and s <= 32 and (s == 1 or (t // s >= 4096 and s * o * i <= 2 ** 24))
+
+
+def test_block_functions_on_cpu_tensors():
+    """On CPU tensors the block helpers are the plain torch expressions (the HIP kernels take device memory)."""
+    from mind_amd.esa.activations import Mish, mab_epilogue, mish
+    from mind_amd.esa.layer_norm import layer_norm
+    from mind_amd.esa.linear import linear, qkv_projection
+    torch.manual_seed(0)
+    fc = torch.nn.Linear(8, 8)
+    o, x = torch.randn(5, 8), torch.randn(5, 8)
+    assert torch.allclose(mab_epilogue(o, fc), o + torch.nn.functional.mish(fc(o)))
+    assert torch.allclose(mab_epilogue(o, fc, x), x + o + torch.nn.functional.mish(fc(o)))
+    assert torch.allclose(mish(o, x), x + torch.nn.functional.mish(o))
+    assert torch.allclose(Mish()(o), torch.nn.functional.mish(o))
+    assert torch.allclose(linear(o, fc.weight, fc.bias), fc(o))
+    fcs = [torch.nn.Linear(8, 8) for _ in range(3)]
+    q, k, v = qkv_projection(*fcs, o, x)
+    assert torch.allclose(q, fcs[0](o)) and torch.allclose(k, fcs[1](x)) and torch.allclose(v, fcs[2](x))
+    ln = torch.nn.LayerNorm(8, eps=1e-8)
+    y, y_lp = layer_norm(o, ln, full=True, lowp=True)
+    assert torch.allclose(y, ln(o)) and y_lp is None
