@@ -177,20 +177,25 @@ def gather_add(a: torch.Tensor, b: torch.Tensor, src: torch.Tensor, dst: torch.T
 
 class _EdgeTokenLinear(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x, weight, bias, src, dst, src_csr, dst_csr):
+    def forward(ctx, x, weight, bias, src, dst, src_csr, dst_csr, edge_attr):
         n, f = x.shape
         d = weight.shape[0]
-        w2 = torch.cat((weight[:, :f], weight[:, f:]), 0)   # [W_s ; W_d], [2D, F]
-        pq = x @ w2.t()                                       # node-level projections [N, 2D]
+        w2 = torch.cat((weight[:, :f], weight[:, f:2 * f]), 0)   # [W_s ; W_d], [2D, F]
+        pq = x @ w2.t()                                             # node-level projections [N, 2D]
         out = gather_add(pq[:, :d], pq[:, d:], src, dst, bias)
-        ctx.save_for_backward(x, w2, src, dst)
+        w_e = None
+        if edge_attr is not None:                                   # the edge-attribute block W_e, [D, F_e]
+            w_e = weight[:, 2 * f:]
+            out.add_(edge_attr @ w_e.t())
+        ctx.save_for_backward(x, w2, src, dst, edge_attr, w_e)
         ctx.csrs = (src_csr, dst_csr)
         ctx.has_bias = bias is not None
         return out
 
     @staticmethod
     def backward(ctx, g):
-        x, w2, src, dst = ctx.saved_tensors
+        from .esa.linear import column_sum, weight_grad
+        x, w2, src, dst, edge_attr, w_e = ctx.saved_tensors
         src_csr, dst_csr = ctx.csrs
         n, f = x.shape
         d = w2.shape[0] // 2
@@ -205,49 +210,64 @@ class _EdgeTokenLinear(torch.autograd.Function):
         dx = dpq @ w2 if ctx.needs_input_grad[0] else None
         dweight = None
         if ctx.needs_input_grad[1]:
-            dw2 = dpq.t() @ x                                  # [2D, F]
-            dweight = torch.cat((dw2[:d], dw2[d:]), 1)         # [D, 2F]
-        dbias = g.sum(0) if ctx.has_bias and ctx.needs_input_grad[2] else None
-        return dx, dweight, dbias, None, None, None, None
+            dw2 = weight_grad(dpq, x).to(w2.dtype)                # [2D, F]
+            parts = [dw2[:d], dw2[d:]]
+            if edge_attr is not None:
+                parts.append(weight_grad(g, edge_attr).to(w2.dtype))   # [D, F_e]
+            dweight = torch.cat(parts, 1)                          # [D, 2F (+ F_e)]
+        dbias = column_sum(g).to(g.dtype) if ctx.has_bias and ctx.needs_input_grad[2] else None
+        dattr = g @ w_e if edge_attr is not None and ctx.needs_input_grad[7] else None
+        return dx, dweight, dbias, None, None, None, None, dattr
 
 
 def edge_token_linear(x: torch.Tensor, src: torch.Tensor, dst: torch.Tensor, weight: torch.Tensor,
                       bias: torch.Tensor | None = None, src_csr: CSR | None = None,
-                      dst_csr: CSR | None = None) -> torch.Tensor:
-    """``F.linear(torch.cat((x[src], x[dst]), 1), weight, bias)`` without the [E, 2F] edge tokens.
+                      dst_csr: CSR | None = None, edge_attr: torch.Tensor | None = None) -> torch.Tensor:
+    """``F.linear(torch.cat((x[src], x[dst](, edge_attr)), 1), weight, bias)`` without the [E, 2F] edge tokens.
 
-    The Linear over concatenated endpoint features (core/pretraining_model.py:153-198, the first layer of
-    the edge MLP, esa/mlp_utils.py:28-32) splits by input half, W = [W_s | W_d]: one node-level GEMM
-    x [W_s ; W_d]^T gives both halves' projections, and the gather-add kernel writes
-    out[e] = (x W_s^T)[src e] + (x W_d^T)[dst e] + bias.  The backward sums the edge gradients per node
-    through two CSRs (deterministic) and finishes with GEMMs.  Computes in the dtype of x (float32 or
-    bfloat16); weight and bias must share it.  Mathematically equal to the reference; results differ
-    from it only by summation order.
+    The Linear over concatenated endpoint features (core/pretraining_model.py:153-198, with the edge
+    attributes appended when the batch has them, :157-159; the first layer of the edge MLP,
+    esa/mlp_utils.py:28-32) splits by input block, W = [W_s | W_d (| W_e)]: one node-level GEMM
+    x [W_s ; W_d]^T gives both endpoint projections, and the gather-add kernel writes
+    out[e] = (x W_s^T)[src e] + (x W_d^T)[dst e] + bias; edge attributes add edge_attr W_e^T (one GEMM over
+    the edges).  The backward sums the edge gradients per node through two CSRs (deterministic) and finishes
+    with GEMMs (split-K weight gradients, a deterministic bias gradient).  Computes in the dtype of x
+    (float32 or bfloat16); weight, bias and edge_attr must share it.  Mathematically equal to the
+    reference; results differ from it only by summation order.
     """
     if x.dim() != 2:
         raise ValueError("x must be [N, F]")
-    if weight.dim() != 2 or weight.shape[1] != 2 * x.shape[1]:
-        raise ValueError("weight must be [D, 2F]")
-    if weight.dtype != x.dtype or (bias is not None and bias.dtype != x.dtype):
-        raise TypeError("x, weight and bias must share one dtype")
+    fe = 0 if edge_attr is None else edge_attr.shape[-1]
+    if weight.dim() != 2 or weight.shape[1] != 2 * x.shape[1] + fe:
+        raise ValueError("weight must be [D, 2F + F_e]")
+    if (weight.dtype != x.dtype or (bias is not None and bias.dtype != x.dtype)
+            or (edge_attr is not None and edge_attr.dtype != x.dtype)):
+        raise TypeError("x, weight, bias and edge_attr must share one dtype")
     src = _as_index(src, "src")
     dst = _as_index(dst, "dst")
     if src.shape != dst.shape or src.dim() != 1:
         raise ValueError("src and dst must be 1-D and of equal length")
-    return _EdgeTokenLinear.apply(x, weight, bias, src, dst, src_csr, dst_csr)
+    if edge_attr is not None and (edge_attr.dim() != 2 or edge_attr.shape[0] != src.shape[0]):
+        raise ValueError("edge_attr must be [E, F_e]")
+    return _EdgeTokenLinear.apply(x, weight, bias, src, dst, src_csr, dst_csr,
+                                  None if edge_attr is None else edge_attr.contiguous())
 
 
 class EdgeTokenLinear(torch.nn.Module):
-    """Drop-in for the ``nn.Linear(2F, D)`` applied to ``torch.cat((x[src], x[dst]), 1)``: same parameter
-    names and shapes (a reference state_dict loads), forward(x, src, dst) via ``edge_token_linear``."""
+    """Drop-in for the ``nn.Linear(2F (+ F_e), D)`` applied to ``torch.cat((x[src], x[dst](, edge_attr)), 1)``:
+    same parameter names and shapes (a reference state_dict loads), forward(x, src, dst, edge_attr=None) via
+    ``edge_token_linear``."""
 
-    def __init__(self, in_features: int, out_features: int, bias: bool = True):
+    def __init__(self, in_features: int, out_features: int, bias: bool = True, edge_features: int = 0):
         super().__init__()
-        lin = torch.nn.Linear(2 * in_features, out_features, bias=bias)
+        lin = torch.nn.Linear(2 * in_features + edge_features, out_features, bias=bias)
         self.weight = lin.weight
         self.bias = lin.bias
-        self.in_features, self.out_features = in_features, out_features
+        self.in_features, self.out_features, self.edge_features = in_features, out_features, edge_features
 
     def forward(self, x: torch.Tensor, src: torch.Tensor, dst: torch.Tensor, src_csr: CSR | None = None,
-                dst_csr: CSR | None = None) -> torch.Tensor:
-        return edge_token_linear(x, src, dst, self.weight, self.bias, src_csr, dst_csr)
+                dst_csr: CSR | None = None, edge_attr: torch.Tensor | None = None) -> torch.Tensor:
+        if (edge_attr is None) != (self.edge_features == 0):
+            raise ValueError(f"this layer takes {self.edge_features} edge features; got "
+                             f"{'none' if edge_attr is None else edge_attr.shape[-1]}")
+        return edge_token_linear(x, src, dst, self.weight, self.bias, src_csr, dst_csr, edge_attr)

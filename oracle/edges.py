@@ -10,10 +10,14 @@ def edge_gather(x: np.ndarray, src: np.ndarray, dst: np.ndarray) -> np.ndarray:
 
 
 def edge_token_linear(x: np.ndarray, src: np.ndarray, dst: np.ndarray, weight: np.ndarray,
-                      bias: np.ndarray | None = None) -> np.ndarray:
-    """Linear over the edge tokens: edge_gather(x, src, dst) @ weight^T + bias, in float64 —
-    core/pretraining_model.py:153-198 with the MLP's first Linear (esa/mlp_utils.py:28-32)."""
-    h = edge_gather(np.asarray(x, np.float64), src, dst) @ np.asarray(weight, np.float64).T
+                      bias: np.ndarray | None = None, edge_attr: np.ndarray | None = None) -> np.ndarray:
+    """Linear over the edge tokens: [x[src] || x[dst] (|| edge_attr)] @ weight^T + bias, in float64 —
+    core/pretraining_model.py:153-198 (edge attributes appended at :157-159) with the MLP's first Linear
+    (esa/mlp_utils.py:28-32)."""
+    h = edge_gather(np.asarray(x, np.float64), src, dst)
+    if edge_attr is not None:
+        h = np.concatenate([h, np.asarray(edge_attr, np.float64)], axis=1)
+    h = h @ np.asarray(weight, np.float64).T
     return h if bias is None else h + np.asarray(bias, np.float64)
 
 

@@ -193,34 +193,42 @@ def test_gather_add_without_bias_and_empty(device):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_edge_token_linear_fwd_bwd(device, dtype):
-    # Linear(cat(x[src], x[dst])) of the reference against the oracle (float64): forward, and the
-    # gradients of x, weight and bias through torch autograd of the oracle's expression
+@pytest.mark.parametrize("edge_dim", [0, 12])
+def test_edge_token_linear_fwd_bwd(device, dtype, edge_dim):
+    # Linear(cat(x[src], x[dst](, edge_attr))) of the reference against the oracle (float64): forward, and
+    # the gradients of x, weight, bias (and edge_attr) through torch autograd of the oracle's expression
     n, f, d, e = 300, 64, 96, 2500
     src, dst = _graph(3, n, e)
-    g = torch.Generator().manual_seed(5)
+    g = torch.Generator().manual_seed(5 + edge_dim)
     x = torch.randn(n, f, generator=g)
-    lin = torch.nn.Linear(2 * f, d)
+    ea = torch.randn(e, edge_dim, generator=g) if edge_dim else None
+    lin = torch.nn.Linear(2 * f + edge_dim, d)
     gy = torch.randn(e, d, generator=g)
     xd = x.to(dtype).to(device).requires_grad_(True)
+    ead = ea.to(dtype).to(device).requires_grad_(True) if edge_dim else None
     w = lin.weight.detach().to(dtype).to(device).requires_grad_(True)
     bb = lin.bias.detach().to(dtype).to(device).requires_grad_(True)
-    out = edges.edge_token_linear(xd, torch.as_tensor(src).to(device), torch.as_tensor(dst).to(device), w, bb)
+    out = edges.edge_token_linear(xd, torch.as_tensor(src).to(device), torch.as_tensor(dst).to(device), w, bb,
+                                  edge_attr=ead)
     out.backward(gy.to(dtype).to(device))
     xr = x.to(dtype).double().requires_grad_(True)
+    ear = ea.to(dtype).double().requires_grad_(True) if edge_dim else None
     wr = lin.weight.detach().to(dtype).double().requires_grad_(True)
     br = lin.bias.detach().to(dtype).double().requires_grad_(True)
-    ref = torch.nn.functional.linear(torch.cat((xr[torch.as_tensor(src).long()], xr[torch.as_tensor(dst).long()]), 1),
-                                     wr, br)
+    toks = [xr[torch.as_tensor(src).long()], xr[torch.as_tensor(dst).long()]] + ([ear] if edge_dim else [])
+    ref = torch.nn.functional.linear(torch.cat(toks, 1), wr, br)
     ref.backward(gy.to(dtype).double())
     assert np.abs(OE.edge_token_linear(x.to(dtype).double().numpy(), src, dst, wr.detach().numpy(),
-                                       br.detach().numpy()) - ref.detach().numpy()).max() < 1e-10
+                                       br.detach().numpy(), None if ear is None else ear.detach().numpy())
+                  - ref.detach().numpy()).max() < 1e-10
     check = assert_f32_close if dtype == torch.float32 else \
         (lambda got, r, what: assert_bf16_close(got, r, grad_scale(r), what))
     check(out.detach().cpu().double(), ref.detach(), "out")
     check(xd.grad.cpu().double(), xr.grad, "dx")
     check(w.grad.cpu().double(), wr.grad, "dweight")
     check(bb.grad.cpu().double(), br.grad, "dbias")
+    if edge_dim:
+        check(ead.grad.cpu().double(), ear.grad, "d edge_attr")
 
 
 def test_edge_token_linear_module_loads_linear_state(device):
@@ -234,3 +242,14 @@ def test_edge_token_linear_module_loads_linear_state(device):
     ref = lin.to(device)(torch.cat((x[src.long()], x[dst.long()]), 1))
     got = m(x, src, dst)
     assert float((got - ref).abs().max()) <= 1e-5 * max(1.0, float(ref.abs().max()))
+    # with edge attributes: nn.Linear(2F + F_e, D) over cat(x[src], x[dst], edge_attr)
+    lin3 = torch.nn.Linear(2 * 32 + 5, 48)
+    m3 = edges.EdgeTokenLinear(32, 48, edge_features=5)
+    m3.load_state_dict(lin3.state_dict())
+    m3, lin3 = m3.to(device), lin3.to(device)
+    ea = torch.randn(400, 5, device=device)
+    ref3 = lin3(torch.cat((x[src.long()], x[dst.long()], ea), 1))
+    got3 = m3(x, src, dst, edge_attr=ea)
+    assert float((got3 - ref3).abs().max()) <= 1e-5 * max(1.0, float(ref3.abs().max()))
+    with pytest.raises(ValueError):
+        m3(x, src, dst)

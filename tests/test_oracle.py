@@ -260,6 +260,12 @@ def test_edge_token_linear_matches_reference_expression():
     w = lin.weight.detach().numpy()
     split = x[src] @ w[:, :5].T + x[dst] @ w[:, 5:].T + lin.bias.detach().numpy()
     assert np.abs(got - split).max() < 1e-12
+    # with edge attributes appended (core/pretraining_model.py:157-159): torch.cat((x[src], x[dst], e), 1)
+    e = rng.standard_normal((40, 3))
+    lin3 = torch.nn.Linear(13, 7).double()
+    ref3 = lin3(torch.cat((xt[torch.as_tensor(src)], xt[torch.as_tensor(dst)], torch.as_tensor(e)), 1))
+    got3 = OE.edge_token_linear(x, src, dst, lin3.weight.detach().numpy(), lin3.bias.detach().numpy(), e)
+    assert np.abs(got3 - ref3.detach().numpy()).max() < 1e-12
 
 
 @given(st.lists(st.integers(0, 9), min_size=0, max_size=60))
