@@ -111,6 +111,28 @@ ESA_API int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k,
                         void* dq, void* dk, void* dv,
                         void* workspace, size_t workspace_bytes, void* stream);
 
+/* ------------------------------------------------------------------------ */
+/* PMA seed pooling: PMA.forward = MAB(S.repeat(B, 1, 1), X) (esa/mha.py:   */
+/* 101-109; PMAFlashVarlen, esa/mha_flash_varlen.py:233-248) over packed     */
+/* sets.  q [k_seeds, H, 16] holds the projected seeds fc_q(S), shared by all */
+/* batch sets; k, v [total_k, H, 16] with cu_seqlens_k [batch + 1].  out is   */
+/* [batch * k_seeds, H, 16] set-major, softmax_lse [H][batch * k_seeds].     */
+/* The backward's dq [k_seeds, H, 16] sums the sets' seed gradients in set    */
+/* order (deterministic).  Workspace size from esa_pma_workspace_size.       */
+/* ------------------------------------------------------------------------ */
+ESA_API int esa_pma_workspace_size(int batch, int k_seeds, int total_k, int heads,
+                           int head_dim, int dtype, int backward, size_t* bytes);
+ESA_API int esa_pma_fwd(const void* q, const void* k, const void* v, const int* cu_seqlens_k,
+                int batch, int k_seeds, int total_k, int max_seqlen_k, int heads,
+                int head_dim, int dtype, float softmax_scale, void* out,
+                float* softmax_lse, void* workspace, size_t workspace_bytes,
+                void* stream);
+ESA_API int esa_pma_bwd(const void* dout, const void* q, const void* k, const void* v,
+                const void* out, const float* softmax_lse, const int* cu_seqlens_k,
+                int batch, int k_seeds, int total_k, int max_seqlen_k, int heads,
+                int head_dim, int dtype, float softmax_scale, void* dq, void* dk,
+                void* dv, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Materialises the edge-adjacency mask of each segment as a padded
  * [batch, max_items, max_items] uint8 array (1 = attend), the same entries
  * get_adj_mask_from_edge_index_edge (esa/masked_layers.py:217-268) sets to 0

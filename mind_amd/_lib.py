@@ -48,6 +48,15 @@ _PROTOS = {
                                      _c_int, _c_int, _c_int, _c_f, _c_int, _vp, _vp, _c_int, _vp, _vp, _vp, _vp, _c_sz,
                                      _vp]),
     "esa_edge_mask_dense": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _vp]),
+    # batch k_seeds total_k heads head_dim dtype backward bytes
+    "esa_pma_workspace_size": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
+                                        ctypes.POINTER(_c_sz)]),
+    # q k v cu_k | batch k_seeds tk maxk heads hd dtype | scale | out lse ws bytes stream
+    "esa_pma_fwd": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_f,
+                             _vp, _vp, _vp, _c_sz, _vp]),
+    # dout q k v out lse cu_k | batch k_seeds tk maxk heads hd dtype | scale | dq dk dv ws bytes stream
+    "esa_pma_bwd": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
+                             _c_int, _c_f, _vp, _vp, _vp, _vp, _c_sz, _vp]),
     "esa_edge_gather": (_c_int, [_vp, _vp, _vp, _c_i64, _c_int, _c_int, _c_int, _vp, _vp]),
     "esa_csr_workspace_size": (_c_int, [_c_i64, _c_int, ctypes.POINTER(_c_sz)]),
     "esa_csr_build": (_c_int, [_vp, _c_i64, _c_int, _vp, _vp, _vp, _c_sz, _vp]),

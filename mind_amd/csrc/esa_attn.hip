@@ -1105,6 +1105,32 @@ __global__ void zero16_kernel(uint4* __restrict__ p, long n) {
     p[i] = make_uint4(0u, 0u, 0u, 0u);
 }
 
+// ======================================================================== PMA seed pooling
+// k seed queries shared by all B sets (PMA = MAB(S.repeat(B, 1, 1), X)):
+// the expanded query row b * k + s is seed s, and set b's queries are rows
+// [b k, (b + 1) k).  The seed gradient sums the B sets' rows in set order.
+__global__ void pma_expand_kernel(const uint4* __restrict__ q, int row16, int k_seeds, int batch,
+                                  uint4* __restrict__ q_rep, int* __restrict__ cu_q) {
+  const long n = (long)batch * k_seeds * row16;
+  const long i0 = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  for (long i = i0; i < n; i += (long)gridDim.x * blockDim.x) {
+    const long row = i / row16;
+    q_rep[i] = q[(row % k_seeds) * row16 + (i - row * row16)];
+  }
+  if (i0 <= batch) cu_q[i0] = (int)i0 * k_seeds;
+}
+
+template <typename T>
+__global__ void pma_reduce_kernel(const T* __restrict__ dq_rep, int row_elems, int k_seeds, int batch,
+                                  T* __restrict__ dq) {
+  const long n = (long)k_seeds * row_elems;
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) {
+    float acc = 0.f;
+    for (int b = 0; b < batch; ++b) acc += (float)dq_rep[(long)b * n + i];
+    dq[i] = (T)acc;
+  }
+}
+
 // ======================================================================== host side
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
@@ -1438,6 +1464,95 @@ int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k, const vo
   a.bounds = pa.bounds_q;
   const unsigned eqgrid = (unsigned)groups_of(total_q) * (unsigned)((heads + kEdgeHeads - 1) / kEdgeHeads);
   ESA_TIMED(esa_profile::kAttnBwdDqMasked, st, hipLaunchKernelGGL(edge_dq_kernel, dim3(eqgrid), dim3(256), 0, st, a));
+  ESA_LAUNCH_CHECK();
+  return ESA_OK;
+}
+
+// ---- PMA entry points: expansion + varlen attention (+ seed-gradient reduction)
+static int pma_layout(int batch, int k_seeds, int total_k, int heads, int head_dim, int dtype, bool backward,
+                      size_t off[4], size_t* total) {
+  if (batch < 1 || k_seeds < 1 || total_k < 0 || heads < 1) return ESA_ERR_SHAPE;
+  if (head_dim != kHd) return ESA_ERR_HEAD_DIM;
+  if (dtype != ESA_BF16 && dtype != ESA_F32) return ESA_ERR_DTYPE;
+  const long tq = (long)batch * k_seeds;
+  if (tq > INT32_MAX / 2) return ESA_ERR_SHAPE;
+  const size_t rows = (size_t)tq * heads * kHd * (dtype == ESA_F32 ? 4 : 2);
+  size_t inner = 0;
+  const int rc = esa_varlen_attn_workspace_size((int)tq, total_k, heads, head_dim, dtype, ESA_MASK_NONE, 0,
+                                                backward ? 1 : 0, &inner);
+  if (rc) return rc;
+  size_t o = 0;
+  off[0] = o; o += align256(rows);                               // expanded seed queries
+  off[1] = o; o += align256((size_t)(batch + 1) * 4);            // cu_seqlens of the expanded queries
+  off[2] = o; o += backward ? align256(rows) : 0;                // per-set seed gradients
+  off[3] = o; o += inner;                                        // the varlen call's own workspace
+  *total = o;
+  return ESA_OK;
+}
+
+static int pma_expand(const void* q, int batch, int k_seeds, int heads, int dtype, char* ws, const size_t off[4],
+                      hipStream_t st) {
+  const int row16 = heads * kHd * (dtype == ESA_F32 ? 4 : 2) / 16;
+  const long n = (long)batch * k_seeds * row16;
+  const long g = std::min<long>(std::max<long>((n + 255) / 256, (batch + 1 + 255) / 256), 65536);
+  hipLaunchKernelGGL(pma_expand_kernel, dim3((unsigned)g), dim3(256), 0, st, static_cast<const uint4*>(q), row16,
+                     k_seeds, batch, reinterpret_cast<uint4*>(ws + off[0]), reinterpret_cast<int*>(ws + off[1]));
+  ESA_LAUNCH_CHECK();
+  return ESA_OK;
+}
+
+int esa_pma_workspace_size(int batch, int k_seeds, int total_k, int heads, int head_dim, int dtype, int backward,
+                           size_t* bytes) {
+  if (!bytes) return ESA_ERR_NULL;
+  size_t off[4];
+  return pma_layout(batch, k_seeds, total_k, heads, head_dim, dtype, backward != 0, off, bytes);
+}
+
+int esa_pma_fwd(const void* q, const void* k, const void* v, const int* cu_seqlens_k, int batch, int k_seeds,
+                int total_k, int max_seqlen_k, int heads, int head_dim, int dtype, float softmax_scale, void* out,
+                float* softmax_lse, void* workspace, size_t workspace_bytes, void* stream) {
+  size_t off[4], need = 0;
+  int rc = pma_layout(batch, k_seeds, total_k, heads, head_dim, dtype, false, off, &need);
+  if (rc) return rc;
+  if (!q || !k || !v || !cu_seqlens_k || !out || !softmax_lse || !workspace) return ESA_ERR_NULL;
+  if (workspace_bytes < need) return ESA_ERR_WORKSPACE;
+  if (misaligned(q) || misaligned(workspace)) return ESA_ERR_ALIGN;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  if ((rc = pma_expand(q, batch, k_seeds, heads, dtype, ws, off, st))) return rc;
+  return esa_varlen_attn_fwd(ws + off[0], k, v, reinterpret_cast<const int*>(ws + off[1]), cu_seqlens_k, batch,
+                             batch * k_seeds, total_k, k_seeds, max_seqlen_k, heads, head_dim, dtype, softmax_scale,
+                             ESA_MASK_NONE, nullptr, nullptr, 0, out, softmax_lse, ws + off[3], need - off[3], stream);
+}
+
+int esa_pma_bwd(const void* dout, const void* q, const void* k, const void* v, const void* out,
+                const float* softmax_lse, const int* cu_seqlens_k, int batch, int k_seeds, int total_k,
+                int max_seqlen_k, int heads, int head_dim, int dtype, float softmax_scale, void* dq, void* dk,
+                void* dv, void* workspace, size_t workspace_bytes, void* stream) {
+  size_t off[4], need = 0;
+  int rc = pma_layout(batch, k_seeds, total_k, heads, head_dim, dtype, true, off, &need);
+  if (rc) return rc;
+  if (!dout || !q || !k || !v || !out || !softmax_lse || !cu_seqlens_k || !dq || !dk || !dv || !workspace)
+    return ESA_ERR_NULL;
+  if (workspace_bytes < need) return ESA_ERR_WORKSPACE;
+  if (misaligned(q) || misaligned(workspace)) return ESA_ERR_ALIGN;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  if ((rc = pma_expand(q, batch, k_seeds, heads, dtype, ws, off, st))) return rc;
+  rc = esa_varlen_attn_bwd(dout, ws + off[0], k, v, out, softmax_lse, reinterpret_cast<const int*>(ws + off[1]),
+                           cu_seqlens_k, batch, batch * k_seeds, total_k, k_seeds, max_seqlen_k, heads, head_dim,
+                           dtype, softmax_scale, ESA_MASK_NONE, nullptr, nullptr, 0, ws + off[2], dk, dv,
+                           ws + off[3], need - off[3], stream);
+  if (rc) return rc;
+  const int row_elems = heads * kHd;
+  const long n = (long)k_seeds * row_elems;
+  const unsigned g = (unsigned)std::min<long>((n + 255) / 256, 65536);
+  if (dtype == ESA_F32)
+    hipLaunchKernelGGL(pma_reduce_kernel<float>, dim3(g), dim3(256), 0, st,
+                       reinterpret_cast<const float*>(ws + off[2]), row_elems, k_seeds, batch, static_cast<float*>(dq));
+  else
+    hipLaunchKernelGGL(pma_reduce_kernel<bf16>, dim3(g), dim3(256), 0, st,
+                       reinterpret_cast<const bf16*>(ws + off[2]), row_elems, k_seeds, batch, static_cast<bf16*>(dq));
   ESA_LAUNCH_CHECK();
   return ESA_OK;
 }

@@ -179,6 +179,64 @@ def varlen_attention(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seql
     return (out, lse) if return_lse else out
 
 
+def _pma_workspace(device, batch, k_seeds, total_k, heads, dtype, backward):
+    lib = _lib.load()
+    n = _lib.ctypes.c_size_t(0)
+    _lib.check(lib.esa_pma_workspace_size(batch, k_seeds, total_k, heads, HEAD_DIM, dtype, int(backward),
+                                          _lib.ctypes.byref(n)), "esa_pma_workspace_size")
+    return torch.empty(max(int(n.value), 256), dtype=torch.uint8, device=device)
+
+
+class _PMAAttention(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, cu_k, max_k, scale):
+        batch, k_seeds, heads = cu_k.numel() - 1, q.shape[0], q.shape[1]
+        dt = _dtype_code(q)
+        out = torch.empty((batch * k_seeds, heads, HEAD_DIM), dtype=q.dtype, device=q.device)
+        lse = torch.empty((heads, batch * k_seeds), dtype=torch.float32, device=q.device)
+        ws = _pma_workspace(q.device, batch, k_seeds, k.shape[0], heads, dt, False)
+        rc = _lib.load().esa_pma_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), cu_k.data_ptr(), batch, k_seeds,
+                                     k.shape[0], int(max_k), heads, HEAD_DIM, dt, float(scale), out.data_ptr(),
+                                     lse.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_of(q))
+        _lib.check(rc, "esa_pma_fwd")
+        ctx.save_for_backward(q, k, v, out, lse, cu_k)
+        ctx.meta = (max_k, scale)
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        q, k, v, out, lse, cu_k = ctx.saved_tensors
+        max_k, scale = ctx.meta
+        batch, k_seeds, heads = cu_k.numel() - 1, q.shape[0], q.shape[1]
+        dt = _dtype_code(q)
+        g = g.to(q.dtype).contiguous()
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        ws = _pma_workspace(q.device, batch, k_seeds, k.shape[0], heads, dt, True)
+        rc = _lib.load().esa_pma_bwd(g.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                                     lse.data_ptr(), cu_k.data_ptr(), batch, k_seeds, k.shape[0], int(max_k), heads,
+                                     HEAD_DIM, dt, float(scale), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                                     ws.data_ptr(), ws.numel(), _lib.stream_of(q))
+        _lib.check(rc, "esa_pma_bwd")
+        return dq, dk, dv, None, None, None
+
+
+def pma_attention(q, k, v, cu_seqlens_k, max_seqlen_k, softmax_scale=None):
+    """Seed pooling of PMA (esa/mha.py:101-109): the k seed queries q [k, H, 16] (fc_q(S), shared by every
+    set) attend over each set's keys k, v [Tk, H, 16] (sets by cu_seqlens_k [B+1], int32) -> [B * k, H, 16],
+    set-major.  Equals varlen attention with the seeds repeated per set; q's gradient sums the sets'."""
+    _lib.require_gpu(q, k, v, cu_seqlens_k)
+    heads = q.shape[1]
+    _check_tokens("q", q)
+    _check_tokens("k", k, heads, q.dtype)
+    _check_tokens("v", v, heads, q.dtype)
+    if k.shape[0] != v.shape[0]:
+        raise ValueError("k and v must have the same number of tokens")
+    _check_index("cu_seqlens_k", cu_seqlens_k)
+    if softmax_scale is None:
+        softmax_scale = 1.0 / math.sqrt(q.shape[-1])
+    return _PMAAttention.apply(q, k, v, cu_seqlens_k, max_seqlen_k, float(softmax_scale))
+
+
 def edge_mask_dense(edge_src, edge_dst, cu_seqlens, max_items):
     """Debug materialisation of the edge mask: uint8 [B, max_items, max_items]."""
     _lib.require_gpu(edge_src, edge_dst, cu_seqlens)

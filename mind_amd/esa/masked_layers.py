@@ -32,10 +32,10 @@ from torch import nn
 from torch.nn import functional as F
 
 from .activations import mab_epilogue, mish
-from .attention import varlen_attention
+from .attention import pma_attention, varlen_attention
 from .layer_norm import layer_norm
 from .linear import apply, qkv_projection
-from .mha import PMA, SAB, _heads, _uniform_cu, pooled_attention
+from .mha import PMA, SAB, _heads, pooled_attention
 from .mha_flash_varlen import PMAFlashVarlen, SABFlashVarlen
 from .mlp_utils import GatedMLPMulti, SmallMLP
 from .norm_layers import LN
@@ -194,9 +194,12 @@ def _pma_forward_packed(blk: "PMAComplete", X: torch.Tensor, tokens: PackedSets)
     X, x_mm = layer_norm(X, blk.norm.ln, full=True, lowp=True)
     x_mm = X if x_mm is None else x_mm
     b, (k_seeds, d) = tokens.batch_size, blk.pma.S.shape[1:]
-    seeds = blk.pma.S.reshape(k_seeds, d).repeat(b, 1)
-    out = _packed_mab(blk.pma.mab, seeds, x_mm, _uniform_cu(b, k_seeds, X.device), tokens.cu_seqlens, k_seeds,
-                      tokens.max_items, {}).reshape(b, k_seeds, d)
+    mab = blk.pma.mab
+    # MAB(S.repeat(B, 1, 1), X): the seeds are projected once and shared by every set (esa_pma_*)
+    q, k, v = qkv_projection(mab.fc_q, mab.fc_k, mab.fc_v, blk.pma.S.reshape(k_seeds, d), x_mm)
+    h = mab.num_heads
+    o = pma_attention(_heads(q, h), _heads(k, h), _heads(v, h), tokens.cu_seqlens, tokens.max_items)
+    out = mab_epilogue(o.reshape(-1, d).to(q.dtype), mab.fc_o).reshape(b, k_seeds, d)
     if k_seeds == tokens.max_items:   # the reference's residual when the seed count equals N
         out = tokens.pad(X) + out
     if blk.use_mlp:

@@ -207,3 +207,42 @@ def test_argument_errors(device):
         A.attn_fwd(torch.zeros(8, 4, 32, dtype=torch.bfloat16, device=device), q, q, cu, cu, 8, 8, 0.25)
     with pytest.raises(TypeError):
         A.attn_fwd(q, q, q, cu.long(), cu, 8, 8, 0.25)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("seeds", [1, 4, 32])
+def test_pma_seed_pooling(device, dtype, seeds):
+    """esa_pma_fwd/_bwd: k shared seeds over each set's keys equal varlen attention with the seeds repeated per
+    set (bit for bit: the same kernels run on the expanded queries), and against the oracle; the seed gradient
+    is the sum over sets of the repeated queries' gradients."""
+    lk = [50, 0, 130, 77, 1, 300]
+    cu_k = cu_from_lengths(lk)
+    b, tk = len(lk), int(cu_k[-1])
+    qs = seeded_normal((seeds, H, D), 700 + seeds, dtype)
+    k = seeded_normal((tk, H, D), 701, dtype)
+    v = seeded_normal((tk, H, D), 702, dtype)
+    g = seeded_normal((b * seeds, H, D), 703, dtype)
+    qd, kd, vd = (t.to(device).requires_grad_(True) for t in (qs, k, v))
+    ck = torch.as_tensor(cu_k).to(device)
+    out = A.pma_attention(qd, kd, vd, ck, max(lk), softmax_scale=0.25)
+    out.backward(g.to(device))
+    qr = qs.repeat(b, 1, 1)
+    cu_q = cu_from_lengths([seeds] * b)
+    qrd, krd, vrd = (t.to(device).requires_grad_(True) for t in (qr, k, v))
+    ref_dev = A.varlen_attention(qrd, krd, vrd, torch.as_tensor(cu_q).to(device), ck, seeds, max(lk), softmax_scale=0.25)
+    ref_dev.backward(g.to(device))
+    assert torch.equal(out.detach(), ref_dev.detach())
+    assert torch.equal(kd.grad, krd.grad) and torch.equal(vd.grad, vrd.grad)
+    ref, _ = OA.varlen_attention(qr, k, v, cu_q, cu_k, 0.25)
+    rdq, rdk, rdv = OA.varlen_attention_bwd(g, qr, k, v, cu_q, cu_k, 0.25)
+    rdq_seeds = rdq.reshape(b, seeds, H, D).sum(0)
+    if dtype == torch.float32:
+        from tests._util import assert_f32_close
+        assert_f32_close(out.detach().cpu(), ref, "out")
+        assert_f32_close(qd.grad.cpu(), rdq_seeds, "d seeds")
+        assert_f32_close(kd.grad.cpu(), rdk, "dk")
+    else:
+        assert_bf16_close(out.detach().cpu(), ref, what="out")
+        assert_bf16_close(qd.grad.cpu(), rdq_seeds, grad_scale(rdq_seeds), "d seeds")
+        assert_bf16_close(kd.grad.cpu(), rdk, grad_scale(rdk), "dk")
+        assert_bf16_close(vd.grad.cpu(), rdv, grad_scale(rdv), "dv")
