@@ -1,4 +1,4 @@
-"""Edge-token gather and deterministic CSR segmented sums on the gfx950 kernels.
+"""Edge-token gather, deterministic CSR segmented sums and scatter_add on the gfx950 kernels.
 
 ``edge_gather(x, src, dst)`` builds the edge tokens ``[x[src] || x[dst]]`` of
 core/pretraining_model.py:153-155 and esa/models.py:307-309 in one pass (no
@@ -173,6 +173,47 @@ def gather_add(a: torch.Tensor, b: torch.Tensor, src: torch.Tensor, dst: torch.T
                                          _lib.stream_of(a))
     _lib.check(rc, "esa_edge_gather_add")
     return out
+
+
+class _ScatterAdd(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, src, index, dim_size, csr):
+        y = src.reshape(src.shape[0], -1)
+        out = segment_sum_csr(y, csr.indptr, csr.perm)
+        ctx.save_for_backward(index)
+        ctx.dim_size = dim_size
+        return out.reshape((dim_size,) + tuple(src.shape[1:]))
+
+    @staticmethod
+    def backward(ctx, g):
+        (index,) = ctx.saved_tensors
+        idx = index.to(torch.int64)
+        valid = (idx >= 0) & (idx < ctx.dim_size)
+        grad = g.reshape(ctx.dim_size, -1).index_select(0, idx.clamp(0, max(ctx.dim_size - 1, 0)))
+        grad = grad * valid.unsqueeze(1).to(grad.dtype)
+        return grad.reshape((idx.numel(),) + tuple(g.shape[1:])), None, None, None
+
+
+def scatter_add(src: torch.Tensor, index: torch.Tensor, dim: int = 0, dim_size: int | None = None,
+                csr: CSR | None = None) -> torch.Tensor:
+    """``torch_scatter.scatter_add(src, index, dim=0, dim_size)`` as the reference's encoder calls it
+    (core/molecular_encoder.py:195-200, 213-215, 241-242): out[n] = sum of src[e] over edges with
+    index[e] == n, on the deterministic CSR segment sum (fp32, ascending e, one rounding; the reference's
+    atomic scatter sums in arbitrary order).  src is [E] or [E, ...] float32 / bfloat16 on the device;
+    entries with an index outside [0, dim_size) are dropped.  ``csr`` (CSR.build(index, dim_size)) may be
+    passed to reuse one grouping for several sums.  Differentiable in src (the gradient is a row gather)."""
+    if dim != 0:
+        raise NotImplementedError("scatter_add: only dim=0 (edge -> node rows) is on the reference path")
+    index = _as_index(index, "index")
+    if index.dim() != 1 or index.numel() != src.shape[0]:
+        raise ValueError("index must be 1-D with one entry per row of src")
+    if dim_size is None:
+        dim_size = int(index.max()) + 1 if index.numel() else 0
+    if csr is None:
+        csr = CSR.build(index, dim_size)
+    elif csr.num_nodes != dim_size:
+        raise ValueError("csr was built for another dim_size")
+    return _ScatterAdd.apply(src, index, dim_size, csr)
 
 
 class _EdgeTokenLinear(torch.autograd.Function):

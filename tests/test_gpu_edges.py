@@ -253,3 +253,31 @@ def test_edge_token_linear_module_loads_linear_state(device):
     assert float((got3 - ref3).abs().max()) <= 1e-5 * max(1.0, float(ref3.abs().max()))
     with pytest.raises(ValueError):
         m3(x, src, dst)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("shape", [(), (8,), (64,), (3, 5)])
+def test_scatter_add_matches_index_add(device, dtype, shape):
+    """scatter_add (torch_scatter's signature, dim=0) against fp64 index_add_ (the oracle's segment sum
+    definition): fp32 1e-5 relative / bf16 one rounding; indices outside [0, N) dropped; bitwise repeatable;
+    gradient = the output gradient gathered by index."""
+    n, e = 97, 3000
+    g = torch.Generator().manual_seed(len(shape) * 10 + sum(shape))
+    src = torch.randn((e,) + shape, generator=g).to(dtype)
+    index = torch.randint(-3, n + 3, (e,), generator=g)
+    sd = src.to(device).requires_grad_(True)
+    idd = index.to(device)
+    out = edges.scatter_add(sd, idd, dim_size=n)
+    again = edges.scatter_add(sd.detach(), idd, dim_size=n)
+    assert torch.equal(out.detach(), again)
+    keep = (index >= 0) & (index < n)
+    ref = torch.zeros((n,) + shape, dtype=torch.float64).index_add_(0, index[keep], src[keep].double())
+    got = out.detach().double().cpu()
+    acc = e * 2.0 ** -24 * float(src.double().abs().max())
+    rel = 1e-5 if dtype == torch.float32 else 2.0 ** -8
+    assert bool(((got - ref).abs() <= rel * ref.abs() + acc).all())
+    up = torch.randn((n,) + shape, generator=g).to(dtype)
+    out.backward(up.to(device))
+    gref = torch.zeros((e,) + shape, dtype=dtype)
+    gref[keep] = up[index[keep]]
+    assert torch.equal(sd.grad.cpu(), gref)
