@@ -118,6 +118,16 @@ def test_masked_segments_straddle_tiles(device):
     _check(device, gb.edge_counts, gb.edge_counts, seed=91, src=src, dst=dst)
 
 
+def test_masked_star_graph_far_partner_tiles(device):
+    """A star graph (hub 0 and 1,200 leaves, both edge directions): every edge shares the hub, so the edge mask
+    is dense over one 2,400-token segment of 75 tiles and the far partner tiles of each tile lie past the
+    precomputed mask words' 64-tile window (those pairs take the in-kernel predicate)."""
+    leaves = np.arange(1, 1201, dtype=np.int32)
+    src = np.concatenate([np.zeros_like(leaves), leaves])
+    dst = np.concatenate([leaves, np.zeros_like(leaves)])
+    _check(device, [src.size], [src.size], seed=77, src=src, dst=dst)
+
+
 def test_masked_isolated_rows_give_zero(device):
     # Two disjoint edges in one segment: neither shares a node with the other.
     src = np.array([0, 2, 4], np.int32)
