@@ -8,10 +8,12 @@ softmax scale 1/4.  A step is one forward and one backward over the batch,
 with inputs already resident in HBM.
 
 Prints one JSON line: throughput in edge-tokens/s, MFMA utilisation of the
-dense-bf16 peak, the roofline of the dominant kernel (HIP events around every
-launch in the timed region) and a CPU baseline (the oracle's per-graph fp32
-attention forward + backward on a bounded sample of the same batch, on this
-host's cores).
+dense-bf16 peak, the roofline of the dominant kernel and a CPU baseline (the
+oracle's per-graph fp32 attention forward + backward on a bounded sample of
+the same batch, on this host's cores).  The step time comes from a timed
+region without instrumentation; the per-kernel durations of the roofline come
+from a second region of as many steps with HIP events around every library
+launch (its step time is reported as ms_per_step_profiled).
 """
 from __future__ import annotations
 
@@ -126,28 +128,38 @@ def main():
      "stack": bench_stack}[args.config](args)
 
 
-def timed(step, steps: int, warmup: int):
-    """Run warm-up steps, then time `steps` steps with HIP events and the per-kernel profiling hook."""
+def timed(step, steps: int, warmup: int, profile: bool = True):
+    """Warm-up steps, then `steps` timed steps without instrumentation: (ms per step by HIP events, wall ms per
+    step, per-kernel records, profiled ms per step).  With `profile`, a second region of `steps` steps runs with
+    the library's per-kernel hook, which records a HIP event pair around every library kernel launch on the
+    launch's own stream; its per-kernel average durations fill the records (empty without `profile`) and its
+    step time, which includes the event records between launches, is the fourth value (None without
+    `profile`)."""
     import torch
 
     from mind_amd import _lib
 
+    def region():
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        wall0 = time.perf_counter()
+        ev0.record()
+        for _ in range(steps):
+            step()
+        ev1.record()
+        torch.cuda.synchronize()
+        return ev0.elapsed_time(ev1) / steps, 1e3 * (time.perf_counter() - wall0) / steps
+
     for _ in range(warmup):
         step()
-    torch.cuda.synchronize()
+    ms, wall = region()
+    if not profile:
+        return ms, wall, {}, None
     _lib.profile_enable(True)
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    wall0 = time.perf_counter()
-    ev0.record()
-    for _ in range(steps):
-        step()
-    ev1.record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - wall0
+    ms_prof, _ = region()
     _lib.profile_enable(False)
-    kern = {name: {"avg_us": 1e3 * ms / n, "launches": n} for name, (ms, n) in _lib.profile_collect().items() if n}
-    return ev0.elapsed_time(ev1) / steps, 1e3 * wall / steps, kern
+    kern = {name: {"avg_us": 1e3 * t / n, "launches": n} for name, (t, n) in _lib.profile_collect().items() if n}
+    return ms, wall, kern, ms_prof
 
 
 def bench_varlen(args):
@@ -172,7 +184,7 @@ def bench_varlen(args):
         out, lse = attention.attn_fwd(q, k, v, cu, cu, maxlen, maxlen, scale)
         attention.attn_bwd(go, q, k, v, out, lse, cu, cu, maxlen, maxlen, scale)
 
-    ms_per_step, wall_ms, per_kernel = timed(step, args.steps, args.warmup)
+    ms_per_step, wall_ms, per_kernel, ms_prof = timed(step, args.steps, args.warmup)
     tokens_per_s = t / (ms_per_step * 1e-3)
     total_flops = 14 * DIM * pairs
     tflops = total_flops / (ms_per_step * 1e-3) / 1e12
@@ -210,7 +222,7 @@ def bench_varlen(args):
         "mfma_util_pct": 100.0 * tflops / PEAK_BF16_TFLOPS,
         "achieved_tflops": tflops,
         "algorithmic_flops_per_step": total_flops,
-        "wall_ms_per_step": wall_ms,
+        "wall_ms_per_step": wall_ms, "ms_per_step_profiled": ms_prof,
         "kernels": per_kernel,
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": achieved, "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": achieved / PEAK_BF16_TFLOPS, "traffic": traffic},
@@ -312,7 +324,7 @@ def bench_masked(args):
         out, lse = attention.attn_fwd(q, k, v, cu, cu, maxlen, maxlen, scale, src, dst)
         attention.attn_bwd(go, q, k, v, out, lse, cu, cu, maxlen, maxlen, scale, src, dst)
 
-    ms_per_step, wall_ms, per_kernel = timed(step, args.steps, args.warmup)
+    ms_per_step, wall_ms, per_kernel, ms_prof = timed(step, args.steps, args.warmup)
     eff_flops = 14 * DIM * stats["nnz"]
     exec_flops = 14 * DIM * stats["tiles_nonempty"] * 32 * 32
     tflops = eff_flops / (ms_per_step * 1e-3) / 1e12
@@ -336,7 +348,7 @@ def bench_masked(args):
         y = sab(x, adj)
         y.backward(gy)
 
-    block_ms, _, _ = timed(block_step, max(5, args.steps // 5), max(2, args.warmup // 5))
+    block_ms, _, _, _ = timed(block_step, max(5, args.steps // 5), max(2, args.warmup // 5), profile=False)
 
     result = {
         "metric": "edge-tokens/sec through ESA attn fwd+bwd; MFMA util % of bf16 peak",
@@ -362,7 +374,7 @@ def bench_masked(args):
         "mfma_util_pct": 100.0 * tflops / PEAK_BF16_TFLOPS,
         "achieved_tflops_effective": tflops,
         "achieved_tflops_executed_tiles": exec_flops / (ms_per_step * 1e-3) / 1e12,
-        "wall_ms_per_step": wall_ms,
+        "wall_ms_per_step": wall_ms, "ms_per_step_profiled": ms_prof,
         "kernels": per_kernel,
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": achieved, "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": achieved / PEAK_BF16_TFLOPS, "traffic": None,
@@ -458,7 +470,7 @@ def bench_gather(args):
             _gather_raw(x, src, dst, out)
             segment_sum_csr(y, indptr, out=agg)
 
-        ms, wall_ms, kern = timed(step, args.steps, args.warmup)
+        ms, wall_ms, kern, ms_prof = timed(step, args.steps, args.warmup)
         by = gather_bytes(GATHER_E, GATHER_N, GATHER_F, s)
         for kname, b in by.items():
             if kname in kern:
@@ -470,8 +482,9 @@ def bench_gather(args):
             _gather_raw(x, src_gen, dst_gen, out)
             segment_sum_csr(y, indptr, csr.perm, out=agg)
 
-        ms_gen, _, kern_gen = timed(step_gen, max(5, args.steps // 2), 2)
-        results[name] = {"ms_per_step": ms, "wall_ms_per_step": wall_ms, "kernels": kern,
+        ms_gen, _, kern_gen, _ = timed(step_gen, max(5, args.steps // 2), 2)
+        results[name] = {"ms_per_step": ms, "wall_ms_per_step": wall_ms, "ms_per_step_profiled": ms_prof,
+                         "kernels": kern,
                          "gb_per_s": (by["edge_gather"] + by["segment_sum"]) / (ms * 1e-3) / 1e9,
                          "generation_order": {"ms_per_step": ms_gen, "kernels": kern_gen}}
         del x, y, out, agg
@@ -481,7 +494,7 @@ def bench_gather(args):
     # streaming rate of this allocation on this box
     a = torch.empty(GATHER_E, GATHER_F, device=dev)
     b = torch.empty_like(a)
-    copy_ms, _, _ = timed(lambda: b.copy_(a), 5, 2)
+    copy_ms, _, _, _ = timed(lambda: b.copy_(a), 5, 2, profile=False)
     copy_gbs = 2 * a.numel() * 4 / (copy_ms * 1e-3) / 1e9
     del a, b
     torch.cuda.empty_cache()
@@ -549,7 +562,7 @@ def bench_fused_projection(x_dtype, src, dst, steps: int, warmup: int, seed: int
         torch.mm(x, w2.t(), out=pq)
         gather_add(pq[:, :f], pq[:, f:], src, dst, b, out=out)
 
-    ms_f, _, kern_f = timed(fused, steps, warmup)
+    ms_f, _, kern_f, _ = timed(fused, steps, warmup)
     fused_out = out[:4096].clone()
     del pq
     h = torch.empty(e, 2 * f, device=dev, dtype=x_dtype)
@@ -558,7 +571,7 @@ def bench_fused_projection(x_dtype, src, dst, steps: int, warmup: int, seed: int
         _gather_raw(x, src, dst, h)
         torch.addmm(b, h, w.t(), out=out)
 
-    ms_u, _, _ = timed(unfused, steps, warmup)
+    ms_u, _, _, _ = timed(unfused, steps, warmup, profile=False)
     diff = float((out[:4096] - fused_out).abs().max() / out[:4096].abs().max())
     del h, out, x
     torch.cuda.empty_cache()
@@ -612,7 +625,7 @@ def bench_block(args):
             x, ei, bm, n = _edge_tokens(gb, types, emb, proj, dev)
             model(x, ei, bm, n)
 
-    ms, wall_ms, kern = timed(step, args.steps, args.warmup)
+    ms, wall_ms, kern, ms_prof = timed(step, args.steps, args.warmup)
     result = {
         "metric": "edge-tokens/sec through the ESA block forward (fp32)",
         "value": t / (ms * 1e-3), "unit": "edge-tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -621,7 +634,7 @@ def bench_block(args):
         "config": {"workload": "config0: edge tokens (embed, gather, project) + ESA block M-S-P(1 seed) forward",
                    "graphs": gb.num_graphs, "edge_tokens": t, "max_seqlen": gb.max_seqlen, "dim": d, "heads": h,
                    "seed": args.seed},
-        "wall_ms_per_step": wall_ms, "kernels": kern,
+        "wall_ms_per_step": wall_ms, "ms_per_step_profiled": ms_prof, "kernels": kern,
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline_block(gb, types, emb, proj, model, h)
@@ -737,7 +750,7 @@ def bench_stack(args):
         opt.step()
         opt.zero_grad(set_to_none=True)
 
-    ms, wall_ms, kern = timed(step, args.steps, args.warmup)
+    ms, wall_ms, kern, ms_prof = timed(step, args.steps, args.warmup)
     attn_ms = sum(k["avg_us"] * k["launches"] for k in kern.values()) / 1e3 / args.steps
     result = {
         "metric": "edge-tokens/sec through the ESA encoder stack train step (fwd+bwd+AdamW, bf16-mixed)",
@@ -748,7 +761,7 @@ def bench_stack(args):
         "config": {"workload": "config4: ESA encoder stack M-M-S-S-M-M-S-S-P(4 seeds) train step",
                    "graphs": gb.num_graphs, "edge_tokens": t, "max_seqlen": gb.max_seqlen, "padded_items": n,
                    "dim": d, "heads": h, "mlp_hidden": 2048, "seed": args.seed},
-        "wall_ms_per_step": wall_ms, "kernels": kern,
+        "wall_ms_per_step": wall_ms, "ms_per_step_profiled": ms_prof, "kernels": kern,
         "library_kernel_ms_per_step": attn_ms,
     }
     print(json.dumps(result), flush=True)
