@@ -892,9 +892,12 @@ __global__ __launch_bounds__(kF32Threads) void attn_dkdv_f32_kernel(const AttnF3
 // is built by one launch whose blocks split into independent tasks: a plan
 // per direction (one block each), per-tile key norms (forward), row
 // statistics (backward), per-token segment bounds and, in masked mode, the
-// packed node pairs and per-tile node metadata.
+// packed node pairs and per-tile node metadata.  Blocks are dispatched in
+// enum order: the latency-bound tasks (the one-block plans, the per-tile
+// metadata, the small per-token tables) come first, so they run beside the
+// bandwidth-bound key norms and row statistics instead of after them.
 
-enum PrepTask { kPlanQ, kPlanK, kKnorm, kRows, kBoundsQ, kBoundsK, kNodes, kMeta, kPrepTasks };
+enum PrepTask { kPlanQ, kPlanK, kMeta, kNodes, kBoundsQ, kBoundsK, kKnorm, kRows, kPrepTasks };
 
 struct PrepArgs {
   const int* cu_q; const int* cu_k; int nseg;
@@ -1020,30 +1023,25 @@ DEVI void bounds_item(const int* __restrict__ cu_outer, const int* __restrict__ 
   bounds[t] = b;
 }
 
-// Per 32-token tile: min / max node id over both endpoints and a 64-bit
-// signature of (node & 63).
-DEVI void meta_item(const int* __restrict__ src, const int* __restrict__ dst, int total, int4* __restrict__ meta,
-                    int tile) {
-  // All 64 loads are independent and issued before the first use.
-  int a[kTile], b[kTile];
-  const int t0 = tile * kTile;
+// Per 32-token tile, one wave: min / max node id over both endpoints and a
+// 64-bit signature of (node & 63).  Lanes 0-31 read the tile's src ids and
+// lanes 32-63 its dst ids (two coalesced loads), then butterfly reductions.
+DEVI void meta_wave(const int* __restrict__ src, const int* __restrict__ dst, int total, int4* __restrict__ meta,
+                    int tile, int lane) {
+  const int t = tile * kTile + (lane & 31);
+  const bool in = t < total;
+  const int v = in ? (lane < 32 ? src[t] : dst[t]) : 0;
+  int lo = in ? v : INT_MAX, hi = in ? v : INT_MIN;
+  unsigned sig_lo = in && (v & 63) < 32 ? 1u << (v & 31) : 0u;
+  unsigned sig_hi = in && (v & 63) >= 32 ? 1u << (v & 31) : 0u;
 #pragma unroll
-  for (int i = 0; i < kTile; ++i) {
-    const bool in = t0 + i < total;
-    a[i] = in ? src[t0 + i] : 0;
-    b[i] = in ? dst[t0 + i] : 0;
+  for (int o = 32; o >= 1; o >>= 1) {
+    lo = min(lo, __shfl_xor(lo, o));
+    hi = max(hi, __shfl_xor(hi, o));
+    sig_lo |= __shfl_xor(sig_lo, o);
+    sig_hi |= __shfl_xor(sig_hi, o);
   }
-  int lo = INT_MAX, hi = INT_MIN;
-  unsigned long long sig = 0ull;
-#pragma unroll
-  for (int i = 0; i < kTile; ++i) {
-    if (t0 + i < total) {
-      lo = min(lo, min(a[i], b[i]));
-      hi = max(hi, max(a[i], b[i]));
-      sig |= (1ull << (a[i] & 63)) | (1ull << (b[i] & 63));
-    }
-  }
-  meta[tile] = make_int4(lo, hi, (int)(sig & 0xffffffffull), (int)(sig >> 32));
+  if (lane == 0) meta[tile] = make_int4(lo, hi, (int)sig_lo, (int)sig_hi);
 }
 
 __global__ __launch_bounds__(256) void prep_kernel(const PrepArgs p) {
@@ -1061,24 +1059,25 @@ __global__ __launch_bounds__(256) void prep_kernel(const PrepArgs p) {
     return;
   }
   b -= p.nb[kPlanK];
-  if (b < p.nb[kKnorm]) { knorm_block(p.k, p.total_k, p.heads, p.tk_pad / kTile, p.knorm, b, tid); return; }
-  b -= p.nb[kKnorm];
-  if (b < p.nb[kRows]) { rowstats_item(p, (long)b * 256 + tid); return; }
-  b -= p.nb[kRows];
-  if (b < p.nb[kBoundsQ]) { bounds_item(p.cu_q, p.cu_k, p.nseg, p.total_q, p.tq_pad, p.bounds_q, b * 256 + tid); return; }
-  b -= p.nb[kBoundsQ];
-  if (b < p.nb[kBoundsK]) { bounds_item(p.cu_k, p.cu_q, p.nseg, p.total_k, p.tk_pad, p.bounds_k, b * 256 + tid); return; }
-  b -= p.nb[kBoundsK];
+  if (b < p.nb[kMeta]) {
+    const int tile = (b * 256 + tid) >> 6;   // wave-uniform
+    if (tile < p.tq_pad / kTile) meta_wave(p.tok_src, p.tok_dst, p.total_q, p.meta, tile, tid & 63);
+    return;
+  }
+  b -= p.nb[kMeta];
   if (b < p.nb[kNodes]) {
     const int t = b * 256 + tid;
     if (t < p.tq_pad) p.nodes[t] = t < p.total_q ? make_int2(p.tok_src[t], p.tok_dst[t]) : make_int2(-1, -1);
     return;
   }
   b -= p.nb[kNodes];
-  if (b < p.nb[kMeta]) {
-    const int tile = b * 256 + tid;
-    if (tile < p.tq_pad / kTile) meta_item(p.tok_src, p.tok_dst, p.total_q, p.meta, tile);
-  }
+  if (b < p.nb[kBoundsQ]) { bounds_item(p.cu_q, p.cu_k, p.nseg, p.total_q, p.tq_pad, p.bounds_q, b * 256 + tid); return; }
+  b -= p.nb[kBoundsQ];
+  if (b < p.nb[kBoundsK]) { bounds_item(p.cu_k, p.cu_q, p.nseg, p.total_k, p.tk_pad, p.bounds_k, b * 256 + tid); return; }
+  b -= p.nb[kBoundsK];
+  if (b < p.nb[kKnorm]) { knorm_block(p.k, p.total_k, p.heads, p.tk_pad / kTile, p.knorm, b, tid); return; }
+  b -= p.nb[kKnorm];
+  if (b < p.nb[kRows]) rowstats_item(p, (long)b * 256 + tid);
 }
 
 __global__ void edge_mask_dense_kernel(const int* __restrict__ src, const int* __restrict__ dst,
@@ -1203,7 +1202,7 @@ int launch_prep(PrepArgs& p, bool forward, bool masked, hipStream_t st) {
   p.nb[kBoundsQ] = blocks_for(p.tq_pad);
   p.nb[kBoundsK] = forward ? 0 : blocks_for(p.tk_pad);
   p.nb[kNodes] = masked ? blocks_for(p.tq_pad) : 0;
-  p.nb[kMeta] = masked ? blocks_for(p.tq_pad / kTile) : 0;
+  p.nb[kMeta] = masked ? blocks_for((long)(p.tq_pad / kTile) * 64) : 0;
   long grid = 0;
   for (int i = 0; i < kPrepTasks; ++i) grid += p.nb[i];
   ESA_TIMED(esa_profile::kAttnPrep, st,
