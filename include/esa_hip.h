@@ -244,14 +244,18 @@ ESA_API int esa_layer_norm_bwd_workspace_size(int64_t rows, int features, size_t
 
 /* Backward: with g = dy + dy_lp (dy of dy_dtype and/or the bf16 gradient of */
 /* y_lp; NULL = zero, not both), dx (x_dtype) = rstd (g w - mean(g w) -      */
-/* xhat mean(g w xhat)) and, when dweight / dbias are given, the fp32 column */
-/* sums of g xhat / g, reduced in a fixed order (deterministic).  The        */
-/* workspace (size from the query) is needed only for dweight / dbias.       */
+/* xhat mean(g w xhat)) + dx_add and, when dweight / dbias are given, the    */
+/* fp32 column sums of g xhat / g, reduced in a fixed order (deterministic). */
+/* dx_add (x_dtype, NULL = none, must not overlap dx) is the gradient of x   */
+/* from its other uses, e.g. a residual add: autograd would otherwise sum    */
+/* the two in a separate pass.  The workspace (size from the query) is       */
+/* needed only for dweight / dbias.                                          */
 ESA_API int esa_layer_norm_bwd(const void* x, int x_dtype, const float* weight,
                        const float* mean, const float* rstd, const void* dy,
-                       int dy_dtype, const void* dy_lp, int64_t rows, int features,
-                       void* dx, float* dweight, float* dbias, void* workspace,
-                       size_t workspace_bytes, void* stream);
+                       int dy_dtype, const void* dy_lp, const void* dx_add,
+                       int64_t rows, int features, void* dx, float* dweight,
+                       float* dbias, void* workspace, size_t workspace_bytes,
+                       void* stream);
 
 /* ------------------------------------------------------------------------ */
 /* Column sums out[c] = sum_r x[r][c] (fp32, [cols]) of x [rows, cols]      */

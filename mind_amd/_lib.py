@@ -69,9 +69,9 @@ _PROTOS = {
     # x x_dtype w b rows features eps y y_dtype y_lp mean rstd stream
     "esa_layer_norm_fwd": (_c_int, [_vp, _c_int, _vp, _vp, _c_i64, _c_int, _c_f, _vp, _c_int, _vp, _vp, _vp, _vp]),
     "esa_layer_norm_bwd_workspace_size": (_c_int, [_c_i64, _c_int, ctypes.POINTER(_c_sz)]),
-    # x x_dtype w mean rstd dy dy_dtype dy_lp rows features dx dw db ws bytes stream
-    "esa_layer_norm_bwd": (_c_int, [_vp, _c_int, _vp, _vp, _vp, _vp, _c_int, _vp, _c_i64, _c_int, _vp, _vp, _vp, _vp,
-                                    _c_sz, _vp]),
+    # x x_dtype w mean rstd dy dy_dtype dy_lp dx_add rows features dx dw db ws bytes stream
+    "esa_layer_norm_bwd": (_c_int, [_vp, _c_int, _vp, _vp, _vp, _vp, _c_int, _vp, _vp, _c_i64, _c_int, _vp, _vp, _vp,
+                                    _vp, _c_sz, _vp]),
     "esa_column_sum_workspace_size": (_c_int, [_c_i64, _c_int, ctypes.POINTER(_c_sz)]),
     "esa_column_sum": (_c_int, [_vp, _c_int, _c_i64, _c_int, _vp, _vp, _c_sz, _vp]),
     "esa_mab_residual_fwd": (_c_int, [_vp, _vp, _vp, _c_i64, _c_int, _vp, _vp]),

@@ -271,7 +271,8 @@ __global__ __launch_bounds__(256) void ln_fwd_kernel(const TX* __restrict__ x, c
   }
 }
 
-// dx = rstd (g w - mean(g w) - xhat mean(g w xhat)), g = dy + dy_lp, per row;
+// dx = rstd (g w - mean(g w) - xhat mean(g w xhat)) + dres, g = dy + dy_lp,
+// per row (dres, the gradient of x from its other uses, or none);
 // dw = sum_rows g xhat, db = sum_rows g per column.  Wave w of block B takes
 // rows 4 B + w, then every 4 gridDim.x further (the next row's loads are in
 // flight while a row is computed); its column sums stay in registers, the
@@ -280,8 +281,8 @@ template <typename TX, typename TG, int K>
 __global__ __launch_bounds__(256) void ln_bwd_kernel(const TX* __restrict__ x, const float* __restrict__ w,
                                                      const float* __restrict__ mean, const float* __restrict__ rstd,
                                                      const TG* __restrict__ dy, const bf16* __restrict__ dylp,
-                                                     int64_t rows, int D, TX* __restrict__ dx,
-                                                     float* __restrict__ part) {
+                                                     const TX* __restrict__ dres, int64_t rows, int D,
+                                                     TX* __restrict__ dx, float* __restrict__ part) {
   __shared__ float red[4][2][256 * K];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t stride = (int64_t)gridDim.x * 4;
@@ -292,11 +293,12 @@ __global__ __launch_bounds__(256) void ln_bwd_kernel(const TX* __restrict__ x, c
     wv[k] = (w && f < D) ? load4(w + f) : f32x4{1.f, 1.f, 1.f, 1.f};
     aw[k] = ab[k] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
-  auto load_row = [&](int64_t r, f32x4 (&xv)[K], f32x4 (&gv)[K]) {
+  auto load_row = [&](int64_t r, f32x4 (&xv)[K], f32x4 (&gv)[K], f32x4 (&rv)[K]) {
 #pragma unroll
     for (int k = 0; k < K; ++k) {
       const int f = 4 * (lane + 64 * k);
       f32x4 g = f32x4{0.f, 0.f, 0.f, 0.f};
+      rv[k] = g;
       if (f < D) {
         xv[k] = load4(x + r * D + f);
         if (dy) g = load4(dy + r * D + f);
@@ -305,6 +307,7 @@ __global__ __launch_bounds__(256) void ln_bwd_kernel(const TX* __restrict__ x, c
 #pragma unroll
           for (int e = 0; e < 4; ++e) g[e] += h[e];
         }
+        if (dres) rv[k] = load4(dres + r * D + f);
       } else {
         xv[k] = g;
       }
@@ -312,12 +315,12 @@ __global__ __launch_bounds__(256) void ln_bwd_kernel(const TX* __restrict__ x, c
     }
   };
   int64_t row = (int64_t)blockIdx.x * 4 + wave;
-  f32x4 xv[K], gv[K];
-  if (row < rows) load_row(row, xv, gv);
+  f32x4 xv[K], gv[K], rv[K];
+  if (row < rows) load_row(row, xv, gv, rv);
   while (row < rows) {
     const int64_t next = row + stride;
-    f32x4 xn[K], gn[K];
-    if (next < rows) load_row(next, xn, gn);
+    f32x4 xn[K], gn[K], rn[K];
+    if (next < rows) load_row(next, xn, gn, rn);
     const float mu = mean[row], rs = rstd[row];
     float c1 = 0.f, c2 = 0.f;
     f32x4 xh[K], dh[K];
@@ -341,13 +344,14 @@ __global__ __launch_bounds__(256) void ln_bwd_kernel(const TX* __restrict__ x, c
       if (f >= D) break;
       f32x4 o;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) o[e] = rs * (dh[k][e] - c2 - xh[k][e] * c1);
+      for (int e = 0; e < 4; ++e) o[e] = rs * (dh[k][e] - c2 - xh[k][e] * c1) + rv[k][e];
       store4(dx + row * D + f, o);
     }
 #pragma unroll
     for (int k = 0; k < K; ++k) {
       xv[k] = xn[k];
       gv[k] = gn[k];
+      rv[k] = rn[k];
     }
     row = next;
   }
@@ -463,9 +467,9 @@ void ln_fwd_go(int K, dim3 grid, hipStream_t st, const TX* x, const float* w, co
 
 template <typename TX, typename TG>
 void ln_bwd_go(int K, dim3 grid, hipStream_t st, const TX* x, const float* w, const float* mean, const float* rstd,
-               const TG* dy, const bf16* dylp, int64_t rows, int D, TX* dx, float* part) {
+               const TG* dy, const bf16* dylp, const TX* dres, int64_t rows, int D, TX* dx, float* part) {
 #define ESA_LN_BWD(KK) hipLaunchKernelGGL((ln_bwd_kernel<TX, TG, KK>), grid, dim3(256), 0, st, x, w, mean, rstd, dy, \
-                                          dylp, rows, D, dx, part)
+                                          dylp, dres, rows, D, dx, part)
   if (K == 1) ESA_LN_BWD(1);
   else if (K == 2) ESA_LN_BWD(2);
   else if (K == 4) ESA_LN_BWD(4);
@@ -651,7 +655,8 @@ extern "C" ESA_API int esa_layer_norm_bwd_workspace_size(int64_t rows, int featu
 
 extern "C" ESA_API int esa_layer_norm_bwd(const void* x, int x_dtype, const float* weight, const float* mean,
                                           const float* rstd, const void* dy, int dy_dtype, const void* dy_lp,
-                                          int64_t rows, int features, void* dx, float* dweight, float* dbias,
+                                          const void* dx_add, int64_t rows, int features, void* dx,
+                                          float* dweight, float* dbias,
                                           void* workspace, size_t workspace_bytes, void* stream) {
   if (rows < 0 || features < 4 || features > kLnMaxFeatures || features % 4) return ESA_ERR_SHAPE;
   if ((x_dtype != ESA_F32 && x_dtype != ESA_BF16) || (dy && dy_dtype != ESA_F32 && dy_dtype != ESA_BF16))
@@ -670,7 +675,8 @@ extern "C" ESA_API int esa_layer_norm_bwd(const void* x, int x_dtype, const floa
     return ESA_OK;
   }
   if (!x || !mean || !rstd || !dx || (!dy && !dy_lp)) return ESA_ERR_NULL;
-  if (!aligned16(x) || !aligned16(weight) || !aligned16(dy) || !aligned16(dy_lp) || !aligned16(dx))
+  if (!aligned16(x) || !aligned16(weight) || !aligned16(dy) || !aligned16(dy_lp) || !aligned16(dx) ||
+      !aligned16(dx_add))
     return ESA_ERR_ALIGN;
   const int blocks = ln_bwd_blocks(rows);
   float* part = params ? (float*)workspace : nullptr;
@@ -680,19 +686,21 @@ extern "C" ESA_API int esa_layer_norm_bwd(const void* x, int x_dtype, const floa
   ESA_TIMED(esa_profile::kLayerNormBwd, st, {
     const dim3 grid((unsigned)blocks);
     if (x_dtype == ESA_F32) {
+      const float* ra = (const float*)dx_add;
       if (!dy || dy_dtype == ESA_F32)
-        ln_bwd_go(K, grid, st, (const float*)x, weight, mean, rstd, (const float*)dy, lp, rows, features, (float*)dx,
-                  part);
+        ln_bwd_go(K, grid, st, (const float*)x, weight, mean, rstd, (const float*)dy, lp, ra, rows, features,
+                  (float*)dx, part);
       else
-        ln_bwd_go(K, grid, st, (const float*)x, weight, mean, rstd, (const bf16*)dy, lp, rows, features, (float*)dx,
-                  part);
+        ln_bwd_go(K, grid, st, (const float*)x, weight, mean, rstd, (const bf16*)dy, lp, ra, rows, features,
+                  (float*)dx, part);
     } else {
+      const bf16* ra = (const bf16*)dx_add;
       if (!dy || dy_dtype == ESA_F32)
-        ln_bwd_go(K, grid, st, (const bf16*)x, weight, mean, rstd, (const float*)dy, lp, rows, features, (bf16*)dx,
-                  part);
+        ln_bwd_go(K, grid, st, (const bf16*)x, weight, mean, rstd, (const float*)dy, lp, ra, rows, features,
+                  (bf16*)dx, part);
       else
-        ln_bwd_go(K, grid, st, (const bf16*)x, weight, mean, rstd, (const bf16*)dy, lp, rows, features, (bf16*)dx,
-                  part);
+        ln_bwd_go(K, grid, st, (const bf16*)x, weight, mean, rstd, (const bf16*)dy, lp, ra, rows, features,
+                  (bf16*)dx, part);
     }
     if (params)
       reduce_columns(part, blocks, 2 * features, part + (size_t)blocks * 2 * features, features, dweight, dbias, st);

@@ -180,9 +180,12 @@ def _sab_forward_packed(blk: "SABComplete", X: torch.Tensor, tokens: PackedSets)
     else:
         out = blk.proj_1(X) + _packed_mab(blk.sab.mab, x_mm, x_mm, cu, cu, n, n, mask_kwargs)
     if blk.use_mlp:
-        out_mlp = blk.mlp(_gemm_input_norm(blk.norm_mlp.ln, out))
+        # out feeds the MLP's LayerNorm and the residual: the pass-through output hands the residual's
+        # gradient to the LayerNorm backward, which adds it to its input gradient in the same pass
+        y, y_mm, out_res = layer_norm(out, blk.norm_mlp.ln, full=False, lowp=True, passthrough=True)
+        out_mlp = blk.mlp(y if y_mm is None else y_mm)
         if out.shape[-1] == out_mlp.shape[-1]:
-            out = out_mlp + out
+            out = out_mlp + out_res
     if blk.residual_dropout > 0:
         out = F.dropout(out, p=blk.residual_dropout)
     return out

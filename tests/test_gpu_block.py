@@ -203,10 +203,13 @@ def _ln_oracle(x, w, b, g, eps=1e-8):
     return y.detach(), xd.grad, wd.grad, bd.grad
 
 
+@pytest.mark.parametrize("passthrough", [False, True], ids=["plain", "passthrough"])
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("rows,feat", [(1, 4), (5, 128), (1000, 512), (4099, 512), (300, 260), (64, 2048)])
-def test_layer_norm_fwd_bwd(device, dtype, rows, feat):
+def test_layer_norm_fwd_bwd(device, dtype, rows, feat, passthrough):
     """y (x's dtype) plus its bf16 copy; backward with gradients on both outputs, against the fp64 oracle.
+    With the pass-through output (x itself, as a residual uses it), its gradient is added to dx in the kernel:
+    dx = the oracle's dx + that gradient.
 
     Bars: fp32 outputs 1e-5 * max(1, max|ref|) (the fp32 bar, norm-wise); bf16 outputs one rounding
     (2^-8 relative) + 1e-5 * scale (the fp32 evaluation's error); dweight / dbias 1e-5 * max(1, max|ref|) plus
@@ -219,11 +222,19 @@ def test_layer_norm_fwd_bwd(device, dtype, rows, feat):
     gy = torch.randn(rows, feat, generator=gen).to(dtype)
     gl = torch.randn(rows, feat, generator=gen).to(torch.bfloat16)
     xd, wd, bd = x.to(device).requires_grad_(True), w.to(device).requires_grad_(True), b.to(device).requires_grad_(True)
-    y, ylp = _LayerNorm.apply(xd, wd, bd, 1e-8, dtype, True, True)
+    outs = _LayerNorm.apply(xd, wd, bd, 1e-8, dtype, True, True, passthrough)
+    y, ylp = outs[:2]
     assert y.dtype == dtype and ylp.dtype == torch.bfloat16
     assert torch.equal(ylp, y.to(torch.bfloat16))
-    torch.autograd.backward([y, ylp], [gy.to(device), gl.to(device)])
+    gr = torch.randn(rows, feat, generator=gen).to(dtype)
+    if passthrough:
+        assert torch.equal(outs[2], xd.detach())
+        torch.autograd.backward(list(outs), [gy.to(device), gl.to(device), gr.to(device)])
+    else:
+        torch.autograd.backward([y, ylp], [gy.to(device), gl.to(device)])
     ref, rdx, rdw, rdb = _ln_oracle(x, w, b, gy.double() + gl.double())
+    if passthrough:
+        rdx = rdx + gr.double()
     if dtype == torch.float32:
         assert_close = lambda got, r, what: _f32_norm_close(got, r, what)  # noqa: E731
     else:
@@ -280,16 +291,21 @@ def test_layer_norm_edge_cases(device):
     w = torch.randn(64, device=device, requires_grad=True)
     b = torch.randn(64, device=device, requires_grad=True)
     x = torch.full((3, 64), 2.5, device=device)
-    y = _LayerNorm.apply(x, w, b, 1e-8, torch.float32, True, False)
+    y = _LayerNorm.apply(x, w, b, 1e-8, torch.float32, True, False, False)
     assert torch.allclose(y, b.detach().expand(3, 64), atol=1e-6)
     e = torch.empty(0, 64, device=device, requires_grad=True)
-    ye = _LayerNorm.apply(e, w, b, 1e-8, torch.float32, True, False)
+    ye = _LayerNorm.apply(e, w, b, 1e-8, torch.float32, True, False, False)
     ye.sum().backward()
     assert torch.equal(w.grad, torch.zeros_like(w)) and torch.equal(b.grad, torch.zeros_like(b))
     ln = torch.nn.LayerNorm(6).to(device)
     x6 = torch.randn(4, 6, device=device)
     assert not supported(x6, ln)
     assert torch.equal(layer_norm(x6, ln)[0], ln(x6))
+    # only the pass-through output carries a gradient: dx is that gradient
+    xp = torch.randn(5, 64, device=device, requires_grad=True)
+    _, _, xr = layer_norm(xp, torch.nn.LayerNorm(64).to(device), passthrough=True)
+    (xr * 3).sum().backward()
+    assert torch.equal(xp.grad, torch.full_like(xp, 3.0))
     lib = _lib.load()
     assert lib.esa_layer_norm_fwd(x.data_ptr(), 0, None, None, 3, 6, 1e-8, x.data_ptr(), 0, None, x.data_ptr(),
                                   x.data_ptr(), None) == -2
