@@ -73,6 +73,9 @@ class _MabEpilogue(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, o, weight, bias, x):
+        from .linear import cast_param   # deferred: linear.py is a sibling with its own imports
+        ctx.dtypes = (weight.dtype, None if bias is None else bias.dtype)   # the gradients are returned in these
+        weight, bias = cast_param(weight, o.dtype), cast_param(bias, o.dtype)
         z = F.linear(o, weight, bias)
         lib, st, code = _lib.load(), _lib.stream_of(o), _DTYPES[o.dtype]
         if x is None:
@@ -84,7 +87,7 @@ class _MabEpilogue(torch.autograd.Function):
             _lib.check(lib.esa_mab_residual_fwd(z.data_ptr(), o.data_ptr(), x.data_ptr(), z.numel(), code,
                                                 y.data_ptr(), st), "esa_mab_residual_fwd")
         ctx.save_for_backward(o, weight, z)
-        ctx.has_x, ctx.has_bias = x is not None, bias is not None
+        ctx.has_x = x is not None
         return y
 
     @staticmethod
@@ -102,9 +105,10 @@ class _MabEpilogue(torch.autograd.Function):
             g_o = g.to(z.dtype).contiguous()
             _lib.check(lib.esa_mish_bwd(z.data_ptr(), g_o.data_ptr(), z.numel(), code, dz.data_ptr(), st),
                        "esa_mish_bwd")
+        wdt, bdt = ctx.dtypes
         do = torch.addmm(g_o, dz, weight) if ctx.needs_input_grad[0] else None
-        dw = weight_grad(dz, o).to(weight.dtype) if ctx.needs_input_grad[1] else None
-        db = column_sum(dz).to(dz.dtype) if ctx.has_bias and ctx.needs_input_grad[2] else None
+        dw = weight_grad(dz, o).to(wdt) if ctx.needs_input_grad[1] else None
+        db = column_sum(dz).to(bdt) if bdt is not None and ctx.needs_input_grad[2] else None
         return do, dw, db, (g if ctx.has_x and ctx.needs_input_grad[3] else None)
 
 
@@ -114,14 +118,17 @@ def mab_epilogue(o: torch.Tensor, fc_o: nn.Linear, residual: torch.Tensor | None
     if not o.is_cuda:
         y = o + F.mish(fc_o(o))
         return y if residual is None else residual + y
-    from .linear import autocast_params
-    o, w, b = autocast_params(o, fc_o.weight, fc_o.bias)
-    if o.dtype not in _DTYPES or w.dtype != o.dtype or (b is not None and b.dtype != o.dtype) or o.dim() != 2:
-        y = mish(F.linear(o, w, b), o)
+    from .linear import compute_dtype
+    w, b = fc_o.weight, fc_o.bias
+    dt = compute_dtype(o, w, b)
+    if dt not in _DTYPES or o.dim() != 2:
+        o = o if dt is None else o.to(dt)
+        y = mish(F.linear(o, w if dt is None else w.to(dt), b if dt is None or b is None else b.to(dt)), o)
         return y if residual is None else residual + y
+    o = o.to(dt).contiguous()
     if residual is not None and (residual.dtype != torch.float32 or residual.shape != o.shape):
-        return residual + _MabEpilogue.apply(o.contiguous(), w, b, None)
-    return _MabEpilogue.apply(o.contiguous(), w, b, None if residual is None else residual.contiguous())
+        return residual + _MabEpilogue.apply(o, w, b, None)
+    return _MabEpilogue.apply(o, w, b, None if residual is None else residual.contiguous())
 
 
 class Mish(nn.Mish):

@@ -9,7 +9,10 @@ reduction fills the chip and is rounded to the weight's dtype once, as the
 single GEMM's fp32 accumulator is.  Forward (F.linear) and dx = g W are
 unchanged; the bias gradient is a deterministic column sum (esa_column_sum).
 Under autocast the inputs are cast as autocast casts F.linear's (x, weight
-and bias to the autocast dtype).
+and bias to the autocast dtype); the autograd functions take the parameters
+in their own dtype and cast them inside, so the fp32 weight and bias
+gradients are returned as they are computed, in fp32, instead of being
+rounded to the autocast dtype and cast back by a second kernel.
 
 Reference: the nn.Linear layers of the MAB (esa/mha.py:12-15) and of the MLPs
 (esa/mlp_utils.py:18-37).
@@ -76,41 +79,47 @@ def column_sum(g: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def compute_dtype(x: torch.Tensor, *params: torch.Tensor | None):
+    """The dtype a Linear over x computes in: the autocast dtype under autocast (x and the parameters are
+    cast to it, as autocast casts F.linear's inputs), else x's dtype when every parameter has it; None for
+    mixed dtypes outside autocast (the callers then leave the call to torch's own checks and errors)."""
+    if x.is_cuda and torch.is_autocast_enabled("cuda"):
+        return torch.get_autocast_dtype("cuda")
+    return x.dtype if all(p is None or p.dtype == x.dtype for p in params) else None
+
+
+def cast_param(p: torch.Tensor | None, dt: torch.dtype):
+    return None if p is None else p.to(dt)
+
+
 class _Linear(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, weight, bias):
-        ctx.save_for_backward(x, weight)
-        ctx.has_bias = bias is not None
-        return F.linear(x, weight, bias)
+        w, b = cast_param(weight, x.dtype), cast_param(bias, x.dtype)
+        ctx.save_for_backward(x, w)
+        ctx.dtypes = (weight.dtype, None if bias is None else bias.dtype)
+        return F.linear(x, w, b)
 
     @staticmethod
     def backward(ctx, g):
-        x, weight = ctx.saved_tensors
+        x, w = ctx.saved_tensors
+        wdt, bdt = ctx.dtypes
         g = g.contiguous()
-        dx = g.mm(weight) if ctx.needs_input_grad[0] else None
-        dw = weight_grad(g, x).to(weight.dtype) if ctx.needs_input_grad[1] else None
-        db = column_sum(g).to(g.dtype) if ctx.has_bias and ctx.needs_input_grad[2] else None
+        dx = g.mm(w) if ctx.needs_input_grad[0] else None
+        dw = weight_grad(g, x).to(wdt) if ctx.needs_input_grad[1] else None
+        db = column_sum(g).to(bdt) if bdt is not None and ctx.needs_input_grad[2] else None
         return dx, dw, db
 
 
 def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None) -> torch.Tensor:
     """F.linear(x, weight, bias) with the split-K weight gradient (device tensors; CPU tensors use F.linear)."""
-    if not x.is_cuda:
-        return F.linear(x, weight, bias)
-    x, weight, bias = autocast_params(x, weight, bias)
-    if x.dtype != weight.dtype or (bias is not None and bias.dtype != x.dtype):
-        return F.linear(x, weight, bias)   # mixed dtypes: torch's own type checks and errors
+    dt = compute_dtype(x, weight, bias) if x.is_cuda else None
+    if dt is None:
+        return F.linear(x, weight, bias)   # CPU, or mixed dtypes: torch's own type checks and errors
+    x = x.to(dt)
     lead = x.shape[:-1]
     y = _Linear.apply(x.reshape(-1, x.shape[-1]).contiguous(), weight, bias)
     return y.view(*lead, weight.shape[0])
-
-
-def autocast_params(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None):
-    """(x, weight, bias) cast as autocast casts F.linear's inputs (unchanged outside autocast)."""
-    if x.is_cuda and torch.is_autocast_enabled("cuda"):
-        dt = torch.get_autocast_dtype("cuda")
-        return x.to(dt), weight.to(dt), None if bias is None else bias.to(dt)
-    return x, weight, bias
 
 
 class _QKV(torch.autograd.Function):
@@ -123,12 +132,15 @@ class _QKV(torch.autograd.Function):
     def forward(ctx, xq, xk, wq, bq, wk, bk, wv, bv):
         same = xk is None
         xk_ = xq if same else xk
+        dt = xq.dtype
+        # the parameters' own dtypes: the backward returns its fp32 gradients in them
+        ctx.params = tuple(None if p is None else p.dtype for p in (wq, bq, wk, bk, wv, bv))
+        wq, bq, wk, bk, wv, bv = (cast_param(p, dt) for p in (wq, bq, wk, bk, wv, bv))
         q = F.linear(xq, wq, bq)
         k = F.linear(xk_, wk, bk)
         v = F.linear(xk_, wv, bv)
         ctx.save_for_backward(xq, None if same else xk, wq, wk, wv)
         ctx.same = same
-        ctx.biases = (bq is not None, bk is not None, bv is not None)
         return q, k, v
 
     @staticmethod
@@ -149,9 +161,10 @@ class _QKV(torch.autograd.Function):
                 dxk = gk.mm(wk)
                 dxk.addmm_(gv, wv)
         grads = [dxq, dxk]
-        for i, (g, x, w) in enumerate(((gq, xq, wq), (gk, xk, wk), (gv, xk, wv))):
-            dw = weight_grad(g, x).to(w.dtype) if ctx.needs_input_grad[2 + 2 * i] else None
-            db = (column_sum(g).to(g.dtype) if ctx.biases[i] and ctx.needs_input_grad[3 + 2 * i] else None)
+        for i, (g, x) in enumerate(((gq, xq), (gk, xk), (gv, xk))):
+            wdt, bdt = ctx.params[2 * i], ctx.params[2 * i + 1]
+            dw = weight_grad(g, x).to(wdt) if ctx.needs_input_grad[2 + 2 * i] else None
+            db = column_sum(g).to(bdt) if bdt is not None and ctx.needs_input_grad[3 + 2 * i] else None
             grads += [dw, db]
         return tuple(grads)
 
@@ -159,16 +172,14 @@ class _QKV(torch.autograd.Function):
 def qkv_projection(fc_q: nn.Linear, fc_k: nn.Linear, fc_v: nn.Linear, xq: torch.Tensor, xk: torch.Tensor):
     """(fc_q(xq), fc_k(xk), fc_v(xk)) on 2-D token rows, with the fused-accumulation backward of _QKV on
     device tensors (``xk is xq`` for self-attention)."""
-    if not xq.is_cuda:
-        return fc_q(xq), fc_k(xk), fc_v(xk)
+    params = (fc_q.weight, fc_q.bias, fc_k.weight, fc_k.bias, fc_v.weight, fc_v.bias)
     same = xk is xq
-    xq, wq, bq = autocast_params(xq, fc_q.weight, fc_q.bias)
-    xk_, wk, bk = autocast_params(xk, fc_k.weight, fc_k.bias)
-    _, wv, bv = autocast_params(xk, fc_v.weight, fc_v.bias)
-    dts = {t.dtype for t in (xq, xk_, wq, wk, wv)}
-    if len(dts) != 1:
-        return F.linear(xq, wq, bq), F.linear(xk_, wk, bk), F.linear(xk_, wv, bv)
-    return _QKV.apply(xq.contiguous(), None if same else xk_.contiguous(), wq, bq, wk, bk, wv, bv)
+    dt = compute_dtype(xq, xk, *params) if xq.is_cuda else None
+    if dt is None:
+        return fc_q(xq), fc_k(xk), fc_v(xk)
+    xq = xq.to(dt)
+    xk_ = None if same else xk.to(dt).contiguous()
+    return _QKV.apply(xq.contiguous(), xk_, *params)
 
 
 def apply(layer: nn.Module, x: torch.Tensor) -> torch.Tensor:
