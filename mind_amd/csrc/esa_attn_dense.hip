@@ -48,6 +48,7 @@ constexpr int kStageTok = 64;      // partner tokens per staging step (two tiles
 struct DenseArgs {
   const bf16* q; const bf16* k; const bf16* v; const bf16* out; const bf16* dout;
   const float2* aux;           // dK/dV: per (head, query) {-LSE2, -D}, [H][tq_pad]
+  float2* aux_out;             // dQ: writes aux for its queries (dQ runs first)
   const float* lse;            // dQ: [H][Tq] natural log
   const float* knorm;          // forward: max |k| per (head, global 32-token tile), [H][tk_tiles]
   int tk_tiles;
@@ -349,6 +350,9 @@ __global__ __launch_bounds__(256) ESA_WAVES_ATTR(ESA_DENSE_WAVES_DQ) void dense_
       const float lq = a.lse[(size_t)head * a.total_q + tc];
       cl[u][qb] = splat4(lq == -INFINITY ? -INFINITY : -lq * kLog2e);   // seed of S': -LSE2
       cd[u][qb] = splat4(-dsum);                                        // seed of dP: -D
+      // the dK/dV pass's row statistics of this query (rows without keys: a finite -LSE2 so that P = 0)
+      if (grp == 0 && t < g.y)
+        a.aux_out[(size_t)head * a.tq_pad + t] = make_float2(lq == -INFINITY ? kDeadRow : -lq * kLog2e, -dsum);
     }
   }
 
@@ -584,30 +588,20 @@ struct DensePrep {
   int4* plan_q; int* count_q; int4* plan_k; int* count_k;
   int gtok_q, gtok_k;                                 // tokens per group of each plan
   const bf16* k; float* knorm;                       // forward
-  const bf16* out; const bf16* dout; const float* lse; float2* aux;   // backward
+  float2* aux;                                       // backward: padding rows of the row statistics
   int nb_plan_k, nb_knorm, nb_rows;
 };
 
 // Row statistics of the dK/dV pass: aux.x = -LSE2 (LSE2 = log2(e) LSE;
 // -1e30 for rows without keys and padding, so their P is 0), aux.y = -D =
-// -rowsum(dO * O).  Thread per (query, head), head fastest.
+// -rowsum(dO * O).  The dQ kernel writes them for every query as it
+// computes its own seeds; this pass writes the padding rows [total_q,
+// tq_pad) that dK/dV's last partial tile reads (masked, but its dS = P dP
+// must stay finite).  Thread per (padding row, head), head fastest.
 DEVI void dense_rows_item(const DensePrep& p, long idx) {
-  if (idx >= (long)p.heads * p.tq_pad) return;
-  const int h = (int)(idx % p.heads), t = (int)(idx / p.heads);
-  float xs = kDeadRow, dsum = 0.f;
-  if (t < p.total_q) {
-    const float l = p.lse[(size_t)h * p.total_q + t];
-    if (l != -INFINITY) xs = -(l * kLog2e);
-    const bf16x8* po = reinterpret_cast<const bf16x8*>(p.out + ((size_t)t * p.heads + h) * kHd);
-    const bf16x8* pd = reinterpret_cast<const bf16x8*>(p.dout + ((size_t)t * p.heads + h) * kHd);
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const bf16x8 o = po[j], g = pd[j];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) dsum = fmaf((float)o[e], (float)g[e], dsum);
-    }
-  }
-  p.aux[(size_t)h * p.tq_pad + t] = make_float2(xs, -dsum);
+  if (idx >= (long)p.heads * (p.tq_pad - p.total_q)) return;
+  const int h = (int)(idx % p.heads), t = p.total_q + (int)(idx / p.heads);
+  p.aux[(size_t)h * p.tq_pad + t] = make_float2(kDeadRow, -0.f);
 }
 
 __global__ __launch_bounds__(256) void dense_prep_kernel(const DensePrep p) {
@@ -700,29 +694,29 @@ int dense_attn_bwd(const DenseAttnCall& c, void* workspace, size_t workspace_byt
   p.count_k = p.count_q + 1;
   p.plan_q = reinterpret_cast<int4*>(ws + w.plan_q);
   p.plan_k = reinterpret_cast<int4*>(ws + w.plan_k);
-  p.out = static_cast<const bf16*>(c.out_in); p.dout = static_cast<const bf16*>(c.dout); p.lse = c.lse_in;
   p.aux = reinterpret_cast<float2*>(ws + w.aux);
   p.gtok_q = kDqGroup; p.gtok_k = kDkdvGroup;
-  p.nb_plan_k = 1; p.nb_knorm = 0; p.nb_rows = (int)(((long)c.heads * p.tq_pad + 255) / 256);
+  p.nb_plan_k = 1; p.nb_knorm = 0; p.nb_rows = (int)(((long)c.heads * (p.tq_pad - c.total_q) + 255) / 256);
   ESA_TIMED(esa_profile::kAttnPrep, st,
             hipLaunchKernelGGL(dense_prep_kernel, dim3(2 + p.nb_rows), dim3(256), 0, st, p));
   ESA_LAUNCH_CHECK();
   DenseArgs a{};
   a.q = static_cast<const bf16*>(c.q); a.k = static_cast<const bf16*>(c.k); a.v = static_cast<const bf16*>(c.v);
   a.out = static_cast<const bf16*>(c.out_in); a.dout = static_cast<const bf16*>(c.dout);
-  a.lse = c.lse_in; a.aux = p.aux;
+  a.lse = c.lse_in; a.aux = p.aux; a.aux_out = p.aux;
   a.total_q = c.total_q; a.total_k = c.total_k; a.heads = c.heads; a.tq_pad = p.tq_pad;
   a.scale = c.scale; a.c = c.scale * kLog2e;
   a.dq = static_cast<bf16*>(c.dq); a.dk = static_cast<bf16*>(c.dk); a.dv = static_cast<bf16*>(c.dv);
-  a.groups = p.plan_k; a.count = p.count_k;
-  ESA_TIMED(esa_profile::kAttnBwdDkdv, st,
-            hipLaunchKernelGGL(dense_dkdv_kernel, dim3(group_grid(c.total_k, c.nseg, c.heads, kDkdvGroup)), dim3(256),
-                               0, st, a));
-  ESA_LAUNCH_CHECK();
+  // dQ first: it writes the row statistics that dK/dV stages
   a.groups = p.plan_q; a.count = p.count_q;
   ESA_TIMED(esa_profile::kAttnBwdDq, st,
             hipLaunchKernelGGL(dense_dq_kernel, dim3(group_grid(c.total_q, c.nseg, c.heads, kDqGroup)), dim3(256), 0,
                                st, a));
+  ESA_LAUNCH_CHECK();
+  a.groups = p.plan_k; a.count = p.count_k;
+  ESA_TIMED(esa_profile::kAttnBwdDkdv, st,
+            hipLaunchKernelGGL(dense_dkdv_kernel, dim3(group_grid(c.total_k, c.nseg, c.heads, kDkdvGroup)), dim3(256),
+                               0, st, a));
   ESA_LAUNCH_CHECK();
   return ESA_OK;
 }
