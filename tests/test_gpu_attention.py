@@ -90,6 +90,13 @@ def test_cross_attention_pma_shape(device, seeds):
     _check(device, lq, lk, seed=seeds + 100)
 
 
+def test_cross_attention_empty_key_segments(device):
+    """Sets without keys (a graph with no edges under PMA): their queries get 0 and lse = -inf, zero dQ, and
+    their row statistics (written by the dQ pass, a finite -LSE2 so that P = 0) leave the dK/dV pass of the
+    neighbouring segments, whose last partial tiles read them, unchanged."""
+    _check(device, [4, 4, 4, 3, 5], [50, 0, 70, 0, 33], seed=321)
+
+
 def test_masked_protein_like_small(device):
     gb = generators.protein_like(seed=2, num_graphs=3, n_min=40, n_max=90)
     src, dst = gb.edge_index[0].astype(np.int32), gb.edge_index[1].astype(np.int32)
