@@ -268,6 +268,17 @@ ESA_API int esa_column_sum_workspace_size(int64_t rows, int cols, size_t* bytes)
 ESA_API int esa_column_sum(const void* x, int dtype, int64_t rows, int cols, float* out,
                    void* workspace, size_t workspace_bytes, void* stream);
 
+/* Mish backward with the bias gradient of the Linear that produced z (an   */
+/* MLP's Linear -> Mish, esa/mlp_utils.py:18-37; autograd of nn.Linear's     */
+/* bias, esa/mlp_utils.py:28-32): dz (dtype) as esa_mish_bwd writes it over  */
+/* a [rows, cols] tensor, and dbias = the fp32 column sums of dz, equal to   */
+/* esa_column_sum over dz, in one pass.  Workspace size from                 */
+/* esa_column_sum_workspace_size(rows, cols).  cols % 4 == 0; 16-byte        */
+/* aligned pointers.                                                         */
+ESA_API int esa_mish_bwd_colsum(const void* z, const void* grad, int64_t rows, int cols,
+                        int dtype, void* dz, float* dbias, void* workspace,
+                        size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* Profiling hook (no counterpart in the reference; used by the benchmark).  */
 /* While enabled, every kernel launch of the entry points above is           */

@@ -74,6 +74,8 @@ _PROTOS = {
                                     _vp, _c_sz, _vp]),
     "esa_column_sum_workspace_size": (_c_int, [_c_i64, _c_int, ctypes.POINTER(_c_sz)]),
     "esa_column_sum": (_c_int, [_vp, _c_int, _c_i64, _c_int, _vp, _vp, _c_sz, _vp]),
+    # z grad rows cols dtype dz dbias ws bytes stream
+    "esa_mish_bwd_colsum": (_c_int, [_vp, _vp, _c_i64, _c_int, _c_int, _vp, _vp, _vp, _c_sz, _vp]),
     "esa_mab_residual_fwd": (_c_int, [_vp, _vp, _vp, _c_i64, _c_int, _vp, _vp]),
     "esa_mab_residual_bwd": (_c_int, [_vp, _vp, _c_i64, _c_int, _vp, _vp, _vp]),
     "esa_profile_enable": (_c_int, [_c_int]),

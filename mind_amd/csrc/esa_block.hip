@@ -612,6 +612,64 @@ int mab_residual_bwd_typed(const T* z, const float* g, T* dz, T* g_o, int64_t n,
   return rc;
 }
 
+// Mish backward of a [rows, cols] tensor together with the column sums of
+// its result, the bias gradient of the Linear whose output z is (an MLP's
+// Linear -> Mish, esa/mlp_utils.py:18-37): dz = r(g mish'(z)) as
+// mish_bwd_kernel computes it, and the grid, row ranges and order of
+// col_sum_partial_kernel over the rounded dz, so the partials (and, through
+// reduce_columns, the sums) equal esa_column_sum's over the stored dz.  One
+// pass instead of a second read of dz.
+template <typename T, int CPT>
+__global__ __launch_bounds__(256) void mish_bwd_colsum_kernel(const T* __restrict__ z, const T* __restrict__ g,
+                                                              int64_t rows, int cols, int64_t rows_per_block,
+                                                              T* __restrict__ dz, float* __restrict__ part) {
+  // The sums add the stored (rounded) products: without this the compiler keeps a multiply for the store and
+  // fuses g * mish'(z) into the accumulation (an fma of the unrounded product).  mish_grad_f keeps its own.
+#pragma clang fp contract(off)
+  constexpr int Q = CPT / 4;   // 4-column quads per thread: one 16-byte access per row for bf16 (CPT = 8)
+  const int c = CPT * (blockIdx.x * blockDim.x + threadIdx.x);
+  if (c >= cols) return;
+  const int64_t r0 = (int64_t)blockIdx.y * rows_per_block;
+  const int64_t r1 = std::min<int64_t>(rows, r0 + rows_per_block);
+  f32x4 a[Q];
+#pragma unroll
+  for (int q = 0; q < Q; ++q) a[q] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+  for (int64_t r = r0; r < r1; ++r) {
+    f32x4 zv[Q], gv[Q], d[Q];
+    if constexpr (Q == 2) {
+      const bf16x8 zz = *reinterpret_cast<const bf16x8*>(z + r * cols + c);
+      const bf16x8 gg = *reinterpret_cast<const bf16x8*>(g + r * cols + c);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        zv[e / 4][e % 4] = (float)zz[e];
+        gv[e / 4][e % 4] = (float)gg[e];
+      }
+    } else {
+      zv[0] = load4(z + r * cols + c);
+      gv[0] = load4(g + r * cols + c);
+    }
+#pragma unroll
+    for (int q = 0; q < Q; ++q)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) d[q][e] = round_to(gv[q][e] * mish_grad_f(zv[q][e]), (T*)nullptr);
+    if constexpr (Q == 2) {
+      bf16x8 o;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = (bf16)d[e / 4][e % 4];
+      *reinterpret_cast<bf16x8*>(dz + r * cols + c) = o;
+    } else {
+      store4(dz + r * cols + c, d[0]);
+    }
+#pragma unroll
+    for (int q = 0; q < Q; ++q)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) a[q][e] += d[q][e];
+  }
+#pragma unroll
+  for (int q = 0; q < Q; ++q) store4(part + (size_t)blockIdx.y * cols + c + 4 * q, a[q]);
+}
+
 }  // namespace
 
 extern "C" ESA_API int esa_layer_norm_fwd(const void* x, int x_dtype, const float* weight, const float* bias,
@@ -740,6 +798,40 @@ extern "C" ESA_API int esa_column_sum(const void* x, int dtype, int64_t rows, in
                            part);
     }
     reduce_columns(part, rows > 0 ? rb : 0, cols, part + (size_t)rb * cols, cols, out, nullptr, st);
+  });
+  ESA_LAUNCH_CHECK();
+  return ESA_OK;
+}
+
+extern "C" ESA_API int esa_mish_bwd_colsum(const void* z, const void* grad, int64_t rows, int cols, int dtype,
+                                           void* dz, float* dbias, void* workspace, size_t workspace_bytes,
+                                           void* stream) {
+  if (rows < 0 || cols < 4 || cols % 4) return ESA_ERR_SHAPE;
+  if (dtype != ESA_F32 && dtype != ESA_BF16) return ESA_ERR_DTYPE;
+  if (!dbias || !workspace || (rows > 0 && (!z || !grad || !dz))) return ESA_ERR_NULL;
+  const int rb = colsum_row_blocks(rows);
+  if (workspace_bytes < ((size_t)rb * cols + reduce_scratch_floats(cols)) * sizeof(float)) return ESA_ERR_WORKSPACE;
+  if (!aligned16(z) || !aligned16(grad) || !aligned16(dz) || !aligned16(workspace)) return ESA_ERR_ALIGN;
+  hipStream_t st = (hipStream_t)stream;
+  float* part = (float*)workspace;
+  ESA_TIMED(esa_profile::kMishBwd, st, {
+    if (rows > 0) {
+      const int cpt = dtype == ESA_BF16 && cols % 8 == 0 ? 8 : 4;   // one 16-byte access per row and thread
+      const int chunks = cols / cpt;
+      const int tpb = std::min(256, (chunks + 63) / 64 * 64);
+      const dim3 grid((unsigned)((chunks + tpb - 1) / tpb), (unsigned)rb);
+      const int64_t rpb = (rows + rb - 1) / rb;
+      if (dtype == ESA_F32)
+        hipLaunchKernelGGL((mish_bwd_colsum_kernel<float, 4>), grid, dim3(tpb), 0, st, (const float*)z,
+                           (const float*)grad, rows, cols, rpb, (float*)dz, part);
+      else if (cpt == 8)
+        hipLaunchKernelGGL((mish_bwd_colsum_kernel<bf16, 8>), grid, dim3(tpb), 0, st, (const bf16*)z,
+                           (const bf16*)grad, rows, cols, rpb, (bf16*)dz, part);
+      else
+        hipLaunchKernelGGL((mish_bwd_colsum_kernel<bf16, 4>), grid, dim3(tpb), 0, st, (const bf16*)z,
+                           (const bf16*)grad, rows, cols, rpb, (bf16*)dz, part);
+    }
+    reduce_columns(part, rows > 0 ? rb : 0, cols, part + (size_t)rb * cols, cols, dbias, nullptr, st);
   });
   ESA_LAUNCH_CHECK();
   return ESA_OK;

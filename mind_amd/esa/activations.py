@@ -131,6 +131,72 @@ def mab_epilogue(o: torch.Tensor, fc_o: nn.Linear, residual: torch.Tensor | None
     return _MabEpilogue.apply(o, w, b, None if residual is None else residual.contiguous())
 
 
+_FUSED_COLSUM_MIN_COLS = 1024
+
+
+class _LinearMish(torch.autograd.Function):
+    """y = mish(x W^T + b), an MLP's Linear -> Mish (esa/mlp_utils.py:18-37).  Forward: the GEMM, then
+    esa_mish_fwd.  Backward: esa_mish_bwd_colsum writes dz and the bias gradient (dz's column sums) in one
+    pass; dx = dz W and the split-K weight gradient follow.  Parameters enter in their own dtype and are cast
+    inside, so their gradients are returned in it (fp32 under autocast)."""
+
+    @staticmethod
+    def forward(ctx, x, weight, bias):
+        from .linear import cast_param   # deferred: linear.py is a sibling with its own imports
+        ctx.dtypes = (weight.dtype, None if bias is None else bias.dtype)
+        w, b = cast_param(weight, x.dtype), cast_param(bias, x.dtype)
+        z = F.linear(x, w, b)
+        y = torch.empty_like(z)
+        _lib.check(_lib.load().esa_mish_fwd(z.data_ptr(), None, z.numel(), _DTYPES[z.dtype], y.data_ptr(),
+                                            _lib.stream_of(z)), "esa_mish_fwd")
+        ctx.save_for_backward(x, w, z)
+        return y
+
+    @staticmethod
+    def backward(ctx, g):
+        import ctypes
+
+        from .linear import column_sum, weight_grad
+        x, w, z = ctx.saved_tensors
+        wdt, bdt = ctx.dtypes
+        lib, st, code = _lib.load(), _lib.stream_of(z), _DTYPES[z.dtype]
+        g = g.to(z.dtype).contiguous()
+        dz = torch.empty_like(z)
+        rows, cols = z.shape
+        db = None
+        # fused from 1024 columns (131,072 x 2048 bf16: 330 vs 399 us); narrower, its grid of one wave per
+        # column tile and row range is latency-bound (x 512: 156 vs 98 us) and the two kernels run instead
+        if bdt is not None and ctx.needs_input_grad[2] and cols % 4 == 0 and cols >= _FUSED_COLSUM_MIN_COLS:
+            n = ctypes.c_size_t(0)
+            _lib.check(lib.esa_column_sum_workspace_size(rows, cols, ctypes.byref(n)), "esa_column_sum_workspace_size")
+            ws = torch.empty(int(n.value), dtype=torch.uint8, device=z.device)
+            db = torch.empty(cols, dtype=torch.float32, device=z.device)
+            _lib.check(lib.esa_mish_bwd_colsum(z.data_ptr(), g.data_ptr(), rows, cols, code, dz.data_ptr(),
+                                               db.data_ptr(), ws.data_ptr(), ws.numel(), st), "esa_mish_bwd_colsum")
+        else:
+            _lib.check(lib.esa_mish_bwd(z.data_ptr(), g.data_ptr(), z.numel(), code, dz.data_ptr(), st),
+                       "esa_mish_bwd")
+            if bdt is not None and ctx.needs_input_grad[2]:
+                db = column_sum(dz)
+        dx = dz.mm(w) if ctx.needs_input_grad[0] else None
+        dw = weight_grad(dz, x).to(wdt) if ctx.needs_input_grad[1] else None
+        return dx, dw, None if db is None else db.to(bdt)
+
+
+def linear_mish(x: torch.Tensor, layer: nn.Linear) -> torch.Tensor:
+    """``mish(layer(x))`` with the fused backward of _LinearMish on device tensors."""
+    if not x.is_cuda:
+        return F.mish(layer(x))
+    from .linear import compute_dtype, linear
+    dt = compute_dtype(x, layer.weight, layer.bias)
+    if dt not in _DTYPES:
+        return mish(linear(x, layer.weight, layer.bias))
+    x = x.to(dt)
+    lead = x.shape[:-1]
+    y = _LinearMish.apply(x.reshape(-1, x.shape[-1]).contiguous(), layer.weight, layer.bias)
+    return y.view(*lead, layer.weight.shape[0])
+
+
 class Mish(nn.Mish):
     """nn.Mish on the HIP kernel (no parameters; state dicts are unchanged)."""
 

@@ -10,7 +10,7 @@ from __future__ import annotations
 from torch import nn
 from torch.nn import functional as F
 
-from .activations import Mish
+from .activations import Mish, linear_mish
 from .linear import apply, linear
 
 
@@ -44,8 +44,15 @@ class SmallMLP(nn.Module):
         self.mlp = nn.Sequential(*layers)
 
     def forward(self, x):
-        for layer in self.mlp:
-            x = apply(layer, x)
+        layers = list(self.mlp)
+        i = 0
+        while i < len(layers):
+            if type(layers[i]) is nn.Linear and i + 1 < len(layers) and isinstance(layers[i + 1], nn.Mish):
+                x = linear_mish(x, layers[i])   # Linear -> Mish: the bias gradient comes with Mish's backward
+                i += 2
+            else:
+                x = apply(layers[i], x)
+                i += 1
         return x
 
 

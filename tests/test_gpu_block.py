@@ -328,6 +328,79 @@ def test_column_sum(device, dtype, rows, cols):
     assert bool(((a.double().cpu() - ref).abs() <= bar).all())
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("rows,cols", [(0, 8), (1, 4), (37, 2048), (5000, 516), (131072, 512)])
+def test_mish_bwd_colsum_matches_unfused(device, dtype, rows, cols):
+    """esa_mish_bwd_colsum: dz bit-equal to esa_mish_bwd's and the bias gradient bit-equal to esa_column_sum over
+    that dz (the same row ranges, order and rounding); no rows gives a zero bias gradient."""
+    import ctypes
+    from mind_amd.esa.linear import column_sum
+    gen = torch.Generator().manual_seed(rows + 3 * cols)
+    z = (torch.randn(rows, cols, generator=gen) * 4).to(dtype).to(device)
+    g = torch.randn(rows, cols, generator=gen).to(dtype).to(device)
+    lib, code = _lib.load(), _lib.ESA_F32 if dtype == torch.float32 else _lib.ESA_BF16
+    st = _lib.stream_of(z)
+    dz_ref = torch.empty_like(z)
+    assert lib.esa_mish_bwd(z.data_ptr(), g.data_ptr(), z.numel(), code, dz_ref.data_ptr(), st) == 0
+    n = ctypes.c_size_t(0)
+    assert lib.esa_column_sum_workspace_size(rows, cols, ctypes.byref(n)) == 0
+    ws = torch.empty(int(n.value), dtype=torch.uint8, device=device)
+    dz = torch.full_like(z, float("nan"))
+    db = torch.full((cols,), float("nan"), device=device)
+    assert lib.esa_mish_bwd_colsum(z.data_ptr(), g.data_ptr(), rows, cols, code, dz.data_ptr(), db.data_ptr(),
+                                   ws.data_ptr(), ws.numel(), st) == 0
+    assert torch.equal(_bits(dz), _bits(dz_ref))
+    if rows:
+        assert torch.equal(db, column_sum(dz_ref))
+    else:
+        assert torch.equal(db, torch.zeros_like(db))
+    assert lib.esa_mish_bwd_colsum(z.data_ptr(), g.data_ptr(), rows, 6, code, dz.data_ptr(), db.data_ptr(),
+                                   ws.data_ptr(), ws.numel(), st) == -2   # ESA_ERR_SHAPE
+
+
+@pytest.mark.parametrize("dout", [512, 2048], ids=["two_kernels", "fused_colsum"])
+@pytest.mark.parametrize("autocast", [False, True], ids=["fp32", "autocast_bf16"])
+def test_linear_mish_fused(device, autocast, dout):
+    """linear_mish(x, fc) = mish(fc(x)) (an MLP's Linear -> Mish) against fp64 autograd on the operands the GEMM
+    gets (bf16-rounded under autocast): output and the gradients of x, weight and bias, which reach the fp32
+    parameters; both backward forms (the fused Mish + bias-gradient kernel from 1024 outputs, the two kernels
+    below); SmallMLP takes this path."""
+    from mind_amd.esa.activations import linear_mish
+    from mind_amd.esa.mlp_utils import SmallMLP
+    gen = torch.Generator().manual_seed(31 + autocast + dout)
+    t, din = 3000, 256
+    fc = torch.nn.Linear(din, dout).to(device)
+    x = torch.randn(t, din, generator=gen)
+    up = torch.randn(t, dout, generator=gen)
+    xd = x.to(device).requires_grad_(True)
+    with torch.autocast("cuda", dtype=torch.bfloat16, enabled=autocast):
+        y = linear_mish(xd, fc)
+    assert y.dtype == (torch.bfloat16 if autocast else torch.float32)
+    y.backward(up.to(device).to(y.dtype))
+    assert fc.weight.grad.dtype == torch.float32 and fc.bias.grad.dtype == torch.float32
+    rnd = (lambda v: v.to(torch.bfloat16).double()) if autocast else (lambda v: v.double())
+    w64 = rnd(fc.weight.detach().cpu()).requires_grad_(True)
+    b64 = rnd(fc.bias.detach().cpu()).requires_grad_(True)
+    x64 = rnd(x).requires_grad_(True)
+    ref = OMod.mish(x64 @ w64.t() + b64)
+    ref.backward(up.to(y.dtype).double())
+    if autocast:
+        _bf16_bar(y, ref.detach(), "y")
+        _bf16_bar(xd.grad, x64.grad, "d x")
+        _bf16_bar(fc.weight.grad, w64.grad, "d weight")
+        _bf16_bar(fc.bias.grad, b64.grad, "d bias")
+    else:   # the fp32 bar, norm-wise
+        for got, r, what in ((y, ref.detach(), "y"), (xd.grad, x64.grad, "d x"), (fc.weight.grad, w64.grad, "dw"),
+                             (fc.bias.grad, b64.grad, "db")):
+            _f32_norm_close(got, r, what)
+    # SmallMLP (Linear -> Mish -> Linear) routes its first pair through linear_mish: same values as the module
+    mlp = SmallMLP(din, dout, din, num_layers=2).to(device)
+    with torch.autocast("cuda", dtype=torch.bfloat16, enabled=autocast):
+        got = mlp(xd.detach())
+        ref_mlp = mlp.mlp[2](linear_mish(xd.detach(), mlp.mlp[0]))
+    assert torch.equal(got, ref_mlp)
+
+
 def _bf16_bar(got, ref, what):
     """The north-star bf16 bar, scaled by the reference's magnitude (at least 1)."""
     from tests._util import assert_bf16_close, grad_scale
