@@ -1,5 +1,6 @@
 """Host-side logic that needs no GPU: generators and the EdgeAdjacency descriptor."""
 import numpy as np
+import pytest
 import torch
 
 from mind_amd import generators
@@ -100,3 +101,16 @@ def test_block_functions_on_cpu_tensors():
     ln = torch.nn.LayerNorm(8, eps=1e-8)
     y, y_lp = layer_norm(o, ln, full=True, lowp=True)
     assert torch.allclose(y, ln(o)) and y_lp is None
+    _, _, xr = layer_norm(o, ln, full=False, lowp=True, passthrough=True)
+    assert xr is o
+
+
+@pytest.mark.parametrize("num_layers,use_ln", [(1, False), (2, False), (3, False), (3, True)])
+def test_small_mlp_walks_every_layer_once(num_layers, use_ln):
+    """SmallMLP.forward pairs each Linear with a following Mish (linear_mish) and applies the rest one by one:
+    on CPU tensors its output equals the Sequential's, whatever the layer pattern."""
+    from mind_amd.esa.mlp_utils import SmallMLP
+    torch.manual_seed(num_layers)
+    mlp = SmallMLP(12, 20, 8, num_layers=num_layers, use_ln=use_ln)
+    x = torch.randn(5, 12)
+    assert torch.allclose(mlp(x), mlp.mlp(x), atol=1e-6)
