@@ -594,14 +594,19 @@ struct DensePrep {
 
 // Row statistics of the dK/dV pass: aux.x = -LSE2 (LSE2 = log2(e) LSE;
 // -1e30 for rows without keys and padding, so their P is 0), aux.y = -D =
-// -rowsum(dO * O).  The dQ kernel writes them for every query as it
-// computes its own seeds; this pass writes the padding rows [total_q,
-// tq_pad) that dK/dV's last partial tile reads (masked, but its dS = P dP
-// must stay finite).  Thread per (padding row, head), head fastest.
-DEVI void dense_rows_item(const DensePrep& p, long idx) {
-  if (idx >= (long)p.heads * (p.tq_pad - p.total_q)) return;
-  const int h = (int)(idx % p.heads), t = p.total_q + (int)(idx / p.heads);
-  p.aux[(size_t)h * p.tq_pad + t] = make_float2(kDeadRow, -0.f);
+// -rowsum(dO * O).  The dQ kernel writes them for every query of a segment as
+// it computes its own seeds; this pass writes the rows after the last
+// segment, [cu_q[nseg], tq_pad): the padding up to the 32-row boundary and
+// any rows of q that no segment covers (cu_q[nseg] < total_q), which dK/dV's
+// last partial tile stages (masked, but its dS = P dP must stay finite).
+// Block-strided over (row, head), head fastest.
+DEVI void dense_rows_block(const DensePrep& p, int b, int tid) {
+  const int t0 = min(max(p.cu_q[p.nseg], 0), p.total_q);
+  const long n = (long)p.heads * (p.tq_pad - t0);
+  for (long idx = (long)b * 256 + tid; idx < n; idx += (long)p.nb_rows * 256) {
+    const int h = (int)(idx % p.heads), t = t0 + (int)(idx / p.heads);
+    p.aux[(size_t)h * p.tq_pad + t] = make_float2(kDeadRow, -0.f);
+  }
 }
 
 __global__ __launch_bounds__(256) void dense_prep_kernel(const DensePrep p) {
@@ -613,7 +618,7 @@ __global__ __launch_bounds__(256) void dense_prep_kernel(const DensePrep p) {
   b -= p.nb_plan_k;
   if (b < p.nb_knorm) { knorm_block(p.k, p.total_k, p.heads, p.tk_tiles, p.knorm, b, tid); return; }
   b -= p.nb_knorm;
-  if (b < p.nb_rows) dense_rows_item(p, (long)b * 256 + tid);
+  if (b < p.nb_rows) dense_rows_block(p, b, tid);
 }
 
 // ------------------------------------------------------------------ host side
@@ -696,7 +701,7 @@ int dense_attn_bwd(const DenseAttnCall& c, void* workspace, size_t workspace_byt
   p.plan_k = reinterpret_cast<int4*>(ws + w.plan_k);
   p.aux = reinterpret_cast<float2*>(ws + w.aux);
   p.gtok_q = kDqGroup; p.gtok_k = kDkdvGroup;
-  p.nb_plan_k = 1; p.nb_knorm = 0; p.nb_rows = (int)(((long)c.heads * (p.tq_pad - c.total_q) + 255) / 256);
+  p.nb_plan_k = 1; p.nb_knorm = 0; p.nb_rows = (int)max(1L, ((long)c.heads * (p.tq_pad - c.total_q) + 255) / 256);
   ESA_TIMED(esa_profile::kAttnPrep, st,
             hipLaunchKernelGGL(dense_prep_kernel, dim3(2 + p.nb_rows), dim3(256), 0, st, p));
   ESA_LAUNCH_CHECK();

@@ -7,6 +7,8 @@
 // esa/models.py:307-309).  Segment sum semantics: out_n = sum over the CSR
 // segment of n in ascending position (GET/utils/sorted_segment_ops.py:40-41),
 // fp32 accumulation, rounded once.
+#include <algorithm>
+
 #include "esa_common.h"
 #include "esa_profile.h"
 #include "../../include/esa_hip.h"
@@ -369,27 +371,99 @@ __global__ __launch_bounds__(kScanBlock) void scan_apply_kernel(const int* __res
   if (blockIdx.x == gridDim.x - 1 && threadIdx.x == kScanBlock - 1) indptr[n] = run;
 }
 
-__global__ void fill_perm_kernel(const int* __restrict__ keys, long num_edges, int num_nodes,
-                                 int* __restrict__ cursor, int* __restrict__ perm) {
-  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < num_edges; i += (long)gridDim.x * blockDim.x) {
-    const int k = keys[i];
-    if ((unsigned)k < (unsigned)num_nodes) perm[atomicAdd(&cursor[k], 1)] = (int)i;
-  }
+// perm by a stable LSD radix sort of (key, edge id) over 8-bit digits, so
+// every edge's position follows from counts alone (no atomic ordering, no
+// per-segment sort): per pass, each block counts the digits of its tile of
+// kSortTile consecutive edges (hist, digit-major: [digit][block]); an
+// exclusive scan of hist in that (digit, block) order gives each (digit,
+// block) its first output slot; the scatter pass then places element i of
+// the tile at that slot + the number of earlier elements of the tile with the
+// same digit.  Earlier means earlier in edge order: the tile is walked in
+// rounds j of kSortThreads consecutive edges (edge base + j * 256 + tid), and
+// inside a round by wave, then lane.  Each pass is therefore stable, and the
+// passes over digits 0, 1, ... leave the edges sorted by key with ties in
+// ascending edge id.  Keys outside [0, num_nodes) sort as num_nodes, after
+// every valid key (past indptr[num_nodes]).
+constexpr int kSortThreads = 256;
+constexpr int kSortItems = 16;
+constexpr int kSortTile = kSortThreads * kSortItems;
+constexpr int kRadixBits = 8;
+constexpr int kRadixBins = 1 << kRadixBits;
+static_assert(kRadixBins == kSortThreads, "one digit per thread in the per-digit steps");
+
+DEVI int sort_key(const int* __restrict__ keys, long i, int num_nodes, bool raw) {
+  const int k = keys[i];
+  return !raw || (unsigned)k < (unsigned)num_nodes ? k : num_nodes;
 }
 
-// The atomic fill leaves each segment in arbitrary order; sorting every
-// segment ascending makes perm the stable (ascending edge id) order, so the
-// result does not depend on atomic timing.  Insertion sort, one thread per
-// node: O(degree^2) per node.
-__global__ void sort_segments_kernel(const int* __restrict__ indptr, int num_nodes, int* __restrict__ perm) {
-  const int n = blockIdx.x * blockDim.x + threadIdx.x;
-  if (n >= num_nodes) return;
-  const int a = indptr[n], b = indptr[n + 1];
-  for (int i = a + 1; i < b; ++i) {
-    const int x = perm[i];
-    int j = i - 1;
-    while (j >= a && perm[j] > x) { perm[j + 1] = perm[j]; --j; }
-    perm[j + 1] = x;
+__global__ __launch_bounds__(kSortThreads) void radix_hist_kernel(const int* __restrict__ keys, long n, int num_nodes,
+                                                                 bool raw, int shift, int nblocks,
+                                                                 int* __restrict__ hist) {
+  __shared__ int h[kRadixBins];
+  const int tid = threadIdx.x;
+  h[tid] = 0;
+  __syncthreads();
+  const long base = (long)blockIdx.x * kSortTile;
+#pragma unroll 4
+  for (int j = 0; j < kSortItems; ++j) {
+    const long i = base + (long)j * kSortThreads + tid;
+    if (i < n) atomicAdd(&h[(sort_key(keys, i, num_nodes, raw) >> shift) & (kRadixBins - 1)], 1);
+  }
+  __syncthreads();
+  hist[(long)tid * nblocks + blockIdx.x] = h[tid];
+}
+
+// offsets: the exclusive scan of hist.  vals_in null: the values are the edge
+// ids.  keys_out null: the last pass (only the values are needed).
+__global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(const int* __restrict__ keys_in,
+                                                                    const int* __restrict__ vals_in, long n,
+                                                                    int num_nodes, bool raw, int shift, int nblocks,
+                                                                    const int* __restrict__ offsets,
+                                                                    int* __restrict__ keys_out,
+                                                                    int* __restrict__ vals_out) {
+  constexpr int kWaves = kSortThreads / 64;
+  __shared__ int run[kRadixBins];           // next slot of each digit
+  __shared__ int wcnt[kWaves][kRadixBins];  // this round's count of each digit per wave
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  run[tid] = offsets[(long)tid * nblocks + blockIdx.x];
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) wcnt[w][tid] = 0;
+  __syncthreads();
+  const long base = (long)blockIdx.x * kSortTile;
+  const uint64_t below_mask = (1ull << lane) - 1;
+  for (int j = 0; j < kSortItems; ++j) {
+    const long i = base + (long)j * kSortThreads + tid;
+    const bool valid = i < n;
+    int k = 0, v = 0, d = 0;
+    if (valid) {
+      k = sort_key(keys_in, i, num_nodes, raw);
+      v = vals_in ? vals_in[i] : (int)i;
+      d = (k >> shift) & (kRadixBins - 1);
+    }
+    // lanes of this wave holding the same digit
+    uint64_t peers = __ballot(valid);
+#pragma unroll
+    for (int b = 0; b < kRadixBits; ++b) {
+      const bool bit = (d >> b) & 1;
+      const uint64_t m = __ballot(bit);
+      peers &= bit ? m : ~m;
+    }
+    const int below = __popcll(peers & below_mask);
+    if (valid && below == 0) wcnt[wave][d] = __popcll(peers);
+    __syncthreads();
+    if (valid) {
+      int pos = run[d] + below;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) pos += w < wave ? wcnt[w][d] : 0;
+      if (keys_out) keys_out[pos] = k;
+      vals_out[pos] = v;
+    }
+    __syncthreads();
+    int add = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) { add += wcnt[w][tid]; wcnt[w][tid] = 0; }
+    run[tid] += add;
+    __syncthreads();
   }
 }
 
@@ -674,14 +748,35 @@ bool misaligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u)
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
-struct CsrWs { size_t counts, cursor, tiles, total; };
-CsrWs csr_ws(int num_nodes) {
+// Exclusive scan of in[0, n) into out[0, n] (out[n] = the total); in may be out.
+void scan_exclusive(const int* in, int n, int* out, int* tiles, hipStream_t st) {
+  const int ntiles = (n + kScanTile - 1) / kScanTile;
+  hipLaunchKernelGGL(scan_reduce_kernel, dim3(ntiles), dim3(kScanBlock), 0, st, in, n, tiles);
+  hipLaunchKernelGGL(scan_tiles_kernel, dim3(1), dim3(kScanBlock), 0, st, tiles, ntiles);
+  hipLaunchKernelGGL(scan_apply_kernel, dim3(ntiles), dim3(kScanBlock), 0, st, in, n, tiles, out, out);
+}
+
+int radix_blocks(int64_t num_edges) { return (int)((num_edges + kSortTile - 1) / kSortTile); }
+
+// Passes of kRadixBits over the keys 0 .. num_nodes (num_nodes: the slot of invalid keys).
+int radix_passes(int num_nodes) {
+  const int bits = 32 - __builtin_clz((unsigned)num_nodes | 1u);
+  return (bits + kRadixBits - 1) / kRadixBits;
+}
+
+struct CsrWs { size_t counts, tiles, hist, keys_a, keys_b, vals, total; };
+CsrWs csr_ws(int64_t num_edges, int num_nodes) {
   CsrWs w;
-  const int ntiles = (num_nodes + kScanTile - 1) / kScanTile;
+  const long nhist = (long)kRadixBins * radix_blocks(num_edges);
+  const long scan_n = std::max((long)num_nodes, nhist);
+  const long ntiles = (scan_n + kScanTile - 1) / kScanTile;
   size_t off = 0;
   w.counts = off; off += align256((size_t)num_nodes * 4);
-  w.cursor = off; off += align256((size_t)num_nodes * 4);
   w.tiles = off; off += align256((size_t)(ntiles > 0 ? ntiles : 1) * 4);
+  w.hist = off; off += align256((size_t)(nhist + 1) * 4);
+  w.keys_a = off; off += align256((size_t)num_edges * 4);
+  w.keys_b = off; off += align256((size_t)num_edges * 4);
+  w.vals = off; off += align256((size_t)num_edges * 4);
   w.total = off;
   return w;
 }
@@ -866,7 +961,7 @@ int esa_edge_gather_add(const void* a, int64_t lda, const void* b, int64_t ldb, 
 int esa_csr_workspace_size(int64_t num_edges, int num_nodes, size_t* bytes) {
   if (!bytes) return ESA_ERR_NULL;
   if (num_edges < 0 || num_nodes < 0 || num_edges >= (1LL << 31)) return ESA_ERR_SHAPE;
-  *bytes = csr_ws(num_nodes).total;
+  *bytes = csr_ws(num_edges, num_nodes).total;
   return ESA_OK;
 }
 
@@ -874,41 +969,49 @@ int esa_csr_build(const int* keys, int64_t num_edges, int num_nodes, int* indptr
                   size_t workspace_bytes, void* stream) {
   if (!indptr || !workspace || (num_edges > 0 && (!keys || !perm))) return ESA_ERR_NULL;
   if (num_edges < 0 || num_nodes < 0 || num_edges >= (1LL << 31)) return ESA_ERR_SHAPE;
-  const CsrWs w = csr_ws(num_nodes);
+  const CsrWs w = csr_ws(num_edges, num_nodes);
   if (workspace_bytes < w.total) return ESA_ERR_WORKSPACE;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
   int* counts = reinterpret_cast<int*>(ws + w.counts);
-  int* cursor = reinterpret_cast<int*>(ws + w.cursor);
   int* tiles = reinterpret_cast<int*>(ws + w.tiles);
-  const int ntiles = (num_nodes + kScanTile - 1) / kScanTile;
   if (num_nodes == 0) {
     hipLaunchKernelGGL(zero_int_kernel, dim3(1), dim3(64), 0, st, indptr, 1L);
     ESA_LAUNCH_CHECK();
     return ESA_OK;
   }
-  hipLaunchKernelGGL(zero_int_kernel, dim3(grid_for(num_nodes, 256, 4096)), dim3(256), 0, st, counts, (long)num_nodes);
+  ESA_TIMED(esa_profile::kCsrBuild, st, {
+    // indptr: key counts (order-independent) and their exclusive scan
+    hipLaunchKernelGGL(zero_int_kernel, dim3(grid_for(num_nodes, 256, 4096)), dim3(256), 0, st, counts,
+                       (long)num_nodes);
+    if (num_edges > 0)
+      hipLaunchKernelGGL(count_keys_kernel, dim3(grid_for(num_edges, 256, 8192)), dim3(256), 0, st, keys,
+                         (long)num_edges, num_nodes, counts);
+    scan_exclusive(counts, num_nodes, indptr, tiles, st);
+    // perm: stable radix sort of the edge ids by key
+    if (num_edges > 0) {
+      const int nblocks = radix_blocks(num_edges), passes = radix_passes(num_nodes);
+      int* hist = reinterpret_cast<int*>(ws + w.hist);
+      int* kbuf[2] = {reinterpret_cast<int*>(ws + w.keys_a), reinterpret_cast<int*>(ws + w.keys_b)};
+      int* vtmp = reinterpret_cast<int*>(ws + w.vals);
+      const int* kin = keys;
+      const int* vin = nullptr;
+      for (int p = 0; p < passes; ++p) {
+        const bool raw = p == 0, last = p == passes - 1;
+        // values ping-pong so that the last pass writes perm
+        int* vout = ((passes - 1 - p) & 1) ? vtmp : perm;
+        int* kout = last ? nullptr : kbuf[p & 1];
+        hipLaunchKernelGGL(radix_hist_kernel, dim3(nblocks), dim3(kSortThreads), 0, st, kin, (long)num_edges,
+                           num_nodes, raw, p * kRadixBits, nblocks, hist);
+        scan_exclusive(hist, kRadixBins * nblocks, hist, tiles, st);
+        hipLaunchKernelGGL(radix_scatter_kernel, dim3(nblocks), dim3(kSortThreads), 0, st, kin, vin,
+                           (long)num_edges, num_nodes, raw, p * kRadixBits, nblocks, hist, kout, vout);
+        kin = kout;
+        vin = vout;
+      }
+    }
+  });
   ESA_LAUNCH_CHECK();
-  if (num_edges > 0) {
-    hipLaunchKernelGGL(count_keys_kernel, dim3(grid_for(num_edges, 256, 8192)), dim3(256), 0, st, keys,
-                       (long)num_edges, num_nodes, counts);
-    ESA_LAUNCH_CHECK();
-  }
-  hipLaunchKernelGGL(scan_reduce_kernel, dim3(ntiles), dim3(kScanBlock), 0, st, counts, num_nodes, tiles);
-  ESA_LAUNCH_CHECK();
-  hipLaunchKernelGGL(scan_tiles_kernel, dim3(1), dim3(kScanBlock), 0, st, tiles, ntiles);
-  ESA_LAUNCH_CHECK();
-  hipLaunchKernelGGL(scan_apply_kernel, dim3(ntiles), dim3(kScanBlock), 0, st, counts, num_nodes, tiles, indptr,
-                     cursor);
-  ESA_LAUNCH_CHECK();
-  if (num_edges > 0) {
-    hipLaunchKernelGGL(fill_perm_kernel, dim3(grid_for(num_edges, 256, 8192)), dim3(256), 0, st, keys,
-                       (long)num_edges, num_nodes, cursor, perm);
-    ESA_LAUNCH_CHECK();
-    hipLaunchKernelGGL(sort_segments_kernel, dim3(grid_for(num_nodes, 256)), dim3(256), 0, st, indptr, num_nodes,
-                       perm);
-    ESA_LAUNCH_CHECK();
-  }
   return ESA_OK;
 }
 

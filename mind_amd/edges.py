@@ -190,7 +190,7 @@ class _ScatterAdd(torch.autograd.Function):
         idx = index.to(torch.int64)
         valid = (idx >= 0) & (idx < ctx.dim_size)
         grad = g.reshape(ctx.dim_size, -1).index_select(0, idx.clamp(0, max(ctx.dim_size - 1, 0)))
-        grad = grad * valid.unsqueeze(1).to(grad.dtype)
+        grad = grad.masked_fill(~valid.unsqueeze(1), 0)   # dropped edges: exactly 0, even beside Inf / NaN
         return grad.reshape((idx.numel(),) + tuple(g.shape[1:])), None, None, None
 
 

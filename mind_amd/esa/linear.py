@@ -182,8 +182,14 @@ def qkv_projection(fc_q: nn.Linear, fc_k: nn.Linear, fc_v: nn.Linear, xq: torch.
     return _QKV.apply(xq.contiguous(), xk_, *params)
 
 
+def hookless(layer: nn.Module) -> bool:
+    """True when calling ``layer`` would run no forward hooks or pre-hooks, so its forward may be replaced
+    by an equivalent fused call."""
+    return not (layer._forward_hooks or layer._forward_pre_hooks)
+
+
 def apply(layer: nn.Module, x: torch.Tensor) -> torch.Tensor:
-    """layer(x), with nn.Linear layers through ``linear``."""
-    if type(layer) is nn.Linear:
+    """layer(x), with hook-free nn.Linear layers through ``linear``."""
+    if type(layer) is nn.Linear and hookless(layer):
         return linear(x, layer.weight, layer.bias)
     return layer(x)

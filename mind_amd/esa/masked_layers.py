@@ -345,20 +345,37 @@ class ESA(nn.Module):
         return mish(self.decoder_linear(enc)), enc
 
     def _forward_packed(self, X, edge_index, batch_mapping, num_max_items, tokens: PackedSets):
-        """The "hip" forward: encoder and PMA keys on the packed tokens; the decoder's later layers act on
-        the [B, k, D] seeds as in the padded forward."""
-        xp = tokens.unpad(X)
+        """The "hip" forward of padded input: unpad, run ``forward_packed``, pad the token embeddings."""
+        g_emb, enc = self.forward_packed(tokens.unpad(X), tokens, edge_index, batch_mapping)
+        return g_emb, tokens.pad(enc)
+
+    def forward_packed(self, tokens_x: torch.Tensor, tokens: PackedSets, edge_index=None, batch_mapping=None):
+        """ESA.forward (esa/masked_layers.py:849-936) on packed tokens, the "hip" backend's native entry.
+
+        tokens_x [T, D] holds the set elements graph after graph (edge tokens straight from the edge MLP, in
+        edge_index order; or node tokens), ``tokens`` their descriptor (``get_adj_mask_from_edge_index_edge``
+        / ``_node`` or ``EdgeAdjacency`` / ``NodeAdjacency.from_edge_index``).  No padded [B, N, D] tensor is
+        built: the reference's to_dense_batch (core/pretraining_model.py:211, esa/models.py:317) and the
+        encoder's work on padding slots go away.  Returns (graph embeddings [B, dim_output], token
+        embeddings before pooling [T, D]); ``enc`` equals the padded forward's at the valid slots.
+        """
+        if self.xformers_or_torch_attn != "hip":
+            raise ValueError("forward_packed is the native 'hip' backend's entry; this ESA was built for "
+                             f"{self.xformers_or_torch_attn!r}")
+        if tokens_x.dim() != 2 or tokens_x.shape[0] != tokens.num_tokens:
+            raise ValueError(f"tokens_x must be [T, D] with T = {tokens.num_tokens} (got {tuple(tokens_x.shape)})")
+        xp = tokens_x
         h = xp
         for blk in self.encoder:
             h = _sab_forward_packed(blk, h, tokens)
         if hasattr(self, "dim_pma") and self.dim_hidden[0] != self.dim_pma:
             xp = self.out_proj(xp)
         enc = h + xp
-        node_embeddings_before_pma = tokens.pad(enc)
         if hasattr(self, "decoder"):
             out = _pma_forward_packed(self.decoder[0], enc, tokens)
             for blk in list(self.decoder)[1:]:
-                out, _, _, _, _ = blk((out, edge_index, batch_mapping, num_max_items, tokens))
+                out, _, _, _, _ = blk((out, edge_index, batch_mapping, tokens.max_items, tokens))
             out = out.mean(dim=1)
-            return mish(self.decoder_linear(out)), node_embeddings_before_pma
-        return mish(self.decoder_linear(node_embeddings_before_pma)), node_embeddings_before_pma
+            return mish(self.decoder_linear(out)), enc
+        # no PMA: the head acts on every token (padding slots of the padded forward give mish(b) there)
+        return mish(self.decoder_linear(enc)), enc

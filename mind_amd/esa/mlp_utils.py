@@ -11,7 +11,7 @@ from torch import nn
 from torch.nn import functional as F
 
 from .activations import Mish, linear_mish
-from .linear import apply, linear
+from .linear import apply, hookless, linear
 
 
 def swiglu(gate, y):
@@ -47,7 +47,9 @@ class SmallMLP(nn.Module):
         layers = list(self.mlp)
         i = 0
         while i < len(layers):
-            if type(layers[i]) is nn.Linear and i + 1 < len(layers) and isinstance(layers[i + 1], nn.Mish):
+            nxt = layers[i + 1] if i + 1 < len(layers) else None
+            if (type(layers[i]) is nn.Linear and type(nxt) in (Mish, nn.Mish) and hookless(layers[i])
+                    and hookless(nxt)):
                 x = linear_mish(x, layers[i])   # Linear -> Mish: the bias gradient comes with Mish's backward
                 i += 2
             else:

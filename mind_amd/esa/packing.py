@@ -74,9 +74,14 @@ class PackedSets:
 
 
 def _positions(graph: torch.Tensor, batch_size: int) -> tuple[torch.Tensor, torch.Tensor]:
-    counts = torch.bincount(graph, minlength=batch_size)
-    cu = cu_seqlens_from_counts(counts)
-    position = torch.arange(graph.numel(), device=graph.device, dtype=torch.int64) - cu[:-1].to(torch.int64)[graph]
+    """cu_seqlens [B+1] and each token's slot in its graph, for tokens grouped by graph in ascending order
+    (a PyG batch; to_dense_batch makes the same assumption).  Binary searches over the sorted graph ids,
+    so no host synchronisation: graph ids outside [0, B) clamp to the nearest graph."""
+    dev = graph.device
+    bounds = torch.arange(batch_size + 1, device=dev, dtype=graph.dtype)
+    cu = torch.searchsorted(graph, bounds).to(torch.int32)
+    g = graph.clamp(0, max(batch_size - 1, 0))
+    position = torch.arange(graph.numel(), device=dev, dtype=torch.int64) - cu[:-1].to(torch.int64)[g]
     return cu, position
 
 
@@ -151,7 +156,9 @@ class NodeAdjacency(PackedSets):
         src, dst = edge_index[0].to(torch.int64), edge_index[1].to(torch.int64)
         key = torch.sort(src * max(nodes, 1) + dst).values
         s_sorted = torch.div(key, max(nodes, 1), rounding_mode="floor")
-        indptr = cu_seqlens_from_counts(torch.bincount(s_sorted, minlength=nodes)[:nodes])
+        # row starts by binary search over the sorted query ids (no host synchronisation)
+        indptr = torch.searchsorted(s_sorted, torch.arange(nodes + 1, device=key.device, dtype=key.dtype))
+        indptr = indptr.to(torch.int32)
         indices = (key - s_sorted * max(nodes, 1)).to(torch.int32).contiguous()
         return cls(graph=graph, position=position, cu_seqlens=cu, batch_size=int(batch_size),
                    max_items=int(max_items), indptr=indptr, indices=indices)

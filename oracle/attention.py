@@ -26,6 +26,12 @@ def _segment_mask(edge_src, edge_dst, qs, qe, ks, ke, adj=None):
     return torch.as_tensor(m)
 
 
+def _head_chunks(h, lq, lk, budget=1 << 26):
+    """Head ranges whose [heads, Lq, Lk] score block stays within ``budget`` elements (bounded memory)."""
+    step = max(1, min(h, budget // max(1, lq * lk)))
+    return [(a, min(h, a + step)) for a in range(0, h, step)]
+
+
 def varlen_attention(q, k, v, cu_q, cu_k, scale, edge_src=None, edge_dst=None, dtype=torch.float64, adj=None):
     """q [Tq,H,D], k/v [Tk,H,D] -> (out [Tq,H,D], lse [H,Tq]) in ``dtype``.
 
@@ -45,18 +51,22 @@ def varlen_attention(q, k, v, cu_q, cu_k, scale, edge_src=None, edge_dst=None, d
             outs.append(torch.zeros(qe - qs, h, d, dtype=dtype))
             lses.append(torch.full((h, qe - qs), float("-inf"), dtype=dtype))
             continue
-        qb = q[qs:qe].permute(1, 0, 2)                  # [H, Lq, D]
-        kb = k[ks:ke].permute(1, 2, 0)                  # [H, D, Lk]
-        vb = v[ks:ke].permute(1, 0, 2)                  # [H, Lk, D]
-        s = torch.matmul(qb, kb) * scale                # [H, Lq, Lk]
         m = _segment_mask(edge_src, edge_dst, qs, qe, ks, ke, adj)
-        if m is not None:
-            s = s.masked_fill(~m, float("-inf"))
-        l = torch.logsumexp(s, dim=-1)                  # [H, Lq]
-        # rows with no admissible key: every s is -inf; keep p = 0 without NaN
-        p = torch.exp(s - torch.where(torch.isfinite(l), l, torch.zeros_like(l))[..., None])
-        outs.append(torch.matmul(p, vb).permute(1, 0, 2))
-        lses.append(l)
+        ob, lb = [], []
+        for h0, h1 in _head_chunks(h, qe - qs, ke - ks):
+            qb = q[qs:qe, h0:h1].permute(1, 0, 2)           # [h, Lq, D]
+            kb = k[ks:ke, h0:h1].permute(1, 2, 0)           # [h, D, Lk]
+            vb = v[ks:ke, h0:h1].permute(1, 0, 2)           # [h, Lk, D]
+            s = torch.matmul(qb, kb) * scale                # [h, Lq, Lk]
+            if m is not None:
+                s = s.masked_fill(~m, float("-inf"))
+            l = torch.logsumexp(s, dim=-1)                  # [h, Lq]
+            # rows with no admissible key: every s is -inf; keep p = 0 without NaN
+            p = torch.exp(s - torch.where(torch.isfinite(l), l, torch.zeros_like(l))[..., None])
+            ob.append(torch.matmul(p, vb).permute(1, 0, 2))
+            lb.append(l)
+        outs.append(torch.cat(ob, 1))
+        lses.append(torch.cat(lb, 0))
     out = torch.cat(outs, 0) if outs else torch.zeros(0, h, d, dtype=dtype)
     lse = torch.cat(lses, 1) if lses else torch.zeros(h, 0, dtype=dtype)
     return out, lse
@@ -74,29 +84,87 @@ def varlen_attention_bwd(dout, q, k, v, cu_q, cu_k, scale, edge_src=None, edge_d
     cu_q = np.asarray(cu_q, dtype=np.int64)
     cu_k = np.asarray(cu_k, dtype=np.int64)
     dq, dk, dv = torch.zeros_like(q), torch.zeros_like(k), torch.zeros_like(v)
+    h = q.shape[1]
     for b in range(len(cu_q) - 1):
         qs, qe, ks, ke = int(cu_q[b]), int(cu_q[b + 1]), int(cu_k[b]), int(cu_k[b + 1])
         if qe == qs or ke == ks:
             continue
-        qb = q[qs:qe].permute(1, 0, 2).contiguous()
-        kb = k[ks:ke].permute(1, 0, 2).contiguous()
-        vb = v[ks:ke].permute(1, 0, 2).contiguous()
-        gb = dout[qs:qe].permute(1, 0, 2).contiguous()
-        s = torch.matmul(qb, kb.transpose(1, 2).contiguous()) * scale
         m = _segment_mask(edge_src, edge_dst, qs, qe, ks, ke, adj)
-        if m is not None:
-            s = s.masked_fill(~m, float("-inf"))
-        l = torch.logsumexp(s, dim=-1)
-        p = torch.exp(s - torch.where(torch.isfinite(l), l, torch.zeros_like(l))[..., None])
-        o = torch.matmul(p, vb)
-        dvb = torch.matmul(p.transpose(1, 2).contiguous(), gb)
-        dp = torch.matmul(gb, vb.transpose(1, 2).contiguous())
-        drow = (gb * o).sum(-1, keepdim=True)
-        ds = p * (dp - drow)
-        dq[qs:qe] = (torch.matmul(ds, kb) * scale).permute(1, 0, 2)
-        dk[ks:ke] = (torch.matmul(ds.transpose(1, 2).contiguous(), qb) * scale).permute(1, 0, 2)
-        dv[ks:ke] = dvb.permute(1, 0, 2)
+        for h0, h1 in _head_chunks(h, qe - qs, ke - ks):
+            qb = q[qs:qe, h0:h1].permute(1, 0, 2).contiguous()
+            kb = k[ks:ke, h0:h1].permute(1, 0, 2).contiguous()
+            vb = v[ks:ke, h0:h1].permute(1, 0, 2).contiguous()
+            gb = dout[qs:qe, h0:h1].permute(1, 0, 2).contiguous()
+            s = torch.matmul(qb, kb.transpose(1, 2).contiguous()) * scale
+            if m is not None:
+                s = s.masked_fill(~m, float("-inf"))
+            l = torch.logsumexp(s, dim=-1)
+            p = torch.exp(s - torch.where(torch.isfinite(l), l, torch.zeros_like(l))[..., None])
+            o = torch.matmul(p, vb)
+            dvb = torch.matmul(p.transpose(1, 2).contiguous(), gb)
+            dp = torch.matmul(gb, vb.transpose(1, 2).contiguous())
+            drow = (gb * o).sum(-1, keepdim=True)
+            ds = p * (dp - drow)
+            dq[qs:qe, h0:h1] = (torch.matmul(ds, kb) * scale).permute(1, 0, 2)
+            dk[ks:ke, h0:h1] = (torch.matmul(ds.transpose(1, 2).contiguous(), qb) * scale).permute(1, 0, 2)
+            dv[ks:ke, h0:h1] = dvb.permute(1, 0, 2)
     return dq, dk, dv
+
+
+class _VarlenAttentionFn(torch.autograd.Function):
+    """varlen_attention with the analytic backward above: saves only q, k, v (bounded memory for long
+    segments; the backward recomputes the scores head chunk by head chunk)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, cu_q, cu_k, scale, edge_src, edge_dst, adj):
+        out, _ = varlen_attention(q, k, v, cu_q, cu_k, scale, edge_src, edge_dst, dtype=q.dtype, adj=adj)
+        ctx.save_for_backward(q, k, v)
+        ctx.meta = (cu_q, cu_k, scale, edge_src, edge_dst, adj)
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        q, k, v = ctx.saved_tensors
+        cu_q, cu_k, scale, edge_src, edge_dst, adj = ctx.meta
+        dq, dk, dv = varlen_attention_bwd(g, q, k, v, cu_q, cu_k, scale, edge_src, edge_dst, dtype=q.dtype, adj=adj)
+        return dq, dk, dv, None, None, None, None, None, None
+
+
+def masked_attention_pairs(q, k, v, cu_q, cu_k, scale, edge_src=None, edge_dst=None, adj=None):
+    """The masked case of ``varlen_attention`` over the admissible (query, key) pairs only, as gathers and
+    scatters that torch autograd differentiates: s_ij = scale q_i . k_j per head for the mask's pairs of each
+    segment, softmax per query row (a row without pairs gives 0), out_i = sum_j p_ij v_j.  Work and memory
+    follow the mask's nonzeros, not L^2 (the protein-like edge masks are about 1 % dense)."""
+    cu_q = np.asarray(cu_q, dtype=np.int64)
+    cu_k = np.asarray(cu_k, dtype=np.int64)
+    rows, cols = [], []
+    for b in range(len(cu_q) - 1):
+        qs, qe, ks, ke = int(cu_q[b]), int(cu_q[b + 1]), int(cu_k[b]), int(cu_k[b + 1])
+        if qe == qs or ke == ks:
+            continue
+        i, j = np.nonzero(np.asarray(_segment_mask(edge_src, edge_dst, qs, qe, ks, ke, adj)))
+        rows.append(i + qs)
+        cols.append(j + ks)
+    tq, h, d = q.shape
+    if not rows or sum(r.size for r in rows) == 0:
+        return q.new_zeros(tq, h, d)
+    r = torch.as_tensor(np.concatenate(rows))
+    c = torch.as_tensor(np.concatenate(cols))
+    sc = (q.index_select(0, r) * k.index_select(0, c)).sum(-1) * scale          # [P, H]
+    mx = torch.full((tq, h), float("-inf"), dtype=q.dtype).scatter_reduce(
+        0, r[:, None].expand(-1, h), sc.detach(), "amax", include_self=True)
+    e = torch.exp(sc - mx.index_select(0, r))
+    den = q.new_zeros(tq, h).index_add(0, r, e)
+    p = e / den.index_select(0, r)
+    return q.new_zeros(tq, h, d).index_add(0, r, p[..., None] * v.index_select(0, c))
+
+
+def varlen_attention_diff(q, k, v, cu_q, cu_k, scale, edge_src=None, edge_dst=None, adj=None):
+    """``varlen_attention``'s output, differentiable in q, k, v: through ``varlen_attention_bwd`` without a
+    mask, through ``masked_attention_pairs`` with one."""
+    if edge_src is not None or adj is not None:
+        return masked_attention_pairs(q, k, v, cu_q, cu_k, scale, edge_src, edge_dst, adj)
+    return _VarlenAttentionFn.apply(q, k, v, cu_q, cu_k, scale, edge_src, edge_dst, adj)
 
 
 def padded_attention(q, k, v, scale, bias=None, dtype=torch.float64):

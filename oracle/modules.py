@@ -6,8 +6,12 @@ restate the forward of the reference block in float64:
   mab_varlen      esa/mha_flash_varlen.py:129-201 (V = fc_v(fc_k(K)), valid tokens)
   mab_packed      the same block over packed valid tokens with an optional
                   boolean per-graph mask (the native "hip" path's arithmetic)
+  mlp_standard    SmallMLP (esa/mlp_utils.py:6-48) without LayerNorm/dropout
   sab_complete    esa/masked_layers.py:408-494 (pre-norm branch)
-  pma_complete    esa/masked_layers.py:574-621 (pre-norm branch)
+  pma_complete    esa/masked_layers.py:574-621 (pre-norm branch), padded or packed keys
+  esa             ESA.forward (esa/masked_layers.py:849-936): encoder, enc + X,
+                  PMA decoder (+ later S layers on the seeds), mean over seeds,
+                  mish(decoder_linear)
 """
 from __future__ import annotations
 
@@ -15,7 +19,8 @@ import numpy as np
 import torch
 import torch.nn.functional as F
 
-from .attention import padded_attention, varlen_attention
+from .attention import padded_attention, varlen_attention, varlen_attention_diff
+from .packing import to_dense_batch
 
 DT = torch.float64   # the checker's precision (the CPU baseline of bench.py times it in float32)
 
@@ -70,8 +75,8 @@ def mab_packed(sd, prefix, Qp, Kp, cu_q, cu_k, heads, edge_src=None, edge_dst=No
     k = linear(sd, prefix + "fc_k.", Kp)
     v = linear(sd, prefix + "fc_v.", k if v_from_k else Kp)
     hd = q.shape[-1] // heads
-    o, _ = varlen_attention(_heads(q, heads), _heads(k, heads), _heads(v, heads), cu_q, cu_k, 1.0 / np.sqrt(hd),
-                            edge_src, edge_dst, dtype=DT, adj=adj)
+    o = varlen_attention_diff(_heads(q, heads).contiguous(), _heads(k, heads).contiguous(),
+                              _heads(v, heads).contiguous(), cu_q, cu_k, 1.0 / np.sqrt(hd), edge_src, edge_dst, adj)
     o = o.reshape(Qp.shape[0], -1)
     return o + mish(linear(sd, prefix + "fc_o.", o))
 
@@ -120,3 +125,68 @@ def sab_complete(sd, prefix, X, heads, attn, num_mlp_layers=None):
     if num_mlp_layers:
         out = out + mlp_standard(sd, prefix + "mlp.", layer_norm(sd, prefix + "norm_mlp.ln.", out), num_mlp_layers)
     return out
+
+
+def pma_complete(sd, prefix, X, heads, num_mlp_layers=None, cu=None, max_items=None):
+    """Pre-norm PMA block (esa/masked_layers.py:574-621) -> [B, k, D].
+
+    X' = LN(X) (:583); A = MAB(S.repeat(B, 1, 1), X') (esa/mha.py:108-109,
+    V = fc_v(K)); the residual X' + A only when the seed count k equals the
+    set size N (:595-603), else out = A; then out += MLP(LN2(out)) (:606-610).
+    X is padded [B, N, D] (``cu`` None: the seeds attend over all N positions,
+    padding included, as the reference does), or packed [T, D] with ``cu`` the
+    set offsets (the seeds attend over each set's valid tokens) and
+    ``max_items`` the padded N of the k == N test (padding slots then hold 0).
+    """
+    X = torch.as_tensor(X).cpu().to(DT)
+    xn = layer_norm(sd, prefix + "norm.ln.", X)
+    S = _p(sd, prefix + "pma.", "S")                       # [1, k, D]
+    k, d = S.shape[1], S.shape[2]
+    if cu is None:
+        b, n = X.shape[0], X.shape[1]
+        out = mab_padded(sd, prefix + "pma.mab.", S.repeat(b, 1, 1), xn, heads)
+        res = xn
+    else:
+        cu = np.asarray(cu, dtype=np.int64)
+        b, n = len(cu) - 1, int(max_items)
+        seeds = S.reshape(k, d).repeat(b, 1)
+        out = mab_packed(sd, prefix + "pma.mab.", seeds, xn, np.arange(b + 1) * k, cu, heads).reshape(b, k, d)
+        graph = np.repeat(np.arange(b), np.diff(cu))
+        res = to_dense_batch(xn, graph, b, n)[0] if k == n else None
+    if k == n:
+        out = res + out
+    if num_mlp_layers:
+        out = out + mlp_standard(sd, prefix + "mlp.", layer_norm(sd, prefix + "norm_mlp.ln.", out), num_mlp_layers)
+    return out
+
+
+def esa(sd, X, layer_types, heads, num_mlp_layers, attn_m, attn_s, pool):
+    """ESA.forward (esa/masked_layers.py:849-936) for equal hidden sizes -> (graph_emb [B, dim_output], enc).
+
+    Encoder (the M/S layers before the first P, :700-760) as pre-norm
+    SABComplete blocks, ``attn_m`` / ``attn_s`` computing the masked /
+    unmasked MAB sub-block (callables ``(sd, mab_prefix, x)``); enc =
+    encoder(X) + X (:917); the decoder's PMAComplete is ``pool(sd, prefix,
+    enc)`` -> [B, k, D] (a later P replaces it, :778); S layers after the P act
+    on the seeds with unmasked attention over the k seeds; out.mean(1) over the
+    seeds (:928); graph_emb = mish(decoder_linear(out)) (:929).
+    """
+    X = torch.as_tensor(X).cpu().to(DT)
+    types = list(layer_types)
+    p_at = types.index("P") if "P" in types else len(types)
+    h = X
+    for i, lt in enumerate(types[:p_at]):
+        h = sab_complete(sd, f"encoder.{i}.", h, heads, attn_m if lt == "M" else attn_s, num_mlp_layers)
+    enc = h + X
+    if p_at == len(types):
+        return mish(linear(sd, "decoder_linear.", enc)), enc
+    p_last = len(types) - 1 - types[::-1].index("P")
+    out = pool(sd, "decoder.0.", enc)
+
+    def seeds_attn(sd_, pre, x):
+        return mab_padded(sd_, pre, x, x, heads)
+
+    later_s = [lt for lt in types[p_last + 1:] if lt == "S"]   # an M after the P is not built (:743)
+    for j in range(len(later_s)):
+        out = sab_complete(sd, f"decoder.{j + 1}.", out, heads, seeds_attn, num_mlp_layers)
+    return mish(linear(sd, "decoder_linear.", out.mean(1))), enc

@@ -263,3 +263,47 @@ def test_pma_seed_pooling(device, dtype, seeds):
         assert_bf16_close(qd.grad.cpu(), rdq_seeds, grad_scale(rdq_seeds), "d seeds")
         assert_bf16_close(kd.grad.cpu(), rdk, grad_scale(rdk), "dk")
         assert_bf16_close(vd.grad.cpu(), rdv, grad_scale(rdv), "dv")
+
+
+@pytest.mark.parametrize("masked", [False, True])
+def test_32_heads(device, masked):
+    """Configuration 4's attention shape: 32 heads of head_dim 16 (dim 512), dense and edge-masked, bf16."""
+    gb = generators.protein_like(seed=12, num_graphs=4, n_min=40, n_max=140)
+    src = gb.edge_index[0].astype(np.int32) if masked else None
+    dst = gb.edge_index[1].astype(np.int32) if masked else None
+    _check(device, gb.edge_counts, gb.edge_counts, seed=1200 + masked, src=src, dst=dst, heads=32)
+
+
+def test_dense_rows_after_last_segment(device):
+    """cu_seqlens_q[-1] < total_q (flash-attn's varlen API allows it): the dK/dV pass stages the row statistics
+    of the rows after the last segment with its last partial tile; the backward prep writes them, so a
+    workspace full of NaN leaves dK / dV of every segment finite and equal to the oracle's."""
+    from mind_amd import _lib
+    lens = [40, 30]
+    cu = cu_from_lengths(lens)
+    tq = 90                                   # rows 70..89 belong to no segment
+    q, _, _, g = _inputs(tq, tq, 901)
+    k, v = seeded_normal((70, H, D), 905), seeded_normal((70, H, D), 906)
+    dev = [t.to(device).contiguous() for t in (q, k, v, g)]
+    qd, kd, vd, gd = dev
+    cud = torch.as_tensor(cu).to(device)
+    out, lse = A.attn_fwd(qd, kd, vd, cud, cud, 40, 40, 0.25)
+    out[70:] = 0                              # rows no segment covers are not written by the forward
+    lse[:, 70:] = 0
+    lib = _lib.load()
+    n = _lib.ctypes.c_size_t(0)
+    _lib.check(lib.esa_varlen_attn_workspace_size(tq, 70, H, D, _lib.ESA_BF16, _lib.ESA_MASK_NONE, 0, 1,
+                                                  _lib.ctypes.byref(n)), "workspace size")
+    ws = torch.full((int(n.value),), 0xFF, dtype=torch.uint8, device=device)   # every float NaN
+    dq, dk, dv = torch.empty_like(qd), torch.empty_like(kd), torch.empty_like(vd)
+    rc = lib.esa_varlen_attn_bwd(gd.data_ptr(), qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), out.data_ptr(),
+                                 lse.data_ptr(), cud.data_ptr(), cud.data_ptr(), 2, tq, 70, 40, 40, H, D,
+                                 _lib.ESA_BF16, 0.25, _lib.ESA_MASK_NONE, None, None, 0, dq.data_ptr(), dk.data_ptr(),
+                                 dv.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_of(qd))
+    _lib.check(rc, "esa_varlen_attn_bwd")
+    torch.cuda.synchronize()
+    assert torch.isfinite(dk.float()).all() and torch.isfinite(dv.float()).all()
+    rdq, rdk, rdv = OA.varlen_attention_bwd(g[:70], q[:70], k, v, cu, cu, 0.25)
+    assert_bf16_close(dk.cpu(), rdk, grad_scale(rdk), "dk")
+    assert_bf16_close(dv.cpu(), rdv, grad_scale(rdv), "dv")
+    assert_bf16_close(dq[:70].cpu(), rdq, grad_scale(rdq), "dq")

@@ -281,3 +281,83 @@ def test_scatter_add_matches_index_add(device, dtype, shape):
     gref = torch.zeros((e,) + shape, dtype=dtype)
     gref[keep] = up[index[keep]]
     assert torch.equal(sd.grad.cpu(), gref)
+
+
+def test_csr_build_one_hub_of_degree_2_20(device):
+    """A key of degree 2^20 beside mixed small degrees (the case a per-segment sort handles in O(deg^2)):
+    indptr and perm bit-exact against the stable sort."""
+    rng = np.random.default_rng(20)
+    n = 100_000
+    keys = np.concatenate([np.full(1 << 20, 7), rng.integers(0, n, size=300_000),
+                           np.repeat(rng.integers(0, n, size=50), 2000)]).astype(np.int32)
+    rng.shuffle(keys)
+    csr = edges.CSR.build(torch.as_tensor(keys).to(device), n)
+    indptr, perm = OE.csr_build(keys, n)
+    assert np.array_equal(csr.indptr.cpu().numpy(), indptr)
+    assert np.array_equal(csr.perm.cpu().numpy(), perm)
+
+
+def test_csr_build_drops_out_of_range_keys(device):
+    """Keys outside [0, N) are not counted; perm[:indptr[N]] is the stable grouping of the valid ones."""
+    rng = np.random.default_rng(3)
+    n = 5000
+    keys = rng.integers(-50, n + 50, size=80_000).astype(np.int32)
+    csr = edges.CSR.build(torch.as_tensor(keys).to(device), n)
+    valid = (keys >= 0) & (keys < n)
+    ids = np.nonzero(valid)[0].astype(np.int32)
+    indptr, sub = OE.csr_build(keys[valid], n)
+    got_ip = csr.indptr.cpu().numpy()
+    assert np.array_equal(got_ip, indptr)
+    assert np.array_equal(csr.perm.cpu().numpy()[: got_ip[-1]], ids[sub])
+
+
+def test_csr_build_keys_beyond_2_24(device):
+    """num_nodes > 2^24 takes four 8-bit digit passes."""
+    rng = np.random.default_rng(24)
+    n = (1 << 24) + 37
+    keys = np.concatenate([rng.integers(0, n, size=200_000), [n - 1, 0, 1 << 24, n - 1]]).astype(np.int32)
+    csr = edges.CSR.build(torch.as_tensor(keys).to(device), n)
+    indptr, perm = OE.csr_build(keys, n)
+    assert np.array_equal(csr.indptr.cpu().numpy(), indptr)
+    assert np.array_equal(csr.perm.cpu().numpy(), perm)
+
+
+def test_config3_full_size(device):
+    """Configuration 3 at its stated size (2^21 nodes x 2^25 edges x 256 features, fp32), through identities
+    that hold exactly at any size: the CSR by dst equals the stable sort; the gather equals torch's row
+    indexing bit for bit (checked in chunks); integer-valued edge rows sum exactly, so the segment sum equals
+    torch's index_add_ (whose atomic order cannot change an exact sum) and deg(n) * x[n] for the gathered dst
+    half; and a random-valued segment sum repeats bit for bit."""
+    n, e, f = 1 << 21, 1 << 25, 256
+    src, dst = generators.block_local_edges(0, num_nodes=n, num_edges=e)
+    print(f"[config3] generated {e} edges", flush=True)
+    s, d = torch.as_tensor(src).to(device), torch.as_tensor(dst).to(device)
+    csr = edges.CSR.build(d, n)
+    indptr, perm = OE.csr_build(dst, n)
+    assert np.array_equal(csr.indptr.cpu().numpy(), indptr)
+    assert np.array_equal(csr.perm.cpu().numpy(), perm)
+    del indptr, perm
+    g = torch.Generator(device=device).manual_seed(3)
+    x = torch.randn(n, f, device=device, generator=g)
+    h = edges.edge_gather(x, s, d)
+    step = 1 << 22
+    for lo in range(0, e, step):
+        sl, dl = s[lo:lo + step].long(), d[lo:lo + step].long()
+        assert torch.equal(h[lo:lo + step, :f].view(torch.int32), x[sl].view(torch.int32))
+        assert torch.equal(h[lo:lo + step, f:].view(torch.int32), x[dl].view(torch.int32))
+    print("[config3] gather bit-exact", flush=True)
+    del h
+    xi = torch.randint(-8, 8, (n, f), device=device, generator=g).float()
+    hi = edges.edge_gather(xi, s, d)
+    y = hi[:, f:].contiguous()
+    del hi
+    agg = edges.segment_sum_csr(y, csr.indptr, csr.perm)
+    deg = torch.diff(csr.indptr).float()
+    assert torch.equal(agg, xi * deg[:, None])
+    ref = torch.zeros(n, f, device=device).index_add_(0, d.long(), y)
+    assert torch.equal(agg, ref)
+    y.normal_(generator=g)
+    a = edges.segment_sum_csr(y, csr.indptr, csr.perm)
+    b = edges.segment_sum_csr(y, csr.indptr, csr.perm)
+    assert torch.equal(a, b)
+    print("[config3] segment sums exact", flush=True)

@@ -202,16 +202,11 @@ def test_esa_hip_packed_backward(device):
     cu = gb.cu_seqlens
     src, dst = gb.edge_index[0], gb.edge_index[1]
     xp = X.double()[valid].clone().requires_grad_(True)
-    h = OMod.sab_complete(sd, "encoder.0.", xp, H, lambda s, p, x: OMod.mab_packed(s, p, x, x, cu, cu, H, src, dst), 2)
-    h = OMod.sab_complete(sd, "encoder.1.", h, H, lambda s, p, x: OMod.mab_packed(s, p, x, x, cu, cu, H), 2)
-    enc_ref = h + xp
-    hn = OMod.layer_norm(sd, "decoder.0.norm.ln.", enc_ref)
-    S = OMod._p(sd, "decoder.0.pma.", "S").reshape(2, D).repeat(gb.num_graphs, 1)
-    pooled = OMod.mab_packed(sd, "decoder.0.pma.mab.", S, hn, np.arange(gb.num_graphs + 1) * 2, cu, H)
-    pooled = pooled + OMod.mlp_standard(sd, "decoder.0.mlp.", OMod.layer_norm(sd, "decoder.0.norm_mlp.ln.", pooled),
-                                        2)
-    pooled = pooled.reshape(gb.num_graphs, 2, D).mean(1)
-    g_ref = OMod.mish(OMod.linear(sd, "decoder_linear.", pooled))
+    g_ref, enc_ref = OMod.esa(
+        sd, xp, "MSP", H, 2,
+        attn_m=lambda s_, p_, x: OMod.mab_packed(s_, p_, x, x, cu, cu, H, src, dst),
+        attn_s=lambda s_, p_, x: OMod.mab_packed(s_, p_, x, x, cu, cu, H),
+        pool=lambda s_, p_, x: OMod.pma_complete(s_, p_, x, H, 2, cu=cu, max_items=n))
     ((g_ref * gg.double()).sum() + (enc_ref * ge.double()[valid]).sum()).backward()
     assert_f32_close(g_emb.detach().cpu(), g_ref.detach(), "ESA graph embedding")
     assert_f32_close(xd.grad.cpu()[valid], xp.grad, "dX (valid rows)")
@@ -241,42 +236,19 @@ def test_esa_block_config0_shape(device, backend):
     src, dst = gb.edge_index[0], gb.edge_index[1]
     gid = np.repeat(np.arange(gb.num_graphs), gb.edge_counts)
     if backend == "hip":
-        def m_attn(sd_, pre, x):
-            return OMod.mab_packed(sd_, pre, x, x, cu, cu, H, src, dst)
-
-        def s_attn(sd_, pre, x):
-            return OMod.mab_packed(sd_, pre, x, x, cu, cu, H)
-
-        xp = X.double()[valid]
-        h = OMod.sab_complete(sd, "encoder.0.", xp, H, m_attn, 2)
-        h = OMod.sab_complete(sd, "encoder.1.", h, H, s_attn, 2)
-        enc_ref = h + xp
-        hn = OMod.layer_norm(sd, "decoder.0.norm.ln.", enc_ref)
-        S = OMod._p(sd, "decoder.0.pma.", "S").reshape(1, D).repeat(gb.num_graphs, 1)
-        pooled = OMod.mab_packed(sd, "decoder.0.pma.mab.", S, hn, np.arange(gb.num_graphs + 1), cu, H)
-        pooled = pooled + OMod.mlp_standard(sd, "decoder.0.mlp.",
-                                            OMod.layer_norm(sd, "decoder.0.norm_mlp.ln.", pooled), 2)
-        g_ref = OMod.mish(OMod.linear(sd, "decoder_linear.", pooled))
+        g_ref, enc_ref = OMod.esa(
+            sd, X.double()[valid], "MSP", H, 2,
+            attn_m=lambda s_, p_, x: OMod.mab_packed(s_, p_, x, x, cu, cu, H, src, dst),
+            attn_s=lambda s_, p_, x: OMod.mab_packed(s_, p_, x, x, cu, cu, H),
+            pool=lambda s_, p_, x: OMod.pma_complete(s_, p_, x, H, 2, cu=cu, max_items=n))
         assert_f32_close(enc[valid], enc_ref, "ESA enc (valid rows)")
     else:
         bias = OM.edge_bias_padded(gb.edge_index, gid, gb.num_graphs, n, dtype=torch.float64)
-
-        def m_attn(sd_, pre, x):
-            return OMod.mab_padded(sd_, pre, x, x, H, bias)
-
-        def s_attn(sd_, pre, x):
-            return OMod.mab_padded(sd_, pre, x, x, H)
-
-        xd = X.double()
-        h = OMod.sab_complete(sd, "encoder.0.", xd, H, m_attn, 2)
-        h = OMod.sab_complete(sd, "encoder.1.", h, H, s_attn, 2)
-        enc_ref = h + xd
-        hn = OMod.layer_norm(sd, "decoder.0.norm.ln.", enc_ref)
-        S = OMod._p(sd, "decoder.0.pma.", "S").repeat(gb.num_graphs, 1, 1)
-        pooled = OMod.mab_padded(sd, "decoder.0.pma.mab.", S, hn, H)
-        pooled = pooled + OMod.mlp_standard(sd, "decoder.0.mlp.",
-                                            OMod.layer_norm(sd, "decoder.0.norm_mlp.ln.", pooled), 2)
-        g_ref = OMod.mish(OMod.linear(sd, "decoder_linear.", pooled.mean(1)))
+        g_ref, enc_ref = OMod.esa(
+            sd, X.double(), "MSP", H, 2,
+            attn_m=lambda s_, p_, x: OMod.mab_padded(s_, p_, x, x, H, bias),
+            attn_s=lambda s_, p_, x: OMod.mab_padded(s_, p_, x, x, H),
+            pool=lambda s_, p_, x: OMod.pma_complete(s_, p_, x, H, 2))
         assert_f32_close(enc, enc_ref, "ESA enc (all rows)")
     assert_f32_close(g_emb.reshape(g_ref.shape), g_ref, "ESA graph embedding")
 
@@ -288,3 +260,42 @@ def test_state_dict_names_match_reference_layout():
     for key in ("encoder.0.sab.mab.fc_q.weight", "encoder.0.norm.ln.weight", "encoder.1.mlp.mlp.0.fc1.weight",
                 "decoder.0.pma.S", "decoder.0.pma.mab.fc_o.bias", "decoder_linear.weight"):
         assert key in names, key
+
+
+def test_config0_full_batch(device):
+    """Configuration 0 at its stated size (64 small molecules, seed 0), fp32 end to end: one-hot atom types
+    embedded to 128, edge tokens Linear(256 -> 128) over [x_src || x_dst] (core/pretraining_model.py:152-198),
+    then the ESA block M(8 heads) - S - PMA(1 seed) on the native packed path, against the fp64 oracle."""
+    from mind_amd.edges import edge_gather
+    from mind_amd.esa.packing import EdgeAdjacency
+    gb, types = generators.small_molecules(seed=0)
+    assert gb.num_graphs == 64
+    n = nearest_multiple_of_8(gb.max_seqlen + 1)
+    torch.manual_seed(0)
+    emb, proj = torch.nn.Linear(16, D).to(device), torch.nn.Linear(2 * D, D).to(device)
+    model = ML.ESA(num_outputs=1, dim_output=D, dim_hidden=[D, D, D], num_heads=[H, H, H], layer_types="MSP",
+                   xformers_or_torch_attn="hip", use_mlps=True, mlp_hidden_size=2 * D, num_mlp_layers=2,
+                   mlp_type="standard").to(device)
+    onehot = torch.nn.functional.one_hot(torch.as_tensor(types), 16).float()
+    ei = torch.as_tensor(gb.edge_index).to(device)
+    bm = torch.as_tensor(gb.batch).to(device)
+    adj = EdgeAdjacency.from_edge_index(ei, bm, gb.num_graphs, n)
+    with torch.no_grad():
+        tok = proj(edge_gather(emb(onehot.to(device)), ei[0].int(), ei[1].int()))
+        g_emb, enc = model.forward_packed(tok, adj)
+        g_pad, enc_pad = model(adj.pad(tok), ei, bm, n)
+    assert torch.equal(g_pad, g_emb) and torch.equal(adj.unpad(enc_pad), enc)
+
+    x = onehot.double() @ emb.weight.detach().cpu().double().T + emb.bias.detach().cpu().double()
+    src, dst = gb.edge_index
+    tok_ref = torch.cat([x[torch.as_tensor(src)], x[torch.as_tensor(dst)]], 1) @ \
+        proj.weight.detach().cpu().double().T + proj.bias.detach().cpu().double()
+    assert_f32_close(tok.cpu(), tok_ref, "edge tokens")
+    cu = gb.cu_seqlens
+    g_ref, enc_ref = OMod.esa(
+        _sd(model), tok_ref, "MSP", H, 2,
+        attn_m=lambda s_, p_, z: OMod.mab_packed(s_, p_, z, z, cu, cu, H, src, dst),
+        attn_s=lambda s_, p_, z: OMod.mab_packed(s_, p_, z, z, cu, cu, H),
+        pool=lambda s_, p_, z: OMod.pma_complete(s_, p_, z, H, 2, cu=cu, max_items=n))
+    assert_f32_close(enc.cpu(), enc_ref, "token embeddings")
+    assert_f32_close(g_emb.cpu(), g_ref, "graph embeddings")

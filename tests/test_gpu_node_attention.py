@@ -161,15 +161,12 @@ def test_esa_node_mode(device):
     cu = na.cu_seqlens.numpy()
     adj = (na.indptr.numpy(), na.indices.numpy())
     xp = X.double()[valid]
-    h1 = OMod.sab_complete(sd, "encoder.0.", xp, h, lambda s_, p_, x: OMod.mab_packed(s_, p_, x, x, cu, cu, h, adj=adj), 2)
-    h2 = OMod.sab_complete(sd, "encoder.1.", h1, h, lambda s_, p_, x: OMod.mab_packed(s_, p_, x, x, cu, cu, h), 2)
-    enc_ref = h2 + xp
+    g_ref, enc_ref = OMod.esa(
+        sd, xp, "MSP", h, 2,
+        attn_m=lambda s_, p_, x: OMod.mab_packed(s_, p_, x, x, cu, cu, h, adj=adj),
+        attn_s=lambda s_, p_, x: OMod.mab_packed(s_, p_, x, x, cu, cu, h),
+        pool=lambda s_, p_, x: OMod.pma_complete(s_, p_, x, h, 2, cu=cu, max_items=n))
     assert_f32_close(enc.cpu()[valid], enc_ref, "ESA node-mode encoder (valid rows)")
-    hn = OMod.layer_norm(sd, "decoder.0.norm.ln.", enc_ref)
-    S = OMod._p(sd, "decoder.0.pma.", "S").reshape(1, dm).repeat(len(sizes), 1)
-    pooled = OMod.mab_packed(sd, "decoder.0.pma.mab.", S, hn, np.arange(len(sizes) + 1), cu, h)
-    pooled = pooled + OMod.mlp_standard(sd, "decoder.0.mlp.", OMod.layer_norm(sd, "decoder.0.norm_mlp.ln.", pooled), 2)
-    g_ref = OMod.mish(OMod.linear(sd, "decoder_linear.", pooled))
     assert_f32_close(g_emb.cpu().reshape(g_ref.shape), g_ref, "ESA node-mode graph embedding")
 
 

@@ -114,3 +114,75 @@ def test_small_mlp_walks_every_layer_once(num_layers, use_ln):
     mlp = SmallMLP(12, 20, 8, num_layers=num_layers, use_ln=use_ln)
     x = torch.randn(5, 12)
     assert torch.allclose(mlp(x), mlp.mlp(x), atol=1e-6)
+
+
+def test_small_mlp_keeps_module_hooks():
+    """A Linear or Mish carrying forward hooks is called as a module (its hooks fire), not fused away."""
+    from mind_amd.esa.mlp_utils import SmallMLP
+    torch.manual_seed(0)
+    mlp = SmallMLP(12, 20, 8, num_layers=3)
+    seen = []
+    mlp.mlp[1].register_forward_hook(lambda m, i, o: seen.append("mish1"))
+    mlp.mlp[2].register_forward_pre_hook(lambda m, i: seen.append("linear2"))
+    x = torch.randn(5, 12)
+    assert torch.allclose(mlp(x), mlp.mlp(x), atol=1e-6)
+    assert seen.count("mish1") == 2 and seen.count("linear2") == 2
+
+
+def test_scatter_add_backward_drops_out_of_range_exactly():
+    """Edges whose index is outside [0, dim_size) get a zero gradient even when the clamped row holds Inf."""
+    from mind_amd.edges import _ScatterAdd
+    index = torch.tensor([0, 5, -1, 1], dtype=torch.int32)
+    ctx = type("Ctx", (), {})()
+    ctx.saved_tensors = (index,)
+    ctx.dim_size = 2
+    g = torch.tensor([[float("inf")], [2.0]])
+    grad = _ScatterAdd.backward(ctx, g)[0]
+    assert grad[1].item() == 0.0 and grad[2].item() == 0.0 and grad[3].item() == 2.0
+
+
+def _radix_pass_model(keys, vals, shift, tile=4096, threads=256, waves=4, bits=8):
+    """numpy model of one pass of esa_csr_build's radix sort, step by step as the kernels take it: digit
+    counts per tile, their exclusive scan in (digit, tile) order, then each element's slot = the scan entry
+    + elements of the same digit in earlier rounds + in earlier waves of its round + in earlier lanes of its
+    wave (the ballot match)."""
+    n = keys.size
+    nb = -(-n // tile)
+    dig = (keys >> shift) & ((1 << bits) - 1)
+    hist = np.zeros((1 << bits, nb), np.int64)
+    for b in range(nb):
+        hist[:, b] = np.bincount(dig[b * tile:(b + 1) * tile], minlength=1 << bits)
+    offs = np.concatenate([[0], np.cumsum(hist.reshape(-1))])[:-1].reshape(hist.shape)
+    out_k, out_v = np.empty_like(keys), np.empty_like(vals)
+    for b in range(nb):
+        run = offs[:, b].copy()
+        for j in range(tile // threads):
+            lo = b * tile + j * threads
+            d = dig[lo:lo + threads]
+            wcnt = np.zeros((waves, 1 << bits), np.int64)
+            slots = []
+            for t in range(d.size):
+                w, lane = divmod(t, 64)
+                same = d[w * 64:w * 64 + lane] == d[t]          # lanes below with the same digit
+                slots.append((w, int(same.sum())))
+            for t in range(d.size):
+                wcnt[t // 64, d[t]] += 1
+            for t in range(d.size):
+                w, below = slots[t]
+                pos = run[d[t]] + wcnt[:w, d[t]].sum() + below
+                out_k[pos], out_v[pos] = keys[lo + t], vals[lo + t]
+            run += wcnt.sum(0)
+    return out_k, out_v
+
+
+def test_radix_csr_order_is_stable():
+    """The kernels' slot rule leaves (key, edge id) sorted by key with ties in ascending edge id: the model
+    of the passes equals numpy's stable argsort on keys with repeated values across several tiles."""
+    rng = np.random.default_rng(0)
+    n_keys = 600
+    keys = rng.integers(0, n_keys, size=9000).astype(np.int64)
+    keys[::7] = 5                                  # a heavy key spread over every tile
+    k, v = keys.copy(), np.arange(keys.size)
+    for shift in (0, 8):                          # 600 < 2^16: two 8-bit passes
+        k, v = _radix_pass_model(k, v, shift)
+    assert np.array_equal(v, np.argsort(keys, kind="stable"))

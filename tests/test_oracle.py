@@ -378,3 +378,272 @@ def test_mish_grad_matches_autograd_and_closed_forms():
     lo, hi = torch.tensor([-1.1925], dtype=torch.float64), torch.tensor([-1.1923], dtype=torch.float64)
     assert float(OMod.mish_grad(lo)) < 0 < float(OMod.mish_grad(hi))
     assert abs(float(OMod.mish(torch.tensor([-1.1924], dtype=torch.float64))) + 0.30884) < 1e-5
+
+
+# ---------------------------------------------------------------- block compositions
+
+def _lin_sd(sd, prefix, d_in, d_out, g, zero=False, eye=False):
+    w = torch.randn(d_out, d_in, generator=g, dtype=torch.float64) / np.sqrt(d_in)
+    b = torch.randn(d_out, generator=g, dtype=torch.float64) * 0.1
+    if zero:
+        w, b = torch.zeros_like(w), torch.zeros_like(b)
+    if eye:
+        w, b = torch.eye(d_out, d_in, dtype=torch.float64), torch.zeros_like(b)
+    sd[prefix + "weight"], sd[prefix + "bias"] = w, b
+
+
+def _ln_sd(sd, prefix, d, g, zero=False):
+    sd[prefix + "weight"] = torch.zeros(d, dtype=torch.float64) if zero else 1 + 0.3 * torch.randn(
+        d, generator=g, dtype=torch.float64)
+    sd[prefix + "bias"] = torch.zeros(d, dtype=torch.float64) if zero else 0.2 * torch.randn(
+        d, generator=g, dtype=torch.float64)
+
+
+def _block_sd(sd, prefix, d, hidden, g, mab_prefix="sab.mab.", zero_q=False, identity_o=False, mlp_last_zero=False,
+              mlp_identity=False, zero_block=False):
+    """Parameters of a pre-norm block with a 2-layer standard MLP under the reference's key names."""
+    _ln_sd(sd, prefix + "norm.ln.", d, g, zero=zero_block)
+    for name in ("fc_q", "fc_k", "fc_v", "fc_o"):
+        _lin_sd(sd, prefix + mab_prefix + name + ".", d, d, g, zero=(name == "fc_q" and zero_q),
+                eye=(name == "fc_o" and identity_o))
+    if zero_block:   # v = 0 and fc_o(0) = 0: the attention sub-block outputs exactly 0
+        sd[prefix + mab_prefix + "fc_v.bias"].zero_()
+        sd[prefix + mab_prefix + "fc_o.bias"].zero_()
+    _ln_sd(sd, prefix + "norm_mlp.ln.", d, g, zero=zero_block)
+    h0 = d if mlp_identity else hidden
+    _lin_sd(sd, prefix + "mlp.mlp.0.", d, h0, g, eye=mlp_identity)
+    _lin_sd(sd, prefix + "mlp.mlp.2.", h0, d, g, zero=mlp_last_zero or zero_block, eye=mlp_identity)
+    if zero_block:
+        sd[prefix + "mlp.mlp.0.bias"].zero_()
+
+
+def _lnf(sd, prefix, x):
+    """torch's own LayerNorm with the block's parameters (eps 1e-8, esa/utils/norm_layers.py:36)."""
+    return F.layer_norm(x, (x.shape[-1],), sd[prefix + "weight"], sd[prefix + "bias"], eps=1e-8)
+
+
+def _linf(sd, prefix, x):
+    return F.linear(x, sd[prefix + "weight"], sd[prefix + "bias"])
+
+
+@pytest.mark.parametrize("num_layers", [1, 2, 3])
+def test_mlp_standard_matches_reference_sequential(num_layers):
+    """SmallMLP's layer walk (esa/mlp_utils.py:18-44) built from torch modules in the reference's order:
+    [Linear, Identity, Mish] for one layer; Linear, Mish, ..., Linear otherwise."""
+    d_in, inter, d_out = 12, 20, 12
+    if num_layers == 1:
+        seq = torch.nn.Sequential(torch.nn.Linear(d_in, d_out), torch.nn.Identity(), torch.nn.Mish())
+    else:
+        layers = []
+        for i in range(num_layers):
+            a = d_in if i == 0 else inter
+            b = d_out if i == num_layers - 1 else inter
+            layers.append(torch.nn.Linear(a, b))
+            if i != num_layers - 1:
+                layers.append(torch.nn.Mish())
+        seq = torch.nn.Sequential(*layers)
+    torch.manual_seed(num_layers)
+    seq = seq.double()
+    sd = {"mlp." + k: v for k, v in seq.state_dict().items()}
+    x = torch.randn(7, d_in, dtype=torch.float64, generator=torch.Generator().manual_seed(3))
+    with torch.no_grad():
+        assert torch.allclose(OMod.mlp_standard(sd, "", x, num_layers), seq(x), atol=1e-12)
+
+
+def _one_segment(n, d, seed):
+    return torch.randn(n, d, dtype=torch.float64, generator=torch.Generator().manual_seed(seed)) * 2 + 0.5
+
+
+def test_sab_complete_closed_forms():
+    """fc_q = 0 makes attention uniform: the MAB gives m + mish(m) with m the key-mean of fc_v(LN(X)), so a
+    zero last MLP layer leaves out = LN(X) + m + mish(m) (the residual is on the normed X,
+    esa/masked_layers.py:471-472); identity MLP Linears then add mish(LN2(out)) (:478-483)."""
+    d, h, n = 16, 2, 9
+    g = torch.Generator().manual_seed(11)
+    X = _one_segment(n, d, 12)
+    cu = [0, n]
+
+    def attn(sd_, pre, x):
+        return OMod.mab_packed(sd_, pre, x, x, cu, cu, h)
+
+    sd = {}
+    _block_sd(sd, "", d, 24, g, zero_q=True, identity_o=True, mlp_last_zero=True)
+    xn = _lnf(sd, "norm.ln.", X)
+    m = _linf(sd, "sab.mab.fc_v.", xn).mean(0, keepdim=True)
+    ref = xn + (m + F.mish(m))
+    got = OMod.sab_complete(sd, "", X, h, attn, 2)
+    assert torch.allclose(got, ref, atol=1e-12)
+    assert not torch.allclose(got, X + m + F.mish(m), atol=1e-3)   # a residual on X would fail
+
+    sd2 = {}
+    _block_sd(sd2, "", d, 24, g, zero_q=True, identity_o=True, mlp_identity=True)
+    xn = _lnf(sd2, "norm.ln.", X)
+    m = _linf(sd2, "sab.mab.fc_v.", xn).mean(0, keepdim=True)
+    o1 = xn + m + F.mish(m)
+    ref2 = o1 + F.mish(_lnf(sd2, "norm_mlp.ln.", o1))
+    assert torch.allclose(OMod.sab_complete(sd2, "", X, h, attn, 2), ref2, atol=1e-12)
+
+
+def test_mab_packed_equals_padded_with_reference_bias():
+    """The packed MAB with the edge mask equals the reference's padded MAB with the restated -99999 bias
+    (esa/masked_layers.py:217-268, esa/mha.py:73-77) on every valid row; likewise in node mode."""
+    d, h = 16, 2
+    g = torch.Generator().manual_seed(21)
+    sd = {}
+    for name in ("fc_q", "fc_k", "fc_v", "fc_o"):
+        _lin_sd(sd, name + ".", d, d, g)
+    gb, _ = generators.small_molecules(seed=4, num_graphs=3)
+    n = OP.nearest_multiple_of_8(int(gb.edge_counts.max()) + 1)
+    t = int(gb.cu_seqlens[-1])
+    Xp = torch.randn(t, d, dtype=torch.float64, generator=g)
+    gid = np.repeat(np.arange(gb.num_graphs), gb.edge_counts)
+    X, valid = OP.to_dense_batch(Xp, gid, gb.num_graphs, n)
+    src, dst = gb.edge_index
+    assert OM.edge_adjacency_global(src, dst).any(1).all()   # every edge has a key: no uniform rows
+    bias = OM.edge_bias_padded(gb.edge_index, gid, gb.num_graphs, n, dtype=torch.float64)
+    ref = OMod.mab_padded(sd, "", X, X, h, bias)[valid]
+    got = OMod.mab_packed(sd, "", Xp, Xp, gb.cu_seqlens, gb.cu_seqlens, h, src, dst)
+    assert torch.allclose(got, ref, atol=1e-10)
+
+    ei, bm = node_graph(5, [7, 11, 4], extra_dup=False, self_loops=False)
+    counts = np.bincount(bm)
+    nn_ = OP.nearest_multiple_of_8(int(counts.max()) + 1)
+    Xn = torch.randn(len(bm), d, dtype=torch.float64, generator=g)
+    Xpad, vmask = OP.to_dense_batch(Xn, bm, len(counts), nn_)
+    nbias = OM.node_bias_padded(ei, bm, len(counts), nn_, dtype=torch.float64)
+    order = np.lexsort((ei[1], ei[0]))
+    indptr = OP.cu_seqlens(np.bincount(ei[0], minlength=len(bm)))
+    indices = ei[1][order]
+    has_key = np.diff(indptr) > 0
+    ref_n = OMod.mab_padded(sd, "", Xpad, Xpad, h, nbias)[vmask]
+    cu = OP.cu_seqlens(counts)
+    got_n = OMod.mab_packed(sd, "", Xn, Xn, cu, cu, h, adj=(indptr, indices))
+    assert torch.allclose(got_n[has_key], ref_n[torch.as_tensor(has_key)], atol=1e-10)
+
+
+@pytest.mark.parametrize("packed", [True, False])
+def test_pma_complete_closed_forms(packed):
+    """fc_q = 0 and fc_o = I: every seed's MAB output is m + mish(m), m the key-mean of fc_v(LN(X)) over the
+    set's valid tokens (packed) or all N positions, padding included (the reference, esa/mha.py:108-109 with
+    no mask at esa/masked_layers.py:593); no residual unless k == N (:595-603), where the padded form adds
+    LN(X) of every slot and the packed form LN(X) at valid slots and 0 at padding."""
+    d, h = 16, 2
+    g = torch.Generator().manual_seed(31)
+    lens = [5, 8, 3]
+    b, n = len(lens), 8
+    cu = OP.cu_seqlens(lens)
+    gid = np.repeat(np.arange(b), lens)
+    Xp = _one_segment(int(cu[-1]), d, 32)
+    X, valid = OP.to_dense_batch(Xp, gid, b, n)
+    for k in (3, n):
+        sd = {"pma.S": torch.randn(1, k, d, dtype=torch.float64, generator=g)}
+        _block_sd(sd, "", d, 24, g, mab_prefix="pma.mab.", zero_q=True, identity_o=True, mlp_last_zero=True)
+        xn = _lnf(sd, "norm.ln.", X)             # padding rows: LN(0) = the LN bias
+        v = _linf(sd, "pma.mab.fc_v.", xn)
+        if packed:
+            m = torch.stack([v[i, :lens[i]].mean(0) for i in range(b)])
+            res = xn * valid[..., None]
+            got = OMod.pma_complete(sd, "", Xp, h, 2, cu=cu, max_items=n)
+        else:
+            m = v.mean(1)
+            res = xn
+            got = OMod.pma_complete(sd, "", X, h, 2)
+        att = (m + F.mish(m))[:, None, :].expand(b, k, d)
+        ref = res + att if k == n else att
+        assert torch.allclose(got, ref, atol=1e-12), (packed, k)
+    # the MLP half: identity Linears give out + mish(LN2(out))
+    sd = {"pma.S": torch.randn(1, 3, d, dtype=torch.float64, generator=g)}
+    _block_sd(sd, "", d, 24, g, mab_prefix="pma.mab.", zero_q=True, identity_o=True, mlp_identity=True)
+    xn = _lnf(sd, "norm.ln.", X)
+    v = _linf(sd, "pma.mab.fc_v.", xn)
+    m = torch.stack([v[i, :lens[i]].mean(0) for i in range(b)]) if packed else v.mean(1)
+    o1 = (m + F.mish(m))[:, None, :].expand(b, 3, d)
+    ref = o1 + F.mish(_lnf(sd, "norm_mlp.ln.", o1))
+    got = OMod.pma_complete(sd, "", Xp, h, 2, cu=cu, max_items=n) if packed else OMod.pma_complete(sd, "", X, h, 2)
+    assert torch.allclose(got, ref, atol=1e-12)
+
+
+@pytest.mark.parametrize("layer_types", ["MSP", "MMSSMMSSP", "MSPS"])
+def test_esa_composition_closed_form(layer_types):
+    """Encoder blocks whose LayerNorms, fc_v / fc_o biases and MLP output are zero output exactly 0, so
+    enc = X (enc = encoder(X) + X, esa/masked_layers.py:917) whatever their other weights; a later S on the
+    seeds is zeroed the same way.  The decoder PMA with fc_q = 0, fc_o = I gives m + mish(m) for every seed,
+    m the key-mean of fc_v(LN(enc)), and graph_emb = mish(W mean_seeds + b) (:928-929).  A zeroed S block
+    after the P maps the seeds to exactly 0 (its residual is on the normed input, also zero), which leaves
+    graph_emb = mish(b)."""
+    d, h, k = 16, 2, 3
+    g = torch.Generator().manual_seed(41)
+    lens = [6, 9, 4]
+    b, n = len(lens), 16
+    cu = OP.cu_seqlens(lens)
+    gid = np.repeat(np.arange(b), lens)
+    Xp = _one_segment(int(cu[-1]), d, 42)
+    X, valid = OP.to_dense_batch(Xp, gid, b, n)
+    sd = {}
+    types = list(layer_types)
+    p_at = types.index("P")
+    for i in range(p_at):
+        _block_sd(sd, f"encoder.{i}.", d, 24, g, zero_block=True)
+    sd["decoder.0.pma.S"] = torch.randn(1, k, d, dtype=torch.float64, generator=g)
+    _block_sd(sd, "decoder.0.", d, 24, g, mab_prefix="pma.mab.", zero_q=True, identity_o=True, mlp_last_zero=True)
+    for j in range(len(types) - p_at - 1):
+        _block_sd(sd, f"decoder.{j + 1}.", d, 24, g, zero_block=True)
+    _lin_sd(sd, "decoder_linear.", d, 5, g)
+
+    def attn(sd_, pre, x):
+        return OMod.mab_packed(sd_, pre, x, x, cu, cu, h)
+
+    def pool(sd_, pre, x):
+        return OMod.pma_complete(sd_, pre, x, h, 2, cu=cu, max_items=n)
+
+    g_emb, enc = OMod.esa(sd, Xp, layer_types, h, 2, attn, attn, pool)
+    assert torch.equal(enc, Xp)
+    v = _linf(sd, "decoder.0.pma.mab.fc_v.", _lnf(sd, "decoder.0.norm.ln.", Xp))
+    m = torch.stack([v[cu[i]:cu[i + 1]].mean(0) for i in range(b)])
+    ref = F.mish(_linf(sd, "decoder_linear.", m + F.mish(m)))
+    if layer_types.endswith("S"):
+        ref = F.mish(sd["decoder_linear.bias"]).expand(b, 5)
+    assert torch.allclose(g_emb, ref, atol=1e-12)
+
+    def attn_p(sd_, pre, x):
+        return OMod.mab_padded(sd_, pre, x, x, h)
+
+    def pool_p(sd_, pre, x):
+        return OMod.pma_complete(sd_, pre, x, h, 2)
+
+    g_pad, enc_pad = OMod.esa(sd, X, layer_types, h, 2, attn_p, attn_p, pool_p)
+    assert torch.equal(enc_pad, X)
+    vp = _linf(sd, "decoder.0.pma.mab.fc_v.", _lnf(sd, "decoder.0.norm.ln.", X)).mean(1)   # padding included
+    ref_p = F.mish(_linf(sd, "decoder_linear.", vp + F.mish(vp)))
+    if layer_types.endswith("S"):
+        ref_p = F.mish(sd["decoder_linear.bias"]).expand(b, 5)
+    assert torch.allclose(g_pad, ref_p, atol=1e-12)
+
+
+@pytest.mark.parametrize("mode", ["none", "edge", "node"])
+def test_varlen_attention_diff_matches_dense_and_analytic_backward(mode):
+    """The differentiable form the module oracle uses (analytic backward without a mask, the pair-list form
+    with one) equals varlen_attention's output and varlen_attention_bwd's gradients."""
+    gb, _ = generators.small_molecules(seed=8, num_graphs=3)
+    cu = gb.cu_seqlens
+    src, dst, adj = None, None, None
+    if mode == "edge":
+        src, dst = gb.edge_index
+    t, h, d = int(cu[-1]), 3, 16
+    if mode == "node":
+        ei, bm = node_graph(9, [13, 8, 21])
+        counts = np.bincount(bm)
+        cu = OP.cu_seqlens(counts)
+        t = len(bm)
+        order = np.lexsort((ei[1], ei[0]))
+        adj = (OP.cu_seqlens(np.bincount(ei[0], minlength=t)), ei[1][order])
+    g = torch.Generator().manual_seed(4)
+    q, k, v, go = (torch.randn(t, h, d, dtype=torch.float64, generator=g) for _ in range(4))
+    qd, kd, vd = (x.clone().requires_grad_(True) for x in (q, k, v))
+    out = OA.varlen_attention_diff(qd, kd, vd, cu, cu, 0.3, src, dst, adj)
+    ref, _ = OA.varlen_attention(q, k, v, cu, cu, 0.3, src, dst, adj=adj)
+    assert torch.allclose(out, ref, atol=1e-12)
+    out.backward(go)
+    rdq, rdk, rdv = OA.varlen_attention_bwd(go, q, k, v, cu, cu, 0.3, src, dst, adj=adj)
+    for a, b in ((qd.grad, rdq), (kd.grad, rdk), (vd.grad, rdv)):
+        assert torch.allclose(a, b, atol=1e-11)
