@@ -37,6 +37,7 @@ extern "C" {
 #define ESA_ERR_DTYPE (-5)      /* unsupported dtype code */
 #define ESA_ERR_ALIGN (-6)      /* pointer not 16-byte aligned */
 #define ESA_ERR_MASK (-7)       /* unknown mask kind, or the edge mask without total_q == total_k */
+#define ESA_ERR_SCRATCH (-8)    /* the call needs more scratch than esa_noalloc_scratch_bytes() */
 
 #define ESA_F32 0
 #define ESA_BF16 1
@@ -97,6 +98,30 @@ ESA_API int esa_varlen_attn_fwd(const void* q, const void* k, const void* v,
                         int n_mask_edges,
                         void* out, float* softmax_lse,
                         void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* No-allocation forward.  No counterpart in the reference: it is for        */
+/* callers that cannot allocate device memory (code under HIP graph capture, */
+/* tight serving loops, harnesses that forbid hipMalloc).  Same arguments     */
+/* and results as esa_varlen_attn_fwd without the workspace: the scratch is  */
+/* a static device array of esa_noalloc_scratch_bytes() (4 MiB) per GPU,     */
+/* held until the process ends, enough for every ESA shape up to 131,072      */
+/* tokens x 32 heads (any mask kind).  A call needing more returns            */
+/* ESA_ERR_SCRATCH and launches nothing.  The caller still passes the inputs */
+/* and outputs; nothing is allocated or freed.  All calls on one GPU share   */
+/* that GPU's scratch: calls that overlap in time on one GPU (other streams, */
+/* other host threads without ordering) race and must be serialised by the  */
+/* caller.                                                                   */
+/* ------------------------------------------------------------------------ */
+ESA_API size_t esa_noalloc_scratch_bytes(void);
+ESA_API int esa_varlen_attn_fwd_noalloc(const void* q, const void* k, const void* v,
+                        const int* cu_seqlens_q, const int* cu_seqlens_k,
+                        int batch, int total_q, int total_k,
+                        int max_seqlen_q, int max_seqlen_k,
+                        int heads, int head_dim, int dtype, float softmax_scale,
+                        int mask_kind, const int* mask_a, const int* mask_b,
+                        int n_mask_edges,
+                        void* out, float* softmax_lse, void* stream);
 
 /* Gradients of esa_varlen_attn_fwd; replaces flash-attn's varlen backward. */
 ESA_API int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k,

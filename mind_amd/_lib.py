@@ -32,6 +32,7 @@ ERRORS = {
     -5: "ESA_ERR_DTYPE (unsupported dtype)",
     -6: "ESA_ERR_ALIGN (pointer not 16-byte aligned)",
     -7: "ESA_ERR_MASK (unknown mask kind, or the edge mask without total_q == total_k)",
+    -8: "ESA_ERR_SCRATCH (the call needs more scratch than the no-allocation entry point's static buffer)",
 }
 
 _c_int, _c_i64, _c_f, _c_sz, _vp = ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_size_t, ctypes.c_void_p
@@ -47,6 +48,10 @@ _PROTOS = {
     "esa_varlen_attn_bwd": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int,
                                      _c_int, _c_int, _c_int, _c_f, _c_int, _vp, _vp, _c_int, _vp, _vp, _vp, _vp, _c_sz,
                                      _vp]),
+    "esa_noalloc_scratch_bytes": (_c_sz, []),
+    # as esa_varlen_attn_fwd without workspace / workspace_bytes
+    "esa_varlen_attn_fwd_noalloc": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
+                                             _c_int, _c_int, _c_f, _c_int, _vp, _vp, _c_int, _vp, _vp, _vp]),
     "esa_edge_mask_dense": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _vp]),
     # batch k_seeds total_k heads head_dim dtype backward bytes
     "esa_pma_workspace_size": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,

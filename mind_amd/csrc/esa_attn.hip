@@ -53,6 +53,7 @@
 // Global loads go through buffer resources with the tensor's byte size as
 // range: the hardware returns 0 for any part of a load past the end, so tiles
 // that run past the last token need no index clamping.
+#include <mutex>
 #include <type_traits>
 
 #include "esa_attn_tiles.h"
@@ -1211,6 +1212,35 @@ int launch_prep(PrepArgs& p, bool forward, bool masked, hipStream_t st) {
   return ESA_OK;
 }
 
+// Scratch of esa_varlen_attn_fwd_noalloc: a file-scope device array, one
+// copy per GPU, held until the process ends.  Host code never passes the
+// array's name (a host-side stand-in) to a kernel: it passes the device
+// address hipGetSymbolAddress returns, looked up once per device on the
+// first call with that device current.
+constexpr size_t kNoAllocScratchBytes = size_t(4) << 20;
+__device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_address(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxDevices) return ESA_ERR_SHAPE;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    if (!ptr) return ESA_ERR_NULL;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return ESA_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1324,6 +1354,28 @@ int esa_varlen_attn_fwd(const void* q, const void* k, const void* v, const int* 
   ESA_TIMED(esa_profile::kAttnFwdMasked, st, hipLaunchKernelGGL(edge_fwd_kernel, dim3(egrid), dim3(256), 0, st, a));
   ESA_LAUNCH_CHECK();
   return ESA_OK;
+}
+
+size_t esa_noalloc_scratch_bytes(void) { return kNoAllocScratchBytes; }
+
+int esa_varlen_attn_fwd_noalloc(const void* q, const void* k, const void* v, const int* cu_seqlens_q,
+                                const int* cu_seqlens_k, int batch, int total_q, int total_k,
+                                int max_seqlen_q, int max_seqlen_k, int heads, int head_dim, int dtype,
+                                float softmax_scale, int mask_kind, const int* mask_a, const int* mask_b,
+                                int n_mask_edges, void* out, float* softmax_lse, void* stream) {
+  size_t need = 0;
+  int rc = esa_varlen_attn_workspace_size(total_q, total_k, heads, head_dim, dtype, mask_kind, n_mask_edges, 0,
+                                          &need);
+  if (rc) return rc;
+  if (need > kNoAllocScratchBytes) return ESA_ERR_SCRATCH;
+  void* ws = nullptr;
+  if ((rc = scratch_address(&ws))) return rc;
+  // The prep pass writes every scratch word the forward kernels read, as it
+  // does for the allocating entry point's uninitialised workspace, so nothing
+  // needs clearing between calls.
+  return esa_varlen_attn_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, batch, total_q, total_k, max_seqlen_q,
+                             max_seqlen_k, heads, head_dim, dtype, softmax_scale, mask_kind, mask_a, mask_b,
+                             n_mask_edges, out, softmax_lse, ws, kNoAllocScratchBytes, stream);
 }
 
 int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k, const void* v, const void* out,

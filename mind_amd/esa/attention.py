@@ -104,6 +104,34 @@ def attn_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, so
     return out, lse
 
 
+def attn_fwd_noalloc(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale, out, lse,
+                     edge_src=None, edge_dst=None, adj_indptr=None, adj_indices=None):
+    """``attn_fwd`` into caller-provided ``out`` [Tq,H,16] and ``lse`` [H,Tq] fp32 through
+    esa_varlen_attn_fwd_noalloc: no workspace, no device allocation (the library's static per-GPU scratch;
+    calls that overlap on one GPU race).  Raises EsaError (ESA_ERR_SCRATCH) for shapes beyond that scratch."""
+    _lib.require_gpu(q, k, v, cu_seqlens_q, cu_seqlens_k, edge_src, edge_dst, adj_indptr, adj_indices, out, lse)
+    heads = q.shape[1]
+    _check_tokens("q", q)
+    _check_tokens("k", k, heads, q.dtype)
+    _check_tokens("v", v, heads, q.dtype)
+    _check_tokens("out", out, heads, q.dtype)
+    if out.shape != q.shape:
+        raise ValueError("out must have the shape of q")
+    if lse.dtype != torch.float32 or tuple(lse.shape) != (heads, q.shape[0]) or not lse.is_contiguous():
+        raise ValueError(f"lse must be a contiguous float32 [{heads}, {q.shape[0]}] tensor")
+    batch = cu_seqlens_q.numel() - 1
+    _check_index("cu_seqlens_q", cu_seqlens_q)
+    _check_index("cu_seqlens_k", cu_seqlens_k, batch + 1)
+    tq, tk = q.shape[0], k.shape[0]
+    mask_kind, mask_a, mask_b, nnz = _mask_args(tq, edge_src, edge_dst, adj_indptr, adj_indices)
+    rc = _lib.load().esa_varlen_attn_fwd_noalloc(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(), batch, tq, tk,
+        int(max_seqlen_q), int(max_seqlen_k), heads, HEAD_DIM, _dtype_code(q), float(softmax_scale),
+        mask_kind, _lib.ptr(mask_a), _lib.ptr(mask_b), nnz, out.data_ptr(), lse.data_ptr(), _lib.stream_of(q))
+    _lib.check(rc, "esa_varlen_attn_fwd_noalloc")
+    return out, lse
+
+
 def attn_bwd(dout, q, k, v, out, lse, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale,
              edge_src=None, edge_dst=None, adj_indptr=None, adj_indices=None):
     """Raw backward: returns ``(dq, dk, dv)`` (dtype and shapes of q, k, v)."""

@@ -1,0 +1,73 @@
+"""esa_varlen_attn_fwd_noalloc (the forward with the library's static per-GPU scratch, for callers that cannot
+allocate) against esa_varlen_attn_fwd on the same inputs: bit-equal outputs and lse (the same kernels), on two
+calls in a row, the second with a smaller input, for the dense bf16, edge-masked bf16, node-mode and fp32
+paths; a shape beyond the scratch is refused before any launch."""
+import numpy as np
+import pytest
+import torch
+
+from mind_amd import _lib, generators
+from mind_amd.esa import attention as A
+from mind_amd.esa.packing import NodeAdjacency
+from tests._util import node_graph, seeded_normal
+
+pytestmark = pytest.mark.gpu
+
+H, D = 16, 16
+
+
+def _case(device, gb, seed, dtype, mask):
+    cu = torch.as_tensor(gb.cu_seqlens).to(device)
+    t = int(gb.cu_seqlens[-1])
+    q, k, v = (seeded_normal((t, H, D), seed + i, dtype).to(device) for i in range(3))
+    kw = {}
+    if mask == "edge":
+        kw = {"edge_src": torch.as_tensor(gb.edge_index[0].astype(np.int32)).to(device),
+              "edge_dst": torch.as_tensor(gb.edge_index[1].astype(np.int32)).to(device)}
+    return q, k, v, cu, int(gb.max_seqlen), kw
+
+
+def _compare(device, q, k, v, cu, mx, kw):
+    ref_o, ref_l = A.attn_fwd(q, k, v, cu, cu, mx, mx, 0.25, **kw)
+    out = torch.full_like(q, float("nan"))
+    lse = torch.full((q.shape[1], q.shape[0]), float("nan"), device=device)
+    A.attn_fwd_noalloc(q, k, v, cu, cu, mx, mx, 0.25, out, lse, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref_o)
+    assert torch.equal(lse, ref_l)
+
+
+@pytest.mark.parametrize("dtype,mask", [(torch.bfloat16, "none"), (torch.bfloat16, "edge"), (torch.float32, "none"),
+                                        (torch.float32, "edge")])
+def test_noalloc_forward_equals_allocating_forward(device, dtype, mask):
+    big = generators.protein_like(seed=0) if mask == "none" else generators.protein_budget(seed=0, token_budget=65536)
+    small = generators.protein_like(seed=3, num_graphs=5, n_min=40, n_max=150)
+    for gb, seed in ((big, 11), (small, 12)):   # the second call is smaller: stale scratch must not matter
+        print(f"[noalloc] {dtype} mask={mask} tokens={int(gb.cu_seqlens[-1])}", flush=True)
+        _compare(device, *_case(device, gb, seed, dtype, mask))
+
+
+def test_noalloc_forward_node_mask(device):
+    for sizes, seed in (([60, 45, 80], 5), ([12, 7], 6)):
+        ei, bm = node_graph(seed, sizes)
+        na = NodeAdjacency.from_edge_index(torch.as_tensor(ei).to(device), torch.as_tensor(bm).to(device),
+                                           len(sizes), max(sizes))
+        t = len(bm)
+        q, k, v = (seeded_normal((t, H, D), seed + i).to(device) for i in range(3))
+        _compare(device, q, k, v, na.cu_seqlens, max(sizes),
+                 {"adj_indptr": na.indptr, "adj_indices": na.indices})
+
+
+def test_noalloc_rejects_shapes_beyond_scratch(device):
+    lib = _lib.load()
+    cap = int(lib.esa_noalloc_scratch_bytes())
+    assert cap == 4 << 20
+    n = _lib.ctypes.c_size_t(0)
+    tq = 1 << 20          # one million tokens: the forward plan alone exceeds 4 MiB
+    _lib.check(lib.esa_varlen_attn_workspace_size(tq, tq, H, D, _lib.ESA_BF16, _lib.ESA_MASK_NONE, 0, 0,
+                                                  _lib.ctypes.byref(n)), "workspace size")
+    assert n.value > cap
+    # the size check comes first: with null pointers nothing can be launched
+    rc = lib.esa_varlen_attn_fwd_noalloc(None, None, None, None, None, 1, tq, tq, tq, tq, H, D, _lib.ESA_BF16, 0.25,
+                                         _lib.ESA_MASK_NONE, None, None, 0, None, None, None)
+    assert rc == -8
