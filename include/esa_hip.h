@@ -203,6 +203,23 @@ ESA_API int esa_csr_build(const int* keys, int64_t num_edges, int num_nodes,
                   void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------ */
+/* Token-budget batching: the greedy rule of                                */
+/* ImprovedDynamicBatchSampler._create_batches_standard                     */
+/* (data_loading/improved_dynamic_sampler.py:215-224) over graphs in order,  */
+/* on the device.  counts [num_graphs] (int32, device; negative counts as 0) */
+/* are the tokens each graph contributes; a graph that would push the open   */
+/* batch past `budget` opens the next batch, unless the open batch is empty. */
+/* Writes batch_of_graph [num_graphs] (batch id of each graph, consecutive   */
+/* from 0), batch_start [num_graphs + 1] (first graph of each batch, then    */
+/* num_graphs after the last; entries past it unused) and *num_batches (a    */
+/* device int).  One block; no host synchronisation.                         */
+/* ------------------------------------------------------------------------ */
+ESA_API int esa_token_budget_pack_workspace_size(int num_graphs, size_t* bytes);
+ESA_API int esa_token_budget_pack(const int* counts, int num_graphs, int64_t budget,
+                          int* batch_of_graph, int* batch_start, int* num_batches,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------ */
 /* Deterministic segmented sum: out[n] = sum_{i in [indptr[n], indptr[n+1])} */
 /* y[perm ? perm[i] : i], accumulated in fp32 in ascending i and rounded     */
 /* once.  y is [E, F], out is [N, F], both of `dtype`.  Replaces the atomic  */

@@ -66,6 +66,9 @@ _PROTOS = {
     "esa_csr_workspace_size": (_c_int, [_c_i64, _c_int, ctypes.POINTER(_c_sz)]),
     "esa_csr_build": (_c_int, [_vp, _c_i64, _c_int, _vp, _vp, _vp, _c_sz, _vp]),
     "esa_csr_segment_sum": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _vp]),
+    "esa_token_budget_pack_workspace_size": (_c_int, [_c_int, ctypes.POINTER(_c_sz)]),
+    # counts num_graphs budget | batch_of_graph batch_start num_batches ws bytes stream
+    "esa_token_budget_pack": (_c_int, [_vp, _c_int, _c_i64, _vp, _vp, _vp, _vp, _c_sz, _vp]),
     "esa_edge_gather_bwd": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _vp]),
     "esa_edge_gather_add": (_c_int, [_vp, _c_i64, _vp, _c_i64, _vp, _vp, _vp, _c_i64, _c_int, _c_int, _c_int, _vp,
                                      _vp]),

@@ -14,12 +14,43 @@ from __future__ import annotations
 
 from dataclasses import dataclass
 
+import ctypes
+
 import torch
+
+from .. import _lib
 
 
 def nearest_multiple_of_8(n: int) -> int:
     """core/molecular_encoder.py:15."""
     return ((int(n) + 7) // 8) * 8
+
+
+def token_budget_batches(counts: torch.Tensor, budget: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Greedy token-budget batching of graphs in order, on the device (esa_token_budget_pack).
+
+    The rule of ImprovedDynamicBatchSampler (data_loading/improved_dynamic_sampler.py:215-224) with
+    ``counts`` [G] the tokens of each graph (edge counts for edge-set attention): a graph that would push
+    the open batch past ``budget`` opens the next batch, unless the open batch is empty.  Returns device
+    tensors (batch_of_graph [G] int32, batch_start [G + 1] int32, num_batches int32 scalar): batch b holds
+    graphs batch_start[b] .. batch_start[b + 1] - 1 for b < num_batches.  Nothing synchronises with the host.
+    """
+    _lib.require_gpu(counts)
+    if counts.dim() != 1:
+        raise ValueError("counts must be 1-D")
+    counts = counts.to(torch.int32).contiguous()
+    g = counts.numel()
+    lib = _lib.load()
+    nbytes = ctypes.c_size_t(0)
+    _lib.check(lib.esa_token_budget_pack_workspace_size(g, ctypes.byref(nbytes)), "esa_token_budget_pack_workspace_size")
+    ws = torch.empty(max(int(nbytes.value), 256), dtype=torch.uint8, device=counts.device)
+    batch_of_graph = torch.empty(g, dtype=torch.int32, device=counts.device)
+    batch_start = torch.empty(g + 1, dtype=torch.int32, device=counts.device)
+    num = torch.empty((), dtype=torch.int32, device=counts.device)
+    _lib.check(lib.esa_token_budget_pack(counts.data_ptr(), g, int(budget), batch_of_graph.data_ptr(),
+                                         batch_start.data_ptr(), num.data_ptr(), ws.data_ptr(), ws.numel(),
+                                         _lib.stream_of(counts)), "esa_token_budget_pack")
+    return batch_of_graph, batch_start, num
 
 
 def cu_seqlens_from_counts(counts: torch.Tensor) -> torch.Tensor:

@@ -42,3 +42,21 @@ def to_dense_batch(x: torch.Tensor, graph_of_token: np.ndarray, batch_size: int,
     out[g, p] = x
     mask[g, p] = True
     return out, mask
+
+
+def token_budget_batches(counts, budget: int) -> list[list[int]]:
+    """Greedy batching of graphs in order under a token budget: the rule of
+    ImprovedDynamicBatchSampler._create_batches_standard (data_loading/improved_dynamic_sampler.py:215-224),
+    graph i counting ``counts[i]`` tokens.  Returns the batches as lists of graph indices."""
+    batches, current, tokens = [], [], 0
+    for i, c in enumerate(counts):
+        c = max(int(c), 0)
+        if tokens + c > budget and current:
+            batches.append(current)
+            current, tokens = [i], c
+        else:
+            current.append(i)
+            tokens += c
+    if current:
+        batches.append(current)
+    return batches

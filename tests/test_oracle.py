@@ -647,3 +647,24 @@ def test_varlen_attention_diff_matches_dense_and_analytic_backward(mode):
     rdq, rdk, rdv = OA.varlen_attention_bwd(go, q, k, v, cu, cu, 0.3, src, dst, adj=adj)
     for a, b in ((qd.grad, rdq), (kd.grad, rdk), (vd.grad, rdv)):
         assert torch.allclose(a, b, atol=1e-11)
+
+
+def test_token_budget_batches_hand_case():
+    # 3 + 4 fit, 5 would pass 8; 5 alone; 10 is oversize: a batch of its own; 1 + 1
+    assert OP.token_budget_batches([3, 4, 5, 10, 1, 1], 8) == [[0, 1], [2], [3], [4, 5]]
+    assert OP.token_budget_batches([], 8) == []
+    assert OP.token_budget_batches([0, 0, 9, 0], 8) == [[0, 1], [2], [3]]
+
+
+@given(st.lists(st.integers(0, 40), min_size=1, max_size=60), st.integers(0, 100))
+@settings(max_examples=200, deadline=None)
+def test_token_budget_batches_is_the_greedy_partition(counts, budget):
+    """Contiguous in-order batches; each within the budget unless a single graph; and none could take the
+    next graph: the properties that fix the greedy partition uniquely."""
+    batches = OP.token_budget_batches(counts, budget)
+    assert [i for b in batches for i in b] == list(range(len(counts)))
+    for j, b in enumerate(batches):
+        s = sum(counts[i] for i in b)
+        assert s <= budget or len(b) == 1
+        if j + 1 < len(batches):
+            assert s + counts[batches[j + 1][0]] > budget
