@@ -9,11 +9,15 @@ with inputs already resident in HBM.
 
 Prints one JSON line: throughput in edge-tokens/s, MFMA utilisation of the
 dense-bf16 peak, the roofline of the dominant kernel and a CPU baseline (the
-oracle's per-graph fp32 attention forward + backward on a bounded sample of
-the same batch, on this host's cores).  The step time comes from a timed
-region without instrumentation; the per-kernel durations of the roofline come
-from a second region of as many steps with HIP events around every library
-launch (its step time is reported as ms_per_step_profiled).
+reference's padded attention path restated in oracle/ -- torch's
+scaled_dot_product_attention over sets padded to N, the fallback of
+esa/mha_flash_varlen.py:81-126 -- on the whole batch, on this host's cores).
+Beside the headline the same line carries the edge-masked attention of
+configuration 2 ("masked") and the gather / segment sum of configuration 3
+("gather"), each with its own roofline and CPU baseline.  Step times come
+from timed regions without instrumentation; the per-kernel durations of the
+rooflines come from a second region of as many steps with HIP events around
+every library launch (its step time is reported as ms_per_step_profiled).
 """
 from __future__ import annotations
 
@@ -47,9 +51,11 @@ def parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--cpu-sample-graphs", type=int, default=3,
-                    help="graphs of the batch timed on the CPU for the baseline")
+    ap.add_argument("--cpu-sample-graphs", type=int, default=8,
+                    help="graphs of the configuration-2 batch timed on the CPU for the masked baseline")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-sub", action="store_true",
+                    help="headline only: skip the masked (configuration 2) and gather (configuration 3) sub-objects")
     ap.add_argument("--config", choices=["varlen", "masked", "gather", "block", "stack"], default="varlen",
                     help="varlen: configuration 1 (default, the headline metric); masked: configuration 2 "
                          "(edge-masked MAB attention fwd+bwd); gather: configuration 3 (edge gather + CSR "
@@ -73,40 +79,62 @@ def copy_calibration():
     print(json.dumps({"copy_bytes_read": 4 * n, "copy_bytes_written": 4 * n, "launches": 3}), flush=True)
 
 
-def cpu_baseline(gb, seed: int, n_graphs: int) -> dict:
-    """Oracle per-graph attention fwd+bwd in fp32 on the host cores, bounded sample."""
-    import numpy as np
-    import torch
-
-    from oracle import attention as oracle_attention
-
-    cores = len(os.sched_getaffinity(0))
-    torch.set_num_threads(cores)
-    order = np.argsort(gb.edge_counts)
-    # a sample spread over the length distribution: shortest, median, longest ...
-    pick = sorted(set(int(order[int(i)]) for i in np.linspace(0, len(order) - 1, n_graphs)))
-    lens = gb.edge_counts[pick]
-    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
-    t = int(cu[-1])
-    g = torch.Generator().manual_seed(seed + 99)
-    q, k, v, go = (torch.randn(t, HEADS, HEAD_DIM, generator=g) for _ in range(4))
-
-    def step():
-        oracle_attention.varlen_attention(q, k, v, cu, cu, 0.25, dtype=torch.float32)
-        oracle_attention.varlen_attention_bwd(go, q, k, v, cu, cu, 0.25, dtype=torch.float32)
-
-    step()
+def _median_time(step, warmup: int = 2, runs: int = 5) -> tuple[float, int]:
+    """Median wall time of `runs` calls after `warmup` untimed ones (BASELINE.md's method)."""
+    for _ in range(warmup):
+        step()
     times = []
-    budget = time.perf_counter() + 12.0
-    while len(times) < 3 or (time.perf_counter() < budget and len(times) < 20):
+    for _ in range(runs):
         t0 = time.perf_counter()
         step()
         times.append(time.perf_counter() - t0)
-    med = float(np.median(times))
+    return float(np.median(times)), len(times)
+
+
+def cpu_baseline(gb, seed: int) -> dict:
+    """The reference's padded attention path on the host cores, fp32, forward + backward on the whole batch.
+
+    oracle.attention.padded_sdpa restates MABFlashVarlen._forward_padded (esa/mha_flash_varlen.py:81-126):
+    every graph padded to N = nearest_multiple_of_8(max L + 1) positions and torch's
+    scaled_dot_product_attention with the key-padding mask, backward by autograd.  Timed with all the
+    process's cores, then with one thread (the reference's own setting, core/train_pretrain.py:850) on the
+    median-length graph alone."""
+    import torch
+
+    from oracle import attention as oracle_attention
+    from oracle.packing import nearest_multiple_of_8
+
+    cores = len(os.sched_getaffinity(0))
+    cu = gb.cu_seqlens.astype(np.int64)
+    t = int(cu[-1])
+    n = nearest_multiple_of_8(gb.max_seqlen + 1)
+    g = torch.Generator().manual_seed(seed + 99)
+    q, k, v, go = (torch.randn(t, HEADS, HEAD_DIM, generator=g) for _ in range(4))
+
+    def make_step(qq, kk, vv, gg, cuq, nn):
+        def step():
+            qd, kd, vd = (x.detach().requires_grad_(True) for x in (qq, kk, vv))
+            out = oracle_attention.padded_sdpa(qd, kd, vd, cuq, cuq, nn, 1.0 / HEAD_DIM ** 0.5)
+            out.backward(gg)
+        return step
+
+    torch.set_num_threads(cores)
+    med, runs = _median_time(make_step(q, k, v, go, cu, n))
+    b = int(np.argsort(gb.edge_counts)[len(gb.edge_counts) // 2])
+    s0, e0 = int(cu[b]), int(cu[b + 1])
+    sub = np.array([0, e0 - s0])
+    torch.set_num_threads(1)
+    med1, runs1 = _median_time(make_step(q[s0:e0], k[s0:e0], v[s0:e0], go[s0:e0], sub, n), warmup=1, runs=3)
+    torch.set_num_threads(cores)
     return {"value": t / med, "unit": "edge-tokens/s", "cores": cores, "kind": "port",
-            "sample": (f"oracle fp32 per-graph attention fwd+bwd (torch CPU, {cores} threads) on {len(pick)} graphs "
-                       f"of the batch ({t} tokens, lengths {lens.tolist()}), median of {len(times)} runs; the "
-                       f"batch's throughput on the CPU would be lower (cost grows with the sum of squared lengths)")}
+            "sample": (f"the whole batch ({t} edge tokens, {gb.num_graphs} graphs padded to N = {n}): the reference's "
+                       f"padded path (esa/mha_flash_varlen.py:81-126) restated in oracle.attention.padded_sdpa, "
+                       f"torch scaled_dot_product_attention fp32 forward + autograd backward on {cores} threads, "
+                       f"median of {runs} runs after 2 warm-ups"),
+            "one_thread": {"value": (e0 - s0) / med1, "unit": "edge-tokens/s", "cores": 1,
+                           "sample": f"the median-length graph ({e0 - s0} edge tokens, padded to {n}), median of "
+                                     f"{runs1} runs after 1 warm-up (padding to N makes shorter graphs cost as "
+                                     f"much as the longest, so the batch runs slower per token)"}}
 
 
 def main():
@@ -124,8 +152,14 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
-    {"varlen": bench_varlen, "masked": bench_masked, "gather": bench_gather, "block": bench_block,
-     "stack": bench_stack}[args.config](args)
+    if args.config == "varlen":
+        result = bench_varlen(args)
+        if not args.no_sub:
+            result["masked"] = bench_masked(args, sub=True)
+            result["gather"] = bench_gather(args, sub=True)
+        print(json.dumps(result), flush=True)
+        return
+    {"masked": bench_masked, "gather": bench_gather, "block": bench_block, "stack": bench_stack}[args.config](args)
 
 
 def timed(step, steps: int, warmup: int, profile: bool = True):
@@ -228,8 +262,8 @@ def bench_varlen(args):
                      "unit": "TFLOP/s", "frac": achieved / PEAK_BF16_TFLOPS, "traffic": traffic},
     }
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(gb, args.seed, args.cpu_sample_graphs)
-    print(json.dumps(result), flush=True)
+        result["cpu_baseline"] = cpu_baseline(gb, args.seed)
+    return result
 
 
 def edge_mask_stats(src: np.ndarray, dst: np.ndarray, cu: np.ndarray, tile: int = 32) -> dict:
@@ -257,13 +291,21 @@ def edge_mask_stats(src: np.ndarray, dst: np.ndarray, cu: np.ndarray, tile: int 
 
 
 def cpu_baseline_masked(gb, seed: int, n_graphs: int) -> dict:
-    """Oracle per-graph edge-masked attention fwd+bwd in fp32 on the host cores, bounded sample."""
+    """The reference's masked MAB attention on the host cores, fp32 forward + backward, on a bounded sample.
+
+    The reference adds the edge bias (0 where two edges share a node, else -99999;
+    esa/masked_layers.py:217-268) to the scores of every graph padded to N (esa/mha.py:73-77); on the CPU its
+    attention call is torch's scaled_dot_product_attention with that additive bias (oracle.attention.
+    padded_sdpa with a per-graph pair bias).  The bias of each graph is built per graph (the entries of the
+    global E x E comparison, without its E^2 temporaries).  Sample: graphs spread over the length
+    distribution, padded to the batch's N."""
     import torch
 
     from oracle import attention as oracle_attention
+    from oracle import mask as oracle_mask
+    from oracle.packing import nearest_multiple_of_8
 
     cores = len(os.sched_getaffinity(0))
-    torch.set_num_threads(cores)
     order = np.argsort(gb.edge_counts)
     pick = sorted(set(int(order[int(i)]) for i in np.linspace(0, len(order) - 1, n_graphs)))
     cu_all = gb.cu_seqlens.astype(np.int64)
@@ -272,28 +314,27 @@ def cpu_baseline_masked(gb, seed: int, n_graphs: int) -> dict:
     cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
     src, dst = gb.edge_index[0][idx], gb.edge_index[1][idx]
     t = int(cu[-1])
+    n = nearest_multiple_of_8(gb.max_seqlen + 1)
+    biases = [torch.where(torch.as_tensor(oracle_mask.edge_adjacency_segment(src, dst, int(cu[b]), int(cu[b + 1]))),
+                          0.0, oracle_mask.MASK_FILL) for b in range(len(pick))]
     g = torch.Generator().manual_seed(seed + 99)
     q, k, v, go = (torch.randn(t, HEADS, HEAD_DIM, generator=g) for _ in range(4))
 
     def step():
-        oracle_attention.varlen_attention(q, k, v, cu, cu, 0.25, src, dst, dtype=torch.float32)
-        oracle_attention.varlen_attention_bwd(go, q, k, v, cu, cu, 0.25, src, dst, dtype=torch.float32)
+        qd, kd, vd = (x.detach().requires_grad_(True) for x in (q, k, v))
+        out = oracle_attention.padded_sdpa(qd, kd, vd, cu, cu, n, 1.0 / HEAD_DIM ** 0.5, pair_bias=lambda b: biases[b])
+        out.backward(go)
 
-    step()
-    times = []
-    budget = time.perf_counter() + 12.0
-    while len(times) < 3 or (time.perf_counter() < budget and len(times) < 20):
-        t0 = time.perf_counter()
-        step()
-        times.append(time.perf_counter() - t0)
-    med = float(np.median(times))
+    torch.set_num_threads(cores)
+    med, runs = _median_time(step)
     return {"value": t / med, "unit": "edge-tokens/s", "cores": cores, "kind": "port",
-            "sample": (f"oracle fp32 per-graph edge-masked attention fwd+bwd (torch CPU, {cores} threads; the mask "
-                       f"built per graph from src/dst) on {len(pick)} graphs of the batch ({t} tokens, lengths "
-                       f"{lens.tolist()}), median of {len(times)} runs")}
+            "sample": (f"{len(pick)} graphs of the batch spread over its lengths ({t} edge tokens, lengths "
+                       f"{lens.tolist()}, padded to N = {n}): torch scaled_dot_product_attention fp32 with the "
+                       f"reference's additive edge bias (oracle.attention.padded_sdpa), forward + autograd "
+                       f"backward on {cores} threads, median of {runs} runs after 2 warm-ups")}
 
 
-def bench_masked(args):
+def bench_masked(args, sub: bool = False):
     """Configuration 2: edge-masked attention fwd+bwd on a 65,536-edge-token budget batch.
 
     The timed step is the attention kernels with the on-the-fly edge mask; the
@@ -331,6 +372,20 @@ def bench_masked(args):
     masked = {n + "_masked": f for n, f in FLOPS_PER_PAIR.items()}
     dom = max((n for n in masked if n in per_kernel), key=lambda n: per_kernel[n]["avg_us"])
     achieved = masked[dom] * stats["nnz"] / (per_kernel[dom]["avg_us"] * 1e-6) / 1e12
+    roofline = {"bound": "mfma", "kernel": dom, "achieved": achieved, "peak": PEAK_BF16_TFLOPS,
+                "unit": "TFLOP/s", "frac": achieved / PEAK_BF16_TFLOPS, "traffic": None,
+                "flops": "effective (nnz of the mask)"}
+    if sub:
+        out = {"workload": "config2: edge-masked attention fwd+bwd (mask evaluated from src/dst in the tile loop)",
+               "graphs": gb.num_graphs, "edge_tokens": t, "mask_nnz": stats["nnz"],
+               "mask_density": stats["nnz"] / gb.sum_sq, "tiles_nonempty": stats["tiles_nonempty"],
+               "ms_per_step": ms_per_step, "edge_tokens_per_s": t / (ms_per_step * 1e-3),
+               "achieved_tflops_effective": tflops,
+               "achieved_tflops_executed_tiles": exec_flops / (ms_per_step * 1e-3) / 1e12,
+               "ms_per_step_profiled": ms_prof, "kernels": per_kernel, "roofline": roofline}
+        if not args.no_cpu_baseline:
+            out["cpu_baseline"] = cpu_baseline_masked(gb, args.seed, args.cpu_sample_graphs)
+        return out
 
     # the SAB block on the same batch: padded [B, N, 256] input, EdgeAdjacency mask
     n_max = nearest_multiple_of_8(maxlen)
@@ -376,9 +431,7 @@ def bench_masked(args):
         "achieved_tflops_executed_tiles": exec_flops / (ms_per_step * 1e-3) / 1e12,
         "wall_ms_per_step": wall_ms, "ms_per_step_profiled": ms_prof,
         "kernels": per_kernel,
-        "roofline": {"bound": "mfma", "kernel": dom, "achieved": achieved, "peak": PEAK_BF16_TFLOPS,
-                     "unit": "TFLOP/s", "frac": achieved / PEAK_BF16_TFLOPS, "traffic": None,
-                     "flops": "effective (nnz of the mask)"},
+        "roofline": roofline,
         "sab_block": {"ms_per_step": block_ms, "edge_tokens_per_s": t / (block_ms * 1e-3),
                       "what": "SAB(256, 256, 16 heads, 'hip') fwd+bwd incl. projections, fc_o + mish, padded "
                               f"[{gb.num_graphs}, {n_max}, {DIM}] fp32 input"},
@@ -399,39 +452,42 @@ def gather_bytes(e: int, n: int, f: int, s: int) -> dict:
 
 
 def cpu_baseline_gather(src, dst, seed: int, slice_edges: int) -> dict:
-    """Oracle gather + fp32 sequential segment sum on a dst-sorted slice, scaled to GB/s of algorithmic bytes."""
+    """The reference's gather and edge->node sum on the host cores (torch, fp32) on a dst-sorted slice.
+
+    oracle.edges.edge_gather_torch is the reference's own torch.cat((x[src], x[dst]), 1)
+    (core/pretraining_model.py:153-155) and oracle.edges.scatter_sum_torch its scatter_add
+    (core/molecular_encoder.py:241-242) as index_add_; both run multi-threaded in torch.  The first
+    `slice_edges` dst-sorted edges; GB/s of the same algorithmic bytes, so the full-size time scales
+    linearly."""
+    import torch
+
     from oracle import edges as oracle_edges
 
-    rng = np.random.default_rng(seed + 7)
-    lo = int(dst[0])
-    s, d = src[:slice_edges].astype(np.int64), dst[:slice_edges].astype(np.int64)
-    hi = int(d[-1]) + 1
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    g = torch.Generator().manual_seed(seed + 7)
+    s = torch.as_tensor(src[:slice_edges].astype(np.int64))
+    d = torch.as_tensor(dst[:slice_edges].astype(np.int64))
+    lo, hi = int(d[0]), int(d[-1]) + 1
     nodes = hi - lo
-    x = rng.standard_normal((int(max(s.max(), d.max())) + 1, GATHER_F), dtype=np.float32)
-    y = rng.standard_normal((slice_edges, GATHER_F), dtype=np.float32)
-    indptr = np.concatenate([[0], np.cumsum(np.bincount(d - lo, minlength=nodes))])
-    bytes_ = gather_bytes(slice_edges, nodes, GATHER_F, 4)
-    total = bytes_["edge_gather"] + bytes_["segment_sum"]
+    x = torch.randn(int(max(int(s.max()), int(d.max()))) + 1, GATHER_F, generator=g)
+    y = torch.randn(slice_edges, GATHER_F, generator=g)
+    dl = d - lo
+    by = gather_bytes(slice_edges, nodes, GATHER_F, 4)
+    total = by["edge_gather"] + by["segment_sum"]
 
     def step():
-        oracle_edges.edge_gather(x, s, d)
-        oracle_edges.segment_sum_sequential(y, None, indptr)
+        oracle_edges.edge_gather_torch(x, s, d)
+        oracle_edges.scatter_sum_torch(y, dl, nodes)
 
-    step()
-    times = []
-    budget = time.perf_counter() + 12.0
-    while len(times) < 3 or (time.perf_counter() < budget and len(times) < 10):
-        t0 = time.perf_counter()
-        step()
-        times.append(time.perf_counter() - t0)
-    med = float(np.median(times))
-    return {"value": total / med / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": (f"oracle numpy gather [x[src] || x[dst]] + fp32 sequential CSR segment sum (single thread) on "
-                       f"the first {slice_edges} dst-sorted edges ({nodes} nodes), fp32, median of {len(times)} runs; "
-                       f"GB/s of the same algorithmic bytes, so the full-size time scales linearly")}
+    med, runs = _median_time(step)
+    return {"value": total / med / 1e9, "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": (f"torch.cat((x[src], x[dst]), 1) + index_add_ by dst (the reference's expressions, "
+                       f"oracle.edges.*_torch) on the first {slice_edges} dst-sorted edges ({nodes} nodes), fp32, "
+                       f"{cores} threads, median of {runs} runs after 2 warm-ups; GB/s of the same algorithmic bytes")}
 
 
-def bench_gather(args):
+def bench_gather(args, sub: bool = False):
     """Configuration 3: edge-token gather and CSR segment sum at 2^21 nodes x 2^25 edges x 256 features."""
     import torch
 
@@ -499,9 +555,6 @@ def bench_gather(args):
     del a, b
     torch.cuda.empty_cache()
 
-    fused = bench_fused_projection(x_dtype=torch.float32, src=src, dst=dst, steps=max(3, args.steps // 2),
-                                   warmup=2, seed=args.seed)
-
     f32 = results["f32"]
     dom = max(("edge_gather", "segment_sum"), key=lambda n: f32["kernels"][n]["avg_us"])
     achieved = f32["kernels"][dom]["achieved_gbs"]
@@ -509,6 +562,23 @@ def bench_gather(args):
     tfile = ROOT / "profiles" / f"{dom}_config3_traffic.json"
     if tfile.exists():
         traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
+    roofline = {"bound": "hbm", "kernel": dom, "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": achieved / PEAK_HBM_GBS, "traffic": traffic}
+    hbm_frac = {f"{name}.{k}": v["achieved_gbs"] / PEAK_HBM_GBS
+                for name in ("f32", "bf16") for k, v in results[name]["kernels"].items() if "achieved_gbs" in v}
+    if sub:
+        out = {"workload": "config3: edge gather [x[src] || x[dst]] + deterministic CSR segment sum to dst",
+               "nodes": GATHER_N, "edges": GATHER_E, "features": GATHER_F, "order": "dst-sorted (CSR)",
+               "ms_per_step_f32": f32["ms_per_step"], "gb_per_s_f32": f32["gb_per_s"],
+               "ms_per_step_bf16": results["bf16"]["ms_per_step"], "gb_per_s_bf16": results["bf16"]["gb_per_s"],
+               "kernels_f32": f32["kernels"], "kernels_bf16": results["bf16"]["kernels"],
+               "hbm_frac": hbm_frac, "csr_build_ms": csr_ms, "reference_copy_gbs": copy_gbs,
+               "roofline": roofline}
+        if not args.no_cpu_baseline:
+            out["cpu_baseline"] = cpu_baseline_gather(src.cpu().numpy(), dst.cpu().numpy(), args.seed, 1 << 21)
+        return out
+    fused = bench_fused_projection(x_dtype=torch.float32, src=src, dst=dst, steps=max(3, args.steps // 2),
+                                   warmup=2, seed=args.seed)
     result = {
         "metric": "GB/s of algorithmic HBM bytes through edge gather + CSR segment sum",
         "value": f32["gb_per_s"],
@@ -532,11 +602,11 @@ def bench_gather(args):
         "fused_projection": fused,
         "f32": f32,
         "bf16": results["bf16"],
-        "roofline": {"bound": "hbm", "kernel": dom, "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": achieved / PEAK_HBM_GBS, "traffic": traffic},
+        "hbm_frac": hbm_frac,
+        "roofline": roofline,
     }
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline_gather(src.cpu().numpy(), dst.cpu().numpy(), args.seed, 1 << 18)
+        result["cpu_baseline"] = cpu_baseline_gather(src.cpu().numpy(), dst.cpu().numpy(), args.seed, 1 << 21)
     print(json.dumps(result), flush=True)
 
 
@@ -678,33 +748,20 @@ def cpu_baseline_block(gb, types, emb, proj, model, heads) -> dict:
             s, e = int(cu[b]), int(cu[b + 1])
             blk = OM.edge_adjacency_segment(gb.edge_index[0], gb.edge_index[1], s, e)
             bias[b, 0, : e - s, : e - s][torch.as_tensor(blk)] = 0.0
-        h = OMod.sab_complete(sd, "encoder.0.", X, heads, lambda s_, p_, x_: OMod.mab_padded(s_, p_, x_, x_, heads,
-                                                                                               bias), 2)
-        h = OMod.sab_complete(sd, "encoder.1.", h, heads, lambda s_, p_, x_: OMod.mab_padded(s_, p_, x_, x_, heads),
-                              2)
-        enc = h + X
-        hn = OMod.layer_norm(sd, "decoder.0.norm.ln.", enc)
-        S = OMod._p(sd, "decoder.0.pma.", "S").repeat(gb.num_graphs, 1, 1)
-        pooled = OMod.mab_padded(sd, "decoder.0.pma.mab.", S, hn, heads)
-        pooled = pooled + OMod.mlp_standard(sd, "decoder.0.mlp.", OMod.layer_norm(sd, "decoder.0.norm_mlp.ln.",
-                                                                                  pooled), 2)
-        OMod.mish(OMod.linear(sd, "decoder_linear.", pooled.mean(1)))
+        OMod.esa(sd, X, "MSP", heads, 2,
+                 attn_m=lambda s_, p_, x_: OMod.mab_padded(s_, p_, x_, x_, heads, bias),
+                 attn_s=lambda s_, p_, x_: OMod.mab_padded(s_, p_, x_, x_, heads),
+                 pool=lambda s_, p_, x_: OMod.pma_complete(s_, p_, x_, heads, 2))
 
     try:
-        step()
-        times = []
-        budget = time.perf_counter() + 15.0
-        while len(times) < 3 or (time.perf_counter() < budget and len(times) < 10):
-            t0 = time.perf_counter()
-            step()
-            times.append(time.perf_counter() - t0)
+        med, runs = _median_time(step)
     finally:
         OMod.DT = torch.float64
-    med = float(np.median(times))
     return {"value": gb.num_tokens / med, "unit": "edge-tokens/s", "cores": cores, "kind": "port",
             "sample": (f"the whole config-0 batch ({gb.num_tokens} edge tokens, {gb.num_graphs} graphs) through the "
                        f"oracle's fp32 restatement of the reference's padded path (torch CPU, {cores} threads: "
-                       f"embedding, gather, per-graph edge bias, M + S + PMA blocks), median of {len(times)} runs")}
+                       f"embedding, gather, per-graph edge bias, M + S + PMA blocks), median of {runs} runs after "
+                       f"2 warm-ups")}
 
 
 def bench_stack(args):

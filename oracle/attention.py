@@ -12,6 +12,7 @@ from __future__ import annotations
 
 import numpy as np
 import torch
+import torch.nn.functional as F
 
 from .mask import edge_adjacency_segment, node_adjacency_segment
 
@@ -165,6 +166,38 @@ def varlen_attention_diff(q, k, v, cu_q, cu_k, scale, edge_src=None, edge_dst=No
     if edge_src is not None or adj is not None:
         return masked_attention_pairs(q, k, v, cu_q, cu_k, scale, edge_src, edge_dst, adj)
     return _VarlenAttentionFn.apply(q, k, v, cu_q, cu_k, scale, edge_src, edge_dst, adj)
+
+
+def padded_sdpa(q, k, v, cu_q, cu_k, n, scale, pair_bias=None, graphs_per_call=4):
+    """The reference's padded fallback on the CPU: MABFlashVarlen._forward_padded (esa/mha_flash_varlen.py:
+    81-126) pads every set to ``n`` positions, [B, H, n, D], and calls torch's
+    scaled_dot_product_attention with the key-padding mask (:112-117) -- here a few sets per call, which
+    changes nothing per set.  ``pair_bias(b)`` may give set b's additive [Lq, Lk] bias (the masked layers'
+    0 / -99999 bias of esa/mha.py:73-77).  Returns the valid query rows [Tq, H, D] (differentiable in q, k,
+    v); padded query rows are computed and dropped, as the reference's unpad does."""
+    cu_q = np.asarray(cu_q, dtype=np.int64)
+    cu_k = np.asarray(cu_k, dtype=np.int64)
+    tq, h, d = q.shape
+    outs = []
+    for b0 in range(0, len(cu_q) - 1, graphs_per_call):
+        bb = list(range(b0, min(b0 + graphs_per_call, len(cu_q) - 1)))
+        qp = q.new_zeros(len(bb), h, n, d)
+        kp = k.new_zeros(len(bb), h, n, d)
+        vp = v.new_zeros(len(bb), h, n, d)
+        mask = torch.full((len(bb), 1, n, n), float("-inf"), dtype=q.dtype)
+        for j, b in enumerate(bb):
+            lq, lk = int(cu_q[b + 1] - cu_q[b]), int(cu_k[b + 1] - cu_k[b])
+            qp[j, :, :lq] = q[cu_q[b]:cu_q[b + 1]].transpose(0, 1)
+            kp[j, :, :lk] = k[cu_k[b]:cu_k[b + 1]].transpose(0, 1)
+            vp[j, :, :lk] = v[cu_k[b]:cu_k[b + 1]].transpose(0, 1)
+            mask[j, 0, :, :lk] = 0.0
+            if pair_bias is not None:
+                mask[j, 0, :lq, :lk] = pair_bias(b).to(q.dtype)
+            mask[j, 0, lq:, :] = 0.0     # padded query rows: any finite row (dropped below)
+        o = F.scaled_dot_product_attention(qp, kp, vp, attn_mask=mask, scale=scale)
+        for j, b in enumerate(bb):
+            outs.append(o[j, :, : int(cu_q[b + 1] - cu_q[b])].transpose(0, 1))
+    return torch.cat(outs, 0) if outs else q.new_zeros(0, h, d)
 
 
 def padded_attention(q, k, v, scale, bias=None, dtype=torch.float64):

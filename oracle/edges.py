@@ -2,6 +2,7 @@
 from __future__ import annotations
 
 import numpy as np
+import torch
 
 
 def edge_gather(x: np.ndarray, src: np.ndarray, dst: np.ndarray) -> np.ndarray:
@@ -59,3 +60,15 @@ def segment_sum_f64(y: np.ndarray, keys: np.ndarray, num_nodes: int) -> np.ndarr
     out = np.zeros((num_nodes,) + y.shape[1:], dtype=np.float64)
     np.add.at(out, np.asarray(keys, dtype=np.int64), y.astype(np.float64))
     return out
+
+
+def edge_gather_torch(x: torch.Tensor, src: torch.Tensor, dst: torch.Tensor) -> torch.Tensor:
+    """The reference's own expression on torch tensors, torch.cat((x[src], x[dst]), 1)
+    (core/pretraining_model.py:153-155): the CPU baseline of the gather (multi-threaded in torch)."""
+    return torch.cat((x[src], x[dst]), 1)
+
+
+def scatter_sum_torch(y: torch.Tensor, index: torch.Tensor, num_nodes: int) -> torch.Tensor:
+    """scatter_add of edge rows to nodes (core/molecular_encoder.py:241-242) as torch's index_add_ on the
+    CPU: the CPU baseline of the segment sum."""
+    return y.new_zeros((num_nodes,) + tuple(y.shape[1:])).index_add_(0, index, y)

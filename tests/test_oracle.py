@@ -668,3 +668,47 @@ def test_token_budget_batches_is_the_greedy_partition(counts, budget):
         assert s <= budget or len(b) == 1
         if j + 1 < len(batches):
             assert s + counts[batches[j + 1][0]] > budget
+
+
+def test_padded_sdpa_equals_varlen_on_valid_rows():
+    """The reference's padded fallback (torch SDPA over [B, H, N, D] with the key-padding mask) equals the
+    per-set attention on every valid query row, forward and backward; with a pair bias it equals the masked
+    attention (the edge mask's 0 / -99999 bias)."""
+    lens = [5, 12, 1, 9]
+    cu = OP.cu_seqlens(lens)
+    t, h, d = int(cu[-1]), 2, 16
+    g = torch.Generator().manual_seed(6)
+    q, k, v, go = (torch.randn(t, h, d, dtype=torch.float64, generator=g) for _ in range(4))
+    qd, kd, vd = (x.clone().requires_grad_(True) for x in (q, k, v))
+    out = OA.padded_sdpa(qd, kd, vd, cu, cu, 16, 0.3, graphs_per_call=3)
+    ref, _ = OA.varlen_attention(q, k, v, cu, cu, 0.3)
+    assert torch.allclose(out, ref, atol=1e-12)
+    out.backward(go)
+    rdq, rdk, rdv = OA.varlen_attention_bwd(go, q, k, v, cu, cu, 0.3)
+    for a, b in ((qd.grad, rdq), (kd.grad, rdk), (vd.grad, rdv)):
+        assert torch.allclose(a, b, atol=1e-11)
+    gb, _ = generators.small_molecules(seed=2, num_graphs=3)
+    cu2 = gb.cu_seqlens
+    src, dst = gb.edge_index
+    t2 = int(cu2[-1])
+    q2, k2, v2 = (torch.randn(t2, h, d, dtype=torch.float64, generator=g) for _ in range(3))
+
+    def bias(b):
+        s_, e_ = int(cu2[b]), int(cu2[b + 1])
+        m = torch.as_tensor(OM.edge_adjacency_segment(src, dst, s_, e_))
+        return torch.where(m, 0.0, OM.MASK_FILL)
+
+    out2 = OA.padded_sdpa(q2, k2, v2, cu2, cu2, int(np.diff(cu2).max()), 0.25, pair_bias=bias)
+    ref2, _ = OA.varlen_attention(q2, k2, v2, cu2, cu2, 0.25, src, dst)
+    assert torch.allclose(out2, ref2, atol=1e-10)
+
+
+def test_torch_gather_and_scatter_baselines_match_the_oracle():
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((50, 6)).astype(np.float32)
+    src, dst = rng.integers(0, 50, 300), rng.integers(0, 50, 300)
+    h = OE.edge_gather_torch(torch.as_tensor(x), torch.as_tensor(src), torch.as_tensor(dst))
+    assert np.array_equal(h.numpy(), OE.edge_gather(x, src, dst))
+    y = rng.standard_normal((300, 6))
+    assert np.allclose(OE.scatter_sum_torch(torch.as_tensor(y), torch.as_tensor(dst), 50).numpy(),
+                       OE.segment_sum_f64(y, dst, 50), atol=1e-12)
