@@ -54,10 +54,10 @@ __global__ __launch_bounds__(256) void edge_gather_kernel(const u32x4* __restric
 // (hardware block b runs on XCD b % 8) walks one contiguous range of edges,
 // so the node rows an edge range touches stay in that XCD's L2.
 #ifndef ESA_GATHER_LOADS
-#define ESA_GATHER_LOADS 16   // 16-byte loads in flight per lane per step
+#define ESA_GATHER_LOADS 32   // 16-byte loads in flight per lane per step
 #endif
-#ifndef ESA_GATHER_EPW
-#define ESA_GATHER_EPW 32     // edges per wave
+#ifndef ESA_GATHER_STEPS
+#define ESA_GATHER_STEPS 1    // steps per wave (a wave moves ESA_GATHER_LOADS / P edges per step)
 #endif
 
 template <int P>
@@ -640,6 +640,12 @@ __global__ __launch_bounds__(256) void segment_sum_rows_kernel(const T* __restri
 #ifndef ESA_STREAM_NODES
 #define ESA_STREAM_NODES 32   // nodes per wave (at most 63)
 #endif
+#ifndef ESA_NODE_MODE
+#define ESA_NODE_MODE 1       // canonical-order CSRs of 512 / 1024-byte rows: the node-per-wave kernel
+#endif
+#ifndef ESA_STREAM_NTSTORE
+#define ESA_STREAM_NTSTORE 0  // nontemporal stores of the node sums
+#endif
 constexpr int kStreamNodes = ESA_STREAM_NODES;
 
 template <int VB> struct StreamU { static constexpr int value = ESA_STREAM_BYTES / VB; };
@@ -685,7 +691,11 @@ __global__ __launch_bounds__(256) void segment_sum_stream_kernel(const T* __rest
     V o;
 #pragma unroll
     for (int c = 0; c < N; ++c) { o[c] = (T)acc[c]; acc[c] = 0.f; }
+#if ESA_STREAM_NTSTORE
+    __builtin_nontemporal_store(o, reinterpret_cast<V*>(out + (size_t)(n0 + k) * F + col));
+#else
     *reinterpret_cast<V*>(out + (size_t)(n0 + k) * F + col) = o;
+#endif
     ++k;
     b = __builtin_amdgcn_readlane(ip, min(k + 1, nn));
   };
@@ -712,6 +722,62 @@ __global__ __launch_bounds__(256) void segment_sum_stream_kernel(const T* __rest
     i += kStreamU;
   }
   while (k < nn) flush();
+}
+
+// Node mode for one CSR in canonical order (no perm) whose rows are 512 or
+// 1024 bytes: NPW nodes per wave, 64 / NPW lanes per node, 16 bytes of every
+// row per lane.  Each step has up to U rows of a node in flight (nontemporal
+// loads, issued only for the node's own rows), then adds them in ascending
+// position, so every lane keeps the fp32 left-to-right sum of its columns.
+// A wave lives for its nodes only; occupancy hides the load latency (the
+// access pattern of a plain streaming read, which reaches about 7 TB/s).
+#ifndef ESA_NODE_U_F32
+#define ESA_NODE_U_F32 32   // rows in flight per node and step, fp32 rows
+#endif
+#ifndef ESA_NODE_U_BF16
+#define ESA_NODE_U_BF16 8   // bf16 rows (their conversions and the two nodes per wave cost registers)
+#endif
+template <typename T, int NPW, int U>
+__global__ __launch_bounds__(256) void segment_sum_node_kernel(const T* __restrict__ y, const int* __restrict__ indptr,
+                                                               int num_nodes, T* __restrict__ out) {
+  constexpr int LPN = 64 / NPW;            // lanes per node
+  constexpr int E = 16 / (int)sizeof(T);   // elements per lane per row
+  constexpr int F = LPN * E;               // row elements
+  const int lane = threadIdx.x & 63;
+  const long n = ((long)blockIdx.x * 4 + (threadIdx.x >> 6)) * NPW + lane / LPN;
+  const int l = lane % LPN;
+  const bool valid = n < num_nodes;
+  const int a = valid ? indptr[n] : 0, b = valid ? indptr[n + 1] : 0;
+  float acc[E];
+#pragma unroll
+  for (int k = 0; k < E; ++k) acc[k] = 0.f;
+  const u32x4* row0 = reinterpret_cast<const u32x4*>(y) + l;
+  for (int i = a; __ballot(i < b); i += U) {
+    u32x4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (i + u < b) v[u] = __builtin_nontemporal_load(row0 + (size_t)(i + u) * (F * sizeof(T) / 16));
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (i + u < b) {
+        if constexpr (sizeof(T) == 4) {
+          const f32x4 f = __builtin_bit_cast(f32x4, v[u]);
+#pragma unroll
+          for (int k = 0; k < 4; ++k) acc[k] += f[k];
+        } else {
+          const bf16x8 h = __builtin_bit_cast(bf16x8, v[u]);
+#pragma unroll
+          for (int k = 0; k < 8; ++k) acc[k] += (float)h[k];
+        }
+      }
+    }
+  }
+  if (!valid) return;
+  typedef T VE __attribute__((ext_vector_type(E)));
+  VE o;
+#pragma unroll
+  for (int k = 0; k < E; ++k) o[k] = (T)acc[k];
+  __builtin_nontemporal_store(o, reinterpret_cast<VE*>(out + (size_t)n * F) + l);
 }
 
 // Element-wise fallback for feature counts that are not a multiple of 16 bytes.
@@ -790,7 +856,22 @@ int launch_segsum(const T* y, long ld, const int* perm1, const int* indptr1, int
   const long row_bytes = (long)features * (long)sizeof(T);
   const bool rows_ok = !misaligned16(y) && !misaligned16(out) && (ld * (long)sizeof(T)) % 16 == 0 &&
                        (off1 * (long)sizeof(T)) % 16 == 0 && (off2 * (long)sizeof(T)) % 16 == 0;
-  if (rows_ok && !perm2 && !indptr2 && off1 == 0 && ld == features && (row_bytes == 64 * 16 || row_bytes == 64 * 8)) {
+  if (ESA_NODE_MODE && rows_ok && !perm1 && !perm2 && !indptr2 && off1 == 0 && ld == features &&
+      (row_bytes == 64 * 16 || row_bytes == 32 * 16)) {
+    constexpr int U = sizeof(T) == 4 ? ESA_NODE_U_F32 : ESA_NODE_U_BF16;
+    if (row_bytes == 64 * 16) {
+      const unsigned blocks = (unsigned)(((long)num_nodes + 3) / 4);
+      ESA_TIMED(esa_profile::kSegmentSum, st,
+                hipLaunchKernelGGL((segment_sum_node_kernel<T, 1, U>), dim3(blocks), dim3(256), 0, st, y, indptr1,
+                                   num_nodes, out));
+    } else {
+      const unsigned blocks = (unsigned)(((long)num_nodes + 7) / 8);
+      ESA_TIMED(esa_profile::kSegmentSum, st,
+                hipLaunchKernelGGL((segment_sum_node_kernel<T, 2, U>), dim3(blocks), dim3(256), 0, st, y, indptr1,
+                                   num_nodes, out));
+    }
+  } else if (rows_ok && !perm2 && !indptr2 && off1 == 0 && ld == features &&
+             (row_bytes == 64 * 16 || row_bytes == 64 * 8)) {
     const long waves = ((long)num_nodes + kStreamNodes - 1) / kStreamNodes;
     const unsigned blocks = (unsigned)((waves + 3) / 4);
     if (row_bytes == 64 * 16)
@@ -842,8 +923,9 @@ int esa_edge_gather(const void* x, const int* src, const int* dst, int64_t num_e
   const int pieces = row_bytes % 16 == 0 ? 2 * row_chunks / 64 : 0;
   if (row_bytes % 512 == 0 && !misaligned16(x) && !misaligned16(out) && x_bytes <= (1L << 31) &&
       (pieces == 1 || pieces == 2 || pieces == 4)) {
-    // Row mode: 32 edges per wave, a multiple of 8 blocks (one share per XCD).
-    const int epw = ESA_GATHER_EPW;
+    // Row mode: one step (all of a wave's gather loads in flight at once) per wave, a multiple of 8 blocks
+    // (one share per XCD).
+    const int epw = ESA_GATHER_LOADS / pieces * ESA_GATHER_STEPS;
     const long waves = (num_edges + epw - 1) / epw;
     const long blocks8 = ((waves + 3) / 4 + 7) / 8 * 8;
     const int per_xcd = (int)(blocks8 / 8);
