@@ -10,6 +10,7 @@ reference's edge->node reductions (core/molecular_encoder.py:241-242).
 from __future__ import annotations
 
 import ctypes
+from typing import Optional
 
 import torch
 
@@ -108,13 +109,47 @@ def _gather_bwd_raw(g: torch.Tensor, src_csr: CSR, dst_csr: CSR, num_nodes: int,
     return gx
 
 
+# ---- torch.library registration of the gather / CSR entry points (torch.ops.esa_hip.*), with fake (shape)
+# implementations for torch.compile / export.
+
+@torch.library.custom_op("esa_hip::edge_gather", mutates_args=())
+def _op_edge_gather(x: torch.Tensor, src: torch.Tensor, dst: torch.Tensor) -> torch.Tensor:
+    return _gather_raw(x, src, dst)
+
+
+@_op_edge_gather.register_fake
+def _(x, src, dst):
+    return x.new_empty((src.shape[0], 2 * x.shape[1]))
+
+
+@torch.library.custom_op("esa_hip::csr_segment_sum", mutates_args=())
+def _op_segment_sum(y: torch.Tensor, indptr: torch.Tensor, perm: Optional[torch.Tensor]) -> torch.Tensor:
+    return segment_sum_csr(y, indptr, perm)
+
+
+@_op_segment_sum.register_fake
+def _(y, indptr, perm):
+    return y.new_empty((indptr.shape[0] - 1, y.shape[1]))
+
+
+@torch.library.custom_op("esa_hip::csr_build", mutates_args=())
+def _op_csr_build(keys: torch.Tensor, num_nodes: int) -> tuple[torch.Tensor, torch.Tensor]:
+    c = CSR.build(keys, num_nodes)
+    return c.indptr, c.perm
+
+
+@_op_csr_build.register_fake
+def _(keys, num_nodes):
+    return keys.new_empty((num_nodes + 1,), dtype=torch.int32), keys.new_empty((keys.shape[0],), dtype=torch.int32)
+
+
 class _EdgeGather(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, src, dst, src_csr, dst_csr):
         ctx.save_for_backward(src, dst)
         ctx.csrs = (src_csr, dst_csr)
         ctx.shape = x.shape
-        return _gather_raw(x, src, dst)
+        return torch.ops.esa_hip.edge_gather(x, src, dst)
 
     @staticmethod
     def backward(ctx, g):

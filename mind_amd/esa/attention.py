@@ -11,6 +11,7 @@ bf16 (MFMA kernels, fp32 softmax) or float32 (fp32 throughout) with int32
 from __future__ import annotations
 
 import math
+from typing import Optional
 
 import torch
 
@@ -158,22 +159,58 @@ def attn_bwd(dout, q, k, v, out, lse, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, 
     return dq, dk, dv
 
 
-class _VarlenAttention(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, q, k, v, cu_q, cu_k, max_q, max_k, scale, edge_src, edge_dst, adj_indptr, adj_indices):
-        out, lse = attn_fwd(q, k, v, cu_q, cu_k, max_q, max_k, scale, edge_src, edge_dst, adj_indptr, adj_indices)
-        ctx.save_for_backward(q, k, v, out, lse, cu_q, cu_k, edge_src, edge_dst, adj_indptr, adj_indices)
-        ctx.meta = (max_q, max_k, scale)
-        ctx.mark_non_differentiable(lse)
-        return out, lse
+# ---- torch.library registration: the C-ABI entry points as torch operators (torch.ops.esa_hip.*), with
+# fake (shape) implementations, so torch.compile / export see them as opaque ops, and autograd on the
+# forward op.
 
-    @staticmethod
-    def backward(ctx, dout, _dlse):
-        q, k, v, out, lse, cu_q, cu_k, edge_src, edge_dst, adj_indptr, adj_indices = ctx.saved_tensors
-        max_q, max_k, scale = ctx.meta
-        dq, dk, dv = attn_bwd(dout.contiguous(), q, k, v, out, lse, cu_q, cu_k, max_q, max_k, scale,
-                              edge_src, edge_dst, adj_indptr, adj_indices)
-        return dq, dk, dv, None, None, None, None, None, None, None, None, None
+@torch.library.custom_op("esa_hip::varlen_attn_fwd", mutates_args=())
+def _op_varlen_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens_q: torch.Tensor,
+                   cu_seqlens_k: torch.Tensor, max_seqlen_q: int, max_seqlen_k: int, softmax_scale: float,
+                   edge_src: Optional[torch.Tensor], edge_dst: Optional[torch.Tensor],
+                   adj_indptr: Optional[torch.Tensor],
+                   adj_indices: Optional[torch.Tensor]) -> tuple[torch.Tensor, torch.Tensor]:
+    return attn_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale, edge_src,
+                    edge_dst, adj_indptr, adj_indices)
+
+
+@_op_varlen_fwd.register_fake
+def _(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale, edge_src, edge_dst,
+      adj_indptr, adj_indices):
+    return torch.empty_like(q), q.new_empty((q.shape[1], q.shape[0]), dtype=torch.float32)
+
+
+@torch.library.custom_op("esa_hip::varlen_attn_bwd", mutates_args=())
+def _op_varlen_bwd(dout: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: torch.Tensor,
+                   lse: torch.Tensor, cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor, max_seqlen_q: int,
+                   max_seqlen_k: int, softmax_scale: float, edge_src: Optional[torch.Tensor],
+                   edge_dst: Optional[torch.Tensor], adj_indptr: Optional[torch.Tensor],
+                   adj_indices: Optional[torch.Tensor]) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    return attn_bwd(dout, q, k, v, out, lse, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale,
+                    edge_src, edge_dst, adj_indptr, adj_indices)
+
+
+@_op_varlen_bwd.register_fake
+def _(dout, q, k, v, out, lse, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale, edge_src,
+      edge_dst, adj_indptr, adj_indices):
+    return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+
+
+def _varlen_setup(ctx, inputs, output):
+    q, k, v, cu_q, cu_k, max_q, max_k, scale, edge_src, edge_dst, adj_indptr, adj_indices = inputs
+    out, lse = output
+    ctx.save_for_backward(q, k, v, out, lse, cu_q, cu_k, edge_src, edge_dst, adj_indptr, adj_indices)
+    ctx.meta = (max_q, max_k, scale)
+
+
+def _varlen_backward(ctx, dout, _dlse):
+    q, k, v, out, lse, cu_q, cu_k, edge_src, edge_dst, adj_indptr, adj_indices = ctx.saved_tensors
+    max_q, max_k, scale = ctx.meta
+    dq, dk, dv = torch.ops.esa_hip.varlen_attn_bwd(dout.contiguous(), q, k, v, out, lse, cu_q, cu_k, max_q, max_k,
+                                                   scale, edge_src, edge_dst, adj_indptr, adj_indices)
+    return dq, dk, dv, None, None, None, None, None, None, None, None, None
+
+
+torch.library.register_autograd("esa_hip::varlen_attn_fwd", _varlen_backward, setup_context=_varlen_setup)
 
 
 def varlen_attention(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, dropout_p=0.0,
@@ -202,8 +239,9 @@ def varlen_attention(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seql
         raise ValueError("edge_src and edge_dst must be given together")
     if (adj_indptr is None) != (adj_indices is None):
         raise ValueError("adj_indptr and adj_indices must be given together")
-    out, lse = _VarlenAttention.apply(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
-                                      float(softmax_scale), edge_src, edge_dst, adj_indptr, adj_indices)
+    out, lse = torch.ops.esa_hip.varlen_attn_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, int(max_seqlen_q),
+                                                 int(max_seqlen_k), float(softmax_scale), edge_src, edge_dst,
+                                                 adj_indptr, adj_indices)
     return (out, lse) if return_lse else out
 
 

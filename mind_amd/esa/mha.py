@@ -11,7 +11,7 @@ state_dicts load.  Attention semantics by ``adj_mask``:
                   evaluated on the fly in the kernel (no [B, 1, N, N] bias).
   NodeAdjacency   the node-mode mask of esa/masked_layers.py:79-118 (query
                   src attends to key dst per edge) as a CSR adjacency.
-                  For either mask ``xformers_or_torch_attn`` picks the semantics:
+                  For either descriptor ``xformers_or_torch_attn`` picks the semantics:
                     "hip"                 packed valid tokens only; a query with
                                           no admissible key gets 0;
                     "xformers" / "torch"  the reference's padded semantics
@@ -24,9 +24,18 @@ state_dicts load.  Attention semantics by ``adj_mask``:
                                           inverted bool mask, esa/masked_layers.py:
                                           264-265, is a reference defect and is
                                           not reproduced.)
+  a tensor        the reference's own mask tensors: an additive float bias
+                  [B, 1 | H, Nq, Nk] of 0 (attend) and -99999 (or any value
+                  <= -1e4), as get_adj_mask_from_edge_index_* build it for
+                  memory_efficient_attention (esa/mha.py:70-77), or a bool mask
+                  (True = attend) as SDPA takes it (:79-84).  It becomes a CSR
+                  adjacency over the padded [B * N] tokens (the node-mode
+                  kernels); a row with no admissible key softmaxes over all Nk
+                  keys, as the -99999 bias does.  Other bias values (a general
+                  additive bias) and masks that differ between heads raise.
 
-Attention is computed in bf16 with fp32 softmax statistics, as the reference's
-bf16-mixed training does; outputs return in the input's dtype.
+float32 inputs run the fp32 kernels; any other dtype runs the bf16 kernels with
+fp32 softmax statistics, as the reference's bf16-mixed training does.
 """
 from __future__ import annotations
 
@@ -81,6 +90,56 @@ def masked_attention(q, k, v, heads, mask: PackedSets, packed: bool):
     return torch.where(dead, out_d, out_m).reshape(b, n, d)
 
 
+MASK_THRESHOLD = -1.0e4   # additive bias at or below this drops the pair (exp underflows to 0 in fp32)
+
+
+def tensor_mask_csr(mask: torch.Tensor, b: int, nq: int, nk: int, heads: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """The reference's dense mask tensor as a CSR adjacency over padded tokens: (indptr [B*Nq + 1], indices
+    [nnz]) with key token b * Nk + j listed for query b * Nq + i when the pair may attend.
+
+    ``mask``: float bias (0 keeps, <= -1e4 drops) or bool (True keeps), shape broadcastable to
+    [B, H, Nq, Nk] with one pattern for all heads (the reference's [B, 1, N, N] expanded over heads,
+    esa/mha.py:73).  Synchronises with the host (the nonzero count sizes the CSR).
+    """
+    if mask.dim() == 3:
+        mask = mask.unsqueeze(1)
+    if mask.dim() != 4 or mask.shape[0] != b or tuple(mask.shape[2:]) != (nq, nk) or mask.shape[1] not in (1, heads):
+        raise ValueError(f"mask of shape {tuple(mask.shape)} does not match [B={b}, 1 or H={heads}, {nq}, {nk}]")
+    if mask.dtype == torch.bool:
+        keep = mask
+    elif mask.is_floating_point():
+        general = (mask != 0) & (mask > MASK_THRESHOLD)
+        if bool(general.any()):
+            raise NotImplementedError("only masking biases are supported: 0 (attend) or <= -1e4 (drop), as "
+                                      "get_adj_mask_from_edge_index_* build them; a general additive bias is not")
+        keep = mask == 0
+    else:
+        raise TypeError(f"a mask tensor must be bool or floating point (got {mask.dtype})")
+    if keep.shape[1] > 1 and not bool((keep == keep[:, :1]).all()):
+        raise NotImplementedError("masks that differ between heads are not supported")
+    nz = keep[:, 0].nonzero()
+    rows = nz[:, 0] * nq + nz[:, 1]
+    indices = (nz[:, 0] * nk + nz[:, 2]).to(torch.int32).contiguous()
+    bounds = torch.arange(b * nq + 1, device=mask.device, dtype=rows.dtype)
+    indptr = torch.searchsorted(rows.contiguous(), bounds).to(torch.int32)
+    return indptr, indices
+
+
+def tensor_masked_attention(q, k, v, heads, mask: torch.Tensor):
+    """Attention over [B, N, D] inputs with the reference's dense mask tensor (padded semantics: a row whose
+    pairs are all dropped attends to all Nk keys, as a constant -99999 bias leaves softmax unchanged)."""
+    b, nq, d = q.shape
+    nk = k.shape[1]
+    indptr, indices = tensor_mask_csr(mask.to(q.device), b, nq, nk, heads)
+    cu_q, cu_k = _uniform_cu(b, nq, q.device), _uniform_cu(b, nk, q.device)
+    qh, kh, vh = _heads(q, heads), _heads(k, heads), _heads(v, heads)
+    out_m, lse = varlen_attention(qh, kh, vh, cu_q, cu_k, nq, nk, return_lse=True, adj_indptr=indptr,
+                                  adj_indices=indices)
+    out_d = varlen_attention(qh, kh, vh, cu_q, cu_k, nq, nk)
+    dead = torch.isneginf(lse[0]).view(-1, 1, 1)   # one pattern for every head
+    return torch.where(dead, out_d, out_m).reshape(b, nq, d)
+
+
 class MAB(nn.Module):
     """Multihead attention block (esa/mha.py:9-89): out = O + mish(fc_o(O)), V = fc_v(K)."""
 
@@ -113,9 +172,10 @@ class MAB(nn.Module):
             out = dense_attention(q, k, v, self.num_heads)
         elif isinstance(adj_mask, PackedSets):
             out = masked_attention(q, k, v, self.num_heads, adj_mask, packed=self.xformers_or_torch_attn == "hip")
+        elif isinstance(adj_mask, torch.Tensor):
+            out = tensor_masked_attention(q, k, v, self.num_heads, adj_mask)
         else:
-            raise TypeError("adj_mask must be None or an EdgeAdjacency / NodeAdjacency (build it with "
-                            "get_adj_mask_from_edge_index_edge / _node); dense bias tensors are not materialised")
+            raise TypeError("adj_mask must be None, an EdgeAdjacency / NodeAdjacency descriptor, or a mask tensor")
         out = out.to(q.dtype)
         return mish(self.fc_o(out), out)
 

@@ -19,7 +19,7 @@ from torch.nn.init import xavier_normal_
 
 from .activations import mish
 from .attention import varlen_attention
-from .mha import _heads, dense_attention, masked_attention
+from .mha import _heads, dense_attention, masked_attention, tensor_masked_attention
 from .packing import PackedSets
 
 
@@ -67,8 +67,10 @@ class MABFlashVarlen(nn.Module):
             out = dense_attention(q, k, v, self.num_heads)
         elif isinstance(adj_mask, PackedSets):
             out = masked_attention(q, k, v, self.num_heads, adj_mask, packed=False)
+        elif isinstance(adj_mask, torch.Tensor):   # SDPA's attn_mask (esa/mha_flash_varlen.py:112-117)
+            out = tensor_masked_attention(q, k, v, self.num_heads, adj_mask)
         else:
-            raise TypeError("adj_mask must be None or an EdgeAdjacency / NodeAdjacency")
+            raise TypeError("adj_mask must be None, an EdgeAdjacency / NodeAdjacency descriptor, or a mask tensor")
         out = out.to(q.dtype)
         out = mish(self.fc_o(out), out)
         return out.to(input_dtype) if out.dtype != input_dtype else out

@@ -299,3 +299,54 @@ def test_config0_full_batch(device):
         pool=lambda s_, p_, z: OMod.pma_complete(s_, p_, z, H, 2, cu=cu, max_items=n))
     assert_f32_close(enc.cpu(), enc_ref, "token embeddings")
     assert_f32_close(g_emb.cpu(), g_ref, "graph embeddings")
+
+
+def test_mab_with_the_reference_bias_tensor(device):
+    """MAB / SAB given the reference's own [B, 1, N, N] mask tensors: the additive 0 / -99999 bias of
+    get_adj_mask_from_edge_index_edge (fp32 and its bf16 rounding -99840), the same bias expanded over heads
+    [B, H, N, N] (esa/mha.py:73), and a bool mask (True = attend); every row, padding included, against the
+    oracle's padded MAB with that bias."""
+    gb, n = _batch(11)
+    torch.manual_seed(11)
+    m = SAB(D, D, H, 0.0, "xformers").to(device)
+    X, _ = _padded_tokens(gb, n, 12)
+    gid = np.repeat(np.arange(gb.num_graphs), gb.edge_counts)
+    bias = OM.edge_bias_padded(gb.edge_index, gid, gb.num_graphs, n, dtype=torch.float64)
+    ref = OMod.mab_padded(_sd(m), "mab.", X, X, H, bias)
+    xd = X.to(device)
+    for what, mask in (("fp32 bias", bias.float()), ("bf16 bias", bias.to(torch.bfloat16)),
+                       ("bias over heads", bias.float().expand(-1, H, -1, -1)), ("bool mask", bias == 0)):
+        got = m(xd, adj_mask=mask.to(device)).cpu()
+        assert_f32_close(got, ref, f"SAB with a {what}")
+    mf = MABFlashVarlen(D, D, D, H).to(device)
+    mf.load_state_dict(m.mab.state_dict())
+    got_f = mf(xd, xd, adj_mask=bias.float().to(device)).cpu()   # the padded SDPA fallback with attn_mask
+    assert_f32_close(got_f, OMod.mab_padded(_sd(mf), "", X, X, H, bias), "MABFlashVarlen padded with a bias")
+    with pytest.raises(NotImplementedError):
+        m(xd, adj_mask=(bias * 0.5 + 1.0).float().to(device))          # a general additive bias
+    per_head = (bias == 0).expand(-1, H, -1, -1).clone()
+    per_head[:, 0, 0, 0] = ~per_head[:, 0, 0, 0]
+    with pytest.raises(NotImplementedError):
+        m(xd, adj_mask=per_head.to(device))
+
+
+def test_torch_library_ops(device):
+    """The C-ABI entry points are registered torch operators: torch.ops.esa_hip.* run the same kernels."""
+    from mind_amd import edges
+    from mind_amd.esa import attention as A
+    gb = generators.protein_like(seed=3, num_graphs=3, n_min=30, n_max=60)
+    cu = torch.as_tensor(gb.cu_seqlens).to(device)
+    t = int(gb.cu_seqlens[-1])
+    q, k, v = (torch.randn(t, 16, 16, generator=torch.Generator().manual_seed(i)).to(torch.bfloat16).to(device)
+               for i in range(3))
+    out, lse = torch.ops.esa_hip.varlen_attn_fwd(q, k, v, cu, cu, gb.max_seqlen, gb.max_seqlen, 0.25, None, None,
+                                                 None, None)
+    ref, ref_lse = A.attn_fwd(q, k, v, cu, cu, gb.max_seqlen, gb.max_seqlen, 0.25)
+    assert torch.equal(out, ref) and torch.equal(lse, ref_lse)
+    x = torch.randn(100, 32, device=device)
+    src = torch.randint(0, 100, (500,), device=device, dtype=torch.int32)
+    dst = torch.randint(0, 100, (500,), device=device, dtype=torch.int32)
+    assert torch.equal(torch.ops.esa_hip.edge_gather(x, src, dst), torch.cat([x[src.long()], x[dst.long()]], 1))
+    indptr, perm = torch.ops.esa_hip.csr_build(dst, 100)
+    y = torch.randn(500, 32, device=device)
+    assert torch.equal(torch.ops.esa_hip.csr_segment_sum(y, indptr, perm), edges.segment_sum_csr(y, indptr, perm))

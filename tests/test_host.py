@@ -186,3 +186,25 @@ def test_radix_csr_order_is_stable():
     for shift in (0, 8):                          # 600 < 2^16: two 8-bit passes
         k, v = _radix_pass_model(k, v, shift)
     assert np.array_equal(v, np.argsort(keys, kind="stable"))
+
+
+def test_torch_library_ops_have_fake_implementations():
+    """torch.ops.esa_hip.* are registered with shape functions: they trace under FakeTensorMode (no GPU)."""
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    import mind_amd.edges  # noqa: F401
+    import mind_amd.esa.attention  # noqa: F401
+    with FakeTensorMode():
+        q = torch.empty(40, 4, 16, dtype=torch.bfloat16)
+        cu = torch.empty(3, dtype=torch.int32)
+        out, lse = torch.ops.esa_hip.varlen_attn_fwd(q, q, q, cu, cu, 20, 20, 0.25, None, None, None, None)
+        assert out.shape == q.shape and lse.shape == (4, 40) and lse.dtype == torch.float32
+        dq, dk, dv = torch.ops.esa_hip.varlen_attn_bwd(q, q, q, q, q, lse, cu, cu, 20, 20, 0.25, None, None, None,
+                                                       None)
+        assert dq.shape == dk.shape == dv.shape == q.shape
+        x = torch.empty(10, 8)
+        idx = torch.empty(30, dtype=torch.int32)
+        assert torch.ops.esa_hip.edge_gather(x, idx, idx).shape == (30, 16)
+        ip, perm = torch.ops.esa_hip.csr_build(idx, 10)
+        assert ip.shape == (11,) and perm.shape == (30,)
+        assert torch.ops.esa_hip.csr_segment_sum(torch.empty(30, 8), ip, perm).shape == (10, 8)
