@@ -104,7 +104,7 @@ ESA_API int esa_varlen_attn_fwd(const void* q, const void* k, const void* v,
 /* callers that cannot allocate device memory (code under HIP graph capture, */
 /* tight serving loops, harnesses that forbid hipMalloc).  Same arguments     */
 /* and results as esa_varlen_attn_fwd without the workspace: the scratch is  */
-/* a static device array of esa_noalloc_scratch_bytes() (4 MiB) per GPU,     */
+/* a static device array of esa_noalloc_scratch_bytes() (16 MiB) per GPU,    */
 /* held until the process ends, enough for every ESA shape up to 131,072      */
 /* tokens x 32 heads (any mask kind).  A call needing more returns            */
 /* ESA_ERR_SCRATCH and launches nothing.  The caller still passes the inputs */

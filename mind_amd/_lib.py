@@ -91,7 +91,7 @@ _PROTOS = {
     "esa_profile_kernel_name": (ctypes.c_char_p, [_c_int]),
 }
 
-PROFILE_KERNELS = 19
+PROFILE_KERNELS = 21
 
 _lock = threading.Lock()
 _lib = None

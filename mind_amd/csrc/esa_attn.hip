@@ -212,6 +212,7 @@ struct AttnArgs {
   const bf16* q; const bf16* k; const bf16* v; const bf16* out; const bf16* dout;
   const float* lse;         // [H][total_q] natural log (forward output / backward input)
   const uint2* aux;         // dK/dV pass: per (head, query) packed bf16 (hi, lo) of -LSE2/c and of -D
+  uint2* aux_out;           // key-list dQ pass: writes aux (it reads dO, O and LSE of its queries anyway)
   const float* knorm;       // forward: max |k| per (head, key tile) [H][tk_tiles]
   const int* cu_q; const int* cu_k; int nseg;
   int total_q, total_k, heads, tq_pad, tk_tiles;
@@ -219,7 +220,12 @@ struct AttnArgs {
   float scale;
   const int2* nodes; const int4* meta;   // masked mode: per-token node pairs (padded), per-tile metadata
   const int4* plan;         // per block group: (group, first partner tile, end partner tile, -)
+  const int* count;         // walk kernels: number of plan entries (the overflow list)
   const int2* bounds;       // per outer token: partner range of its segment
+  const int* info;          // key lists: per outer tile, the number of partners (-1: group overflowed)
+  const int* ids;           // key lists: per outer tile, kListCap partner token ids (-1 pads)
+  const uint32_t* bits;     // key lists: per outer tile, [kListCap / 32][32] mask words
+  const float* kbound;      // key-list forward: per (query tile, head) max |k| over its candidate partner tiles
   bf16* o; float* lse_out;  // forward outputs
   bf16* dq; bf16* dk; bf16* dv;
 };
@@ -309,36 +315,31 @@ template <int NH>
 struct StageEdge { i32x4 k[NH], v[NH], n; };
 
 #ifndef ESA_EDGE_WAVES
-#define ESA_EDGE_WAVES 3
+#define ESA_EDGE_WAVES 2
 #endif
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ESA_EDGE_WAVES))) void edge_fwd_kernel(
-    const AttnArgs a) {
+DEVI void edge_fwd_group(const AttnArgs& a, int item, int hg, const bf16* sOnes) {
   constexpr int NH = kEdgeHeads;
   __shared__ __align__(16) bf16 sK[kWaves][2][NH][kTile * kRowStride];   // K rows [key][16]
   __shared__ __align__(16) bf16 sV[kWaves][2][NH][2 * kTileHalf];        // V rows split by dims half
   __shared__ __align__(16) int2 sN[kWaves][2][kTile];
-  __shared__ __align__(16) bf16 sOnes[4];                                 // the ones rows of [V^T ; 1]
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 31, half = lane >> 5, c16 = lane & 15, grp = lane >> 4;
-  const int H = a.heads, n_hg = (H + NH - 1) / NH;
-  const int item = blockIdx.x / n_hg, hg = blockIdx.x - item * n_hg;
+  const int H = a.heads;
   const int h0 = hg * NH;
   const int nh = min(NH, H - h0);   // heads of this wave
   const int4 pl = a.plan[item];
   const int t0 = pl.x * kGroupTok, o0 = t0 + wave * kTile;
-  if (tid < 4) sOnes[tid] = (bf16)1.f;
-  __syncthreads();
 
   const OuterTile ot = outer_tile(a.bounds, a.total_q, o0, col);
   const int2 qn = a.nodes[ot.oc];
   const int4 own = ot.active ? a.meta[o0 / kTile] : no_touch();
   bf16x8 qh[NH], ql[NH];
-  float bmax = 0.f;
+  float bmax = a.knorm ? 0.f : INFINITY;   // without key norms: the online path
 #pragma unroll
   for (int u = 0; u < NH; ++u) {
     const int hc = min(h0 + u, H - 1);
     const bf16x8 qf = *reinterpret_cast<const bf16x8*>(a.q + ((size_t)ot.oc * H + hc) * kHd + 8 * half);
-    if (ot.active) {
+    if (ot.active && a.knorm) {
       // bound c |q| max|k| over the keys this wave visits
       float qq = 0.f;
 #pragma unroll
@@ -440,6 +441,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ESA_EDGE_WA
   }
 }
 
+// The walk kernels run over a list of groups with a device-side count (the
+// groups whose key lists overflow): a block loops over list items, so a small
+// fixed grid serves any count and costs little when the list is empty.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ESA_EDGE_WAVES))) void edge_fwd_kernel(
+    const AttnArgs a) {
+  __shared__ __align__(16) bf16 sOnes[4];   // the ones rows of [V^T ; 1]
+  const int n_hg = (a.heads + kEdgeHeads - 1) / kEdgeHeads, hg = blockIdx.x % n_hg;
+  const int n_items = *a.count;
+  if ((int)blockIdx.x / n_hg >= n_items) return;
+  if (threadIdx.x < 4) sOnes[threadIdx.x] = (bf16)1.f;
+  __syncthreads();
+  for (int item = blockIdx.x / n_hg; item < n_items; item += gridDim.x / n_hg) edge_fwd_group(a, item, hg, sOnes);
+}
+
 // ======================================================================== edge-mask dQ pass
 // One wave = one 32-query tile and kEdgeHeads heads of it, as the forward:
 // dQ = scale * dS K with dS = P * (dP - D), P recomputed from the saved
@@ -448,18 +463,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ESA_EDGE_WA
 // LDS transpose reads.
 
 #ifndef ESA_EDGE_WAVES_DQ
-#define ESA_EDGE_WAVES_DQ 3
+#define ESA_EDGE_WAVES_DQ 2
 #endif
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ESA_EDGE_WAVES_DQ))) void edge_dq_kernel(
-    const AttnArgs a) {
+DEVI void edge_dq_group(const AttnArgs& a, int item, int hg) {
   constexpr int NH = kEdgeHeads;
   __shared__ __align__(16) bf16 sK[kWaves][2][NH][2 * kTileHalf];   // K rows split by dims half
   __shared__ __align__(16) bf16 sV[kWaves][2][NH][2 * kTileHalf];   // V rows split by dims half
   __shared__ __align__(16) int2 sN[kWaves][2][kTile];
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 31, half = lane >> 5, c16 = lane & 15, grp = lane >> 4;
-  const int H = a.heads, n_hg = (H + NH - 1) / NH;
-  const int item = blockIdx.x / n_hg, hg = blockIdx.x - item * n_hg;
+  const int H = a.heads;
   const int h0 = hg * NH;
   const int nh = min(NH, H - h0);   // heads of this wave
   const int4 pl = a.plan[item];
@@ -544,6 +557,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ESA_EDGE_WA
   }
 }
 
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ESA_EDGE_WAVES_DQ))) void edge_dq_kernel(
+    const AttnArgs a) {
+  const int n_hg = (a.heads + kEdgeHeads - 1) / kEdgeHeads, hg = blockIdx.x % n_hg;
+  const int n_items = *a.count;
+  for (int item = blockIdx.x / n_hg; item < n_items; item += gridDim.x / n_hg) edge_dq_group(a, item, hg);
+}
+
 // ======================================================================== edge-mask dK/dV pass
 // One wave = one 32-key tile (keys on lanes, queries in rows) and
 // kEdgeHeadsKv heads of it: dV = P^T dO, dK = scale * dS^T Q.  Row
@@ -553,7 +573,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ESA_EDGE_WA
 // Q^T and dO^T come from LDS transpose reads.
 
 #ifndef ESA_EDGE_HEADS_KV
-#define ESA_EDGE_HEADS_KV 2
+#define ESA_EDGE_HEADS_KV 1
 #endif
 constexpr int kEdgeHeadsKv = ESA_EDGE_HEADS_KV;
 #ifndef ESA_EDGE_WAVES_DKDV
@@ -563,8 +583,7 @@ constexpr int kEdgeHeadsKv = ESA_EDGE_HEADS_KV;
 template <int NH>
 struct StageKv { i32x4 q[NH], d[NH], x[NH], n; };
 
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ESA_EDGE_WAVES_DKDV))) void edge_dkdv_kernel(
-    const AttnArgs a) {
+DEVI void edge_dkdv_group(const AttnArgs& a, int item, int hg) {
   constexpr int NH = kEdgeHeadsKv;
   __shared__ __align__(16) bf16 sQ[kWaves][2][NH][2 * kTileHalf];    // Q rows split by dims half
   __shared__ __align__(16) bf16 sDO[kWaves][2][NH][2 * kTileHalf];   // dO rows split by dims half
@@ -572,8 +591,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ESA_EDGE_WA
   __shared__ __align__(16) int2 sN[kWaves][2][kTile];
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 31, half = lane >> 5, c16 = lane & 15, grp = lane >> 4;
-  const int H = a.heads, n_hg = (H + NH - 1) / NH;
-  const int item = blockIdx.x / n_hg, hg = blockIdx.x - item * n_hg;
+  const int H = a.heads;
   const int h0 = hg * NH;
   const int nh = min(NH, H - h0);   // heads of this wave
   const int4 pl = a.plan[item];
@@ -666,6 +684,777 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ESA_EDGE_WA
     const int h = h0 + u;
     store_rows8(a.dv + ((size_t)ot.oi * H + h) * kHd, dva[u], 1.f, half);
     store_rows8(a.dk + ((size_t)ot.oi * H + h) * kHd, dka[u], a.scale, half);
+  }
+}
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ESA_EDGE_WAVES_DKDV))) void edge_dkdv_kernel(
+    const AttnArgs a) {
+  const int n_hg = (a.heads + kEdgeHeadsKv - 1) / kEdgeHeadsKv, hg = blockIdx.x % n_hg;
+  const int n_items = *a.count;
+  for (int item = blockIdx.x / n_hg; item < n_items; item += gridDim.x / n_hg) edge_dkdv_group(a, item, hg);
+}
+
+// ======================================================================== edge-mask key lists
+// The walk kernels above evaluate the mask of every candidate partner tile
+// once per head group.  The key lists evaluate it once per call: per 32-token
+// outer tile, the union of the partner tokens that any of its tokens attends
+// (shares an endpoint, lies in its segment, is not itself), in ascending token
+// order, and per outer token one mask bit per union entry.  The list kernels
+// below visit ceil(union / 32) compact tiles per outer tile, gather the
+// partner rows by id and build a tile's bias from one 32-bit word per lane.
+// When the query and key segments coincide the mask is symmetric and the
+// dK/dV pass reads the query tiles' lists.
+//
+// Capacity: kListCap partners per outer tile.  A 128-token group with a tile
+// past capacity gets info -1 on its four tiles and goes to an overflow list,
+// which the walk kernels process.
+
+#ifndef ESA_LIST_CAP
+#define ESA_LIST_CAP 384
+#endif
+constexpr int kListCap = ESA_LIST_CAP;
+static_assert(kListCap % kTile == 0, "list capacity in whole tiles");
+
+struct ListArgs {
+  const int2* nodes; const int4* meta;
+  const float* knorm; int kn_tiles, heads;   // forward: max |k| per (head, key tile), [heads][kn_tiles]
+  float* kbound;                             // forward: per (query tile, head) max of knorm over its candidates
+  int total, n_groups;          // outer (= partner) tokens and 128-token groups per direction
+  const int2* bounds[2];        // per outer token: partner range of its segment (0: queries, 1: keys)
+  int* info[2]; int* ids[2]; uint32_t* bits[2];
+  int4* over[2]; int* over_count[2];
+};
+
+// 32 x 32 bit-matrix transpose across lanes 0..31 (and, separately, 32..63):
+// lane r holds row r (bit c = element (r, c)) and receives column r.  Five
+// butterfly stages swap the off-diagonal blocks of size 16, 8, 4, 2, 1.
+DEVI uint32_t transpose32(uint32_t x, int lane) {
+  uint32_t m = 0x0000FFFFu;
+#pragma unroll
+  for (int j = 16; j > 0; j >>= 1, m ^= m << j) {
+    const uint32_t t = (uint32_t)__shfl_xor((int)x, j);
+    x = (lane & j) ? ((x & ~m) | ((t >> j) & m)) : ((x & m) | ((t & m) << j));
+  }
+  return x;
+}
+
+constexpr int kHashSlots = 128;   // per wave: the outer tile's <= 64 node ids, load <= 1/2
+DEVI int node_slot(int node) { return (int)(((uint32_t)node * 2654435761u) >> 25); }
+
+// Mask of the outer tile's tokens that have `node` as an endpoint (0 if none).
+DEVI uint32_t node_lookup(const int* keys, const uint32_t* masks, int node) {
+  if (node < 0) return 0u;
+  int h = node_slot(node);
+  for (int i = 0; i < kHashSlots; ++i) {
+    const int k = keys[h];
+    if (k == node) return masks[h];
+    if (k < 0) return 0u;
+    h = (h + 1) & (kHashSlots - 1);
+  }
+  return 0u;
+}
+
+// One block = one 128-token group of one direction, one wave per outer tile.
+// A wave hashes its tile's node ids (node -> mask of the tile's tokens with
+// that endpoint, open addressing in LDS) and records the runs of its tokens
+// that share a partner range (one per segment).  Then, per batch of 64
+// partner tiles, the candidates (node-range and signature test of the tile
+// metadata, as the walk kernels) are processed in three data-parallel steps:
+//  A. every candidate token's mask over the outer tokens: the OR of its two
+//     endpoints' lookups, cut to the runs whose range holds it and off the
+//     diagonal (two candidates per step, 16 candidates' loads in flight);
+//  B. a wave prefix scan of the candidates' union sizes gives every kept
+//     token its list position: ids to global, masks to LDS;
+// and at the end, C. each run of 32 entries is transposed into one word per
+// outer token (bit k of word c: entry 32 c + k).
+__global__ __launch_bounds__(256) void edge_lists_kernel(const ListArgs a) {
+  constexpr int kBatch = 64;   // partner tiles per candidate ballot
+  __shared__ int sKey[kWaves][kHashSlots];
+  __shared__ uint32_t sQm[kWaves][kHashSlots];
+  __shared__ int4 sRun[kWaves][kTile];               // (partner begin, partner end, token mask, -)
+  __shared__ int sCand[kWaves][kBatch];              // candidate partner tiles of the batch
+  __shared__ uint32_t sU[kWaves][kBatch];            // their unions (bit j: partner token j kept)
+  __shared__ int sPre[kWaves][kBatch];               // their first list positions
+  __shared__ uint32_t sKmA[kWaves][kBatch * kTile];  // masks of the batch's candidate tokens
+  __shared__ uint32_t sKm[kWaves][kListCap];         // masks of the list entries
+  __shared__ int s_over;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 31, half = lane >> 5;
+  const int dir = (int)blockIdx.x >= a.n_groups ? 1 : 0;
+  const int g = (int)blockIdx.x - dir * a.n_groups;
+  if (tid == 0) s_over = 0;
+  __syncthreads();
+  const int tile = g * kWaves + wave, o0 = tile * kTile;
+  const OuterTile ot = outer_tile(a.bounds[dir], a.total, o0, col);
+  int count = 0;
+  bool over = false;
+  if (ot.active) {
+    const int2 qn = a.nodes[ot.oc];
+    const int4 own = a.meta[tile];
+    int* keys = sKey[wave];
+    uint32_t* qm = sQm[wave];
+    for (int i = lane; i < kHashSlots; i += 64) {
+      keys[i] = -1;
+      qm[i] = 0u;
+    }
+    wave_sync();
+    const int node = half ? qn.y : qn.x;
+    if (ot.valid && node >= 0) {
+      int h = node_slot(node);
+      for (int i = 0; i < kHashSlots; ++i) {
+        const int prev = atomicCAS(&keys[h], -1, node);
+        if (prev < 0 || prev == node) {
+          atomicOr(&qm[h], 1u << col);
+          break;
+        }
+        h = (h + 1) & (kHashSlots - 1);
+      }
+    }
+    // runs of outer tokens with one partner range
+    const int plo_prev = __shfl(ot.plo, max(col - 1, 0)), phi_prev = __shfl(ot.phi, max(col - 1, 0));
+    const uint32_t vmask = (uint32_t)__ballot(ot.valid);
+    const uint32_t starts = (uint32_t)__ballot(ot.valid && (col == 0 || ot.plo != plo_prev || ot.phi != phi_prev));
+    const int nruns = __popc(starts);
+    if (half == 0 && ((starts >> col) & 1u)) {
+      const uint32_t later = starts & ~((2u << col) - 1u);   // starts after this lane (col = 31: none)
+      const uint32_t below_end = later ? (1u << __builtin_ctz(later)) - 1u : 0xFFFFFFFFu;
+      sRun[wave][__popc(starts & ((1u << col) - 1u))] =
+          make_int4(ot.plo, ot.phi, (int)(below_end & ~((1u << col) - 1u) & vmask), 0);
+    }
+    wave_sync();
+
+    // Mask over the outer tokens of partner token p with nodes pn.
+    auto partner_mask = [&](int p, int2 pn) {
+      uint32_t km = node_lookup(keys, qm, pn.x) | node_lookup(keys, qm, pn.y);
+      if (km) {
+        uint32_t sm = 0u;
+        for (int k = 0; k < nruns; ++k) {
+          const int4 r = sRun[wave][k];
+          if (p >= r.x && p < r.y) sm |= (uint32_t)r.z;
+        }
+        km &= sm;
+        if (p >= o0 && p < o0 + kTile) km &= ~(1u << (p - o0));
+      }
+      return km;
+    };
+    int* out_ids = a.ids[dir] + (size_t)tile * kListCap;
+    uint32_t* out_bits = a.bits[dir] + (size_t)tile * kListCap;
+    float kbm = 0.f;   // lane h: max |k| of head h over the candidate partner tiles
+    constexpr int kSteps = 8;   // steps (two candidates each) whose node loads are in flight together
+    for (int base = ot.pt_beg; base < ot.pt_end; base += kBatch) {
+      const int x = base + lane;
+      const bool need = x < ot.pt_end && tiles_may_touch(own, a.meta[x]);
+      const unsigned long long cand = __ballot(need);
+      const int n = __popcll(cand);
+      if (n == 0) continue;
+      if (need) sCand[wave][__popcll(cand & ((1ull << lane) - 1ull))] = x;
+      wave_sync();
+      if (a.kbound && lane < a.heads) {   // lane = head: max |k| over the candidates
+        const float* kn = a.knorm + (size_t)lane * a.kn_tiles;
+        for (int i0 = 0; i0 < n; i0 += 8) {
+          float v[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) v[j] = i0 + j < n ? kn[sCand[wave][i0 + j]] : 0.f;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) kbm = fmaxf(kbm, v[j]);
+        }
+      }
+      // A: candidate i = 2 r + half, its token col
+      for (int r0 = 0; 2 * r0 < n; r0 += kSteps) {
+        int2 pn[kSteps];
+        int pt[kSteps];
+#pragma unroll
+        for (int k = 0; k < kSteps; ++k) {
+          const int i = 2 * (r0 + k) + half;
+          pt[k] = i < n ? sCand[wave][i] : -1;
+          pn[k] = pt[k] >= 0 ? a.nodes[pt[k] * kTile + col] : make_int2(-1, -1);
+        }
+#pragma unroll
+        for (int k = 0; k < kSteps; ++k) {
+          if (2 * (r0 + k) >= n) break;   // wave-uniform
+          const int i = 2 * (r0 + k) + half;
+          const uint32_t km = pt[k] >= 0 ? partner_mask(pt[k] * kTile + col, pn[k]) : 0u;
+          if (i < n) sKmA[wave][i * kTile + col] = km;
+          const unsigned long long ub = __ballot(km != 0u);
+          if (col == 0 && i < n) sU[wave][i] = (uint32_t)(ub >> (32 * half));
+        }
+      }
+      wave_sync();
+      // B: list positions
+      const uint32_t ui = lane < n ? sU[wave][lane] : 0u;
+      const int sz = __popc(ui);
+      int incl = sz;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int t = __shfl_up(incl, o);
+        if (lane >= o) incl += t;
+      }
+      const int batch_total = __shfl(incl, 63);
+      if (count + batch_total > kListCap) {
+        over = true;
+        break;
+      }
+      if (lane < n) sPre[wave][lane] = count + incl - sz;
+      wave_sync();
+      for (int r = 0; 2 * r < n; ++r) {
+        const int i = 2 * r + half;
+        if (i < n) {
+          const uint32_t km = sKmA[wave][i * kTile + col];
+          if (km) {
+            const int e = sPre[wave][i] + __popc(sU[wave][i] & ((1u << col) - 1u));
+            out_ids[e] = sCand[wave][i] * kTile + col;
+            sKm[wave][e] = km;
+          }
+        }
+      }
+      count += batch_total;
+      wave_sync();
+    }
+    if (!over) {
+      // C: one word per outer token per 32 entries
+      for (int c = 0; c * kTile < count; ++c) {
+        const int e = c * kTile + col;
+        const uint32_t w = transpose32(e < count ? sKm[wave][e] : 0u, lane);
+        if (half == 0) out_bits[c * kTile + col] = w;
+      }
+      const int padded = (count + kTile - 1) & ~(kTile - 1);
+      if (lane < padded - count) out_ids[count + lane] = -1;
+      if (a.kbound)
+        for (int h = lane; h < a.heads; h += 64) a.kbound[(size_t)tile * a.heads + h] = h < 64 ? kbm : INFINITY;
+    }
+  }
+  if (over && lane == 0) s_over = 1;
+  __syncthreads();
+  const bool group_over = s_over != 0;
+  if (ot.active && lane == 0) a.info[dir][tile] = group_over ? -1 : count;
+  if (group_over && tid == 0) a.over[dir][atomicAdd(a.over_count[dir], 1)] = make_int4(g, 0, 0, 0);
+}
+
+// Byte offset of dims half `half` of token `id`'s row of head h in [T][H][16]
+// bf16; list pads (id < 0) address past every resource and load zeros.
+DEVI uint32_t list_row_off(int id, int H, int h, int half) {
+  return id < 0 ? 0x80000000u : ((uint32_t)id * H + h) * (kHd * 2) + 16u * half;
+}
+
+// 0 if bit K of w is set, else -inf: v_bfe_i32 (the bit sign-extended to a
+// full mask) and v_bfi_b32 (-inf where the mask is clear).  Written as asm:
+// the compiler turns the C form into a compare and a select, three
+// instructions and a VCC hazard per element.
+template <int K>
+DEVI float bit_bias(uint32_t w, int ninf) {
+  float b;
+  asm("v_bfe_i32 %0, %1, %2, 1\n\tv_bfi_b32 %0, %0, 0, %3" : "=&v"(b) : "v"(w), "i"(K), "s"(ninf));
+  return b;
+}
+template <int R>
+DEVI void word_bias_rows(f32x16& b, uint32_t w, int ninf) {
+  if constexpr (R < 16) {
+    b[R] = bit_bias<16 * (R >> 3) + (R & 7)>(w, ninf);
+    word_bias_rows<R + 1>(b, w, ninf);
+  }
+}
+
+// Bias (0 keep / -inf drop) of the lane's 16 accumulator rows (tile-local
+// partner row_local(r, half)) from its mask word.
+DEVI f32x16 word_bias(uint32_t w, int half) {
+  f32x16 b;
+  word_bias_rows<0>(b, w >> (8 * half), (int)0xff800000);
+  return b;
+}
+
+// x of lane l ^ 32 combined with x by op (sum, max): v_permlane32_swap.
+DEVI float halves_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
+  return __int_as_float(r[0]) + __int_as_float(r[1]);
+}
+DEVI float halves_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
+  return fmaxf(__int_as_float(r[0]), __int_as_float(r[1]));
+}
+
+// XCD-aware block order.  Blocks go to the 8 XCDs round-robin (block b on
+// XCD b % 8), each XCD with its own L2.  Work item i of n (group-major:
+// i = group * head groups + head group) runs on block (i % per) * 8 + i / per,
+// per = ceil(n / 8): XCD x takes items [x per, (x + 1) per) in order, a
+// contiguous token range over all heads, so the partner rows its waves gather
+// (whole 512-byte token rows over the heads) are shared in its L2.  Returns
+// -1 for the grid's spare blocks.
+#ifndef ESA_LIST_XCD
+#define ESA_LIST_XCD 1
+#endif
+constexpr int kXcds = 8;
+DEVI int list_item(int n_items) {
+  if (!ESA_LIST_XCD) return (int)blockIdx.x < n_items ? (int)blockIdx.x : -1;
+  const int per = (n_items + kXcds - 1) / kXcds;
+  const int i = (int)(blockIdx.x % kXcds) * per + (int)(blockIdx.x / kXcds);
+  return i < n_items ? i : -1;
+}
+
+// The wave's outer tile of a list kernel: its number of compact tiles (-1:
+// the group is left to the walk kernels) and its ids, copied to LDS.  The
+// first 128 ids are read together with the count (entries past the count
+// are read but never used).
+DEVI int list_tile(const AttnArgs& a, int tile, int* sid, int lane) {
+  const int* ids = a.ids + (size_t)tile * kListCap;
+  const int pre0 = ids[lane], pre1 = ids[lane + 64];
+  const int n = a.info[tile];
+  if (n < 0) return -1;
+  const int nct = (n + kTile - 1) / kTile;
+  sid[lane] = pre0;
+  sid[lane + 64] = pre1;
+  for (int i = 128 + lane; i < nct * kTile; i += 64) sid[i] = ids[i];
+  wave_sync();
+  return nct;
+}
+static_assert(kListCap >= 128, "list_tile reads the first 128 ids");
+
+#ifndef ESA_LIST_HEADS
+#define ESA_LIST_HEADS 2
+#endif
+#ifndef ESA_LIST_HEADS_KV
+#define ESA_LIST_HEADS_KV 2
+#endif
+constexpr int kListHeads = ESA_LIST_HEADS;       // heads per wave of the forward and dQ list kernels
+constexpr int kListHeadsKv = ESA_LIST_HEADS_KV;  // heads per wave of the dK/dV list kernel
+#ifndef ESA_LIST_WAVES
+#define ESA_LIST_WAVES 3
+#endif
+#ifndef ESA_LIST_VGPRS
+#define ESA_LIST_VGPRS 128
+#endif
+#ifndef ESA_LIST_WAVES_DQ
+#define ESA_LIST_WAVES_DQ 3
+#endif
+#ifndef ESA_LIST_WAVES_DKDV
+#define ESA_LIST_WAVES_DKDV 2
+#endif
+
+template <int NH>
+struct StageList { i32x4 k[NH], v[NH]; uint32_t w; };
+
+
+// ---- LDS-direct staging of the list kernels
+// buffer_load_dwordx4 / _dword with the LDS flag: lane l's 16 (4) bytes land
+// at M0 + 16 l (4 l), so a split-row tile (lane = token col of dims half l >> 5)
+// stages with one instruction per head and tensor and no staging registers.
+// Loads past the buffer range write zeros.  Issued as assembly: the
+// compiler's wait-count pass does not see them (its own waits only get more
+// conservative), and the stage loop waits for them explicitly.  M0 is set
+// right before each load (one SALU wait state); nothing else in these
+// kernels uses M0.
+DEVI uint32_t lds_addr(const void* p) {
+  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p);
+}
+DEVI void dma16(rsrc_t r, uint32_t off, const void* lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %2, 0 offen lds" ::"v"(off), "s"(lds_addr(lds)),
+               "s"(r)
+               : "memory");
+}
+DEVI void dma4(rsrc_t r, uint32_t off, const void* lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_dword %0, %2, 0 offen lds" ::"v"(off), "s"(lds_addr(lds)),
+               "s"(r)
+               : "memory");
+}
+// s_waitcnt vmcnt(n) (gfx9 encoding: vmcnt bits 3:0 and 15:14; expcnt and
+// lgkmcnt at their maxima, i.e. not waited for).
+template <int N>
+DEVI void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Three stage buffers: stage s is staged in buffer s % 3 while stages s + 1
+// and s + 2 are in flight.  issue(stage, buf) issues a stage's loads (kPer
+// of them); past the last stage it re-issues the last one into the spare
+// buffer, so every wait covers exactly two stages of later loads.  A stage's
+// buffer is reloaded only after the stage's compute has consumed its reads.
+constexpr int kDmaDepth = 3;
+template <int kPer, class Issue, class Compute>
+DEVI void dma_pipeline(int n, Issue issue, Compute compute) {
+  if (n <= 0) return;
+  issue(0, 0);
+  issue(min(1, n - 1), 1);
+  int buf = 0;
+  for (int st = 0; st < n; ++st) {
+    const int nxt = buf == 0 ? 2 : buf - 1;   // (st + 2) % 3
+    issue(min(st + 2, n - 1), nxt);
+    wait_vmcnt<2 * kPer>();
+    wave_sync();
+    compute(st, buf);
+    buf = buf == 2 ? 0 : buf + 1;
+  }
+}
+
+// Blocks of the list kernels: one 32-token tile and kWaves head groups (one
+// per wave).  The waves gather complementary slices of the same partner rows
+// ([T][H][16] bf16: a token's heads are contiguous), so the cache lines they
+// pull are shared in the CU's L1 instead of each CU using a fraction of every
+// line; the tile's ids are loaded once per block.
+DEVI int list_block_ids(const AttnArgs& a, int tile, int* sid, int tid) {
+  const int n = a.info[tile];
+  if (n > 0) {
+    const int* ids = a.ids + (size_t)tile * kListCap;
+    const int m = (n + kTile - 1) & ~(kTile - 1);
+    for (int i = tid; i < m; i += 256) sid[i] = ids[i];
+  }
+  __syncthreads();
+  return n < 0 ? -1 : (n + kTile - 1) / kTile;
+}
+
+// Forward over the key lists: one wave = one 32-query tile and kListHeads
+// heads; the bias of a compact tile seeds every head's score MFMA.  The
+// softmax takes the fixed reference of the walk kernels when the bound
+// c |q| max|k| (max |k| over the tile's candidate partner tiles, from the
+// list pass) is at most 60 on every lane, else a running max.
+__global__ __launch_bounds__(256) void list_fwd_kernel(const AttnArgs a) {
+  constexpr int NH = kListHeads;
+  __shared__ __align__(16) bf16 sK[kWaves][kDmaDepth][NH][2 * kTileHalf];   // K rows split by dims half
+  __shared__ __align__(16) bf16 sV[kWaves][kDmaDepth][NH][2 * kTileHalf];   // V rows split by dims half
+  __shared__ __align__(16) uint32_t sW[kWaves][kDmaDepth][64];               // mask words (lane col)
+  __shared__ int sId[kListCap];
+  __shared__ __align__(16) bf16 sOnes[4];                                    // the ones rows of [V^T ; 1]
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 31, half = lane >> 5, c16 = lane & 15, grp = lane >> 4;
+  const int H = a.heads, n_hg = (H + NH - 1) / NH, n_hq = (n_hg + kWaves - 1) / kWaves;
+  const int idx = list_item(((a.total_q + kTile - 1) / kTile) * n_hq);
+  if (idx < 0) return;
+  const int tile = idx / n_hq, hg = (idx - tile * n_hq) * kWaves + wave;
+  const int h0 = hg * NH, nh = min(NH, H - h0);   // nh <= 0: a wave without heads
+  if (tid < 4) sOnes[tid] = (bf16)1.f;
+  const int oi = tile * kTile + col;
+  const bool valid = oi < a.total_q;
+  const int oc = valid ? oi : a.total_q - 1;
+  bf16x8 qf[NH];
+  float kb[NH];
+#pragma unroll
+  for (int u = 0; u < NH; ++u) {
+    const int hc = min(max(h0, 0) + u, H - 1);
+    qf[u] = *reinterpret_cast<const bf16x8*>(a.q + ((size_t)oc * H + hc) * kHd + 8 * half);
+    kb[u] = a.kbound[(size_t)tile * H + hc];
+  }
+  const int nct = list_block_ids(a, tile, sId, tid);
+  if (nct < 0 || nh <= 0) return;
+  if (nct == 0) {   // no partners: zero rows, lse -inf
+    if (!valid) return;
+    for (int u = 0; u < nh; ++u) {
+      store_rows8(a.o + ((size_t)oi * H + h0 + u) * kHd, f32x16{}, 0.f, half);
+      if (half == 0) a.lse_out[(size_t)(h0 + u) * a.total_q + oi] = -INFINITY;
+    }
+    return;
+  }
+  bf16x8 qh[NH], ql[NH];
+  float bmax = 0.f;
+#pragma unroll
+  for (int u = 0; u < NH; ++u) {
+    float qq = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qq = fmaf((float)qf[u][e], (float)qf[u][e], qq);
+    qq = halves_sum(qq);
+    bmax = fmaxf(bmax, valid ? a.c * sqrtf(qq) * kb[u] : 0.f);
+    split_scaled(qf[u], a.c, qh[u], ql[u]);
+  }
+  const bool fixed_ref = __builtin_amdgcn_readfirstlane((int)(wave_max(bmax) <= kStaticBound)) != 0;
+  float m_run[NH];
+  f32x16 acc[NH];
+#pragma unroll
+  for (int u = 0; u < NH; ++u) {
+    m_run[u] = fixed_ref ? 0.f : -INFINITY;
+    acc[u] = f32x16{};
+  }
+  const uint32_t kv_bytes = (uint32_t)a.total_k * H * kHd * 2;
+  const rsrc_t rk = make_rsrc(a.k, kv_bytes), rv = make_rsrc(a.v, kv_bytes);
+  const rsrc_t rw = make_rsrc(a.bits + (size_t)tile * kListCap, (uint32_t)kListCap * 4u);
+  dma_pipeline<2 * NH + 1>(
+      nct,
+      [&](int c, int buf) {
+        const int id = sId[c * kTile + col];
+#pragma unroll
+        for (int u = 0; u < NH; ++u) {
+          const uint32_t off = list_row_off(id, H, min(h0 + u, H - 1), half);
+          dma16(rk, off, sK[wave][buf][u]);
+          dma16(rv, off, sV[wave][buf][u]);
+        }
+        dma4(rw, (uint32_t)(c * kTile + col) * 4u, sW[wave][buf]);
+      },
+      [&](int, int buf) {
+        const f32x16 bias = word_bias(sW[wave][buf][col], half);
+#pragma unroll
+        for (int u = 0; u < NH; ++u) {
+          if (u >= nh) break;   // wave-uniform
+          const bf16x8 kr = half_row8<kTileHalf>(sK[wave][buf][u], kperm(col), half);
+          const f32x16 s = mfma32(kr, ql[u], mfma32(kr, qh[u], bias));
+          float p[16];
+          if (fixed_ref) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) p[r] = fast_exp2(s[r]);
+          } else {
+            float mt = s[0];
+#pragma unroll
+            for (int r = 1; r < 16; ++r) mt = fmaxf(mt, s[r]);
+            mt = halves_max(mt);
+            const float m_new = fmaxf(m_run[u], mt);
+            if (__ballot(m_new > m_run[u])) {
+              const float alpha = fast_exp2(m_run[u] - (m_new == -INFINITY ? 0.f : m_new));
+#pragma unroll
+              for (int r = 0; r < 16; ++r) acc[u][r] *= alpha;
+              m_run[u] = m_new;
+            }
+            const float m_use = m_run[u] == -INFINITY ? 0.f : m_run[u];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) p[r] = fast_exp2(s[r] - m_use);
+          }
+          bf16x8 vt0, vt1;
+          tr_rows32<kTileHalf>(sV[wave][buf][u], 0, sOnes, c16, grp, vt0, vt1);
+          acc[u] = mfma32(vt0, cvt8(p), acc[u]);
+          acc[u] = mfma32(vt1, cvt8(p + 8), acc[u]);
+        }
+      });
+  if (!valid) return;
+#pragma unroll
+  for (int u = 0; u < NH; ++u) {
+    if (u >= nh) break;
+    const int h = h0 + u;
+    const float l = acc[u][8];   // a ones row of [V^T; 1] P^T: the softmax row sum
+    store_rows8(a.o + ((size_t)oi * H + h) * kHd, acc[u], l > 0.f ? 1.f / l : 0.f, half);
+    if (half == 0)
+      a.lse_out[(size_t)h * a.total_q + oi] = l > 0.f ? (m_run[u] + fast_log2(l)) * kLn2 : -INFINITY;
+  }
+}
+
+// dQ over the key lists: one wave = one 32-query tile and kEdgeHeads heads,
+// as the walk kernel's dQ pass.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ESA_LIST_WAVES_DQ))) void list_dq_kernel(
+    const AttnArgs a) {
+  constexpr int NH = kListHeads;
+  __shared__ __align__(16) bf16 sK[kWaves][2][NH][2 * kTileHalf];   // K rows split by dims half
+  __shared__ __align__(16) bf16 sV[kWaves][2][NH][2 * kTileHalf];   // V rows split by dims half
+  __shared__ int sId[kWaves][kListCap];
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 31, half = lane >> 5, c16 = lane & 15, grp = lane >> 4;
+  const int H = a.heads, n_hg = (H + NH - 1) / NH;
+  const int idx = list_item((((a.total_q) + kGroupTok - 1) / kGroupTok) * n_hg);
+  if (idx < 0) return;
+  const int item = idx / n_hg, hg = idx - item * n_hg;
+  const int h0 = hg * NH;
+  const int nh = min(NH, H - h0);   // heads of this wave
+  const int tile = item * kWaves + wave;
+  if (tile * kTile >= a.total_q) return;
+  const int oi = tile * kTile + col;
+  const bool valid = oi < a.total_q;
+  const int oc = valid ? oi : a.total_q - 1;
+  bf16x8 qf[NH], dof[NH], of[NH];
+  float lq[NH];
+#pragma unroll
+  for (int u = 0; u < NH; ++u) {
+    const int hc = min(h0 + u, H - 1);
+    const size_t row = ((size_t)oc * H + hc) * kHd + 8 * half;
+    qf[u] = *reinterpret_cast<const bf16x8*>(a.q + row);
+    dof[u] = *reinterpret_cast<const bf16x8*>(a.dout + row);
+    of[u] = *reinterpret_cast<const bf16x8*>(a.out + row);
+    lq[u] = a.lse[(size_t)hc * a.total_q + oc];
+  }
+  float dsum[NH], lse2q[NH];
+  f32x16 acc[NH];
+#pragma unroll
+  for (int u = 0; u < NH; ++u) {
+    float d = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) d = fmaf((float)dof[u][e], (float)of[u][e], d);
+    dsum[u] = halves_sum(d);
+    lse2q[u] = lq[u] == -INFINITY ? INFINITY : lq[u] * kLog2e;
+    acc[u] = f32x16{};
+    // Row statistics of the dK/dV pass, as bf16 (hi, lo) pairs: -LSE2/c (-1e30
+    // for rows without keys and padding: their P is 0) and -D.  Written for
+    // every tile, also those the walk kernels take.
+    if (half == 0 && u < nh) {
+      const float xs = valid && lq[u] != -INFINITY ? -(lq[u] * kLog2e) / a.c : kDeadRow;
+      a.aux_out[(size_t)(h0 + u) * a.tq_pad + oi] =
+          make_uint2(split_bf16_pair(xs), split_bf16_pair(valid ? -dsum[u] : 0.f));
+    }
+  }
+  const int nct = list_tile(a, tile, sId[wave], lane);
+  if (nct < 0) return;
+  const f32x16 zero = {};
+  const uint32_t kv_bytes = (uint32_t)a.total_k * H * kHd * 2;
+  const rsrc_t rk = make_rsrc(a.k, kv_bytes), rv = make_rsrc(a.v, kv_bytes);
+  const uint32_t* wsrc = a.bits + (size_t)tile * kListCap + col;
+  uint32_t wreg[2] = {0u, 0u};
+  int c_next = 0;
+  tile_pipeline(
+      nct,
+      [&](uint32_t& w) {
+        w = 0xfu;
+        const int c = min(c_next, nct - 1);
+        ++c_next;
+        return c;
+      },
+      [&](int c) {
+        StageList<NH> g;
+        const int id = sId[wave][c * kTile + col];
+#pragma unroll
+        for (int u = 0; u < NH; ++u) {
+          const uint32_t off = list_row_off(id, H, min(h0 + u, H - 1), half);
+          g.k[u] = bload(rk, off);
+          g.v[u] = bload(rv, off);
+        }
+        g.w = wsrc[c * kTile];
+        return g;
+      },
+      [&](int st, const StageList<NH>& g) {
+#pragma unroll
+        for (int u = 0; u < NH; ++u) {
+          put_half<kTileHalf>(sK[wave][st][u], col, half, g.k[u]);
+          put_half<kTileHalf>(sV[wave][st][u], col, half, g.v[u]);
+        }
+        wreg[st] = g.w;
+      },
+      wave_sync,
+      [&](int, int cur, uint32_t) {
+        const f32x16 bias = word_bias(wreg[cur], half);
+#pragma unroll
+        for (int u = 0; u < NH; ++u) {
+          if (u >= nh) break;   // wave-uniform
+          const f32x16 s = mfma32(half_row8<kTileHalf>(sK[wave][cur][u], kperm(col), half), qf[u], bias);
+          const f32x16 dp = mfma32(half_row8<kTileHalf>(sV[wave][cur][u], kperm(col), half), dof[u], zero);
+          float ds[16];
+#pragma unroll
+          for (int r = 0; r < 16; ++r) ds[r] = fast_exp2(fmaf(s[r], a.c, -lse2q[u])) * (dp[r] - dsum[u]);
+          bf16x8 kt0, kt1;
+          tr_rows32<kTileHalf>(sK[wave][cur][u], 0, nullptr, c16, grp, kt0, kt1);
+          acc[u] = mfma32(kt0, cvt8(ds), acc[u]);
+          acc[u] = mfma32(kt1, cvt8(ds + 8), acc[u]);
+        }
+      });
+  if (!valid) return;
+#pragma unroll
+  for (int u = 0; u < NH; ++u) {
+    if (u >= nh) break;
+    store_rows8(a.dq + ((size_t)oi * H + h0 + u) * kHd, acc[u], a.scale, half);
+  }
+}
+
+template <int NH>
+struct StageListKv { i32x4 q[NH], d[NH]; uint2 x[(NH + 1) / 2]; uint32_t w; };
+
+// dK/dV over the key lists (of the key tiles, or of the query tiles when the
+// mask is symmetric): one wave = one 32-key tile and kEdgeHeadsKv heads, as
+// the walk kernel's dK/dV pass.  Lanes of half j load the row statistics of
+// head 2 i + j of the partner queries.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ESA_LIST_WAVES_DKDV))) void list_dkdv_kernel(
+    const AttnArgs a) {
+  constexpr int NH = kListHeadsKv;
+  __shared__ __align__(16) bf16 sQ[kWaves][2][NH][2 * kTileHalf];    // Q rows split by dims half
+  __shared__ __align__(16) bf16 sDO[kWaves][2][NH][2 * kTileHalf];   // dO rows split by dims half
+  __shared__ __align__(16) uint2 sAux[kWaves][2][NH][kTile];         // row-statistic MFMA operands
+  __shared__ int sId[kWaves][kListCap];
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 31, half = lane >> 5, c16 = lane & 15, grp = lane >> 4;
+  const int H = a.heads, n_hg = (H + NH - 1) / NH;
+  const int idx = list_item((((a.total_k) + kGroupTok - 1) / kGroupTok) * n_hg);
+  if (idx < 0) return;
+  const int item = idx / n_hg, hg = idx - item * n_hg;
+  const int h0 = hg * NH;
+  const int nh = min(NH, H - h0);   // heads of this wave
+  const int tile = item * kWaves + wave;
+  if (tile * kTile >= a.total_k) return;
+  const int oi = tile * kTile + col;
+  const bool valid = oi < a.total_k;
+  const int oc = valid ? oi : a.total_k - 1;
+  bf16x8 kf[NH], vf[NH];
+  f32x16 dva[NH], dka[NH];
+#pragma unroll
+  for (int u = 0; u < NH; ++u) {
+    const size_t row = ((size_t)oc * H + min(h0 + u, H - 1)) * kHd + 8 * half;
+    kf[u] = *reinterpret_cast<const bf16x8*>(a.k + row);
+    vf[u] = *reinterpret_cast<const bf16x8*>(a.v + row);
+    dva[u] = dka[u] = f32x16{};
+  }
+  const int nct = list_tile(a, tile, sId[wave], lane);
+  if (nct < 0) return;
+  // B operand of the row-statistic MFMAs: ones in slots 0 and 1 (half 0).
+  bf16x8 ones2 = {};
+  if (half == 0) { ones2[0] = (bf16)1.f; ones2[1] = (bf16)1.f; }
+  const f32x16 zero = {};
+  const uint32_t q_bytes = (uint32_t)a.total_q * H * kHd * 2;
+  const rsrc_t rq = make_rsrc(a.q, q_bytes), rd = make_rsrc(a.dout, q_bytes);
+  const rsrc_t rx = make_rsrc(a.aux, (uint32_t)H * a.tq_pad * 8u);
+  const uint32_t* wsrc = a.bits + (size_t)tile * kListCap + col;
+  uint32_t wreg[2] = {0u, 0u};
+  int c_next = 0;
+  tile_pipeline(
+      nct,
+      [&](uint32_t& w) {
+        w = 0xfu;
+        const int c = min(c_next, nct - 1);
+        ++c_next;
+        return c;
+      },
+      [&](int c) {
+        StageListKv<NH> g;
+        const int id = sId[wave][c * kTile + col];
+#pragma unroll
+        for (int u = 0; u < NH; ++u) {
+          const uint32_t off = list_row_off(id, H, min(h0 + u, H - 1), half);
+          g.q[u] = bload(rq, off);
+          g.d[u] = bload(rd, off);
+        }
+#pragma unroll
+        for (int i = 0; i < (NH + 1) / 2; ++i) {
+          const int hc = min(h0 + 2 * i + half, H - 1);
+          const uint32_t off = id < 0 ? 0x80000000u : ((uint32_t)hc * a.tq_pad + id) * 8u;
+          const auto x = __builtin_amdgcn_raw_buffer_load_b64(rx, off, 0, 0);
+          g.x[i] = make_uint2(x[0], x[1]);
+        }
+        g.w = wsrc[c * kTile];
+        return g;
+      },
+      [&](int st, const StageListKv<NH>& g) {
+#pragma unroll
+        for (int u = 0; u < NH; ++u) {
+          put_half<kTileHalf>(sQ[wave][st][u], col, half, g.q[u]);
+          put_half<kTileHalf>(sDO[wave][st][u], col, half, g.d[u]);
+        }
+#pragma unroll
+        for (int i = 0; i < (NH + 1) / 2; ++i)
+          if (2 * i + half < NH) sAux[wave][st][2 * i + half][col] = g.x[i];
+        wreg[st] = g.w;
+      },
+      wave_sync,
+      [&](int, int cur, uint32_t) {
+        const f32x16 bias = word_bias(wreg[cur], half);
+#pragma unroll
+        for (int u = 0; u < NH; ++u) {
+          if (u >= nh) break;   // wave-uniform
+          const uint2 ax = sAux[wave][cur][u][kperm(col)];
+          const bf16x8 aux_s = as_bf16x8(i32x4{(int)ax.x, 0, 0, 0});
+          const bf16x8 aux_d = as_bf16x8(i32x4{(int)ax.y, 0, 0, 0});
+          // S' = Q K^T - LSE2/c + bias and dP' = dO V^T - D, rows = queries, lanes = keys.
+          const f32x16 s =
+              mfma32(half_row8<kTileHalf>(sQ[wave][cur][u], kperm(col), half), kf[u], mfma32(aux_s, ones2, bias));
+          const f32x16 dp =
+              mfma32(half_row8<kTileHalf>(sDO[wave][cur][u], kperm(col), half), vf[u], mfma32(aux_d, ones2, zero));
+          float p[16], ds[16];
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            p[r] = fast_exp2(s[r] * a.c);
+            ds[r] = p[r] * dp[r];
+          }
+          bf16x8 d0, d1, q0t, q1t;
+          tr_rows32<kTileHalf>(sDO[wave][cur][u], 0, nullptr, c16, grp, d0, d1);
+          tr_rows32<kTileHalf>(sQ[wave][cur][u], 0, nullptr, c16, grp, q0t, q1t);
+          dva[u] = mfma32(d0, cvt8(p), dva[u]);
+          dva[u] = mfma32(d1, cvt8(p + 8), dva[u]);
+          dka[u] = mfma32(q0t, cvt8(ds), dka[u]);
+          dka[u] = mfma32(q1t, cvt8(ds + 8), dka[u]);
+        }
+      });
+  if (!valid) return;
+#pragma unroll
+  for (int u = 0; u < NH; ++u) {
+    if (u >= nh) break;
+    const int h = h0 + u;
+    store_rows8(a.dv + ((size_t)oi * H + h) * kHd, dva[u], 1.f, half);
+    store_rows8(a.dk + ((size_t)oi * H + h) * kHd, dka[u], a.scale, half);
   }
 }
 
@@ -910,6 +1699,7 @@ struct PrepArgs {
   const bf16* dout; const bf16* out; const float* lse; float c; uint2* aux;   // backward (bf16)
   const float* dout_f; const float* out_f; float2* rows_f;                  // backward (fp32)
   const int* tok_src; const int* tok_dst; int2* nodes; int4* meta;          // masked
+  int* over_count;                     // bf16 masked: the two overflow-list counts, zeroed here
   int nb[kPrepTasks];                  // blocks per task, in dispatch order
 };
 
@@ -1067,6 +1857,7 @@ __global__ __launch_bounds__(256) void prep_kernel(const PrepArgs p) {
   }
   b -= p.nb[kMeta];
   if (b < p.nb[kNodes]) {
+    if (b == 0 && p.over_count && tid < 2) p.over_count[tid] = 0;
     const int t = b * 256 + tid;
     if (t < p.tq_pad) p.nodes[t] = t < p.total_q ? make_int2(p.tok_src[t], p.tok_dst[t]) : make_int2(-1, -1);
     return;
@@ -1138,15 +1929,19 @@ int round32(int x) { return (x + kTile - 1) / kTile * kTile; }
 int groups_of(int total) { return (total + kGroupTok - 1) / kGroupTok; }
 
 struct WsLayout {
-  size_t knorm = 0, aux = 0, plan_q = 0, plan_k = 0, bounds_q = 0, bounds_k = 0, nodes = 0, meta = 0, total = 0;
+  size_t knorm = 0, kbound = 0, aux = 0, plan_q = 0, plan_k = 0, bounds_q = 0, bounds_k = 0, nodes = 0, meta = 0;
+  size_t over_count = 0, info[2] = {0, 0}, ids[2] = {0, 0}, bits[2] = {0, 0}, over[2] = {0, 0};
+  size_t total = 0;
 };
 
 WsLayout ws_layout(int total_q, int total_k, int heads, int dtype, bool masked, bool backward) {
   WsLayout L;
   const int tqp = round32(total_q), tkp = round32(total_k);
+  const bool lists = masked && dtype == ESA_BF16;
   size_t off = 0;
   if (!backward) {
     if (dtype == ESA_BF16) { L.knorm = off; off += align256((size_t)heads * (tkp / kTile) * 4); }
+    if (lists) { L.kbound = off; off += align256((size_t)(tqp / kTile) * heads * 4); }
   } else {
     L.aux = off; off += align256((size_t)heads * tqp * 8);   // bf16: uint2 (hi, lo) pairs; fp32: float2 rows
   }
@@ -1163,6 +1958,18 @@ WsLayout ws_layout(int total_q, int total_k, int heads, int dtype, bool masked, 
   if (masked) {
     L.nodes = off; off += align256((size_t)tqp * 8);
     L.meta = off; off += align256((size_t)(tqp / kTile) * 16);
+  }
+  if (lists) {
+    // Key lists per direction (queries; keys in the backward pass): per outer
+    // tile a count, kListCap ids and kListCap mask words; the overflow groups.
+    L.over_count = off; off += 256;
+    for (int d = 0; d < (backward ? 2 : 1); ++d) {
+      const size_t tiles = (size_t)(d ? tkp : tqp) / kTile;
+      L.info[d] = off; off += align256(tiles * 4);
+      L.ids[d] = off; off += align256(tiles * kListCap * 4);
+      L.bits[d] = off; off += align256(tiles * kListCap * 4);
+      L.over[d] = off; off += align256((size_t)groups_of(d ? total_k : total_q) * 16);
+    }
   }
   L.total = off;
   return L;
@@ -1195,11 +2002,13 @@ int launch_zero(void* p, size_t bytes, hipStream_t st) {
 
 int blocks_for(long items) { return (int)((items + 255) / 256); }
 
-int launch_prep(PrepArgs& p, bool forward, bool masked, hipStream_t st) {
-  p.nb[kPlanQ] = 1;
-  p.nb[kPlanK] = forward ? 0 : 1;
+// `lists`: the bf16 edge-mask path, whose kernels need no plans (block order
+// is XCD-aware) and whose dQ pass writes the row statistics itself.
+int launch_prep(PrepArgs& p, bool forward, bool masked, hipStream_t st, bool lists = false) {
+  p.nb[kPlanQ] = lists ? 0 : 1;
+  p.nb[kPlanK] = forward || lists ? 0 : 1;
   p.nb[kKnorm] = forward && p.knorm ? p.tk_pad / kTile : 0;
-  p.nb[kRows] = forward ? 0 : blocks_for((long)p.heads * p.tq_pad);
+  p.nb[kRows] = forward || lists ? 0 : blocks_for((long)p.heads * p.tq_pad);
   p.nb[kBoundsQ] = blocks_for(p.tq_pad);
   p.nb[kBoundsK] = forward ? 0 : blocks_for(p.tk_pad);
   p.nb[kNodes] = masked ? blocks_for(p.tq_pad) : 0;
@@ -1212,12 +2021,55 @@ int launch_prep(PrepArgs& p, bool forward, bool masked, hipStream_t st) {
   return ESA_OK;
 }
 
+// Blocks of a list kernel: groups x head groups, rounded up to whole XCD rounds.
+unsigned list_blocks(int total, unsigned n_hg) {
+  const unsigned n = (unsigned)groups_of(total) * n_hg;
+  return (n + kXcds - 1) / kXcds * kXcds;
+}
+
+// Blocks of a one-wave-per-block list kernel: 32-token tiles x head ranges,
+// rounded up to whole XCD rounds.
+unsigned list_tile_blocks(int total, unsigned n_hw) {
+  const unsigned n = (unsigned)((total + kTile - 1) / kTile) * n_hw;
+  return (n + kXcds - 1) / kXcds * kXcds;
+}
+
+constexpr int kOverflowGroups = 64;   // groups in flight in a walk kernel over the overflow list
+unsigned overflow_blocks(int total) { return (unsigned)std::min(groups_of(total), kOverflowGroups); }
+
+// Key lists of the query tiles (and of the key tiles when `both`), after the
+// prep pass that writes the nodes, tile metadata, bounds and zero counts.
+int launch_lists(const PrepArgs& pa, const WsLayout& L, char* ws, bool forward, bool both, hipStream_t st) {
+  ListArgs la{};
+  la.nodes = pa.nodes; la.meta = pa.meta;
+  la.heads = pa.heads;
+  if (forward) {   // the per-tile key-norm bounds of the fixed-reference softmax
+    la.knorm = pa.knorm; la.kn_tiles = pa.tk_pad / kTile;
+    la.kbound = reinterpret_cast<float*>(ws + L.kbound);
+  }
+  la.total = pa.total_q;
+  la.n_groups = groups_of(pa.total_q);
+  la.bounds[0] = pa.bounds_q; la.bounds[1] = pa.bounds_k;
+  for (int d = 0; d < 2; ++d) {
+    const int dd = both ? d : 0;
+    la.info[d] = reinterpret_cast<int*>(ws + L.info[dd]);
+    la.ids[d] = reinterpret_cast<int*>(ws + L.ids[dd]);
+    la.bits[d] = reinterpret_cast<uint32_t*>(ws + L.bits[dd]);
+    la.over[d] = reinterpret_cast<int4*>(ws + L.over[dd]);
+    la.over_count[d] = reinterpret_cast<int*>(ws + L.over_count) + dd;
+  }
+  const unsigned grid = (unsigned)la.n_groups * (both ? 2u : 1u);
+  ESA_TIMED(esa_profile::kAttnEdgeLists, st, hipLaunchKernelGGL(edge_lists_kernel, dim3(grid), dim3(256), 0, st, la));
+  ESA_LAUNCH_CHECK();
+  return ESA_OK;
+}
+
 // Scratch of esa_varlen_attn_fwd_noalloc: a file-scope device array, one
 // copy per GPU, held until the process ends.  Host code never passes the
 // array's name (a host-side stand-in) to a kernel: it passes the device
 // address hipGetSymbolAddress returns, looked up once per device on the
 // first call with that device current.
-constexpr size_t kNoAllocScratchBytes = size_t(4) << 20;
+constexpr size_t kNoAllocScratchBytes = size_t(16) << 20;
 __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 
 constexpr int kMaxDevices = 64;
@@ -1321,8 +2173,8 @@ int esa_varlen_attn_fwd(const void* q, const void* k, const void* v, const int* 
     pa.nodes = reinterpret_cast<int2*>(ws + L.nodes);
     pa.meta = reinterpret_cast<int4*>(ws + L.meta);
   }
-  if ((rc = launch_prep(pa, true, masked, st))) return rc;
-  const unsigned grid = (unsigned)groups_of(total_q) * (unsigned)heads;
+  if (masked && !f32) pa.over_count = reinterpret_cast<int*>(ws + L.over_count);
+  if ((rc = launch_prep(pa, true, masked, st, masked && !f32))) return rc;
 
   if (f32) {
     AttnF32Args a{};
@@ -1350,8 +2202,21 @@ int esa_varlen_attn_fwd(const void* q, const void* k, const void* v, const int* 
   a.plan = pa.plan_q; a.bounds = pa.bounds_q;
   a.nodes = pa.nodes; a.meta = pa.meta;
   a.o = static_cast<bf16*>(out); a.lse_out = softmax_lse;
-  const unsigned egrid = (unsigned)groups_of(total_q) * (unsigned)((heads + kEdgeHeads - 1) / kEdgeHeads);
-  ESA_TIMED(esa_profile::kAttnFwdMasked, st, hipLaunchKernelGGL(edge_fwd_kernel, dim3(egrid), dim3(256), 0, st, a));
+  if ((rc = launch_lists(pa, L, ws, true, false, st))) return rc;
+  const unsigned n_hg = (unsigned)((heads + kListHeads - 1) / kListHeads);
+  const unsigned n_hg_walk = (unsigned)((heads + kEdgeHeads - 1) / kEdgeHeads);
+  a.info = reinterpret_cast<const int*>(ws + L.info[0]);
+  a.ids = reinterpret_cast<const int*>(ws + L.ids[0]);
+  a.bits = reinterpret_cast<const uint32_t*>(ws + L.bits[0]);
+  a.kbound = reinterpret_cast<const float*>(ws + L.kbound);
+  const unsigned n_hq = (n_hg + kWaves - 1) / kWaves;
+  ESA_TIMED(esa_profile::kAttnFwdMasked, st,
+            hipLaunchKernelGGL(list_fwd_kernel, dim3(list_tile_blocks(total_q, n_hq)), dim3(256), 0, st, a));
+  ESA_LAUNCH_CHECK();
+  a.plan = reinterpret_cast<const int4*>(ws + L.over[0]);
+  a.count = reinterpret_cast<const int*>(ws + L.over_count);
+  ESA_TIMED(esa_profile::kAttnEdgeOverflow, st,
+            hipLaunchKernelGGL(edge_fwd_kernel, dim3(overflow_blocks(total_q) * n_hg_walk), dim3(256), 0, st, a));
   ESA_LAUNCH_CHECK();
   return ESA_OK;
 }
@@ -1462,10 +2327,9 @@ int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k, const vo
     pa.tok_src = mask_a; pa.tok_dst = mask_b;
     pa.nodes = reinterpret_cast<int2*>(ws + L.nodes);
     pa.meta = reinterpret_cast<int4*>(ws + L.meta);
+    if (!f32) pa.over_count = reinterpret_cast<int*>(ws + L.over_count);
   }
-  if ((rc = launch_prep(pa, false, masked, st))) return rc;
-  const unsigned kgrid = (unsigned)groups_of(total_k) * (unsigned)heads;
-  const unsigned qgrid = (unsigned)groups_of(total_q) * (unsigned)heads;
+  if ((rc = launch_prep(pa, false, masked, st, masked && !f32))) return rc;
 
   if (f32) {
     AttnF32Args a{};
@@ -1504,17 +2368,45 @@ int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k, const vo
   a.nodes = pa.nodes; a.meta = pa.meta;
   a.dq = static_cast<bf16*>(dq); a.dk = static_cast<bf16*>(dk); a.dv = static_cast<bf16*>(dv);
 
-  a.plan = pa.plan_k;
-  a.bounds = pa.bounds_k;
-  const unsigned ekgrid = (unsigned)groups_of(total_k) * (unsigned)((heads + kEdgeHeadsKv - 1) / kEdgeHeadsKv);
-  ESA_TIMED(esa_profile::kAttnBwdDkdvMasked, st,
-            hipLaunchKernelGGL(edge_dkdv_kernel, dim3(ekgrid), dim3(256), 0, st, a));
-  ESA_LAUNCH_CHECK();
+  // Equal cu_seqlens pointers: the query and key segments coincide, the mask
+  // is symmetric and the key tiles use the query tiles' lists.
+  const bool symmetric = cu_seqlens_q == cu_seqlens_k;
+  if ((rc = launch_lists(pa, L, ws, false, !symmetric, st))) return rc;
+  const int kd = symmetric ? 0 : 1;
+  const int* over_count = reinterpret_cast<const int*>(ws + L.over_count);
 
+  // dQ first: the key-list dQ pass writes the row statistics the dK/dV passes read.
+  const unsigned n_hg = (unsigned)((heads + kListHeads - 1) / kListHeads);
+  const unsigned n_hg_walk = (unsigned)((heads + kEdgeHeads - 1) / kEdgeHeads);
+  a.aux_out = pa.aux;
   a.plan = pa.plan_q;
   a.bounds = pa.bounds_q;
-  const unsigned eqgrid = (unsigned)groups_of(total_q) * (unsigned)((heads + kEdgeHeads - 1) / kEdgeHeads);
-  ESA_TIMED(esa_profile::kAttnBwdDqMasked, st, hipLaunchKernelGGL(edge_dq_kernel, dim3(eqgrid), dim3(256), 0, st, a));
+  a.info = reinterpret_cast<const int*>(ws + L.info[0]);
+  a.ids = reinterpret_cast<const int*>(ws + L.ids[0]);
+  a.bits = reinterpret_cast<const uint32_t*>(ws + L.bits[0]);
+  ESA_TIMED(esa_profile::kAttnBwdDqMasked, st,
+            hipLaunchKernelGGL(list_dq_kernel, dim3(list_blocks(total_q, n_hg)), dim3(256), 0, st, a));
+  ESA_LAUNCH_CHECK();
+  a.plan = reinterpret_cast<const int4*>(ws + L.over[0]);
+  a.count = over_count;
+  ESA_TIMED(esa_profile::kAttnEdgeOverflow, st,
+            hipLaunchKernelGGL(edge_dq_kernel, dim3(overflow_blocks(total_q) * n_hg_walk), dim3(256), 0, st, a));
+  ESA_LAUNCH_CHECK();
+
+  const unsigned n_hg_kv = (unsigned)((heads + kListHeadsKv - 1) / kListHeadsKv);
+  const unsigned n_hg_kv_walk = (unsigned)((heads + kEdgeHeadsKv - 1) / kEdgeHeadsKv);
+  a.plan = pa.plan_k;
+  a.bounds = pa.bounds_k;
+  a.info = reinterpret_cast<const int*>(ws + L.info[kd]);
+  a.ids = reinterpret_cast<const int*>(ws + L.ids[kd]);
+  a.bits = reinterpret_cast<const uint32_t*>(ws + L.bits[kd]);
+  ESA_TIMED(esa_profile::kAttnBwdDkdvMasked, st,
+            hipLaunchKernelGGL(list_dkdv_kernel, dim3(list_blocks(total_k, n_hg_kv)), dim3(256), 0, st, a));
+  ESA_LAUNCH_CHECK();
+  a.plan = reinterpret_cast<const int4*>(ws + L.over[kd]);
+  a.count = over_count + kd;
+  ESA_TIMED(esa_profile::kAttnEdgeOverflow, st,
+            hipLaunchKernelGGL(edge_dkdv_kernel, dim3(overflow_blocks(total_k) * n_hg_kv_walk), dim3(256), 0, st, a));
   ESA_LAUNCH_CHECK();
   return ESA_OK;
 }

@@ -26,6 +26,8 @@ enum Kernel : int {
   kLayerNormFwd,    // block prologue: pre-norm
   kLayerNormBwd,
   kColumnSum,       // Linear bias gradients
+  kAttnEdgeLists,   // edge-mask key lists
+  kAttnEdgeOverflow,  // edge-mask walk kernels over the overflow groups
   kNumKernels
 };
 

@@ -27,11 +27,12 @@ def _inputs(tq, tk, seed, heads=H):
     return q, k, v, g
 
 
-def _run(device, q, k, v, g, cu_q, cu_k, src=None, dst=None, scale=0.25):
+def _run(device, q, k, v, g, cu_q, cu_k, src=None, dst=None, scale=0.25, shared_cu=False):
     qd, kd, vd = (t.to(device).requires_grad_(True) for t in (q, k, v))
     gd = g.to(device)
     cq = torch.as_tensor(cu_q, dtype=torch.int32).to(device)
-    ck = torch.as_tensor(cu_k, dtype=torch.int32).to(device)
+    # One cu_seqlens tensor for queries and keys (as self-attention modules pass it) or two equal ones.
+    ck = cq if shared_cu else torch.as_tensor(cu_k, dtype=torch.int32).to(device)
     s = None if src is None else torch.as_tensor(src, dtype=torch.int32).to(device)
     d = None if dst is None else torch.as_tensor(dst, dtype=torch.int32).to(device)
     mq = int(np.diff(cu_q).max()) if len(cu_q) > 1 else 0
@@ -42,10 +43,10 @@ def _run(device, q, k, v, g, cu_q, cu_k, src=None, dst=None, scale=0.25):
     return out.detach().cpu(), qd.grad.cpu(), kd.grad.cpu(), vd.grad.cpu()
 
 
-def _check(device, lengths_q, lengths_k, seed, src=None, dst=None, heads=H, check_lse=True):
+def _check(device, lengths_q, lengths_k, seed, src=None, dst=None, heads=H, check_lse=True, shared_cu=False):
     cu_q, cu_k = cu_from_lengths(lengths_q), cu_from_lengths(lengths_k)
     q, k, v, g = _inputs(int(cu_q[-1]), int(cu_k[-1]), seed, heads)
-    out, dq, dk, dv = _run(device, q, k, v, g, cu_q, cu_k, src, dst)
+    out, dq, dk, dv = _run(device, q, k, v, g, cu_q, cu_k, src, dst, shared_cu=shared_cu)
     ref, lse_ref = OA.varlen_attention(q, k, v, cu_q, cu_k, 0.25, src, dst)
     assert_bf16_close(out, ref, what="out")
     if check_lse:
@@ -127,12 +128,37 @@ def test_masked_segments_straddle_tiles(device):
 
 def test_masked_star_graph_far_partner_tiles(device):
     """A star graph (hub 0 and 1,200 leaves, both edge directions): every edge shares the hub, so the edge mask
-    is dense over one 2,400-token segment of 75 tiles and the far partner tiles of each tile lie past the
-    precomputed mask words' 64-tile window (those pairs take the in-kernel predicate)."""
+    is dense over one 2,400-token segment of 75 tiles.  Every tile's partner union (2,399 tokens) is past the
+    key-list capacity, so all groups take the walk kernels over the overflow list."""
     leaves = np.arange(1, 1201, dtype=np.int32)
     src = np.concatenate([np.zeros_like(leaves), leaves])
     dst = np.concatenate([leaves, np.zeros_like(leaves)])
     _check(device, [src.size], [src.size], seed=77, src=src, dst=dst)
+
+
+@pytest.mark.parametrize("shared_cu", [False, True])
+def test_masked_mixed_overflow(device, shared_cu):
+    """Protein-like graphs around a 600-token star segment: the star's groups overflow the key lists (walk
+    kernels), the others take the lists, in one call; with one cu_seqlens tensor for queries and keys the
+    dK/dV pass reads the query tiles' lists (symmetric mask), with two it builds the key tiles' own."""
+    gb = generators.protein_like(seed=12, num_graphs=4, n_min=64, n_max=160)
+    src_p, dst_p = gb.edge_index[0].astype(np.int32), gb.edge_index[1].astype(np.int32)
+    hub = int(max(src_p.max(), dst_p.max())) + 1
+    leaves = np.arange(hub + 1, hub + 301, dtype=np.int32)
+    star_s = np.concatenate([np.full_like(leaves, hub), leaves])
+    star_d = np.concatenate([leaves, np.full_like(leaves, hub)])
+    c = gb.edge_counts
+    src = np.concatenate([src_p[:c[0] + c[1]], star_s, src_p[c[0] + c[1]:]])
+    dst = np.concatenate([dst_p[:c[0] + c[1]], star_d, dst_p[c[0] + c[1]:]])
+    lengths = [int(c[0]), int(c[1]), star_s.size, int(c[2]), int(c[3])]
+    _check(device, lengths, lengths, seed=78, src=src, dst=dst, shared_cu=shared_cu)
+
+
+def test_masked_shared_cu_protein(device):
+    """The symmetric-mask path (one cu_seqlens tensor) on protein-like graphs with ragged segment ends."""
+    gb = generators.protein_like(seed=13, num_graphs=5, n_min=40, n_max=200)
+    src, dst = gb.edge_index[0].astype(np.int32), gb.edge_index[1].astype(np.int32)
+    _check(device, gb.edge_counts, gb.edge_counts, seed=79, src=src, dst=dst, shared_cu=True)
 
 
 def test_masked_isolated_rows_give_zero(device):
