@@ -46,6 +46,7 @@ extern "C" {
 #define ESA_MASK_NONE 0
 #define ESA_MASK_EDGE 1
 #define ESA_MASK_NODE 2
+#define ESA_MASK_EDGE_PLAN 3
 
 /* Library version and build target, e.g. "esa_hip 0.1 gfx950". */
 ESA_API const char* esa_version(void);
@@ -68,8 +69,12 @@ ESA_API const char* esa_version(void);
 /* i != j and {src_i, dst_i} and {src_j, dst_j} share a node — the predicate */
 /* of create_edge_adjacency_mask (esa/masked_layers.py:121-142) that          */
 /* get_adj_mask_from_edge_index_edge (:217-268) turns into a 0 / -99999      */
-/* bias.  It is evaluated on the fly; no mask is stored.  n_mask_edges is    */
-/* unused.  ESA_MASK_NONE: mask_a, mask_b unused.                            */
+/* bias.  No E x E mask is stored: the call builds an edge-mask plan (below) */
+/* in its workspace.  n_mask_edges is unused.                                */
+/*                                                                           */
+/* mask_kind ESA_MASK_EDGE_PLAN: the same mask from a plan built once by     */
+/* esa_edge_plan_build with the same cu_seqlens pointers; mask_a = the plan */
+/* (cast), mask_b unused.  ESA_MASK_NONE: mask_a, mask_b unused.             */
 /*                                                                           */
 /* mask_kind ESA_MASK_NODE: a CSR adjacency by query, mask_a = indptr        */
 /* [total_q + 1], mask_b = indices [n_mask_edges] (key token ids); query i   */
@@ -84,6 +89,26 @@ ESA_API const char* esa_version(void);
 /*                                                                           */
 /* softmax_lse is [heads, total_q] fp32 (natural log), as flash-attn's.      */
 /* ------------------------------------------------------------------------ */
+/* ------------------------------------------------------------------------ */
+/* Edge-mask plan: the per-batch data of the ESA_MASK_EDGE mask (packed node */
+/* pairs, per-tile node metadata, per-token segment bounds, and per 32-token */
+/* tile the union of its admissible partners with one mask bit per token and */
+/* partner), built once and read by every attention call over the same       */
+/* tokens and segments.  It replaces the [B, N, N] bias that                 */
+/* get_adj_mask_from_edge_index_edge (esa/masked_layers.py:217-268) builds   */
+/* once per batch and every masked layer reads (esa/masked_layers.py:849-    */
+/* 936).  `symmetric`: the attention calls pass one pointer as both          */
+/* cu_seqlens (self-attention over one segment array); otherwise the plan   */
+/* also holds the key tiles' lists.  The build uses the pointer equality of  */
+/* its own cu_seqlens arguments; later calls must pass the same arrays.      */
+/* The plan stays valid while tok_src / tok_dst / cu_seqlens are unchanged.  */
+/* ------------------------------------------------------------------------ */
+ESA_API int esa_edge_plan_size(int total_q, int total_k, int symmetric, size_t* bytes);
+ESA_API int esa_edge_plan_build(const int* tok_src, const int* tok_dst,
+                        const int* cu_seqlens_q, const int* cu_seqlens_k,
+                        int batch, int total_q, int total_k,
+                        void* plan, size_t plan_bytes, void* stream);
+
 ESA_API int esa_varlen_attn_workspace_size(int total_q, int total_k, int heads,
                                    int head_dim, int dtype, int mask_kind,
                                    int n_mask_edges, int backward,

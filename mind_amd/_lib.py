@@ -23,6 +23,7 @@ ESA_BF16 = 1
 ESA_MASK_NONE = 0
 ESA_MASK_EDGE = 1
 ESA_MASK_NODE = 2
+ESA_MASK_EDGE_PLAN = 3
 
 ERRORS = {
     -1: "ESA_ERR_NULL (a required pointer is null)",
@@ -67,6 +68,8 @@ _PROTOS = {
     "esa_csr_build": (_c_int, [_vp, _c_i64, _c_int, _vp, _vp, _vp, _c_sz, _vp]),
     "esa_csr_segment_sum": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _vp]),
     "esa_token_budget_pack_workspace_size": (_c_int, [_c_int, ctypes.POINTER(_c_sz)]),
+    "esa_edge_plan_size": (_c_int, [_c_int, _c_int, _c_int, ctypes.POINTER(_c_sz)]),
+    "esa_edge_plan_build": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _c_sz, _vp]),
     # counts num_graphs budget | batch_of_graph batch_start num_batches ws bytes stream
     "esa_token_budget_pack": (_c_int, [_vp, _c_int, _c_i64, _vp, _vp, _vp, _vp, _c_sz, _vp]),
     "esa_edge_gather_bwd": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _vp]),

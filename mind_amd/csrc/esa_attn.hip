@@ -66,16 +66,6 @@
 namespace {
 
 
-// Partner-tile range of a 128-token group: from the segment of its first
-// token to the segment of its last valid token.
-DEVI void group_range(const int* cu_outer, const int* cu_inner, int nseg, int total_outer, int t0, int& beg,
-                      int& end) {
-  const int last = min(t0 + kGroupTok - 1, total_outer - 1);
-  const int s0 = seg_of(cu_outer, nseg, t0), s1 = seg_of(cu_outer, nseg, last);
-  beg = (cu_inner[s0] >> 5);
-  end = max(beg, ((cu_inner[s1 + 1] + kTile - 1) >> 5));
-}
-
 // The outer tile a wave owns: per-lane partner range and wave-level bounds.
 struct OuterTile {
   bool active;         // tile starts before `total`
@@ -225,7 +215,11 @@ struct AttnArgs {
   const int* info;          // key lists: per outer tile, the number of partners (-1: group overflowed)
   const int* ids;           // key lists: per outer tile, kListCap partner token ids (-1 pads)
   const uint32_t* bits;     // key lists: per outer tile, [kListCap / 32][32] mask words
-  const float* kbound;      // key-list forward: per (query tile, head) max |k| over its candidate partner tiles
+  // Edge plans: the key tiles' own lists and overflow groups, used by the dK/dV
+  // passes unless *sym (the plan's flag: query and key segments coincide, the
+  // mask is symmetric and the query tiles' lists serve the key tiles).
+  const int* sym;
+  const int* kinfo; const int* kids; const uint32_t* kbits; const int4* kover; const int* kcount;
   bf16* o; float* lse_out;  // forward outputs
   bf16* dq; bf16* dk; bf16* dv;
 };
@@ -688,7 +682,12 @@ DEVI void edge_dkdv_group(const AttnArgs& a, int item, int hg) {
 }
 
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ESA_EDGE_WAVES_DKDV))) void edge_dkdv_kernel(
-    const AttnArgs a) {
+    const AttnArgs a0) {
+  AttnArgs a = a0;
+  if (a0.sym && !*a0.sym) {   // the key tiles' own overflow groups
+    a.plan = a0.kover;
+    a.count = a0.kcount;
+  }
   const int n_hg = (a.heads + kEdgeHeadsKv - 1) / kEdgeHeadsKv, hg = blockIdx.x % n_hg;
   const int n_items = *a.count;
   for (int item = blockIdx.x / n_hg; item < n_items; item += gridDim.x / n_hg) edge_dkdv_group(a, item, hg);
@@ -717,8 +716,6 @@ static_assert(kListCap % kTile == 0, "list capacity in whole tiles");
 
 struct ListArgs {
   const int2* nodes; const int4* meta;
-  const float* knorm; int kn_tiles, heads;   // forward: max |k| per (head, key tile), [heads][kn_tiles]
-  float* kbound;                             // forward: per (query tile, head) max of knorm over its candidates
   int total, n_groups;          // outer (= partner) tokens and 128-token groups per direction
   const int2* bounds[2];        // per outer token: partner range of its segment (0: queries, 1: keys)
   int* info[2]; int* ids[2]; uint32_t* bits[2];
@@ -839,7 +836,6 @@ __global__ __launch_bounds__(256) void edge_lists_kernel(const ListArgs a) {
     };
     int* out_ids = a.ids[dir] + (size_t)tile * kListCap;
     uint32_t* out_bits = a.bits[dir] + (size_t)tile * kListCap;
-    float kbm = 0.f;   // lane h: max |k| of head h over the candidate partner tiles
     constexpr int kSteps = 8;   // steps (two candidates each) whose node loads are in flight together
     for (int base = ot.pt_beg; base < ot.pt_end; base += kBatch) {
       const int x = base + lane;
@@ -849,16 +845,6 @@ __global__ __launch_bounds__(256) void edge_lists_kernel(const ListArgs a) {
       if (n == 0) continue;
       if (need) sCand[wave][__popcll(cand & ((1ull << lane) - 1ull))] = x;
       wave_sync();
-      if (a.kbound && lane < a.heads) {   // lane = head: max |k| over the candidates
-        const float* kn = a.knorm + (size_t)lane * a.kn_tiles;
-        for (int i0 = 0; i0 < n; i0 += 8) {
-          float v[8];
-#pragma unroll
-          for (int j = 0; j < 8; ++j) v[j] = i0 + j < n ? kn[sCand[wave][i0 + j]] : 0.f;
-#pragma unroll
-          for (int j = 0; j < 8; ++j) kbm = fmaxf(kbm, v[j]);
-        }
-      }
       // A: candidate i = 2 r + half, its token col
       for (int r0 = 0; 2 * r0 < n; r0 += kSteps) {
         int2 pn[kSteps];
@@ -919,8 +905,6 @@ __global__ __launch_bounds__(256) void edge_lists_kernel(const ListArgs a) {
       }
       const int padded = (count + kTile - 1) & ~(kTile - 1);
       if (lane < padded - count) out_ids[count + lane] = -1;
-      if (a.kbound)
-        for (int h = lane; h < a.heads; h += 64) a.kbound[(size_t)tile * a.heads + h] = h < 64 ? kbm : INFINITY;
     }
   }
   if (over && lane == 0) s_over = 1;
@@ -1102,10 +1086,8 @@ DEVI int list_block_ids(const AttnArgs& a, int tile, int* sid, int tid) {
 }
 
 // Forward over the key lists: one wave = one 32-query tile and kListHeads
-// heads; the bias of a compact tile seeds every head's score MFMA.  The
-// softmax takes the fixed reference of the walk kernels when the bound
-// c |q| max|k| (max |k| over the tile's candidate partner tiles, from the
-// list pass) is at most 60 on every lane, else a running max.
+// heads; the bias of a compact tile seeds every head's score MFMA; online
+// softmax (running max per query, rescaled when it grows).
 __global__ __launch_bounds__(256) void list_fwd_kernel(const AttnArgs a) {
   constexpr int NH = kListHeads;
   __shared__ __align__(16) bf16 sK[kWaves][kDmaDepth][NH][2 * kTileHalf];   // K rows split by dims half
@@ -1125,12 +1107,10 @@ __global__ __launch_bounds__(256) void list_fwd_kernel(const AttnArgs a) {
   const bool valid = oi < a.total_q;
   const int oc = valid ? oi : a.total_q - 1;
   bf16x8 qf[NH];
-  float kb[NH];
 #pragma unroll
   for (int u = 0; u < NH; ++u) {
     const int hc = min(max(h0, 0) + u, H - 1);
     qf[u] = *reinterpret_cast<const bf16x8*>(a.q + ((size_t)oc * H + hc) * kHd + 8 * half);
-    kb[u] = a.kbound[(size_t)tile * H + hc];
   }
   const int nct = list_block_ids(a, tile, sId, tid);
   if (nct < 0 || nh <= 0) return;
@@ -1143,22 +1123,12 @@ __global__ __launch_bounds__(256) void list_fwd_kernel(const AttnArgs a) {
     return;
   }
   bf16x8 qh[NH], ql[NH];
-  float bmax = 0.f;
-#pragma unroll
-  for (int u = 0; u < NH; ++u) {
-    float qq = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) qq = fmaf((float)qf[u][e], (float)qf[u][e], qq);
-    qq = halves_sum(qq);
-    bmax = fmaxf(bmax, valid ? a.c * sqrtf(qq) * kb[u] : 0.f);
-    split_scaled(qf[u], a.c, qh[u], ql[u]);
-  }
-  const bool fixed_ref = __builtin_amdgcn_readfirstlane((int)(wave_max(bmax) <= kStaticBound)) != 0;
   float m_run[NH];
   f32x16 acc[NH];
 #pragma unroll
   for (int u = 0; u < NH; ++u) {
-    m_run[u] = fixed_ref ? 0.f : -INFINITY;
+    split_scaled(qf[u], a.c, qh[u], ql[u]);
+    m_run[u] = -INFINITY;
     acc[u] = f32x16{};
   }
   const uint32_t kv_bytes = (uint32_t)a.total_k * H * kHd * 2;
@@ -1183,26 +1153,21 @@ __global__ __launch_bounds__(256) void list_fwd_kernel(const AttnArgs a) {
           if (u >= nh) break;   // wave-uniform
           const bf16x8 kr = half_row8<kTileHalf>(sK[wave][buf][u], kperm(col), half);
           const f32x16 s = mfma32(kr, ql[u], mfma32(kr, qh[u], bias));
-          float p[16];
-          if (fixed_ref) {
+          float mt = s[0];
 #pragma unroll
-            for (int r = 0; r < 16; ++r) p[r] = fast_exp2(s[r]);
-          } else {
-            float mt = s[0];
+          for (int r = 1; r < 16; ++r) mt = fmaxf(mt, s[r]);
+          mt = halves_max(mt);
+          const float m_new = fmaxf(m_run[u], mt);
+          if (__ballot(m_new > m_run[u])) {
+            const float alpha = fast_exp2(m_run[u] - (m_new == -INFINITY ? 0.f : m_new));
 #pragma unroll
-            for (int r = 1; r < 16; ++r) mt = fmaxf(mt, s[r]);
-            mt = halves_max(mt);
-            const float m_new = fmaxf(m_run[u], mt);
-            if (__ballot(m_new > m_run[u])) {
-              const float alpha = fast_exp2(m_run[u] - (m_new == -INFINITY ? 0.f : m_new));
-#pragma unroll
-              for (int r = 0; r < 16; ++r) acc[u][r] *= alpha;
-              m_run[u] = m_new;
-            }
-            const float m_use = m_run[u] == -INFINITY ? 0.f : m_run[u];
-#pragma unroll
-            for (int r = 0; r < 16; ++r) p[r] = fast_exp2(s[r] - m_use);
+            for (int r = 0; r < 16; ++r) acc[u][r] *= alpha;
+            m_run[u] = m_new;
           }
+          const float m_use = m_run[u] == -INFINITY ? 0.f : m_run[u];
+          float p[16];
+#pragma unroll
+          for (int r = 0; r < 16; ++r) p[r] = fast_exp2(s[r] - m_use);
           bf16x8 vt0, vt1;
           tr_rows32<kTileHalf>(sV[wave][buf][u], 0, sOnes, c16, grp, vt0, vt1);
           acc[u] = mfma32(vt0, cvt8(p), acc[u]);
@@ -1341,7 +1306,13 @@ struct StageListKv { i32x4 q[NH], d[NH]; uint2 x[(NH + 1) / 2]; uint32_t w; };
 // the walk kernel's dK/dV pass.  Lanes of half j load the row statistics of
 // head 2 i + j of the partner queries.
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ESA_LIST_WAVES_DKDV))) void list_dkdv_kernel(
-    const AttnArgs a) {
+    const AttnArgs a0) {
+  AttnArgs a = a0;
+  if (!*a0.sym) {   // the key tiles' own lists
+    a.info = a0.kinfo;
+    a.ids = a0.kids;
+    a.bits = a0.kbits;
+  }
   constexpr int NH = kListHeadsKv;
   __shared__ __align__(16) bf16 sQ[kWaves][2][NH][2 * kTileHalf];    // Q rows split by dims half
   __shared__ __align__(16) bf16 sDO[kWaves][2][NH][2 * kTileHalf];   // dO rows split by dims half
@@ -1678,90 +1649,30 @@ __global__ __launch_bounds__(kF32Threads) void attn_dkdv_f32_kernel(const AttnF3
 }
 
 // ======================================================================== prep kernel
-// Everything the attention kernels need besides q, k, v (per-call metadata)
-// is built by one launch whose blocks split into independent tasks: a plan
-// per direction (one block each), per-tile key norms (forward), row
-// statistics (backward), per-token segment bounds and, in masked mode, the
-// packed node pairs and per-tile node metadata.  Blocks are dispatched in
-// enum order: the latency-bound tasks (the one-block plans, the per-tile
-// metadata, the small per-token tables) come first, so they run beside the
-// bandwidth-bound key norms and row statistics instead of after them.
+// One launch whose blocks split into independent tasks.  Per call (fp32
+// kernels): a per-segment plan per direction (one block each) and the row
+// statistics of the backward pass.  Edge-mask plan build: the packed node
+// pairs and per-tile node metadata, the per-token segment bounds of both
+// directions, the plan's flag and zero overflow counts.  Blocks are
+// dispatched in enum order: the latency-bound tasks (the one-block plans,
+// the per-tile metadata, the small per-token tables) come first, so they run
+// beside the bandwidth-bound row statistics instead of after them.
 
-enum PrepTask { kPlanQ, kPlanK, kMeta, kNodes, kBoundsQ, kBoundsK, kKnorm, kRows, kPrepTasks };
+enum PrepTask { kPlanQ, kPlanK, kMeta, kNodes, kBoundsQ, kBoundsK, kRows, kPrepTasks };
 
 struct PrepArgs {
   const int* cu_q; const int* cu_k; int nseg;
   int total_q, total_k, heads, tq_pad, tk_pad;
-  int4* plan_q; int4* plan_k;          // plan_k: backward only
-  int* count_q; int* count_k;          // fp32: per-segment plans (seg_plan_block) and their group counts
-  int2* bounds_q; int2* bounds_k;      // bounds_k: backward only
-  const bf16* k; float* knorm;         // forward
+  int4* plan_q; int4* plan_k;          // fp32: per-segment plans (seg_plan_block), plan_k backward only
+  int* count_q; int* count_k;          // fp32: their group counts
+  int2* bounds_q; int2* bounds_k;      // edge plan
   const bf16* dout; const bf16* out; const float* lse; float c; uint2* aux;   // backward (bf16)
   const float* dout_f; const float* out_f; float2* rows_f;                  // backward (fp32)
   const int* tok_src; const int* tok_dst; int2* nodes; int4* meta;          // masked
-  int* over_count;                     // bf16 masked: the two overflow-list counts, zeroed here
+  int* over_count;                     // edge plan: the two overflow-list counts, zeroed here
+  int* flags; int sym;                 // edge plan: flags[0] = sym (query and key segments coincide)
   int nb[kPrepTasks];                  // blocks per task, in dispatch order
 };
-
-// Longest-first order of the 128-token outer groups by the number of partner
-// tiles they visit (capped at 1023): a counting sort in one block.
-// plan[i] = (group, first partner tile, end partner tile, 0).  Groups with
-// equal counts may come in any order: every group's outputs are computed by
-// one block, so the order changes no result, only the schedule.  The
-// cu_seqlens arrays are staged in LDS when they fit (kCuCap entries), so the
-// per-group segment searches do not wait on memory.
-constexpr int kCuCap = 2048;
-
-DEVI void plan_block(const int* __restrict__ cu_outer_g, const int* __restrict__ cu_inner_g, int nseg,
-                     int total_outer, int4* __restrict__ plan, int tid) {
-  constexpr int NB = 1024, PER = NB / 256;
-  __shared__ int hist[NB];
-  __shared__ int part[256];
-  __shared__ int scu[2][kCuCap];
-  const int n_groups = (total_outer + kGroupTok - 1) / kGroupTok;
-  const bool staged = nseg + 1 <= kCuCap;
-  if (staged) {
-    for (int i = tid; i <= nseg; i += 256) {
-      scu[0][i] = cu_outer_g[i];
-      scu[1][i] = cu_inner_g[i];
-    }
-  }
-  for (int i = tid; i < NB; i += 256) hist[i] = 0;
-  __syncthreads();
-  const int* cu_outer = staged ? scu[0] : cu_outer_g;
-  const int* cu_inner = staged ? scu[1] : cu_inner_g;
-  auto bucket = [&](int beg, int end) { return NB - 1 - min(end - beg, NB - 1); };
-  for (int g = tid; g < n_groups; g += 256) {
-    int beg, end;
-    group_range(cu_outer, cu_inner, nseg, total_outer, g * kGroupTok, beg, end);
-    atomicAdd(&hist[bucket(beg, end)], 1);
-  }
-  __syncthreads();
-  int loc[PER], sum = 0;
-#pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    loc[i] = sum;
-    sum += hist[tid * PER + i];
-  }
-  part[tid] = sum;
-  __syncthreads();
-  for (int off = 1; off < 256; off <<= 1) {
-    const int add = tid >= off ? part[tid - off] : 0;
-    __syncthreads();
-    part[tid] += add;
-    __syncthreads();
-  }
-  const int base = part[tid] - sum;
-#pragma unroll
-  for (int i = 0; i < PER; ++i) hist[tid * PER + i] = base + loc[i];
-  __syncthreads();
-  for (int g = tid; g < n_groups; g += 256) {
-    int beg, end;
-    group_range(cu_outer, cu_inner, nseg, total_outer, g * kGroupTok, beg, end);
-    plan[atomicAdd(&hist[bucket(beg, end)], 1)] = make_int4(g, beg, end, 0);
-  }
-}
-
 
 // Row statistics of the dK/dV pass, as bf16 (hi, lo) pairs (x = hi + lo to
 // ~2^-16 relative): aux.x for -LSE2/c (LSE2 = log2(e) LSE), aux.y for
@@ -1839,14 +1750,12 @@ __global__ __launch_bounds__(256) void prep_kernel(const PrepArgs p) {
   const int tid = threadIdx.x;
   int b = blockIdx.x;
   if (b < p.nb[kPlanQ]) {
-    if (p.count_q) seg_plan_block(p.cu_q, p.cu_k, p.nseg, kGroupTok, p.plan_q, p.count_q, tid);
-    else plan_block(p.cu_q, p.cu_k, p.nseg, p.total_q, p.plan_q, tid);
+    seg_plan_block(p.cu_q, p.cu_k, p.nseg, kGroupTok, p.plan_q, p.count_q, tid);
     return;
   }
   b -= p.nb[kPlanQ];
   if (b < p.nb[kPlanK]) {
-    if (p.count_k) seg_plan_block(p.cu_k, p.cu_q, p.nseg, kGroupTok, p.plan_k, p.count_k, tid);
-    else plan_block(p.cu_k, p.cu_q, p.nseg, p.total_k, p.plan_k, tid);
+    seg_plan_block(p.cu_k, p.cu_q, p.nseg, kGroupTok, p.plan_k, p.count_k, tid);
     return;
   }
   b -= p.nb[kPlanK];
@@ -1857,7 +1766,8 @@ __global__ __launch_bounds__(256) void prep_kernel(const PrepArgs p) {
   }
   b -= p.nb[kMeta];
   if (b < p.nb[kNodes]) {
-    if (b == 0 && p.over_count && tid < 2) p.over_count[tid] = 0;
+    if (b == 0 && tid < 2) p.over_count[tid] = 0;
+    if (b == 0 && tid == 0) p.flags[0] = p.sym;
     const int t = b * 256 + tid;
     if (t < p.tq_pad) p.nodes[t] = t < p.total_q ? make_int2(p.tok_src[t], p.tok_dst[t]) : make_int2(-1, -1);
     return;
@@ -1867,8 +1777,6 @@ __global__ __launch_bounds__(256) void prep_kernel(const PrepArgs p) {
   b -= p.nb[kBoundsQ];
   if (b < p.nb[kBoundsK]) { bounds_item(p.cu_k, p.cu_q, p.nseg, p.total_k, p.tk_pad, p.bounds_k, b * 256 + tid); return; }
   b -= p.nb[kBoundsK];
-  if (b < p.nb[kKnorm]) { knorm_block(p.k, p.total_k, p.heads, p.tk_pad / kTile, p.knorm, b, tid); return; }
-  b -= p.nb[kKnorm];
   if (b < p.nb[kRows]) rowstats_item(p, (long)b * 256 + tid);
 }
 
@@ -1928,51 +1836,88 @@ size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 int round32(int x) { return (x + kTile - 1) / kTile * kTile; }
 int groups_of(int total) { return (total + kGroupTok - 1) / kGroupTok; }
 
-struct WsLayout {
-  size_t knorm = 0, kbound = 0, aux = 0, plan_q = 0, plan_k = 0, bounds_q = 0, bounds_k = 0, nodes = 0, meta = 0;
-  size_t over_count = 0, info[2] = {0, 0}, ids[2] = {0, 0}, bits[2] = {0, 0}, over[2] = {0, 0};
+// ---- edge-mask plans
+// The per-batch data of the share-an-endpoint mask, shared by every attention
+// call over the same tokens and segments (the reference builds its mask once
+// per batch and passes it to every masked layer): the packed node pairs, the
+// per-tile node metadata, the per-token partner ranges of both directions,
+// the key lists of the query tiles and, when the query and key segments are
+// not the same array, of the key tiles, with their overflow groups.  The key
+// tiles' lists come last, so their offsets do not depend on whether they
+// exist; a flag word tells the dK/dV passes which lists to read.
+struct PlanLayout {
+  size_t flags = 0, nodes = 0, meta = 0, bounds_q = 0, bounds_k = 0, over_count = 0;
+  size_t info[2] = {0, 0}, ids[2] = {0, 0}, bits[2] = {0, 0}, over[2] = {0, 0};
   size_t total = 0;
 };
 
-WsLayout ws_layout(int total_q, int total_k, int heads, int dtype, bool masked, bool backward) {
-  WsLayout L;
+PlanLayout plan_layout(int total_q, int total_k, bool key_lists) {
+  PlanLayout P;
   const int tqp = round32(total_q), tkp = round32(total_k);
-  const bool lists = masked && dtype == ESA_BF16;
   size_t off = 0;
-  if (!backward) {
-    if (dtype == ESA_BF16) { L.knorm = off; off += align256((size_t)heads * (tkp / kTile) * 4); }
-    if (lists) { L.kbound = off; off += align256((size_t)(tqp / kTile) * heads * 4); }
-  } else {
-    L.aux = off; off += align256((size_t)heads * tqp * 8);   // bf16: uint2 (hi, lo) pairs; fp32: float2 rows
+  P.flags = off; off += 256;
+  P.nodes = off; off += align256((size_t)tqp * 8);
+  P.meta = off; off += align256((size_t)(tqp / kTile) * 16);
+  P.bounds_q = off; off += align256((size_t)tqp * 8);
+  P.bounds_k = off; off += align256((size_t)tkp * 8);
+  P.over_count = off; off += 256;
+  for (int d = 0; d < 2; ++d) {
+    const size_t tiles = (size_t)(d ? tkp : tqp) / kTile;
+    P.info[d] = off; off += align256(tiles * 4);
+    P.ids[d] = off; off += align256(tiles * kListCap * 4);
+    P.bits[d] = off; off += align256(tiles * kListCap * 4);
+    P.over[d] = off; off += align256((size_t)groups_of(d ? total_k : total_q) * 16);
+    if (d == 0) P.total = off;
   }
-  // fp32: a 16-byte group count, then per-segment groups (at most ceil(T / 128) + number of segments <= T).
-  auto plan_size = [&](int t) {
-    return align256(dtype == ESA_F32 ? 16 + ((size_t)groups_of(t) + t + 1) * 16 : (size_t)groups_of(t) * 16 + 16);
-  };
-  L.plan_q = off; off += plan_size(total_q);
-  L.bounds_q = off; off += align256((size_t)tqp * 8);
-  if (backward) {
-    L.plan_k = off; off += plan_size(total_k);
-    L.bounds_k = off; off += align256((size_t)tkp * 8);
+  if (key_lists) P.total = off;
+  return P;
+}
+
+// Per-call workspace: the backward row statistics, the fp32 kernels'
+// per-segment plans and, for an edge mask given as node ids, the plan the
+// call builds (the key tiles' lists only when `key_lists`).
+struct WsLayout {
+  size_t aux = 0, plan_q = 0, plan_k = 0, plan = 0, total = 0;
+};
+
+WsLayout ws_layout(int total_q, int total_k, int heads, int dtype, int mask_kind, bool backward, bool key_lists) {
+  WsLayout L;
+  const int tqp = round32(total_q);
+  size_t off = 0;
+  if (backward) { L.aux = off; off += align256((size_t)heads * tqp * 8); }   // bf16: uint2 (hi, lo); fp32: float2
+  if (dtype == ESA_F32) {
+    // a 16-byte group count, then per-segment groups (at most ceil(T / 128) + number of segments <= T)
+    auto plan_size = [&](int t) { return align256(16 + ((size_t)groups_of(t) + t + 1) * 16); };
+    L.plan_q = off; off += plan_size(total_q);
+    if (backward) { L.plan_k = off; off += plan_size(total_k); }
   }
-  if (masked) {
-    L.nodes = off; off += align256((size_t)tqp * 8);
-    L.meta = off; off += align256((size_t)(tqp / kTile) * 16);
-  }
-  if (lists) {
-    // Key lists per direction (queries; keys in the backward pass): per outer
-    // tile a count, kListCap ids and kListCap mask words; the overflow groups.
-    L.over_count = off; off += 256;
-    for (int d = 0; d < (backward ? 2 : 1); ++d) {
-      const size_t tiles = (size_t)(d ? tkp : tqp) / kTile;
-      L.info[d] = off; off += align256(tiles * 4);
-      L.ids[d] = off; off += align256(tiles * kListCap * 4);
-      L.bits[d] = off; off += align256(tiles * kListCap * 4);
-      L.over[d] = off; off += align256((size_t)groups_of(d ? total_k : total_q) * 16);
-    }
-  }
+  if (mask_kind == ESA_MASK_EDGE) { L.plan = off; off += plan_layout(total_q, total_k, key_lists).total; }
   L.total = off;
   return L;
+}
+
+// Device pointers into a built plan.
+struct PlanView {
+  const int* flags; const int2* nodes; const int4* meta; const int2* bounds_q; const int2* bounds_k;
+  const int* over_count; const int* info[2]; const int* ids[2]; const uint32_t* bits[2]; const int4* over[2];
+};
+PlanView plan_view(const void* plan, int total_q, int total_k) {
+  const PlanLayout P = plan_layout(total_q, total_k, true);
+  const char* b = static_cast<const char*>(plan);
+  PlanView V;
+  V.flags = reinterpret_cast<const int*>(b + P.flags);
+  V.nodes = reinterpret_cast<const int2*>(b + P.nodes);
+  V.meta = reinterpret_cast<const int4*>(b + P.meta);
+  V.bounds_q = reinterpret_cast<const int2*>(b + P.bounds_q);
+  V.bounds_k = reinterpret_cast<const int2*>(b + P.bounds_k);
+  V.over_count = reinterpret_cast<const int*>(b + P.over_count);
+  for (int d = 0; d < 2; ++d) {
+    V.info[d] = reinterpret_cast<const int*>(b + P.info[d]);
+    V.ids[d] = reinterpret_cast<const int*>(b + P.ids[d]);
+    V.bits[d] = reinterpret_cast<const uint32_t*>(b + P.bits[d]);
+    V.over[d] = reinterpret_cast<const int4*>(b + P.over[d]);
+  }
+  return V;
 }
 
 bool misaligned(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) != 0; }
@@ -1984,8 +1929,10 @@ int check_common(int batch, int total_q, int total_k, int heads, int head_dim, i
   // Buffer-resource ranges are 32-bit byte counts.
   const long lim = (1L << 31) - 1;
   if ((long)round32(total_q) * heads * 32 > lim || (long)round32(total_k) * heads * 32 > lim) return ESA_ERR_SHAPE;
-  if (mask_kind != ESA_MASK_NONE && mask_kind != ESA_MASK_EDGE && mask_kind != ESA_MASK_NODE) return ESA_ERR_MASK;
-  if (mask_kind == ESA_MASK_EDGE && total_q != total_k) return ESA_ERR_MASK;
+  if (mask_kind != ESA_MASK_NONE && mask_kind != ESA_MASK_EDGE && mask_kind != ESA_MASK_NODE &&
+      mask_kind != ESA_MASK_EDGE_PLAN)
+    return ESA_ERR_MASK;
+  if ((mask_kind == ESA_MASK_EDGE || mask_kind == ESA_MASK_EDGE_PLAN) && total_q != total_k) return ESA_ERR_MASK;
   return ESA_OK;
 }
 
@@ -2002,19 +1949,22 @@ int launch_zero(void* p, size_t bytes, hipStream_t st) {
 
 int blocks_for(long items) { return (int)((items + 255) / 256); }
 
-// `lists`: the bf16 edge-mask path, whose kernels need no plans (block order
-// is XCD-aware) and whose dQ pass writes the row statistics itself.
-int launch_prep(PrepArgs& p, bool forward, bool masked, hipStream_t st, bool lists = false) {
-  p.nb[kPlanQ] = lists ? 0 : 1;
-  p.nb[kPlanK] = forward || lists ? 0 : 1;
-  p.nb[kKnorm] = forward && p.knorm ? p.tk_pad / kTile : 0;
-  p.nb[kRows] = forward || lists ? 0 : blocks_for((long)p.heads * p.tq_pad);
-  p.nb[kBoundsQ] = blocks_for(p.tq_pad);
-  p.nb[kBoundsK] = forward ? 0 : blocks_for(p.tk_pad);
-  p.nb[kNodes] = masked ? blocks_for(p.tq_pad) : 0;
-  p.nb[kMeta] = masked ? blocks_for((long)(p.tq_pad / kTile) * 64) : 0;
+enum : unsigned { kTaskPlanQ = 1u, kTaskPlanK = 2u, kTaskMask = 4u, kTaskRows = 8u };
+
+// One prep launch over the selected tasks (kTaskMask: the edge-mask plan's
+// node pairs, tile metadata, both directions' bounds, flag and counts).
+int launch_prep(PrepArgs& p, unsigned tasks, hipStream_t st) {
+  p.nb[kPlanQ] = (tasks & kTaskPlanQ) ? 1 : 0;
+  p.nb[kPlanK] = (tasks & kTaskPlanK) ? 1 : 0;
+  p.nb[kRows] = (tasks & kTaskRows) ? blocks_for((long)p.heads * p.tq_pad) : 0;
+  const bool mask = (tasks & kTaskMask) != 0;
+  p.nb[kBoundsQ] = mask ? blocks_for(p.tq_pad) : 0;
+  p.nb[kBoundsK] = mask ? blocks_for(p.tk_pad) : 0;
+  p.nb[kNodes] = mask ? blocks_for(p.tq_pad) : 0;
+  p.nb[kMeta] = mask ? blocks_for((long)(p.tq_pad / kTile) * 64) : 0;
   long grid = 0;
   for (int i = 0; i < kPrepTasks; ++i) grid += p.nb[i];
+  if (grid == 0) return ESA_OK;
   ESA_TIMED(esa_profile::kAttnPrep, st,
             hipLaunchKernelGGL(prep_kernel, dim3((unsigned)grid), dim3(256), 0, st, p));
   ESA_LAUNCH_CHECK();
@@ -2037,31 +1987,57 @@ unsigned list_tile_blocks(int total, unsigned n_hw) {
 constexpr int kOverflowGroups = 64;   // groups in flight in a walk kernel over the overflow list
 unsigned overflow_blocks(int total) { return (unsigned)std::min(groups_of(total), kOverflowGroups); }
 
-// Key lists of the query tiles (and of the key tiles when `both`), after the
-// prep pass that writes the nodes, tile metadata, bounds and zero counts.
-int launch_lists(const PrepArgs& pa, const WsLayout& L, char* ws, bool forward, bool both, hipStream_t st) {
+// Builds an edge-mask plan: one prep launch (node pairs, tile metadata,
+// bounds, flag, zero counts), then the key lists of the query tiles and, when
+// `key_lists`, of the key tiles.  The flag is 1 without key-tile lists (the
+// query and key segments are one array: the mask is symmetric).
+int build_edge_plan(const int* tok_src, const int* tok_dst, const int* cu_q, const int* cu_k, int batch,
+                    int total_q, int total_k, void* plan, bool key_lists, hipStream_t st) {
+  const PlanLayout P = plan_layout(total_q, total_k, key_lists);
+  char* b = static_cast<char*>(plan);
+  PrepArgs pa{};
+  pa.cu_q = cu_q; pa.cu_k = cu_k; pa.nseg = batch;
+  pa.total_q = total_q; pa.total_k = total_k; pa.heads = 1;
+  pa.tq_pad = round32(total_q); pa.tk_pad = round32(total_k);
+  pa.tok_src = tok_src; pa.tok_dst = tok_dst;
+  pa.nodes = reinterpret_cast<int2*>(b + P.nodes);
+  pa.meta = reinterpret_cast<int4*>(b + P.meta);
+  pa.bounds_q = reinterpret_cast<int2*>(b + P.bounds_q);
+  pa.bounds_k = reinterpret_cast<int2*>(b + P.bounds_k);
+  pa.over_count = reinterpret_cast<int*>(b + P.over_count);
+  pa.flags = reinterpret_cast<int*>(b + P.flags);
+  pa.sym = key_lists ? 0 : 1;
+  int rc = launch_prep(pa, kTaskMask, st);
+  if (rc) return rc;
   ListArgs la{};
   la.nodes = pa.nodes; la.meta = pa.meta;
-  la.heads = pa.heads;
-  if (forward) {   // the per-tile key-norm bounds of the fixed-reference softmax
-    la.knorm = pa.knorm; la.kn_tiles = pa.tk_pad / kTile;
-    la.kbound = reinterpret_cast<float*>(ws + L.kbound);
-  }
-  la.total = pa.total_q;
-  la.n_groups = groups_of(pa.total_q);
+  la.total = total_q;
+  la.n_groups = groups_of(total_q);
   la.bounds[0] = pa.bounds_q; la.bounds[1] = pa.bounds_k;
   for (int d = 0; d < 2; ++d) {
-    const int dd = both ? d : 0;
-    la.info[d] = reinterpret_cast<int*>(ws + L.info[dd]);
-    la.ids[d] = reinterpret_cast<int*>(ws + L.ids[dd]);
-    la.bits[d] = reinterpret_cast<uint32_t*>(ws + L.bits[dd]);
-    la.over[d] = reinterpret_cast<int4*>(ws + L.over[dd]);
-    la.over_count[d] = reinterpret_cast<int*>(ws + L.over_count) + dd;
+    la.info[d] = reinterpret_cast<int*>(b + P.info[d]);
+    la.ids[d] = reinterpret_cast<int*>(b + P.ids[d]);
+    la.bits[d] = reinterpret_cast<uint32_t*>(b + P.bits[d]);
+    la.over[d] = reinterpret_cast<int4*>(b + P.over[d]);
+    la.over_count[d] = pa.over_count + d;
   }
-  const unsigned grid = (unsigned)la.n_groups * (both ? 2u : 1u);
+  const unsigned grid = (unsigned)la.n_groups * (key_lists ? 2u : 1u);
   ESA_TIMED(esa_profile::kAttnEdgeLists, st, hipLaunchKernelGGL(edge_lists_kernel, dim3(grid), dim3(256), 0, st, la));
   ESA_LAUNCH_CHECK();
   return ESA_OK;
+}
+
+// The plan of a masked call: the caller's (ESA_MASK_EDGE_PLAN: mask_a points
+// at it) or one built into the call's workspace from the node ids.
+int call_plan(int mask_kind, const int* mask_a, const int* mask_b, const int* cu_q, const int* cu_k, int batch,
+              int total_q, int total_k, char* ws, const WsLayout& L, bool key_lists, hipStream_t st,
+              const void** plan) {
+  if (mask_kind == ESA_MASK_EDGE_PLAN) {
+    *plan = mask_a;
+    return ESA_OK;
+  }
+  *plan = ws + L.plan;
+  return build_edge_plan(mask_a, mask_b, cu_q, cu_k, batch, total_q, total_k, ws + L.plan, key_lists, st);
 }
 
 // Scratch of esa_varlen_attn_fwd_noalloc: a file-scope device array, one
@@ -2112,8 +2088,28 @@ int esa_varlen_attn_workspace_size(int total_q, int total_k, int heads, int head
     *bytes = dense_attn_workspace_size(total_q, total_k, heads, backward != 0);
     return ESA_OK;
   }
-  *bytes = ws_layout(total_q, total_k, heads, dtype, mask_kind == ESA_MASK_EDGE, backward != 0).total;
+  // a backward call that builds its plan may need the key tiles' lists (distinct segment arrays)
+  *bytes = ws_layout(total_q, total_k, heads, dtype, mask_kind, backward != 0, backward != 0).total;
   return ESA_OK;
+}
+
+int esa_edge_plan_size(int total_q, int total_k, int symmetric, size_t* bytes) {
+  if (!bytes) return ESA_ERR_NULL;
+  if (total_q < 0 || total_k < 0 || total_q != total_k) return ESA_ERR_SHAPE;
+  *bytes = plan_layout(total_q, total_k, symmetric == 0).total;
+  return ESA_OK;
+}
+
+int esa_edge_plan_build(const int* tok_src, const int* tok_dst, const int* cu_seqlens_q, const int* cu_seqlens_k,
+                        int batch, int total_q, int total_k, void* plan, size_t plan_bytes, void* stream) {
+  if (!tok_src || !tok_dst || !cu_seqlens_q || !cu_seqlens_k || !plan) return ESA_ERR_NULL;
+  if (batch < 1 || total_q < 0 || total_q != total_k) return ESA_ERR_SHAPE;
+  if (misaligned(plan)) return ESA_ERR_ALIGN;
+  const bool key_lists = cu_seqlens_q != cu_seqlens_k;
+  if (plan_bytes < plan_layout(total_q, total_k, key_lists).total) return ESA_ERR_WORKSPACE;
+  if (total_q == 0) return ESA_OK;
+  return build_edge_plan(tok_src, tok_dst, cu_seqlens_q, cu_seqlens_k, batch, total_q, total_k, plan, key_lists,
+                         reinterpret_cast<hipStream_t>(stream));
 }
 
 int esa_varlen_attn_fwd(const void* q, const void* k, const void* v, const int* cu_seqlens_q,
@@ -2141,47 +2137,46 @@ int esa_varlen_attn_fwd(const void* q, const void* k, const void* v, const int* 
     (void)workspace; (void)workspace_bytes;
     return graph_attn_fwd(g, dtype, reinterpret_cast<hipStream_t>(stream));
   }
-  const bool masked = mask_kind == ESA_MASK_EDGE;
-  if (masked && (!mask_a || !mask_b)) return ESA_ERR_NULL;
+  const bool masked = mask_kind == ESA_MASK_EDGE || mask_kind == ESA_MASK_EDGE_PLAN;
+  if (mask_kind == ESA_MASK_EDGE && (!mask_a || !mask_b)) return ESA_ERR_NULL;
+  if (mask_kind == ESA_MASK_EDGE_PLAN && !mask_a) return ESA_ERR_NULL;
   if (total_q == 0) return ESA_OK;
-  if (!q || !k || !v || !cu_seqlens_q || !cu_seqlens_k || !out || !softmax_lse || !workspace) return ESA_ERR_NULL;
+  if (!q || !k || !v || !cu_seqlens_q || !cu_seqlens_k || !out || !softmax_lse) return ESA_ERR_NULL;
   if (misaligned(q) || misaligned(k) || misaligned(v) || misaligned(out) || misaligned(workspace)) return ESA_ERR_ALIGN;
   if (!(softmax_scale > 0.f)) return ESA_ERR_SHAPE;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const bool f32 = dtype == ESA_F32;
   if (!masked && !f32) {
+    if (!workspace) return ESA_ERR_NULL;
     DenseAttnCall c{};
     c.q = q; c.k = k; c.v = v; c.cu_q = cu_seqlens_q; c.cu_k = cu_seqlens_k; c.nseg = batch;
     c.total_q = total_q; c.total_k = total_k; c.heads = heads; c.scale = softmax_scale;
     c.out = out; c.lse = softmax_lse;
     return dense_attn_fwd(c, workspace, workspace_bytes, st);
   }
-  const WsLayout L = ws_layout(total_q, total_k, heads, dtype, masked, false);
+  const WsLayout L = ws_layout(total_q, total_k, heads, dtype, mask_kind, false, false);
   if (workspace_bytes < L.total) return ESA_ERR_WORKSPACE;
+  if (L.total && !workspace) return ESA_ERR_NULL;
   char* ws = static_cast<char*>(workspace);
-
-  PrepArgs pa{};
-  pa.cu_q = cu_seqlens_q; pa.cu_k = cu_seqlens_k; pa.nseg = batch;
-  pa.total_q = total_q; pa.total_k = total_k; pa.heads = heads;
-  pa.tq_pad = round32(total_q); pa.tk_pad = round32(total_k);
-  pa.plan_q = reinterpret_cast<int4*>(ws + L.plan_q + (f32 ? 16 : 0));
-  if (f32) pa.count_q = reinterpret_cast<int*>(ws + L.plan_q);
-  pa.bounds_q = reinterpret_cast<int2*>(ws + L.bounds_q);
-  if (!f32) { pa.k = static_cast<const bf16*>(k); pa.knorm = reinterpret_cast<float*>(ws + L.knorm); }
-  if (masked) {
-    pa.tok_src = mask_a; pa.tok_dst = mask_b;
-    pa.nodes = reinterpret_cast<int2*>(ws + L.nodes);
-    pa.meta = reinterpret_cast<int4*>(ws + L.meta);
-  }
-  if (masked && !f32) pa.over_count = reinterpret_cast<int*>(ws + L.over_count);
-  if ((rc = launch_prep(pa, true, masked, st, masked && !f32))) return rc;
+  const void* plan = nullptr;
+  if (masked && (rc = call_plan(mask_kind, mask_a, mask_b, cu_seqlens_q, cu_seqlens_k, batch, total_q, total_k, ws,
+                                L, false, st, &plan)))
+    return rc;
 
   if (f32) {
+    PrepArgs pa{};
+    pa.cu_q = cu_seqlens_q; pa.cu_k = cu_seqlens_k; pa.nseg = batch;
+    pa.total_q = total_q; pa.total_k = total_k; pa.heads = heads;
+    pa.tq_pad = round32(total_q); pa.tk_pad = round32(total_k);
+    pa.plan_q = reinterpret_cast<int4*>(ws + L.plan_q + 16);
+    pa.count_q = reinterpret_cast<int*>(ws + L.plan_q);
+    if ((rc = launch_prep(pa, kTaskPlanQ, st))) return rc;
     AttnF32Args a{};
     a.q = static_cast<const float*>(q); a.k = static_cast<const float*>(k); a.v = static_cast<const float*>(v);
     a.total_q = total_q; a.total_k = total_k; a.heads = heads; a.tq_pad = pa.tq_pad;
     a.c = softmax_scale * kLog2e; a.scale = softmax_scale;
-    a.nodes = pa.nodes; a.plan = pa.plan_q; a.count = pa.count_q;
+    a.nodes = masked ? plan_view(plan, total_q, total_k).nodes : nullptr;
+    a.plan = pa.plan_q; a.count = pa.count_q;
     a.o = static_cast<float*>(out); a.lse_out = softmax_lse;
     const dim3 fgrid((unsigned)(groups_of(total_q) + batch) * (unsigned)heads);
     if (masked)
@@ -2192,29 +2187,25 @@ int esa_varlen_attn_fwd(const void* q, const void* k, const void* v, const int* 
     return ESA_OK;
   }
 
+  // bf16 edge mask: the key-list forward, then the walk kernel over the overflowing groups
+  const PlanView V = plan_view(plan, total_q, total_k);
   AttnArgs a{};
   a.q = static_cast<const bf16*>(q); a.k = static_cast<const bf16*>(k); a.v = static_cast<const bf16*>(v);
-  a.knorm = pa.knorm;
   a.cu_q = cu_seqlens_q; a.cu_k = cu_seqlens_k; a.nseg = batch;
-  a.total_q = total_q; a.total_k = total_k; a.heads = heads; a.tq_pad = pa.tq_pad;
-  a.tk_tiles = pa.tk_pad / kTile;
+  a.total_q = total_q; a.total_k = total_k; a.heads = heads; a.tq_pad = round32(total_q);
+  a.tk_tiles = round32(total_k) / kTile;
   a.scale = softmax_scale; a.c = softmax_scale * kLog2e;
-  a.plan = pa.plan_q; a.bounds = pa.bounds_q;
-  a.nodes = pa.nodes; a.meta = pa.meta;
+  a.bounds = V.bounds_q;
+  a.nodes = V.nodes; a.meta = V.meta;
+  a.info = V.info[0]; a.ids = V.ids[0]; a.bits = V.bits[0];
   a.o = static_cast<bf16*>(out); a.lse_out = softmax_lse;
-  if ((rc = launch_lists(pa, L, ws, true, false, st))) return rc;
-  const unsigned n_hg = (unsigned)((heads + kListHeads - 1) / kListHeads);
-  const unsigned n_hg_walk = (unsigned)((heads + kEdgeHeads - 1) / kEdgeHeads);
-  a.info = reinterpret_cast<const int*>(ws + L.info[0]);
-  a.ids = reinterpret_cast<const int*>(ws + L.ids[0]);
-  a.bits = reinterpret_cast<const uint32_t*>(ws + L.bits[0]);
-  a.kbound = reinterpret_cast<const float*>(ws + L.kbound);
-  const unsigned n_hq = (n_hg + kWaves - 1) / kWaves;
+  const unsigned n_hq = ((heads + kListHeads - 1) / kListHeads + kWaves - 1) / kWaves;
   ESA_TIMED(esa_profile::kAttnFwdMasked, st,
             hipLaunchKernelGGL(list_fwd_kernel, dim3(list_tile_blocks(total_q, n_hq)), dim3(256), 0, st, a));
   ESA_LAUNCH_CHECK();
-  a.plan = reinterpret_cast<const int4*>(ws + L.over[0]);
-  a.count = reinterpret_cast<const int*>(ws + L.over_count);
+  a.plan = V.over[0];
+  a.count = V.over_count;
+  const unsigned n_hg_walk = (unsigned)((heads + kEdgeHeads - 1) / kEdgeHeads);
   ESA_TIMED(esa_profile::kAttnEdgeOverflow, st,
             hipLaunchKernelGGL(edge_fwd_kernel, dim3(overflow_blocks(total_q) * n_hg_walk), dim3(256), 0, st, a));
   ESA_LAUNCH_CHECK();
@@ -2272,8 +2263,9 @@ int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k, const vo
     g.dq = dq; g.dk = dk; g.dv = dv;
     return graph_attn_bwd(g, dtype, workspace, workspace_bytes, reinterpret_cast<hipStream_t>(stream));
   }
-  const bool masked = mask_kind == ESA_MASK_EDGE;
-  if (masked && (!mask_a || !mask_b)) return ESA_ERR_NULL;
+  const bool masked = mask_kind == ESA_MASK_EDGE || mask_kind == ESA_MASK_EDGE_PLAN;
+  if (mask_kind == ESA_MASK_EDGE && (!mask_a || !mask_b)) return ESA_ERR_NULL;
+  if (mask_kind == ESA_MASK_EDGE_PLAN && !mask_a) return ESA_ERR_NULL;
   if (total_q == 0 && total_k == 0) return ESA_OK;
   if (!dout || !q || !k || !v || !out || !softmax_lse || !cu_seqlens_q || !cu_seqlens_k || !dq || !dk ||
       !dv || !workspace)
@@ -2300,45 +2292,36 @@ int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k, const vo
     c.out_in = out; c.dout = dout; c.lse_in = softmax_lse; c.dq = dq; c.dk = dk; c.dv = dv;
     return dense_attn_bwd(c, workspace, workspace_bytes, st);
   }
-  const WsLayout L = ws_layout(total_q, total_k, heads, dtype, masked, true);
+  // A plan built here has the key tiles' own lists when the segment arrays are distinct.
+  const bool key_lists = cu_seqlens_q != cu_seqlens_k;
+  const WsLayout L = ws_layout(total_q, total_k, heads, dtype, mask_kind, true, key_lists);
   if (workspace_bytes < L.total) return ESA_ERR_WORKSPACE;
   char* ws = static_cast<char*>(workspace);
-  PrepArgs pa{};
-  pa.cu_q = cu_seqlens_q; pa.cu_k = cu_seqlens_k; pa.nseg = batch;
-  pa.total_q = total_q; pa.total_k = total_k; pa.heads = heads;
-  pa.tq_pad = round32(total_q); pa.tk_pad = round32(total_k);
-  pa.plan_q = reinterpret_cast<int4*>(ws + L.plan_q + (f32 ? 16 : 0));
-  pa.plan_k = reinterpret_cast<int4*>(ws + L.plan_k + (f32 ? 16 : 0));
-  if (f32) {
-    pa.count_q = reinterpret_cast<int*>(ws + L.plan_q);
-    pa.count_k = reinterpret_cast<int*>(ws + L.plan_k);
-  }
-  pa.bounds_q = reinterpret_cast<int2*>(ws + L.bounds_q);
-  pa.bounds_k = reinterpret_cast<int2*>(ws + L.bounds_k);
-  pa.lse = softmax_lse; pa.c = softmax_scale * kLog2e;
-  if (f32) {
-    pa.dout_f = static_cast<const float*>(dout); pa.out_f = static_cast<const float*>(out);
-    pa.rows_f = reinterpret_cast<float2*>(ws + L.aux);
-  } else {
-    pa.dout = static_cast<const bf16*>(dout); pa.out = static_cast<const bf16*>(out);
-    pa.aux = reinterpret_cast<uint2*>(ws + L.aux);
-  }
-  if (masked) {
-    pa.tok_src = mask_a; pa.tok_dst = mask_b;
-    pa.nodes = reinterpret_cast<int2*>(ws + L.nodes);
-    pa.meta = reinterpret_cast<int4*>(ws + L.meta);
-    if (!f32) pa.over_count = reinterpret_cast<int*>(ws + L.over_count);
-  }
-  if ((rc = launch_prep(pa, false, masked, st, masked && !f32))) return rc;
+  const void* plan = nullptr;
+  if (masked && (rc = call_plan(mask_kind, mask_a, mask_b, cu_seqlens_q, cu_seqlens_k, batch, total_q, total_k, ws,
+                                L, key_lists, st, &plan)))
+    return rc;
 
   if (f32) {
+    PrepArgs pa{};
+    pa.cu_q = cu_seqlens_q; pa.cu_k = cu_seqlens_k; pa.nseg = batch;
+    pa.total_q = total_q; pa.total_k = total_k; pa.heads = heads;
+    pa.tq_pad = round32(total_q); pa.tk_pad = round32(total_k);
+    pa.plan_q = reinterpret_cast<int4*>(ws + L.plan_q + 16);
+    pa.plan_k = reinterpret_cast<int4*>(ws + L.plan_k + 16);
+    pa.count_q = reinterpret_cast<int*>(ws + L.plan_q);
+    pa.count_k = reinterpret_cast<int*>(ws + L.plan_k);
+    pa.lse = softmax_lse; pa.c = softmax_scale * kLog2e;
+    pa.dout_f = static_cast<const float*>(dout); pa.out_f = static_cast<const float*>(out);
+    pa.rows_f = reinterpret_cast<float2*>(ws + L.aux);
+    if ((rc = launch_prep(pa, kTaskPlanQ | kTaskPlanK | kTaskRows, st))) return rc;
     AttnF32Args a{};
     a.q = static_cast<const float*>(q); a.k = static_cast<const float*>(k); a.v = static_cast<const float*>(v);
     a.out = static_cast<const float*>(out); a.dout = static_cast<const float*>(dout);
     a.rows = pa.rows_f;
     a.total_q = total_q; a.total_k = total_k; a.heads = heads; a.tq_pad = pa.tq_pad;
     a.c = softmax_scale * kLog2e; a.scale = softmax_scale;
-    a.nodes = pa.nodes;
+    a.nodes = masked ? plan_view(plan, total_q, total_k).nodes : nullptr;
     a.dq = static_cast<float*>(dq); a.dk = static_cast<float*>(dk); a.dv = static_cast<float*>(dv);
     a.plan = pa.plan_k; a.count = pa.count_k;
     const dim3 fkgrid((unsigned)(groups_of(total_k) + batch) * (unsigned)heads);
@@ -2357,54 +2340,43 @@ int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k, const vo
     return ESA_OK;
   }
 
+  // bf16 edge mask: dQ first (its list pass writes the row statistics the
+  // dK/dV passes read), each list pass followed by the walk kernel over the
+  // overflowing groups.
+  const PlanView V = plan_view(plan, total_q, total_k);
   AttnArgs a{};
   a.q = static_cast<const bf16*>(q); a.k = static_cast<const bf16*>(k); a.v = static_cast<const bf16*>(v);
   a.out = static_cast<const bf16*>(out); a.dout = static_cast<const bf16*>(dout); a.lse = softmax_lse;
-  a.aux = pa.aux;
+  a.aux = reinterpret_cast<const uint2*>(ws + L.aux);
+  a.aux_out = reinterpret_cast<uint2*>(ws + L.aux);
   a.cu_q = cu_seqlens_q; a.cu_k = cu_seqlens_k; a.nseg = batch;
-  a.total_q = total_q; a.total_k = total_k; a.heads = heads; a.tq_pad = pa.tq_pad;
-  a.tk_tiles = pa.tk_pad / kTile;
+  a.total_q = total_q; a.total_k = total_k; a.heads = heads; a.tq_pad = round32(total_q);
+  a.tk_tiles = round32(total_k) / kTile;
   a.scale = softmax_scale; a.c = softmax_scale * kLog2e;
-  a.nodes = pa.nodes; a.meta = pa.meta;
+  a.nodes = V.nodes; a.meta = V.meta;
+  a.sym = V.flags;
+  a.kinfo = V.info[1]; a.kids = V.ids[1]; a.kbits = V.bits[1]; a.kover = V.over[1]; a.kcount = V.over_count + 1;
   a.dq = static_cast<bf16*>(dq); a.dk = static_cast<bf16*>(dk); a.dv = static_cast<bf16*>(dv);
 
-  // Equal cu_seqlens pointers: the query and key segments coincide, the mask
-  // is symmetric and the key tiles use the query tiles' lists.
-  const bool symmetric = cu_seqlens_q == cu_seqlens_k;
-  if ((rc = launch_lists(pa, L, ws, false, !symmetric, st))) return rc;
-  const int kd = symmetric ? 0 : 1;
-  const int* over_count = reinterpret_cast<const int*>(ws + L.over_count);
-
-  // dQ first: the key-list dQ pass writes the row statistics the dK/dV passes read.
   const unsigned n_hg = (unsigned)((heads + kListHeads - 1) / kListHeads);
   const unsigned n_hg_walk = (unsigned)((heads + kEdgeHeads - 1) / kEdgeHeads);
-  a.aux_out = pa.aux;
-  a.plan = pa.plan_q;
-  a.bounds = pa.bounds_q;
-  a.info = reinterpret_cast<const int*>(ws + L.info[0]);
-  a.ids = reinterpret_cast<const int*>(ws + L.ids[0]);
-  a.bits = reinterpret_cast<const uint32_t*>(ws + L.bits[0]);
+  a.bounds = V.bounds_q;
+  a.info = V.info[0]; a.ids = V.ids[0]; a.bits = V.bits[0];
   ESA_TIMED(esa_profile::kAttnBwdDqMasked, st,
             hipLaunchKernelGGL(list_dq_kernel, dim3(list_blocks(total_q, n_hg)), dim3(256), 0, st, a));
   ESA_LAUNCH_CHECK();
-  a.plan = reinterpret_cast<const int4*>(ws + L.over[0]);
-  a.count = over_count;
+  a.plan = V.over[0];
+  a.count = V.over_count;
   ESA_TIMED(esa_profile::kAttnEdgeOverflow, st,
             hipLaunchKernelGGL(edge_dq_kernel, dim3(overflow_blocks(total_q) * n_hg_walk), dim3(256), 0, st, a));
   ESA_LAUNCH_CHECK();
 
   const unsigned n_hg_kv = (unsigned)((heads + kListHeadsKv - 1) / kListHeadsKv);
   const unsigned n_hg_kv_walk = (unsigned)((heads + kEdgeHeadsKv - 1) / kEdgeHeadsKv);
-  a.plan = pa.plan_k;
-  a.bounds = pa.bounds_k;
-  a.info = reinterpret_cast<const int*>(ws + L.info[kd]);
-  a.ids = reinterpret_cast<const int*>(ws + L.ids[kd]);
-  a.bits = reinterpret_cast<const uint32_t*>(ws + L.bits[kd]);
+  a.bounds = V.bounds_k;
   ESA_TIMED(esa_profile::kAttnBwdDkdvMasked, st,
             hipLaunchKernelGGL(list_dkdv_kernel, dim3(list_blocks(total_k, n_hg_kv)), dim3(256), 0, st, a));
   ESA_LAUNCH_CHECK();
-  a.plan = reinterpret_cast<const int4*>(ws + L.over[kd]);
-  a.count = over_count + kd;
   ESA_TIMED(esa_profile::kAttnEdgeOverflow, st,
             hipLaunchKernelGGL(edge_dkdv_kernel, dim3(overflow_blocks(total_k) * n_hg_kv_walk), dim3(256), 0, st, a));
   ESA_LAUNCH_CHECK();

@@ -61,10 +61,40 @@ def _check_index(name: str, t: torch.Tensor | None, n: int | None = None) -> Non
         raise ValueError(f"{name} has {t.numel()} entries, expected {n}")
 
 
-def _mask_args(tq: int, edge_src, edge_dst, adj_indptr, adj_indices):
+def edge_plan(edge_src, edge_dst, cu_seqlens_q, cu_seqlens_k=None) -> torch.Tensor:
+    """The edge-mask plan of a batch (esa_edge_plan_build): a uint8 device tensor holding the share-an-endpoint
+    mask of the edge tokens with node ids ``edge_src`` / ``edge_dst`` (int32 [T]) over the segments
+    ``cu_seqlens_q`` / ``cu_seqlens_k`` (``cu_seqlens_k`` defaults to the same tensor: self-attention, a
+    symmetric mask).  Built once per batch and passed as ``edge_plan=`` to every attention call over those
+    tokens, as the reference builds its [B, N, N] mask once per batch (get_adj_mask_from_edge_index_edge,
+    esa/masked_layers.py:217-268) for all masked layers.  Later calls must pass the same cu_seqlens tensors."""
+    cu_k = cu_seqlens_q if cu_seqlens_k is None else cu_seqlens_k
+    _lib.require_gpu(edge_src, edge_dst, cu_seqlens_q, cu_k)
+    t = edge_src.numel()
+    _check_index("edge_src", edge_src, t)
+    _check_index("edge_dst", edge_dst, t)
+    _check_index("cu_seqlens_q", cu_seqlens_q)
+    batch = cu_seqlens_q.numel() - 1
+    _check_index("cu_seqlens_k", cu_k, batch + 1)
+    lib = _lib.load()
+    n = _lib.ctypes.c_size_t(0)
+    sym = cu_k.data_ptr() == cu_seqlens_q.data_ptr()
+    _lib.check(lib.esa_edge_plan_size(t, t, int(sym), _lib.ctypes.byref(n)), "esa_edge_plan_size")
+    plan = torch.empty(max(int(n.value), 256), dtype=torch.uint8, device=edge_src.device)
+    rc = lib.esa_edge_plan_build(edge_src.data_ptr(), edge_dst.data_ptr(), cu_seqlens_q.data_ptr(), cu_k.data_ptr(),
+                                 batch, t, t, plan.data_ptr(), plan.numel(), _lib.stream_of(edge_src))
+    _lib.check(rc, "esa_edge_plan_build")
+    return plan
+
+
+def _mask_args(tq: int, edge_src, edge_dst, adj_indptr, adj_indices, edge_plan=None):
     """(mask_kind, mask_a, mask_b, n_mask_edges) of the C ABI for the given mask tensors."""
-    if edge_src is not None and adj_indptr is not None:
-        raise ValueError("give either the edge mask (edge_src / edge_dst) or the node adjacency, not both")
+    if sum(x is not None for x in (edge_src, adj_indptr, edge_plan)) > 1:
+        raise ValueError("give one mask: the edge mask (edge_src / edge_dst), its plan, or the node adjacency")
+    if edge_plan is not None:
+        if edge_plan.dtype != torch.uint8 or not edge_plan.is_cuda:
+            raise ValueError("edge_plan must be the uint8 device tensor edge_plan() returns")
+        return _lib.ESA_MASK_EDGE_PLAN, edge_plan, None, 0
     if edge_src is not None:
         _check_index("edge_src", edge_src, tq)
         _check_index("edge_dst", edge_dst, tq)
@@ -77,9 +107,9 @@ def _mask_args(tq: int, edge_src, edge_dst, adj_indptr, adj_indices):
 
 
 def attn_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale,
-             edge_src=None, edge_dst=None, adj_indptr=None, adj_indices=None):
+             edge_src=None, edge_dst=None, adj_indptr=None, adj_indices=None, edge_plan=None):
     """Raw forward: returns ``(out [Tq,H,16] (dtype of q), softmax_lse [H,Tq] fp32)``."""
-    _lib.require_gpu(q, k, v, cu_seqlens_q, cu_seqlens_k, edge_src, edge_dst, adj_indptr, adj_indices)
+    _lib.require_gpu(q, k, v, cu_seqlens_q, cu_seqlens_k, edge_src, edge_dst, adj_indptr, adj_indices, edge_plan)
     heads = q.shape[1]
     _check_tokens("q", q)
     _check_tokens("k", k, heads, q.dtype)
@@ -90,7 +120,7 @@ def attn_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, so
     _check_index("cu_seqlens_q", cu_seqlens_q)
     _check_index("cu_seqlens_k", cu_seqlens_k, batch + 1)
     tq, tk = q.shape[0], k.shape[0]
-    mask_kind, mask_a, mask_b, nnz = _mask_args(tq, edge_src, edge_dst, adj_indptr, adj_indices)
+    mask_kind, mask_a, mask_b, nnz = _mask_args(tq, edge_src, edge_dst, adj_indptr, adj_indices, edge_plan)
     dt = _dtype_code(q)
     out = torch.empty_like(q)
     lse = torch.empty((heads, tq), dtype=torch.float32, device=q.device)
@@ -106,11 +136,12 @@ def attn_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, so
 
 
 def attn_fwd_noalloc(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale, out, lse,
-                     edge_src=None, edge_dst=None, adj_indptr=None, adj_indices=None):
+                     edge_src=None, edge_dst=None, adj_indptr=None, adj_indices=None, edge_plan=None):
     """``attn_fwd`` into caller-provided ``out`` [Tq,H,16] and ``lse`` [H,Tq] fp32 through
     esa_varlen_attn_fwd_noalloc: no workspace, no device allocation (the library's static per-GPU scratch;
     calls that overlap on one GPU race).  Raises EsaError (ESA_ERR_SCRATCH) for shapes beyond that scratch."""
-    _lib.require_gpu(q, k, v, cu_seqlens_q, cu_seqlens_k, edge_src, edge_dst, adj_indptr, adj_indices, out, lse)
+    _lib.require_gpu(q, k, v, cu_seqlens_q, cu_seqlens_k, edge_src, edge_dst, adj_indptr, adj_indices, out, lse,
+                     edge_plan)
     heads = q.shape[1]
     _check_tokens("q", q)
     _check_tokens("k", k, heads, q.dtype)
@@ -124,7 +155,7 @@ def attn_fwd_noalloc(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seql
     _check_index("cu_seqlens_q", cu_seqlens_q)
     _check_index("cu_seqlens_k", cu_seqlens_k, batch + 1)
     tq, tk = q.shape[0], k.shape[0]
-    mask_kind, mask_a, mask_b, nnz = _mask_args(tq, edge_src, edge_dst, adj_indptr, adj_indices)
+    mask_kind, mask_a, mask_b, nnz = _mask_args(tq, edge_src, edge_dst, adj_indptr, adj_indices, edge_plan)
     rc = _lib.load().esa_varlen_attn_fwd_noalloc(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(), batch, tq, tk,
         int(max_seqlen_q), int(max_seqlen_k), heads, HEAD_DIM, _dtype_code(q), float(softmax_scale),
@@ -134,7 +165,7 @@ def attn_fwd_noalloc(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seql
 
 
 def attn_bwd(dout, q, k, v, out, lse, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale,
-             edge_src=None, edge_dst=None, adj_indptr=None, adj_indices=None):
+             edge_src=None, edge_dst=None, adj_indptr=None, adj_indices=None, edge_plan=None):
     """Raw backward: returns ``(dq, dk, dv)`` (dtype and shapes of q, k, v)."""
     _lib.require_gpu(dout, q, k, v, out, lse)
     heads = q.shape[1]
@@ -145,7 +176,7 @@ def attn_bwd(dout, q, k, v, out, lse, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, 
         raise ValueError("dout and out must have the shape of q")
     batch = cu_seqlens_q.numel() - 1
     tq, tk = q.shape[0], k.shape[0]
-    mask_kind, mask_a, mask_b, nnz = _mask_args(tq, edge_src, edge_dst, adj_indptr, adj_indices)
+    mask_kind, mask_a, mask_b, nnz = _mask_args(tq, edge_src, edge_dst, adj_indptr, adj_indices, edge_plan)
     dt = _dtype_code(q)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     ws = _workspace(q.device, tq, tk, heads, dt, mask_kind, nnz, True)
@@ -167,15 +198,15 @@ def attn_bwd(dout, q, k, v, out, lse, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, 
 def _op_varlen_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens_q: torch.Tensor,
                    cu_seqlens_k: torch.Tensor, max_seqlen_q: int, max_seqlen_k: int, softmax_scale: float,
                    edge_src: Optional[torch.Tensor], edge_dst: Optional[torch.Tensor],
-                   adj_indptr: Optional[torch.Tensor],
-                   adj_indices: Optional[torch.Tensor]) -> tuple[torch.Tensor, torch.Tensor]:
+                   adj_indptr: Optional[torch.Tensor], adj_indices: Optional[torch.Tensor],
+                   edge_plan: Optional[torch.Tensor] = None) -> tuple[torch.Tensor, torch.Tensor]:
     return attn_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale, edge_src,
-                    edge_dst, adj_indptr, adj_indices)
+                    edge_dst, adj_indptr, adj_indices, edge_plan)
 
 
 @_op_varlen_fwd.register_fake
 def _(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale, edge_src, edge_dst,
-      adj_indptr, adj_indices):
+      adj_indptr, adj_indices, edge_plan=None):
     return torch.empty_like(q), q.new_empty((q.shape[1], q.shape[0]), dtype=torch.float32)
 
 
@@ -184,30 +215,31 @@ def _op_varlen_bwd(dout: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torc
                    lse: torch.Tensor, cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor, max_seqlen_q: int,
                    max_seqlen_k: int, softmax_scale: float, edge_src: Optional[torch.Tensor],
                    edge_dst: Optional[torch.Tensor], adj_indptr: Optional[torch.Tensor],
-                   adj_indices: Optional[torch.Tensor]) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+                   adj_indices: Optional[torch.Tensor],
+                   edge_plan: Optional[torch.Tensor] = None) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     return attn_bwd(dout, q, k, v, out, lse, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale,
-                    edge_src, edge_dst, adj_indptr, adj_indices)
+                    edge_src, edge_dst, adj_indptr, adj_indices, edge_plan)
 
 
 @_op_varlen_bwd.register_fake
 def _(dout, q, k, v, out, lse, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale, edge_src,
-      edge_dst, adj_indptr, adj_indices):
+      edge_dst, adj_indptr, adj_indices, edge_plan=None):
     return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
 
 
 def _varlen_setup(ctx, inputs, output):
-    q, k, v, cu_q, cu_k, max_q, max_k, scale, edge_src, edge_dst, adj_indptr, adj_indices = inputs
+    q, k, v, cu_q, cu_k, max_q, max_k, scale, edge_src, edge_dst, adj_indptr, adj_indices, edge_plan = inputs
     out, lse = output
-    ctx.save_for_backward(q, k, v, out, lse, cu_q, cu_k, edge_src, edge_dst, adj_indptr, adj_indices)
+    ctx.save_for_backward(q, k, v, out, lse, cu_q, cu_k, edge_src, edge_dst, adj_indptr, adj_indices, edge_plan)
     ctx.meta = (max_q, max_k, scale)
 
 
 def _varlen_backward(ctx, dout, _dlse):
-    q, k, v, out, lse, cu_q, cu_k, edge_src, edge_dst, adj_indptr, adj_indices = ctx.saved_tensors
+    q, k, v, out, lse, cu_q, cu_k, edge_src, edge_dst, adj_indptr, adj_indices, edge_plan = ctx.saved_tensors
     max_q, max_k, scale = ctx.meta
     dq, dk, dv = torch.ops.esa_hip.varlen_attn_bwd(dout.contiguous(), q, k, v, out, lse, cu_q, cu_k, max_q, max_k,
-                                                   scale, edge_src, edge_dst, adj_indptr, adj_indices)
-    return dq, dk, dv, None, None, None, None, None, None, None, None, None
+                                                   scale, edge_src, edge_dst, adj_indptr, adj_indices, edge_plan)
+    return dq, dk, dv, None, None, None, None, None, None, None, None, None, None
 
 
 torch.library.register_autograd("esa_hip::varlen_attn_fwd", _varlen_backward, setup_context=_varlen_setup)
@@ -215,7 +247,7 @@ torch.library.register_autograd("esa_hip::varlen_attn_fwd", _varlen_backward, se
 
 def varlen_attention(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, dropout_p=0.0,
                      softmax_scale=None, causal=False, edge_src=None, edge_dst=None, return_lse=False,
-                     adj_indptr=None, adj_indices=None):
+                     adj_indptr=None, adj_indices=None, edge_plan=None):
     """``flash_attn_varlen_func``-compatible entry (plus the ESA masks).
 
     q: [Tq, H, 16]; k, v: [Tk, H, 16], all bfloat16 or all float32;
@@ -223,6 +255,8 @@ def varlen_attention(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seql
     edge_src / edge_dst: optional int32 [Tq] node ids per token (self-attention
     only); token i then attends to token j of its segment iff i != j and the
     two edges share an endpoint (edge mode).
+    edge_plan: optional, the same edge mask prebuilt by ``edge_plan()`` (instead of
+    edge_src / edge_dst) and shared by every call over the batch.
     adj_indptr [Tq+1] / adj_indices [nnz]: optional int32 CSR adjacency (node
     mode): token i attends to the keys listed in its row, ascending, a
     repeated entry counting once.  With return_lse, also returns the
@@ -241,7 +275,7 @@ def varlen_attention(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seql
         raise ValueError("adj_indptr and adj_indices must be given together")
     out, lse = torch.ops.esa_hip.varlen_attn_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, int(max_seqlen_q),
                                                  int(max_seqlen_k), float(softmax_scale), edge_src, edge_dst,
-                                                 adj_indptr, adj_indices)
+                                                 adj_indptr, adj_indices, edge_plan)
     return (out, lse) if return_lse else out
 
 

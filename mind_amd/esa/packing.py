@@ -6,13 +6,14 @@ builds a dense [B, 1, N, N] adjacency bias over the whole batch
 (esa/masked_layers.py:79-118 node mode, :217-268 edge mode).  Here a batch is
 described once by a ``PackedSets`` descriptor: int32 ``cu_seqlens``, each
 token's slot in the padded [B, N] layout and the mask in O(tokens + edges)
-memory — per-token endpoint ids (``EdgeAdjacency``: the kernels evaluate the
-share-an-endpoint predicate on the fly) or a CSR adjacency (``NodeAdjacency``).
+memory — per-token endpoint ids (``EdgeAdjacency``, whose edge-mask plan of
+per-tile partner lists is built once on first use and shared by every masked
+layer) or a CSR adjacency (``NodeAdjacency``).
 It is passed where the reference passes ``adj_mask``.
 """
 from __future__ import annotations
 
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 
 import ctypes
 
@@ -126,6 +127,7 @@ class EdgeAdjacency(PackedSets):
 
     edge_src: torch.Tensor = None
     edge_dst: torch.Tensor = None
+    _plan: torch.Tensor | None = field(default=None, repr=False, compare=False)
 
     @classmethod
     def from_edge_index(cls, edge_index: torch.Tensor, batch_mapping: torch.Tensor, batch_size: int,
@@ -153,11 +155,20 @@ class EdgeAdjacency(PackedSets):
         dst = (fill - n).index_copy(0, self.padded_index, self.edge_dst)
         return src, dst
 
+    def plan(self) -> torch.Tensor:
+        """The batch's edge-mask plan over the packed tokens and ``cu_seqlens`` (esa_edge_plan_build), built on
+        first use and reused by every masked layer's forward and backward, as the reference builds its mask
+        once per batch (esa/masked_layers.py:849-936)."""
+        if self._plan is None:
+            from .attention import edge_plan
+            self._plan = edge_plan(self.edge_src, self.edge_dst, self.cu_seqlens)
+        return self._plan
+
     def kernel_mask(self, padded: bool) -> dict:
         if padded:
             src, dst = self.padded_nodes()
             return {"edge_src": src, "edge_dst": dst}
-        return {"edge_src": self.edge_src, "edge_dst": self.edge_dst}
+        return {"edge_plan": self.plan()}
 
 
 @dataclass

@@ -333,3 +333,60 @@ def test_dense_rows_after_last_segment(device):
     assert_bf16_close(dk.cpu(), rdk, grad_scale(rdk), "dk")
     assert_bf16_close(dv.cpu(), rdv, grad_scale(rdv), "dv")
     assert_bf16_close(dq[:70].cpu(), rdq, grad_scale(rdq), "dq")
+
+
+@pytest.mark.parametrize("shared_cu", [True, False])
+def test_edge_plan_reuse_matches_per_call_mask(device, shared_cu):
+    """A plan built once (esa_edge_plan_build) and passed to several forward / backward calls gives the same
+    bits as the per-call edge mask (the kernels are the same); with two cu_seqlens tensors the plan carries
+    the key tiles' own lists.  A group that overflows the key lists (a 600-token star) is part of the batch."""
+    gb = generators.protein_like(seed=14, num_graphs=4, n_min=64, n_max=200)
+    src_p, dst_p = gb.edge_index[0].astype(np.int32), gb.edge_index[1].astype(np.int32)
+    hub = int(max(src_p.max(), dst_p.max())) + 1
+    leaves = np.arange(hub + 1, hub + 301, dtype=np.int32)
+    c = gb.edge_counts
+    src = np.concatenate([src_p[:c[0]], np.full_like(leaves, hub), leaves, src_p[c[0]:]])
+    dst = np.concatenate([dst_p[:c[0]], leaves, np.full_like(leaves, hub), dst_p[c[0]:]])
+    lengths = [int(c[0]), 2 * leaves.size] + [int(x) for x in c[1:]]
+    cu_np = cu_from_lengths(lengths)
+    t = int(cu_np[-1])
+    cq = torch.as_tensor(cu_np, dtype=torch.int32).to(device)
+    ck = cq if shared_cu else torch.as_tensor(cu_np, dtype=torch.int32).to(device)
+    s_d, d_d = torch.as_tensor(src).to(device), torch.as_tensor(dst).to(device)
+    mx = int(max(lengths))
+    plan = A.edge_plan(s_d, d_d, cq, ck)
+    for seed in (301, 302):   # two different inputs over one plan
+        q, k, v, g = (x.to(device) for x in _inputs(t, t, seed))
+        o1, l1 = A.attn_fwd(q, k, v, cq, ck, mx, mx, 0.25, s_d, d_d)
+        o2, l2 = A.attn_fwd(q, k, v, cq, ck, mx, mx, 0.25, edge_plan=plan)
+        assert torch.equal(o1, o2) and torch.equal(l1, l2)
+        g1 = A.attn_bwd(g, q, k, v, o1, l1, cq, ck, mx, mx, 0.25, s_d, d_d)
+        g2 = A.attn_bwd(g, q, k, v, o1, l1, cq, ck, mx, mx, 0.25, edge_plan=plan)
+        for x1, x2 in zip(g1, g2):
+            assert torch.equal(x1, x2)
+    torch.cuda.synchronize()
+    ref, _ = OA.varlen_attention(q.cpu(), k.cpu(), v.cpu(), cu_np, cu_np, 0.25, src, dst)
+    assert_bf16_close(o2.cpu(), ref, what="out")
+
+
+def test_edge_plan_through_autograd_and_module_descriptor(device):
+    """varlen_attention(edge_plan=...) differentiates like the edge-mask call, and the EdgeAdjacency descriptor
+    builds its plan once and hands it to every masked layer."""
+    from mind_amd.esa.packing import EdgeAdjacency
+    gb = generators.protein_like(seed=15, num_graphs=3, n_min=50, n_max=120)
+    ei = torch.as_tensor(gb.edge_index).to(device)
+    bm = torch.as_tensor(gb.batch).to(device)
+    adj = EdgeAdjacency.from_edge_index(ei, bm, gb.num_graphs, int(gb.max_seqlen))
+    kw = adj.kernel_mask(padded=False)
+    assert set(kw) == {"edge_plan"} and adj.kernel_mask(padded=False)["edge_plan"] is kw["edge_plan"]
+    t = adj.num_tokens
+    q, k, v, g = _inputs(t, t, 401)
+    res = []
+    for mask in (kw, {"edge_src": adj.edge_src, "edge_dst": adj.edge_dst}):
+        qd, kd, vd = (x.to(device).requires_grad_(True) for x in (q, k, v))
+        out = A.varlen_attention(qd, kd, vd, adj.cu_seqlens, adj.cu_seqlens, adj.max_items, adj.max_items,
+                                 softmax_scale=0.25, **mask)
+        out.backward(g.to(device))
+        res.append((out.detach(), qd.grad, kd.grad, vd.grad))
+    for x1, x2 in zip(*res):
+        assert torch.equal(x1, x2)
