@@ -1047,25 +1047,30 @@ DEVI void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
-// Three stage buffers: stage s is staged in buffer s % 3 while stages s + 1
-// and s + 2 are in flight.  issue(stage, buf) issues a stage's loads (kPer
-// of them); past the last stage it re-issues the last one into the spare
-// buffer, so every wait covers exactly two stages of later loads.  A stage's
-// buffer is reloaded only after the stage's compute has consumed its reads.
-constexpr int kDmaDepth = 3;
+// kDmaDepth stage buffers: stage s is staged in buffer s % kDmaDepth while
+// the next kDmaDepth - 1 stages are in flight.  issue(stage, buf) issues a
+// stage's loads (kPer of them); past the last stage it re-issues the last one
+// into a spare buffer, so every wait covers exactly kDmaDepth - 1 stages of
+// later loads.  A stage's buffer is reloaded only after the stage's compute
+// has consumed its reads.
+#ifndef ESA_DMA_DEPTH
+#define ESA_DMA_DEPTH 2
+#endif
+constexpr int kDmaDepth = ESA_DMA_DEPTH;
+static_assert(kDmaDepth >= 2 && kDmaDepth <= 4, "stage buffers");
 template <int kPer, class Issue, class Compute>
 DEVI void dma_pipeline(int n, Issue issue, Compute compute) {
   if (n <= 0) return;
-  issue(0, 0);
-  issue(min(1, n - 1), 1);
-  int buf = 0;
+#pragma unroll
+  for (int i = 0; i < kDmaDepth - 1; ++i) issue(min(i, n - 1), i);
+  int buf = 0, nxt = kDmaDepth - 1;   // st % kDmaDepth, (st + kDmaDepth - 1) % kDmaDepth
   for (int st = 0; st < n; ++st) {
-    const int nxt = buf == 0 ? 2 : buf - 1;   // (st + 2) % 3
-    issue(min(st + 2, n - 1), nxt);
-    wait_vmcnt<2 * kPer>();
+    issue(min(st + kDmaDepth - 1, n - 1), nxt);
+    wait_vmcnt<(kDmaDepth - 1) * kPer>();
     wave_sync();
     compute(st, buf);
-    buf = buf == 2 ? 0 : buf + 1;
+    buf = buf == kDmaDepth - 1 ? 0 : buf + 1;
+    nxt = nxt == kDmaDepth - 1 ? 0 : nxt + 1;
   }
 }
 
@@ -1112,16 +1117,8 @@ __global__ __launch_bounds__(256) void list_fwd_kernel(const AttnArgs a) {
     const int hc = min(max(h0, 0) + u, H - 1);
     qf[u] = *reinterpret_cast<const bf16x8*>(a.q + ((size_t)oc * H + hc) * kHd + 8 * half);
   }
-  const int nct = list_block_ids(a, tile, sId, tid);
+  const int nct = list_block_ids(a, tile, sId, tid);   // no partners: acc stays 0, rows 0, lse -inf
   if (nct < 0 || nh <= 0) return;
-  if (nct == 0) {   // no partners: zero rows, lse -inf
-    if (!valid) return;
-    for (int u = 0; u < nh; ++u) {
-      store_rows8(a.o + ((size_t)oi * H + h0 + u) * kHd, f32x16{}, 0.f, half);
-      if (half == 0) a.lse_out[(size_t)(h0 + u) * a.total_q + oi] = -INFINITY;
-    }
-    return;
-  }
   bf16x8 qh[NH], ql[NH];
   float m_run[NH];
   f32x16 acc[NH];
@@ -1186,24 +1183,22 @@ __global__ __launch_bounds__(256) void list_fwd_kernel(const AttnArgs a) {
   }
 }
 
-// dQ over the key lists: one wave = one 32-query tile and kEdgeHeads heads,
-// as the walk kernel's dQ pass.
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ESA_LIST_WAVES_DQ))) void list_dq_kernel(
-    const AttnArgs a) {
+// dQ over the key lists: one wave = one 32-query tile and kListHeads heads,
+// blocks and staging as the forward.  Each wave also writes its heads' row
+// statistics of the dK/dV pass (every tile, also those the walk kernels take).
+__global__ __launch_bounds__(256) void list_dq_kernel(const AttnArgs a) {
   constexpr int NH = kListHeads;
-  __shared__ __align__(16) bf16 sK[kWaves][2][NH][2 * kTileHalf];   // K rows split by dims half
-  __shared__ __align__(16) bf16 sV[kWaves][2][NH][2 * kTileHalf];   // V rows split by dims half
-  __shared__ int sId[kWaves][kListCap];
+  __shared__ __align__(16) bf16 sK[kWaves][kDmaDepth][NH][2 * kTileHalf];   // K rows split by dims half
+  __shared__ __align__(16) bf16 sV[kWaves][kDmaDepth][NH][2 * kTileHalf];   // V rows split by dims half
+  __shared__ __align__(16) uint32_t sW[kWaves][kDmaDepth][64];               // mask words (lane col)
+  __shared__ int sId[kListCap];
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 31, half = lane >> 5, c16 = lane & 15, grp = lane >> 4;
-  const int H = a.heads, n_hg = (H + NH - 1) / NH;
-  const int idx = list_item((((a.total_q) + kGroupTok - 1) / kGroupTok) * n_hg);
+  const int H = a.heads, n_hg = (H + NH - 1) / NH, n_hq = (n_hg + kWaves - 1) / kWaves;
+  const int idx = list_item(((a.total_q + kTile - 1) / kTile) * n_hq);
   if (idx < 0) return;
-  const int item = idx / n_hg, hg = idx - item * n_hg;
-  const int h0 = hg * NH;
-  const int nh = min(NH, H - h0);   // heads of this wave
-  const int tile = item * kWaves + wave;
-  if (tile * kTile >= a.total_q) return;
+  const int tile = idx / n_hq, hg = (idx - tile * n_hq) * kWaves + wave;
+  const int h0 = hg * NH, nh = min(NH, H - h0);   // nh <= 0: a wave without heads
   const int oi = tile * kTile + col;
   const bool valid = oi < a.total_q;
   const int oc = valid ? oi : a.total_q - 1;
@@ -1211,7 +1206,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ESA_LIST_WA
   float lq[NH];
 #pragma unroll
   for (int u = 0; u < NH; ++u) {
-    const int hc = min(h0 + u, H - 1);
+    const int hc = min(max(h0, 0) + u, H - 1);
     const size_t row = ((size_t)oc * H + hc) * kHd + 8 * half;
     qf[u] = *reinterpret_cast<const bf16x8*>(a.q + row);
     dof[u] = *reinterpret_cast<const bf16x8*>(a.dout + row);
@@ -1229,63 +1224,43 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ESA_LIST_WA
     lse2q[u] = lq[u] == -INFINITY ? INFINITY : lq[u] * kLog2e;
     acc[u] = f32x16{};
     // Row statistics of the dK/dV pass, as bf16 (hi, lo) pairs: -LSE2/c (-1e30
-    // for rows without keys and padding: their P is 0) and -D.  Written for
-    // every tile, also those the walk kernels take.
+    // for rows without keys and padding: their P is 0) and -D.
     if (half == 0 && u < nh) {
       const float xs = valid && lq[u] != -INFINITY ? -(lq[u] * kLog2e) / a.c : kDeadRow;
       a.aux_out[(size_t)(h0 + u) * a.tq_pad + oi] =
           make_uint2(split_bf16_pair(xs), split_bf16_pair(valid ? -dsum[u] : 0.f));
     }
   }
-  const int nct = list_tile(a, tile, sId[wave], lane);
-  if (nct < 0) return;
+  const int nct = list_block_ids(a, tile, sId, tid);
+  if (nct < 0 || nh <= 0) return;
   const f32x16 zero = {};
   const uint32_t kv_bytes = (uint32_t)a.total_k * H * kHd * 2;
   const rsrc_t rk = make_rsrc(a.k, kv_bytes), rv = make_rsrc(a.v, kv_bytes);
-  const uint32_t* wsrc = a.bits + (size_t)tile * kListCap + col;
-  uint32_t wreg[2] = {0u, 0u};
-  int c_next = 0;
-  tile_pipeline(
+  const rsrc_t rw = make_rsrc(a.bits + (size_t)tile * kListCap, (uint32_t)kListCap * 4u);
+  dma_pipeline<2 * NH + 1>(
       nct,
-      [&](uint32_t& w) {
-        w = 0xfu;
-        const int c = min(c_next, nct - 1);
-        ++c_next;
-        return c;
-      },
-      [&](int c) {
-        StageList<NH> g;
-        const int id = sId[wave][c * kTile + col];
+      [&](int c, int buf) {
+        const int id = sId[c * kTile + col];
 #pragma unroll
         for (int u = 0; u < NH; ++u) {
           const uint32_t off = list_row_off(id, H, min(h0 + u, H - 1), half);
-          g.k[u] = bload(rk, off);
-          g.v[u] = bload(rv, off);
+          dma16(rk, off, sK[wave][buf][u]);
+          dma16(rv, off, sV[wave][buf][u]);
         }
-        g.w = wsrc[c * kTile];
-        return g;
+        dma4(rw, (uint32_t)(c * kTile + col) * 4u, sW[wave][buf]);
       },
-      [&](int st, const StageList<NH>& g) {
-#pragma unroll
-        for (int u = 0; u < NH; ++u) {
-          put_half<kTileHalf>(sK[wave][st][u], col, half, g.k[u]);
-          put_half<kTileHalf>(sV[wave][st][u], col, half, g.v[u]);
-        }
-        wreg[st] = g.w;
-      },
-      wave_sync,
-      [&](int, int cur, uint32_t) {
-        const f32x16 bias = word_bias(wreg[cur], half);
+      [&](int, int buf) {
+        const f32x16 bias = word_bias(sW[wave][buf][col], half);
 #pragma unroll
         for (int u = 0; u < NH; ++u) {
           if (u >= nh) break;   // wave-uniform
-          const f32x16 s = mfma32(half_row8<kTileHalf>(sK[wave][cur][u], kperm(col), half), qf[u], bias);
-          const f32x16 dp = mfma32(half_row8<kTileHalf>(sV[wave][cur][u], kperm(col), half), dof[u], zero);
+          const f32x16 s = mfma32(half_row8<kTileHalf>(sK[wave][buf][u], kperm(col), half), qf[u], bias);
+          const f32x16 dp = mfma32(half_row8<kTileHalf>(sV[wave][buf][u], kperm(col), half), dof[u], zero);
           float ds[16];
 #pragma unroll
           for (int r = 0; r < 16; ++r) ds[r] = fast_exp2(fmaf(s[r], a.c, -lse2q[u])) * (dp[r] - dsum[u]);
           bf16x8 kt0, kt1;
-          tr_rows32<kTileHalf>(sK[wave][cur][u], 0, nullptr, c16, grp, kt0, kt1);
+          tr_rows32<kTileHalf>(sK[wave][buf][u], 0, nullptr, c16, grp, kt0, kt1);
           acc[u] = mfma32(kt0, cvt8(ds), acc[u]);
           acc[u] = mfma32(kt1, cvt8(ds + 8), acc[u]);
         }
@@ -1298,15 +1273,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ESA_LIST_WA
   }
 }
 
-template <int NH>
-struct StageListKv { i32x4 q[NH], d[NH]; uint2 x[(NH + 1) / 2]; uint32_t w; };
-
 // dK/dV over the key lists (of the key tiles, or of the query tiles when the
-// mask is symmetric): one wave = one 32-key tile and kEdgeHeadsKv heads, as
-// the walk kernel's dK/dV pass.  Lanes of half j load the row statistics of
-// head 2 i + j of the partner queries.
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ESA_LIST_WAVES_DKDV))) void list_dkdv_kernel(
-    const AttnArgs a0) {
+// mask is symmetric): one wave = one 32-key tile and kListHeadsKv heads,
+// blocks and staging as the forward.  A stage gathers the partner queries'
+// Q and dO rows and their row statistics (per two heads, the records'
+// two words in [2][64] arrays: lanes of half j carry head 2 i + j).
+__global__ __launch_bounds__(256) void list_dkdv_kernel(const AttnArgs a0) {
   AttnArgs a = a0;
   if (!*a0.sym) {   // the key tiles' own lists
     a.info = a0.kinfo;
@@ -1314,20 +1286,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ESA_LIST_WA
     a.bits = a0.kbits;
   }
   constexpr int NH = kListHeadsKv;
-  __shared__ __align__(16) bf16 sQ[kWaves][2][NH][2 * kTileHalf];    // Q rows split by dims half
-  __shared__ __align__(16) bf16 sDO[kWaves][2][NH][2 * kTileHalf];   // dO rows split by dims half
-  __shared__ __align__(16) uint2 sAux[kWaves][2][NH][kTile];         // row-statistic MFMA operands
-  __shared__ int sId[kWaves][kListCap];
+  constexpr int NA = (NH + 1) / 2;   // row-statistic record pairs per stage
+  __shared__ __align__(16) bf16 sQ[kWaves][kDmaDepth][NH][2 * kTileHalf];    // Q rows split by dims half
+  __shared__ __align__(16) bf16 sDO[kWaves][kDmaDepth][NH][2 * kTileHalf];   // dO rows split by dims half
+  __shared__ __align__(16) uint32_t sAux[kWaves][kDmaDepth][NA][2][64];     // row-statistic MFMA operands
+  __shared__ __align__(16) uint32_t sW[kWaves][kDmaDepth][64];               // mask words (lane col)
+  __shared__ int sId[kListCap];
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 31, half = lane >> 5, c16 = lane & 15, grp = lane >> 4;
-  const int H = a.heads, n_hg = (H + NH - 1) / NH;
-  const int idx = list_item((((a.total_k) + kGroupTok - 1) / kGroupTok) * n_hg);
+  const int H = a.heads, n_hg = (H + NH - 1) / NH, n_hq = (n_hg + kWaves - 1) / kWaves;
+  const int idx = list_item(((a.total_k + kTile - 1) / kTile) * n_hq);
   if (idx < 0) return;
-  const int item = idx / n_hg, hg = idx - item * n_hg;
-  const int h0 = hg * NH;
-  const int nh = min(NH, H - h0);   // heads of this wave
-  const int tile = item * kWaves + wave;
-  if (tile * kTile >= a.total_k) return;
+  const int tile = idx / n_hq, hg = (idx - tile * n_hq) * kWaves + wave;
+  const int h0 = hg * NH, nh = min(NH, H - h0);   // nh <= 0: a wave without heads
   const int oi = tile * kTile + col;
   const bool valid = oi < a.total_k;
   const int oc = valid ? oi : a.total_k - 1;
@@ -1335,13 +1306,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ESA_LIST_WA
   f32x16 dva[NH], dka[NH];
 #pragma unroll
   for (int u = 0; u < NH; ++u) {
-    const size_t row = ((size_t)oc * H + min(h0 + u, H - 1)) * kHd + 8 * half;
+    const size_t row = ((size_t)oc * H + min(max(h0, 0) + u, H - 1)) * kHd + 8 * half;
     kf[u] = *reinterpret_cast<const bf16x8*>(a.k + row);
     vf[u] = *reinterpret_cast<const bf16x8*>(a.v + row);
     dva[u] = dka[u] = f32x16{};
   }
-  const int nct = list_tile(a, tile, sId[wave], lane);
-  if (nct < 0) return;
+  const int nct = list_block_ids(a, tile, sId, tid);
+  if (nct < 0 || nh <= 0) return;
   // B operand of the row-statistic MFMAs: ones in slots 0 and 1 (half 0).
   bf16x8 ones2 = {};
   if (half == 0) { ones2[0] = (bf16)1.f; ones2[1] = (bf16)1.f; }
@@ -1349,61 +1320,39 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ESA_LIST_WA
   const uint32_t q_bytes = (uint32_t)a.total_q * H * kHd * 2;
   const rsrc_t rq = make_rsrc(a.q, q_bytes), rd = make_rsrc(a.dout, q_bytes);
   const rsrc_t rx = make_rsrc(a.aux, (uint32_t)H * a.tq_pad * 8u);
-  const uint32_t* wsrc = a.bits + (size_t)tile * kListCap + col;
-  uint32_t wreg[2] = {0u, 0u};
-  int c_next = 0;
-  tile_pipeline(
+  const rsrc_t rw = make_rsrc(a.bits + (size_t)tile * kListCap, (uint32_t)kListCap * 4u);
+  dma_pipeline<2 * NH + 2 * NA + 1>(
       nct,
-      [&](uint32_t& w) {
-        w = 0xfu;
-        const int c = min(c_next, nct - 1);
-        ++c_next;
-        return c;
-      },
-      [&](int c) {
-        StageListKv<NH> g;
-        const int id = sId[wave][c * kTile + col];
+      [&](int c, int buf) {
+        const int id = sId[c * kTile + col];
 #pragma unroll
         for (int u = 0; u < NH; ++u) {
           const uint32_t off = list_row_off(id, H, min(h0 + u, H - 1), half);
-          g.q[u] = bload(rq, off);
-          g.d[u] = bload(rd, off);
+          dma16(rq, off, sQ[wave][buf][u]);
+          dma16(rd, off, sDO[wave][buf][u]);
         }
 #pragma unroll
-        for (int i = 0; i < (NH + 1) / 2; ++i) {
+        for (int i = 0; i < NA; ++i) {
           const int hc = min(h0 + 2 * i + half, H - 1);
           const uint32_t off = id < 0 ? 0x80000000u : ((uint32_t)hc * a.tq_pad + id) * 8u;
-          const auto x = __builtin_amdgcn_raw_buffer_load_b64(rx, off, 0, 0);
-          g.x[i] = make_uint2(x[0], x[1]);
+          dma4(rx, off, sAux[wave][buf][i][0]);
+          dma4(rx, off + 4u, sAux[wave][buf][i][1]);
         }
-        g.w = wsrc[c * kTile];
-        return g;
+        dma4(rw, (uint32_t)(c * kTile + col) * 4u, sW[wave][buf]);
       },
-      [&](int st, const StageListKv<NH>& g) {
-#pragma unroll
-        for (int u = 0; u < NH; ++u) {
-          put_half<kTileHalf>(sQ[wave][st][u], col, half, g.q[u]);
-          put_half<kTileHalf>(sDO[wave][st][u], col, half, g.d[u]);
-        }
-#pragma unroll
-        for (int i = 0; i < (NH + 1) / 2; ++i)
-          if (2 * i + half < NH) sAux[wave][st][2 * i + half][col] = g.x[i];
-        wreg[st] = g.w;
-      },
-      wave_sync,
-      [&](int, int cur, uint32_t) {
-        const f32x16 bias = word_bias(wreg[cur], half);
+      [&](int, int buf) {
+        const f32x16 bias = word_bias(sW[wave][buf][col], half);
 #pragma unroll
         for (int u = 0; u < NH; ++u) {
           if (u >= nh) break;   // wave-uniform
-          const uint2 ax = sAux[wave][cur][u][kperm(col)];
-          const bf16x8 aux_s = as_bf16x8(i32x4{(int)ax.x, 0, 0, 0});
-          const bf16x8 aux_d = as_bf16x8(i32x4{(int)ax.y, 0, 0, 0});
+          const int ar = (u & 1) * kTile + kperm(col);
+          const bf16x8 aux_s = as_bf16x8(i32x4{(int)sAux[wave][buf][u >> 1][0][ar], 0, 0, 0});
+          const bf16x8 aux_d = as_bf16x8(i32x4{(int)sAux[wave][buf][u >> 1][1][ar], 0, 0, 0});
           // S' = Q K^T - LSE2/c + bias and dP' = dO V^T - D, rows = queries, lanes = keys.
           const f32x16 s =
-              mfma32(half_row8<kTileHalf>(sQ[wave][cur][u], kperm(col), half), kf[u], mfma32(aux_s, ones2, bias));
+              mfma32(half_row8<kTileHalf>(sQ[wave][buf][u], kperm(col), half), kf[u], mfma32(aux_s, ones2, bias));
           const f32x16 dp =
-              mfma32(half_row8<kTileHalf>(sDO[wave][cur][u], kperm(col), half), vf[u], mfma32(aux_d, ones2, zero));
+              mfma32(half_row8<kTileHalf>(sDO[wave][buf][u], kperm(col), half), vf[u], mfma32(aux_d, ones2, zero));
           float p[16], ds[16];
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
@@ -1411,8 +1360,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ESA_LIST_WA
             ds[r] = p[r] * dp[r];
           }
           bf16x8 d0, d1, q0t, q1t;
-          tr_rows32<kTileHalf>(sDO[wave][cur][u], 0, nullptr, c16, grp, d0, d1);
-          tr_rows32<kTileHalf>(sQ[wave][cur][u], 0, nullptr, c16, grp, q0t, q1t);
+          tr_rows32<kTileHalf>(sDO[wave][buf][u], 0, nullptr, c16, grp, d0, d1);
+          tr_rows32<kTileHalf>(sQ[wave][buf][u], 0, nullptr, c16, grp, q0t, q1t);
           dva[u] = mfma32(d0, cvt8(p), dva[u]);
           dva[u] = mfma32(d1, cvt8(p + 8), dva[u]);
           dka[u] = mfma32(q0t, cvt8(ds), dka[u]);
@@ -1984,7 +1933,10 @@ unsigned list_tile_blocks(int total, unsigned n_hw) {
   return (n + kXcds - 1) / kXcds * kXcds;
 }
 
-constexpr int kOverflowGroups = 64;   // groups in flight in a walk kernel over the overflow list
+#ifndef ESA_OVERFLOW_GROUPS
+#define ESA_OVERFLOW_GROUPS 64
+#endif
+constexpr int kOverflowGroups = ESA_OVERFLOW_GROUPS;   // groups in flight in a walk kernel over the overflow list
 unsigned overflow_blocks(int total) { return (unsigned)std::min(groups_of(total), kOverflowGroups); }
 
 // Builds an edge-mask plan: one prep launch (node pairs, tile metadata,
@@ -2363,7 +2315,8 @@ int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k, const vo
   a.bounds = V.bounds_q;
   a.info = V.info[0]; a.ids = V.ids[0]; a.bits = V.bits[0];
   ESA_TIMED(esa_profile::kAttnBwdDqMasked, st,
-            hipLaunchKernelGGL(list_dq_kernel, dim3(list_blocks(total_q, n_hg)), dim3(256), 0, st, a));
+            hipLaunchKernelGGL(list_dq_kernel, dim3(list_tile_blocks(total_q, (n_hg + kWaves - 1) / kWaves)), dim3(256),
+                               0, st, a));
   ESA_LAUNCH_CHECK();
   a.plan = V.over[0];
   a.count = V.over_count;
@@ -2375,7 +2328,8 @@ int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k, const vo
   const unsigned n_hg_kv_walk = (unsigned)((heads + kEdgeHeadsKv - 1) / kEdgeHeadsKv);
   a.bounds = V.bounds_k;
   ESA_TIMED(esa_profile::kAttnBwdDkdvMasked, st,
-            hipLaunchKernelGGL(list_dkdv_kernel, dim3(list_blocks(total_k, n_hg_kv)), dim3(256), 0, st, a));
+            hipLaunchKernelGGL(list_dkdv_kernel, dim3(list_tile_blocks(total_k, (n_hg_kv + kWaves - 1) / kWaves)),
+                               dim3(256), 0, st, a));
   ESA_LAUNCH_CHECK();
   ESA_TIMED(esa_profile::kAttnEdgeOverflow, st,
             hipLaunchKernelGGL(edge_dkdv_kernel, dim3(overflow_blocks(total_k) * n_hg_kv_walk), dim3(256), 0, st, a));
