@@ -1944,7 +1944,7 @@ unsigned overflow_blocks(int total) { return (unsigned)std::min(groups_of(total)
 // `key_lists`, of the key tiles.  The flag is 1 without key-tile lists (the
 // query and key segments are one array: the mask is symmetric).
 int build_edge_plan(const int* tok_src, const int* tok_dst, const int* cu_q, const int* cu_k, int batch,
-                    int total_q, int total_k, void* plan, bool key_lists, hipStream_t st) {
+                    int total_q, int total_k, void* plan, bool key_lists, hipStream_t st, bool lists = true) {
   const PlanLayout P = plan_layout(total_q, total_k, key_lists);
   char* b = static_cast<char*>(plan);
   PrepArgs pa{};
@@ -1960,7 +1960,7 @@ int build_edge_plan(const int* tok_src, const int* tok_dst, const int* cu_q, con
   pa.flags = reinterpret_cast<int*>(b + P.flags);
   pa.sym = key_lists ? 0 : 1;
   int rc = launch_prep(pa, kTaskMask, st);
-  if (rc) return rc;
+  if (rc || !lists) return rc;
   ListArgs la{};
   la.nodes = pa.nodes; la.meta = pa.meta;
   la.total = total_q;
@@ -1980,16 +1980,17 @@ int build_edge_plan(const int* tok_src, const int* tok_dst, const int* cu_q, con
 }
 
 // The plan of a masked call: the caller's (ESA_MASK_EDGE_PLAN: mask_a points
-// at it) or one built into the call's workspace from the node ids.
+// at it) or one built into the call's workspace from the node ids (without
+// key lists for the fp32 kernels, which read only the node pairs).
 int call_plan(int mask_kind, const int* mask_a, const int* mask_b, const int* cu_q, const int* cu_k, int batch,
-              int total_q, int total_k, char* ws, const WsLayout& L, bool key_lists, hipStream_t st,
+              int total_q, int total_k, char* ws, const WsLayout& L, bool key_lists, bool lists, hipStream_t st,
               const void** plan) {
   if (mask_kind == ESA_MASK_EDGE_PLAN) {
     *plan = mask_a;
     return ESA_OK;
   }
   *plan = ws + L.plan;
-  return build_edge_plan(mask_a, mask_b, cu_q, cu_k, batch, total_q, total_k, ws + L.plan, key_lists, st);
+  return build_edge_plan(mask_a, mask_b, cu_q, cu_k, batch, total_q, total_k, ws + L.plan, key_lists, st, lists);
 }
 
 // Scratch of esa_varlen_attn_fwd_noalloc: a file-scope device array, one
@@ -2112,7 +2113,7 @@ int esa_varlen_attn_fwd(const void* q, const void* k, const void* v, const int* 
   char* ws = static_cast<char*>(workspace);
   const void* plan = nullptr;
   if (masked && (rc = call_plan(mask_kind, mask_a, mask_b, cu_seqlens_q, cu_seqlens_k, batch, total_q, total_k, ws,
-                                L, false, st, &plan)))
+                                L, false, !f32, st, &plan)))
     return rc;
 
   if (f32) {
@@ -2251,7 +2252,7 @@ int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k, const vo
   char* ws = static_cast<char*>(workspace);
   const void* plan = nullptr;
   if (masked && (rc = call_plan(mask_kind, mask_a, mask_b, cu_seqlens_q, cu_seqlens_k, batch, total_q, total_k, ws,
-                                L, key_lists, st, &plan)))
+                                L, key_lists, !f32, st, &plan)))
     return rc;
 
   if (f32) {
