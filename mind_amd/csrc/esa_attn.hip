@@ -1017,36 +1017,8 @@ template <int NH>
 struct StageList { i32x4 k[NH], v[NH]; uint32_t w; };
 
 
-// ---- LDS-direct staging of the list kernels
-// buffer_load_dwordx4 / _dword with the LDS flag: lane l's 16 (4) bytes land
-// at M0 + 16 l (4 l), so a split-row tile (lane = token col of dims half l >> 5)
-// stages with one instruction per head and tensor and no staging registers.
-// Loads past the buffer range write zeros.  Issued as assembly: the
-// compiler's wait-count pass does not see them (its own waits only get more
-// conservative), and the stage loop waits for them explicitly.  M0 is set
-// right before each load (one SALU wait state); nothing else in these
-// kernels uses M0.
-DEVI uint32_t lds_addr(const void* p) {
-  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p);
-}
-DEVI void dma16(rsrc_t r, uint32_t off, const void* lds) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %2, 0 offen lds" ::"v"(off), "s"(lds_addr(lds)),
-               "s"(r)
-               : "memory");
-}
-DEVI void dma4(rsrc_t r, uint32_t off, const void* lds) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_dword %0, %2, 0 offen lds" ::"v"(off), "s"(lds_addr(lds)),
-               "s"(r)
-               : "memory");
-}
-// s_waitcnt vmcnt(n) (gfx9 encoding: vmcnt bits 3:0 and 15:14; expcnt and
-// lgkmcnt at their maxima, i.e. not waited for).
-template <int N>
-DEVI void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
+// ---- LDS-direct staging of the list kernels (dma16 / dma4 / wait_vmcnt:
+// esa_attn_tiles.h)
 // kDmaDepth stage buffers: stage s is staged in buffer s % kDmaDepth while
 // the next kDmaDepth - 1 stages are in flight.  issue(stage, buf) issues a
 // stage's loads (kPer of them); past the last stage it re-issues the last one
@@ -1072,6 +1044,7 @@ DEVI void dma_pipeline(int n, Issue issue, Compute compute) {
     buf = buf == kDmaDepth - 1 ? 0 : buf + 1;
     nxt = nxt == kDmaDepth - 1 ? 0 : nxt + 1;
   }
+  wait_vmcnt<0>();   // the re-issued loads land before the wave's LDS can be reallocated
 }
 
 // Blocks of the list kernels: one 32-token tile and kWaves head groups (one

@@ -234,6 +234,36 @@ DEVI uint32_t split_bf16_pair(float x) {
   return (uint32_t)__builtin_bit_cast(uint16_t, hi) | ((uint32_t)__builtin_bit_cast(uint16_t, lo) << 16);
 }
 
+// ---- LDS-direct staging (list kernels, dense dK/dV)
+// buffer_load_dwordx4 / _dword with the LDS flag: lane l's 16 (4) bytes land
+// at M0 + 16 l (4 l), so a split-row tile (lane = token col of dims half l >> 5)
+// stages with one instruction per head and tensor and no staging registers.
+// Loads past the buffer range write zeros.  Issued as assembly: the
+// compiler's wait-count pass does not see them (its own waits only get more
+// conservative), and the stage loop waits for them explicitly.  M0 is set
+// right before each load (one SALU wait state); nothing else in these
+// kernels uses M0.
+DEVI uint32_t lds_addr(const void* p) {
+  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p);
+}
+DEVI void dma16(rsrc_t r, uint32_t off, const void* lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %2, 0 offen lds" ::"v"(off), "s"(lds_addr(lds)),
+               "s"(r)
+               : "memory");
+}
+DEVI void dma4(rsrc_t r, uint32_t off, const void* lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_dword %0, %2, 0 offen lds" ::"v"(off), "s"(lds_addr(lds)),
+               "s"(r)
+               : "memory");
+}
+// s_waitcnt vmcnt(n) (gfx9 encoding: vmcnt bits 3:0 and 15:14; expcnt and
+// lgkmcnt at their maxima, i.e. not waited for).
+template <int N>
+DEVI void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
 // ---- per-segment work plans (dense bf16 and fp32 attention kernels)
 // Groups of one direction: every segment's outer tokens cut into groups of
 // `gtok` tokens (one block each), segments ordered by partner tiles (longest first, counting sort in
