@@ -62,20 +62,24 @@ struct DenseArgs {
 // ------------------------------------------------------------------ block mapping
 // Hardware block b runs on XCD b % 8, and each XCD has its own L2.  A 128-byte
 // line of a [T][H][16] bf16 tensor holds one token's rows of four
-// consecutive heads, so with 16 heads the blocks are mapped so that XCD x
-// serves the heads of one line (4 (x / 2) .. 4 (x / 2) + 3) and every other
-// group (parity x % 2): each line is fetched by two XCDs, not four.  Other
-// head counts use head = b % heads.
+// consecutive heads ("a line group").  For H = 4, 8, 16 or 32 the blocks are
+// mapped so that each XCD serves the four heads of one line group: with
+// lines = H / 4 groups, r = 8 / lines XCDs share one line group and each
+// takes every r-th work item (H = 32: one XCD per line group, each line
+// fetched by one L2; H = 16: two).  Other head counts use head = b % heads.
 #ifndef ESA_DENSE_XCD_LINES
 #define ESA_DENSE_XCD_LINES 1
 #endif
 
+DEVI bool xcd_lines(int H) { return ESA_DENSE_XCD_LINES && (H == 4 || H == 8 || H == 16 || H == 32); }
+
 DEVI void block_item_head(int H, int& item, int& head) {
   const int b = blockIdx.x;
-  if (ESA_DENSE_XCD_LINES && H == 16) {
+  if (xcd_lines(H)) {
+    const int r = 32 / H;   // XCDs per line group: 8 / (H / 4)
     const int xcd = b & 7, slot = b >> 3;
-    head = 4 * (xcd >> 1) + (slot & 3);
-    item = 2 * (slot >> 2) + (xcd & 1);
+    head = 4 * (xcd / r) + (slot & 3);
+    item = r * (slot >> 2) + xcd % r;
   } else {
     item = b / H;
     head = b - item * H;
@@ -83,7 +87,10 @@ DEVI void block_item_head(int H, int& item, int& head) {
 }
 
 unsigned group_blocks(int groups, int H) {
-  if (ESA_DENSE_XCD_LINES && H == 16) return (unsigned)(((groups + 1) / 2) * 2 * H);
+  if (ESA_DENSE_XCD_LINES && (H == 4 || H == 8 || H == 16 || H == 32)) {
+    const int r = 32 / H;
+    return (unsigned)(32 * ((groups + r - 1) / r));   // 8 XCDs x 4 heads x ceil(groups / r) items
+  }
   return (unsigned)(groups * H);
 }
 

@@ -83,6 +83,14 @@ def test_dense_heads_not_multiple_of_four(device):
     _check(device, [40, 70], [40, 70], seed=5, heads=6)
 
 
+@pytest.mark.parametrize("heads", [4, 8, 32])
+def test_dense_xcd_line_mappings(device, heads):
+    """Head counts whose blocks are mapped by 128-byte line group onto the XCDs (one XCD per line group at 32
+    heads, two at 16, four at 8, eight at 4): every (group, head) work item runs once, with ragged segments
+    longer than a group and an odd number of groups."""
+    _check(device, [300, 1, 129, 64, 0, 257], [300, 1, 129, 64, 0, 257], seed=40 + heads, heads=heads)
+
+
 @pytest.mark.parametrize("seeds", [1, 4, 32])
 def test_cross_attention_pma_shape(device, seeds):
     # PMA: k seeds per graph attend over the graph's tokens.
