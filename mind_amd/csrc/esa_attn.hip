@@ -551,13 +551,6 @@ DEVI void edge_dq_group(const AttnArgs& a, int item, int hg) {
   }
 }
 
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ESA_EDGE_WAVES_DQ))) void edge_dq_kernel(
-    const AttnArgs a) {
-  const int n_hg = (a.heads + kEdgeHeads - 1) / kEdgeHeads, hg = blockIdx.x % n_hg;
-  const int n_items = *a.count;
-  for (int item = blockIdx.x / n_hg; item < n_items; item += gridDim.x / n_hg) edge_dq_group(a, item, hg);
-}
-
 // ======================================================================== edge-mask dK/dV pass
 // One wave = one 32-key tile (keys on lanes, queries in rows) and
 // kEdgeHeadsKv heads of it: dV = P^T dO, dK = scale * dS^T Q.  Row
@@ -681,16 +674,27 @@ DEVI void edge_dkdv_group(const AttnArgs& a, int item, int hg) {
   }
 }
 
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ESA_EDGE_WAVES_DKDV))) void edge_dkdv_kernel(
-    const AttnArgs a0) {
-  AttnArgs a = a0;
-  if (a0.sym && !*a0.sym) {   // the key tiles' own overflow groups
-    a.plan = a0.kover;
-    a.count = a0.kcount;
+// The backward walks over the overflowing groups in one launch: both read only the row statistics the list
+// dQ pass wrote, and they write disjoint outputs (dQ of the query tiles' groups, dK / dV of the key tiles'),
+// so blocks [0, dq_blocks) take the dQ walk and the rest the dK/dV walk.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(
+    ESA_EDGE_WAVES_DQ < ESA_EDGE_WAVES_DKDV ? ESA_EDGE_WAVES_DQ : ESA_EDGE_WAVES_DKDV))) void edge_bwd_walk_kernel(
+    const AttnArgs adq, const AttnArgs akv, int dq_blocks) {
+  if ((int)blockIdx.x < dq_blocks) {
+    const int n_hg = (adq.heads + kEdgeHeads - 1) / kEdgeHeads, hg = blockIdx.x % n_hg;
+    const int n_items = *adq.count;
+    for (int item = blockIdx.x / n_hg; item < n_items; item += dq_blocks / n_hg) edge_dq_group(adq, item, hg);
+    return;
   }
-  const int n_hg = (a.heads + kEdgeHeadsKv - 1) / kEdgeHeadsKv, hg = blockIdx.x % n_hg;
+  AttnArgs a = akv;
+  if (akv.sym && !*akv.sym) {   // the key tiles' own overflow groups
+    a.plan = akv.kover;
+    a.count = akv.kcount;
+  }
+  const int b = blockIdx.x - dq_blocks, nb = gridDim.x - dq_blocks;
+  const int n_hg = (a.heads + kEdgeHeadsKv - 1) / kEdgeHeadsKv, hg = b % n_hg;
   const int n_items = *a.count;
-  for (int item = blockIdx.x / n_hg; item < n_items; item += gridDim.x / n_hg) edge_dkdv_group(a, item, hg);
+  for (int item = b / n_hg; item < n_items; item += nb / n_hg) edge_dkdv_group(a, item, hg);
 }
 
 // ======================================================================== edge-mask key lists
@@ -2266,9 +2270,9 @@ int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k, const vo
     return ESA_OK;
   }
 
-  // bf16 edge mask: dQ first (its list pass writes the row statistics the
-  // dK/dV passes read), each list pass followed by the walk kernel over the
-  // overflowing groups.
+  // bf16 edge mask: the dQ list pass first (it writes the row statistics the
+  // dK/dV passes read), then the dK/dV list pass, then one launch of the dQ
+  // and dK/dV walk kernels over the overflowing groups.
   const PlanView V = plan_view(plan, total_q, total_k);
   AttnArgs a{};
   a.q = static_cast<const bf16*>(q); a.k = static_cast<const bf16*>(k); a.v = static_cast<const bf16*>(v);
@@ -2294,9 +2298,7 @@ int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k, const vo
   ESA_LAUNCH_CHECK();
   a.plan = V.over[0];
   a.count = V.over_count;
-  ESA_TIMED(esa_profile::kAttnEdgeOverflow, st,
-            hipLaunchKernelGGL(edge_dq_kernel, dim3(overflow_blocks(total_q) * n_hg_walk), dim3(256), 0, st, a));
-  ESA_LAUNCH_CHECK();
+  AttnArgs adq = a;   // the dQ walk's arguments (query tiles' overflow groups and bounds)
 
   const unsigned n_hg_kv = (unsigned)((heads + kListHeadsKv - 1) / kListHeadsKv);
   const unsigned n_hg_kv_walk = (unsigned)((heads + kEdgeHeadsKv - 1) / kEdgeHeadsKv);
@@ -2305,8 +2307,10 @@ int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k, const vo
             hipLaunchKernelGGL(list_dkdv_kernel, dim3(list_tile_blocks(total_k, (n_hg_kv + kWaves - 1) / kWaves)),
                                dim3(256), 0, st, a));
   ESA_LAUNCH_CHECK();
+  const unsigned dq_blocks = overflow_blocks(total_q) * n_hg_walk;
   ESA_TIMED(esa_profile::kAttnEdgeOverflow, st,
-            hipLaunchKernelGGL(edge_dkdv_kernel, dim3(overflow_blocks(total_k) * n_hg_kv_walk), dim3(256), 0, st, a));
+            hipLaunchKernelGGL(edge_bwd_walk_kernel, dim3(dq_blocks + overflow_blocks(total_k) * n_hg_kv_walk),
+                               dim3(256), 0, st, adq, a, (int)dq_blocks));
   ESA_LAUNCH_CHECK();
   return ESA_OK;
 }
