@@ -1362,8 +1362,12 @@ __global__ __launch_bounds__(256) void list_dkdv_kernel(const AttnArgs a0) {
 // first: a block walks only its own segment's partners, so few-query
 // segments such as PMA seeds get one block per segment and head), partner
 // runs of 32 tokens staged in LDS and read by broadcast.  Scores, softmax and both
-// products are fp32 FMA chains in a fixed order; exp2f / log2f are the
-// device library's correctly rounded-to-1-ulp versions.
+// products are fp32 FMA chains in a fixed order.  Exponentials and the
+// log-sum-exp use the hardware v_exp_f32 / v_log_f32 (about 1 ulp): every
+// exponent is <= 0 (a score minus the running maximum or the row's LSE2) and
+// every log argument >= 1 (the row sum includes the maximum's 1), so the
+// flushed denormal results of the hardware ops are below 2^-126 of the
+// row's weights.
 
 struct AttnF32Args {
   const float* q; const float* k; const float* v; const float* out; const float* dout;
@@ -1472,7 +1476,7 @@ __global__ __launch_bounds__(kF32Threads) void attn_fwd_f32_kernel(const AttnF32
     }
     if (mt == -INFINITY) continue;
     if (mt > m) {
-      const float alpha = exp2f(m - mt);   // 0 while m = -inf
+      const float alpha = fast_exp2(m - mt);   // 0 while m = -inf
       l *= alpha;
 #pragma unroll
       for (int i = 0; i < 16; ++i) acc[i] *= alpha;
@@ -1480,14 +1484,14 @@ __global__ __launch_bounds__(kF32Threads) void attn_fwd_f32_kernel(const AttnF32
     }
 #pragma unroll
     for (int j = 0; j < kTile; ++j) {
-      const float p = exp2f(s[j] - m);
+      const float p = fast_exp2(s[j] - m);
       l += p;
       axpy16(p, sV[j], acc);
     }
   }
   if (!valid) return;
   store16(a.o + ((size_t)oi * H + head) * kHd, acc, l > 0.f ? 1.f / l : 0.f);
-  a.lse_out[(size_t)head * a.total_q + oi] = l > 0.f ? (m + log2f(l)) * kLn2 : -INFINITY;
+  a.lse_out[(size_t)head * a.total_q + oi] = l > 0.f ? (m + fast_log2(l)) * kLn2 : -INFINITY;
 }
 
 // dQ = scale * sum_j P_ij (dP_ij - D_i) k_j, P recomputed from the saved LSE.
@@ -1519,7 +1523,7 @@ __global__ __launch_bounds__(kF32Threads) void attn_dq_f32_kernel(const AttnF32A
     for (int j = 0; j < kTile; ++j) {
       const int2 pn = MASKED ? sN[j] : make_int2(0, 0);
       if (!admissible_f32<MASKED>(k0 + j, phi, oi, pn, own)) continue;
-      const float p = exp2f(a.c * dot16(q, sK[j]) - rs.x);
+      const float p = fast_exp2(a.c * dot16(q, sK[j]) - rs.x);
       const float ds = p * (dot16(g, sV[j]) - rs.y);
       axpy16(ds, sK[j], acc);
     }
@@ -1563,7 +1567,7 @@ __global__ __launch_bounds__(kF32Threads) void attn_dkdv_f32_kernel(const AttnF3
       const int2 pn = MASKED ? sN[i] : make_int2(0, 0);
       if (!admissible_f32<MASKED>(q0 + i, phi, oi, pn, own)) continue;
       const float2 rs = sR[i];
-      const float p = exp2f(a.c * dot16(kx, sQ[i]) - rs.x);
+      const float p = fast_exp2(a.c * dot16(kx, sQ[i]) - rs.x);
       axpy16(p, sG[i], dv);
       const float ds = p * (dot16(vx, sG[i]) - rs.y);
       axpy16(ds, sQ[i], dk);
