@@ -289,101 +289,26 @@ __global__ void edge_gather_add_scalar_kernel(const T* __restrict__ a, long lda,
 
 // ------------------------------------------------------------------ CSR
 
-__global__ void zero_int_kernel(int* __restrict__ p, long n) {
-  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) p[i] = 0;
-}
-
-__global__ void count_keys_kernel(const int* __restrict__ keys, long num_edges, int num_nodes,
-                                  int* __restrict__ counts) {
-  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < num_edges; i += (long)gridDim.x * blockDim.x) {
-    const int k = keys[i];
-    if ((unsigned)k < (unsigned)num_nodes) atomicAdd(&counts[k], 1);
-  }
-}
-
-constexpr int kScanBlock = 1024;
-constexpr int kScanItems = 4;  // per thread
-constexpr int kScanTile = kScanBlock * kScanItems;
-
-// Block-wide exclusive scan of one value per thread (Hillis-Steele in LDS).
-DEVI int block_exclusive_scan(int v, int* sh, int& total) {
-  const int tid = threadIdx.x;
-  sh[tid] = v;
-  __syncthreads();
-  for (int off = 1; off < kScanBlock; off <<= 1) {
-    const int add = tid >= off ? sh[tid - off] : 0;
-    __syncthreads();
-    sh[tid] += add;
-    __syncthreads();
-  }
-  total = sh[kScanBlock - 1];
-  const int incl = sh[tid];
-  __syncthreads();
-  return incl - v;
-}
-
-// Pass 1: per-tile sums of counts[0..n).
-__global__ __launch_bounds__(kScanBlock) void scan_reduce_kernel(const int* __restrict__ in, int n,
-                                                                 int* __restrict__ tile_sums) {
-  __shared__ int sh[kScanBlock];
-  const int base = blockIdx.x * kScanTile + threadIdx.x * kScanItems;
-  int s = 0;
-#pragma unroll
-  for (int j = 0; j < kScanItems; ++j) s += base + j < n ? in[base + j] : 0;
-  int total;
-  block_exclusive_scan(s, sh, total);
-  if (threadIdx.x == 0) tile_sums[blockIdx.x] = total;
-}
-
-// Pass 2: exclusive scan of the tile sums in one block (loops over chunks).
-__global__ __launch_bounds__(kScanBlock) void scan_tiles_kernel(int* __restrict__ tile_sums, int ntiles) {
-  __shared__ int sh[kScanBlock];
-  int carry = 0;
-  for (int base = 0; base < ntiles; base += kScanBlock) {
-    const int i = base + threadIdx.x;
-    const int v = i < ntiles ? tile_sums[i] : 0;
-    int total;
-    const int ex = block_exclusive_scan(v, sh, total);
-    if (i < ntiles) tile_sums[i] = carry + ex;
-    carry += total;
-  }
-}
-
-// Pass 3: indptr[i] = exclusive prefix of counts, indptr[n] = total;
-// cursor[i] = indptr[i] (fill cursor).
-__global__ __launch_bounds__(kScanBlock) void scan_apply_kernel(const int* __restrict__ in, int n,
-                                                                const int* __restrict__ tile_offsets,
-                                                                int* __restrict__ indptr,
-                                                                int* __restrict__ cursor) {
-  __shared__ int sh[kScanBlock];
-  const int base = blockIdx.x * kScanTile + threadIdx.x * kScanItems;
-  int v[kScanItems];
-  int s = 0;
-#pragma unroll
-  for (int j = 0; j < kScanItems; ++j) { v[j] = base + j < n ? in[base + j] : 0; s += v[j]; }
-  int total;
-  int run = block_exclusive_scan(s, sh, total) + tile_offsets[blockIdx.x];
-#pragma unroll
-  for (int j = 0; j < kScanItems; ++j) {
-    if (base + j < n) { indptr[base + j] = run; cursor[base + j] = run; }
-    run += v[j];
-  }
-  if (blockIdx.x == gridDim.x - 1 && threadIdx.x == kScanBlock - 1) indptr[n] = run;
-}
-
 // perm by a stable LSD radix sort of (key, edge id) over 8-bit digits, so
 // every edge's position follows from counts alone (no atomic ordering, no
 // per-segment sort): per pass, each block counts the digits of its tile of
-// kSortTile consecutive edges (hist, digit-major: [digit][block]); an
-// exclusive scan of hist in that (digit, block) order gives each (digit,
-// block) its first output slot; the scatter pass then places element i of
-// the tile at that slot + the number of earlier elements of the tile with the
-// same digit.  Earlier means earlier in edge order: the tile is walked in
-// rounds j of kSortThreads consecutive edges (edge base + j * 256 + tid), and
-// inside a round by wave, then lane.  Each pass is therefore stable, and the
+// kSortTile consecutive edges (hist, one row of kRadixBins counts per tile,
+// written and read as whole rows); an exclusive scan of hist in (digit, tile)
+// order gives each (digit, tile) its first output slot; the scatter pass then
+// places element i of the tile at that slot + the number of earlier elements
+// of the tile with the same digit.  Earlier means earlier in edge order: wave
+// w of the block owns the tile's edges [w * 1024, (w + 1) * 1024), walked in
+// rounds j of 64 consecutive edges (lane order inside a round), so (wave,
+// round, lane) order is edge order.  Each pass is therefore stable, and the
 // passes over digits 0, 1, ... leave the edges sorted by key with ties in
 // ascending edge id.  Keys outside [0, num_nodes) sort as num_nodes, after
 // every valid key (past indptr[num_nodes]).
+//
+// Between passes the edges travel as interleaved (key, edge id) pairs: the
+// scatter's output runs (one per digit and tile, 16 elements on average) are
+// then 128 bytes instead of two 64-byte pieces.  Pass 0 reads the caller's keys
+// (the ids are the positions); the last pass writes the sorted keys and perm
+// as two arrays.
 constexpr int kSortThreads = 256;
 constexpr int kSortItems = 16;
 constexpr int kSortTile = kSortThreads * kSortItems;
@@ -391,56 +316,244 @@ constexpr int kRadixBits = 8;
 constexpr int kRadixBins = 1 << kRadixBits;
 static_assert(kRadixBins == kSortThreads, "one digit per thread in the per-digit steps");
 
-DEVI int sort_key(const int* __restrict__ keys, long i, int num_nodes, bool raw) {
-  const int k = keys[i];
-  return !raw || (unsigned)k < (unsigned)num_nodes ? k : num_nodes;
+DEVI int clamp_key(int k, int num_nodes) { return (unsigned)k < (unsigned)num_nodes ? k : num_nodes; }
+
+// Tile of block b.  Hardware block b runs on XCD b % 8; the tiles are dealt so
+// that each XCD takes one contiguous range of them.  A digit's output runs of
+// consecutive tiles are adjacent in the output, so a line shared by two runs
+// is then mostly completed in one XCD's L2 instead of being written in parts
+// from two.
+DEVI int xcd_tile(int b, int ntiles) {
+  const int q = ntiles >> 3, rem = ntiles & 7, x = b & 7, s = b >> 3;
+  return x * q + min(x, rem) + s;
 }
 
-__global__ __launch_bounds__(kSortThreads) void radix_hist_kernel(const int* __restrict__ keys, long n, int num_nodes,
-                                                                 bool raw, int shift, int nblocks,
-                                                                 int* __restrict__ hist) {
+// One row of hist: the digit counts of the tile.  PAIRS: the input is (key, id)
+// pairs; else the caller's keys (clamped).  Digit order inside the tile is
+// irrelevant here, so full tiles read 16-byte vectors.
+template <bool PAIRS>
+__global__ __launch_bounds__(kSortThreads) void radix_hist_kernel(const int* __restrict__ in, long n, int num_nodes,
+                                                                 int shift, bool vec, int* __restrict__ hist) {
   __shared__ int h[kRadixBins];
   const int tid = threadIdx.x;
   h[tid] = 0;
-  __syncthreads();
-  const long base = (long)blockIdx.x * kSortTile;
-#pragma unroll 4
-  for (int j = 0; j < kSortItems; ++j) {
-    const long i = base + (long)j * kSortThreads + tid;
-    if (i < n) atomicAdd(&h[(sort_key(keys, i, num_nodes, raw) >> shift) & (kRadixBins - 1)], 1);
+  const long tile = (long)blockIdx.x * kSortTile;
+  int d[kSortItems];
+  if (vec && tile + kSortTile <= n) {
+    if (PAIRS) {
+      const int4* p = reinterpret_cast<const int4*>(in + 2 * tile);
+#pragma unroll
+      for (int r = 0; r < kSortItems / 2; ++r) {
+        const int4 x = p[r * kSortThreads + tid];
+        d[2 * r] = (x.x >> shift) & (kRadixBins - 1);
+        d[2 * r + 1] = (x.z >> shift) & (kRadixBins - 1);
+      }
+    } else {
+      const int4* p = reinterpret_cast<const int4*>(in + tile);
+#pragma unroll
+      for (int r = 0; r < kSortItems / 4; ++r) {
+        const int4 x = p[r * kSortThreads + tid];
+        d[4 * r] = (clamp_key(x.x, num_nodes) >> shift) & (kRadixBins - 1);
+        d[4 * r + 1] = (clamp_key(x.y, num_nodes) >> shift) & (kRadixBins - 1);
+        d[4 * r + 2] = (clamp_key(x.z, num_nodes) >> shift) & (kRadixBins - 1);
+        d[4 * r + 3] = (clamp_key(x.w, num_nodes) >> shift) & (kRadixBins - 1);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < kSortItems; ++j) {
+      const long i = tile + (long)j * kSortThreads + tid;
+      const int k = i < n ? (PAIRS ? in[2 * i] : clamp_key(in[i], num_nodes)) : -1;
+      d[j] = k >= 0 ? (k >> shift) & (kRadixBins - 1) : -1;
+    }
   }
   __syncthreads();
-  hist[(long)tid * nblocks + blockIdx.x] = h[tid];
+#pragma unroll
+  for (int j = 0; j < kSortItems; ++j)
+    if (d[j] >= 0) atomicAdd(&h[d[j]], 1);
+  __syncthreads();
+  hist[(long)blockIdx.x * kRadixBins + tid] = h[tid];
 }
 
-// offsets: the exclusive scan of hist.  vals_in null: the values are the edge
-// ids.  keys_out null: the last pass (only the values are needed).
-__global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(const int* __restrict__ keys_in,
-                                                                    const int* __restrict__ vals_in, long n,
-                                                                    int num_nodes, bool raw, int shift, int nblocks,
+// The (digit, tile)-order exclusive scan of hist, in place, over its
+// [tile][digit] rows: per chunk of kHistChunk tiles the column sums (part);
+// one block scans part down each digit's column and adds the digit's base
+// (the exclusive scan of the digit totals); per chunk, each digit's column
+// is then walked down its kHistChunk rows.
+constexpr int kHistChunk = 64;
+
+int hist_chunks(int ntiles) { return (ntiles + kHistChunk - 1) / kHistChunk; }
+
+__global__ __launch_bounds__(kRadixBins) void hist_chunk_sum_kernel(const int* __restrict__ hist, int ntiles,
+                                                                   int* __restrict__ part) {
+  const int b0 = blockIdx.x * kHistChunk, tid = threadIdx.x;
+  int x[kHistChunk];
+#pragma unroll
+  for (int r = 0; r < kHistChunk; ++r) x[r] = b0 + r < ntiles ? hist[(long)(b0 + r) * kRadixBins + tid] : 0;
+  int s = 0;
+#pragma unroll
+  for (int r = 0; r < kHistChunk; ++r) s += x[r];
+  part[(long)blockIdx.x * kRadixBins + tid] = s;
+}
+
+__global__ __launch_bounds__(4 * kRadixBins) void hist_chunk_scan_kernel(int* __restrict__ part, int nchunks) {
+  // thread: digit d, quarter q of the chunks
+  __shared__ int qsum[4][kRadixBins];
+  __shared__ int wtot[4][kRadixBins / 64];
+  const int d = threadIdx.x & (kRadixBins - 1), q = threadIdx.x / kRadixBins;
+  const int lane = threadIdx.x & 63, wv = d >> 6;
+  const int per = (nchunks + 3) / 4, c0 = min(nchunks, q * per), c1 = min(nchunks, c0 + per);
+  int s = 0;
+#pragma unroll 8
+  for (int c = c0; c < c1; ++c) s += part[(long)c * kRadixBins + d];
+  qsum[q][d] = s;
+  __syncthreads();
+  int tot = 0, base = 0;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const int x = qsum[w][d];
+    base += w < q ? x : 0;
+    tot += x;
+  }
+  // exclusive scan of the digit totals (each quarter computes the same one)
+  int x = tot;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) wtot[q][wv] = x;
+  __syncthreads();
+#pragma unroll
+  for (int w = 0; w < kRadixBins / 64; ++w) base += w < wv ? wtot[q][w] : 0;
+  base += x - tot;
+  for (int c = c0; c < c1; ++c) {
+    const int y = part[(long)c * kRadixBins + d];
+    part[(long)c * kRadixBins + d] = base;
+    base += y;
+  }
+}
+
+__global__ __launch_bounds__(kRadixBins) void hist_chunk_apply_kernel(int* __restrict__ hist, int ntiles,
+                                                                     const int* __restrict__ part) {
+  const int b0 = blockIdx.x * kHistChunk, tid = threadIdx.x;
+  int x[kHistChunk];
+#pragma unroll
+  for (int r = 0; r < kHistChunk; ++r) x[r] = b0 + r < ntiles ? hist[(long)(b0 + r) * kRadixBins + tid] : 0;
+  int run = part[(long)blockIdx.x * kRadixBins + tid];
+#pragma unroll
+  for (int r = 0; r < kHistChunk; ++r) {
+    if (b0 + r < ntiles) hist[(long)(b0 + r) * kRadixBins + tid] = run;
+    run += x[r];
+  }
+}
+
+// Exclusive scan of one value per thread over a 256-thread block (sh: 4 ints).
+DEVI int block_exclusive_scan256(int v, int* sh) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) sh[wave] = x;
+  __syncthreads();
+  int before = 0;
+#pragma unroll
+  for (int w = 0; w < kSortThreads / 64; ++w) before += w < wave ? sh[w] : 0;
+  __syncthreads();
+  return before + x - v;
+}
+
+// offsets: the exclusive scan of hist in (digit, tile) order, in hist's
+// [tile][digit] rows: offsets[t * kRadixBins + d] is the first output slot of
+// tile t's digit-d elements.  IN_PAIRS: the input is (key, id) pairs, else the
+// caller's keys (clamped) with the positions as ids.  OUT_PAIRS: the output is
+// pairs, else keys_out and vals_out.  Each wave ranks its 1024 edges on its
+// own (a running count per digit in its own LDS row, peers of a round found
+// by ballots over the digit bits); the block then turns the per-wave counts
+// into the tile-local start of each digit and each wave's first slot in it,
+// places the tile into LDS in (digit, edge) order and writes it out in that
+// order, so consecutive threads write consecutive slots of one digit's run
+// instead of one slot per digit.  vec: the input may be read as 16-byte
+// vectors (full waves read theirs through their LDS slice).
+template <bool IN_PAIRS, bool OUT_PAIRS>
+__global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(const int* __restrict__ in, long n,
+                                                                    int num_nodes, int shift, bool vec,
                                                                     const int* __restrict__ offsets,
-                                                                    int* __restrict__ keys_out,
+                                                                    int* __restrict__ out,
                                                                     int* __restrict__ vals_out) {
   constexpr int kWaves = kSortThreads / 64;
-  __shared__ int run[kRadixBins];           // next slot of each digit
-  __shared__ int wcnt[kWaves][kRadixBins];  // this round's count of each digit per wave
+  constexpr int kWaveItems = kSortItems * 64;
+  __shared__ int gbase[kRadixBins];         // output slot of the tile's local slot 0, per digit
+  __shared__ int wrun[kWaves][kRadixBins];  // per wave: running count, then first tile-local slot, per digit
+  __shared__ int2 skv[kSortTile];           // the wave's inputs in edge order, then the tile in output order
+  __shared__ int sh[kWaves];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  run[tid] = offsets[(long)tid * nblocks + blockIdx.x];
+  const int t_idx = xcd_tile(blockIdx.x, gridDim.x);
+  const long tile = (long)t_idx * kSortTile;
+  const long wbase = tile + (long)wave * kWaveItems;
+  int2* stage = skv + wave * kWaveItems;
+  int k[kSortItems], v[kSortItems];
+  if (wbase + kWaveItems <= n && (IN_PAIRS || vec)) {
+    // 16-byte loads of the wave's edges into its own LDS slice in edge order, read back lane-strided
+    if (IN_PAIRS) {
+      const int4* p = reinterpret_cast<const int4*>(in + 2 * wbase);
+      int4 x[kSortItems / 2];
 #pragma unroll
-  for (int w = 0; w < kWaves; ++w) wcnt[w][tid] = 0;
-  __syncthreads();
-  const long base = (long)blockIdx.x * kSortTile;
-  const uint64_t below_mask = (1ull << lane) - 1;
-  for (int j = 0; j < kSortItems; ++j) {
-    const long i = base + (long)j * kSortThreads + tid;
-    const bool valid = i < n;
-    int k = 0, v = 0, d = 0;
-    if (valid) {
-      k = sort_key(keys_in, i, num_nodes, raw);
-      v = vals_in ? vals_in[i] : (int)i;
-      d = (k >> shift) & (kRadixBins - 1);
+      for (int r = 0; r < kSortItems / 2; ++r) x[r] = p[r * 64 + lane];
+#pragma unroll
+      for (int r = 0; r < kSortItems / 2; ++r) reinterpret_cast<int4*>(stage)[r * 64 + lane] = x[r];
+    } else {
+      const int4* p = reinterpret_cast<const int4*>(in + wbase);
+      int4 x[kSortItems / 4];
+#pragma unroll
+      for (int r = 0; r < kSortItems / 4; ++r) x[r] = p[r * 64 + lane];
+#pragma unroll
+      for (int r = 0; r < kSortItems / 4; ++r) {
+        const int e = 4 * (r * 64 + lane);
+        reinterpret_cast<int4*>(stage)[(r * 64 + lane) * 2] =
+            int4{clamp_key(x[r].x, num_nodes), (int)(wbase + e), clamp_key(x[r].y, num_nodes), (int)(wbase + e + 1)};
+        reinterpret_cast<int4*>(stage)[(r * 64 + lane) * 2 + 1] =
+            int4{clamp_key(x[r].z, num_nodes), (int)(wbase + e + 2), clamp_key(x[r].w, num_nodes), (int)(wbase + e + 3)};
+      }
     }
-    // lanes of this wave holding the same digit
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int j = 0; j < kSortItems; ++j) {
+      const int2 x = stage[j * 64 + lane];
+      k[j] = x.x;
+      v[j] = x.y;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < kSortItems; ++j) {
+      const long i = wbase + (long)j * 64 + lane;
+      if (IN_PAIRS) {
+        const int2 x = i < n ? reinterpret_cast<const int2*>(in)[i] : int2{-1, 0};
+        k[j] = x.x;
+        v[j] = x.y;
+      } else {
+        k[j] = i < n ? clamp_key(in[i], num_nodes) : -1;
+        v[j] = (int)i;
+      }
+    }
+  }
+  const int g0 = offsets[(long)t_idx * kRadixBins + tid];
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) wrun[w][tid] = 0;
+  __syncthreads();
+  // rank inside the wave: slot among the wave's earlier edges of the same digit
+  const uint64_t below_mask = (1ull << lane) - 1;
+  int* run = wrun[wave];
+  int r[kSortItems];
+#pragma unroll
+  for (int j = 0; j < kSortItems; ++j) {
+    const bool valid = k[j] >= 0;
+    const int d = valid ? (k[j] >> shift) & (kRadixBins - 1) : 0;
     uint64_t peers = __ballot(valid);
 #pragma unroll
     for (int b = 0; b < kRadixBits; ++b) {
@@ -449,21 +562,96 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(const int* 
       peers &= bit ? m : ~m;
     }
     const int below = __popcll(peers & below_mask);
-    if (valid && below == 0) wcnt[wave][d] = __popcll(peers);
-    __syncthreads();
-    if (valid) {
-      int pos = run[d] + below;
+    const int before = valid ? run[d] : 0;
+    __builtin_amdgcn_wave_barrier();
+    if (valid && below == 0) run[d] = before + __popcll(peers);
+    __builtin_amdgcn_wave_barrier();
+    r[j] = before + below;
+  }
+  __syncthreads();
+  // digit tid: tile-local start, and each wave's first slot in it
+  {
+    int c[kWaves], tot = 0;
 #pragma unroll
-      for (int w = 0; w < kWaves; ++w) pos += w < wave ? wcnt[w][d] : 0;
-      if (keys_out) keys_out[pos] = k;
-      vals_out[pos] = v;
+    for (int w = 0; w < kWaves; ++w) { c[w] = wrun[w][tid]; tot += c[w]; }
+    int acc = block_exclusive_scan256(tot, sh);
+    gbase[tid] = g0 - acc;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) { wrun[w][tid] = acc; acc += c[w]; }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < kSortItems; ++j)
+    if (k[j] >= 0) skv[run[(k[j] >> shift) & (kRadixBins - 1)] + r[j]] = int2{k[j], v[j]};
+  __syncthreads();
+  const int m = (int)min((long)kSortTile, n - tile);
+  for (int t = tid; t < m; t += kSortThreads) {
+    const int2 x = skv[t];
+    const int g = gbase[(x.x >> shift) & (kRadixBins - 1)] + t;
+    if (OUT_PAIRS) {
+      reinterpret_cast<int2*>(out)[g] = x;
+    } else {
+      out[g] = x.x;
+      vals_out[g] = x.y;
     }
-    __syncthreads();
-    int add = 0;
+  }
+}
+
+// indptr from the sorted keys s (values in [0, num_nodes], num_nodes standing
+// for the invalid keys): indptr[j] = the number of keys below j.  Boundary i
+// in [0, n] lies between prev = s[i - 1] (-1 at i = 0) and cur = s[i]
+// (num_nodes at i = n); every j in (prev, cur] gets i.  Each j has exactly one
+// such boundary, so there are no write conflicts and no atomics.  A boundary
+// fills at most kGapFill entries itself; longer gaps (runs of absent keys) get
+// only indptr[cur] and leave the rest at -1 for indptr_gap_kernel.  Thread t
+// owns boundaries [4t, 4t + 4).
+constexpr int kGapFill = 64;
+
+__global__ void fill_int_kernel(int* __restrict__ p, long n, int value) {
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) p[i] = value;
+}
+
+__global__ __launch_bounds__(256) void indptr_runs_kernel(const int* __restrict__ s, long n, int num_nodes,
+                                                         int* __restrict__ indptr) {
+  const long t = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long i0 = 4 * t;
+  if (i0 > n) return;
+  int cur[4];
+  if (i0 + 4 <= n) {
+    const int4 x = reinterpret_cast<const int4*>(s)[t];
+    cur[0] = x.x; cur[1] = x.y; cur[2] = x.z; cur[3] = x.w;
+  } else {
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) { add += wcnt[w][tid]; wcnt[w][tid] = 0; }
-    run[tid] += add;
-    __syncthreads();
+    for (int q = 0; q < 4; ++q) cur[q] = i0 + q < n ? s[i0 + q] : num_nodes;
+  }
+  int prev = i0 == 0 ? -1 : s[i0 - 1];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const long i = i0 + q;
+    if (i > n) break;
+    const int c = cur[q];
+    if (c > prev) {
+      if (c - prev <= kGapFill) {
+        for (int j = prev + 1; j <= c; ++j) indptr[j] = (int)i;
+      } else {
+        indptr[c] = (int)i;
+      }
+    }
+    prev = c;
+  }
+}
+
+// Entries left at -1 (inside a gap longer than kGapFill): the first position
+// whose key is >= j, by binary search.
+__global__ void indptr_gap_kernel(const int* __restrict__ s, long n, int num_nodes, int* __restrict__ indptr) {
+  for (long j = (long)blockIdx.x * blockDim.x + threadIdx.x; j <= num_nodes; j += (long)gridDim.x * blockDim.x) {
+    if (indptr[j] >= 0) continue;
+    long lo = 0, hi = n;
+    while (lo < hi) {
+      const long mid = (lo + hi) >> 1;
+      if (s[mid] < (int)j) lo = mid + 1; else hi = mid;
+    }
+    indptr[j] = (int)lo;
   }
 }
 
@@ -814,14 +1002,6 @@ bool misaligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u)
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
-// Exclusive scan of in[0, n) into out[0, n] (out[n] = the total); in may be out.
-void scan_exclusive(const int* in, int n, int* out, int* tiles, hipStream_t st) {
-  const int ntiles = (n + kScanTile - 1) / kScanTile;
-  hipLaunchKernelGGL(scan_reduce_kernel, dim3(ntiles), dim3(kScanBlock), 0, st, in, n, tiles);
-  hipLaunchKernelGGL(scan_tiles_kernel, dim3(1), dim3(kScanBlock), 0, st, tiles, ntiles);
-  hipLaunchKernelGGL(scan_apply_kernel, dim3(ntiles), dim3(kScanBlock), 0, st, in, n, tiles, out, out);
-}
-
 int radix_blocks(int64_t num_edges) { return (int)((num_edges + kSortTile - 1) / kSortTile); }
 
 // Passes of kRadixBits over the keys 0 .. num_nodes (num_nodes: the slot of invalid keys).
@@ -830,19 +1010,20 @@ int radix_passes(int num_nodes) {
   return (bits + kRadixBits - 1) / kRadixBits;
 }
 
-struct CsrWs { size_t counts, tiles, hist, keys_a, keys_b, vals, total; };
+// Workspace: hist and its chunk sums, and two buffers of E (key, id) pairs
+// (pass p writes pair buffer p & 1; the last pass writes the sorted keys into
+// the buffer it does not read).
+struct CsrWs { size_t hist, part, pairs_a, pairs_b, total; };
 CsrWs csr_ws(int64_t num_edges, int num_nodes) {
+  (void)num_nodes;
   CsrWs w;
   const long nhist = (long)kRadixBins * radix_blocks(num_edges);
-  const long scan_n = std::max((long)num_nodes, nhist);
-  const long ntiles = (scan_n + kScanTile - 1) / kScanTile;
+  const long npart = (long)kRadixBins * hist_chunks(radix_blocks(num_edges));
   size_t off = 0;
-  w.counts = off; off += align256((size_t)num_nodes * 4);
-  w.tiles = off; off += align256((size_t)(ntiles > 0 ? ntiles : 1) * 4);
-  w.hist = off; off += align256((size_t)(nhist + 1) * 4);
-  w.keys_a = off; off += align256((size_t)num_edges * 4);
-  w.keys_b = off; off += align256((size_t)num_edges * 4);
-  w.vals = off; off += align256((size_t)num_edges * 4);
+  w.hist = off; off += align256((size_t)(nhist > 0 ? nhist : 1) * 4);
+  w.part = off; off += align256((size_t)(npart > 0 ? npart : 1) * 4);
+  w.pairs_a = off; off += align256((size_t)num_edges * 8);
+  w.pairs_b = off; off += align256((size_t)num_edges * 8);
   w.total = off;
   return w;
 }
@@ -1055,43 +1236,45 @@ int esa_csr_build(const int* keys, int64_t num_edges, int num_nodes, int* indptr
   if (workspace_bytes < w.total) return ESA_ERR_WORKSPACE;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
-  int* counts = reinterpret_cast<int*>(ws + w.counts);
-  int* tiles = reinterpret_cast<int*>(ws + w.tiles);
-  if (num_nodes == 0) {
-    hipLaunchKernelGGL(zero_int_kernel, dim3(1), dim3(64), 0, st, indptr, 1L);
-    ESA_LAUNCH_CHECK();
-    return ESA_OK;
-  }
   ESA_TIMED(esa_profile::kCsrBuild, st, {
-    // indptr: key counts (order-independent) and their exclusive scan
-    hipLaunchKernelGGL(zero_int_kernel, dim3(grid_for(num_nodes, 256, 4096)), dim3(256), 0, st, counts,
-                       (long)num_nodes);
-    if (num_edges > 0)
-      hipLaunchKernelGGL(count_keys_kernel, dim3(grid_for(num_edges, 256, 8192)), dim3(256), 0, st, keys,
-                         (long)num_edges, num_nodes, counts);
-    scan_exclusive(counts, num_nodes, indptr, tiles, st);
-    // perm: stable radix sort of the edge ids by key
+    const int* sorted = nullptr;
     if (num_edges > 0) {
-      const int nblocks = radix_blocks(num_edges), passes = radix_passes(num_nodes);
+      // perm: stable radix sort of the edge ids by key
+      const int ntiles = radix_blocks(num_edges), passes = radix_passes(num_nodes);
+      const int nchunks = hist_chunks(ntiles);
       int* hist = reinterpret_cast<int*>(ws + w.hist);
-      int* kbuf[2] = {reinterpret_cast<int*>(ws + w.keys_a), reinterpret_cast<int*>(ws + w.keys_b)};
-      int* vtmp = reinterpret_cast<int*>(ws + w.vals);
-      const int* kin = keys;
-      const int* vin = nullptr;
+      int* part = reinterpret_cast<int*>(ws + w.part);
+      int* pairs[2] = {reinterpret_cast<int*>(ws + w.pairs_a), reinterpret_cast<int*>(ws + w.pairs_b)};
+      int* skeys = pairs[(passes - 1) & 1];
+      const bool vec_keys = !misaligned16(keys);
       for (int p = 0; p < passes; ++p) {
-        const bool raw = p == 0, last = p == passes - 1;
-        // values ping-pong so that the last pass writes perm
-        int* vout = ((passes - 1 - p) & 1) ? vtmp : perm;
-        int* kout = last ? nullptr : kbuf[p & 1];
-        hipLaunchKernelGGL(radix_hist_kernel, dim3(nblocks), dim3(kSortThreads), 0, st, kin, (long)num_edges,
-                           num_nodes, raw, p * kRadixBits, nblocks, hist);
-        scan_exclusive(hist, kRadixBins * nblocks, hist, tiles, st);
-        hipLaunchKernelGGL(radix_scatter_kernel, dim3(nblocks), dim3(kSortThreads), 0, st, kin, vin,
-                           (long)num_edges, num_nodes, raw, p * kRadixBits, nblocks, hist, kout, vout);
-        kin = kout;
-        vin = vout;
+        const int shift = p * kRadixBits;
+        const bool first = p == 0, last = p == passes - 1;
+        const int* in = first ? keys : pairs[(p - 1) & 1];
+        int* out = last ? skeys : pairs[p & 1];
+        if (first)
+          hipLaunchKernelGGL(radix_hist_kernel<false>, dim3(ntiles), dim3(kSortThreads), 0, st, in,
+                             (long)num_edges, num_nodes, shift, vec_keys, hist);
+        else
+          hipLaunchKernelGGL(radix_hist_kernel<true>, dim3(ntiles), dim3(kSortThreads), 0, st, in,
+                             (long)num_edges, num_nodes, shift, true, hist);
+        hipLaunchKernelGGL(hist_chunk_sum_kernel, dim3(nchunks), dim3(kRadixBins), 0, st, hist, ntiles, part);
+        hipLaunchKernelGGL(hist_chunk_scan_kernel, dim3(1), dim3(4 * kRadixBins), 0, st, part, nchunks);
+        hipLaunchKernelGGL(hist_chunk_apply_kernel, dim3(nchunks), dim3(kRadixBins), 0, st, hist, ntiles, part);
+        auto scatter = first ? (last ? radix_scatter_kernel<false, false> : radix_scatter_kernel<false, true>)
+                             : (last ? radix_scatter_kernel<true, false> : radix_scatter_kernel<true, true>);
+        hipLaunchKernelGGL(scatter, dim3(ntiles), dim3(kSortThreads), 0, st, in, (long)num_edges, num_nodes,
+                           shift, !first || vec_keys, hist, out, perm);
       }
+      sorted = skeys;
     }
+    // indptr: the boundaries of the sorted keys' runs
+    hipLaunchKernelGGL(fill_int_kernel, dim3(grid_for((long)num_nodes + 1, 256, 4096)), dim3(256), 0, st, indptr,
+                       (long)num_nodes + 1, -1);
+    hipLaunchKernelGGL(indptr_runs_kernel, dim3(grid_for(num_edges / 4 + 1, 256)), dim3(256), 0, st, sorted,
+                       (long)num_edges, num_nodes, indptr);
+    hipLaunchKernelGGL(indptr_gap_kernel, dim3(grid_for((long)num_nodes + 1, 256, 4096)), dim3(256), 0, st,
+                       sorted, (long)num_edges, num_nodes, indptr);
   });
   ESA_LAUNCH_CHECK();
   return ESA_OK;

@@ -311,6 +311,35 @@ def test_csr_build_drops_out_of_range_keys(device):
     assert np.array_equal(csr.perm.cpu().numpy()[: got_ip[-1]], ids[sub])
 
 
+def test_csr_build_invalid_keys_follow_in_edge_order(device):
+    """Past indptr[N], perm lists the edges whose key is outside [0, N), in ascending edge id; with N = 0
+    every key is invalid and perm is the identity."""
+    rng = np.random.default_rng(5)
+    for n in (300, 0):
+        keys = rng.integers(-20, n + 20, size=9_001).astype(np.int32)
+        csr = edges.CSR.build(torch.as_tensor(keys).to(device), n)
+        bad = np.nonzero((keys < 0) | (keys >= n))[0]
+        ip = csr.indptr.cpu().numpy()
+        assert ip[-1] == keys.size - bad.size
+        assert np.array_equal(csr.perm.cpu().numpy()[ip[-1]:], bad)
+
+
+def test_csr_build_misaligned_keys_and_long_gaps(device):
+    """Keys read through a view that starts 4 bytes past a 16-byte boundary (the element-wise load path),
+    a partial last tile, and runs of thousands of absent keys (indptr entries inside such a run are found by
+    search rather than by the run boundary)."""
+    rng = np.random.default_rng(41)
+    n = 3_000_000
+    present = np.sort(rng.choice(n - 10, size=700, replace=False)) + 5
+    keys = rng.choice(present, size=1 + 3 * 4096 + 20_011).astype(np.int32)
+    dev = torch.as_tensor(keys).to(device)[1:]
+    assert dev.data_ptr() % 16 != 0
+    csr = edges.CSR.build(dev, n)
+    indptr, perm = OE.csr_build(keys[1:], n)
+    assert np.array_equal(csr.indptr.cpu().numpy(), indptr)
+    assert np.array_equal(csr.perm.cpu().numpy(), perm)
+
+
 def test_csr_build_keys_beyond_2_24(device):
     """num_nodes > 2^24 takes four 8-bit digit passes."""
     rng = np.random.default_rng(24)
