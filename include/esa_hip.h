@@ -47,6 +47,7 @@ extern "C" {
 #define ESA_MASK_EDGE 1
 #define ESA_MASK_NODE 2
 #define ESA_MASK_EDGE_PLAN 3
+#define ESA_MASK_NODE_PLAN 4
 
 /* Library version and build target, e.g. "esa_hip 0.1 gfx950". */
 ESA_API const char* esa_version(void);
@@ -85,6 +86,11 @@ ESA_API const char* esa_version(void);
 /* counts once (a repeated edge); entries outside the query's segment are    */
 /* ignored.  Work is O(n_mask_edges * heads * 16).                           */
 /*                                                                           */
+/* mask_kind ESA_MASK_NODE_PLAN: the same mask with mask_b = a node plan     */
+/* built once by esa_node_plan_build from (mask_a, indices): its first       */
+/* n_mask_edges ints are a copy of the indices, followed by the transposed   */
+/* CSR the backward reads, so the backward does not rebuild it per call.     */
+/*                                                                           */
 /* A query with no admissible key gets output 0 and lse = -inf.              */
 /*                                                                           */
 /* softmax_lse is [heads, total_q] fp32 (natural log), as flash-attn's.      */
@@ -108,6 +114,21 @@ ESA_API int esa_edge_plan_build(const int* tok_src, const int* tok_dst,
                         const int* cu_seqlens_q, const int* cu_seqlens_k,
                         int batch, int total_q, int total_k,
                         void* plan, size_t plan_bytes, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Node-mode plan: the per-batch data of the ESA_MASK_NODE mask, i.e. a copy */
+/* of the CSR's indices and the transposed CSR (per key token, the query     */
+/* rows that list it, in ascending position) that the backward's dK / dV    */
+/* pass gathers over.  Built once per batch and read by every attention     */
+/* call over the same adjacency, as the reference builds its [B, 1, N, N]    */
+/* node bias once per batch (get_adj_mask_from_edge_index_node,             */
+/* esa/masked_layers.py:79-118) for all its layers (:849-936).  The plan's   */
+/* tail is the build's scratch.  It stays valid while indptr / indices are   */
+/* unchanged; calls pass the same indptr as mask_a.                          */
+/* ------------------------------------------------------------------------ */
+ESA_API int esa_node_plan_size(int total_q, int total_k, int n_mask_edges, size_t* bytes);
+ESA_API int esa_node_plan_build(const int* indptr, const int* indices, int total_q, int total_k,
+                        int n_mask_edges, void* plan, size_t plan_bytes, void* stream);
 
 ESA_API int esa_varlen_attn_workspace_size(int total_q, int total_k, int heads,
                                    int head_dim, int dtype, int mask_kind,

@@ -24,6 +24,7 @@ ESA_MASK_NONE = 0
 ESA_MASK_EDGE = 1
 ESA_MASK_NODE = 2
 ESA_MASK_EDGE_PLAN = 3
+ESA_MASK_NODE_PLAN = 4
 
 ERRORS = {
     -1: "ESA_ERR_NULL (a required pointer is null)",
@@ -70,6 +71,8 @@ _PROTOS = {
     "esa_token_budget_pack_workspace_size": (_c_int, [_c_int, ctypes.POINTER(_c_sz)]),
     "esa_edge_plan_size": (_c_int, [_c_int, _c_int, _c_int, ctypes.POINTER(_c_sz)]),
     "esa_edge_plan_build": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _c_sz, _vp]),
+    "esa_node_plan_size": (_c_int, [_c_int, _c_int, _c_int, ctypes.POINTER(_c_sz)]),
+    "esa_node_plan_build": (_c_int, [_vp, _vp, _c_int, _c_int, _c_int, _vp, _c_sz, _vp]),
     # counts num_graphs budget | batch_of_graph batch_start num_batches ws bytes stream
     "esa_token_budget_pack": (_c_int, [_vp, _c_int, _c_i64, _vp, _vp, _vp, _vp, _c_sz, _vp]),
     "esa_edge_gather_bwd": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _vp]),

@@ -1860,7 +1860,7 @@ int check_common(int batch, int total_q, int total_k, int heads, int head_dim, i
   const long lim = (1L << 31) - 1;
   if ((long)round32(total_q) * heads * 32 > lim || (long)round32(total_k) * heads * 32 > lim) return ESA_ERR_SHAPE;
   if (mask_kind != ESA_MASK_NONE && mask_kind != ESA_MASK_EDGE && mask_kind != ESA_MASK_NODE &&
-      mask_kind != ESA_MASK_EDGE_PLAN)
+      mask_kind != ESA_MASK_EDGE_PLAN && mask_kind != ESA_MASK_NODE_PLAN)
     return ESA_ERR_MASK;
   if ((mask_kind == ESA_MASK_EDGE || mask_kind == ESA_MASK_EDGE_PLAN) && total_q != total_k) return ESA_ERR_MASK;
   return ESA_OK;
@@ -2014,9 +2014,10 @@ int esa_varlen_attn_workspace_size(int total_q, int total_k, int heads, int head
   if (!bytes) return ESA_ERR_NULL;
   const int rc = check_common(1, total_q, total_k, heads, head_dim, dtype, mask_kind);
   if (rc) return rc;
-  if (mask_kind == ESA_MASK_NODE) {
+  if (mask_kind == ESA_MASK_NODE || mask_kind == ESA_MASK_NODE_PLAN) {
     if (n_mask_edges < 0) return ESA_ERR_SHAPE;
-    return graph_attn_workspace_size(total_q, total_k, heads, n_mask_edges, backward != 0, bytes);
+    return graph_attn_workspace_size(total_q, total_k, heads, n_mask_edges, backward != 0,
+                                     mask_kind == ESA_MASK_NODE_PLAN, bytes);
   }
   if (mask_kind == ESA_MASK_NONE && dtype == ESA_BF16) {
     *bytes = dense_attn_workspace_size(total_q, total_k, heads, backward != 0);
@@ -2046,6 +2047,21 @@ int esa_edge_plan_build(const int* tok_src, const int* tok_dst, const int* cu_se
                          reinterpret_cast<hipStream_t>(stream));
 }
 
+int esa_node_plan_size(int total_q, int total_k, int n_mask_edges, size_t* bytes) {
+  if (!bytes) return ESA_ERR_NULL;
+  if (total_q < 0 || total_k < 0 || n_mask_edges < 0) return ESA_ERR_SHAPE;
+  return graph_node_plan_size(total_q, total_k, n_mask_edges, bytes);
+}
+
+int esa_node_plan_build(const int* indptr, const int* indices, int total_q, int total_k, int n_mask_edges,
+                        void* plan, size_t plan_bytes, void* stream) {
+  if (!indptr || !plan || (n_mask_edges > 0 && !indices)) return ESA_ERR_NULL;
+  if (total_q < 0 || total_k < 0 || n_mask_edges < 0) return ESA_ERR_SHAPE;
+  if (misaligned(plan)) return ESA_ERR_ALIGN;
+  return graph_node_plan_build(indptr, indices, total_q, total_k, n_mask_edges, plan, plan_bytes,
+                               reinterpret_cast<hipStream_t>(stream));
+}
+
 int esa_varlen_attn_fwd(const void* q, const void* k, const void* v, const int* cu_seqlens_q,
                         const int* cu_seqlens_k, int batch, int total_q, int total_k,
                         int max_seqlen_q, int max_seqlen_k, int heads, int head_dim, int dtype,
@@ -2055,9 +2071,10 @@ int esa_varlen_attn_fwd(const void* q, const void* k, const void* v, const int* 
   (void)max_seqlen_q; (void)max_seqlen_k;
   int rc = check_common(batch, total_q, total_k, heads, head_dim, dtype, mask_kind);
   if (rc) return rc;
-  if (mask_kind == ESA_MASK_NODE) {
+  if (mask_kind == ESA_MASK_NODE || mask_kind == ESA_MASK_NODE_PLAN) {
     if (n_mask_edges < 0) return ESA_ERR_SHAPE;
-    if (!mask_a || (n_mask_edges > 0 && !mask_b)) return ESA_ERR_NULL;
+    if (!mask_a || ((n_mask_edges > 0 || mask_kind == ESA_MASK_NODE_PLAN) && !mask_b)) return ESA_ERR_NULL;
+    if (mask_kind == ESA_MASK_NODE_PLAN && misaligned(mask_b)) return ESA_ERR_ALIGN;
     if (total_q == 0) return ESA_OK;
     if (!q || !k || !v || !cu_seqlens_q || !cu_seqlens_k || !out || !softmax_lse) return ESA_ERR_NULL;
     if (misaligned(q) || misaligned(k) || misaligned(v) || misaligned(out)) return ESA_ERR_ALIGN;
@@ -2177,9 +2194,11 @@ int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k, const vo
   (void)max_seqlen_q; (void)max_seqlen_k;
   int rc = check_common(batch, total_q, total_k, heads, head_dim, dtype, mask_kind);
   if (rc) return rc;
-  if (mask_kind == ESA_MASK_NODE) {
+  if (mask_kind == ESA_MASK_NODE || mask_kind == ESA_MASK_NODE_PLAN) {
+    const bool planned = mask_kind == ESA_MASK_NODE_PLAN;
     if (n_mask_edges < 0) return ESA_ERR_SHAPE;
-    if (!mask_a || (n_mask_edges > 0 && !mask_b)) return ESA_ERR_NULL;
+    if (!mask_a || ((n_mask_edges > 0 || planned) && !mask_b)) return ESA_ERR_NULL;
+    if (planned && misaligned(mask_b)) return ESA_ERR_ALIGN;
     if (total_q == 0 && total_k == 0) return ESA_OK;
     if (!dout || !q || !k || !v || !out || !softmax_lse || !cu_seqlens_q || !cu_seqlens_k || !dq || !dk || !dv ||
         !workspace)
@@ -2195,7 +2214,8 @@ int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k, const vo
     g.c = softmax_scale * kLog2e; g.scale = softmax_scale;
     g.out_in = out; g.dout = dout; g.lse_in = softmax_lse;
     g.dq = dq; g.dk = dk; g.dv = dv;
-    return graph_attn_bwd(g, dtype, workspace, workspace_bytes, reinterpret_cast<hipStream_t>(stream));
+    return graph_attn_bwd(g, dtype, planned ? mask_b : nullptr, workspace, workspace_bytes,
+                          reinterpret_cast<hipStream_t>(stream));
   }
   const bool masked = mask_kind == ESA_MASK_EDGE || mask_kind == ESA_MASK_EDGE_PLAN;
   if (mask_kind == ESA_MASK_EDGE && (!mask_a || !mask_b)) return ESA_ERR_NULL;

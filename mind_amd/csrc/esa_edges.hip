@@ -331,12 +331,17 @@ DEVI int xcd_tile(int b, int ntiles) {
 // One row of hist: the digit counts of the tile.  PAIRS: the input is (key, id)
 // pairs; else the caller's keys (clamped).  Digit order inside the tile is
 // irrelevant here, so full tiles read 16-byte vectors.
+// fill / fill_n: also set fill[0, fill_n) to -1 (indptr before its run pass),
+// so that no launch of its own is spent on it.
 template <bool PAIRS>
 __global__ __launch_bounds__(kSortThreads) void radix_hist_kernel(const int* __restrict__ in, long n, int num_nodes,
-                                                                 int shift, bool vec, int* __restrict__ hist) {
+                                                                 int shift, bool vec, int* __restrict__ hist,
+                                                                 int* __restrict__ fill, long fill_n) {
   __shared__ int h[kRadixBins];
   const int tid = threadIdx.x;
   h[tid] = 0;
+  if (fill)
+    for (long i = (long)blockIdx.x * kSortThreads + tid; i < fill_n; i += (long)gridDim.x * kSortThreads) fill[i] = -1;
   const long tile = (long)blockIdx.x * kSortTile;
   int d[kSortItems];
   if (vec && tile + kSortTile <= n) {
@@ -444,6 +449,37 @@ __global__ __launch_bounds__(kRadixBins) void hist_chunk_apply_kernel(int* __res
 #pragma unroll
   for (int r = 0; r < kHistChunk; ++r) {
     if (b0 + r < ntiles) hist[(long)(b0 + r) * kRadixBins + tid] = run;
+    run += x[r];
+  }
+}
+
+// The same scan in one block when all tiles form one chunk (ntiles <=
+// kHistChunk): each digit's column is walked twice (totals, then the scan
+// plus the digit's base), its counts held in registers.
+__global__ __launch_bounds__(kRadixBins) void hist_scan_small_kernel(int* __restrict__ hist, int ntiles) {
+  __shared__ int wtot[kRadixBins / 64];
+  const int d = threadIdx.x, lane = d & 63, wv = d >> 6;
+  int x[kHistChunk];
+  int tot = 0;
+#pragma unroll
+  for (int r = 0; r < kHistChunk; ++r) {
+    x[r] = r < ntiles ? hist[(long)r * kRadixBins + d] : 0;
+    tot += x[r];
+  }
+  int incl = tot;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(incl, o);
+    if (lane >= o) incl += y;
+  }
+  if (lane == 63) wtot[wv] = incl;
+  __syncthreads();
+  int run = incl - tot;
+#pragma unroll
+  for (int w = 0; w < kRadixBins / 64; ++w) run += w < wv ? wtot[w] : 0;
+#pragma unroll
+  for (int r = 0; r < kHistChunk; ++r) {
+    if (r < ntiles) hist[(long)r * kRadixBins + d] = run;
     run += x[r];
   }
 }
@@ -1254,13 +1290,18 @@ int esa_csr_build(const int* keys, int64_t num_edges, int num_nodes, int* indptr
         int* out = last ? skeys : pairs[p & 1];
         if (first)
           hipLaunchKernelGGL(radix_hist_kernel<false>, dim3(ntiles), dim3(kSortThreads), 0, st, in,
-                             (long)num_edges, num_nodes, shift, vec_keys, hist);
+                             (long)num_edges, num_nodes, shift, vec_keys, hist, indptr, (long)num_nodes + 1);
         else
           hipLaunchKernelGGL(radix_hist_kernel<true>, dim3(ntiles), dim3(kSortThreads), 0, st, in,
-                             (long)num_edges, num_nodes, shift, true, hist);
-        hipLaunchKernelGGL(hist_chunk_sum_kernel, dim3(nchunks), dim3(kRadixBins), 0, st, hist, ntiles, part);
-        hipLaunchKernelGGL(hist_chunk_scan_kernel, dim3(1), dim3(4 * kRadixBins), 0, st, part, nchunks);
-        hipLaunchKernelGGL(hist_chunk_apply_kernel, dim3(nchunks), dim3(kRadixBins), 0, st, hist, ntiles, part);
+                             (long)num_edges, num_nodes, shift, true, hist, nullptr, 0L);
+        if (nchunks == 1) {
+          hipLaunchKernelGGL(hist_scan_small_kernel, dim3(1), dim3(kRadixBins), 0, st, hist, ntiles);
+        } else {
+          hipLaunchKernelGGL(hist_chunk_sum_kernel, dim3(nchunks), dim3(kRadixBins), 0, st, hist, ntiles, part);
+          hipLaunchKernelGGL(hist_chunk_scan_kernel, dim3(1), dim3(4 * kRadixBins), 0, st, part, nchunks);
+          hipLaunchKernelGGL(hist_chunk_apply_kernel, dim3(nchunks), dim3(kRadixBins), 0, st, hist, ntiles,
+                             part);
+        }
         auto scatter = first ? (last ? radix_scatter_kernel<false, false> : radix_scatter_kernel<false, true>)
                              : (last ? radix_scatter_kernel<true, false> : radix_scatter_kernel<true, true>);
         hipLaunchKernelGGL(scatter, dim3(ntiles), dim3(kSortThreads), 0, st, in, (long)num_edges, num_nodes,
@@ -1268,9 +1309,10 @@ int esa_csr_build(const int* keys, int64_t num_edges, int num_nodes, int* indptr
       }
       sorted = skeys;
     }
-    // indptr: the boundaries of the sorted keys' runs
-    hipLaunchKernelGGL(fill_int_kernel, dim3(grid_for((long)num_nodes + 1, 256, 4096)), dim3(256), 0, st, indptr,
-                       (long)num_nodes + 1, -1);
+    // indptr: the boundaries of the sorted keys' runs (set to -1 by the first histogram pass)
+    if (num_edges == 0)
+      hipLaunchKernelGGL(fill_int_kernel, dim3(grid_for((long)num_nodes + 1, 256, 4096)), dim3(256), 0, st, indptr,
+                         (long)num_nodes + 1, -1);
     hipLaunchKernelGGL(indptr_runs_kernel, dim3(grid_for(num_edges / 4 + 1, 256)), dim3(256), 0, st, sorted,
                        (long)num_edges, num_nodes, indptr);
     hipLaunchKernelGGL(indptr_gap_kernel, dim3(grid_for((long)num_nodes + 1, 256, 4096)), dim3(256), 0, st,

@@ -13,8 +13,10 @@
 // gathered per token instead of tiled for MFMA: one wave per token, four lanes
 // per head with four dims each (a wave covers 16 heads per pass), fp32 scores,
 // softmax and accumulation.  The forward and dQ gather over the token's CSR
-// row; dK / dV gather over the transposed CSR (entries grouped by key, in
-// ascending position), built per call by the library's stable counting sort.
+// row; dK / dV gather over the transposed CSR (per key, the query rows that
+// list it, in ascending position), built with the library's stable CSR sort
+// per call, or once per batch into a node plan that every layer's backward
+// reads.
 // Every sum runs in a fixed order: the backward is deterministic.
 #include "esa_common.h"
 #include "esa_graph_attn.h"
@@ -62,6 +64,25 @@ template <> DEVI float ex2<float>(float x) { return exp2f(x); }
 template <typename T> DEVI float lg2(float x) { return fast_log2(x); }
 template <> DEVI float lg2<float>(float x) { return log2f(x); }
 
+// Segment of the wave's token t (wave-uniform): the largest s in [0, nseg)
+// with cu[s] <= t, as seg_of's binary search finds it, but with the wave's
+// 64 lanes sampling the range at once: each round narrows it 64-fold with one
+// load per lane and a ballot (two rounds up to 4096 segments, instead of
+// log2(nseg) dependent loads).
+DEVI int wave_seg_of(const int* __restrict__ cu, int nseg, int t) {
+  const int lane = threadIdx.x & 63;
+  int base = 0, span = nseg;
+  while (span > 1) {
+    const int step = (span + 63) >> 6, end = base + span;
+    const int s = base + lane * step;
+    const uint64_t m = __ballot(s < end && cu[s] <= t);
+    if (m == 0) break;   // cu[base] > t: only possible at base 0 (seg_of's answer as well)
+    base += (63 - __builtin_clzll(m)) * step;
+    span = min(step, end - base);
+  }
+  return base;
+}
+
 // This wave's token (one wave per token, four waves per block).
 DEVI int wave_token() { return blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
@@ -95,7 +116,7 @@ __global__ __launch_bounds__(256) void graph_attn_fwd_kernel(const GraphAttnArgs
   const int t = wave_token();
   if (t >= a.total_q) return;
   const int lane = threadIdx.x & 63, H = a.heads, d0 = 4 * (lane & 3);
-  const int sg = seg_of(a.cu_q, a.nseg, t);
+  const int sg = wave_seg_of(a.cu_q, a.nseg, t);
   const int lo = max(a.cu_k[sg], 0), hi = min(a.cu_k[sg + 1], a.total_k);
   int pa, pb;
   csr_row(a.indptr, t, a.nnz, pa, pb);
@@ -157,7 +178,7 @@ __global__ __launch_bounds__(256) void graph_attn_dq_kernel(const GraphAttnArgs 
   const int t = wave_token();
   if (t >= a.total_q) return;
   const int lane = threadIdx.x & 63, H = a.heads, d0 = 4 * (lane & 3);
-  const int sg = seg_of(a.cu_q, a.nseg, t);
+  const int sg = wave_seg_of(a.cu_q, a.nseg, t);
   const int lo = max(a.cu_k[sg], 0), hi = min(a.cu_k[sg + 1], a.total_k);
   int pa, pb;
   csr_row(a.indptr, t, a.nnz, pa, pb);
@@ -198,7 +219,7 @@ __global__ __launch_bounds__(256) void graph_attn_dq_kernel(const GraphAttnArgs 
 }
 
 // dV_j = sum_i P_ij dO_i, dK_j = scale * sum_i P_ij (dP_ij - D_i) q_i over the
-// queries i whose rows list key j (the transposed CSR, ascending position).
+// queries i whose rows list key j (t_rows[t_indptr[j] ..], ascending position).
 template <typename T>
 __global__ __launch_bounds__(256) void graph_attn_dkdv_kernel(const GraphAttnArgs a) {
   const T* __restrict__ q = static_cast<const T*>(a.q);
@@ -208,7 +229,7 @@ __global__ __launch_bounds__(256) void graph_attn_dkdv_kernel(const GraphAttnArg
   const int t = wave_token();
   if (t >= a.total_k) return;
   const int lane = threadIdx.x & 63, H = a.heads, d0 = 4 * (lane & 3);
-  const int sg = seg_of(a.cu_k, a.nseg, t);
+  const int sg = wave_seg_of(a.cu_k, a.nseg, t);
   const int lo = max(a.cu_q[sg], 0), hi = min(a.cu_q[sg + 1], a.total_q);
   const int pa = a.t_indptr[t], pb = hi > lo ? a.t_indptr[t + 1] : pa;
   for (int h0 = 0; h0 < H; h0 += 16) {
@@ -222,7 +243,7 @@ __global__ __launch_bounds__(256) void graph_attn_dkdv_kernel(const GraphAttnArg
     for (int p = pa; p < pb; p += kGU) {
       int i[kGU];
       bool ok[kGU];
-      next_entries(a.t_perm, a.row_of, p, pb, lo, hi, prev, i, ok);
+      next_entries(a.t_rows, nullptr, p, pb, lo, hi, prev, i, ok);
       float qr[kGU][4], gr[kGU][4], l2[kGU], ds_[kGU];
 #pragma unroll
       for (int u = 0; u < kGU; ++u) {
@@ -261,23 +282,83 @@ __global__ void row_of_kernel(const int* __restrict__ indptr, int rows, int nnz,
   csr_row(indptr, t, nnz, pa, pb);
   for (int p = pa; p < pb; ++p) row_of[p] = t;
 }
+// t_rows[p] = row_of[t_perm[p]]: the query row of each transposed entry; and
+// the plan's copy of the indices.
+__global__ void transpose_rows_kernel(const int* __restrict__ t_perm, const int* __restrict__ row_of, int nnz,
+                                      int* __restrict__ t_rows, const int* __restrict__ indices,
+                                      int* __restrict__ indices_copy) {
+  for (long p = (long)blockIdx.x * blockDim.x + threadIdx.x; p < nnz; p += (long)gridDim.x * blockDim.x) {
+    t_rows[p] = row_of[t_perm[p]];
+    if (indices_copy) indices_copy[p] = indices[p];
+  }
+}
 
 size_t al256(size_t x) { return (x + 255) & ~size_t(255); }
 
-struct GraphWs { size_t dsum, row_of, t_indptr, t_perm, csr, total; };
+// Node plan (mask_b of ESA_MASK_NODE_PLAN): the CSR's indices [nnz] first (so
+// the plan reads as the indices array), the transposed CSR t_indptr
+// [total_k + 1] and t_rows [nnz], then the build's scratch (row_of, t_perm
+// and the CSR sort's workspace).  The per-call backward lays the same
+// transposed CSR and scratch out in its workspace.
+struct NodePlan { size_t indices, t_indptr, t_rows, row_of, t_perm, csr, csr_bytes, total; };
 
-int graph_ws(int total_q, int total_k, int heads, int nnz, bool backward, GraphWs& w) {
-  w = GraphWs{};
-  if (!backward) { w.total = 0; return ESA_OK; }
-  size_t csr_bytes = 0;
-  const int rc = esa_csr_workspace_size(nnz, total_k, &csr_bytes);
+int node_plan_layout(int total_k, int nnz, NodePlan& w) {
+  w = NodePlan{};
+  const int rc = esa_csr_workspace_size(nnz, total_k, &w.csr_bytes);
   if (rc) return rc;
   size_t off = 0;
-  w.dsum = off; off += al256((size_t)heads * total_q * 4);
-  w.row_of = off; off += al256((size_t)nnz * 4 + 4);
+  w.indices = off; off += al256((size_t)nnz * 4 + 4);
   w.t_indptr = off; off += al256(((size_t)total_k + 1) * 4);
+  w.t_rows = off; off += al256((size_t)nnz * 4 + 4);
+  w.row_of = off; off += al256((size_t)nnz * 4 + 4);
   w.t_perm = off; off += al256((size_t)nnz * 4 + 4);
-  w.csr = off; off += al256(csr_bytes);
+  w.csr = off; off += al256(w.csr_bytes);
+  w.total = off;
+  return ESA_OK;
+}
+
+unsigned grid_of(long n) { const long b = (n + 255) / 256; return (unsigned)(b < 1 ? 1 : b < 4096 ? b : 4096); }
+
+// The transposed CSR of (indptr, indices) into base's NodePlan layout;
+// copy_indices: also the plan's copy of the indices.
+int build_transposed(const int* indptr, const int* indices, int total_q, int total_k, int nnz, char* base,
+                     const NodePlan& w, bool copy_indices, hipStream_t st) {
+  int* row_of = reinterpret_cast<int*>(base + w.row_of);
+  int* t_perm = reinterpret_cast<int*>(base + w.t_perm);
+  int* t_indptr = reinterpret_cast<int*>(base + w.t_indptr);
+  int* t_rows = reinterpret_cast<int*>(base + w.t_rows);
+  if (nnz > 0) {
+    hipLaunchKernelGGL(fill_minus_one_kernel, dim3(grid_of(nnz)), dim3(256), 0, st, row_of, (long)nnz);
+    ESA_LAUNCH_CHECK();
+    if (total_q > 0) {
+      hipLaunchKernelGGL(row_of_kernel, dim3((unsigned)((total_q + 255) / 256)), dim3(256), 0, st, indptr, total_q,
+                         nnz, row_of);
+      ESA_LAUNCH_CHECK();
+    }
+  }
+  int rc = esa_csr_build(indices, nnz, total_k, t_indptr, t_perm, base + w.csr, w.csr_bytes, st);
+  if (rc) return rc;
+  if (nnz > 0) {
+    hipLaunchKernelGGL(transpose_rows_kernel, dim3(grid_of(nnz)), dim3(256), 0, st, t_perm, row_of, nnz, t_rows,
+                       indices, copy_indices ? reinterpret_cast<int*>(base + w.indices) : nullptr);
+    ESA_LAUNCH_CHECK();
+  }
+  return ESA_OK;
+}
+
+struct GraphWs { size_t dsum, plan, total; };
+
+int graph_ws(int total_q, int total_k, int heads, int nnz, bool backward, bool planned, GraphWs& w) {
+  w = GraphWs{};
+  if (!backward) return ESA_OK;
+  size_t off = 0;
+  w.dsum = off; off += al256((size_t)heads * total_q * 4);
+  if (!planned) {
+    NodePlan np;
+    const int rc = node_plan_layout(total_k, nnz, np);
+    if (rc) return rc;
+    w.plan = off; off += np.total;
+  }
   w.total = off;
   return ESA_OK;
 }
@@ -286,12 +367,31 @@ unsigned token_blocks(int tokens) { return (unsigned)((tokens + 3) / 4); }
 
 }  // namespace
 
-int graph_attn_workspace_size(int total_q, int total_k, int heads, int nnz, bool backward, size_t* bytes) {
+int graph_attn_workspace_size(int total_q, int total_k, int heads, int nnz, bool backward, bool planned,
+                              size_t* bytes) {
   GraphWs w;
-  const int rc = graph_ws(total_q, total_k, heads, nnz, backward, w);
+  const int rc = graph_ws(total_q, total_k, heads, nnz, backward, planned, w);
   if (rc) return rc;
   *bytes = w.total;
   return ESA_OK;
+}
+
+int graph_node_plan_size(int total_q, int total_k, int nnz, size_t* bytes) {
+  (void)total_q;
+  NodePlan w;
+  const int rc = node_plan_layout(total_k, nnz, w);
+  if (rc) return rc;
+  *bytes = w.total;
+  return ESA_OK;
+}
+
+int graph_node_plan_build(const int* indptr, const int* indices, int total_q, int total_k, int nnz, void* plan,
+                          size_t plan_bytes, hipStream_t st) {
+  NodePlan w;
+  int rc = node_plan_layout(total_k, nnz, w);
+  if (rc) return rc;
+  if (plan_bytes < w.total) return ESA_ERR_WORKSPACE;
+  return build_transposed(indptr, indices, total_q, total_k, nnz, static_cast<char*>(plan), w, true, st);
 }
 
 int graph_attn_fwd(GraphAttnArgs a, int dtype, hipStream_t st) {
@@ -305,31 +405,26 @@ int graph_attn_fwd(GraphAttnArgs a, int dtype, hipStream_t st) {
   return ESA_OK;
 }
 
-int graph_attn_bwd(GraphAttnArgs a, int dtype, void* workspace, size_t workspace_bytes, hipStream_t st) {
+int graph_attn_bwd(GraphAttnArgs a, int dtype, const void* plan, void* workspace, size_t workspace_bytes,
+                   hipStream_t st) {
   GraphWs w;
-  int rc = graph_ws(a.total_q, a.total_k, a.heads, a.nnz, true, w);
+  int rc = graph_ws(a.total_q, a.total_k, a.heads, a.nnz, true, plan != nullptr, w);
   if (rc) return rc;
   if (workspace_bytes < w.total) return ESA_ERR_WORKSPACE;
   char* ws = static_cast<char*>(workspace);
   a.dsum = reinterpret_cast<float*>(ws + w.dsum);
-  a.row_of = reinterpret_cast<int*>(ws + w.row_of);
-  a.t_indptr = reinterpret_cast<int*>(ws + w.t_indptr);
-  a.t_perm = reinterpret_cast<int*>(ws + w.t_perm);
-  // transposed CSR: entries grouped by key, ascending position inside a key
-  if (a.nnz > 0) {
-    const long nb = ((long)a.nnz + 255) / 256;
-    hipLaunchKernelGGL(fill_minus_one_kernel, dim3((unsigned)(nb < 4096 ? nb : 4096)), dim3(256), 0, st, a.row_of,
-                       (long)a.nnz);
-    ESA_LAUNCH_CHECK();
-    if (a.total_q > 0) {
-      hipLaunchKernelGGL(row_of_kernel, dim3((unsigned)((a.total_q + 255) / 256)), dim3(256), 0, st, a.indptr,
-                         a.total_q, a.nnz, a.row_of);
-      ESA_LAUNCH_CHECK();
-    }
+  NodePlan np;
+  if ((rc = node_plan_layout(a.total_k, a.nnz, np))) return rc;
+  const char* tbase;
+  if (plan) {
+    tbase = static_cast<const char*>(plan);
+  } else {
+    if ((rc = build_transposed(a.indptr, a.indices, a.total_q, a.total_k, a.nnz, ws + w.plan, np, false, st)))
+      return rc;
+    tbase = ws + w.plan;
   }
-  size_t csr_bytes = 0;
-  if ((rc = esa_csr_workspace_size(a.nnz, a.total_k, &csr_bytes))) return rc;
-  if ((rc = esa_csr_build(a.indices, a.nnz, a.total_k, a.t_indptr, a.t_perm, ws + w.csr, csr_bytes, st))) return rc;
+  a.t_indptr = reinterpret_cast<const int*>(tbase + np.t_indptr);
+  a.t_rows = reinterpret_cast<const int*>(tbase + np.t_rows);
   const dim3 block(256);
   if (a.total_q > 0) {
     if (dtype == ESA_F32)

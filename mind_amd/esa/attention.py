@@ -87,10 +87,39 @@ def edge_plan(edge_src, edge_dst, cu_seqlens_q, cu_seqlens_k=None) -> torch.Tens
     return plan
 
 
-def _mask_args(tq: int, edge_src, edge_dst, adj_indptr, adj_indices, edge_plan=None):
+def node_plan(adj_indptr, adj_indices, total_k: int) -> torch.Tensor:
+    """The node-mode plan of a batch (esa_node_plan_build): a uint8 device tensor holding a copy of the CSR's
+    indices and its transpose (per key token, the query rows that list it), over ``total_k`` key tokens.
+    Built once per batch and passed as ``adj_plan=`` (with the same ``adj_indptr`` / ``adj_indices``) to
+    every attention call over that adjacency, so the backward does not rebuild the transpose per call, as
+    the reference builds its node bias once per batch (get_adj_mask_from_edge_index_node,
+    esa/masked_layers.py:79-118) for all layers."""
+    _lib.require_gpu(adj_indptr, adj_indices)
+    _check_index("adj_indptr", adj_indptr)
+    _check_index("adj_indices", adj_indices)
+    tq, nnz = adj_indptr.numel() - 1, adj_indices.numel()
+    lib = _lib.load()
+    n = _lib.ctypes.c_size_t(0)
+    _lib.check(lib.esa_node_plan_size(tq, int(total_k), nnz, _lib.ctypes.byref(n)), "esa_node_plan_size")
+    plan = torch.empty(max(int(n.value), 256), dtype=torch.uint8, device=adj_indptr.device)
+    rc = lib.esa_node_plan_build(adj_indptr.data_ptr(), adj_indices.data_ptr(), tq, int(total_k), nnz,
+                                 plan.data_ptr(), plan.numel(), _lib.stream_of(adj_indptr))
+    _lib.check(rc, "esa_node_plan_build")
+    return plan
+
+
+def _mask_args(tq: int, edge_src, edge_dst, adj_indptr, adj_indices, edge_plan=None, adj_plan=None):
     """(mask_kind, mask_a, mask_b, n_mask_edges) of the C ABI for the given mask tensors."""
     if sum(x is not None for x in (edge_src, adj_indptr, edge_plan)) > 1:
         raise ValueError("give one mask: the edge mask (edge_src / edge_dst), its plan, or the node adjacency")
+    if adj_plan is not None:
+        if adj_indptr is None or adj_indices is None:
+            raise ValueError("adj_plan goes with the adj_indptr / adj_indices it was built from")
+        if adj_plan.dtype != torch.uint8 or not adj_plan.is_cuda:
+            raise ValueError("adj_plan must be the uint8 device tensor node_plan() returns")
+        _check_index("adj_indptr", adj_indptr, tq + 1)
+        _check_index("adj_indices", adj_indices)
+        return _lib.ESA_MASK_NODE_PLAN, adj_indptr, adj_plan, adj_indices.numel()
     if edge_plan is not None:
         if edge_plan.dtype != torch.uint8 or not edge_plan.is_cuda:
             raise ValueError("edge_plan must be the uint8 device tensor edge_plan() returns")
@@ -107,9 +136,10 @@ def _mask_args(tq: int, edge_src, edge_dst, adj_indptr, adj_indices, edge_plan=N
 
 
 def attn_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale,
-             edge_src=None, edge_dst=None, adj_indptr=None, adj_indices=None, edge_plan=None):
+             edge_src=None, edge_dst=None, adj_indptr=None, adj_indices=None, edge_plan=None, adj_plan=None):
     """Raw forward: returns ``(out [Tq,H,16] (dtype of q), softmax_lse [H,Tq] fp32)``."""
-    _lib.require_gpu(q, k, v, cu_seqlens_q, cu_seqlens_k, edge_src, edge_dst, adj_indptr, adj_indices, edge_plan)
+    _lib.require_gpu(q, k, v, cu_seqlens_q, cu_seqlens_k, edge_src, edge_dst, adj_indptr, adj_indices, edge_plan,
+                     adj_plan)
     heads = q.shape[1]
     _check_tokens("q", q)
     _check_tokens("k", k, heads, q.dtype)
@@ -120,7 +150,7 @@ def attn_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, so
     _check_index("cu_seqlens_q", cu_seqlens_q)
     _check_index("cu_seqlens_k", cu_seqlens_k, batch + 1)
     tq, tk = q.shape[0], k.shape[0]
-    mask_kind, mask_a, mask_b, nnz = _mask_args(tq, edge_src, edge_dst, adj_indptr, adj_indices, edge_plan)
+    mask_kind, mask_a, mask_b, nnz = _mask_args(tq, edge_src, edge_dst, adj_indptr, adj_indices, edge_plan, adj_plan)
     dt = _dtype_code(q)
     out = torch.empty_like(q)
     lse = torch.empty((heads, tq), dtype=torch.float32, device=q.device)
@@ -136,12 +166,12 @@ def attn_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, so
 
 
 def attn_fwd_noalloc(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale, out, lse,
-                     edge_src=None, edge_dst=None, adj_indptr=None, adj_indices=None, edge_plan=None):
+                     edge_src=None, edge_dst=None, adj_indptr=None, adj_indices=None, edge_plan=None, adj_plan=None):
     """``attn_fwd`` into caller-provided ``out`` [Tq,H,16] and ``lse`` [H,Tq] fp32 through
     esa_varlen_attn_fwd_noalloc: no workspace, no device allocation (the library's static per-GPU scratch;
     calls that overlap on one GPU race).  Raises EsaError (ESA_ERR_SCRATCH) for shapes beyond that scratch."""
     _lib.require_gpu(q, k, v, cu_seqlens_q, cu_seqlens_k, edge_src, edge_dst, adj_indptr, adj_indices, out, lse,
-                     edge_plan)
+                     edge_plan, adj_plan)
     heads = q.shape[1]
     _check_tokens("q", q)
     _check_tokens("k", k, heads, q.dtype)
@@ -155,7 +185,7 @@ def attn_fwd_noalloc(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seql
     _check_index("cu_seqlens_q", cu_seqlens_q)
     _check_index("cu_seqlens_k", cu_seqlens_k, batch + 1)
     tq, tk = q.shape[0], k.shape[0]
-    mask_kind, mask_a, mask_b, nnz = _mask_args(tq, edge_src, edge_dst, adj_indptr, adj_indices, edge_plan)
+    mask_kind, mask_a, mask_b, nnz = _mask_args(tq, edge_src, edge_dst, adj_indptr, adj_indices, edge_plan, adj_plan)
     rc = _lib.load().esa_varlen_attn_fwd_noalloc(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(), batch, tq, tk,
         int(max_seqlen_q), int(max_seqlen_k), heads, HEAD_DIM, _dtype_code(q), float(softmax_scale),
@@ -165,7 +195,7 @@ def attn_fwd_noalloc(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seql
 
 
 def attn_bwd(dout, q, k, v, out, lse, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale,
-             edge_src=None, edge_dst=None, adj_indptr=None, adj_indices=None, edge_plan=None):
+             edge_src=None, edge_dst=None, adj_indptr=None, adj_indices=None, edge_plan=None, adj_plan=None):
     """Raw backward: returns ``(dq, dk, dv)`` (dtype and shapes of q, k, v)."""
     _lib.require_gpu(dout, q, k, v, out, lse)
     heads = q.shape[1]
@@ -176,7 +206,7 @@ def attn_bwd(dout, q, k, v, out, lse, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, 
         raise ValueError("dout and out must have the shape of q")
     batch = cu_seqlens_q.numel() - 1
     tq, tk = q.shape[0], k.shape[0]
-    mask_kind, mask_a, mask_b, nnz = _mask_args(tq, edge_src, edge_dst, adj_indptr, adj_indices, edge_plan)
+    mask_kind, mask_a, mask_b, nnz = _mask_args(tq, edge_src, edge_dst, adj_indptr, adj_indices, edge_plan, adj_plan)
     dt = _dtype_code(q)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     ws = _workspace(q.device, tq, tk, heads, dt, mask_kind, nnz, True)
@@ -199,14 +229,15 @@ def _op_varlen_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens
                    cu_seqlens_k: torch.Tensor, max_seqlen_q: int, max_seqlen_k: int, softmax_scale: float,
                    edge_src: Optional[torch.Tensor], edge_dst: Optional[torch.Tensor],
                    adj_indptr: Optional[torch.Tensor], adj_indices: Optional[torch.Tensor],
-                   edge_plan: Optional[torch.Tensor] = None) -> tuple[torch.Tensor, torch.Tensor]:
+                   edge_plan: Optional[torch.Tensor] = None,
+                   adj_plan: Optional[torch.Tensor] = None) -> tuple[torch.Tensor, torch.Tensor]:
     return attn_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale, edge_src,
-                    edge_dst, adj_indptr, adj_indices, edge_plan)
+                    edge_dst, adj_indptr, adj_indices, edge_plan, adj_plan)
 
 
 @_op_varlen_fwd.register_fake
 def _(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale, edge_src, edge_dst,
-      adj_indptr, adj_indices, edge_plan=None):
+      adj_indptr, adj_indices, edge_plan=None, adj_plan=None):
     return torch.empty_like(q), q.new_empty((q.shape[1], q.shape[0]), dtype=torch.float32)
 
 
@@ -216,30 +247,33 @@ def _op_varlen_bwd(dout: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torc
                    max_seqlen_k: int, softmax_scale: float, edge_src: Optional[torch.Tensor],
                    edge_dst: Optional[torch.Tensor], adj_indptr: Optional[torch.Tensor],
                    adj_indices: Optional[torch.Tensor],
-                   edge_plan: Optional[torch.Tensor] = None) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+                   edge_plan: Optional[torch.Tensor] = None,
+                   adj_plan: Optional[torch.Tensor] = None) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     return attn_bwd(dout, q, k, v, out, lse, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale,
-                    edge_src, edge_dst, adj_indptr, adj_indices, edge_plan)
+                    edge_src, edge_dst, adj_indptr, adj_indices, edge_plan, adj_plan)
 
 
 @_op_varlen_bwd.register_fake
 def _(dout, q, k, v, out, lse, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale, edge_src,
-      edge_dst, adj_indptr, adj_indices, edge_plan=None):
+      edge_dst, adj_indptr, adj_indices, edge_plan=None, adj_plan=None):
     return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
 
 
 def _varlen_setup(ctx, inputs, output):
-    q, k, v, cu_q, cu_k, max_q, max_k, scale, edge_src, edge_dst, adj_indptr, adj_indices, edge_plan = inputs
+    q, k, v, cu_q, cu_k, max_q, max_k, scale, edge_src, edge_dst, adj_indptr, adj_indices, edge_plan, adj_plan = inputs
     out, lse = output
-    ctx.save_for_backward(q, k, v, out, lse, cu_q, cu_k, edge_src, edge_dst, adj_indptr, adj_indices, edge_plan)
+    ctx.save_for_backward(q, k, v, out, lse, cu_q, cu_k, edge_src, edge_dst, adj_indptr, adj_indices, edge_plan,
+                          adj_plan)
     ctx.meta = (max_q, max_k, scale)
 
 
 def _varlen_backward(ctx, dout, _dlse):
-    q, k, v, out, lse, cu_q, cu_k, edge_src, edge_dst, adj_indptr, adj_indices, edge_plan = ctx.saved_tensors
+    q, k, v, out, lse, cu_q, cu_k, edge_src, edge_dst, adj_indptr, adj_indices, edge_plan, adj_plan = ctx.saved_tensors
     max_q, max_k, scale = ctx.meta
     dq, dk, dv = torch.ops.esa_hip.varlen_attn_bwd(dout.contiguous(), q, k, v, out, lse, cu_q, cu_k, max_q, max_k,
-                                                   scale, edge_src, edge_dst, adj_indptr, adj_indices, edge_plan)
-    return dq, dk, dv, None, None, None, None, None, None, None, None, None, None
+                                                   scale, edge_src, edge_dst, adj_indptr, adj_indices, edge_plan,
+                                                   adj_plan)
+    return dq, dk, dv, None, None, None, None, None, None, None, None, None, None, None
 
 
 torch.library.register_autograd("esa_hip::varlen_attn_fwd", _varlen_backward, setup_context=_varlen_setup)
@@ -247,7 +281,7 @@ torch.library.register_autograd("esa_hip::varlen_attn_fwd", _varlen_backward, se
 
 def varlen_attention(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, dropout_p=0.0,
                      softmax_scale=None, causal=False, edge_src=None, edge_dst=None, return_lse=False,
-                     adj_indptr=None, adj_indices=None, edge_plan=None):
+                     adj_indptr=None, adj_indices=None, edge_plan=None, adj_plan=None):
     """``flash_attn_varlen_func``-compatible entry (plus the ESA masks).
 
     q: [Tq, H, 16]; k, v: [Tk, H, 16], all bfloat16 or all float32;
@@ -259,7 +293,9 @@ def varlen_attention(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seql
     edge_src / edge_dst) and shared by every call over the batch.
     adj_indptr [Tq+1] / adj_indices [nnz]: optional int32 CSR adjacency (node
     mode): token i attends to the keys listed in its row, ascending, a
-    repeated entry counting once.  With return_lse, also returns the
+    repeated entry counting once.  adj_plan: optional, the node plan of that
+    CSR from ``node_plan()``, shared by every call over the batch (the
+    backward then reads its transpose).  With return_lse, also returns the
     (non-differentiable) softmax log-sum-exp [H, Tq]; -inf marks a query with
     no admissible key (its output is 0).
     """
@@ -275,7 +311,7 @@ def varlen_attention(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seql
         raise ValueError("adj_indptr and adj_indices must be given together")
     out, lse = torch.ops.esa_hip.varlen_attn_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, int(max_seqlen_q),
                                                  int(max_seqlen_k), float(softmax_scale), edge_src, edge_dst,
-                                                 adj_indptr, adj_indices, edge_plan)
+                                                 adj_indptr, adj_indices, edge_plan, adj_plan)
     return (out, lse) if return_lse else out
 
 

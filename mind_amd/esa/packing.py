@@ -186,6 +186,7 @@ class NodeAdjacency(PackedSets):
 
     indptr: torch.Tensor = None
     indices: torch.Tensor = None
+    _plan: torch.Tensor | None = field(default=None, repr=False, compare=False)
 
     @classmethod
     def from_edge_index(cls, edge_index: torch.Tensor, batch_mapping: torch.Tensor, batch_size: int,
@@ -213,8 +214,17 @@ class NodeAdjacency(PackedSets):
         counts.index_copy_(0, pidx, deg)
         return cu_seqlens_from_counts(counts), pidx.index_select(0, self.indices.to(torch.int64)).to(torch.int32)
 
+    def plan(self) -> torch.Tensor:
+        """The batch's node plan (esa_node_plan_build: the CSR's transpose by key), built on first use and
+        reused by every node-mode layer's backward, as the reference builds its node bias once per batch
+        (esa/masked_layers.py:849-936)."""
+        if self._plan is None:
+            from .attention import node_plan
+            self._plan = node_plan(self.indptr, self.indices, self.indptr.numel() - 1)
+        return self._plan
+
     def kernel_mask(self, padded: bool) -> dict:
         if padded:
             ip, ix = self.padded_csr()
             return {"adj_indptr": ip, "adj_indices": ix}
-        return {"adj_indptr": self.indptr, "adj_indices": self.indices}
+        return {"adj_indptr": self.indptr, "adj_indices": self.indices, "adj_plan": self.plan()}

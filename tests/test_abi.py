@@ -74,3 +74,12 @@ def test_argument_errors_need_no_gpu():
     assert rc == -4
     assert lib.esa_edge_gather(16, 16, 16, 10, 10, 8, 7, 16, None) == -5
     assert lib.esa_csr_workspace_size(-1, 10, ctypes.byref(n)) == -2
+    # node plan: size errors, and a planned backward needs only its row statistics
+    node, node_plan = _lib.ESA_MASK_NODE, _lib.ESA_MASK_NODE_PLAN
+    assert lib.esa_node_plan_size(100, 100, -1, ctypes.byref(n)) == -2
+    assert lib.esa_node_plan_size(100, 100, 500, ctypes.byref(n)) == 0 and n.value > 500 * 8
+    m = ctypes.c_size_t(0)
+    assert lib.esa_varlen_attn_workspace_size(100, 100, 16, 16, bf16, node, 500, 1, ctypes.byref(n)) == 0
+    assert lib.esa_varlen_attn_workspace_size(100, 100, 16, 16, bf16, node_plan, 500, 1, ctypes.byref(m)) == 0
+    assert 0 < m.value < n.value
+    assert lib.esa_node_plan_build(None, None, 100, 100, 0, 256, 1 << 20, None) == -1

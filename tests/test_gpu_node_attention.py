@@ -88,6 +88,35 @@ def test_node_mask_isolated_nodes_and_empty_graph(device, dtype):
         assert torch.isneginf(lse[:, node]).all()
 
 
+@pytest.mark.parametrize("planned", [False, True])
+def test_node_mask_many_segments(device, planned):
+    """300 graphs of 0-6 nodes (a third of them empty): every token finds its segment among more than 64 (the
+    wave-parallel segment search takes two rounds; empty segments share their start with the next one)."""
+    rng = np.random.default_rng(77)
+    sizes = [int(x) for x in rng.integers(0, 7, size=300)]
+    sizes[-1] = max(sizes[-1], 1)
+    if planned:
+        ei, bm = node_graph(78, sizes)
+        na = NodeAdjacency.from_edge_index(torch.as_tensor(ei).to(device), torch.as_tensor(bm).to(device),
+                                           len(sizes), max(sizes))
+        t = len(bm)
+        q, k, v, g = (seeded_normal((t, 3, D), 600 + i, torch.float32) for i in range(4))
+        qd, kd, vd = (x.to(device).requires_grad_(True) for x in (q, k, v))
+        cu = na.cu_seqlens
+        out = A.varlen_attention(qd, kd, vd, cu, cu, 0, 0, softmax_scale=0.25, **na.kernel_mask(padded=False))
+        out.backward(g.to(device))
+        adj = (na.indptr.cpu().numpy(), na.indices.cpu().numpy())
+        cun = cu.cpu().numpy()
+        ref, _ = OA.varlen_attention(q, k, v, cun, cun, 0.25, adj=adj)
+        rdq, rdk, rdv = OA.varlen_attention_bwd(g, q, k, v, cun, cun, 0.25, adj=adj)
+        assert_f32_close(out.detach().cpu(), ref, "out")
+        for name, a, b in (("dq", qd.grad, rdq), ("dk", kd.grad, rdk), ("dv", vd.grad, rdv)):
+            assert_f32_close(a.cpu(), b, name)
+    else:
+        got, ref, _ = _run(device, sizes, 79, 3, torch.float32)
+        _check(got, ref, torch.float32)
+
+
 def test_node_mask_protein_like_full_size(device):
     """Config-1 protein graphs in node mode (radius edges, cap 16): every node attends to its neighbours."""
     gb = generators.protein_like(seed=0)
@@ -168,6 +197,54 @@ def test_esa_node_mode(device):
         pool=lambda s_, p_, x: OMod.pma_complete(s_, p_, x, h, 2, cu=cu, max_items=n))
     assert_f32_close(enc.cpu()[valid], enc_ref, "ESA node-mode encoder (valid rows)")
     assert_f32_close(g_emb.cpu().reshape(g_ref.shape), g_ref, "ESA node-mode graph embedding")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_node_plan_equals_per_call_transpose(device, dtype):
+    """A node plan built once (esa_node_plan_build, passed as adj_plan) gives the per-call path's forward and
+    backward bit for bit on two calls in a row (repeated edges, self-loops, an empty and a one-node graph),
+    and its first nnz ints are the CSR's indices (the forward reads the plan as the indices array)."""
+    sizes = [37, 0, 64, 1, 90]
+    ei, bm = node_graph(31, sizes)
+    na = NodeAdjacency.from_edge_index(torch.as_tensor(ei).to(device), torch.as_tensor(bm).to(device), len(sizes),
+                                       max(sizes))
+    t, heads = len(bm), 16
+    q, k, v, g = (seeded_normal((t, heads, D), 400 + i, dtype).to(device) for i in range(4))
+    cu, ip, ix = na.cu_seqlens, na.indptr, na.indices
+    plan = na.plan()
+    assert torch.equal(plan[: 4 * ix.numel()].view(torch.int32), ix)
+    out0, lse0 = A.attn_fwd(q, k, v, cu, cu, 0, 0, 0.25, adj_indptr=ip, adj_indices=ix)
+    ref = A.attn_bwd(g, q, k, v, out0, lse0, cu, cu, 0, 0, 0.25, adj_indptr=ip, adj_indices=ix)
+    for _ in range(2):
+        out, lse = A.attn_fwd(q, k, v, cu, cu, 0, 0, 0.25, adj_indptr=ip, adj_indices=ix, adj_plan=plan)
+        assert torch.equal(out, out0) and torch.equal(lse, lse0)
+        got = A.attn_bwd(g, q, k, v, out, lse, cu, cu, 0, 0, 0.25, adj_indptr=ip, adj_indices=ix, adj_plan=plan)
+        for name, a, b in zip(("dq", "dk", "dv"), got, ref):
+            assert torch.equal(a, b), name
+
+
+def test_node_plan_entries_outside_segment(device):
+    """Entries naming a key of another segment are ignored by the planned backward as by the per-call one
+    (the transposed rows list such a query under the foreign key; the key pass drops it by segment)."""
+    cu = torch.tensor([0, 3, 7], dtype=torch.int32, device=device)
+    # segments {0, 1, 2} and {3, .., 6}; row 0 lists key 5 (segment 1) beside its own keys, row 4 lists key 1
+    rows = [[1, 2, 5], [0], [0, 1], [4, 6], [1, 3], [6], [3, 5]]
+    ip = torch.tensor(np.cumsum([0] + [len(r) for r in rows]), dtype=torch.int32, device=device)
+    ix = torch.tensor([j for r in rows for j in r], dtype=torch.int32, device=device)
+    plan = A.node_plan(ip, ix, 7)
+    q, k, v, g = (seeded_normal((7, 3, D), 500 + i, torch.float32).to(device) for i in range(4))
+    out0, lse0 = A.attn_fwd(q, k, v, cu, cu, 0, 0, 0.25, adj_indptr=ip, adj_indices=ix)
+    out, lse = A.attn_fwd(q, k, v, cu, cu, 0, 0, 0.25, adj_indptr=ip, adj_indices=ix, adj_plan=plan)
+    assert torch.equal(out, out0) and torch.equal(lse, lse0)
+    ref = A.attn_bwd(g, q, k, v, out0, lse0, cu, cu, 0, 0, 0.25, adj_indptr=ip, adj_indices=ix)
+    got = A.attn_bwd(g, q, k, v, out, lse, cu, cu, 0, 0, 0.25, adj_indptr=ip, adj_indices=ix, adj_plan=plan)
+    for a, b in zip(got, ref):
+        assert torch.equal(a, b)
+    adj = (ip.cpu().numpy(), ix.cpu().numpy())
+    cun = cu.cpu().numpy()
+    rdq, rdk, rdv = OA.varlen_attention_bwd(g.cpu(), q.cpu(), k.cpu(), v.cpu(), cun, cun, 0.25, adj=adj)
+    for a, b in zip(got, (rdq, rdk, rdv)):
+        assert_f32_close(a.cpu(), b, "planned grads vs oracle")
 
 
 def test_node_mask_argument_errors(device):
