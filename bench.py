@@ -55,11 +55,13 @@ def parse():
                     help="graphs of the configuration-2 batch timed on the CPU for the masked baseline")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-sub", action="store_true",
-                    help="headline only: skip the masked (configuration 2) and gather (configuration 3) sub-objects")
-    ap.add_argument("--config", choices=["varlen", "masked", "gather", "block", "stack"], default="varlen",
+                    help="headline only: skip the masked (configuration 2), gather (configuration 3) and node "
+                         "sub-objects")
+    ap.add_argument("--config", choices=["varlen", "masked", "gather", "node", "block", "stack"], default="varlen",
                     help="varlen: configuration 1 (default, the headline metric); masked: configuration 2 "
                          "(edge-masked MAB attention fwd+bwd); gather: configuration 3 (edge gather + CSR "
-                         "segment sum, HBM-bound); block: configuration 0 (fp32 ESA block forward on small "
+                         "segment sum, HBM-bound); node: node-mode (CSR adjacency) attention fwd+bwd on a "
+                         "65,536-node batch; block: configuration 0 (fp32 ESA block forward on small "
                          "molecules); stack: configuration 4 (bf16 ESA encoder stack train step)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy three times (HBM counter calibration)")
@@ -157,9 +159,11 @@ def main():
         if not args.no_sub:
             result["masked"] = bench_masked(args, sub=True)
             result["gather"] = bench_gather(args, sub=True)
+            result["node"] = bench_node(args, sub=True)
         print(json.dumps(result), flush=True)
         return
-    {"masked": bench_masked, "gather": bench_gather, "block": bench_block, "stack": bench_stack}[args.config](args)
+    {"masked": bench_masked, "gather": bench_gather, "node": bench_node, "block": bench_block,
+     "stack": bench_stack}[args.config](args)
 
 
 def timed(step, steps: int, warmup: int, profile: bool = True):
@@ -332,6 +336,126 @@ def cpu_baseline_masked(gb, seed: int, n_graphs: int) -> dict:
                        f"{lens.tolist()}, padded to N = {n}): torch scaled_dot_product_attention fp32 with the "
                        f"reference's additive edge bias (oracle.attention.padded_sdpa), forward + autograd "
                        f"backward on {cores} threads, median of {runs} runs after 2 warm-ups")}
+
+
+def node_bytes(t: int, nnz: int, heads: int = HEADS) -> dict:
+    """Compulsory HBM bytes per launch of the node-mode kernels (bf16 [T, H, 16] tensors of T*H*32 bytes, fp32
+    [H, T] row statistics, int32 CSR): forward reads Q, K, V and writes O and the LSE; dQ reads Q, K, V, O, dO
+    and the LSE and writes dQ and D; dK/dV reads K, V, Q, dO, the LSE and D and the transposed CSR and
+    writes dK and dV.  Each gathered row counted once (the rows of a graph are reused from cache)."""
+    row = t * heads * HEAD_DIM * 2
+    stat = heads * t * 4
+    csr = 4 * (t + 1) + 4 * nnz
+    return {"graph_attn_fwd": 4 * row + stat + csr, "graph_attn_bwd_dq": 6 * row + 2 * stat + csr,
+            "graph_attn_bwd_dkdv": 6 * row + 2 * stat + csr}
+
+
+def cpu_baseline_node(gb, seed: int, n_graphs: int) -> dict:
+    """The reference's node-mode attention on the host cores, fp32 forward + backward, on a bounded sample: the
+    node bias (0 at (src, dst) of every edge, else -99999; get_adj_mask_from_edge_index_node,
+    esa/masked_layers.py:79-118) added to the scores of every graph padded to N (esa/mha.py:73-77), i.e.
+    torch's scaled_dot_product_attention with that additive bias (oracle.attention.padded_sdpa).  Sample:
+    graphs spread over the size distribution, padded to the batch's N."""
+    import torch
+
+    from oracle import attention as oracle_attention
+    from oracle import mask as oracle_mask
+    from oracle.packing import nearest_multiple_of_8
+
+    cores = len(os.sched_getaffinity(0))
+    order = np.argsort(gb.node_counts)
+    pick = sorted(set(int(order[int(i)]) for i in np.linspace(0, len(order) - 1, n_graphs)))
+    first = np.concatenate([[0], np.cumsum(gb.node_counts)]).astype(np.int64)
+    lens = gb.node_counts[pick].astype(np.int64)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    # the sample's CSR over its own node numbering
+    src, dst = gb.edge_index
+    rows, cols = [], []
+    for b, g in enumerate(pick):
+        sel = (src >= first[g]) & (src < first[g + 1])
+        rows.append(src[sel] - first[g] + cu[b])
+        cols.append(dst[sel] - first[g] + cu[b])
+    rows, cols = np.concatenate(rows), np.concatenate(cols)
+    t = int(cu[-1])
+    o = np.lexsort((cols, rows))
+    indptr = np.searchsorted(rows[o], np.arange(t + 1))
+    indices = cols[o]
+    n = nearest_multiple_of_8(int(gb.node_counts.max()) + 1)
+    biases = [torch.where(torch.as_tensor(oracle_mask.node_adjacency_segment(indptr, indices, int(cu[b]),
+                                                                             int(cu[b + 1]), int(cu[b]),
+                                                                             int(cu[b + 1]))),
+                          0.0, oracle_mask.MASK_FILL) for b in range(len(pick))]
+    g = torch.Generator().manual_seed(seed + 97)
+    q, k, v, go = (torch.randn(t, HEADS, HEAD_DIM, generator=g) for _ in range(4))
+
+    def step():
+        qd, kd, vd = (x.detach().requires_grad_(True) for x in (q, k, v))
+        out = oracle_attention.padded_sdpa(qd, kd, vd, cu, cu, n, 1.0 / HEAD_DIM ** 0.5, pair_bias=lambda b: biases[b])
+        out.backward(go)
+
+    torch.set_num_threads(cores)
+    med, runs = _median_time(step)
+    return {"value": t / med, "unit": "node-tokens/s", "cores": cores, "kind": "port",
+            "sample": (f"{len(pick)} graphs of the batch spread over its sizes ({t} nodes, sizes {lens.tolist()}, "
+                       f"padded to N = {n}): torch scaled_dot_product_attention fp32 with the reference's additive "
+                       f"node bias (oracle.attention.padded_sdpa), forward + autograd backward on {cores} threads, "
+                       f"median of {runs} runs after 2 warm-ups")}
+
+
+def bench_node(args, sub: bool = False):
+    """Node-mode attention fwd+bwd (the mask every MIND YAML applies: query node src attends to key node dst per
+    edge, esa/masked_layers.py:79-118) on a 65,536-node budget batch of protein-like graphs (radius 8 A, at most
+    16 neighbours), 16 heads x 16.  The timed step builds the batch's node plan from the CSR (once per batch,
+    as the reference builds its node bias) and runs the attention forward and backward over it."""
+    import torch
+
+    from mind_amd import generators
+    from mind_amd.esa import attention
+    from mind_amd.esa.packing import NodeAdjacency
+
+    dev = torch.device("cuda", 0)
+    gb = generators.protein_budget(seed=args.seed, token_budget=65536, count="nodes")
+    ei = torch.as_tensor(gb.edge_index).to(dev)
+    bm = torch.as_tensor(gb.batch).to(dev)
+    na = NodeAdjacency.from_edge_index(ei, bm, gb.num_graphs, int(gb.node_counts.max()))
+    t, nnz = int(gb.node_counts.sum()), int(na.indices.numel())
+    g = torch.Generator().manual_seed(args.seed)
+    q, k, v, go = (torch.randn(t, HEADS, HEAD_DIM, generator=g).to(torch.bfloat16).to(dev) for _ in range(4))
+    cu, ip, ix = na.cu_seqlens, na.indptr, na.indices
+    scale = 1.0 / HEAD_DIM ** 0.5
+
+    def step():
+        plan = attention.node_plan(ip, ix, t)
+        out, lse = attention.attn_fwd(q, k, v, cu, cu, 0, 0, scale, adj_indptr=ip, adj_indices=ix, adj_plan=plan)
+        attention.attn_bwd(go, q, k, v, out, lse, cu, cu, 0, 0, scale, adj_indptr=ip, adj_indices=ix, adj_plan=plan)
+
+    ms_per_step, wall_ms, per_kernel, ms_prof = timed(step, args.steps, args.warmup)
+    by = node_bytes(t, nnz)
+    for name, rec in per_kernel.items():
+        if name in by:
+            rec["algorithmic_bytes"] = by[name]
+            rec["achieved_gbs"] = by[name] / (rec["avg_us"] * 1e-6) / 1e9
+    dom = max((n for n in by if n in per_kernel), key=lambda n: per_kernel[n]["avg_us"])
+    achieved = per_kernel[dom]["achieved_gbs"]
+    roofline = {"bound": "hbm", "kernel": dom, "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": achieved / PEAK_HBM_GBS, "traffic": None,
+                "bytes": "compulsory: every tensor row and CSR entry once (node_bytes)"}
+    out = {"workload": "node-mode attention fwd+bwd over a 65,536-node budget batch (node plan built each step)",
+           "graphs": gb.num_graphs, "node_tokens": t, "mask_nnz": nnz, "heads": HEADS, "head_dim": HEAD_DIM,
+           "ms_per_step": ms_per_step, "wall_ms_per_step": wall_ms, "node_tokens_per_s": t / (ms_per_step * 1e-3),
+           "ms_per_step_profiled": ms_prof, "kernels": per_kernel, "roofline": roofline}
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline_node(gb, args.seed, args.cpu_sample_graphs)
+    if sub:
+        return out
+    result = {"metric": "node-tokens/sec through node-mode ESA attn fwd+bwd", "value": t / (ms_per_step * 1e-3),
+              "unit": "node-tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+              "ms_per_step": ms_per_step, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+              "dtype": "bf16", "data": "synthetic (seeded protein-like radius graphs; q, k, v, dO ~ N(0,1))",
+              "config": {"workload": out["workload"], "graphs": gb.num_graphs, "node_tokens": t, "mask_nnz": nnz,
+                         "heads": HEADS, "head_dim": HEAD_DIM, "seed": args.seed}}
+    result.update({k: v for k, v in out.items() if k not in ("workload", "graphs", "node_tokens", "mask_nnz")})
+    print(json.dumps(result), flush=True)
 
 
 def bench_masked(args, sub: bool = False):

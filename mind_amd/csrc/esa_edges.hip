@@ -453,33 +453,47 @@ __global__ __launch_bounds__(kRadixBins) void hist_chunk_apply_kernel(int* __res
   }
 }
 
-// The same scan in one block when all tiles form one chunk (ntiles <=
-// kHistChunk): each digit's column is walked twice (totals, then the scan
-// plus the digit's base), its counts held in registers.
-__global__ __launch_bounds__(kRadixBins) void hist_scan_small_kernel(int* __restrict__ hist, int ntiles) {
+// The same scan in one block of 4 x 256 threads when ntiles <= 4 kHistChunk:
+// thread (q, d) holds rows [64 q, 64 q + 64) of digit d's column in registers;
+// the quarters' sums and the digit totals' exclusive scan go through LDS.
+constexpr int kSmallScanTiles = 4 * kHistChunk;
+
+__global__ __launch_bounds__(4 * kRadixBins) void hist_scan_small_kernel(int* __restrict__ hist, int ntiles) {
+  __shared__ int qsum[4][kRadixBins];
   __shared__ int wtot[kRadixBins / 64];
-  const int d = threadIdx.x, lane = d & 63, wv = d >> 6;
+  const int d = threadIdx.x & (kRadixBins - 1), q = threadIdx.x / kRadixBins;
+  const int lane = threadIdx.x & 63, wv = d >> 6, r0 = q * kHistChunk;
   int x[kHistChunk];
-  int tot = 0;
+  int s = 0;
 #pragma unroll
   for (int r = 0; r < kHistChunk; ++r) {
-    x[r] = r < ntiles ? hist[(long)r * kRadixBins + d] : 0;
-    tot += x[r];
+    x[r] = r0 + r < ntiles ? hist[(long)(r0 + r) * kRadixBins + d] : 0;
+    s += x[r];
   }
+  qsum[q][d] = s;
+  __syncthreads();
+  int tot = 0, run = 0;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const int y = qsum[w][d];
+    run += w < q ? y : 0;
+    tot += y;
+  }
+  // exclusive scan of the digit totals, by the first quarter's waves
   int incl = tot;
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
     const int y = __shfl_up(incl, o);
     if (lane >= o) incl += y;
   }
-  if (lane == 63) wtot[wv] = incl;
+  if (q == 0 && lane == 63) wtot[wv] = incl;
   __syncthreads();
-  int run = incl - tot;
 #pragma unroll
   for (int w = 0; w < kRadixBins / 64; ++w) run += w < wv ? wtot[w] : 0;
+  run += incl - tot;
 #pragma unroll
   for (int r = 0; r < kHistChunk; ++r) {
-    if (r < ntiles) hist[(long)r * kRadixBins + d] = run;
+    if (r0 + r < ntiles) hist[(long)(r0 + r) * kRadixBins + d] = run;
     run += x[r];
   }
 }
@@ -1294,8 +1308,8 @@ int esa_csr_build(const int* keys, int64_t num_edges, int num_nodes, int* indptr
         else
           hipLaunchKernelGGL(radix_hist_kernel<true>, dim3(ntiles), dim3(kSortThreads), 0, st, in,
                              (long)num_edges, num_nodes, shift, true, hist, nullptr, 0L);
-        if (nchunks == 1) {
-          hipLaunchKernelGGL(hist_scan_small_kernel, dim3(1), dim3(kRadixBins), 0, st, hist, ntiles);
+        if (ntiles <= kSmallScanTiles) {
+          hipLaunchKernelGGL(hist_scan_small_kernel, dim3(1), dim3(4 * kRadixBins), 0, st, hist, ntiles);
         } else {
           hipLaunchKernelGGL(hist_chunk_sum_kernel, dim3(nchunks), dim3(kRadixBins), 0, st, hist, ntiles, part);
           hipLaunchKernelGGL(hist_chunk_scan_kernel, dim3(1), dim3(4 * kRadixBins), 0, st, part, nchunks);

@@ -83,8 +83,15 @@ DEVI int wave_seg_of(const int* __restrict__ cu, int nseg, int t) {
   return base;
 }
 
-// This wave's token (one wave per token, four waves per block).
-DEVI int wave_token() { return blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+// This wave's token (one wave per token, four waves per block).  Hardware
+// block b runs on XCD b % 8; blocks are dealt so that each XCD takes one
+// contiguous range of tokens, whose partners (mostly nearby tokens of the same
+// graph) are then read into that XCD's L2 only.
+DEVI int wave_token() {
+  const int nb = gridDim.x, q = nb >> 3, rem = nb & 7, x = blockIdx.x & 7, s = blockIdx.x >> 3;
+  const int b = x * q + min(x, rem) + s;
+  return b * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+}
 
 // Row [pa, pb) of a CSR clamped into [0, nnz).
 DEVI void csr_row(const int* __restrict__ indptr, int t, int nnz, int& pa, int& pb) {

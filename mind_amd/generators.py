@@ -138,27 +138,33 @@ def protein_like(seed: int = 0, num_graphs: int = 32, n_min: int = 64, n_max: in
 
 
 def protein_budget(seed: int = 0, token_budget: int = 65536, mu: float = 5.5, sigma: float = 0.5,
-                   n_min: int = 32, n_max: int = 1024, r: float = 8.0, cap: int = 16) -> GraphBatch:
-    """Config 2 (masked MAB): lognormal node counts, greedy packing to an edge-token budget.
+                   n_min: int = 32, n_max: int = 1024, r: float = 8.0, cap: int = 16,
+                   count: str = "edges") -> GraphBatch:
+    """Config 2 (masked MAB): lognormal node counts, greedy packing to a token budget.
 
     Graphs are drawn until the next one would push the batch past
-    ``token_budget`` edge tokens; that graph is not included (it would open the
-    next batch).
+    ``token_budget`` tokens; that graph is not included (it would open the
+    next batch).  ``count``: "edges" (edge tokens, edge mode) or "nodes" (node
+    tokens, node mode).
     """
+    if count not in ("edges", "nodes"):
+        raise ValueError("count is 'edges' or 'nodes'")
     rng = np.random.default_rng(seed)
     graphs, total = [], 0
     while True:
         n = int(np.clip(round(rng.lognormal(mu, sigma)), n_min, n_max))
         p = random_walk(rng, n)
-        ne = radius_edges(p, r, cap).shape[1]
+        ne = radius_edges(p, r, cap).shape[1] if count == "edges" else n
         if total + ne > token_budget and graphs:
             break
         graphs.append(p)
         total += ne
         if total >= token_budget:
             break
-    return _assemble(graphs, r, cap, {"generator": "protein_budget", "seed": seed, "budget": token_budget,
-                                      "r": r, "cap": cap})
+    meta = {"generator": "protein_budget", "seed": seed, "budget": token_budget, "r": r, "cap": cap}
+    if count != "edges":
+        meta["count"] = count
+    return _assemble(graphs, r, cap, meta)
 
 
 def block_local_edges(seed: int = 0, num_nodes: int = 1 << 21, num_edges: int = 1 << 25,

@@ -35,7 +35,7 @@ def test_gather_empty(device):
     assert edges.edge_gather(x, e, e).shape == (0, 16)
 
 
-@pytest.mark.parametrize("n,e", [(1, 0), (5, 7), (1000, 20000), (70000, 100000)])
+@pytest.mark.parametrize("n,e", [(1, 0), (5, 7), (1000, 20000), (70000, 100000), (50000, 600000), (300, 1000000)])
 def test_csr_build_matches_stable_sort(device, n, e):
     rng = np.random.default_rng(n + e)
     keys = rng.integers(0, n, size=e).astype(np.int32)

@@ -90,8 +90,9 @@ def test_node_mask_isolated_nodes_and_empty_graph(device, dtype):
 
 @pytest.mark.parametrize("planned", [False, True])
 def test_node_mask_many_segments(device, planned):
-    """300 graphs of 0-6 nodes (a third of them empty): every token finds its segment among more than 64 (the
-    wave-parallel segment search takes two rounds; empty segments share their start with the next one)."""
+    """300 graphs of 0-6 nodes (a third of them empty): every token finds its segment among more than 64
+    (empty segments share their start with the next one), with several tokens of different segments and row
+    lengths in one wave."""
     rng = np.random.default_rng(77)
     sizes = [int(x) for x in rng.integers(0, 7, size=300)]
     sizes[-1] = max(sizes[-1], 1)
