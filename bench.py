@@ -425,7 +425,7 @@ def bench_node(args, sub: bool = False):
     scale = 1.0 / HEAD_DIM ** 0.5
 
     def step():
-        plan = attention.node_plan(ip, ix, t)
+        plan = attention.node_plan(ip, ix, cu)
         out, lse = attention.attn_fwd(q, k, v, cu, cu, 0, 0, scale, adj_indptr=ip, adj_indices=ix, adj_plan=plan)
         attention.attn_bwd(go, q, k, v, out, lse, cu, cu, 0, 0, scale, adj_indptr=ip, adj_indices=ix, adj_plan=plan)
 

@@ -119,16 +119,21 @@ ESA_API int esa_edge_plan_build(const int* tok_src, const int* tok_dst,
 /* Node-mode plan: the per-batch data of the ESA_MASK_NODE mask, i.e. a copy */
 /* of the CSR's indices and the transposed CSR (per key token, the query     */
 /* rows that list it, in ascending position) that the backward's dK / dV    */
-/* pass gathers over.  Built once per batch and read by every attention     */
-/* call over the same adjacency, as the reference builds its [B, 1, N, N]    */
+/* pass gathers over, and per query and key token its partner range and row */
+/* bounds (from cu_seqlens).  Built once per batch and read by every        */
+/* attention call over the same adjacency, as the reference builds its       */
+/* [B, 1, N, N]                                                              */
 /* node bias once per batch (get_adj_mask_from_edge_index_node,             */
 /* esa/masked_layers.py:79-118) for all its layers (:849-936).  The plan's   */
-/* tail is the build's scratch.  It stays valid while indptr / indices are   */
-/* unchanged; calls pass the same indptr as mask_a.                          */
+/* tail is the build's scratch.  It stays valid while indptr / indices and   */
+/* the cu_seqlens are unchanged; calls pass the same indptr as mask_a and    */
+/* the same cu_seqlens.                                                      */
 /* ------------------------------------------------------------------------ */
 ESA_API int esa_node_plan_size(int total_q, int total_k, int n_mask_edges, size_t* bytes);
-ESA_API int esa_node_plan_build(const int* indptr, const int* indices, int total_q, int total_k,
-                        int n_mask_edges, void* plan, size_t plan_bytes, void* stream);
+ESA_API int esa_node_plan_build(const int* indptr, const int* indices,
+                        const int* cu_seqlens_q, const int* cu_seqlens_k, int batch,
+                        int total_q, int total_k, int n_mask_edges,
+                        void* plan, size_t plan_bytes, void* stream);
 
 ESA_API int esa_varlen_attn_workspace_size(int total_q, int total_k, int heads,
                                    int head_dim, int dtype, int mask_kind,

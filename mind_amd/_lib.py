@@ -72,7 +72,7 @@ _PROTOS = {
     "esa_edge_plan_size": (_c_int, [_c_int, _c_int, _c_int, ctypes.POINTER(_c_sz)]),
     "esa_edge_plan_build": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _c_sz, _vp]),
     "esa_node_plan_size": (_c_int, [_c_int, _c_int, _c_int, ctypes.POINTER(_c_sz)]),
-    "esa_node_plan_build": (_c_int, [_vp, _vp, _c_int, _c_int, _c_int, _vp, _c_sz, _vp]),
+    "esa_node_plan_build": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _c_sz, _vp]),
     # counts num_graphs budget | batch_of_graph batch_start num_batches ws bytes stream
     "esa_token_budget_pack": (_c_int, [_vp, _c_int, _c_i64, _vp, _vp, _vp, _vp, _c_sz, _vp]),
     "esa_edge_gather_bwd": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _vp]),

@@ -2053,13 +2053,14 @@ int esa_node_plan_size(int total_q, int total_k, int n_mask_edges, size_t* bytes
   return graph_node_plan_size(total_q, total_k, n_mask_edges, bytes);
 }
 
-int esa_node_plan_build(const int* indptr, const int* indices, int total_q, int total_k, int n_mask_edges,
-                        void* plan, size_t plan_bytes, void* stream) {
-  if (!indptr || !plan || (n_mask_edges > 0 && !indices)) return ESA_ERR_NULL;
-  if (total_q < 0 || total_k < 0 || n_mask_edges < 0) return ESA_ERR_SHAPE;
+int esa_node_plan_build(const int* indptr, const int* indices, const int* cu_seqlens_q, const int* cu_seqlens_k,
+                        int batch, int total_q, int total_k, int n_mask_edges, void* plan, size_t plan_bytes,
+                        void* stream) {
+  if (!indptr || !plan || !cu_seqlens_q || !cu_seqlens_k || (n_mask_edges > 0 && !indices)) return ESA_ERR_NULL;
+  if (batch < 1 || total_q < 0 || total_k < 0 || n_mask_edges < 0) return ESA_ERR_SHAPE;
   if (misaligned(plan)) return ESA_ERR_ALIGN;
-  return graph_node_plan_build(indptr, indices, total_q, total_k, n_mask_edges, plan, plan_bytes,
-                               reinterpret_cast<hipStream_t>(stream));
+  return graph_node_plan_build(indptr, indices, cu_seqlens_q, cu_seqlens_k, batch, total_q, total_k, n_mask_edges,
+                               plan, plan_bytes, reinterpret_cast<hipStream_t>(stream));
 }
 
 int esa_varlen_attn_fwd(const void* q, const void* k, const void* v, const int* cu_seqlens_q,
@@ -2086,7 +2087,8 @@ int esa_varlen_attn_fwd(const void* q, const void* k, const void* v, const int* 
     g.c = softmax_scale * kLog2e; g.scale = softmax_scale;
     g.out = out; g.lse = softmax_lse;
     (void)workspace; (void)workspace_bytes;
-    return graph_attn_fwd(g, dtype, reinterpret_cast<hipStream_t>(stream));
+    return graph_attn_fwd(g, dtype, mask_kind == ESA_MASK_NODE_PLAN ? mask_b : nullptr,
+                          reinterpret_cast<hipStream_t>(stream));
   }
   const bool masked = mask_kind == ESA_MASK_EDGE || mask_kind == ESA_MASK_EDGE_PLAN;
   if (mask_kind == ESA_MASK_EDGE && (!mask_a || !mask_b)) return ESA_ERR_NULL;

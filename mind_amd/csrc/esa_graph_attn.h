@@ -17,16 +17,18 @@ struct GraphAttnArgs {
   void* dq; void* dk; void* dv;                     // backward outputs
   float* dsum;                                      // backward workspace: D_i per head
   const int* t_indptr; const int* t_rows;           // transposed CSR: per key, the query rows listing it
+  const int4* q_desc; const int4* k_desc;           // per-token {lo, hi, pa, pb} from a node plan, or null
 };
 
 // planned: the transposed CSR comes from a node plan (mask_b of
 // ESA_MASK_NODE_PLAN) instead of being built in the workspace.
 int graph_attn_workspace_size(int total_q, int total_k, int heads, int nnz, bool backward, bool planned,
                               size_t* bytes);
-int graph_attn_fwd(GraphAttnArgs a, int dtype, hipStream_t st);
+// plan: null, or a node plan whose query descriptors the forward reads.
+int graph_attn_fwd(GraphAttnArgs a, int dtype, const void* plan, hipStream_t st);
 // plan: null, or a node plan whose transposed CSR the backward reads.
 int graph_attn_bwd(GraphAttnArgs a, int dtype, const void* plan, void* workspace, size_t workspace_bytes,
                    hipStream_t st);
 int graph_node_plan_size(int total_q, int total_k, int nnz, size_t* bytes);
-int graph_node_plan_build(const int* indptr, const int* indices, int total_q, int total_k, int nnz, void* plan,
-                          size_t plan_bytes, hipStream_t st);
+int graph_node_plan_build(const int* indptr, const int* indices, const int* cu_q, const int* cu_k, int nseg,
+                          int total_q, int total_k, int nnz, void* plan, size_t plan_bytes, hipStream_t st);

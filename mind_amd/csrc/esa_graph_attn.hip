@@ -83,32 +83,52 @@ DEVI int wave_seg_of(const int* __restrict__ cu, int nseg, int t) {
   return base;
 }
 
-// This wave's token (one wave per token, four waves per block).  Hardware
-// block b runs on XCD b % 8; blocks are dealt so that each XCD takes one
-// contiguous range of tokens, whose partners (mostly nearby tokens of the same
-// graph) are then read into that XCD's L2 only.
-DEVI int wave_token() {
-  const int nb = gridDim.x, q = nb >> 3, rem = nb & 7, x = blockIdx.x & 7, s = blockIdx.x >> 3;
-  const int b = x * q + min(x, rem) + s;
-  return b * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-}
-
 // Row [pa, pb) of a CSR clamped into [0, nnz).
 DEVI void csr_row(const int* __restrict__ indptr, int t, int nnz, int& pa, int& pb) {
   pa = min(max(indptr[t], 0), nnz);
   pb = min(max(indptr[t + 1], pa), nnz);
 }
 
+// Token descriptor {lo, hi, pa, pb}: the partner range [lo, hi) of token t
+// (segment sg by cu_own, range by cu_other) and its CSR row [pa, pb), emptied
+// when the range is.  A node plan stores them: one 16-byte load per token
+// instead of the segment search, the range and the row bounds (forward, dQ
+// and dK / dV 7-11 % faster); without a plan they are computed here.
+DEVI int4 make_desc(const int* __restrict__ cu_other, int total_other, const int* __restrict__ indptr, int nnz,
+                    int sg, int t) {
+  const int lo = max(cu_other[sg], 0), hi = min(cu_other[sg + 1], total_other);
+  int pa, pb;
+  csr_row(indptr, t, nnz, pa, pb);
+  return make_int4(lo, hi, pa, hi > lo ? pb : pa);
+}
+DEVI int4 token_desc(const int4* __restrict__ plan_desc, const int* __restrict__ cu_own,
+                     const int* __restrict__ cu_other, int nseg, int total_other, const int* __restrict__ indptr,
+                     int nnz, int t) {
+  if (plan_desc) return plan_desc[t];
+  return make_desc(cu_other, total_other, indptr, nnz, wave_seg_of(cu_own, nseg, t), t);
+}
+
+// This wave's token (one wave per token, four waves per block; more tokens per
+// wave, each wave walking a run of them with the next token's descriptor in
+// flight, measured slower: a fresh wave per token keeps every slot busy).
+// Hardware block b runs on XCD b % 8; blocks are dealt so that each XCD takes
+// one contiguous range of tokens, whose partners (mostly nearby tokens of the
+// same graph) are then read into that XCD's L2.
+DEVI int wave_token() {
+  const int nb = gridDim.x, q = nb >> 3, rem = nb & 7, x = blockIdx.x & 7, s = blockIdx.x >> 3;
+  const int b = x * q + min(x, rem) + s;
+  return b * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+}
+
 // kGU entries of a CSR row starting at position p: partner token, and whether
 // it counts (inside the row, inside [lo, hi), not a repeat of the previous
 // entry).  `prev` carries the last partner across steps.
-DEVI void next_entries(const int* __restrict__ list, const int* __restrict__ map, int p, int pb, int lo, int hi,
-                       int& prev, int j[kGU], bool ok[kGU]) {
+DEVI void next_entries(const int* __restrict__ list, int p, int pb, int lo, int hi, int& prev, int j[kGU],
+                       bool ok[kGU]) {
 #pragma unroll
   for (int u = 0; u < kGU; ++u) {
     const int pp = min(p + u, pb - 1);
-    const int e = list[pp];
-    const int x = map ? map[e] : e;
+    const int x = list[pp];
     ok[u] = p + u < pb && x >= lo && x < hi && x != prev;
     if (p + u < pb) prev = x;
     j[u] = ok[u] ? x : lo;
@@ -116,18 +136,12 @@ DEVI void next_entries(const int* __restrict__ list, const int* __restrict__ map
 }
 
 template <typename T>
-__global__ __launch_bounds__(256) void graph_attn_fwd_kernel(const GraphAttnArgs a) {
+DEVI void fwd_token(const GraphAttnArgs& a, int t, int4 d) {
   const T* __restrict__ q = static_cast<const T*>(a.q);
   const T* __restrict__ k = static_cast<const T*>(a.k);
   const T* __restrict__ v = static_cast<const T*>(a.v);
-  const int t = wave_token();
-  if (t >= a.total_q) return;
   const int lane = threadIdx.x & 63, H = a.heads, d0 = 4 * (lane & 3);
-  const int sg = wave_seg_of(a.cu_q, a.nseg, t);
-  const int lo = max(a.cu_k[sg], 0), hi = min(a.cu_k[sg + 1], a.total_k);
-  int pa, pb;
-  csr_row(a.indptr, t, a.nnz, pa, pb);
-  if (hi <= lo) pb = pa;
+  const int lo = d.x, hi = d.y, pa = d.z, pb = d.w;
   for (int h0 = 0; h0 < H; h0 += 16) {
     const int h = h0 + (lane >> 2);
     const int hc = min(h, H - 1);
@@ -138,7 +152,7 @@ __global__ __launch_bounds__(256) void graph_attn_fwd_kernel(const GraphAttnArgs
     for (int p = pa; p < pb; p += kGU) {
       int j[kGU];
       bool ok[kGU];
-      next_entries(a.indices, nullptr, p, pb, lo, hi, prev, j, ok);
+      next_entries(a.indices, p, pb, lo, hi, prev, j, ok);
       float kr[kGU][4], vr[kGU][4];
 #pragma unroll
       for (int u = 0; u < kGU; ++u) {
@@ -176,20 +190,14 @@ __global__ __launch_bounds__(256) void graph_attn_fwd_kernel(const GraphAttnArgs
 // dQ_i = scale * sum_j P_ij (dP_ij - D_i) k_j over row i; also writes
 // D_i = rowsum(dO_i * O_i) per head for the dK / dV pass.
 template <typename T>
-__global__ __launch_bounds__(256) void graph_attn_dq_kernel(const GraphAttnArgs a) {
+DEVI void dq_token(const GraphAttnArgs& a, int t, int4 d) {
   const T* __restrict__ q = static_cast<const T*>(a.q);
   const T* __restrict__ k = static_cast<const T*>(a.k);
   const T* __restrict__ v = static_cast<const T*>(a.v);
   const T* __restrict__ o = static_cast<const T*>(a.out_in);
   const T* __restrict__ g = static_cast<const T*>(a.dout);
-  const int t = wave_token();
-  if (t >= a.total_q) return;
   const int lane = threadIdx.x & 63, H = a.heads, d0 = 4 * (lane & 3);
-  const int sg = wave_seg_of(a.cu_q, a.nseg, t);
-  const int lo = max(a.cu_k[sg], 0), hi = min(a.cu_k[sg + 1], a.total_k);
-  int pa, pb;
-  csr_row(a.indptr, t, a.nnz, pa, pb);
-  if (hi <= lo) pb = pa;
+  const int lo = d.x, hi = d.y, pa = d.z, pb = d.w;
   for (int h0 = 0; h0 < H; h0 += 16) {
     const int h = h0 + (lane >> 2);
     const int hc = min(h, H - 1);
@@ -206,7 +214,7 @@ __global__ __launch_bounds__(256) void graph_attn_dq_kernel(const GraphAttnArgs 
     for (int p = pa; p < pb; p += kGU) {
       int j[kGU];
       bool ok[kGU];
-      next_entries(a.indices, nullptr, p, pb, lo, hi, prev, j, ok);
+      next_entries(a.indices, p, pb, lo, hi, prev, j, ok);
       float kr[kGU][4], vr[kGU][4];
 #pragma unroll
       for (int u = 0; u < kGU; ++u) {
@@ -228,17 +236,13 @@ __global__ __launch_bounds__(256) void graph_attn_dq_kernel(const GraphAttnArgs 
 // dV_j = sum_i P_ij dO_i, dK_j = scale * sum_i P_ij (dP_ij - D_i) q_i over the
 // queries i whose rows list key j (t_rows[t_indptr[j] ..], ascending position).
 template <typename T>
-__global__ __launch_bounds__(256) void graph_attn_dkdv_kernel(const GraphAttnArgs a) {
+DEVI void dkdv_token(const GraphAttnArgs& a, int t, int4 d) {
   const T* __restrict__ q = static_cast<const T*>(a.q);
   const T* __restrict__ k = static_cast<const T*>(a.k);
   const T* __restrict__ v = static_cast<const T*>(a.v);
   const T* __restrict__ g = static_cast<const T*>(a.dout);
-  const int t = wave_token();
-  if (t >= a.total_k) return;
   const int lane = threadIdx.x & 63, H = a.heads, d0 = 4 * (lane & 3);
-  const int sg = wave_seg_of(a.cu_k, a.nseg, t);
-  const int lo = max(a.cu_q[sg], 0), hi = min(a.cu_q[sg + 1], a.total_q);
-  const int pa = a.t_indptr[t], pb = hi > lo ? a.t_indptr[t + 1] : pa;
+  const int lo = d.x, hi = d.y, pa = d.z, pb = d.w;
   for (int h0 = 0; h0 < H; h0 += 16) {
     const int h = h0 + (lane >> 2);
     const int hc = min(h, H - 1);
@@ -250,7 +254,7 @@ __global__ __launch_bounds__(256) void graph_attn_dkdv_kernel(const GraphAttnArg
     for (int p = pa; p < pb; p += kGU) {
       int i[kGU];
       bool ok[kGU];
-      next_entries(a.t_rows, nullptr, p, pb, lo, hi, prev, i, ok);
+      next_entries(a.t_rows, p, pb, lo, hi, prev, i, ok);
       float qr[kGU][4], gr[kGU][4], l2[kGU], ds_[kGU];
 #pragma unroll
       for (int u = 0; u < kGU; ++u) {
@@ -276,6 +280,36 @@ __global__ __launch_bounds__(256) void graph_attn_dkdv_kernel(const GraphAttnArg
       store4<T>(static_cast<T*>(a.dv) + ((size_t)t * H + h) * kHd16 + d0, dv, 1.f);
     }
   }
+}
+
+// The three kernels; the key pass (dK / dV) walks key tokens over the
+// transposed CSR.
+template <typename T>
+__global__ __launch_bounds__(256) void graph_attn_fwd_kernel(const GraphAttnArgs a) {
+  const int t = wave_token();
+  if (t >= a.total_q) return;
+  fwd_token<T>(a, t, token_desc(a.q_desc, a.cu_q, a.cu_k, a.nseg, a.total_k, a.indptr, a.nnz, t));
+}
+template <typename T>
+__global__ __launch_bounds__(256) void graph_attn_dq_kernel(const GraphAttnArgs a) {
+  const int t = wave_token();
+  if (t >= a.total_q) return;
+  dq_token<T>(a, t, token_desc(a.q_desc, a.cu_q, a.cu_k, a.nseg, a.total_k, a.indptr, a.nnz, t));
+}
+template <typename T>
+__global__ __launch_bounds__(256) void graph_attn_dkdv_kernel(const GraphAttnArgs a) {
+  const int t = wave_token();
+  if (t >= a.total_k) return;
+  dkdv_token<T>(a, t, token_desc(a.k_desc, a.cu_k, a.cu_q, a.nseg, a.total_q, a.t_indptr, a.nnz, t));
+}
+
+// Descriptors of tokens [0, n) for a node plan (one thread per token).
+__global__ void desc_kernel(const int* __restrict__ cu_own, const int* __restrict__ cu_other, int nseg,
+                            int total_other, const int* __restrict__ indptr, int nnz, int n,
+                            int4* __restrict__ desc) {
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= n) return;
+  desc[t] = make_desc(cu_other, total_other, indptr, nnz, seg_of(cu_own, nseg, t), t);
 }
 
 // row_of[e] = the CSR row holding entry e (-1 for an entry no row covers).
@@ -304,12 +338,13 @@ size_t al256(size_t x) { return (x + 255) & ~size_t(255); }
 
 // Node plan (mask_b of ESA_MASK_NODE_PLAN): the CSR's indices [nnz] first (so
 // the plan reads as the indices array), the transposed CSR t_indptr
-// [total_k + 1] and t_rows [nnz], then the build's scratch (row_of, t_perm
-// and the CSR sort's workspace).  The per-call backward lays the same
-// transposed CSR and scratch out in its workspace.
-struct NodePlan { size_t indices, t_indptr, t_rows, row_of, t_perm, csr, csr_bytes, total; };
+// [total_k + 1] and t_rows [nnz], the token descriptors of the queries
+// (q_desc [total_q]) and keys (k_desc [total_k]), then the build's scratch
+// (row_of, t_perm and the CSR sort's workspace).  The per-call backward lays
+// the same arrays and scratch out in its workspace.
+struct NodePlan { size_t indices, t_indptr, t_rows, q_desc, k_desc, row_of, t_perm, csr, csr_bytes, total; };
 
-int node_plan_layout(int total_k, int nnz, NodePlan& w) {
+int node_plan_layout(int total_q, int total_k, int nnz, NodePlan& w) {
   w = NodePlan{};
   const int rc = esa_csr_workspace_size(nnz, total_k, &w.csr_bytes);
   if (rc) return rc;
@@ -317,6 +352,8 @@ int node_plan_layout(int total_k, int nnz, NodePlan& w) {
   w.indices = off; off += al256((size_t)nnz * 4 + 4);
   w.t_indptr = off; off += al256(((size_t)total_k + 1) * 4);
   w.t_rows = off; off += al256((size_t)nnz * 4 + 4);
+  w.q_desc = off; off += al256((size_t)total_q * 16 + 16);
+  w.k_desc = off; off += al256((size_t)total_k * 16 + 16);
   w.row_of = off; off += al256((size_t)nnz * 4 + 4);
   w.t_perm = off; off += al256((size_t)nnz * 4 + 4);
   w.csr = off; off += al256(w.csr_bytes);
@@ -326,10 +363,12 @@ int node_plan_layout(int total_k, int nnz, NodePlan& w) {
 
 unsigned grid_of(long n) { const long b = (n + 255) / 256; return (unsigned)(b < 1 ? 1 : b < 4096 ? b : 4096); }
 
-// The transposed CSR of (indptr, indices) into base's NodePlan layout;
-// copy_indices: also the plan's copy of the indices.
-int build_transposed(const int* indptr, const int* indices, int total_q, int total_k, int nnz, char* base,
-                     const NodePlan& w, bool copy_indices, hipStream_t st) {
+// The transposed CSR of (indptr, indices) and both sides' token descriptors
+// into base's NodePlan layout; copy_indices: also the plan's copy of the
+// indices.
+int build_transposed(const int* indptr, const int* indices, const int* cu_q, const int* cu_k, int nseg,
+                     int total_q, int total_k, int nnz, char* base, const NodePlan& w, bool copy_indices,
+                     hipStream_t st) {
   int* row_of = reinterpret_cast<int*>(base + w.row_of);
   int* t_perm = reinterpret_cast<int*>(base + w.t_perm);
   int* t_indptr = reinterpret_cast<int*>(base + w.t_indptr);
@@ -350,6 +389,16 @@ int build_transposed(const int* indptr, const int* indices, int total_q, int tot
                        indices, copy_indices ? reinterpret_cast<int*>(base + w.indices) : nullptr);
     ESA_LAUNCH_CHECK();
   }
+  if (total_q > 0) {
+    hipLaunchKernelGGL(desc_kernel, dim3((unsigned)((total_q + 255) / 256)), dim3(256), 0, st, cu_q, cu_k, nseg,
+                       total_k, indptr, nnz, total_q, reinterpret_cast<int4*>(base + w.q_desc));
+    ESA_LAUNCH_CHECK();
+  }
+  if (total_k > 0) {
+    hipLaunchKernelGGL(desc_kernel, dim3((unsigned)((total_k + 255) / 256)), dim3(256), 0, st, cu_k, cu_q, nseg,
+                       total_q, t_indptr, nnz, total_k, reinterpret_cast<int4*>(base + w.k_desc));
+    ESA_LAUNCH_CHECK();
+  }
   return ESA_OK;
 }
 
@@ -362,7 +411,7 @@ int graph_ws(int total_q, int total_k, int heads, int nnz, bool backward, bool p
   w.dsum = off; off += al256((size_t)heads * total_q * 4);
   if (!planned) {
     NodePlan np;
-    const int rc = node_plan_layout(total_k, nnz, np);
+    const int rc = node_plan_layout(total_q, total_k, nnz, np);
     if (rc) return rc;
     w.plan = off; off += np.total;
   }
@@ -384,25 +433,32 @@ int graph_attn_workspace_size(int total_q, int total_k, int heads, int nnz, bool
 }
 
 int graph_node_plan_size(int total_q, int total_k, int nnz, size_t* bytes) {
-  (void)total_q;
   NodePlan w;
-  const int rc = node_plan_layout(total_k, nnz, w);
+  const int rc = node_plan_layout(total_q, total_k, nnz, w);
   if (rc) return rc;
   *bytes = w.total;
   return ESA_OK;
 }
 
-int graph_node_plan_build(const int* indptr, const int* indices, int total_q, int total_k, int nnz, void* plan,
-                          size_t plan_bytes, hipStream_t st) {
+int graph_node_plan_build(const int* indptr, const int* indices, const int* cu_q, const int* cu_k, int nseg,
+                          int total_q, int total_k, int nnz, void* plan, size_t plan_bytes, hipStream_t st) {
   NodePlan w;
-  int rc = node_plan_layout(total_k, nnz, w);
+  int rc = node_plan_layout(total_q, total_k, nnz, w);
   if (rc) return rc;
   if (plan_bytes < w.total) return ESA_ERR_WORKSPACE;
-  return build_transposed(indptr, indices, total_q, total_k, nnz, static_cast<char*>(plan), w, true, st);
+  return build_transposed(indptr, indices, cu_q, cu_k, nseg, total_q, total_k, nnz, static_cast<char*>(plan), w,
+                          true, st);
 }
 
-int graph_attn_fwd(GraphAttnArgs a, int dtype, hipStream_t st) {
+int graph_attn_fwd(GraphAttnArgs a, int dtype, const void* plan, hipStream_t st) {
   if (a.total_q == 0) return ESA_OK;
+  a.q_desc = nullptr;
+  if (plan) {
+    NodePlan np;
+    const int rc = node_plan_layout(a.total_q, a.total_k, a.nnz, np);
+    if (rc) return rc;
+    a.q_desc = reinterpret_cast<const int4*>(static_cast<const char*>(plan) + np.q_desc);
+  }
   const dim3 grid(token_blocks(a.total_q)), block(256);
   if (dtype == ESA_F32)
     ESA_TIMED(esa_profile::kGraphFwd, st, hipLaunchKernelGGL(graph_attn_fwd_kernel<float>, grid, block, 0, st, a));
@@ -421,17 +477,20 @@ int graph_attn_bwd(GraphAttnArgs a, int dtype, const void* plan, void* workspace
   char* ws = static_cast<char*>(workspace);
   a.dsum = reinterpret_cast<float*>(ws + w.dsum);
   NodePlan np;
-  if ((rc = node_plan_layout(a.total_k, a.nnz, np))) return rc;
+  if ((rc = node_plan_layout(a.total_q, a.total_k, a.nnz, np))) return rc;
   const char* tbase;
   if (plan) {
     tbase = static_cast<const char*>(plan);
   } else {
-    if ((rc = build_transposed(a.indptr, a.indices, a.total_q, a.total_k, a.nnz, ws + w.plan, np, false, st)))
+    if ((rc = build_transposed(a.indptr, a.indices, a.cu_q, a.cu_k, a.nseg, a.total_q, a.total_k, a.nnz,
+                               ws + w.plan, np, false, st)))
       return rc;
     tbase = ws + w.plan;
   }
   a.t_indptr = reinterpret_cast<const int*>(tbase + np.t_indptr);
   a.t_rows = reinterpret_cast<const int*>(tbase + np.t_rows);
+  a.q_desc = reinterpret_cast<const int4*>(tbase + np.q_desc);
+  a.k_desc = reinterpret_cast<const int4*>(tbase + np.k_desc);
   const dim3 block(256);
   if (a.total_q > 0) {
     if (dtype == ESA_F32)

@@ -87,23 +87,30 @@ def edge_plan(edge_src, edge_dst, cu_seqlens_q, cu_seqlens_k=None) -> torch.Tens
     return plan
 
 
-def node_plan(adj_indptr, adj_indices, total_k: int) -> torch.Tensor:
+def node_plan(adj_indptr, adj_indices, cu_seqlens_q, cu_seqlens_k=None, total_k: int | None = None) -> torch.Tensor:
     """The node-mode plan of a batch (esa_node_plan_build): a uint8 device tensor holding a copy of the CSR's
-    indices and its transpose (per key token, the query rows that list it), over ``total_k`` key tokens.
-    Built once per batch and passed as ``adj_plan=`` (with the same ``adj_indptr`` / ``adj_indices``) to
-    every attention call over that adjacency, so the backward does not rebuild the transpose per call, as
-    the reference builds its node bias once per batch (get_adj_mask_from_edge_index_node,
-    esa/masked_layers.py:79-118) for all layers."""
-    _lib.require_gpu(adj_indptr, adj_indices)
+    indices, its transpose (per key token, the query rows that list it) and per query and key token its
+    partner range and row bounds over the segments ``cu_seqlens_q`` / ``cu_seqlens_k`` (``cu_seqlens_k``
+    defaults to the same tensor, ``total_k`` to the number of queries: self-attention).  Built once per batch
+    and passed as ``adj_plan=`` (with the same ``adj_indptr`` / ``adj_indices`` and cu_seqlens) to every
+    attention call over that adjacency, so no call rebuilds it, as the reference builds its node bias once per
+    batch (get_adj_mask_from_edge_index_node, esa/masked_layers.py:79-118) for all layers."""
+    cu_k = cu_seqlens_q if cu_seqlens_k is None else cu_seqlens_k
+    _lib.require_gpu(adj_indptr, adj_indices, cu_seqlens_q, cu_k)
     _check_index("adj_indptr", adj_indptr)
     _check_index("adj_indices", adj_indices)
+    _check_index("cu_seqlens_q", cu_seqlens_q)
+    batch = cu_seqlens_q.numel() - 1
+    _check_index("cu_seqlens_k", cu_k, batch + 1)
     tq, nnz = adj_indptr.numel() - 1, adj_indices.numel()
+    tk = tq if total_k is None else int(total_k)
     lib = _lib.load()
     n = _lib.ctypes.c_size_t(0)
-    _lib.check(lib.esa_node_plan_size(tq, int(total_k), nnz, _lib.ctypes.byref(n)), "esa_node_plan_size")
+    _lib.check(lib.esa_node_plan_size(tq, tk, nnz, _lib.ctypes.byref(n)), "esa_node_plan_size")
     plan = torch.empty(max(int(n.value), 256), dtype=torch.uint8, device=adj_indptr.device)
-    rc = lib.esa_node_plan_build(adj_indptr.data_ptr(), adj_indices.data_ptr(), tq, int(total_k), nnz,
-                                 plan.data_ptr(), plan.numel(), _lib.stream_of(adj_indptr))
+    rc = lib.esa_node_plan_build(adj_indptr.data_ptr(), adj_indices.data_ptr(), cu_seqlens_q.data_ptr(),
+                                 cu_k.data_ptr(), batch, tq, tk, nnz, plan.data_ptr(), plan.numel(),
+                                 _lib.stream_of(adj_indptr))
     _lib.check(rc, "esa_node_plan_build")
     return plan
 

@@ -220,7 +220,7 @@ class NodeAdjacency(PackedSets):
         (esa/masked_layers.py:849-936)."""
         if self._plan is None:
             from .attention import node_plan
-            self._plan = node_plan(self.indptr, self.indices, self.indptr.numel() - 1)
+            self._plan = node_plan(self.indptr, self.indices, self.cu_seqlens)
         return self._plan
 
     def kernel_mask(self, padded: bool) -> dict:

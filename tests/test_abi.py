@@ -82,4 +82,4 @@ def test_argument_errors_need_no_gpu():
     assert lib.esa_varlen_attn_workspace_size(100, 100, 16, 16, bf16, node, 500, 1, ctypes.byref(n)) == 0
     assert lib.esa_varlen_attn_workspace_size(100, 100, 16, 16, bf16, node_plan, 500, 1, ctypes.byref(m)) == 0
     assert 0 < m.value < n.value
-    assert lib.esa_node_plan_build(None, None, 100, 100, 0, 256, 1 << 20, None) == -1
+    assert lib.esa_node_plan_build(None, None, None, None, 1, 100, 100, 0, 256, 1 << 20, None) == -1

@@ -232,7 +232,7 @@ def test_node_plan_entries_outside_segment(device):
     rows = [[1, 2, 5], [0], [0, 1], [4, 6], [1, 3], [6], [3, 5]]
     ip = torch.tensor(np.cumsum([0] + [len(r) for r in rows]), dtype=torch.int32, device=device)
     ix = torch.tensor([j for r in rows for j in r], dtype=torch.int32, device=device)
-    plan = A.node_plan(ip, ix, 7)
+    plan = A.node_plan(ip, ix, cu)
     q, k, v, g = (seeded_normal((7, 3, D), 500 + i, torch.float32).to(device) for i in range(4))
     out0, lse0 = A.attn_fwd(q, k, v, cu, cu, 0, 0, 0.25, adj_indptr=ip, adj_indices=ix)
     out, lse = A.attn_fwd(q, k, v, cu, cu, 0, 0, 0.25, adj_indptr=ip, adj_indices=ix, adj_plan=plan)
