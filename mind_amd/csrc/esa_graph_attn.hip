@@ -25,7 +25,8 @@
 
 namespace {
 
-constexpr int kGU = 4;   // CSR entries per step: their K / V (or Q / dO) rows are loaded together
+constexpr int kGU = 2;   // CSR entries per step: their K / V (or Q / dO) rows are loaded together (two
+                         // per step keeps every kernel at 8 waves per SIMD; 1, 4 and 8 measured slower)
 
 template <typename T> struct Row4;
 template <> struct Row4<float> { typedef f32x4 type; };
