@@ -304,34 +304,36 @@ __global__ __launch_bounds__(256) void graph_attn_dkdv_kernel(const GraphAttnArg
   dkdv_token<T>(a, t, token_desc(a.k_desc, a.cu_k, a.cu_q, a.nseg, a.total_q, a.t_indptr, a.nnz, t));
 }
 
-// Descriptors of tokens [0, n) for a node plan (one thread per token).
-__global__ void desc_kernel(const int* __restrict__ cu_own, const int* __restrict__ cu_other, int nseg,
-                            int total_other, const int* __restrict__ indptr, int nnz, int n,
-                            int4* __restrict__ desc) {
-  const int t = blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= n) return;
-  desc[t] = make_desc(cu_other, total_other, indptr, nnz, seg_of(cu_own, nseg, t), t);
-}
-
 // row_of[e] = the CSR row holding entry e (-1 for an entry no row covers).
 __global__ void fill_minus_one_kernel(int* __restrict__ p, long n) {
   for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) p[i] = -1;
 }
-__global__ void row_of_kernel(const int* __restrict__ indptr, int rows, int nnz, int* __restrict__ row_of) {
+// Per query token t: row_of over its row, and its descriptor.
+__global__ void query_rows_kernel(const int* __restrict__ indptr, const int* __restrict__ cu_q,
+                                  const int* __restrict__ cu_k, int nseg, int total_q, int total_k, int nnz,
+                                  int* __restrict__ row_of, int4* __restrict__ q_desc) {
   const int t = blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= rows) return;
+  if (t >= total_q) return;
   int pa, pb;
   csr_row(indptr, t, nnz, pa, pb);
   for (int p = pa; p < pb; ++p) row_of[p] = t;
+  q_desc[t] = make_desc(cu_k, total_k, indptr, nnz, seg_of(cu_q, nseg, t), t);
 }
-// t_rows[p] = row_of[t_perm[p]]: the query row of each transposed entry; and
-// the plan's copy of the indices.
-__global__ void transpose_rows_kernel(const int* __restrict__ t_perm, const int* __restrict__ row_of, int nnz,
-                                      int* __restrict__ t_rows, const int* __restrict__ indices,
-                                      int* __restrict__ indices_copy) {
-  for (long p = (long)blockIdx.x * blockDim.x + threadIdx.x; p < nnz; p += (long)gridDim.x * blockDim.x) {
-    t_rows[p] = row_of[t_perm[p]];
-    if (indices_copy) indices_copy[p] = indices[p];
+// Per entry p: t_rows[p] = row_of[t_perm[p]], the query row of each
+// transposed entry, and the plan's copy of the indices; per key token t (the
+// first total_k threads): its descriptor over the transposed CSR.
+__global__ void key_rows_kernel(const int* __restrict__ t_perm, const int* __restrict__ row_of, int nnz,
+                                int* __restrict__ t_rows, const int* __restrict__ indices,
+                                int* __restrict__ indices_copy, const int* __restrict__ t_indptr,
+                                const int* __restrict__ cu_q, const int* __restrict__ cu_k, int nseg, int total_q,
+                                int total_k, int4* __restrict__ k_desc) {
+  for (long p = (long)blockIdx.x * blockDim.x + threadIdx.x; p < max(nnz, total_k);
+       p += (long)gridDim.x * blockDim.x) {
+    if (p < nnz) {
+      t_rows[p] = row_of[t_perm[p]];
+      if (indices_copy) indices_copy[p] = indices[p];
+    }
+    if (p < total_k) k_desc[p] = make_desc(cu_q, total_q, t_indptr, nnz, seg_of(cu_k, nseg, (int)p), (int)p);
   }
 }
 
@@ -373,31 +375,22 @@ int build_transposed(const int* indptr, const int* indices, const int* cu_q, con
   int* row_of = reinterpret_cast<int*>(base + w.row_of);
   int* t_perm = reinterpret_cast<int*>(base + w.t_perm);
   int* t_indptr = reinterpret_cast<int*>(base + w.t_indptr);
-  int* t_rows = reinterpret_cast<int*>(base + w.t_rows);
   if (nnz > 0) {
     hipLaunchKernelGGL(fill_minus_one_kernel, dim3(grid_of(nnz)), dim3(256), 0, st, row_of, (long)nnz);
     ESA_LAUNCH_CHECK();
-    if (total_q > 0) {
-      hipLaunchKernelGGL(row_of_kernel, dim3((unsigned)((total_q + 255) / 256)), dim3(256), 0, st, indptr, total_q,
-                         nnz, row_of);
-      ESA_LAUNCH_CHECK();
-    }
+  }
+  if (total_q > 0) {
+    hipLaunchKernelGGL(query_rows_kernel, dim3((unsigned)((total_q + 255) / 256)), dim3(256), 0, st, indptr, cu_q,
+                       cu_k, nseg, total_q, total_k, nnz, row_of, reinterpret_cast<int4*>(base + w.q_desc));
+    ESA_LAUNCH_CHECK();
   }
   int rc = esa_csr_build(indices, nnz, total_k, t_indptr, t_perm, base + w.csr, w.csr_bytes, st);
   if (rc) return rc;
-  if (nnz > 0) {
-    hipLaunchKernelGGL(transpose_rows_kernel, dim3(grid_of(nnz)), dim3(256), 0, st, t_perm, row_of, nnz, t_rows,
-                       indices, copy_indices ? reinterpret_cast<int*>(base + w.indices) : nullptr);
-    ESA_LAUNCH_CHECK();
-  }
-  if (total_q > 0) {
-    hipLaunchKernelGGL(desc_kernel, dim3((unsigned)((total_q + 255) / 256)), dim3(256), 0, st, cu_q, cu_k, nseg,
-                       total_k, indptr, nnz, total_q, reinterpret_cast<int4*>(base + w.q_desc));
-    ESA_LAUNCH_CHECK();
-  }
-  if (total_k > 0) {
-    hipLaunchKernelGGL(desc_kernel, dim3((unsigned)((total_k + 255) / 256)), dim3(256), 0, st, cu_k, cu_q, nseg,
-                       total_q, t_indptr, nnz, total_k, reinterpret_cast<int4*>(base + w.k_desc));
+  if (nnz > 0 || total_k > 0) {
+    hipLaunchKernelGGL(key_rows_kernel, dim3(grid_of(nnz > total_k ? nnz : total_k)), dim3(256), 0, st, t_perm,
+                       row_of, nnz, reinterpret_cast<int*>(base + w.t_rows), indices,
+                       copy_indices ? reinterpret_cast<int*>(base + w.indices) : nullptr, t_indptr, cu_q, cu_k,
+                       nseg, total_q, total_k, reinterpret_cast<int4*>(base + w.k_desc));
     ESA_LAUNCH_CHECK();
   }
   return ESA_OK;
