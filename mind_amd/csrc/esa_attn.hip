@@ -1004,18 +1004,6 @@ static_assert(kListCap >= 128, "list_tile reads the first 128 ids");
 #endif
 constexpr int kListHeads = ESA_LIST_HEADS;       // heads per wave of the forward and dQ list kernels
 constexpr int kListHeadsKv = ESA_LIST_HEADS_KV;  // heads per wave of the dK/dV list kernel
-#ifndef ESA_LIST_WAVES
-#define ESA_LIST_WAVES 3
-#endif
-#ifndef ESA_LIST_VGPRS
-#define ESA_LIST_VGPRS 128
-#endif
-#ifndef ESA_LIST_WAVES_DQ
-#define ESA_LIST_WAVES_DQ 3
-#endif
-#ifndef ESA_LIST_WAVES_DKDV
-#define ESA_LIST_WAVES_DKDV 2
-#endif
 
 template <int NH>
 struct StageList { i32x4 k[NH], v[NH]; uint32_t w; };
