@@ -978,22 +978,6 @@ DEVI int list_item(int n_items) {
   return i < n_items ? i : -1;
 }
 
-// The wave's outer tile of a list kernel: its number of compact tiles (-1:
-// the group is left to the walk kernels) and its ids, copied to LDS.  The
-// first 128 ids are read together with the count (entries past the count
-// are read but never used).
-DEVI int list_tile(const AttnArgs& a, int tile, int* sid, int lane) {
-  const int* ids = a.ids + (size_t)tile * kListCap;
-  const int pre0 = ids[lane], pre1 = ids[lane + 64];
-  const int n = a.info[tile];
-  if (n < 0) return -1;
-  const int nct = (n + kTile - 1) / kTile;
-  sid[lane] = pre0;
-  sid[lane + 64] = pre1;
-  for (int i = 128 + lane; i < nct * kTile; i += 64) sid[i] = ids[i];
-  wave_sync();
-  return nct;
-}
 static_assert(kListCap >= 128, "list_tile reads the first 128 ids");
 
 #ifndef ESA_LIST_HEADS
@@ -1887,12 +1871,6 @@ int launch_prep(PrepArgs& p, unsigned tasks, hipStream_t st) {
             hipLaunchKernelGGL(prep_kernel, dim3((unsigned)grid), dim3(256), 0, st, p));
   ESA_LAUNCH_CHECK();
   return ESA_OK;
-}
-
-// Blocks of a list kernel: groups x head groups, rounded up to whole XCD rounds.
-unsigned list_blocks(int total, unsigned n_hg) {
-  const unsigned n = (unsigned)groups_of(total) * n_hg;
-  return (n + kXcds - 1) / kXcds * kXcds;
 }
 
 // Blocks of a one-wave-per-block list kernel: 32-token tiles x head ranges,

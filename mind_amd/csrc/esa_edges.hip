@@ -134,12 +134,7 @@ __global__ void edge_gather_scalar_kernel(const T* __restrict__ x, const int* __
 // a contiguous edge range (XCD-contiguous, as the row gather).
 
 template <typename T>
-DEVI float4 chunk_f32(u32x4 v, int k);   // elements 4k..4k+3 of a 16-byte chunk as fp32
-template <>
-DEVI float4 chunk_f32<float>(u32x4 v, int k) {
-  (void)k;
-  return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
-}
+DEVI float4 chunk_f32(u32x4 v, int k);   // elements 4k..4k+3 of a 16-byte bf16 chunk as fp32
 template <>
 DEVI float4 chunk_f32<bf16>(u32x4 v, int k) {
   const uint32_t lo = k == 0 ? v.x : v.z, hi = k == 0 ? v.y : v.w;
