@@ -91,10 +91,13 @@ def node_plan(adj_indptr, adj_indices, cu_seqlens_q, cu_seqlens_k=None, total_k:
     """The node-mode plan of a batch (esa_node_plan_build): a uint8 device tensor holding a copy of the CSR's
     indices, its transpose (per key token, the query rows that list it) and per query and key token its
     partner range and row bounds over the segments ``cu_seqlens_q`` / ``cu_seqlens_k`` (``cu_seqlens_k``
-    defaults to the same tensor, ``total_k`` to the number of queries: self-attention).  Built once per batch
+    defaults to the same tensor and ``total_k`` to the number of queries: self-attention; with distinct key
+    segments ``total_k`` is required).  Built once per batch
     and passed as ``adj_plan=`` (with the same ``adj_indptr`` / ``adj_indices`` and cu_seqlens) to every
     attention call over that adjacency, so no call rebuilds it, as the reference builds its node bias once per
     batch (get_adj_mask_from_edge_index_node, esa/masked_layers.py:79-118) for all layers."""
+    if cu_seqlens_k is not None and total_k is None:
+        raise ValueError("node_plan over distinct key segments needs total_k (the number of key tokens)")
     cu_k = cu_seqlens_q if cu_seqlens_k is None else cu_seqlens_k
     _lib.require_gpu(adj_indptr, adj_indices, cu_seqlens_q, cu_k)
     _check_index("adj_indptr", adj_indptr)

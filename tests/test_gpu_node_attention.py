@@ -248,6 +248,43 @@ def test_node_plan_entries_outside_segment(device):
         assert_f32_close(a.cpu(), b, "planned grads vs oracle")
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_node_plan_cross_attention(device, dtype):
+    """Queries and keys in different segment arrays (3 segments: 5/0/9 queries over 7/4/6 keys, an empty
+    query segment and entries naming keys of other segments): the planned and per-call paths agree bit for
+    bit and both meet the oracle bar; a plan over distinct key segments needs total_k."""
+    rng = np.random.default_rng(90)
+    lq, lk = [5, 0, 9], [7, 4, 6]
+    cq, ck = np.cumsum([0] + lq), np.cumsum([0] + lk)
+    rows = []
+    for b in range(3):
+        for _ in range(lq[b]):
+            own = rng.choice(np.arange(ck[b], ck[b + 1]), size=int(rng.integers(0, lk[b] + 1)), replace=False)
+            other = rng.integers(0, ck[-1], size=int(rng.integers(0, 3)))
+            rows.append(sorted(int(x) for x in np.concatenate([own, other])))
+    ip = torch.tensor(np.cumsum([0] + [len(r) for r in rows]), dtype=torch.int32, device=device)
+    ix = torch.tensor([j for r in rows for j in r], dtype=torch.int32, device=device)
+    cu_q = torch.tensor(cq, dtype=torch.int32, device=device)
+    cu_k = torch.tensor(ck, dtype=torch.int32, device=device)
+    tq, tk = int(cq[-1]), int(ck[-1])
+    q, g = (seeded_normal((tq, 4, D), 700 + i, dtype).to(device) for i in range(2))
+    k, v = (seeded_normal((tk, 4, D), 710 + i, dtype).to(device) for i in range(2))
+    with pytest.raises(ValueError):
+        A.node_plan(ip, ix, cu_q, cu_k)
+    plan = A.node_plan(ip, ix, cu_q, cu_k, total_k=tk)
+    out0, lse0 = A.attn_fwd(q, k, v, cu_q, cu_k, 0, 0, 0.25, adj_indptr=ip, adj_indices=ix)
+    out, lse = A.attn_fwd(q, k, v, cu_q, cu_k, 0, 0, 0.25, adj_indptr=ip, adj_indices=ix, adj_plan=plan)
+    assert torch.equal(out, out0) and torch.equal(lse, lse0)
+    ref_g = A.attn_bwd(g, q, k, v, out0, lse0, cu_q, cu_k, 0, 0, 0.25, adj_indptr=ip, adj_indices=ix)
+    got_g = A.attn_bwd(g, q, k, v, out, lse, cu_q, cu_k, 0, 0, 0.25, adj_indptr=ip, adj_indices=ix, adj_plan=plan)
+    for a_, b_ in zip(got_g, ref_g):
+        assert torch.equal(a_, b_)
+    adj = (ip.cpu().numpy(), ix.cpu().numpy())
+    rout, rlse = OA.varlen_attention(q.cpu(), k.cpu(), v.cpu(), cq, ck, 0.25, adj=adj)
+    rdq, rdk, rdv = OA.varlen_attention_bwd(g.cpu(), q.cpu(), k.cpu(), v.cpu(), cq, ck, 0.25, adj=adj)
+    _check((out.cpu(), lse.cpu()) + tuple(x.cpu() for x in got_g), (rout, rlse, rdq, rdk, rdv), dtype)
+
+
 def test_node_mask_argument_errors(device):
     q = torch.zeros(4, 16, 16, dtype=torch.bfloat16, device=device)
     cu = torch.tensor([0, 4], dtype=torch.int32, device=device)
