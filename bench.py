@@ -437,8 +437,12 @@ def bench_node(args, sub: bool = False):
             rec["achieved_gbs"] = by[name] / (rec["avg_us"] * 1e-6) / 1e9
     dom = max((n for n in by if n in per_kernel), key=lambda n: per_kernel[n]["avg_us"])
     achieved = per_kernel[dom]["achieved_gbs"]
+    traffic = None
+    tfile = ROOT / "profiles" / f"{dom}_node_traffic.json"
+    if tfile.exists():
+        traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
     roofline = {"bound": "hbm", "kernel": dom, "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                "frac": achieved / PEAK_HBM_GBS, "traffic": None,
+                "frac": achieved / PEAK_HBM_GBS, "traffic": traffic,
                 "bytes": "compulsory: every tensor row and CSR entry once (node_bytes)"}
     out = {"workload": "node-mode attention fwd+bwd over a 65,536-node budget batch (node plan built each step)",
            "graphs": gb.num_graphs, "node_tokens": t, "mask_nnz": nnz, "heads": HEADS, "head_dim": HEAD_DIM,
