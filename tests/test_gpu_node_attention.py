@@ -294,3 +294,71 @@ def test_node_mask_argument_errors(device):
         A.attn_fwd(q, q, q, cu, cu, 4, 4, 0.25, adj_indptr=ip, adj_indices=ix)
     with pytest.raises(ValueError):
         A.attn_fwd(q, q, q, cu, cu, 4, 4, 0.25, edge_src=ix, edge_dst=ix, adj_indptr=ip, adj_indices=ix)
+
+
+def test_esa_node_mode_bf16_train_step(device):
+    """ESA in node mode trained bf16-mixed (fp32 parameters under torch.autocast(bfloat16),
+    core/train_pretrain.py:753) on the 32 protein-like graphs of configuration 1 as node graphs (9,603 nodes,
+    radius edges), layers M-S-M-S-P, D = 256, 16 heads, MLP 2 x 512, through the packed entry: the masked
+    layers run on the batch's node plan (forward and backward).  The loss is restricted to the smallest and
+    the largest graph, so the fp64 oracle over those two graphs alone gives the embeddings, dX and the
+    parameter gradients.  Bar: bf16, scaled by max(1, max |reference|)."""
+    from mind_amd.esa.masked_layers import ESA
+    dm, h, layers = 256, 16, "MSMSP"
+    gb = generators.protein_like(seed=3)
+    sizes = gb.node_counts.astype(np.int64)
+    t = int(sizes.sum())
+    n = nearest_multiple_of_8(int(sizes.max()) + 1)
+    torch.manual_seed(0)
+    model = ESA(num_outputs=2, dim_output=dm, dim_hidden=[dm] * len(layers), num_heads=[h] * len(layers),
+                layer_types=layers, node_or_edge="node", xformers_or_torch_attn="hip", use_mlps=True,
+                mlp_hidden_size=2 * dm, num_mlp_layers=2, mlp_type="standard")
+    gen = torch.Generator().manual_seed(1)
+    with torch.no_grad():
+        for name, prm in model.named_parameters():
+            base = (1.0 if name.endswith("weight") else 0.0) if ".ln." in name else 0.0
+            prm.copy_(base + (0.1 if ".ln." in name else 0.05) * torch.randn(prm.shape, generator=gen))
+    model = model.to(device)
+    ei, bm = torch.as_tensor(gb.edge_index).to(device), torch.as_tensor(gb.batch).to(device)
+    na = NodeAdjacency.from_edge_index(ei, bm, gb.num_graphs, n)
+    x = torch.randn(t, dm, generator=torch.Generator().manual_seed(2))
+    xd = x.to(device).requires_grad_(True)
+    sel = [int(np.argmin(sizes)), int(np.argmax(sizes))]
+    first = np.concatenate([[0], np.cumsum(sizes)])
+    rows = np.concatenate([np.arange(first[b], first[b + 1]) for b in sel])
+    gg = torch.randn(2, dm, generator=torch.Generator().manual_seed(3))
+    ge = torch.randn(rows.size, dm, generator=torch.Generator().manual_seed(4))
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        g_emb, enc = model.forward_packed(xd, na)
+    rows_d, sel_d = torch.as_tensor(rows).to(device), torch.as_tensor(sel).to(device)
+    loss = (g_emb.float().index_select(0, sel_d) * gg.to(device)).sum() + \
+        (enc.float().index_select(0, rows_d) * ge.to(device)).sum()
+    loss.backward()
+    torch.cuda.synchronize()
+    # the two graphs' CSR over their own node numbering (graph sel[0]'s nodes first)
+    src, dst = gb.edge_index
+    local = np.full(t, -1, np.int64)
+    local[rows] = np.arange(rows.size)
+    keep = local[src] >= 0
+    rs, cs = local[src[keep]], local[dst[keep]]
+    o = np.lexsort((cs, rs))
+    indptr = np.searchsorted(rs[o], np.arange(rows.size + 1))
+    adj = (indptr, cs[o])
+    cu = np.array([0, sizes[sel[0]], sizes[sel[0]] + sizes[sel[1]]])
+    sd = {k: v.detach().cpu().double().requires_grad_(True) for k, v in model.state_dict().items()}
+    xr = x.double()[torch.as_tensor(rows)].clone().requires_grad_(True)
+    g_ref, enc_ref = OMod.esa(
+        sd, xr, layers, h, 2,
+        attn_m=lambda s_, p_, z: OMod.mab_packed(s_, p_, z, z, cu, cu, h, adj=adj),
+        attn_s=lambda s_, p_, z: OMod.mab_packed(s_, p_, z, z, cu, cu, h),
+        pool=lambda s_, p_, z: OMod.pma_complete(s_, p_, z, h, 2, cu=cu, max_items=n))
+    ((g_ref * gg.double()).sum() + (enc_ref * ge.double()).sum()).backward()
+    assert_bf16_close(g_emb.detach().float().cpu()[sel], g_ref.detach(), grad_scale(g_ref.detach()), "graph emb")
+    assert_bf16_close(enc.detach().float().cpu()[torch.as_tensor(rows)], enc_ref.detach(),
+                      grad_scale(enc_ref.detach()), "token emb")
+    assert_bf16_close(xd.grad.cpu()[torch.as_tensor(rows)], xr.grad, grad_scale(xr.grad), "dX")
+    params = dict(model.named_parameters())
+    for name in ("encoder.0.sab.mab.fc_q.weight", "encoder.0.sab.mab.fc_k.weight", "encoder.0.norm.ln.weight",
+                 "encoder.2.sab.mab.fc_v.bias", "encoder.2.mlp.mlp.0.weight", "decoder.0.pma.S"):
+        ref = sd[name].grad
+        assert_bf16_close(params[name].grad.float().cpu().reshape(ref.shape), ref, grad_scale(ref), f"d {name}")
