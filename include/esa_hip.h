@@ -126,8 +126,10 @@ ESA_API int esa_edge_plan_build(const int* tok_src, const int* tok_dst,
 /* node bias once per batch (get_adj_mask_from_edge_index_node,             */
 /* esa/masked_layers.py:79-118) for all its layers (:849-936).  The plan's   */
 /* tail is the build's scratch.  It stays valid while indptr / indices and   */
-/* the cu_seqlens are unchanged; calls pass the same indptr as mask_a and    */
-/* the same cu_seqlens.                                                      */
+/* the cu_seqlens are unchanged; calls pass the same indptr as mask_a, the   */
+/* same cu_seqlens, and the total_q, total_k and n_mask_edges it was built   */
+/* with (the call locates the plan's sections from them; the plan is not     */
+/* read back to check).                                                      */
 /* ------------------------------------------------------------------------ */
 ESA_API int esa_node_plan_size(int total_q, int total_k, int n_mask_edges, size_t* bytes);
 ESA_API int esa_node_plan_build(const int* indptr, const int* indices,
