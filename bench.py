@@ -503,8 +503,12 @@ def bench_masked(args, sub: bool = False):
     masked = {n + "_masked": f for n, f in FLOPS_PER_PAIR.items()}
     dom = max((n for n in masked if n in per_kernel), key=lambda n: per_kernel[n]["avg_us"])
     achieved = masked[dom] * stats["nnz"] / (per_kernel[dom]["avg_us"] * 1e-6) / 1e12
+    traffic = None
+    tfile = ROOT / "profiles" / f"{dom}_config2_traffic.json"
+    if tfile.exists():
+        traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
     roofline = {"bound": "mfma", "kernel": dom, "achieved": achieved, "peak": PEAK_BF16_TFLOPS,
-                "unit": "TFLOP/s", "frac": achieved / PEAK_BF16_TFLOPS, "traffic": None,
+                "unit": "TFLOP/s", "frac": achieved / PEAK_BF16_TFLOPS, "traffic": traffic,
                 "flops": "effective (nnz of the mask)"}
     if sub:
         out = {"workload": "config2: edge-masked attention fwd+bwd (edge-mask plan built from src/dst each step)",
