@@ -45,6 +45,14 @@ def test_generators_are_deterministic_and_consistent():
     assert not np.any(a.edge_index[0] == a.edge_index[1])
     c = generators.protein_budget(seed=1, token_budget=20000)
     assert c.num_tokens <= 20000
+    # node budget (the node-mode line): the node count stays within the budget and the next graph would exceed
+    # it; the edge-budget batch with the same seed is the same sequence of graphs cut at another point
+    d = generators.protein_budget(seed=1, token_budget=5000, count="nodes")
+    assert int(d.node_counts.sum()) <= 5000 and len(d.node_counts) >= 2
+    assert np.array_equal(d.node_counts, c.node_counts[: len(d.node_counts)]) or \
+        np.array_equal(c.node_counts, d.node_counts[: len(c.node_counts)])
+    with pytest.raises(ValueError):
+        generators.protein_budget(seed=1, count="graphs")
     src, dst = generators.block_local_edges(0, num_nodes=4096, num_edges=10000)
     assert np.all(src // 512 == dst // 512) and src.max() < 4096
 
