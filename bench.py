@@ -82,7 +82,7 @@ def copy_calibration():
 
 
 def _median_time(step, warmup: int = 2, runs: int = 5) -> tuple[float, int]:
-    """Median wall time of `runs` calls after `warmup` untimed ones (BASELINE.md's method)."""
+    """Median wall time of `runs` calls after `warmup` untimed ones (perf_counter, the CPU baselines' method)."""
     for _ in range(warmup):
         step()
     times = []
