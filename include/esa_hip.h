@@ -211,6 +211,35 @@ ESA_API int esa_pma_bwd(const void* dout, const void* q, const void* k, const vo
                 int head_dim, int dtype, float softmax_scale, void* dq, void* dk,
                 void* dv, void* workspace, size_t workspace_bytes, void* stream);
 
+/* ------------------------------------------------------------------------ */
+/* Debug decode of an edge-mask plan (tests and debugging): the admissible   */
+/* partners of every outer token, read from the plan the way the attention   */
+/* kernels read it — per 32-token tile the partner list entries whose mask  */
+/* bit is set, or, for a tile whose group overflowed the lists, the walk     */
+/* kernels' predicate over its partner range if the group is on the plan's   */
+/* overflow list.  The result is the mask that get_adj_mask_from_edge_index_ */
+/* edge (esa/masked_layers.py:217-268) encodes as 0 entries of its bias,     */
+/* row by row, as a CSR over the packed tokens.                              */
+/* direction 0: the query tiles (forward and dQ passes); 1: what the dK/dV   */
+/* passes read (the key tiles' lists, or the query tiles' lists when the     */
+/* plan was built symmetric).  Two calls: with indptr NULL, out[t] (total_q  */
+/* ints) receives outer token t's partner count; with indptr = the counts'   */
+/* exclusive scan [total_q + 1], out[indptr[t] .. indptr[t+1]) receives its  */
+/* partner token ids in ascending order.  Sizes as the plan was built with.  */
+/* ------------------------------------------------------------------------ */
+ESA_API int esa_edge_plan_decode(const void* plan, int total_q, int total_k, int direction,
+                         const int* indptr, int* out, void* stream);
+
+/* Byte offsets in a node plan (esa_node_plan_build) of its sections, for   */
+/* tests and debugging: offsets[0] the copy of the indices [n_mask_edges],  */
+/* [1] t_indptr [total_k + 1] and [2] t_rows [n_mask_edges] (the transposed */
+/* CSR: per key token the query rows listing it, in ascending entry         */
+/* position; keys outside [0, total_k) after t_indptr[total_k]), [3] the    */
+/* query descriptors int4 [total_q] and [4] the key descriptors int4        */
+/* [total_k] ({partner range lo, hi, row begin, row end}, the row emptied   */
+/* when the range is).  No device access.                                    */
+ESA_API int esa_node_plan_sections(int total_q, int total_k, int n_mask_edges, size_t* offsets);
+
 /* Materialises the edge-adjacency mask of each segment as a padded
  * [batch, max_items, max_items] uint8 array (1 = attend), the same entries
  * get_adj_mask_from_edge_index_edge (esa/masked_layers.py:217-268) sets to 0
@@ -382,7 +411,7 @@ ESA_API int esa_mish_bwd_colsum(const void* z, const void* grad, int64_t rows, i
 /* launch count per kernel id (capacity >= ESA_PROFILE_KERNELS) and clears   */
 /* the record.  Not for concurrent use from several threads.                 */
 /* ------------------------------------------------------------------------ */
-#define ESA_PROFILE_KERNELS 19
+#define ESA_PROFILE_KERNELS 21
 ESA_API int esa_profile_enable(int on);
 ESA_API int esa_profile_collect(float* total_ms, int* launches, int capacity);
 ESA_API const char* esa_profile_kernel_name(int kernel);

@@ -55,6 +55,9 @@ _PROTOS = {
     "esa_varlen_attn_fwd_noalloc": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
                                              _c_int, _c_int, _c_f, _c_int, _vp, _vp, _c_int, _vp, _vp, _vp]),
     "esa_edge_mask_dense": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _vp]),
+    # plan tq tk direction indptr out stream
+    "esa_edge_plan_decode": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _vp, _vp]),
+    "esa_node_plan_sections": (_c_int, [_c_int, _c_int, _c_int, ctypes.POINTER(_c_sz)]),
     # batch k_seeds total_k heads head_dim dtype backward bytes
     "esa_pma_workspace_size": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
                                         ctypes.POINTER(_c_sz)]),

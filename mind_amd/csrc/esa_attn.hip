@@ -1750,6 +1750,7 @@ int groups_of(int total) { return (total + kGroupTok - 1) / kGroupTok; }
 struct PlanLayout {
   size_t flags = 0, nodes = 0, meta = 0, bounds_q = 0, bounds_k = 0, over_count = 0;
   size_t info[2] = {0, 0}, ids[2] = {0, 0}, bits[2] = {0, 0}, over[2] = {0, 0};
+  size_t prep_end = 0;   // end of the sections the prep launch writes (all the fp32 kernels read)
   size_t total = 0;
 };
 
@@ -1763,6 +1764,7 @@ PlanLayout plan_layout(int total_q, int total_k, bool key_lists) {
   P.bounds_q = off; off += align256((size_t)tqp * 8);
   P.bounds_k = off; off += align256((size_t)tkp * 8);
   P.over_count = off; off += 256;
+  P.prep_end = off;
   for (int d = 0; d < 2; ++d) {
     const size_t tiles = (size_t)(d ? tkp : tqp) / kTile;
     P.info[d] = off; off += align256(tiles * 4);
@@ -1777,7 +1779,9 @@ PlanLayout plan_layout(int total_q, int total_k, bool key_lists) {
 
 // Per-call workspace: the backward row statistics, the fp32 kernels'
 // per-segment plans and, for an edge mask given as node ids, the plan the
-// call builds (the key tiles' lists only when `key_lists`).
+// call builds (the key tiles' lists only when `key_lists`; for the fp32
+// kernels only the prep sections, since they evaluate the predicate from the
+// node pairs and read no lists).
 struct WsLayout {
   size_t aux = 0, plan_q = 0, plan_k = 0, plan = 0, total = 0;
 };
@@ -1793,7 +1797,11 @@ WsLayout ws_layout(int total_q, int total_k, int heads, int dtype, int mask_kind
     L.plan_q = off; off += plan_size(total_q);
     if (backward) { L.plan_k = off; off += plan_size(total_k); }
   }
-  if (mask_kind == ESA_MASK_EDGE) { L.plan = off; off += plan_layout(total_q, total_k, key_lists).total; }
+  if (mask_kind == ESA_MASK_EDGE) {
+    const PlanLayout P = plan_layout(total_q, total_k, key_lists);
+    L.plan = off;
+    off += dtype == ESA_F32 ? align256(P.prep_end) : P.total;
+  }
   L.total = off;
   return L;
 }
@@ -1820,6 +1828,70 @@ PlanView plan_view(const void* plan, int total_q, int total_k) {
     V.over[d] = reinterpret_cast<const int4*>(b + P.over[d]);
   }
   return V;
+}
+
+// ---- edge-mask plan decode (debug): the admissible partners of every outer
+// token as the attention kernels read them from a plan.  One wave per outer
+// tile, lane l (< 32) for its token l.
+//  - A listed tile (info n >= 0): the ceil(n / 32) compact tiles the list
+//    kernels visit; bit k of the lane's word c selects list entry 32 c + k
+//    (the kernels' score seed), whose id is the partner (a set bit over a -1
+//    pad is decoded as -1: the kernels would attend a zero row there).
+//  - An overflowing tile (info -1): the walk kernels take its 128-token group
+//    only if the group is on the overflow list; they visit the partner tiles
+//    of the wave's range that pass the tile-metadata test and keep the
+//    partners in the lane's range, other than the token itself, that share an
+//    endpoint with it.  A group missing from the list decodes as no partners.
+// Direction 1 is what the dK/dV passes read: the key tiles' own lists, or the
+// query tiles' when the plan's flag says the mask is symmetric.  Without
+// indptr the kernel writes each outer token's partner count to out[t]; with
+// indptr (the counts' exclusive scan) the partners, ascending, to
+// out[indptr[t] ..].
+__global__ __launch_bounds__(256) void edge_plan_decode_kernel(const PlanView V, int dir, int total,
+                                                               const int* __restrict__ indptr,
+                                                               int* __restrict__ out) {
+  const int lane = threadIdx.x & 63, col = lane & 31, half = lane >> 5;
+  const int tile = (int)blockIdx.x * kWaves + (threadIdx.x >> 6), o0 = tile * kTile;
+  if (o0 >= total) return;   // wave-uniform
+  const int ld = (dir == 1 && V.flags[0] != 0) ? 0 : dir;
+  const OuterTile ot = outer_tile(dir ? V.bounds_k : V.bounds_q, total, o0, col);
+  const bool mine = ot.valid && half == 0;
+  const bool fill = indptr != nullptr;
+  int* dst = fill && mine ? out + indptr[ot.oi] : nullptr;
+  int cnt = 0;
+  const int n = V.info[ld][tile];
+  if (n >= 0) {
+    const int* ids = V.ids[ld] + (size_t)tile * kListCap;
+    const uint32_t* bits = V.bits[ld] + (size_t)tile * kListCap;
+    for (int c = 0; c * kTile < n; ++c) {
+      uint32_t w = mine ? bits[c * kTile + col] : 0u;
+      while (w) {
+        const int k = __builtin_ctz(w);
+        w &= w - 1u;
+        if (dst) dst[cnt] = ids[c * kTile + k];
+        ++cnt;
+      }
+    }
+  } else {
+    const int g = tile / kWaves;
+    bool listed = false;
+    for (int i = 0; i < V.over_count[ld]; ++i) listed = listed || V.over[ld][i].x == g;
+    if (listed) {
+      const int4 own = V.meta[tile];
+      const int2 qn = V.nodes[ot.oc];
+      for (int pt = ot.pt_beg; pt < ot.pt_end; ++pt) {
+        if (!tiles_may_touch(own, V.meta[pt])) continue;   // wave-uniform
+        for (int j = 0; j < kTile; ++j) {
+          const int p = pt * kTile + j;
+          if (mine && p >= ot.plo && p < ot.phi && p != ot.oi && node_adjacent(V.nodes[p], qn)) {
+            if (dst) dst[cnt] = p;
+            ++cnt;
+          }
+        }
+      }
+    }
+  }
+  if (!fill && mine) out[ot.oi] = cnt;
 }
 
 bool misaligned(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) != 0; }
@@ -2394,6 +2466,26 @@ int esa_pma_bwd(const void* dout, const void* q, const void* k, const void* v, c
                        reinterpret_cast<const bf16*>(ws + off[2]), row_elems, k_seeds, batch, static_cast<bf16*>(dq));
   ESA_LAUNCH_CHECK();
   return ESA_OK;
+}
+
+int esa_edge_plan_decode(const void* plan, int total_q, int total_k, int direction, const int* indptr, int* out,
+                         void* stream) {
+  if (!plan || !out) return ESA_ERR_NULL;
+  if (total_q < 0 || total_q != total_k || (direction != 0 && direction != 1)) return ESA_ERR_SHAPE;
+  if (misaligned(plan)) return ESA_ERR_ALIGN;
+  if (total_q == 0) return ESA_OK;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const unsigned tiles = (unsigned)round32(total_q) / kTile;
+  hipLaunchKernelGGL(edge_plan_decode_kernel, dim3((tiles + kWaves - 1) / kWaves), dim3(256), 0, st,
+                     plan_view(plan, total_q, total_k), direction, total_q, indptr, out);
+  ESA_LAUNCH_CHECK();
+  return ESA_OK;
+}
+
+int esa_node_plan_sections(int total_q, int total_k, int n_mask_edges, size_t* offsets) {
+  if (!offsets) return ESA_ERR_NULL;
+  if (total_q < 0 || total_k < 0 || n_mask_edges < 0) return ESA_ERR_SHAPE;
+  return graph_node_plan_sections(total_q, total_k, n_mask_edges, offsets);
 }
 
 int esa_edge_mask_dense(const int* tok_src, const int* tok_dst, const int* cu_seqlens, int batch, int total,

@@ -30,5 +30,7 @@ int graph_attn_fwd(GraphAttnArgs a, int dtype, const void* plan, hipStream_t st)
 int graph_attn_bwd(GraphAttnArgs a, int dtype, const void* plan, void* workspace, size_t workspace_bytes,
                    hipStream_t st);
 int graph_node_plan_size(int total_q, int total_k, int nnz, size_t* bytes);
+// Byte offsets of a node plan's sections: indices, t_indptr, t_rows, q_desc, k_desc.
+int graph_node_plan_sections(int total_q, int total_k, int nnz, size_t offsets[5]);
 int graph_node_plan_build(const int* indptr, const int* indices, const int* cu_q, const int* cu_k, int nseg,
                           int total_q, int total_k, int nnz, void* plan, size_t plan_bytes, hipStream_t st);

@@ -434,6 +434,18 @@ int graph_node_plan_size(int total_q, int total_k, int nnz, size_t* bytes) {
   return ESA_OK;
 }
 
+int graph_node_plan_sections(int total_q, int total_k, int nnz, size_t offsets[5]) {
+  NodePlan w;
+  const int rc = node_plan_layout(total_q, total_k, nnz, w);
+  if (rc) return rc;
+  offsets[0] = w.indices;
+  offsets[1] = w.t_indptr;
+  offsets[2] = w.t_rows;
+  offsets[3] = w.q_desc;
+  offsets[4] = w.k_desc;
+  return ESA_OK;
+}
+
 int graph_node_plan_build(const int* indptr, const int* indices, const int* cu_q, const int* cu_k, int nseg,
                           int total_q, int total_k, int nnz, void* plan, size_t plan_bytes, hipStream_t st) {
   NodePlan w;

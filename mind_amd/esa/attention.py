@@ -118,19 +118,49 @@ def node_plan(adj_indptr, adj_indices, cu_seqlens_q, cu_seqlens_k=None, total_k:
     return plan
 
 
-def _mask_args(tq: int, edge_src, edge_dst, adj_indptr, adj_indices, edge_plan=None, adj_plan=None):
-    """(mask_kind, mask_a, mask_b, n_mask_edges) of the C ABI for the given mask tensors."""
+def edge_plan_bytes(total: int, symmetric: bool) -> int:
+    """Bytes of an edge-mask plan over ``total`` tokens (esa_edge_plan_size); ``symmetric``: one cu_seqlens
+    array for queries and keys (the plan then holds no key-tile lists)."""
+    n = _lib.ctypes.c_size_t(0)
+    _lib.check(_lib.load().esa_edge_plan_size(total, total, int(symmetric), _lib.ctypes.byref(n)),
+               "esa_edge_plan_size")
+    return int(n.value)
+
+
+def node_plan_bytes(total_q: int, total_k: int, nnz: int) -> int:
+    """Bytes of a node plan (esa_node_plan_size)."""
+    n = _lib.ctypes.c_size_t(0)
+    _lib.check(_lib.load().esa_node_plan_size(total_q, total_k, nnz, _lib.ctypes.byref(n)), "esa_node_plan_size")
+    return int(n.value)
+
+
+def _mask_args(tq: int, edge_src, edge_dst, adj_indptr, adj_indices, edge_plan=None, adj_plan=None, tk=None,
+               symmetric=True):
+    """(mask_kind, mask_a, mask_b, n_mask_edges) of the C ABI for the given mask tensors.
+
+    The C ABI takes a plan without its size and reads it at the offsets the call's token counts give, so a
+    plan smaller than those sizes need (one built for another batch) is refused here, before any launch."""
     if sum(x is not None for x in (edge_src, adj_indptr, edge_plan)) > 1:
         raise ValueError("give one mask: the edge mask (edge_src / edge_dst), its plan, or the node adjacency")
+    tk = tq if tk is None else tk
     if adj_plan is not None:
         if adj_indptr is None or adj_indices is None:
             raise ValueError("adj_plan goes with the adj_indptr / adj_indices it was built from")
-        if adj_plan.dtype != torch.uint8 or not adj_plan.is_cuda:
-            raise ValueError("adj_plan must be the uint8 device tensor node_plan() returns")
         _check_index("adj_indptr", adj_indptr, tq + 1)
         _check_index("adj_indices", adj_indices)
+        need = node_plan_bytes(tq, tk, adj_indices.numel())
+        if adj_plan.numel() < need:
+            raise ValueError(f"adj_plan holds {adj_plan.numel()} bytes; a node plan over {tq} queries, {tk} keys "
+                             f"and {adj_indices.numel()} entries needs {need} (built for another batch?)")
+        if adj_plan.dtype != torch.uint8 or not adj_plan.is_cuda:
+            raise ValueError("adj_plan must be the uint8 device tensor node_plan() returns")
         return _lib.ESA_MASK_NODE_PLAN, adj_indptr, adj_plan, adj_indices.numel()
     if edge_plan is not None:
+        need = edge_plan_bytes(tq, symmetric)
+        if edge_plan.numel() < need:
+            raise ValueError(f"edge_plan holds {edge_plan.numel()} bytes; a plan over {tq} tokens"
+                             f"{'' if symmetric else ' with distinct key segments'} needs {need} "
+                             "(built for another batch?)")
         if edge_plan.dtype != torch.uint8 or not edge_plan.is_cuda:
             raise ValueError("edge_plan must be the uint8 device tensor edge_plan() returns")
         return _lib.ESA_MASK_EDGE_PLAN, edge_plan, None, 0
@@ -160,7 +190,8 @@ def attn_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, so
     _check_index("cu_seqlens_q", cu_seqlens_q)
     _check_index("cu_seqlens_k", cu_seqlens_k, batch + 1)
     tq, tk = q.shape[0], k.shape[0]
-    mask_kind, mask_a, mask_b, nnz = _mask_args(tq, edge_src, edge_dst, adj_indptr, adj_indices, edge_plan, adj_plan)
+    mask_kind, mask_a, mask_b, nnz = _mask_args(tq, edge_src, edge_dst, adj_indptr, adj_indices, edge_plan, adj_plan,
+                                             tk, cu_seqlens_k.data_ptr() == cu_seqlens_q.data_ptr())
     dt = _dtype_code(q)
     out = torch.empty_like(q)
     lse = torch.empty((heads, tq), dtype=torch.float32, device=q.device)
@@ -195,7 +226,8 @@ def attn_fwd_noalloc(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seql
     _check_index("cu_seqlens_q", cu_seqlens_q)
     _check_index("cu_seqlens_k", cu_seqlens_k, batch + 1)
     tq, tk = q.shape[0], k.shape[0]
-    mask_kind, mask_a, mask_b, nnz = _mask_args(tq, edge_src, edge_dst, adj_indptr, adj_indices, edge_plan, adj_plan)
+    mask_kind, mask_a, mask_b, nnz = _mask_args(tq, edge_src, edge_dst, adj_indptr, adj_indices, edge_plan, adj_plan,
+                                             tk, cu_seqlens_k.data_ptr() == cu_seqlens_q.data_ptr())
     rc = _lib.load().esa_varlen_attn_fwd_noalloc(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(), batch, tq, tk,
         int(max_seqlen_q), int(max_seqlen_k), heads, HEAD_DIM, _dtype_code(q), float(softmax_scale),
@@ -216,7 +248,8 @@ def attn_bwd(dout, q, k, v, out, lse, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, 
         raise ValueError("dout and out must have the shape of q")
     batch = cu_seqlens_q.numel() - 1
     tq, tk = q.shape[0], k.shape[0]
-    mask_kind, mask_a, mask_b, nnz = _mask_args(tq, edge_src, edge_dst, adj_indptr, adj_indices, edge_plan, adj_plan)
+    mask_kind, mask_a, mask_b, nnz = _mask_args(tq, edge_src, edge_dst, adj_indptr, adj_indices, edge_plan, adj_plan,
+                                             tk, cu_seqlens_k.data_ptr() == cu_seqlens_q.data_ptr())
     dt = _dtype_code(q)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     ws = _workspace(q.device, tq, tk, heads, dt, mask_kind, nnz, True)
@@ -395,3 +428,39 @@ def edge_mask_dense(edge_src, edge_dst, cu_seqlens, max_items):
                                          edge_src.numel(), int(max_items), out.data_ptr(), _lib.stream_of(edge_src))
     _lib.check(rc, "esa_edge_mask_dense")
     return out
+
+
+def edge_plan_decode(plan: torch.Tensor, total: int, direction: int = 0) -> tuple[torch.Tensor, torch.Tensor]:
+    """Debug decode of an edge-mask plan (esa_edge_plan_decode): the admissible partners of every token as the
+    attention kernels read them from ``plan`` (direction 0: the forward and dQ passes; 1: the dK/dV passes),
+    as a CSR ``(indptr [total + 1], indices)`` of int32 device tensors, each row ascending."""
+    _lib.require_gpu(plan)
+    if plan.dtype != torch.uint8 or plan.numel() < edge_plan_bytes(total, True):
+        raise ValueError("plan must be the uint8 device tensor edge_plan() returns for these tokens")
+    lib = _lib.load()
+    counts = torch.empty(max(total, 1), dtype=torch.int32, device=plan.device)
+    st = _lib.stream_of(plan)
+    _lib.check(lib.esa_edge_plan_decode(plan.data_ptr(), total, total, int(direction), None, counts.data_ptr(), st),
+               "esa_edge_plan_decode")
+    indptr = torch.zeros(total + 1, dtype=torch.int32, device=plan.device)
+    indptr[1:] = torch.cumsum(counts[:total], 0)
+    indices = torch.empty(max(int(indptr[-1]), 1), dtype=torch.int32, device=plan.device)
+    _lib.check(lib.esa_edge_plan_decode(plan.data_ptr(), total, total, int(direction), indptr.data_ptr(),
+                                        indices.data_ptr(), st), "esa_edge_plan_decode")
+    return indptr, indices[: int(indptr[-1])]
+
+
+def node_plan_sections(plan: torch.Tensor, total_q: int, total_k: int, nnz: int) -> dict[str, torch.Tensor]:
+    """Views of a node plan's sections (esa_node_plan_sections): ``indices`` [nnz] (the CSR's copy),
+    ``t_indptr`` [total_k + 1] and ``t_rows`` [nnz] (the transposed CSR the dK/dV pass reads), ``q_desc``
+    [total_q, 4] and ``k_desc`` [total_k, 4] (per token: partner range lo, hi and row begin, end)."""
+    if plan.dtype != torch.uint8 or plan.numel() < node_plan_bytes(total_q, total_k, nnz):
+        raise ValueError("plan must be the uint8 tensor node_plan() returns for these sizes")
+    off = (_lib.ctypes.c_size_t * 5)()
+    _lib.check(_lib.load().esa_node_plan_sections(total_q, total_k, nnz, off), "esa_node_plan_sections")
+
+    def ints(i, n):
+        return plan[off[i]: off[i] + 4 * n].view(torch.int32)
+
+    return {"indices": ints(0, nnz), "t_indptr": ints(1, total_k + 1), "t_rows": ints(2, nnz),
+            "q_desc": ints(3, 4 * total_q).view(total_q, 4), "k_desc": ints(4, 4 * total_k).view(total_k, 4)}

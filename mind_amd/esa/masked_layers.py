@@ -345,9 +345,34 @@ class ESA(nn.Module):
         return mish(self.decoder_linear(enc)), enc
 
     def _forward_packed(self, X, edge_index, batch_mapping, num_max_items, tokens: PackedSets):
-        """The "hip" forward of padded input: unpad, run ``forward_packed``, pad the token embeddings."""
-        g_emb, enc = self.forward_packed(tokens.unpad(X), tokens, edge_index, batch_mapping)
-        return g_emb, tokens.pad(enc)
+        """The "hip" forward of padded input: unpad, encode the packed tokens, pad the token embeddings.
+
+        Without a PMA the head acts per token, and the result keeps the padded forward's [B, N, dim_output]
+        shape (esa/masked_layers.py:929-936): the head runs on the padded embeddings, which are zero at the
+        padding slots, so those slots hold mish(bias)."""
+        enc = self._encode_packed(tokens.unpad(X), tokens)
+        enc_pad = tokens.pad(enc)
+        if hasattr(self, "decoder"):
+            return self._decode_packed(enc, tokens, edge_index, batch_mapping), enc_pad
+        return mish(self.decoder_linear(enc_pad)), enc_pad
+
+    def _encode_packed(self, tokens_x: torch.Tensor, tokens: PackedSets) -> torch.Tensor:
+        """Encoder blocks and the input residual on packed tokens [T, D] (esa/masked_layers.py:914-921)."""
+        xp = tokens_x
+        h = xp
+        for blk in self.encoder:
+            h = _sab_forward_packed(blk, h, tokens)
+        if hasattr(self, "dim_pma") and self.dim_hidden[0] != self.dim_pma:
+            xp = self.out_proj(xp)
+        return h + xp
+
+    def _decode_packed(self, enc: torch.Tensor, tokens: PackedSets, edge_index, batch_mapping) -> torch.Tensor:
+        """PMA decoder, mean over seeds and the Mish head (esa/masked_layers.py:926-934) -> [B, dim_output]."""
+        out = _pma_forward_packed(self.decoder[0], enc, tokens)
+        for blk in list(self.decoder)[1:]:
+            out, _, _, _, _ = blk((out, edge_index, batch_mapping, tokens.max_items, tokens))
+        out = out.mean(dim=1)
+        return mish(self.decoder_linear(out))
 
     def forward_packed(self, tokens_x: torch.Tensor, tokens: PackedSets, edge_index=None, batch_mapping=None):
         """ESA.forward (esa/masked_layers.py:849-936) on packed tokens, the "hip" backend's native entry.
@@ -364,18 +389,8 @@ class ESA(nn.Module):
                              f"{self.xformers_or_torch_attn!r}")
         if tokens_x.dim() != 2 or tokens_x.shape[0] != tokens.num_tokens:
             raise ValueError(f"tokens_x must be [T, D] with T = {tokens.num_tokens} (got {tuple(tokens_x.shape)})")
-        xp = tokens_x
-        h = xp
-        for blk in self.encoder:
-            h = _sab_forward_packed(blk, h, tokens)
-        if hasattr(self, "dim_pma") and self.dim_hidden[0] != self.dim_pma:
-            xp = self.out_proj(xp)
-        enc = h + xp
+        enc = self._encode_packed(tokens_x, tokens)
         if hasattr(self, "decoder"):
-            out = _pma_forward_packed(self.decoder[0], enc, tokens)
-            for blk in list(self.decoder)[1:]:
-                out, _, _, _, _ = blk((out, edge_index, batch_mapping, tokens.max_items, tokens))
-            out = out.mean(dim=1)
-            return mish(self.decoder_linear(out)), enc
-        # no PMA: the head acts on every token (padding slots of the padded forward give mish(b) there)
+            return self._decode_packed(enc, tokens, edge_index, batch_mapping), enc
+        # no PMA: the head acts on every token; packed, it returns [T, dim_output] (the padded entry pads)
         return mish(self.decoder_linear(enc)), enc

@@ -83,3 +83,30 @@ def test_argument_errors_need_no_gpu():
     assert lib.esa_varlen_attn_workspace_size(100, 100, 16, 16, bf16, node_plan, 500, 1, ctypes.byref(m)) == 0
     assert 0 < m.value < n.value
     assert lib.esa_node_plan_build(None, None, None, None, 1, 100, 100, 0, 256, 1 << 20, None) == -1
+
+
+def test_short_plans_are_refused_before_launch():
+    """A plan is passed to the C ABI without its size and read at the offsets the call's token counts give:
+    the Python boundary refuses a plan smaller than those counts need (one built for a smaller batch)."""
+    from mind_amd import _lib
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("library not built")
+    import torch
+    from mind_amd.esa import attention as A
+    tq = 1000
+    indptr = torch.zeros(tq + 1, dtype=torch.int32)
+    indices = torch.zeros(50, dtype=torch.int32)
+    sym, full = A.edge_plan_bytes(tq, True), A.edge_plan_bytes(tq, False)
+    assert 0 < A.edge_plan_bytes(tq // 2, True) < sym < full
+    with pytest.raises(ValueError, match="edge_plan holds"):
+        A._mask_args(tq, None, None, None, None, edge_plan=torch.empty(sym - 1, dtype=torch.uint8))
+    with pytest.raises(ValueError, match="distinct key segments"):
+        A._mask_args(tq, None, None, None, None, edge_plan=torch.empty(sym, dtype=torch.uint8), symmetric=False)
+    need = A.node_plan_bytes(tq, tq, indices.numel())
+    with pytest.raises(ValueError, match="adj_plan holds"):
+        A._mask_args(tq, None, None, indptr, indices, adj_plan=torch.empty(need - 1, dtype=torch.uint8))
+    # plans of the right size get past the size check (then the device check refuses host tensors)
+    with pytest.raises(ValueError, match="device tensor"):
+        A._mask_args(tq, None, None, None, None, edge_plan=torch.empty(sym, dtype=torch.uint8))
+    with pytest.raises(ValueError, match="device tensor"):
+        A._mask_args(tq, None, None, indptr, indices, adj_plan=torch.empty(need, dtype=torch.uint8))

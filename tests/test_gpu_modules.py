@@ -253,6 +253,41 @@ def test_esa_block_config0_shape(device, backend):
     assert_f32_close(g_emb.reshape(g_ref.shape), g_ref, "ESA graph embedding")
 
 
+def test_esa_hip_without_pma_keeps_padded_shape(device):
+    """layer_types without a P (core/pretraining_config_rna.yaml's pattern): ESA.forward returns the head
+    applied per token as [B, N, dim_output] (esa/masked_layers.py:929-936), mish(bias) at padding slots, and
+    forward_packed the same values packed [T, dim_output]; both against the fp64 oracle."""
+    gb, n = _batch(11, num_graphs=5)
+    torch.manual_seed(11)
+    d_out = 24
+    model = ML.ESA(num_outputs=1, dim_output=d_out, dim_hidden=[D, D], num_heads=[H, H], layer_types="MS",
+                   xformers_or_torch_attn="hip", use_mlps=True, mlp_hidden_size=2 * D, num_mlp_layers=2,
+                   mlp_type="standard").to(device)
+    X, valid = _padded_tokens(gb, n, 12)
+    ei = torch.as_tensor(gb.edge_index).to(device)
+    bm = torch.as_tensor(gb.batch).to(device)
+    with torch.no_grad():
+        g_emb, enc = model(X.to(device), ei, bm, n)
+        adj = EdgeAdjacency.from_edge_index(ei, bm, gb.num_graphs, n)
+        g_pk, enc_pk = model.forward_packed(adj.unpad(X.to(device)), adj)
+    assert g_emb.shape == (gb.num_graphs, n, d_out) and enc.shape == (gb.num_graphs, n, D)
+    assert g_pk.shape == (int(gb.cu_seqlens[-1]), d_out)
+    assert torch.equal(adj.unpad(g_emb), g_pk) and torch.equal(adj.unpad(enc), enc_pk)
+    g_emb, enc = g_emb.cpu(), enc.cpu()
+    sd = _sd(model)
+    pad_ref = torch.nn.functional.mish(sd["decoder_linear.bias"].double())
+    assert_f32_close(g_emb[~valid], pad_ref.expand(int((~valid).sum()), d_out), "head at padding slots")
+    cu = gb.cu_seqlens
+    src, dst = gb.edge_index[0], gb.edge_index[1]
+    g_ref, enc_ref = OMod.esa(
+        sd, X.double()[valid], "MS", H, 2,
+        attn_m=lambda s_, p_, x: OMod.mab_packed(s_, p_, x, x, cu, cu, H, src, dst),
+        attn_s=lambda s_, p_, x: OMod.mab_packed(s_, p_, x, x, cu, cu, H),
+        pool=None)
+    assert_f32_close(enc[valid], enc_ref, "ESA enc (valid rows)")
+    assert_f32_close(g_emb[valid], g_ref, "ESA per-token head (valid rows)")
+
+
 def test_state_dict_names_match_reference_layout():
     m = ML.ESA(num_outputs=4, dim_output=32, dim_hidden=[32, 32, 32], num_heads=[2, 2, 2], layer_types="MSP",
                xformers_or_torch_attn="hip", use_mlps=True, mlp_hidden_size=64, mlp_type="gated_mlp")

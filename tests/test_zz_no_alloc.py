@@ -47,6 +47,28 @@ def test_noalloc_forward_equals_allocating_forward(device, dtype, mask):
         _compare(device, *_case(device, gb, seed, dtype, mask))
 
 
+@pytest.mark.parametrize("dtype,heads", [(torch.float32, 16), (torch.bfloat16, 32)])
+def test_noalloc_edge_mask_at_the_documented_limit(device, dtype, heads):
+    """131,072 edge tokens (configuration 4's batch), the size the scratch is documented to cover for every
+    mask kind: the edge-masked forward fits (fp32 reserves only the plan sections its kernels read) and equals
+    the allocating forward; then a small call."""
+    lib = _lib.load()
+    big = generators.protein_budget(seed=4, token_budget=131072)
+    small = generators.protein_like(seed=5, num_graphs=4, n_min=40, n_max=120)
+    for gb, seed in ((big, 21), (small, 22)):
+        t = int(gb.cu_seqlens[-1])
+        n = _lib.ctypes.c_size_t(0)
+        _lib.check(lib.esa_varlen_attn_workspace_size(t, t, heads, D, A._dtype_code(torch.empty(0, dtype=dtype)),
+                                                      _lib.ESA_MASK_EDGE, 0, 0, _lib.ctypes.byref(n)), "ws")
+        assert n.value <= int(lib.esa_noalloc_scratch_bytes())
+        print(f"[noalloc] {dtype} edge heads={heads} tokens={t} scratch={n.value}", flush=True)
+        cu = torch.as_tensor(gb.cu_seqlens).to(device)
+        q, k, v = (seeded_normal((t, heads, D), seed + i, dtype).to(device) for i in range(3))
+        kw = {"edge_src": torch.as_tensor(gb.edge_index[0].astype(np.int32)).to(device),
+              "edge_dst": torch.as_tensor(gb.edge_index[1].astype(np.int32)).to(device)}
+        _compare(device, q, k, v, cu, int(gb.max_seqlen), kw)
+
+
 def test_noalloc_forward_node_mask(device):
     for sizes, seed in (([60, 45, 80], 5), ([12, 7], 6)):
         ei, bm = node_graph(seed, sizes)
