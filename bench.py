@@ -55,8 +55,8 @@ def parse():
                     help="graphs of the configuration-2 batch timed on the CPU for the masked baseline")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-sub", action="store_true",
-                    help="headline only: skip the masked (configuration 2), gather (configuration 3) and node "
-                         "sub-objects")
+                    help="headline only: skip the masked (configuration 2), gather (configuration 3), node, block "
+                         "(configuration 0) and stack (configuration 4) sub-objects")
     ap.add_argument("--config", choices=["varlen", "masked", "gather", "node", "block", "stack"], default="varlen",
                     help="varlen: configuration 1 (default, the headline metric); masked: configuration 2 "
                          "(edge-masked MAB attention fwd+bwd); gather: configuration 3 (edge gather + CSR "
@@ -160,6 +160,8 @@ def main():
             result["masked"] = bench_masked(args, sub=True)
             result["gather"] = bench_gather(args, sub=True)
             result["node"] = bench_node(args, sub=True)
+            result["block"] = bench_block(args, sub=True)
+            result["stack"] = bench_stack(args, sub=True)
         print(json.dumps(result), flush=True)
         return
     {"masked": bench_masked, "gather": bench_gather, "node": bench_node, "block": bench_block,
@@ -271,12 +273,17 @@ def bench_varlen(args):
 
 
 def edge_mask_stats(src: np.ndarray, dst: np.ndarray, cu: np.ndarray, tile: int = 32) -> dict:
-    """Exact pair count of the share-an-endpoint mask and its 32x32 tile occupancy, per graph.
+    """Exact pair count of the share-an-endpoint mask, its 32x32 tile occupancy per graph, and the work the
+    key-list kernels execute.
 
-    nnz = #{(i, j): i != j, {s_i, d_i} and {s_j, d_j} intersect}; tiles count
-    the (query tile, key tile) blocks of each graph with at least one such pair.
+    nnz = #{(i, j): i != j, {s_i, d_i} and {s_j, d_j} intersect}; tiles count the (query tile, key tile)
+    blocks of each graph with at least one such pair.  The list kernels visit, per 32-token tile of the
+    packed token order, ceil(u / 32) compact tiles of 32 x 32 score slots, u the size of the union of the
+    tile's tokens' partners (the edge-mask plan's list of the tile): compact_tiles sums those, list_entries
+    the u.
     """
     nnz = tiles_any = tiles_all = 0
+    pair_tile, pair_col = [], []
     for b in range(len(cu) - 1):
         s, e = int(cu[b]), int(cu[b + 1])
         if e == s:
@@ -291,7 +298,29 @@ def edge_mask_stats(src: np.ndarray, dst: np.ndarray, cu: np.ndarray, tile: int 
         pad[: e - s, : e - s] = m
         tiles_any += int(pad.reshape(nt, tile, nt, tile).any(axis=(1, 3)).sum())
         tiles_all += nt * nt
-    return {"nnz": nnz, "tiles_nonempty": tiles_any, "tiles_total": tiles_all}
+        i, j = np.nonzero(m)
+        pair_tile.append((i + s) // tile)
+        pair_col.append(j + s)
+    if pair_tile:
+        key = np.unique(np.concatenate(pair_tile).astype(np.int64) * (int(cu[-1]) + 1) + np.concatenate(pair_col))
+        union = np.bincount(key // (int(cu[-1]) + 1))
+    else:
+        union = np.zeros(0, np.int64)
+    return {"nnz": nnz, "tiles_nonempty": tiles_any, "tiles_total": tiles_all,
+            "list_entries": int(union.sum()), "compact_tiles": int(((union + tile - 1) // tile).sum())}
+
+
+def masked_bytes(t: int, compact_tiles: int, heads: int = HEADS) -> dict:
+    """Compulsory HBM bytes per launch of the key-list kernels (bf16 [T, H, 16] tensors of T*H*32 bytes, the
+    fp32 LSE [H, T], the dK/dV pass's 8-byte row statistics per (head, query), and per compact tile 32 list
+    ids and 32 mask words of 4 bytes): forward reads Q, K, V and writes O and the LSE; dQ reads Q, K, V, O,
+    dO and the LSE and writes dQ and the row statistics; dK/dV reads K, V, Q, dO and the row statistics and
+    writes dK and dV.  Each gathered row counted once."""
+    row = t * heads * HEAD_DIM * 2
+    lists = compact_tiles * 32 * 8
+    return {"attn_fwd_masked": 4 * row + heads * t * 4 + lists,
+            "attn_bwd_dq_masked": 6 * row + heads * t * (4 + 8) + lists,
+            "attn_bwd_dkdv_masked": 6 * row + heads * t * 8 + lists}
 
 
 def cpu_baseline_masked(gb, seed: int, n_graphs: int) -> dict:
@@ -498,26 +527,43 @@ def bench_masked(args, sub: bool = False):
 
     ms_per_step, wall_ms, per_kernel, ms_prof = timed(step, args.steps, args.warmup)
     eff_flops = 14 * DIM * stats["nnz"]
-    exec_flops = 14 * DIM * stats["tiles_nonempty"] * 32 * 32
+    # score slots the list kernels compute: every compact tile is 32 x 32 (query and key tiles' lists are one
+    # list when the mask is symmetric, as here)
+    exec_flops = 14 * DIM * stats["compact_tiles"] * 32 * 32
     tflops = eff_flops / (ms_per_step * 1e-3) / 1e12
     masked = {n + "_masked": f for n, f in FLOPS_PER_PAIR.items()}
+    by = masked_bytes(t, stats["compact_tiles"])
+    for name, rec in per_kernel.items():
+        if name in masked:
+            rec["effective_tflops"] = masked[name] * stats["nnz"] / (rec["avg_us"] * 1e-6) / 1e12
+            rec["executed_tflops"] = masked[name] * stats["compact_tiles"] * 1024 / (rec["avg_us"] * 1e-6) / 1e12
+            rec["algorithmic_bytes"] = by[name]
+            rec["achieved_gbs"] = by[name] / (rec["avg_us"] * 1e-6) / 1e9
     dom = max((n for n in masked if n in per_kernel), key=lambda n: per_kernel[n]["avg_us"])
-    achieved = masked[dom] * stats["nnz"] / (per_kernel[dom]["avg_us"] * 1e-6) / 1e12
+    achieved = per_kernel[dom]["effective_tflops"]
     traffic = None
     tfile = ROOT / "profiles" / f"{dom}_config2_traffic.json"
     if tfile.exists():
         traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
     roofline = {"bound": "mfma", "kernel": dom, "achieved": achieved, "peak": PEAK_BF16_TFLOPS,
                 "unit": "TFLOP/s", "frac": achieved / PEAK_BF16_TFLOPS, "traffic": traffic,
-                "flops": "effective (nnz of the mask)"}
+                "flops": "effective (nnz of the mask)",
+                "executed_frac": per_kernel[dom]["executed_tflops"] / PEAK_BF16_TFLOPS}
+    roofline_hbm = {"bound": "hbm", "kernel": dom, "achieved": per_kernel[dom]["achieved_gbs"],
+                    "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": per_kernel[dom]["achieved_gbs"] / PEAK_HBM_GBS,
+                    "traffic": traffic, "bytes": "compulsory: every tensor row, statistic and list word once "
+                                                 "(masked_bytes)"}
     if sub:
         out = {"workload": "config2: edge-masked attention fwd+bwd (edge-mask plan built from src/dst each step)",
                "graphs": gb.num_graphs, "edge_tokens": t, "mask_nnz": stats["nnz"],
                "mask_density": stats["nnz"] / gb.sum_sq, "tiles_nonempty": stats["tiles_nonempty"],
+               "compact_tiles": stats["compact_tiles"], "list_entries": stats["list_entries"],
+               "compact_tile_fill": stats["nnz"] / (stats["compact_tiles"] * 1024),
                "ms_per_step": ms_per_step, "edge_tokens_per_s": t / (ms_per_step * 1e-3),
                "achieved_tflops_effective": tflops,
-               "achieved_tflops_executed_tiles": exec_flops / (ms_per_step * 1e-3) / 1e12,
-               "ms_per_step_profiled": ms_prof, "kernels": per_kernel, "roofline": roofline}
+               "achieved_tflops_executed": exec_flops / (ms_per_step * 1e-3) / 1e12,
+               "ms_per_step_profiled": ms_prof, "kernels": per_kernel, "roofline": roofline,
+               "roofline_hbm": roofline_hbm}
         if not args.no_cpu_baseline:
             out["cpu_baseline"] = cpu_baseline_masked(gb, args.seed, args.cpu_sample_graphs)
         return out
@@ -559,14 +605,17 @@ def bench_masked(args, sub: bool = False):
             "graphs": gb.num_graphs, "edge_tokens": t, "max_seqlen": maxlen, "sum_L2": gb.sum_sq,
             "mask_nnz": stats["nnz"], "mask_density": stats["nnz"] / gb.sum_sq,
             "tiles_nonempty": stats["tiles_nonempty"], "tiles_total": stats["tiles_total"],
+            "compact_tiles": stats["compact_tiles"], "list_entries": stats["list_entries"],
             "heads": HEADS, "head_dim": HEAD_DIM, "dim": DIM, "seed": args.seed,
         },
         "mfma_util_pct": 100.0 * tflops / PEAK_BF16_TFLOPS,
         "achieved_tflops_effective": tflops,
-        "achieved_tflops_executed_tiles": exec_flops / (ms_per_step * 1e-3) / 1e12,
+        "achieved_tflops_executed": exec_flops / (ms_per_step * 1e-3) / 1e12,
+        "compact_tile_fill": stats["nnz"] / (stats["compact_tiles"] * 1024),
         "wall_ms_per_step": wall_ms, "ms_per_step_profiled": ms_prof,
         "kernels": per_kernel,
         "roofline": roofline,
+        "roofline_hbm": roofline_hbm,
         "sab_block": {"ms_per_step": block_ms, "edge_tokens_per_s": t / (block_ms * 1e-3),
                       "what": "SAB(256, 256, 16 heads, 'hip') fwd+bwd incl. projections, fc_o + mish, padded "
                               f"[{gb.num_graphs}, {n_max}, {DIM}] fp32 input"},
@@ -808,7 +857,7 @@ def _edge_tokens(gb, types, emb, proj, device):
     return adj.pad(tok), ei, bm, n
 
 
-def bench_block(args):
+def bench_block(args, sub: bool = False):
     """Configuration 0: the ESA block forward in fp32 (edge tokens, masked MAB + SAB + PMA(1 seed), D=128, H=8)."""
     import torch
 
@@ -831,6 +880,18 @@ def bench_block(args):
             model(x, ei, bm, n)
 
     ms, wall_ms, kern, ms_prof = timed(step, args.steps, args.warmup)
+    lib_ms = sum(k["avg_us"] * k["launches"] for k in kern.values()) / 1e3 / args.steps
+    if sub:
+        out = {"workload": "config0: edge tokens (embed, gather, project) + ESA block M-S-P(1 seed) forward, fp32",
+               "graphs": gb.num_graphs, "edge_tokens": t, "dim": d, "heads": h, "ms_per_step": ms,
+               "wall_ms_per_step": wall_ms, "edge_tokens_per_s": t / (ms * 1e-3), "ms_per_step_profiled": ms_prof,
+               "kernels": kern, "library_kernel_ms_per_step": lib_ms,
+               "other_ms_per_step": ms - lib_ms,
+               "split": "kernels: this library's launches (HIP events per launch); other: the step's remaining "
+                        "time (torch GEMMs, embedding, gathers of the padded views, launch gaps)"}
+        if not args.no_cpu_baseline:
+            out["cpu_baseline"] = cpu_baseline_block(gb, types, emb, proj, model, h)
+        return out
     result = {
         "metric": "edge-tokens/sec through the ESA block forward (fp32)",
         "value": t / (ms * 1e-3), "unit": "edge-tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -840,6 +901,7 @@ def bench_block(args):
                    "graphs": gb.num_graphs, "edge_tokens": t, "max_seqlen": gb.max_seqlen, "dim": d, "heads": h,
                    "seed": args.seed},
         "wall_ms_per_step": wall_ms, "ms_per_step_profiled": ms_prof, "kernels": kern,
+        "library_kernel_ms_per_step": lib_ms,
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline_block(gb, types, emb, proj, model, h)
@@ -899,7 +961,54 @@ def cpu_baseline_block(gb, types, emb, proj, model, heads) -> dict:
                        f"2 warm-ups")}
 
 
-def bench_stack(args):
+def count_gemm_flops(step) -> int:
+    """FLOPs of the matrix products one call of `step` runs (forward and backward): every aten mm / addmm /
+    bmm / baddbmm dispatched (in-place forms included), 2 m n k each (batch included), from its operands'
+    shapes."""
+    from torch.utils._python_dispatch import TorchDispatchMode
+
+    class GemmCount(TorchDispatchMode):
+        flops = 0
+
+        def __torch_dispatch__(self, func, types, args=(), kwargs=None):
+            name = func._overloadpacket.__name__.rstrip("_")
+            if name in ("mm", "bmm"):
+                a, b = args[0], args[1]
+            elif name in ("addmm", "baddbmm"):
+                a, b = args[1], args[2]
+            else:
+                a = b = None
+            if a is not None:
+                batch = a.shape[0] if a.dim() == 3 else 1
+                GemmCount.flops += 2 * batch * a.shape[-2] * a.shape[-1] * b.shape[-1]
+            return func(*args, **(kwargs or {}))
+
+    with GemmCount():
+        step()
+    return GemmCount.flops
+
+
+def stack_flops(step, gb, d: int, layers: str, k_seeds: int, mlp: int) -> dict:
+    """Exact FLOPs of one configuration-4 train step: the GEMMs counted as they are dispatched over one step
+    (projections, MLPs, weight and input gradients, each product with its real shape), plus the attention by
+    pair counts, 14 D per (query, key) pair for forward + backward (QK^T and PV; QK^T recomputation, dP, dV,
+    dK, dQ): the S layers' pairs are sum L^2, the masked M layers' the mask's nnz (effective), PMA's
+    k_seeds * T.  gemm_analytic restates the GEMMs from the layer shapes (3x the forward products: forward,
+    input and weight gradients) as a check of the count."""
+    gemm = count_gemm_flops(step)
+    stats = edge_mask_stats(gb.edge_index[0].astype(np.int64), gb.edge_index[1].astype(np.int64), gb.cu_seqlens)
+    t, b = gb.num_tokens, gb.num_graphs
+    n_enc = sum(1 for lt in layers[: layers.index("P")] if lt in "MS")
+    enc = n_enc * (4 * 2 * t * d * d + 2 * 2 * t * d * mlp)                  # Q, K, V, O; MLP up and down
+    pma = 2 * k_seeds * d * d + 2 * 2 * t * d * d + 2 * b * k_seeds * d * d   # seeds' Q; K, V over tokens; O
+    pma += 2 * 2 * b * k_seeds * d * mlp + 2 * b * d * d                      # PMA MLP; decoder_linear
+    attn = {"S": 14 * d * gb.sum_sq * layers.count("S"), "M": 14 * d * stats["nnz"] * layers.count("M"),
+            "P": 14 * d * k_seeds * t * layers.count("P")}
+    return {"gemm": gemm, "gemm_analytic": 3 * (enc + pma), "attention": attn, "total": gemm + sum(attn.values()),
+            "mask_nnz": stats["nnz"], "sum_L2": gb.sum_sq}
+
+
+def bench_stack(args, sub: bool = False):
     """Configuration 4: ESA encoder stack M-M-S-S-M-M-S-S-P(4 seeds), D=512, H=32, MLP 2048, bf16 train step.
 
     bf16-mixed as the reference trains (core/train_pretrain.py:753): fp32 parameters under
@@ -943,7 +1052,24 @@ def bench_stack(args):
         opt.zero_grad(set_to_none=True)
 
     ms, wall_ms, kern, ms_prof = timed(step, args.steps, args.warmup)
-    attn_ms = sum(k["avg_us"] * k["launches"] for k in kern.values()) / 1e3 / args.steps
+    lib_ms = sum(k["avg_us"] * k["launches"] for k in kern.values()) / 1e3 / args.steps
+    attn_ms = sum(k["avg_us"] * k["launches"] for n, k in kern.items() if n.startswith("attn")) / 1e3 / args.steps
+    fl = stack_flops(step, gb, d, layers, 4, 2048)
+    achieved = fl["total"] / (ms * 1e-3) / 1e12
+    roofline = {"bound": "mfma", "kernel": "whole train step (GEMMs + attention)", "achieved": achieved,
+                "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": achieved / PEAK_BF16_TFLOPS, "traffic": None,
+                "flops": "exact: GEMMs counted as dispatched over one step, attention 14 D per pair "
+                         "(S: sum L^2, M: mask nnz, P: seeds x tokens)"}
+    split = {"library_kernels_ms": lib_ms, "attention_ms": attn_ms, "other_ms": ms - lib_ms,
+             "what": "library_kernels: this library's launches by HIP events (attention, LayerNorm, Mish, column "
+                     "sums, ...), attention_ms the attention kernels among them; other: hipBLASLt GEMMs, AdamW, "
+                     "torch elementwise ops and gaps"}
+    if sub:
+        return {"workload": "config4: ESA encoder stack M-M-S-S-M-M-S-S-P(4 seeds) train step, bf16-mixed",
+                "graphs": gb.num_graphs, "edge_tokens": t, "dim": d, "heads": h, "mlp_hidden": 2048,
+                "ms_per_step": ms, "wall_ms_per_step": wall_ms, "edge_tokens_per_s": t / (ms * 1e-3),
+                "ms_per_step_profiled": ms_prof, "flops_per_step": fl, "roofline": roofline, "split": split,
+                "kernels": kern}
     result = {
         "metric": "edge-tokens/sec through the ESA encoder stack train step (fwd+bwd+AdamW, bf16-mixed)",
         "value": t / (ms * 1e-3), "unit": "edge-tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -954,7 +1080,7 @@ def bench_stack(args):
                    "graphs": gb.num_graphs, "edge_tokens": t, "max_seqlen": gb.max_seqlen, "padded_items": n,
                    "dim": d, "heads": h, "mlp_hidden": 2048, "seed": args.seed},
         "wall_ms_per_step": wall_ms, "ms_per_step_profiled": ms_prof, "kernels": kern,
-        "library_kernel_ms_per_step": attn_ms,
+        "flops_per_step": fl, "roofline": roofline, "split": split,
     }
     print(json.dumps(result), flush=True)
 

@@ -2171,9 +2171,11 @@ int esa_varlen_attn_fwd(const void* q, const void* k, const void* v, const int* 
     a.o = static_cast<float*>(out); a.lse_out = softmax_lse;
     const dim3 fgrid((unsigned)(groups_of(total_q) + batch) * (unsigned)heads);
     if (masked)
-      hipLaunchKernelGGL((attn_fwd_f32_kernel<true>), fgrid, dim3(kF32Threads), 0, st, a);
+      ESA_TIMED(esa_profile::kAttnFwdMasked, st,
+                hipLaunchKernelGGL((attn_fwd_f32_kernel<true>), fgrid, dim3(kF32Threads), 0, st, a));
     else
-      hipLaunchKernelGGL((attn_fwd_f32_kernel<false>), fgrid, dim3(kF32Threads), 0, st, a);
+      ESA_TIMED(esa_profile::kAttnFwd, st,
+                hipLaunchKernelGGL((attn_fwd_f32_kernel<false>), fgrid, dim3(kF32Threads), 0, st, a));
     ESA_LAUNCH_CHECK();
     return ESA_OK;
   }
@@ -2321,15 +2323,19 @@ int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k, const vo
     const dim3 fkgrid((unsigned)(groups_of(total_k) + batch) * (unsigned)heads);
     const dim3 fqgrid((unsigned)(groups_of(total_q) + batch) * (unsigned)heads);
     if (masked)
-      hipLaunchKernelGGL((attn_dkdv_f32_kernel<true>), fkgrid, dim3(kF32Threads), 0, st, a);
+      ESA_TIMED(esa_profile::kAttnBwdDkdvMasked, st,
+                hipLaunchKernelGGL((attn_dkdv_f32_kernel<true>), fkgrid, dim3(kF32Threads), 0, st, a));
     else
-      hipLaunchKernelGGL((attn_dkdv_f32_kernel<false>), fkgrid, dim3(kF32Threads), 0, st, a);
+      ESA_TIMED(esa_profile::kAttnBwdDkdv, st,
+                hipLaunchKernelGGL((attn_dkdv_f32_kernel<false>), fkgrid, dim3(kF32Threads), 0, st, a));
     ESA_LAUNCH_CHECK();
     a.plan = pa.plan_q; a.count = pa.count_q;
     if (masked)
-      hipLaunchKernelGGL((attn_dq_f32_kernel<true>), fqgrid, dim3(kF32Threads), 0, st, a);
+      ESA_TIMED(esa_profile::kAttnBwdDqMasked, st,
+                hipLaunchKernelGGL((attn_dq_f32_kernel<true>), fqgrid, dim3(kF32Threads), 0, st, a));
     else
-      hipLaunchKernelGGL((attn_dq_f32_kernel<false>), fqgrid, dim3(kF32Threads), 0, st, a);
+      ESA_TIMED(esa_profile::kAttnBwdDq, st,
+                hipLaunchKernelGGL((attn_dq_f32_kernel<false>), fqgrid, dim3(kF32Threads), 0, st, a));
     ESA_LAUNCH_CHECK();
     return ESA_OK;
   }
