@@ -1354,44 +1354,53 @@ struct AttnF32Args {
 
 constexpr int kF32Threads = kGroupTok;
 
-DEVI void load16(const float* p, float x[16]) {
+// Rows of HD fp32 values (HD = 16, 32 or 64) as float4 chunks.
+template <int HD>
+DEVI void loadn(const float* p, float x[HD]) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < HD / 4; ++i) {
     const float4 v = reinterpret_cast<const float4*>(p)[i];
     x[4 * i] = v.x; x[4 * i + 1] = v.y; x[4 * i + 2] = v.z; x[4 * i + 3] = v.w;
   }
 }
-DEVI void store16(float* p, const float x[16], float mul) {
+template <int HD>
+DEVI void storen(float* p, const float x[HD], float mul) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < HD / 4; ++i)
     reinterpret_cast<float4*>(p)[i] = make_float4(x[4 * i] * mul, x[4 * i + 1] * mul, x[4 * i + 2] * mul,
                                                   x[4 * i + 3] * mul);
 }
-DEVI float dot16(const float x[16], const float4* y) {
+template <int HD>
+DEVI float dotn(const float x[HD], const float4* y) {
   float s = 0.f;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < HD / 4; ++i) {
     const float4 v = y[i];
     s = fmaf(x[4 * i], v.x, s); s = fmaf(x[4 * i + 1], v.y, s);
     s = fmaf(x[4 * i + 2], v.z, s); s = fmaf(x[4 * i + 3], v.w, s);
   }
   return s;
 }
-DEVI void axpy16(float a, const float4* y, float x[16]) {
+template <int HD>
+DEVI void axpyn(float a, const float4* y, float x[HD]) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < HD / 4; ++i) {
     const float4 v = y[i];
     x[4 * i] = fmaf(a, v.x, x[4 * i]); x[4 * i + 1] = fmaf(a, v.y, x[4 * i + 1]);
     x[4 * i + 2] = fmaf(a, v.z, x[4 * i + 2]); x[4 * i + 3] = fmaf(a, v.w, x[4 * i + 3]);
   }
 }
 
-// Stage the 32 tokens from t0 of a [T][H][16] fp32 tensor into LDS [32][4]
-// float4 (128 threads, one float4 each); tokens at or past `end` read as zeros.
-DEVI void stage_rows_f32(float4 (*dst)[4], const float* src, int end, int H, int head, int t0, int tid) {
-  const int t = t0 + (tid >> 2), part = tid & 3;
-  dst[tid >> 2][part] = t < end ? reinterpret_cast<const float4*>(src + ((size_t)t * H + head) * kHd)[part]
-                                : make_float4(0.f, 0.f, 0.f, 0.f);
+// Stage the 32 tokens from t0 of a [T][H][HD] fp32 tensor into LDS [32][HD / 4]
+// float4 (128 threads, HD / 16 float4 each); tokens at or past `end` read as zeros.
+template <int HD>
+DEVI void stage_rows_f32(float4 (*dst)[HD / 4], const float* src, int end, int H, int head, int t0, int tid) {
+#pragma unroll
+  for (int i = tid; i < kTile * HD / 4; i += kF32Threads) {
+    const int t = t0 + i / (HD / 4), part = i % (HD / 4);
+    dst[i / (HD / 4)][part] = t < end ? reinterpret_cast<const float4*>(src + ((size_t)t * H + head) * HD)[part]
+                                      : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
 }
 
 // Admissible partner p (below the segment's partner end phi) of outer token oi.
@@ -1415,9 +1424,9 @@ DEVI F32Outer f32_outer(const int4& g, int tid) {
   return o;
 }
 
-template <bool MASKED>
+template <bool MASKED, int HD>
 __global__ __launch_bounds__(kF32Threads) void attn_fwd_f32_kernel(const AttnF32Args a) {
-  __shared__ float4 sK[kTile][4], sV[kTile][4];
+  __shared__ float4 sK[kTile][HD / 4], sV[kTile][HD / 4];
   __shared__ int2 sN[kTile];
   const int tid = threadIdx.x, H = a.heads;
   const int item = blockIdx.x / H, head = blockIdx.x - item * H;
@@ -1425,16 +1434,16 @@ __global__ __launch_bounds__(kF32Threads) void attn_fwd_f32_kernel(const AttnF32
   const F32Outer ot = f32_outer(a.plan[item], tid);
   const int oi = ot.oi, oc = ot.oc, phi = ot.phi;
   const bool valid = ot.valid;
-  float q[16], acc[16];
-  load16(a.q + ((size_t)oc * H + head) * kHd, q);
+  float q[HD], acc[HD];
+  loadn<HD>(a.q + ((size_t)oc * H + head) * HD, q);
 #pragma unroll
-  for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+  for (int i = 0; i < HD; ++i) acc[i] = 0.f;
   const int2 own = MASKED ? a.nodes[oc] : make_int2(0, 0);
   float m = -INFINITY, l = 0.f;
   for (int k0 = ot.plo; k0 < phi; k0 += kTile) {
     __syncthreads();
-    stage_rows_f32(sK, a.k, phi, H, head, k0, tid);
-    stage_rows_f32(sV, a.v, phi, H, head, k0, tid);
+    stage_rows_f32<HD>(sK, a.k, phi, H, head, k0, tid);
+    stage_rows_f32<HD>(sV, a.v, phi, H, head, k0, tid);
     if (MASKED && tid < kTile) sN[tid] = k0 + tid < phi ? a.nodes[k0 + tid] : make_int2(-1, -1);
     __syncthreads();
     if (!valid) continue;
@@ -1443,7 +1452,7 @@ __global__ __launch_bounds__(kF32Threads) void attn_fwd_f32_kernel(const AttnF32
 #pragma unroll
     for (int j = 0; j < kTile; ++j) {
       const int2 pn = MASKED ? sN[j] : make_int2(0, 0);
-      s[j] = admissible_f32<MASKED>(k0 + j, phi, oi, pn, own) ? a.c * dot16(q, sK[j]) : -INFINITY;
+      s[j] = admissible_f32<MASKED>(k0 + j, phi, oi, pn, own) ? a.c * dotn<HD>(q, sK[j]) : -INFINITY;
       mt = fmaxf(mt, s[j]);
     }
     if (mt == -INFINITY) continue;
@@ -1451,25 +1460,25 @@ __global__ __launch_bounds__(kF32Threads) void attn_fwd_f32_kernel(const AttnF32
       const float alpha = fast_exp2(m - mt);   // 0 while m = -inf
       l *= alpha;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) acc[i] *= alpha;
+      for (int i = 0; i < HD; ++i) acc[i] *= alpha;
       m = mt;
     }
 #pragma unroll
     for (int j = 0; j < kTile; ++j) {
       const float p = fast_exp2(s[j] - m);
       l += p;
-      axpy16(p, sV[j], acc);
+      axpyn<HD>(p, sV[j], acc);
     }
   }
   if (!valid) return;
-  store16(a.o + ((size_t)oi * H + head) * kHd, acc, l > 0.f ? 1.f / l : 0.f);
+  storen<HD>(a.o + ((size_t)oi * H + head) * HD, acc, l > 0.f ? 1.f / l : 0.f);
   a.lse_out[(size_t)head * a.total_q + oi] = l > 0.f ? (m + fast_log2(l)) * kLn2 : -INFINITY;
 }
 
 // dQ = scale * sum_j P_ij (dP_ij - D_i) k_j, P recomputed from the saved LSE.
-template <bool MASKED>
+template <bool MASKED, int HD>
 __global__ __launch_bounds__(kF32Threads) void attn_dq_f32_kernel(const AttnF32Args a) {
-  __shared__ float4 sK[kTile][4], sV[kTile][4];
+  __shared__ float4 sK[kTile][HD / 4], sV[kTile][HD / 4];
   __shared__ int2 sN[kTile];
   const int tid = threadIdx.x, H = a.heads;
   const int item = blockIdx.x / H, head = blockIdx.x - item * H;
@@ -1477,17 +1486,17 @@ __global__ __launch_bounds__(kF32Threads) void attn_dq_f32_kernel(const AttnF32A
   const F32Outer ot = f32_outer(a.plan[item], tid);
   const int oi = ot.oi, oc = ot.oc, phi = ot.phi;
   const bool valid = ot.valid;
-  float q[16], g[16], acc[16];
-  load16(a.q + ((size_t)oc * H + head) * kHd, q);
-  load16(a.dout + ((size_t)oc * H + head) * kHd, g);
+  float q[HD], g[HD], acc[HD];
+  loadn<HD>(a.q + ((size_t)oc * H + head) * HD, q);
+  loadn<HD>(a.dout + ((size_t)oc * H + head) * HD, g);
 #pragma unroll
-  for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+  for (int i = 0; i < HD; ++i) acc[i] = 0.f;
   const float2 rs = a.rows[(size_t)head * a.tq_pad + oc];   // (LSE2, D)
   const int2 own = MASKED ? a.nodes[oc] : make_int2(0, 0);
   for (int k0 = ot.plo; k0 < phi; k0 += kTile) {
     __syncthreads();
-    stage_rows_f32(sK, a.k, phi, H, head, k0, tid);
-    stage_rows_f32(sV, a.v, phi, H, head, k0, tid);
+    stage_rows_f32<HD>(sK, a.k, phi, H, head, k0, tid);
+    stage_rows_f32<HD>(sV, a.v, phi, H, head, k0, tid);
     if (MASKED && tid < kTile) sN[tid] = k0 + tid < phi ? a.nodes[k0 + tid] : make_int2(-1, -1);
     __syncthreads();
     if (!valid) continue;
@@ -1495,20 +1504,20 @@ __global__ __launch_bounds__(kF32Threads) void attn_dq_f32_kernel(const AttnF32A
     for (int j = 0; j < kTile; ++j) {
       const int2 pn = MASKED ? sN[j] : make_int2(0, 0);
       if (!admissible_f32<MASKED>(k0 + j, phi, oi, pn, own)) continue;
-      const float p = fast_exp2(a.c * dot16(q, sK[j]) - rs.x);
-      const float ds = p * (dot16(g, sV[j]) - rs.y);
-      axpy16(ds, sK[j], acc);
+      const float p = fast_exp2(a.c * dotn<HD>(q, sK[j]) - rs.x);
+      const float ds = p * (dotn<HD>(g, sV[j]) - rs.y);
+      axpyn<HD>(ds, sK[j], acc);
     }
   }
   if (!valid) return;
-  store16(a.dq + ((size_t)oi * H + head) * kHd, acc, a.scale);
+  storen<HD>(a.dq + ((size_t)oi * H + head) * HD, acc, a.scale);
 }
 
 // dV = sum_i P_ij dO_i, dK = scale * sum_i P_ij (dP_ij - D_i) q_i, one thread
 // per key; the partner tiles are query tiles with their (LSE2, D).
-template <bool MASKED>
+template <bool MASKED, int HD>
 __global__ __launch_bounds__(kF32Threads) void attn_dkdv_f32_kernel(const AttnF32Args a) {
-  __shared__ float4 sQ[kTile][4], sG[kTile][4];
+  __shared__ float4 sQ[kTile][HD / 4], sG[kTile][HD / 4];
   __shared__ float2 sR[kTile];
   __shared__ int2 sN[kTile];
   const int tid = threadIdx.x, H = a.heads;
@@ -1517,16 +1526,16 @@ __global__ __launch_bounds__(kF32Threads) void attn_dkdv_f32_kernel(const AttnF3
   const F32Outer ot = f32_outer(a.plan[item], tid);
   const int oi = ot.oi, oc = ot.oc, phi = ot.phi;
   const bool valid = ot.valid;
-  float kx[16], vx[16], dk[16], dv[16];
-  load16(a.k + ((size_t)oc * H + head) * kHd, kx);
-  load16(a.v + ((size_t)oc * H + head) * kHd, vx);
+  float kx[HD], vx[HD], dk[HD], dv[HD];
+  loadn<HD>(a.k + ((size_t)oc * H + head) * HD, kx);
+  loadn<HD>(a.v + ((size_t)oc * H + head) * HD, vx);
 #pragma unroll
-  for (int i = 0; i < 16; ++i) dk[i] = dv[i] = 0.f;
+  for (int i = 0; i < HD; ++i) dk[i] = dv[i] = 0.f;
   const int2 own = MASKED ? a.nodes[oc] : make_int2(0, 0);
   for (int q0 = ot.plo; q0 < phi; q0 += kTile) {
     __syncthreads();
-    stage_rows_f32(sQ, a.q, phi, H, head, q0, tid);
-    stage_rows_f32(sG, a.dout, phi, H, head, q0, tid);
+    stage_rows_f32<HD>(sQ, a.q, phi, H, head, q0, tid);
+    stage_rows_f32<HD>(sG, a.dout, phi, H, head, q0, tid);
     if (tid < kTile) {
       const bool in = q0 + tid < phi;
       sR[tid] = in ? a.rows[(size_t)head * a.tq_pad + q0 + tid] : make_float2(INFINITY, 0.f);
@@ -1539,15 +1548,15 @@ __global__ __launch_bounds__(kF32Threads) void attn_dkdv_f32_kernel(const AttnF3
       const int2 pn = MASKED ? sN[i] : make_int2(0, 0);
       if (!admissible_f32<MASKED>(q0 + i, phi, oi, pn, own)) continue;
       const float2 rs = sR[i];
-      const float p = fast_exp2(a.c * dot16(kx, sQ[i]) - rs.x);
-      axpy16(p, sG[i], dv);
-      const float ds = p * (dot16(vx, sG[i]) - rs.y);
-      axpy16(ds, sQ[i], dk);
+      const float p = fast_exp2(a.c * dotn<HD>(kx, sQ[i]) - rs.x);
+      axpyn<HD>(p, sG[i], dv);
+      const float ds = p * (dotn<HD>(vx, sG[i]) - rs.y);
+      axpyn<HD>(ds, sQ[i], dk);
     }
   }
   if (!valid) return;
-  store16(a.dv + ((size_t)oi * H + head) * kHd, dv, 1.f);
-  store16(a.dk + ((size_t)oi * H + head) * kHd, dk, a.scale);
+  storen<HD>(a.dv + ((size_t)oi * H + head) * HD, dv, 1.f);
+  storen<HD>(a.dk + ((size_t)oi * H + head) * HD, dk, a.scale);
 }
 
 // ======================================================================== prep kernel
@@ -1565,6 +1574,7 @@ enum PrepTask { kPlanQ, kPlanK, kMeta, kNodes, kBoundsQ, kBoundsK, kRows, kPrepT
 struct PrepArgs {
   const int* cu_q; const int* cu_k; int nseg;
   int total_q, total_k, heads, tq_pad, tk_pad;
+  int head_dim;                        // backward row statistics (fp32): dims per head row
   int4* plan_q; int4* plan_k;          // fp32: per-segment plans (seg_plan_block), plan_k backward only
   int* count_q; int* count_k;          // fp32: their group counts
   int2* bounds_q; int2* bounds_k;      // edge plan
@@ -1589,11 +1599,12 @@ DEVI void rowstats_item(const PrepArgs& p, long idx) {
     if (t < p.total_q) {
       const float l = p.lse[(size_t)h * p.total_q + t];
       if (l != -INFINITY) l2 = l * kLog2e;
-      float o[16], g[16];
-      load16(p.out_f + ((size_t)t * p.heads + h) * kHd, o);
-      load16(p.dout_f + ((size_t)t * p.heads + h) * kHd, g);
-#pragma unroll
-      for (int e = 0; e < 16; ++e) d = fmaf(g[e], o[e], d);
+      const float4* po = reinterpret_cast<const float4*>(p.out_f + ((size_t)t * p.heads + h) * p.head_dim);
+      const float4* pg = reinterpret_cast<const float4*>(p.dout_f + ((size_t)t * p.heads + h) * p.head_dim);
+      for (int i = 0; i < p.head_dim / 4; ++i) {
+        const float4 o = po[i], g = pg[i];
+        d = fmaf(g.x, o.x, d); d = fmaf(g.y, o.y, d); d = fmaf(g.z, o.z, d); d = fmaf(g.w, o.w, d);
+      }
     }
     p.rows_f[(size_t)h * p.tq_pad + t] = make_float2(l2, d);
     return;
@@ -1786,12 +1797,21 @@ struct WsLayout {
   size_t aux = 0, plan_q = 0, plan_k = 0, plan = 0, total = 0;
 };
 
-WsLayout ws_layout(int total_q, int total_k, int heads, int dtype, int mask_kind, bool backward, bool key_lists) {
+// The edge mask at head dims other than 16 runs the gather kernels over the
+// plan's lists (both dtypes): the plan with its lists, and for the backward
+// the per-(head, query) D of the gather kernels, which fits in the aux region.
+bool edge_gathered(int mask_kind, int head_dim) {
+  return (mask_kind == ESA_MASK_EDGE || mask_kind == ESA_MASK_EDGE_PLAN) && head_dim != kHd;
+}
+
+WsLayout ws_layout(int total_q, int total_k, int heads, int dtype, int mask_kind, bool backward, bool key_lists,
+                   int head_dim) {
   WsLayout L;
   const int tqp = round32(total_q);
+  const bool gathered = edge_gathered(mask_kind, head_dim);
   size_t off = 0;
   if (backward) { L.aux = off; off += align256((size_t)heads * tqp * 8); }   // bf16: uint2 (hi, lo); fp32: float2
-  if (dtype == ESA_F32) {
+  if (dtype == ESA_F32 && !gathered) {
     // a 16-byte group count, then per-segment groups (at most ceil(T / 128) + number of segments <= T)
     auto plan_size = [&](int t) { return align256(16 + ((size_t)groups_of(t) + t + 1) * 16); };
     L.plan_q = off; off += plan_size(total_q);
@@ -1800,7 +1820,7 @@ WsLayout ws_layout(int total_q, int total_k, int heads, int dtype, int mask_kind
   if (mask_kind == ESA_MASK_EDGE) {
     const PlanLayout P = plan_layout(total_q, total_k, key_lists);
     L.plan = off;
-    off += dtype == ESA_F32 ? align256(P.prep_end) : P.total;
+    off += dtype == ESA_F32 && !gathered ? align256(P.prep_end) : P.total;
   }
   L.total = off;
   return L;
@@ -1896,13 +1916,18 @@ __global__ __launch_bounds__(256) void edge_plan_decode_kernel(const PlanView V,
 
 bool misaligned(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) != 0; }
 
+// Head dims: 16 on every path; 32 and 64 on the node-mode and edge-mask
+// gather kernels, the fp32 kernels and the dense bf16 kernels of
+// esa_attn_wide.hip.
+bool head_dim_ok(int head_dim) { return head_dim == 16 || head_dim == 32 || head_dim == 64; }
+
 int check_common(int batch, int total_q, int total_k, int heads, int head_dim, int dtype, int mask_kind) {
-  if (head_dim != kHd) return ESA_ERR_HEAD_DIM;
+  if (!head_dim_ok(head_dim)) return ESA_ERR_HEAD_DIM;
   if (dtype != ESA_BF16 && dtype != ESA_F32) return ESA_ERR_DTYPE;
   if (batch < 1 || heads < 1 || total_q < 0 || total_k < 0) return ESA_ERR_SHAPE;
   // Buffer-resource ranges are 32-bit byte counts.
-  const long lim = (1L << 31) - 1;
-  if ((long)round32(total_q) * heads * 32 > lim || (long)round32(total_k) * heads * 32 > lim) return ESA_ERR_SHAPE;
+  const long lim = (1L << 31) - 1, row = (long)heads * head_dim * (dtype == ESA_F32 ? 4 : 2);
+  if ((long)round32(total_q) * row > lim || (long)round32(total_k) * row > lim) return ESA_ERR_SHAPE;
   if (mask_kind != ESA_MASK_NONE && mask_kind != ESA_MASK_EDGE && mask_kind != ESA_MASK_NODE &&
       mask_kind != ESA_MASK_EDGE_PLAN && mask_kind != ESA_MASK_NODE_PLAN)
     return ESA_ERR_MASK;
@@ -2012,6 +2037,34 @@ int call_plan(int mask_kind, const int* mask_a, const int* mask_b, const int* cu
   return build_edge_plan(mask_a, mask_b, cu_q, cu_k, batch, total_q, total_k, ws + L.plan, key_lists, st, lists);
 }
 
+// Arguments of the gather kernels for the edge mask at head dims 32 / 64: the
+// plan's lists, node pairs, flag and per-token partner ranges.
+GraphAttnArgs edge_gather_args(const void* plan, const void* q, const void* k, const void* v, const int* cu_q,
+                               const int* cu_k, int batch, int total_q, int total_k, int heads, int head_dim,
+                               float scale) {
+  const PlanView V = plan_view(plan, total_q, total_k);
+  GraphAttnArgs g{};
+  g.q = q; g.k = k; g.v = v; g.cu_q = cu_q; g.cu_k = cu_k; g.nseg = batch;
+  g.total_q = total_q; g.total_k = total_k; g.heads = heads; g.head_dim = head_dim;
+  g.c = scale * kLog2e; g.scale = scale;
+  g.q_bounds = V.bounds_q; g.k_bounds = V.bounds_k;
+  g.edge.sym = V.flags; g.edge.nodes = V.nodes; g.edge.cap = kListCap;
+  for (int d = 0; d < 2; ++d) {
+    g.edge.info[d] = V.info[d];
+    g.edge.ids[d] = V.ids[d];
+    g.edge.bits[d] = V.bits[d];
+  }
+  return g;
+}
+
+// KERNEL<false, HD> (the fp32 kernels without a mask) for head dim 16, 32 or 64.
+#define ESA_F32_LAUNCH(KERNEL, hd, grid, st, a)                                             \
+  do {                                                                                      \
+    if (hd == 16) hipLaunchKernelGGL((KERNEL<false, 16>), grid, dim3(kF32Threads), 0, st, a);       \
+    else if (hd == 32) hipLaunchKernelGGL((KERNEL<false, 32>), grid, dim3(kF32Threads), 0, st, a);  \
+    else hipLaunchKernelGGL((KERNEL<false, 64>), grid, dim3(kF32Threads), 0, st, a);               \
+  } while (0)
+
 // Scratch of esa_varlen_attn_fwd_noalloc: a file-scope device array, one
 // copy per GPU, held until the process ends.  Host code never passes the
 // array's name (a host-side stand-in) to a kernel: it passes the device
@@ -2057,12 +2110,10 @@ int esa_varlen_attn_workspace_size(int total_q, int total_k, int heads, int head
     return graph_attn_workspace_size(total_q, total_k, heads, n_mask_edges, backward != 0,
                                      mask_kind == ESA_MASK_NODE_PLAN, bytes);
   }
-  if (mask_kind == ESA_MASK_NONE && dtype == ESA_BF16) {
-    *bytes = dense_attn_workspace_size(total_q, total_k, heads, backward != 0);
-    return ESA_OK;
-  }
+  if (mask_kind == ESA_MASK_NONE && dtype == ESA_BF16)
+    return dense_attn_workspace_size(total_q, total_k, heads, head_dim, backward != 0, bytes);
   // a backward call that builds its plan may need the key tiles' lists (distinct segment arrays)
-  *bytes = ws_layout(total_q, total_k, heads, dtype, mask_kind, backward != 0, backward != 0).total;
+  *bytes = ws_layout(total_q, total_k, heads, dtype, mask_kind, backward != 0, backward != 0, head_dim).total;
   return ESA_OK;
 }
 
@@ -2120,7 +2171,7 @@ int esa_varlen_attn_fwd(const void* q, const void* k, const void* v, const int* 
     if (!(softmax_scale > 0.f)) return ESA_ERR_SHAPE;
     GraphAttnArgs g{};
     g.q = q; g.k = k; g.v = v; g.cu_q = cu_seqlens_q; g.cu_k = cu_seqlens_k; g.nseg = batch;
-    g.total_q = total_q; g.total_k = total_k; g.heads = heads;
+    g.total_q = total_q; g.total_k = total_k; g.heads = heads; g.head_dim = head_dim;
     g.indptr = mask_a; g.indices = mask_b; g.nnz = n_mask_edges;
     g.c = softmax_scale * kLog2e; g.scale = softmax_scale;
     g.out = out; g.lse = softmax_lse;
@@ -2141,19 +2192,26 @@ int esa_varlen_attn_fwd(const void* q, const void* k, const void* v, const int* 
     if (!workspace) return ESA_ERR_NULL;
     DenseAttnCall c{};
     c.q = q; c.k = k; c.v = v; c.cu_q = cu_seqlens_q; c.cu_k = cu_seqlens_k; c.nseg = batch;
-    c.total_q = total_q; c.total_k = total_k; c.heads = heads; c.scale = softmax_scale;
+    c.total_q = total_q; c.total_k = total_k; c.heads = heads; c.head_dim = head_dim; c.scale = softmax_scale;
     c.out = out; c.lse = softmax_lse;
     return dense_attn_fwd(c, workspace, workspace_bytes, st);
   }
-  const WsLayout L = ws_layout(total_q, total_k, heads, dtype, mask_kind, false, false);
+  const bool gathered = edge_gathered(mask_kind, head_dim);
+  const WsLayout L = ws_layout(total_q, total_k, heads, dtype, mask_kind, false, false, head_dim);
   if (workspace_bytes < L.total) return ESA_ERR_WORKSPACE;
   if (L.total && !workspace) return ESA_ERR_NULL;
   char* ws = static_cast<char*>(workspace);
   const void* plan = nullptr;
   if (masked && (rc = call_plan(mask_kind, mask_a, mask_b, cu_seqlens_q, cu_seqlens_k, batch, total_q, total_k, ws,
-                                L, false, !f32, st, &plan)))
+                                L, false, !f32 || gathered, st, &plan)))
     return rc;
 
+  if (gathered) {   // the edge mask at head dims 32 / 64: gather kernels over the plan's lists
+    GraphAttnArgs g = edge_gather_args(plan, q, k, v, cu_seqlens_q, cu_seqlens_k, batch, total_q, total_k, heads,
+                                       head_dim, softmax_scale);
+    g.out = out; g.lse = softmax_lse;
+    return graph_edge_attn_fwd(g, dtype, st);
+  }
   if (f32) {
     PrepArgs pa{};
     pa.cu_q = cu_seqlens_q; pa.cu_k = cu_seqlens_k; pa.nseg = batch;
@@ -2170,12 +2228,11 @@ int esa_varlen_attn_fwd(const void* q, const void* k, const void* v, const int* 
     a.plan = pa.plan_q; a.count = pa.count_q;
     a.o = static_cast<float*>(out); a.lse_out = softmax_lse;
     const dim3 fgrid((unsigned)(groups_of(total_q) + batch) * (unsigned)heads);
-    if (masked)
+    if (masked)   // head_dim 16 (other head dims take the gather kernels)
       ESA_TIMED(esa_profile::kAttnFwdMasked, st,
-                hipLaunchKernelGGL((attn_fwd_f32_kernel<true>), fgrid, dim3(kF32Threads), 0, st, a));
+                hipLaunchKernelGGL((attn_fwd_f32_kernel<true, 16>), fgrid, dim3(kF32Threads), 0, st, a));
     else
-      ESA_TIMED(esa_profile::kAttnFwd, st,
-                hipLaunchKernelGGL((attn_fwd_f32_kernel<false>), fgrid, dim3(kF32Threads), 0, st, a));
+      ESA_TIMED(esa_profile::kAttnFwd, st, ESA_F32_LAUNCH(attn_fwd_f32_kernel, head_dim, fgrid, st, a));
     ESA_LAUNCH_CHECK();
     return ESA_OK;
   }
@@ -2251,7 +2308,7 @@ int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k, const vo
     if (!(softmax_scale > 0.f)) return ESA_ERR_SHAPE;
     GraphAttnArgs g{};
     g.q = q; g.k = k; g.v = v; g.cu_q = cu_seqlens_q; g.cu_k = cu_seqlens_k; g.nseg = batch;
-    g.total_q = total_q; g.total_k = total_k; g.heads = heads;
+    g.total_q = total_q; g.total_k = total_k; g.heads = heads; g.head_dim = head_dim;
     g.indptr = mask_a; g.indices = mask_b; g.nnz = n_mask_edges;
     g.c = softmax_scale * kLog2e; g.scale = softmax_scale;
     g.out_in = out; g.dout = dout; g.lse_in = softmax_lse;
@@ -2276,28 +2333,36 @@ int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k, const vo
   if (total_q == 0 || total_k == 0) {
     // No query/key pairs: every gradient is zero (a fill kernel, so the call
     // stays capturable in a HIP graph).
-    if ((rc = launch_zero(dq, (size_t)total_q * heads * kHd * esz, st))) return rc;
-    if ((rc = launch_zero(dk, (size_t)total_k * heads * kHd * esz, st))) return rc;
-    if ((rc = launch_zero(dv, (size_t)total_k * heads * kHd * esz, st))) return rc;
+    if ((rc = launch_zero(dq, (size_t)total_q * heads * head_dim * esz, st))) return rc;
+    if ((rc = launch_zero(dk, (size_t)total_k * heads * head_dim * esz, st))) return rc;
+    if ((rc = launch_zero(dv, (size_t)total_k * heads * head_dim * esz, st))) return rc;
     return ESA_OK;
   }
   if (!masked && !f32) {
     DenseAttnCall c{};
     c.q = q; c.k = k; c.v = v; c.cu_q = cu_seqlens_q; c.cu_k = cu_seqlens_k; c.nseg = batch;
-    c.total_q = total_q; c.total_k = total_k; c.heads = heads; c.scale = softmax_scale;
+    c.total_q = total_q; c.total_k = total_k; c.heads = heads; c.head_dim = head_dim; c.scale = softmax_scale;
     c.out_in = out; c.dout = dout; c.lse_in = softmax_lse; c.dq = dq; c.dk = dk; c.dv = dv;
     return dense_attn_bwd(c, workspace, workspace_bytes, st);
   }
   // A plan built here has the key tiles' own lists when the segment arrays are distinct.
   const bool key_lists = cu_seqlens_q != cu_seqlens_k;
-  const WsLayout L = ws_layout(total_q, total_k, heads, dtype, mask_kind, true, key_lists);
+  const bool gathered = edge_gathered(mask_kind, head_dim);
+  const WsLayout L = ws_layout(total_q, total_k, heads, dtype, mask_kind, true, key_lists, head_dim);
   if (workspace_bytes < L.total) return ESA_ERR_WORKSPACE;
   char* ws = static_cast<char*>(workspace);
   const void* plan = nullptr;
   if (masked && (rc = call_plan(mask_kind, mask_a, mask_b, cu_seqlens_q, cu_seqlens_k, batch, total_q, total_k, ws,
-                                L, key_lists, !f32, st, &plan)))
+                                L, key_lists, !f32 || gathered, st, &plan)))
     return rc;
 
+  if (gathered) {   // the edge mask at head dims 32 / 64: gather kernels over the plan's lists
+    GraphAttnArgs g = edge_gather_args(plan, q, k, v, cu_seqlens_q, cu_seqlens_k, batch, total_q, total_k, heads,
+                                       head_dim, softmax_scale);
+    g.out_in = out; g.dout = dout; g.lse_in = softmax_lse;
+    g.dq = dq; g.dk = dk; g.dv = dv;
+    return graph_edge_attn_bwd(g, dtype, ws + L.aux, workspace_bytes - L.aux, st);
+  }
   if (f32) {
     PrepArgs pa{};
     pa.cu_q = cu_seqlens_q; pa.cu_k = cu_seqlens_k; pa.nseg = batch;
@@ -2310,6 +2375,7 @@ int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k, const vo
     pa.lse = softmax_lse; pa.c = softmax_scale * kLog2e;
     pa.dout_f = static_cast<const float*>(dout); pa.out_f = static_cast<const float*>(out);
     pa.rows_f = reinterpret_cast<float2*>(ws + L.aux);
+    pa.head_dim = head_dim;
     if ((rc = launch_prep(pa, kTaskPlanQ | kTaskPlanK | kTaskRows, st))) return rc;
     AttnF32Args a{};
     a.q = static_cast<const float*>(q); a.k = static_cast<const float*>(k); a.v = static_cast<const float*>(v);
@@ -2322,20 +2388,18 @@ int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k, const vo
     a.plan = pa.plan_k; a.count = pa.count_k;
     const dim3 fkgrid((unsigned)(groups_of(total_k) + batch) * (unsigned)heads);
     const dim3 fqgrid((unsigned)(groups_of(total_q) + batch) * (unsigned)heads);
-    if (masked)
+    if (masked)   // head_dim 16 (other head dims take the gather kernels)
       ESA_TIMED(esa_profile::kAttnBwdDkdvMasked, st,
-                hipLaunchKernelGGL((attn_dkdv_f32_kernel<true>), fkgrid, dim3(kF32Threads), 0, st, a));
+                hipLaunchKernelGGL((attn_dkdv_f32_kernel<true, 16>), fkgrid, dim3(kF32Threads), 0, st, a));
     else
-      ESA_TIMED(esa_profile::kAttnBwdDkdv, st,
-                hipLaunchKernelGGL((attn_dkdv_f32_kernel<false>), fkgrid, dim3(kF32Threads), 0, st, a));
+      ESA_TIMED(esa_profile::kAttnBwdDkdv, st, ESA_F32_LAUNCH(attn_dkdv_f32_kernel, head_dim, fkgrid, st, a));
     ESA_LAUNCH_CHECK();
     a.plan = pa.plan_q; a.count = pa.count_q;
     if (masked)
       ESA_TIMED(esa_profile::kAttnBwdDqMasked, st,
-                hipLaunchKernelGGL((attn_dq_f32_kernel<true>), fqgrid, dim3(kF32Threads), 0, st, a));
+                hipLaunchKernelGGL((attn_dq_f32_kernel<true, 16>), fqgrid, dim3(kF32Threads), 0, st, a));
     else
-      ESA_TIMED(esa_profile::kAttnBwdDq, st,
-                hipLaunchKernelGGL((attn_dq_f32_kernel<false>), fqgrid, dim3(kF32Threads), 0, st, a));
+      ESA_TIMED(esa_profile::kAttnBwdDq, st, ESA_F32_LAUNCH(attn_dq_f32_kernel, head_dim, fqgrid, st, a));
     ESA_LAUNCH_CHECK();
     return ESA_OK;
   }
@@ -2389,11 +2453,11 @@ int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k, const vo
 static int pma_layout(int batch, int k_seeds, int total_k, int heads, int head_dim, int dtype, bool backward,
                       size_t off[4], size_t* total) {
   if (batch < 1 || k_seeds < 1 || total_k < 0 || heads < 1) return ESA_ERR_SHAPE;
-  if (head_dim != kHd) return ESA_ERR_HEAD_DIM;
+  if (!head_dim_ok(head_dim)) return ESA_ERR_HEAD_DIM;
   if (dtype != ESA_BF16 && dtype != ESA_F32) return ESA_ERR_DTYPE;
   const long tq = (long)batch * k_seeds;
   if (tq > INT32_MAX / 2) return ESA_ERR_SHAPE;
-  const size_t rows = (size_t)tq * heads * kHd * (dtype == ESA_F32 ? 4 : 2);
+  const size_t rows = (size_t)tq * heads * head_dim * (dtype == ESA_F32 ? 4 : 2);
   size_t inner = 0;
   const int rc = esa_varlen_attn_workspace_size((int)tq, total_k, heads, head_dim, dtype, ESA_MASK_NONE, 0,
                                                 backward ? 1 : 0, &inner);
@@ -2407,9 +2471,9 @@ static int pma_layout(int batch, int k_seeds, int total_k, int heads, int head_d
   return ESA_OK;
 }
 
-static int pma_expand(const void* q, int batch, int k_seeds, int heads, int dtype, char* ws, const size_t off[4],
-                      hipStream_t st) {
-  const int row16 = heads * kHd * (dtype == ESA_F32 ? 4 : 2) / 16;
+static int pma_expand(const void* q, int batch, int k_seeds, int heads, int head_dim, int dtype, char* ws,
+                      const size_t off[4], hipStream_t st) {
+  const int row16 = heads * head_dim * (dtype == ESA_F32 ? 4 : 2) / 16;
   const long n = (long)batch * k_seeds * row16;
   const long g = std::min<long>(std::max<long>((n + 255) / 256, (batch + 1 + 255) / 256), 65536);
   hipLaunchKernelGGL(pma_expand_kernel, dim3((unsigned)g), dim3(256), 0, st, static_cast<const uint4*>(q), row16,
@@ -2436,7 +2500,7 @@ int esa_pma_fwd(const void* q, const void* k, const void* v, const int* cu_seqle
   if (misaligned(q) || misaligned(workspace)) return ESA_ERR_ALIGN;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
-  if ((rc = pma_expand(q, batch, k_seeds, heads, dtype, ws, off, st))) return rc;
+  if ((rc = pma_expand(q, batch, k_seeds, heads, head_dim, dtype, ws, off, st))) return rc;
   return esa_varlen_attn_fwd(ws + off[0], k, v, reinterpret_cast<const int*>(ws + off[1]), cu_seqlens_k, batch,
                              batch * k_seeds, total_k, k_seeds, max_seqlen_k, heads, head_dim, dtype, softmax_scale,
                              ESA_MASK_NONE, nullptr, nullptr, 0, out, softmax_lse, ws + off[3], need - off[3], stream);
@@ -2455,13 +2519,13 @@ int esa_pma_bwd(const void* dout, const void* q, const void* k, const void* v, c
   if (misaligned(q) || misaligned(workspace)) return ESA_ERR_ALIGN;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
-  if ((rc = pma_expand(q, batch, k_seeds, heads, dtype, ws, off, st))) return rc;
+  if ((rc = pma_expand(q, batch, k_seeds, heads, head_dim, dtype, ws, off, st))) return rc;
   rc = esa_varlen_attn_bwd(dout, ws + off[0], k, v, out, softmax_lse, reinterpret_cast<const int*>(ws + off[1]),
                            cu_seqlens_k, batch, batch * k_seeds, total_k, k_seeds, max_seqlen_k, heads, head_dim,
                            dtype, softmax_scale, ESA_MASK_NONE, nullptr, nullptr, 0, ws + off[2], dk, dv,
                            ws + off[3], need - off[3], stream);
   if (rc) return rc;
-  const int row_elems = heads * kHd;
+  const int row_elems = heads * head_dim;
   const long n = (long)k_seeds * row_elems;
   const unsigned g = (unsigned)std::min<long>((n + 255) / 256, 65536);
   if (dtype == ESA_F32)

@@ -8,13 +8,19 @@
 struct DenseAttnCall {
   const void* q; const void* k; const void* v;
   const int* cu_q; const int* cu_k; int nseg;
-  int total_q, total_k, heads;
+  int total_q, total_k, heads, head_dim;
   float scale;
   void* out; float* lse;                             // forward outputs
   const void* out_in; const void* dout; const float* lse_in;   // backward inputs
   void* dq; void* dk; void* dv;                      // backward outputs
 };
 
-size_t dense_attn_workspace_size(int total_q, int total_k, int heads, bool backward);
+// head_dim 16: the kernels of esa_attn_dense.hip; 32 and 64: esa_attn_wide.hip.
+int dense_attn_workspace_size(int total_q, int total_k, int heads, int head_dim, bool backward, size_t* bytes);
 int dense_attn_fwd(const DenseAttnCall& c, void* workspace, size_t workspace_bytes, hipStream_t st);
 int dense_attn_bwd(const DenseAttnCall& c, void* workspace, size_t workspace_bytes, hipStream_t st);
+
+// The head-dim 32 / 64 kernels (esa_attn_wide.hip).
+size_t wide_attn_workspace_size(int total_q, int total_k, int heads, int head_dim, bool backward);
+int wide_attn_fwd(const DenseAttnCall& c, void* workspace, size_t workspace_bytes, hipStream_t st);
+int wide_attn_bwd(const DenseAttnCall& c, void* workspace, size_t workspace_bytes, hipStream_t st);

@@ -660,11 +660,18 @@ unsigned group_grid(int total_outer, int nseg, int heads, int gtok) {
 
 }  // namespace
 
-size_t dense_attn_workspace_size(int total_q, int total_k, int heads, bool backward) {
-  return dense_ws(total_q, total_k, heads, backward).total;
+int dense_attn_workspace_size(int total_q, int total_k, int heads, int head_dim, bool backward, size_t* bytes) {
+  if (head_dim == kHd) {
+    *bytes = dense_ws(total_q, total_k, heads, backward).total;
+    return ESA_OK;
+  }
+  if (head_dim != 32 && head_dim != 64) return ESA_ERR_HEAD_DIM;
+  *bytes = wide_attn_workspace_size(total_q, total_k, heads, head_dim, backward);
+  return ESA_OK;
 }
 
 int dense_attn_fwd(const DenseAttnCall& c, void* workspace, size_t workspace_bytes, hipStream_t st) {
+  if (c.head_dim != kHd) return wide_attn_fwd(c, workspace, workspace_bytes, st);
   const DenseWs w = dense_ws(c.total_q, c.total_k, c.heads, false);
   if (workspace_bytes < w.total) return ESA_ERR_WORKSPACE;
   char* ws = static_cast<char*>(workspace);
@@ -695,6 +702,7 @@ int dense_attn_fwd(const DenseAttnCall& c, void* workspace, size_t workspace_byt
 }
 
 int dense_attn_bwd(const DenseAttnCall& c, void* workspace, size_t workspace_bytes, hipStream_t st) {
+  if (c.head_dim != kHd) return wide_attn_bwd(c, workspace, workspace_bytes, st);
   const DenseWs w = dense_ws(c.total_q, c.total_k, c.heads, true);
   if (workspace_bytes < w.total) return ESA_ERR_WORKSPACE;
   char* ws = static_cast<char*>(workspace);

@@ -1,6 +1,7 @@
-// Node-mode (graph-adjacency) masked attention on gfx950.
+// Gathered (per-token) masked attention on gfx950: node mode, and the edge
+// mask at head dims other than 16.
 //
-// Query token i attends to the key tokens listed in row i of a CSR
+// Node mode: query token i attends to the key tokens listed in row i of a CSR
 // (indptr [total_q + 1], indices [nnz]): the mask that
 // get_adj_mask_from_edge_index_node (esa/masked_layers.py:79-118) builds as a
 // padded [B, 1, N, N] bias, 0 at (graph, src_local, dst_local) of every edge
@@ -9,15 +10,22 @@
 // predecessor is a repeated edge and counts once, as repeated writes of 0 into
 // the reference's bias do.  Entries outside the query's segment are ignored.
 //
-// The work is O(nnz * heads * 16) — a few neighbours per node — so it is
-// gathered per token instead of tiled for MFMA: one wave per token, four lanes
-// per head with four dims each (a wave covers 16 heads per pass), fp32 scores,
-// softmax and accumulation.  The forward and dQ gather over the token's CSR
-// row; dK / dV gather over the transposed CSR (per key, the query rows that
-// list it, in ascending position), built with the library's stable CSR sort
-// per call, or once per batch into a node plan that every layer's backward
-// reads.
-// Every sum runs in a fixed order: the backward is deterministic.
+// Edge mask (share an endpoint, esa/masked_layers.py:121-142, 217-268) at
+// head dims 32 and 64: the same kernels take a token's partners from the
+// edge-mask plan, i.e. from its 32-token tile's partner list (the entries
+// whose mask bit the token has set, ascending) or, for a tile past the list
+// capacity, from the predicate over the token's segment.
+//
+// The work is O(partners * heads * head_dim) -- a few to a few tens of
+// partners per token -- so it is gathered per token instead of tiled for
+// MFMA: one wave per token, head_dim / 4 lanes per head with four dims each
+// (a wave covers 256 / head_dim heads per pass), scores reduced over a head's
+// lanes by DPP butterflies (identical in all of them), fp32 online softmax.
+// The forward and dQ gather over the token's partners; dK / dV over the
+// queries that attend to the key (node mode: the transposed CSR, built per
+// call with the library's stable CSR sort or once per batch into a node plan;
+// edge mask: the key tiles' lists, or the query tiles' when the mask is
+// symmetric).  Every sum runs in a fixed order: the backward is deterministic.
 #include "esa_common.h"
 #include "esa_graph_attn.h"
 #include "esa_profile.h"
@@ -25,14 +33,14 @@
 
 namespace {
 
-constexpr int kGU = 2;   // CSR entries per step: their K / V (or Q / dO) rows are loaded together (two
+constexpr int kGU = 2;   // partners per step: their K / V (or Q / dO) rows are loaded together (two
                          // per step keeps every kernel at 8 waves per SIMD; 1, 4 and 8 measured slower)
 
 template <typename T> struct Row4;
 template <> struct Row4<float> { typedef f32x4 type; };
 template <> struct Row4<bf16> { typedef bf16x4 type; };
 
-// Four consecutive values of a [T][H][16] row: this lane's dims of one head.
+// Four consecutive values of a [T][H][head_dim] row: this lane's dims of one head.
 template <typename T>
 DEVI void load4(const T* __restrict__ p, float v[4]) {
   const typename Row4<T>::type x = *reinterpret_cast<const typename Row4<T>::type*>(p);
@@ -47,11 +55,22 @@ DEVI void store4(T* __restrict__ p, const float v[4], float mul) {
   *reinterpret_cast<typename Row4<T>::type*>(p) = x;
 }
 
-// Sum over the four lanes of a head (quad DPP butterfly).  Addition is
-// commutative, so all four lanes hold the identical result.
-DEVI float quad_sum(float x) {
-  x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0xB1, 0xF, 0xF, true));
-  x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x4E, 0xF, 0xF, true));
+template <int CTRL>
+DEVI float dpp(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
+}
+
+// Sum over the L = head_dim / 4 lanes of a head (aligned groups of 4, 8 or
+// 16 lanes): butterflies within each quad ([1,0,3,2], [2,3,0,1]), then the
+// other quad of each half row (row_half_mirror) and the other half of each
+// row (row_mirror).  Addition is commutative, so every lane of the group
+// holds the identical result.
+template <int L>
+DEVI float head_sum(float x) {
+  x += dpp<0xB1>(x);
+  x += dpp<0x4E>(x);
+  if (L >= 8) x += dpp<0x141>(x);
+  if (L >= 16) x += dpp<0x140>(x);
   return x;
 }
 DEVI float dot4(const float a[4], const float b[4]) {
@@ -121,50 +140,136 @@ DEVI int wave_token() {
   return b * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 }
 
-// kGU entries of a CSR row starting at position p: partner token, and whether
-// it counts (inside the row, inside [lo, hi), not a repeat of the previous
-// entry).  `prev` carries the last partner across steps.
-DEVI void next_entries(const int* __restrict__ list, int p, int pb, int lo, int hi, int& prev, int j[kGU],
-                       bool ok[kGU]) {
+// ---- partner sources: next(j, ok) yields the next kGU partners of the wave's
+// token (j a valid row index even where !ok), false once exhausted.  All
+// state is wave-uniform; a copy restarts the walk (one per head pass).
+
+// A CSR row [p, pb): entries in [lo, hi), each once (an entry equal to its
+// predecessor is a repeat).
+struct CsrSrc {
+  const int* list; int p, pb, lo, hi, prev;
+  DEVI bool next(int j[kGU], bool ok[kGU]) {
+    if (p >= pb) return false;
 #pragma unroll
-  for (int u = 0; u < kGU; ++u) {
-    const int pp = min(p + u, pb - 1);
-    const int x = list[pp];
-    ok[u] = p + u < pb && x >= lo && x < hi && x != prev;
-    if (p + u < pb) prev = x;
-    j[u] = ok[u] ? x : lo;
+    for (int u = 0; u < kGU; ++u) {
+      const int pp = min(p + u, pb - 1);
+      const int x = list[pp];
+      ok[u] = p + u < pb && x >= lo && x < hi && x != prev;
+      if (p + u < pb) prev = x;
+      j[u] = ok[u] ? x : lo;
+    }
+    p += kGU;
+    return true;
   }
+};
+
+// An edge-mask plan's list for one token: the entries of its tile's list
+// whose mask bit the token has set, in list (= ascending token) order.  Word
+// c of the token's mask bits is held by lane c (at most kListCap / 32 words).
+struct ListSrc {
+  const int* ids; uint32_t words; int nct, c; uint32_t w; int fallback;
+  DEVI bool next(int j[kGU], bool ok[kGU]) {
+    bool any = false;
+#pragma unroll
+    for (int u = 0; u < kGU; ++u) {
+      while (w == 0u && c + 1 < nct) {
+        ++c;
+        w = (uint32_t)__builtin_amdgcn_readlane((int)words, c);
+      }
+      ok[u] = w != 0u;
+      j[u] = fallback;
+      if (ok[u]) {
+        j[u] = ids[32 * c + __builtin_ctz(w)];
+        w &= w - 1u;
+        any = true;
+      }
+    }
+    return any;
+  }
+};
+DEVI ListSrc list_src(const GraphEdgeLists& e, int d, int t, int n) {
+  const int lane = threadIdx.x & 63, tile = t >> 5;
+  ListSrc s;
+  s.ids = e.ids[d] + (size_t)tile * e.cap;
+  s.nct = (n + 31) >> 5;
+  s.words = lane < s.nct ? e.bits[d][(size_t)tile * e.cap + 32 * lane + (t & 31)] : 0u;
+  s.c = 0;
+  s.w = s.nct > 0 ? (uint32_t)__builtin_amdgcn_readlane((int)s.words, 0) : 0u;
+  s.fallback = t;
+  return s;
 }
 
-template <typename T>
-DEVI void fwd_token(const GraphAttnArgs& a, int t, int4 d) {
+// A token of a tile past the list capacity: the partners p in [lo, hi), p !=
+// t, that share an endpoint with t, 64 candidates per ballot.
+struct WalkSrc {
+  const int2* nodes; int2 own; int t, base, hi, cur; uint64_t mask;
+  DEVI bool next(int j[kGU], bool ok[kGU]) {
+    const int lane = threadIdx.x & 63;
+    bool any = false;
+#pragma unroll
+    for (int u = 0; u < kGU; ++u) {
+      while (mask == 0 && base < hi) {
+        const int p = base + lane;
+        bool keep = false;
+        if (p < hi && p != t) {
+          const int2 n = nodes[p];
+          keep = n.x == own.x || n.x == own.y || n.y == own.x || n.y == own.y;
+        }
+        mask = __ballot(keep);
+        cur = base;
+        base += 64;
+      }
+      ok[u] = mask != 0;
+      j[u] = t;
+      if (ok[u]) {
+        j[u] = cur + __builtin_ctzll(mask);
+        mask &= mask - 1;
+        any = true;
+      }
+    }
+    return any;
+  }
+};
+DEVI WalkSrc walk_src(const GraphEdgeLists& e, int2 bounds, int t) {
+  WalkSrc s;
+  s.nodes = e.nodes;
+  s.own = e.nodes[t];
+  s.t = t;
+  s.base = bounds.x;
+  s.hi = bounds.y;
+  s.cur = 0;
+  s.mask = 0;
+  return s;
+}
+
+template <typename T, int HD, class Src>
+DEVI void fwd_token(const GraphAttnArgs& a, int t, const Src& src0) {
+  constexpr int L = HD / 4, HPP = 64 / L;
   const T* __restrict__ q = static_cast<const T*>(a.q);
   const T* __restrict__ k = static_cast<const T*>(a.k);
   const T* __restrict__ v = static_cast<const T*>(a.v);
-  const int lane = threadIdx.x & 63, H = a.heads, d0 = 4 * (lane & 3);
-  const int lo = d.x, hi = d.y, pa = d.z, pb = d.w;
-  for (int h0 = 0; h0 < H; h0 += 16) {
-    const int h = h0 + (lane >> 2);
+  const int lane = threadIdx.x & 63, H = a.heads, d0 = 4 * (lane % L);
+  for (int h0 = 0; h0 < H; h0 += HPP) {
+    const int h = h0 + lane / L;
     const int hc = min(h, H - 1);
     float qv[4], acc[4] = {0.f, 0.f, 0.f, 0.f};
-    load4<T>(q + ((size_t)t * H + hc) * kHd16 + d0, qv);
+    load4<T>(q + ((size_t)t * H + hc) * HD + d0, qv);
     float m = -INFINITY, l = 0.f;
-    int prev = INT_MIN;
-    for (int p = pa; p < pb; p += kGU) {
-      int j[kGU];
-      bool ok[kGU];
-      next_entries(a.indices, p, pb, lo, hi, prev, j, ok);
+    Src src = src0;
+    int j[kGU];
+    bool ok[kGU];
+    while (src.next(j, ok)) {
       float kr[kGU][4], vr[kGU][4];
 #pragma unroll
       for (int u = 0; u < kGU; ++u) {
-        load4<T>(k + ((size_t)j[u] * H + hc) * kHd16 + d0, kr[u]);
-        load4<T>(v + ((size_t)j[u] * H + hc) * kHd16 + d0, vr[u]);
+        load4<T>(k + ((size_t)j[u] * H + hc) * HD + d0, kr[u]);
+        load4<T>(v + ((size_t)j[u] * H + hc) * HD + d0, vr[u]);
       }
       float s[kGU];
       float mt = m;
 #pragma unroll
       for (int u = 0; u < kGU; ++u) {
-        s[u] = ok[u] ? quad_sum(dot4(qv, kr[u])) * a.c : -INFINITY;
+        s[u] = ok[u] ? head_sum<L>(dot4(qv, kr[u])) * a.c : -INFINITY;
         mt = fmaxf(mt, s[u]);
       }
       if (mt == -INFINITY) continue;   // nothing admissible yet (uniform per head)
@@ -182,84 +287,82 @@ DEVI void fwd_token(const GraphAttnArgs& a, int t, int4 d) {
       m = mt;
     }
     if (h < H) {
-      store4<T>(static_cast<T*>(a.out) + ((size_t)t * H + h) * kHd16 + d0, acc, l > 0.f ? 1.f / l : 0.f);
-      if ((lane & 3) == 0) a.lse[(size_t)h * a.total_q + t] = l > 0.f ? (m + lg2<T>(l)) * kLn2 : -INFINITY;
+      store4<T>(static_cast<T*>(a.out) + ((size_t)t * H + h) * HD + d0, acc, l > 0.f ? 1.f / l : 0.f);
+      if (lane % L == 0) a.lse[(size_t)h * a.total_q + t] = l > 0.f ? (m + lg2<T>(l)) * kLn2 : -INFINITY;
     }
   }
 }
 
-// dQ_i = scale * sum_j P_ij (dP_ij - D_i) k_j over row i; also writes
+// dQ_i = scale * sum_j P_ij (dP_ij - D_i) k_j over i's partners; also writes
 // D_i = rowsum(dO_i * O_i) per head for the dK / dV pass.
-template <typename T>
-DEVI void dq_token(const GraphAttnArgs& a, int t, int4 d) {
+template <typename T, int HD, class Src>
+DEVI void dq_token(const GraphAttnArgs& a, int t, const Src& src0) {
+  constexpr int L = HD / 4, HPP = 64 / L;
   const T* __restrict__ q = static_cast<const T*>(a.q);
   const T* __restrict__ k = static_cast<const T*>(a.k);
   const T* __restrict__ v = static_cast<const T*>(a.v);
   const T* __restrict__ o = static_cast<const T*>(a.out_in);
   const T* __restrict__ g = static_cast<const T*>(a.dout);
-  const int lane = threadIdx.x & 63, H = a.heads, d0 = 4 * (lane & 3);
-  const int lo = d.x, hi = d.y, pa = d.z, pb = d.w;
-  for (int h0 = 0; h0 < H; h0 += 16) {
-    const int h = h0 + (lane >> 2);
+  const int lane = threadIdx.x & 63, H = a.heads, d0 = 4 * (lane % L);
+  for (int h0 = 0; h0 < H; h0 += HPP) {
+    const int h = h0 + lane / L;
     const int hc = min(h, H - 1);
-    const size_t row = ((size_t)t * H + hc) * kHd16 + d0;
+    const size_t row = ((size_t)t * H + hc) * HD + d0;
     float qv[4], gv[4], ov[4], acc[4] = {0.f, 0.f, 0.f, 0.f};
     load4<T>(q + row, qv);
     load4<T>(g + row, gv);
     load4<T>(o + row, ov);
-    const float dsum = quad_sum(dot4(gv, ov));
+    const float dsum = head_sum<L>(dot4(gv, ov));
     const float l = a.lse_in[(size_t)hc * a.total_q + t];
     const float l2 = l == -INFINITY ? INFINITY : l * kLog2e;
-    if (h < H && (lane & 3) == 0) a.dsum[(size_t)h * a.total_q + t] = dsum;
-    int prev = INT_MIN;
-    for (int p = pa; p < pb; p += kGU) {
-      int j[kGU];
-      bool ok[kGU];
-      next_entries(a.indices, p, pb, lo, hi, prev, j, ok);
+    if (h < H && lane % L == 0) a.dsum[(size_t)h * a.total_q + t] = dsum;
+    Src src = src0;
+    int j[kGU];
+    bool ok[kGU];
+    while (src.next(j, ok)) {
       float kr[kGU][4], vr[kGU][4];
 #pragma unroll
       for (int u = 0; u < kGU; ++u) {
-        load4<T>(k + ((size_t)j[u] * H + hc) * kHd16 + d0, kr[u]);
-        load4<T>(v + ((size_t)j[u] * H + hc) * kHd16 + d0, vr[u]);
+        load4<T>(k + ((size_t)j[u] * H + hc) * HD + d0, kr[u]);
+        load4<T>(v + ((size_t)j[u] * H + hc) * HD + d0, vr[u]);
       }
 #pragma unroll
       for (int u = 0; u < kGU; ++u) {
-        const float pu = ok[u] ? ex2<T>(fmaf(quad_sum(dot4(qv, kr[u])), a.c, -l2)) : 0.f;
-        const float ds = pu * (quad_sum(dot4(gv, vr[u])) - dsum);
+        const float pu = ok[u] ? ex2<T>(fmaf(head_sum<L>(dot4(qv, kr[u])), a.c, -l2)) : 0.f;
+        const float ds = pu * (head_sum<L>(dot4(gv, vr[u])) - dsum);
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[i] = fmaf(ds, kr[u][i], acc[i]);
       }
     }
-    if (h < H) store4<T>(static_cast<T*>(a.dq) + ((size_t)t * H + h) * kHd16 + d0, acc, a.scale);
+    if (h < H) store4<T>(static_cast<T*>(a.dq) + ((size_t)t * H + h) * HD + d0, acc, a.scale);
   }
 }
 
 // dV_j = sum_i P_ij dO_i, dK_j = scale * sum_i P_ij (dP_ij - D_i) q_i over the
-// queries i whose rows list key j (t_rows[t_indptr[j] ..], ascending position).
-template <typename T>
-DEVI void dkdv_token(const GraphAttnArgs& a, int t, int4 d) {
+// queries i that attend to key j (ascending).
+template <typename T, int HD, class Src>
+DEVI void dkdv_token(const GraphAttnArgs& a, int t, const Src& src0) {
+  constexpr int L = HD / 4, HPP = 64 / L;
   const T* __restrict__ q = static_cast<const T*>(a.q);
   const T* __restrict__ k = static_cast<const T*>(a.k);
   const T* __restrict__ v = static_cast<const T*>(a.v);
   const T* __restrict__ g = static_cast<const T*>(a.dout);
-  const int lane = threadIdx.x & 63, H = a.heads, d0 = 4 * (lane & 3);
-  const int lo = d.x, hi = d.y, pa = d.z, pb = d.w;
-  for (int h0 = 0; h0 < H; h0 += 16) {
-    const int h = h0 + (lane >> 2);
+  const int lane = threadIdx.x & 63, H = a.heads, d0 = 4 * (lane % L);
+  for (int h0 = 0; h0 < H; h0 += HPP) {
+    const int h = h0 + lane / L;
     const int hc = min(h, H - 1);
-    const size_t row = ((size_t)t * H + hc) * kHd16 + d0;
+    const size_t row = ((size_t)t * H + hc) * HD + d0;
     float kv[4], vv[4], dk[4] = {0.f, 0.f, 0.f, 0.f}, dv[4] = {0.f, 0.f, 0.f, 0.f};
     load4<T>(k + row, kv);
     load4<T>(v + row, vv);
-    int prev = INT_MIN;
-    for (int p = pa; p < pb; p += kGU) {
-      int i[kGU];
-      bool ok[kGU];
-      next_entries(a.t_rows, p, pb, lo, hi, prev, i, ok);
+    Src src = src0;
+    int i[kGU];
+    bool ok[kGU];
+    while (src.next(i, ok)) {
       float qr[kGU][4], gr[kGU][4], l2[kGU], ds_[kGU];
 #pragma unroll
       for (int u = 0; u < kGU; ++u) {
-        const size_t r = ((size_t)i[u] * H + hc) * kHd16 + d0;
+        const size_t r = ((size_t)i[u] * H + hc) * HD + d0;
         load4<T>(q + r, qr[u]);
         load4<T>(g + r, gr[u]);
         l2[u] = a.lse_in[(size_t)hc * a.total_q + i[u]] * kLog2e;
@@ -267,8 +370,8 @@ DEVI void dkdv_token(const GraphAttnArgs& a, int t, int4 d) {
       }
 #pragma unroll
       for (int u = 0; u < kGU; ++u) {
-        const float pu = ok[u] ? ex2<T>(fmaf(quad_sum(dot4(qr[u], kv)), a.c, -l2[u])) : 0.f;
-        const float ds = pu * (quad_sum(dot4(gr[u], vv)) - ds_[u]);
+        const float pu = ok[u] ? ex2<T>(fmaf(head_sum<L>(dot4(qr[u], kv)), a.c, -l2[u])) : 0.f;
+        const float ds = pu * (head_sum<L>(dot4(gr[u], vv)) - ds_[u]);
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
           dv[c] = fmaf(pu, gr[u][c], dv[c]);
@@ -277,32 +380,58 @@ DEVI void dkdv_token(const GraphAttnArgs& a, int t, int4 d) {
       }
     }
     if (h < H) {
-      store4<T>(static_cast<T*>(a.dk) + ((size_t)t * H + h) * kHd16 + d0, dk, a.scale);
-      store4<T>(static_cast<T*>(a.dv) + ((size_t)t * H + h) * kHd16 + d0, dv, 1.f);
+      store4<T>(static_cast<T*>(a.dk) + ((size_t)t * H + h) * HD + d0, dk, a.scale);
+      store4<T>(static_cast<T*>(a.dv) + ((size_t)t * H + h) * HD + d0, dv, 1.f);
     }
   }
 }
 
-// The three kernels; the key pass (dK / dV) walks key tokens over the
-// transposed CSR.
-template <typename T>
+DEVI CsrSrc csr_src(const int* list, int4 d) { return CsrSrc{list, d.z, d.w, d.x, d.y, INT_MIN}; }
+
+// The kernels: node mode over a CSR (the key pass over the transposed CSR).
+template <typename T, int HD>
 __global__ __launch_bounds__(256) void graph_attn_fwd_kernel(const GraphAttnArgs a) {
   const int t = wave_token();
   if (t >= a.total_q) return;
-  fwd_token<T>(a, t, token_desc(a.q_desc, a.cu_q, a.cu_k, a.nseg, a.total_k, a.indptr, a.nnz, t));
+  fwd_token<T, HD>(a, t, csr_src(a.indices, token_desc(a.q_desc, a.cu_q, a.cu_k, a.nseg, a.total_k, a.indptr, a.nnz, t)));
 }
-template <typename T>
+template <typename T, int HD>
 __global__ __launch_bounds__(256) void graph_attn_dq_kernel(const GraphAttnArgs a) {
   const int t = wave_token();
   if (t >= a.total_q) return;
-  dq_token<T>(a, t, token_desc(a.q_desc, a.cu_q, a.cu_k, a.nseg, a.total_k, a.indptr, a.nnz, t));
+  dq_token<T, HD>(a, t, csr_src(a.indices, token_desc(a.q_desc, a.cu_q, a.cu_k, a.nseg, a.total_k, a.indptr, a.nnz, t)));
 }
-template <typename T>
+template <typename T, int HD>
 __global__ __launch_bounds__(256) void graph_attn_dkdv_kernel(const GraphAttnArgs a) {
   const int t = wave_token();
   if (t >= a.total_k) return;
-  dkdv_token<T>(a, t, token_desc(a.k_desc, a.cu_k, a.cu_q, a.nseg, a.total_q, a.t_indptr, a.nnz, t));
+  dkdv_token<T, HD>(a, t, csr_src(a.t_rows, token_desc(a.k_desc, a.cu_k, a.cu_q, a.nseg, a.total_q, a.t_indptr, a.nnz, t)));
 }
+
+// Edge mask over a plan's lists: the query side reads direction 0, the key
+// side direction 1, or direction 0 when the plan is symmetric.
+template <typename T, int HD, int PASS>   // 0 forward, 1 dQ, 2 dK / dV
+DEVI void graph_edge_pass(const GraphAttnArgs& a) {
+  const int t = wave_token();
+  if (t >= (PASS == 2 ? a.total_k : a.total_q)) return;
+  const int d = (PASS == 2 && a.edge.sym[0] == 0) ? 1 : 0;
+  const int n = a.edge.info[d][t >> 5];
+  auto run = [&](const auto& src) {
+    if (PASS == 0) fwd_token<T, HD>(a, t, src);
+    if (PASS == 1) dq_token<T, HD>(a, t, src);
+    if (PASS == 2) dkdv_token<T, HD>(a, t, src);
+  };
+  if (n >= 0)
+    run(list_src(a.edge, d, t, n));
+  else
+    run(walk_src(a.edge, (PASS == 2 ? a.k_bounds : a.q_bounds)[t], t));
+}
+template <typename T, int HD>
+__global__ __launch_bounds__(256) void graph_edge_fwd_kernel(const GraphAttnArgs a) { graph_edge_pass<T, HD, 0>(a); }
+template <typename T, int HD>
+__global__ __launch_bounds__(256) void graph_edge_dq_kernel(const GraphAttnArgs a) { graph_edge_pass<T, HD, 1>(a); }
+template <typename T, int HD>
+__global__ __launch_bounds__(256) void graph_edge_dkdv_kernel(const GraphAttnArgs a) { graph_edge_pass<T, HD, 2>(a); }
 
 // row_of[e] = the CSR row holding entry e (-1 for an entry no row covers).
 __global__ void fill_minus_one_kernel(int* __restrict__ p, long n) {
@@ -456,8 +585,27 @@ int graph_node_plan_build(const int* indptr, const int* indices, const int* cu_q
                           true, st);
 }
 
+namespace {
+
+// Launches KERNEL<T, HD> for the call's dtype and head dim.
+#define ESA_GRAPH_LAUNCH(KERNEL, dtype, hd, grid, st, a)                                          \
+  do {                                                                                            \
+    if (dtype == ESA_F32) {                                                                       \
+      if (hd == 16) hipLaunchKernelGGL((KERNEL<float, 16>), grid, dim3(256), 0, st, a);           \
+      else if (hd == 32) hipLaunchKernelGGL((KERNEL<float, 32>), grid, dim3(256), 0, st, a);      \
+      else hipLaunchKernelGGL((KERNEL<float, 64>), grid, dim3(256), 0, st, a);                    \
+    } else {                                                                                      \
+      if (hd == 16) hipLaunchKernelGGL((KERNEL<bf16, 16>), grid, dim3(256), 0, st, a);            \
+      else if (hd == 32) hipLaunchKernelGGL((KERNEL<bf16, 32>), grid, dim3(256), 0, st, a);       \
+      else hipLaunchKernelGGL((KERNEL<bf16, 64>), grid, dim3(256), 0, st, a);                     \
+    }                                                                                             \
+  } while (0)
+
+}  // namespace
+
 int graph_attn_fwd(GraphAttnArgs a, int dtype, const void* plan, hipStream_t st) {
   if (a.total_q == 0) return ESA_OK;
+  if (!graph_head_dim_ok(a.head_dim)) return ESA_ERR_HEAD_DIM;
   a.q_desc = nullptr;
   if (plan) {
     NodePlan np;
@@ -465,17 +613,15 @@ int graph_attn_fwd(GraphAttnArgs a, int dtype, const void* plan, hipStream_t st)
     if (rc) return rc;
     a.q_desc = reinterpret_cast<const int4*>(static_cast<const char*>(plan) + np.q_desc);
   }
-  const dim3 grid(token_blocks(a.total_q)), block(256);
-  if (dtype == ESA_F32)
-    ESA_TIMED(esa_profile::kGraphFwd, st, hipLaunchKernelGGL(graph_attn_fwd_kernel<float>, grid, block, 0, st, a));
-  else
-    ESA_TIMED(esa_profile::kGraphFwd, st, hipLaunchKernelGGL(graph_attn_fwd_kernel<bf16>, grid, block, 0, st, a));
+  const dim3 grid(token_blocks(a.total_q));
+  ESA_TIMED(esa_profile::kGraphFwd, st, ESA_GRAPH_LAUNCH(graph_attn_fwd_kernel, dtype, a.head_dim, grid, st, a));
   ESA_LAUNCH_CHECK();
   return ESA_OK;
 }
 
 int graph_attn_bwd(GraphAttnArgs a, int dtype, const void* plan, void* workspace, size_t workspace_bytes,
                    hipStream_t st) {
+  if (!graph_head_dim_ok(a.head_dim)) return ESA_ERR_HEAD_DIM;
   GraphWs w;
   int rc = graph_ws(a.total_q, a.total_k, a.heads, a.nnz, true, plan != nullptr, w);
   if (rc) return rc;
@@ -497,23 +643,43 @@ int graph_attn_bwd(GraphAttnArgs a, int dtype, const void* plan, void* workspace
   a.t_rows = reinterpret_cast<const int*>(tbase + np.t_rows);
   a.q_desc = reinterpret_cast<const int4*>(tbase + np.q_desc);
   a.k_desc = reinterpret_cast<const int4*>(tbase + np.k_desc);
-  const dim3 block(256);
   if (a.total_q > 0) {
-    if (dtype == ESA_F32)
-      ESA_TIMED(esa_profile::kGraphDq, st,
-                hipLaunchKernelGGL(graph_attn_dq_kernel<float>, dim3(token_blocks(a.total_q)), block, 0, st, a));
-    else
-      ESA_TIMED(esa_profile::kGraphDq, st,
-                hipLaunchKernelGGL(graph_attn_dq_kernel<bf16>, dim3(token_blocks(a.total_q)), block, 0, st, a));
+    ESA_TIMED(esa_profile::kGraphDq, st,
+              ESA_GRAPH_LAUNCH(graph_attn_dq_kernel, dtype, a.head_dim, dim3(token_blocks(a.total_q)), st, a));
     ESA_LAUNCH_CHECK();
   }
   if (a.total_k > 0) {
-    if (dtype == ESA_F32)
-      ESA_TIMED(esa_profile::kGraphDkdv, st,
-                hipLaunchKernelGGL(graph_attn_dkdv_kernel<float>, dim3(token_blocks(a.total_k)), block, 0, st, a));
-    else
-      ESA_TIMED(esa_profile::kGraphDkdv, st,
-                hipLaunchKernelGGL(graph_attn_dkdv_kernel<bf16>, dim3(token_blocks(a.total_k)), block, 0, st, a));
+    ESA_TIMED(esa_profile::kGraphDkdv, st,
+              ESA_GRAPH_LAUNCH(graph_attn_dkdv_kernel, dtype, a.head_dim, dim3(token_blocks(a.total_k)), st, a));
+    ESA_LAUNCH_CHECK();
+  }
+  return ESA_OK;
+}
+
+int graph_edge_attn_fwd(GraphAttnArgs a, int dtype, hipStream_t st) {
+  if (a.total_q == 0) return ESA_OK;
+  if (!graph_head_dim_ok(a.head_dim)) return ESA_ERR_HEAD_DIM;
+  ESA_TIMED(esa_profile::kAttnFwdMasked, st,
+            ESA_GRAPH_LAUNCH(graph_edge_fwd_kernel, dtype, a.head_dim, dim3(token_blocks(a.total_q)), st, a));
+  ESA_LAUNCH_CHECK();
+  return ESA_OK;
+}
+
+int graph_edge_attn_bwd(GraphAttnArgs a, int dtype, void* workspace, size_t workspace_bytes, hipStream_t st) {
+  if (!graph_head_dim_ok(a.head_dim)) return ESA_ERR_HEAD_DIM;
+  GraphWs w;
+  int rc = graph_ws(a.total_q, a.total_k, a.heads, 0, true, true, w);
+  if (rc) return rc;
+  if (workspace_bytes < w.total) return ESA_ERR_WORKSPACE;
+  a.dsum = reinterpret_cast<float*>(static_cast<char*>(workspace) + w.dsum);
+  if (a.total_q > 0) {
+    ESA_TIMED(esa_profile::kAttnBwdDqMasked, st,
+              ESA_GRAPH_LAUNCH(graph_edge_dq_kernel, dtype, a.head_dim, dim3(token_blocks(a.total_q)), st, a));
+    ESA_LAUNCH_CHECK();
+  }
+  if (a.total_k > 0) {
+    ESA_TIMED(esa_profile::kAttnBwdDkdvMasked, st,
+              ESA_GRAPH_LAUNCH(graph_edge_dkdv_kernel, dtype, a.head_dim, dim3(token_blocks(a.total_k)), st, a));
     ESA_LAUNCH_CHECK();
   }
   return ESA_OK;

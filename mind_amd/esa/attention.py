@@ -4,9 +4,10 @@
 reference calls it (esa/mha_flash_varlen.py:177-184: causal=False, dropout 0,
 ``softmax_scale=None`` meaning 1/sqrt(head_dim)), extended with the
 edge-adjacency mask of esa/masked_layers.py:121-142 evaluated on the fly from
-per-token ``(src, dst)`` node ids.  Tensors are packed ``[total, heads, 16]``
-bf16 (MFMA kernels, fp32 softmax) or float32 (fp32 throughout) with int32
-``cu_seqlens``.  Backward is deterministic.
+per-token ``(src, dst)`` node ids.  Tensors are packed ``[total, heads,
+head_dim]`` (head_dim 16, 32 or 64: ESA's dim / heads) bf16 (MFMA kernels, fp32
+softmax) or float32 (fp32 throughout) with int32 ``cu_seqlens``.  Backward is
+deterministic.
 """
 from __future__ import annotations
 
@@ -17,7 +18,7 @@ import torch
 
 from .. import _lib
 
-HEAD_DIM = 16
+HEAD_DIMS = (16, 32, 64)   # head dims the kernels take
 
 
 _DTYPES = {torch.bfloat16: _lib.ESA_BF16, torch.float32: _lib.ESA_F32}
@@ -30,22 +31,26 @@ def _dtype_code(t: torch.Tensor) -> int:
         raise TypeError(f"attention tensors must be bfloat16 or float32 (got {t.dtype})") from None
 
 
-def _workspace(device: torch.device, total_q: int, total_k: int, heads: int, dtype: int, mask_kind: int,
-               nnz: int, backward: bool):
+def _workspace(device: torch.device, total_q: int, total_k: int, heads: int, head_dim: int, dtype: int,
+               mask_kind: int, nnz: int, backward: bool):
     lib = _lib.load()
     n = _lib.ctypes.c_size_t(0)
-    _lib.check(lib.esa_varlen_attn_workspace_size(total_q, total_k, heads, HEAD_DIM, dtype, mask_kind, nnz,
+    _lib.check(lib.esa_varlen_attn_workspace_size(total_q, total_k, heads, head_dim, dtype, mask_kind, nnz,
                                                   int(backward), _lib.ctypes.byref(n)),
                "esa_varlen_attn_workspace_size")
     return torch.empty(max(int(n.value), 256), dtype=torch.uint8, device=device)
 
 
-def _check_tokens(name: str, t: torch.Tensor, heads: int | None = None, dtype: torch.dtype | None = None) -> None:
+def _check_tokens(name: str, t: torch.Tensor, heads: int | None = None, dtype: torch.dtype | None = None,
+                  head_dim: int | None = None) -> None:
     _dtype_code(t)
     if dtype is not None and t.dtype != dtype:
         raise TypeError(f"{name} is {t.dtype}; all attention tensors must share one dtype ({dtype})")
-    if t.dim() != 3 or t.shape[2] != HEAD_DIM:
-        raise ValueError(f"{name} must be [total, heads, {HEAD_DIM}] (got {tuple(t.shape)})")
+    if t.dim() != 3 or t.shape[2] not in HEAD_DIMS:
+        raise ValueError(f"{name} must be [total, heads, head_dim] with head_dim in {HEAD_DIMS} "
+                         f"(got {tuple(t.shape)})")
+    if head_dim is not None and t.shape[2] != head_dim:
+        raise ValueError(f"{name} has head_dim {t.shape[2]}, expected {head_dim}")
     if heads is not None and t.shape[1] != heads:
         raise ValueError(f"{name} has {t.shape[1]} heads, expected {heads}")
     if not t.is_contiguous():
@@ -177,13 +182,13 @@ def _mask_args(tq: int, edge_src, edge_dst, adj_indptr, adj_indices, edge_plan=N
 
 def attn_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale,
              edge_src=None, edge_dst=None, adj_indptr=None, adj_indices=None, edge_plan=None, adj_plan=None):
-    """Raw forward: returns ``(out [Tq,H,16] (dtype of q), softmax_lse [H,Tq] fp32)``."""
+    """Raw forward: returns ``(out [Tq,H,hd] (dtype of q), softmax_lse [H,Tq] fp32)``."""
     _lib.require_gpu(q, k, v, cu_seqlens_q, cu_seqlens_k, edge_src, edge_dst, adj_indptr, adj_indices, edge_plan,
                      adj_plan)
-    heads = q.shape[1]
+    heads, hd = q.shape[1], q.shape[-1]
     _check_tokens("q", q)
-    _check_tokens("k", k, heads, q.dtype)
-    _check_tokens("v", v, heads, q.dtype)
+    _check_tokens("k", k, heads, q.dtype, hd)
+    _check_tokens("v", v, heads, q.dtype, hd)
     if k.shape[0] != v.shape[0]:
         raise ValueError("k and v must have the same number of tokens")
     batch = cu_seqlens_q.numel() - 1
@@ -195,11 +200,11 @@ def attn_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, so
     dt = _dtype_code(q)
     out = torch.empty_like(q)
     lse = torch.empty((heads, tq), dtype=torch.float32, device=q.device)
-    ws = _workspace(q.device, tq, tk, heads, dt, mask_kind, nnz, False)
+    ws = _workspace(q.device, tq, tk, heads, hd, dt, mask_kind, nnz, False)
     lib = _lib.load()
     rc = lib.esa_varlen_attn_fwd(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(), batch, tq, tk,
-        int(max_seqlen_q), int(max_seqlen_k), heads, HEAD_DIM, dt, float(softmax_scale),
+        int(max_seqlen_q), int(max_seqlen_k), heads, hd, dt, float(softmax_scale),
         mask_kind, _lib.ptr(mask_a), _lib.ptr(mask_b), nnz, out.data_ptr(), lse.data_ptr(), ws.data_ptr(),
         ws.numel(), _lib.stream_of(q))
     _lib.check(rc, "esa_varlen_attn_fwd")
@@ -208,16 +213,16 @@ def attn_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, so
 
 def attn_fwd_noalloc(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale, out, lse,
                      edge_src=None, edge_dst=None, adj_indptr=None, adj_indices=None, edge_plan=None, adj_plan=None):
-    """``attn_fwd`` into caller-provided ``out`` [Tq,H,16] and ``lse`` [H,Tq] fp32 through
+    """``attn_fwd`` into caller-provided ``out`` [Tq,H,hd] and ``lse`` [H,Tq] fp32 through
     esa_varlen_attn_fwd_noalloc: no workspace, no device allocation (the library's static per-GPU scratch;
     calls that overlap on one GPU race).  Raises EsaError (ESA_ERR_SCRATCH) for shapes beyond that scratch."""
     _lib.require_gpu(q, k, v, cu_seqlens_q, cu_seqlens_k, edge_src, edge_dst, adj_indptr, adj_indices, out, lse,
                      edge_plan, adj_plan)
-    heads = q.shape[1]
+    heads, hd = q.shape[1], q.shape[-1]
     _check_tokens("q", q)
-    _check_tokens("k", k, heads, q.dtype)
-    _check_tokens("v", v, heads, q.dtype)
-    _check_tokens("out", out, heads, q.dtype)
+    _check_tokens("k", k, heads, q.dtype, hd)
+    _check_tokens("v", v, heads, q.dtype, hd)
+    _check_tokens("out", out, heads, q.dtype, hd)
     if out.shape != q.shape:
         raise ValueError("out must have the shape of q")
     if lse.dtype != torch.float32 or tuple(lse.shape) != (heads, q.shape[0]) or not lse.is_contiguous():
@@ -230,7 +235,7 @@ def attn_fwd_noalloc(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seql
                                              tk, cu_seqlens_k.data_ptr() == cu_seqlens_q.data_ptr())
     rc = _lib.load().esa_varlen_attn_fwd_noalloc(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(), batch, tq, tk,
-        int(max_seqlen_q), int(max_seqlen_k), heads, HEAD_DIM, _dtype_code(q), float(softmax_scale),
+        int(max_seqlen_q), int(max_seqlen_k), heads, hd, _dtype_code(q), float(softmax_scale),
         mask_kind, _lib.ptr(mask_a), _lib.ptr(mask_b), nnz, out.data_ptr(), lse.data_ptr(), _lib.stream_of(q))
     _lib.check(rc, "esa_varlen_attn_fwd_noalloc")
     return out, lse
@@ -240,10 +245,10 @@ def attn_bwd(dout, q, k, v, out, lse, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, 
              edge_src=None, edge_dst=None, adj_indptr=None, adj_indices=None, edge_plan=None, adj_plan=None):
     """Raw backward: returns ``(dq, dk, dv)`` (dtype and shapes of q, k, v)."""
     _lib.require_gpu(dout, q, k, v, out, lse)
-    heads = q.shape[1]
+    heads, hd = q.shape[1], q.shape[-1]
     _check_tokens("q", q)
     for name, t in (("dout", dout), ("k", k), ("v", v), ("out", out)):
-        _check_tokens(name, t, heads, q.dtype)
+        _check_tokens(name, t, heads, q.dtype, hd)
     if dout.shape != q.shape or out.shape != q.shape:
         raise ValueError("dout and out must have the shape of q")
     batch = cu_seqlens_q.numel() - 1
@@ -252,12 +257,12 @@ def attn_bwd(dout, q, k, v, out, lse, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, 
                                              tk, cu_seqlens_k.data_ptr() == cu_seqlens_q.data_ptr())
     dt = _dtype_code(q)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
-    ws = _workspace(q.device, tq, tk, heads, dt, mask_kind, nnz, True)
+    ws = _workspace(q.device, tq, tk, heads, hd, dt, mask_kind, nnz, True)
     lib = _lib.load()
     rc = lib.esa_varlen_attn_bwd(
         dout.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr(),
         cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(), batch, tq, tk, int(max_seqlen_q), int(max_seqlen_k),
-        heads, HEAD_DIM, dt, float(softmax_scale), mask_kind, _lib.ptr(mask_a), _lib.ptr(mask_b), nnz,
+        heads, hd, dt, float(softmax_scale), mask_kind, _lib.ptr(mask_a), _lib.ptr(mask_b), nnz,
         dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_of(q))
     _lib.check(rc, "esa_varlen_attn_bwd")
     return dq, dk, dv
@@ -327,7 +332,7 @@ def varlen_attention(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seql
                      adj_indptr=None, adj_indices=None, edge_plan=None, adj_plan=None):
     """``flash_attn_varlen_func``-compatible entry (plus the ESA masks).
 
-    q: [Tq, H, 16]; k, v: [Tk, H, 16], all bfloat16 or all float32;
+    q: [Tq, H, hd]; k, v: [Tk, H, hd] (hd 16, 32 or 64), all bfloat16 or all float32;
     cu_seqlens_*: int32 [B+1].
     edge_src / edge_dst: optional int32 [Tq] node ids per token (self-attention
     only); token i then attends to token j of its segment iff i != j and the
@@ -358,10 +363,10 @@ def varlen_attention(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seql
     return (out, lse) if return_lse else out
 
 
-def _pma_workspace(device, batch, k_seeds, total_k, heads, dtype, backward):
+def _pma_workspace(device, batch, k_seeds, total_k, heads, head_dim, dtype, backward):
     lib = _lib.load()
     n = _lib.ctypes.c_size_t(0)
-    _lib.check(lib.esa_pma_workspace_size(batch, k_seeds, total_k, heads, HEAD_DIM, dtype, int(backward),
+    _lib.check(lib.esa_pma_workspace_size(batch, k_seeds, total_k, heads, head_dim, dtype, int(backward),
                                           _lib.ctypes.byref(n)), "esa_pma_workspace_size")
     return torch.empty(max(int(n.value), 256), dtype=torch.uint8, device=device)
 
@@ -369,13 +374,13 @@ def _pma_workspace(device, batch, k_seeds, total_k, heads, dtype, backward):
 class _PMAAttention(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, v, cu_k, max_k, scale):
-        batch, k_seeds, heads = cu_k.numel() - 1, q.shape[0], q.shape[1]
+        batch, k_seeds, heads, hd = cu_k.numel() - 1, q.shape[0], q.shape[1], q.shape[2]
         dt = _dtype_code(q)
-        out = torch.empty((batch * k_seeds, heads, HEAD_DIM), dtype=q.dtype, device=q.device)
+        out = torch.empty((batch * k_seeds, heads, hd), dtype=q.dtype, device=q.device)
         lse = torch.empty((heads, batch * k_seeds), dtype=torch.float32, device=q.device)
-        ws = _pma_workspace(q.device, batch, k_seeds, k.shape[0], heads, dt, False)
+        ws = _pma_workspace(q.device, batch, k_seeds, k.shape[0], heads, hd, dt, False)
         rc = _lib.load().esa_pma_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), cu_k.data_ptr(), batch, k_seeds,
-                                     k.shape[0], int(max_k), heads, HEAD_DIM, dt, float(scale), out.data_ptr(),
+                                     k.shape[0], int(max_k), heads, hd, dt, float(scale), out.data_ptr(),
                                      lse.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_of(q))
         _lib.check(rc, "esa_pma_fwd")
         ctx.save_for_backward(q, k, v, out, lse, cu_k)
@@ -386,28 +391,28 @@ class _PMAAttention(torch.autograd.Function):
     def backward(ctx, g):
         q, k, v, out, lse, cu_k = ctx.saved_tensors
         max_k, scale = ctx.meta
-        batch, k_seeds, heads = cu_k.numel() - 1, q.shape[0], q.shape[1]
+        batch, k_seeds, heads, hd = cu_k.numel() - 1, q.shape[0], q.shape[1], q.shape[2]
         dt = _dtype_code(q)
         g = g.to(q.dtype).contiguous()
         dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
-        ws = _pma_workspace(q.device, batch, k_seeds, k.shape[0], heads, dt, True)
+        ws = _pma_workspace(q.device, batch, k_seeds, k.shape[0], heads, hd, dt, True)
         rc = _lib.load().esa_pma_bwd(g.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
                                      lse.data_ptr(), cu_k.data_ptr(), batch, k_seeds, k.shape[0], int(max_k), heads,
-                                     HEAD_DIM, dt, float(scale), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                                     hd, dt, float(scale), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
                                      ws.data_ptr(), ws.numel(), _lib.stream_of(q))
         _lib.check(rc, "esa_pma_bwd")
         return dq, dk, dv, None, None, None
 
 
 def pma_attention(q, k, v, cu_seqlens_k, max_seqlen_k, softmax_scale=None):
-    """Seed pooling of PMA (esa/mha.py:101-109): the k seed queries q [k, H, 16] (fc_q(S), shared by every
-    set) attend over each set's keys k, v [Tk, H, 16] (sets by cu_seqlens_k [B+1], int32) -> [B * k, H, 16],
+    """Seed pooling of PMA (esa/mha.py:101-109): the k seed queries q [k, H, hd] (fc_q(S), shared by every
+    set) attend over each set's keys k, v [Tk, H, hd] (sets by cu_seqlens_k [B+1], int32) -> [B * k, H, hd],
     set-major.  Equals varlen attention with the seeds repeated per set; q's gradient sums the sets'."""
     _lib.require_gpu(q, k, v, cu_seqlens_k)
-    heads = q.shape[1]
+    heads, hd = q.shape[1], q.shape[-1]
     _check_tokens("q", q)
-    _check_tokens("k", k, heads, q.dtype)
-    _check_tokens("v", v, heads, q.dtype)
+    _check_tokens("k", k, heads, q.dtype, hd)
+    _check_tokens("v", v, heads, q.dtype, hd)
     if k.shape[0] != v.shape[0]:
         raise ValueError("k and v must have the same number of tokens")
     _check_index("cu_seqlens_k", cu_seqlens_k)

@@ -44,7 +44,7 @@ from torch import nn
 from torch.nn.init import xavier_normal_
 
 from .activations import mish
-from .attention import HEAD_DIM, varlen_attention
+from .attention import HEAD_DIMS, varlen_attention
 from .packing import PackedSets
 
 BACKENDS = ("xformers", "torch", "flash_varlen", "hip")
@@ -55,7 +55,7 @@ def _uniform_cu(batch: int, n: int, device) -> torch.Tensor:
 
 
 def _heads(x: torch.Tensor, heads: int) -> torch.Tensor:
-    """[..., H * 16] -> contiguous [tokens, H, 16]: float32 stays float32 (the fp32 kernels), any other
+    """[..., H * hd] -> contiguous [tokens, H, hd]: float32 stays float32 (the fp32 kernels), any other
     dtype runs on the bf16 kernels."""
     dt = torch.float32 if x.dtype == torch.float32 else torch.bfloat16
     return x.reshape(-1, heads, x.shape[-1] // heads).to(dt).contiguous()
@@ -65,8 +65,8 @@ def dense_attention(q, k, v, heads):
     """Per-batch-element attention over all positions: q [B, Nq, D], k/v [B, Nk, D] -> [B, Nq, D]."""
     b, nq, d = q.shape
     nk = k.shape[1]
-    if d // heads != HEAD_DIM:
-        raise ValueError(f"head_dim {d // heads} is not supported by the kernels (16)")
+    if d % heads or d // heads not in HEAD_DIMS:
+        raise ValueError(f"head_dim {d / heads:g} is not supported by the kernels {HEAD_DIMS}")
     out = varlen_attention(_heads(q, heads), _heads(k, heads), _heads(v, heads), _uniform_cu(b, nq, q.device),
                            _uniform_cu(b, nk, q.device), nq, nk)
     return out.reshape(b, nq, d)
