@@ -1,9 +1,517 @@
-// Dense varlen attention at head dims 32 and 64 (bf16 MFMA): placeholder
-// entry points until the kernels land; calls report ESA_ERR_HEAD_DIM.
+// Dense varlen attention (no mask) at head dims 32 and 64, bf16 operands,
+// fp32 softmax, on gfx950: the flash_attn_varlen_func drop-in
+// (esa/mha_flash_varlen.py:177-184, causal=False, dropout 0) for the ESA
+// configurations whose dim / num_heads is 32 or 64 (esa/mha.py:50-52).
+//
+// Work items are 128-token groups cut from each segment on its own (the
+// segment plans of the head-dim-16 kernels): a block's four waves own four
+// consecutive 32-token tiles of one segment and one head and walk the same
+// partner range, staged 64 tokens at a time into double-buffered LDS (one
+// barrier per stage, the next stage's global loads in flight in registers).
+//
+// Register layouts (v_mfma_f32_32x32x16_bf16, helpers in esa_attn_tiles.h):
+//  - Scores: S^T = X Y^T summed over head_dim / 16 chunks of 16 dims, the
+//    partner rows X in the A operand from LDS with rows permuted (kperm), the
+//    owned token's row in the B operand from registers.  Lane l owns token
+//    column l % 32; its 16 accumulators hold partners row_local(r, l / 32):
+//    registers 0..7 are partners 8 h .. 8 h + 7 and 8..15 are 16 + 8 h ..,
+//    exactly the K slots lane l supplies to a product over the tile's
+//    partners (h = l / 32), so probabilities feed the next MFMA's B operand
+//    without data movement.
+//  - Products over partners (P V, dS K, P^T dO, dS^T Q): M = 32 output dims
+//    per block (head_dim / 32 blocks), the A operand [dims x partners] from
+//    LDS transpose reads (ds_read_b64_tr_b16) of the staged rows.
+//  - LDS rows: [dim octet][token][8 dims], octet stride padded by 4 tokens so
+//    the two octets of a transpose read fall in different banks.
+// The softmax scale c = scale * log2(e) is applied inside the exponent (one
+// FMA per score, exp2(c s - c m)); the backward's -LSE2 / c and -D row
+// statistics are MFMA accumulator seeds.  Every sum has a fixed order: the
+// backward is deterministic (dQ pass, then dK/dV pass; no atomics).
+#include "esa_attn_tiles.h"
 #include "esa_attn_dense.h"
-#include "esa_common.h"
+#include "esa_profile.h"
 #include "../../include/esa_hip.h"
 
-size_t wide_attn_workspace_size(int, int, int, int, bool) { return 0; }
-int wide_attn_fwd(const DenseAttnCall&, void*, size_t, hipStream_t) { return ESA_ERR_HEAD_DIM; }
-int wide_attn_bwd(const DenseAttnCall&, void*, size_t, hipStream_t) { return ESA_ERR_HEAD_DIM; }
+namespace {
+
+constexpr int kWStage = 64;              // partner tokens per stage (two tiles)
+constexpr int kWTokPad = kWStage + 4;    // LDS octet stride in tokens
+
+struct WideArgs {
+  const bf16* q; const bf16* k; const bf16* v; const bf16* out; const bf16* dout;
+  const float* lse;            // dQ pass input [H][Tq]
+  float2* aux;                 // per (head, query) {-LSE2 / c, -D}, [H][tq_pad]: written by dQ, read by dK/dV
+  const int4* groups; const int* count;
+  int total_q, total_k, heads, tq_pad;
+  float c, scale;
+  bf16* o; float* lse_out; bf16* dq; bf16* dk; bf16* dv;
+};
+
+// 16 bytes of the A operand of a score MFMA: dims 16 c + 8 h .. + 7 (octet
+// 2 c + h) of staged token t.
+template <int NO>
+DEVI bf16x8 row_octet(const bf16* rows, int t, int o) { return lds8(rows + ((size_t)o * kWTokPad + t) * 8); }
+
+// A operand [32 dims x 16 partners] of a product over partners: dims
+// 32 m + (lane % 32), partners 16 j + 8 h .. + 7 (h = lane / 32), by two
+// transpose reads of four tokens each.  In a 16-lane group, lane L
+// addresses token t0 + L / 4 (+ 4 in the second read), dims 4 (L % 4) .. + 3
+// of the group's 16 dims, so lane i receives dim i of the four tokens.
+DEVI bf16x8 tr_dims(const bf16* rows, int m, int j, int lane) {
+  const int i = lane & 15, grp = lane >> 4;
+  const int d = 32 * m + 16 * (grp & 1) + 4 * (i & 3);
+  const int t = 16 * j + 8 * (grp >> 1) + (i >> 2);
+  const bf16* p = rows + ((size_t)(d >> 3) * kWTokPad + t) * 8 + (d & 7);
+  const bf16x4 lo = lds_tr4(p), hi = lds_tr4(p + 4 * 8);
+  return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+// Output dims 32 m + 8 (r / 4) + 4 h + (r % 4) of a product accumulator, 4
+// consecutive dims per register quad: written as bf16 x 4.
+template <int HD>
+DEVI void store_acc(bf16* __restrict__ row, const f32x16 (&acc)[HD / 32], float mul, int h) {
+#pragma unroll
+  for (int m = 0; m < HD / 32; ++m)
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      bf16x4 x;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x[e] = (bf16)(acc[m][4 * a + e] * mul);
+      *reinterpret_cast<bf16x4*>(row + 32 * m + 8 * a + 4 * h) = x;
+    }
+}
+
+// Block -> (work item, head): head fastest, so the blocks of one head land on
+// one XCD (block b runs on XCD b % 8) and share its L2.
+DEVI void wide_item_head(int H, int& item, int& head) {
+  item = (int)blockIdx.x / H;
+  head = (int)blockIdx.x - item * H;
+}
+
+// ---- staging: stage st covers partner tokens g0 + 64 st .. + 63 of tensors
+// A and B ([T][H][HD] bf16); each thread holds CPT 16-byte chunks (token-major
+// over (tensor, token, octet), so consecutive threads read consecutive bytes of
+// a row) in a ring of two register sets.
+template <int HD>
+struct WStage {
+  static constexpr int NO = HD / 8;
+  static constexpr int CPT = 2 * kWStage * NO / 256;
+  i32x4 r[CPT];
+};
+
+template <int HD>
+DEVI WStage<HD> wide_gload(const bf16* a, const bf16* b, int g0, int total, int H, int head, int tid) {
+  constexpr int NO = HD / 8;
+  WStage<HD> s;
+#pragma unroll
+  for (int i = 0; i < WStage<HD>::CPT; ++i) {
+    const int c = tid + 256 * i;
+    const int tensor = c / (kWStage * NO), rem = c - tensor * (kWStage * NO);
+    const int tok = rem / NO, o = rem - tok * NO;
+    const int t = min(g0 + tok, total - 1);
+    s.r[i] = *reinterpret_cast<const i32x4*>((tensor ? b : a) + ((size_t)t * H + head) * HD + 8 * o);
+  }
+  return s;
+}
+template <int HD>
+DEVI void wide_lstore(bf16* sa, bf16* sb, const WStage<HD>& s, int tid) {
+  constexpr int NO = HD / 8;
+#pragma unroll
+  for (int i = 0; i < WStage<HD>::CPT; ++i) {
+    const int c = tid + 256 * i;
+    const int tensor = c / (kWStage * NO), rem = c - tensor * (kWStage * NO);
+    const int tok = rem / NO, o = rem - tok * NO;
+    *reinterpret_cast<i32x4*>((tensor ? sb : sa) + ((size_t)o * kWTokPad + tok) * 8) = s.r[i];
+  }
+}
+
+// Two LDS buffers and two stages' loads in flight: stage s + 2 is requested
+// before stage s is consumed; stage s + 1 is written to LDS after it.
+template <class Load, class Store, class Compute>
+DEVI void wide_walk(int n_stages, Load gload, Store lstore, Compute compute) {
+  if (n_stages <= 0) return;
+  auto r0 = gload(0);
+  auto r1 = gload(min(1, n_stages - 1));
+  lstore(0, r0);
+  __syncthreads();
+  for (int st = 0; st < n_stages; st += 2) {
+    r0 = gload(min(st + 2, n_stages - 1));
+    compute(0, st);
+    if (st + 1 >= n_stages) return;
+    lstore(1, r1);
+    __syncthreads();
+    r1 = gload(min(st + 3, n_stages - 1));
+    compute(1, st + 1);
+    if (st + 2 >= n_stages) return;
+    lstore(0, r0);
+    __syncthreads();
+  }
+}
+
+constexpr int kWGroup = kWaves * kTile;   // 128 owned tokens per block
+
+// ------------------------------------------------------------------ forward
+template <int HD>
+__global__ __launch_bounds__(256) void wide_fwd_kernel(const WideArgs a) {
+  constexpr int NC = HD / 16, NM = HD / 32, NO = HD / 8;
+  __shared__ __align__(16) bf16 sK[2][NO * kWTokPad * 8];
+  __shared__ __align__(16) bf16 sV[2][NO * kWTokPad * 8];
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 31, h = lane >> 5;
+  const int H = a.heads;
+  int item, head;
+  wide_item_head(H, item, head);
+  if (item >= *a.count) return;
+  const int4 g = a.groups[item];
+  const int t = g.x + wave * kTile + col;
+  const bool valid = t < g.y, active = g.x + wave * kTile < g.y;
+  const bf16* qrow = a.q + ((size_t)(valid ? t : g.x) * H + head) * HD;
+  bf16x8 qop[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) qop[c] = *reinterpret_cast<const bf16x8*>(qrow + 16 * c + 8 * h);
+  f32x16 acc[NM];
+#pragma unroll
+  for (int m = 0; m < NM; ++m) acc[m] = f32x16{};
+  float m_run = -INFINITY, l_run = 0.f;
+  const int n_tiles = (g.w - g.z + kTile - 1) >> 5;
+  const int n_stages = (n_tiles + 1) >> 1;
+  const f32x16 zero = {};
+  wide_walk(
+      n_stages, [&](int st) { return wide_gload<HD>(a.k, a.v, g.z + st * kWStage, a.total_k, H, head, tid); },
+      [&](int buf, const WStage<HD>& s) { wide_lstore<HD>(sK[buf], sV[buf], s, tid); },
+      [&](int buf, int st) {
+        if (!active) return;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          if (2 * st + u >= n_tiles) break;
+          const int k0 = g.z + st * kWStage + u * kTile;
+          f32x16 s = zero;
+#pragma unroll
+          for (int c = 0; c < NC; ++c) s = mfma32(row_octet<NO>(sK[buf], u * kTile + kperm(col), 2 * c + h), qop[c], s);
+          if (k0 + kTile > g.w) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) s[r] = k0 + row_local(r, h) < g.w ? s[r] : -INFINITY;
+          }
+          float mt = s[0];
+#pragma unroll
+          for (int r = 1; r < 16; ++r) mt = fmaxf(mt, s[r]);
+          mt = fmaxf(mt, __shfl_xor(mt, 32));
+          const float m_new = fmaxf(m_run, mt);
+          if (__ballot(m_new > m_run)) {
+            const float alpha = m_run == -INFINITY ? 0.f : fast_exp2(a.c * (m_run - m_new));
+            l_run *= alpha;
+#pragma unroll
+            for (int m = 0; m < NM; ++m)
+#pragma unroll
+              for (int r = 0; r < 16; ++r) acc[m][r] *= alpha;
+            m_run = m_new;
+          }
+          const float cm = m_run == -INFINITY ? 0.f : a.c * m_run;
+          float p[16];
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            p[r] = fast_exp2(fmaf(s[r], a.c, -cm));
+            l_run += p[r];
+          }
+#pragma unroll
+          for (int m = 0; m < NM; ++m)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) acc[m] = mfma32(tr_dims(sV[buf], m, 2 * u + j, lane), cvt8(p + 8 * j), acc[m]);
+        }
+      });
+  if (!valid) return;
+  const float l = l_run + __shfl_xor(l_run, 32);
+  store_acc<HD>(a.o + ((size_t)t * H + head) * HD, acc, l > 0.f ? 1.f / l : 0.f, h);
+  if (h == 0) a.lse_out[(size_t)head * a.total_q + t] = l > 0.f ? (a.c * m_run + fast_log2(l)) * kLn2 : -INFINITY;
+}
+
+// ------------------------------------------------------------------ dQ pass
+// Queries on lanes: S^T = K q^T, dP^T = V dO^T, P = exp2(c S - LSE2),
+// dS = P (dP - D), dQ^T += K^T dS^T.  Also writes the dK/dV pass's row
+// statistics {-LSE2 / c, -D} of its queries.
+template <int HD>
+__global__ __launch_bounds__(256) void wide_dq_kernel(const WideArgs a) {
+  constexpr int NC = HD / 16, NM = HD / 32, NO = HD / 8;
+  __shared__ __align__(16) bf16 sK[2][NO * kWTokPad * 8];
+  __shared__ __align__(16) bf16 sV[2][NO * kWTokPad * 8];
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 31, h = lane >> 5;
+  const int H = a.heads;
+  int item, head;
+  wide_item_head(H, item, head);
+  if (item >= *a.count) return;
+  const int4 g = a.groups[item];
+  const int t = g.x + wave * kTile + col;
+  const bool valid = t < g.y, active = g.x + wave * kTile < g.y;
+  const size_t row = ((size_t)(valid ? t : g.x) * H + head) * HD;
+  bf16x8 qop[NC], gop[NC];
+  float dsum = 0.f;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    qop[c] = *reinterpret_cast<const bf16x8*>(a.q + row + 16 * c + 8 * h);
+    gop[c] = *reinterpret_cast<const bf16x8*>(a.dout + row + 16 * c + 8 * h);
+    const bf16x8 o = *reinterpret_cast<const bf16x8*>(a.out + row + 16 * c + 8 * h);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) dsum = fmaf((float)gop[c][e], (float)o[e], dsum);
+  }
+  dsum += __shfl_xor(dsum, 32);
+  const float lq = a.lse[(size_t)head * a.total_q + (valid ? t : g.x)];
+  const float lse2 = lq == -INFINITY ? INFINITY : lq * kLog2e;   // rows without keys: P = 0
+  if (valid && h == 0)
+    a.aux[(size_t)head * a.tq_pad + t] = make_float2(lq == -INFINITY ? kDeadRow : -lse2 / a.c, -dsum);
+  f32x16 acc[NM];
+#pragma unroll
+  for (int m = 0; m < NM; ++m) acc[m] = f32x16{};
+  const int n_tiles = (g.w - g.z + kTile - 1) >> 5;
+  const int n_stages = (n_tiles + 1) >> 1;
+  const f32x16 zero = {};
+  wide_walk(
+      n_stages, [&](int st) { return wide_gload<HD>(a.k, a.v, g.z + st * kWStage, a.total_k, H, head, tid); },
+      [&](int buf, const WStage<HD>& s) { wide_lstore<HD>(sK[buf], sV[buf], s, tid); },
+      [&](int buf, int st) {
+        if (!active) return;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          if (2 * st + u >= n_tiles) break;
+          const int k0 = g.z + st * kWStage + u * kTile;
+          f32x16 s = zero, dp = zero;
+#pragma unroll
+          for (int c = 0; c < NC; ++c) {
+            s = mfma32(row_octet<NO>(sK[buf], u * kTile + kperm(col), 2 * c + h), qop[c], s);
+            dp = mfma32(row_octet<NO>(sV[buf], u * kTile + kperm(col), 2 * c + h), gop[c], dp);
+          }
+          if (k0 + kTile > g.w) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) s[r] = k0 + row_local(r, h) < g.w ? s[r] : -INFINITY;
+          }
+          float ds[16];
+#pragma unroll
+          for (int r = 0; r < 16; ++r) ds[r] = fast_exp2(fmaf(s[r], a.c, -lse2)) * (dp[r] - dsum);
+#pragma unroll
+          for (int m = 0; m < NM; ++m)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) acc[m] = mfma32(tr_dims(sK[buf], m, 2 * u + j, lane), cvt8(ds + 8 * j), acc[m]);
+        }
+      });
+  if (!valid) return;
+  store_acc<HD>(a.dq + ((size_t)t * H + head) * HD, acc, a.scale, h);
+}
+
+// ------------------------------------------------------------------ dK/dV pass
+// Keys on lanes, queries in rows: S = Q k^T - LSE2 / c and dP = dO v^T - D
+// (the row statistics as accumulator seeds), P = exp2(c S), dS = P dP,
+// dV^T += dO^T P, dK^T += Q^T dS.  A stage holds 64 queries' Q and dO rows
+// and their statistics.
+template <int HD>
+__global__ __launch_bounds__(256) void wide_dkdv_kernel(const WideArgs a) {
+  constexpr int NC = HD / 16, NM = HD / 32, NO = HD / 8;
+  __shared__ __align__(16) bf16 sQ[2][NO * kWTokPad * 8];
+  __shared__ __align__(16) bf16 sG[2][NO * kWTokPad * 8];
+  __shared__ __align__(16) float sLse[2][kWStage], sDel[2][kWStage];
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 31, h = lane >> 5;
+  const int H = a.heads;
+  int item, head;
+  wide_item_head(H, item, head);
+  if (item >= *a.count) return;
+  const int4 g = a.groups[item];   // outer = keys, inner = queries
+  const int t = g.x + wave * kTile + col;
+  const bool valid = t < g.y, active = g.x + wave * kTile < g.y;
+  const size_t row = ((size_t)(valid ? t : g.x) * H + head) * HD;
+  bf16x8 kop[NC], vop[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    kop[c] = *reinterpret_cast<const bf16x8*>(a.k + row + 16 * c + 8 * h);
+    vop[c] = *reinterpret_cast<const bf16x8*>(a.v + row + 16 * c + 8 * h);
+  }
+  f32x16 dva[NM], dka[NM];
+#pragma unroll
+  for (int m = 0; m < NM; ++m) dva[m] = dka[m] = f32x16{};
+  const int n_tiles = (g.w - g.z + kTile - 1) >> 5;
+  const int n_stages = (n_tiles + 1) >> 1;
+  struct Stage { WStage<HD> rows; float2 st; };
+  wide_walk(
+      n_stages,
+      [&](int st) {
+        Stage s;
+        s.rows = wide_gload<HD>(a.q, a.dout, g.z + st * kWStage, a.total_q, H, head, tid);
+        const int qi = g.z + st * kWStage + tid;
+        s.st = tid < kWStage ? a.aux[(size_t)head * a.tq_pad + min(qi, a.tq_pad - 1)] : make_float2(0.f, 0.f);
+        return s;
+      },
+      [&](int buf, const Stage& s) {
+        wide_lstore<HD>(sQ[buf], sG[buf], s.rows, tid);
+        if (tid < kWStage) {
+          sLse[buf][tid] = s.st.x;
+          sDel[buf][tid] = s.st.y;
+        }
+      },
+      [&](int buf, int st) {
+        if (!active) return;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          if (2 * st + u >= n_tiles) break;
+          const int q0 = g.z + st * kWStage + u * kTile;
+          // seeds: register r of lane (col, h) is query row_local(r, h) = 8 h + r (r < 8), 16 + 8 h + r - 8
+          f32x16 s, dp;
+#pragma unroll
+          for (int b = 0; b < 2; ++b) {
+            const f32x4 l0 = ldsf4(&sLse[buf][u * kTile + 16 * b + 8 * h]);
+            const f32x4 l1 = ldsf4(&sLse[buf][u * kTile + 16 * b + 8 * h + 4]);
+            const f32x4 d0 = ldsf4(&sDel[buf][u * kTile + 16 * b + 8 * h]);
+            const f32x4 d1 = ldsf4(&sDel[buf][u * kTile + 16 * b + 8 * h + 4]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              s[8 * b + e] = l0[e]; s[8 * b + 4 + e] = l1[e];
+              dp[8 * b + e] = d0[e]; dp[8 * b + 4 + e] = d1[e];
+            }
+          }
+#pragma unroll
+          for (int c = 0; c < NC; ++c) {
+            s = mfma32(row_octet<NO>(sQ[buf], u * kTile + kperm(col), 2 * c + h), kop[c], s);
+            dp = mfma32(row_octet<NO>(sG[buf], u * kTile + kperm(col), 2 * c + h), vop[c], dp);
+          }
+          float p[16], ds[16];
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            p[r] = q0 + row_local(r, h) < g.w ? fast_exp2(s[r] * a.c) : 0.f;
+            ds[r] = p[r] * dp[r];
+          }
+#pragma unroll
+          for (int m = 0; m < NM; ++m)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+              dva[m] = mfma32(tr_dims(sG[buf], m, 2 * u + j, lane), cvt8(p + 8 * j), dva[m]);
+              dka[m] = mfma32(tr_dims(sQ[buf], m, 2 * u + j, lane), cvt8(ds + 8 * j), dka[m]);
+            }
+        }
+      });
+  if (!valid) return;
+  store_acc<HD>(a.dv + ((size_t)t * H + head) * HD, dva, 1.f, h);
+  store_acc<HD>(a.dk + ((size_t)t * H + head) * HD, dka, a.scale, h);
+}
+
+// ------------------------------------------------------------------ prep
+// Segment plans of both directions (128-token groups, longest partner range
+// first) and, for the backward, the row statistics of the queries after the
+// last segment up to the 32-row boundary (the dK/dV pass stages them; dead
+// rows give P = 0).
+struct WidePrep {
+  const int* cu_q; const int* cu_k; int nseg;
+  int total_q, heads, tq_pad;
+  int4* plan_q; int* count_q; int4* plan_k; int* count_k;
+  float2* aux;
+  int nb_plan_k, nb_rows;
+};
+
+__global__ __launch_bounds__(256) void wide_prep_kernel(const WidePrep p) {
+  const int tid = threadIdx.x;
+  int b = blockIdx.x;
+  if (b == 0) { seg_plan_block(p.cu_q, p.cu_k, p.nseg, kWGroup, p.plan_q, p.count_q, tid); return; }
+  b -= 1;
+  if (b < p.nb_plan_k) { seg_plan_block(p.cu_k, p.cu_q, p.nseg, kWGroup, p.plan_k, p.count_k, tid); return; }
+  b -= p.nb_plan_k;
+  const int t0 = min(max(p.cu_q[p.nseg], 0), p.total_q);
+  const long n = (long)p.heads * (p.tq_pad - t0);
+  for (long idx = (long)b * 256 + tid; idx < n; idx += (long)p.nb_rows * 256) {
+    const int hh = (int)(idx % p.heads), t = t0 + (int)(idx / p.heads);
+    p.aux[(size_t)hh * p.tq_pad + t] = make_float2(kDeadRow, -0.f);
+  }
+}
+
+size_t wal256(size_t x) { return (x + 255) & ~size_t(255); }
+int wr32(int x) { return (x + kTile - 1) / kTile * kTile; }
+// Groups of one direction: at most ceil(T / 128) + (non-empty segments) <= ceil(T / 128) + T.
+size_t wplan_bytes(int total) { return wal256(((size_t)(total + kWGroup - 1) / kWGroup + (size_t)total + 1) * 16); }
+
+struct WideWs { size_t counts, plan_q, plan_k, aux, total; };
+WideWs wide_ws(int total_q, int total_k, int heads, bool backward) {
+  WideWs w{};
+  size_t off = 0;
+  w.counts = off; off += 256;
+  w.plan_q = off; off += wplan_bytes(total_q);
+  if (backward) {
+    w.plan_k = off; off += wplan_bytes(total_k);
+    w.aux = off; off += wal256((size_t)heads * wr32(total_q) * 8);
+  }
+  w.total = off;
+  return w;
+}
+
+unsigned wide_grid(int total_outer, int nseg, int heads) {
+  return (unsigned)(((total_outer + kWGroup - 1) / kWGroup + min(nseg, total_outer)) * heads);
+}
+
+#define ESA_WIDE_LAUNCH(KERNEL, hd, grid, st, a)                                      \
+  do {                                                                                \
+    if (hd == 32) hipLaunchKernelGGL((KERNEL<32>), grid, dim3(256), 0, st, a);       \
+    else hipLaunchKernelGGL((KERNEL<64>), grid, dim3(256), 0, st, a);                \
+  } while (0)
+
+}  // namespace
+
+size_t wide_attn_workspace_size(int total_q, int total_k, int heads, int head_dim, bool backward) {
+  (void)head_dim;
+  return wide_ws(total_q, total_k, heads, backward).total;
+}
+
+int wide_attn_fwd(const DenseAttnCall& c, void* workspace, size_t workspace_bytes, hipStream_t st) {
+  if (c.head_dim != 32 && c.head_dim != 64) return ESA_ERR_HEAD_DIM;
+  const WideWs w = wide_ws(c.total_q, c.total_k, c.heads, false);
+  if (workspace_bytes < w.total) return ESA_ERR_WORKSPACE;
+  char* ws = static_cast<char*>(workspace);
+  WidePrep p{};
+  p.cu_q = c.cu_q; p.cu_k = c.cu_k; p.nseg = c.nseg;
+  p.total_q = c.total_q; p.heads = c.heads; p.tq_pad = wr32(c.total_q);
+  p.count_q = reinterpret_cast<int*>(ws + w.counts);
+  p.plan_q = reinterpret_cast<int4*>(ws + w.plan_q);
+  ESA_TIMED(esa_profile::kAttnPrep, st, hipLaunchKernelGGL(wide_prep_kernel, dim3(1), dim3(256), 0, st, p));
+  ESA_LAUNCH_CHECK();
+  WideArgs a{};
+  a.q = static_cast<const bf16*>(c.q); a.k = static_cast<const bf16*>(c.k); a.v = static_cast<const bf16*>(c.v);
+  a.groups = p.plan_q; a.count = p.count_q;
+  a.total_q = c.total_q; a.total_k = c.total_k; a.heads = c.heads; a.tq_pad = p.tq_pad;
+  a.c = c.scale * kLog2e; a.scale = c.scale;
+  a.o = static_cast<bf16*>(c.out); a.lse_out = c.lse;
+  ESA_TIMED(esa_profile::kAttnFwd, st,
+            ESA_WIDE_LAUNCH(wide_fwd_kernel, c.head_dim, dim3(wide_grid(c.total_q, c.nseg, c.heads)), st, a));
+  ESA_LAUNCH_CHECK();
+  return ESA_OK;
+}
+
+int wide_attn_bwd(const DenseAttnCall& c, void* workspace, size_t workspace_bytes, hipStream_t st) {
+  if (c.head_dim != 32 && c.head_dim != 64) return ESA_ERR_HEAD_DIM;
+  const WideWs w = wide_ws(c.total_q, c.total_k, c.heads, true);
+  if (workspace_bytes < w.total) return ESA_ERR_WORKSPACE;
+  char* ws = static_cast<char*>(workspace);
+  WidePrep p{};
+  p.cu_q = c.cu_q; p.cu_k = c.cu_k; p.nseg = c.nseg;
+  p.total_q = c.total_q; p.heads = c.heads; p.tq_pad = wr32(c.total_q);
+  p.count_q = reinterpret_cast<int*>(ws + w.counts);
+  p.count_k = p.count_q + 1;
+  p.plan_q = reinterpret_cast<int4*>(ws + w.plan_q);
+  p.plan_k = reinterpret_cast<int4*>(ws + w.plan_k);
+  p.aux = reinterpret_cast<float2*>(ws + w.aux);
+  p.nb_plan_k = 1;
+  p.nb_rows = (int)std::max(1L, ((long)c.heads * (p.tq_pad - c.total_q) + 255) / 256);
+  ESA_TIMED(esa_profile::kAttnPrep, st,
+            hipLaunchKernelGGL(wide_prep_kernel, dim3(2 + p.nb_rows), dim3(256), 0, st, p));
+  ESA_LAUNCH_CHECK();
+  WideArgs a{};
+  a.q = static_cast<const bf16*>(c.q); a.k = static_cast<const bf16*>(c.k); a.v = static_cast<const bf16*>(c.v);
+  a.out = static_cast<const bf16*>(c.out_in); a.dout = static_cast<const bf16*>(c.dout);
+  a.lse = c.lse_in; a.aux = p.aux;
+  a.total_q = c.total_q; a.total_k = c.total_k; a.heads = c.heads; a.tq_pad = p.tq_pad;
+  a.c = c.scale * kLog2e; a.scale = c.scale;
+  a.dq = static_cast<bf16*>(c.dq); a.dk = static_cast<bf16*>(c.dk); a.dv = static_cast<bf16*>(c.dv);
+  // dQ first: it writes the row statistics the dK/dV pass stages
+  a.groups = p.plan_q; a.count = p.count_q;
+  ESA_TIMED(esa_profile::kAttnBwdDq, st,
+            ESA_WIDE_LAUNCH(wide_dq_kernel, c.head_dim, dim3(wide_grid(c.total_q, c.nseg, c.heads)), st, a));
+  ESA_LAUNCH_CHECK();
+  a.groups = p.plan_k; a.count = p.count_k;
+  ESA_TIMED(esa_profile::kAttnBwdDkdv, st,
+            ESA_WIDE_LAUNCH(wide_dkdv_kernel, c.head_dim, dim3(wide_grid(c.total_k, c.nseg, c.heads)), st, a));
+  ESA_LAUNCH_CHECK();
+  return ESA_OK;
+}

@@ -185,3 +185,94 @@ def test_dense_f32(device, hd, heads, cross):
     cu_q, cu_k = cu_from_lengths(lengths_q), cu_from_lengths(lengths_k)
     q, k, v, g = _inputs(int(cu_q[-1]), int(cu_k[-1]), heads, hd, 11 * hd + heads, torch.float32)
     _run_and_check(device, q, k, v, g, cu_q, cu_k, torch.float32, {}, {})
+
+
+@pytest.mark.parametrize("hd,heads", [(32, 8), (32, 3), (64, 8), (64, 5)])
+def test_dense_bf16(device, hd, heads):
+    """Dense bf16 attention at wide heads (the MFMA kernels): segments of 1, tile-edge (32, 64, 65) and ragged
+    lengths, a 300-token one, and an empty segment."""
+    lengths = [1, 32, 64, 65, 0, 300, 17]
+    cu = cu_from_lengths(lengths)
+    t = int(cu[-1])
+    print(f"[head-dims] dense bf16 hd={hd} heads={heads} tokens={t}", flush=True)
+    q, k, v, g = _inputs(t, t, heads, hd, 5 * hd + heads, torch.bfloat16)
+    _run_and_check(device, q, k, v, g, cu, cu, torch.bfloat16, {}, {})
+
+
+@pytest.mark.parametrize("hd", [32, 64])
+def test_dense_bf16_cross(device, hd):
+    """Cross-attention: distinct query and key segments, one set without keys (its rows 0, LSE -inf) and one
+    without queries."""
+    cu_q, cu_k = cu_from_lengths([5, 40, 3, 0, 70]), cu_from_lengths([100, 0, 47, 33, 129])
+    q, k, v, g = _inputs(int(cu_q[-1]), int(cu_k[-1]), 4, hd, 17 + hd, torch.bfloat16)
+    _run_and_check(device, q, k, v, g, cu_q, cu_k, torch.bfloat16, {}, {})
+
+
+@pytest.mark.parametrize("hd", [32, 64])
+def test_dense_bf16_config1_wide(device, hd):
+    """Configuration 1's batch (32 protein-like graphs, 43,670 edge tokens) at head dim `hd`, dim 256: every
+    output finite; the first, largest and last graphs against the oracle."""
+    gb = generators.protein_like(seed=0)
+    cu = gb.cu_seqlens
+    t = int(cu[-1])
+    heads = 256 // hd
+    q, k, v, g = _inputs(t, t, heads, hd, 1234 + hd, torch.bfloat16)
+    scale = 1.0 / math.sqrt(hd)
+    qd, kd, vd = (x.to(device).requires_grad_(True) for x in (q, k, v))
+    cud = torch.as_tensor(cu).to(device)
+    out = A.varlen_attention(qd, kd, vd, cud, cud, gb.max_seqlen, gb.max_seqlen, softmax_scale=scale)
+    out.backward(g.to(device))
+    torch.cuda.synchronize()
+    for x in (out, qd.grad, kd.grad, vd.grad):
+        assert torch.isfinite(x.float()).all()
+    for b in (0, int(np.argmax(gb.edge_counts)), gb.num_graphs - 1):
+        s, e = int(cu[b]), int(cu[b + 1])
+        sub = np.array([0, e - s], np.int32)
+        ref, _ = OA.varlen_attention(q[s:e], k[s:e], v[s:e], sub, sub, scale)
+        assert_bf16_close(out.detach()[s:e].cpu(), ref, what=f"segment {b}")
+        rdq, rdk, rdv = OA.varlen_attention_bwd(g[s:e], q[s:e], k[s:e], v[s:e], sub, sub, scale)
+        assert_bf16_close(qd.grad[s:e].cpu(), rdq, grad_scale(rdq), f"dq segment {b}")
+        assert_bf16_close(kd.grad[s:e].cpu(), rdk, grad_scale(rdk), f"dk segment {b}")
+        assert_bf16_close(vd.grad[s:e].cpu(), rdv, grad_scale(rdv), f"dv segment {b}")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("hd", [32, 64])
+def test_pma_wide(device, hd, dtype):
+    """PMA seed pooling (esa_pma_fwd / _bwd) at wide heads: 4 seeds shared by every set, the seed gradient
+    summed over sets, against the oracle on the seeds repeated per set."""
+    lengths = [37, 130, 1, 64, 90]
+    cu_k = cu_from_lengths(lengths)
+    b, k_seeds, heads = len(lengths), 4, 4
+    q = seeded_normal((k_seeds, heads, hd), 3 + hd, dtype)
+    k = seeded_normal((int(cu_k[-1]), heads, hd), 4 + hd, dtype)
+    v = seeded_normal((int(cu_k[-1]), heads, hd), 5 + hd, dtype)
+    g = seeded_normal((b * k_seeds, heads, hd), 6 + hd, dtype)
+    scale = 1.0 / math.sqrt(hd)
+    qd, kd, vd = (x.to(device).requires_grad_(True) for x in (q, k, v))
+    out = A.pma_attention(qd, kd, vd, torch.as_tensor(cu_k).to(device), max(lengths), softmax_scale=scale)
+    out.backward(g.to(device))
+    torch.cuda.synchronize()
+    q_rep = q.repeat(b, 1, 1)
+    cu_q = cu_from_lengths([k_seeds] * b)
+    ref, _ = OA.varlen_attention(q_rep, k, v, cu_q, cu_k, scale)
+    rdq, rdk, rdv = OA.varlen_attention_bwd(g, q_rep, k, v, cu_q, cu_k, scale)
+    rdq = rdq.view(b, k_seeds, heads, hd).sum(0)
+    _close(out.detach().cpu(), ref, dtype, "out")
+    _close(qd.grad.cpu(), rdq, dtype, "dseeds", grad=True)
+    _close(kd.grad.cpu(), rdk, dtype, "dk", grad=True)
+    _close(vd.grad.cpu(), rdv, dtype, "dv", grad=True)
+
+
+@pytest.mark.parametrize("hd", [32, 64])
+def test_dense_bf16_deterministic(device, hd):
+    gb = generators.protein_like(seed=4, num_graphs=3, n_min=60, n_max=120)
+    cu = torch.as_tensor(gb.cu_seqlens).to(device)
+    t = int(gb.cu_seqlens[-1])
+    q, k, v, g = (x.to(device) for x in _inputs(t, t, 4, hd, 41, torch.bfloat16))
+    res = []
+    for _ in range(2):
+        out, lse = A.attn_fwd(q, k, v, cu, cu, 0, 0, 1.0 / math.sqrt(hd))
+        res.append((out, lse) + A.attn_bwd(g, q, k, v, out, lse, cu, cu, 0, 0, 1.0 / math.sqrt(hd)))
+    for a, b in zip(*res):
+        assert torch.equal(a, b)
