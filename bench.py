@@ -57,12 +57,14 @@ def parse():
     ap.add_argument("--no-sub", action="store_true",
                     help="headline only: skip the masked (configuration 2), gather (configuration 3), node, block "
                          "(configuration 0) and stack (configuration 4) sub-objects")
-    ap.add_argument("--config", choices=["varlen", "masked", "gather", "node", "block", "stack"], default="varlen",
+    ap.add_argument("--config", choices=["varlen", "masked", "gather", "node", "block", "stack", "wide"],
+                    default="varlen",
                     help="varlen: configuration 1 (default, the headline metric); masked: configuration 2 "
                          "(edge-masked MAB attention fwd+bwd); gather: configuration 3 (edge gather + CSR "
                          "segment sum, HBM-bound); node: node-mode (CSR adjacency) attention fwd+bwd on a "
                          "65,536-node batch; block: configuration 0 (fp32 ESA block forward on small "
-                         "molecules); stack: configuration 4 (bf16 ESA encoder stack train step)")
+                         "molecules); stack: configuration 4 (bf16 ESA encoder stack train step); wide: dense "
+                         "attention at head dims 64 and 32 (D = 512) on configuration 1's graphs")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy three times (HBM counter calibration)")
     return ap.parse_args()
@@ -160,9 +162,14 @@ def main():
             result["masked"] = bench_masked(args, sub=True)
             result["gather"] = bench_gather(args, sub=True)
             result["node"] = bench_node(args, sub=True)
+            result["wide"] = bench_wide(args)
             result["block"] = bench_block(args, sub=True)
             result["stack"] = bench_stack(args, sub=True)
         print(json.dumps(result), flush=True)
+        return
+    if args.config == "wide":
+        print(json.dumps({"metric": "edge-tokens/sec through ESA attn fwd+bwd at head dims 64 / 32",
+                          "value": None, "unit": "edge-tokens/s", **bench_wide(args)}), flush=True)
         return
     {"masked": bench_masked, "gather": bench_gather, "node": bench_node, "block": bench_block,
      "stack": bench_stack}[args.config](args)
@@ -270,6 +277,54 @@ def bench_varlen(args):
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(gb, args.seed)
     return result
+
+
+def bench_wide(args) -> dict:
+    """Dense varlen attention fwd+bwd at the wide head dims of MIND's larger configurations (D = 512: 8 heads of
+    64 in core/pretraining_config_qm9.yaml:27-28 / unimol / lba, 16 heads of 32 in pretraining_config_coconut.yaml:
+    21-22) on configuration 1's batch (the same graphs and token counts as the headline), bf16; the MFMA kernels of
+    esa_attn_wide.hip.  Per head dim: step time, edge-tokens/s, the step's fraction of dense-bf16 peak on 14 D per
+    pair, and the dominant kernel's roofline (the kernel FLOPs of the headline: forward 4 D, dK/dV 8 D, dQ 2 D
+    per pair)."""
+    import torch
+
+    from mind_amd import generators
+    from mind_amd.esa import attention
+
+    dev = torch.device("cuda", 0)
+    gb = generators.protein_like(seed=args.seed)
+    t, pairs, maxlen = int(gb.cu_seqlens[-1]), gb.sum_sq, gb.max_seqlen
+    cu = torch.as_tensor(gb.cu_seqlens).to(dev)
+    out = {"workload": "config1 graphs, dense varlen attention fwd+bwd at D = 512 (head dims 64 and 32), bf16",
+           "graphs": gb.num_graphs, "edge_tokens": t, "sum_L2": pairs, "dim": 512}
+    for hd in (64, 32):
+        heads = 512 // hd
+        d = heads * hd
+        g = torch.Generator().manual_seed(args.seed + hd)
+        q, k, v, go = (torch.randn(t, heads, hd, generator=g).to(torch.bfloat16).to(dev) for _ in range(4))
+        scale = 1.0 / hd ** 0.5
+
+        def step():
+            o, lse = attention.attn_fwd(q, k, v, cu, cu, maxlen, maxlen, scale)
+            attention.attn_bwd(go, q, k, v, o, lse, cu, cu, maxlen, maxlen, scale)
+
+        ms, wall_ms, kern, ms_prof = timed(step, args.steps, args.warmup)
+        per_pair = {"attn_fwd": 4 * d, "attn_bwd_dkdv": 8 * d, "attn_bwd_dq": 2 * d}
+        for name, rec in kern.items():
+            if name in per_pair:
+                rec["algorithmic_tflops"] = per_pair[name] * pairs / (rec["avg_us"] * 1e-6) / 1e12
+        dom = max((n for n in per_pair if n in kern), key=lambda n: kern[n]["avg_us"])
+        achieved = kern[dom]["algorithmic_tflops"]
+        tflops = 14 * d * pairs / (ms * 1e-3) / 1e12
+        out[f"hd{hd}"] = {"heads": heads, "head_dim": hd, "ms_per_step": ms, "wall_ms_per_step": wall_ms,
+                          "edge_tokens_per_s": t / (ms * 1e-3), "achieved_tflops": tflops,
+                          "mfma_util_pct": 100.0 * tflops / PEAK_BF16_TFLOPS, "ms_per_step_profiled": ms_prof,
+                          "kernels": kern,
+                          "roofline": {"bound": "mfma", "kernel": dom, "achieved": achieved,
+                                       "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                                       "frac": achieved / PEAK_BF16_TFLOPS}}
+        del q, k, v, go
+    return out
 
 
 def edge_mask_stats(src: np.ndarray, dst: np.ndarray, cu: np.ndarray, tile: int = 32) -> dict:

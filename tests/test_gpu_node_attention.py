@@ -296,15 +296,24 @@ def test_node_mask_argument_errors(device):
         A.attn_fwd(q, q, q, cu, cu, 4, 4, 0.25, edge_src=ix, edge_dst=ix, adj_indptr=ip, adj_indices=ix)
 
 
-def test_esa_node_mode_bf16_train_step(device):
+@pytest.mark.parametrize("dm,h", [(256, 16), (512, 32), (512, 16), (512, 8)])
+def test_esa_node_mode_bf16_train_step(device, dm, h):
     """ESA in node mode trained bf16-mixed (fp32 parameters under torch.autocast(bfloat16),
     core/train_pretrain.py:753) on the 32 protein-like graphs of configuration 1 as node graphs (9,603 nodes,
-    radius edges), layers M-S-M-S-P, D = 256, 16 heads, MLP 2 x 512, through the packed entry: the masked
-    layers run on the batch's node plan (forward and backward).  The loss is restricted to the smallest and
-    the largest graph, so the fp64 oracle over those two graphs alone gives the embeddings, dX and the
-    parameter gradients.  Bar: bf16, scaled by max(1, max |reference|)."""
+    radius edges), layers M-S-M-S-P, MLP 2 x (2 D), through the packed entry: the masked layers run on the
+    batch's node plan (forward and backward).  D = 256 with 16 heads (head dim 16); D = 512 with 8 heads (head
+    dim 64, the qm9 / unimol YAMLs' dim and heads, core/pretraining_config_qm9.yaml:27-28) and with 16 heads
+    (head dim 32, pretraining_config_coconut.yaml:21-22), and D = 512 with 32 heads of 16 as the control of the
+    head-dim-16 kernels at that width.  The loss is restricted to the smallest and the largest graph, so the
+    fp64 oracle over those two graphs alone gives the embeddings, dX and the parameter gradients.  Bar: bf16,
+    scaled by max(1, max |reference|).  At D = 512 the parameter gradients are checked by their relative L2 error
+    (<= 3e-2) and the max-abs bar: a weight gradient sums bf16 products over D-wide rows through five
+    bf16-mixed layers, and there the head-dim-16 control reaches the same errors as head dims 32 and 64
+    (relative norm 0.7-2.5e-2, mean-abs 0.5-4.3e-3 of max |ref|, by parameter) while each attention call's
+    own error is the same at all three head dims (relative 2.2-2.5e-3 for out, dQ, dK, dV)."""
     from mind_amd.esa.masked_layers import ESA
-    dm, h, layers = 256, 16, "MSMSP"
+    layers = "MSMSP"
+    print(f"[node-esa] D={dm} heads={h} head_dim={dm // h}", flush=True)
     gb = generators.protein_like(seed=3)
     sizes = gb.node_counts.astype(np.int64)
     t = int(sizes.sum())
@@ -361,4 +370,10 @@ def test_esa_node_mode_bf16_train_step(device):
     for name in ("encoder.0.sab.mab.fc_q.weight", "encoder.0.sab.mab.fc_k.weight", "encoder.0.norm.ln.weight",
                  "encoder.2.sab.mab.fc_v.bias", "encoder.2.mlp.mlp.0.weight", "decoder.0.pma.S"):
         ref = sd[name].grad
-        assert_bf16_close(params[name].grad.float().cpu().reshape(ref.shape), ref, grad_scale(ref), f"d {name}")
+        got = params[name].grad.float().cpu().reshape(ref.shape)
+        if dm == 256:
+            assert_bf16_close(got, ref, grad_scale(ref), f"d {name}")
+        else:
+            rel = float((got.double() - ref).norm() / ref.norm())
+            assert rel <= 3e-2, f"d {name}: relative L2 error {rel:.3e}"
+            assert float((got.double() - ref).abs().max()) <= 2e-2 * grad_scale(ref), f"d {name}: max-abs"

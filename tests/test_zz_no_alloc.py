@@ -69,6 +69,33 @@ def test_noalloc_edge_mask_at_the_documented_limit(device, dtype, heads):
         _compare(device, q, k, v, cu, int(gb.max_seqlen), kw)
 
 
+@pytest.mark.parametrize("hd", [32, 64])
+@pytest.mark.parametrize("mask", ["none", "edge", "node"])
+def test_noalloc_wide_heads(device, hd, mask):
+    """Head dims 32 / 64 (the dense MFMA kernels for wide heads, the gather kernels over the edge-mask plan and
+    over a node CSR): the no-allocation forward equals the allocating one, two calls in a row, the second
+    smaller."""
+    heads = 256 // hd
+    cases = ((generators.protein_like(seed=1, num_graphs=6), 31), (generators.protein_like(seed=2, num_graphs=2), 32))
+    for gb, seed in cases:
+        t = int(gb.cu_seqlens[-1])
+        print(f"[noalloc] wide hd={hd} mask={mask} tokens={t}", flush=True)
+        cu = torch.as_tensor(gb.cu_seqlens).to(device)
+        q, k, v = (seeded_normal((t, heads, hd), seed + i, torch.bfloat16).to(device) for i in range(3))
+        kw = {}
+        if mask == "edge":
+            kw = {"edge_src": torch.as_tensor(gb.edge_index[0].astype(np.int32)).to(device),
+                  "edge_dst": torch.as_tensor(gb.edge_index[1].astype(np.int32)).to(device)}
+        elif mask == "node":
+            ei, bm = node_graph(seed, [40, 70, 25])
+            na = NodeAdjacency.from_edge_index(torch.as_tensor(ei).to(device), torch.as_tensor(bm).to(device), 3, 70)
+            t = len(bm)
+            cu = na.cu_seqlens
+            q, k, v = (seeded_normal((t, heads, hd), seed + i, torch.bfloat16).to(device) for i in range(3))
+            kw = {"adj_indptr": na.indptr, "adj_indices": na.indices}
+        _compare(device, q, k, v, cu, int(gb.max_seqlen), kw)
+
+
 def test_noalloc_forward_node_mask(device):
     for sizes, seed in (([60, 45, 80], 5), ([12, 7], 6)):
         ei, bm = node_graph(seed, sizes)
