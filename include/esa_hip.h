@@ -32,7 +32,7 @@ extern "C" {
 #define ESA_OK 0
 #define ESA_ERR_NULL (-1)       /* a required pointer is null */
 #define ESA_ERR_SHAPE (-2)      /* a size or count is out of range */
-#define ESA_ERR_HEAD_DIM (-3)   /* head_dim other than 16 */
+#define ESA_ERR_HEAD_DIM (-3)   /* head_dim other than 16, 24, 32 or 64 */
 #define ESA_ERR_WORKSPACE (-4)  /* workspace smaller than the query says */
 #define ESA_ERR_DTYPE (-5)      /* unsupported dtype code */
 #define ESA_ERR_ALIGN (-6)      /* pointer not 16-byte aligned */
@@ -60,9 +60,11 @@ ESA_API const char* esa_version(void);
 /* called at esa/mha_flash_varlen.py:177-184, and the per-graph attention of */
 /* memory_efficient_attention / SDPA at esa/mha.py:76 and :80-83.            */
 /*                                                                           */
-/* q [total_q, heads, 16], k and v [total_k, heads, 16], out like q, all of  */
-/* `dtype`: ESA_BF16 (bf16 MFMA, fp32 softmax; the bf16-mixed training path) */
-/* or ESA_F32 (fp32 throughout; the reference's fp32 modules).               */
+/* q [total_q, heads, head_dim], k and v [total_k, heads, head_dim], out     */
+/* like q, all of `dtype`: ESA_BF16 (bf16 MFMA, fp32 softmax; the bf16-mixed */
+/* training path) or ESA_F32 (fp32 throughout; the reference's fp32          */
+/* modules).  head_dim is 16, 24, 32 or 64 (dim / num_heads of every MIND    */
+/* configuration, esa/mha.py:50-52).                                         */
 /*                                                                           */
 /* mask_kind ESA_MASK_EDGE: mask_a / mask_b are the per-token endpoint node  */
 /* ids src / dst [total_q] (self-attention, total_q == total_k, same         */
@@ -84,7 +86,7 @@ ESA_API const char* esa_version(void);
 /* as bias[b, src, dst] = 0 per edge src -> dst (query = src).  Each row     */
 /* lists its keys in ascending order; an entry equal to its predecessor      */
 /* counts once (a repeated edge); entries outside the query's segment are    */
-/* ignored.  Work is O(n_mask_edges * heads * 16).                           */
+/* ignored.  Work is O(n_mask_edges * heads * head_dim).                     */
 /*                                                                           */
 /* mask_kind ESA_MASK_NODE_PLAN: the same mask with mask_b = a node plan     */
 /* built once by esa_node_plan_build from (mask_a, indices): its first       */
@@ -192,11 +194,12 @@ ESA_API int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k,
 /* ------------------------------------------------------------------------ */
 /* PMA seed pooling: PMA.forward = MAB(S.repeat(B, 1, 1), X) (esa/mha.py:   */
 /* 101-109; PMAFlashVarlen, esa/mha_flash_varlen.py:233-248) over packed     */
-/* sets.  q [k_seeds, H, 16] holds the projected seeds fc_q(S), shared by all */
-/* batch sets; k, v [total_k, H, 16] with cu_seqlens_k [batch + 1].  out is   */
-/* [batch * k_seeds, H, 16] set-major, softmax_lse [H][batch * k_seeds].     */
-/* The backward's dq [k_seeds, H, 16] sums the sets' seed gradients in set    */
-/* order (deterministic).  Workspace size from esa_pma_workspace_size.       */
+/* sets.  q [k_seeds, H, head_dim] holds the projected seeds fc_q(S), shared */
+/* by all batch sets; k, v [total_k, H, head_dim] with cu_seqlens_k          */
+/* [batch + 1].  out is [batch * k_seeds, H, head_dim] set-major,            */
+/* softmax_lse [H][batch * k_seeds].  The backward's dq [k_seeds, H,         */
+/* head_dim] sums the sets' seed gradients in set order (deterministic).     */
+/* Workspace size from esa_pma_workspace_size.                               */
 /* ------------------------------------------------------------------------ */
 ESA_API int esa_pma_workspace_size(int batch, int k_seeds, int total_k, int heads,
                            int head_dim, int dtype, int backward, size_t* bytes);

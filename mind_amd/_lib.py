@@ -29,7 +29,7 @@ ESA_MASK_NODE_PLAN = 4
 ERRORS = {
     -1: "ESA_ERR_NULL (a required pointer is null)",
     -2: "ESA_ERR_SHAPE (a size or count is out of range)",
-    -3: "ESA_ERR_HEAD_DIM (head_dim must be 16, 32 or 64)",
+    -3: "ESA_ERR_HEAD_DIM (head_dim must be 16, 24, 32 or 64)",
     -4: "ESA_ERR_WORKSPACE (workspace too small)",
     -5: "ESA_ERR_DTYPE (unsupported dtype)",
     -6: "ESA_ERR_ALIGN (pointer not 16-byte aligned)",

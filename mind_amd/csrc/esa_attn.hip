@@ -1354,7 +1354,7 @@ struct AttnF32Args {
 
 constexpr int kF32Threads = kGroupTok;
 
-// Rows of HD fp32 values (HD = 16, 32 or 64) as float4 chunks.
+// Rows of HD fp32 values (HD = 16, 24, 32 or 64) as float4 chunks.
 template <int HD>
 DEVI void loadn(const float* p, float x[HD]) {
 #pragma unroll
@@ -1916,10 +1916,10 @@ __global__ __launch_bounds__(256) void edge_plan_decode_kernel(const PlanView V,
 
 bool misaligned(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) != 0; }
 
-// Head dims: 16 on every path; 32 and 64 on the node-mode and edge-mask
+// Head dims: 16 on every path; 24, 32 and 64 on the node-mode and edge-mask
 // gather kernels, the fp32 kernels and the dense bf16 kernels of
 // esa_attn_wide.hip.
-bool head_dim_ok(int head_dim) { return head_dim == 16 || head_dim == 32 || head_dim == 64; }
+bool head_dim_ok(int head_dim) { return head_dim == 16 || head_dim == 24 || head_dim == 32 || head_dim == 64; }
 
 int check_common(int batch, int total_q, int total_k, int heads, int head_dim, int dtype, int mask_kind) {
   if (!head_dim_ok(head_dim)) return ESA_ERR_HEAD_DIM;
@@ -2057,10 +2057,11 @@ GraphAttnArgs edge_gather_args(const void* plan, const void* q, const void* k, c
   return g;
 }
 
-// KERNEL<false, HD> (the fp32 kernels without a mask) for head dim 16, 32 or 64.
+// KERNEL<false, HD> (the fp32 kernels without a mask) for head dim 16, 24, 32 or 64.
 #define ESA_F32_LAUNCH(KERNEL, hd, grid, st, a)                                             \
   do {                                                                                      \
     if (hd == 16) hipLaunchKernelGGL((KERNEL<false, 16>), grid, dim3(kF32Threads), 0, st, a);       \
+    else if (hd == 24) hipLaunchKernelGGL((KERNEL<false, 24>), grid, dim3(kF32Threads), 0, st, a);  \
     else if (hd == 32) hipLaunchKernelGGL((KERNEL<false, 32>), grid, dim3(kF32Threads), 0, st, a);  \
     else hipLaunchKernelGGL((KERNEL<false, 64>), grid, dim3(kF32Threads), 0, st, a);               \
   } while (0)

@@ -665,7 +665,7 @@ int dense_attn_workspace_size(int total_q, int total_k, int heads, int head_dim,
     *bytes = dense_ws(total_q, total_k, heads, backward).total;
     return ESA_OK;
   }
-  if (head_dim != 32 && head_dim != 64) return ESA_ERR_HEAD_DIM;
+  if (head_dim != 24 && head_dim != 32 && head_dim != 64) return ESA_ERR_HEAD_DIM;
   *bytes = wide_attn_workspace_size(total_q, total_k, heads, head_dim, backward);
   return ESA_OK;
 }

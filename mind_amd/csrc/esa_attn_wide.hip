@@ -1,7 +1,9 @@
-// Dense varlen attention (no mask) at head dims 32 and 64, bf16 operands,
+// Dense varlen attention (no mask) at head dims 24, 32 and 64, bf16 operands,
 // fp32 softmax, on gfx950: the flash_attn_varlen_func drop-in
 // (esa/mha_flash_varlen.py:177-184, causal=False, dropout 0) for the ESA
-// configurations whose dim / num_heads is 32 or 64 (esa/mha.py:50-52).
+// configurations whose dim / num_heads is 24, 32 or 64 (esa/mha.py:50-52).
+// Head dim 24 computes as 32: its rows are read as three 8-dim octets, the
+// fourth octet of every operand is zero, and output dims 24..31 are dropped.
 //
 // Work items are 128-token groups cut from each segment on its own (the
 // segment plans of the head-dim-16 kernels): a block's four waves own four
@@ -69,16 +71,24 @@ DEVI bf16x8 tr_dims(const bf16* rows, int m, int j, int lane) {
 // Output dims 32 m + 8 (r / 4) + 4 h + (r % 4) of a product accumulator, 4
 // consecutive dims per register quad: written as bf16 x 4.
 template <int HD>
-DEVI void store_acc(bf16* __restrict__ row, const f32x16 (&acc)[HD / 32], float mul, int h) {
+DEVI void store_acc(bf16* __restrict__ row, const f32x16 (&acc)[(HD + 31) / 32], float mul, int h) {
 #pragma unroll
-  for (int m = 0; m < HD / 32; ++m)
+  for (int m = 0; m < (HD + 31) / 32; ++m)
 #pragma unroll
     for (int a = 0; a < 4; ++a) {
+      if (32 * m + 8 * a >= HD) continue;   // the padding dims of head dim 24
       bf16x4 x;
 #pragma unroll
       for (int e = 0; e < 4; ++e) x[e] = (bf16)(acc[m][4 * a + e] * mul);
       *reinterpret_cast<bf16x4*>(row + 32 * m + 8 * a + 4 * h) = x;
     }
+}
+
+// Dims 8 o .. 8 o + 7 of a global row; zeros for the padding octet of head dim 24.
+template <int HD>
+DEVI bf16x8 row_op(const bf16* __restrict__ row, int o) {
+  if (8 * o >= HD) return bf16x8{};
+  return *reinterpret_cast<const bf16x8*>(row + 8 * o);
 }
 
 // Block -> (work item, head): head fastest, so the blocks of one head land on
@@ -91,23 +101,26 @@ DEVI void wide_item_head(int H, int& item, int& head) {
 // ---- staging: stage st covers partner tokens g0 + 64 st .. + 63 of tensors
 // A and B ([T][H][HD] bf16); each thread holds CPT 16-byte chunks (token-major
 // over (tensor, token, octet), so consecutive threads read consecutive bytes of
-// a row) in a ring of two register sets.
+// a row) in a ring of two register sets.  The NR = HD / 8 octets of a row are
+// staged; LDS holds NO = 4 ceil(HD / 32) octets per token.
 template <int HD>
 struct WStage {
-  static constexpr int NO = HD / 8;
-  static constexpr int CPT = 2 * kWStage * NO / 256;
+  static constexpr int NR = HD / 8;
+  static constexpr int NCH = 2 * kWStage * NR;            // chunks per stage
+  static constexpr int CPT = (NCH + 255) / 256;
   i32x4 r[CPT];
 };
 
 template <int HD>
 DEVI WStage<HD> wide_gload(const bf16* a, const bf16* b, int g0, int total, int H, int head, int tid) {
-  constexpr int NO = HD / 8;
+  constexpr int NR = HD / 8;
   WStage<HD> s;
 #pragma unroll
   for (int i = 0; i < WStage<HD>::CPT; ++i) {
     const int c = tid + 256 * i;
-    const int tensor = c / (kWStage * NO), rem = c - tensor * (kWStage * NO);
-    const int tok = rem / NO, o = rem - tok * NO;
+    if (WStage<HD>::NCH % 256 != 0 && c >= WStage<HD>::NCH) { s.r[i] = i32x4{}; continue; }
+    const int tensor = c / (kWStage * NR), rem = c - tensor * (kWStage * NR);
+    const int tok = rem / NR, o = rem - tok * NR;
     const int t = min(g0 + tok, total - 1);
     s.r[i] = *reinterpret_cast<const i32x4*>((tensor ? b : a) + ((size_t)t * H + head) * HD + 8 * o);
   }
@@ -115,13 +128,28 @@ DEVI WStage<HD> wide_gload(const bf16* a, const bf16* b, int g0, int total, int 
 }
 template <int HD>
 DEVI void wide_lstore(bf16* sa, bf16* sb, const WStage<HD>& s, int tid) {
-  constexpr int NO = HD / 8;
+  constexpr int NR = HD / 8;
 #pragma unroll
   for (int i = 0; i < WStage<HD>::CPT; ++i) {
     const int c = tid + 256 * i;
-    const int tensor = c / (kWStage * NO), rem = c - tensor * (kWStage * NO);
-    const int tok = rem / NO, o = rem - tok * NO;
+    if (WStage<HD>::NCH % 256 != 0 && c >= WStage<HD>::NCH) continue;
+    const int tensor = c / (kWStage * NR), rem = c - tensor * (kWStage * NR);
+    const int tok = rem / NR, o = rem - tok * NR;
     *reinterpret_cast<i32x4*>((tensor ? sb : sa) + ((size_t)o * kWTokPad + tok) * 8) = s.r[i];
+  }
+}
+// Head dim 24: the padding octet of the four staging buffers (two tensors,
+// two buffers) is zeroed once, before the first stage's barrier; staging never
+// writes it.
+template <int HD>
+DEVI void wide_zero_pad(bf16* a0, bf16* a1, bf16* b0, bf16* b1, int tid) {
+  constexpr int NR = HD / 8, NO = (HD + 31) / 32 * 4, NP = NO - NR;
+  if (NP == 0) return;
+  for (int i = tid; i < 4 * kWStage * NP; i += 256) {
+    const int buf = i / (kWStage * NP), rem = i - buf * (kWStage * NP);
+    const int tok = rem / NP, o = NR + rem - tok * NP;
+    bf16* base = buf == 0 ? a0 : buf == 1 ? a1 : buf == 2 ? b0 : b1;
+    *reinterpret_cast<i32x4*>(base + ((size_t)o * kWTokPad + tok) * 8) = i32x4{};
   }
 }
 
@@ -153,7 +181,7 @@ constexpr int kWGroup = kWaves * kTile;   // 128 owned tokens per block
 // ------------------------------------------------------------------ forward
 template <int HD>
 __global__ __launch_bounds__(256) void wide_fwd_kernel(const WideArgs a) {
-  constexpr int NC = HD / 16, NM = HD / 32, NO = HD / 8;
+  constexpr int HP = (HD + 31) / 32 * 32, NC = HP / 16, NM = HP / 32, NO = HP / 8;
   __shared__ __align__(16) bf16 sK[2][NO * kWTokPad * 8];
   __shared__ __align__(16) bf16 sV[2][NO * kWTokPad * 8];
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -168,7 +196,8 @@ __global__ __launch_bounds__(256) void wide_fwd_kernel(const WideArgs a) {
   const bf16* qrow = a.q + ((size_t)(valid ? t : g.x) * H + head) * HD;
   bf16x8 qop[NC];
 #pragma unroll
-  for (int c = 0; c < NC; ++c) qop[c] = *reinterpret_cast<const bf16x8*>(qrow + 16 * c + 8 * h);
+  for (int c = 0; c < NC; ++c) qop[c] = row_op<HD>(qrow, 2 * c + h);
+  wide_zero_pad<HD>(sK[0], sK[1], sV[0], sV[1], tid);
   f32x16 acc[NM];
 #pragma unroll
   for (int m = 0; m < NM; ++m) acc[m] = f32x16{};
@@ -231,7 +260,7 @@ __global__ __launch_bounds__(256) void wide_fwd_kernel(const WideArgs a) {
 // statistics {-LSE2 / c, -D} of its queries.
 template <int HD>
 __global__ __launch_bounds__(256) void wide_dq_kernel(const WideArgs a) {
-  constexpr int NC = HD / 16, NM = HD / 32, NO = HD / 8;
+  constexpr int HP = (HD + 31) / 32 * 32, NC = HP / 16, NM = HP / 32, NO = HP / 8;
   __shared__ __align__(16) bf16 sK[2][NO * kWTokPad * 8];
   __shared__ __align__(16) bf16 sV[2][NO * kWTokPad * 8];
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -248,12 +277,13 @@ __global__ __launch_bounds__(256) void wide_dq_kernel(const WideArgs a) {
   float dsum = 0.f;
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
-    qop[c] = *reinterpret_cast<const bf16x8*>(a.q + row + 16 * c + 8 * h);
-    gop[c] = *reinterpret_cast<const bf16x8*>(a.dout + row + 16 * c + 8 * h);
-    const bf16x8 o = *reinterpret_cast<const bf16x8*>(a.out + row + 16 * c + 8 * h);
+    qop[c] = row_op<HD>(a.q + row, 2 * c + h);
+    gop[c] = row_op<HD>(a.dout + row, 2 * c + h);
+    const bf16x8 o = row_op<HD>(a.out + row, 2 * c + h);
 #pragma unroll
     for (int e = 0; e < 8; ++e) dsum = fmaf((float)gop[c][e], (float)o[e], dsum);
   }
+  wide_zero_pad<HD>(sK[0], sK[1], sV[0], sV[1], tid);
   dsum += __shfl_xor(dsum, 32);
   const float lq = a.lse[(size_t)head * a.total_q + (valid ? t : g.x)];
   const float lse2 = lq == -INFINITY ? INFINITY : lq * kLog2e;   // rows without keys: P = 0
@@ -304,7 +334,7 @@ __global__ __launch_bounds__(256) void wide_dq_kernel(const WideArgs a) {
 // and their statistics.
 template <int HD>
 __global__ __launch_bounds__(256) void wide_dkdv_kernel(const WideArgs a) {
-  constexpr int NC = HD / 16, NM = HD / 32, NO = HD / 8;
+  constexpr int HP = (HD + 31) / 32 * 32, NC = HP / 16, NM = HP / 32, NO = HP / 8;
   __shared__ __align__(16) bf16 sQ[2][NO * kWTokPad * 8];
   __shared__ __align__(16) bf16 sG[2][NO * kWTokPad * 8];
   __shared__ __align__(16) float sLse[2][kWStage], sDel[2][kWStage];
@@ -321,9 +351,10 @@ __global__ __launch_bounds__(256) void wide_dkdv_kernel(const WideArgs a) {
   bf16x8 kop[NC], vop[NC];
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
-    kop[c] = *reinterpret_cast<const bf16x8*>(a.k + row + 16 * c + 8 * h);
-    vop[c] = *reinterpret_cast<const bf16x8*>(a.v + row + 16 * c + 8 * h);
+    kop[c] = row_op<HD>(a.k + row, 2 * c + h);
+    vop[c] = row_op<HD>(a.v + row, 2 * c + h);
   }
+  wide_zero_pad<HD>(sQ[0], sQ[1], sG[0], sG[1], tid);
   f32x16 dva[NM], dka[NM];
 #pragma unroll
   for (int m = 0; m < NM; ++m) dva[m] = dka[m] = f32x16{};
@@ -444,7 +475,8 @@ unsigned wide_grid(int total_outer, int nseg, int heads) {
 
 #define ESA_WIDE_LAUNCH(KERNEL, hd, grid, st, a)                                      \
   do {                                                                                \
-    if (hd == 32) hipLaunchKernelGGL((KERNEL<32>), grid, dim3(256), 0, st, a);       \
+    if (hd == 24) hipLaunchKernelGGL((KERNEL<24>), grid, dim3(256), 0, st, a);       \
+    else if (hd == 32) hipLaunchKernelGGL((KERNEL<32>), grid, dim3(256), 0, st, a);  \
     else hipLaunchKernelGGL((KERNEL<64>), grid, dim3(256), 0, st, a);                \
   } while (0)
 
@@ -456,7 +488,7 @@ size_t wide_attn_workspace_size(int total_q, int total_k, int heads, int head_di
 }
 
 int wide_attn_fwd(const DenseAttnCall& c, void* workspace, size_t workspace_bytes, hipStream_t st) {
-  if (c.head_dim != 32 && c.head_dim != 64) return ESA_ERR_HEAD_DIM;
+  if (c.head_dim != 24 && c.head_dim != 32 && c.head_dim != 64) return ESA_ERR_HEAD_DIM;
   const WideWs w = wide_ws(c.total_q, c.total_k, c.heads, false);
   if (workspace_bytes < w.total) return ESA_ERR_WORKSPACE;
   char* ws = static_cast<char*>(workspace);
@@ -480,7 +512,7 @@ int wide_attn_fwd(const DenseAttnCall& c, void* workspace, size_t workspace_byte
 }
 
 int wide_attn_bwd(const DenseAttnCall& c, void* workspace, size_t workspace_bytes, hipStream_t st) {
-  if (c.head_dim != 32 && c.head_dim != 64) return ESA_ERR_HEAD_DIM;
+  if (c.head_dim != 24 && c.head_dim != 32 && c.head_dim != 64) return ESA_ERR_HEAD_DIM;
   const WideWs w = wide_ws(c.total_q, c.total_k, c.heads, true);
   if (workspace_bytes < w.total) return ESA_ERR_WORKSPACE;
   char* ws = static_cast<char*>(workspace);

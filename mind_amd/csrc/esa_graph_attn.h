@@ -33,7 +33,7 @@ struct GraphAttnArgs {
 };
 
 // Head dims of the gather kernels.
-inline bool graph_head_dim_ok(int hd) { return hd == 16 || hd == 32 || hd == 64; }
+inline bool graph_head_dim_ok(int hd) { return hd == 16 || hd == 24 || hd == 32 || hd == 64; }
 
 // Edge-mask attention over a plan's lists (a.edge set, a.q_bounds / k_bounds
 // the plan's bounds): the same gather kernels with the partners of a token

@@ -18,9 +18,10 @@
 //
 // The work is O(partners * heads * head_dim) -- a few to a few tens of
 // partners per token -- so it is gathered per token instead of tiled for
-// MFMA: one wave per token, head_dim / 4 lanes per head with four dims each
-// (a wave covers 256 / head_dim heads per pass), scores reduced over a head's
-// lanes by DPP butterflies (identical in all of them), fp32 online softmax.
+// MFMA: one wave per token, a power-of-two group of lanes per head with four
+// dims on each lane (head dim 16: 4 lanes, 32: 8, 64: 16; 24: 8 lanes of
+// which the last two hold zeros), scores reduced over a head's lanes by DPP
+// butterflies (identical in all of them), fp32 online softmax.
 // The forward and dQ gather over the token's partners; dK / dV over the
 // queries that attend to the key (node mode: the transposed CSR, built per
 // call with the library's stable CSR sort or once per batch into a node plan;
@@ -60,10 +61,9 @@ DEVI float dpp(float x) {
   return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
 }
 
-// Sum over the L = head_dim / 4 lanes of a head (aligned groups of 4, 8 or
-// 16 lanes): butterflies within each quad ([1,0,3,2], [2,3,0,1]), then the
-// other quad of each half row (row_half_mirror) and the other half of each
-// row (row_mirror).  Addition is commutative, so every lane of the group
+// Sum over the L lanes of a head (aligned groups of 4, 8 or 16 lanes):
+// butterflies within each quad ([1,0,3,2], [2,3,0,1]), then the other quad of
+// each half row (row_half_mirror) and the other half of each row (row_mirror).  Addition is commutative, so every lane of the group
 // holds the identical result.
 template <int L>
 DEVI float head_sum(float x) {
@@ -76,6 +76,24 @@ DEVI float head_sum(float x) {
 DEVI float dot4(const float a[4], const float b[4]) {
   return fmaf(a[3], b[3], fmaf(a[2], b[2], fmaf(a[1], b[1], a[0] * b[0])));
 }
+
+// Lanes of one head: HD / 4 of them carry four dims each, rounded up to a
+// power of two (head dim 24: 6 of 8).  A lane past the head's dims reads the
+// last dims (an in-row address), zeroes its own token's operand so that its
+// terms of every dot product are 0, and stores nothing.
+template <int HD>
+struct HeadLanes {
+  static constexpr int L = HD == 24 ? 8 : HD / 4;
+  static constexpr int HPP = 64 / L;   // heads per pass of a wave
+  int li, d0;
+  bool dims;
+  DEVI HeadLanes(int lane) : li(lane % L), d0(4 * min(lane % L, HD / 4 - 1)), dims(lane % L < HD / 4) {}
+  DEVI void own(float v[4]) const {
+    if (HD / 4 == L) return;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = dims ? v[i] : 0.f;
+  }
+};
 
 // fp32 path: the device library's exp2f / log2f; bf16 path: the hardware
 // approximations (as in the tiled kernels).
@@ -244,16 +262,19 @@ DEVI WalkSrc walk_src(const GraphEdgeLists& e, int2 bounds, int t) {
 
 template <typename T, int HD, class Src>
 DEVI void fwd_token(const GraphAttnArgs& a, int t, const Src& src0) {
-  constexpr int L = HD / 4, HPP = 64 / L;
+  constexpr int L = HeadLanes<HD>::L, HPP = HeadLanes<HD>::HPP;
   const T* __restrict__ q = static_cast<const T*>(a.q);
   const T* __restrict__ k = static_cast<const T*>(a.k);
   const T* __restrict__ v = static_cast<const T*>(a.v);
-  const int lane = threadIdx.x & 63, H = a.heads, d0 = 4 * (lane % L);
+  const int lane = threadIdx.x & 63, H = a.heads;
+  const HeadLanes<HD> hl(lane);
+  const int d0 = hl.d0;
   for (int h0 = 0; h0 < H; h0 += HPP) {
     const int h = h0 + lane / L;
     const int hc = min(h, H - 1);
     float qv[4], acc[4] = {0.f, 0.f, 0.f, 0.f};
     load4<T>(q + ((size_t)t * H + hc) * HD + d0, qv);
+    hl.own(qv);
     float m = -INFINITY, l = 0.f;
     Src src = src0;
     int j[kGU];
@@ -287,8 +308,8 @@ DEVI void fwd_token(const GraphAttnArgs& a, int t, const Src& src0) {
       m = mt;
     }
     if (h < H) {
-      store4<T>(static_cast<T*>(a.out) + ((size_t)t * H + h) * HD + d0, acc, l > 0.f ? 1.f / l : 0.f);
-      if (lane % L == 0) a.lse[(size_t)h * a.total_q + t] = l > 0.f ? (m + lg2<T>(l)) * kLn2 : -INFINITY;
+      if (hl.dims) store4<T>(static_cast<T*>(a.out) + ((size_t)t * H + h) * HD + d0, acc, l > 0.f ? 1.f / l : 0.f);
+      if (hl.li == 0) a.lse[(size_t)h * a.total_q + t] = l > 0.f ? (m + lg2<T>(l)) * kLn2 : -INFINITY;
     }
   }
 }
@@ -297,13 +318,15 @@ DEVI void fwd_token(const GraphAttnArgs& a, int t, const Src& src0) {
 // D_i = rowsum(dO_i * O_i) per head for the dK / dV pass.
 template <typename T, int HD, class Src>
 DEVI void dq_token(const GraphAttnArgs& a, int t, const Src& src0) {
-  constexpr int L = HD / 4, HPP = 64 / L;
+  constexpr int L = HeadLanes<HD>::L, HPP = HeadLanes<HD>::HPP;
   const T* __restrict__ q = static_cast<const T*>(a.q);
   const T* __restrict__ k = static_cast<const T*>(a.k);
   const T* __restrict__ v = static_cast<const T*>(a.v);
   const T* __restrict__ o = static_cast<const T*>(a.out_in);
   const T* __restrict__ g = static_cast<const T*>(a.dout);
-  const int lane = threadIdx.x & 63, H = a.heads, d0 = 4 * (lane % L);
+  const int lane = threadIdx.x & 63, H = a.heads;
+  const HeadLanes<HD> hl(lane);
+  const int d0 = hl.d0;
   for (int h0 = 0; h0 < H; h0 += HPP) {
     const int h = h0 + lane / L;
     const int hc = min(h, H - 1);
@@ -312,10 +335,12 @@ DEVI void dq_token(const GraphAttnArgs& a, int t, const Src& src0) {
     load4<T>(q + row, qv);
     load4<T>(g + row, gv);
     load4<T>(o + row, ov);
+    hl.own(qv);
+    hl.own(gv);
     const float dsum = head_sum<L>(dot4(gv, ov));
     const float l = a.lse_in[(size_t)hc * a.total_q + t];
     const float l2 = l == -INFINITY ? INFINITY : l * kLog2e;
-    if (h < H && lane % L == 0) a.dsum[(size_t)h * a.total_q + t] = dsum;
+    if (h < H && hl.li == 0) a.dsum[(size_t)h * a.total_q + t] = dsum;
     Src src = src0;
     int j[kGU];
     bool ok[kGU];
@@ -334,7 +359,7 @@ DEVI void dq_token(const GraphAttnArgs& a, int t, const Src& src0) {
         for (int i = 0; i < 4; ++i) acc[i] = fmaf(ds, kr[u][i], acc[i]);
       }
     }
-    if (h < H) store4<T>(static_cast<T*>(a.dq) + ((size_t)t * H + h) * HD + d0, acc, a.scale);
+    if (h < H && hl.dims) store4<T>(static_cast<T*>(a.dq) + ((size_t)t * H + h) * HD + d0, acc, a.scale);
   }
 }
 
@@ -342,12 +367,14 @@ DEVI void dq_token(const GraphAttnArgs& a, int t, const Src& src0) {
 // queries i that attend to key j (ascending).
 template <typename T, int HD, class Src>
 DEVI void dkdv_token(const GraphAttnArgs& a, int t, const Src& src0) {
-  constexpr int L = HD / 4, HPP = 64 / L;
+  constexpr int L = HeadLanes<HD>::L, HPP = HeadLanes<HD>::HPP;
   const T* __restrict__ q = static_cast<const T*>(a.q);
   const T* __restrict__ k = static_cast<const T*>(a.k);
   const T* __restrict__ v = static_cast<const T*>(a.v);
   const T* __restrict__ g = static_cast<const T*>(a.dout);
-  const int lane = threadIdx.x & 63, H = a.heads, d0 = 4 * (lane % L);
+  const int lane = threadIdx.x & 63, H = a.heads;
+  const HeadLanes<HD> hl(lane);
+  const int d0 = hl.d0;
   for (int h0 = 0; h0 < H; h0 += HPP) {
     const int h = h0 + lane / L;
     const int hc = min(h, H - 1);
@@ -355,6 +382,8 @@ DEVI void dkdv_token(const GraphAttnArgs& a, int t, const Src& src0) {
     float kv[4], vv[4], dk[4] = {0.f, 0.f, 0.f, 0.f}, dv[4] = {0.f, 0.f, 0.f, 0.f};
     load4<T>(k + row, kv);
     load4<T>(v + row, vv);
+    hl.own(kv);
+    hl.own(vv);
     Src src = src0;
     int i[kGU];
     bool ok[kGU];
@@ -379,7 +408,7 @@ DEVI void dkdv_token(const GraphAttnArgs& a, int t, const Src& src0) {
         }
       }
     }
-    if (h < H) {
+    if (h < H && hl.dims) {
       store4<T>(static_cast<T*>(a.dk) + ((size_t)t * H + h) * HD + d0, dk, a.scale);
       store4<T>(static_cast<T*>(a.dv) + ((size_t)t * H + h) * HD + d0, dv, 1.f);
     }
@@ -592,10 +621,12 @@ namespace {
   do {                                                                                            \
     if (dtype == ESA_F32) {                                                                       \
       if (hd == 16) hipLaunchKernelGGL((KERNEL<float, 16>), grid, dim3(256), 0, st, a);           \
+      else if (hd == 24) hipLaunchKernelGGL((KERNEL<float, 24>), grid, dim3(256), 0, st, a);      \
       else if (hd == 32) hipLaunchKernelGGL((KERNEL<float, 32>), grid, dim3(256), 0, st, a);      \
       else hipLaunchKernelGGL((KERNEL<float, 64>), grid, dim3(256), 0, st, a);                    \
     } else {                                                                                      \
       if (hd == 16) hipLaunchKernelGGL((KERNEL<bf16, 16>), grid, dim3(256), 0, st, a);            \
+      else if (hd == 24) hipLaunchKernelGGL((KERNEL<bf16, 24>), grid, dim3(256), 0, st, a);       \
       else if (hd == 32) hipLaunchKernelGGL((KERNEL<bf16, 32>), grid, dim3(256), 0, st, a);       \
       else hipLaunchKernelGGL((KERNEL<bf16, 64>), grid, dim3(256), 0, st, a);                     \
     }                                                                                             \

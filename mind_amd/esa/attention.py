@@ -5,7 +5,7 @@ reference calls it (esa/mha_flash_varlen.py:177-184: causal=False, dropout 0,
 ``softmax_scale=None`` meaning 1/sqrt(head_dim)), extended with the
 edge-adjacency mask of esa/masked_layers.py:121-142 evaluated on the fly from
 per-token ``(src, dst)`` node ids.  Tensors are packed ``[total, heads,
-head_dim]`` (head_dim 16, 32 or 64: ESA's dim / heads) bf16 (MFMA kernels, fp32
+head_dim]`` (head_dim 16, 24, 32 or 64: ESA's dim / heads) bf16 (MFMA kernels, fp32
 softmax) or float32 (fp32 throughout) with int32 ``cu_seqlens``.  Backward is
 deterministic.
 """
@@ -18,7 +18,7 @@ import torch
 
 from .. import _lib
 
-HEAD_DIMS = (16, 32, 64)   # head dims the kernels take
+HEAD_DIMS = (16, 24, 32, 64)   # head dims the kernels take
 
 
 _DTYPES = {torch.bfloat16: _lib.ESA_BF16, torch.float32: _lib.ESA_F32}
@@ -332,7 +332,7 @@ def varlen_attention(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seql
                      adj_indptr=None, adj_indices=None, edge_plan=None, adj_plan=None):
     """``flash_attn_varlen_func``-compatible entry (plus the ESA masks).
 
-    q: [Tq, H, hd]; k, v: [Tk, H, hd] (hd 16, 32 or 64), all bfloat16 or all float32;
+    q: [Tq, H, hd]; k, v: [Tk, H, hd] (hd 16, 24, 32 or 64), all bfloat16 or all float32;
     cu_seqlens_*: int32 [B+1].
     edge_src / edge_dst: optional int32 [Tq] node ids per token (self-attention
     only); token i then attends to token j of its segment iff i != j and the
@@ -350,7 +350,8 @@ def varlen_attention(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seql
     if causal:
         raise NotImplementedError("causal attention is not on the ESA path (the reference uses causal=False)")
     if dropout_p:
-        raise NotImplementedError("attention dropout is not supported (dropout is 0 in every reference config)")
+        raise NotImplementedError("attention dropout is not supported on the HIP path (MIND's RNA configuration "
+                                  "trains with sab/mab dropout 0.08 and pma dropout 0.05; its other configurations use 0)")
     if softmax_scale is None:
         softmax_scale = 1.0 / math.sqrt(q.shape[-1])
     if (edge_src is None) != (edge_dst is None):

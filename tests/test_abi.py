@@ -61,9 +61,9 @@ def test_argument_errors_need_no_gpu():
     lib = _lib.load()
     n = ctypes.c_size_t(0)
     bf16, f32, none, edge = _lib.ESA_BF16, _lib.ESA_F32, _lib.ESA_MASK_NONE, _lib.ESA_MASK_EDGE
-    for hd in (8, 24, 48, 128):   # head dims outside 16, 32, 64
+    for hd in (8, 12, 20, 48, 128):   # head dims outside 16, 24, 32, 64
         assert lib.esa_varlen_attn_workspace_size(100, 100, 16, hd, bf16, none, 0, 0, ctypes.byref(n)) == -3
-    for hd in (32, 64):
+    for hd in (24, 32, 64):
         for dt in (bf16, f32):
             for mk in (none, edge, _lib.ESA_MASK_NODE):
                 assert lib.esa_varlen_attn_workspace_size(100, 100, 8, hd, dt, mk, 0, 1, ctypes.byref(n)) == 0

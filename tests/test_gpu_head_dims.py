@@ -1,5 +1,5 @@
-"""GPU parity at head dims 32 and 64 (ESA's dim / num_heads in MIND's YAMLs: 512 / 8 = 64 in qm9, unimol and lba,
-512 / 16 = 32 in coconut; esa/mha.py:50-52 computes head_dim for any size).
+"""GPU parity at head dims 24, 32 and 64 (ESA's dim / num_heads in MIND's YAMLs: 512 / 8 = 64 in qm9, unimol and
+lba, 512 / 16 = 32 in coconut, 192 / 8 = 24 in rna; esa/mha.py:50-52 computes head_dim for any size).
 
 Every path that takes a head dim: node-mode attention (the gather kernels over a CSR), the edge mask (the gather
 kernels over the edge-mask plan's lists, including tiles past the list capacity), fp32 attention (the tiled fp32
@@ -61,7 +61,7 @@ def _run_and_check(device, q, k, v, g, cu_q, cu_k, dtype, kernel_kw, oracle_kw, 
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("hd,heads", [(32, 8), (32, 3), (64, 8), (64, 5)])
+@pytest.mark.parametrize("hd,heads", [(24, 8), (24, 3), (32, 8), (32, 3), (64, 8), (64, 5)])
 def test_node_mode(device, hd, heads, dtype):
     """Node mode (CSR by query, repeated edges and self-loops, a one-node graph) at head dim 32 / 64, with head
     counts that fill and that do not fill a wave's heads per pass (8 at 32, 4 at 64)."""
@@ -77,7 +77,7 @@ def test_node_mode(device, hd, heads, dtype):
                    {"adj": (na.indptr.numpy(), na.indices.numpy())})
 
 
-@pytest.mark.parametrize("hd", [32, 64])
+@pytest.mark.parametrize("hd", [24, 32, 64])
 def test_node_mode_planned_equals_per_call(device, hd):
     """A node plan built once gives bit-equal outputs and gradients to the per-call transpose at wide heads."""
     sizes = [70, 33, 90]
@@ -111,7 +111,7 @@ def _mixed_star_batch(seed):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("hd,heads", [(32, 8), (64, 8), (64, 3)])
+@pytest.mark.parametrize("hd,heads", [(24, 8), (32, 8), (64, 8), (64, 3)])
 @pytest.mark.parametrize("shared_cu", [True, False])
 def test_edge_mask(device, hd, heads, dtype, shared_cu):
     """The edge mask at head dim 32 / 64: listed tiles and tiles past the list capacity in one batch, one
@@ -126,7 +126,7 @@ def test_edge_mask(device, hd, heads, dtype, shared_cu):
                    {"edge_src": src, "edge_dst": dst}, shared_cu=shared_cu)
 
 
-@pytest.mark.parametrize("hd", [32, 64])
+@pytest.mark.parametrize("hd", [24, 32, 64])
 def test_edge_plan_reuse_wide(device, hd):
     """A plan built once (esa_edge_plan_build) serves wide-head calls as it serves head dim 16: bit-equal to the
     per-call mask."""
@@ -175,7 +175,7 @@ def test_edge_mask_config2_wide(device, hd):
         assert_bf16_close(vd.grad[s:e].cpu(), rdv, grad_scale(rdv), f"dv segment {b}")
 
 
-@pytest.mark.parametrize("hd,heads", [(32, 4), (64, 8), (64, 3)])
+@pytest.mark.parametrize("hd,heads", [(24, 8), (32, 4), (64, 8), (64, 3)])
 @pytest.mark.parametrize("cross", [False, True])
 def test_dense_f32(device, hd, heads, cross):
     """fp32 dense attention at wide heads, self-attention and cross-attention (distinct query and key
@@ -187,7 +187,7 @@ def test_dense_f32(device, hd, heads, cross):
     _run_and_check(device, q, k, v, g, cu_q, cu_k, torch.float32, {}, {})
 
 
-@pytest.mark.parametrize("hd,heads", [(32, 8), (32, 3), (64, 8), (64, 5)])
+@pytest.mark.parametrize("hd,heads", [(24, 8), (24, 5), (32, 8), (32, 3), (64, 8), (64, 5)])
 def test_dense_bf16(device, hd, heads):
     """Dense bf16 attention at wide heads (the MFMA kernels): segments of 1, tile-edge (32, 64, 65) and ragged
     lengths, a 300-token one, and an empty segment."""
@@ -199,7 +199,7 @@ def test_dense_bf16(device, hd, heads):
     _run_and_check(device, q, k, v, g, cu, cu, torch.bfloat16, {}, {})
 
 
-@pytest.mark.parametrize("hd", [32, 64])
+@pytest.mark.parametrize("hd", [24, 32, 64])
 def test_dense_bf16_cross(device, hd):
     """Cross-attention: distinct query and key segments, one set without keys (its rows 0, LSE -inf) and one
     without queries."""
@@ -208,14 +208,13 @@ def test_dense_bf16_cross(device, hd):
     _run_and_check(device, q, k, v, g, cu_q, cu_k, torch.bfloat16, {}, {})
 
 
-@pytest.mark.parametrize("hd", [32, 64])
-def test_dense_bf16_config1_wide(device, hd):
-    """Configuration 1's batch (32 protein-like graphs, 43,670 edge tokens) at head dim `hd`, dim 256: every
-    output finite; the first, largest and last graphs against the oracle."""
+@pytest.mark.parametrize("hd,heads", [(24, 8), (32, 8), (64, 4)])
+def test_dense_bf16_config1_wide(device, hd, heads):
+    """Configuration 1's batch (32 protein-like graphs, 43,670 edge tokens) at head dim `hd` (dims 192, 256 and
+    256): every output finite; the first, largest and last graphs against the oracle."""
     gb = generators.protein_like(seed=0)
     cu = gb.cu_seqlens
     t = int(cu[-1])
-    heads = 256 // hd
     q, k, v, g = _inputs(t, t, heads, hd, 1234 + hd, torch.bfloat16)
     scale = 1.0 / math.sqrt(hd)
     qd, kd, vd = (x.to(device).requires_grad_(True) for x in (q, k, v))
@@ -237,7 +236,7 @@ def test_dense_bf16_config1_wide(device, hd):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("hd", [32, 64])
+@pytest.mark.parametrize("hd", [24, 32, 64])
 def test_pma_wide(device, hd, dtype):
     """PMA seed pooling (esa_pma_fwd / _bwd) at wide heads: 4 seeds shared by every set, the seed gradient
     summed over sets, against the oracle on the seeds repeated per set."""
@@ -264,7 +263,7 @@ def test_pma_wide(device, hd, dtype):
     _close(vd.grad.cpu(), rdv, dtype, "dv", grad=True)
 
 
-@pytest.mark.parametrize("hd", [32, 64])
+@pytest.mark.parametrize("hd", [24, 32, 64])
 def test_dense_bf16_deterministic(device, hd):
     gb = generators.protein_like(seed=4, num_graphs=3, n_min=60, n_max=120)
     cu = torch.as_tensor(gb.cu_seqlens).to(device)

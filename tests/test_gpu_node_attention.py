@@ -296,17 +296,18 @@ def test_node_mask_argument_errors(device):
         A.attn_fwd(q, q, q, cu, cu, 4, 4, 0.25, edge_src=ix, edge_dst=ix, adj_indptr=ip, adj_indices=ix)
 
 
-@pytest.mark.parametrize("dm,h", [(256, 16), (512, 32), (512, 16), (512, 8)])
+@pytest.mark.parametrize("dm,h", [(256, 16), (512, 32), (512, 16), (512, 8), (192, 8)])
 def test_esa_node_mode_bf16_train_step(device, dm, h):
     """ESA in node mode trained bf16-mixed (fp32 parameters under torch.autocast(bfloat16),
     core/train_pretrain.py:753) on the 32 protein-like graphs of configuration 1 as node graphs (9,603 nodes,
     radius edges), layers M-S-M-S-P, MLP 2 x (2 D), through the packed entry: the masked layers run on the
     batch's node plan (forward and backward).  D = 256 with 16 heads (head dim 16); D = 512 with 8 heads (head
     dim 64, the qm9 / unimol YAMLs' dim and heads, core/pretraining_config_qm9.yaml:27-28) and with 16 heads
-    (head dim 32, pretraining_config_coconut.yaml:21-22), and D = 512 with 32 heads of 16 as the control of the
-    head-dim-16 kernels at that width.  The loss is restricted to the smallest and the largest graph, so the
+    (head dim 32, pretraining_config_coconut.yaml:21-22), D = 192 with 8 heads (head dim 24, the rna YAML,
+    pretraining_config_rna.yaml:51-54), and D = 512 with 32 heads of 16 as the control of the head-dim-16 kernels
+    at that width.  The loss is restricted to the smallest and the largest graph, so the
     fp64 oracle over those two graphs alone gives the embeddings, dX and the parameter gradients.  Bar: bf16,
-    scaled by max(1, max |reference|).  At D = 512 the parameter gradients are checked by their relative L2 error
+    scaled by max(1, max |reference|).  At D = 512 and 192 the parameter gradients are checked by their relative L2 error
     (<= 3e-2) and the max-abs bar: a weight gradient sums bf16 products over D-wide rows through five
     bf16-mixed layers, and there the head-dim-16 control reaches the same errors as head dims 32 and 64
     (relative norm 0.7-2.5e-2, mean-abs 0.5-4.3e-3 of max |ref|, by parameter) while each attention call's

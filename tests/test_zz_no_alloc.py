@@ -69,13 +69,13 @@ def test_noalloc_edge_mask_at_the_documented_limit(device, dtype, heads):
         _compare(device, q, k, v, cu, int(gb.max_seqlen), kw)
 
 
-@pytest.mark.parametrize("hd", [32, 64])
+@pytest.mark.parametrize("hd", [24, 32, 64])
 @pytest.mark.parametrize("mask", ["none", "edge", "node"])
 def test_noalloc_wide_heads(device, hd, mask):
-    """Head dims 32 / 64 (the dense MFMA kernels for wide heads, the gather kernels over the edge-mask plan and
+    """Head dims 24 / 32 / 64 (the dense MFMA kernels for wide heads, the gather kernels over the edge-mask plan and
     over a node CSR): the no-allocation forward equals the allocating one, two calls in a row, the second
     smaller."""
-    heads = 256 // hd
+    heads = 192 // hd if hd == 24 else 256 // hd
     cases = ((generators.protein_like(seed=1, num_graphs=6), 31), (generators.protein_like(seed=2, num_graphs=2), 32))
     for gb, seed in cases:
         t = int(gb.cu_seqlens[-1])
