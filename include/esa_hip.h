@@ -38,6 +38,7 @@ extern "C" {
 #define ESA_ERR_ALIGN (-6)      /* pointer not 16-byte aligned */
 #define ESA_ERR_MASK (-7)       /* unknown mask kind, or the edge mask without total_q == total_k */
 #define ESA_ERR_SCRATCH (-8)    /* the call needs more scratch than esa_noalloc_scratch_bytes() */
+#define ESA_ERR_DROPOUT (-9)    /* dropout_p outside [0, 1) */
 
 #define ESA_F32 0
 #define ESA_BF16 1
@@ -56,7 +57,7 @@ ESA_API const char* esa_version(void);
 /* Varlen attention over packed segments.                                    */
 /*                                                                           */
 /* Replaces flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k,      */
-/* max_seqlen_q, max_seqlen_k, dropout_p=0, softmax_scale, causal=False)     */
+/* max_seqlen_q, max_seqlen_k, dropout_p, softmax_scale, causal=False)       */
 /* called at esa/mha_flash_varlen.py:177-184, and the per-graph attention of */
 /* memory_efficient_attention / SDPA at esa/mha.py:76 and :80-83.            */
 /*                                                                           */
@@ -94,6 +95,17 @@ ESA_API const char* esa_version(void);
 /* CSR the backward reads, so the backward does not rebuild it per call.     */
 /*                                                                           */
 /* A query with no admissible key gets output 0 and lse = -inf.              */
+/*                                                                           */
+/* dropout_p in [0, 1): attention dropout on the softmax probabilities, as   */
+/* the reference's p / dropout_p in training (esa/mha.py:76,82): out =       */
+/* (P o Z / (1 - dropout_p)) V with the keep mask Z a counter-based hash of  */
+/* (dropout_seed, head, query token, key token) — query q keeps key k in    */
+/* head h iff fmix32(row(q, h) ^ col(k)) >= round(dropout_p 2^32), row(q, h) */
+/* = fmix32(s0 ^ fmix32(q heads + h)), col(k) = fmix32(s1 ^ fmix32(k)), s0 / */
+/* s1 the seed's low / high words (s1 xor 0x9E3779B9), fmix32 MurmurHash3's */
+/* 32-bit finalizer, q and k the global token indices.  softmax_lse is that  */
+/* of the undropped scores.  The backward takes the same dropout_p and seed. */
+/* 0 disables dropout (the seed is then unused).                             */
 /*                                                                           */
 /* softmax_lse is [heads, total_q] fp32 (natural log), as flash-attn's.      */
 /* ------------------------------------------------------------------------ */
@@ -149,6 +161,7 @@ ESA_API int esa_varlen_attn_fwd(const void* q, const void* k, const void* v,
                         int batch, int total_q, int total_k,
                         int max_seqlen_q, int max_seqlen_k,
                         int heads, int head_dim, int dtype, float softmax_scale,
+                        float dropout_p, unsigned long long dropout_seed,
                         int mask_kind, const int* mask_a, const int* mask_b,
                         int n_mask_edges,
                         void* out, float* softmax_lse,
@@ -174,6 +187,7 @@ ESA_API int esa_varlen_attn_fwd_noalloc(const void* q, const void* k, const void
                         int batch, int total_q, int total_k,
                         int max_seqlen_q, int max_seqlen_k,
                         int heads, int head_dim, int dtype, float softmax_scale,
+                        float dropout_p, unsigned long long dropout_seed,
                         int mask_kind, const int* mask_a, const int* mask_b,
                         int n_mask_edges,
                         void* out, float* softmax_lse, void* stream);
@@ -186,6 +200,7 @@ ESA_API int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k,
                         int batch, int total_q, int total_k,
                         int max_seqlen_q, int max_seqlen_k,
                         int heads, int head_dim, int dtype, float softmax_scale,
+                        float dropout_p, unsigned long long dropout_seed,
                         int mask_kind, const int* mask_a, const int* mask_b,
                         int n_mask_edges,
                         void* dq, void* dk, void* dv,
@@ -199,19 +214,23 @@ ESA_API int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k,
 /* [batch + 1].  out is [batch * k_seeds, H, head_dim] set-major,            */
 /* softmax_lse [H][batch * k_seeds].  The backward's dq [k_seeds, H,         */
 /* head_dim] sums the sets' seed gradients in set order (deterministic).     */
-/* Workspace size from esa_pma_workspace_size.                               */
+/* Workspace size from esa_pma_workspace_size.  dropout_p / dropout_seed as  */
+/* esa_varlen_attn_fwd's, over the expanded queries (query b * k_seeds + s   */
+/* is seed s of set b).                                                      */
 /* ------------------------------------------------------------------------ */
 ESA_API int esa_pma_workspace_size(int batch, int k_seeds, int total_k, int heads,
                            int head_dim, int dtype, int backward, size_t* bytes);
 ESA_API int esa_pma_fwd(const void* q, const void* k, const void* v, const int* cu_seqlens_k,
                 int batch, int k_seeds, int total_k, int max_seqlen_k, int heads,
-                int head_dim, int dtype, float softmax_scale, void* out,
+                int head_dim, int dtype, float softmax_scale,
+                float dropout_p, unsigned long long dropout_seed, void* out,
                 float* softmax_lse, void* workspace, size_t workspace_bytes,
                 void* stream);
 ESA_API int esa_pma_bwd(const void* dout, const void* q, const void* k, const void* v,
                 const void* out, const float* softmax_lse, const int* cu_seqlens_k,
                 int batch, int k_seeds, int total_k, int max_seqlen_k, int heads,
-                int head_dim, int dtype, float softmax_scale, void* dq, void* dk,
+                int head_dim, int dtype, float softmax_scale,
+                float dropout_p, unsigned long long dropout_seed, void* dq, void* dk,
                 void* dv, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------ */

@@ -35,25 +35,30 @@ ERRORS = {
     -6: "ESA_ERR_ALIGN (pointer not 16-byte aligned)",
     -7: "ESA_ERR_MASK (unknown mask kind, or the edge mask without total_q == total_k)",
     -8: "ESA_ERR_SCRATCH (the call needs more scratch than the no-allocation entry point's static buffer)",
+    -9: "ESA_ERR_DROPOUT (dropout_p outside [0, 1))",
 }
 
 _c_int, _c_i64, _c_f, _c_sz, _vp = ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_size_t, ctypes.c_void_p
+_c_u64 = ctypes.c_ulonglong
 
 _PROTOS = {
     "esa_version": (ctypes.c_char_p, []),
     "esa_varlen_attn_workspace_size": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
                                                 ctypes.POINTER(_c_sz)]),
-    # q k v cu_q cu_k | batch tq tk maxq maxk heads hd dtype | scale | mask_kind a b n | out lse ws bytes stream
+    # q k v cu_q cu_k | batch tq tk maxq maxk heads hd dtype | scale dropout_p seed | mask_kind a b n |
+    # out lse ws bytes stream
     "esa_varlen_attn_fwd": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
-                                     _c_int, _c_f, _c_int, _vp, _vp, _c_int, _vp, _vp, _vp, _c_sz, _vp]),
-    # dout q k v out lse cu_q cu_k | batch tq tk maxq maxk heads hd dtype | scale | mask_kind a b n | dq dk dv ws ...
+                                     _c_int, _c_f, _c_f, _c_u64, _c_int, _vp, _vp, _c_int, _vp, _vp, _vp, _c_sz, _vp]),
+    # dout q k v out lse cu_q cu_k | batch tq tk maxq maxk heads hd dtype | scale dropout_p seed |
+    # mask_kind a b n | dq dk dv ws bytes stream
     "esa_varlen_attn_bwd": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int,
-                                     _c_int, _c_int, _c_int, _c_f, _c_int, _vp, _vp, _c_int, _vp, _vp, _vp, _vp, _c_sz,
-                                     _vp]),
+                                     _c_int, _c_int, _c_int, _c_f, _c_f, _c_u64, _c_int, _vp, _vp, _c_int, _vp, _vp,
+                                     _vp, _vp, _c_sz, _vp]),
     "esa_noalloc_scratch_bytes": (_c_sz, []),
     # as esa_varlen_attn_fwd without workspace / workspace_bytes
     "esa_varlen_attn_fwd_noalloc": (_c_int, [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
-                                             _c_int, _c_int, _c_f, _c_int, _vp, _vp, _c_int, _vp, _vp, _vp]),
+                                             _c_int, _c_int, _c_f, _c_f, _c_u64, _c_int, _vp, _vp, _c_int, _vp, _vp,
+                                             _vp]),
     "esa_edge_mask_dense": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _vp]),
     # plan tq tk direction indptr out stream
     "esa_edge_plan_decode": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _vp, _vp]),
@@ -61,12 +66,13 @@ _PROTOS = {
     # batch k_seeds total_k heads head_dim dtype backward bytes
     "esa_pma_workspace_size": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
                                         ctypes.POINTER(_c_sz)]),
-    # q k v cu_k | batch k_seeds tk maxk heads hd dtype | scale | out lse ws bytes stream
+    # q k v cu_k | batch k_seeds tk maxk heads hd dtype | scale dropout_p seed | out lse ws bytes stream
     "esa_pma_fwd": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_f,
-                             _vp, _vp, _vp, _c_sz, _vp]),
-    # dout q k v out lse cu_k | batch k_seeds tk maxk heads hd dtype | scale | dq dk dv ws bytes stream
+                             _c_f, _c_u64, _vp, _vp, _vp, _c_sz, _vp]),
+    # dout q k v out lse cu_k | batch k_seeds tk maxk heads hd dtype | scale dropout_p seed | dq dk dv ws bytes
+    # stream
     "esa_pma_bwd": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
-                             _c_int, _c_f, _vp, _vp, _vp, _vp, _c_sz, _vp]),
+                             _c_int, _c_f, _c_f, _c_u64, _vp, _vp, _vp, _vp, _c_sz, _vp]),
     "esa_edge_gather": (_c_int, [_vp, _vp, _vp, _c_i64, _c_int, _c_int, _c_int, _vp, _vp]),
     "esa_csr_workspace_size": (_c_int, [_c_i64, _c_int, ctypes.POINTER(_c_sz)]),
     "esa_csr_build": (_c_int, [_vp, _c_i64, _c_int, _vp, _vp, _vp, _c_sz, _vp]),

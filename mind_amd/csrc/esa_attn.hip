@@ -1339,9 +1339,13 @@ __global__ __launch_bounds__(256) void list_dkdv_kernel(const AttnArgs a0) {
 // exponent is <= 0 (a score minus the running maximum or the row's LSE2) and
 // every log argument >= 1 (the row sum includes the maximum's 1), so the
 // flushed denormal results of the hardware ops are below 2^-126 of the
-// row's weights.
+// row's weights.  With attention dropout (DROP, unmasked calls) the staged
+// partner tile carries the partners' keys of the keep mask (esa_common.h):
+// a dropped partner's probability leaves the products over partners and its
+// dP leaves dS; outputs carry 1 / (1 - p).
 
 struct AttnF32Args {
+  DropoutCfg drop;
   const float* q; const float* k; const float* v; const float* out; const float* dout;
   const float2* rows;       // backward: per (head, query) (LSE2 or +inf for rows without keys, D) [H][tq_pad]
   int total_q, total_k, heads, tq_pad;
@@ -1424,10 +1428,11 @@ DEVI F32Outer f32_outer(const int4& g, int tid) {
   return o;
 }
 
-template <bool MASKED, int HD>
+template <bool MASKED, int HD, bool DROP>
 __global__ __launch_bounds__(kF32Threads) void attn_fwd_f32_kernel(const AttnF32Args a) {
   __shared__ float4 sK[kTile][HD / 4], sV[kTile][HD / 4];
   __shared__ int2 sN[kTile];
+  __shared__ uint32_t sKey[DROP ? kTile : 1];   // column keys of the staged keys
   const int tid = threadIdx.x, H = a.heads;
   const int item = blockIdx.x / H, head = blockIdx.x - item * H;
   if (item >= *a.count) return;
@@ -1439,12 +1444,14 @@ __global__ __launch_bounds__(kF32Threads) void attn_fwd_f32_kernel(const AttnF32
 #pragma unroll
   for (int i = 0; i < HD; ++i) acc[i] = 0.f;
   const int2 own = MASKED ? a.nodes[oc] : make_int2(0, 0);
+  const uint32_t rk = DROP ? drop_row(a.drop, oc, head) : 0u;
   float m = -INFINITY, l = 0.f;
   for (int k0 = ot.plo; k0 < phi; k0 += kTile) {
     __syncthreads();
     stage_rows_f32<HD>(sK, a.k, phi, H, head, k0, tid);
     stage_rows_f32<HD>(sV, a.v, phi, H, head, k0, tid);
     if (MASKED && tid < kTile) sN[tid] = k0 + tid < phi ? a.nodes[k0 + tid] : make_int2(-1, -1);
+    if (DROP && tid < kTile) sKey[tid] = drop_col(a.drop, k0 + tid);
     __syncthreads();
     if (!valid) continue;
     float s[kTile];
@@ -1467,19 +1474,20 @@ __global__ __launch_bounds__(kF32Threads) void attn_fwd_f32_kernel(const AttnF32
     for (int j = 0; j < kTile; ++j) {
       const float p = fast_exp2(s[j] - m);
       l += p;
-      axpyn<HD>(p, sV[j], acc);
+      axpyn<HD>(DROP && !drop_keep(a.drop, rk, sKey[j]) ? 0.f : p, sV[j], acc);
     }
   }
   if (!valid) return;
-  storen<HD>(a.o + ((size_t)oi * H + head) * HD, acc, l > 0.f ? 1.f / l : 0.f);
+  storen<HD>(a.o + ((size_t)oi * H + head) * HD, acc, l > 0.f ? (DROP ? a.drop.inv_keep : 1.f) / l : 0.f);
   a.lse_out[(size_t)head * a.total_q + oi] = l > 0.f ? (m + fast_log2(l)) * kLn2 : -INFINITY;
 }
 
 // dQ = scale * sum_j P_ij (dP_ij - D_i) k_j, P recomputed from the saved LSE.
-template <bool MASKED, int HD>
+template <bool MASKED, int HD, bool DROP>
 __global__ __launch_bounds__(kF32Threads) void attn_dq_f32_kernel(const AttnF32Args a) {
   __shared__ float4 sK[kTile][HD / 4], sV[kTile][HD / 4];
   __shared__ int2 sN[kTile];
+  __shared__ uint32_t sKey[DROP ? kTile : 1];   // column keys of the staged keys
   const int tid = threadIdx.x, H = a.heads;
   const int item = blockIdx.x / H, head = blockIdx.x - item * H;
   if (item >= *a.count) return;
@@ -1493,11 +1501,13 @@ __global__ __launch_bounds__(kF32Threads) void attn_dq_f32_kernel(const AttnF32A
   for (int i = 0; i < HD; ++i) acc[i] = 0.f;
   const float2 rs = a.rows[(size_t)head * a.tq_pad + oc];   // (LSE2, D)
   const int2 own = MASKED ? a.nodes[oc] : make_int2(0, 0);
+  const uint32_t rk = DROP ? drop_row(a.drop, oc, head) : 0u;
   for (int k0 = ot.plo; k0 < phi; k0 += kTile) {
     __syncthreads();
     stage_rows_f32<HD>(sK, a.k, phi, H, head, k0, tid);
     stage_rows_f32<HD>(sV, a.v, phi, H, head, k0, tid);
     if (MASKED && tid < kTile) sN[tid] = k0 + tid < phi ? a.nodes[k0 + tid] : make_int2(-1, -1);
+    if (DROP && tid < kTile) sKey[tid] = drop_col(a.drop, k0 + tid);
     __syncthreads();
     if (!valid) continue;
 #pragma unroll
@@ -1505,7 +1515,9 @@ __global__ __launch_bounds__(kF32Threads) void attn_dq_f32_kernel(const AttnF32A
       const int2 pn = MASKED ? sN[j] : make_int2(0, 0);
       if (!admissible_f32<MASKED>(k0 + j, phi, oi, pn, own)) continue;
       const float p = fast_exp2(a.c * dotn<HD>(q, sK[j]) - rs.x);
-      const float ds = p * (dotn<HD>(g, sV[j]) - rs.y);
+      float dp = dotn<HD>(g, sV[j]);
+      if (DROP) dp = drop_keep(a.drop, rk, sKey[j]) ? dp * a.drop.inv_keep : 0.f;
+      const float ds = p * (dp - rs.y);
       axpyn<HD>(ds, sK[j], acc);
     }
   }
@@ -1515,11 +1527,12 @@ __global__ __launch_bounds__(kF32Threads) void attn_dq_f32_kernel(const AttnF32A
 
 // dV = sum_i P_ij dO_i, dK = scale * sum_i P_ij (dP_ij - D_i) q_i, one thread
 // per key; the partner tiles are query tiles with their (LSE2, D).
-template <bool MASKED, int HD>
+template <bool MASKED, int HD, bool DROP>
 __global__ __launch_bounds__(kF32Threads) void attn_dkdv_f32_kernel(const AttnF32Args a) {
   __shared__ float4 sQ[kTile][HD / 4], sG[kTile][HD / 4];
   __shared__ float2 sR[kTile];
   __shared__ int2 sN[kTile];
+  __shared__ uint32_t sKey[DROP ? kTile : 1];   // row keys of the staged queries
   const int tid = threadIdx.x, H = a.heads;
   const int item = blockIdx.x / H, head = blockIdx.x - item * H;
   if (item >= *a.count) return;
@@ -1532,6 +1545,7 @@ __global__ __launch_bounds__(kF32Threads) void attn_dkdv_f32_kernel(const AttnF3
 #pragma unroll
   for (int i = 0; i < HD; ++i) dk[i] = dv[i] = 0.f;
   const int2 own = MASKED ? a.nodes[oc] : make_int2(0, 0);
+  const uint32_t ck = DROP ? drop_col(a.drop, oc) : 0u;
   for (int q0 = ot.plo; q0 < phi; q0 += kTile) {
     __syncthreads();
     stage_rows_f32<HD>(sQ, a.q, phi, H, head, q0, tid);
@@ -1540,6 +1554,7 @@ __global__ __launch_bounds__(kF32Threads) void attn_dkdv_f32_kernel(const AttnF3
       const bool in = q0 + tid < phi;
       sR[tid] = in ? a.rows[(size_t)head * a.tq_pad + q0 + tid] : make_float2(INFINITY, 0.f);
       if (MASKED) sN[tid] = in ? a.nodes[q0 + tid] : make_int2(-1, -1);
+      if (DROP) sKey[tid] = drop_row(a.drop, q0 + tid, head);
     }
     __syncthreads();
     if (!valid) continue;
@@ -1549,13 +1564,16 @@ __global__ __launch_bounds__(kF32Threads) void attn_dkdv_f32_kernel(const AttnF3
       if (!admissible_f32<MASKED>(q0 + i, phi, oi, pn, own)) continue;
       const float2 rs = sR[i];
       const float p = fast_exp2(a.c * dotn<HD>(kx, sQ[i]) - rs.x);
-      axpyn<HD>(p, sG[i], dv);
-      const float ds = p * (dotn<HD>(vx, sG[i]) - rs.y);
+      const bool keep = !DROP || drop_keep(a.drop, sKey[i], ck);
+      axpyn<HD>(keep ? p : 0.f, sG[i], dv);
+      float dp = dotn<HD>(vx, sG[i]);
+      if (DROP) dp = keep ? dp * a.drop.inv_keep : 0.f;
+      const float ds = p * (dp - rs.y);
       axpyn<HD>(ds, sQ[i], dk);
     }
   }
   if (!valid) return;
-  storen<HD>(a.dv + ((size_t)oi * H + head) * HD, dv, 1.f);
+  storen<HD>(a.dv + ((size_t)oi * H + head) * HD, dv, DROP ? a.drop.inv_keep : 1.f);
   storen<HD>(a.dk + ((size_t)oi * H + head) * HD, dk, a.scale);
 }
 
@@ -1797,18 +1815,18 @@ struct WsLayout {
   size_t aux = 0, plan_q = 0, plan_k = 0, plan = 0, total = 0;
 };
 
-// The edge mask at head dims other than 16 runs the gather kernels over the
-// plan's lists (both dtypes): the plan with its lists, and for the backward
+// The edge mask at head dims other than 16, and with attention dropout at
+// any head dim, runs the gather kernels over the plan's lists (both dtypes): the plan with its lists, and for the backward
 // the per-(head, query) D of the gather kernels, which fits in the aux region.
-bool edge_gathered(int mask_kind, int head_dim) {
-  return (mask_kind == ESA_MASK_EDGE || mask_kind == ESA_MASK_EDGE_PLAN) && head_dim != kHd;
+bool edge_gathered(int mask_kind, int head_dim, bool drop) {
+  return (mask_kind == ESA_MASK_EDGE || mask_kind == ESA_MASK_EDGE_PLAN) && (head_dim != kHd || drop);
 }
 
 WsLayout ws_layout(int total_q, int total_k, int heads, int dtype, int mask_kind, bool backward, bool key_lists,
-                   int head_dim) {
+                   int head_dim, bool drop) {
   WsLayout L;
   const int tqp = round32(total_q);
-  const bool gathered = edge_gathered(mask_kind, head_dim);
+  const bool gathered = edge_gathered(mask_kind, head_dim, drop);
   size_t off = 0;
   if (backward) { L.aux = off; off += align256((size_t)heads * tqp * 8); }   // bf16: uint2 (hi, lo); fp32: float2
   if (dtype == ESA_F32 && !gathered) {
@@ -2057,13 +2075,18 @@ GraphAttnArgs edge_gather_args(const void* plan, const void* q, const void* k, c
   return g;
 }
 
-// KERNEL<false, HD> (the fp32 kernels without a mask) for head dim 16, 24, 32 or 64.
-#define ESA_F32_LAUNCH(KERNEL, hd, grid, st, a)                                             \
-  do {                                                                                      \
-    if (hd == 16) hipLaunchKernelGGL((KERNEL<false, 16>), grid, dim3(kF32Threads), 0, st, a);       \
-    else if (hd == 24) hipLaunchKernelGGL((KERNEL<false, 24>), grid, dim3(kF32Threads), 0, st, a);  \
-    else if (hd == 32) hipLaunchKernelGGL((KERNEL<false, 32>), grid, dim3(kF32Threads), 0, st, a);  \
-    else hipLaunchKernelGGL((KERNEL<false, 64>), grid, dim3(kF32Threads), 0, st, a);               \
+// KERNEL<false, HD, DROP> (the fp32 kernels without a mask) for head dim 16, 24, 32 or 64.
+#define ESA_F32_LAUNCH_HD(KERNEL, D, hd, grid, st, a)                                                \
+  do {                                                                                               \
+    if (hd == 16) hipLaunchKernelGGL((KERNEL<false, 16, D>), grid, dim3(kF32Threads), 0, st, a);      \
+    else if (hd == 24) hipLaunchKernelGGL((KERNEL<false, 24, D>), grid, dim3(kF32Threads), 0, st, a); \
+    else if (hd == 32) hipLaunchKernelGGL((KERNEL<false, 32, D>), grid, dim3(kF32Threads), 0, st, a); \
+    else hipLaunchKernelGGL((KERNEL<false, 64, D>), grid, dim3(kF32Threads), 0, st, a);              \
+  } while (0)
+#define ESA_F32_LAUNCH(KERNEL, hd, drop, grid, st, a)                                                \
+  do {                                                                                               \
+    if (drop) ESA_F32_LAUNCH_HD(KERNEL, true, hd, grid, st, a);                                     \
+    else ESA_F32_LAUNCH_HD(KERNEL, false, hd, grid, st, a);                                         \
   } while (0)
 
 // Scratch of esa_varlen_attn_fwd_noalloc: a file-scope device array, one
@@ -2113,8 +2136,12 @@ int esa_varlen_attn_workspace_size(int total_q, int total_k, int heads, int head
   }
   if (mask_kind == ESA_MASK_NONE && dtype == ESA_BF16)
     return dense_attn_workspace_size(total_q, total_k, heads, head_dim, backward != 0, bytes);
-  // a backward call that builds its plan may need the key tiles' lists (distinct segment arrays)
-  *bytes = ws_layout(total_q, total_k, heads, dtype, mask_kind, backward != 0, backward != 0, head_dim).total;
+  // a backward call that builds its plan may need the key tiles' lists (distinct segment arrays); the
+  // size covers the calls with and without dropout (which may take different kernels)
+  *bytes = std::max(ws_layout(total_q, total_k, heads, dtype, mask_kind, backward != 0, backward != 0, head_dim,
+                              false).total,
+                    ws_layout(total_q, total_k, heads, dtype, mask_kind, backward != 0, backward != 0, head_dim,
+                              true).total);
   return ESA_OK;
 }
 
@@ -2156,12 +2183,15 @@ int esa_node_plan_build(const int* indptr, const int* indices, const int* cu_seq
 int esa_varlen_attn_fwd(const void* q, const void* k, const void* v, const int* cu_seqlens_q,
                         const int* cu_seqlens_k, int batch, int total_q, int total_k,
                         int max_seqlen_q, int max_seqlen_k, int heads, int head_dim, int dtype,
-                        float softmax_scale, int mask_kind, const int* mask_a, const int* mask_b,
-                        int n_mask_edges, void* out, float* softmax_lse, void* workspace,
-                        size_t workspace_bytes, void* stream) {
+                        float softmax_scale, float dropout_p, unsigned long long dropout_seed, int mask_kind,
+                        const int* mask_a, const int* mask_b, int n_mask_edges, void* out, float* softmax_lse,
+                        void* workspace, size_t workspace_bytes, void* stream) {
   (void)max_seqlen_q; (void)max_seqlen_k;
   int rc = check_common(batch, total_q, total_k, heads, head_dim, dtype, mask_kind);
   if (rc) return rc;
+  if (!(dropout_p >= 0.f && dropout_p < 1.f)) return ESA_ERR_DROPOUT;
+  const bool drop = dropout_p > 0.f;
+  const DropoutCfg dcfg = make_dropout(dropout_p, dropout_seed, heads);
   if (mask_kind == ESA_MASK_NODE || mask_kind == ESA_MASK_NODE_PLAN) {
     if (n_mask_edges < 0) return ESA_ERR_SHAPE;
     if (!mask_a || ((n_mask_edges > 0 || mask_kind == ESA_MASK_NODE_PLAN) && !mask_b)) return ESA_ERR_NULL;
@@ -2175,6 +2205,7 @@ int esa_varlen_attn_fwd(const void* q, const void* k, const void* v, const int* 
     g.total_q = total_q; g.total_k = total_k; g.heads = heads; g.head_dim = head_dim;
     g.indptr = mask_a; g.indices = mask_b; g.nnz = n_mask_edges;
     g.c = softmax_scale * kLog2e; g.scale = softmax_scale;
+    g.drop = dcfg; g.dropout = drop;
     g.out = out; g.lse = softmax_lse;
     (void)workspace; (void)workspace_bytes;
     return graph_attn_fwd(g, dtype, mask_kind == ESA_MASK_NODE_PLAN ? mask_b : nullptr,
@@ -2194,11 +2225,12 @@ int esa_varlen_attn_fwd(const void* q, const void* k, const void* v, const int* 
     DenseAttnCall c{};
     c.q = q; c.k = k; c.v = v; c.cu_q = cu_seqlens_q; c.cu_k = cu_seqlens_k; c.nseg = batch;
     c.total_q = total_q; c.total_k = total_k; c.heads = heads; c.head_dim = head_dim; c.scale = softmax_scale;
+    c.drop = dcfg; c.dropout = drop;
     c.out = out; c.lse = softmax_lse;
     return dense_attn_fwd(c, workspace, workspace_bytes, st);
   }
-  const bool gathered = edge_gathered(mask_kind, head_dim);
-  const WsLayout L = ws_layout(total_q, total_k, heads, dtype, mask_kind, false, false, head_dim);
+  const bool gathered = edge_gathered(mask_kind, head_dim, drop);
+  const WsLayout L = ws_layout(total_q, total_k, heads, dtype, mask_kind, false, false, head_dim, drop);
   if (workspace_bytes < L.total) return ESA_ERR_WORKSPACE;
   if (L.total && !workspace) return ESA_ERR_NULL;
   char* ws = static_cast<char*>(workspace);
@@ -2207,9 +2239,10 @@ int esa_varlen_attn_fwd(const void* q, const void* k, const void* v, const int* 
                                 L, false, !f32 || gathered, st, &plan)))
     return rc;
 
-  if (gathered) {   // the edge mask at head dims 32 / 64: gather kernels over the plan's lists
+  if (gathered) {   // the edge mask at head dims 24 / 32 / 64 or with dropout: gather kernels over the plan's lists
     GraphAttnArgs g = edge_gather_args(plan, q, k, v, cu_seqlens_q, cu_seqlens_k, batch, total_q, total_k, heads,
                                        head_dim, softmax_scale);
+    g.drop = dcfg; g.dropout = drop;
     g.out = out; g.lse = softmax_lse;
     return graph_edge_attn_fwd(g, dtype, st);
   }
@@ -2225,15 +2258,16 @@ int esa_varlen_attn_fwd(const void* q, const void* k, const void* v, const int* 
     a.q = static_cast<const float*>(q); a.k = static_cast<const float*>(k); a.v = static_cast<const float*>(v);
     a.total_q = total_q; a.total_k = total_k; a.heads = heads; a.tq_pad = pa.tq_pad;
     a.c = softmax_scale * kLog2e; a.scale = softmax_scale;
+    a.drop = dcfg;
     a.nodes = masked ? plan_view(plan, total_q, total_k).nodes : nullptr;
     a.plan = pa.plan_q; a.count = pa.count_q;
     a.o = static_cast<float*>(out); a.lse_out = softmax_lse;
     const dim3 fgrid((unsigned)(groups_of(total_q) + batch) * (unsigned)heads);
-    if (masked)   // head_dim 16 (other head dims take the gather kernels)
+    if (masked)   // head_dim 16 without dropout (the rest take the gather kernels)
       ESA_TIMED(esa_profile::kAttnFwdMasked, st,
-                hipLaunchKernelGGL((attn_fwd_f32_kernel<true, 16>), fgrid, dim3(kF32Threads), 0, st, a));
+                hipLaunchKernelGGL((attn_fwd_f32_kernel<true, 16, false>), fgrid, dim3(kF32Threads), 0, st, a));
     else
-      ESA_TIMED(esa_profile::kAttnFwd, st, ESA_F32_LAUNCH(attn_fwd_f32_kernel, head_dim, fgrid, st, a));
+      ESA_TIMED(esa_profile::kAttnFwd, st, ESA_F32_LAUNCH(attn_fwd_f32_kernel, head_dim, drop, fgrid, st, a));
     ESA_LAUNCH_CHECK();
     return ESA_OK;
   }
@@ -2268,8 +2302,9 @@ size_t esa_noalloc_scratch_bytes(void) { return kNoAllocScratchBytes; }
 int esa_varlen_attn_fwd_noalloc(const void* q, const void* k, const void* v, const int* cu_seqlens_q,
                                 const int* cu_seqlens_k, int batch, int total_q, int total_k,
                                 int max_seqlen_q, int max_seqlen_k, int heads, int head_dim, int dtype,
-                                float softmax_scale, int mask_kind, const int* mask_a, const int* mask_b,
-                                int n_mask_edges, void* out, float* softmax_lse, void* stream) {
+                                float softmax_scale, float dropout_p, unsigned long long dropout_seed,
+                                int mask_kind, const int* mask_a, const int* mask_b, int n_mask_edges, void* out,
+                                float* softmax_lse, void* stream) {
   size_t need = 0;
   int rc = esa_varlen_attn_workspace_size(total_q, total_k, heads, head_dim, dtype, mask_kind, n_mask_edges, 0,
                                           &need);
@@ -2281,19 +2316,23 @@ int esa_varlen_attn_fwd_noalloc(const void* q, const void* k, const void* v, con
   // does for the allocating entry point's uninitialised workspace, so nothing
   // needs clearing between calls.
   return esa_varlen_attn_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, batch, total_q, total_k, max_seqlen_q,
-                             max_seqlen_k, heads, head_dim, dtype, softmax_scale, mask_kind, mask_a, mask_b,
-                             n_mask_edges, out, softmax_lse, ws, kNoAllocScratchBytes, stream);
+                             max_seqlen_k, heads, head_dim, dtype, softmax_scale, dropout_p, dropout_seed, mask_kind,
+                             mask_a, mask_b, n_mask_edges, out, softmax_lse, ws, kNoAllocScratchBytes, stream);
 }
 
 int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k, const void* v, const void* out,
                         const float* softmax_lse, const int* cu_seqlens_q, const int* cu_seqlens_k,
                         int batch, int total_q, int total_k, int max_seqlen_q, int max_seqlen_k,
-                        int heads, int head_dim, int dtype, float softmax_scale, int mask_kind,
-                        const int* mask_a, const int* mask_b, int n_mask_edges, void* dq, void* dk,
-                        void* dv, void* workspace, size_t workspace_bytes, void* stream) {
+                        int heads, int head_dim, int dtype, float softmax_scale, float dropout_p,
+                        unsigned long long dropout_seed, int mask_kind, const int* mask_a, const int* mask_b,
+                        int n_mask_edges, void* dq, void* dk, void* dv, void* workspace, size_t workspace_bytes,
+                        void* stream) {
   (void)max_seqlen_q; (void)max_seqlen_k;
   int rc = check_common(batch, total_q, total_k, heads, head_dim, dtype, mask_kind);
   if (rc) return rc;
+  if (!(dropout_p >= 0.f && dropout_p < 1.f)) return ESA_ERR_DROPOUT;
+  const bool drop = dropout_p > 0.f;
+  const DropoutCfg dcfg = make_dropout(dropout_p, dropout_seed, heads);
   if (mask_kind == ESA_MASK_NODE || mask_kind == ESA_MASK_NODE_PLAN) {
     const bool planned = mask_kind == ESA_MASK_NODE_PLAN;
     if (n_mask_edges < 0) return ESA_ERR_SHAPE;
@@ -2312,6 +2351,7 @@ int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k, const vo
     g.total_q = total_q; g.total_k = total_k; g.heads = heads; g.head_dim = head_dim;
     g.indptr = mask_a; g.indices = mask_b; g.nnz = n_mask_edges;
     g.c = softmax_scale * kLog2e; g.scale = softmax_scale;
+    g.drop = dcfg; g.dropout = drop;
     g.out_in = out; g.dout = dout; g.lse_in = softmax_lse;
     g.dq = dq; g.dk = dk; g.dv = dv;
     return graph_attn_bwd(g, dtype, planned ? mask_b : nullptr, workspace, workspace_bytes,
@@ -2344,12 +2384,13 @@ int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k, const vo
     c.q = q; c.k = k; c.v = v; c.cu_q = cu_seqlens_q; c.cu_k = cu_seqlens_k; c.nseg = batch;
     c.total_q = total_q; c.total_k = total_k; c.heads = heads; c.head_dim = head_dim; c.scale = softmax_scale;
     c.out_in = out; c.dout = dout; c.lse_in = softmax_lse; c.dq = dq; c.dk = dk; c.dv = dv;
+    c.drop = dcfg; c.dropout = drop;
     return dense_attn_bwd(c, workspace, workspace_bytes, st);
   }
   // A plan built here has the key tiles' own lists when the segment arrays are distinct.
   const bool key_lists = cu_seqlens_q != cu_seqlens_k;
-  const bool gathered = edge_gathered(mask_kind, head_dim);
-  const WsLayout L = ws_layout(total_q, total_k, heads, dtype, mask_kind, true, key_lists, head_dim);
+  const bool gathered = edge_gathered(mask_kind, head_dim, drop);
+  const WsLayout L = ws_layout(total_q, total_k, heads, dtype, mask_kind, true, key_lists, head_dim, drop);
   if (workspace_bytes < L.total) return ESA_ERR_WORKSPACE;
   char* ws = static_cast<char*>(workspace);
   const void* plan = nullptr;
@@ -2357,9 +2398,10 @@ int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k, const vo
                                 L, key_lists, !f32 || gathered, st, &plan)))
     return rc;
 
-  if (gathered) {   // the edge mask at head dims 32 / 64: gather kernels over the plan's lists
+  if (gathered) {   // the edge mask at head dims 24 / 32 / 64 or with dropout: gather kernels over the plan's lists
     GraphAttnArgs g = edge_gather_args(plan, q, k, v, cu_seqlens_q, cu_seqlens_k, batch, total_q, total_k, heads,
                                        head_dim, softmax_scale);
+    g.drop = dcfg; g.dropout = drop;
     g.out_in = out; g.dout = dout; g.lse_in = softmax_lse;
     g.dq = dq; g.dk = dk; g.dv = dv;
     return graph_edge_attn_bwd(g, dtype, ws + L.aux, workspace_bytes - L.aux, st);
@@ -2384,23 +2426,24 @@ int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k, const vo
     a.rows = pa.rows_f;
     a.total_q = total_q; a.total_k = total_k; a.heads = heads; a.tq_pad = pa.tq_pad;
     a.c = softmax_scale * kLog2e; a.scale = softmax_scale;
+    a.drop = dcfg;
     a.nodes = masked ? plan_view(plan, total_q, total_k).nodes : nullptr;
     a.dq = static_cast<float*>(dq); a.dk = static_cast<float*>(dk); a.dv = static_cast<float*>(dv);
     a.plan = pa.plan_k; a.count = pa.count_k;
     const dim3 fkgrid((unsigned)(groups_of(total_k) + batch) * (unsigned)heads);
     const dim3 fqgrid((unsigned)(groups_of(total_q) + batch) * (unsigned)heads);
-    if (masked)   // head_dim 16 (other head dims take the gather kernels)
+    if (masked)   // head_dim 16 without dropout (the rest take the gather kernels)
       ESA_TIMED(esa_profile::kAttnBwdDkdvMasked, st,
-                hipLaunchKernelGGL((attn_dkdv_f32_kernel<true, 16>), fkgrid, dim3(kF32Threads), 0, st, a));
+                hipLaunchKernelGGL((attn_dkdv_f32_kernel<true, 16, false>), fkgrid, dim3(kF32Threads), 0, st, a));
     else
-      ESA_TIMED(esa_profile::kAttnBwdDkdv, st, ESA_F32_LAUNCH(attn_dkdv_f32_kernel, head_dim, fkgrid, st, a));
+      ESA_TIMED(esa_profile::kAttnBwdDkdv, st, ESA_F32_LAUNCH(attn_dkdv_f32_kernel, head_dim, drop, fkgrid, st, a));
     ESA_LAUNCH_CHECK();
     a.plan = pa.plan_q; a.count = pa.count_q;
     if (masked)
       ESA_TIMED(esa_profile::kAttnBwdDqMasked, st,
-                hipLaunchKernelGGL((attn_dq_f32_kernel<true, 16>), fqgrid, dim3(kF32Threads), 0, st, a));
+                hipLaunchKernelGGL((attn_dq_f32_kernel<true, 16, false>), fqgrid, dim3(kF32Threads), 0, st, a));
     else
-      ESA_TIMED(esa_profile::kAttnBwdDq, st, ESA_F32_LAUNCH(attn_dq_f32_kernel, head_dim, fqgrid, st, a));
+      ESA_TIMED(esa_profile::kAttnBwdDq, st, ESA_F32_LAUNCH(attn_dq_f32_kernel, head_dim, drop, fqgrid, st, a));
     ESA_LAUNCH_CHECK();
     return ESA_OK;
   }
@@ -2491,8 +2534,9 @@ int esa_pma_workspace_size(int batch, int k_seeds, int total_k, int heads, int h
 }
 
 int esa_pma_fwd(const void* q, const void* k, const void* v, const int* cu_seqlens_k, int batch, int k_seeds,
-                int total_k, int max_seqlen_k, int heads, int head_dim, int dtype, float softmax_scale, void* out,
-                float* softmax_lse, void* workspace, size_t workspace_bytes, void* stream) {
+                int total_k, int max_seqlen_k, int heads, int head_dim, int dtype, float softmax_scale,
+                float dropout_p, unsigned long long dropout_seed, void* out, float* softmax_lse, void* workspace,
+                size_t workspace_bytes, void* stream) {
   size_t off[4], need = 0;
   int rc = pma_layout(batch, k_seeds, total_k, heads, head_dim, dtype, false, off, &need);
   if (rc) return rc;
@@ -2504,13 +2548,15 @@ int esa_pma_fwd(const void* q, const void* k, const void* v, const int* cu_seqle
   if ((rc = pma_expand(q, batch, k_seeds, heads, head_dim, dtype, ws, off, st))) return rc;
   return esa_varlen_attn_fwd(ws + off[0], k, v, reinterpret_cast<const int*>(ws + off[1]), cu_seqlens_k, batch,
                              batch * k_seeds, total_k, k_seeds, max_seqlen_k, heads, head_dim, dtype, softmax_scale,
-                             ESA_MASK_NONE, nullptr, nullptr, 0, out, softmax_lse, ws + off[3], need - off[3], stream);
+                             dropout_p, dropout_seed, ESA_MASK_NONE, nullptr, nullptr, 0, out, softmax_lse, ws + off[3],
+                             need - off[3], stream);
 }
 
 int esa_pma_bwd(const void* dout, const void* q, const void* k, const void* v, const void* out,
                 const float* softmax_lse, const int* cu_seqlens_k, int batch, int k_seeds, int total_k,
-                int max_seqlen_k, int heads, int head_dim, int dtype, float softmax_scale, void* dq, void* dk,
-                void* dv, void* workspace, size_t workspace_bytes, void* stream) {
+                int max_seqlen_k, int heads, int head_dim, int dtype, float softmax_scale, float dropout_p,
+                unsigned long long dropout_seed, void* dq, void* dk, void* dv, void* workspace,
+                size_t workspace_bytes, void* stream) {
   size_t off[4], need = 0;
   int rc = pma_layout(batch, k_seeds, total_k, heads, head_dim, dtype, true, off, &need);
   if (rc) return rc;
@@ -2523,8 +2569,8 @@ int esa_pma_bwd(const void* dout, const void* q, const void* k, const void* v, c
   if ((rc = pma_expand(q, batch, k_seeds, heads, head_dim, dtype, ws, off, st))) return rc;
   rc = esa_varlen_attn_bwd(dout, ws + off[0], k, v, out, softmax_lse, reinterpret_cast<const int*>(ws + off[1]),
                            cu_seqlens_k, batch, batch * k_seeds, total_k, k_seeds, max_seqlen_k, heads, head_dim,
-                           dtype, softmax_scale, ESA_MASK_NONE, nullptr, nullptr, 0, ws + off[2], dk, dv,
-                           ws + off[3], need - off[3], stream);
+                           dtype, softmax_scale, dropout_p, dropout_seed, ESA_MASK_NONE, nullptr, nullptr, 0,
+                           ws + off[2], dk, dv, ws + off[3], need - off[3], stream);
   if (rc) return rc;
   const int row_elems = heads * head_dim;
   const long n = (long)k_seeds * row_elems;

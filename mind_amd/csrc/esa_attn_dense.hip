@@ -661,8 +661,9 @@ unsigned group_grid(int total_outer, int nseg, int heads, int gtok) {
 }  // namespace
 
 int dense_attn_workspace_size(int total_q, int total_k, int heads, int head_dim, bool backward, size_t* bytes) {
-  if (head_dim == kHd) {
-    *bytes = dense_ws(total_q, total_k, heads, backward).total;
+  if (head_dim == kHd) {   // either kernel set (dropout runs the wide kernels)
+    *bytes = max(dense_ws(total_q, total_k, heads, backward).total,
+                 wide_attn_workspace_size(total_q, total_k, heads, head_dim, backward));
     return ESA_OK;
   }
   if (head_dim != 24 && head_dim != 32 && head_dim != 64) return ESA_ERR_HEAD_DIM;
@@ -671,7 +672,7 @@ int dense_attn_workspace_size(int total_q, int total_k, int heads, int head_dim,
 }
 
 int dense_attn_fwd(const DenseAttnCall& c, void* workspace, size_t workspace_bytes, hipStream_t st) {
-  if (c.head_dim != kHd) return wide_attn_fwd(c, workspace, workspace_bytes, st);
+  if (c.head_dim != kHd || c.dropout) return wide_attn_fwd(c, workspace, workspace_bytes, st);
   const DenseWs w = dense_ws(c.total_q, c.total_k, c.heads, false);
   if (workspace_bytes < w.total) return ESA_ERR_WORKSPACE;
   char* ws = static_cast<char*>(workspace);
@@ -702,7 +703,7 @@ int dense_attn_fwd(const DenseAttnCall& c, void* workspace, size_t workspace_byt
 }
 
 int dense_attn_bwd(const DenseAttnCall& c, void* workspace, size_t workspace_bytes, hipStream_t st) {
-  if (c.head_dim != kHd) return wide_attn_bwd(c, workspace, workspace_bytes, st);
+  if (c.head_dim != kHd || c.dropout) return wide_attn_bwd(c, workspace, workspace_bytes, st);
   const DenseWs w = dense_ws(c.total_q, c.total_k, c.heads, true);
   if (workspace_bytes < w.total) return ESA_ERR_WORKSPACE;
   char* ws = static_cast<char*>(workspace);

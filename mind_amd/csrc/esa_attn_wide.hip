@@ -1,9 +1,17 @@
 // Dense varlen attention (no mask) at head dims 24, 32 and 64, bf16 operands,
 // fp32 softmax, on gfx950: the flash_attn_varlen_func drop-in
-// (esa/mha_flash_varlen.py:177-184, causal=False, dropout 0) for the ESA
-// configurations whose dim / num_heads is 24, 32 or 64 (esa/mha.py:50-52).
-// Head dim 24 computes as 32: its rows are read as three 8-dim octets, the
-// fourth octet of every operand is zero, and output dims 24..31 are dropped.
+// (esa/mha_flash_varlen.py:177-184, causal=False) for the ESA configurations
+// whose dim / num_heads is 24, 32 or 64 (esa/mha.py:50-52), and, with
+// attention dropout (DROP), for every head dim including 16.  Products over
+// partners compute 32 output dims per block: head dims 16 and 24 read their
+// rows as two / three 8-dim octets, the other octets of every operand are
+// zero, and output dims past the head dim are not stored.
+//
+// Dropout: the keep mask of esa_common.h, from each lane's own row (forward,
+// dQ) or column (dK/dV) key and the staged partners' keys, computed once per
+// token during staging and held in LDS beside the rows; a dropped partner's
+// probability is zeroed in the products over partners (and its dP in dS),
+// the outputs carry 1 / (1 - p), the softmax statistics are undropped.
 //
 // Work items are 128-token groups cut from each segment on its own (the
 // segment plans of the head-dim-16 kernels): a block's four waves own four
@@ -40,6 +48,7 @@ constexpr int kWStage = 64;              // partner tokens per stage (two tiles)
 constexpr int kWTokPad = kWStage + 4;    // LDS octet stride in tokens
 
 struct WideArgs {
+  DropoutCfg drop;
   const bf16* q; const bf16* k; const bf16* v; const bf16* out; const bf16* dout;
   const float* lse;            // dQ pass input [H][Tq]
   float2* aux;                 // per (head, query) {-LSE2 / c, -D}, [H][tq_pad]: written by dQ, read by dK/dV
@@ -153,6 +162,27 @@ DEVI void wide_zero_pad(bf16* a0, bf16* a1, bf16* b0, bf16* b1, int tid) {
   }
 }
 
+// A stage's rows with the dropout key of partner token tid (tid < 64).
+template <int HD>
+struct WStageK {
+  WStage<HD> rows;
+  uint32_t key;
+};
+
+// Zeroes x[r] for the partners the keep mask drops: register r of lane half
+// h holds partner row_local(r, h) of the tile whose 32 partner keys start at
+// `keys` (LDS), the lane's own key is `own`.
+DEVI void drop_tile(const DropoutCfg& d, uint32_t own, const uint32_t* keys, int h, float (&x)[16]) {
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    const uint4 k0 = *reinterpret_cast<const uint4*>(keys + 16 * b + 8 * h);
+    const uint4 k1 = *reinterpret_cast<const uint4*>(keys + 16 * b + 8 * h + 4);
+    const uint32_t kk[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[8 * b + e] = drop_keep(d, own, kk[e]) ? x[8 * b + e] : 0.f;
+  }
+}
+
 // Two LDS buffers and two stages' loads in flight: stage s + 2 is requested
 // before stage s is consumed; stage s + 1 is written to LDS after it.
 template <class Load, class Store, class Compute>
@@ -179,11 +209,12 @@ DEVI void wide_walk(int n_stages, Load gload, Store lstore, Compute compute) {
 constexpr int kWGroup = kWaves * kTile;   // 128 owned tokens per block
 
 // ------------------------------------------------------------------ forward
-template <int HD>
+template <int HD, bool DROP>
 __global__ __launch_bounds__(256) void wide_fwd_kernel(const WideArgs a) {
-  constexpr int HP = (HD + 31) / 32 * 32, NC = HP / 16, NM = HP / 32, NO = HP / 8;
+  constexpr int HP = (HD + 31) / 32 * 32, NC = (HD + 15) / 16, NM = HP / 32, NO = HP / 8;
   __shared__ __align__(16) bf16 sK[2][NO * kWTokPad * 8];
   __shared__ __align__(16) bf16 sV[2][NO * kWTokPad * 8];
+  __shared__ __align__(16) uint32_t sKey[2][DROP ? kWStage : 4];   // column keys of the staged keys
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 31, h = lane >> 5;
   const int H = a.heads;
@@ -198,6 +229,7 @@ __global__ __launch_bounds__(256) void wide_fwd_kernel(const WideArgs a) {
 #pragma unroll
   for (int c = 0; c < NC; ++c) qop[c] = row_op<HD>(qrow, 2 * c + h);
   wide_zero_pad<HD>(sK[0], sK[1], sV[0], sV[1], tid);
+  const uint32_t rk = DROP ? drop_row(a.drop, valid ? t : g.x, head) : 0u;
   f32x16 acc[NM];
 #pragma unroll
   for (int m = 0; m < NM; ++m) acc[m] = f32x16{};
@@ -206,8 +238,17 @@ __global__ __launch_bounds__(256) void wide_fwd_kernel(const WideArgs a) {
   const int n_stages = (n_tiles + 1) >> 1;
   const f32x16 zero = {};
   wide_walk(
-      n_stages, [&](int st) { return wide_gload<HD>(a.k, a.v, g.z + st * kWStage, a.total_k, H, head, tid); },
-      [&](int buf, const WStage<HD>& s) { wide_lstore<HD>(sK[buf], sV[buf], s, tid); },
+      n_stages,
+      [&](int st) {
+        WStageK<HD> s;
+        s.rows = wide_gload<HD>(a.k, a.v, g.z + st * kWStage, a.total_k, H, head, tid);
+        s.key = DROP && tid < kWStage ? drop_col(a.drop, g.z + st * kWStage + tid) : 0u;
+        return s;
+      },
+      [&](int buf, const WStageK<HD>& s) {
+        wide_lstore<HD>(sK[buf], sV[buf], s.rows, tid);
+        if (DROP && tid < kWStage) sKey[buf][tid] = s.key;
+      },
       [&](int buf, int st) {
         if (!active) return;
 #pragma unroll
@@ -242,6 +283,7 @@ __global__ __launch_bounds__(256) void wide_fwd_kernel(const WideArgs a) {
             p[r] = fast_exp2(fmaf(s[r], a.c, -cm));
             l_run += p[r];
           }
+          if (DROP) drop_tile(a.drop, rk, &sKey[buf][u * kTile], h, p);
 #pragma unroll
           for (int m = 0; m < NM; ++m)
 #pragma unroll
@@ -250,7 +292,7 @@ __global__ __launch_bounds__(256) void wide_fwd_kernel(const WideArgs a) {
       });
   if (!valid) return;
   const float l = l_run + __shfl_xor(l_run, 32);
-  store_acc<HD>(a.o + ((size_t)t * H + head) * HD, acc, l > 0.f ? 1.f / l : 0.f, h);
+  store_acc<HD>(a.o + ((size_t)t * H + head) * HD, acc, l > 0.f ? (DROP ? a.drop.inv_keep : 1.f) / l : 0.f, h);
   if (h == 0) a.lse_out[(size_t)head * a.total_q + t] = l > 0.f ? (a.c * m_run + fast_log2(l)) * kLn2 : -INFINITY;
 }
 
@@ -258,11 +300,12 @@ __global__ __launch_bounds__(256) void wide_fwd_kernel(const WideArgs a) {
 // Queries on lanes: S^T = K q^T, dP^T = V dO^T, P = exp2(c S - LSE2),
 // dS = P (dP - D), dQ^T += K^T dS^T.  Also writes the dK/dV pass's row
 // statistics {-LSE2 / c, -D} of its queries.
-template <int HD>
+template <int HD, bool DROP>
 __global__ __launch_bounds__(256) void wide_dq_kernel(const WideArgs a) {
-  constexpr int HP = (HD + 31) / 32 * 32, NC = HP / 16, NM = HP / 32, NO = HP / 8;
+  constexpr int HP = (HD + 31) / 32 * 32, NC = (HD + 15) / 16, NM = HP / 32, NO = HP / 8;
   __shared__ __align__(16) bf16 sK[2][NO * kWTokPad * 8];
   __shared__ __align__(16) bf16 sV[2][NO * kWTokPad * 8];
+  __shared__ __align__(16) uint32_t sKey[2][DROP ? kWStage : 4];   // column keys of the staged keys
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 31, h = lane >> 5;
   const int H = a.heads;
@@ -289,6 +332,7 @@ __global__ __launch_bounds__(256) void wide_dq_kernel(const WideArgs a) {
   const float lse2 = lq == -INFINITY ? INFINITY : lq * kLog2e;   // rows without keys: P = 0
   if (valid && h == 0)
     a.aux[(size_t)head * a.tq_pad + t] = make_float2(lq == -INFINITY ? kDeadRow : -lse2 / a.c, -dsum);
+  const uint32_t rk = DROP ? drop_row(a.drop, valid ? t : g.x, head) : 0u;
   f32x16 acc[NM];
 #pragma unroll
   for (int m = 0; m < NM; ++m) acc[m] = f32x16{};
@@ -296,8 +340,17 @@ __global__ __launch_bounds__(256) void wide_dq_kernel(const WideArgs a) {
   const int n_stages = (n_tiles + 1) >> 1;
   const f32x16 zero = {};
   wide_walk(
-      n_stages, [&](int st) { return wide_gload<HD>(a.k, a.v, g.z + st * kWStage, a.total_k, H, head, tid); },
-      [&](int buf, const WStage<HD>& s) { wide_lstore<HD>(sK[buf], sV[buf], s, tid); },
+      n_stages,
+      [&](int st) {
+        WStageK<HD> s;
+        s.rows = wide_gload<HD>(a.k, a.v, g.z + st * kWStage, a.total_k, H, head, tid);
+        s.key = DROP && tid < kWStage ? drop_col(a.drop, g.z + st * kWStage + tid) : 0u;
+        return s;
+      },
+      [&](int buf, const WStageK<HD>& s) {
+        wide_lstore<HD>(sK[buf], sV[buf], s.rows, tid);
+        if (DROP && tid < kWStage) sKey[buf][tid] = s.key;
+      },
       [&](int buf, int st) {
         if (!active) return;
 #pragma unroll
@@ -315,8 +368,17 @@ __global__ __launch_bounds__(256) void wide_dq_kernel(const WideArgs a) {
             for (int r = 0; r < 16; ++r) s[r] = k0 + row_local(r, h) < g.w ? s[r] : -INFINITY;
           }
           float ds[16];
+          if (DROP) {
+            float dpk[16];
 #pragma unroll
-          for (int r = 0; r < 16; ++r) ds[r] = fast_exp2(fmaf(s[r], a.c, -lse2)) * (dp[r] - dsum);
+            for (int r = 0; r < 16; ++r) dpk[r] = dp[r] * a.drop.inv_keep;
+            drop_tile(a.drop, rk, &sKey[buf][u * kTile], h, dpk);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) ds[r] = fast_exp2(fmaf(s[r], a.c, -lse2)) * (dpk[r] - dsum);
+          } else {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) ds[r] = fast_exp2(fmaf(s[r], a.c, -lse2)) * (dp[r] - dsum);
+          }
 #pragma unroll
           for (int m = 0; m < NM; ++m)
 #pragma unroll
@@ -332,12 +394,13 @@ __global__ __launch_bounds__(256) void wide_dq_kernel(const WideArgs a) {
 // (the row statistics as accumulator seeds), P = exp2(c S), dS = P dP,
 // dV^T += dO^T P, dK^T += Q^T dS.  A stage holds 64 queries' Q and dO rows
 // and their statistics.
-template <int HD>
+template <int HD, bool DROP>
 __global__ __launch_bounds__(256) void wide_dkdv_kernel(const WideArgs a) {
-  constexpr int HP = (HD + 31) / 32 * 32, NC = HP / 16, NM = HP / 32, NO = HP / 8;
+  constexpr int HP = (HD + 31) / 32 * 32, NC = (HD + 15) / 16, NM = HP / 32, NO = HP / 8;
   __shared__ __align__(16) bf16 sQ[2][NO * kWTokPad * 8];
   __shared__ __align__(16) bf16 sG[2][NO * kWTokPad * 8];
   __shared__ __align__(16) float sLse[2][kWStage], sDel[2][kWStage];
+  __shared__ __align__(16) uint32_t sKey[2][DROP ? kWStage : 4];   // row keys of the staged queries
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 31, h = lane >> 5;
   const int H = a.heads;
@@ -355,12 +418,13 @@ __global__ __launch_bounds__(256) void wide_dkdv_kernel(const WideArgs a) {
     vop[c] = row_op<HD>(a.v + row, 2 * c + h);
   }
   wide_zero_pad<HD>(sQ[0], sQ[1], sG[0], sG[1], tid);
+  const uint32_t ck = DROP ? drop_col(a.drop, valid ? t : g.x) : 0u;
   f32x16 dva[NM], dka[NM];
 #pragma unroll
   for (int m = 0; m < NM; ++m) dva[m] = dka[m] = f32x16{};
   const int n_tiles = (g.w - g.z + kTile - 1) >> 5;
   const int n_stages = (n_tiles + 1) >> 1;
-  struct Stage { WStage<HD> rows; float2 st; };
+  struct Stage { WStage<HD> rows; float2 st; uint32_t key; };
   wide_walk(
       n_stages,
       [&](int st) {
@@ -368,6 +432,7 @@ __global__ __launch_bounds__(256) void wide_dkdv_kernel(const WideArgs a) {
         s.rows = wide_gload<HD>(a.q, a.dout, g.z + st * kWStage, a.total_q, H, head, tid);
         const int qi = g.z + st * kWStage + tid;
         s.st = tid < kWStage ? a.aux[(size_t)head * a.tq_pad + min(qi, a.tq_pad - 1)] : make_float2(0.f, 0.f);
+        s.key = DROP && tid < kWStage ? drop_row(a.drop, qi, head) : 0u;
         return s;
       },
       [&](int buf, const Stage& s) {
@@ -375,6 +440,7 @@ __global__ __launch_bounds__(256) void wide_dkdv_kernel(const WideArgs a) {
         if (tid < kWStage) {
           sLse[buf][tid] = s.st.x;
           sDel[buf][tid] = s.st.y;
+          if (DROP) sKey[buf][tid] = s.key;
         }
       },
       [&](int buf, int st) {
@@ -408,6 +474,26 @@ __global__ __launch_bounds__(256) void wide_dkdv_kernel(const WideArgs a) {
             p[r] = q0 + row_local(r, h) < g.w ? fast_exp2(s[r] * a.c) : 0.f;
             ds[r] = p[r] * dp[r];
           }
+          if (DROP) {
+            // dp holds dO v - D: a kept partner's dS is P ((dO v) / (1 - p) - D), a dropped one's -P D
+            float nd[16], pk[16];
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {
+              const f32x4 d0 = ldsf4(&sDel[buf][u * kTile + 16 * b + 8 * h]);
+              const f32x4 d1 = ldsf4(&sDel[buf][u * kTile + 16 * b + 8 * h + 4]);
+#pragma unroll
+              for (int e = 0; e < 4; ++e) { nd[8 * b + e] = d0[e]; nd[8 * b + 4 + e] = d1[e]; }
+            }
+#pragma unroll
+            for (int r = 0; r < 16; ++r) pk[r] = 1.f;
+            drop_tile(a.drop, ck, &sKey[buf][u * kTile], h, pk);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const bool keep = pk[r] != 0.f;
+              ds[r] = p[r] * (keep ? fmaf(a.drop.inv_keep, dp[r] - nd[r], nd[r]) : nd[r]);
+              p[r] = keep ? p[r] : 0.f;
+            }
+          }
 #pragma unroll
           for (int m = 0; m < NM; ++m)
 #pragma unroll
@@ -418,7 +504,7 @@ __global__ __launch_bounds__(256) void wide_dkdv_kernel(const WideArgs a) {
         }
       });
   if (!valid) return;
-  store_acc<HD>(a.dv + ((size_t)t * H + head) * HD, dva, 1.f, h);
+  store_acc<HD>(a.dv + ((size_t)t * H + head) * HD, dva, DROP ? a.drop.inv_keep : 1.f, h);
   store_acc<HD>(a.dk + ((size_t)t * H + head) * HD, dka, a.scale, h);
 }
 
@@ -473,11 +559,18 @@ unsigned wide_grid(int total_outer, int nseg, int heads) {
   return (unsigned)(((total_outer + kWGroup - 1) / kWGroup + min(nseg, total_outer)) * heads);
 }
 
-#define ESA_WIDE_LAUNCH(KERNEL, hd, grid, st, a)                                      \
-  do {                                                                                \
-    if (hd == 24) hipLaunchKernelGGL((KERNEL<24>), grid, dim3(256), 0, st, a);       \
-    else if (hd == 32) hipLaunchKernelGGL((KERNEL<32>), grid, dim3(256), 0, st, a);  \
-    else hipLaunchKernelGGL((KERNEL<64>), grid, dim3(256), 0, st, a);                \
+#define ESA_WIDE_LAUNCH_HD(KERNEL, D, hd, grid, st, a)                                   \
+  do {                                                                                    \
+    if (hd == 16) hipLaunchKernelGGL((KERNEL<16, D>), grid, dim3(256), 0, st, a);         \
+    else if (hd == 24) hipLaunchKernelGGL((KERNEL<24, D>), grid, dim3(256), 0, st, a);    \
+    else if (hd == 32) hipLaunchKernelGGL((KERNEL<32, D>), grid, dim3(256), 0, st, a);    \
+    else hipLaunchKernelGGL((KERNEL<64, D>), grid, dim3(256), 0, st, a);                  \
+  } while (0)
+// Head dim 16 only with dropout (without, esa_attn_dense.hip's kernels run).
+#define ESA_WIDE_LAUNCH(KERNEL, hd, drop, grid, st, a)                                   \
+  do {                                                                                    \
+    if (drop) ESA_WIDE_LAUNCH_HD(KERNEL, true, hd, grid, st, a);                         \
+    else ESA_WIDE_LAUNCH_HD(KERNEL, false, hd, grid, st, a);                             \
   } while (0)
 
 }  // namespace
@@ -488,7 +581,8 @@ size_t wide_attn_workspace_size(int total_q, int total_k, int heads, int head_di
 }
 
 int wide_attn_fwd(const DenseAttnCall& c, void* workspace, size_t workspace_bytes, hipStream_t st) {
-  if (c.head_dim != 24 && c.head_dim != 32 && c.head_dim != 64) return ESA_ERR_HEAD_DIM;
+  if (c.head_dim != 24 && c.head_dim != 32 && c.head_dim != 64 && !(c.head_dim == 16 && c.dropout))
+    return ESA_ERR_HEAD_DIM;
   const WideWs w = wide_ws(c.total_q, c.total_k, c.heads, false);
   if (workspace_bytes < w.total) return ESA_ERR_WORKSPACE;
   char* ws = static_cast<char*>(workspace);
@@ -504,15 +598,18 @@ int wide_attn_fwd(const DenseAttnCall& c, void* workspace, size_t workspace_byte
   a.groups = p.plan_q; a.count = p.count_q;
   a.total_q = c.total_q; a.total_k = c.total_k; a.heads = c.heads; a.tq_pad = p.tq_pad;
   a.c = c.scale * kLog2e; a.scale = c.scale;
+  a.drop = c.drop;
   a.o = static_cast<bf16*>(c.out); a.lse_out = c.lse;
   ESA_TIMED(esa_profile::kAttnFwd, st,
-            ESA_WIDE_LAUNCH(wide_fwd_kernel, c.head_dim, dim3(wide_grid(c.total_q, c.nseg, c.heads)), st, a));
+            ESA_WIDE_LAUNCH(wide_fwd_kernel, c.head_dim, c.dropout, dim3(wide_grid(c.total_q, c.nseg, c.heads)), st,
+                            a));
   ESA_LAUNCH_CHECK();
   return ESA_OK;
 }
 
 int wide_attn_bwd(const DenseAttnCall& c, void* workspace, size_t workspace_bytes, hipStream_t st) {
-  if (c.head_dim != 24 && c.head_dim != 32 && c.head_dim != 64) return ESA_ERR_HEAD_DIM;
+  if (c.head_dim != 24 && c.head_dim != 32 && c.head_dim != 64 && !(c.head_dim == 16 && c.dropout))
+    return ESA_ERR_HEAD_DIM;
   const WideWs w = wide_ws(c.total_q, c.total_k, c.heads, true);
   if (workspace_bytes < w.total) return ESA_ERR_WORKSPACE;
   char* ws = static_cast<char*>(workspace);
@@ -535,15 +632,18 @@ int wide_attn_bwd(const DenseAttnCall& c, void* workspace, size_t workspace_byte
   a.lse = c.lse_in; a.aux = p.aux;
   a.total_q = c.total_q; a.total_k = c.total_k; a.heads = c.heads; a.tq_pad = p.tq_pad;
   a.c = c.scale * kLog2e; a.scale = c.scale;
+  a.drop = c.drop;
   a.dq = static_cast<bf16*>(c.dq); a.dk = static_cast<bf16*>(c.dk); a.dv = static_cast<bf16*>(c.dv);
   // dQ first: it writes the row statistics the dK/dV pass stages
   a.groups = p.plan_q; a.count = p.count_q;
   ESA_TIMED(esa_profile::kAttnBwdDq, st,
-            ESA_WIDE_LAUNCH(wide_dq_kernel, c.head_dim, dim3(wide_grid(c.total_q, c.nseg, c.heads)), st, a));
+            ESA_WIDE_LAUNCH(wide_dq_kernel, c.head_dim, c.dropout, dim3(wide_grid(c.total_q, c.nseg, c.heads)), st,
+                            a));
   ESA_LAUNCH_CHECK();
   a.groups = p.plan_k; a.count = p.count_k;
   ESA_TIMED(esa_profile::kAttnBwdDkdv, st,
-            ESA_WIDE_LAUNCH(wide_dkdv_kernel, c.head_dim, dim3(wide_grid(c.total_k, c.nseg, c.heads)), st, a));
+            ESA_WIDE_LAUNCH(wide_dkdv_kernel, c.head_dim, c.dropout, dim3(wide_grid(c.total_k, c.nseg, c.heads)), st,
+                            a));
   ESA_LAUNCH_CHECK();
   return ESA_OK;
 }

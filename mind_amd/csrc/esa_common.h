@@ -64,3 +64,49 @@ DEVI int ceil_div(int a, int b) { return (a + b - 1) / b; }
 DEVI __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
 }
+
+// ---- attention dropout on the softmax probabilities, as xformers'
+// memory_efficient_attention(p=...) and SDPA(dropout_p=...) apply it
+// (esa/mha.py:76,82): the output is (P o Z / (1 - p)) V for a keep mask Z;
+// the log-sum-exp is that of the undropped scores.  Query token q keeps key
+// token k in head h iff
+//   fmix32(row(q, h) ^ col(k)) >= thr,
+//   row(q, h) = fmix32(s0 ^ fmix32(q * heads + h)),
+//   col(k)    = fmix32(s1 ^ fmix32(k)),
+// with q, k the global token indices of the call ([0, total_q), [0,
+// total_k)), s0 / s1 the low / high 32-bit words of the 64-bit seed (s1
+// xor 0x9E3779B9), thr = round(p 2^32) capped at 2^32 - 1, and fmix32 the
+// 32-bit finalizer of MurmurHash3 (A. Appleby, SMHasher, public domain).
+// A counter-based hash: the mask is a pure function of (seed, h, q, k), so
+// the forward and both backward passes evaluate the same mask whatever their
+// tiling, and row / column keys are computed once per token.
+struct DropoutCfg {
+  uint32_t s0, s1, thr;
+  float inv_keep;   // 1 / (1 - p)
+  int heads;
+};
+
+inline DropoutCfg make_dropout(float p, unsigned long long seed, int heads) {
+  DropoutCfg d{};
+  d.s0 = (uint32_t)seed;
+  d.s1 = (uint32_t)(seed >> 32) ^ 0x9E3779B9u;
+  const double t = (double)p * 4294967296.0 + 0.5;
+  d.thr = t >= 4294967295.0 ? 0xFFFFFFFFu : (uint32_t)t;
+  d.inv_keep = (float)(1.0 / (1.0 - (double)p));
+  d.heads = heads;
+  return d;
+}
+
+DEVI uint32_t fmix32(uint32_t h) {
+  h ^= h >> 16;
+  h *= 0x85EBCA6Bu;
+  h ^= h >> 13;
+  h *= 0xC2B2AE35u;
+  h ^= h >> 16;
+  return h;
+}
+DEVI uint32_t drop_row(const DropoutCfg& d, int q, int head) {
+  return fmix32(d.s0 ^ fmix32((uint32_t)q * (uint32_t)d.heads + (uint32_t)head));
+}
+DEVI uint32_t drop_col(const DropoutCfg& d, int k) { return fmix32(d.s1 ^ fmix32((uint32_t)k)); }
+DEVI bool drop_keep(const DropoutCfg& d, uint32_t row, uint32_t col) { return fmix32(row ^ col) >= d.thr; }

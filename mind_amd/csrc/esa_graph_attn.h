@@ -3,6 +3,7 @@
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stddef.h>
+#include "esa_common.h"
 
 // Edge-mask plan sections the gather kernels read for ESA_MASK_EDGE(_PLAN) at
 // head dims other than 16 (the plan's layout is esa_attn.hip's): per 32-token
@@ -30,6 +31,7 @@ struct GraphAttnArgs {
   const int4* q_desc; const int4* k_desc;           // per-token {lo, hi, pa, pb} from a node plan, or null
   const int2* q_bounds; const int2* k_bounds;       // edge lists: per-token partner range (the plan's bounds)
   GraphEdgeLists edge;                              // edge lists (edge.ids[0] non-null): the mask's partners
+  DropoutCfg drop; bool dropout;                    // attention dropout (esa_common.h) when `dropout`
 };
 
 // Head dims of the gather kernels.

@@ -27,6 +27,10 @@
 // call with the library's stable CSR sort or once per batch into a node plan;
 // edge mask: the key tiles' lists, or the query tiles' when the mask is
 // symmetric).  Every sum runs in a fixed order: the backward is deterministic.
+// With attention dropout (DROP), each partner's probability enters the
+// products over partners only where the call's keep mask (esa_common.h) keeps
+// it, and the outputs carry the 1 / (1 - p) factor; the softmax statistics
+// are those of the undropped scores.
 #include "esa_common.h"
 #include "esa_graph_attn.h"
 #include "esa_profile.h"
@@ -260,7 +264,7 @@ DEVI WalkSrc walk_src(const GraphEdgeLists& e, int2 bounds, int t) {
   return s;
 }
 
-template <typename T, int HD, class Src>
+template <typename T, int HD, bool DROP, class Src>
 DEVI void fwd_token(const GraphAttnArgs& a, int t, const Src& src0) {
   constexpr int L = HeadLanes<HD>::L, HPP = HeadLanes<HD>::HPP;
   const T* __restrict__ q = static_cast<const T*>(a.q);
@@ -275,6 +279,7 @@ DEVI void fwd_token(const GraphAttnArgs& a, int t, const Src& src0) {
     float qv[4], acc[4] = {0.f, 0.f, 0.f, 0.f};
     load4<T>(q + ((size_t)t * H + hc) * HD + d0, qv);
     hl.own(qv);
+    const uint32_t rk = DROP ? drop_row(a.drop, t, hc) : 0u;
     float m = -INFINITY, l = 0.f;
     Src src = src0;
     int j[kGU];
@@ -302,13 +307,16 @@ DEVI void fwd_token(const GraphAttnArgs& a, int t, const Src& src0) {
       for (int u = 0; u < kGU; ++u) {
         const float pu = ex2<T>(s[u] - mt);
         l += pu;
+        const float pv = !DROP || drop_keep(a.drop, rk, drop_col(a.drop, j[u])) ? pu : 0.f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[i] = fmaf(pu, vr[u][i], acc[i]);
+        for (int i = 0; i < 4; ++i) acc[i] = fmaf(pv, vr[u][i], acc[i]);
       }
       m = mt;
     }
     if (h < H) {
-      if (hl.dims) store4<T>(static_cast<T*>(a.out) + ((size_t)t * H + h) * HD + d0, acc, l > 0.f ? 1.f / l : 0.f);
+      if (hl.dims)
+        store4<T>(static_cast<T*>(a.out) + ((size_t)t * H + h) * HD + d0, acc,
+                  l > 0.f ? (DROP ? a.drop.inv_keep : 1.f) / l : 0.f);
       if (hl.li == 0) a.lse[(size_t)h * a.total_q + t] = l > 0.f ? (m + lg2<T>(l)) * kLn2 : -INFINITY;
     }
   }
@@ -316,7 +324,7 @@ DEVI void fwd_token(const GraphAttnArgs& a, int t, const Src& src0) {
 
 // dQ_i = scale * sum_j P_ij (dP_ij - D_i) k_j over i's partners; also writes
 // D_i = rowsum(dO_i * O_i) per head for the dK / dV pass.
-template <typename T, int HD, class Src>
+template <typename T, int HD, bool DROP, class Src>
 DEVI void dq_token(const GraphAttnArgs& a, int t, const Src& src0) {
   constexpr int L = HeadLanes<HD>::L, HPP = HeadLanes<HD>::HPP;
   const T* __restrict__ q = static_cast<const T*>(a.q);
@@ -338,6 +346,7 @@ DEVI void dq_token(const GraphAttnArgs& a, int t, const Src& src0) {
     hl.own(qv);
     hl.own(gv);
     const float dsum = head_sum<L>(dot4(gv, ov));
+    const uint32_t rk = DROP ? drop_row(a.drop, t, hc) : 0u;
     const float l = a.lse_in[(size_t)hc * a.total_q + t];
     const float l2 = l == -INFINITY ? INFINITY : l * kLog2e;
     if (h < H && hl.li == 0) a.dsum[(size_t)h * a.total_q + t] = dsum;
@@ -354,7 +363,9 @@ DEVI void dq_token(const GraphAttnArgs& a, int t, const Src& src0) {
 #pragma unroll
       for (int u = 0; u < kGU; ++u) {
         const float pu = ok[u] ? ex2<T>(fmaf(head_sum<L>(dot4(qv, kr[u])), a.c, -l2)) : 0.f;
-        const float ds = pu * (head_sum<L>(dot4(gv, vr[u])) - dsum);
+        float dp = head_sum<L>(dot4(gv, vr[u]));
+        if (DROP) dp = drop_keep(a.drop, rk, drop_col(a.drop, j[u])) ? dp * a.drop.inv_keep : 0.f;
+        const float ds = pu * (dp - dsum);
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[i] = fmaf(ds, kr[u][i], acc[i]);
       }
@@ -365,7 +376,7 @@ DEVI void dq_token(const GraphAttnArgs& a, int t, const Src& src0) {
 
 // dV_j = sum_i P_ij dO_i, dK_j = scale * sum_i P_ij (dP_ij - D_i) q_i over the
 // queries i that attend to key j (ascending).
-template <typename T, int HD, class Src>
+template <typename T, int HD, bool DROP, class Src>
 DEVI void dkdv_token(const GraphAttnArgs& a, int t, const Src& src0) {
   constexpr int L = HeadLanes<HD>::L, HPP = HeadLanes<HD>::HPP;
   const T* __restrict__ q = static_cast<const T*>(a.q);
@@ -384,6 +395,7 @@ DEVI void dkdv_token(const GraphAttnArgs& a, int t, const Src& src0) {
     load4<T>(v + row, vv);
     hl.own(kv);
     hl.own(vv);
+    const uint32_t ck = DROP ? drop_col(a.drop, t) : 0u;
     Src src = src0;
     int i[kGU];
     bool ok[kGU];
@@ -400,17 +412,20 @@ DEVI void dkdv_token(const GraphAttnArgs& a, int t, const Src& src0) {
 #pragma unroll
       for (int u = 0; u < kGU; ++u) {
         const float pu = ok[u] ? ex2<T>(fmaf(head_sum<L>(dot4(qr[u], kv)), a.c, -l2[u])) : 0.f;
-        const float ds = pu * (head_sum<L>(dot4(gr[u], vv)) - ds_[u]);
+        float dp = head_sum<L>(dot4(gr[u], vv)), pv = pu;
+        if (DROP && !drop_keep(a.drop, drop_row(a.drop, i[u], hc), ck)) dp = pv = 0.f;
+        if (DROP) dp *= a.drop.inv_keep;
+        const float ds = pu * (dp - ds_[u]);
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-          dv[c] = fmaf(pu, gr[u][c], dv[c]);
+          dv[c] = fmaf(pv, gr[u][c], dv[c]);
           dk[c] = fmaf(ds, qr[u][c], dk[c]);
         }
       }
     }
     if (h < H && hl.dims) {
       store4<T>(static_cast<T*>(a.dk) + ((size_t)t * H + h) * HD + d0, dk, a.scale);
-      store4<T>(static_cast<T*>(a.dv) + ((size_t)t * H + h) * HD + d0, dv, 1.f);
+      store4<T>(static_cast<T*>(a.dv) + ((size_t)t * H + h) * HD + d0, dv, DROP ? a.drop.inv_keep : 1.f);
     }
   }
 }
@@ -418,49 +433,55 @@ DEVI void dkdv_token(const GraphAttnArgs& a, int t, const Src& src0) {
 DEVI CsrSrc csr_src(const int* list, int4 d) { return CsrSrc{list, d.z, d.w, d.x, d.y, INT_MIN}; }
 
 // The kernels: node mode over a CSR (the key pass over the transposed CSR).
-template <typename T, int HD>
+template <typename T, int HD, bool DROP>
 __global__ __launch_bounds__(256) void graph_attn_fwd_kernel(const GraphAttnArgs a) {
   const int t = wave_token();
   if (t >= a.total_q) return;
-  fwd_token<T, HD>(a, t, csr_src(a.indices, token_desc(a.q_desc, a.cu_q, a.cu_k, a.nseg, a.total_k, a.indptr, a.nnz, t)));
+  fwd_token<T, HD, DROP>(a, t, csr_src(a.indices, token_desc(a.q_desc, a.cu_q, a.cu_k, a.nseg, a.total_k, a.indptr, a.nnz, t)));
 }
-template <typename T, int HD>
+template <typename T, int HD, bool DROP>
 __global__ __launch_bounds__(256) void graph_attn_dq_kernel(const GraphAttnArgs a) {
   const int t = wave_token();
   if (t >= a.total_q) return;
-  dq_token<T, HD>(a, t, csr_src(a.indices, token_desc(a.q_desc, a.cu_q, a.cu_k, a.nseg, a.total_k, a.indptr, a.nnz, t)));
+  dq_token<T, HD, DROP>(a, t, csr_src(a.indices, token_desc(a.q_desc, a.cu_q, a.cu_k, a.nseg, a.total_k, a.indptr, a.nnz, t)));
 }
-template <typename T, int HD>
+template <typename T, int HD, bool DROP>
 __global__ __launch_bounds__(256) void graph_attn_dkdv_kernel(const GraphAttnArgs a) {
   const int t = wave_token();
   if (t >= a.total_k) return;
-  dkdv_token<T, HD>(a, t, csr_src(a.t_rows, token_desc(a.k_desc, a.cu_k, a.cu_q, a.nseg, a.total_q, a.t_indptr, a.nnz, t)));
+  dkdv_token<T, HD, DROP>(a, t, csr_src(a.t_rows, token_desc(a.k_desc, a.cu_k, a.cu_q, a.nseg, a.total_q, a.t_indptr, a.nnz, t)));
 }
 
 // Edge mask over a plan's lists: the query side reads direction 0, the key
 // side direction 1, or direction 0 when the plan is symmetric.
-template <typename T, int HD, int PASS>   // 0 forward, 1 dQ, 2 dK / dV
+template <typename T, int HD, bool DROP, int PASS>   // 0 forward, 1 dQ, 2 dK / dV
 DEVI void graph_edge_pass(const GraphAttnArgs& a) {
   const int t = wave_token();
   if (t >= (PASS == 2 ? a.total_k : a.total_q)) return;
   const int d = (PASS == 2 && a.edge.sym[0] == 0) ? 1 : 0;
   const int n = a.edge.info[d][t >> 5];
   auto run = [&](const auto& src) {
-    if (PASS == 0) fwd_token<T, HD>(a, t, src);
-    if (PASS == 1) dq_token<T, HD>(a, t, src);
-    if (PASS == 2) dkdv_token<T, HD>(a, t, src);
+    if (PASS == 0) fwd_token<T, HD, DROP>(a, t, src);
+    if (PASS == 1) dq_token<T, HD, DROP>(a, t, src);
+    if (PASS == 2) dkdv_token<T, HD, DROP>(a, t, src);
   };
   if (n >= 0)
     run(list_src(a.edge, d, t, n));
   else
     run(walk_src(a.edge, (PASS == 2 ? a.k_bounds : a.q_bounds)[t], t));
 }
-template <typename T, int HD>
-__global__ __launch_bounds__(256) void graph_edge_fwd_kernel(const GraphAttnArgs a) { graph_edge_pass<T, HD, 0>(a); }
-template <typename T, int HD>
-__global__ __launch_bounds__(256) void graph_edge_dq_kernel(const GraphAttnArgs a) { graph_edge_pass<T, HD, 1>(a); }
-template <typename T, int HD>
-__global__ __launch_bounds__(256) void graph_edge_dkdv_kernel(const GraphAttnArgs a) { graph_edge_pass<T, HD, 2>(a); }
+template <typename T, int HD, bool DROP>
+__global__ __launch_bounds__(256) void graph_edge_fwd_kernel(const GraphAttnArgs a) {
+  graph_edge_pass<T, HD, DROP, 0>(a);
+}
+template <typename T, int HD, bool DROP>
+__global__ __launch_bounds__(256) void graph_edge_dq_kernel(const GraphAttnArgs a) {
+  graph_edge_pass<T, HD, DROP, 1>(a);
+}
+template <typename T, int HD, bool DROP>
+__global__ __launch_bounds__(256) void graph_edge_dkdv_kernel(const GraphAttnArgs a) {
+  graph_edge_pass<T, HD, DROP, 2>(a);
+}
 
 // row_of[e] = the CSR row holding entry e (-1 for an entry no row covers).
 __global__ void fill_minus_one_kernel(int* __restrict__ p, long n) {
@@ -616,19 +637,22 @@ int graph_node_plan_build(const int* indptr, const int* indices, const int* cu_q
 
 namespace {
 
-// Launches KERNEL<T, HD> for the call's dtype and head dim.
+// Launches KERNEL<T, HD, DROP> for the call's dtype, head dim and dropout.
+#define ESA_GRAPH_LAUNCH_HD(KERNEL, T, D, hd, grid, st, a)                                        \
+  do {                                                                                            \
+    if (hd == 16) hipLaunchKernelGGL((KERNEL<T, 16, D>), grid, dim3(256), 0, st, a);              \
+    else if (hd == 24) hipLaunchKernelGGL((KERNEL<T, 24, D>), grid, dim3(256), 0, st, a);         \
+    else if (hd == 32) hipLaunchKernelGGL((KERNEL<T, 32, D>), grid, dim3(256), 0, st, a);         \
+    else hipLaunchKernelGGL((KERNEL<T, 64, D>), grid, dim3(256), 0, st, a);                       \
+  } while (0)
 #define ESA_GRAPH_LAUNCH(KERNEL, dtype, hd, grid, st, a)                                          \
   do {                                                                                            \
     if (dtype == ESA_F32) {                                                                       \
-      if (hd == 16) hipLaunchKernelGGL((KERNEL<float, 16>), grid, dim3(256), 0, st, a);           \
-      else if (hd == 24) hipLaunchKernelGGL((KERNEL<float, 24>), grid, dim3(256), 0, st, a);      \
-      else if (hd == 32) hipLaunchKernelGGL((KERNEL<float, 32>), grid, dim3(256), 0, st, a);      \
-      else hipLaunchKernelGGL((KERNEL<float, 64>), grid, dim3(256), 0, st, a);                    \
+      if (a.dropout) ESA_GRAPH_LAUNCH_HD(KERNEL, float, true, hd, grid, st, a);                   \
+      else ESA_GRAPH_LAUNCH_HD(KERNEL, float, false, hd, grid, st, a);                            \
     } else {                                                                                      \
-      if (hd == 16) hipLaunchKernelGGL((KERNEL<bf16, 16>), grid, dim3(256), 0, st, a);            \
-      else if (hd == 24) hipLaunchKernelGGL((KERNEL<bf16, 24>), grid, dim3(256), 0, st, a);       \
-      else if (hd == 32) hipLaunchKernelGGL((KERNEL<bf16, 32>), grid, dim3(256), 0, st, a);       \
-      else hipLaunchKernelGGL((KERNEL<bf16, 64>), grid, dim3(256), 0, st, a);                     \
+      if (a.dropout) ESA_GRAPH_LAUNCH_HD(KERNEL, bf16, true, hd, grid, st, a);                    \
+      else ESA_GRAPH_LAUNCH_HD(KERNEL, bf16, false, hd, grid, st, a);                             \
     }                                                                                             \
   } while (0)
 

@@ -1,8 +1,8 @@
 """Varlen attention over packed edge-token segments, on the gfx950 kernels.
 
 ``varlen_attention`` is the drop-in for ``flash_attn_varlen_func`` as the
-reference calls it (esa/mha_flash_varlen.py:177-184: causal=False, dropout 0,
-``softmax_scale=None`` meaning 1/sqrt(head_dim)), extended with the
+reference calls it (esa/mha_flash_varlen.py:177-184: causal=False, dropout_p
+in training, ``softmax_scale=None`` meaning 1/sqrt(head_dim)), extended with the
 edge-adjacency mask of esa/masked_layers.py:121-142 evaluated on the fly from
 per-token ``(src, dst)`` node ids.  Tensors are packed ``[total, heads,
 head_dim]`` (head_dim 16, 24, 32 or 64: ESA's dim / heads) bf16 (MFMA kernels, fp32
@@ -19,6 +19,20 @@ import torch
 from .. import _lib
 
 HEAD_DIMS = (16, 24, 32, 64)   # head dims the kernels take
+_SEED_MASK = (1 << 63) - 1
+
+
+def _check_dropout(p: float) -> float:
+    p = float(p)
+    if not 0.0 <= p < 1.0:
+        raise ValueError(f"dropout_p must be in [0, 1) (got {p})")
+    return p
+
+
+def draw_dropout_seed() -> int:
+    """A fresh 62-bit dropout seed from torch's default CPU generator (so ``torch.manual_seed`` reproduces the
+    keep masks of a run)."""
+    return int(torch.randint(0, 1 << 62, (), dtype=torch.int64))
 
 
 _DTYPES = {torch.bfloat16: _lib.ESA_BF16, torch.float32: _lib.ESA_F32}
@@ -181,8 +195,12 @@ def _mask_args(tq: int, edge_src, edge_dst, adj_indptr, adj_indices, edge_plan=N
 
 
 def attn_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale,
-             edge_src=None, edge_dst=None, adj_indptr=None, adj_indices=None, edge_plan=None, adj_plan=None):
-    """Raw forward: returns ``(out [Tq,H,hd] (dtype of q), softmax_lse [H,Tq] fp32)``."""
+             edge_src=None, edge_dst=None, adj_indptr=None, adj_indices=None, edge_plan=None, adj_plan=None,
+             dropout_p=0.0, dropout_seed=0):
+    """Raw forward: returns ``(out [Tq,H,hd] (dtype of q), softmax_lse [H,Tq] fp32)``.  With ``dropout_p`` > 0
+    the keep mask is the hash of ``(dropout_seed, head, q, k)`` the C ABI defines; the backward must get the same
+    ``dropout_p`` and seed."""
+    dropout_p = _check_dropout(dropout_p)
     _lib.require_gpu(q, k, v, cu_seqlens_q, cu_seqlens_k, edge_src, edge_dst, adj_indptr, adj_indices, edge_plan,
                      adj_plan)
     heads, hd = q.shape[1], q.shape[-1]
@@ -204,15 +222,16 @@ def attn_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, so
     lib = _lib.load()
     rc = lib.esa_varlen_attn_fwd(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(), batch, tq, tk,
-        int(max_seqlen_q), int(max_seqlen_k), heads, hd, dt, float(softmax_scale),
-        mask_kind, _lib.ptr(mask_a), _lib.ptr(mask_b), nnz, out.data_ptr(), lse.data_ptr(), ws.data_ptr(),
-        ws.numel(), _lib.stream_of(q))
+        int(max_seqlen_q), int(max_seqlen_k), heads, hd, dt, float(softmax_scale), dropout_p,
+        int(dropout_seed) & _SEED_MASK, mask_kind, _lib.ptr(mask_a), _lib.ptr(mask_b), nnz, out.data_ptr(),
+        lse.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_of(q))
     _lib.check(rc, "esa_varlen_attn_fwd")
     return out, lse
 
 
 def attn_fwd_noalloc(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale, out, lse,
-                     edge_src=None, edge_dst=None, adj_indptr=None, adj_indices=None, edge_plan=None, adj_plan=None):
+                     edge_src=None, edge_dst=None, adj_indptr=None, adj_indices=None, edge_plan=None, adj_plan=None,
+                     dropout_p=0.0, dropout_seed=0):
     """``attn_fwd`` into caller-provided ``out`` [Tq,H,hd] and ``lse`` [H,Tq] fp32 through
     esa_varlen_attn_fwd_noalloc: no workspace, no device allocation (the library's static per-GPU scratch;
     calls that overlap on one GPU race).  Raises EsaError (ESA_ERR_SCRATCH) for shapes beyond that scratch."""
@@ -236,14 +255,16 @@ def attn_fwd_noalloc(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seql
     rc = _lib.load().esa_varlen_attn_fwd_noalloc(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(), batch, tq, tk,
         int(max_seqlen_q), int(max_seqlen_k), heads, hd, _dtype_code(q), float(softmax_scale),
-        mask_kind, _lib.ptr(mask_a), _lib.ptr(mask_b), nnz, out.data_ptr(), lse.data_ptr(), _lib.stream_of(q))
+        _check_dropout(dropout_p), int(dropout_seed) & _SEED_MASK, mask_kind, _lib.ptr(mask_a), _lib.ptr(mask_b), nnz, out.data_ptr(), lse.data_ptr(), _lib.stream_of(q))
     _lib.check(rc, "esa_varlen_attn_fwd_noalloc")
     return out, lse
 
 
 def attn_bwd(dout, q, k, v, out, lse, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale,
-             edge_src=None, edge_dst=None, adj_indptr=None, adj_indices=None, edge_plan=None, adj_plan=None):
+             edge_src=None, edge_dst=None, adj_indptr=None, adj_indices=None, edge_plan=None, adj_plan=None,
+             dropout_p=0.0, dropout_seed=0):
     """Raw backward: returns ``(dq, dk, dv)`` (dtype and shapes of q, k, v)."""
+    dropout_p = _check_dropout(dropout_p)
     _lib.require_gpu(dout, q, k, v, out, lse)
     heads, hd = q.shape[1], q.shape[-1]
     _check_tokens("q", q)
@@ -262,8 +283,9 @@ def attn_bwd(dout, q, k, v, out, lse, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, 
     rc = lib.esa_varlen_attn_bwd(
         dout.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr(),
         cu_seqlens_q.data_ptr(), cu_seqlens_k.data_ptr(), batch, tq, tk, int(max_seqlen_q), int(max_seqlen_k),
-        heads, hd, dt, float(softmax_scale), mask_kind, _lib.ptr(mask_a), _lib.ptr(mask_b), nnz,
-        dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_of(q))
+        heads, hd, dt, float(softmax_scale), dropout_p, int(dropout_seed) & _SEED_MASK, mask_kind,
+        _lib.ptr(mask_a), _lib.ptr(mask_b), nnz, dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(),
+        ws.numel(), _lib.stream_of(q))
     _lib.check(rc, "esa_varlen_attn_bwd")
     return dq, dk, dv
 
@@ -278,14 +300,15 @@ def _op_varlen_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens
                    edge_src: Optional[torch.Tensor], edge_dst: Optional[torch.Tensor],
                    adj_indptr: Optional[torch.Tensor], adj_indices: Optional[torch.Tensor],
                    edge_plan: Optional[torch.Tensor] = None,
-                   adj_plan: Optional[torch.Tensor] = None) -> tuple[torch.Tensor, torch.Tensor]:
+                   adj_plan: Optional[torch.Tensor] = None, dropout_p: float = 0.0,
+                   dropout_seed: int = 0) -> tuple[torch.Tensor, torch.Tensor]:
     return attn_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale, edge_src,
-                    edge_dst, adj_indptr, adj_indices, edge_plan, adj_plan)
+                    edge_dst, adj_indptr, adj_indices, edge_plan, adj_plan, dropout_p, dropout_seed)
 
 
 @_op_varlen_fwd.register_fake
 def _(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale, edge_src, edge_dst,
-      adj_indptr, adj_indices, edge_plan=None, adj_plan=None):
+      adj_indptr, adj_indices, edge_plan=None, adj_plan=None, dropout_p=0.0, dropout_seed=0):
     return torch.empty_like(q), q.new_empty((q.shape[1], q.shape[0]), dtype=torch.float32)
 
 
@@ -296,32 +319,34 @@ def _op_varlen_bwd(dout: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torc
                    edge_dst: Optional[torch.Tensor], adj_indptr: Optional[torch.Tensor],
                    adj_indices: Optional[torch.Tensor],
                    edge_plan: Optional[torch.Tensor] = None,
-                   adj_plan: Optional[torch.Tensor] = None) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+                   adj_plan: Optional[torch.Tensor] = None, dropout_p: float = 0.0,
+                   dropout_seed: int = 0) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     return attn_bwd(dout, q, k, v, out, lse, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale,
-                    edge_src, edge_dst, adj_indptr, adj_indices, edge_plan, adj_plan)
+                    edge_src, edge_dst, adj_indptr, adj_indices, edge_plan, adj_plan, dropout_p, dropout_seed)
 
 
 @_op_varlen_bwd.register_fake
 def _(dout, q, k, v, out, lse, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, softmax_scale, edge_src,
-      edge_dst, adj_indptr, adj_indices, edge_plan=None, adj_plan=None):
+      edge_dst, adj_indptr, adj_indices, edge_plan=None, adj_plan=None, dropout_p=0.0, dropout_seed=0):
     return torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
 
 
 def _varlen_setup(ctx, inputs, output):
-    q, k, v, cu_q, cu_k, max_q, max_k, scale, edge_src, edge_dst, adj_indptr, adj_indices, edge_plan, adj_plan = inputs
+    (q, k, v, cu_q, cu_k, max_q, max_k, scale, edge_src, edge_dst, adj_indptr, adj_indices, edge_plan, adj_plan,
+     dropout_p, dropout_seed) = inputs
     out, lse = output
     ctx.save_for_backward(q, k, v, out, lse, cu_q, cu_k, edge_src, edge_dst, adj_indptr, adj_indices, edge_plan,
                           adj_plan)
-    ctx.meta = (max_q, max_k, scale)
+    ctx.meta = (max_q, max_k, scale, dropout_p, dropout_seed)
 
 
 def _varlen_backward(ctx, dout, _dlse):
     q, k, v, out, lse, cu_q, cu_k, edge_src, edge_dst, adj_indptr, adj_indices, edge_plan, adj_plan = ctx.saved_tensors
-    max_q, max_k, scale = ctx.meta
+    max_q, max_k, scale, dropout_p, dropout_seed = ctx.meta
     dq, dk, dv = torch.ops.esa_hip.varlen_attn_bwd(dout.contiguous(), q, k, v, out, lse, cu_q, cu_k, max_q, max_k,
                                                    scale, edge_src, edge_dst, adj_indptr, adj_indices, edge_plan,
-                                                   adj_plan)
-    return dq, dk, dv, None, None, None, None, None, None, None, None, None, None, None
+                                                   adj_plan, dropout_p, dropout_seed)
+    return (dq, dk, dv) + (None,) * 13
 
 
 torch.library.register_autograd("esa_hip::varlen_attn_fwd", _varlen_backward, setup_context=_varlen_setup)
@@ -329,7 +354,7 @@ torch.library.register_autograd("esa_hip::varlen_attn_fwd", _varlen_backward, se
 
 def varlen_attention(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k, dropout_p=0.0,
                      softmax_scale=None, causal=False, edge_src=None, edge_dst=None, return_lse=False,
-                     adj_indptr=None, adj_indices=None, edge_plan=None, adj_plan=None):
+                     adj_indptr=None, adj_indices=None, edge_plan=None, adj_plan=None, dropout_seed=None):
     """``flash_attn_varlen_func``-compatible entry (plus the ESA masks).
 
     q: [Tq, H, hd]; k, v: [Tk, H, hd] (hd 16, 24, 32 or 64), all bfloat16 or all float32;
@@ -346,12 +371,16 @@ def varlen_attention(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seql
     backward then reads its transpose).  With return_lse, also returns the
     (non-differentiable) softmax log-sum-exp [H, Tq]; -inf marks a query with
     no admissible key (its output is 0).
+    dropout_p: attention dropout on the softmax probabilities (the reference's
+    training-time p, esa/mha.py:76,82); the keep mask is a hash of
+    (dropout_seed, head, query, key), the seed drawn from torch's CPU generator
+    when None.  The lse is that of the undropped scores.
     """
     if causal:
         raise NotImplementedError("causal attention is not on the ESA path (the reference uses causal=False)")
-    if dropout_p:
-        raise NotImplementedError("attention dropout is not supported on the HIP path (MIND's RNA configuration "
-                                  "trains with sab/mab dropout 0.08 and pma dropout 0.05; its other configurations use 0)")
+    dropout_p = _check_dropout(dropout_p)
+    if dropout_p > 0.0 and dropout_seed is None:
+        dropout_seed = draw_dropout_seed()
     if softmax_scale is None:
         softmax_scale = 1.0 / math.sqrt(q.shape[-1])
     if (edge_src is None) != (edge_dst is None):
@@ -360,7 +389,8 @@ def varlen_attention(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seql
         raise ValueError("adj_indptr and adj_indices must be given together")
     out, lse = torch.ops.esa_hip.varlen_attn_fwd(q, k, v, cu_seqlens_q, cu_seqlens_k, int(max_seqlen_q),
                                                  int(max_seqlen_k), float(softmax_scale), edge_src, edge_dst,
-                                                 adj_indptr, adj_indices, edge_plan, adj_plan)
+                                                 adj_indptr, adj_indices, edge_plan, adj_plan, dropout_p,
+                                                 int(dropout_seed or 0) & _SEED_MASK)
     return (out, lse) if return_lse else out
 
 
@@ -374,24 +404,24 @@ def _pma_workspace(device, batch, k_seeds, total_k, heads, head_dim, dtype, back
 
 class _PMAAttention(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, q, k, v, cu_k, max_k, scale):
+    def forward(ctx, q, k, v, cu_k, max_k, scale, dropout_p, dropout_seed):
         batch, k_seeds, heads, hd = cu_k.numel() - 1, q.shape[0], q.shape[1], q.shape[2]
         dt = _dtype_code(q)
         out = torch.empty((batch * k_seeds, heads, hd), dtype=q.dtype, device=q.device)
         lse = torch.empty((heads, batch * k_seeds), dtype=torch.float32, device=q.device)
         ws = _pma_workspace(q.device, batch, k_seeds, k.shape[0], heads, hd, dt, False)
         rc = _lib.load().esa_pma_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), cu_k.data_ptr(), batch, k_seeds,
-                                     k.shape[0], int(max_k), heads, hd, dt, float(scale), out.data_ptr(),
-                                     lse.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_of(q))
+                                     k.shape[0], int(max_k), heads, hd, dt, float(scale), dropout_p, dropout_seed,
+                                     out.data_ptr(), lse.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_of(q))
         _lib.check(rc, "esa_pma_fwd")
         ctx.save_for_backward(q, k, v, out, lse, cu_k)
-        ctx.meta = (max_k, scale)
+        ctx.meta = (max_k, scale, dropout_p, dropout_seed)
         return out
 
     @staticmethod
     def backward(ctx, g):
         q, k, v, out, lse, cu_k = ctx.saved_tensors
-        max_k, scale = ctx.meta
+        max_k, scale, dropout_p, dropout_seed = ctx.meta
         batch, k_seeds, heads, hd = cu_k.numel() - 1, q.shape[0], q.shape[1], q.shape[2]
         dt = _dtype_code(q)
         g = g.to(q.dtype).contiguous()
@@ -399,16 +429,17 @@ class _PMAAttention(torch.autograd.Function):
         ws = _pma_workspace(q.device, batch, k_seeds, k.shape[0], heads, hd, dt, True)
         rc = _lib.load().esa_pma_bwd(g.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
                                      lse.data_ptr(), cu_k.data_ptr(), batch, k_seeds, k.shape[0], int(max_k), heads,
-                                     hd, dt, float(scale), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
-                                     ws.data_ptr(), ws.numel(), _lib.stream_of(q))
+                                     hd, dt, float(scale), dropout_p, dropout_seed, dq.data_ptr(), dk.data_ptr(),
+                                     dv.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_of(q))
         _lib.check(rc, "esa_pma_bwd")
-        return dq, dk, dv, None, None, None
+        return dq, dk, dv, None, None, None, None, None
 
 
-def pma_attention(q, k, v, cu_seqlens_k, max_seqlen_k, softmax_scale=None):
+def pma_attention(q, k, v, cu_seqlens_k, max_seqlen_k, softmax_scale=None, dropout_p=0.0, dropout_seed=None):
     """Seed pooling of PMA (esa/mha.py:101-109): the k seed queries q [k, H, hd] (fc_q(S), shared by every
     set) attend over each set's keys k, v [Tk, H, hd] (sets by cu_seqlens_k [B+1], int32) -> [B * k, H, hd],
-    set-major.  Equals varlen attention with the seeds repeated per set; q's gradient sums the sets'."""
+    set-major.  Equals varlen attention with the seeds repeated per set; q's gradient sums the sets'.
+    dropout_p / dropout_seed as ``varlen_attention``'s, over the repeated seeds (query b * k + s)."""
     _lib.require_gpu(q, k, v, cu_seqlens_k)
     heads, hd = q.shape[1], q.shape[-1]
     _check_tokens("q", q)
@@ -419,7 +450,11 @@ def pma_attention(q, k, v, cu_seqlens_k, max_seqlen_k, softmax_scale=None):
     _check_index("cu_seqlens_k", cu_seqlens_k)
     if softmax_scale is None:
         softmax_scale = 1.0 / math.sqrt(q.shape[-1])
-    return _PMAAttention.apply(q, k, v, cu_seqlens_k, max_seqlen_k, float(softmax_scale))
+    dropout_p = _check_dropout(dropout_p)
+    if dropout_p > 0.0 and dropout_seed is None:
+        dropout_seed = draw_dropout_seed()
+    return _PMAAttention.apply(q, k, v, cu_seqlens_k, max_seqlen_k, float(softmax_scale), dropout_p,
+                               int(dropout_seed or 0) & _SEED_MASK)
 
 
 def edge_mask_dense(edge_src, edge_dst, cu_seqlens, max_items):

@@ -35,7 +35,7 @@ from .activations import mab_epilogue, mish
 from .attention import pma_attention, varlen_attention
 from .layer_norm import layer_norm
 from .linear import apply, qkv_projection
-from .mha import PMA, SAB, _heads, pooled_attention
+from .mha import PMA, SAB, _heads, attn_dropout, pooled_attention
 from .mha_flash_varlen import PMAFlashVarlen, SABFlashVarlen
 from .mlp_utils import GatedMLPMulti, SmallMLP
 from .norm_layers import LN
@@ -145,7 +145,7 @@ def _sab_valid_only(sab: SAB, X: torch.Tensor, tokens: PackedSets) -> torch.Tens
     h, d, n = mab.num_heads, q.shape[-1], X.shape[1]
     cu = tokens.cu_seqlens
     out = varlen_attention(_heads(tokens.unpad(q), h), _heads(tokens.unpad(k), h), _heads(tokens.unpad(v), h),
-                           cu, cu, n, n)
+                           cu, cu, n, n, dropout_p=attn_dropout(mab))
     out = tokens.pad(out.reshape(-1, d)).to(q.dtype)
     return mish(apply(mab.fc_o, out), out)
 
@@ -157,7 +157,8 @@ def _packed_mab(mab, xq: torch.Tensor, xk: torch.Tensor, cu_q: torch.Tensor, cu_
     projections and the fc_o + Mish epilogue run fused (qkv_projection, mab_epilogue)."""
     q, k, v = qkv_projection(mab.fc_q, mab.fc_k, mab.fc_v, xq, xk)
     h, d = mab.num_heads, q.shape[-1]
-    out = varlen_attention(_heads(q, h), _heads(k, h), _heads(v, h), cu_q, cu_k, max_q, max_k, **mask_kwargs)
+    out = varlen_attention(_heads(q, h), _heads(k, h), _heads(v, h), cu_q, cu_k, max_q, max_k,
+                           dropout_p=attn_dropout(mab), **mask_kwargs)
     return mab_epilogue(out.reshape(-1, d).to(q.dtype), mab.fc_o, residual)
 
 
@@ -201,7 +202,8 @@ def _pma_forward_packed(blk: "PMAComplete", X: torch.Tensor, tokens: PackedSets)
     # MAB(S.repeat(B, 1, 1), X): the seeds are projected once and shared by every set (esa_pma_*)
     q, k, v = qkv_projection(mab.fc_q, mab.fc_k, mab.fc_v, blk.pma.S.reshape(k_seeds, d), x_mm)
     h = mab.num_heads
-    o = pma_attention(_heads(q, h), _heads(k, h), _heads(v, h), tokens.cu_seqlens, tokens.max_items)
+    o = pma_attention(_heads(q, h), _heads(k, h), _heads(v, h), tokens.cu_seqlens, tokens.max_items,
+                      dropout_p=attn_dropout(mab))
     out = mab_epilogue(o.reshape(-1, d).to(q.dtype), mab.fc_o).reshape(b, k_seeds, d)
     if k_seeds == tokens.max_items:   # the reference's residual when the seed count equals N
         out = tokens.pad(X) + out

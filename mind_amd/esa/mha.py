@@ -36,6 +36,11 @@ state_dicts load.  Attention semantics by ``adj_mask``:
 
 float32 inputs run the fp32 kernels; any other dtype runs the bf16 kernels with
 fp32 softmax statistics, as the reference's bf16-mixed training does.
+
+Attention dropout: ``dropout_p`` applies to the softmax probabilities in
+training and not in eval, as ``p=self.dropout_p if self.training else 0`` at
+esa/mha.py:76,82; the kernels evaluate a hashed keep mask per (seed, head,
+query, key), the seed drawn per call from torch's CPU generator.
 """
 from __future__ import annotations
 
@@ -44,7 +49,7 @@ from torch import nn
 from torch.nn.init import xavier_normal_
 
 from .activations import mish
-from .attention import HEAD_DIMS, varlen_attention
+from .attention import HEAD_DIMS, draw_dropout_seed, varlen_attention
 from .packing import PackedSets
 
 BACKENDS = ("xformers", "torch", "flash_varlen", "hip")
@@ -61,18 +66,23 @@ def _heads(x: torch.Tensor, heads: int) -> torch.Tensor:
     return x.reshape(-1, heads, x.shape[-1] // heads).to(dt).contiguous()
 
 
-def dense_attention(q, k, v, heads):
+def attn_dropout(mab) -> float:
+    """The attention dropout a MAB applies now: its dropout_p in training, 0 in eval (esa/mha.py:76,82)."""
+    return float(mab.dropout_p) if mab.training else 0.0
+
+
+def dense_attention(q, k, v, heads, dropout_p=0.0):
     """Per-batch-element attention over all positions: q [B, Nq, D], k/v [B, Nk, D] -> [B, Nq, D]."""
     b, nq, d = q.shape
     nk = k.shape[1]
     if d % heads or d // heads not in HEAD_DIMS:
         raise ValueError(f"head_dim {d / heads:g} is not supported by the kernels {HEAD_DIMS}")
     out = varlen_attention(_heads(q, heads), _heads(k, heads), _heads(v, heads), _uniform_cu(b, nq, q.device),
-                           _uniform_cu(b, nk, q.device), nq, nk)
+                           _uniform_cu(b, nk, q.device), nq, nk, dropout_p=dropout_p)
     return out.reshape(b, nq, d)
 
 
-def masked_attention(q, k, v, heads, mask: PackedSets, packed: bool):
+def masked_attention(q, k, v, heads, mask: PackedSets, packed: bool, dropout_p=0.0):
     """Masked self-attention (edge or node mode) over [B, N, D] inputs laid out as ``mask`` says."""
     b, n, d = q.shape
     if k.shape[1] != n or n != mask.max_items or b != mask.batch_size:
@@ -80,12 +90,15 @@ def masked_attention(q, k, v, heads, mask: PackedSets, packed: bool):
     if packed:
         cu = mask.cu_seqlens
         out = varlen_attention(_heads(mask.unpad(q), heads), _heads(mask.unpad(k), heads),
-                               _heads(mask.unpad(v), heads), cu, cu, n, n, **mask.kernel_mask(padded=False))
+                               _heads(mask.unpad(v), heads), cu, cu, n, n, dropout_p=dropout_p,
+                               **mask.kernel_mask(padded=False))
         return mask.pad(out.reshape(-1, d))
     cu = _uniform_cu(b, n, q.device)
     qh, kh, vh = _heads(q, heads), _heads(k, heads), _heads(v, heads)
-    out_m, lse = varlen_attention(qh, kh, vh, cu, cu, n, n, return_lse=True, **mask.kernel_mask(padded=True))
-    out_d = varlen_attention(qh, kh, vh, cu, cu, n, n)
+    seed = draw_dropout_seed() if dropout_p > 0 else 0   # one keep mask for both calls
+    out_m, lse = varlen_attention(qh, kh, vh, cu, cu, n, n, return_lse=True, dropout_p=dropout_p, dropout_seed=seed,
+                                  **mask.kernel_mask(padded=True))
+    out_d = varlen_attention(qh, kh, vh, cu, cu, n, n, dropout_p=dropout_p, dropout_seed=seed)
     dead = torch.isneginf(lse[0]).view(-1, 1, 1)   # the mask is the same for every head
     return torch.where(dead, out_d, out_m).reshape(b, n, d)
 
@@ -125,7 +138,7 @@ def tensor_mask_csr(mask: torch.Tensor, b: int, nq: int, nk: int, heads: int) ->
     return indptr, indices
 
 
-def tensor_masked_attention(q, k, v, heads, mask: torch.Tensor):
+def tensor_masked_attention(q, k, v, heads, mask: torch.Tensor, dropout_p=0.0):
     """Attention over [B, N, D] inputs with the reference's dense mask tensor (padded semantics: a row whose
     pairs are all dropped attends to all Nk keys, as a constant -99999 bias leaves softmax unchanged)."""
     b, nq, d = q.shape
@@ -133,9 +146,10 @@ def tensor_masked_attention(q, k, v, heads, mask: torch.Tensor):
     indptr, indices = tensor_mask_csr(mask.to(q.device), b, nq, nk, heads)
     cu_q, cu_k = _uniform_cu(b, nq, q.device), _uniform_cu(b, nk, q.device)
     qh, kh, vh = _heads(q, heads), _heads(k, heads), _heads(v, heads)
+    seed = draw_dropout_seed() if dropout_p > 0 else 0   # one keep mask for both calls
     out_m, lse = varlen_attention(qh, kh, vh, cu_q, cu_k, nq, nk, return_lse=True, adj_indptr=indptr,
-                                  adj_indices=indices)
-    out_d = varlen_attention(qh, kh, vh, cu_q, cu_k, nq, nk)
+                                  adj_indices=indices, dropout_p=dropout_p, dropout_seed=seed)
+    out_d = varlen_attention(qh, kh, vh, cu_q, cu_k, nq, nk, dropout_p=dropout_p, dropout_seed=seed)
     dead = torch.isneginf(lse[0]).view(-1, 1, 1)   # one pattern for every head
     return torch.where(dead, out_d, out_m).reshape(b, nq, d)
 
@@ -163,17 +177,17 @@ class MAB(nn.Module):
     def forward(self, Q, K, adj_mask=None):
         if self.dim_V % self.num_heads:
             raise ValueError("Embedding dim is not divisible by nheads")
-        if self.training and self.dropout_p > 0:
-            raise NotImplementedError("attention dropout is not supported on the HIP path")
+        p = attn_dropout(self)
         q = self.fc_q(Q)
         v = self.fc_v(K)
         k = self.fc_k(K)
         if adj_mask is None:
-            out = dense_attention(q, k, v, self.num_heads)
+            out = dense_attention(q, k, v, self.num_heads, p)
         elif isinstance(adj_mask, PackedSets):
-            out = masked_attention(q, k, v, self.num_heads, adj_mask, packed=self.xformers_or_torch_attn == "hip")
+            out = masked_attention(q, k, v, self.num_heads, adj_mask, packed=self.xformers_or_torch_attn == "hip",
+                                   dropout_p=p)
         elif isinstance(adj_mask, torch.Tensor):
-            out = tensor_masked_attention(q, k, v, self.num_heads, adj_mask)
+            out = tensor_masked_attention(q, k, v, self.num_heads, adj_mask, p)
         else:
             raise TypeError("adj_mask must be None, an EdgeAdjacency / NodeAdjacency descriptor, or a mask tensor")
         out = out.to(q.dtype)
@@ -231,7 +245,7 @@ def pooled_attention(mab: MAB, S: torch.Tensor, X: torch.Tensor, seq_lens) -> to
     k = mab.fc_k(xk)
     h = mab.num_heads
     out = varlen_attention(_heads(q, h), _heads(k, h), _heads(v, h), _uniform_cu(b, k_seeds, X.device), cu_k,
-                           k_seeds, n)
+                           k_seeds, n, dropout_p=attn_dropout(mab))
     out = out.reshape(b, k_seeds, d).to(q.dtype)
     return mish(mab.fc_o(out), out)
 

@@ -19,7 +19,7 @@ from torch.nn.init import xavier_normal_
 
 from .activations import mish
 from .attention import varlen_attention
-from .mha import _heads, dense_attention, masked_attention, tensor_masked_attention
+from .mha import _heads, attn_dropout, dense_attention, masked_attention, tensor_masked_attention
 from .packing import PackedSets
 
 
@@ -45,8 +45,7 @@ class MABFlashVarlen(nn.Module):
         xavier_normal_(self.fc_o.weight)
 
     def forward(self, Q, K, seq_lens=None, adj_mask=None):
-        if self.training and self.dropout_p > 0:
-            raise NotImplementedError("attention dropout is not supported on the HIP path")
+        # attention dropout: dropout_p in training, 0 in eval (esa/mha_flash_varlen.py:115,181)
         if seq_lens is None:
             return self._forward_padded(Q, K, adj_mask)
         return self._forward_varlen(Q, K, seq_lens, adj_mask)
@@ -63,12 +62,13 @@ class MABFlashVarlen(nn.Module):
         q = self.fc_q(Q)
         v = self.fc_v(K)
         k = self.fc_k(K)
+        p = attn_dropout(self)
         if adj_mask is None:
-            out = dense_attention(q, k, v, self.num_heads)
+            out = dense_attention(q, k, v, self.num_heads, p)
         elif isinstance(adj_mask, PackedSets):
-            out = masked_attention(q, k, v, self.num_heads, adj_mask, packed=False)
+            out = masked_attention(q, k, v, self.num_heads, adj_mask, packed=False, dropout_p=p)
         elif isinstance(adj_mask, torch.Tensor):   # SDPA's attn_mask (esa/mha_flash_varlen.py:112-117)
-            out = tensor_masked_attention(q, k, v, self.num_heads, adj_mask)
+            out = tensor_masked_attention(q, k, v, self.num_heads, adj_mask, p)
         else:
             raise TypeError("adj_mask must be None, an EdgeAdjacency / NodeAdjacency descriptor, or a mask tensor")
         out = out.to(q.dtype)
@@ -97,7 +97,7 @@ class MABFlashVarlen(nn.Module):
         qp = _heads(q.reshape(b * n, d).index_select(0, index), h)
         kp = _heads(k.reshape(b * n, d).index_select(0, index), h)
         vp = _heads(v.reshape(b * n, d).index_select(0, index), h)
-        out_p = varlen_attention(qp, kp, vp, cu, cu, n, n).reshape(-1, d).to(q.dtype)
+        out_p = varlen_attention(qp, kp, vp, cu, cu, n, n, dropout_p=attn_dropout(self)).reshape(-1, d).to(q.dtype)
         out = q.new_zeros(b * n, d).index_copy(0, index, out_p).view(b, n, d)
         out = mish(_linear(self.fc_o, out), out)
         return out.to(input_dtype) if out.dtype != input_dtype else out

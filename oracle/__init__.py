@@ -26,6 +26,14 @@ torch_geometric and torch_scatter are absent):
       single admissible key (out = that v), -inf bias == -99999 bias.
   attention.varlen_attention_bwd
       torch.autograd through the fp64 forward and central finite differences.
+  dropout.fmix32 / keep_mask, attention with dropout=(p, seed)
+      fmix32 inside the whole MurmurHash3_x86_32 equals scikit-learn's
+      murmurhash3_32 on random keys and seeds; keep rate 1 - p within
+      binomial bounds, no correlation between neighbouring queries / keys /
+      heads or seeds; p = 0 equals the plain oracle; the forward is the
+      definition (P o Z / (1 - p)) V, its mean over seeds tends to P V; the
+      backward equals torch.autograd through a dense fp64 forward with the
+      same materialised Z.
   edges.edge_gather / csr_build / segment_sum
       bitwise copy identities; numpy stable argsort + bincount; constant rows
       give degree * value exactly; fp64 index_add agrees to rounding.

@@ -7,6 +7,10 @@ memory_efficient_attention / SDPA with the additive edge bias (esa/mha.py:76,
 is -inf here; the reference's -99999 bias gives the same probabilities
 whenever a row has an admissible key (exp(-99999 + s - max) underflows to 0).
 A row with no admissible key returns 0 and lse = -inf.
+
+``dropout=(p, seed)``: attention dropout on the probabilities, out =
+(P o Z / (1 - p)) V with the keep mask Z of oracle/dropout.py (the reference's
+training-time p, esa/mha.py:76,82); lse is that of the undropped scores.
 """
 from __future__ import annotations
 
@@ -14,7 +18,17 @@ import numpy as np
 import torch
 import torch.nn.functional as F
 
+from . import dropout as _drop
 from .mask import edge_adjacency_segment, node_adjacency_segment
+
+
+def _dropout_scale(dropout, heads, qs, qe, ks, ke, h0, h1, dtype):
+    """Z / (1 - p) as a [h1 - h0, Lq, Lk] tensor for the global query / key ranges, or None."""
+    if dropout is None or dropout[0] == 0:
+        return None
+    p, seed = dropout
+    z = _drop.keep_mask(p, seed, heads, np.arange(qs, qe), np.arange(ks, ke), h0, h1)
+    return torch.as_tensor(z).to(dtype) * _drop.params(p, seed)[3]
 
 
 def _segment_mask(edge_src, edge_dst, qs, qe, ks, ke, adj=None):
@@ -33,7 +47,8 @@ def _head_chunks(h, lq, lk, budget=1 << 26):
     return [(a, min(h, a + step)) for a in range(0, h, step)]
 
 
-def varlen_attention(q, k, v, cu_q, cu_k, scale, edge_src=None, edge_dst=None, dtype=torch.float64, adj=None):
+def varlen_attention(q, k, v, cu_q, cu_k, scale, edge_src=None, edge_dst=None, dtype=torch.float64, adj=None,
+                     dropout=None):
     """q [Tq,H,D], k/v [Tk,H,D] -> (out [Tq,H,D], lse [H,Tq]) in ``dtype``.
 
     ``edge_src`` / ``edge_dst``: edge-mode mask; ``adj`` = (indptr, indices):
@@ -64,6 +79,9 @@ def varlen_attention(q, k, v, cu_q, cu_k, scale, edge_src=None, edge_dst=None, d
             l = torch.logsumexp(s, dim=-1)                  # [h, Lq]
             # rows with no admissible key: every s is -inf; keep p = 0 without NaN
             p = torch.exp(s - torch.where(torch.isfinite(l), l, torch.zeros_like(l))[..., None])
+            zs = _dropout_scale(dropout, h, qs, qe, ks, ke, h0, h1, dtype)
+            if zs is not None:
+                p = p * zs
             ob.append(torch.matmul(p, vb).permute(1, 0, 2))
             lb.append(l)
         outs.append(torch.cat(ob, 1))
@@ -74,12 +92,14 @@ def varlen_attention(q, k, v, cu_q, cu_k, scale, edge_src=None, edge_dst=None, d
 
 
 def varlen_attention_bwd(dout, q, k, v, cu_q, cu_k, scale, edge_src=None, edge_dst=None, dtype=torch.float64,
-                         adj=None):
+                         adj=None, dropout=None):
     """Analytic gradients of ``varlen_attention``: (dq, dk, dv).
 
     With P = softmax(scale Q K^T + mask), O = P V, D = rowsum(dO * O):
     dV = P^T dO, dP = dO V^T, dS = P * (dP - D), dQ = scale dS K,
-    dK = scale dS^T Q.
+    dK = scale dS^T Q.  With dropout, W = Z / (1 - p): O = (P o W) V,
+    dV = (P o W)^T dO, dS = P * (dP o W - D) (D = rowsum(dO * O) still,
+    since sum_j P_ij W_ij dP_ij = dO_i . O_i).
     """
     dout, q, k, v = (torch.as_tensor(t).detach().cpu().to(dtype) for t in (dout, q, k, v))
     cu_q = np.asarray(cu_q, dtype=np.int64)
@@ -101,9 +121,13 @@ def varlen_attention_bwd(dout, q, k, v, cu_q, cu_k, scale, edge_src=None, edge_d
                 s = s.masked_fill(~m, float("-inf"))
             l = torch.logsumexp(s, dim=-1)
             p = torch.exp(s - torch.where(torch.isfinite(l), l, torch.zeros_like(l))[..., None])
-            o = torch.matmul(p, vb)
-            dvb = torch.matmul(p.transpose(1, 2).contiguous(), gb)
+            zs = _dropout_scale(dropout, h, qs, qe, ks, ke, h0, h1, dtype)
+            pw = p if zs is None else p * zs
+            o = torch.matmul(pw, vb)
+            dvb = torch.matmul(pw.transpose(1, 2).contiguous(), gb)
             dp = torch.matmul(gb, vb.transpose(1, 2).contiguous())
+            if zs is not None:
+                dp = dp * zs
             drow = (gb * o).sum(-1, keepdim=True)
             ds = p * (dp - drow)
             dq[qs:qe, h0:h1] = (torch.matmul(ds, kb) * scale).permute(1, 0, 2)

@@ -74,9 +74,14 @@ def test_argument_errors_need_no_gpu():
         assert lib.esa_varlen_attn_workspace_size(100, 100, 16, 16, dt, none, 0, 1, ctypes.byref(n)) == 0
         assert n.value > 0
     # fwd with a too-small workspace is rejected before anything is launched
-    rc = lib.esa_varlen_attn_fwd(16, 16, 16, 16, 16, 1, 100, 100, 100, 100, 16, 16, bf16, 0.25, none, None, None, 0,
-                                 16, 16, 256, 10, None)
+    rc = lib.esa_varlen_attn_fwd(16, 16, 16, 16, 16, 1, 100, 100, 100, 100, 16, 16, bf16, 0.25, 0.0, 0, none, None,
+                                 None, 0, 16, 16, 256, 10, None)
     assert rc == -4
+    # dropout_p outside [0, 1) is rejected before anything is launched
+    for p in (-0.1, 1.0, 1.5, float("nan")):
+        rc = lib.esa_varlen_attn_fwd(16, 16, 16, 16, 16, 1, 100, 100, 100, 100, 16, 16, bf16, 0.25, p, 7, none, None,
+                                     None, 0, 16, 16, 1 << 20, 1 << 20, None)
+        assert rc == -9, p
     assert lib.esa_edge_gather(16, 16, 16, 10, 10, 8, 7, 16, None) == -5
     assert lib.esa_csr_workspace_size(-1, 10, ctypes.byref(n)) == -2
     # node plan: size errors, and a planned backward needs only its row statistics

@@ -332,7 +332,7 @@ def test_dense_rows_after_last_segment(device):
     dq, dk, dv = torch.empty_like(qd), torch.empty_like(kd), torch.empty_like(vd)
     rc = lib.esa_varlen_attn_bwd(gd.data_ptr(), qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), out.data_ptr(),
                                  lse.data_ptr(), cud.data_ptr(), cud.data_ptr(), 2, tq, 70, 40, 40, H, D,
-                                 _lib.ESA_BF16, 0.25, _lib.ESA_MASK_NONE, None, None, 0, dq.data_ptr(), dk.data_ptr(),
+                                 _lib.ESA_BF16, 0.25, 0.0, 0, _lib.ESA_MASK_NONE, None, None, 0, dq.data_ptr(), dk.data_ptr(),
                                  dv.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_of(qd))
     _lib.check(rc, "esa_varlen_attn_bwd")
     torch.cuda.synchronize()

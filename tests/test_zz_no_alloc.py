@@ -118,5 +118,5 @@ def test_noalloc_rejects_shapes_beyond_scratch(device):
     assert n.value > cap
     # the size check comes first: with null pointers nothing can be launched
     rc = lib.esa_varlen_attn_fwd_noalloc(None, None, None, None, None, 1, tq, tq, tq, tq, H, D, _lib.ESA_BF16, 0.25,
-                                         _lib.ESA_MASK_NONE, None, None, 0, None, None, None)
+                                         0.0, 0, _lib.ESA_MASK_NONE, None, None, 0, None, None, None)
     assert rc == -8
