@@ -11,6 +11,8 @@ A row with no admissible key returns 0 and lse = -inf.
 ``dropout=(p, seed)``: attention dropout on the probabilities, out =
 (P o Z / (1 - p)) V with the keep mask Z of oracle/dropout.py (the reference's
 training-time p, esa/mha.py:76,82); lse is that of the undropped scores.
+``dropout=(p, seed, q_ids, k_ids)``: the same with the tokens' global indices
+(the mask's q and k) given per query / key row, for a subset of a batch.
 """
 from __future__ import annotations
 
@@ -22,12 +24,20 @@ from . import dropout as _drop
 from .mask import edge_adjacency_segment, node_adjacency_segment
 
 
-def _dropout_scale(dropout, heads, qs, qe, ks, ke, h0, h1, dtype):
-    """Z / (1 - p) as a [h1 - h0, Lq, Lk] tensor for the global query / key ranges, or None."""
+def _dropout_ids(dropout, tq, tk):
+    """(p, seed, global query ids [tq], global key ids [tk]) of a dropout argument."""
+    p, seed = dropout[0], dropout[1]
+    q_ids = np.arange(tq) if len(dropout) < 3 else np.asarray(dropout[2], dtype=np.int64)
+    k_ids = np.arange(tk) if len(dropout) < 4 else np.asarray(dropout[3], dtype=np.int64)
+    return p, seed, q_ids, k_ids
+
+
+def _dropout_scale(dropout, heads, qs, qe, ks, ke, h0, h1, dtype, tq=None, tk=None):
+    """Z / (1 - p) as a [h1 - h0, Lq, Lk] tensor for the query / key rows qs..qe, ks..ke, or None."""
     if dropout is None or dropout[0] == 0:
         return None
-    p, seed = dropout
-    z = _drop.keep_mask(p, seed, heads, np.arange(qs, qe), np.arange(ks, ke), h0, h1)
+    p, seed, q_ids, k_ids = _dropout_ids(dropout, max(qe, tq or 0), max(ke, tk or 0))
+    z = _drop.keep_mask(p, seed, heads, q_ids[qs:qe], k_ids[ks:ke], h0, h1)
     return torch.as_tensor(z).to(dtype) * _drop.params(p, seed)[3]
 
 
@@ -79,7 +89,7 @@ def varlen_attention(q, k, v, cu_q, cu_k, scale, edge_src=None, edge_dst=None, d
             l = torch.logsumexp(s, dim=-1)                  # [h, Lq]
             # rows with no admissible key: every s is -inf; keep p = 0 without NaN
             p = torch.exp(s - torch.where(torch.isfinite(l), l, torch.zeros_like(l))[..., None])
-            zs = _dropout_scale(dropout, h, qs, qe, ks, ke, h0, h1, dtype)
+            zs = _dropout_scale(dropout, h, qs, qe, ks, ke, h0, h1, dtype, tq, k.shape[0])
             if zs is not None:
                 p = p * zs
             ob.append(torch.matmul(p, vb).permute(1, 0, 2))
@@ -121,7 +131,7 @@ def varlen_attention_bwd(dout, q, k, v, cu_q, cu_k, scale, edge_src=None, edge_d
                 s = s.masked_fill(~m, float("-inf"))
             l = torch.logsumexp(s, dim=-1)
             p = torch.exp(s - torch.where(torch.isfinite(l), l, torch.zeros_like(l))[..., None])
-            zs = _dropout_scale(dropout, h, qs, qe, ks, ke, h0, h1, dtype)
+            zs = _dropout_scale(dropout, h, qs, qe, ks, ke, h0, h1, dtype, q.shape[0], k.shape[0])
             pw = p if zs is None else p * zs
             o = torch.matmul(pw, vb)
             dvb = torch.matmul(pw.transpose(1, 2).contiguous(), gb)
@@ -141,25 +151,28 @@ class _VarlenAttentionFn(torch.autograd.Function):
     segments; the backward recomputes the scores head chunk by head chunk)."""
 
     @staticmethod
-    def forward(ctx, q, k, v, cu_q, cu_k, scale, edge_src, edge_dst, adj):
-        out, _ = varlen_attention(q, k, v, cu_q, cu_k, scale, edge_src, edge_dst, dtype=q.dtype, adj=adj)
+    def forward(ctx, q, k, v, cu_q, cu_k, scale, edge_src, edge_dst, adj, dropout=None):
+        out, _ = varlen_attention(q, k, v, cu_q, cu_k, scale, edge_src, edge_dst, dtype=q.dtype, adj=adj,
+                                  dropout=dropout)
         ctx.save_for_backward(q, k, v)
-        ctx.meta = (cu_q, cu_k, scale, edge_src, edge_dst, adj)
+        ctx.meta = (cu_q, cu_k, scale, edge_src, edge_dst, adj, dropout)
         return out
 
     @staticmethod
     def backward(ctx, g):
         q, k, v = ctx.saved_tensors
-        cu_q, cu_k, scale, edge_src, edge_dst, adj = ctx.meta
-        dq, dk, dv = varlen_attention_bwd(g, q, k, v, cu_q, cu_k, scale, edge_src, edge_dst, dtype=q.dtype, adj=adj)
-        return dq, dk, dv, None, None, None, None, None, None
+        cu_q, cu_k, scale, edge_src, edge_dst, adj, dropout = ctx.meta
+        dq, dk, dv = varlen_attention_bwd(g, q, k, v, cu_q, cu_k, scale, edge_src, edge_dst, dtype=q.dtype, adj=adj,
+                                          dropout=dropout)
+        return dq, dk, dv, None, None, None, None, None, None, None
 
 
-def masked_attention_pairs(q, k, v, cu_q, cu_k, scale, edge_src=None, edge_dst=None, adj=None):
+def masked_attention_pairs(q, k, v, cu_q, cu_k, scale, edge_src=None, edge_dst=None, adj=None, dropout=None):
     """The masked case of ``varlen_attention`` over the admissible (query, key) pairs only, as gathers and
     scatters that torch autograd differentiates: s_ij = scale q_i . k_j per head for the mask's pairs of each
-    segment, softmax per query row (a row without pairs gives 0), out_i = sum_j p_ij v_j.  Work and memory
-    follow the mask's nonzeros, not L^2 (the protein-like edge masks are about 1 % dense)."""
+    segment, softmax per query row (a row without pairs gives 0), out_i = sum_j p_ij v_j (p_ij Z_ij / (1 - p)
+    with dropout).  Work and memory follow the mask's nonzeros, not L^2 (the protein-like edge masks are about
+    1 % dense)."""
     cu_q = np.asarray(cu_q, dtype=np.int64)
     cu_k = np.asarray(cu_k, dtype=np.int64)
     rows, cols = [], []
@@ -181,15 +194,19 @@ def masked_attention_pairs(q, k, v, cu_q, cu_k, scale, edge_src=None, edge_dst=N
     e = torch.exp(sc - mx.index_select(0, r))
     den = q.new_zeros(tq, h).index_add(0, r, e)
     p = e / den.index_select(0, r)
+    if dropout is not None and dropout[0] > 0:
+        pd, seed, q_ids, k_ids = _dropout_ids(dropout, tq, k.shape[0])
+        z = _drop.keep_pairs(pd, seed, h, q_ids[r.numpy()], k_ids[c.numpy()])              # [H, P]
+        p = p * torch.as_tensor(z.T).to(p.dtype) * _drop.params(pd, seed)[3]
     return q.new_zeros(tq, h, d).index_add(0, r, p[..., None] * v.index_select(0, c))
 
 
-def varlen_attention_diff(q, k, v, cu_q, cu_k, scale, edge_src=None, edge_dst=None, adj=None):
+def varlen_attention_diff(q, k, v, cu_q, cu_k, scale, edge_src=None, edge_dst=None, adj=None, dropout=None):
     """``varlen_attention``'s output, differentiable in q, k, v: through ``varlen_attention_bwd`` without a
     mask, through ``masked_attention_pairs`` with one."""
     if edge_src is not None or adj is not None:
-        return masked_attention_pairs(q, k, v, cu_q, cu_k, scale, edge_src, edge_dst, adj)
-    return _VarlenAttentionFn.apply(q, k, v, cu_q, cu_k, scale, edge_src, edge_dst, adj)
+        return masked_attention_pairs(q, k, v, cu_q, cu_k, scale, edge_src, edge_dst, adj, dropout)
+    return _VarlenAttentionFn.apply(q, k, v, cu_q, cu_k, scale, edge_src, edge_dst, adj, dropout)
 
 
 def padded_sdpa(q, k, v, cu_q, cu_k, n, scale, pair_bias=None, graphs_per_call=4):

@@ -83,6 +83,13 @@ def col_keys(seed: int, k_idx):
     return fmix32(s1 ^ fmix32(np.asarray(k_idx, dtype=np.int64).astype(np.uint32)))
 
 
+def keep_pairs(p: float, seed: int, heads: int, q_idx, k_idx):
+    """Bool [heads, n]: Z of the pairs (q_idx[i], k_idx[i]) (global token indices) in every head."""
+    _, _, thr, _ = params(p, seed)
+    c = col_keys(seed, k_idx)
+    return np.stack([fmix32(row_keys(seed, heads, q_idx, h) ^ c) >= thr for h in range(heads)])
+
+
 def keep_mask(p: float, seed: int, heads: int, q_idx, k_idx, head_lo: int = 0, head_hi: int | None = None):
     """Bool [head_hi - head_lo, len(q_idx), len(k_idx)]: Z for the global query / key token indices given."""
     _, _, thr, _ = params(p, seed)

@@ -67,16 +67,18 @@ def mab_padded(sd, prefix, Q, K, heads, bias=None):
     return o + mish(linear(sd, prefix + "fc_o.", o))
 
 
-def mab_packed(sd, prefix, Qp, Kp, cu_q, cu_k, heads, edge_src=None, edge_dst=None, v_from_k=False, adj=None):
+def mab_packed(sd, prefix, Qp, Kp, cu_q, cu_k, heads, edge_src=None, edge_dst=None, v_from_k=False, adj=None,
+               dropout=None):
     """MAB over packed tokens [T, D] per segment; optional edge mask or node CSR ``adj``; V = fc_v(K) or
-    fc_v(fc_k(K))."""
+    fc_v(fc_k(K)); ``dropout`` as oracle.attention's (esa/mha.py:76,82 in training)."""
     Qp, Kp = torch.as_tensor(Qp).cpu().to(DT), torch.as_tensor(Kp).cpu().to(DT)
     q = linear(sd, prefix + "fc_q.", Qp)
     k = linear(sd, prefix + "fc_k.", Kp)
     v = linear(sd, prefix + "fc_v.", k if v_from_k else Kp)
     hd = q.shape[-1] // heads
     o = varlen_attention_diff(_heads(q, heads).contiguous(), _heads(k, heads).contiguous(),
-                              _heads(v, heads).contiguous(), cu_q, cu_k, 1.0 / np.sqrt(hd), edge_src, edge_dst, adj)
+                              _heads(v, heads).contiguous(), cu_q, cu_k, 1.0 / np.sqrt(hd), edge_src, edge_dst, adj,
+                              dropout)
     o = o.reshape(Qp.shape[0], -1)
     return o + mish(linear(sd, prefix + "fc_o.", o))
 
@@ -127,7 +129,7 @@ def sab_complete(sd, prefix, X, heads, attn, num_mlp_layers=None):
     return out
 
 
-def pma_complete(sd, prefix, X, heads, num_mlp_layers=None, cu=None, max_items=None):
+def pma_complete(sd, prefix, X, heads, num_mlp_layers=None, cu=None, max_items=None, dropout=None):
     """Pre-norm PMA block (esa/masked_layers.py:574-621) -> [B, k, D].
 
     X' = LN(X) (:583); A = MAB(S.repeat(B, 1, 1), X') (esa/mha.py:108-109,
@@ -150,7 +152,8 @@ def pma_complete(sd, prefix, X, heads, num_mlp_layers=None, cu=None, max_items=N
         cu = np.asarray(cu, dtype=np.int64)
         b, n = len(cu) - 1, int(max_items)
         seeds = S.reshape(k, d).repeat(b, 1)
-        out = mab_packed(sd, prefix + "pma.mab.", seeds, xn, np.arange(b + 1) * k, cu, heads).reshape(b, k, d)
+        out = mab_packed(sd, prefix + "pma.mab.", seeds, xn, np.arange(b + 1) * k, cu, heads,
+                         dropout=dropout).reshape(b, k, d)
         graph = np.repeat(np.arange(b), np.diff(cu))
         res = to_dense_batch(xn, graph, b, n)[0] if k == n else None
     if k == n:

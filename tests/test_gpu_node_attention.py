@@ -296,8 +296,9 @@ def test_node_mask_argument_errors(device):
         A.attn_fwd(q, q, q, cu, cu, 4, 4, 0.25, edge_src=ix, edge_dst=ix, adj_indptr=ip, adj_indices=ix)
 
 
-@pytest.mark.parametrize("dm,h", [(256, 16), (512, 32), (512, 16), (512, 8), (192, 8)])
-def test_esa_node_mode_bf16_train_step(device, dm, h):
+@pytest.mark.parametrize("dm,h,drop", [(256, 16, False), (512, 32, False), (512, 16, False), (512, 8, False),
+                                       (192, 8, False), (192, 8, True)])
+def test_esa_node_mode_bf16_train_step(device, dm, h, drop, monkeypatch):
     """ESA in node mode trained bf16-mixed (fp32 parameters under torch.autocast(bfloat16),
     core/train_pretrain.py:753) on the 32 protein-like graphs of configuration 1 as node graphs (9,603 nodes,
     radius edges), layers M-S-M-S-P, MLP 2 x (2 D), through the packed entry: the masked layers run on the
@@ -311,7 +312,10 @@ def test_esa_node_mode_bf16_train_step(device, dm, h):
     (<= 3e-2) and the max-abs bar: a weight gradient sums bf16 products over D-wide rows through five
     bf16-mixed layers, and there the head-dim-16 control reaches the same errors as head dims 32 and 64
     (relative norm 0.7-2.5e-2, mean-abs 0.5-4.3e-3 of max |ref|, by parameter) while each attention call's
-    own error is the same at all three head dims (relative 2.2-2.5e-3 for out, dQ, dK, dV)."""
+    own error is the same at all three head dims (relative 2.2-2.5e-3 for out, dQ, dK, dV).
+    With ``drop`` the model trains with the rna YAML's attention dropout (sab / mab 0.08, pma 0.05,
+    pretraining_config_rna.yaml:76-78): the seeds the library draws per attention call are recorded in call
+    order and the oracle's layers take the same seeds with the two graphs' global token ids."""
     from mind_amd.esa.masked_layers import ESA
     layers = "MSMSP"
     print(f"[node-esa] D={dm} heads={h} head_dim={dm // h}", flush=True)
@@ -320,9 +324,19 @@ def test_esa_node_mode_bf16_train_step(device, dm, h):
     t = int(sizes.sum())
     n = nearest_multiple_of_8(int(sizes.max()) + 1)
     torch.manual_seed(0)
+    rates = {"sab_dropout": 0.08, "mab_dropout": 0.08, "pma_dropout": 0.05} if drop else {}
     model = ESA(num_outputs=2, dim_output=dm, dim_hidden=[dm] * len(layers), num_heads=[h] * len(layers),
                 layer_types=layers, node_or_edge="node", xformers_or_torch_attn="hip", use_mlps=True,
-                mlp_hidden_size=2 * dm, num_mlp_layers=2, mlp_type="standard")
+                mlp_hidden_size=2 * dm, num_mlp_layers=2, mlp_type="standard", **rates)
+    model.train()
+    seeds = []
+    if drop:
+        draw = A.draw_dropout_seed
+
+        def record():
+            seeds.append(draw())
+            return seeds[-1]
+        monkeypatch.setattr(A, "draw_dropout_seed", record)
     gen = torch.Generator().manual_seed(1)
     with torch.no_grad():
         for name, prm in model.named_parameters():
@@ -357,11 +371,20 @@ def test_esa_node_mode_bf16_train_step(device, dm, h):
     cu = np.array([0, sizes[sel[0]], sizes[sel[0]] + sizes[sel[1]]])
     sd = {k: v.detach().cpu().double().requires_grad_(True) for k, v in model.state_dict().items()}
     xr = x.double()[torch.as_tensor(rows)].clone().requires_grad_(True)
+    calls = iter(seeds)
+    if drop:
+        assert len(seeds) == len(layers)   # one attention call per layer
+    k_seeds = 2
+    seed_ids = np.concatenate([np.arange(b * k_seeds, (b + 1) * k_seeds) for b in sel])   # PMA queries b * k + s
+
+    def drop_of(p, q_ids):
+        return (p, next(calls), q_ids, rows) if drop else None
     g_ref, enc_ref = OMod.esa(
         sd, xr, layers, h, 2,
-        attn_m=lambda s_, p_, z: OMod.mab_packed(s_, p_, z, z, cu, cu, h, adj=adj),
-        attn_s=lambda s_, p_, z: OMod.mab_packed(s_, p_, z, z, cu, cu, h),
-        pool=lambda s_, p_, z: OMod.pma_complete(s_, p_, z, h, 2, cu=cu, max_items=n))
+        attn_m=lambda s_, p_, z: OMod.mab_packed(s_, p_, z, z, cu, cu, h, adj=adj, dropout=drop_of(0.08, rows)),
+        attn_s=lambda s_, p_, z: OMod.mab_packed(s_, p_, z, z, cu, cu, h, dropout=drop_of(0.08, rows)),
+        pool=lambda s_, p_, z: OMod.pma_complete(s_, p_, z, h, 2, cu=cu, max_items=n,
+                                                 dropout=drop_of(0.05, seed_ids)))
     ((g_ref * gg.double()).sum() + (enc_ref * ge.double()).sum()).backward()
     assert_bf16_close(g_emb.detach().float().cpu()[sel], g_ref.detach(), grad_scale(g_ref.detach()), "graph emb")
     assert_bf16_close(enc.detach().float().cpu()[torch.as_tensor(rows)], enc_ref.detach(),

@@ -150,3 +150,36 @@ def test_backward_equals_autograd_through_the_dense_forward(mask):
     dense.backward(g)
     for got, ref in ((dq, qa.grad), (dk, ka.grad), (dv, va.grad)):
         assert torch.allclose(got, ref, atol=1e-11)
+
+
+def test_pair_path_and_global_ids_agree_with_the_segment_path():
+    """masked_attention_pairs (the gathers the module oracle differentiates) with dropout equals varlen_attention
+    with dropout under a node mask; a subset of the batch given its global token ids reproduces the full batch's
+    rows (the mask hashes global indices)."""
+    p, seed, h, d = 0.3, 31337, 2, 16
+    lengths = [11, 17, 6]
+    cu = np.concatenate([[0], np.cumsum(lengths)])
+    t = int(cu[-1])
+    q, k, v, _ = _seg_inputs(8, t, t, h, d)
+    rng = np.random.default_rng(2)
+    rows = []
+    for b in range(len(lengths)):
+        s, e = int(cu[b]), int(cu[b + 1])
+        rows += [sorted(set(rng.integers(s, e, size=3).tolist())) for _ in range(s, e)]
+    indptr = np.concatenate([[0], np.cumsum([len(r) for r in rows])])
+    adj = (indptr, np.array([j for r in rows for j in r]))
+    full, _ = OA.varlen_attention(q, k, v, cu, cu, 0.4, adj=adj, dropout=(p, seed))
+    pairs = OA.masked_attention_pairs(q, k, v, cu, cu, 0.4, adj=adj, dropout=(p, seed))
+    assert torch.allclose(pairs, full, atol=1e-12)
+    # graph 1 alone, renumbered from 0, with its global ids
+    s, e = int(cu[1]), int(cu[2])
+    sub_rows = rows[s:e]
+    sub_ptr = np.concatenate([[0], np.cumsum([len(r) for r in sub_rows])])
+    sub_adj = (sub_ptr, np.array([j - s for r in sub_rows for j in r]))
+    ids = np.arange(s, e)
+    sub, _ = OA.varlen_attention(q[s:e], k[s:e], v[s:e], [0, e - s], [0, e - s], 0.4, adj=sub_adj,
+                                 dropout=(p, seed, ids, ids))
+    assert torch.allclose(sub, full[s:e], atol=1e-12)
+    sub_pairs = OA.masked_attention_pairs(q[s:e], k[s:e], v[s:e], [0, e - s], [0, e - s], 0.4, adj=sub_adj,
+                                          dropout=(p, seed, ids, ids))
+    assert torch.allclose(sub_pairs, full[s:e], atol=1e-12)
