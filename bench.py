@@ -22,6 +22,7 @@ every library launch (its step time is reported as ms_per_step_profiled).
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import os
 import sys
@@ -55,16 +56,18 @@ def parse():
                     help="graphs of the configuration-2 batch timed on the CPU for the masked baseline")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-sub", action="store_true",
-                    help="headline only: skip the masked (configuration 2), gather (configuration 3), node, block "
-                         "(configuration 0) and stack (configuration 4) sub-objects")
-    ap.add_argument("--config", choices=["varlen", "masked", "gather", "node", "block", "stack", "wide"],
+                    help="headline only: skip the masked (configuration 2), gather (configuration 3), node, wide, "
+                         "dropout, block (configuration 0) and stack (configuration 4) sub-objects")
+    ap.add_argument("--config", choices=["varlen", "masked", "gather", "node", "block", "stack", "wide", "dropout"],
                     default="varlen",
                     help="varlen: configuration 1 (default, the headline metric); masked: configuration 2 "
                          "(edge-masked MAB attention fwd+bwd); gather: configuration 3 (edge gather + CSR "
                          "segment sum, HBM-bound); node: node-mode (CSR adjacency) attention fwd+bwd on a "
                          "65,536-node batch; block: configuration 0 (fp32 ESA block forward on small "
                          "molecules); stack: configuration 4 (bf16 ESA encoder stack train step); wide: dense "
-                         "attention at head dims 64 and 32 (D = 512) on configuration 1's graphs")
+                         "attention at head dims 64 and 32 (D = 512) on configuration 1's graphs; dropout: "
+                         "step time without and with attention dropout (configuration 1 dense, rna-shaped node "
+                         "mode)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device-to-device copy three times (HBM counter calibration)")
     return ap.parse_args()
@@ -162,14 +165,21 @@ def main():
             result["masked"] = bench_masked(args, sub=True)
             result["gather"] = bench_gather(args, sub=True)
             result["node"] = bench_node(args, sub=True)
-            result["wide"] = bench_wide(args)
             result["block"] = bench_block(args, sub=True)
             result["stack"] = bench_stack(args, sub=True)
+            # the heavy wide / dropout lines last: configuration 0's launch-bound step measured 2.5x slower when
+            # it followed them in one process
+            result["wide"] = bench_wide(args)
+            result["dropout"] = bench_dropout(args)
         print(json.dumps(result), flush=True)
         return
     if args.config == "wide":
         print(json.dumps({"metric": "edge-tokens/sec through ESA attn fwd+bwd at head dims 64 / 32",
                           "value": None, "unit": "edge-tokens/s", **bench_wide(args)}), flush=True)
+        return
+    if args.config == "dropout":
+        print(json.dumps({"metric": "ESA attn fwd+bwd step time without / with attention dropout", "value": None,
+                          "unit": "ms", **bench_dropout(args)}), flush=True)
         return
     {"masked": bench_masked, "gather": bench_gather, "node": bench_node, "block": bench_block,
      "stack": bench_stack}[args.config](args)
@@ -188,13 +198,18 @@ def timed(step, steps: int, warmup: int, profile: bool = True):
 
     def region():
         ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        wall0 = time.perf_counter()
-        ev0.record()
-        for _ in range(steps):
-            step()
-        ev1.record()
-        torch.cuda.synchronize()
+        gc.collect()
+        gc.disable()   # as timeit does: no collector pauses inside the timed host loop
+        try:
+            torch.cuda.synchronize()
+            wall0 = time.perf_counter()
+            ev0.record()
+            for _ in range(steps):
+                step()
+            ev1.record()
+            torch.cuda.synchronize()
+        finally:
+            gc.enable()
         return ev0.elapsed_time(ev1) / steps, 1e3 * (time.perf_counter() - wall0) / steps
 
     for _ in range(warmup):
@@ -324,6 +339,58 @@ def bench_wide(args) -> dict:
                                        "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                                        "frac": achieved / PEAK_BF16_TFLOPS}}
         del q, k, v, go
+    return out
+
+
+def bench_dropout(args) -> dict:
+    """The cost of attention dropout (the reference's training-time p, esa/mha.py:76,82; MIND's rna YAML trains
+    with 0.08, core/pretraining_config_rna.yaml:76-78) on two workloads, each timed without and with dropout:
+    configuration 1's dense fwd+bwd at 16 heads of 16 (with dropout the MFMA kernels of esa_attn_wide.hip take
+    the call: they evaluate the keep mask per score) and node-mode fwd+bwd at the rna YAML's 8 heads of 24 over a
+    65,536-node budget batch with its node plan (the gather kernels)."""
+    import torch
+
+    from mind_amd import generators
+    from mind_amd.esa import attention
+    from mind_amd.esa.packing import NodeAdjacency
+
+    dev = torch.device("cuda", 0)
+    out = {"workload": "attention fwd+bwd without and with dropout p = 0.08 (seeded hashed keep mask)"}
+    gb = generators.protein_like(seed=args.seed)
+    t, maxlen = int(gb.cu_seqlens[-1]), gb.max_seqlen
+    cu = torch.as_tensor(gb.cu_seqlens).to(dev)
+    g = torch.Generator().manual_seed(args.seed)
+    q, k, v, go = (torch.randn(t, HEADS, HEAD_DIM, generator=g).to(torch.bfloat16).to(dev) for _ in range(4))
+    rec = {"edge_tokens": t, "heads": HEADS, "head_dim": HEAD_DIM}
+    for p in (0.0, 0.08):
+        def step():
+            o, lse = attention.attn_fwd(q, k, v, cu, cu, maxlen, maxlen, 0.25, dropout_p=p, dropout_seed=1)
+            attention.attn_bwd(go, q, k, v, o, lse, cu, cu, maxlen, maxlen, 0.25, dropout_p=p, dropout_seed=1)
+        ms, _, kern, _ = timed(step, args.steps, args.warmup)
+        rec[f"p{p:g}"] = {"ms_per_step": ms, "edge_tokens_per_s": t / (ms * 1e-3),
+                          "kernels": {n: r["avg_us"] for n, r in kern.items()}}
+    rec["slowdown"] = rec["p0.08"]["ms_per_step"] / rec["p0"]["ms_per_step"]
+    out["dense_config1"] = rec
+    del q, k, v, go
+    gn = generators.protein_budget(seed=args.seed, token_budget=65536, count="nodes")
+    na = NodeAdjacency.from_edge_index(torch.as_tensor(gn.edge_index).to(dev), torch.as_tensor(gn.batch).to(dev),
+                                       gn.num_graphs, int(gn.node_counts.max()))
+    tn = int(gn.node_counts.sum())
+    q, k, v, go = (torch.randn(tn, 8, 24, generator=g).to(torch.bfloat16).to(dev) for _ in range(4))
+    ip, ix, cun = na.indptr, na.indices, na.cu_seqlens
+    plan = attention.node_plan(ip, ix, cun)
+    rec = {"node_tokens": tn, "mask_nnz": int(ix.numel()), "heads": 8, "head_dim": 24}
+    for p in (0.0, 0.08):
+        def step():
+            o, lse = attention.attn_fwd(q, k, v, cun, cun, 0, 0, 24 ** -0.5, adj_indptr=ip, adj_indices=ix,
+                                        adj_plan=plan, dropout_p=p, dropout_seed=1)
+            attention.attn_bwd(go, q, k, v, o, lse, cun, cun, 0, 0, 24 ** -0.5, adj_indptr=ip, adj_indices=ix,
+                               adj_plan=plan, dropout_p=p, dropout_seed=1)
+        ms, _, kern, _ = timed(step, args.steps, args.warmup)
+        rec[f"p{p:g}"] = {"ms_per_step": ms, "node_tokens_per_s": tn / (ms * 1e-3),
+                          "kernels": {n: r["avg_us"] for n, r in kern.items()}}
+    rec["slowdown"] = rec["p0.08"]["ms_per_step"] / rec["p0"]["ms_per_step"]
+    out["node_rna_shape"] = rec
     return out
 
 
