@@ -339,6 +339,39 @@ def bench_wide(args) -> dict:
                                        "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                                        "frac": achieved / PEAK_BF16_TFLOPS}}
         del q, k, v, go
+    # node mode at the same widths (the qm9 / unimol / lba M layers: node mode, 8 heads of 64; coconut: 16 of 32)
+    from mind_amd.esa.packing import NodeAdjacency
+    gn = generators.protein_budget(seed=args.seed, token_budget=65536, count="nodes")
+    na = NodeAdjacency.from_edge_index(torch.as_tensor(gn.edge_index).to(dev), torch.as_tensor(gn.batch).to(dev),
+                                       gn.num_graphs, int(gn.node_counts.max()))
+    tn, ip, ix, cun = int(gn.node_counts.sum()), na.indptr, na.indices, na.cu_seqlens
+    plan = attention.node_plan(ip, ix, cun)
+    for hd in (64, 32):
+        heads = 512 // hd
+        g = torch.Generator().manual_seed(args.seed + hd)
+        q, k, v, go = (torch.randn(tn, heads, hd, generator=g).to(torch.bfloat16).to(dev) for _ in range(4))
+
+        def step():
+            o, lse = attention.attn_fwd(q, k, v, cun, cun, 0, 0, hd ** -0.5, adj_indptr=ip, adj_indices=ix,
+                                        adj_plan=plan)
+            attention.attn_bwd(go, q, k, v, o, lse, cun, cun, 0, 0, hd ** -0.5, adj_indptr=ip, adj_indices=ix,
+                               adj_plan=plan)
+
+        ms, _, kern, _ = timed(step, args.steps, args.warmup)
+        by = node_bytes(tn, int(ix.numel()), heads, hd)
+        for name, rec in kern.items():
+            if name in by:
+                rec["algorithmic_bytes"] = by[name]
+                rec["achieved_gbs"] = by[name] / (rec["avg_us"] * 1e-6) / 1e9
+        dom = max((n for n in by if n in kern), key=lambda n: kern[n]["avg_us"])
+        out[f"node_hd{hd}"] = {"workload": "node-mode attention fwd+bwd over a 65,536-node budget batch, node plan "
+                                           "prebuilt (once per batch)",
+                               "node_tokens": tn, "mask_nnz": int(ix.numel()), "heads": heads, "head_dim": hd,
+                               "ms_per_step": ms, "node_tokens_per_s": tn / (ms * 1e-3), "kernels": kern,
+                               "roofline": {"bound": "hbm", "kernel": dom, "achieved": kern[dom]["achieved_gbs"],
+                                            "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                                            "frac": kern[dom]["achieved_gbs"] / PEAK_HBM_GBS}}
+        del q, k, v, go
     return out
 
 
@@ -489,12 +522,12 @@ def cpu_baseline_masked(gb, seed: int, n_graphs: int) -> dict:
                        f"backward on {cores} threads, median of {runs} runs after 2 warm-ups")}
 
 
-def node_bytes(t: int, nnz: int, heads: int = HEADS) -> dict:
-    """Compulsory HBM bytes per launch of the node-mode kernels (bf16 [T, H, 16] tensors of T*H*32 bytes, fp32
-    [H, T] row statistics, int32 CSR): forward reads Q, K, V and writes O and the LSE; dQ reads Q, K, V, O, dO
-    and the LSE and writes dQ and D; dK/dV reads K, V, Q, dO, the LSE and D and the transposed CSR and
+def node_bytes(t: int, nnz: int, heads: int = HEADS, head_dim: int = HEAD_DIM) -> dict:
+    """Compulsory HBM bytes per launch of the node-mode kernels (bf16 [T, H, hd] tensors of T*H*hd*2 bytes,
+    fp32 [H, T] row statistics, int32 CSR): forward reads Q, K, V and writes O and the LSE; dQ reads Q, K, V, O,
+    dO and the LSE and writes dQ and D; dK/dV reads K, V, Q, dO, the LSE and D and the transposed CSR and
     writes dK and dV.  Each gathered row counted once (the rows of a graph are reused from cache)."""
-    row = t * heads * HEAD_DIM * 2
+    row = t * heads * head_dim * 2
     stat = heads * t * 4
     csr = 4 * (t + 1) + 4 * nnz
     return {"graph_attn_fwd": 4 * row + stat + csr, "graph_attn_bwd_dq": 6 * row + 2 * stat + csr,

@@ -18,10 +18,14 @@
 //
 // The work is O(partners * heads * head_dim) -- a few to a few tens of
 // partners per token -- so it is gathered per token instead of tiled for
-// MFMA: one wave per token, a power-of-two group of lanes per head with four
-// dims on each lane (head dim 16: 4 lanes, 32: 8, 64: 16; 24: 8 lanes of
-// which the last two hold zeros), scores reduced over a head's lanes by DPP
-// butterflies (identical in all of them), fp32 online softmax.
+// MFMA: one wave per token, a power-of-two group of lanes per head with N = 4
+// or 8 dims on each lane (N = 4: head dim 16 on 4 lanes, 32 on 8, 64 on 16,
+// 24 on 8 lanes of which the last two hold zeros; N = 8 halves the lanes per
+// head, so a wave covers 512 dims at once), scores reduced over a head's lanes
+// by DPP butterflies (identical in all of them), fp32 online softmax.  Every
+// pass of a wave over its heads walks the token's whole partner list, a chain
+// of dependent loads, so the launch takes N = 8 where it needs fewer passes
+// (dim 512: one pass instead of two).
 // The forward and dQ gather over the token's partners; dK / dV over the
 // queries that attend to the key (node mode: the transposed CSR, built per
 // call with the library's stable CSR sort or once per batch into a node plan;
@@ -38,26 +42,38 @@
 
 namespace {
 
-constexpr int kGU = 2;   // partners per step: their K / V (or Q / dO) rows are loaded together (two
-                         // per step keeps every kernel at 8 waves per SIMD; 1, 4 and 8 measured slower)
+// Partners per step: their K / V (or Q / dO) rows are loaded together.  Two
+// at 4 dims per lane keeps every kernel at 8 waves per SIMD (1, 4 and 8
+// measured slower).  At 8 dims per lane (dim 512): two for the forward and dQ
+// (8 and 7 waves per SIMD; one measured 9 % and 2 % slower), one for dK / dV
+// (66 VGPRs, 7 waves; two, at 85 VGPRs and 5 waves, measured 3 % slower).
+template <int N, bool KEY_SIDE> constexpr int partners_per_step() { return N == 8 && KEY_SIDE ? 1 : 2; }
 
 template <typename T> struct Row4;
 template <> struct Row4<float> { typedef f32x4 type; };
 template <> struct Row4<bf16> { typedef bf16x4 type; };
 
-// Four consecutive values of a [T][H][head_dim] row: this lane's dims of one head.
-template <typename T>
-DEVI void load4(const T* __restrict__ p, float v[4]) {
-  const typename Row4<T>::type x = *reinterpret_cast<const typename Row4<T>::type*>(p);
+// N (4 or 8) consecutive values of a [T][H][head_dim] row: this lane's dims
+// of one head, as 16-byte (or, fp32 at N = 4, one 16-byte; bf16 at N = 4, one
+// 8-byte) loads and stores.
+template <typename T, int N>
+DEVI void load_dims(const T* __restrict__ p, float v[N]) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) v[i] = (float)x[i];
+  for (int c = 0; c < N / 4; ++c) {
+    const typename Row4<T>::type x = reinterpret_cast<const typename Row4<T>::type*>(p)[c];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[4 * c + i] = (float)x[i];
+  }
 }
-template <typename T>
-DEVI void store4(T* __restrict__ p, const float v[4], float mul) {
-  typename Row4<T>::type x;
+template <typename T, int N>
+DEVI void store_dims(T* __restrict__ p, const float v[N], float mul) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) x[i] = (T)(v[i] * mul);
-  *reinterpret_cast<typename Row4<T>::type*>(p) = x;
+  for (int c = 0; c < N / 4; ++c) {
+    typename Row4<T>::type x;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = (T)(v[4 * c + i] * mul);
+    reinterpret_cast<typename Row4<T>::type*>(p)[c] = x;
+  }
 }
 
 template <int CTRL>
@@ -65,37 +81,42 @@ DEVI float dpp(float x) {
   return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
 }
 
-// Sum over the L lanes of a head (aligned groups of 4, 8 or 16 lanes):
+// Sum over the L lanes of a head (aligned groups of 2, 4, 8 or 16 lanes):
 // butterflies within each quad ([1,0,3,2], [2,3,0,1]), then the other quad of
 // each half row (row_half_mirror) and the other half of each row (row_mirror).  Addition is commutative, so every lane of the group
 // holds the identical result.
 template <int L>
 DEVI float head_sum(float x) {
   x += dpp<0xB1>(x);
-  x += dpp<0x4E>(x);
+  if (L >= 4) x += dpp<0x4E>(x);
   if (L >= 8) x += dpp<0x141>(x);
   if (L >= 16) x += dpp<0x140>(x);
   return x;
 }
-DEVI float dot4(const float a[4], const float b[4]) {
-  return fmaf(a[3], b[3], fmaf(a[2], b[2], fmaf(a[1], b[1], a[0] * b[0])));
+template <int N>
+DEVI float dotn(const float a[N], const float b[N]) {
+  float s = a[0] * b[0];
+#pragma unroll
+  for (int i = 1; i < N; ++i) s = fmaf(a[i], b[i], s);
+  return s;
 }
 
-// Lanes of one head: HD / 4 of them carry four dims each, rounded up to a
-// power of two (head dim 24: 6 of 8).  A lane past the head's dims reads the
+// Lanes of one head: HD / N of them carry N dims each, rounded up to a power
+// of two (head dim 24, N = 4: 6 of 8).  A lane past the head's dims reads the
 // last dims (an in-row address), zeroes its own token's operand so that its
 // terms of every dot product are 0, and stores nothing.
-template <int HD>
+template <int HD, int N>
 struct HeadLanes {
-  static constexpr int L = HD == 24 ? 8 : HD / 4;
+  static_assert(N == 4 || (N == 8 && HD % 16 == 0), "8 dims per lane need a head dim of 16, 32 or 64");
+  static constexpr int L = HD == 24 ? 8 : HD / N;
   static constexpr int HPP = 64 / L;   // heads per pass of a wave
   int li, d0;
   bool dims;
-  DEVI HeadLanes(int lane) : li(lane % L), d0(4 * min(lane % L, HD / 4 - 1)), dims(lane % L < HD / 4) {}
-  DEVI void own(float v[4]) const {
-    if (HD / 4 == L) return;
+  DEVI HeadLanes(int lane) : li(lane % L), d0(N * min(lane % L, HD / N - 1)), dims(lane % L < HD / N) {}
+  DEVI void own(float v[N]) const {
+    if (HD / N == L) return;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = dims ? v[i] : 0.f;
+    for (int i = 0; i < N; ++i) v[i] = dims ? v[i] : 0.f;
   }
 };
 
@@ -162,25 +183,26 @@ DEVI int wave_token() {
   return b * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 }
 
-// ---- partner sources: next(j, ok) yields the next kGU partners of the wave's
-// token (j a valid row index even where !ok), false once exhausted.  All
+// ---- partner sources: next<G>(j, ok) yields the next G partners of the
+// wave's token (j a valid row index even where !ok), false once exhausted.  All
 // state is wave-uniform; a copy restarts the walk (one per head pass).
 
 // A CSR row [p, pb): entries in [lo, hi), each once (an entry equal to its
 // predecessor is a repeat).
 struct CsrSrc {
   const int* list; int p, pb, lo, hi, prev;
-  DEVI bool next(int j[kGU], bool ok[kGU]) {
+  template <int G>
+  DEVI bool next(int (&j)[G], bool (&ok)[G]) {
     if (p >= pb) return false;
 #pragma unroll
-    for (int u = 0; u < kGU; ++u) {
+    for (int u = 0; u < G; ++u) {
       const int pp = min(p + u, pb - 1);
       const int x = list[pp];
       ok[u] = p + u < pb && x >= lo && x < hi && x != prev;
       if (p + u < pb) prev = x;
       j[u] = ok[u] ? x : lo;
     }
-    p += kGU;
+    p += G;
     return true;
   }
 };
@@ -190,10 +212,11 @@ struct CsrSrc {
 // c of the token's mask bits is held by lane c (at most kListCap / 32 words).
 struct ListSrc {
   const int* ids; uint32_t words; int nct, c; uint32_t w; int fallback;
-  DEVI bool next(int j[kGU], bool ok[kGU]) {
+  template <int G>
+  DEVI bool next(int (&j)[G], bool (&ok)[G]) {
     bool any = false;
 #pragma unroll
-    for (int u = 0; u < kGU; ++u) {
+    for (int u = 0; u < G; ++u) {
       while (w == 0u && c + 1 < nct) {
         ++c;
         w = (uint32_t)__builtin_amdgcn_readlane((int)words, c);
@@ -225,11 +248,12 @@ DEVI ListSrc list_src(const GraphEdgeLists& e, int d, int t, int n) {
 // t, that share an endpoint with t, 64 candidates per ballot.
 struct WalkSrc {
   const int2* nodes; int2 own; int t, base, hi, cur; uint64_t mask;
-  DEVI bool next(int j[kGU], bool ok[kGU]) {
+  template <int G>
+  DEVI bool next(int (&j)[G], bool (&ok)[G]) {
     const int lane = threadIdx.x & 63;
     bool any = false;
 #pragma unroll
-    for (int u = 0; u < kGU; ++u) {
+    for (int u = 0; u < G; ++u) {
       while (mask == 0 && base < hi) {
         const int p = base + lane;
         bool keep = false;
@@ -264,58 +288,60 @@ DEVI WalkSrc walk_src(const GraphEdgeLists& e, int2 bounds, int t) {
   return s;
 }
 
-template <typename T, int HD, bool DROP, class Src>
+template <typename T, int HD, int N, bool DROP, class Src>
 DEVI void fwd_token(const GraphAttnArgs& a, int t, const Src& src0) {
-  constexpr int L = HeadLanes<HD>::L, HPP = HeadLanes<HD>::HPP;
+  constexpr int L = HeadLanes<HD, N>::L, HPP = HeadLanes<HD, N>::HPP, G = partners_per_step<N, false>();
   const T* __restrict__ q = static_cast<const T*>(a.q);
   const T* __restrict__ k = static_cast<const T*>(a.k);
   const T* __restrict__ v = static_cast<const T*>(a.v);
   const int lane = threadIdx.x & 63, H = a.heads;
-  const HeadLanes<HD> hl(lane);
+  const HeadLanes<HD, N> hl(lane);
   const int d0 = hl.d0;
   for (int h0 = 0; h0 < H; h0 += HPP) {
     const int h = h0 + lane / L;
     const int hc = min(h, H - 1);
-    float qv[4], acc[4] = {0.f, 0.f, 0.f, 0.f};
-    load4<T>(q + ((size_t)t * H + hc) * HD + d0, qv);
+    float qv[N], acc[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) acc[i] = 0.f;
+    load_dims<T, N>(q + ((size_t)t * H + hc) * HD + d0, qv);
     hl.own(qv);
     const uint32_t rk = DROP ? drop_row(a.drop, t, hc) : 0u;
     float m = -INFINITY, l = 0.f;
     Src src = src0;
-    int j[kGU];
-    bool ok[kGU];
-    while (src.next(j, ok)) {
-      float kr[kGU][4], vr[kGU][4];
+    int j[G];
+    bool ok[G];
+    while (src.template next<G>(j, ok)) {
+      float kr[G][N], vr[G][N];
 #pragma unroll
-      for (int u = 0; u < kGU; ++u) {
-        load4<T>(k + ((size_t)j[u] * H + hc) * HD + d0, kr[u]);
-        load4<T>(v + ((size_t)j[u] * H + hc) * HD + d0, vr[u]);
+      for (int u = 0; u < G; ++u) {
+        load_dims<T, N>(k + ((size_t)j[u] * H + hc) * HD + d0, kr[u]);
+        load_dims<T, N>(v + ((size_t)j[u] * H + hc) * HD + d0, vr[u]);
       }
-      float s[kGU];
+      float s[G];
       float mt = m;
 #pragma unroll
-      for (int u = 0; u < kGU; ++u) {
-        s[u] = ok[u] ? head_sum<L>(dot4(qv, kr[u])) * a.c : -INFINITY;
+      for (int u = 0; u < G; ++u) {
+        s[u] = ok[u] ? head_sum<L>(dotn<N>(qv, kr[u])) * a.c : -INFINITY;
         mt = fmaxf(mt, s[u]);
       }
       if (mt == -INFINITY) continue;   // nothing admissible yet (uniform per head)
       const float alpha = ex2<T>(m - mt);   // 0 while m = -inf
       l *= alpha;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i] *= alpha;
+      for (int i = 0; i < N; ++i) acc[i] *= alpha;
 #pragma unroll
-      for (int u = 0; u < kGU; ++u) {
+      for (int u = 0; u < G; ++u) {
         const float pu = ex2<T>(s[u] - mt);
         l += pu;
         const float pv = !DROP || drop_keep(a.drop, rk, drop_col(a.drop, j[u])) ? pu : 0.f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[i] = fmaf(pv, vr[u][i], acc[i]);
+        for (int i = 0; i < N; ++i) acc[i] = fmaf(pv, vr[u][i], acc[i]);
       }
       m = mt;
     }
     if (h < H) {
       if (hl.dims)
-        store4<T>(static_cast<T*>(a.out) + ((size_t)t * H + h) * HD + d0, acc,
+        store_dims<T, N>(static_cast<T*>(a.out) + ((size_t)t * H + h) * HD + d0, acc,
                   l > 0.f ? (DROP ? a.drop.inv_keep : 1.f) / l : 0.f);
       if (hl.li == 0) a.lse[(size_t)h * a.total_q + t] = l > 0.f ? (m + lg2<T>(l)) * kLn2 : -INFINITY;
     }
@@ -324,108 +350,112 @@ DEVI void fwd_token(const GraphAttnArgs& a, int t, const Src& src0) {
 
 // dQ_i = scale * sum_j P_ij (dP_ij - D_i) k_j over i's partners; also writes
 // D_i = rowsum(dO_i * O_i) per head for the dK / dV pass.
-template <typename T, int HD, bool DROP, class Src>
+template <typename T, int HD, int N, bool DROP, class Src>
 DEVI void dq_token(const GraphAttnArgs& a, int t, const Src& src0) {
-  constexpr int L = HeadLanes<HD>::L, HPP = HeadLanes<HD>::HPP;
+  constexpr int L = HeadLanes<HD, N>::L, HPP = HeadLanes<HD, N>::HPP, G = partners_per_step<N, false>();
   const T* __restrict__ q = static_cast<const T*>(a.q);
   const T* __restrict__ k = static_cast<const T*>(a.k);
   const T* __restrict__ v = static_cast<const T*>(a.v);
   const T* __restrict__ o = static_cast<const T*>(a.out_in);
   const T* __restrict__ g = static_cast<const T*>(a.dout);
   const int lane = threadIdx.x & 63, H = a.heads;
-  const HeadLanes<HD> hl(lane);
+  const HeadLanes<HD, N> hl(lane);
   const int d0 = hl.d0;
   for (int h0 = 0; h0 < H; h0 += HPP) {
     const int h = h0 + lane / L;
     const int hc = min(h, H - 1);
     const size_t row = ((size_t)t * H + hc) * HD + d0;
-    float qv[4], gv[4], ov[4], acc[4] = {0.f, 0.f, 0.f, 0.f};
-    load4<T>(q + row, qv);
-    load4<T>(g + row, gv);
-    load4<T>(o + row, ov);
+    float qv[N], gv[N], ov[N], acc[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) acc[i] = 0.f;
+    load_dims<T, N>(q + row, qv);
+    load_dims<T, N>(g + row, gv);
+    load_dims<T, N>(o + row, ov);
     hl.own(qv);
     hl.own(gv);
-    const float dsum = head_sum<L>(dot4(gv, ov));
+    const float dsum = head_sum<L>(dotn<N>(gv, ov));
     const uint32_t rk = DROP ? drop_row(a.drop, t, hc) : 0u;
     const float l = a.lse_in[(size_t)hc * a.total_q + t];
     const float l2 = l == -INFINITY ? INFINITY : l * kLog2e;
     if (h < H && hl.li == 0) a.dsum[(size_t)h * a.total_q + t] = dsum;
     Src src = src0;
-    int j[kGU];
-    bool ok[kGU];
-    while (src.next(j, ok)) {
-      float kr[kGU][4], vr[kGU][4];
+    int j[G];
+    bool ok[G];
+    while (src.template next<G>(j, ok)) {
+      float kr[G][N], vr[G][N];
 #pragma unroll
-      for (int u = 0; u < kGU; ++u) {
-        load4<T>(k + ((size_t)j[u] * H + hc) * HD + d0, kr[u]);
-        load4<T>(v + ((size_t)j[u] * H + hc) * HD + d0, vr[u]);
+      for (int u = 0; u < G; ++u) {
+        load_dims<T, N>(k + ((size_t)j[u] * H + hc) * HD + d0, kr[u]);
+        load_dims<T, N>(v + ((size_t)j[u] * H + hc) * HD + d0, vr[u]);
       }
 #pragma unroll
-      for (int u = 0; u < kGU; ++u) {
-        const float pu = ok[u] ? ex2<T>(fmaf(head_sum<L>(dot4(qv, kr[u])), a.c, -l2)) : 0.f;
-        float dp = head_sum<L>(dot4(gv, vr[u]));
+      for (int u = 0; u < G; ++u) {
+        const float pu = ok[u] ? ex2<T>(fmaf(head_sum<L>(dotn<N>(qv, kr[u])), a.c, -l2)) : 0.f;
+        float dp = head_sum<L>(dotn<N>(gv, vr[u]));
         if (DROP) dp = drop_keep(a.drop, rk, drop_col(a.drop, j[u])) ? dp * a.drop.inv_keep : 0.f;
         const float ds = pu * (dp - dsum);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[i] = fmaf(ds, kr[u][i], acc[i]);
+        for (int i = 0; i < N; ++i) acc[i] = fmaf(ds, kr[u][i], acc[i]);
       }
     }
-    if (h < H && hl.dims) store4<T>(static_cast<T*>(a.dq) + ((size_t)t * H + h) * HD + d0, acc, a.scale);
+    if (h < H && hl.dims) store_dims<T, N>(static_cast<T*>(a.dq) + ((size_t)t * H + h) * HD + d0, acc, a.scale);
   }
 }
 
 // dV_j = sum_i P_ij dO_i, dK_j = scale * sum_i P_ij (dP_ij - D_i) q_i over the
 // queries i that attend to key j (ascending).
-template <typename T, int HD, bool DROP, class Src>
+template <typename T, int HD, int N, bool DROP, class Src>
 DEVI void dkdv_token(const GraphAttnArgs& a, int t, const Src& src0) {
-  constexpr int L = HeadLanes<HD>::L, HPP = HeadLanes<HD>::HPP;
+  constexpr int L = HeadLanes<HD, N>::L, HPP = HeadLanes<HD, N>::HPP, G = partners_per_step<N, true>();
   const T* __restrict__ q = static_cast<const T*>(a.q);
   const T* __restrict__ k = static_cast<const T*>(a.k);
   const T* __restrict__ v = static_cast<const T*>(a.v);
   const T* __restrict__ g = static_cast<const T*>(a.dout);
   const int lane = threadIdx.x & 63, H = a.heads;
-  const HeadLanes<HD> hl(lane);
+  const HeadLanes<HD, N> hl(lane);
   const int d0 = hl.d0;
   for (int h0 = 0; h0 < H; h0 += HPP) {
     const int h = h0 + lane / L;
     const int hc = min(h, H - 1);
     const size_t row = ((size_t)t * H + hc) * HD + d0;
-    float kv[4], vv[4], dk[4] = {0.f, 0.f, 0.f, 0.f}, dv[4] = {0.f, 0.f, 0.f, 0.f};
-    load4<T>(k + row, kv);
-    load4<T>(v + row, vv);
+    float kv[N], vv[N], dk[N], dv[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) dk[i] = dv[i] = 0.f;
+    load_dims<T, N>(k + row, kv);
+    load_dims<T, N>(v + row, vv);
     hl.own(kv);
     hl.own(vv);
     const uint32_t ck = DROP ? drop_col(a.drop, t) : 0u;
     Src src = src0;
-    int i[kGU];
-    bool ok[kGU];
-    while (src.next(i, ok)) {
-      float qr[kGU][4], gr[kGU][4], l2[kGU], ds_[kGU];
+    int i[G];
+    bool ok[G];
+    while (src.template next<G>(i, ok)) {
+      float qr[G][N], gr[G][N], l2[G], ds_[G];
 #pragma unroll
-      for (int u = 0; u < kGU; ++u) {
+      for (int u = 0; u < G; ++u) {
         const size_t r = ((size_t)i[u] * H + hc) * HD + d0;
-        load4<T>(q + r, qr[u]);
-        load4<T>(g + r, gr[u]);
+        load_dims<T, N>(q + r, qr[u]);
+        load_dims<T, N>(g + r, gr[u]);
         l2[u] = a.lse_in[(size_t)hc * a.total_q + i[u]] * kLog2e;
         ds_[u] = a.dsum[(size_t)hc * a.total_q + i[u]];
       }
 #pragma unroll
-      for (int u = 0; u < kGU; ++u) {
-        const float pu = ok[u] ? ex2<T>(fmaf(head_sum<L>(dot4(qr[u], kv)), a.c, -l2[u])) : 0.f;
-        float dp = head_sum<L>(dot4(gr[u], vv)), pv = pu;
+      for (int u = 0; u < G; ++u) {
+        const float pu = ok[u] ? ex2<T>(fmaf(head_sum<L>(dotn<N>(qr[u], kv)), a.c, -l2[u])) : 0.f;
+        float dp = head_sum<L>(dotn<N>(gr[u], vv)), pv = pu;
         if (DROP && !drop_keep(a.drop, drop_row(a.drop, i[u], hc), ck)) dp = pv = 0.f;
         if (DROP) dp *= a.drop.inv_keep;
         const float ds = pu * (dp - ds_[u]);
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
+        for (int c = 0; c < N; ++c) {
           dv[c] = fmaf(pv, gr[u][c], dv[c]);
           dk[c] = fmaf(ds, qr[u][c], dk[c]);
         }
       }
     }
     if (h < H && hl.dims) {
-      store4<T>(static_cast<T*>(a.dk) + ((size_t)t * H + h) * HD + d0, dk, a.scale);
-      store4<T>(static_cast<T*>(a.dv) + ((size_t)t * H + h) * HD + d0, dv, DROP ? a.drop.inv_keep : 1.f);
+      store_dims<T, N>(static_cast<T*>(a.dk) + ((size_t)t * H + h) * HD + d0, dk, a.scale);
+      store_dims<T, N>(static_cast<T*>(a.dv) + ((size_t)t * H + h) * HD + d0, dv, DROP ? a.drop.inv_keep : 1.f);
     }
   }
 }
@@ -433,54 +463,54 @@ DEVI void dkdv_token(const GraphAttnArgs& a, int t, const Src& src0) {
 DEVI CsrSrc csr_src(const int* list, int4 d) { return CsrSrc{list, d.z, d.w, d.x, d.y, INT_MIN}; }
 
 // The kernels: node mode over a CSR (the key pass over the transposed CSR).
-template <typename T, int HD, bool DROP>
+template <typename T, int HD, int N, bool DROP>
 __global__ __launch_bounds__(256) void graph_attn_fwd_kernel(const GraphAttnArgs a) {
   const int t = wave_token();
   if (t >= a.total_q) return;
-  fwd_token<T, HD, DROP>(a, t, csr_src(a.indices, token_desc(a.q_desc, a.cu_q, a.cu_k, a.nseg, a.total_k, a.indptr, a.nnz, t)));
+  fwd_token<T, HD, N, DROP>(a, t, csr_src(a.indices, token_desc(a.q_desc, a.cu_q, a.cu_k, a.nseg, a.total_k, a.indptr, a.nnz, t)));
 }
-template <typename T, int HD, bool DROP>
+template <typename T, int HD, int N, bool DROP>
 __global__ __launch_bounds__(256) void graph_attn_dq_kernel(const GraphAttnArgs a) {
   const int t = wave_token();
   if (t >= a.total_q) return;
-  dq_token<T, HD, DROP>(a, t, csr_src(a.indices, token_desc(a.q_desc, a.cu_q, a.cu_k, a.nseg, a.total_k, a.indptr, a.nnz, t)));
+  dq_token<T, HD, N, DROP>(a, t, csr_src(a.indices, token_desc(a.q_desc, a.cu_q, a.cu_k, a.nseg, a.total_k, a.indptr, a.nnz, t)));
 }
-template <typename T, int HD, bool DROP>
+template <typename T, int HD, int N, bool DROP>
 __global__ __launch_bounds__(256) void graph_attn_dkdv_kernel(const GraphAttnArgs a) {
   const int t = wave_token();
   if (t >= a.total_k) return;
-  dkdv_token<T, HD, DROP>(a, t, csr_src(a.t_rows, token_desc(a.k_desc, a.cu_k, a.cu_q, a.nseg, a.total_q, a.t_indptr, a.nnz, t)));
+  dkdv_token<T, HD, N, DROP>(a, t, csr_src(a.t_rows, token_desc(a.k_desc, a.cu_k, a.cu_q, a.nseg, a.total_q, a.t_indptr, a.nnz, t)));
 }
 
 // Edge mask over a plan's lists: the query side reads direction 0, the key
 // side direction 1, or direction 0 when the plan is symmetric.
-template <typename T, int HD, bool DROP, int PASS>   // 0 forward, 1 dQ, 2 dK / dV
+template <typename T, int HD, int N, bool DROP, int PASS>   // 0 forward, 1 dQ, 2 dK / dV
 DEVI void graph_edge_pass(const GraphAttnArgs& a) {
   const int t = wave_token();
   if (t >= (PASS == 2 ? a.total_k : a.total_q)) return;
   const int d = (PASS == 2 && a.edge.sym[0] == 0) ? 1 : 0;
   const int n = a.edge.info[d][t >> 5];
   auto run = [&](const auto& src) {
-    if (PASS == 0) fwd_token<T, HD, DROP>(a, t, src);
-    if (PASS == 1) dq_token<T, HD, DROP>(a, t, src);
-    if (PASS == 2) dkdv_token<T, HD, DROP>(a, t, src);
+    if (PASS == 0) fwd_token<T, HD, N, DROP>(a, t, src);
+    if (PASS == 1) dq_token<T, HD, N, DROP>(a, t, src);
+    if (PASS == 2) dkdv_token<T, HD, N, DROP>(a, t, src);
   };
   if (n >= 0)
     run(list_src(a.edge, d, t, n));
   else
     run(walk_src(a.edge, (PASS == 2 ? a.k_bounds : a.q_bounds)[t], t));
 }
-template <typename T, int HD, bool DROP>
+template <typename T, int HD, int N, bool DROP>
 __global__ __launch_bounds__(256) void graph_edge_fwd_kernel(const GraphAttnArgs a) {
-  graph_edge_pass<T, HD, DROP, 0>(a);
+  graph_edge_pass<T, HD, N, DROP, 0>(a);
 }
-template <typename T, int HD, bool DROP>
+template <typename T, int HD, int N, bool DROP>
 __global__ __launch_bounds__(256) void graph_edge_dq_kernel(const GraphAttnArgs a) {
-  graph_edge_pass<T, HD, DROP, 1>(a);
+  graph_edge_pass<T, HD, N, DROP, 1>(a);
 }
-template <typename T, int HD, bool DROP>
+template <typename T, int HD, int N, bool DROP>
 __global__ __launch_bounds__(256) void graph_edge_dkdv_kernel(const GraphAttnArgs a) {
-  graph_edge_pass<T, HD, DROP, 2>(a);
+  graph_edge_pass<T, HD, N, DROP, 2>(a);
 }
 
 // row_of[e] = the CSR row holding entry e (-1 for an entry no row covers).
@@ -637,22 +667,38 @@ int graph_node_plan_build(const int* indptr, const int* indices, const int* cu_q
 
 namespace {
 
-// Launches KERNEL<T, HD, DROP> for the call's dtype, head dim and dropout.
-#define ESA_GRAPH_LAUNCH_HD(KERNEL, T, D, hd, grid, st, a)                                        \
+// Dims per lane: 8 where a wave then needs fewer passes over the heads than
+// with 4 (never at head dim 24).
+int dims_per_lane(int heads, int head_dim) {
+  if (head_dim == 24) return 4;
+  auto passes = [&](int n) { const int hpp = 64 / (head_dim / n); return (heads + hpp - 1) / hpp; };
+  return passes(8) < passes(4) ? 8 : 4;
+}
+
+// Launches KERNEL<T, HD, N, DROP> for the call's dtype, head dim, dims per
+// lane and dropout.
+#define ESA_GRAPH_LAUNCH_N(KERNEL, T, D, hd, n, grid, st, a)                                      \
   do {                                                                                            \
-    if (hd == 16) hipLaunchKernelGGL((KERNEL<T, 16, D>), grid, dim3(256), 0, st, a);              \
-    else if (hd == 24) hipLaunchKernelGGL((KERNEL<T, 24, D>), grid, dim3(256), 0, st, a);         \
-    else if (hd == 32) hipLaunchKernelGGL((KERNEL<T, 32, D>), grid, dim3(256), 0, st, a);         \
-    else hipLaunchKernelGGL((KERNEL<T, 64, D>), grid, dim3(256), 0, st, a);                       \
+    if (n == 8) {                                                                                 \
+      if (hd == 16) hipLaunchKernelGGL((KERNEL<T, 16, 8, D>), grid, dim3(256), 0, st, a);         \
+      else if (hd == 32) hipLaunchKernelGGL((KERNEL<T, 32, 8, D>), grid, dim3(256), 0, st, a);    \
+      else hipLaunchKernelGGL((KERNEL<T, 64, 8, D>), grid, dim3(256), 0, st, a);                  \
+    } else {                                                                                      \
+      if (hd == 16) hipLaunchKernelGGL((KERNEL<T, 16, 4, D>), grid, dim3(256), 0, st, a);         \
+      else if (hd == 24) hipLaunchKernelGGL((KERNEL<T, 24, 4, D>), grid, dim3(256), 0, st, a);    \
+      else if (hd == 32) hipLaunchKernelGGL((KERNEL<T, 32, 4, D>), grid, dim3(256), 0, st, a);    \
+      else hipLaunchKernelGGL((KERNEL<T, 64, 4, D>), grid, dim3(256), 0, st, a);                  \
+    }                                                                                             \
   } while (0)
 #define ESA_GRAPH_LAUNCH(KERNEL, dtype, hd, grid, st, a)                                          \
   do {                                                                                            \
+    const int n_ = dims_per_lane(a.heads, hd);                                                    \
     if (dtype == ESA_F32) {                                                                       \
-      if (a.dropout) ESA_GRAPH_LAUNCH_HD(KERNEL, float, true, hd, grid, st, a);                   \
-      else ESA_GRAPH_LAUNCH_HD(KERNEL, float, false, hd, grid, st, a);                            \
+      if (a.dropout) ESA_GRAPH_LAUNCH_N(KERNEL, float, true, hd, n_, grid, st, a);                \
+      else ESA_GRAPH_LAUNCH_N(KERNEL, float, false, hd, n_, grid, st, a);                         \
     } else {                                                                                      \
-      if (a.dropout) ESA_GRAPH_LAUNCH_HD(KERNEL, bf16, true, hd, grid, st, a);                    \
-      else ESA_GRAPH_LAUNCH_HD(KERNEL, bf16, false, hd, grid, st, a);                             \
+      if (a.dropout) ESA_GRAPH_LAUNCH_N(KERNEL, bf16, true, hd, n_, grid, st, a);                 \
+      else ESA_GRAPH_LAUNCH_N(KERNEL, bf16, false, hd, n_, grid, st, a);                          \
     }                                                                                             \
   } while (0)
 
