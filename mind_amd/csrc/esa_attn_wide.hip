@@ -35,7 +35,13 @@
 //    the two octets of a transpose read fall in different banks.
 // The softmax scale c = scale * log2(e) is applied inside the exponent (one
 // FMA per score, exp2(c s - c m)); the backward's -LSE2 / c and -D row
-// statistics are MFMA accumulator seeds.  Every sum has a fixed order: the
+// statistics are MFMA accumulator seeds.  Forward reference point: by
+// Cauchy-Schwarz c |s| <= c |q| max|k|; when that bound is <= 60 for all of a
+// wave's queries over their partner range (max |k| per 32-key tile from the
+// prep pass), exp2(c s) stays in [2^-60, 2^60] and the wave skips the running
+// maximum and its rescales; otherwise the online path runs.  The row sum adds
+// the bf16 probabilities the P V products take (v_dot2c_f32_bf16), so the
+// normalisation matches the products exactly (a one-key row gives out = v).  Every sum has a fixed order: the
 // backward is deterministic (dQ pass, then dK/dV pass; no atomics).
 #include "esa_attn_tiles.h"
 #include "esa_attn_dense.h"
@@ -49,6 +55,7 @@ constexpr int kWTokPad = kWStage + 4;    // LDS octet stride in tokens
 
 struct WideArgs {
   DropoutCfg drop;
+  const float* knorm; int tk_tiles;   // forward: max |k| per (head, 32-key tile), [H][tk_tiles]
   const bf16* q; const bf16* k; const bf16* v; const bf16* out; const bf16* dout;
   const float* lse;            // dQ pass input [H][Tq]
   float2* aux;                 // per (head, query) {-LSE2 / c, -D}, [H][tq_pad]: written by dQ, read by dK/dV
@@ -98,6 +105,15 @@ template <int HD>
 DEVI bf16x8 row_op(const bf16* __restrict__ row, int o) {
   if (8 * o >= HD) return bf16x8{};
   return *reinterpret_cast<const bf16x8*>(row + 8 * o);
+}
+
+// c + the sum of the eight bf16 values of x, by v_dot2c_f32_bf16 against (1, 1).
+DEVI float bf16_sum8(const bf16x8& x, float c) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  const bf16x2 ones = {(bf16)1.f, (bf16)1.f};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) c = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{x[2 * i], x[2 * i + 1]}, ones, c, false);
+  return c;
 }
 
 // Block -> (work item, head): head fastest, so the blocks of one head land on
@@ -230,13 +246,28 @@ __global__ __launch_bounds__(256) void wide_fwd_kernel(const WideArgs a) {
   for (int c = 0; c < NC; ++c) qop[c] = row_op<HD>(qrow, 2 * c + h);
   wide_zero_pad<HD>(sK[0], sK[1], sV[0], sV[1], tid);
   const uint32_t rk = DROP ? drop_row(a.drop, valid ? t : g.x, head) : 0u;
+  // the wave's bound c |q| max|k| over its partner range
+  float km = 0.f;
+  for (int tt = (g.z >> 5) + lane; tt < ((g.w + kTile - 1) >> 5); tt += 64)
+    km = fmaxf(km, a.knorm[(size_t)head * a.tk_tiles + tt]);
+  km = wave_max(km);
+  float qq = 0.f;
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qq = fmaf((float)qop[c][e], (float)qop[c][e], qq);
+  qq += __shfl_xor(qq, 32);
+  const float bnd = valid ? a.c * sqrtf(qq) * km : 0.f;
+  const bool fixed_ref = __builtin_amdgcn_readfirstlane((int)(wave_max(bnd) <= kStaticBound)) != 0;
   f32x16 acc[NM];
 #pragma unroll
   for (int m = 0; m < NM; ++m) acc[m] = f32x16{};
-  float m_run = -INFINITY, l_run = 0.f;
+  float m_run = fixed_ref ? 0.f : -INFINITY, l_run = 0.f;
   const int n_tiles = (g.w - g.z + kTile - 1) >> 5;
   const int n_stages = (n_tiles + 1) >> 1;
   const f32x16 zero = {};
+  auto run = [&](auto online_tag) {
+  constexpr bool ONLINE = decltype(online_tag)::value;
   wide_walk(
       n_stages,
       [&](int st) {
@@ -262,34 +293,48 @@ __global__ __launch_bounds__(256) void wide_fwd_kernel(const WideArgs a) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) s[r] = k0 + row_local(r, h) < g.w ? s[r] : -INFINITY;
           }
-          float mt = s[0];
-#pragma unroll
-          for (int r = 1; r < 16; ++r) mt = fmaxf(mt, s[r]);
-          mt = fmaxf(mt, __shfl_xor(mt, 32));
-          const float m_new = fmaxf(m_run, mt);
-          if (__ballot(m_new > m_run)) {
-            const float alpha = m_run == -INFINITY ? 0.f : fast_exp2(a.c * (m_run - m_new));
-            l_run *= alpha;
-#pragma unroll
-            for (int m = 0; m < NM; ++m)
-#pragma unroll
-              for (int r = 0; r < 16; ++r) acc[m][r] *= alpha;
-            m_run = m_new;
-          }
-          const float cm = m_run == -INFINITY ? 0.f : a.c * m_run;
           float p[16];
+          if (ONLINE) {
+            float mt = s[0];
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            p[r] = fast_exp2(fmaf(s[r], a.c, -cm));
-            l_run += p[r];
+            for (int r = 1; r < 16; ++r) mt = fmaxf(mt, s[r]);
+            mt = fmaxf(mt, __shfl_xor(mt, 32));
+            const float m_new = fmaxf(m_run, mt);
+            if (__ballot(m_new > m_run)) {
+              const float alpha = m_run == -INFINITY ? 0.f : fast_exp2(a.c * (m_run - m_new));
+              l_run *= alpha;
+#pragma unroll
+              for (int m = 0; m < NM; ++m)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[m][r] *= alpha;
+              m_run = m_new;
+            }
+            const float cm = m_run == -INFINITY ? 0.f : a.c * m_run;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) p[r] = fast_exp2(fmaf(s[r], a.c, -cm));
+          } else {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) p[r] = fast_exp2(s[r] * a.c);
           }
-          if (DROP) drop_tile(a.drop, rk, &sKey[buf][u * kTile], h, p);
+          // the row sum of exactly the bf16 probabilities the products use, two per instruction
+          bf16x8 pb[2] = {cvt8(p), cvt8(p + 8)};
+          l_run = bf16_sum8(pb[0], bf16_sum8(pb[1], l_run));
+          if (DROP) {
+            drop_tile(a.drop, rk, &sKey[buf][u * kTile], h, p);
+            pb[0] = cvt8(p);
+            pb[1] = cvt8(p + 8);
+          }
 #pragma unroll
           for (int m = 0; m < NM; ++m)
 #pragma unroll
-            for (int j = 0; j < 2; ++j) acc[m] = mfma32(tr_dims(sV[buf], m, 2 * u + j, lane), cvt8(p + 8 * j), acc[m]);
+            for (int j = 0; j < 2; ++j) acc[m] = mfma32(tr_dims(sV[buf], m, 2 * u + j, lane), pb[j], acc[m]);
         }
       });
+  };
+  if (fixed_ref)
+    run(std::integral_constant<bool, false>{});
+  else
+    run(std::integral_constant<bool, true>{});
   if (!valid) return;
   const float l = l_run + __shfl_xor(l_run, 32);
   store_acc<HD>(a.o + ((size_t)t * H + head) * HD, acc, l > 0.f ? (DROP ? a.drop.inv_keep : 1.f) / l : 0.f, h);
@@ -470,10 +515,13 @@ __global__ __launch_bounds__(256) void wide_dkdv_kernel(const WideArgs a) {
           }
           float p[16], ds[16];
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            p[r] = q0 + row_local(r, h) < g.w ? fast_exp2(s[r] * a.c) : 0.f;
-            ds[r] = p[r] * dp[r];
+          for (int r = 0; r < 16; ++r) p[r] = fast_exp2(s[r] * a.c);
+          if (q0 + kTile > g.w) {   // the segment's last, partial query tile
+#pragma unroll
+            for (int r = 0; r < 16; ++r) p[r] = q0 + row_local(r, h) < g.w ? p[r] : 0.f;
           }
+#pragma unroll
+          for (int r = 0; r < 16; ++r) ds[r] = p[r] * dp[r];
           if (DROP) {
             // dp holds dO v - D: a kept partner's dS is P ((dO v) / (1 - p) - D), a dropped one's -P D
             float nd[16], pk[16];
@@ -515,12 +563,62 @@ __global__ __launch_bounds__(256) void wide_dkdv_kernel(const WideArgs a) {
 // rows give P = 0).
 struct WidePrep {
   const int* cu_q; const int* cu_k; int nseg;
-  int total_q, heads, tq_pad;
+  int total_q, total_k, heads, tq_pad, tk_tiles;
   int4* plan_q; int* count_q; int4* plan_k; int* count_k;
   float2* aux;
-  int nb_plan_k, nb_rows;
+  const bf16* k; float* knorm;   // forward: max |k| per (head, 32-key tile)
+  int nb_plan_k, nb_knorm, nb_rows;
 };
 
+// max |k_t| over key tile `tile` per head: knorm[h * n_tiles + tile].  Lanes
+// read consecutive 16-byte chunks of the tile's rows (heads fastest), a row's
+// C = HD / 8 chunks on C consecutive lanes summed by shuffles (head dim 24:
+// a row per lane); with a power-of-two head count and H C <= 64 the rows of
+// one head in a wave are then combined by shuffles too, so one LDS atomic per
+// head and wave remains.  (A row per lane with eight 16-byte loads, each
+// instruction touching 64 lines at hd 64, took 4x longer.)
+template <int HD>
+DEVI void wide_knorm_block(const WidePrep& p, int tile, int tid) {
+  constexpr int C = (HD / 8 & (HD / 8 - 1)) == 0 ? HD / 8 : 1;   // chunks per lane group
+  constexpr int CPL = HD / 8 / C;                                  // chunks per lane
+  __shared__ int smax[256];
+  const int H = p.heads, lane = tid & 63;
+  for (int h0 = 0; h0 < H; h0 += 256) {
+    const int hn = min(256, H - h0);
+    const bool wave_heads = hn == H && (H & (H - 1)) == 0 && H * C <= 64;
+    if (tid < hn) smax[tid] = 0;
+    __syncthreads();
+    const int items = kTile * hn * C;
+    for (int i0 = 0; i0 < items; i0 += 256) {   // block-uniform trip count: every lane reaches the shuffles
+      const int i = i0 + tid;
+      const int rr = i / C, c = i - rr * C;
+      const int t = tile * kTile + rr / hn, h = h0 + rr % hn;
+      float x = 0.f;
+      if (i < items && t < p.total_k) {
+        const bf16x8* r = reinterpret_cast<const bf16x8*>(p.k + ((size_t)t * H + h) * HD) + c * CPL;
+#pragma unroll
+        for (int o = 0; o < CPL; ++o) {
+          const bf16x8 u = r[o];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) x = fmaf((float)u[e], (float)u[e], x);
+        }
+      }
+#pragma unroll
+      for (int o = 1; o < C; o <<= 1) x += __shfl_xor(x, o);   // the row's |k|^2 on all its lanes
+      if (wave_heads) {
+        for (int o = H * C; o < 64; o <<= 1) x = fmaxf(x, __shfl_xor(x, o));
+        if (lane < H * C && c == 0 && i < items) atomicMax(&smax[h - h0], __float_as_int(x));
+      } else if (c == 0 && i < items) {
+        atomicMax(&smax[h - h0], __float_as_int(x));   // x >= 0: int order is float order
+      }
+    }
+    __syncthreads();
+    if (tid < hn) p.knorm[(size_t)(h0 + tid) * p.tk_tiles + tile] = sqrtf(__int_as_float(smax[tid]));
+    __syncthreads();
+  }
+}
+
+template <int HD>
 __global__ __launch_bounds__(256) void wide_prep_kernel(const WidePrep p) {
   const int tid = threadIdx.x;
   int b = blockIdx.x;
@@ -528,6 +626,8 @@ __global__ __launch_bounds__(256) void wide_prep_kernel(const WidePrep p) {
   b -= 1;
   if (b < p.nb_plan_k) { seg_plan_block(p.cu_k, p.cu_q, p.nseg, kWGroup, p.plan_k, p.count_k, tid); return; }
   b -= p.nb_plan_k;
+  if (b < p.nb_knorm) { wide_knorm_block<HD>(p, b, tid); return; }
+  b -= p.nb_knorm;
   const int t0 = min(max(p.cu_q[p.nseg], 0), p.total_q);
   const long n = (long)p.heads * (p.tq_pad - t0);
   for (long idx = (long)b * 256 + tid; idx < n; idx += (long)p.nb_rows * 256) {
@@ -541,7 +641,7 @@ int wr32(int x) { return (x + kTile - 1) / kTile * kTile; }
 // Groups of one direction: at most ceil(T / 128) + (non-empty segments) <= ceil(T / 128) + T.
 size_t wplan_bytes(int total) { return wal256(((size_t)(total + kWGroup - 1) / kWGroup + (size_t)total + 1) * 16); }
 
-struct WideWs { size_t counts, plan_q, plan_k, aux, total; };
+struct WideWs { size_t counts, plan_q, plan_k, aux, knorm, total; };
 WideWs wide_ws(int total_q, int total_k, int heads, bool backward) {
   WideWs w{};
   size_t off = 0;
@@ -550,6 +650,8 @@ WideWs wide_ws(int total_q, int total_k, int heads, bool backward) {
   if (backward) {
     w.plan_k = off; off += wplan_bytes(total_k);
     w.aux = off; off += wal256((size_t)heads * wr32(total_q) * 8);
+  } else {
+    w.knorm = off; off += wal256((size_t)heads * (wr32(total_k) / kTile) * 4);
   }
   w.total = off;
   return w;
@@ -565,6 +667,13 @@ unsigned wide_grid(int total_outer, int nseg, int heads) {
     else if (hd == 24) hipLaunchKernelGGL((KERNEL<24, D>), grid, dim3(256), 0, st, a);    \
     else if (hd == 32) hipLaunchKernelGGL((KERNEL<32, D>), grid, dim3(256), 0, st, a);    \
     else hipLaunchKernelGGL((KERNEL<64, D>), grid, dim3(256), 0, st, a);                  \
+  } while (0)
+#define ESA_WIDE_PREP(hd, grid, st, p)                                                         \
+  do {                                                                                    \
+    if (hd == 16) hipLaunchKernelGGL((wide_prep_kernel<16>), grid, dim3(256), 0, st, p);  \
+    else if (hd == 24) hipLaunchKernelGGL((wide_prep_kernel<24>), grid, dim3(256), 0, st, p); \
+    else if (hd == 32) hipLaunchKernelGGL((wide_prep_kernel<32>), grid, dim3(256), 0, st, p); \
+    else hipLaunchKernelGGL((wide_prep_kernel<64>), grid, dim3(256), 0, st, p);           \
   } while (0)
 // Head dim 16 only with dropout (without, esa_attn_dense.hip's kernels run).
 #define ESA_WIDE_LAUNCH(KERNEL, hd, drop, grid, st, a)                                   \
@@ -588,10 +697,13 @@ int wide_attn_fwd(const DenseAttnCall& c, void* workspace, size_t workspace_byte
   char* ws = static_cast<char*>(workspace);
   WidePrep p{};
   p.cu_q = c.cu_q; p.cu_k = c.cu_k; p.nseg = c.nseg;
-  p.total_q = c.total_q; p.heads = c.heads; p.tq_pad = wr32(c.total_q);
+  p.total_q = c.total_q; p.total_k = c.total_k; p.heads = c.heads; p.tq_pad = wr32(c.total_q);
+  p.tk_tiles = wr32(c.total_k) / kTile;
   p.count_q = reinterpret_cast<int*>(ws + w.counts);
   p.plan_q = reinterpret_cast<int4*>(ws + w.plan_q);
-  ESA_TIMED(esa_profile::kAttnPrep, st, hipLaunchKernelGGL(wide_prep_kernel, dim3(1), dim3(256), 0, st, p));
+  p.k = static_cast<const bf16*>(c.k); p.knorm = reinterpret_cast<float*>(ws + w.knorm);
+  p.nb_knorm = p.tk_tiles;
+  ESA_TIMED(esa_profile::kAttnPrep, st, ESA_WIDE_PREP(c.head_dim, dim3(1 + p.nb_knorm), st, p));
   ESA_LAUNCH_CHECK();
   WideArgs a{};
   a.q = static_cast<const bf16*>(c.q); a.k = static_cast<const bf16*>(c.k); a.v = static_cast<const bf16*>(c.v);
@@ -599,6 +711,7 @@ int wide_attn_fwd(const DenseAttnCall& c, void* workspace, size_t workspace_byte
   a.total_q = c.total_q; a.total_k = c.total_k; a.heads = c.heads; a.tq_pad = p.tq_pad;
   a.c = c.scale * kLog2e; a.scale = c.scale;
   a.drop = c.drop;
+  a.knorm = p.knorm; a.tk_tiles = p.tk_tiles;
   a.o = static_cast<bf16*>(c.out); a.lse_out = c.lse;
   ESA_TIMED(esa_profile::kAttnFwd, st,
             ESA_WIDE_LAUNCH(wide_fwd_kernel, c.head_dim, c.dropout, dim3(wide_grid(c.total_q, c.nseg, c.heads)), st,
@@ -623,8 +736,7 @@ int wide_attn_bwd(const DenseAttnCall& c, void* workspace, size_t workspace_byte
   p.aux = reinterpret_cast<float2*>(ws + w.aux);
   p.nb_plan_k = 1;
   p.nb_rows = (int)std::max(1L, ((long)c.heads * (p.tq_pad - c.total_q) + 255) / 256);
-  ESA_TIMED(esa_profile::kAttnPrep, st,
-            hipLaunchKernelGGL(wide_prep_kernel, dim3(2 + p.nb_rows), dim3(256), 0, st, p));
+  ESA_TIMED(esa_profile::kAttnPrep, st, ESA_WIDE_PREP(c.head_dim, dim3(2 + p.nb_rows), st, p));
   ESA_LAUNCH_CHECK();
   WideArgs a{};
   a.q = static_cast<const bf16*>(c.q); a.k = static_cast<const bf16*>(c.k); a.v = static_cast<const bf16*>(c.v);
