@@ -331,13 +331,17 @@ def bench_wide(args) -> dict:
         dom = max((n for n in per_pair if n in kern), key=lambda n: kern[n]["avg_us"])
         achieved = kern[dom]["algorithmic_tflops"]
         tflops = 14 * d * pairs / (ms * 1e-3) / 1e12
+        traffic = None   # HBM bytes per launch of the dominant kernel (rocprofv3 FETCH_SIZE + WRITE_SIZE)
+        tfile = ROOT / "profiles" / "attn_bwd_dkdv_wide_traffic.json"
+        if dom == "attn_bwd_dkdv" and tfile.exists():
+            traffic = json.loads(tfile.read_text()).get(f"hd{hd}", {}).get("hbm_bytes_per_launch")
         out[f"hd{hd}"] = {"heads": heads, "head_dim": hd, "ms_per_step": ms, "wall_ms_per_step": wall_ms,
                           "edge_tokens_per_s": t / (ms * 1e-3), "achieved_tflops": tflops,
                           "mfma_util_pct": 100.0 * tflops / PEAK_BF16_TFLOPS, "ms_per_step_profiled": ms_prof,
                           "kernels": kern,
                           "roofline": {"bound": "mfma", "kernel": dom, "achieved": achieved,
                                        "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                                       "frac": achieved / PEAK_BF16_TFLOPS}}
+                                       "frac": achieved / PEAK_BF16_TFLOPS, "traffic": traffic}}
         del q, k, v, go
     # node mode at the same widths (the qm9 / unimol / lba M layers: node mode, 8 heads of 64; coconut: 16 of 32)
     from mind_amd.esa.packing import NodeAdjacency
@@ -379,8 +383,9 @@ def bench_dropout(args) -> dict:
     """The cost of attention dropout (the reference's training-time p, esa/mha.py:76,82; MIND's rna YAML trains
     with 0.08, core/pretraining_config_rna.yaml:76-78) on two workloads, each timed without and with dropout:
     configuration 1's dense fwd+bwd at 16 heads of 16 (with dropout the MFMA kernels of esa_attn_wide.hip take
-    the call: they evaluate the keep mask per score) and node-mode fwd+bwd at the rna YAML's 8 heads of 24 over a
-    65,536-node budget batch with its node plan (the gather kernels)."""
+    the call: they evaluate the keep mask per score), the same graphs at the rna YAML's 8 heads of 24 (its S
+    layers; the wide kernels with and without dropout), and node-mode fwd+bwd at 8 heads of 24 over a
+    65,536-node budget batch with its node plan (the gather kernels; its M layers)."""
     import torch
 
     from mind_amd import generators
@@ -404,6 +409,19 @@ def bench_dropout(args) -> dict:
                           "kernels": {n: r["avg_us"] for n, r in kern.items()}}
     rec["slowdown"] = rec["p0.08"]["ms_per_step"] / rec["p0"]["ms_per_step"]
     out["dense_config1"] = rec
+    del q, k, v, go
+    # the rna YAML's S layers: dense self-attention at 8 heads of 24 (dim 192) with dropout 0.08
+    q, k, v, go = (torch.randn(t, 8, 24, generator=g).to(torch.bfloat16).to(dev) for _ in range(4))
+    rec = {"edge_tokens": t, "heads": 8, "head_dim": 24}
+    for p in (0.0, 0.08):
+        def step():
+            o, lse = attention.attn_fwd(q, k, v, cu, cu, maxlen, maxlen, 24 ** -0.5, dropout_p=p, dropout_seed=1)
+            attention.attn_bwd(go, q, k, v, o, lse, cu, cu, maxlen, maxlen, 24 ** -0.5, dropout_p=p, dropout_seed=1)
+        ms, _, kern, _ = timed(step, args.steps, args.warmup)
+        rec[f"p{p:g}"] = {"ms_per_step": ms, "edge_tokens_per_s": t / (ms * 1e-3),
+                          "kernels": {n: r["avg_us"] for n, r in kern.items()}}
+    rec["slowdown"] = rec["p0.08"]["ms_per_step"] / rec["p0"]["ms_per_step"]
+    out["dense_rna_shape"] = rec
     del q, k, v, go
     gn = generators.protein_budget(seed=args.seed, token_budget=65536, count="nodes")
     na = NodeAdjacency.from_edge_index(torch.as_tensor(gn.edge_index).to(dev), torch.as_tensor(gn.batch).to(dev),

@@ -50,6 +50,12 @@
 
 namespace {
 
+// Build-time tuning: minimum waves per SIMD the dK/dV kernel is compiled for
+// (0 = the compiler's choice).
+#ifndef ESA_WIDE_WAVES_DKDV
+#define ESA_WIDE_WAVES_DKDV 0
+#endif
+
 constexpr int kWStage = 64;              // partner tokens per stage (two tiles)
 constexpr int kWTokPad = kWStage + 4;    // LDS octet stride in tokens
 
@@ -116,11 +122,27 @@ DEVI float bf16_sum8(const bf16x8& x, float c) {
   return c;
 }
 
-// Block -> (work item, head): head fastest, so the blocks of one head land on
-// one XCD (block b runs on XCD b % 8) and share its L2.
+// Block -> (work item, head).  Block b runs on XCD b % 8, each XCD with its
+// own L2, and a 128-byte line of a [T][H][HD] bf16 tensor holds the rows of
+// L = 128 / (2 HD) consecutive heads of one token (head dim 32: 2, 64: 1).
+// When H is a multiple of 8 L, XCD x serves the line groups x, x + 8, ..., so
+// a line's heads share one L2 and each line is fetched once (head dim 32 at 16
+// heads read 1.5-2x its algorithmic bytes with head = b % H); otherwise head
+// fastest, head = b % H.
+template <int HD>
 DEVI void wide_item_head(int H, int& item, int& head) {
-  item = (int)blockIdx.x / H;
-  head = (int)blockIdx.x - item * H;
+  constexpr int L = HD == 32 ? 2 : 1;   // head dims 16 and 24 run only with dropout; 64 fills a line
+  const int b = (int)blockIdx.x;
+  if (L > 1 && H % (8 * L) == 0) {
+    const int per_xcd = H / 8;   // heads served by one XCD: H / (8 L) line groups of L heads
+    const int x = b & 7, slot = b >> 3;
+    const int j = slot % per_xcd;
+    head = (x + 8 * (j / L)) * L + j % L;
+    item = slot / per_xcd;
+  } else {
+    item = b / H;
+    head = b - item * H;
+  }
 }
 
 // ---- staging: stage st covers partner tokens g0 + 64 st .. + 63 of tensors
@@ -235,7 +257,7 @@ __global__ __launch_bounds__(256) void wide_fwd_kernel(const WideArgs a) {
   const int col = lane & 31, h = lane >> 5;
   const int H = a.heads;
   int item, head;
-  wide_item_head(H, item, head);
+  wide_item_head<HD>(H, item, head);
   if (item >= *a.count) return;
   const int4 g = a.groups[item];
   const int t = g.x + wave * kTile + col;
@@ -355,7 +377,7 @@ __global__ __launch_bounds__(256) void wide_dq_kernel(const WideArgs a) {
   const int col = lane & 31, h = lane >> 5;
   const int H = a.heads;
   int item, head;
-  wide_item_head(H, item, head);
+  wide_item_head<HD>(H, item, head);
   if (item >= *a.count) return;
   const int4 g = a.groups[item];
   const int t = g.x + wave * kTile + col;
@@ -440,7 +462,8 @@ __global__ __launch_bounds__(256) void wide_dq_kernel(const WideArgs a) {
 // dV^T += dO^T P, dK^T += Q^T dS.  A stage holds 64 queries' Q and dO rows
 // and their statistics.
 template <int HD, bool DROP>
-__global__ __launch_bounds__(256) void wide_dkdv_kernel(const WideArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(ESA_WIDE_WAVES_DKDV > 0 ? ESA_WIDE_WAVES_DKDV : 1)))
+void wide_dkdv_kernel(const WideArgs a) {
   constexpr int HP = (HD + 31) / 32 * 32, NC = (HD + 15) / 16, NM = HP / 32, NO = HP / 8;
   __shared__ __align__(16) bf16 sQ[2][NO * kWTokPad * 8];
   __shared__ __align__(16) bf16 sG[2][NO * kWTokPad * 8];
@@ -450,7 +473,7 @@ __global__ __launch_bounds__(256) void wide_dkdv_kernel(const WideArgs a) {
   const int col = lane & 31, h = lane >> 5;
   const int H = a.heads;
   int item, head;
-  wide_item_head(H, item, head);
+  wide_item_head<HD>(H, item, head);
   if (item >= *a.count) return;
   const int4 g = a.groups[item];   // outer = keys, inner = queries
   const int t = g.x + wave * kTile + col;
