@@ -55,6 +55,14 @@ namespace {
 #ifndef ESA_WIDE_WAVES_DKDV
 #define ESA_WIDE_WAVES_DKDV 0
 #endif
+// Minimum waves per SIMD of the dQ kernel at head dim 64.
+#ifndef ESA_WIDE_WAVES_DQ64
+#define ESA_WIDE_WAVES_DQ64 3
+#endif
+// Build-time switch: 1 = staged tokens swizzled per octet pair (below), 0 = plain layout.
+#ifndef ESA_WIDE_SWZ
+#define ESA_WIDE_SWZ 1
+#endif
 
 constexpr int kWStage = 64;              // partner tokens per stage (two tiles)
 constexpr int kWTokPad = kWStage + 4;    // LDS octet stride in tokens
@@ -71,21 +79,34 @@ struct WideArgs {
   bf16* o; float* lse_out; bf16* dq; bf16* dk; bf16* dv;
 };
 
+// LDS position of staged token t in octet o of an NO-octet layout.  The
+// octet stride (68 tokens = 1088 bytes, 64 mod 128) puts octets of equal
+// parity on the same banks of a 128-byte window, where the 16-byte staging
+// stores of 8 consecutive lanes (one token's 8 octets at head dim 64, two
+// tokens' 4 at head dim 32) collided 4- and 2-way.  XORing the token's low
+// two bits with a value per octet pair ((o / 2) mod 4 for 8 octets,
+// 2 ((o / 2) mod 2) for 4) spreads them over the window's eight 16-byte
+// slots.  Every read covers aligned blocks of 4 or 8 tokens of one octet
+// pair, which the XOR only permutes, so the reads keep their bank pattern.
+template <int NO>
+DEVI int wtok(int t, int o) { return ESA_WIDE_SWZ ? t ^ (((o >> 1) & (NO / 2 - 1)) * (8 / NO)) : t; }
+
 // 16 bytes of the A operand of a score MFMA: dims 16 c + 8 h .. + 7 (octet
 // 2 c + h) of staged token t.
 template <int NO>
-DEVI bf16x8 row_octet(const bf16* rows, int t, int o) { return lds8(rows + ((size_t)o * kWTokPad + t) * 8); }
+DEVI bf16x8 row_octet(const bf16* rows, int t, int o) { return lds8(rows + ((size_t)o * kWTokPad + wtok<NO>(t, o)) * 8); }
 
 // A operand [32 dims x 16 partners] of a product over partners: dims
 // 32 m + (lane % 32), partners 16 j + 8 h .. + 7 (h = lane / 32), by two
 // transpose reads of four tokens each.  In a 16-lane group, lane L
 // addresses token t0 + L / 4 (+ 4 in the second read), dims 4 (L % 4) .. + 3
 // of the group's 16 dims, so lane i receives dim i of the four tokens.
+template <int NO>
 DEVI bf16x8 tr_dims(const bf16* rows, int m, int j, int lane) {
   const int i = lane & 15, grp = lane >> 4;
   const int d = 32 * m + 16 * (grp & 1) + 4 * (i & 3);
-  const int t = 16 * j + 8 * (grp >> 1) + (i >> 2);
-  const bf16* p = rows + ((size_t)(d >> 3) * kWTokPad + t) * 8 + (d & 7);
+  const int t = 16 * j + 8 * (grp >> 1) + (i >> 2), o = d >> 3;
+  const bf16* p = rows + ((size_t)o * kWTokPad + wtok<NO>(t, o)) * 8 + (d & 7);
   const bf16x4 lo = lds_tr4(p), hi = lds_tr4(p + 4 * 8);
   return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
@@ -182,7 +203,8 @@ DEVI void wide_lstore(bf16* sa, bf16* sb, const WStage<HD>& s, int tid) {
     if (WStage<HD>::NCH % 256 != 0 && c >= WStage<HD>::NCH) continue;
     const int tensor = c / (kWStage * NR), rem = c - tensor * (kWStage * NR);
     const int tok = rem / NR, o = rem - tok * NR;
-    *reinterpret_cast<i32x4*>((tensor ? sb : sa) + ((size_t)o * kWTokPad + tok) * 8) = s.r[i];
+    *reinterpret_cast<i32x4*>((tensor ? sb : sa) + ((size_t)o * kWTokPad + wtok<(HD + 31) / 32 * 4>(tok, o)) * 8) =
+        s.r[i];
   }
 }
 // Head dim 24: the padding octet of the four staging buffers (two tensors,
@@ -349,7 +371,7 @@ __global__ __launch_bounds__(256) void wide_fwd_kernel(const WideArgs a) {
 #pragma unroll
           for (int m = 0; m < NM; ++m)
 #pragma unroll
-            for (int j = 0; j < 2; ++j) acc[m] = mfma32(tr_dims(sV[buf], m, 2 * u + j, lane), pb[j], acc[m]);
+            for (int j = 0; j < 2; ++j) acc[m] = mfma32(tr_dims<NO>(sV[buf], m, 2 * u + j, lane), pb[j], acc[m]);
         }
       });
   };
@@ -368,7 +390,8 @@ __global__ __launch_bounds__(256) void wide_fwd_kernel(const WideArgs a) {
 // dS = P (dP - D), dQ^T += K^T dS^T.  Also writes the dK/dV pass's row
 // statistics {-LSE2 / c, -D} of its queries.
 template <int HD, bool DROP>
-__global__ __launch_bounds__(256) void wide_dq_kernel(const WideArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HD == 64 && !DROP ? ESA_WIDE_WAVES_DQ64 : 1)))
+void wide_dq_kernel(const WideArgs a) {
   constexpr int HP = (HD + 31) / 32 * 32, NC = (HD + 15) / 16, NM = HP / 32, NO = HP / 8;
   __shared__ __align__(16) bf16 sK[2][NO * kWTokPad * 8];
   __shared__ __align__(16) bf16 sV[2][NO * kWTokPad * 8];
@@ -449,7 +472,7 @@ __global__ __launch_bounds__(256) void wide_dq_kernel(const WideArgs a) {
 #pragma unroll
           for (int m = 0; m < NM; ++m)
 #pragma unroll
-            for (int j = 0; j < 2; ++j) acc[m] = mfma32(tr_dims(sK[buf], m, 2 * u + j, lane), cvt8(ds + 8 * j), acc[m]);
+            for (int j = 0; j < 2; ++j) acc[m] = mfma32(tr_dims<NO>(sK[buf], m, 2 * u + j, lane), cvt8(ds + 8 * j), acc[m]);
         }
       });
   if (!valid) return;
@@ -569,8 +592,8 @@ void wide_dkdv_kernel(const WideArgs a) {
           for (int m = 0; m < NM; ++m)
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
-              dva[m] = mfma32(tr_dims(sG[buf], m, 2 * u + j, lane), cvt8(p + 8 * j), dva[m]);
-              dka[m] = mfma32(tr_dims(sQ[buf], m, 2 * u + j, lane), cvt8(ds + 8 * j), dka[m]);
+              dva[m] = mfma32(tr_dims<NO>(sG[buf], m, 2 * u + j, lane), cvt8(p + 8 * j), dva[m]);
+              dka[m] = mfma32(tr_dims<NO>(sQ[buf], m, 2 * u + j, lane), cvt8(ds + 8 * j), dka[m]);
             }
         }
       });
