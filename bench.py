@@ -844,6 +844,66 @@ def cpu_baseline_gather(src, dst, seed: int, slice_edges: int) -> dict:
                        f"{cores} threads, median of {runs} runs after 2 warm-ups; GB/s of the same algorithmic bytes")}
 
 
+def minmax_bytes(e: int, n: int) -> int:
+    """Compulsory HBM bytes of a 1-D segmented minimum with argument: the CSR permutation and one fp32 value
+    per edge, indptr, one fp32 value and one int64 argument per node."""
+    return 8 * e + 4 * (n + 1) + 12 * n
+
+
+def bench_encoder_min(args, dev, src) -> dict:
+    """The encoder's closest-neighbour reduction (core/molecular_encoder.py:214, scatter_min of a per-edge
+    distance by edge_src) over configuration 3's graph: fp32 distances in [0.5, 3) on 2^25 edges to 2^21
+    nodes, edges in the canonical dst-sorted order, so each node's edges are scattered; the CSR by src is
+    built once outside the timed steps (csr_build_ms times that build).  Beside it: torch's scatter_reduce
+    ('amin', the atomic library form of the same reduction) on the same GPU, and on the host cores over a
+    2^21-edge slice."""
+    import torch
+
+    from mind_amd.edges import CSR, segment_minmax_csr
+
+    csr_src = CSR.build(src, GATHER_N)
+    g = torch.Generator(device=dev).manual_seed(args.seed + 3)
+    dist = (torch.rand(GATHER_E, 1, device=dev, generator=g) * 2.5 + 0.5).contiguous()
+    ms, _, kern, _ = timed(lambda: segment_minmax_csr(dist, csr_src.indptr, csr_src.perm),
+                           max(5, args.steps // 2), 2)
+    by = minmax_bytes(GATHER_E, GATHER_N)
+    rec = kern.get("segment_minmax", {})
+    if rec:
+        rec["algorithmic_bytes"] = by
+        rec["achieved_gbs"] = by / (rec["avg_us"] * 1e-6) / 1e9
+    flat, src_l = dist.view(-1), src.long()
+    base = torch.zeros(GATHER_N, device=dev)
+    t_ms, _, _, _ = timed(lambda: base.clone().scatter_reduce_(0, src_l, flat, "amin", include_self=False),
+                          max(5, args.steps // 2), 2, profile=False)
+    out = {"workload": "scatter_min(dist, edge_src, dim=0, dim_size=N) over configuration 3's graph (fp32, 1-D)",
+           "ms_per_step": ms, "algorithmic_bytes": by, "gb_per_s": by / (ms * 1e-3) / 1e9,
+           "edges_per_s": GATHER_E / (ms * 1e-3), "kernels": kern, "csr_build_ms": None,
+           "torch_scatter_reduce_gpu_ms": t_ms}
+    if not args.no_cpu_baseline:
+        from oracle import edges as oracle_edges
+
+        k = 1 << 21
+        d_cpu, s_cpu = flat[:k].cpu(), src_l[:k].cpu()
+        oracle_edges.scatter_min_torch(d_cpu, s_cpu, GATHER_N)
+        t0 = time.perf_counter()
+        for _ in range(3):
+            oracle_edges.scatter_min_torch(d_cpu, s_cpu, GATHER_N)
+        cpu_ms = (time.perf_counter() - t0) / 3 * 1e3
+        out["cpu_baseline"] = {"value": k / (cpu_ms * 1e-3), "unit": "edges/s", "cores": torch.get_num_threads(),
+                               "kind": "port", "sample": (f"oracle.edges.scatter_min_torch (torch scatter_reduce "
+                                                          f"amin) on the host over the first {k} edges of the batch")}
+    t1 = torch.cuda.Event(enable_timing=True)
+    t2 = torch.cuda.Event(enable_timing=True)
+    t1.record()
+    CSR.build(src, GATHER_N)
+    t2.record()
+    torch.cuda.synchronize()
+    out["csr_build_ms"] = t1.elapsed_time(t2)
+    del dist, csr_src, base
+    torch.cuda.empty_cache()
+    return out
+
+
 def bench_gather(args, sub: bool = False):
     """Configuration 3: edge-token gather and CSR segment sum at 2^21 nodes x 2^25 edges x 256 features."""
     import torch
@@ -903,6 +963,8 @@ def bench_gather(args, sub: bool = False):
         del x, y, out, agg
         torch.cuda.empty_cache()
 
+    encoder_min = bench_encoder_min(args, dev, src)
+
     # in-process reference: a plain device-to-device copy (torch) of the fp32 edge-output size, the practical
     # streaming rate of this allocation on this box
     a = torch.empty(GATHER_E, GATHER_F, device=dev)
@@ -930,7 +992,7 @@ def bench_gather(args, sub: bool = False):
                "ms_per_step_bf16": results["bf16"]["ms_per_step"], "gb_per_s_bf16": results["bf16"]["gb_per_s"],
                "kernels_f32": f32["kernels"], "kernels_bf16": results["bf16"]["kernels"],
                "hbm_frac": hbm_frac, "csr_build_ms": csr_ms, "reference_copy_gbs": copy_gbs,
-               "roofline": roofline}
+               "roofline": roofline, "encoder_min": encoder_min}
         if not args.no_cpu_baseline:
             out["cpu_baseline"] = cpu_baseline_gather(src.cpu().numpy(), dst.cpu().numpy(), args.seed, 1 << 21)
         return out
@@ -957,6 +1019,7 @@ def bench_gather(args, sub: bool = False):
         "csr_build_ms": csr_ms,
         "reference_copy_gbs": copy_gbs,
         "fused_projection": fused,
+        "encoder_min": encoder_min,
         "f32": f32,
         "bf16": results["bf16"],
         "hbm_frac": hbm_frac,

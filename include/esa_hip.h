@@ -334,6 +334,27 @@ ESA_API int esa_csr_segment_sum(const void* y, const int* perm, const int* indpt
                         int num_nodes, int features, int dtype, void* out,
                         void* stream);
 
+/* ------------------------------------------------------------------------ */
+/* Deterministic segmented minimum / maximum with argument: torch_scatter's  */
+/* scatter_min / scatter_max over dim 0 without `out` (torch_scatter 2.1,    */
+/* pyg::pytorch-scatter in GET/env.yml), as the encoder takes each node's    */
+/* closest close-range neighbour distance (core/molecular_encoder.py:214,    */
+/* `scatter_min(close_dists, close_src, dim=0, dim_size=num_nodes)`).  For   */
+/* node n and feature f the value starts at the largest finite value of      */
+/* `dtype` (the lowest when is_max) and, over i in [indptr[n], indptr[n+1])  */
+/* in ascending i with e = perm ? perm[i] : i, is replaced by y[e, f] when   */
+/* that is strictly smaller (larger), arg[n, f] = e; a value never replaced  */
+/* (empty segment, or only NaN / values beyond the start) is written as 0    */
+/* with arg[n, f] = num_edges.  With the stable CSR of esa_csr_build a tie   */
+/* keeps the lowest edge id (torch_scatter's CPU order; its GPU kernel keeps */
+/* any tied edge).  y is [num_edges, F], out [N, F] of `dtype` (ESA_F32 or   */
+/* ESA_BF16), arg [N, F] int64 or NULL.                                      */
+/* ------------------------------------------------------------------------ */
+ESA_API int esa_csr_segment_minmax(const void* y, const int* perm, const int* indptr,
+                           int num_nodes, int features, int dtype, int is_max,
+                           int64_t num_edges, void* out, int64_t* arg,
+                           void* stream);
+
 /* Backward of esa_edge_gather: gx[n] = sum over edges with src == n of
  * g[e, :F] + sum over edges with dst == n of g[e, F:], via two CSRs, each
  * accumulated in fp32 in ascending edge order (deterministic). */
@@ -433,7 +454,7 @@ ESA_API int esa_mish_bwd_colsum(const void* z, const void* grad, int64_t rows, i
 /* launch count per kernel id (capacity >= ESA_PROFILE_KERNELS) and clears   */
 /* the record.  Not for concurrent use from several threads.                 */
 /* ------------------------------------------------------------------------ */
-#define ESA_PROFILE_KERNELS 21
+#define ESA_PROFILE_KERNELS 22
 ESA_API int esa_profile_enable(int on);
 ESA_API int esa_profile_collect(float* total_ms, int* launches, int capacity);
 ESA_API const char* esa_profile_kernel_name(int kernel);

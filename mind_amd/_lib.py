@@ -77,6 +77,7 @@ _PROTOS = {
     "esa_csr_workspace_size": (_c_int, [_c_i64, _c_int, ctypes.POINTER(_c_sz)]),
     "esa_csr_build": (_c_int, [_vp, _c_i64, _c_int, _vp, _vp, _vp, _c_sz, _vp]),
     "esa_csr_segment_sum": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _vp]),
+    "esa_csr_segment_minmax": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_i64, _vp, _vp, _vp]),
     "esa_token_budget_pack_workspace_size": (_c_int, [_c_int, ctypes.POINTER(_c_sz)]),
     "esa_edge_plan_size": (_c_int, [_c_int, _c_int, _c_int, ctypes.POINTER(_c_sz)]),
     "esa_edge_plan_build": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _c_sz, _vp]),
@@ -106,7 +107,7 @@ _PROTOS = {
     "esa_profile_kernel_name": (ctypes.c_char_p, [_c_int]),
 }
 
-PROFILE_KERNELS = 21
+PROFILE_KERNELS = 22
 
 _lock = threading.Lock()
 _lib = None

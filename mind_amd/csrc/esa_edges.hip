@@ -1036,6 +1036,53 @@ __global__ void segment_sum_scalar_kernel(const T* __restrict__ y, long ld, cons
   }
 }
 
+// Largest finite value of T (torch_scatter's initial value for a minimum).
+template <typename T> DEVI float max_finite();
+template <> DEVI float max_finite<float>() { return 3.40282347e38f; }
+template <> DEVI float max_finite<bf16>() { return __uint_as_float(0x7F7F0000u); }
+
+constexpr int kMinMaxRound = 8;   // CSR positions a lane loads per round
+
+// Segmented minimum (MAX = false) or maximum with its argument: one lane per
+// (node, feature), consecutive lanes on consecutive features of a node.  The
+// running value starts at the largest finite value (the lowest for MAX) and is
+// replaced only by a strictly smaller (larger) element, taken in ascending CSR
+// position, so with a stable CSR a tie keeps the lowest edge id and NaN and
+// values beyond the start never win; a value never replaced is written as 0
+// with arg = num_edges.  Comparisons are exact (bf16 values compare as fp32).
+template <typename T, bool MAX>
+__global__ __launch_bounds__(256) void segment_minmax_kernel(const T* __restrict__ y, const int* __restrict__ perm,
+                                                             const int* __restrict__ indptr, int num_nodes,
+                                                             int features, long long num_edges, T* __restrict__ out,
+                                                             long long* __restrict__ arg) {
+  const long total = (long)num_nodes * features;
+  const float start = MAX ? -max_finite<T>() : max_finite<T>();
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (long)gridDim.x * blockDim.x) {
+    const int n = (int)(i / features), f = (int)(i - (long)n * features);
+    float best = start;
+    long long at = num_edges;
+    const int j1 = indptr[n + 1];
+    // 8 positions per round: their edge ids and then their values load independently (a chain of two
+    // dependent loads per round, not per position); the compares keep ascending position order.
+    for (int j = indptr[n]; j < j1; j += kMinMaxRound) {
+      long e[kMinMaxRound];
+      float v[kMinMaxRound];
+#pragma unroll
+      for (int k = 0; k < kMinMaxRound; ++k) e[k] = j + k < j1 ? (perm ? perm[j + k] : j + k) : -1;
+#pragma unroll
+      for (int k = 0; k < kMinMaxRound; ++k) v[k] = e[k] >= 0 ? (float)y[e[k] * features + f] : start;
+#pragma unroll
+      for (int k = 0; k < kMinMaxRound; ++k)
+        if (MAX ? v[k] > best : v[k] < best) {
+          best = v[k];
+          at = e[k];
+        }
+    }
+    out[i] = at == num_edges ? (T)0.f : (T)best;
+    if (arg) arg[i] = at;
+  }
+}
+
 unsigned grid_for(long n, int block, long cap = 1L << 20) {
   long g = (n + block - 1) / block;
   if (g < 1) g = 1;
@@ -1343,6 +1390,42 @@ int esa_csr_segment_sum(const void* y, const int* perm, const int* indptr, int n
                                 num_nodes, features, static_cast<float*>(out), st);
   return launch_segsum<bf16>(static_cast<const bf16*>(y), features, perm, indptr, 0, nullptr, nullptr, 0, num_nodes,
                              features, static_cast<bf16*>(out), st);
+}
+
+int esa_csr_segment_minmax(const void* y, const int* perm, const int* indptr, int num_nodes, int features, int dtype,
+                           int is_max, int64_t num_edges, void* out, int64_t* arg, void* stream) {
+  if (!indptr || !out || (!y && num_nodes > 0 && num_edges > 0)) return ESA_ERR_NULL;
+  if (num_nodes < 0 || features < 1 || num_edges < 0) return ESA_ERR_SHAPE;
+  if (dtype != ESA_F32 && dtype != ESA_BF16) return ESA_ERR_DTYPE;
+  if (num_nodes == 0) return ESA_OK;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const unsigned blocks = grid_for((long)num_nodes * features, 256);
+  long long* a = reinterpret_cast<long long*>(arg);
+  if (dtype == ESA_F32) {
+    const float* yf = static_cast<const float*>(y);
+    float* of = static_cast<float*>(out);
+    if (is_max)
+      ESA_TIMED(esa_profile::kSegmentMinMax, st,
+                hipLaunchKernelGGL((segment_minmax_kernel<float, true>), dim3(blocks), dim3(256), 0, st, yf, perm,
+                                   indptr, num_nodes, features, (long long)num_edges, of, a));
+    else
+      ESA_TIMED(esa_profile::kSegmentMinMax, st,
+                hipLaunchKernelGGL((segment_minmax_kernel<float, false>), dim3(blocks), dim3(256), 0, st, yf, perm,
+                                   indptr, num_nodes, features, (long long)num_edges, of, a));
+  } else {
+    const bf16* yb = static_cast<const bf16*>(y);
+    bf16* ob = static_cast<bf16*>(out);
+    if (is_max)
+      ESA_TIMED(esa_profile::kSegmentMinMax, st,
+                hipLaunchKernelGGL((segment_minmax_kernel<bf16, true>), dim3(blocks), dim3(256), 0, st, yb, perm,
+                                   indptr, num_nodes, features, (long long)num_edges, ob, a));
+    else
+      ESA_TIMED(esa_profile::kSegmentMinMax, st,
+                hipLaunchKernelGGL((segment_minmax_kernel<bf16, false>), dim3(blocks), dim3(256), 0, st, yb, perm,
+                                   indptr, num_nodes, features, (long long)num_edges, ob, a));
+  }
+  ESA_LAUNCH_CHECK();
+  return ESA_OK;
 }
 
 int esa_edge_gather_bwd(const void* g, const int* src_perm, const int* src_indptr, const int* dst_perm,

@@ -28,6 +28,7 @@ enum Kernel : int {
   kColumnSum,       // Linear bias gradients
   kAttnEdgeLists,   // edge-mask key lists
   kAttnEdgeOverflow,  // edge-mask walk kernels over the overflow groups
+  kSegmentMinMax,     // segmented minimum / maximum with argument
   kNumKernels
 };
 

@@ -10,6 +10,7 @@ reference's edge->node reductions (core/molecular_encoder.py:241-242).
 from __future__ import annotations
 
 import ctypes
+import math
 from typing import Optional
 
 import torch
@@ -213,7 +214,7 @@ def gather_add(a: torch.Tensor, b: torch.Tensor, src: torch.Tensor, dst: torch.T
 class _ScatterAdd(torch.autograd.Function):
     @staticmethod
     def forward(ctx, src, index, dim_size, csr):
-        y = src.reshape(src.shape[0], -1)
+        y = src.reshape(src.shape[0], math.prod(src.shape[1:]))
         out = segment_sum_csr(y, csr.indptr, csr.perm)
         ctx.save_for_backward(index)
         ctx.dim_size = dim_size
@@ -224,7 +225,7 @@ class _ScatterAdd(torch.autograd.Function):
         (index,) = ctx.saved_tensors
         idx = index.to(torch.int64)
         valid = (idx >= 0) & (idx < ctx.dim_size)
-        grad = g.reshape(ctx.dim_size, -1).index_select(0, idx.clamp(0, max(ctx.dim_size - 1, 0)))
+        grad = g.reshape(ctx.dim_size, math.prod(g.shape[1:])).index_select(0, idx.clamp(0, max(ctx.dim_size - 1, 0)))
         grad = grad.masked_fill(~valid.unsqueeze(1), 0)   # dropped edges: exactly 0, even beside Inf / NaN
         return grad.reshape((idx.numel(),) + tuple(g.shape[1:])), None, None, None
 
@@ -249,6 +250,89 @@ def scatter_add(src: torch.Tensor, index: torch.Tensor, dim: int = 0, dim_size: 
     elif csr.num_nodes != dim_size:
         raise ValueError("csr was built for another dim_size")
     return _ScatterAdd.apply(src, index, dim_size, csr)
+
+
+def segment_minmax_csr(y: torch.Tensor, indptr: torch.Tensor, perm: torch.Tensor | None = None,
+                       maximum: bool = False, num_edges: int | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """(out [N, F], arg [N, F] int64): per CSR segment the minimum (``maximum``: the maximum) of the rows
+    y[perm[indptr[n]:indptr[n+1]]] with the edge id attaining it, the semantics of torch_scatter's
+    scatter_min / scatter_max (no ``out``): strict comparison in ascending CSR position from the dtype's
+    largest finite value (lowest for the maximum), so a tie keeps the first (lowest, with a stable CSR)
+    edge id; a segment with nothing smaller (larger) than that start gives 0 and arg = num_edges
+    (default: y's row count)."""
+    _lib.require_gpu(y)
+    y = y.contiguous()
+    if y.dim() != 2:
+        raise ValueError("y must be [E, F]")
+    n = indptr.numel() - 1
+    e = y.shape[0] if num_edges is None else int(num_edges)
+    out = torch.empty((n, y.shape[1]), dtype=y.dtype, device=y.device)
+    arg = torch.empty((n, y.shape[1]), dtype=torch.int64, device=y.device)
+    rc = _lib.load().esa_csr_segment_minmax(y.data_ptr(), _lib.ptr(perm), indptr.data_ptr(), n, y.shape[1],
+                                           _dtype_code(y), int(maximum), e, out.data_ptr(), arg.data_ptr(),
+                                           _lib.stream_of(y))
+    _lib.check(rc, "esa_csr_segment_minmax")
+    return out, arg
+
+
+class _ScatterMinMax(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, src, dim_size, csr, maximum):
+        y = src.reshape(src.shape[0], math.prod(src.shape[1:]))
+        out, arg = segment_minmax_csr(y, csr.indptr, csr.perm, maximum)
+        ctx.save_for_backward(arg)
+        ctx.src_shape = tuple(src.shape)
+        ctx.mark_non_differentiable(arg)
+        tail = tuple(src.shape[1:])
+        return out.reshape((dim_size,) + tail), arg.reshape((dim_size,) + tail)
+
+    @staticmethod
+    def backward(ctx, g, _g_arg):
+        # torch_scatter's rule: the output's gradient goes to the element that attained it; untouched
+        # outputs (arg = E) send theirs to a row past the end, which is cut off.  Every edge belongs to one
+        # segment, so no two outputs of a feature share a target: the scatter is a permutation.
+        (arg,) = ctx.saved_tensors
+        e = ctx.src_shape[0]
+        g2 = g.reshape(g.shape[0], math.prod(g.shape[1:]))
+        grad = torch.zeros((e + 1, g2.shape[1]), dtype=g.dtype, device=g.device)
+        grad.scatter_(0, arg.reshape(g2.shape), g2)
+        return grad[:e].reshape(ctx.src_shape), None, None, None
+
+
+def _scatter_minmax(src, index, dim, out, dim_size, csr, maximum, name):
+    if out is not None:
+        raise NotImplementedError(f"{name}: `out` is not on the reference path (core/molecular_encoder.py:214)")
+    if dim not in (0, -src.dim()):
+        raise NotImplementedError(f"{name}: only dim=0 (edge -> node rows) is on the reference path")
+    index = _as_index(index, "index")
+    if index.dim() != 1 or index.numel() != src.shape[0]:
+        raise ValueError("index must be 1-D with one entry per row of src")
+    if dim_size is None:
+        dim_size = int(index.max()) + 1 if index.numel() else 0
+    if csr is None:
+        csr = CSR.build(index, dim_size)
+    elif csr.num_nodes != dim_size:
+        raise ValueError("csr was built for another dim_size")
+    return _ScatterMinMax.apply(src, dim_size, csr, maximum)
+
+
+def scatter_min(src: torch.Tensor, index: torch.Tensor, dim: int = 0, out: torch.Tensor | None = None,
+                dim_size: int | None = None, csr: CSR | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """``torch_scatter.scatter_min(src, index, dim=0, dim_size=...)`` -> (out, argmin), as the encoder takes
+    each node's closest close-range neighbour distance (core/molecular_encoder.py:214): out[n] = the minimum
+    of src[e] over edges with index[e] == n, argmin[n] the edge attaining it (the lowest edge id on a tie;
+    the reference's GPU kernel keeps any tied edge), 0 and src.shape[0] where no edge of n has a value below
+    the dtype's largest finite value (torch_scatter's start).  On the deterministic CSR; src is [E] or
+    [E, ...] float32 / bfloat16 on the device; edges with an index outside [0, dim_size) are dropped.
+    Differentiable in src: the gradient of out[n] goes to src[argmin[n]]."""
+    return _scatter_minmax(src, index, dim, out, dim_size, csr, False, "scatter_min")
+
+
+def scatter_max(src: torch.Tensor, index: torch.Tensor, dim: int = 0, out: torch.Tensor | None = None,
+                dim_size: int | None = None, csr: CSR | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """``torch_scatter.scatter_max`` -> (out, argmax): :func:`scatter_min` with the maximum (start: the
+    dtype's lowest finite value)."""
+    return _scatter_minmax(src, index, dim, out, dim_size, csr, True, "scatter_max")
 
 
 class _EdgeTokenLinear(torch.autograd.Function):

@@ -37,6 +37,11 @@ torch_geometric and torch_scatter are absent):
   edges.edge_gather / csr_build / segment_sum
       bitwise copy identities; numpy stable argsort + bincount; constant rows
       give degree * value exactly; fp64 index_add agrees to rounding.
+  edges.scatter_minmax (torch_scatter 2.1's scatter_min / scatter_max)
+      the literal sequential update and the vectorised form agree bit for
+      bit (ties, NaN, +-inf, the largest finite value, -0, dropped indices);
+      values equal torch.scatter_reduce amin / amax; args by brute force;
+      the scatter_max example of torch_scatter's documentation.
   modules (MAB / MABFlashVarlen / SAB / PMA / SmallMLP / LN / blocks)
       closed forms: fc_q = 0 gives uniform attention, whose output is the
       key-mean of V = fc_v(K) (esa/mha.py:55) or fc_v(fc_k(K))

@@ -68,7 +68,78 @@ def edge_gather_torch(x: torch.Tensor, src: torch.Tensor, dst: torch.Tensor) -> 
     return torch.cat((x[src], x[dst]), 1)
 
 
+def scatter_min_torch(y: torch.Tensor, index: torch.Tensor, num_nodes: int) -> torch.Tensor:
+    """The values of scatter_min(y, index, dim=0, dim_size=num_nodes) (core/molecular_encoder.py:214) for
+    finite y as torch's scatter_reduce('amin') on the CPU (nodes without edges 0): the CPU baseline of the
+    segmented minimum."""
+    return y.new_zeros(num_nodes).scatter_reduce_(0, index, y, "amin", include_self=False)
+
+
 def scatter_sum_torch(y: torch.Tensor, index: torch.Tensor, num_nodes: int) -> torch.Tensor:
     """scatter_add of edge rows to nodes (core/molecular_encoder.py:241-242) as torch's index_add_ on the
     CPU: the CPU baseline of the segment sum."""
     return y.new_zeros((num_nodes,) + tuple(y.shape[1:])).index_add_(0, index, y)
+
+
+# torch_scatter's scatter_min / scatter_max (core/molecular_encoder.py:6,214; GET/get_clean/tools.py:110) --
+# torch_scatter is absent here and unpinned by the reference (GET/env.yml: pyg::pytorch-scatter beside
+# pytorch 1.13.1, the 2.1 series).  Its published CPU algorithm for dim 0 without `out`: out filled with the
+# reduction's start value (numeric_limits::max() for the minimum, lowest() for the maximum) and arg with
+# src.size(0); elements visited in ascending index, each replacing out[index[e]] and arg[index[e]] when
+# strictly smaller (larger); finally out == start is set to 0.  Its CUDA kernel computes the same out by
+# atomics and sets arg to any e whose value equals out.
+def _rows(y) -> np.ndarray:
+    y = np.asarray(y, np.float32)
+    return y.reshape(-1, 1) if y.ndim == 1 else y.reshape(y.shape[0], int(np.prod(y.shape[1:])))
+
+
+_START = {"float32": float(np.finfo(np.float32).max), "bfloat16": float(np.uint32(0x7F7F0000).view(np.float32))}
+
+
+def scatter_minmax_loop(y: np.ndarray, index: np.ndarray, dim_size: int, maximum: bool = False,
+                        dtype: str = "float32") -> tuple[np.ndarray, np.ndarray]:
+    """The CPU algorithm above, literally, on [E] or [E, F] values (small inputs): (out, arg).
+    Indices outside [0, dim_size) are skipped (the library drops them)."""
+    y2 = _rows(y)
+    e_n, f_n = y2.shape
+    start = -_START[dtype] if maximum else _START[dtype]
+    out = np.full((dim_size, f_n), start, np.float32)
+    arg = np.full((dim_size, f_n), e_n, np.int64)
+    for e in range(e_n):
+        n = int(index[e])
+        if not 0 <= n < dim_size:
+            continue
+        for f in range(f_n):
+            v = y2[e, f]
+            if (v > out[n, f]) if maximum else (v < out[n, f]):
+                out[n, f] = v
+                arg[n, f] = e
+    out[out == np.float32(start)] = 0.0
+    return out, arg
+
+
+def scatter_minmax(y: np.ndarray, index: np.ndarray, dim_size: int, maximum: bool = False,
+                   dtype: str = "float32") -> tuple[np.ndarray, np.ndarray]:
+    """scatter_minmax_loop vectorised (any size): per (node, feature) the first edge, in ascending e, of
+    those with the extreme value among the values strictly below (above) the start -- the element the
+    sequential strict update keeps; NaN never compares below the start.  out is that edge's value."""
+    y2 = _rows(y)
+    e_n, f_n = y2.shape
+    idx = np.asarray(index, np.int64)
+    start = np.float32(-_START[dtype] if maximum else _START[dtype])
+    out = np.zeros((dim_size, f_n), np.float32)
+    arg = np.full((dim_size, f_n), e_n, np.int64)
+    valid = (idx >= 0) & (idx < dim_size)
+    for f in range(f_n):
+        v = y2[:, f]
+        ok = valid & ((v > start) if maximum else (v < start))
+        e_ok = np.nonzero(ok)[0]
+        if e_ok.size == 0:
+            continue
+        n_ok, v_ok = idx[e_ok], v[e_ok]
+        order = np.lexsort((e_ok, -v_ok if maximum else v_ok, n_ok))
+        n_sorted = n_ok[order]
+        first = order[np.concatenate([[True], n_sorted[1:] != n_sorted[:-1]])]
+        arg[n_ok[first], f] = e_ok[first]
+        out[n_ok[first], f] = v_ok[first]
+    return out, arg

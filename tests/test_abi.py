@@ -20,6 +20,20 @@ def test_header_declares_entry_points():
     assert len(names) >= 10
 
 
+def test_profile_kernel_count_matches_the_header():
+    """The Python hook's buffer size is the header's ESA_PROFILE_KERNELS, and every id has a name."""
+    import re
+    from mind_amd import _lib
+    text = (Path(__file__).resolve().parents[1] / "include" / "esa_hip.h").read_text()
+    assert int(re.search(r"#define ESA_PROFILE_KERNELS (\d+)", text).group(1)) == _lib.PROFILE_KERNELS
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("library not built")
+    lib = _lib.load()
+    names = [lib.esa_profile_kernel_name(i).decode() for i in range(_lib.PROFILE_KERNELS)]
+    assert all(names) and len(set(names)) == len(names) and lib.esa_profile_kernel_name(_lib.PROFILE_KERNELS) == b""
+    assert "segment_minmax" in names
+
+
 def test_library_exports_every_declared_symbol():
     from mind_amd import _lib
     if not _lib.LIB_PATH.exists():
@@ -84,6 +98,12 @@ def test_argument_errors_need_no_gpu():
         assert rc == -9, p
     assert lib.esa_edge_gather(16, 16, 16, 10, 10, 8, 7, 16, None) == -5
     assert lib.esa_csr_workspace_size(-1, 10, ctypes.byref(n)) == -2
+    # segmented min / max: null, shape and dtype errors before any launch; no nodes is a no-op
+    assert lib.esa_csr_segment_minmax(16, None, None, 10, 1, f32, 0, 5, 16, 16, None) == -1
+    assert lib.esa_csr_segment_minmax(16, None, 16, 10, 0, f32, 0, 5, 16, 16, None) == -2
+    assert lib.esa_csr_segment_minmax(16, None, 16, 10, 1, f32, 1, -1, 16, 16, None) == -2
+    assert lib.esa_csr_segment_minmax(16, None, 16, 10, 1, 7, 0, 5, 16, 16, None) == -5
+    assert lib.esa_csr_segment_minmax(16, None, 16, 0, 1, bf16, 1, 5, 16, None, None) == 0
     # node plan: size errors, and a planned backward needs only its row statistics
     node, node_plan = _lib.ESA_MASK_NODE, _lib.ESA_MASK_NODE_PLAN
     assert lib.esa_node_plan_size(100, 100, -1, ctypes.byref(n)) == -2
