@@ -42,12 +42,30 @@
 
 namespace {
 
-// Partners per step: their K / V (or Q / dO) rows are loaded together.  Two
-// at 4 dims per lane keeps every kernel at 8 waves per SIMD (1, 4 and 8
-// measured slower).  At 8 dims per lane (dim 512): two for the forward and dQ
-// (8 and 7 waves per SIMD; one measured 9 % and 2 % slower), one for dK / dV
-// (66 VGPRs, 7 waves; two, at 85 VGPRs and 5 waves, measured 3 % slower).
-template <int N, bool KEY_SIDE> constexpr int partners_per_step() { return N == 8 && KEY_SIDE ? 1 : 2; }
+// Partners per step: their K / V (or Q / dO) rows are loaded together; the
+// partner indices come from registers (CsrSrc), so a step's row loads wait on
+// no index load.  At 4 dims per lane (16 heads of 16, bf16): four for the
+// forward and dQ (two: 1-2 % slower, three: 10 % slower), two for dK / dV
+// (four: 6 % slower); fp32 rows take two (four would cost the forward and dQ
+// their eighth wave per SIMD).  At 8 dims per lane (dim 512): two everywhere
+// (one: forward 9 %, dQ 2 %, dK / dV 3 % slower).  Build-time overrides for
+// measurement.
+#ifndef ESA_NODE_G4
+#define ESA_NODE_G4 4
+#endif
+#ifndef ESA_NODE_G4K
+#define ESA_NODE_G4K 2
+#endif
+#ifndef ESA_NODE_G8
+#define ESA_NODE_G8 2
+#endif
+#ifndef ESA_NODE_G8K
+#define ESA_NODE_G8K 2
+#endif
+template <typename T, int N, bool KEY_SIDE> constexpr int partners_per_step() {
+  return N == 8 ? (KEY_SIDE ? ESA_NODE_G8K : ESA_NODE_G8)
+                : (KEY_SIDE || sizeof(T) != 2 ? ESA_NODE_G4K : ESA_NODE_G4);
+}
 
 template <typename T> struct Row4;
 template <> struct Row4<float> { typedef f32x4 type; };
@@ -188,18 +206,31 @@ DEVI int wave_token() {
 // state is wave-uniform; a copy restarts the walk (one per head pass).
 
 // A CSR row [p, pb): entries in [lo, hi), each once (an entry equal to its
-// predecessor is a repeat).
+// predecessor is a repeat).  The row is read 64 entries at a time by one
+// vector load (lane l holds entry base + l) and a step takes its entries by
+// readlane, so the partner rows of a step wait on no index load of their own.
 struct CsrSrc {
-  const int* list; int p, pb, lo, hi, prev;
+  const int* list; int p, pb, lo, hi, prev, base, blk;
+  DEVI void fill() {
+    const int i = base + (int)(threadIdx.x & 63);
+    blk = i < pb ? list[i] : 0;
+  }
   template <int G>
   DEVI bool next(int (&j)[G], bool (&ok)[G]) {
     if (p >= pb) return false;
 #pragma unroll
     for (int u = 0; u < G; ++u) {
-      const int pp = min(p + u, pb - 1);
-      const int x = list[pp];
-      ok[u] = p + u < pb && x >= lo && x < hi && x != prev;
-      if (p + u < pb) prev = x;
+      const int pp = p + u;
+      int x = prev;
+      if (pp < pb) {
+        if (pp >= base + 64) {   // wave-uniform: the next 64 entries
+          base += 64;
+          fill();
+        }
+        x = __builtin_amdgcn_readlane(blk, pp - base);
+      }
+      ok[u] = pp < pb && x >= lo && x < hi && x != prev;
+      if (pp < pb) prev = x;
       j[u] = ok[u] ? x : lo;
     }
     p += G;
@@ -290,7 +321,7 @@ DEVI WalkSrc walk_src(const GraphEdgeLists& e, int2 bounds, int t) {
 
 template <typename T, int HD, int N, bool DROP, class Src>
 DEVI void fwd_token(const GraphAttnArgs& a, int t, const Src& src0) {
-  constexpr int L = HeadLanes<HD, N>::L, HPP = HeadLanes<HD, N>::HPP, G = partners_per_step<N, false>();
+  constexpr int L = HeadLanes<HD, N>::L, HPP = HeadLanes<HD, N>::HPP, G = partners_per_step<T, N, false>();
   const T* __restrict__ q = static_cast<const T*>(a.q);
   const T* __restrict__ k = static_cast<const T*>(a.k);
   const T* __restrict__ v = static_cast<const T*>(a.v);
@@ -352,7 +383,7 @@ DEVI void fwd_token(const GraphAttnArgs& a, int t, const Src& src0) {
 // D_i = rowsum(dO_i * O_i) per head for the dK / dV pass.
 template <typename T, int HD, int N, bool DROP, class Src>
 DEVI void dq_token(const GraphAttnArgs& a, int t, const Src& src0) {
-  constexpr int L = HeadLanes<HD, N>::L, HPP = HeadLanes<HD, N>::HPP, G = partners_per_step<N, false>();
+  constexpr int L = HeadLanes<HD, N>::L, HPP = HeadLanes<HD, N>::HPP, G = partners_per_step<T, N, false>();
   const T* __restrict__ q = static_cast<const T*>(a.q);
   const T* __restrict__ k = static_cast<const T*>(a.k);
   const T* __restrict__ v = static_cast<const T*>(a.v);
@@ -406,7 +437,7 @@ DEVI void dq_token(const GraphAttnArgs& a, int t, const Src& src0) {
 // queries i that attend to key j (ascending).
 template <typename T, int HD, int N, bool DROP, class Src>
 DEVI void dkdv_token(const GraphAttnArgs& a, int t, const Src& src0) {
-  constexpr int L = HeadLanes<HD, N>::L, HPP = HeadLanes<HD, N>::HPP, G = partners_per_step<N, true>();
+  constexpr int L = HeadLanes<HD, N>::L, HPP = HeadLanes<HD, N>::HPP, G = partners_per_step<T, N, true>();
   const T* __restrict__ q = static_cast<const T*>(a.q);
   const T* __restrict__ k = static_cast<const T*>(a.k);
   const T* __restrict__ v = static_cast<const T*>(a.v);
@@ -460,7 +491,11 @@ DEVI void dkdv_token(const GraphAttnArgs& a, int t, const Src& src0) {
   }
 }
 
-DEVI CsrSrc csr_src(const int* list, int4 d) { return CsrSrc{list, d.z, d.w, d.x, d.y, INT_MIN}; }
+DEVI CsrSrc csr_src(const int* list, int4 d) {
+  CsrSrc s{list, d.z, d.w, d.x, d.y, INT_MIN, d.z, 0};
+  s.fill();
+  return s;
+}
 
 // The kernels: node mode over a CSR (the key pass over the transposed CSR).
 template <typename T, int HD, int N, bool DROP>
