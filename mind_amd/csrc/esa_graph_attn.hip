@@ -240,22 +240,28 @@ struct CsrSrc {
 
 // An edge-mask plan's list for one token: the entries of its tile's list
 // whose mask bit the token has set, in list (= ascending token) order.  Word
-// c of the token's mask bits is held by lane c (at most kListCap / 32 words).
+// c of the token's mask bits is held by lane c (at most kListCap / 32 words);
+// the 32 ids of word c's entries are held by lanes 0..31 (one vector load per
+// word) and taken by readlane, so no partner waits on an id load of its own.
 struct ListSrc {
-  const int* ids; uint32_t words; int nct, c; uint32_t w; int fallback;
+  const int* ids; uint32_t words; int nct, c; uint32_t w; int fallback, idv;
+  DEVI void fetch() { idv = ids[32 * c + (int)(threadIdx.x & 31)]; }
   template <int G>
   DEVI bool next(int (&j)[G], bool (&ok)[G]) {
     bool any = false;
 #pragma unroll
     for (int u = 0; u < G; ++u) {
-      while (w == 0u && c + 1 < nct) {
-        ++c;
-        w = (uint32_t)__builtin_amdgcn_readlane((int)words, c);
+      if (w == 0u && c + 1 < nct) {   // wave-uniform: the next word with a set bit
+        do {
+          ++c;
+          w = (uint32_t)__builtin_amdgcn_readlane((int)words, c);
+        } while (w == 0u && c + 1 < nct);
+        fetch();
       }
       ok[u] = w != 0u;
       j[u] = fallback;
       if (ok[u]) {
-        j[u] = ids[32 * c + __builtin_ctz(w)];
+        j[u] = __builtin_amdgcn_readlane(idv, __builtin_ctz(w));
         w &= w - 1u;
         any = true;
       }
@@ -272,6 +278,8 @@ DEVI ListSrc list_src(const GraphEdgeLists& e, int d, int t, int n) {
   s.c = 0;
   s.w = s.nct > 0 ? (uint32_t)__builtin_amdgcn_readlane((int)s.words, 0) : 0u;
   s.fallback = t;
+  s.idv = 0;
+  if (s.nct > 0) s.fetch();
   return s;
 }
 
