@@ -143,7 +143,11 @@ ESA_API int esa_edge_plan_build(const int* tok_src, const int* tok_dst,
 /* the cu_seqlens are unchanged; calls pass the same indptr as mask_a, the   */
 /* same cu_seqlens, and the total_q, total_k and n_mask_edges it was built   */
 /* with (the call locates the plan's sections from them; the plan is not     */
-/* read back to check).                                                      */
+/* read back to check).  With one cu_seqlens pointer for queries and keys    */
+/* and total_q == total_k, a CSR that is its own transpose (ascending rows,  */
+/* each entry (i, j) matched by as many (j, i); undirected graphs) is found  */
+/* so on the device and copied instead of sorted: the same plan, fewer       */
+/* cycles.                                                                   */
 /* ------------------------------------------------------------------------ */
 ESA_API int esa_node_plan_size(int total_q, int total_k, int n_mask_edges, size_t* bytes);
 ESA_API int esa_node_plan_build(const int* indptr, const int* indices,

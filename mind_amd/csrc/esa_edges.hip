@@ -10,6 +10,7 @@
 #include <algorithm>
 
 #include "esa_common.h"
+#include "esa_csr.h"
 #include "esa_profile.h"
 #include "../../include/esa_hip.h"
 
@@ -323,6 +324,10 @@ DEVI int xcd_tile(int b, int ntiles) {
   return x * q + min(x, rem) + s;
 }
 
+// A CSR build the caller has made unnecessary (a device flag it set) skips
+// every launch: each block returns before touching memory.
+DEVI bool skipped(const int* skip) { return skip && *skip; }
+
 // One row of hist: the digit counts of the tile.  PAIRS: the input is (key, id)
 // pairs; else the caller's keys (clamped).  Digit order inside the tile is
 // irrelevant here, so full tiles read 16-byte vectors.
@@ -331,7 +336,9 @@ DEVI int xcd_tile(int b, int ntiles) {
 template <bool PAIRS>
 __global__ __launch_bounds__(kSortThreads) void radix_hist_kernel(const int* __restrict__ in, long n, int num_nodes,
                                                                  int shift, bool vec, int* __restrict__ hist,
-                                                                 int* __restrict__ fill, long fill_n) {
+                                                                 int* __restrict__ fill, long fill_n,
+                                                                 const int* __restrict__ skip) {
+  if (skipped(skip)) return;
   __shared__ int h[kRadixBins];
   const int tid = threadIdx.x;
   h[tid] = 0;
@@ -385,7 +392,8 @@ constexpr int kHistChunk = 64;
 int hist_chunks(int ntiles) { return (ntiles + kHistChunk - 1) / kHistChunk; }
 
 __global__ __launch_bounds__(kRadixBins) void hist_chunk_sum_kernel(const int* __restrict__ hist, int ntiles,
-                                                                   int* __restrict__ part) {
+                                                                   int* __restrict__ part, const int* __restrict__ skip) {
+  if (skipped(skip)) return;
   const int b0 = blockIdx.x * kHistChunk, tid = threadIdx.x;
   int x[kHistChunk];
 #pragma unroll
@@ -396,7 +404,9 @@ __global__ __launch_bounds__(kRadixBins) void hist_chunk_sum_kernel(const int* _
   part[(long)blockIdx.x * kRadixBins + tid] = s;
 }
 
-__global__ __launch_bounds__(4 * kRadixBins) void hist_chunk_scan_kernel(int* __restrict__ part, int nchunks) {
+__global__ __launch_bounds__(4 * kRadixBins) void hist_chunk_scan_kernel(int* __restrict__ part, int nchunks,
+                                                                        const int* __restrict__ skip) {
+  if (skipped(skip)) return;
   // thread: digit d, quarter q of the chunks
   __shared__ int qsum[4][kRadixBins];
   __shared__ int wtot[4][kRadixBins / 64];
@@ -435,7 +445,9 @@ __global__ __launch_bounds__(4 * kRadixBins) void hist_chunk_scan_kernel(int* __
 }
 
 __global__ __launch_bounds__(kRadixBins) void hist_chunk_apply_kernel(int* __restrict__ hist, int ntiles,
-                                                                     const int* __restrict__ part) {
+                                                                     const int* __restrict__ part,
+                                                                     const int* __restrict__ skip) {
+  if (skipped(skip)) return;
   const int b0 = blockIdx.x * kHistChunk, tid = threadIdx.x;
   int x[kHistChunk];
 #pragma unroll
@@ -453,7 +465,9 @@ __global__ __launch_bounds__(kRadixBins) void hist_chunk_apply_kernel(int* __res
 // the quarters' sums and the digit totals' exclusive scan go through LDS.
 constexpr int kSmallScanTiles = 4 * kHistChunk;
 
-__global__ __launch_bounds__(4 * kRadixBins) void hist_scan_small_kernel(int* __restrict__ hist, int ntiles) {
+__global__ __launch_bounds__(4 * kRadixBins) void hist_scan_small_kernel(int* __restrict__ hist, int ntiles,
+                                                                        const int* __restrict__ skip) {
+  if (skipped(skip)) return;
   __shared__ int qsum[4][kRadixBins];
   __shared__ int wtot[kRadixBins / 64];
   const int d = threadIdx.x & (kRadixBins - 1), q = threadIdx.x / kRadixBins;
@@ -528,7 +542,9 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(const int* 
                                                                     int num_nodes, int shift, bool vec,
                                                                     const int* __restrict__ offsets,
                                                                     int* __restrict__ out,
-                                                                    int* __restrict__ vals_out) {
+                                                                    int* __restrict__ vals_out,
+                                                                    const int* __restrict__ skip) {
+  if (skipped(skip)) return;
   constexpr int kWaves = kSortThreads / 64;
   constexpr int kWaveItems = kSortItems * 64;
   __shared__ int gbase[kRadixBins];         // output slot of the tile's local slot 0, per digit
@@ -652,12 +668,14 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(const int* 
 // owns boundaries [4t, 4t + 4).
 constexpr int kGapFill = 64;
 
-__global__ void fill_int_kernel(int* __restrict__ p, long n, int value) {
+__global__ void fill_int_kernel(int* __restrict__ p, long n, int value, const int* __restrict__ skip) {
+  if (skipped(skip)) return;
   for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) p[i] = value;
 }
 
 __global__ __launch_bounds__(256) void indptr_runs_kernel(const int* __restrict__ s, long n, int num_nodes,
-                                                         int* __restrict__ indptr) {
+                                                         int* __restrict__ indptr, const int* __restrict__ skip) {
+  if (skipped(skip)) return;
   const long t = (long)blockIdx.x * blockDim.x + threadIdx.x;
   const long i0 = 4 * t;
   if (i0 > n) return;
@@ -688,7 +706,9 @@ __global__ __launch_bounds__(256) void indptr_runs_kernel(const int* __restrict_
 
 // Entries left at -1 (inside a gap longer than kGapFill): the first position
 // whose key is >= j, by binary search.
-__global__ void indptr_gap_kernel(const int* __restrict__ s, long n, int num_nodes, int* __restrict__ indptr) {
+__global__ void indptr_gap_kernel(const int* __restrict__ s, long n, int num_nodes, int* __restrict__ indptr,
+                                  const int* __restrict__ skip) {
+  if (skipped(skip)) return;
   for (long j = (long)blockIdx.x * blockDim.x + threadIdx.x; j <= num_nodes; j += (long)gridDim.x * blockDim.x) {
     if (indptr[j] >= 0) continue;
     long lo = 0, hi = n;
@@ -1322,11 +1342,18 @@ int esa_csr_workspace_size(int64_t num_edges, int num_nodes, size_t* bytes) {
 
 int esa_csr_build(const int* keys, int64_t num_edges, int num_nodes, int* indptr, int* perm, void* workspace,
                   size_t workspace_bytes, void* stream) {
+  return csr_build_impl(keys, num_edges, num_nodes, indptr, perm, workspace, workspace_bytes,
+                        reinterpret_cast<hipStream_t>(stream), nullptr);
+}
+
+}  // extern "C"
+
+int csr_build_impl(const int* keys, int64_t num_edges, int num_nodes, int* indptr, int* perm, void* workspace,
+                   size_t workspace_bytes, hipStream_t st, const int* skip) {
   if (!indptr || !workspace || (num_edges > 0 && (!keys || !perm))) return ESA_ERR_NULL;
   if (num_edges < 0 || num_nodes < 0 || num_edges >= (1LL << 31)) return ESA_ERR_SHAPE;
   const CsrWs w = csr_ws(num_edges, num_nodes);
   if (workspace_bytes < w.total) return ESA_ERR_WORKSPACE;
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
   ESA_TIMED(esa_profile::kCsrBuild, st, {
     const int* sorted = nullptr;
@@ -1346,37 +1373,39 @@ int esa_csr_build(const int* keys, int64_t num_edges, int num_nodes, int* indptr
         int* out = last ? skeys : pairs[p & 1];
         if (first)
           hipLaunchKernelGGL(radix_hist_kernel<false>, dim3(ntiles), dim3(kSortThreads), 0, st, in,
-                             (long)num_edges, num_nodes, shift, vec_keys, hist, indptr, (long)num_nodes + 1);
+                             (long)num_edges, num_nodes, shift, vec_keys, hist, indptr, (long)num_nodes + 1, skip);
         else
           hipLaunchKernelGGL(radix_hist_kernel<true>, dim3(ntiles), dim3(kSortThreads), 0, st, in,
-                             (long)num_edges, num_nodes, shift, true, hist, nullptr, 0L);
+                             (long)num_edges, num_nodes, shift, true, hist, nullptr, 0L, skip);
         if (ntiles <= kSmallScanTiles) {
-          hipLaunchKernelGGL(hist_scan_small_kernel, dim3(1), dim3(4 * kRadixBins), 0, st, hist, ntiles);
+          hipLaunchKernelGGL(hist_scan_small_kernel, dim3(1), dim3(4 * kRadixBins), 0, st, hist, ntiles, skip);
         } else {
-          hipLaunchKernelGGL(hist_chunk_sum_kernel, dim3(nchunks), dim3(kRadixBins), 0, st, hist, ntiles, part);
-          hipLaunchKernelGGL(hist_chunk_scan_kernel, dim3(1), dim3(4 * kRadixBins), 0, st, part, nchunks);
+          hipLaunchKernelGGL(hist_chunk_sum_kernel, dim3(nchunks), dim3(kRadixBins), 0, st, hist, ntiles, part, skip);
+          hipLaunchKernelGGL(hist_chunk_scan_kernel, dim3(1), dim3(4 * kRadixBins), 0, st, part, nchunks, skip);
           hipLaunchKernelGGL(hist_chunk_apply_kernel, dim3(nchunks), dim3(kRadixBins), 0, st, hist, ntiles,
-                             part);
+                             part, skip);
         }
         auto scatter = first ? (last ? radix_scatter_kernel<false, false> : radix_scatter_kernel<false, true>)
                              : (last ? radix_scatter_kernel<true, false> : radix_scatter_kernel<true, true>);
         hipLaunchKernelGGL(scatter, dim3(ntiles), dim3(kSortThreads), 0, st, in, (long)num_edges, num_nodes,
-                           shift, !first || vec_keys, hist, out, perm);
+                           shift, !first || vec_keys, hist, out, perm, skip);
       }
       sorted = skeys;
     }
     // indptr: the boundaries of the sorted keys' runs (set to -1 by the first histogram pass)
     if (num_edges == 0)
       hipLaunchKernelGGL(fill_int_kernel, dim3(grid_for((long)num_nodes + 1, 256, 4096)), dim3(256), 0, st, indptr,
-                         (long)num_nodes + 1, -1);
+                         (long)num_nodes + 1, -1, skip);
     hipLaunchKernelGGL(indptr_runs_kernel, dim3(grid_for(num_edges / 4 + 1, 256)), dim3(256), 0, st, sorted,
-                       (long)num_edges, num_nodes, indptr);
+                       (long)num_edges, num_nodes, indptr, skip);
     hipLaunchKernelGGL(indptr_gap_kernel, dim3(grid_for((long)num_nodes + 1, 256, 4096)), dim3(256), 0, st,
-                       sorted, (long)num_edges, num_nodes, indptr);
+                       sorted, (long)num_edges, num_nodes, indptr, skip);
   });
   ESA_LAUNCH_CHECK();
   return ESA_OK;
 }
+
+extern "C" {
 
 int esa_csr_segment_sum(const void* y, const int* perm, const int* indptr, int num_nodes, int features, int dtype,
                         void* out, void* stream) {

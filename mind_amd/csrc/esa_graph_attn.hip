@@ -36,6 +36,7 @@
 // it, and the outputs carry the 1 / (1 - p) factor; the softmax statistics
 // are those of the undropped scores.
 #include "esa_common.h"
+#include "esa_csr.h"
 #include "esa_graph_attn.h"
 #include "esa_profile.h"
 #include "../../include/esa_hip.h"
@@ -556,20 +557,55 @@ __global__ __launch_bounds__(256) void graph_edge_dkdv_kernel(const GraphAttnArg
   graph_edge_pass<T, HD, N, DROP, 2>(a);
 }
 
-// row_of[e] = the CSR row holding entry e (-1 for an entry no row covers).
-__global__ void fill_minus_one_kernel(int* __restrict__ p, long n) {
+// row_of[e] = the CSR row holding entry e (-1 for an entry no row covers);
+// with `sym`, *sym = 1 (the query pass clears it when the CSR is not its own
+// transpose).
+__global__ void fill_minus_one_kernel(int* __restrict__ p, long n, int* __restrict__ sym) {
+  if (sym && blockIdx.x == 0 && threadIdx.x == 0) *sym = 1;
   for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) p[i] = -1;
 }
-// Per query token t: row_of over its row, and its descriptor.
-__global__ void query_rows_kernel(const int* __restrict__ indptr, const int* __restrict__ cu_q,
-                                  const int* __restrict__ cu_k, int nseg, int total_q, int total_k, int nnz,
-                                  int* __restrict__ row_of, int4* __restrict__ q_desc) {
+// Per query token t: row_of over its row, and its descriptor.  With `sym`
+// (one segment array, as many queries as keys): clears *sym unless the CSR
+// equals its transpose as far as row t shows -- its bounds in order (row 0
+// from 0, the last row to nnz), its entries keys in [0, total_k) in
+// ascending order, and each entry (t, x), the r-th of equal ones, matched by
+// an r-th entry t in row x (a binary search there; an unsorted row x clears
+// the flag from its own thread).  Over all rows this is a bijection between
+// the entries (t, x) and (x, t) with multiplicity, i.e. indptr = t_indptr and
+// indices = t_rows.
+__global__ void query_rows_kernel(const int* __restrict__ indptr, const int* __restrict__ indices,
+                                  const int* __restrict__ cu_q, const int* __restrict__ cu_k, int nseg, int total_q,
+                                  int total_k, int nnz, int* __restrict__ row_of, int4* __restrict__ q_desc,
+                                  int* __restrict__ sym) {
   const int t = blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= total_q) return;
   int pa, pb;
   csr_row(indptr, t, nnz, pa, pb);
   for (int p = pa; p < pb; ++p) row_of[p] = t;
   q_desc[t] = make_desc(cu_k, total_k, indptr, nnz, seg_of(cu_q, nseg, t), t);
+  if (!sym) return;
+  const int ra = indptr[t], rb = indptr[t + 1];
+  bool ok = ra >= 0 && ra <= rb && rb <= nnz && (t > 0 || ra == 0) && (t + 1 < total_q || rb == nnz);
+  int prev = INT_MIN, rank = 0;
+  for (int p = pa; ok && p < pb; ++p) {
+    const int x = indices[p];
+    if (x < 0 || x >= total_k || x < prev) {
+      ok = false;
+      break;
+    }
+    rank = x == prev ? rank + 1 : 0;
+    prev = x;
+    int lo, hi;
+    csr_row(indptr, x, nnz, lo, hi);
+    const int end = hi;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (indices[mid] < t) lo = mid + 1;
+      else hi = mid;
+    }
+    ok = lo + rank < end && indices[lo + rank] == t;
+  }
+  if (!ok) *sym = 0;
 }
 // Per entry p: t_rows[p] = row_of[t_perm[p]], the query row of each
 // transposed entry, and the plan's copy of the indices; per key token t (the
@@ -578,7 +614,8 @@ __global__ void key_rows_kernel(const int* __restrict__ t_perm, const int* __res
                                 int* __restrict__ t_rows, const int* __restrict__ indices,
                                 int* __restrict__ indices_copy, const int* __restrict__ t_indptr,
                                 const int* __restrict__ cu_q, const int* __restrict__ cu_k, int nseg, int total_q,
-                                int total_k, int4* __restrict__ k_desc) {
+                                int total_k, int4* __restrict__ k_desc, const int* __restrict__ sym) {
+  if (sym && *sym) return;   // symmetric: sym_copy_kernel writes the transpose
   for (long p = (long)blockIdx.x * blockDim.x + threadIdx.x; p < max(nnz, total_k);
        p += (long)gridDim.x * blockDim.x) {
     if (p < nnz) {
@@ -586,6 +623,26 @@ __global__ void key_rows_kernel(const int* __restrict__ t_perm, const int* __res
       if (indices_copy) indices_copy[p] = indices[p];
     }
     if (p < total_k) k_desc[p] = make_desc(cu_q, total_q, t_indptr, nnz, seg_of(cu_k, nseg, (int)p), (int)p);
+  }
+}
+
+// A symmetric CSR (*sym set by the query pass) is its own transpose:
+// t_indptr = indptr, t_rows = indices and, with one segment array, each key's
+// descriptor is its query descriptor; plus the plan's copy of the indices.
+__global__ void sym_copy_kernel(const int* __restrict__ sym, const int* __restrict__ indptr,
+                                const int* __restrict__ indices, const int4* __restrict__ q_desc, int nnz,
+                                int total_k, int* __restrict__ t_indptr, int* __restrict__ t_rows,
+                                int4* __restrict__ k_desc, int* __restrict__ indices_copy) {
+  if (!*sym) return;
+  const long n = max((long)nnz, (long)total_k + 1);
+  for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) {
+    if (i < nnz) {
+      const int x = indices[i];
+      t_rows[i] = x;
+      if (indices_copy) indices_copy[i] = x;
+    }
+    if (i <= total_k) t_indptr[i] = indptr[i];
+    if (i < total_k) k_desc[i] = q_desc[i];
   }
 }
 
@@ -597,7 +654,7 @@ size_t al256(size_t x) { return (x + 255) & ~size_t(255); }
 // (q_desc [total_q]) and keys (k_desc [total_k]), then the build's scratch
 // (row_of, t_perm and the CSR sort's workspace).  The per-call backward lays
 // the same arrays and scratch out in its workspace.
-struct NodePlan { size_t indices, t_indptr, t_rows, q_desc, k_desc, row_of, t_perm, csr, csr_bytes, total; };
+struct NodePlan { size_t indices, t_indptr, t_rows, q_desc, k_desc, row_of, t_perm, sym, csr, csr_bytes, total; };
 
 int node_plan_layout(int total_q, int total_k, int nnz, NodePlan& w) {
   w = NodePlan{};
@@ -611,6 +668,7 @@ int node_plan_layout(int total_q, int total_k, int nnz, NodePlan& w) {
   w.k_desc = off; off += al256((size_t)total_k * 16 + 16);
   w.row_of = off; off += al256((size_t)nnz * 4 + 4);
   w.t_perm = off; off += al256((size_t)nnz * 4 + 4);
+  w.sym = off; off += 256;
   w.csr = off; off += al256(w.csr_bytes);
   w.total = off;
   return ESA_OK;
@@ -627,22 +685,34 @@ int build_transposed(const int* indptr, const int* indices, const int* cu_q, con
   int* row_of = reinterpret_cast<int*>(base + w.row_of);
   int* t_perm = reinterpret_cast<int*>(base + w.t_perm);
   int* t_indptr = reinterpret_cast<int*>(base + w.t_indptr);
+  int* t_rows = reinterpret_cast<int*>(base + w.t_rows);
+  int4* q_desc = reinterpret_cast<int4*>(base + w.q_desc);
+  int4* k_desc = reinterpret_cast<int4*>(base + w.k_desc);
+  int* indices_copy = copy_indices ? reinterpret_cast<int*>(base + w.indices) : nullptr;
+  // One segment array and as many queries as keys: the query pass tests whether the CSR is its own
+  // transpose (a device flag, no host synchronisation); if it is, the sort's and the key pass's launches
+  // return at once and sym_copy_kernel copies the CSR into the transposed sections.
+  int* sym = (cu_q == cu_k && total_q == total_k && nnz > 0) ? reinterpret_cast<int*>(base + w.sym) : nullptr;
   if (nnz > 0) {
-    hipLaunchKernelGGL(fill_minus_one_kernel, dim3(grid_of(nnz)), dim3(256), 0, st, row_of, (long)nnz);
+    hipLaunchKernelGGL(fill_minus_one_kernel, dim3(grid_of(nnz)), dim3(256), 0, st, row_of, (long)nnz, sym);
     ESA_LAUNCH_CHECK();
   }
   if (total_q > 0) {
-    hipLaunchKernelGGL(query_rows_kernel, dim3((unsigned)((total_q + 255) / 256)), dim3(256), 0, st, indptr, cu_q,
-                       cu_k, nseg, total_q, total_k, nnz, row_of, reinterpret_cast<int4*>(base + w.q_desc));
+    hipLaunchKernelGGL(query_rows_kernel, dim3((unsigned)((total_q + 255) / 256)), dim3(256), 0, st, indptr,
+                       indices, cu_q, cu_k, nseg, total_q, total_k, nnz, row_of, q_desc, sym);
     ESA_LAUNCH_CHECK();
   }
-  int rc = esa_csr_build(indices, nnz, total_k, t_indptr, t_perm, base + w.csr, w.csr_bytes, st);
+  int rc = csr_build_impl(indices, nnz, total_k, t_indptr, t_perm, base + w.csr, w.csr_bytes, st, sym);
   if (rc) return rc;
   if (nnz > 0 || total_k > 0) {
     hipLaunchKernelGGL(key_rows_kernel, dim3(grid_of(nnz > total_k ? nnz : total_k)), dim3(256), 0, st, t_perm,
-                       row_of, nnz, reinterpret_cast<int*>(base + w.t_rows), indices,
-                       copy_indices ? reinterpret_cast<int*>(base + w.indices) : nullptr, t_indptr, cu_q, cu_k,
-                       nseg, total_q, total_k, reinterpret_cast<int4*>(base + w.k_desc));
+                       row_of, nnz, t_rows, indices, indices_copy, t_indptr, cu_q, cu_k, nseg, total_q, total_k,
+                       k_desc, sym);
+    ESA_LAUNCH_CHECK();
+  }
+  if (sym) {
+    hipLaunchKernelGGL(sym_copy_kernel, dim3(grid_of(nnz > total_k + 1 ? nnz : total_k + 1)), dim3(256), 0, st,
+                       sym, indptr, indices, q_desc, nnz, total_k, t_indptr, t_rows, k_desc, indices_copy);
     ESA_LAUNCH_CHECK();
   }
   return ESA_OK;

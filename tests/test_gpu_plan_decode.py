@@ -157,3 +157,58 @@ def test_node_plan_sections(device, which):
         s, n = int(first[b]), int(sizes[b])
         blk = OM.node_adjacency_segment(indptr, indices, s, s + n, s, s + n)
         assert np.array_equal(blk, (bias[b, :n, :n] == 0).numpy())
+
+
+def _csr(rows):
+    ip = np.cumsum([0] + [len(r) for r in rows]).astype(np.int32)
+    ix = np.array([j for r in rows for j in r], dtype=np.int32)
+    return ip, ix
+
+
+@pytest.mark.parametrize("case", ["symmetric", "symmetric_repeats", "repeat_count_differs", "unsorted_row",
+                                  "key_out_of_range", "one_way_edge"])
+def test_node_plan_symmetric_and_general_builds(device, case):
+    """A CSR that equals its own transpose (sorted rows, every entry (i, j) matched by (j, i) as often) is
+    copied into the plan instead of sorted; every other CSR takes the sort.  Either way the sections equal a
+    numpy transpose and the descriptors' closed forms, bit for bit: the cases below sit one entry away from
+    symmetric in each way the test on the device must catch."""
+    rng = np.random.default_rng(17)
+    sizes = [40, 1, 23, 57]
+    cu_np = np.cumsum([0] + sizes)
+    t = int(cu_np[-1])
+    adj = [set() for _ in range(t)]
+    for b, n in enumerate(sizes):
+        s = int(cu_np[b])
+        for _ in range(3 * n):
+            i, j = rng.integers(s, s + n, size=2)
+            if i != j:
+                adj[i].add(int(j))
+                adj[j].add(int(i))
+    rows = [sorted(a) for a in adj]
+    i0 = next(i for i, r in enumerate(rows) if r)
+    j0 = rows[i0][0]
+    if case == "symmetric_repeats":          # the edge (i0, j0) listed twice in both directions
+        rows[i0] = sorted(rows[i0] + [j0])
+        rows[j0] = sorted(rows[j0] + [i0])
+    elif case == "repeat_count_differs":     # twice one way, once the other
+        rows[i0] = sorted(rows[i0] + [j0])
+    elif case == "unsorted_row":             # symmetric as a set, one row out of order
+        r = next(i for i, r in enumerate(rows) if len(r) >= 2)
+        rows[r] = rows[r][::-1]
+    elif case == "key_out_of_range":         # one entry naming key t (past the last token)
+        rows[i0] = rows[i0] + [t]
+    elif case == "one_way_edge":             # (i0, j0) without (j0, i0)
+        rows[j0] = [x for x in rows[j0] if x != i0]
+    ip, ix = _csr(rows)
+    nnz = len(ix)
+    cu = torch.as_tensor(cu_np.astype(np.int32)).to(device)
+    plan = A.node_plan(torch.as_tensor(ip).to(device), torch.as_tensor(ix).to(device), cu)
+    sec = {k: v.cpu().numpy().astype(np.int64) for k, v in A.node_plan_sections(plan, t, t, nnz).items()}
+    t_indptr, t_rows = _numpy_transpose(ip.astype(np.int64), ix.astype(np.int64), t)
+    assert np.array_equal(sec["indices"], ix)
+    assert np.array_equal(sec["t_indptr"], t_indptr)
+    assert np.array_equal(sec["t_rows"][: int(t_indptr[-1])], t_rows)
+    assert np.array_equal(sec["q_desc"], _descriptors(cu_np, cu_np, t, ip.astype(np.int64), nnz))
+    assert np.array_equal(sec["k_desc"], _descriptors(cu_np, cu_np, t, t_indptr, nnz))
+    if case in ("symmetric", "symmetric_repeats"):
+        assert np.array_equal(t_indptr, ip) and np.array_equal(t_rows, ix)   # its own transpose
