@@ -1,7 +1,8 @@
 """The attention-dropout oracle, pinned on the CPU.
 
 - fmix32 (MurmurHash3's finalizer) inside the whole MurmurHash3_x86_32 equals scikit-learn's murmurhash3_32,
-  an independent implementation, on random 4-byte keys and seeds (a wrong constant or shift fails it).
+  an independent implementation, on random 4-byte keys and seeds (a wrong constant or shift fails it), and the
+  hash's published test vectors hold.
 - The keep mask: rate 1 - p within binomial bounds; no correlation between neighbouring queries, keys, heads,
   seeds, and the four entries of random 2x2 blocks are jointly independent (the per-element hash mixes a row key
   with a column key by xor, which a weak finalizer would leave visible there).
@@ -26,6 +27,17 @@ def test_fmix32_inside_murmurhash3_matches_scikit_learn():
     for seed in (0, 1, 0x9747B28C, 2 ** 31 + 5, 2 ** 32 - 1):
         ref = np.array([sk.murmurhash3_32(int(k), seed, positive=True) for k in keys], dtype=np.uint64)
         assert np.array_equal(D.murmurhash3_x86_32(keys, seed).astype(np.uint64), ref), seed
+
+
+def test_murmurhash3_published_vectors():
+    """The test vectors published for MurmurHash3_x86_32: the empty key (the hash is then fmix32(seed) alone)
+    with seeds 0, 1 and 2^32 - 1, and the 4-byte keys 00 00 00 00, "test" and "aaaa"."""
+    for seed, want in ((0, 0x00000000), (1, 0x514E28B7), (0xFFFFFFFF, 0x81F16F39)):
+        assert int(D.fmix32(np.uint32(seed))) == want
+    for key, seed, want in ((b"\0\0\0\0", 0, 0x2362F9DE), (b"test", 0, 0xBA6BD213), (b"test", 0x9747B28C, 0x704B81DC),
+                            (b"aaaa", 0x9747B28C, 0x5A97808A)):
+        k = np.array([int.from_bytes(key, "little")], dtype=np.int64)
+        assert int(D.murmurhash3_x86_32(k, seed)[0]) == want, key
 
 
 def test_params_threshold_and_scale():
