@@ -98,14 +98,17 @@ ESA_API const char* esa_version(void);
 /*                                                                           */
 /* dropout_p in [0, 1): attention dropout on the softmax probabilities, as   */
 /* the reference's p / dropout_p in training (esa/mha.py:76,82): out =       */
-/* (P o Z / (1 - dropout_p)) V with the keep mask Z a counter-based hash of  */
-/* (dropout_seed, head, query token, key token) — query q keeps key k in    */
-/* head h iff fmix32(row(q, h) ^ col(k)) >= round(dropout_p 2^32), row(q, h) */
-/* = fmix32(s0 ^ fmix32(q heads + h)), col(k) = fmix32(s1 ^ fmix32(k)), s0 / */
-/* s1 the seed's low / high words (s1 xor 0x9E3779B9), fmix32 MurmurHash3's */
-/* 32-bit finalizer, q and k the global token indices.  softmax_lse is that  */
-/* of the undropped scores.  The backward takes the same dropout_p and seed. */
-/* 0 disables dropout (the seed is then unused).                             */
+/* (P o Z s) V with the keep mask Z a counter-based hash of (dropout_seed,   */
+/* head, query token, key token) — query q keeps key k in head h iff         */
+/* half(fmix32(row(q, h) ^ col(k)), k mod 2) >= thr, row(q, h) =             */
+/* fmix32(s0 ^ fmix32(q heads + h)), col(k) = fmix32(s1 ^ fmix32(k / 2))     */
+/* (integer division: keys 2i and 2i + 1 share one hash), half(x, 0) / (x, 1) */
+/* its low / high 16 bits, thr = round(dropout_p 2^16) capped at 2^16 - 1,   */
+/* s = 2^16 / (2^16 - thr) (1 / (1 - dropout_p) with dropout_p quantised to  */
+/* 2^-16), s0 / s1 the seed's low / high words (s1 xor 0x9E3779B9), fmix32   */
+/* MurmurHash3's 32-bit finalizer, q and k the global token indices.         */
+/* softmax_lse is that of the undropped scores.  The backward takes the same */
+/* dropout_p and seed.  0 disables dropout (the seed is then unused).        */
 /*                                                                           */
 /* softmax_lse is [heads, total_q] fp32 (natural log), as flash-attn's.      */
 /* ------------------------------------------------------------------------ */

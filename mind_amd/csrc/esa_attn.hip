@@ -1474,7 +1474,7 @@ __global__ __launch_bounds__(kF32Threads) void attn_fwd_f32_kernel(const AttnF32
     for (int j = 0; j < kTile; ++j) {
       const float p = fast_exp2(s[j] - m);
       l += p;
-      axpyn<HD>(DROP && !drop_keep(a.drop, rk, sKey[j]) ? 0.f : p, sV[j], acc);
+      axpyn<HD>(DROP && !drop_keep(a.drop, rk, sKey[j], k0 + j) ? 0.f : p, sV[j], acc);
     }
   }
   if (!valid) return;
@@ -1516,7 +1516,7 @@ __global__ __launch_bounds__(kF32Threads) void attn_dq_f32_kernel(const AttnF32A
       if (!admissible_f32<MASKED>(k0 + j, phi, oi, pn, own)) continue;
       const float p = fast_exp2(a.c * dotn<HD>(q, sK[j]) - rs.x);
       float dp = dotn<HD>(g, sV[j]);
-      if (DROP) dp = drop_keep(a.drop, rk, sKey[j]) ? dp * a.drop.inv_keep : 0.f;
+      if (DROP) dp = drop_keep(a.drop, rk, sKey[j], k0 + j) ? dp * a.drop.inv_keep : 0.f;
       const float ds = p * (dp - rs.y);
       axpyn<HD>(ds, sK[j], acc);
     }
@@ -1564,7 +1564,7 @@ __global__ __launch_bounds__(kF32Threads) void attn_dkdv_f32_kernel(const AttnF3
       if (!admissible_f32<MASKED>(q0 + i, phi, oi, pn, own)) continue;
       const float2 rs = sR[i];
       const float p = fast_exp2(a.c * dotn<HD>(kx, sQ[i]) - rs.x);
-      const bool keep = !DROP || drop_keep(a.drop, sKey[i], ck);
+      const bool keep = !DROP || drop_keep(a.drop, sKey[i], ck, oc);
       axpyn<HD>(keep ? p : 0.f, sG[i], dv);
       float dp = dotn<HD>(vx, sG[i]);
       if (DROP) dp = keep ? dp * a.drop.inv_keep : 0.f;

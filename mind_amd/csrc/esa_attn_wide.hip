@@ -231,15 +231,48 @@ struct WStageK {
 
 // Zeroes x[r] for the partners the keep mask drops: register r of lane half
 // h holds partner row_local(r, h) of the tile whose 32 partner keys start at
-// `keys` (LDS), the lane's own key is `own`.
-DEVI void drop_tile(const DropoutCfg& d, uint32_t own, const uint32_t* keys, int h, float (&x)[16]) {
+// `keys` (LDS), the lane's own key is `own`.  Forward and dQ: the partners
+// are the keys, register 8 b + e holding key base + 16 b + 8 h + e, so the
+// global key pair {2i, 2i + 1} sits in two neighbouring registers of a run of
+// 8 and shares one hash: with the tile base `bp` = base mod 2 even the pairs
+// are registers (0, 1) .. (6, 7), 4 hashes per run; odd, (1, 2) .. (5, 6)
+// with registers 0 and 7 alone (their pairs lie in other runs), 5.
+DEVI void drop_tile(const DropoutCfg& d, uint32_t own, const uint32_t* keys, int h, int bp, float (&x)[16]) {
+#pragma unroll
+  for (int b = 0; b < 2; ++b) {
+    const uint4 k0 = *reinterpret_cast<const uint4*>(keys + 16 * b + 8 * h);
+    const uint4 k1 = *reinterpret_cast<const uint4*>(keys + 16 * b + 8 * h + 4);
+    const uint32_t kk[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+    float* y = x + 8 * b;
+    if (bp == 0) {
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        const uint32_t bits = drop_bits(own, kk[e]);
+        y[e] = drop_half(d, bits, 0) ? y[e] : 0.f;
+        y[e + 1] = drop_half(d, bits, 1) ? y[e + 1] : 0.f;
+      }
+    } else {
+      y[0] = drop_half(d, drop_bits(own, kk[0]), 1) ? y[0] : 0.f;
+#pragma unroll
+      for (int e = 1; e < 7; e += 2) {
+        const uint32_t bits = drop_bits(own, kk[e]);
+        y[e] = drop_half(d, bits, 0) ? y[e] : 0.f;
+        y[e + 1] = drop_half(d, bits, 1) ? y[e + 1] : 0.f;
+      }
+      y[7] = drop_half(d, drop_bits(own, kk[7]), 0) ? y[7] : 0.f;
+    }
+  }
+}
+// dK / dV (the partners are queries, the lane's own token the key, of parity
+// kpar): each score takes its key's half of its own hash.
+DEVI void drop_tile_key(const DropoutCfg& d, uint32_t own, const uint32_t* keys, int h, int kpar, float (&x)[16]) {
 #pragma unroll
   for (int b = 0; b < 2; ++b) {
     const uint4 k0 = *reinterpret_cast<const uint4*>(keys + 16 * b + 8 * h);
     const uint4 k1 = *reinterpret_cast<const uint4*>(keys + 16 * b + 8 * h + 4);
     const uint32_t kk[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
 #pragma unroll
-    for (int e = 0; e < 8; ++e) x[8 * b + e] = drop_keep(d, own, kk[e]) ? x[8 * b + e] : 0.f;
+    for (int e = 0; e < 8; ++e) x[8 * b + e] = drop_half(d, drop_bits(kk[e], own), kpar) ? x[8 * b + e] : 0.f;
   }
 }
 
@@ -364,7 +397,7 @@ __global__ __launch_bounds__(256) void wide_fwd_kernel(const WideArgs a) {
           bf16x8 pb[2] = {cvt8(p), cvt8(p + 8)};
           l_run = bf16_sum8(pb[0], bf16_sum8(pb[1], l_run));
           if (DROP) {
-            drop_tile(a.drop, rk, &sKey[buf][u * kTile], h, p);
+            drop_tile(a.drop, rk, &sKey[buf][u * kTile], h, g.z & 1, p);
             pb[0] = cvt8(p);
             pb[1] = cvt8(p + 8);
           }
@@ -462,7 +495,7 @@ void wide_dq_kernel(const WideArgs a) {
             float dpk[16];
 #pragma unroll
             for (int r = 0; r < 16; ++r) dpk[r] = dp[r] * a.drop.inv_keep;
-            drop_tile(a.drop, rk, &sKey[buf][u * kTile], h, dpk);
+            drop_tile(a.drop, rk, &sKey[buf][u * kTile], h, g.z & 1, dpk);
 #pragma unroll
             for (int r = 0; r < 16; ++r) ds[r] = fast_exp2(fmaf(s[r], a.c, -lse2)) * (dpk[r] - dsum);
           } else {
@@ -580,7 +613,7 @@ void wide_dkdv_kernel(const WideArgs a) {
             }
 #pragma unroll
             for (int r = 0; r < 16; ++r) pk[r] = 1.f;
-            drop_tile(a.drop, ck, &sKey[buf][u * kTile], h, pk);
+            drop_tile_key(a.drop, ck, &sKey[buf][u * kTile], h, t & 1, pk);
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
               const bool keep = pk[r] != 0.f;

@@ -70,19 +70,23 @@ DEVI __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
 // (esa/mha.py:76,82): the output is (P o Z / (1 - p)) V for a keep mask Z;
 // the log-sum-exp is that of the undropped scores.  Query token q keeps key
 // token k in head h iff
-//   fmix32(row(q, h) ^ col(k)) >= thr,
+//   half(fmix32(row(q, h) ^ col(k)), k mod 2) >= thr,
 //   row(q, h) = fmix32(s0 ^ fmix32(q * heads + h)),
-//   col(k)    = fmix32(s1 ^ fmix32(k)),
-// with q, k the global token indices of the call ([0, total_q), [0,
-// total_k)), s0 / s1 the low / high 32-bit words of the 64-bit seed (s1
-// xor 0x9E3779B9), thr = round(p 2^32) capped at 2^32 - 1, and fmix32 the
-// 32-bit finalizer of MurmurHash3 (A. Appleby, SMHasher, public domain).
+//   col(k)    = fmix32(s1 ^ fmix32(floor(k / 2))),
+// half(x, 0) = x mod 2^16, half(x, 1) = floor(x / 2^16): the keys 2i and
+// 2i + 1 share one hash and take its low and high 16 bits.  q, k are the
+// global token indices of the call ([0, total_q), [0, total_k)), s0 / s1 the
+// low / high 32-bit words of the 64-bit seed (s1 xor 0x9E3779B9),
+// thr = round(p 2^16) capped at 2^16 - 1, and fmix32 the 32-bit finalizer of
+// MurmurHash3 (A. Appleby, SMHasher, public domain); kept values are scaled
+// by inv_keep = 2^16 / (2^16 - thr), the inverse of the exact keep rate.
 // A counter-based hash: the mask is a pure function of (seed, h, q, k), so
 // the forward and both backward passes evaluate the same mask whatever their
 // tiling, and row / column keys are computed once per token.
 struct DropoutCfg {
-  uint32_t s0, s1, thr;
-  float inv_keep;   // 1 / (1 - p)
+  uint32_t s0, s1, thr_hi;   // thr_hi = thr 2^16: half(x, 1) >= thr iff x >= thr_hi,
+                             // half(x, 0) >= thr iff x 2^16 (mod 2^32) >= thr_hi
+  float inv_keep;            // 2^16 / (2^16 - thr)
   int heads;
 };
 
@@ -90,9 +94,10 @@ inline DropoutCfg make_dropout(float p, unsigned long long seed, int heads) {
   DropoutCfg d{};
   d.s0 = (uint32_t)seed;
   d.s1 = (uint32_t)(seed >> 32) ^ 0x9E3779B9u;
-  const double t = (double)p * 4294967296.0 + 0.5;
-  d.thr = t >= 4294967295.0 ? 0xFFFFFFFFu : (uint32_t)t;
-  d.inv_keep = (float)(1.0 / (1.0 - (double)p));
+  const double t = (double)p * 65536.0 + 0.5;
+  const uint32_t thr = t >= 65535.0 ? 65535u : (uint32_t)t;
+  d.thr_hi = thr << 16;
+  d.inv_keep = (float)(65536.0 / (65536.0 - (double)thr));
   d.heads = heads;
   return d;
 }
@@ -108,5 +113,10 @@ DEVI uint32_t fmix32(uint32_t h) {
 DEVI uint32_t drop_row(const DropoutCfg& d, int q, int head) {
   return fmix32(d.s0 ^ fmix32((uint32_t)q * (uint32_t)d.heads + (uint32_t)head));
 }
-DEVI uint32_t drop_col(const DropoutCfg& d, int k) { return fmix32(d.s1 ^ fmix32((uint32_t)k)); }
-DEVI bool drop_keep(const DropoutCfg& d, uint32_t row, uint32_t col) { return fmix32(row ^ col) >= d.thr; }
+DEVI uint32_t drop_col(const DropoutCfg& d, int k) { return fmix32(d.s1 ^ fmix32((uint32_t)k >> 1)); }
+// The hash of a (row, col) pair; drop_half takes key k's 16 bits of it.
+DEVI uint32_t drop_bits(uint32_t row, uint32_t col) { return fmix32(row ^ col); }
+DEVI bool drop_half(const DropoutCfg& d, uint32_t bits, int k) { return (bits << (((k & 1) ^ 1) << 4)) >= d.thr_hi; }
+DEVI bool drop_keep(const DropoutCfg& d, uint32_t row, uint32_t col, int k) {
+  return drop_half(d, drop_bits(row, col), k);
+}

@@ -373,7 +373,7 @@ DEVI void fwd_token(const GraphAttnArgs& a, int t, const Src& src0) {
       for (int u = 0; u < G; ++u) {
         const float pu = ex2<T>(s[u] - mt);
         l += pu;
-        const float pv = !DROP || drop_keep(a.drop, rk, drop_col(a.drop, j[u])) ? pu : 0.f;
+        const float pv = !DROP || drop_keep(a.drop, rk, drop_col(a.drop, j[u]), j[u]) ? pu : 0.f;
 #pragma unroll
         for (int i = 0; i < N; ++i) acc[i] = fmaf(pv, vr[u][i], acc[i]);
       }
@@ -432,7 +432,7 @@ DEVI void dq_token(const GraphAttnArgs& a, int t, const Src& src0) {
       for (int u = 0; u < G; ++u) {
         const float pu = ok[u] ? ex2<T>(fmaf(head_sum<L>(dotn<N>(qv, kr[u])), a.c, -l2)) : 0.f;
         float dp = head_sum<L>(dotn<N>(gv, vr[u]));
-        if (DROP) dp = drop_keep(a.drop, rk, drop_col(a.drop, j[u])) ? dp * a.drop.inv_keep : 0.f;
+        if (DROP) dp = drop_keep(a.drop, rk, drop_col(a.drop, j[u]), j[u]) ? dp * a.drop.inv_keep : 0.f;
         const float ds = pu * (dp - dsum);
 #pragma unroll
         for (int i = 0; i < N; ++i) acc[i] = fmaf(ds, kr[u][i], acc[i]);
@@ -483,7 +483,7 @@ DEVI void dkdv_token(const GraphAttnArgs& a, int t, const Src& src0) {
       for (int u = 0; u < G; ++u) {
         const float pu = ok[u] ? ex2<T>(fmaf(head_sum<L>(dotn<N>(qr[u], kv)), a.c, -l2[u])) : 0.f;
         float dp = head_sum<L>(dotn<N>(gr[u], vv)), pv = pu;
-        if (DROP && !drop_keep(a.drop, drop_row(a.drop, i[u], hc), ck)) dp = pv = 0.f;
+        if (DROP && !drop_keep(a.drop, drop_row(a.drop, i[u], hc), ck, t)) dp = pv = 0.f;
         if (DROP) dp *= a.drop.inv_keep;
         const float ds = pu * (dp - ds_[u]);
 #pragma unroll

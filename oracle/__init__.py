@@ -28,7 +28,9 @@ torch_geometric and torch_scatter are absent):
       torch.autograd through the fp64 forward and central finite differences.
   dropout.fmix32 / keep_mask, attention with dropout=(p, seed)
       fmix32 inside the whole MurmurHash3_x86_32 equals scikit-learn's
-      murmurhash3_32 on random keys and seeds; keep rate 1 - p within
+      murmurhash3_32 on random keys and seeds, and the hash's published
+      test vectors hold; the two 16-bit halves a key pair shares are
+      independent (correlation, joint keep rate); keep rate 1 - p within
       binomial bounds, no correlation between neighbouring queries / keys /
       heads or seeds; p = 0 equals the plain oracle; the forward is the
       definition (P o Z / (1 - p)) V, its mean over seeds tends to P V; the

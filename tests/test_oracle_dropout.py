@@ -3,9 +3,10 @@
 - fmix32 (MurmurHash3's finalizer) inside the whole MurmurHash3_x86_32 equals scikit-learn's murmurhash3_32,
   an independent implementation, on random 4-byte keys and seeds (a wrong constant or shift fails it), and the
   hash's published test vectors hold.
-- The keep mask: rate 1 - p within binomial bounds; no correlation between neighbouring queries, keys, heads,
-  seeds, and the four entries of random 2x2 blocks are jointly independent (the per-element hash mixes a row key
-  with a column key by xor, which a weak finalizer would leave visible there).
+- The keep mask: rate 1 - p within binomial bounds; no correlation between neighbouring queries, keys (a key
+  pair {2i, 2i + 1} shares one hash, its halves), heads, seeds, and the four entries of random 2x2 blocks are
+  jointly independent (the per-element hash mixes a row key with a column key by xor, which a weak finalizer
+  would leave visible there).
 - Attention with dropout: p = 0 is the plain oracle; the mean over many seeds of the dropped output tends to
   the undropped output (the 1 / (1 - p) scale and the mask on the probabilities); the analytic backward equals
   torch.autograd through a dense fp64 forward on the same materialised mask.
@@ -41,10 +42,12 @@ def test_murmurhash3_published_vectors():
 
 
 def test_params_threshold_and_scale():
-    assert D.params(0.0, 5)[2] == 0                        # keep everything
-    assert D.params(0.5, 5)[2] == 2 ** 31
-    assert D.params(np.nextafter(np.float32(1), np.float32(0)), 5)[2] == 2 ** 32 - 2 ** 8   # 1 - 2^-24, exact
-    assert D.params(0.08, 5)[3] == pytest.approx(1 / 0.92, rel=1e-7)
+    assert D.params(0.0, 5)[2] == 0 and D.params(0.0, 5)[3] == 1.0   # keep everything, unscaled
+    assert D.params(0.5, 5)[2] == 2 ** 15 and D.params(0.5, 5)[3] == 2.0
+    assert D.params(np.nextafter(np.float32(1), np.float32(0)), 5)[2] == 2 ** 16 - 1   # capped: one value in 2^16 kept
+    assert D.params(0.08, 5)[2] == 5243                                   # round(0.08 * 2^16)
+    assert D.params(0.08, 5)[3] == pytest.approx(65536 / (65536 - 5243), rel=1e-7)
+    assert abs(D.params(0.08, 5)[3] * 0.92 - 1) < 3e-5                   # p quantised to 2^-16
     s0, s1, _, _ = D.params(0.1, (7 << 32) | 9)
     assert (int(s0), int(s1)) == (9, 7 ^ 0x9E3779B9)
 
@@ -195,3 +198,15 @@ def test_pair_path_and_global_ids_agree_with_the_segment_path():
     sub_pairs = OA.masked_attention_pairs(q[s:e], k[s:e], v[s:e], [0, e - s], [0, e - s], 0.4, adj=sub_adj,
                                           dropout=(p, seed, ids, ids))
     assert torch.allclose(sub_pairs, full[s:e], atol=1e-12)
+
+
+@pytest.mark.parametrize("p", [0.08, 0.5])
+def test_key_pair_halves_are_independent(p):
+    """Keys 2i and 2i + 1 take the low and high 16 bits of one hash: their keep decisions are uncorrelated and
+    both are kept at rate (1 - p)^2, within 5 sigma."""
+    z = D.keep_mask(p, 20260102, 2, np.arange(1500), np.arange(1200))
+    even, odd = z[:, :, 0::2], z[:, :, 1::2]
+    n = even.size
+    assert abs(_corr(even, odd)) < 5 / math.sqrt(n)
+    q = (1 - p) ** 2
+    assert abs((even & odd).mean() - q) < 5 * math.sqrt(q * (1 - q) / n)
