@@ -203,8 +203,10 @@ DEVI int wave_token() {
 }
 
 // ---- partner sources: next<G>(j, ok) yields the next G partners of the
-// wave's token (j a valid row index even where !ok), false once exhausted.  All
-// state is wave-uniform; a copy restarts the walk (one per head pass).
+// wave's token (j a valid row index even where !ok), false once exhausted.  The
+// walk position and the partners yielded are wave-uniform (a source may hold a
+// block of entries spread over the lanes); a copy restarts the walk (one per
+// head pass).
 
 // A CSR row [p, pb): entries in [lo, hi), each once (an entry equal to its
 // predecessor is a repeat).  The row is read 64 entries at a time by one
