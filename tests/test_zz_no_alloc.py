@@ -96,6 +96,26 @@ def test_noalloc_wide_heads(device, hd, mask):
         _compare(device, q, k, v, cu, int(gb.max_seqlen), kw)
 
 
+@pytest.mark.parametrize("dtype,hd,mask", [(torch.bfloat16, 16, "none"), (torch.bfloat16, 24, "none"),
+                                           (torch.bfloat16, 16, "edge"), (torch.float32, 16, "none")])
+def test_noalloc_with_dropout(device, dtype, hd, mask):
+    """Attention dropout (p = 0.08, a fixed seed) through the no-allocation forward: equal to the allocating
+    forward with the same p and seed (head dim 16 with dropout runs the wide MFMA kernels, whose workspace the
+    scratch also covers), two calls in a row, the second smaller."""
+    heads = 8 if hd == 24 else 16
+    cases = ((generators.protein_like(seed=7, num_graphs=6), 41), (generators.protein_like(seed=8, num_graphs=2), 42))
+    for gb, seed in cases:
+        t = int(gb.cu_seqlens[-1])
+        print(f"[noalloc] dropout {dtype} hd={hd} mask={mask} tokens={t}", flush=True)
+        cu = torch.as_tensor(gb.cu_seqlens).to(device)
+        q, k, v = (seeded_normal((t, heads, hd), seed + i, dtype).to(device) for i in range(3))
+        kw = {"dropout_p": 0.08, "dropout_seed": 1000 + seed}
+        if mask == "edge":
+            kw.update(edge_src=torch.as_tensor(gb.edge_index[0].astype(np.int32)).to(device),
+                      edge_dst=torch.as_tensor(gb.edge_index[1].astype(np.int32)).to(device))
+        _compare(device, q, k, v, cu, int(gb.max_seqlen), kw)
+
+
 def test_noalloc_forward_node_mask(device):
     for sizes, seed in (([60, 45, 80], 5), ([12, 7], 6)):
         ei, bm = node_graph(seed, sizes)
