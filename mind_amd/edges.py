@@ -260,10 +260,12 @@ def segment_minmax_csr(y: torch.Tensor, indptr: torch.Tensor, perm: torch.Tensor
     largest finite value (lowest for the maximum), so a tie keeps the first (lowest, with a stable CSR)
     edge id; a segment with nothing smaller (larger) than that start gives 0 and arg = num_edges
     (default: y's row count)."""
-    _lib.require_gpu(y)
-    y = y.contiguous()
+    _lib.require_gpu(y, indptr, perm)
     if y.dim() != 2:
         raise ValueError("y must be [E, F]")
+    y = y.contiguous()
+    indptr = _as_index(indptr, "indptr")
+    perm = None if perm is None else _as_index(perm, "perm")
     n = indptr.numel() - 1
     e = y.shape[0] if num_edges is None else int(num_edges)
     out = torch.empty((n, y.shape[1]), dtype=y.dtype, device=y.device)
