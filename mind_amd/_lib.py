@@ -164,8 +164,18 @@ def version() -> str:
     return load().esa_version().decode()
 
 
+_profiling = False
+
+
 def profile_enable(on: bool) -> None:
+    global _profiling
     check(load().esa_profile_enable(int(on)), "esa_profile_enable")
+    _profiling = bool(on)
+
+
+def profiling() -> bool:
+    """Whether this process turned the per-kernel profiling hook on (profile_enable)."""
+    return _profiling
 
 
 def profile_collect() -> dict[str, tuple[float, int]]:
