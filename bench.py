@@ -55,6 +55,8 @@ def parse():
     ap.add_argument("--cpu-sample-graphs", type=int, default=8,
                     help="graphs of the configuration-2 batch timed on the CPU for the masked baseline")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="skip configuration 0's HIP-graph leg (for profiler runs that time eager launches only)")
     ap.add_argument("--no-sub", action="store_true",
                     help="headline only: skip the masked (configuration 2), gather (configuration 3), node, wide, "
                          "dropout, block (configuration 0) and stack (configuration 4) sub-objects")
@@ -1128,15 +1130,17 @@ def bench_block(args, sub: bool = False):
 
     ms, wall_ms, kern, ms_prof = timed(step, args.steps, args.warmup)
     lib_ms = sum(k["avg_us"] * k["launches"] for k in kern.values()) / 1e3 / args.steps
-    ref = tuple(y.clone() for y in forward(types_d, ei, bm))
-    gf = GraphedForward(forward, types_d, ei, bm)
-    g_ms, g_wall, _, _ = timed(lambda: gf(types_d, ei, bm), args.steps, args.warmup, profile=False)
-    got = gf(types_d, ei, bm)
-    torch.cuda.synchronize()
-    graph = {"ms_per_step": g_ms, "wall_ms_per_step": g_wall, "edge_tokens_per_s": t / (g_ms * 1e-3),
-             "bit_identical_to_eager": all(torch.equal(a, b) for a, b in zip(got, ref)),
-             "what": "the same step captured once into a HIP graph and replayed (inputs copied into the graph's "
-                     "input buffers each step): one launch per step instead of about a hundred"}
+    graph = None
+    if not args.no_graph:
+        ref = tuple(y.clone() for y in forward(types_d, ei, bm))
+        gf = GraphedForward(forward, types_d, ei, bm)
+        g_ms, g_wall, _, _ = timed(lambda: gf(types_d, ei, bm), args.steps, args.warmup, profile=False)
+        got = gf(types_d, ei, bm)
+        torch.cuda.synchronize()
+        graph = {"ms_per_step": g_ms, "wall_ms_per_step": g_wall, "edge_tokens_per_s": t / (g_ms * 1e-3),
+                 "bit_identical_to_eager": all(torch.equal(a, b) for a, b in zip(got, ref)),
+                 "what": "the same step captured once into a HIP graph and replayed (inputs copied into the "
+                         "graph's input buffers each step): one launch per step instead of about a hundred"}
     if sub:
         out = {"workload": "config0: edge tokens (embed, gather, project) + ESA block M-S-P(1 seed) forward, fp32",
                "graphs": gb.num_graphs, "edge_tokens": t, "dim": d, "heads": h, "ms_per_step": ms,

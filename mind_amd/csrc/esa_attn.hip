@@ -1333,8 +1333,10 @@ __global__ __launch_bounds__(256) void list_dkdv_kernel(const AttnArgs a0) {
 // 128 outer tokens of one segment (a per-segment plan, longest partner range
 // first: a block walks only its own segment's partners, so few-query
 // segments such as PMA seeds get one block per segment and head), partner
-// runs of 32 tokens staged in LDS and read by broadcast.  Scores, softmax and both
-// products are fp32 FMA chains in a fixed order.  Exponentials and the
+// runs of 32 tokens staged in LDS and read by broadcast (the forward holds a
+// partner row across each 16-lane wave row instead and splits a group's key
+// tiles over several thread groups; see attn_fwd_f32_kernel).  Scores,
+// softmax and both products are fp32 FMA chains in a fixed order.  Exponentials and the
 // log-sum-exp use the hardware v_exp_f32 / v_log_f32 (about 1 ulp): every
 // exponent is <= 0 (a score minus the running maximum or the row's LSE2) and
 // every log argument >= 1 (the row sum includes the maximum's 1), so the
@@ -1428,58 +1430,302 @@ DEVI F32Outer f32_outer(const int4& g, int tid) {
   return o;
 }
 
+// Partner rows across a wave row.  A staged partner row of HD fp32 values is
+// held by the 16 lanes of each wave row: lane l holds dims l % 16,
+// 16 + l % 16, ... (NR = ceil(HD / 16) registers, zeros past HD), and all
+// four rows of the wave hold the same partner.  `v_fmac_f32_dpp` with
+// row_newbcast:i hands dim 16 r + i of that partner to the 16 lanes of each
+// row inside the multiply-add, so a product with a partner row costs one VALU
+// instruction per dim and one 4-byte LDS read per partner and lane.  Read as
+// whole rows per lane, the same partner costs HD / 4 16-byte reads per lane:
+// the broadcast reads move 64 x 16 bytes through the LDS pipe each, and they,
+// not the FMAs, bounded the kernels.  DPP reads the source lane's register,
+// so every lane of the wave is active at these instructions (lanes past
+// their group's end compute on a clamped token and store nothing).  The
+// leading s_nop 1 covers the two wait states a DPP read of a VGPR needs
+// after a VALU write of it.
+#define F32_FM(ACC, SRC, MUL, I) \
+  "v_fmac_f32_dpp %" #ACC ", %" #SRC ", %" #MUL " row_newbcast:" #I " row_mask:0xf bank_mask:0xf\n\t"
+#define F32_DOT4(I, Q) F32_FM(0, 4, Q, I) F32_FM(1, 5, Q, I) F32_FM(2, 6, Q, I) F32_FM(3, 7, Q, I)
+#define F32_AXPY8(V, P)                                                                                 \
+  F32_FM(0, V, P, 0) F32_FM(1, V, P, 1) F32_FM(2, V, P, 2) F32_FM(3, V, P, 3) F32_FM(4, V, P, 4)         \
+  F32_FM(5, V, P, 5) F32_FM(6, V, P, 6) F32_FM(7, V, P, 7)
+#define F32_AXPY16(V, P)                                                                                \
+  F32_AXPY8(V, P) F32_FM(8, V, P, 8) F32_FM(9, V, P, 9) F32_FM(10, V, P, 10) F32_FM(11, V, P, 11)        \
+  F32_FM(12, V, P, 12) F32_FM(13, V, P, 13) F32_FM(14, V, P, 14) F32_FM(15, V, P, 15)
+
+// s[k] += sum over the register's N dims (8 or 16, ascending) of x[i] * dim i
+// of partner k's row register y[k], for four partners.
+template <int N>
+DEVI void dot4_rows(float (&s)[4], const float (&y)[4], const float* x) {
+  if constexpr (N == 16)
+    asm("s_nop 1\n\t"
+        F32_DOT4(0, 8) F32_DOT4(1, 9) F32_DOT4(2, 10) F32_DOT4(3, 11) F32_DOT4(4, 12) F32_DOT4(5, 13)
+        F32_DOT4(6, 14) F32_DOT4(7, 15) F32_DOT4(8, 16) F32_DOT4(9, 17) F32_DOT4(10, 18) F32_DOT4(11, 19)
+        F32_DOT4(12, 20) F32_DOT4(13, 21) F32_DOT4(14, 22) F32_DOT4(15, 23)
+        : "+v"(s[0]), "+v"(s[1]), "+v"(s[2]), "+v"(s[3])
+        : "v"(y[0]), "v"(y[1]), "v"(y[2]), "v"(y[3]), "v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]), "v"(x[4]),
+          "v"(x[5]), "v"(x[6]), "v"(x[7]), "v"(x[8]), "v"(x[9]), "v"(x[10]), "v"(x[11]), "v"(x[12]),
+          "v"(x[13]), "v"(x[14]), "v"(x[15]));
+  else
+    asm("s_nop 1\n\t"
+        F32_DOT4(0, 8) F32_DOT4(1, 9) F32_DOT4(2, 10) F32_DOT4(3, 11) F32_DOT4(4, 12) F32_DOT4(5, 13)
+        F32_DOT4(6, 14) F32_DOT4(7, 15)
+        : "+v"(s[0]), "+v"(s[1]), "+v"(s[2]), "+v"(s[3])
+        : "v"(y[0]), "v"(y[1]), "v"(y[2]), "v"(y[3]), "v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]), "v"(x[4]),
+          "v"(x[5]), "v"(x[6]), "v"(x[7]));
+}
+
+// x[i] += a * dim i of the row register y, over the register's N dims (8 or 16).
+template <int N>
+DEVI void axpy_row(float* x, float y, float a) {
+  if constexpr (N == 16)
+    asm("s_nop 1\n\t" F32_AXPY16(16, 17)
+        : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]), "+v"(x[4]), "+v"(x[5]), "+v"(x[6]), "+v"(x[7]),
+          "+v"(x[8]), "+v"(x[9]), "+v"(x[10]), "+v"(x[11]), "+v"(x[12]), "+v"(x[13]), "+v"(x[14]), "+v"(x[15])
+        : "v"(y), "v"(a));
+  else
+    asm("s_nop 1\n\t" F32_AXPY8(8, 9)
+        : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]), "+v"(x[4]), "+v"(x[5]), "+v"(x[6]), "+v"(x[7])
+        : "v"(y), "v"(a));
+}
+
+// Dims held by register r of an HD-wide row (16, or 8 for the last register of HD 24).
+template <int HD>
+DEVI constexpr int row_dims(int r) { return HD - 16 * r >= 16 ? 16 : HD - 16 * r; }
+
+// A partner row's registers for lane li: y[r] = dim 16 r + li of the row.
+template <int HD>
+DEVI void row_regs(float (&y)[(HD + 15) / 16], const float* row, int li) {
+#pragma unroll
+  for (int r = 0; r < (HD + 15) / 16; ++r) y[r] = row[16 * r + li];
+}
+
+// Four partners' dot products with the lane's row x (HD dims, ascending):
+// s[k] = sum_d x[d] * dim d of partner k, from the partners' row registers.
+template <int HD, int R = 0>
+DEVI void dot4(float (&s)[4], const float* x, const float (&y)[4][(HD + 15) / 16]) {
+  if constexpr (R == 0) s[0] = s[1] = s[2] = s[3] = 0.f;
+  if constexpr (16 * R < HD) {
+    const float yr[4] = {y[0][R], y[1][R], y[2][R], y[3][R]};
+    dot4_rows<row_dims<HD>(R)>(s, yr, x + 16 * R);
+    dot4<HD, R + 1>(s, x, y);
+  }
+}
+
+// x[d] += a * dim d of a partner row (HD dims) from its row registers.
+template <int HD, int R = 0>
+DEVI void axpy(float* x, float a, const float (&y)[(HD + 15) / 16]) {
+  if constexpr (16 * R < HD) {
+    axpy_row<row_dims<HD>(R)>(x + 16 * R, y[R], a);
+    axpy<HD, R + 1>(x, a, y);
+  }
+}
+
+// Stage the 32 tokens from t0 of a [T][H][HD] fp32 tensor into LDS rows of
+// 16 NR floats (128 threads): dims past HD and tokens at or past `end` are zeros.
+template <int HD>
+DEVI void stage_rows_lane(float (*dst)[16 * ((HD + 15) / 16)], const float* src, int end, int H, int head, int t0,
+                          int tid) {
+  constexpr int C = 4 * ((HD + 15) / 16);   // float4 chunks per staged row
+#pragma unroll
+  for (int i = tid; i < kTile * C; i += kF32Threads) {
+    const int t = t0 + i / C, part = i % C;
+    reinterpret_cast<float4*>(dst[i / C])[part] =
+        t < end && part < HD / 4 ? reinterpret_cast<const float4*>(src + ((size_t)t * H + head) * HD)[part]
+                                 : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+}
+
+// Key splits of the fp32 forward: S groups of 128 threads per block take the
+// group's key tiles in turn (tile i goes to split i mod S), each with its own
+// staging buffers, and merge their (max, sum, output) partials at the end in
+// split order.  One thread per (query, head) gives only a few thousand waves
+// per call (configuration 0: 2,392 for 1,024 SIMDs) with per-block work
+// proportional to the segment length; with the splits the long segments'
+// blocks finish S times sooner and the SIMDs hold S times the waves.
+template <int HD>
+constexpr int f32_splits() { return HD >= 64 ? 2 : 4; }
+
 template <bool MASKED, int HD, bool DROP>
-__global__ __launch_bounds__(kF32Threads) void attn_fwd_f32_kernel(const AttnF32Args a) {
-  __shared__ float4 sK[kTile][HD / 4], sV[kTile][HD / 4];
-  __shared__ int2 sN[kTile];
-  __shared__ uint32_t sKey[DROP ? kTile : 1];   // column keys of the staged keys
-  const int tid = threadIdx.x, H = a.heads;
+__global__ __launch_bounds__(kF32Threads * f32_splits<HD>()) void attn_fwd_f32_kernel(const AttnF32Args a) {
+  constexpr int NR = (HD + 15) / 16, S = f32_splits<HD>();
+  __shared__ float sK[S][kTile][16 * NR], sV[S][kTile][16 * NR];
+  __shared__ int2 sN[S][kTile];
+  __shared__ uint32_t sKey[S][DROP ? kTile : 1];   // column keys of the staged keys
+  __shared__ float sAcc[kF32Threads][16 * NR + 1];   // a later split's partial: output row, then m and l
+  __shared__ float sML[kF32Threads][2];
+  const int split = threadIdx.x / kF32Threads, tid = threadIdx.x - split * kF32Threads, li = tid & 15;
+  const int H = a.heads;
   const int item = blockIdx.x / H, head = blockIdx.x - item * H;
   if (item >= *a.count) return;
   const F32Outer ot = f32_outer(a.plan[item], tid);
   const int oi = ot.oi, oc = ot.oc, phi = ot.phi;
-  const bool valid = ot.valid;
-  float q[HD], acc[HD];
+  float q[16 * NR], acc[16 * NR];
   loadn<HD>(a.q + ((size_t)oc * H + head) * HD, q);
 #pragma unroll
-  for (int i = 0; i < HD; ++i) acc[i] = 0.f;
+  for (int i = 0; i < 16 * NR; ++i) {
+    if (i >= HD) q[i] = 0.f;
+    acc[i] = 0.f;
+  }
   const int2 own = MASKED ? a.nodes[oc] : make_int2(0, 0);
   const uint32_t rk = DROP ? drop_row(a.drop, oc, head) : 0u;
   float m = -INFINITY, l = 0.f;
-  for (int k0 = ot.plo; k0 < phi; k0 += kTile) {
+  const int rounds = (phi - ot.plo + S * kTile - 1) / (S * kTile);
+  for (int it = 0; it < rounds; ++it) {
+    const int k0 = ot.plo + (it * S + split) * kTile;   // past phi: nothing to do this round (split-uniform)
     __syncthreads();
-    stage_rows_f32<HD>(sK, a.k, phi, H, head, k0, tid);
-    stage_rows_f32<HD>(sV, a.v, phi, H, head, k0, tid);
-    if (MASKED && tid < kTile) sN[tid] = k0 + tid < phi ? a.nodes[k0 + tid] : make_int2(-1, -1);
-    if (DROP && tid < kTile) sKey[tid] = drop_col(a.drop, k0 + tid);
+    if (k0 < phi) {
+      stage_rows_lane<HD>(sK[split], a.k, phi, H, head, k0, tid);
+      stage_rows_lane<HD>(sV[split], a.v, phi, H, head, k0, tid);
+      if (MASKED && tid < kTile) sN[split][tid] = k0 + tid < phi ? a.nodes[k0 + tid] : make_int2(-1, -1);
+      if (DROP && tid < kTile) sKey[split][tid] = drop_col(a.drop, k0 + tid);
+    }
     __syncthreads();
-    if (!valid) continue;
+    if (k0 >= phi) continue;
     float s[kTile];
     float mt = -INFINITY;
+    float ky[kTile][NR];   // the tile's key rows, loaded one group of four ahead of their products
 #pragma unroll
-    for (int j = 0; j < kTile; ++j) {
-      const int2 pn = MASKED ? sN[j] : make_int2(0, 0);
-      s[j] = admissible_f32<MASKED>(k0 + j, phi, oi, pn, own) ? a.c * dotn<HD>(q, sK[j]) : -INFINITY;
-      mt = fmaxf(mt, s[j]);
+    for (int u = 0; u < 4; ++u) row_regs<HD>(ky[u], sK[split][u], li);
+#pragma unroll
+    for (int j = 0; j < kTile; j += 4) {
+      if (j + 4 < kTile) {
+#pragma unroll
+        for (int u = 4; u < 8; ++u) row_regs<HD>(ky[j + u], sK[split][j + u], li);
+      }
+      __builtin_amdgcn_sched_barrier(0);   // keep the next group's reads ahead of these products
+      float d[4];
+      dot4<HD>(d, q, *reinterpret_cast<const float(*)[4][NR]>(&ky[j]));
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int2 pn = MASKED ? sN[split][j + u] : make_int2(0, 0);
+        s[j + u] = admissible_f32<MASKED>(k0 + j + u, phi, oi, pn, own) ? a.c * d[u] : -INFINITY;
+        mt = fmaxf(mt, s[j + u]);
+      }
     }
-    if (mt == -INFINITY) continue;
     if (mt > m) {
       const float alpha = fast_exp2(m - mt);   // 0 while m = -inf
       l *= alpha;
 #pragma unroll
-      for (int i = 0; i < HD; ++i) acc[i] *= alpha;
+      for (int i = 0; i < 16 * NR; ++i) acc[i] *= alpha;
       m = mt;
     }
+    const float mb = m == -INFINITY ? 0.f : m;   // no admissible key yet: every p is exp2(-inf) = 0
+    float vy[kTile][NR];   // value rows, loaded four keys ahead of their products
+#pragma unroll
+    for (int j = 0; j < 4; ++j) row_regs<HD>(vy[j], sV[split][j], li);
 #pragma unroll
     for (int j = 0; j < kTile; ++j) {
-      const float p = fast_exp2(s[j] - m);
+      if (j + 4 < kTile) row_regs<HD>(vy[j + 4], sV[split][j + 4], li);
+      __builtin_amdgcn_sched_barrier(0);   // keep the reads four keys ahead of their product
+      const float p = fast_exp2(s[j] - mb);
       l += p;
-      axpyn<HD>(DROP && !drop_keep(a.drop, rk, sKey[j], k0 + j) ? 0.f : p, sV[j], acc);
+      axpy<HD>(acc, DROP && !drop_keep(a.drop, rk, sKey[split][j], k0 + j) ? 0.f : p, vy[j]);
     }
   }
-  if (!valid) return;
+  // Merge in split order: split 0 takes over split 1's partial, then split 2's, ...
+  // (m = -inf marks an empty partial; its output and sum are 0).
+#pragma unroll
+  for (int src = 1; src < S; ++src) {
+    __syncthreads();
+    if (split == src) {
+#pragma unroll
+      for (int i = 0; i < HD; ++i) sAcc[tid][i] = acc[i];
+      sML[tid][0] = m;
+      sML[tid][1] = l;
+    }
+    __syncthreads();
+    if (split == 0) {
+      const float m2 = sML[tid][0], l2 = sML[tid][1];
+      const float mn = fmaxf(m, m2);
+      if (mn != -INFINITY) {
+        const float a1 = fast_exp2(m - mn), a2 = fast_exp2(m2 - mn);
+        l = l * a1 + l2 * a2;
+#pragma unroll
+        for (int i = 0; i < HD; ++i) acc[i] = acc[i] * a1 + sAcc[tid][i] * a2;
+        m = mn;
+      }
+    }
+  }
+  if (split != 0 || !ot.valid) return;
   storen<HD>(a.o + ((size_t)oi * H + head) * HD, acc, l > 0.f ? (DROP ? a.drop.inv_keep : 1.f) / l : 0.f);
   a.lse_out[(size_t)head * a.total_q + oi] = l > 0.f ? (m + fast_log2(l)) * kLn2 : -INFINITY;
+}
+
+// fp32 forward for segments of a few queries (the PMA's seeds: the expanded
+// call has k queries per set).  The tiled kernel gives each (segment, head) a
+// 128-thread block in which k lanes walk every key of the segment, so its
+// time is that of the longest segment's walk; here one wave takes one
+// (segment, query slot, head), its 64 lanes take the segment's keys in turn
+// (key kb + lane + 64 i) with a running maximum and sum per lane, and the
+// lanes' partials merge by a butterfly in a fixed order.  A slot past the
+// hint's count walks the segment's later queries (slot + slots, ...), so any
+// number of queries per segment is computed; the hint only sets the grid.
+struct AttnF32FewArgs {
+  DropoutCfg drop;
+  const float* q; const float* k; const float* v;
+  const int* cu_q; const int* cu_k;
+  int nseg, heads, total_q, slots, blocks_per_seg;
+  float c;
+  float* o; float* lse_out;
+};
+
+template <int HD, bool DROP>
+__global__ __launch_bounds__(256) void attn_fwd_f32_few_kernel(const AttnF32FewArgs a) {
+  const int H = a.heads, lane = threadIdx.x & 63;
+  const int seg = blockIdx.x / a.blocks_per_seg;
+  const int w = (blockIdx.x - seg * a.blocks_per_seg) * 4 + (int)(threadIdx.x >> 6);
+  const int slot = w / H, head = w - slot * H;
+  if (seg >= a.nseg || slot >= a.slots) return;   // wave-uniform: no barriers in this kernel
+  const int qb = a.cu_q[seg], qe = a.cu_q[seg + 1], kb = a.cu_k[seg], ke = a.cu_k[seg + 1];
+  for (int qi = qb + slot; qi < qe; qi += a.slots) {
+    float q[HD], acc[HD];
+    loadn<HD>(a.q + ((size_t)qi * H + head) * HD, q);
+#pragma unroll
+    for (int i = 0; i < HD; ++i) acc[i] = 0.f;
+    const uint32_t rk = DROP ? drop_row(a.drop, qi, head) : 0u;
+    float m = -INFINITY, l = 0.f;
+    for (int kj = kb + lane; kj < ke; kj += 64) {
+      float kx[HD];
+      loadn<HD>(a.k + ((size_t)kj * H + head) * HD, kx);
+      float d = 0.f;
+#pragma unroll
+      for (int i = 0; i < HD; ++i) d = fmaf(q[i], kx[i], d);
+      const float sc = a.c * d;
+      if (sc > m) {
+        const float alpha = fast_exp2(m - sc);   // 0 while m = -inf
+        l *= alpha;
+#pragma unroll
+        for (int i = 0; i < HD; ++i) acc[i] *= alpha;
+        m = sc;
+      }
+      const float p = fast_exp2(sc - m);
+      l += p;
+      const float pv = DROP && !drop_keep(a.drop, rk, drop_col(a.drop, kj), kj) ? 0.f : p;
+      float vx[HD];
+      loadn<HD>(a.v + ((size_t)kj * H + head) * HD, vx);
+#pragma unroll
+      for (int i = 0; i < HD; ++i) acc[i] = fmaf(pv, vx[i], acc[i]);
+    }
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {   // merge partials: max, rescaled sums and outputs
+      const float m2 = __shfl_xor(m, off), l2 = __shfl_xor(l, off);
+      const float mn = fmaxf(m, m2);
+      const float a1 = mn == -INFINITY ? 0.f : fast_exp2(m - mn), a2 = mn == -INFINITY ? 0.f : fast_exp2(m2 - mn);
+      l = l * a1 + l2 * a2;
+#pragma unroll
+      for (int i = 0; i < HD; ++i) {
+        const float o2 = __shfl_xor(acc[i], off);
+        acc[i] = acc[i] * a1 + o2 * a2;
+      }
+      m = mn;
+    }
+    if (lane == 0) {
+      storen<HD>(a.o + ((size_t)qi * H + head) * HD, acc, l > 0.f ? (DROP ? a.drop.inv_keep : 1.f) / l : 0.f);
+      a.lse_out[(size_t)head * a.total_q + qi] = l > 0.f ? (m + fast_log2(l)) * kLn2 : -INFINITY;
+    }
+  }
 }
 
 // dQ = scale * sum_j P_ij (dP_ij - D_i) k_j, P recomputed from the saved LSE.
@@ -2083,6 +2329,37 @@ GraphAttnArgs edge_gather_args(const void* plan, const void* q, const void* k, c
     else if (hd == 32) hipLaunchKernelGGL((KERNEL<false, 32, D>), grid, dim3(kF32Threads), 0, st, a); \
     else hipLaunchKernelGGL((KERNEL<false, 64, D>), grid, dim3(kF32Threads), 0, st, a);              \
   } while (0)
+constexpr unsigned kF32FwdThreads(int hd) { return kF32Threads * (hd >= 64 ? f32_splits<64>() : f32_splits<16>()); }
+#define ESA_F32_FWD_HD(D, hd, grid, st, a)                                                                 \
+  do {                                                                                                     \
+    if (hd == 16)                                                                                          \
+      hipLaunchKernelGGL((attn_fwd_f32_kernel<false, 16, D>), grid, dim3(kF32FwdThreads(16)), 0, st, a);    \
+    else if (hd == 24)                                                                                     \
+      hipLaunchKernelGGL((attn_fwd_f32_kernel<false, 24, D>), grid, dim3(kF32FwdThreads(24)), 0, st, a);    \
+    else if (hd == 32)                                                                                     \
+      hipLaunchKernelGGL((attn_fwd_f32_kernel<false, 32, D>), grid, dim3(kF32FwdThreads(32)), 0, st, a);    \
+    else                                                                                                   \
+      hipLaunchKernelGGL((attn_fwd_f32_kernel<false, 64, D>), grid, dim3(kF32FwdThreads(64)), 0, st, a);    \
+  } while (0)
+// Query segments of at most this many tokens (the caller's max_seqlen_q) take attn_fwd_f32_few_kernel.
+constexpr int kF32FewQueries = 4;
+#define ESA_F32_FEW_HD(D, hd, grid, st, a)                                                        \
+  do {                                                                                            \
+    if (hd == 16) hipLaunchKernelGGL((attn_fwd_f32_few_kernel<16, D>), grid, dim3(256), 0, st, a);  \
+    else if (hd == 24) hipLaunchKernelGGL((attn_fwd_f32_few_kernel<24, D>), grid, dim3(256), 0, st, a); \
+    else if (hd == 32) hipLaunchKernelGGL((attn_fwd_f32_few_kernel<32, D>), grid, dim3(256), 0, st, a); \
+    else hipLaunchKernelGGL((attn_fwd_f32_few_kernel<64, D>), grid, dim3(256), 0, st, a);         \
+  } while (0)
+#define ESA_F32_FEW_LAUNCH(hd, drop, grid, st, a)   \
+  do {                                              \
+    if (drop) ESA_F32_FEW_HD(true, hd, grid, st, a); \
+    else ESA_F32_FEW_HD(false, hd, grid, st, a);     \
+  } while (0)
+#define ESA_F32_FWD_LAUNCH(hd, drop, grid, st, a)  \
+  do {                                             \
+    if (drop) ESA_F32_FWD_HD(true, hd, grid, st, a); \
+    else ESA_F32_FWD_HD(false, hd, grid, st, a);     \
+  } while (0)
 #define ESA_F32_LAUNCH(KERNEL, hd, drop, grid, st, a)                                                \
   do {                                                                                               \
     if (drop) ESA_F32_LAUNCH_HD(KERNEL, true, hd, grid, st, a);                                     \
@@ -2186,7 +2463,7 @@ int esa_varlen_attn_fwd(const void* q, const void* k, const void* v, const int* 
                         float softmax_scale, float dropout_p, unsigned long long dropout_seed, int mask_kind,
                         const int* mask_a, const int* mask_b, int n_mask_edges, void* out, float* softmax_lse,
                         void* workspace, size_t workspace_bytes, void* stream) {
-  (void)max_seqlen_q; (void)max_seqlen_k;
+  (void)max_seqlen_k;   // max_seqlen_q routes fp32 calls with few queries per segment; results never depend on it
   int rc = check_common(batch, total_q, total_k, heads, head_dim, dtype, mask_kind);
   if (rc) return rc;
   if (!(dropout_p >= 0.f && dropout_p < 1.f)) return ESA_ERR_DROPOUT;
@@ -2246,6 +2523,18 @@ int esa_varlen_attn_fwd(const void* q, const void* k, const void* v, const int* 
     g.out = out; g.lse = softmax_lse;
     return graph_edge_attn_fwd(g, dtype, st);
   }
+  if (f32 && !masked && max_seqlen_q > 0 && max_seqlen_q <= kF32FewQueries) {
+    AttnF32FewArgs fa{};
+    fa.q = static_cast<const float*>(q); fa.k = static_cast<const float*>(k); fa.v = static_cast<const float*>(v);
+    fa.cu_q = cu_seqlens_q; fa.cu_k = cu_seqlens_k; fa.nseg = batch; fa.heads = heads; fa.total_q = total_q;
+    fa.slots = max_seqlen_q; fa.blocks_per_seg = (max_seqlen_q * heads + 3) / 4;
+    fa.c = softmax_scale * kLog2e; fa.drop = dcfg;
+    fa.o = static_cast<float*>(out); fa.lse_out = softmax_lse;
+    const dim3 grid((unsigned)batch * (unsigned)fa.blocks_per_seg);
+    ESA_TIMED(esa_profile::kAttnFwd, st, ESA_F32_FEW_LAUNCH(head_dim, drop, grid, st, fa));
+    ESA_LAUNCH_CHECK();
+    return ESA_OK;
+  }
   if (f32) {
     PrepArgs pa{};
     pa.cu_q = cu_seqlens_q; pa.cu_k = cu_seqlens_k; pa.nseg = batch;
@@ -2265,9 +2554,9 @@ int esa_varlen_attn_fwd(const void* q, const void* k, const void* v, const int* 
     const dim3 fgrid((unsigned)(groups_of(total_q) + batch) * (unsigned)heads);
     if (masked)   // head_dim 16 without dropout (the rest take the gather kernels)
       ESA_TIMED(esa_profile::kAttnFwdMasked, st,
-                hipLaunchKernelGGL((attn_fwd_f32_kernel<true, 16, false>), fgrid, dim3(kF32Threads), 0, st, a));
+                hipLaunchKernelGGL((attn_fwd_f32_kernel<true, 16, false>), fgrid, dim3(kF32FwdThreads(16)), 0, st, a));
     else
-      ESA_TIMED(esa_profile::kAttnFwd, st, ESA_F32_LAUNCH(attn_fwd_f32_kernel, head_dim, drop, fgrid, st, a));
+      ESA_TIMED(esa_profile::kAttnFwd, st, ESA_F32_FWD_LAUNCH(head_dim, drop, fgrid, st, a));
     ESA_LAUNCH_CHECK();
     return ESA_OK;
   }

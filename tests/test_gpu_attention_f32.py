@@ -25,20 +25,21 @@ def _close(got, ref, what):
     assert mx <= bar, f"{what}: max-abs {mx:.3e} > {bar:.3e}"
 
 
-def _inputs(tq, tk, seed, heads=H):
+def _inputs(tq, tk, seed, heads=H, hd=D):
     f = torch.float32
-    return (seeded_normal((tq, heads, D), seed, f), seeded_normal((tk, heads, D), seed + 1, f),
-            seeded_normal((tk, heads, D), seed + 2, f), seeded_normal((tq, heads, D), seed + 3, f))
+    return (seeded_normal((tq, heads, hd), seed, f), seeded_normal((tk, heads, hd), seed + 1, f),
+            seeded_normal((tk, heads, hd), seed + 2, f), seeded_normal((tq, heads, hd), seed + 3, f))
 
 
-def _check(device, lengths_q, lengths_k, seed, src=None, dst=None, heads=H, scale=0.25):
+def _check(device, lengths_q, lengths_k, seed, src=None, dst=None, heads=H, scale=0.25, hd=D, max_q=None):
+    """max_q: the max_seqlen_q passed to the call (default: the true maximum); it only selects the route."""
     cu_q, cu_k = cu_from_lengths(lengths_q), cu_from_lengths(lengths_k)
-    q, k, v, g = _inputs(int(cu_q[-1]), int(cu_k[-1]), seed, heads)
+    q, k, v, g = _inputs(int(cu_q[-1]), int(cu_k[-1]), seed, heads, hd)
     qd, kd, vd = (t.to(device).requires_grad_(True) for t in (q, k, v))
     cq, ck = torch.as_tensor(cu_q).to(device), torch.as_tensor(cu_k).to(device)
     s = None if src is None else torch.as_tensor(src, dtype=torch.int32).to(device)
     d = None if dst is None else torch.as_tensor(dst, dtype=torch.int32).to(device)
-    mq = int(np.diff(cu_q).max()) if len(cu_q) > 1 else 0
+    mq = (int(np.diff(cu_q).max()) if len(cu_q) > 1 else 0) if max_q is None else max_q
     mk = int(np.diff(cu_k).max()) if len(cu_k) > 1 else 0
     out, lse = A.varlen_attention(qd, kd, vd, cq, ck, mq, mk, softmax_scale=scale, edge_src=s, edge_dst=d,
                                   return_lse=True)
@@ -69,6 +70,39 @@ def test_f32_cross_attention_pma_shape(device, seeds, lk):
     """PMA: k seeds per graph over the graph's tokens; graphs without tokens give zero rows; many short
     segments (each segment's queries form their own group)."""
     _check(device, [seeds] * len(lk), lk, seed=seeds + 1100 + len(lk))
+
+
+@pytest.mark.parametrize("hd", [16, 24, 32, 64])
+@pytest.mark.parametrize("seeds", [1, 3])
+def test_f32_few_query_route_head_dims(device, hd, seeds):
+    """Segments of at most four queries (max_seqlen_q <= 4: the PMA's expanded call) take the one-wave-per-query
+    forward: long, empty and one-token key sets, every head dim; the backward is the tiled one."""
+    _check(device, [seeds] * 5, [800, 0, 1, 63, 257], seed=1150 + hd + seeds, heads=128 // hd if hd != 24 else 8,
+           hd=hd)
+
+
+@pytest.mark.parametrize("hint", [1, 2])
+def test_f32_few_query_hint_below_the_true_maximum(device, hint):
+    """max_seqlen_q only chooses the route: with a hint below the true maximum (segments of up to 9 queries),
+    the few-query forward walks the extra queries and the results still match the oracle."""
+    _check(device, [9, 1, 0, 4, 7], [40, 3, 5, 130, 64], seed=1170 + hint, max_q=hint)
+
+
+@pytest.mark.parametrize("hd", [16, 64])
+def test_f32_few_query_dropout_matches_tiled(device, hd):
+    """With dropout the few-query forward applies the keep mask of the tiled forward: both routes on one seed
+    agree to the fp32 bar (outputs and log-sum-exp)."""
+    heads = 128 // hd
+    cu = torch.as_tensor(cu_from_lengths([2] * 6)).to(device)
+    ck = torch.as_tensor(cu_from_lengths([300, 1, 0, 77, 128, 64])).to(device)
+    q, k, v, _ = (t.to(device) for t in _inputs(12, int(ck[-1]), 1190 + hd, heads, hd))
+    few = A.attn_fwd(q, k, v, cu, ck, 2, 300, 0.25, dropout_p=0.1, dropout_seed=77)
+    tiled = A.attn_fwd(q, k, v, cu, ck, 0, 300, 0.25, dropout_p=0.1, dropout_seed=77)
+    for a, b, what in zip(few, tiled, ("out", "lse")):
+        a, b = a.cpu(), b.cpu()
+        fin = torch.isfinite(b)
+        assert torch.equal(torch.isfinite(a), fin), what
+        _close(a[fin].double(), b[fin].double(), what)
 
 
 def test_f32_masked_small_molecules(device):
