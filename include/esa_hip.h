@@ -453,6 +453,23 @@ ESA_API int esa_mish_bwd_colsum(const void* z, const void* grad, int64_t rows, i
                         int dtype, void* dz, float* dbias, void* workspace,
                         size_t workspace_bytes, void* stream);
 
+/* fp32 Linear layers of the blocks: y_i = x W_i^T + b_i for i < n_out      */
+/* (1-3) weights over one input, as nn.Linear computes them in fp32         */
+/* (fc_q / fc_k / fc_v share their input, esa/mha.py:54-56; fc_o and the    */
+/* MLP Linears take one, esa/mha.py:87, esa/mlp_utils.py:18-37).  Replaces  */
+/* F.linear for fp32 device tensors of these shapes; the modules call it    */
+/* for two or three weights over one input (one launch instead of several;  */
+/* a single weight runs as fast in the library GEMM).  x [rows, K], W_i     */
+/* [N_i, K], b_i [N_i] (or null), y_i [rows, N_i], all fp32, row-major and  */
+/* contiguous; K % 16 == 0, N_i % 64 == 0; x, W_i, y_i 16-byte aligned.     */
+/* weight, bias, y and out_features are host arrays of n_out entries.       */
+/* fp32 products accumulated in fp32 (an order of its own: results agree    */
+/* with a library GEMM to fp32 rounding, not bit for bit).  One launch;     */
+/* rows == 0 launches nothing (then x, W_i and y_i may be null).            */
+ESA_API int esa_linear_f32(const float* x, int rows, int in_features, int n_out,
+                   const float* const* weight, const float* const* bias, float* const* y,
+                   const int* out_features, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* Profiling hook (no counterpart in the reference; used by the benchmark).  */
 /* While enabled, every kernel launch of the entry points above is           */
@@ -461,7 +478,7 @@ ESA_API int esa_mish_bwd_colsum(const void* z, const void* grad, int64_t rows, i
 /* launch count per kernel id (capacity >= ESA_PROFILE_KERNELS) and clears   */
 /* the record.  Not for concurrent use from several threads.                 */
 /* ------------------------------------------------------------------------ */
-#define ESA_PROFILE_KERNELS 22
+#define ESA_PROFILE_KERNELS 23
 ESA_API int esa_profile_enable(int on);
 ESA_API int esa_profile_collect(float* total_ms, int* launches, int capacity);
 ESA_API const char* esa_profile_kernel_name(int kernel);

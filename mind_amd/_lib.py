@@ -100,6 +100,9 @@ _PROTOS = {
     "esa_column_sum": (_c_int, [_vp, _c_int, _c_i64, _c_int, _vp, _vp, _c_sz, _vp]),
     # z grad rows cols dtype dz dbias ws bytes stream
     "esa_mish_bwd_colsum": (_c_int, [_vp, _vp, _c_i64, _c_int, _c_int, _vp, _vp, _vp, _c_sz, _vp]),
+    # x rows in n_out | weight[] bias[] y[] out_features[] stream
+    "esa_linear_f32": (_c_int, [_vp, _c_int, _c_int, _c_int, ctypes.POINTER(_vp), ctypes.POINTER(_vp),
+                                ctypes.POINTER(_vp), ctypes.POINTER(_c_int), _vp]),
     "esa_mab_residual_fwd": (_c_int, [_vp, _vp, _vp, _c_i64, _c_int, _vp, _vp]),
     "esa_mab_residual_bwd": (_c_int, [_vp, _vp, _c_i64, _c_int, _vp, _vp, _vp]),
     "esa_profile_enable": (_c_int, [_c_int]),
@@ -107,7 +110,7 @@ _PROTOS = {
     "esa_profile_kernel_name": (ctypes.c_char_p, [_c_int]),
 }
 
-PROFILE_KERNELS = 22
+PROFILE_KERNELS = 23
 
 _lock = threading.Lock()
 _lib = None

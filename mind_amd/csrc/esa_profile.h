@@ -29,6 +29,7 @@ enum Kernel : int {
   kAttnEdgeLists,   // edge-mask key lists
   kAttnEdgeOverflow,  // edge-mask walk kernels over the overflow groups
   kSegmentMinMax,     // segmented minimum / maximum with argument
+  kLinearF32,         // fp32 Linear layers of the blocks
   kNumKernels
 };
 

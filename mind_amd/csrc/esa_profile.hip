@@ -21,7 +21,7 @@ const char* const kNames[kNumKernels] = {
     "attn_fwd", "attn_fwd_masked", "attn_bwd_dkdv", "attn_bwd_dkdv_masked", "attn_bwd_dq",
     "attn_bwd_dq_masked", "attn_prep", "edge_gather", "segment_sum", "csr_build", "graph_attn_fwd",
     "graph_attn_bwd_dq", "graph_attn_bwd_dkdv", "edge_gather_add", "mish_fwd", "mish_bwd", "layer_norm_fwd", "layer_norm_bwd", "column_sum",
-    "attn_edge_lists", "attn_edge_overflow", "segment_minmax",
+    "attn_edge_lists", "attn_edge_overflow", "segment_minmax", "linear_f32",
 };
 
 std::atomic<bool> g_enabled{false};

@@ -73,10 +73,10 @@ class _MabEpilogue(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, o, weight, bias, x):
-        from .linear import cast_param   # deferred: linear.py is a sibling with its own imports
+        from .linear import cast_param, linear_fwd   # deferred: linear.py is a sibling with its own imports
         ctx.dtypes = (weight.dtype, None if bias is None else bias.dtype)   # the gradients are returned in these
         weight, bias = cast_param(weight, o.dtype), cast_param(bias, o.dtype)
-        z = F.linear(o, weight, bias)
+        (z,) = linear_fwd(o, [(weight, bias)])
         lib, st, code = _lib.load(), _lib.stream_of(o), _DTYPES[o.dtype]
         if x is None:
             y = torch.empty_like(z)
@@ -142,10 +142,10 @@ class _LinearMish(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x, weight, bias):
-        from .linear import cast_param   # deferred: linear.py is a sibling with its own imports
+        from .linear import cast_param, linear_fwd   # deferred: linear.py is a sibling with its own imports
         ctx.dtypes = (weight.dtype, None if bias is None else bias.dtype)
         w, b = cast_param(weight, x.dtype), cast_param(bias, x.dtype)
-        z = F.linear(x, w, b)
+        (z,) = linear_fwd(x, [(w, b)])
         y = torch.empty_like(z)
         _lib.check(_lib.load().esa_mish_fwd(z.data_ptr(), None, z.numel(), _DTYPES[z.dtype], y.data_ptr(),
                                             _lib.stream_of(z)), "esa_mish_fwd")

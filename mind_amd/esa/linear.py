@@ -79,6 +79,60 @@ def column_sum(g: torch.Tensor) -> torch.Tensor:
     return out
 
 
+_MAX_LINEAR_OUT = 3
+
+
+def _aligned(t: torch.Tensor) -> bool:
+    return t.data_ptr() % 16 == 0
+
+
+def _f32_linear_ok(x: torch.Tensor, pairs) -> bool:
+    """Whether esa_linear_f32 takes F.linear(x, w, b) for every (w, b): fp32 device tensors, x [rows, K] and
+    W [N, K] contiguous, K % 16 == 0, N % 64 == 0, 16-byte aligned rows."""
+    if not (x.is_cuda and x.dtype == torch.float32 and x.dim() == 2 and x.is_contiguous() and _aligned(x)):
+        return False
+    k = x.shape[1]
+    if k < 16 or k % 16 or x.shape[0] >= 2 ** 31:
+        return False
+    for w, b in pairs:
+        if not (w.dtype == torch.float32 and w.dim() == 2 and w.shape[1] == k and w.shape[0] % 64 == 0
+                and w.is_contiguous() and _aligned(w) and w.device == x.device):
+            return False
+        if b is not None and not (b.dtype == torch.float32 and b.shape == (w.shape[0],) and b.is_contiguous()
+                                  and b.device == x.device):
+            return False
+    return True
+
+
+def esa_linear(x: torch.Tensor, pairs) -> list[torch.Tensor]:
+    """[F.linear(x, w, b) for (w, b) in pairs] through one launch of esa_linear_f32 (1-3 weights over one fp32
+    input of the shapes ``_f32_linear_ok`` accepts; raises otherwise)."""
+    pairs = list(pairs)
+    if not 1 <= len(pairs) <= _MAX_LINEAR_OUT or not _f32_linear_ok(x, pairs):
+        raise ValueError("esa_linear takes 1-3 fp32 weights [N % 64 == 0, K] over a contiguous fp32 x [rows, K], "
+                         "K % 16 == 0")
+    n = len(pairs)
+    ys = [torch.empty(x.shape[0], w.shape[0], dtype=torch.float32, device=x.device) for w, _ in pairs]
+    vp = ctypes.c_void_p
+    w_arr = (vp * n)(*[w.data_ptr() for w, _ in pairs])
+    b_arr = (vp * n)(*[None if b is None else b.data_ptr() for _, b in pairs])
+    y_arr = (vp * n)(*[y.data_ptr() for y in ys])
+    n_arr = (ctypes.c_int * n)(*[w.shape[0] for w, _ in pairs])
+    _lib.check(_lib.load().esa_linear_f32(x.data_ptr(), x.shape[0], x.shape[1], n, w_arr, b_arr, y_arr, n_arr,
+                                          _lib.stream_of(x)), "esa_linear_f32")
+    return ys
+
+
+def linear_fwd(x: torch.Tensor, pairs) -> list[torch.Tensor]:
+    """[F.linear(x, w, b) for (w, b) in pairs] over 2-D x.  Two or three fp32 weights sharing the input (the
+    MAB's Q / K / V projections) of the shapes esa_linear_f32 takes run as one launch of it; a single weight,
+    and everything else, is F.linear (at one weight the library GEMM is as fast or faster)."""
+    pairs = list(pairs)
+    if 2 <= len(pairs) <= _MAX_LINEAR_OUT and _f32_linear_ok(x, pairs):
+        return esa_linear(x, pairs)
+    return [F.linear(x, w, b) for w, b in pairs]
+
+
 def compute_dtype(x: torch.Tensor, *params: torch.Tensor | None):
     """The dtype a Linear over x computes in: the autocast dtype under autocast (x and the parameters are
     cast to it, as autocast casts F.linear's inputs), else x's dtype when every parameter has it; None for
@@ -98,7 +152,7 @@ class _Linear(torch.autograd.Function):
         w, b = cast_param(weight, x.dtype), cast_param(bias, x.dtype)
         ctx.save_for_backward(x, w)
         ctx.dtypes = (weight.dtype, None if bias is None else bias.dtype)
-        return F.linear(x, w, b)
+        return linear_fwd(x, [(w, b)])[0]
 
     @staticmethod
     def backward(ctx, g):
@@ -136,9 +190,11 @@ class _QKV(torch.autograd.Function):
         # the parameters' own dtypes: the backward returns its fp32 gradients in them
         ctx.params = tuple(None if p is None else p.dtype for p in (wq, bq, wk, bk, wv, bv))
         wq, bq, wk, bk, wv, bv = (cast_param(p, dt) for p in (wq, bq, wk, bk, wv, bv))
-        q = F.linear(xq, wq, bq)
-        k = F.linear(xk_, wk, bk)
-        v = F.linear(xk_, wv, bv)
+        if same:
+            q, k, v = linear_fwd(xq, [(wq, bq), (wk, bk), (wv, bv)])
+        else:
+            (q,) = linear_fwd(xq, [(wq, bq)])
+            k, v = linear_fwd(xk_, [(wk, bk), (wv, bv)])
         ctx.save_for_backward(xq, None if same else xk, wq, wk, wv)
         ctx.same = same
         return q, k, v

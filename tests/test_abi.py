@@ -104,6 +104,27 @@ def test_argument_errors_need_no_gpu():
     assert lib.esa_csr_segment_minmax(16, None, 16, 10, 1, f32, 1, -1, 16, 16, None) == -2
     assert lib.esa_csr_segment_minmax(16, None, 16, 10, 1, 7, 0, 5, 16, 16, None) == -5
     assert lib.esa_csr_segment_minmax(16, None, 16, 0, 1, bf16, 1, 5, 16, None, None) == 0
+    # fp32 Linear: shape, null and alignment errors before any launch; zero rows is a no-op
+    vp, ci = ctypes.c_void_p, ctypes.c_int
+
+    def lin(x, rows, k, ws, bs, ys, ns, n_out=None):
+        n_out = len(ws) if n_out is None else n_out
+        m = max(len(ws), 1)
+        return lib.esa_linear_f32(x, rows, k, n_out, (vp * m)(*ws), (vp * m)(*bs), (vp * m)(*ys), (ci * m)(*ns),
+                                  None)
+    assert lin(16, 10, 128, [16], [None], [16], [64], n_out=0) == -2
+    assert lin(16, 10, 128, [16] * 4, [None] * 4, [16] * 4, [64] * 4) == -2
+    assert lin(16, 10, 120, [16], [None], [16], [64]) == -2          # K % 16
+    assert lin(16, 10, 8, [16], [None], [16], [64]) == -2            # K < 16
+    assert lin(16, 10, 128, [16], [None], [16], [96]) == -2          # N % 64
+    assert lin(16, -1, 128, [16], [None], [16], [64]) == -2
+    assert lin(16, 10, 128, [None], [None], [16], [64]) == -1
+    assert lin(None, 10, 128, [16], [None], [16], [64]) == -1
+    assert lin(16, 10, 128, [24], [None], [16], [64]) == -6
+    assert lin(8, 10, 128, [16], [None], [16], [64]) == -6
+    assert lib.esa_linear_f32(16, 10, 128, 1, None, None, None, None, None) == -1
+    assert lin(None, 0, 128, [16, 32], [None, 16], [16, 48], [64, 128]) == 0
+    assert lin(None, 0, 128, [None], [None], [None], [64]) == 0   # empty tensors may have null pointers
     # node plan: size errors, and a planned backward needs only its row statistics
     node, node_plan = _lib.ESA_MASK_NODE, _lib.ESA_MASK_NODE_PLAN
     assert lib.esa_node_plan_size(100, 100, -1, ctypes.byref(n)) == -2
