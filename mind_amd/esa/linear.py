@@ -19,6 +19,8 @@ Reference: the nn.Linear layers of the MAB (esa/mha.py:12-15) and of the MLPs
 """
 from __future__ import annotations
 
+import contextlib
+import contextvars
 import ctypes
 
 import torch
@@ -47,15 +49,16 @@ def weight_grad(g: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
     t, o = g.shape
     i = x.shape[1]
     s = split_count(t, o, i)
+    # bf16 device operands: products accumulated and returned in fp32 by the GEMM itself (out_dtype), no casts
+    kw = {} if g.dtype == torch.float32 or not g.is_cuda else {"out_dtype": torch.float32}
     if t < _MIN_CHUNK:
-        return g.t().float().mm(x.float())
+        return torch.mm(g.t(), x, **kw) if kw else g.t().float().mm(x.float())
     c = t // s
     t0 = s * c
-    kw = {} if g.dtype == torch.float32 else {"out_dtype": torch.float32}
     parts = torch.bmm(g[:t0].view(s, c, o).transpose(1, 2), x[:t0].view(s, c, i), **kw)
     dw = parts.sum(0)
-    if t0 < t:   # fewer than S leftover tokens
-        dw += g[t0:].t().float().mm(x[t0:].float())
+    if t0 < t:   # fewer than S leftover tokens: added by the GEMM's epilogue
+        dw = torch.addmm(dw, g[t0:].t(), x[t0:], **kw)
     return dw
 
 
@@ -142,8 +145,53 @@ def compute_dtype(x: torch.Tensor, *params: torch.Tensor | None):
     return x.dtype if all(p is None or p.dtype == x.dtype for p in params) else None
 
 
+_CAST_CACHE: contextvars.ContextVar = contextvars.ContextVar("esa_param_cast_cache", default=None)
+_CAST_ALIGN = 128   # elements per cache slot boundary: every cached view starts 256-byte aligned in bf16
+
+
 def cast_param(p: torch.Tensor | None, dt: torch.dtype):
-    return None if p is None else p.to(dt)
+    """p in dtype dt: the view cached by an enclosing ``param_casts`` when there is one, else p.to(dt)."""
+    if p is None or p.dtype == dt:
+        return p
+    cache = _CAST_CACHE.get()
+    if cache is not None:
+        hit = cache.get(id(p))
+        if hit is not None and hit[0] is p and hit[1].dtype == dt:
+            return hit[1]
+    return p.to(dt)
+
+
+@contextlib.contextmanager
+def param_casts(params, dt: torch.dtype):
+    """Within the block, the Linear functions take the given fp32 device parameters cast to ``dt`` from one
+    concatenated cast (a forward under autocast casts every Linear's weight and bias, about a hundred launches of
+    a few microseconds for configuration 4's stack; here two or three).  The cached values equal p.to(dt) bit
+    for bit; each parameter's slot starts 256-byte aligned."""
+    ps, seen = [], set()
+    for p in params:
+        if p is not None and p.is_cuda and p.dtype == torch.float32 and p.dtype != dt and id(p) not in seen:
+            seen.add(id(p))
+            ps.append(p)
+    if not ps:
+        yield
+        return
+    pad = torch.zeros(_CAST_ALIGN, dtype=torch.float32, device=ps[0].device)
+    pieces, offsets, off = [], [], 0
+    for p in ps:
+        pieces.append(p.detach().reshape(-1))
+        offsets.append(off)
+        off += p.numel()
+        r = -off % _CAST_ALIGN
+        if r:
+            pieces.append(pad[:r])
+            off += r
+    flat = torch.cat(pieces).to(dt)
+    cache = {id(p): (p, flat[o:o + p.numel()].view(p.shape)) for p, o in zip(ps, offsets)}
+    token = _CAST_CACHE.set(cache)
+    try:
+        yield
+    finally:
+        _CAST_CACHE.reset(token)
 
 
 class _Linear(torch.autograd.Function):

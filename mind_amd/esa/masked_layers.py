@@ -27,6 +27,8 @@ Backend ``xformers_or_torch_attn``:
 """
 from __future__ import annotations
 
+import contextlib
+
 import torch
 from torch import nn
 from torch.nn import functional as F
@@ -34,7 +36,7 @@ from torch.nn import functional as F
 from .activations import mab_epilogue, mish
 from .attention import pma_attention, varlen_attention
 from .layer_norm import layer_norm
-from .linear import apply, qkv_projection
+from .linear import apply, param_casts, qkv_projection
 from .mha import PMA, SAB, _heads, attn_dropout, pooled_attention
 from .mha_flash_varlen import PMAFlashVarlen, SABFlashVarlen
 from .mlp_utils import GatedMLPMulti, SmallMLP
@@ -352,11 +354,20 @@ class ESA(nn.Module):
         Without a PMA the head acts per token, and the result keeps the padded forward's [B, N, dim_output]
         shape (esa/masked_layers.py:929-936): the head runs on the padded embeddings, which are zero at the
         padding slots, so those slots hold mish(bias)."""
-        enc = self._encode_packed(tokens.unpad(X), tokens)
-        enc_pad = tokens.pad(enc)
-        if hasattr(self, "decoder"):
-            return self._decode_packed(enc, tokens, edge_index, batch_mapping), enc_pad
-        return mish(self.decoder_linear(enc_pad)), enc_pad
+        with self._linear_casts():
+            enc = self._encode_packed(tokens.unpad(X), tokens)
+            enc_pad = tokens.pad(enc)
+            if hasattr(self, "decoder"):
+                return self._decode_packed(enc, tokens, edge_index, batch_mapping), enc_pad
+            return mish(self.decoder_linear(enc_pad)), enc_pad
+
+    def _linear_casts(self):
+        """Under autocast, the blocks' Linear parameters cast once per forward in one concatenated cast
+        (``linear.param_casts``) instead of one cast per parameter and call."""
+        if not torch.is_autocast_enabled("cuda"):
+            return contextlib.nullcontext()
+        params = [t for m in self.modules() if isinstance(m, nn.Linear) for t in (m.weight, m.bias)]
+        return param_casts(params, torch.get_autocast_dtype("cuda"))
 
     def _encode_packed(self, tokens_x: torch.Tensor, tokens: PackedSets) -> torch.Tensor:
         """Encoder blocks and the input residual on packed tokens [T, D] (esa/masked_layers.py:914-921)."""
@@ -391,8 +402,9 @@ class ESA(nn.Module):
                              f"{self.xformers_or_torch_attn!r}")
         if tokens_x.dim() != 2 or tokens_x.shape[0] != tokens.num_tokens:
             raise ValueError(f"tokens_x must be [T, D] with T = {tokens.num_tokens} (got {tuple(tokens_x.shape)})")
-        enc = self._encode_packed(tokens_x, tokens)
-        if hasattr(self, "decoder"):
-            return self._decode_packed(enc, tokens, edge_index, batch_mapping), enc
-        # no PMA: the head acts on every token; packed, it returns [T, dim_output] (the padded entry pads)
-        return mish(self.decoder_linear(enc)), enc
+        with self._linear_casts():
+            enc = self._encode_packed(tokens_x, tokens)
+            if hasattr(self, "decoder"):
+                return self._decode_packed(enc, tokens, edge_index, batch_mapping), enc
+            # no PMA: the head acts on every token; packed, it returns [T, dim_output] (the padded entry pads)
+            return mish(self.decoder_linear(enc)), enc
