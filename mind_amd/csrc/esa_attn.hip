@@ -1653,42 +1653,59 @@ __global__ __launch_bounds__(kF32Threads * f32_splits<HD>()) void attn_fwd_f32_k
   a.lse_out[(size_t)head * a.total_q + oi] = l > 0.f ? (m + fast_log2(l)) * kLn2 : -INFINITY;
 }
 
-// fp32 forward for segments of a few queries (the PMA's seeds: the expanded
-// call has k queries per set).  The tiled kernel gives each (segment, head) a
-// 128-thread block in which k lanes walk every key of the segment, so its
-// time is that of the longest segment's walk; here one wave takes one
-// (segment, query slot, head), its 64 lanes take the segment's keys in turn
-// (key kb + lane + 64 i) with a running maximum and sum per lane, and the
-// lanes' partials merge by a butterfly in a fixed order.  A slot past the
-// hint's count walks the segment's later queries (slot + slots, ...), so any
-// number of queries per segment is computed; the hint only sets the grid.
-struct AttnF32FewArgs {
+// fp32 calls with segments of a few queries (the PMA's seeds: the expanded
+// call has k queries per set).  The tiled fp32 kernels give each (segment,
+// head) a 128-thread block in which k lanes are live and that walks every
+// key of the segment, so their time is that of the longest segment's walk.
+// Here the forward and dQ take one wave per (segment, query slot, head): its
+// 64 lanes take the segment's keys in turn (key kb + lane + 64 i) with
+// per-lane partials (running maximum and sum, or the dQ sum) that merge by a
+// butterfly in a fixed order.  A slot also walks the segment's later queries
+// (slot + slots, ...), so any number of queries per segment is computed; the
+// caller's max_seqlen_q only sets the grid.  dK/dV takes one thread per (key,
+// head) that walks its segment's queries.  (bf16 calls keep the MFMA
+// kernels: with many heads and seeds, each slot's wave re-reading its
+// segment's key rows costs more than the MFMA kernels' single pass.)
+struct AttnFewArgs {
   DropoutCfg drop;
-  const float* q; const float* k; const float* v;
+  const float* q; const float* k; const float* v; const float* out; const float* dout;
+  const float* lse;
   const int* cu_q; const int* cu_k;
-  int nseg, heads, total_q, slots, blocks_per_seg;
-  float c;
-  float* o; float* lse_out;
+  int nseg, heads, total_q, total_k, slots, blocks_per_seg;
+  float c, scale;
+  float2* rows;   // backward: (LSE2, D) per (head, query), written by dQ, read by dK/dV; row stride total_q
+  float* o; float* lse_out; float* dq; float* dk; float* dv;
 };
 
+// The wave's (segment, query slot, head) for the forward and dQ; false for a
+// wave past the hint's slots (wave-uniform).
+struct FewWave { int seg, slot, head; };
+DEVI bool few_wave(const AttnFewArgs& a, FewWave& f) {
+  f.seg = blockIdx.x / a.blocks_per_seg;
+  const int w = (blockIdx.x - f.seg * a.blocks_per_seg) * 4 + (int)(threadIdx.x >> 6);
+  f.slot = w / a.heads;
+  f.head = w - f.slot * a.heads;
+  return f.seg < a.nseg && f.slot < a.slots;
+}
+
 template <int HD, bool DROP>
-__global__ __launch_bounds__(256) void attn_fwd_f32_few_kernel(const AttnF32FewArgs a) {
+__global__ __launch_bounds__(256) void attn_fwd_few_kernel(const AttnFewArgs a) {
   const int H = a.heads, lane = threadIdx.x & 63;
-  const int seg = blockIdx.x / a.blocks_per_seg;
-  const int w = (blockIdx.x - seg * a.blocks_per_seg) * 4 + (int)(threadIdx.x >> 6);
-  const int slot = w / H, head = w - slot * H;
-  if (seg >= a.nseg || slot >= a.slots) return;   // wave-uniform: no barriers in this kernel
-  const int qb = a.cu_q[seg], qe = a.cu_q[seg + 1], kb = a.cu_k[seg], ke = a.cu_k[seg + 1];
-  for (int qi = qb + slot; qi < qe; qi += a.slots) {
+  FewWave f;
+  if (!few_wave(a, f)) return;   // wave-uniform: no barriers in this kernel
+  const int head = f.head;
+  const int qb = a.cu_q[f.seg], qe = a.cu_q[f.seg + 1], kb = a.cu_k[f.seg], ke = a.cu_k[f.seg + 1];
+  const float *Q = a.q, *K = a.k, *V = a.v;
+  for (int qi = qb + f.slot; qi < qe; qi += a.slots) {
     float q[HD], acc[HD];
-    loadn<HD>(a.q + ((size_t)qi * H + head) * HD, q);
+    loadn<HD>(Q + ((size_t)qi * H + head) * HD, q);
 #pragma unroll
     for (int i = 0; i < HD; ++i) acc[i] = 0.f;
     const uint32_t rk = DROP ? drop_row(a.drop, qi, head) : 0u;
     float m = -INFINITY, l = 0.f;
     for (int kj = kb + lane; kj < ke; kj += 64) {
       float kx[HD];
-      loadn<HD>(a.k + ((size_t)kj * H + head) * HD, kx);
+      loadn<HD>(K + ((size_t)kj * H + head) * HD, kx);
       float d = 0.f;
 #pragma unroll
       for (int i = 0; i < HD; ++i) d = fmaf(q[i], kx[i], d);
@@ -1704,7 +1721,7 @@ __global__ __launch_bounds__(256) void attn_fwd_f32_few_kernel(const AttnF32FewA
       l += p;
       const float pv = DROP && !drop_keep(a.drop, rk, drop_col(a.drop, kj), kj) ? 0.f : p;
       float vx[HD];
-      loadn<HD>(a.v + ((size_t)kj * H + head) * HD, vx);
+      loadn<HD>(V + ((size_t)kj * H + head) * HD, vx);
 #pragma unroll
       for (int i = 0; i < HD; ++i) acc[i] = fmaf(pv, vx[i], acc[i]);
     }
@@ -1722,10 +1739,116 @@ __global__ __launch_bounds__(256) void attn_fwd_f32_few_kernel(const AttnF32FewA
       m = mn;
     }
     if (lane == 0) {
-      storen<HD>(a.o + ((size_t)qi * H + head) * HD, acc, l > 0.f ? (DROP ? a.drop.inv_keep : 1.f) / l : 0.f);
+      storen<HD>(a.o + ((size_t)qi * H + head) * HD, acc,
+                       l > 0.f ? (DROP ? a.drop.inv_keep : 1.f) / l : 0.f);
       a.lse_out[(size_t)head * a.total_q + qi] = l > 0.f ? (m + fast_log2(l)) * kLn2 : -INFINITY;
     }
   }
+}
+
+// dQ_i = scale sum_j P_ij (dP_ij - D_i) k_j with P recomputed from the saved
+// LSE and D_i = rowsum(dO_i * O_i); writes (LSE2, D) for the dK/dV pass.
+template <int HD, bool DROP>
+__global__ __launch_bounds__(256) void attn_dq_few_kernel(const AttnFewArgs a) {
+  const int H = a.heads, lane = threadIdx.x & 63;
+  FewWave f;
+  if (!few_wave(a, f)) return;   // wave-uniform: no barriers in this kernel
+  const int head = f.head;
+  const int qb = a.cu_q[f.seg], qe = a.cu_q[f.seg + 1], kb = a.cu_k[f.seg], ke = a.cu_k[f.seg + 1];
+  const float *Q = a.q, *K = a.k, *V = a.v;
+  for (int qi = qb + f.slot; qi < qe; qi += a.slots) {
+    float q[HD], g[HD], acc[HD];
+    loadn<HD>(Q + ((size_t)qi * H + head) * HD, q);
+    loadn<HD>(a.dout + ((size_t)qi * H + head) * HD, g);
+    {
+      float o[HD];
+      loadn<HD>(a.out + ((size_t)qi * H + head) * HD, o);
+      float d = 0.f;
+#pragma unroll
+      for (int i = 0; i < HD; ++i) d = fmaf(g[i], o[i], d);
+      acc[0] = d;   // D_i, the same in every lane
+    }
+    const float D = acc[0];
+#pragma unroll
+    for (int i = 0; i < HD; ++i) acc[i] = 0.f;
+    const float lse = a.lse[(size_t)head * a.total_q + qi];
+    const float lse2 = lse * kLog2e;   // a query without keys (-inf) walks no key
+    const uint32_t rk = DROP ? drop_row(a.drop, qi, head) : 0u;
+    for (int kj = kb + lane; kj < ke; kj += 64) {
+      float kx[HD], vx[HD];
+      loadn<HD>(K + ((size_t)kj * H + head) * HD, kx);
+      loadn<HD>(V + ((size_t)kj * H + head) * HD, vx);
+      float s = 0.f, dp = 0.f;
+#pragma unroll
+      for (int i = 0; i < HD; ++i) {
+        s = fmaf(q[i], kx[i], s);
+        dp = fmaf(g[i], vx[i], dp);
+      }
+      const float p = fast_exp2(a.c * s - lse2);
+      if (DROP) dp = drop_keep(a.drop, rk, drop_col(a.drop, kj), kj) ? dp * a.drop.inv_keep : 0.f;
+      const float ds = p * (dp - D);
+#pragma unroll
+      for (int i = 0; i < HD; ++i) acc[i] = fmaf(ds, kx[i], acc[i]);
+    }
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1)
+#pragma unroll
+      for (int i = 0; i < HD; ++i) acc[i] += __shfl_xor(acc[i], off);
+    if (lane == 0) {
+      storen<HD>(a.dq + ((size_t)qi * H + head) * HD, acc, a.scale);
+      a.rows[(size_t)head * a.total_q + qi] = make_float2(lse2, D);
+    }
+  }
+}
+
+// dV_j = sum_i P_ij dO_i, dK_j = scale sum_i P_ij (dP_ij - D_i) q_i: one
+// thread per (key, head), heads fastest; the key's segment by a binary search
+// over cu_k; keys in no segment get zeros.
+template <int HD, bool DROP>
+__global__ __launch_bounds__(256) void attn_dkdv_few_kernel(const AttnFewArgs a) {
+  const int H = a.heads;
+  const long gid = (long)blockIdx.x * 256 + threadIdx.x;
+  if (gid >= (long)a.total_k * H) return;
+  const int kj = (int)(gid / H), head = (int)(gid - (long)kj * H);
+  int lo = 0, hi = a.nseg;   // the last segment whose start is <= kj
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (a.cu_k[mid] <= kj) lo = mid; else hi = mid - 1;
+  }
+  const int seg = lo;
+  float dk[HD], dv[HD];
+#pragma unroll
+  for (int i = 0; i < HD; ++i) dk[i] = dv[i] = 0.f;
+  if (seg < a.nseg && kj >= a.cu_k[seg] && kj < a.cu_k[seg + 1]) {
+    const int qb = a.cu_q[seg], qe = a.cu_q[seg + 1];
+    float kx[HD], vx[HD];
+    loadn<HD>(a.k + ((size_t)kj * H + head) * HD, kx);
+    loadn<HD>(a.v + ((size_t)kj * H + head) * HD, vx);
+    const uint32_t ck = DROP ? drop_col(a.drop, kj) : 0u;
+    for (int qi = qb; qi < qe; ++qi) {
+      float q[HD], g[HD];
+      loadn<HD>(a.q + ((size_t)qi * H + head) * HD, q);
+      loadn<HD>(a.dout + ((size_t)qi * H + head) * HD, g);
+      const float2 rs = a.rows[(size_t)head * a.total_q + qi];
+      float s = 0.f, dp = 0.f;
+#pragma unroll
+      for (int i = 0; i < HD; ++i) {
+        s = fmaf(kx[i], q[i], s);
+        dp = fmaf(vx[i], g[i], dp);
+      }
+      const float p = fast_exp2(a.c * s - rs.x);
+      const bool keep = !DROP || drop_keep(a.drop, drop_row(a.drop, qi, head), ck, kj);
+      const float pv = keep ? p : 0.f;
+#pragma unroll
+      for (int i = 0; i < HD; ++i) dv[i] = fmaf(pv, g[i], dv[i]);
+      if (DROP) dp = keep ? dp * a.drop.inv_keep : 0.f;
+      const float ds = p * (dp - rs.y);
+#pragma unroll
+      for (int i = 0; i < HD; ++i) dk[i] = fmaf(ds, q[i], dk[i]);
+    }
+  }
+  storen<HD>(a.dv + ((size_t)kj * H + head) * HD, dv, DROP ? a.drop.inv_keep : 1.f);
+  storen<HD>(a.dk + ((size_t)kj * H + head) * HD, dk, a.scale);
 }
 
 // dQ = scale * sum_j P_ij (dP_ij - D_i) k_j, P recomputed from the saved LSE.
@@ -2341,20 +2464,43 @@ constexpr unsigned kF32FwdThreads(int hd) { return kF32Threads * (hd >= 64 ? f32
     else                                                                                                   \
       hipLaunchKernelGGL((attn_fwd_f32_kernel<false, 64, D>), grid, dim3(kF32FwdThreads(64)), 0, st, a);    \
   } while (0)
-// Query segments of at most this many tokens (the caller's max_seqlen_q) take attn_fwd_f32_few_kernel.
-constexpr int kF32FewQueries = 4;
-#define ESA_F32_FEW_HD(D, hd, grid, st, a)                                                        \
-  do {                                                                                            \
-    if (hd == 16) hipLaunchKernelGGL((attn_fwd_f32_few_kernel<16, D>), grid, dim3(256), 0, st, a);  \
-    else if (hd == 24) hipLaunchKernelGGL((attn_fwd_f32_few_kernel<24, D>), grid, dim3(256), 0, st, a); \
-    else if (hd == 32) hipLaunchKernelGGL((attn_fwd_f32_few_kernel<32, D>), grid, dim3(256), 0, st, a); \
-    else hipLaunchKernelGGL((attn_fwd_f32_few_kernel<64, D>), grid, dim3(256), 0, st, a);         \
+// Unmasked fp32 calls whose max_seqlen_q is 1..kFewQueries take the few-query kernels (the forward at
+// every head dim, the backward at head dims up to kFewBwdMaxHd: a dK/dV thread holds six rows of the head dim).
+constexpr int kFewQueries = 4, kFewBwdMaxHd = 32;
+template <bool D>
+void few_launch(int which, int hd, dim3 grid, hipStream_t st, const AttnFewArgs& a) {
+#define ESA_FEW_K(KERNEL, HD) hipLaunchKernelGGL((KERNEL<HD, D>), grid, dim3(256), 0, st, a)
+#define ESA_FEW_HD(KERNEL)                                       \
+  do {                                                           \
+    if (hd == 16) ESA_FEW_K(KERNEL, 16);                         \
+    else if (hd == 24) ESA_FEW_K(KERNEL, 24);                    \
+    else ESA_FEW_K(KERNEL, 32);                                  \
   } while (0)
-#define ESA_F32_FEW_LAUNCH(hd, drop, grid, st, a)   \
-  do {                                              \
-    if (drop) ESA_F32_FEW_HD(true, hd, grid, st, a); \
-    else ESA_F32_FEW_HD(false, hd, grid, st, a);     \
-  } while (0)
+  if (which == 0) {
+    if (hd == 64) ESA_FEW_K(attn_fwd_few_kernel, 64);
+    else ESA_FEW_HD(attn_fwd_few_kernel);
+  } else if (which == 1) {
+    ESA_FEW_HD(attn_dq_few_kernel);
+  } else {
+    ESA_FEW_HD(attn_dkdv_few_kernel);
+  }
+#undef ESA_FEW_HD
+#undef ESA_FEW_K
+}
+void few_go(int which, bool drop, int hd, dim3 grid, hipStream_t st, const AttnFewArgs& a) {
+  if (drop) few_launch<true>(which, hd, grid, st, a); else few_launch<false>(which, hd, grid, st, a);
+}
+// Arguments of the few-query kernels; the forward and dQ grid (waves per segment: slots x heads, 4 per block).
+AttnFewArgs few_args(const void* q, const void* k, const void* v, const int* cu_q, const int* cu_k, int nseg,
+                     int total_q, int total_k, int heads, int slots, float scale, const DropoutCfg& drop) {
+  AttnFewArgs f{};
+  f.q = static_cast<const float*>(q); f.k = static_cast<const float*>(k); f.v = static_cast<const float*>(v); f.cu_q = cu_q; f.cu_k = cu_k; f.nseg = nseg;
+  f.total_q = total_q; f.total_k = total_k; f.heads = heads; f.slots = slots;
+  f.blocks_per_seg = (slots * heads + 3) / 4;
+  f.c = scale * kLog2e; f.scale = scale; f.drop = drop;
+  return f;
+}
+
 #define ESA_F32_FWD_LAUNCH(hd, drop, grid, st, a)  \
   do {                                             \
     if (drop) ESA_F32_FWD_HD(true, hd, grid, st, a); \
@@ -2497,6 +2643,15 @@ int esa_varlen_attn_fwd(const void* q, const void* k, const void* v, const int* 
   if (!(softmax_scale > 0.f)) return ESA_ERR_SHAPE;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const bool f32 = dtype == ESA_F32;
+  if (f32 && !masked && max_seqlen_q > 0 && max_seqlen_q <= kFewQueries) {   // the PMA's seeds: no workspace
+    AttnFewArgs fa = few_args(q, k, v, cu_seqlens_q, cu_seqlens_k, batch, total_q, total_k, heads, max_seqlen_q,
+                              softmax_scale, dcfg);
+    fa.o = static_cast<float*>(out); fa.lse_out = softmax_lse;
+    ESA_TIMED(esa_profile::kAttnFwd, st,
+              few_go(0, drop, head_dim, dim3((unsigned)batch * (unsigned)fa.blocks_per_seg), st, fa));
+    ESA_LAUNCH_CHECK();
+    return ESA_OK;
+  }
   if (!masked && !f32) {
     if (!workspace) return ESA_ERR_NULL;
     DenseAttnCall c{};
@@ -2522,18 +2677,6 @@ int esa_varlen_attn_fwd(const void* q, const void* k, const void* v, const int* 
     g.drop = dcfg; g.dropout = drop;
     g.out = out; g.lse = softmax_lse;
     return graph_edge_attn_fwd(g, dtype, st);
-  }
-  if (f32 && !masked && max_seqlen_q > 0 && max_seqlen_q <= kF32FewQueries) {
-    AttnF32FewArgs fa{};
-    fa.q = static_cast<const float*>(q); fa.k = static_cast<const float*>(k); fa.v = static_cast<const float*>(v);
-    fa.cu_q = cu_seqlens_q; fa.cu_k = cu_seqlens_k; fa.nseg = batch; fa.heads = heads; fa.total_q = total_q;
-    fa.slots = max_seqlen_q; fa.blocks_per_seg = (max_seqlen_q * heads + 3) / 4;
-    fa.c = softmax_scale * kLog2e; fa.drop = dcfg;
-    fa.o = static_cast<float*>(out); fa.lse_out = softmax_lse;
-    const dim3 grid((unsigned)batch * (unsigned)fa.blocks_per_seg);
-    ESA_TIMED(esa_profile::kAttnFwd, st, ESA_F32_FEW_LAUNCH(head_dim, drop, grid, st, fa));
-    ESA_LAUNCH_CHECK();
-    return ESA_OK;
   }
   if (f32) {
     PrepArgs pa{};
@@ -2616,7 +2759,7 @@ int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k, const vo
                         unsigned long long dropout_seed, int mask_kind, const int* mask_a, const int* mask_b,
                         int n_mask_edges, void* dq, void* dk, void* dv, void* workspace, size_t workspace_bytes,
                         void* stream) {
-  (void)max_seqlen_q; (void)max_seqlen_k;
+  (void)max_seqlen_k;   // max_seqlen_q routes calls with few queries per segment; results never depend on it
   int rc = check_common(batch, total_q, total_k, heads, head_dim, dtype, mask_kind);
   if (rc) return rc;
   if (!(dropout_p >= 0.f && dropout_p < 1.f)) return ESA_ERR_DROPOUT;
@@ -2666,6 +2809,21 @@ int esa_varlen_attn_bwd(const void* dout, const void* q, const void* k, const vo
     if ((rc = launch_zero(dq, (size_t)total_q * heads * head_dim * esz, st))) return rc;
     if ((rc = launch_zero(dk, (size_t)total_k * heads * head_dim * esz, st))) return rc;
     if ((rc = launch_zero(dv, (size_t)total_k * heads * head_dim * esz, st))) return rc;
+    return ESA_OK;
+  }
+  if (f32 && !masked && max_seqlen_q > 0 && max_seqlen_q <= kFewQueries && head_dim <= kFewBwdMaxHd) {
+    // the PMA's seeds: dQ (writing the row statistics at the workspace's start), then dK/dV
+    if (workspace_bytes < (size_t)heads * total_q * sizeof(float2)) return ESA_ERR_WORKSPACE;
+    AttnFewArgs fa = few_args(q, k, v, cu_seqlens_q, cu_seqlens_k, batch, total_q, total_k, heads, max_seqlen_q,
+                              softmax_scale, dcfg);
+    fa.out = static_cast<const float*>(out); fa.dout = static_cast<const float*>(dout); fa.lse = softmax_lse;
+    fa.rows = static_cast<float2*>(workspace);
+    fa.dq = static_cast<float*>(dq); fa.dk = static_cast<float*>(dk); fa.dv = static_cast<float*>(dv);
+    ESA_TIMED(esa_profile::kAttnBwdDq, st,
+              few_go(1, drop, head_dim, dim3((unsigned)batch * (unsigned)fa.blocks_per_seg), st, fa));
+    ESA_TIMED(esa_profile::kAttnBwdDkdv, st,
+              few_go(2, drop, head_dim, dim3((unsigned)(((long)total_k * heads + 255) / 256)), st, fa));
+    ESA_LAUNCH_CHECK();
     return ESA_OK;
   }
   if (!masked && !f32) {
