@@ -96,6 +96,12 @@ ESA_API const char* esa_version(void);
 /*                                                                           */
 /* A query with no admissible key gets output 0 and lse = -inf.              */
 /*                                                                           */
+/* max_seqlen_q / max_seqlen_k never change a result.  max_seqlen_q selects */
+/* a route: unmasked ESA_F32 calls with 1 <= max_seqlen_q <= 4 (the PMA's   */
+/* seeds) take kernels with one wave per (segment, query, head) that walk   */
+/* every query of a segment whatever the value, so a value below the true   */
+/* maximum costs time, not correctness.                                     */
+/*                                                                           */
 /* dropout_p in [0, 1): attention dropout on the softmax probabilities, as   */
 /* the reference's p / dropout_p in training (esa/mha.py:76,82): out =       */
 /* (P o Z s) V with the keep mask Z a counter-based hash of (dropout_seed,   */
