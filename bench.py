@@ -1100,7 +1100,8 @@ def bench_block(args, sub: bool = False):
     The batch's atom types, edge_index and batch mapping are in HBM before the timed region; a step computes
     the edge tokens from them and runs the block.  Timed twice: launched eagerly, and captured once into a HIP
     graph (mind_amd.esa.graphs.GraphedForward) whose replays take the same inputs (copied into the graph's
-    input buffers each step); the replay's outputs are checked bit for bit against the eager step's."""
+    input buffers each step); the replay's outputs are checked bit for bit against the eager step's.  The
+    replay is the reported step (ms_per_step, value); the eager step is the `eager` sub-object."""
     import torch
 
     from mind_amd import generators
@@ -1141,27 +1142,33 @@ def bench_block(args, sub: bool = False):
                  "bit_identical_to_eager": all(torch.equal(a, b) for a, b in zip(got, ref)),
                  "what": "the same step captured once into a HIP graph and replayed (inputs copied into the "
                          "graph's input buffers each step): one launch per step instead of about a hundred"}
+    # The step as it runs: replayed as one HIP graph (every kernel of the step, inputs copied in each step);
+    # the eager step (about a hundred host launches, host-bound) is reported beside it.  --no-graph: eager.
+    p_ms, p_wall = (g_ms, g_wall) if graph else (ms, wall_ms)
+    eager = {"ms_per_step": ms, "wall_ms_per_step": wall_ms, "edge_tokens_per_s": t / (ms * 1e-3),
+             "ms_per_step_profiled": ms_prof, "library_kernel_ms_per_step": lib_ms, "other_ms_per_step": ms - lib_ms,
+             "what": "the step launched eagerly from Python; kernels: this library's launches (HIP events per "
+                     "launch); other: the rest of the step (torch GEMMs, embedding, gathers of the padded views, "
+                     "launch gaps)"}
+    mode = "HIP graph replay (mind_amd.esa.graphs.GraphedForward)" if graph else "eager launches"
     if sub:
         out = {"workload": "config0: edge tokens (embed, gather, project) + ESA block M-S-P(1 seed) forward, fp32",
-               "graphs": gb.num_graphs, "edge_tokens": t, "dim": d, "heads": h, "ms_per_step": ms,
-               "wall_ms_per_step": wall_ms, "edge_tokens_per_s": t / (ms * 1e-3), "ms_per_step_profiled": ms_prof,
-               "kernels": kern, "library_kernel_ms_per_step": lib_ms,
-               "other_ms_per_step": ms - lib_ms, "graph": graph,
-               "split": "kernels: this library's launches (HIP events per launch); other: the step's remaining "
-                        "time (torch GEMMs, embedding, gathers of the padded views, launch gaps)"}
+               "graphs": gb.num_graphs, "edge_tokens": t, "dim": d, "heads": h, "ms_per_step": p_ms,
+               "wall_ms_per_step": p_wall, "edge_tokens_per_s": t / (p_ms * 1e-3), "execution": mode,
+               "kernels": kern, "eager": eager, "graph": graph}
         if not args.no_cpu_baseline:
             out["cpu_baseline"] = cpu_baseline_block(gb, types, emb, proj, model, h)
         return out
     result = {
         "metric": "edge-tokens/sec through the ESA block forward (fp32)",
-        "value": t / (ms * 1e-3), "unit": "edge-tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "value": t / (p_ms * 1e-3), "unit": "edge-tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": p_ms, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32",
         "data": "synthetic (seeded small molecules: 64 graphs, 9-29 atoms, radius 5 A; random-init weights)",
         "config": {"workload": "config0: edge tokens (embed, gather, project) + ESA block M-S-P(1 seed) forward",
                    "graphs": gb.num_graphs, "edge_tokens": t, "max_seqlen": gb.max_seqlen, "dim": d, "heads": h,
                    "seed": args.seed},
-        "wall_ms_per_step": wall_ms, "ms_per_step_profiled": ms_prof, "kernels": kern,
-        "library_kernel_ms_per_step": lib_ms, "graph": graph,
+        "wall_ms_per_step": p_wall, "execution": mode, "kernels": kern, "eager": eager, "graph": graph,
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline_block(gb, types, emb, proj, model, h)
