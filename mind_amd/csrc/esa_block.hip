@@ -422,11 +422,15 @@ void reduce_columns(const float* part, int nparts, int width, float* part2, int 
 // esa/mlp_utils.py:18-37).  Block (i, j) sums 4-column chunks of column tile
 // i over row range j, in row order, into part[j]; reduce_columns adds the
 // row ranges in order.
-constexpr int kColMaxRowBlocks = 1024;
+// Row ranges: at most 1024, or 2048 from 1024 columns on, where a row range's
+// blocks are few (one or two column tiles) and the extra waves keep more loads
+// in flight (esa_mish_bwd_colsum at 129,850 x 2048 bf16: 404 -> 334 us; the
+// column sum alone 119 -> 112 us); at 512 columns 2048 ranges gave no gain.
 constexpr int kColMinRows = 32;   // rows per row range at least
 
-int colsum_row_blocks(int64_t rows) {
-  return (int)std::max<int64_t>(1, std::min<int64_t>(kColMaxRowBlocks, (rows + kColMinRows - 1) / kColMinRows));
+int colsum_row_blocks(int64_t rows, int cols) {
+  const int64_t cap = cols >= 1024 ? 2048 : 1024;
+  return (int)std::max<int64_t>(1, std::min<int64_t>(cap, (rows + kColMinRows - 1) / kColMinRows));
 }
 
 template <typename T>
@@ -619,6 +623,21 @@ int mab_residual_bwd_typed(const T* z, const float* g, T* dz, T* g_o, int64_t n,
 // col_sum_partial_kernel over the rounded dz, so the partials (and, through
 // reduce_columns, the sums) equal esa_column_sum's over the stored dz.  One
 // pass instead of a second read of dz.
+// Raw 16- or 8-byte row chunk of CPT columns as the kernel loads it.
+template <typename T, int CPT> struct RowChunk;
+template <> struct RowChunk<float, 4> {
+  typedef f32x4 V;
+  DEVI static float get(const V& v, int e) { return v[e]; }
+};
+template <> struct RowChunk<bf16, 8> {
+  typedef bf16x8 V;
+  DEVI static float get(const V& v, int e) { return (float)v[e]; }
+};
+template <> struct RowChunk<bf16, 4> {
+  typedef bf16x4 V;
+  DEVI static float get(const V& v, int e) { return (float)v[e]; }
+};
+
 template <typename T, int CPT>
 __global__ __launch_bounds__(256) void mish_bwd_colsum_kernel(const T* __restrict__ z, const T* __restrict__ g,
                                                               int64_t rows, int cols, int64_t rows_per_block,
@@ -626,7 +645,10 @@ __global__ __launch_bounds__(256) void mish_bwd_colsum_kernel(const T* __restric
   // The sums add the stored (rounded) products: without this the compiler keeps a multiply for the store and
   // fuses g * mish'(z) into the accumulation (an fma of the unrounded product).  mish_grad_f keeps its own.
 #pragma clang fp contract(off)
+  typedef RowChunk<T, CPT> R;
+  typedef typename R::V V;
   constexpr int Q = CPT / 4;   // 4-column quads per thread: one 16-byte access per row for bf16 (CPT = 8)
+  constexpr int U = 4;         // rows per batch; two batches in registers
   const int c = CPT * (blockIdx.x * blockDim.x + threadIdx.x);
   if (c >= cols) return;
   const int64_t r0 = (int64_t)blockIdx.y * rows_per_block;
@@ -634,37 +656,55 @@ __global__ __launch_bounds__(256) void mish_bwd_colsum_kernel(const T* __restric
   f32x4 a[Q];
 #pragma unroll
   for (int q = 0; q < Q; ++q) a[q] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
-  for (int64_t r = r0; r < r1; ++r) {
-    f32x4 zv[Q], gv[Q], d[Q];
-    if constexpr (Q == 2) {
-      const bf16x8 zz = *reinterpret_cast<const bf16x8*>(z + r * cols + c);
-      const bf16x8 gg = *reinterpret_cast<const bf16x8*>(g + r * cols + c);
+  // Each thread walks its rows in order; the loads of the next batch of U
+  // rows are issued before the current batch's arithmetic, so a wave keeps
+  // two batches of loads in flight (the slope's range test is a branch per
+  // element, which the compiler will not hoist loads across).  Loads past r1
+  // re-read row r1 - 1 and are not used: the waits stay exact.
+  V zr[2][U], gr[2][U];
+  auto load = [&](int b, int64_t rb) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        zv[e / 4][e % 4] = (float)zz[e];
-        gv[e / 4][e % 4] = (float)gg[e];
+    for (int u = 0; u < U; ++u) {
+      const int64_t r = std::min<int64_t>(rb + u, r1 - 1);
+      zr[b][u] = *reinterpret_cast<const V*>(z + r * cols + c);
+      gr[b][u] = *reinterpret_cast<const V*>(g + r * cols + c);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto batch = [&](int b, int64_t rb) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (rb + u >= r1) break;   // uniform over the block
+      f32x4 d[Q];
+#pragma unroll
+      for (int q = 0; q < Q; ++q)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          d[q][e] = round_to(R::get(gr[b][u], 4 * q + e) * mish_grad_f(R::get(zr[b][u], 4 * q + e)), (T*)nullptr);
+      T* out = dz + (rb + u) * cols + c;
+      if constexpr (Q == 2) {
+        bf16x8 o;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = (bf16)d[e / 4][e % 4];
+        *reinterpret_cast<bf16x8*>(out) = o;
+      } else {
+        store4(out, d[0]);
       }
-    } else {
-      zv[0] = load4(z + r * cols + c);
-      gv[0] = load4(g + r * cols + c);
+#pragma unroll
+      for (int q = 0; q < Q; ++q)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) a[q][e] += d[q][e];
     }
-#pragma unroll
-    for (int q = 0; q < Q; ++q)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) d[q][e] = round_to(gv[q][e] * mish_grad_f(zv[q][e]), (T*)nullptr);
-    if constexpr (Q == 2) {
-      bf16x8 o;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = (bf16)d[e / 4][e % 4];
-      *reinterpret_cast<bf16x8*>(dz + r * cols + c) = o;
-    } else {
-      store4(dz + r * cols + c, d[0]);
+  };
+  if (r0 < r1) {
+    load(0, r0);
+    for (int64_t rb = r0; rb < r1; rb += 2 * U) {
+      load(1, rb + U);
+      batch(0, rb);
+      if (rb + U >= r1) break;
+      load(0, rb + 2 * U);
+      batch(1, rb + U);
     }
-#pragma unroll
-    for (int q = 0; q < Q; ++q)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) a[q][e] += d[q][e];
   }
 #pragma unroll
   for (int q = 0; q < Q; ++q) store4(part + (size_t)blockIdx.y * cols + c + 4 * q, a[q]);
@@ -770,7 +810,7 @@ extern "C" ESA_API int esa_layer_norm_bwd(const void* x, int x_dtype, const floa
 extern "C" ESA_API int esa_column_sum_workspace_size(int64_t rows, int cols, size_t* bytes) {
   if (!bytes) return ESA_ERR_NULL;
   if (rows < 0 || cols < 4 || cols % 4) return ESA_ERR_SHAPE;
-  *bytes = ((size_t)colsum_row_blocks(rows) * cols + reduce_scratch_floats(cols)) * sizeof(float);
+  *bytes = ((size_t)colsum_row_blocks(rows, cols) * cols + reduce_scratch_floats(cols)) * sizeof(float);
   return ESA_OK;
 }
 
@@ -779,7 +819,7 @@ extern "C" ESA_API int esa_column_sum(const void* x, int dtype, int64_t rows, in
   if (rows < 0 || cols < 4 || cols % 4) return ESA_ERR_SHAPE;
   if (dtype != ESA_F32 && dtype != ESA_BF16) return ESA_ERR_DTYPE;
   if (!out || !workspace || (rows > 0 && !x)) return ESA_ERR_NULL;
-  const int rb = colsum_row_blocks(rows);
+  const int rb = colsum_row_blocks(rows, cols);
   if (workspace_bytes < ((size_t)rb * cols + reduce_scratch_floats(cols)) * sizeof(float)) return ESA_ERR_WORKSPACE;
   if (!aligned16(x) || !aligned16(workspace)) return ESA_ERR_ALIGN;
   hipStream_t st = (hipStream_t)stream;
@@ -809,7 +849,7 @@ extern "C" ESA_API int esa_mish_bwd_colsum(const void* z, const void* grad, int6
   if (rows < 0 || cols < 4 || cols % 4) return ESA_ERR_SHAPE;
   if (dtype != ESA_F32 && dtype != ESA_BF16) return ESA_ERR_DTYPE;
   if (!dbias || !workspace || (rows > 0 && (!z || !grad || !dz))) return ESA_ERR_NULL;
-  const int rb = colsum_row_blocks(rows);
+  const int rb = colsum_row_blocks(rows, cols);
   if (workspace_bytes < ((size_t)rb * cols + reduce_scratch_floats(cols)) * sizeof(float)) return ESA_ERR_WORKSPACE;
   if (!aligned16(z) || !aligned16(grad) || !aligned16(dz) || !aligned16(workspace)) return ESA_ERR_ALIGN;
   hipStream_t st = (hipStream_t)stream;

@@ -164,8 +164,8 @@ class _LinearMish(torch.autograd.Function):
         dz = torch.empty_like(z)
         rows, cols = z.shape
         db = None
-        # fused from 1024 columns (131,072 x 2048 bf16: 330 vs 399 us); narrower, its grid of one wave per
-        # column tile and row range is latency-bound (x 512: 156 vs 98 us) and the two kernels run instead
+        # fused from 1024 columns (129,850 x 2048 bf16: 334 vs 397 us for the two kernels); at 512 columns the
+        # two cost the same (104 vs 105 us) and the two kernels run
         if bdt is not None and ctx.needs_input_grad[2] and cols % 4 == 0 and cols >= _FUSED_COLSUM_MIN_COLS:
             n = ctypes.c_size_t(0)
             _lib.check(lib.esa_column_sum_workspace_size(rows, cols, ctypes.byref(n)), "esa_column_sum_workspace_size")

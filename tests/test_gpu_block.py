@@ -312,7 +312,8 @@ def test_layer_norm_edge_cases(device):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("rows,cols", [(0, 8), (1, 4), (31, 12), (1000, 512), (131072, 512), (5000, 2052)])
+@pytest.mark.parametrize("rows,cols", [(0, 8), (1, 4), (31, 12), (1000, 512), (131072, 512), (5000, 2052),
+                                       (70001, 1024)])
 def test_column_sum(device, dtype, rows, cols):
     """esa_column_sum against the fp64 sum (bar: 1e-5 relative + rows 2^-24 max|x| of fp32 accumulation) and
     bitwise repeatable."""
@@ -329,10 +330,11 @@ def test_column_sum(device, dtype, rows, cols):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("rows,cols", [(0, 8), (1, 4), (37, 2048), (5000, 516), (131072, 512)])
+@pytest.mark.parametrize("rows,cols", [(0, 8), (1, 4), (37, 2048), (5000, 516), (131072, 512), (65539, 1024)])
 def test_mish_bwd_colsum_matches_unfused(device, dtype, rows, cols):
     """esa_mish_bwd_colsum: dz bit-equal to esa_mish_bwd's and the bias gradient bit-equal to esa_column_sum over
-    that dz (the same row ranges, order and rounding); no rows gives a zero bias gradient."""
+    that dz (the same row ranges, order and rounding); no rows gives a zero bias gradient.  65,539 x 1024: 2048
+    row ranges of 33 rows, one of them holding a single row and the 61 after it empty."""
     import ctypes
     from mind_amd.esa.linear import column_sum
     gen = torch.Generator().manual_seed(rows + 3 * cols)
