@@ -566,37 +566,43 @@ __global__ void fill_minus_one_kernel(int* __restrict__ p, long n, int* __restri
   if (sym && blockIdx.x == 0 && threadIdx.x == 0) *sym = 1;
   for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long)gridDim.x * blockDim.x) p[i] = -1;
 }
-// Per query token t: row_of over its row, and its descriptor.  With `sym`
-// (one segment array, as many queries as keys): clears *sym unless the CSR
-// equals its transpose as far as row t shows -- its bounds in order (row 0
-// from 0, the last row to nnz), its entries keys in [0, total_k) in
-// ascending order, and each entry (t, x), the r-th of equal ones, matched by
-// an r-th entry t in row x (a binary search there; an unsorted row x clears
-// the flag from its own thread).  Over all rows this is a bijection between
-// the entries (t, x) and (x, t) with multiplicity, i.e. indptr = t_indptr and
-// indices = t_rows.
-__global__ void query_rows_kernel(const int* __restrict__ indptr, const int* __restrict__ indices,
-                                  const int* __restrict__ cu_q, const int* __restrict__ cu_k, int nseg, int total_q,
-                                  int total_k, int nnz, int* __restrict__ row_of, int4* __restrict__ q_desc,
-                                  int* __restrict__ sym) {
-  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+// Per query token t, kRowLanes lanes: row_of over its row (entries strided
+// over the lanes), and its descriptor.  With `sym` (one segment array, as
+// many queries as keys): clears *sym unless the CSR equals its transpose as
+// far as row t shows -- its bounds in order (row 0 from 0, the last row to
+// nnz), its entries keys in [0, total_k) in ascending order, and each entry
+// (t, x), the r-th of equal ones, matched by an r-th entry t in row x (a
+// binary search there).  Over all rows this is a bijection between the
+// entries (t, x) and (x, t) with multiplicity, i.e. indptr = t_indptr and
+// indices = t_rows.  Each lane checks its own entries against their
+// predecessors (order, and r from the run of equal ones before it), so a
+// row's checks run side by side: the chain of dependent loads per lane is one
+// entry's (with one thread per row it was the whole row's, 15.8 us at 65,486
+// tokens of degree 4.6).
+constexpr int kRowLanes = 8;
+__global__ __launch_bounds__(256) void query_rows_kernel(const int* __restrict__ indptr,
+                                                         const int* __restrict__ indices, const int* __restrict__ cu_q,
+                                                         const int* __restrict__ cu_k, int nseg, int total_q,
+                                                         int total_k, int nnz, int* __restrict__ row_of,
+                                                         int4* __restrict__ q_desc, int* __restrict__ sym) {
+  const long g = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const int t = (int)(g / kRowLanes), j = (int)(g % kRowLanes);
   if (t >= total_q) return;
   int pa, pb;
   csr_row(indptr, t, nnz, pa, pb);
-  for (int p = pa; p < pb; ++p) row_of[p] = t;
-  q_desc[t] = make_desc(cu_k, total_k, indptr, nnz, seg_of(cu_q, nseg, t), t);
+  for (int p = pa + j; p < pb; p += kRowLanes) row_of[p] = t;
+  if (j == 0) q_desc[t] = make_desc(cu_k, total_k, indptr, nnz, seg_of(cu_q, nseg, t), t);
   if (!sym) return;
   const int ra = indptr[t], rb = indptr[t + 1];
   bool ok = ra >= 0 && ra <= rb && rb <= nnz && (t > 0 || ra == 0) && (t + 1 < total_q || rb == nnz);
-  int prev = INT_MIN, rank = 0;
-  for (int p = pa; ok && p < pb; ++p) {
+  for (int p = pa + j; ok && p < pb; p += kRowLanes) {
     const int x = indices[p];
-    if (x < 0 || x >= total_k || x < prev) {
+    if (x < 0 || x >= total_k || (p > pa && x < indices[p - 1])) {
       ok = false;
       break;
     }
-    rank = x == prev ? rank + 1 : 0;
-    prev = x;
+    int rank = 0;   // equal entries right before p (in a sorted row: all the earlier equal ones)
+    while (p - rank > pa && indices[p - rank - 1] == x) ++rank;
     int lo, hi;
     csr_row(indptr, x, nnz, lo, hi);
     const int end = hi;
@@ -700,8 +706,8 @@ int build_transposed(const int* indptr, const int* indices, const int* cu_q, con
     ESA_LAUNCH_CHECK();
   }
   if (total_q > 0) {
-    hipLaunchKernelGGL(query_rows_kernel, dim3((unsigned)((total_q + 255) / 256)), dim3(256), 0, st, indptr,
-                       indices, cu_q, cu_k, nseg, total_q, total_k, nnz, row_of, q_desc, sym);
+    hipLaunchKernelGGL(query_rows_kernel, dim3((unsigned)(((long)total_q * kRowLanes + 255) / 256)), dim3(256), 0, st,
+                       indptr, indices, cu_q, cu_k, nseg, total_q, total_k, nnz, row_of, q_desc, sym);
     ESA_LAUNCH_CHECK();
   }
   int rc = csr_build_impl(indices, nnz, total_k, t_indptr, t_perm, base + w.csr, w.csr_bytes, st, sym);
