@@ -577,9 +577,25 @@ __global__ void fill_minus_one_kernel(int* __restrict__ p, long n, int* __restri
 // indices = t_rows.  Each lane checks its own entries against their
 // predecessors (order, and r from the run of equal ones before it), so a
 // row's checks run side by side: the chain of dependent loads per lane is one
-// entry's (with one thread per row it was the whole row's, 15.8 us at 65,486
-// tokens of degree 4.6).
+// entry's (with one thread per row it was the whole row's: 15.8 -> 7.6 us at
+// 65,486 tokens of degree 4.6, the group's segment search included).
 constexpr int kRowLanes = 8;
+
+// seg_of(cu, nseg, t) by the kRowLanes lanes of one row (lane j of the group
+// at bit offset `shift` of the wave's ballot): an 8-ary search, one dependent
+// load per step instead of one per halving (wave_seg_of's method per group).
+DEVI int group_seg_of(const int* __restrict__ cu, int nseg, int t, int j, int shift) {
+  int base = 0, span = nseg;
+  while (span > 1) {
+    const int step = (span + kRowLanes - 1) / kRowLanes, end = base + span;
+    const int s = base + j * step;
+    const uint32_t m = (uint32_t)(__ballot(s < end && cu[s] <= t) >> shift) & ((1u << kRowLanes) - 1u);
+    if (m == 0) break;   // cu[base] > t: only possible at base 0 (seg_of's answer as well)
+    base += (31 - __builtin_clz(m)) * step;
+    span = min(step, end - base);
+  }
+  return base;
+}
 __global__ __launch_bounds__(256) void query_rows_kernel(const int* __restrict__ indptr,
                                                          const int* __restrict__ indices, const int* __restrict__ cu_q,
                                                          const int* __restrict__ cu_k, int nseg, int total_q,
@@ -591,7 +607,8 @@ __global__ __launch_bounds__(256) void query_rows_kernel(const int* __restrict__
   int pa, pb;
   csr_row(indptr, t, nnz, pa, pb);
   for (int p = pa + j; p < pb; p += kRowLanes) row_of[p] = t;
-  if (j == 0) q_desc[t] = make_desc(cu_k, total_k, indptr, nnz, seg_of(cu_q, nseg, t), t);
+  const int sg = group_seg_of(cu_q, nseg, t, j, (int)(threadIdx.x & 63) - j);   // all lanes of the row
+  if (j == 0) q_desc[t] = make_desc(cu_k, total_k, indptr, nnz, sg, t);
   if (!sym) return;
   const int ra = indptr[t], rb = indptr[t + 1];
   bool ok = ra >= 0 && ra <= rb && rb <= nnz && (t > 0 || ra == 0) && (t + 1 < total_q || rb == nnz);
